@@ -1,0 +1,285 @@
+"""Write the golden vectors that pin the CPU oracle to the reference's own code.
+
+Run in the build container only (the reference tree is not present on the GPU
+box):
+
+    python tests/golden/make_golden.py /root/reference/src
+
+It imports pherber3/bmx from the given ``src`` directory, runs the reference's
+codec / attention / cache functions on small seeded inputs, and writes the inputs
+and outputs as ``.npz`` fixtures next to this script.  Only data is written.
+
+``bmx.decomp``'s package ``__init__`` imports ``tensorly`` for the CP/Tucker
+baselines, which this image does not ship.  The hot path only needs
+``bmx/decomp/lrs.py`` (``truncated_svd``) and ``bmx/decomp/base.py``, so the
+script registers ``bmx.decomp`` as a bare package pointing at the real directory
+(its ``__init__`` is not executed) and then imports those two real modules.
+
+Functions covered (reference file:line, paths under ``src/bmx``):
+  * gaussian_codebook            cache/codecs.py:346-380
+  * _hadamard_signs              cache/codecs.py:114-124
+  * fwht                         quant/hadamard.py:12-25
+  * quantize_packed (k2b K, V, rtn arms)  cache/codecs.py:698-796
+  * PackedStreamingLayer._pack_k_block frozen-subspace logic
+                                 cache/packed_streaming.py:475-542
+  * pack_codes / pack_signed_codes  cache/triton_dequant_attention.py:49-165
+  * rope_cos_sin                 cache/rope.py:19-58
+  * naive_dense_attention / chunked_dequant_attention
+                                 cache/chunked_attention.py:254-317, 398-530
+  * _tail_partial + merge math   cache/triton_dequant_attention.py:324-360, 409-461
+  * PackedStreamingCache under HF generate (tiny Llama, head_dim 128)
+                                 cache/packed_streaming.py:1067-1222
+"""
+
+from __future__ import annotations
+
+import importlib
+import math
+import os
+import sys
+import types
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+
+
+def _import_reference(src: str):
+    src = os.path.abspath(src)
+    sys.path.insert(0, src)
+    import bmx  # noqa: F401  (top-level package, empty __init__)
+
+    pkg = types.ModuleType("bmx.decomp")
+    pkg.__path__ = [os.path.join(src, "bmx", "decomp")]
+    sys.modules["bmx.decomp"] = pkg
+    importlib.import_module("bmx.decomp.base")
+    importlib.import_module("bmx.decomp.lrs")
+
+
+def synthetic_k2b_keys(h_kv, S, d, rank, seed):
+    """Pre-RoPE keys = U c + residual (per KV head), U a seeded-QR orthonormal basis."""
+    g = torch.Generator().manual_seed(seed)
+    out = torch.empty(h_kv, S, d)
+    for h in range(h_kv):
+        A = torch.randn(d, rank, generator=g)
+        Q, R = torch.linalg.qr(A)
+        sgn = torch.sign(torch.diagonal(R))
+        sgn[sgn == 0] = 1
+        U = Q * sgn
+        std = torch.arange(1, rank + 1, dtype=torch.float32) ** (-0.35)
+        c = torch.randn(S, rank, generator=g) * std
+        out[h] = c @ U.T + 0.05 * torch.randn(S, d, generator=g)
+    return out.half()
+
+
+def codec_fixtures():
+    from bmx.cache import codecs
+    from bmx.cache.collect import to_matrix
+    from bmx.cache.streaming import compute_flush_schedule
+    from bmx.cache.triton_dequant_attention import pack_codes, pack_signed_codes
+    from bmx.decomp.lrs import truncated_svd
+    from bmx.quant.hadamard import fwht
+
+    out = {}
+    for b in (2, 3, 4):
+        out[f"codebook_b{b}"] = codecs.gaussian_codebook(b).numpy()
+    for s in (0, 7):
+        out[f"signs_d128_s{s}"] = codecs._hadamard_signs(128, s).numpy().astype(np.int8)
+    out["signs_d64_s0"] = codecs._hadamard_signs(64, 0).numpy().astype(np.int8)
+
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(8, 128, generator=g)
+    out["fwht_in"] = x.numpy()
+    out["fwht_out"] = fwht(x).numpy()
+
+    # k2b pages: 3 codec pages of 128 tokens, h_kv=2, d=128 (C=256).
+    h_kv, d, S, PAGE = 2, 128, 384, 128
+    for rank in (16, 32):
+        kpre = synthetic_k2b_keys(h_kv, S, d, rank, seed=100 + rank)
+        gv = torch.Generator().manual_seed(200 + rank)
+        v = torch.randn(h_kv, S, d, generator=gv).half()
+        out[f"k2b_r{rank}_kpre"] = kpre.numpy()
+        out[f"k2b_r{rank}_v"] = v.numpy()
+        frozen = None
+        for p in range(S // PAGE):
+            M = to_matrix(kpre[:, p * PAGE:(p + 1) * PAGE, :].float())
+            if frozen is None:  # packed_streaming.py:513-516
+                Us, V = truncated_svd(M, rank)
+                frozen = (Us, V)
+                out[f"k2b_r{rank}_svd_us_fp32"] = Us.numpy()
+                out[f"k2b_r{rank}_svd_v_fp32"] = V.numpy()
+            else:  # :517-520
+                Us = M @ frozen[1]
+            kp, bpe_k = codecs.quantize_packed(
+                "lowrank_rtn_channel", M, bits=3, group=64, rank=rank,
+                svd_factors=(Us, frozen[1]), seed=0)
+            pre = f"k2b_r{rank}_p{p}_"
+            out[pre + "us"] = kp["Us"].numpy()
+            out[pre + "v"] = kp["V"].numpy()
+            out[pre + "res"] = kp["res_Q_int"].numpy()
+            out[pre + "scale"] = kp["res_scale"].numpy()
+            out[pre + "bpe_k"] = np.float64(bpe_k)
+            Mv = to_matrix(v[:, p * PAGE:(p + 1) * PAGE, :].float())
+            vp, bpe_v = codecs.quantize_packed(
+                "turboquant_mse_perhead", Mv, bits=2, seed=0, h_heads=h_kv)
+            out[pre + "vidx"] = vp["indices"].numpy()
+            out[pre + "vnorm"] = vp["norms"].numpy()
+            out[pre + "bpe_v"] = np.float64(bpe_v)
+            if p == 0:
+                out[pre + "vidx_packed"] = pack_codes(vp["indices"], 2).numpy()
+                out[pre + "res_packed"] = pack_signed_codes(kp["res_Q_int"], 3).numpy()
+                deq = codecs.dequant_packed("lowrank_rtn_channel", kp, group=64)
+                out[pre + "kdeq"] = deq.numpy()
+                vdeq = codecs.dequant_packed("turboquant_mse_perhead", vp, seed=0)
+                out[pre + "vdeq"] = vdeq.numpy()
+
+    # RTN arms (config-1 analogues): rtn_channel K 4b g32, rtn_token V 4b g32.
+    g = torch.Generator().manual_seed(5)
+    K = torch.randn(128, 256, generator=g)
+    K[:, [3, 77, 130, 201]] *= 10.0
+    Vv = torch.randn(128, 256, generator=g)
+    out["rtn_k_in"] = K.numpy()
+    out["rtn_v_in"] = Vv.numpy()
+    kp, bk = codecs.quantize_packed("rtn_channel", K, bits=4, group=32)
+    vp, bv = codecs.quantize_packed("rtn_token", Vv, bits=4, group=32)
+    out["rtn_channel_q"] = kp["Q_int"].numpy()
+    out["rtn_channel_scale"] = kp["scale"].numpy()
+    out["rtn_channel_bpe"] = np.float64(bk)
+    out["rtn_channel_deq"] = codecs.dequant_packed("rtn_channel", kp, group=32).numpy()
+    out["rtn_token_q"] = vp["Q_int"].numpy()
+    out["rtn_token_scale"] = vp["scale"].numpy()
+    out["rtn_token_bpe"] = np.float64(bv)
+    out["rtn_token_deq"] = codecs.dequant_packed("rtn_token", vp, group=32).numpy()
+
+    sched = [(S, W, gq, compute_flush_schedule(S, W, gq))
+             for S in (0, 31, 32, 33, 160, 161, 300, 4096, 65536 + 200)
+             for W in (32, 128) for gq in (64, 128)]
+    out["flush_schedule"] = np.array(sched, dtype=np.int64)
+    return out
+
+
+def attention_fixtures():
+    from transformers import LlamaConfig
+
+    from bmx.cache import codecs
+    from bmx.cache.chunked_attention import chunked_dequant_attention, naive_dense_attention
+    from bmx.cache.collect import to_matrix
+    from bmx.cache.rope import rope_cos_sin
+    from bmx.cache.triton_dequant_attention import _tail_partial
+    from bmx.decomp.lrs import truncated_svd
+
+    out = {}
+    h_kv, G, d, PAGE, n_pages, T = 2, 4, 128, 128, 3, 40
+    S = n_pages * PAGE
+    for rank, vseed in ((16, 0), (32, 7)):
+        cfg = LlamaConfig(hidden_size=h_kv * G * d, num_attention_heads=h_kv * G,
+                          num_key_value_heads=h_kv, head_dim=d, rope_theta=500000.0,
+                          max_position_embeddings=4096)
+        cos, sin = rope_cos_sin(cfg, S + T)
+        kpre = synthetic_k2b_keys(h_kv, S + T, d, rank, seed=300 + rank)
+        gq = torch.Generator().manual_seed(400 + rank)
+        v = torch.randn(h_kv, S + T, d, generator=gq).half()
+        q = torch.randn(h_kv * G, 1, d, generator=gq)
+        k_blocks, v_blocks, frozen = [], [], None
+        for p in range(n_pages):
+            M = to_matrix(kpre[:, p * PAGE:(p + 1) * PAGE, :].float())
+            if frozen is None:
+                frozen = truncated_svd(M, rank)
+                Us = frozen[0]
+            else:
+                Us = M @ frozen[1]
+            kp, _ = codecs.quantize_packed("lowrank_rtn_channel", M, bits=3, group=64,
+                                           rank=rank, svd_factors=(Us, frozen[1]))
+            Mv = to_matrix(v[:, p * PAGE:(p + 1) * PAGE, :].float())
+            vp, _ = codecs.quantize_packed("turboquant_mse_perhead", Mv, bits=2,
+                                           seed=vseed, h_heads=h_kv)
+            k_blocks.append((kp, p * PAGE, (p + 1) * PAGE))
+            v_blocks.append((vp, p * PAGE, (p + 1) * PAGE))
+        # fp16 recent window: post-RoPE keys (HF applies RoPE in fp32, slab is fp16).
+        k_tail = (kpre[:, S:, :].float() * cos[S:] +
+                  torch.cat([-kpre[:, S:, d // 2:].float(), kpre[:, S:, :d // 2].float()],
+                            dim=-1) * sin[S:]).half()
+        v_tail = v[:, S:, :]
+        kw = dict(k_arm="lowrank_rtn_channel", v_arm="turboquant_mse_perhead",
+                  group=64, seed=0, k_pre_rope=True, rope_cos=cos, rope_sin=sin,
+                  k_tail=k_tail, v_tail=v_tail, n_q_groups=G, scale=d ** -0.5,
+                  v_group=64, v_seed=vseed)
+        o_naive = naive_dense_attention(q, k_blocks, v_blocks, **kw)
+        o_chunk = chunked_dequant_attention(q, k_blocks, v_blocks, **kw)
+        # the packed cache's fp16 tables (packed_streaming.py:106-111)
+        kw16 = dict(kw, rope_cos=cos.half(), rope_sin=sin.half())
+        o_chunk16 = chunked_dequant_attention(q, k_blocks, v_blocks, **kw16)
+        acc_t, m_t, lse_t = _tail_partial(q.view(h_kv, G, d), k_tail, v_tail, d ** -0.5)
+        pre = f"attn_r{rank}_"
+        out[pre + "kpre"] = kpre.numpy()
+        out[pre + "v"] = v.numpy()
+        out[pre + "q"] = q.numpy()
+        out[pre + "k_tail"] = k_tail.numpy()
+        pos = np.arange(0, S + T, 7)
+        out[pre + "rope_pos"] = pos
+        out[pre + "cos"] = cos[pos].numpy()
+        out[pre + "sin"] = sin[pos].numpy()
+        out[pre + "vseed"] = np.int64(vseed)
+        out[pre + "naive"] = o_naive.numpy()
+        out[pre + "chunked"] = o_chunk.numpy()
+        out[pre + "chunked_fp16rope"] = o_chunk16.numpy()
+        out[pre + "tail_acc"] = acc_t.numpy()
+        out[pre + "tail_m"] = m_t.numpy()
+        out[pre + "tail_lse"] = lse_t.numpy()
+        out[pre + "svd_us"] = frozen[0].numpy()
+        out[pre + "svd_v"] = frozen[1].numpy()
+    return out
+
+
+def tiny_model_config():
+    from transformers import LlamaConfig
+
+    return LlamaConfig(
+        vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+        num_attention_heads=4, num_key_value_heads=2, head_dim=128,
+        max_position_embeddings=4096, rope_theta=500000.0, initializer_range=0.1)
+
+
+def e2e_fixtures():
+    from transformers import LlamaForCausalLM
+
+    from bmx.cache.packed_streaming import PackedStreamingCache
+    from bmx.cache.recipes import spec_pair
+
+    cfg = tiny_model_config()
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).eval()
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (1, 300), generator=g)
+    out = {"prompt": ids.numpy()}
+    for rank in (16, 32):
+        k_spec, v_spec = spec_pair("k2b_ph", rank=rank)
+        cache = PackedStreamingCache(cfg, k_spec, v_spec, recent_window=32)
+        cache.attach(model)
+        with torch.no_grad():
+            res = model.generate(ids, past_key_values=cache, max_new_tokens=140, min_new_tokens=140,
+                                 do_sample=False, output_logits=True,
+                                 return_dict_in_generate=True, pad_token_id=0)
+        bpe = cache.bits_per_entry()
+        cache.detach()
+        out[f"r{rank}_tokens"] = res.sequences.numpy()
+        out[f"r{rank}_logits"] = torch.stack(res.logits, 0).squeeze(1).numpy()
+        out[f"r{rank}_bpe"] = np.array(bpe, dtype=np.float64)
+    return out
+
+
+def main():
+    src = sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src"
+    torch.set_num_threads(min(8, os.cpu_count() or 1))
+    _import_reference(src)
+    np.savez_compressed(HERE / "codecs.npz", **codec_fixtures())
+    np.savez_compressed(HERE / "attention.npz", **attention_fixtures())
+    np.savez_compressed(HERE / "e2e_tiny_llama.npz", **e2e_fixtures())
+    for f in sorted(HERE.glob("*.npz")):
+        print(f.name, f.stat().st_size)
+
+
+if __name__ == "__main__":
+    main()
