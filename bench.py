@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark of the k2b packed-KV path on one MI355X.
+
+Workload (BASELINE.json configs[2] geometry at the headline 64k context):
+Llama-3.1-8B attention geometry (32 layers, 32 query / 8 KV heads, head_dim
+128), batch 1, k2b recipe at rank 32 (752 bytes per token per layer = 2.94
+bits per entry), total context 65,536 tokens = 65,408 committed (packed) +
+128 fp16 recent-window tokens, RoPE theta 5e5 applied at read.  32 distinct
+synthetic layer caches (1.6 GB of pages) so a step streams from HBM, not from
+the 256 MB MALL.  Inputs are resident in HBM before timing starts.
+
+A "step" is one decode-attention call per layer for all 32 layers (the
+attention part of one generated token).  Printed: one JSON line with the
+step time, the split kernel's live HIP-event duration against the HBM
+roofline on its algorithmic bytes, and the CPU chunked-path baseline (the
+oracle's restatement of chunked_dequant_attention) timed on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+METRIC = "decode-attn µs/step + % HBM roofline, k2b 3.0 bpe, 64k ctx, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+H_KV, G, D = 8, 4, 128
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ctx", type=int, default=65536)
+    ap.add_argument("--rank", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--window", type=int, default=128)
+    ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=16384)
+    ap.add_argument("--cpu-reps", type=int, default=7)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(args, packed: int, tail: int) -> dict:
+    """Time the CPU chunked path (oracle restatement of chunked_dequant_attention,
+    fp32 torch) on one layer of cpu_sample_tokens committed + tail tokens and
+    scale linearly (the chunked path is per-page work) to the full step."""
+    import torch
+
+    from bmx_amd import k2b, synth
+    from oracle import attention as A
+
+    gen = torch.Generator().manual_seed(1234)
+    S = args.cpu_sample_tokens
+    k_pre = synth.k2b_keys(H_KV, S + tail, args.rank, gen)
+    v = synth.values(H_KV, S + tail, gen)
+    cache = A.K2bOracleCache(H_KV, D, args.rank)
+    svd = synth.first_page_svd(k_pre, args.rank)
+    for p in range(S // 128):
+        cache.commit(k_pre[:, p * 128:(p + 1) * 128], v[:, p * 128:(p + 1) * 128],
+                     us_override=svd if p == 0 else None)
+    consts = k2b.CodecConsts.make()
+    inv = torch.tensor(consts.inv_freq)
+    k_tail = synth.rope_keys(k_pre[:, S:], S, consts)
+    q = torch.randn(H_KV * G, 1, D, generator=gen)
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    A.k2b_chunked_attention(q, cache, inv, k_tail, v[:, S:], G, D ** -0.5)  # warm-up
+    times = []
+    for _ in range(args.cpu_reps):
+        t0 = time.perf_counter()
+        A.k2b_chunked_attention(q, cache, inv, k_tail, v[:, S:], G, D ** -0.5)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    scale = (packed + tail) / (S + tail) * args.layers
+    return {"value": round(t * scale * 1e6, 1), "unit": "us/step", "cores": threads,
+            "kind": "port",
+            "sample": (f"1 layer of {S} packed + {tail} tail tokens (h_kv 8, G 4, rank {args.rank}), "
+                       f"median of {args.cpu_reps} after 1 warm-up = {t * 1e3:.1f} ms/layer-call, "
+                       f"scaled x{(packed + tail) / (S + tail):.2f} tokens x {args.layers} layers"),
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "how the k2b decode path would shard across GPUs is described in DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from bmx_amd import k2b, synth
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    W = args.window
+    packed = ((args.ctx - W) // 128) * 128
+    tail = args.ctx - packed
+    consts = k2b.CodecConsts.make()
+    page_bytes = k2b.page_bytes(H_KV, args.rank)
+    n_pages = packed // 16
+
+    # ---- build the 32 layer caches with the HIP write kernel ----
+    t_build = time.perf_counter()
+    gen = torch.Generator(device=dev).manual_seed(2024)
+    layers = []
+    pool = synth.PagePool(n_pages * args.layers, H_KV, args.rank, dev,
+                          gen=torch.Generator().manual_seed(7))
+    for li in range(args.layers):
+        k_pre = synth.k2b_keys(H_KV, args.ctx, args.rank, gen)
+        v = synth.values(H_KV, args.ctx, gen)
+        seq = synth.encode_sequence(pool, k_pre[:, :packed], v[:, :packed], args.rank, consts)
+        lay = {
+            "seq": seq,
+            "pt": synth.page_table([seq], device=dev),
+            "len": torch.tensor([packed], dtype=torch.int32, device=dev),
+            "k_tail": synth.rope_keys(k_pre[:, packed:], packed, consts).unsqueeze(0).contiguous(),
+            "v_tail": v[:, packed:].unsqueeze(0).contiguous(),
+            "tail_len": torch.tensor([tail], dtype=torch.int32, device=dev),
+            "q": torch.randn(1, H_KV, G, D, generator=gen, device=dev),
+            "out": torch.empty(1, H_KV, G, D, device=dev),
+        }
+        layers.append(lay)
+        del k_pre, v
+        if li % 8 == 7:
+            torch.cuda.synchronize()
+            print(f"bench: built {li + 1}/{args.layers} layer caches", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t_build = time.perf_counter() - t_build
+
+    ws = k2b.DecodeWorkspace()
+    for lay in layers:
+        lay["plan"] = k2b.DecodePlan(
+            lay["q"], pool.pages, lay["pt"], lay["len"], packed, lay["seq"].basis16, consts,
+            D ** -0.5, rank=args.rank, k_tail=lay["k_tail"], v_tail=lay["v_tail"],
+            tail_len=lay["tail_len"], tail_cap=tail, out=lay["out"],
+            split_tokens=args.split_tokens, workspace=ws)
+
+    for _ in range(args.warmup):
+        for lay in layers:
+            lay["plan"].run()
+    torch.cuda.synchronize()
+
+    # untimed wall-clock pass: host + GPU, one step after another
+    t_wall = time.perf_counter()
+    for _ in range(args.steps):
+        for lay in layers:
+            lay["plan"].run()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+
+    def gpu_sleep():
+        # queue the region behind a GPU sleep so the host enqueues everything
+        # first and the kernels then run back to back (device time only)
+        try:
+            torch.cuda._sleep(int(2e8))
+        except Exception:  # pragma: no cover - sleep helper missing in this torch build
+            pass
+
+    # timed pass (the reported value): K steps back to back, bracketed by events
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    gpu_sleep()
+    start.record()
+    for _ in range(args.steps):
+        for lay in layers:
+            lay["plan"].run()
+    end.record()
+    torch.cuda.synchronize()
+    step_us = start.elapsed_time(end) * 1e3 / args.steps
+
+    # breakdown pass: split kernel and combine kernel timed per call with events
+    # on the stream they run on (events between calls add small gaps, which is
+    # why the reported value comes from the pass above)
+    n_calls = args.steps * args.layers
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_calls)]
+    torch.cuda.synchronize()
+    gpu_sleep()
+    i = 0
+    for _ in range(args.steps):
+        for lay in layers:
+            e0, e1, e2 = ev[i]
+            e0.record()
+            e1.record()  # marks the event recorded for torch; the library re-records it
+            lay["plan"].run(e1)  # after the split kernel
+            e2.record()
+            i += 1
+    torch.cuda.synchronize()
+    split_us = [e0.elapsed_time(e1) * 1e3 for e0, e1, _ in ev]
+    comb_us = [e1.elapsed_time(e2) * 1e3 for _, e1, e2 in ev]
+    split_avg = statistics.mean(split_us)
+    comb_avg = statistics.mean(comb_us)
+
+    C = H_KV * D
+    bytes_split = packed * page_bytes // 16 + C * args.rank * 2            # pages + basis
+    bytes_call = bytes_split + tail * C * 2 * 2 + 2 * H_KV * G * D * 2      # + fp16 tail, q/out
+    achieved = bytes_split / (split_avg * 1e-6) / 1e9
+    call_gbs = bytes_call / ((split_avg + comb_avg) * 1e-6) / 1e9
+    bpe = page_bytes * 8 / 16 / (2 * C)
+    res = {
+        "metric": METRIC,
+        "value": round(step_us, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_us / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"k2b rank-{args.rank} decode attention, Llama-3.1-8B geometry "
+                         f"({args.layers} layers, 32q/8kv heads, d 128), batch 1, ctx {args.ctx} "
+                         f"= {packed} packed + {tail} fp16 tail, 16-token pages, RoPE 5e5 at read"),
+            "ctx": args.ctx, "packed_tokens": packed, "tail_tokens": tail, "layers": args.layers,
+            "batch": 1, "rank": args.rank, "bits_per_entry_kv_avg": round(bpe, 4),
+            "bytes_per_token_layer": page_bytes // 16,
+            "split_tokens": args.split_tokens or "auto",
+        },
+        "per_layer_us": round(step_us / args.layers, 3),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k2b_decode_split_kernel",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": bytes_split,
+            "avg_launch_us": round(split_avg, 3),
+        },
+        "decode_call": {
+            "split_us": round(split_avg, 3), "combine_us": round(comb_avg, 3),
+            "algorithmic_bytes": bytes_call, "gbs": round(call_gbs, 1),
+            "frac": round(call_gbs / HBM_PEAK_GBS, 4),
+            "wall_us_per_step": round(t_wall * 1e6 / args.steps, 1),
+        },
+        "build_s": round(t_build, 1),
+    }
+    if not args.no_cpu_baseline:
+        print(f"bench: GPU timing done ({step_us:.1f} us/step); timing the CPU baseline",
+              file=sys.stderr, flush=True)
+        res["cpu_baseline"] = cpu_baseline(args, packed, tail)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+"""ctypes binding of libbmx_k2b.so (the C-ABI declared in include/bmx_k2b.h).
+
+The library is the product path: there is no fallback.  ``lib()`` raises if the
+shared object was not built (python -m bmx_amd.build) and every wrapper raises
+RuntimeError with the library's own message when a call returns non-zero.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libbmx_k2b.so"
+
+BMX_OK = 0
+SECTIONS = ("us", "vnorm", "kscale", "kres", "vcode")
+
+
+class Geom(ct.Structure):
+    _fields_ = [("h_kv", ct.c_int32), ("rank", ct.c_int32), ("n_q_groups", ct.c_int32)]
+
+
+class DecodeArgs(ct.Structure):
+    _fields_ = [
+        ("geom", Geom),
+        ("batch", ct.c_int32),
+        ("q", ct.c_void_p),
+        ("out", ct.c_void_p),
+        ("pages", ct.c_void_p),
+        ("n_pool_pages", ct.c_int32),
+        ("page_table", ct.c_void_p),
+        ("max_pages", ct.c_int32),
+        ("packed_len", ct.c_void_p),
+        ("max_packed_len", ct.c_int32),
+        ("basis", ct.c_void_p),
+        ("basis_stride", ct.c_int64),
+        ("inv_freq", ct.c_float * 64),
+        ("rope_scaling", ct.c_float),
+        ("sm_scale", ct.c_float),
+        ("codebook", ct.c_float * 4),
+        ("v_sign_bits", ct.c_uint32 * 4),
+        ("k_tail", ct.c_void_p),
+        ("v_tail", ct.c_void_p),
+        ("tail_stride_b", ct.c_int64),
+        ("tail_stride_h", ct.c_int64),
+        ("tail_stride_t", ct.c_int64),
+        ("tail_len", ct.c_void_p),
+        ("tail_cap", ct.c_int32),
+        ("split_tokens", ct.c_int32),
+        ("workspace", ct.c_void_p),
+        ("workspace_bytes", ct.c_size_t),
+        ("split_end_event", ct.c_void_p),
+    ]
+
+
+class AppendArgs(ct.Structure):
+    _fields_ = [
+        ("geom", Geom),
+        ("n_codec_pages", ct.c_int32),
+        ("k_pre", ct.c_void_p),
+        ("k_stride_h", ct.c_int64),
+        ("k_stride_t", ct.c_int64),
+        ("v", ct.c_void_p),
+        ("v_stride_h", ct.c_int64),
+        ("v_stride_t", ct.c_int64),
+        ("basis32", ct.c_void_p),
+        ("basis16", ct.c_void_p),
+        ("us_first", ct.c_void_p),
+        ("codebook", ct.c_float * 4),
+        ("v_sign_bits", ct.c_uint32 * 4),
+        ("pages", ct.c_void_p),
+        ("n_pool_pages", ct.c_int32),
+        ("page_ids", ct.c_void_p),
+    ]
+
+
+class DequantArgs(ct.Structure):
+    _fields_ = [
+        ("geom", Geom),
+        ("pages", ct.c_void_p),
+        ("n_pool_pages", ct.c_int32),
+        ("page_table", ct.c_void_p),
+        ("n_tokens", ct.c_int32),
+        ("basis", ct.c_void_p),
+        ("inv_freq", ct.c_float * 64),
+        ("rope_scaling", ct.c_float),
+        ("apply_rope", ct.c_int32),
+        ("codebook", ct.c_float * 4),
+        ("v_sign_bits", ct.c_uint32 * 4),
+        ("k_out", ct.c_void_p),
+        ("v_out", ct.c_void_p),
+    ]
+
+
+EXPORTS = {
+    "bmx_last_error": (ct.c_char_p, []),
+    "bmx_k2b_page_bytes": (ct.c_size_t, [ct.POINTER(Geom)]),
+    "bmx_k2b_page_section": (ct.c_int, [ct.POINTER(Geom), ct.c_int, ct.POINTER(ct.c_size_t),
+                                        ct.POINTER(ct.c_size_t)]),
+    "bmx_k2b_decode_workspace_bytes": (ct.c_size_t, [ct.POINTER(DecodeArgs)]),
+    "bmx_k2b_decode": (ct.c_int, [ct.POINTER(DecodeArgs), ct.c_void_p]),
+    "bmx_k2b_append": (ct.c_int, [ct.POINTER(AppendArgs), ct.c_void_p]),
+    "bmx_k2b_dequant": (ct.c_int, [ct.POINTER(DequantArgs), ct.c_void_p]),
+}
+
+_LIB = None
+
+
+def lib():
+    """Load libbmx_k2b.so once; raise if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m bmx_amd.build` "
+                "(the k2b decode path has no non-HIP fallback)")
+        h = ct.CDLL(str(LIB_PATH))
+        for name, (res, args) in EXPORTS.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = h
+    return _LIB
+
+
+def check(rc: int, what: str) -> None:
+    if rc != BMX_OK:
+        msg = lib().bmx_last_error().decode()
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def page_bytes(h_kv: int, rank: int) -> int:
+    g = Geom(h_kv, rank, 1)
+    n = lib().bmx_k2b_page_bytes(ct.byref(g))
+    if n == 0:
+        raise RuntimeError(lib().bmx_last_error().decode())
+    return int(n)
+
+
+def page_sections(h_kv: int, rank: int) -> dict:
+    g = Geom(h_kv, rank, 1)
+    out = {}
+    for i, name in enumerate(SECTIONS):
+        off, sz = ct.c_size_t(), ct.c_size_t()
+        check(lib().bmx_k2b_page_section(ct.byref(g), i, ct.byref(off), ct.byref(sz)),
+              "bmx_k2b_page_section")
+        out[name] = (off.value, sz.value)
+    return out

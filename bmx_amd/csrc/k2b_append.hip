@@ -1,0 +1,243 @@
+// Quantize-on-append: encode 128-token codec pages of pre-RoPE keys and values
+// straight into 16-token physical pages, gfx950.
+//
+// Three launches per call (all codec pages of the call in each):
+//   k2b_us_kernel    Us = M * basis32 (or the first page's SVD factor), fp16
+//   k2b_kres_kernel  R = M - Us16 * basis16^T, per-channel 64-token RTN at 3 bits
+//   k2b_v_kernel     per (token, head): fp16 norm, sign flip, FWHT, Lloyd codes
+// Reference semantics: cache/packed_streaming.py:475-580 (page commit),
+// cache/codecs.py:616-636, 677-695, 786-796 (codecs), quant/rtn.py:23-44 (RTN),
+// quant/hadamard.py:12-33 (FWHT).  Element-wise steps follow the reference's
+// operation order (divide, round-half-even, divide-then-multiply by sqrt(d)) and
+// this file is built without floating-point contraction, so codes are identical
+// to the reference's whenever the reduction results (Us, the norm) agree.
+
+#include "k2b_common.h"
+
+namespace bmx {
+
+struct AppendKArgs {
+  int h_kv, R, n_codec_pages, n_pool;
+  const uint16_t* k_pre;
+  int64_t ksh, kst;
+  const uint16_t* v;
+  int64_t vsh, vst;
+  const float* basis32;
+  const uint16_t* basis16;
+  const float* us_first;
+  uint8_t* pages;
+  const int32_t* page_ids;
+  PageLayout L;
+  float codebook[4];
+  uint32_t v_sign_bits[4];
+};
+
+// grid (n_codec_pages * 8), block 256: 16 tokens x 16 rank lanes.
+__global__ __launch_bounds__(256) void k2b_us_kernel(const AppendKArgs a) {
+  const int pg = blockIdx.x;              // physical page slot (16 tokens)
+  const int cp = pg / 8, pl = pg % 8;
+  const int tl = threadIdx.x >> 4, rg = threadIdx.x & 15;
+  const int t = pg * kPT + tl;            // token index within the call
+  const int C = kD * a.h_kv;
+  uint8_t* page = a.pages + clamp_page(a.page_ids[pg], a.n_pool) * a.L.bytes;
+  for (int r = rg; r < a.R; r += 16) {
+    float us;
+    if (a.us_first != nullptr && cp == 0) {
+      us = a.us_first[(pl * kPT + tl) * a.R + r];
+    } else {
+      float acc = 0.f;
+      for (int c = 0; c < C; ++c) {
+        const float m = half_bits_to_float(a.k_pre[(c / kD) * a.ksh + (int64_t)t * a.kst + (c % kD)]);
+        acc = __builtin_fmaf(m, a.basis32[(int64_t)c * a.R + r], acc);
+      }
+      us = acc;
+    }
+    *reinterpret_cast<uint16_t*>(page + a.L.us + (tl * a.R + r) * 2) = float_to_half_bits(us);
+  }
+}
+
+// grid (n_codec_pages * 2 groups, h_kv), block 256: 64 tokens x 128 channels.
+__global__ __launch_bounds__(256) void k2b_kres_kernel(const AppendKArgs a) {
+  const int gi = blockIdx.x;        // 64-token group index within the call
+  const int h = blockIdx.y;
+  const int cp = gi / 2, grp_in = gi % 2;
+  const int C = kD * a.h_kv;
+  const int R = a.R;
+  __shared__ float s_us[kGroup][33];
+  __shared__ float s_b[kD][33];
+  __shared__ float s_amax[2][kD];
+  __shared__ int8_t s_code[kGroup][kD + 4];
+
+  const int tid = threadIdx.x;
+  // Us16 of the group's 64 tokens (already written to the 4 pages)
+  for (int e = tid; e < kGroup * R; e += 256) {
+    const int t = e / R, r = e % R;
+    const int pslot = cp * 8 + grp_in * 4 + t / kPT;
+    const uint8_t* page = a.pages + clamp_page(a.page_ids[pslot], a.n_pool) * a.L.bytes;
+    s_us[t][r] = half_bits_to_float(*reinterpret_cast<const uint16_t*>(page + a.L.us + ((t % kPT) * R + r) * 2));
+  }
+  for (int e = tid; e < kD * R; e += 256) {
+    const int j = e / R, r = e % R;
+    s_b[j][r] = half_bits_to_float(a.basis16[(int64_t)(h * kD + j) * R + r]);
+  }
+  __syncthreads();
+
+  const int j = tid & 127, half = tid >> 7;
+  float res[32];
+  float amax = 0.f;
+#pragma unroll
+  for (int tt = 0; tt < 32; ++tt) {
+    const int t = half * 32 + tt;                                  // token within group
+    const int tg = cp * kCodec + grp_in * kGroup + t;             // token within call
+    float L = 0.f;
+    for (int r = 0; r < R; ++r) L = __builtin_fmaf(s_us[t][r], s_b[j][r], L);
+    const float m = half_bits_to_float(a.k_pre[h * a.ksh + (int64_t)tg * a.kst + j]);
+    res[tt] = m - L;
+    amax = fmaxf(amax, fabsf(res[tt]));
+  }
+  s_amax[half][j] = amax;
+  __syncthreads();
+  const float scale = fmaxf(fmaxf(s_amax[0][j], s_amax[1][j]), 1e-12f) / 3.0f;
+#pragma unroll
+  for (int tt = 0; tt < 32; ++tt) {
+    float cq = rintf(res[tt] / scale);
+    cq = fminf(fmaxf(cq, -4.0f), 3.0f);
+    s_code[half * 32 + tt][j] = (int8_t)cq;
+  }
+  if (half == 0) {
+    const int c = h * kD + j, quarter = C / 4;
+    const int slot = c / quarter, off = c % quarter;
+    uint8_t* page = a.pages + clamp_page(a.page_ids[cp * 8 + grp_in * 4 + slot], a.n_pool) * a.L.bytes;
+    *reinterpret_cast<uint16_t*>(page + a.L.kscale + off * 2) = float_to_half_bits(scale);
+  }
+  __syncthreads();
+  // pack: thread -> (page pl, lane 16q+n)
+  {
+    const int pl = tid >> 6, lane = tid & 63, q = lane >> 4, n = lane & 15;
+    const int t = pl * kPT + n;
+    uint32_t w[3] = {0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      const int jj = 16 * (k >> 2) + 4 * q + (k & 3);
+      const uint32_t v = (uint32_t)(s_code[t][jj]) & 7u;
+      const int bit = 3 * k;
+      w[bit >> 5] |= v << (bit & 31);
+      if ((bit & 31) > 29) w[(bit >> 5) + 1] |= v >> (32 - (bit & 31));
+    }
+    uint8_t* page = a.pages + clamp_page(a.page_ids[cp * 8 + grp_in * 4 + pl], a.n_pool) * a.L.bytes;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(page + a.L.kres + h * 768 + lane * 12);
+    dst[0] = w[0]; dst[1] = w[1]; dst[2] = w[2];
+  }
+}
+
+// grid (n_codec_pages * 8, h_kv), block 256: 16 tokens x 128 channels.
+__global__ __launch_bounds__(256) void k2b_v_kernel(const AppendKArgs a) {
+  const int pg = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x;
+  __shared__ float x[kPT][kD];
+  __shared__ float s_norm[kPT];
+  __shared__ uint8_t code[kPT][kD];
+  uint8_t* page = a.pages + clamp_page(a.page_ids[pg], a.n_pool) * a.L.bytes;
+
+  for (int e = tid; e < kPT * kD; e += 256) {
+    const int t = e / kD, c = e % kD;
+    x[t][c] = half_bits_to_float(a.v[h * a.vsh + (int64_t)(pg * kPT + t) * a.vst + c]);
+  }
+  __syncthreads();
+  // norms: one thread per token, in the order torch's CPU 2-norm reduces a
+  // 128-float row (8 strided FMA accumulators, then a left-to-right sum, then a
+  // correctly rounded sqrt), so the fp16 norm is identical to the reference's
+  if (tid < kPT) {
+    const int t = tid;
+    float acc8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc8[j] = 0.f;
+    for (int i = 0; i < kD; i += 8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc8[j] = __builtin_fmaf(x[t][i + j], x[t][i + j], acc8[j]);
+    }
+    float ss = acc8[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) ss = ss + acc8[j];
+    {
+      const float nrm = fmaxf(__builtin_sqrtf(ss), 1e-12f);
+      const uint16_t nb = float_to_half_bits(nrm);
+      s_norm[t] = half_bits_to_float(nb);
+      *reinterpret_cast<uint16_t*>(page + a.L.vnorm + (h * kPT + t) * 2) = nb;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < kPT * kD; e += 256) {
+    const int t = e / kD, c = e % kD;
+    const float u = x[t][c] / s_norm[t];
+    x[t][c] = sign_neg(a.v_sign_bits, c) ? -u : u;
+  }
+  __syncthreads();
+  // FWHT stages (i, i+hb) inside blocks of 2hb, as quant/hadamard.py:19-25
+  for (int hb = 1; hb < kD; hb <<= 1) {
+    for (int e = tid; e < kPT * kD / 2; e += 256) {
+      const int t = e / (kD / 2), pidx = e % (kD / 2);
+      const int i0 = (pidx / hb) * 2 * hb + (pidx % hb);
+      const float u = x[t][i0], w = x[t][i0 + hb];
+      x[t][i0] = u + w;
+      x[t][i0 + hb] = u - w;
+    }
+    __syncthreads();
+  }
+  const float sqrt_d = 11.313708498984761f;  // fl32(sqrt(128)), applied as / then *
+  const float mid0 = (a.codebook[0] + a.codebook[1]) / 2.0f;
+  const float mid1 = (a.codebook[1] + a.codebook[2]) / 2.0f;
+  const float mid2 = (a.codebook[2] + a.codebook[3]) / 2.0f;
+  for (int e = tid; e < kPT * kD; e += 256) {
+    const int t = e / kD, c = e % kD;
+    const float r = (x[t][c] / sqrt_d) * sqrt_d;
+    code[t][c] = (uint8_t)((r > mid0) + (r > mid1) + (r > mid2));
+  }
+  __syncthreads();
+  if (tid < 128) {
+    const int lane = tid >> 1, w = tid & 1, q = lane >> 4, m = lane & 15;
+    uint32_t dword = 0;
+    for (int bb = 0; bb < 4; ++bb) {
+      const int c = 16 * (4 * w + bb) + m;
+      for (int t = 0; t < 4; ++t)
+        dword |= (uint32_t)code[4 * q + t][c] << (16 * (t & 1) + 4 * bb + 2 * (t >> 1));
+    }
+    *reinterpret_cast<uint32_t*>(page + a.L.vcode + h * 512 + lane * 8 + w * 4) = dword;
+  }
+}
+
+}  // namespace bmx
+
+using namespace bmx;
+
+static int afail(int code, const std::string& msg) {
+  bmx_set_error(msg);
+  return code;
+}
+
+extern "C" int bmx_k2b_append(const bmx_k2b_append_args* a, void* stream) {
+  if (!a) return afail(BMX_E_INVALID, "bmx_k2b_append: args is NULL");
+  const bmx_k2b_geom& g = a->geom;
+  if (g.h_kv < 1 || g.h_kv > 16) return afail(BMX_E_INVALID, "bmx_k2b_append: h_kv must be 1..16");
+  if (g.rank != 16 && g.rank != 32) return afail(BMX_E_INVALID, "bmx_k2b_append: rank must be 16 or 32");
+  if (a->n_codec_pages < 0) return afail(BMX_E_INVALID, "bmx_k2b_append: n_codec_pages < 0");
+  if (a->n_codec_pages == 0) return BMX_OK;
+  if (!a->k_pre || !a->v || !a->basis32 || !a->basis16 || !a->pages || !a->page_ids)
+    return afail(BMX_E_INVALID, "bmx_k2b_append: null pointer argument");
+  if (a->n_pool_pages < 1) return afail(BMX_E_INVALID, "bmx_k2b_append: n_pool_pages must be >= 1");
+  AppendKArgs k{};
+  k.h_kv = g.h_kv; k.R = g.rank; k.n_codec_pages = a->n_codec_pages;
+  k.k_pre = a->k_pre; k.ksh = a->k_stride_h; k.kst = a->k_stride_t;
+  k.v = a->v; k.vsh = a->v_stride_h; k.vst = a->v_stride_t;
+  k.basis32 = a->basis32; k.basis16 = a->basis16; k.us_first = a->us_first;
+  k.pages = a->pages; k.page_ids = a->page_ids; k.n_pool = a->n_pool_pages;
+  k.L = PageLayout::make(g.h_kv, g.rank);
+  for (int i = 0; i < 4; ++i) { k.codebook[i] = a->codebook[i]; k.v_sign_bits[i] = a->v_sign_bits[i]; }
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k2b_us_kernel, dim3(a->n_codec_pages * 8), dim3(256), 0, st, k);
+  hipLaunchKernelGGL(k2b_kres_kernel, dim3(a->n_codec_pages * 2, g.h_kv), dim3(256), 0, st, k);
+  hipLaunchKernelGGL(k2b_v_kernel, dim3(a->n_codec_pages * 8, g.h_kv), dim3(256), 0, st, k);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return afail(BMX_E_HIP, std::string("bmx_k2b_append: launch: ") + hipGetErrorString(e));
+  return BMX_OK;
+}

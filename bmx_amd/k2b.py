@@ -1,0 +1,246 @@
+"""torch-facing wrappers over the k2b C-ABI (decode, append, dequant).
+
+Tensors are HIP device tensors; the calls enqueue on torch's current stream of
+the tensors' device and never allocate inside the library (workspaces come from
+here).  Any non-zero status raises RuntimeError with the library's message: the
+k2b decode path has no non-HIP fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from . import codecs as K
+
+HEAD_DIM = 128
+PAGE_TOKENS = 16
+GROUP = 64
+CODEC_PAGE = 128
+
+
+@dataclass(frozen=True)
+class CodecConsts:
+    """Numbers the kernels take by value: V codebook, V sign bits, RoPE."""
+
+    codebook: tuple
+    sign_bits: tuple
+    inv_freq: tuple
+    rope_scaling: float = 1.0
+
+    @staticmethod
+    def make(*, v_bits: int = 2, v_seed: int = 0, inv_freq=None, rope_scaling: float = 1.0,
+             theta: float = 500000.0):
+        if v_bits != 2:
+            raise ValueError("the k2b kernels implement 2-bit V codes only")
+        if inv_freq is None:
+            inv_freq, rope_scaling = K.rope_inv_freq(head_dim=HEAD_DIM, theta=theta)
+        inv = tuple(float(x) for x in torch.as_tensor(inv_freq, dtype=torch.float32).tolist())
+        if len(inv) != HEAD_DIM // 2:
+            raise ValueError(f"inv_freq must have {HEAD_DIM // 2} entries")
+        return CodecConsts(K.gaussian_codebook(v_bits),
+                           tuple(K.sign_bits(K.hadamard_signs(HEAD_DIM, v_seed))),
+                           inv, float(rope_scaling))
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> ct.c_void_p:
+    return ct.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _need(cond: bool, msg: str):
+    if not cond:
+        raise ValueError(msg)
+
+
+def page_bytes(h_kv: int, rank: int) -> int:
+    return _lib.page_bytes(h_kv, rank)
+
+
+def append(k_pre: torch.Tensor, v: torch.Tensor, basis32: torch.Tensor, basis16: torch.Tensor,
+           pages: torch.Tensor, page_ids: torch.Tensor, consts: CodecConsts, *, rank: int,
+           us_first: torch.Tensor | None = None) -> None:
+    """Encode n codec pages (k_pre/v: (h_kv, 128n, 128) fp16 views, last dim
+    contiguous) into the 8n physical pages listed in page_ids (int32, device)."""
+    h_kv, T, d = k_pre.shape
+    _need(d == HEAD_DIM and T % CODEC_PAGE == 0, "k_pre must be (h_kv, 128*n, 128)")
+    _need(v.shape == k_pre.shape, "v must match k_pre")
+    _need(k_pre.dtype == torch.float16 and v.dtype == torch.float16, "k_pre/v must be fp16")
+    _need(k_pre.stride(2) == 1 and v.stride(2) == 1, "k_pre/v last dim must be contiguous")
+    n = T // CODEC_PAGE
+    C = h_kv * HEAD_DIM
+    _need(basis32.shape == (C, rank) and basis32.dtype == torch.float32 and basis32.is_contiguous(),
+          "basis32 must be contiguous fp32 (C, rank)")
+    _need(basis16.shape == (C, rank) and basis16.dtype == torch.float16 and basis16.is_contiguous(),
+          "basis16 must be contiguous fp16 (C, rank)")
+    _need(page_ids.dtype == torch.int32 and page_ids.numel() == 8 * n, "page_ids must be int32[8n]")
+    _need(pages.dtype == torch.uint8 and pages.dim() == 2 and pages.shape[1] == page_bytes(h_kv, rank)
+          and pages.is_contiguous(), "pages must be a contiguous uint8 (n_pages, page_bytes) pool")
+    if us_first is not None:
+        _need(us_first.shape == (CODEC_PAGE, rank) and us_first.dtype == torch.float32
+              and us_first.is_contiguous(), "us_first must be contiguous fp32 (128, rank)")
+    a = _lib.AppendArgs()
+    a.geom = _lib.Geom(h_kv, rank, 1)
+    a.n_codec_pages = n
+    a.k_pre, a.k_stride_h, a.k_stride_t = _ptr(k_pre), k_pre.stride(0), k_pre.stride(1)
+    a.v, a.v_stride_h, a.v_stride_t = _ptr(v), v.stride(0), v.stride(1)
+    a.basis32, a.basis16, a.us_first = _ptr(basis32), _ptr(basis16), _ptr(us_first)
+    a.codebook[:] = consts.codebook
+    a.v_sign_bits[:] = consts.sign_bits
+    a.pages, a.page_ids, a.n_pool_pages = _ptr(pages), _ptr(page_ids), pages.shape[0]
+    _lib.check(_lib.lib().bmx_k2b_append(ct.byref(a), _stream(pages.device)), "bmx_k2b_append")
+
+
+class DecodeWorkspace:
+    """Grow-only device scratch for split partials (reused across calls)."""
+
+    def __init__(self):
+        self.buf = None
+
+    def get(self, nbytes: int, device) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
+            self.buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        return self.buf
+
+
+_DEFAULT_WS: dict = {}
+
+
+def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor,
+           packed_len: torch.Tensor, max_packed_len: int, basis16: torch.Tensor,
+           consts: CodecConsts, sm_scale: float, *, rank: int,
+           k_tail: torch.Tensor | None = None, v_tail: torch.Tensor | None = None,
+           tail_len: torch.Tensor | None = None, tail_cap: int = 0,
+           out: torch.Tensor | None = None, split_tokens: int = 0,
+           workspace: DecodeWorkspace | None = None,
+           split_end_event: torch.cuda.Event | None = None, _capture=None) -> torch.Tensor:
+    """One decode step.  q (B, h_kv, G, 128) fp32 post-RoPE -> (B, h_kv, G, 128) fp32.
+
+    page_table (B, max_pages) int32; packed_len (B,) int32 committed tokens
+    (multiples of 128, <= max_packed_len); basis16 (B, C, rank) or (C, rank) fp16;
+    k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 post-RoPE recent window with
+    tail_len (B,) int32 valid rows."""
+    B, h_kv, G, d = q.shape
+    dev = q.device
+    _need(d == HEAD_DIM and q.dtype == torch.float32 and q.is_contiguous(),
+          "q must be contiguous fp32 (B, h_kv, G, 128)")
+    _need(pages.dtype == torch.uint8 and pages.shape[1] == page_bytes(h_kv, rank),
+          "pages must be (n_pages, page_bytes) uint8")
+    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B
+          and page_table.is_contiguous(), "page_table must be contiguous int32 (B, max_pages)")
+    _need(packed_len.dtype == torch.int32 and packed_len.numel() == B, "packed_len must be int32[B]")
+    C = h_kv * HEAD_DIM
+    if basis16.dim() == 2:
+        _need(basis16.shape == (C, rank), "basis16 must be (C, rank)")
+        bstride = 0
+    else:
+        _need(basis16.shape == (B, C, rank), "basis16 must be (B, C, rank)")
+        bstride = basis16.stride(0)
+    _need(basis16.dtype == torch.float16 and basis16.stride(-1) == 1 and basis16.stride(-2) == rank,
+          "basis16 rows must be contiguous fp16")
+    if out is None:
+        out = torch.empty_like(q)
+    if tail_len is None:
+        tail_len = torch.zeros(B, dtype=torch.int32, device=dev)
+    a = _lib.DecodeArgs()
+    a.geom = _lib.Geom(h_kv, rank, G)
+    a.batch = B
+    a.q, a.out = _ptr(q), _ptr(out)
+    a.pages, a.page_table, a.max_pages = _ptr(pages), _ptr(page_table), page_table.shape[1]
+    a.n_pool_pages = pages.shape[0]
+    _need(page_table.shape[1] * PAGE_TOKENS >= max_packed_len, "page_table too narrow for max_packed_len")
+    a.packed_len, a.max_packed_len = _ptr(packed_len), int(max_packed_len)
+    a.basis, a.basis_stride = _ptr(basis16), bstride
+    a.inv_freq[:] = consts.inv_freq
+    a.rope_scaling = consts.rope_scaling
+    a.sm_scale = float(sm_scale)
+    a.codebook[:] = consts.codebook
+    a.v_sign_bits[:] = consts.sign_bits
+    if tail_cap > 0:
+        _need(k_tail is not None and v_tail is not None and k_tail.shape == v_tail.shape
+              and k_tail.stride() == v_tail.stride(), "k_tail/v_tail must share shape and strides")
+        _need(k_tail.dtype == torch.float16 and k_tail.dim() == 4 and k_tail.shape[0] == B
+              and k_tail.shape[1] == h_kv and k_tail.shape[2] >= tail_cap and k_tail.stride(3) == 1,
+              "k_tail must be fp16 (B, h_kv, >=tail_cap, 128) with contiguous last dim")
+        a.k_tail, a.v_tail = _ptr(k_tail), _ptr(v_tail)
+        a.tail_stride_b, a.tail_stride_h, a.tail_stride_t = k_tail.stride(0), k_tail.stride(1), k_tail.stride(2)
+    a.tail_len, a.tail_cap = _ptr(tail_len), int(tail_cap)
+    a.split_tokens = int(split_tokens)
+    lib = _lib.lib()
+    need = int(lib.bmx_k2b_decode_workspace_bytes(ct.byref(a)))
+    ws = workspace if workspace is not None else _DEFAULT_WS.setdefault(dev, DecodeWorkspace())
+    buf = ws.get(need, dev)
+    a.workspace, a.workspace_bytes = buf.data_ptr(), buf.numel()
+    if split_end_event is not None:
+        a.split_end_event = split_end_event.cuda_event
+    if _capture is not None:
+        _capture(a)
+        return out
+    _lib.check(lib.bmx_k2b_decode(ct.byref(a), _stream(dev)), "bmx_k2b_decode")
+    return out
+
+
+class DecodePlan:
+    """A decode call with every argument bound once: ``run()`` is one C call.
+
+    Serving loops re-issue the same decode for a layer every step with only the
+    tensors' contents changing (q, the page table, lengths, the tail); binding
+    the pointers once removes the per-step host work (argument checks, struct
+    fill, workspace sizing).  The bound tensors must stay alive and must not be
+    reallocated while the plan is used."""
+
+    def __init__(self, q, pages, page_table, packed_len, max_packed_len, basis16, consts,
+                 sm_scale, *, rank, k_tail=None, v_tail=None, tail_len=None, tail_cap=0,
+                 out=None, split_tokens=0, workspace: DecodeWorkspace | None = None):
+        self.out = torch.empty_like(q) if out is None else out
+        self._keep = (q, pages, page_table, packed_len, basis16, k_tail, v_tail, tail_len)
+        if tail_len is None:
+            tail_len = torch.zeros(q.shape[0], dtype=torch.int32, device=q.device)
+            self._keep = self._keep + (tail_len,)
+        self.ws = workspace or DecodeWorkspace()
+        captured = {}
+
+        def capture(a):
+            captured["a"] = a
+        decode(q, pages, page_table, packed_len, max_packed_len, basis16, consts, sm_scale,
+               rank=rank, k_tail=k_tail, v_tail=v_tail, tail_len=tail_len, tail_cap=tail_cap,
+               out=self.out, split_tokens=split_tokens, workspace=self.ws, _capture=capture)
+        self.args = captured["a"]
+        self.stream = _stream(q.device)
+        self._fn = _lib.lib().bmx_k2b_decode
+
+    def run(self, split_end_event: torch.cuda.Event | None = None) -> torch.Tensor:
+        self.args.split_end_event = None if split_end_event is None else split_end_event.cuda_event
+        rc = self._fn(ct.byref(self.args), self.stream)
+        if rc != 0:
+            _lib.check(rc, "bmx_k2b_decode")
+        return self.out
+
+
+def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis16: torch.Tensor,
+            consts: CodecConsts, *, h_kv: int, rank: int, apply_rope: bool = False):
+    """Committed pages of one sequence -> dense fp32 (K (h_kv, n, 128), V (h_kv, n, 128))."""
+    dev = pages.device
+    k = torch.empty(h_kv, n_tokens, HEAD_DIM, dtype=torch.float32, device=dev)
+    v = torch.empty_like(k)
+    _need(page_table.dtype == torch.int32 and page_table.numel() >= n_tokens // PAGE_TOKENS,
+          "page_table must hold n_tokens/16 int32 page ids")
+    a = _lib.DequantArgs()
+    a.geom = _lib.Geom(h_kv, rank, 1)
+    a.pages, a.page_table, a.n_tokens = _ptr(pages), _ptr(page_table), int(n_tokens)
+    a.n_pool_pages = pages.shape[0]
+    a.basis = _ptr(basis16)
+    a.inv_freq[:] = consts.inv_freq
+    a.rope_scaling = consts.rope_scaling
+    a.apply_rope = int(bool(apply_rope))
+    a.codebook[:] = consts.codebook
+    a.v_sign_bits[:] = consts.sign_bits
+    a.k_out, a.v_out = _ptr(k), _ptr(v)
+    _lib.check(_lib.lib().bmx_k2b_dequant(ct.byref(a), _stream(dev)), "bmx_k2b_dequant")
+    return k, v

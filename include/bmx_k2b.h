@@ -1,0 +1,186 @@
+/*
+ * bmx_k2b.h — C-ABI of the MI355X (gfx950) packed-KV "k2b" decode path.
+ *
+ * Drop-in boundary for pherber3/bmx's packed k2b decode path.  Plain C, plain
+ * pointers and sizes; every pointer argument named "device" is HIP device
+ * memory.  Calls are asynchronous on the HIP stream passed in (NULL = default
+ * stream); they do not allocate.  Return value 0 = success, otherwise a
+ * BMX_E_* code, with a message from bmx_last_error().
+ *
+ * Packed page format (one layer, PT = 16 tokens, head_dim 128, C = 128*h_kv
+ * channels, rank R; sections in this order, little-endian):
+ *   US     [16][R]      fp16  low-rank key coefficients Us (per token)
+ *   VNORM  [h_kv][16]   fp16  value norm per (head, token)
+ *   KSCALE [C/4]        fp16  key-residual scales of the page's 64-token group:
+ *                             slot j = (logical page index mod 4) holds channels
+ *                             [j*C/4, (j+1)*C/4)
+ *   KRES   [h_kv][64][3] u32  3-bit two's-complement key residual; lane
+ *                             16q+n holds token n, channels 16b+4q+i (code k=4b+i
+ *                             at bits [3k,3k+3) of the 96-bit lane string)
+ *   VCODE  [h_kv][64][2] u32  2-bit Lloyd value codes; lane 16q+m, dword w holds
+ *                             channel 16b+m (b = 4w+bb) for token 4q+t at bit
+ *                             16*(t&1) + 4*bb + 2*(t>>1)
+ * Bytes per token = 2R + 86*h_kv  (752 at h_kv 8, R 32; 720 at R 16), i.e.
+ * exactly the k2b bits-per-entry: 3 (residual) + 16/64 (scales) + 2 (V codes)
+ * + 16*h_kv/C (norms) + 16R/C (Us).  The frozen basis V (C x R fp16) is stored
+ * once per sequence and layer, outside the pages.
+ *
+ * Codec geometry fixed by the reference recipe: codec page 128 tokens
+ * (packed_streaming.py:438), key-scale group 64 tokens (recipes.py:31-42),
+ * 3-bit keys / 2-bit values.
+ */
+#ifndef BMX_K2B_H
+#define BMX_K2B_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BMX_K2B_PAGE_TOKENS 16
+#define BMX_K2B_HEAD_DIM 128
+#define BMX_K2B_GROUP 64
+#define BMX_K2B_CODEC_PAGE 128
+
+#define BMX_OK 0
+#define BMX_E_INVALID 1     /* bad argument (shape, pointer, unsupported geometry) */
+#define BMX_E_WORKSPACE 2   /* workspace missing or too small */
+#define BMX_E_HIP 3         /* a HIP runtime call failed */
+
+enum bmx_k2b_section {
+  BMX_K2B_SEC_US = 0,
+  BMX_K2B_SEC_VNORM = 1,
+  BMX_K2B_SEC_KSCALE = 2,
+  BMX_K2B_SEC_KRES = 3,
+  BMX_K2B_SEC_VCODE = 4
+};
+
+typedef struct {
+  int32_t h_kv;        /* KV heads, 1..16 */
+  int32_t rank;        /* low-rank key rank R: 16 or 32 */
+  int32_t n_q_groups;  /* query heads per KV head G, 1..16 */
+} bmx_k2b_geom;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* bmx_last_error(void);
+
+/* Bytes of one 16-token page, and the (offset, size) of one section. */
+size_t bmx_k2b_page_bytes(const bmx_k2b_geom* geom);
+int bmx_k2b_page_section(const bmx_k2b_geom* geom, int section, size_t* offset,
+                         size_t* bytes);
+
+/* ------------------------------------------------------------------------
+ * Decode attention.  Replaces fused_decode_attention_k2b + _finalize_decode
+ * (cache/triton_dequant_attention.py:1232-1368, 504-575, 409-461) and the
+ * chunked_dequant_attention decode loop (cache/chunked_attention.py:478-530).
+ *
+ * For each sequence b: one query step (G query heads per KV head) attends to
+ * the packed_len[b] committed tokens held in pages (keys rebuilt as
+ * Us*V^T + residual*scale, RoPE applied at read with angle fl32(inv_freq*pos))
+ * and to the tail_len[b] fp16 recent-window tokens (post-RoPE keys), with one
+ * base-e softmax over their union.  Output = softmax(q.K^T * sm_scale) . V.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  bmx_k2b_geom geom;
+  int32_t batch;
+  const float* q;             /* device [batch][h_kv][G][128] fp32, post-RoPE */
+  float* out;                 /* device [batch][h_kv][G][128] fp32 */
+  const uint8_t* pages;       /* device page pool; page i at pages + i*page_bytes */
+  int32_t n_pool_pages;       /* pages in the pool; table entries are clamped into
+                                 [0, n_pool_pages) so a bad entry cannot fault */
+  const int32_t* page_table;  /* device [batch][max_pages] logical -> physical page */
+  int32_t max_pages;          /* row stride of page_table */
+  const int32_t* packed_len;  /* device [batch] committed tokens, multiple of 128;
+                                 clamped to max_packed_len on the device */
+  int32_t max_packed_len;     /* host upper bound of packed_len (sizes the grid) */
+  const uint16_t* basis;      /* device fp16 [C][R] frozen key basis of sequence 0 */
+  int64_t basis_stride;       /* elements between sequences' bases (0 = shared) */
+  float inv_freq[64];         /* RoPE inverse frequencies (HF inv_freq, fp32) */
+  float rope_scaling;         /* cos/sin multiplier (HF attention_scaling, 1.0) */
+  float sm_scale;             /* softmax scale (HF module.scaling) */
+  float codebook[4];          /* 2-bit Lloyd levels, ascending */
+  uint32_t v_sign_bits[4];    /* bit c set <=> V Hadamard sign of channel c is -1 */
+  const uint16_t* k_tail;     /* device fp16 post-RoPE recent-window keys */
+  const uint16_t* v_tail;     /* device fp16 recent-window values */
+  int64_t tail_stride_b;      /* element strides of k_tail/v_tail (dim 128 contiguous) */
+  int64_t tail_stride_h;
+  int64_t tail_stride_t;
+  const int32_t* tail_len;    /* device [batch] recent-window length (clamped to tail_cap) */
+  int32_t tail_cap;           /* host upper bound of tail_len, <= 1024 */
+  int32_t split_tokens;       /* tokens per split-KV work item; 0 = choose */
+  void* workspace;            /* device scratch for split partials */
+  size_t workspace_bytes;
+  void* split_end_event;      /* optional hipEvent_t recorded on the stream between
+                                 the split kernel and the combine kernel (timing) */
+} bmx_k2b_decode_args;
+
+size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* args);
+int bmx_k2b_decode(const bmx_k2b_decode_args* args, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Quantize-on-append (page commit).  Replaces the write path of
+ * PackedStreamingLayer.update (cache/packed_streaming.py:582-730):
+ * _pack_k_block -> quantize_packed("lowrank_rtn_channel") (codecs.py:786-796,
+ * 677-695; quant/rtn.py:23-44) and _pack_v_block -> quantize_packed(
+ * "turboquant_mse_perhead") (codecs.py:616-636, 734-745).
+ *
+ * Encodes n_codec_pages consecutive 128-token codec pages into 8 physical
+ * pages each.  Keys: Us = M * basis32 (or us_first for codec page 0 of a
+ * sequence, the SVD factor of the first page), Us16 = fp16(Us),
+ * R = M - Us16*basis16^T, per channel and 64-token group
+ * scale = max|R|/3, code = clamp(rint(R/scale), -4, 3).  Values per
+ * (token, head): n = fp16(||v||), x = fwht((v/n)*signs)*sqrt(128),
+ * code = #{midpoints < x}.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  bmx_k2b_geom geom;
+  int32_t n_codec_pages;
+  const uint16_t* k_pre;      /* device fp16 pre-RoPE keys: (h, t, j) at
+                                 h*k_stride_h + t*k_stride_t + j, t in [0, 128*n) */
+  int64_t k_stride_h;
+  int64_t k_stride_t;
+  const uint16_t* v;          /* device fp16 values, same indexing */
+  int64_t v_stride_h;
+  int64_t v_stride_t;
+  const float* basis32;       /* device fp32 [C][R] frozen basis (projection) */
+  const uint16_t* basis16;    /* device fp16 [C][R] (= fp16(basis32)) */
+  const float* us_first;      /* device fp32 [128][R] or NULL: Us of codec page 0 */
+  float codebook[4];
+  uint32_t v_sign_bits[4];
+  uint8_t* pages;             /* device page pool */
+  int32_t n_pool_pages;       /* pages in the pool (ids are clamped into range) */
+  const int32_t* page_ids;    /* device [n_codec_pages*8] physical page of each
+                                 16-token page, in token order */
+} bmx_k2b_append_args;
+
+int bmx_k2b_append(const bmx_k2b_append_args* args, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dequantize committed pages of one sequence to dense fp32 (prefill path and
+ * checks).  Replaces _dequant_block / _dense_kv (cache/chunked_attention.py:
+ * 52-194): keys are returned pre-RoPE unless apply_rope != 0.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  bmx_k2b_geom geom;
+  const uint8_t* pages;
+  int32_t n_pool_pages;       /* pages in the pool (ids are clamped into range) */
+  const int32_t* page_table;  /* device [n_tokens/16] logical -> physical page */
+  int32_t n_tokens;           /* multiple of 64 */
+  const uint16_t* basis;      /* device fp16 [C][R] */
+  float inv_freq[64];
+  float rope_scaling;
+  int32_t apply_rope;
+  float codebook[4];
+  uint32_t v_sign_bits[4];
+  float* k_out;               /* device fp32 [h_kv][n_tokens][128] */
+  float* v_out;               /* device fp32 [h_kv][n_tokens][128] */
+} bmx_k2b_dequant_args;
+
+int bmx_k2b_dequant(const bmx_k2b_dequant_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BMX_K2B_H */

@@ -16,9 +16,9 @@ rank R.  Sections in order (all little-endian):
   KRES   [h_kv][64 lanes][3 x u32]         3-bit two's-complement key residual
          lane = 16q + n (token n, quarter q); code k=4b+i (b<8, i<4) is channel
          16b + 4q + i of the head, at bits [3k, 3k+3) of the 96-bit lane string
-  VCODE  [h_kv][64 lanes][8 bytes]         2-bit value codes
-         lane = 16q + m; byte b holds channel 16b + m for tokens 4q + t (t<4)
-         at bits [2t, 2t+2)
+  VCODE  [h_kv][64 lanes][2 x u32]         2-bit value codes
+         lane = 16q + m; dword w holds channel 16b + m, b = 4w + bb (bb<4), for
+         token 4q + t (t<4) at bit 16*(t&1) + 4*bb + 2*(t>>1)
 """
 
 from __future__ import annotations
@@ -101,15 +101,16 @@ def pack_pages(us16, res, scale16, vidx, vnorm16, h_kv: int, rank: int) -> np.nd
         out[p, o:o + s] = kres.astype(np.uint32).reshape(-1).view(np.uint8)
         # VCODE
         o, s = sec["vcode"]
-        vc = np.zeros((h_kv, 4, 16, 8), dtype=np.uint8)
+        vc = np.zeros((h_kv, 4, 16, 2), dtype=np.uint64)
         for h in range(h_kv):
             for b in range(8):
-                # codes[t, m] for channel 16b+m, tokens t0..t0+15
-                cm = vidx[t0:t0 + PT, h * D + 16 * b + np.arange(16)]  # (16 tok, 16 m)
-                cm = cm.reshape(4, 4, 16)  # (q, t, m)
-                byte = (cm[:, 0] | (cm[:, 1] << 2) | (cm[:, 2] << 4) | (cm[:, 3] << 6))
-                vc[h, :, :, b] = byte.astype(np.uint8)
-        out[p, o:o + s] = vc.reshape(-1)
+                w, bb = b // 4, b % 4
+                # codes[q, t, m] of channel 16b+m, token t0 + 4q + t
+                cm = vidx[t0:t0 + PT, h * D + 16 * b + np.arange(16)].reshape(4, 4, 16)
+                for t in range(4):
+                    sh = 16 * (t & 1) + 4 * bb + 2 * (t >> 1)
+                    vc[h, :, :, w] |= cm[:, t, :].astype(np.uint64) << np.uint64(sh)
+        out[p, o:o + s] = vc.astype(np.uint32).reshape(-1).view(np.uint8)
     return out
 
 
@@ -149,11 +150,12 @@ def unpack_pages(pages: np.ndarray, h_kv: int, rank: int):
             for h in range(h_kv):
                 res[h * D + chan[:, k][:, None], t0 + np.arange(PT)[None, :]] = val[h]
         o, s = sec["vcode"]
-        vc = pages[p, o:o + s].reshape(h_kv, 4, 16, 8).astype(np.int64)
+        vc = pages[p, o:o + s].view(np.uint32).reshape(h_kv, 4, 16, 2).astype(np.int64)
         for h in range(h_kv):
             for b in range(8):
-                byte = vc[h, :, :, b]  # (q, m)
+                w, bb = b // 4, b % 4
                 for t in range(4):
+                    sh = 16 * (t & 1) + 4 * bb + 2 * (t >> 1)
                     vidx[t0 + 4 * np.arange(4)[:, None] + t,
-                         h * D + 16 * b + np.arange(16)[None, :]] = (byte >> (2 * t)) & 3
+                         h * D + 16 * b + np.arange(16)[None, :]] = (vc[h, :, :, w] >> sh) & 3
     return us16, res, scale16, vidx, vnorm16

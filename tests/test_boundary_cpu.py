@@ -1,0 +1,96 @@
+"""The C-ABI library loads, exports every symbol include/bmx_k2b.h declares,
+agrees with the numpy page format, and rejects bad arguments on the host — all
+without a GPU (no compute call is made)."""
+
+import ctypes as ct
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from bmx_amd import _lib, codecs as K
+from oracle import codecs as OC
+from oracle import layout as OL
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def test_library_exports_every_declared_symbol():
+    header = (ROOT / "include" / "bmx_k2b.h").read_text()
+    declared = set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(bmx_\w+)\s*\(", header, re.M))
+    assert declared == set(_lib.EXPORTS), declared ^ set(_lib.EXPORTS)
+    h = _lib.lib()
+    for name in declared:
+        assert getattr(h, name) is not None
+
+
+@pytest.mark.parametrize("h_kv,rank", [(8, 32), (8, 16), (2, 16), (1, 32), (16, 32)])
+def test_page_geometry_matches_numpy_layout(h_kv, rank):
+    assert _lib.page_bytes(h_kv, rank) == OL.page_bytes(h_kv, rank)
+    secs = _lib.page_sections(h_kv, rank)
+    ref = OL.sections(h_kv, rank)
+    for name in _lib.SECTIONS:
+        assert secs[name] == ref[name]
+    # bytes per token = 2R + 86 h_kv = exact k2b bits per entry
+    C = 128 * h_kv
+    bpt = OL.page_bytes(h_kv, rank) / 16
+    bits = bpt * 8 / C
+    assert bits == pytest.approx(3 + 16 / 64 + 2 + 16 * h_kv / C + 16 * rank / C)
+
+
+def test_headline_bytes_per_token():
+    assert OL.page_bytes(8, 32) == 16 * 752
+    assert OL.page_bytes(8, 16) == 16 * 720
+
+
+def test_bad_geometry_is_rejected_with_message():
+    with pytest.raises(RuntimeError, match="unsupported geometry"):
+        _lib.page_bytes(8, 24)
+    a = _lib.DecodeArgs()
+    a.geom = _lib.Geom(8, 32, 32)  # G too large
+    a.batch = 1
+    rc = _lib.lib().bmx_k2b_decode(ct.byref(a), None)
+    assert rc != 0 and b"n_q_groups" in _lib.lib().bmx_last_error()
+    a.geom = _lib.Geom(8, 32, 4)
+    a.max_packed_len = 100  # not a multiple of 128
+    rc = _lib.lib().bmx_k2b_decode(ct.byref(a), None)
+    assert rc != 0 and b"multiple of 128" in _lib.lib().bmx_last_error()
+    ap = _lib.AppendArgs()
+    ap.geom = _lib.Geom(8, 7, 1)
+    assert _lib.lib().bmx_k2b_append(ct.byref(ap), None) != 0
+    ap.geom = _lib.Geom(8, 32, 1)
+    ap.n_codec_pages = 2
+    rc = _lib.lib().bmx_k2b_append(ct.byref(ap), None)
+    assert rc != 0 and b"null pointer" in _lib.lib().bmx_last_error()
+
+
+def test_decode_workspace_size_formula():
+    a = _lib.DecodeArgs()
+    a.geom = _lib.Geom(8, 32, 4)
+    a.batch = 2
+    a.max_packed_len = 65536
+    a.split_tokens = 1024
+    n = _lib.lib().bmx_k2b_decode_workspace_bytes(ct.byref(a))
+    assert n == 2 * 64 * 8 * 4 * 130 * 4
+
+
+def test_product_codec_constants_match_reference():
+    g = np.load(ROOT / "tests" / "golden" / "codecs.npz")
+    assert np.array_equal(np.array(K.gaussian_codebook(2), dtype=np.float32), g["codebook_b2"])
+    assert np.array_equal(np.array(K.hadamard_signs(128, 0)), g["signs_d128_s0"])
+    bits = K.sign_bits(K.hadamard_signs(128, 7))
+    signs = [(-1 if (bits[c >> 5] >> (c & 31)) & 1 else 1) for c in range(128)]
+    assert signs == g["signs_d128_s7"].tolist()
+    assert K.compute_flush_schedule(300, 32, 128) == OC.compute_flush_schedule(300, 32, 128) == 256
+
+
+def test_product_inv_freq_matches_hf_config():
+    from transformers import LlamaConfig
+
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8,
+                      rope_theta=500000.0)
+    inv, scale = K.rope_inv_freq(cfg)
+    inv0, scale0 = K.rope_inv_freq(head_dim=128, theta=500000.0)
+    assert torch.equal(inv, inv0) and scale == scale0 == 1.0
