@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void k2b_us_kernel(const AppendKArgs a) {
       }
       us = acc;
     }
-    *reinterpret_cast<uint16_t*>(page + a.L.us + (tl * a.R + r) * 2) = float_to_half_bits(us);
+    *reinterpret_cast<uint16_t*>(page + a.L.us + us_half(a.R, tl, r) * 2) = float_to_half_bits(us);
   }
 }
 
@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256) void k2b_kres_kernel(const AppendKArgs a) {
     const int t = e / R, r = e % R;
     const int pslot = cp * 8 + grp_in * 4 + t / kPT;
     const uint8_t* page = a.pages + clamp_page(a.page_ids[pslot], a.n_pool) * a.L.bytes;
-    s_us[t][r] = half_bits_to_float(*reinterpret_cast<const uint16_t*>(page + a.L.us + ((t % kPT) * R + r) * 2));
+    s_us[t][r] = half_bits_to_float(*reinterpret_cast<const uint16_t*>(page + a.L.us + us_half(R, t % kPT, r) * 2));
   }
   for (int e = tid; e < kD * R; e += 256) {
     const int j = e / R, r = e % R;
@@ -105,24 +105,28 @@ __global__ __launch_bounds__(256) void k2b_kres_kernel(const AppendKArgs a) {
     s_code[half * 32 + tt][j] = (int8_t)cq;
   }
   if (half == 0) {
-    const int c = h * kD + j, quarter = C / 4;
-    const int slot = c / quarter, off = c % quarter;
+    const int f = kscale_flat(h * kD + j), quarter = C / 4;
+    const int slot = f / quarter, off = f % quarter;
     uint8_t* page = a.pages + clamp_page(a.page_ids[cp * 8 + grp_in * 4 + slot], a.n_pool) * a.L.bytes;
     *reinterpret_cast<uint16_t*>(page + a.L.kscale + off * 2) = float_to_half_bits(scale);
   }
   __syncthreads();
-  // pack: thread -> (page pl, lane 16q+n)
+  // pack: thread -> (page pl, lane 16q+n); pair p = 4b+i is channels (j, j+64),
+  // j = 16b + 4q + i, stored offset-binary
   {
     const int pl = tid >> 6, lane = tid & 63, q = lane >> 4, n = lane & 15;
     const int t = pl * kPT + n;
     uint32_t w[3] = {0u, 0u, 0u};
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-      const int jj = 16 * (k >> 2) + 4 * q + (k & 3);
-      const uint32_t v = (uint32_t)(s_code[t][jj]) & 7u;
-      const int bit = 3 * k;
-      w[bit >> 5] |= v << (bit & 31);
-      if ((bit & 31) > 29) w[(bit >> 5) + 1] |= v >> (32 - (bit & 31));
+    for (int p = 0; p < 16; ++p) {
+      const int jj = 16 * (p >> 2) + 4 * q + (p & 3);
+      const uint32_t lo = (uint32_t)(s_code[t][jj] + 4), hi = (uint32_t)(s_code[t][jj + 64] + 4);
+      if (p < 15) {
+        w[p / 5] |= (lo << (3 * (p % 5))) | (hi << (16 + 3 * (p % 5)));
+      } else {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) w[k] |= (((lo >> k) & 1u) << 15) | (((hi >> k) & 1u) << 31);
+      }
     }
     uint8_t* page = a.pages + clamp_page(a.page_ids[cp * 8 + grp_in * 4 + pl], a.n_pool) * a.L.bytes;
     uint32_t* dst = reinterpret_cast<uint32_t*>(page + a.L.kres + h * 768 + lane * 12);
@@ -194,13 +198,12 @@ __global__ __launch_bounds__(256) void k2b_v_kernel(const AppendKArgs a) {
     code[t][c] = (uint8_t)((r > mid0) + (r > mid1) + (r > mid2));
   }
   __syncthreads();
-  if (tid < 128) {
+  if (tid < 128) {  // lane 16q+m, dword w: channel 16b + m (b = 4w + bb), token 4q + t at bit 8bb + 2t
     const int lane = tid >> 1, w = tid & 1, q = lane >> 4, m = lane & 15;
     uint32_t dword = 0;
     for (int bb = 0; bb < 4; ++bb) {
       const int c = 16 * (4 * w + bb) + m;
-      for (int t = 0; t < 4; ++t)
-        dword |= (uint32_t)code[4 * q + t][c] << (16 * (t & 1) + 4 * bb + 2 * (t >> 1));
+      for (int t = 0; t < 4; ++t) dword |= (uint32_t)code[4 * q + t][c] << (8 * bb + 2 * t);
     }
     *reinterpret_cast<uint32_t*>(page + a.L.vcode + h * 512 + lane * 8 + w * 4) = dword;
   }

@@ -65,23 +65,32 @@ __device__ __forceinline__ bool sign_neg(const uint32_t bits[4], int c) {
   return (bits[c >> 5] >> (c & 31)) & 1u;
 }
 
-// 3-bit two's-complement residual code k (0..31) of a 96-bit lane string.
-__device__ __forceinline__ int kres_code(uint32_t w0, uint32_t w1, uint32_t w2, int k) {
-  const int bit = 3 * k;
-  uint32_t word;
-  int sh;
-  if (bit + 3 <= 32) {
-    word = w0; sh = bit;
-  } else if (bit < 32) {
-    word = __builtin_amdgcn_alignbit(w1, w0, 30); sh = 0;   // bits 30..61
-  } else if (bit + 3 <= 64) {
-    word = w1; sh = bit - 32;
-  } else if (bit < 64) {
-    word = __builtin_amdgcn_alignbit(w2, w1, 31); sh = 0;   // bits 63..94
+// US: half index of (token t, rank r); lane 16q+n of an MFMA reads R/4 halfs
+// Us[n][(R/4)q ..] contiguously.
+__host__ __device__ __forceinline__ int us_half(int R, int t, int r) {
+  const int kpl = R / 4;
+  return ((r / kpl) * kPT + t) * kpl + r % kpl;
+}
+
+// KSCALE: position of channel c (0..C-1) in the group's pair-ordered scale
+// array F (F[128h + 2j + e] = scale of channel 128h + j + 64e).
+__host__ __device__ __forceinline__ int kscale_flat(int c) {
+  const int j = c & (kD - 1);
+  return (c - j) + 2 * (j & 63) + (j >> 6);
+}
+
+// KRES: signed residual code of pair p (0..15), half e (0: channel j, 1: j+64)
+// from the lane's three dwords (offset-binary 3-bit codes).
+__device__ __forceinline__ int kres_pair_code(uint32_t w0, uint32_t w1, uint32_t w2, int p, int e) {
+  uint32_t v;
+  if (p < 15) {
+    const uint32_t w = p < 5 ? w0 : (p < 10 ? w1 : w2);
+    v = (w >> (3 * (p % 5) + 16 * e)) & 7u;
   } else {
-    word = w2; sh = bit - 64;
+    const int sh = 15 + 16 * e;
+    v = ((w0 >> sh) & 1u) | (((w1 >> sh) & 1u) << 1) | (((w2 >> sh) & 1u) << 2);
   }
-  return ((int)(word << (29 - sh))) >> 29;
+  return (int)v - 4;
 }
 
 }  // namespace bmx

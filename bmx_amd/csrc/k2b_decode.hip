@@ -1,27 +1,41 @@
 // Split-KV decode attention over packed k2b pages, gfx950.
 //
-// Work decomposition.  One workgroup of 8 waves per (split, sequence); wave w
-// owns KV head w for the whole split, and all waves walk the same 64-token
-// groups (4 pages, one key-scale group):
-//   * the group's pages are copied HBM -> LDS with direct-to-LDS loads
-//     (global_load_lds_dwordx4), one group ahead of the compute, so the HBM
-//     stream is deep without holding prefetch data in VGPRs;
+// Two launches per call.
+//
+// k2b_decode_split_kernel: one workgroup of 8 waves per (split, sequence); wave
+// w owns KV head w, and all waves walk the same 64-token groups (4 pages, one
+// key-scale group) of the split's balanced share of the packed tokens:
+//   * each wave streams its head's slice of every page (3-bit key residual and
+//     2-bit value codes, 20 bytes per lane per page, 83% of the page bytes)
+//     straight into VGPRs: all loads of the next group are issued at the top
+//     of a group and first waited on at its end;
+//   * the page prefix every head reads (Us, value norms, key scales) is loaded
+//     cooperatively one group ahead and staged in a two-slot LDS ring;
 //   * the RoPE cos/sin of the group's 64 positions is produced once per
-//     workgroup (angle-addition recurrence from an exact start, corrected to
-//     HF's fp32 angle fl(inv_freq * pos)) and shared by all heads through LDS;
+//     workgroup, one group ahead (angle-addition recurrence from an exact start,
+//     corrected to HF's fp32 angle fl(inv_freq * pos)), as fp16 pairs in LDS
+//     shared by all heads;
 //   * per page and head the wave rebuilds K^T (128 ch x 16 tok) on MFMA
-//     (8 x mfma_16x16x32(V_h tile, Us^T)), adds the 3-bit residual * scale and
-//     applies RoPE in registers (lane 16q+n owns token n, channels 16b+4q+i, so
-//     the RoPE pair (j, j+64) is lane-local), scores the G query heads on MFMA
-//     (the score layout, lane 16q+g: tokens 4q..4q+3 of query g, is exactly the
-//     B operand of P.V), runs a base-2 online softmax with the accumulator
-//     rescaled only when a running max grows, and accumulates P*norm against
-//     the codebook levels on MFMA, i.e. V stays in the Hadamard-rotated domain.
-// One extra workgroup per sequence attends the fp16 recent window with the same
-// MFMA shapes and maps its accumulator into the rotated domain (signs, then the
-// unnormalised Hadamard), so every partial merges the same way.  The combine
-// kernel merges the partials, applies the one inverse Hadamard per (head,
-// query), the signs and the normalisation.
+//     (8 x mfma(V_h tile, Us^T)); lane 16q+n then holds token n, channels
+//     j = 16b+4q+i and j+64 (b, i < 4), i.e. 16 RoPE pairs, which it converts to
+//     packed fp16, adds residual*scale with one packed FMA per pair (3-bit codes
+//     turned into fp16 integers by a mantissa/exponent trick, no per-code
+//     convert), rotates with two packed ops per pair, and scores the G query
+//     heads on MFMA;
+//   * the 4 pages' score tiles (G useful columns of 16 each) are compacted into
+//     one register set with DPP row shifts, so the online softmax runs once per
+//     group on fully used lanes; the accumulator is rescaled only when a
+//     running max grows;
+//   * P*norm is accumulated against the codebook levels on MFMA (V stays in
+//     the Hadamard-rotated domain); each level is an exact fp16 head+remainder
+//     pair, looked up four codes (one code byte, one MFMA operand) at a time in
+//     a 256-entry LDS table.
+//
+// k2b_combine_kernel: one workgroup per (query, head, sequence) attends the
+// fp16 recent window in fp32 (post-RoPE keys), merges the packed partials
+// (base-2 LSE), applies the one inverse Hadamard, the signs and the
+// normalisation, and joins the two; all of its first-round loads are issued
+// before any reduction.
 //
 // Reference semantics: cache/triton_dequant_attention.py:863-1115 (kernel),
 // 409-461 (merge), 324-360 (tail), 504-575 (finalize);
@@ -34,77 +48,114 @@ namespace bmx {
 constexpr int kWaves = 8;                   // waves per workgroup; wave w = head w
 constexpr int kThreads = 64 * kWaves;
 constexpr int kGroupPages = kGroup / kPT;   // 4 pages per 64-token group
-constexpr int kCsBytes = kGroupPages * 8 * 64 * 16;  // cos/sin of one group, lane order
+constexpr int kCsRow = 68;                  // dwords per position row of the cos/sin table
+                                            // (64 + 4: rows start 4 banks apart)
+constexpr int kCsBuf = kGroup * kCsRow;     // dwords per group table
+constexpr int kPidWindow = 64;              // page ids held per lane-vector
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 struct DecodeKArgs {
-  int h_kv, G, split_tokens, max_splits, max_pages, max_packed_len, n_pool, tail_cap;
+  int h_kv, G, max_splits, max_pages, max_packed_len, n_pool;
+  int shared_bytes;    // page prefix read by every head: US, VNORM, KSCALE (multiple of 16)
   const float* q;
-  float* ws_acc;   // [B][max_splits + 1][h_kv][G][128]; row max_splits = recent window
-  float* ws_ml;    // [B][max_splits + 1][h_kv][G][2]
+  float* ws_acc;       // [B][max_splits][h_kv][G][128] rotated-domain accumulators
+  float* ws_ml;        // [B][max_splits][h_kv][G][2]   (running max, sum), base 2
   const uint8_t* pages;
   const int32_t* page_table;
   const int32_t* packed_len;
   const uint16_t* basis;
   int64_t basis_stride;
-  const uint16_t* k_tail;
-  const uint16_t* v_tail;
-  int64_t ts_b, ts_h, ts_t;
-  const int32_t* tail_len;
   PageLayout L;
-  float qscale;        // sm_scale * log2(e)
-  float rope_scaling;
+  float qscale_rope;   // sm_scale * log2(e) * rope_scaling (the cos/sin table is unscaled)
   float inv_freq[64];
   float step_c[64];    // cos / sin of 64 * inv_freq_j (exact angle), the per-group step
   float step_s[64];
   float step8_c[64];   // cos / sin of 8 * inv_freq_j, between a thread's positions
   float step8_s[64];
   float codebook[4];
-  uint32_t v_sign_bits[4];
 };
 
-// s_waitcnt vmcnt(0) without waiting on LDS / export counters (gfx9 encoding).
-__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+// v_mov_b32_dpp: lanes enabled by BANK (4-lane banks of each 16-lane row) take
+// src from the DPP-selected lane, the others keep old.
+template <int CTRL, int BANK = 0xF>
+__device__ __forceinline__ float dpp(float old, float src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, src), CTRL, 0xF,
+                                                               BANK, false));
+}
+constexpr int kRowShr = 0x110;  // + n: lane i of a row reads lane i - n
+constexpr int kRowRor = 0x120;  // + n: rotate within the row
+
+// x from the DPP-selected lane, every lane written (foldable into a DPP ALU op).
+template <int CTRL>
+__device__ __forceinline__ float dpp_all(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
-// Query fragments (B operand of the scores): chunk kk covers channels
-// {32kk + 4q + i, 32kk + 16 + 4q + i}; column n is query n (zero when n >= G).
-__device__ __forceinline__ void load_query(const DecodeKArgs& a, int b, int h, int n, int q,
-                                           half8_t qf[4]) {
+// Query fragments of the packed pages: chunk bb holds the RoPE pairs
+// B[8q + 2i + e][n] = q_n[16bb + 4q + i + 64e] (i < 4, e < 2), the order in
+// which the key pairs leave the rotation; column n is query n (zero if n >= G).
+__device__ __forceinline__ void load_query_pairs(const DecodeKArgs& a, int b, int h, int n, int q,
+                                                 half8_t qf[4]) {
   const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
-  const float sc = (n < a.G) ? a.qscale : 0.0f;
+  const float sc = (n < a.G) ? a.qscale_rope : 0.0f;
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
+  for (int bb = 0; bb < 4; ++bb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      qf[kk][i] = (_Float16)(qrow[32 * kk + 4 * q + i] * sc);
-      qf[kk][4 + i] = (_Float16)(qrow[32 * kk + 16 + 4 * q + i] * sc);
+      qf[bb][2 * i] = (_Float16)(qrow[16 * bb + 4 * q + i] * sc);
+      qf[bb][2 * i + 1] = (_Float16)(qrow[16 * bb + 4 * q + i + 64] * sc);
     }
-  }
 }
 
-// Base-2 online softmax over the 4 scores of this lane (tokens 4q..4q+3 of
-// query g); lanes of one query share the running max.  The common case (no
-// score above the running max) costs a lane-local max and a wave vote; only
-// when some max grows do the lanes exchange maxima and rescale.
-__device__ __forceinline__ void softmax_step(const float4_t& s, float& m_run, float& l_run,
-                                             float4_t acc[8], float p[4]) {
-  float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  if (__any(mx > m_run)) {
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    l_run *= alpha;
-#pragma unroll
-    for (int bt = 0; bt < 8; ++bt) acc[bt] *= alpha;
-    m_run = m_new;
+// The masks arrive in VGPRs (KresMasks) so each half pair is one v_and_or_b32.
+struct KresMasks {
+  uint32_t m0, m1, m2;   // code bits of slots 0, 3, 6 (both halves)
+  uint32_t e0, e1, e2;   // exponent fields 25, 22, 19 (both halves)
+  __device__ __forceinline__ void init() {
+    m0 = 0x00070007u; m1 = 0x00380038u; m2 = 0x01C001C0u;
+    e0 = 0x64006400u; e1 = 0x58005800u; e2 = 0x4C004C00u;
+    // opaque to the optimiser: keeps them in registers, out of literal operands
+    asm volatile("" : "+v"(m0), "+v"(m1), "+v"(m2));
+    asm volatile("" : "+s"(e0), "+s"(e1), "+s"(e2));
   }
+};
+
+// The lane's 16 key-residual pairs (channels j, j+64) as exact fp16 integers.
+// An offset-binary 3-bit code c' at mantissa bits [s, s+3) under exponent field
+// 25 - s reads as 2^(10-s) + c'; one AND-OR builds two such halves and one
+// packed add removes 2^(10-s) + 4, leaving code = c' - 4.
+__device__ __forceinline__ void kres_pairs(const KresMasks& km, uint32_t w0, uint32_t w1, uint32_t w2,
+                                           half2_t c[16]) {
+  const half2_t b0 = {(_Float16)-1028.0f, (_Float16)-1028.0f};
+  const half2_t b1 = {(_Float16)-132.0f, (_Float16)-132.0f};
+  const half2_t b2 = {(_Float16)-20.0f, (_Float16)-20.0f};
+  const uint32_t w[3] = {w0, w1, w2};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(s[i] - m_run);
-  l_run += (p[0] + p[1]) + (p[2] + p[3]);
+  for (int d = 0; d < 3; ++d) {
+    const uint32_t x = w[d], y = x >> 9;
+    c[5 * d + 0] = as_h2((x & km.m0) | km.e0) + b0;
+    c[5 * d + 1] = as_h2((x & km.m1) | km.e1) + b1;
+    c[5 * d + 2] = as_h2((x & km.m2) | km.e2) + b2;
+    c[5 * d + 3] = as_h2((y & km.m0) | km.e0) + b0;
+    c[5 * d + 4] = as_h2((y & km.m1) | km.e1) + b1;
+  }
+  c[15] = as_h2(((w0 >> 15) & 0x00010001u) | ((w1 >> 14) & 0x00020002u) |
+                ((w2 >> 13) & 0x00040004u) | km.e0) + b0;
+}
+
+// RoPE of one packed pair (k_j, k_{j+64}) by the packed (cos, sin):
+// (k_j c - k_{j+64} s, k_{j+64} c + k_j s) in two packed ops.
+__device__ __forceinline__ half2_t rope2(half2_t p, uint32_t csu) {
+  const half2_t cs = as_h2(csu);
+  const half2_t cc = {cs[0], cs[0]};
+  const half2_t sn = {-cs[1], cs[1]};
+  const half2_t sw = {p[1], p[0]};
+  return __builtin_elementwise_fma(sw, sn, p * cc);
 }
 
 // Partial (acc, m, l) of this lane's query into the workspace row.
@@ -114,7 +165,7 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
   if (n < a.G) {
-    const int64_t row = (((int64_t)b * (a.max_splits + 1) + split) * a.h_kv + h) * a.G + n;
+    const int64_t row = (((int64_t)b * a.max_splits + split) * a.h_kv + h) * a.G + n;
     float* dst = a.ws_acc + row * kD;
 #pragma unroll
     for (int bt = 0; bt < 8; ++bt) *reinterpret_cast<float4_t*>(dst + 16 * bt + 4 * q) = acc[bt];
@@ -122,160 +173,127 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
   }
 }
 
-// ---------------------------------------------------------------------------
-// fp16 recent window (post-RoPE keys, plain values) of one sequence: wave =
-// head; each wave double-buffers its own 16-token K and V tiles (row-major
-// 16 x 256 B) in a private LDS slice with direct-to-LDS loads, so the loop
-// needs no workgroup barrier.  Rows past the window re-read the last valid row
-// and are masked out of the softmax.
-// ---------------------------------------------------------------------------
-constexpr int kTailSlice = 2 * 2 * kPT * kD * 2;  // 2 buffers x (K, V) tiles, bytes per wave
-
-__device__ void tail_partial(const DecodeKArgs& a, uint8_t* smem, int b) {
-  const int tid = threadIdx.x, h = tid >> 6, lane = tid & 63;
-  const int n = lane & 15, q = lane >> 4;
-  const int T = min(max(a.tail_len[b], 0), a.tail_cap);
-  if (T == 0 || h >= a.h_kv) return;
-  uint8_t* slice = smem + h * kTailSlice;
-  const uint16_t* kt = a.k_tail + b * a.ts_b + h * a.ts_h;
-  const uint16_t* vt = a.v_tail + b * a.ts_b + h * a.ts_h;
-  // one wave instruction moves 4 rows (64 lanes x 16 B)
-  auto issue_chunk = [&](int t0, int buf) {
-    uint8_t* kdst = slice + buf * (2 * kPT * kD * 2);
-    uint8_t* vdst = kdst + kPT * kD * 2;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = min(t0 + 4 * r + (lane >> 4), T - 1);
-      const int64_t off = (int64_t)row * a.ts_t + (lane & 15) * 8;
-      lds_dma16(kt + off, kdst + r * 1024);
-      lds_dma16(vt + off, vdst + r * 1024);
-    }
-  };
-  half8_t qf[4];
-  load_query(a, b, h, n, q, qf);
-  float4_t acc[8];
-#pragma unroll
-  for (int bt = 0; bt < 8; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-  issue_chunk(0, 0);
-  for (int t0 = 0, buf = 0; t0 < T; t0 += kPT, buf ^= 1) {
-    wait_vmem_all();
-    __builtin_amdgcn_wave_barrier();
-    if (t0 + kPT < T) issue_chunk(t0 + kPT, buf ^ 1);
-    const uint16_t* kst = reinterpret_cast<const uint16_t*>(slice + buf * (2 * kPT * kD * 2));
-    const uint16_t* vst = kst + kPT * kD;
-    float4_t s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      union { uint2 u[2]; half8_t v; } ka;
-      ka.u[0] = *reinterpret_cast<const uint2*>(kst + n * kD + 32 * kk + 4 * q);
-      ka.u[1] = *reinterpret_cast<const uint2*>(kst + n * kD + 32 * kk + 16 + 4 * q);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, qf[kk], s, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (t0 + 4 * q + i >= T) s[i] = -INFINITY;
-    float p[4];
-    softmax_step(s, m_run, l_run, acc, p);
-    half4_t pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
-#pragma unroll
-    for (int bt = 0; bt < 8; ++bt) {
-      union { uint16_t u[4]; half4_t v; } va;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) va.u[i] = vst[(4 * q + i) * kD + 16 * bt + n];
-      acc[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va.v, pb, acc[bt], 0, 0, 0);
-    }
-    // every lane's reads of this buffer precede the next overwrite of it
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
-  }
-  // into the rotated domain: x = H (signs * acc), H the unnormalised Sylvester
-  // Hadamard, channel c = 16bt + 4q + i (bits: i -> 0,1; q -> 2,3; bt -> 4,5,6)
-#pragma unroll
-  for (int bt = 0; bt < 8; ++bt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (sign_neg(a.v_sign_bits, 16 * bt + 4 * q + i)) acc[bt][i] = -acc[bt][i];
-#pragma unroll
-  for (int bt = 0; bt < 8; ++bt) {
-    const float4_t x = acc[bt];
-    const float y0 = x[0] + x[1], y1 = x[0] - x[1], y2 = x[2] + x[3], y3 = x[2] - x[3];
-    acc[bt] = float4_t{y0 + y2, y1 + y3, y0 - y2, y1 - y3};
-  }
-#pragma unroll
-  for (int hb = 16; hb <= 32; hb <<= 1) {
-#pragma unroll
-    for (int bt = 0; bt < 8; ++bt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float o = __shfl_xor(acc[bt][i], hb);
-        acc[bt][i] = (lane & hb) ? (o - acc[bt][i]) : (acc[bt][i] + o);
-      }
-  }
-#pragma unroll
-  for (int sb = 1; sb < 8; sb <<= 1)
-#pragma unroll
-    for (int bt = 0; bt < 8; ++bt)
-      if (!(bt & sb)) {
-        const float4_t u = acc[bt], w = acc[bt | sb];
-        acc[bt] = u + w;
-        acc[bt | sb] = u - w;
-      }
-  store_partial(a, b, a.max_splits, h, n, q, acc, m_run, l_run);
-}
-
-template <int R>
+// R: key rank (16 or 32).  SW: query slot width (G rounded up to 4, 8 or 16);
+// the 16 score columns of a page hold 16/SW pages after compaction.
+template <int R, int SW>
 __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const DecodeKArgs a) {
+  constexpr int NSLOT = 16 / SW;             // pages per compacted score register
+  constexpr int NCR = kGroupPages / NSLOT;   // compacted registers per group
+  constexpr int KQ = R / 4;                  // rank elements per lane in the K^T MFMA
+  typedef _Float16 hvec_t __attribute__((ext_vector_type(KQ)));
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  // codebook levels of 4 codes (one VCODE byte) as exact fp16 head + remainder
+  // pairs: s_vlut[v] = {hr(c0), hr(c1), hr(c2), hr(c3)}, c_t = (v >> 2t) & 3 --
+  // the whole A operand of one P.V tile, read with one ds_read_b128 (static LDS:
+  // the byte index scales straight into the address)
+  __shared__ uint4 s_vlut[256];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int n = lane & 15;   // token within page (K side) / query column (score side)
+  const int n = lane & 15;   // token within page (K side) / score column (softmax side)
   const int q = lane >> 4;   // quarter
   const int split = blockIdx.x, b = blockIdx.y;
-  // Balanced static partition of the sequence's work units over the max_splits
-  // workgroups: units [0, NG) are 64-token packed groups, [NG, NG + TU) the fp16
-  // recent window (64 tokens per unit), owned by the last workgroup.
-  const int len = min(a.packed_len[b], a.max_packed_len) & ~(kGroup - 1);
-  const int NG = len / kGroup;
-  const int T = min(max(a.tail_len[b], 0), a.tail_cap);
-  const int TU = (T + kGroup - 1) / kGroup;
-  const int U = NG + TU;
-  const int S = a.max_splits;
-  const int g0 = min((int)(((int64_t)split * U) / S), NG);
-  const int g1 = min((int)(((int64_t)(split + 1) * U) / S), NG);
-  const bool own_tail = (split == S - 1) && TU > 0;
-  const int n_groups = g1 - g0;
-  const int t_begin = g0 * kGroup;
-  const int C = kD * a.h_kv;
-  const int pb = a.L.bytes;
-  uint8_t* ring = smem;                                      // [2][4 pages]
-  float4_t* cs = reinterpret_cast<float4_t*>(smem + 2 * kGroupPages * pb);
-  const int32_t* ptab = a.page_table + (int64_t)b * a.max_pages + t_begin / kPT;
   const bool active = wave < a.h_kv;
   const int h = active ? wave : 0;
-  if (n_groups == 0) {  // uniform: nothing packed here; an empty partial keeps the merge blind
+
+  // ---- loads that depend on nothing: basis fragments, query ----
+  hvec_t vh[8];
+  const uint16_t* basis = a.basis + (int64_t)b * a.basis_stride;
+#pragma unroll
+  for (int bt = 0; bt < 8; ++bt)
+    vh[bt] = *reinterpret_cast<const hvec_t*>(basis + (int64_t)(h * kD + 16 * bt + n) * R + KQ * q);
+  half8_t qf[4];
+  load_query_pairs(a, b, h, n, q, qf);
+
+  // Balanced static partition of the sequence's 64-token groups over the
+  // max_splits workgroups.  The page-table read is issued for the host bound
+  // max_packed_len before the device length arrives, and redone in the rare
+  // case that the sequence is shorter.
+  const int S = a.max_splits;
+  const int len_spec = a.max_packed_len & ~(kGroup - 1);
+  auto range = [&](int L, int& r0, int& r1) {
+    const int NG = L / kGroup;
+    r0 = (int)(((int64_t)split * NG) / S);
+    r1 = (int)(((int64_t)(split + 1) * NG) / S);
+  };
+  int g0, g1;
+  range(len_spec, g0, g1);
+  const int32_t* ptab_row = a.page_table + (int64_t)b * a.max_pages;
+  auto load_ids = [&](int first, int count) {   // ids of pages first .. first+63 of the range
+    if (count <= 0) return 0;                    // uniform: an empty range reads nothing
+    return (int)clamp_page(ptab_row[g0 * kGroupPages + min(first + lane, count - 1)], a.n_pool);
+  };
+  int pidv = load_ids(0, (g1 - g0) * kGroupPages);
+  const int len = min(a.packed_len[b], a.max_packed_len) & ~(kGroup - 1);
+  if (len != len_spec) {
+    range(len, g0, g1);
+    pidv = load_ids(0, (g1 - g0) * kGroupPages);
+  }
+  const int n_groups = g1 - g0;
+  if (n_groups == 0) {  // nothing packed here; an empty partial keeps the merge blind
     if (active) {
       float4_t zero[8];
 #pragma unroll
       for (int bt = 0; bt < 8; ++bt) zero[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
       store_partial(a, b, split, h, n, q, zero, -INFINITY, 0.f);
     }
-    if (own_tail) tail_partial(a, smem, b);
     return;
   }
+  const int t_begin = g0 * kGroup;
+  const int C = kD * a.h_kv;
+  const int quarter = C / 4;
+  const int pb = a.L.bytes;
+  const int SHB = a.shared_bytes;
+  const int sh_chunks = SHB / 4;       // 16-byte chunks of the 4 pages' prefixes
+  const int chunks_pp = SHB / 16;
+  // dynamic LDS: the two cos/sin tables, then the prefix ring
+  uint32_t* cst = reinterpret_cast<uint32_t*>(smem);                            // [2][64][kCsRow]
+  uint8_t* ring = smem + 2 * kCsBuf * 4;                                        // [2][4][SHB]
+  const int n_pages = n_groups * kGroupPages;
 
-  // ---- group copy HBM -> LDS (1 KB per wave instruction) ----
-  const int chunks_pp = (pb + 1023) >> 10;
-  auto issue_group = [&](int gi, int slot) {
-    uint8_t* dst0 = ring + slot * kGroupPages * pb;
-    for (int c = wave; c < kGroupPages * chunks_pp; c += kWaves) {
-      const int pp = c / chunks_pp, off = (c - pp * chunks_pp) << 10;
-      const int64_t pid = clamp_page(ptab[gi * kGroupPages + pp], a.n_pool);
-      if (off + lane * 16 < pb)
-        lds_dma16(a.pages + pid * pb + off + lane * 16, dst0 + pp * pb + off);
-    }
+  // page ids of the range, a window of 64 per lane-vector
+  int pid_base = 0;
+  auto page_ptr = [&](int gi, int pp) -> const uint8_t* {   // uniform (gi, pp)
+    const int id = __builtin_amdgcn_readlane(pidv, gi * kGroupPages + pp - pid_base);
+    return a.pages + (int64_t)id * pb;
   };
-  issue_group(0, 0);
+  auto load_prefix = [&](int gi) -> uint4 {                   // thread tid's 16 B of the prefixes
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    const int pp = min(tid / chunks_pp, kGroupPages - 1);
+    const int id = __shfl(pidv, gi * kGroupPages + pp - pid_base);
+    if (tid < sh_chunks)
+      v = *reinterpret_cast<const uint4*>(a.pages + (int64_t)id * pb + (tid - pp * chunks_pp) * 16);
+    return v;
+  };
+  auto store_prefix = [&](uint4 v, int slot) {
+    if (tid < sh_chunks) *reinterpret_cast<uint4*>(ring + slot * kGroupPages * SHB + tid * 16) = v;
+  };
+  // uniform page base + 32-bit lane offset: the scalar-base load form
+  const uint32_t kres_off = (uint32_t)(a.L.kres + h * 768 + lane * 12);
+  const uint32_t vcode_off = (uint32_t)(a.L.vcode + h * 512 + lane * 8);
+  auto load_kres = [&](int gi, int pp) -> uint3 {
+    return *reinterpret_cast<const uint3*>(page_ptr(gi, pp) + kres_off);
+  };
+  auto load_vcode = [&](int gi, int pp) -> uint2 {
+    return *reinterpret_cast<const uint2*>(page_ptr(gi, pp) + vcode_off);
+  };
+
+  // ---- first group in flight ----
+  uint4 pre = load_prefix(0);
+  uint3 kres[kGroupPages];   // this group's codes (the next group's are fetched
+  uint2 vcd[kGroupPages];    // into separate registers at the top of the group)
+#pragma unroll
+  for (int pp = 0; pp < kGroupPages; ++pp) {
+    kres[pp] = load_kres(0, pp);
+    vcd[pp] = load_vcode(0, pp);
+  }
+
+  if (tid < 256) {
+    auto hr = [&](int c) {
+      const _Float16 hd = (_Float16)a.codebook[c];
+      return half_bits(hd) | (half_bits((_Float16)(a.codebook[c] - (float)hd)) << 16);
+    };
+    s_vlut[tid] = make_uint4(hr(tid & 3), hr((tid >> 2) & 3), hr((tid >> 4) & 3), hr(tid >> 6));
+  }
 
   // ---- cos/sin recurrence state: this thread owns frequency j = tid & 63 at
   // group-local positions tl = wave + 8k, k < 8 ----
@@ -283,10 +301,13 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const float fq = a.inv_freq[fj];
   float cc[8], ss[8];
   {
-    double sd, cd;  // one exact-angle start per thread, then 8-position steps
-    sincos((double)fq * (double)(t_begin + wave), &sd, &cd);
-    cc[0] = (float)cd;
-    ss[0] = (float)sd;
+    // one exact-angle start per thread, then 8-position steps: the angle in
+    // revolutions (exact product, scaled in double), its fraction, and the
+    // hardware sin/cos of revolutions
+    const double rev = (double)fq * (double)(t_begin + wave) * 0.15915494309189535;
+    const float fr = (float)(rev - floor(rev));
+    cc[0] = __builtin_amdgcn_cosf(fr);
+    ss[0] = __builtin_amdgcn_sinf(fr);
     const float c8 = a.step8_c[fj], s8 = a.step8_s[fj];
 #pragma unroll
     for (int k = 1; k < 8; ++k) {
@@ -295,240 +316,238 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     }
   }
   const float stc = a.step_c[fj], sts = a.step_s[fj];
-
-  // ---- per-wave constants ----
-  constexpr int KQ = R / 4;
-  typedef _Float16 hvec_t __attribute__((ext_vector_type(KQ)));
-  hvec_t vh[8];
-  const uint16_t* basis = a.basis + (int64_t)b * a.basis_stride;
-#pragma unroll
-  for (int bt = 0; bt < 8; ++bt)
-    vh[bt] = *reinterpret_cast<const hvec_t*>(basis + (int64_t)(h * kD + 16 * bt + n) * R + KQ * q);
-  half8_t qf[4];
-  load_query(a, b, h, n, q, qf);
-  uint32_t cbh[2], cbl[2];
-#pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    const _Float16 h0 = (_Float16)a.codebook[2 * w], h1 = (_Float16)a.codebook[2 * w + 1];
-    cbh[w] = half_bits(h0) | (half_bits(h1) << 16);
-    cbl[w] = half_bits((_Float16)(a.codebook[2 * w] - (float)h0)) |
-             (half_bits((_Float16)(a.codebook[2 * w + 1] - (float)h1)) << 16);
-  }
-  float4_t acc[8];
-#pragma unroll
-  for (int bt = 0; bt < 8; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.0f;
-
-  for (int gi = 0; gi < n_groups; ++gi) {
-    wait_vmem_all();   // this wave's copies of group gi have landed
-    __syncthreads();   // ... and every wave's; slot (gi+1)&1 and cs are free again
-    if (gi + 1 < n_groups) issue_group(gi + 1, (gi + 1) & 1);
-
-    // cos/sin of fl32(inv_freq * pos) for the group's 64 positions
+  // fp16 (cos, sin) of HF's angle fl(fq * pos) for the group's 64 positions,
+  // row = position, column = frequency; then step the state by 64 positions
+  auto produce_cs = [&](int gi, int buf) {
+    uint32_t* dst = cst + buf * kCsBuf;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int tl = wave + 8 * k;
       const float tf = (float)(t_begin + gi * kGroup + tl);
       const float ang = fq * tf;
-      const float e = __builtin_fmaf(fq, tf, -ang);          // exact: fq*tf - ang
-      const float e2 = 0.5f * e * e;
-      const float c_hf = __builtin_fmaf(ss[k], e, __builtin_fmaf(-cc[k], e2, cc[k]));
-      const float s_hf = __builtin_fmaf(-cc[k], e, __builtin_fmaf(-ss[k], e2, ss[k]));
-      // lane-order slot: page p, lane 16*qq + nn, read r = 2*bt + (i >> 1), half i & 1
-      const int p = tl >> 4, nn = tl & 15;
-      const int bt = fj >> 4, qq = (fj >> 2) & 3, i = fj & 3;
-      float2* dst = reinterpret_cast<float2*>(cs + (p * 8 + 2 * bt + (i >> 1)) * 64 + 16 * qq + nn);
-      dst[i & 1] = make_float2(c_hf * a.rope_scaling, s_hf * a.rope_scaling);
+      const float e = __builtin_fmaf(fq, tf, -ang);  // exact: fq*tf - fl(fq*tf)
+      const half2_t v = {(_Float16)__builtin_fmaf(ss[k], e, cc[k]),
+                         (_Float16)__builtin_fmaf(-cc[k], e, ss[k])};
+      dst[tl * kCsRow + fj] = as_u32(v);
       const float cn = cc[k] * stc - ss[k] * sts;
       ss[k] = ss[k] * stc + cc[k] * sts;
       cc[k] = cn;
     }
-    __syncthreads();
-    if (!active) continue;
+  };
+  produce_cs(0, 0);
+  store_prefix(pre, 0);
 
-    const uint8_t* grp = ring + (gi & 1) * kGroupPages * pb;
-    // key-residual scales of the group: 8 runs of 4 channels from the pages' KSCALE
-    _Float16 sc[32];
-    {
-      const int quarter = C / 4;
+  // ---- per-wave state ----
+  float4_t acc[8];
 #pragma unroll
-      for (int bt = 0; bt < 8; ++bt) {
-        const int c0 = h * kD + 16 * bt + 4 * q;
-        const int slot = c0 / quarter, off = c0 - slot * quarter;
-        const uint2 raw = *reinterpret_cast<const uint2*>(grp + slot * pb + a.L.kscale + 2 * off);
-        const uint16_t r4[4] = {(uint16_t)(raw.x & 0xffff), (uint16_t)(raw.x >> 16),
-                                (uint16_t)(raw.y & 0xffff), (uint16_t)(raw.y >> 16)};
+  for (int bt = 0; bt < 8; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  const int my_slot = NSLOT > 1 ? n / SW : 0;   // page slot of this lane after compaction
+  KresMasks km;
+  km.init();
+  __syncthreads();   // LUT, table 0 and prefix slot 0 are visible
+
+  for (int gi = 0; gi < n_groups; ++gi) {
+    const int gn = min(gi + 1, n_groups - 1);   // group fetched during this one
+    if ((gn + 1) * kGroupPages - pid_base > kPidWindow) {   // slide the page-id window
+      pid_base = gi * kGroupPages;
+      pidv = load_ids(pid_base, n_pages);
+    }
+    // every load of group gn is issued here, a whole group before its first use
+    const uint4 pre_n = load_prefix(gn);
+    uint3 kres_n[kGroupPages];
+    uint2 vcd_n[kGroupPages];
+    if (active) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) __builtin_memcpy(&sc[4 * bt + i], &r4[i], 2);
+      for (int pp = 0; pp < kGroupPages; ++pp) {
+        kres_n[pp] = load_kres(gn, pp);
+        vcd_n[pp] = load_vcode(gn, pp);
       }
     }
-    for (int pp = 0; pp < kGroupPages; ++pp) {
-      const uint8_t* page = grp + pp * pb;
-      // ---- K^T tile on MFMA ----
-      const hvec_t us = *reinterpret_cast<const hvec_t*>(page + a.L.us + n * (2 * R) + q * (2 * KQ));
-      float4_t kt[8];
+    if (gi + 1 < n_groups) produce_cs(gi + 1, (gi + 1) & 1);
+
+    if (active) {
+      const uint8_t* grp = ring + (gi & 1) * kGroupPages * SHB;
+      const uint32_t* csb = cst + (gi & 1) * kCsBuf;
+      // key-residual scale pairs (s_j, s_{j+64}), j = 16bb + 4q + i: 16 bytes
+      // per bb in the group's prefix (re-read per page: fewer live VGPRs)
+      const uint8_t* scl[4];
 #pragma unroll
-      for (int bt = 0; bt < 8; ++bt) {
-        const float4_t z = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (R == 32)
-          kt[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[bt], us, z, 0, 0, 0);
-        else
-          kt[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh[bt], us, z, 0, 0, 0);
+      for (int bb = 0; bb < 4; ++bb) {
+        const int f = h * kD + 2 * (16 * bb + 4 * q);
+        const int slot = f / quarter, off = f - slot * quarter;
+        scl[bb] = grp + slot * SHB + a.L.kscale + 2 * off;
       }
-      // ---- residual ----
-      {
-        const uint32_t* kr = reinterpret_cast<const uint32_t*>(page + a.L.kres + h * 768 + lane * 12);
-        const uint32_t w0 = kr[0], w1 = kr[1], w2 = kr[2];
+      // ---- K side: scores of the 4 pages ----
+      float4_t sc[kGroupPages];
 #pragma unroll
-        for (int k = 0; k < 32; ++k)
-          kt[k >> 2][k & 3] = __builtin_fmaf((float)sc[k], (float)kres_code(w0, w1, w2, k), kt[k >> 2][k & 3]);
+      for (int pp = 0; pp < kGroupPages; ++pp) {
+        const uint8_t* pre_p = grp + pp * SHB;
+        const hvec_t us = *reinterpret_cast<const hvec_t*>(pre_p + a.L.us + lane * (2 * KQ));
+        float4_t kt[8];
+#pragma unroll
+        for (int bt = 0; bt < 8; ++bt) {
+          const float4_t z = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (R == 32)
+            kt[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[bt], us, z, 0, 0, 0);
+          else
+            kt[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh[bt], us, z, 0, 0, 0);
+        }
+        half2_t cp[16];
+        kres_pairs(km, kres[pp].x, kres[pp].y, kres[pp].z, cp);
+        float4_t s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+          const uint4 c4 = *reinterpret_cast<const uint4*>(csb + (pp * kPT + n) * kCsRow + 16 * bb + 4 * q);
+          const uint4 s4 = *reinterpret_cast<const uint4*>(scl[bb]);
+          const uint32_t cv[4] = {c4.x, c4.y, c4.z, c4.w};
+          const uint32_t sv[4] = {s4.x, s4.y, s4.z, s4.w};
+          union { half2_t h2[4]; half8_t v; } ka;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            half2_t pr = {(_Float16)kt[bb][i], (_Float16)kt[bb + 4][i]};
+            pr = __builtin_elementwise_fma(cp[4 * bb + i], as_h2(sv[i]), pr);
+            ka.h2[i] = rope2(pr, cv[i]);
+          }
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, qf[bb], s, 0, 0, 0);
+        }
+        sc[pp] = s;
+        __builtin_amdgcn_sched_barrier(0);   // bound the cross-page overlap (VGPR budget)
       }
-      // ---- RoPE at read: channel j pairs with j+64 (tile bt with bt+4) ----
+      // ---- compaction: page r*NSLOT + s moves to columns [s*SW, (s+1)*SW) ----
+      float4_t cr[NCR];
 #pragma unroll
-      for (int bt = 0; bt < 4; ++bt) {
-        const float4_t c01 = cs[(pp * 8 + 2 * bt) * 64 + lane];
-        const float4_t c23 = cs[(pp * 8 + 2 * bt + 1) * 64 + lane];
-        const float cosv[4] = {c01[0], c01[2], c23[0], c23[2]};
-        const float sinv[4] = {c01[1], c01[3], c23[1], c23[3]};
+      for (int r = 0; r < NCR; ++r) {
+        cr[r] = sc[r * NSLOT];
+        if constexpr (NSLOT == 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float k1 = kt[bt][i], k2 = kt[bt + 4][i];
-          kt[bt][i] = k1 * cosv[i] - k2 * sinv[i];
-          kt[bt + 4][i] = k2 * cosv[i] + k1 * sinv[i];
+          for (int i = 0; i < 4; ++i) {
+            cr[r][i] = dpp<kRowShr + 4, 0x2>(cr[r][i], sc[r * NSLOT + 1][i]);
+            cr[r][i] = dpp<kRowShr + 8, 0x4>(cr[r][i], sc[r * NSLOT + 2][i]);
+            cr[r][i] = dpp<kRowShr + 12, 0x8>(cr[r][i], sc[r * NSLOT + 3][i]);
+          }
+        } else if constexpr (NSLOT == 2) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) cr[r][i] = dpp<kRowShr + 8, 0xC>(cr[r][i], sc[r * NSLOT + 1][i]);
         }
       }
-      // ---- scores on MFMA: S[token][query] ----
-      float4_t s = {0.f, 0.f, 0.f, 0.f};
+      // ---- online softmax over the group (one running max per query) ----
+      float mx = -INFINITY;
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        half8_t ka;
+      for (int r = 0; r < NCR; ++r)
+        mx = fmaxf(mx, fmaxf(fmaxf(cr[r][0], cr[r][1]), fmaxf(cr[r][2], cr[r][3])));
+      if (__any(mx > m_run)) {
+        if constexpr (NSLOT == 4) mx = fmaxf(mx, dpp_all<kRowRor + 4>(mx));
+        if constexpr (NSLOT >= 2) mx = fmaxf(mx, dpp_all<kRowRor + 8>(mx));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int bt = 0; bt < 8; ++bt) acc[bt] *= alpha;
+        m_run = m_new;
+      }
+      // ---- P*norm as the B operand (tokens 4q..4q+3, each twice: head, remainder) ----
+      half8_t pd[NCR];
+#pragma unroll
+      for (int r = 0; r < NCR; ++r) {
+        const int pg = r * NSLOT + my_slot;
+        const uint2 nr = *reinterpret_cast<const uint2*>(grp + pg * SHB + a.L.vnorm + h * 32 + q * 8);
+        const float nv[4] = {half_bits_to_float(nr.x & 0xffff), half_bits_to_float(nr.x >> 16),
+                             half_bits_to_float(nr.y & 0xffff), half_bits_to_float(nr.y >> 16)};
+        union { half2_t h2[4]; half8_t v; } pu;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          ka[i] = (_Float16)kt[2 * kk][i];
-          ka[4 + i] = (_Float16)kt[2 * kk + 1][i];
+          const float p = __builtin_amdgcn_exp2f(cr[r][i] - m_run);
+          l_run += p;
+          const float x = p * nv[i];
+          pu.h2[i] = half2_t{(_Float16)x, (_Float16)x};
         }
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[kk], s, 0, 0, 0);
+        pd[r] = pu.v;
       }
-      float p[4];
-      softmax_step(s, m_run, l_run, acc, p);
-      // ---- P*norm (B operand: tokens 4q..4q+3 of query g, twice) ----
-      const uint2 nr = *reinterpret_cast<const uint2*>(page + a.L.vnorm + h * 32 + q * 8);
-      half8_t pb8;
-      pb8[0] = (_Float16)(p[0] * half_bits_to_float(nr.x & 0xffff));
-      pb8[1] = (_Float16)(p[1] * half_bits_to_float(nr.x >> 16));
-      pb8[2] = (_Float16)(p[2] * half_bits_to_float(nr.y & 0xffff));
-      pb8[3] = (_Float16)(p[3] * half_bits_to_float(nr.y >> 16));
-      pb8[4] = pb8[0]; pb8[5] = pb8[1]; pb8[6] = pb8[2]; pb8[7] = pb8[3];
-      // ---- V codes -> codebook head/remainder (A operand), rotated-domain P.V:
-      // K index 8q+i pairs level-head(token 4q+i), 8q+4+i level-remainder ----
-      const uint2 vc = *reinterpret_cast<const uint2*>(page + a.L.vcode + h * 512 + lane * 8);
+      // ---- P.V on MFMA, per page (B masked to the page's slot) ----
 #pragma unroll
-      for (int bt = 0; bt < 8; ++bt) {
-        const uint32_t D = bt < 4 ? vc.x : vc.y;
-        const int bb = bt & 3;
-        const uint32_t s01 = ((D >> (4 * bb)) & 0x00030003u) * 0x202u + 0x01000100u;
-        const uint32_t s23 = ((D >> (4 * bb + 2)) & 0x00030003u) * 0x202u + 0x01000100u;
-        union { uint32_t u[4]; half8_t v; } va;
-        va.u[0] = __builtin_amdgcn_perm(cbh[1], cbh[0], s01);
-        va.u[1] = __builtin_amdgcn_perm(cbh[1], cbh[0], s23);
-        va.u[2] = __builtin_amdgcn_perm(cbl[1], cbl[0], s01);
-        va.u[3] = __builtin_amdgcn_perm(cbl[1], cbl[0], s23);
-        acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va.v, pb8, acc[bt], 0, 0, 0);
+      for (int pp = 0; pp < kGroupPages; ++pp) {
+        half8_t bp = pd[pp / NSLOT];
+        if constexpr (NSLOT > 1) {
+          if (my_slot != pp % NSLOT) bp = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        const uint2 vc = vcd[pp];
+        union { uint4 e; half8_t v; } va[8];
+#pragma unroll
+        for (int bt = 0; bt < 8; ++bt) {
+          const uint32_t D = bt < 4 ? vc.x : vc.y;
+          va[bt].e = s_vlut[(D >> (8 * (bt & 3))) & 0xFFu];
+        }
+#pragma unroll
+        for (int bt = 0; bt < 8; ++bt)
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[bt].v, bp, acc[bt], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    if (gi + 1 < n_groups) store_prefix(pre_n, (gi + 1) & 1);   // slot last read by group gi-1
+    if (active) {
+#pragma unroll
+      for (int pp = 0; pp < kGroupPages; ++pp) {
+        kres[pp] = kres_n[pp];
+        vcd[pp] = vcd_n[pp];
+      }
+    }
+    __syncthreads();   // table and prefix of group gi+1 visible; group gi's slots free
   }
-  if (active) store_partial(a, b, split, h, n, q, acc, m_run, l_run);
-  if (own_tail) {
-    __syncthreads();  // the tail stages its tiles in the LDS the groups used
-    tail_partial(a, smem, b);
+  if (active) {
+    // fold the page slots: column s*SW + g -> g
+    if constexpr (NSLOT == 4) {
+#pragma unroll
+      for (int bt = 0; bt < 8; ++bt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[bt][i] += dpp_all<kRowRor + 4>(acc[bt][i]);
+      l_run += dpp_all<kRowRor + 4>(l_run);
+    }
+    if constexpr (NSLOT >= 2) {
+#pragma unroll
+      for (int bt = 0; bt < 8; ++bt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[bt][i] += dpp_all<kRowRor + 8>(acc[bt][i]);
+      l_run += dpp_all<kRowRor + 8>(l_run);
+    }
+    store_partial(a, b, split, h, n, q, acc, m_run, l_run);
   }
 }
 
+// ---------------------------------------------------------------------------
+// Combine: recent window + merge of the packed partials.  One workgroup per
+// (query, head, sequence); every load of the first partial block and the first
+// window block is issued before any reduction, so the kernel pays one memory
+// round trip, not one per phase.
+// ---------------------------------------------------------------------------
+constexpr int kCmbThreads = 512;
+constexpr int kCmbWaves = kCmbThreads / 64;
+constexpr int kCmbStrides = kCmbThreads / 32;   // partial strides per channel quad
+constexpr int kCmbBatch = 16;                   // partials per thread per block
+constexpr int kCmbBlock = kCmbStrides * kCmbBatch;   // 256 partials per block
+constexpr int kWinBlock = kCmbThreads / 4;      // window tokens per block (4 threads each)
+
 struct CombineKArgs {
   int h_kv, G, max_splits, tail_cap;
+  float qscale;        // sm_scale * log2(e) (window keys are already rotated and scaled)
   float* out;
+  const float* q;
   const float* ws_acc;
   const float* ws_ml;
+  const uint16_t* k_tail;
+  const uint16_t* v_tail;
+  int64_t ts_b, ts_h, ts_t;
   const int32_t* tail_len;
   uint32_t v_sign_bits[4];
 };
 
-constexpr int kCombineThreads = 512;
-constexpr int kCombineStrides = kCombineThreads / 32;  // partial strides per channel quad
-
-// One workgroup per (query, head, sequence).  Thread (channel quad cq, stride
-// ps) sums partials ps, ps + 16, ... of its quad with every load issued before
-// the first use; the 16 stride sums meet in LDS; one wave applies the inverse
-// Hadamard, the signs and the normalisation.
-__global__ __launch_bounds__(kCombineThreads) void k2b_combine_kernel(const CombineKArgs a) {
-  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const bool has_tail = min(max(a.tail_len[b], 0), a.tail_cap) > 0;
-  const int n_parts = a.max_splits + (has_tail ? 1 : 0);  // tail partial sits at index max_splits
-  const int64_t row0 = ((int64_t)b * (a.max_splits + 1) * a.h_kv + h) * a.G + g;
-  const int64_t rstride = (int64_t)a.h_kv * a.G;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  float* s_w = reinterpret_cast<float*>(smem);               // [max_splits + 1]
-  float4_t* s_x = reinterpret_cast<float4_t*>(s_w + ((a.max_splits + 4) & ~3));  // [16][32]
-  float* s_red = reinterpret_cast<float*>(s_x + kCombineStrides * 32);  // [16]
-  // (1) running max, weights, denominator (threads over partials)
-  float mx = -INFINITY;
-  for (int i = tid; i < n_parts; i += kCombineThreads) mx = fmaxf(mx, a.ws_ml[(row0 + i * rstride) * 2]);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if (lane == 0) s_red[wave] = mx;
-  __syncthreads();
-  float m_star = s_red[0];
-#pragma unroll
-  for (int w = 1; w < kCombineThreads / 64; ++w) m_star = fmaxf(m_star, s_red[w]);
-  float lsum = 0.f;
-  for (int i = tid; i < n_parts; i += kCombineThreads) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + (row0 + i * rstride) * 2);
-    const float w = __builtin_amdgcn_exp2f(ml.x - m_star);
-    s_w[i] = w;
-    lsum += ml.y * w;
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) lsum += __shfl_xor(lsum, o);
-  __syncthreads();
-  if (lane == 0) s_red[8 + wave] = lsum;
-  __syncthreads();
-  // (2) weighted sum of the rotated accumulators
-  {
-    const int cq = tid & 31, ps = tid >> 5;
-    const float* base = a.ws_acc + row0 * kD + 4 * cq;
-    float4_t x = {0.f, 0.f, 0.f, 0.f};
-    constexpr int kBatch = 16;
-    for (int i0 = ps; i0 < n_parts; i0 += kBatch * kCombineStrides) {
-      float4_t v[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int i = i0 + u * kCombineStrides;
-        v[u] = i < n_parts ? *reinterpret_cast<const float4_t*>(base + (int64_t)i * rstride * kD)
-                           : float4_t{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int i = i0 + u * kCombineStrides;
-        if (i < n_parts) x += v[u] * s_w[i];
-      }
-    }
-    s_x[ps * 32 + cq] = x;
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  // lane holds channels 2*lane, 2*lane + 1
-  float x0 = 0.f, x1 = 0.f;
-#pragma unroll
-  for (int ps = 0; ps < kCombineStrides; ++ps) {
-    const float4_t v = s_x[ps * 32 + (lane >> 1)];
-    x0 += (lane & 1) ? v[2] : v[0];
-    x1 += (lane & 1) ? v[3] : v[1];
-  }
-  {
-    const float y0 = x0 + x1, y1 = x0 - x1;
-    x0 = y0; x1 = y1;
-  }
+// 128-point unnormalised Hadamard in one wave: lane holds channels 2l, 2l+1.
+__device__ __forceinline__ void wave_fwht128(float& x0, float& x1, int lane) {
+  const float y0 = x0 + x1, y1 = x0 - x1;
+  x0 = y0;
+  x1 = y1;
 #pragma unroll
   for (int hb = 1; hb < 64; hb <<= 1) {
     const float p0 = __shfl_xor(x0, hb), p1 = __shfl_xor(x1, hb);
@@ -536,15 +555,184 @@ __global__ __launch_bounds__(kCombineThreads) void k2b_combine_kernel(const Comb
     x0 = upper ? (p0 - x0) : (x0 + p0);
     x1 = upper ? (p1 - x1) : (x1 + p1);
   }
-  float l_tot = 0.f;
+}
+
+__global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineKArgs a) {
+  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int S = a.max_splits;
+  const int T = min(max(a.tail_len[b], 0), a.tail_cap);
+  const int64_t row0 = ((int64_t)b * S * a.h_kv + h) * a.G + g;   // partial i at row0 + i*rstride
+  const int64_t rstride = (int64_t)a.h_kv * a.G;
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  __shared__ float s_red[2 * kCmbWaves];
+  __shared__ float s_w[kCmbBlock];
+  __shared__ float s_p[kWinBlock];
+  __shared__ float4_t s_x[kCmbThreads];
+  __shared__ f2_t s_v[kCmbThreads];
+
+  // thread roles: partial (channel quad cq, stride ps); window score (token
+  // tk, channel quarter kq); window value (channel pair cp, token part)
+  const int cq = tid & 31, ps = tid >> 5;
+  const int tk = tid >> 2, kq = tid & 3;
+  const int cp = tid & 63, part = tid >> 6;
+  const uint16_t* kb = a.k_tail + b * a.ts_b + h * a.ts_h;
+  const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h;
+  const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + g) * kD + 32 * kq;
+
+  float4_t v[kCmbBatch];
+  f2_t ml = {-INFINITY, 0.f};   // raw (max, sum) of partial ib + tid; masked where used
+  uint4 kv[4];
+  uint32_t vv[kWinBlock / kCmbWaves];
+  auto load_block = [&](int k) {   // partial block k and window block k, no waits
+    const int ib = k * kCmbBlock, t0 = k * kWinBlock;
+    if (ib < S) {
+      const int i = ib + (tid & (kCmbBlock - 1));
+      ml = *reinterpret_cast<const f2_t*>(a.ws_ml + (row0 + (int64_t)min(i, S - 1) * rstride) * 2);
 #pragma unroll
-  for (int w = 0; w < kCombineThreads / 64; ++w) l_tot += s_red[8 + w];
-  const float scale = 1.0f / ((float)kD * l_tot);
+      for (int u = 0; u < kCmbBatch; ++u) {
+        const int iu = min(ib + ps + kCmbStrides * u, S - 1);
+        v[u] = *reinterpret_cast<const float4_t*>(a.ws_acc + (row0 + (int64_t)iu * rstride) * kD + 4 * cq);
+      }
+    }
+    if (t0 < T) {
+      const int t = min(t0 + tk, T - 1);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        kv[u] = *reinterpret_cast<const uint4*>(kb + (int64_t)t * a.ts_t + 32 * kq + 8 * u);
+#pragma unroll
+      for (int k2 = 0; k2 < kWinBlock / kCmbWaves; ++k2) {
+        const int tv = min(t0 + part + kCmbWaves * k2, T - 1);
+        vv[k2] = *reinterpret_cast<const uint32_t*>(vb + (int64_t)tv * a.ts_t + 2 * cp);
+      }
+    }
+  };
+  load_block(0);
+  float4_t qf[8];
+  if (T > 0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) qf[u] = *reinterpret_cast<const float4_t*>(qrow + 4 * u);
+  }
+
+  float4_t xp = {0.f, 0.f, 0.f, 0.f};
+  f2_t vacc = {0.f, 0.f};
+  float mp = -INFINITY, mt = -INFINITY, lp = 0.f, lt = 0.f;   // lp, lt: this thread's share
+  const int n_blk = max((S + kCmbBlock - 1) / kCmbBlock, (T + kWinBlock - 1) / kWinBlock);
+  for (int k = 0; k < n_blk; ++k) {   // uniform trip count
+    if (k != 0) load_block(k);
+    const int ib = k * kCmbBlock, t0 = k * kWinBlock;
+    const bool own_p = tid < kCmbBlock && ib + tid < S;
+    const bool own_t = t0 + tk < T;
+    const float mi = own_p ? ml[0] : -INFINITY;
+    float s = -INFINITY;
+    if (t0 < T) {
+      float d = 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t w[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
+        const float4_t q0 = qf[2 * u], q1 = qf[2 * u + 1];
+        d = __builtin_fmaf(half_bits_to_float(w[0] & 0xffff), q0[0], d);
+        d = __builtin_fmaf(half_bits_to_float(w[0] >> 16), q0[1], d);
+        d = __builtin_fmaf(half_bits_to_float(w[1] & 0xffff), q0[2], d);
+        d = __builtin_fmaf(half_bits_to_float(w[1] >> 16), q0[3], d);
+        d = __builtin_fmaf(half_bits_to_float(w[2] & 0xffff), q1[0], d);
+        d = __builtin_fmaf(half_bits_to_float(w[2] >> 16), q1[1], d);
+        d = __builtin_fmaf(half_bits_to_float(w[3] & 0xffff), q1[2], d);
+        d = __builtin_fmaf(half_bits_to_float(w[3] >> 16), q1[3], d);
+      }
+      d += __shfl_xor(d, 1);
+      d += __shfl_xor(d, 2);
+      s = own_t ? d * a.qscale : -INFINITY;
+    }
+    // one joint block max of (partial max, window score)
+    float r0 = mi, r1 = s;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      r0 = fmaxf(r0, __shfl_xor(r0, o));
+      r1 = fmaxf(r1, __shfl_xor(r1, o));
+    }
+    if (lane == 0) {
+      s_red[2 * wave] = r0;
+      s_red[2 * wave + 1] = r1;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kCmbWaves; ++w) {
+      r0 = fmaxf(r0, s_red[2 * w]);
+      r1 = fmaxf(r1, s_red[2 * w + 1]);
+    }
+    const float mp_new = fmaxf(mp, r0), mt_new = fmaxf(mt, r1);
+    const float ap = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mp_new);
+    const float at = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - mt_new);
+    const float wi = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - mp_new);
+    const float pt = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mt_new);
+    if (tid < kCmbBlock) s_w[tid] = wi;
+    if (kq == 0) s_p[tk] = pt;
+    lp = lp * ap + (own_p ? ml[1] * wi : 0.f);
+    lt = lt * at + (kq == 0 ? pt : 0.f);
+    xp *= ap;
+    vacc *= at;
+    __syncthreads();
+    if (ib < S) {
+#pragma unroll
+      for (int u = 0; u < kCmbBatch; ++u) xp += v[u] * s_w[ps + kCmbStrides * u];
+    }
+    if (t0 < T) {
+#pragma unroll
+      for (int k2 = 0; k2 < kWinBlock / kCmbWaves; ++k2) {
+        const float p2 = s_p[part + kCmbWaves * k2];
+        vacc[0] = __builtin_fmaf(p2, half_bits_to_float(vv[k2] & 0xffff), vacc[0]);
+        vacc[1] = __builtin_fmaf(p2, half_bits_to_float(vv[k2] >> 16), vacc[1]);
+      }
+    }
+    mp = mp_new;
+    mt = mt_new;
+    __syncthreads();   // s_w, s_p, s_red are rewritten by the next block
+  }
+  // ---- gather: strides, parts, denominators ----
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lp += __shfl_xor(lp, o);
+    lt += __shfl_xor(lt, o);
+  }
+  s_x[tid] = xp;
+  s_v[tid] = vacc;
+  if (lane == 0) {
+    s_red[2 * wave] = lp;
+    s_red[2 * wave + 1] = lt;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float lpt = 0.f, ltt = 0.f;
+#pragma unroll
+  for (int w = 0; w < kCmbWaves; ++w) {
+    lpt += s_red[2 * w];
+    ltt += s_red[2 * w + 1];
+  }
+  // lane holds channels 2l, 2l+1: quad l/2 of the packed sum, pair l of the window
   const int c0 = 2 * lane, c1 = 2 * lane + 1;
-  const float o0 = (sign_neg(a.v_sign_bits, c0) ? -x0 : x0) * scale;
-  const float o1 = (sign_neg(a.v_sign_bits, c1) ? -x1 : x1) * scale;
+  float x0 = 0.f, x1 = 0.f, w0 = 0.f, w1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kCmbStrides; ++k) {
+    const float4_t u = s_x[32 * k + (lane >> 1)];
+    x0 += (lane & 1) ? u[2] : u[0];
+    x1 += (lane & 1) ? u[3] : u[1];
+  }
+#pragma unroll
+  for (int k = 0; k < kCmbWaves; ++k) {
+    const f2_t u = s_v[64 * k + lane];
+    w0 += u[0];
+    w1 += u[1];
+  }
+  wave_fwht128(x0, x1, lane);
+  x0 = (sign_neg(a.v_sign_bits, c0) ? -x0 : x0) * (1.0f / kD);
+  x1 = (sign_neg(a.v_sign_bits, c1) ? -x1 : x1) * (1.0f / kD);
+  const float M = fmaxf(mp, mt);
+  const float wp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
+  const float wt = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - M);
+  const float inv = 1.0f / (lpt * wp + ltt * wt);
   float* dst = a.out + (((int64_t)b * a.h_kv + h) * a.G + g) * kD;
-  *reinterpret_cast<float2*>(dst + c0) = make_float2(o0, o1);
+  *reinterpret_cast<float2*>(dst + c0) = make_float2((x0 * wp + w0 * wt) * inv, (x1 * wp + w1 * wt) * inv);
 }
 
 }  // namespace bmx
@@ -566,20 +754,22 @@ static int device_cu_count() {
 
 // Workgroups per sequence: one wave of workgroups over the device's CUs (one
 // 8-wave workgroup per CU), or as many as split_tokens asks for; never more
-// than the sequence has 64-token work units.
+// than the sequence has 64-token groups.
 static int choose_splits(const bmx_k2b_decode_args* a) {
-  const int units = (a->max_packed_len + kGroup - 1) / kGroup + (a->tail_cap + kGroup - 1) / kGroup;
+  const int units = (a->max_packed_len + kGroup - 1) / kGroup;
   int S;
   if (a->split_tokens > 0)
-    S = (a->max_packed_len + a->tail_cap + a->split_tokens - 1) / a->split_tokens;
+    S = (a->max_packed_len + a->split_tokens - 1) / a->split_tokens;
   else
     S = device_cu_count() / a->batch;
   if (S > units) S = units;
   return S < 1 ? 1 : S;
 }
 
+// Workspace: split partials, accumulators [B][S][h_kv][G][128] then
+// (max, sum) [B][S][h_kv][G][2], fp32.
 static size_t ws_bytes(const bmx_k2b_decode_args* a, int splits) {
-  const size_t rows = (size_t)a->batch * (splits + 1) * a->geom.h_kv * a->geom.n_q_groups;
+  const size_t rows = (size_t)a->batch * splits * a->geom.h_kv * a->geom.n_q_groups;
   return rows * (kD + 2) * sizeof(float);
 }
 
@@ -593,17 +783,24 @@ static int fail(int code, const std::string& msg) {
   return code;
 }
 
-template <int R>
-static hipError_t launch_split(const DecodeKArgs& k, dim3 grid, size_t smem, hipStream_t st) {
+template <int R, int SW>
+static hipError_t launch_split_sw(const DecodeKArgs& k, dim3 grid, size_t smem, hipStream_t st) {
   static size_t attr_bytes = 0;
   if (attr_bytes < smem) {
-    hipError_t e = hipFuncSetAttribute((const void*)k2b_decode_split_kernel<R>,
+    hipError_t e = hipFuncSetAttribute((const void*)k2b_decode_split_kernel<R, SW>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) return e;
     attr_bytes = smem;
   }
-  hipLaunchKernelGGL(k2b_decode_split_kernel<R>, grid, dim3(kThreads), smem, st, k);
+  hipLaunchKernelGGL((k2b_decode_split_kernel<R, SW>), grid, dim3(kThreads), smem, st, k);
   return hipGetLastError();
+}
+
+template <int R>
+static hipError_t launch_split(const DecodeKArgs& k, dim3 grid, size_t smem, hipStream_t st) {
+  if (k.G <= 4) return launch_split_sw<R, 4>(k, grid, smem, st);
+  if (k.G <= 8) return launch_split_sw<R, 8>(k, grid, smem, st);
+  return launch_split_sw<R, 16>(k, grid, smem, st);
 }
 
 extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
@@ -635,30 +832,27 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
     return fail(BMX_E_INVALID, "bmx_k2b_decode: tail strides must be multiples of 8 elements");
   const int max_splits = choose_splits(a);
   const size_t need = ws_bytes(a, max_splits);
-  if (max_splits + 1 > 8192)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: more than 8191 splits; use a larger split_tokens");
+  if (max_splits > 8192)
+    return fail(BMX_E_INVALID, "bmx_k2b_decode: more than 8192 splits; use a larger split_tokens");
   if (!a->workspace || a->workspace_bytes < need)
     return fail(BMX_E_WORKSPACE, "bmx_k2b_decode: workspace missing or smaller than "
                                  "bmx_k2b_decode_workspace_bytes()");
   hipStream_t st = (hipStream_t)stream;
-  const size_t rows = (size_t)a->batch * (max_splits + 1) * g.h_kv * g.n_q_groups;
+  const size_t rows = (size_t)a->batch * max_splits * g.h_kv * g.n_q_groups;
   float* ws_acc = (float*)a->workspace;
   float* ws_ml = ws_acc + rows * kD;
   const float qscale = a->sm_scale * 1.4426950408889634f;
 
   DecodeKArgs k{};
-  k.h_kv = g.h_kv; k.G = g.n_q_groups; k.split_tokens = 0;
+  k.h_kv = g.h_kv; k.G = g.n_q_groups;
   k.max_splits = max_splits; k.max_pages = a->max_pages;
   k.max_packed_len = a->max_packed_len; k.n_pool = a->n_pool_pages > 0 ? a->n_pool_pages : 1;
-  k.tail_cap = a->tail_cap;
+  k.L = PageLayout::make(g.h_kv, g.rank);
+  k.shared_bytes = k.L.kres;   // US, VNORM, KSCALE precede KRES
   k.q = a->q; k.ws_acc = ws_acc; k.ws_ml = ws_ml;
   k.pages = a->pages; k.page_table = a->page_table; k.packed_len = a->packed_len;
   k.basis = a->basis; k.basis_stride = a->basis_stride;
-  k.k_tail = a->k_tail; k.v_tail = a->v_tail;
-  k.ts_b = a->tail_stride_b; k.ts_h = a->tail_stride_h; k.ts_t = a->tail_stride_t;
-  k.tail_len = a->tail_len;
-  k.L = PageLayout::make(g.h_kv, g.rank);
-  k.qscale = qscale; k.rope_scaling = a->rope_scaling;
+  k.qscale_rope = qscale * a->rope_scaling;
   for (int j = 0; j < 64; ++j) {
     k.inv_freq[j] = a->inv_freq[j];
     const double step = 64.0 * (double)a->inv_freq[j];  // exact: 64 * fp32
@@ -667,13 +861,11 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
     k.step8_c[j] = (float)cos(step / 8.0);
     k.step8_s[j] = (float)sin(step / 8.0);
   }
-  for (int j = 0; j < 4; ++j) { k.codebook[j] = a->codebook[j]; k.v_sign_bits[j] = a->v_sign_bits[j]; }
-  const size_t smem = (size_t)2 * kGroupPages * k.L.bytes + kCsBytes;
-  const size_t tail_smem = (size_t)kWaves * kTailSlice;
-  const size_t smem_all = smem > tail_smem ? smem : tail_smem;
-  dim3 grid(max_splits + 1, a->batch);
-  hipError_t e = g.rank == 32 ? launch_split<32>(k, grid, smem_all, st)
-                              : launch_split<16>(k, grid, smem_all, st);
+  for (int j = 0; j < 4; ++j) k.codebook[j] = a->codebook[j];
+  const size_t smem = (size_t)2 * kCsBuf * 4 + (size_t)2 * kGroupPages * k.shared_bytes;
+  dim3 grid(max_splits, a->batch);
+  hipError_t e = g.rank == 32 ? launch_split<32>(k, grid, smem, st)
+                              : launch_split<16>(k, grid, smem, st);
   if (e != hipSuccess)
     return fail(BMX_E_HIP, std::string("bmx_k2b_decode: split kernel launch: ") + hipGetErrorString(e));
   if (a->split_end_event) {
@@ -684,12 +876,13 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   CombineKArgs c{};
   c.h_kv = g.h_kv; c.G = g.n_q_groups;
   c.max_splits = max_splits; c.tail_cap = a->tail_cap;
-  c.out = a->out; c.ws_acc = ws_acc; c.ws_ml = ws_ml;
+  c.qscale = qscale;
+  c.out = a->out; c.q = a->q; c.ws_acc = ws_acc; c.ws_ml = ws_ml;
+  c.k_tail = a->k_tail; c.v_tail = a->v_tail;
+  c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
   c.tail_len = a->tail_len;
   for (int j = 0; j < 4; ++j) c.v_sign_bits[j] = a->v_sign_bits[j];
-  const size_t csmem = (size_t)(((max_splits + 4) & ~3) + kCombineStrides * 32 * 4 + 16) * sizeof(float);
-  hipLaunchKernelGGL(k2b_combine_kernel, dim3(g.n_q_groups, g.h_kv, a->batch), dim3(kCombineThreads),
-                     csmem, st, c);
+  hipLaunchKernelGGL(k2b_combine_kernel, dim3(g.n_q_groups, g.h_kv, a->batch), dim3(kCmbThreads), 0, st, c);
   e = hipGetLastError();
   if (e != hipSuccess)
     return fail(BMX_E_HIP, std::string("bmx_k2b_decode: combine kernel launch: ") + hipGetErrorString(e));

@@ -30,7 +30,8 @@ __global__ __launch_bounds__(256) void k2b_dequant_kernel(const DequantKArgs a) 
   __shared__ float s_us[kPT][33];
   __shared__ float x[kPT][kD];
   for (int e = tid; e < kPT * R; e += 256)
-    s_us[e / R][e % R] = half_bits_to_float(*reinterpret_cast<const uint16_t*>(page + a.L.us + e * 2));
+    s_us[e / R][e % R] = half_bits_to_float(
+        *reinterpret_cast<const uint16_t*>(page + a.L.us + us_half(R, e / R, e % R) * 2));
   __syncthreads();
 
   // keys: thread handles (token t, channel pair j, j+64) for 4 pairs
@@ -44,12 +45,12 @@ __global__ __launch_bounds__(256) void k2b_dequant_kernel(const DequantKArgs a) 
       float acc = 0.f;
       for (int r = 0; r < R; ++r)
         acc = __builtin_fmaf(s_us[t][r], half_bits_to_float(a.basis[(int64_t)c * R + r]), acc);
-      const int quarter = C / 4, slot = c / quarter, off = c % quarter;
+      const int f = kscale_flat(c), quarter = C / 4, slot = f / quarter, off = f % quarter;
       const uint8_t* sp = a.pages + clamp_page(a.page_table[grp * 4 + slot], a.n_pool) * a.L.bytes + a.L.kscale;
       const float scale = half_bits_to_float(*reinterpret_cast<const uint16_t*>(sp + off * 2));
-      const int bt = j / 16, q = (j % 16) / 4, i = j % 4;
+      const int b = j0 / 16, q = (j0 % 16) / 4, i = j0 % 4;
       const uint32_t* kr = reinterpret_cast<const uint32_t*>(page + a.L.kres + h * 768 + (16 * q + t) * 12);
-      const int code = kres_code(kr[0], kr[1], kr[2], 4 * bt + i);
+      const int code = kres_pair_code(kr[0], kr[1], kr[2], 4 * b + i, s);
       kv[s] = acc + scale * (float)code;
     }
     const int64_t base = ((int64_t)h * a.n_tokens + lp * kPT + t) * kD;
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(256) void k2b_dequant_kernel(const DequantKArgs a) 
     const int b = c / 16, m = c % 16, q = t / 4, tt = t % 4;
     const uint32_t* vc = reinterpret_cast<const uint32_t*>(page + a.L.vcode + h * 512 + (16 * q + m) * 8);
     const uint32_t D = vc[b / 4];
-    const int idx = (D >> (16 * (tt & 1) + 4 * (b % 4) + 2 * (tt >> 1))) & 3;
+    const int idx = (D >> (8 * (b % 4) + 2 * tt)) & 3;
     x[t][c] = a.codebook[idx];
   }
   __syncthreads();

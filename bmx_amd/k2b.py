@@ -98,14 +98,17 @@ def append(k_pre: torch.Tensor, v: torch.Tensor, basis32: torch.Tensor, basis16:
 
 
 class DecodeWorkspace:
-    """Grow-only device scratch for split partials (reused across calls)."""
+    """Grow-only device scratch for split partials (reused across calls).
+
+    Zero-filled when (re)allocated: the merge counters at its head must start at
+    zero, and every completed call leaves them at zero again."""
 
     def __init__(self):
         self.buf = None
 
     def get(self, nbytes: int, device) -> torch.Tensor:
         if self.buf is None or self.buf.numel() < nbytes or self.buf.device != device:
-            self.buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+            self.buf = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
         return self.buf
 
 

@@ -58,7 +58,7 @@ enum bmx_k2b_section {
 };
 
 typedef struct {
-  int32_t h_kv;        /* KV heads, 1..16 */
+  int32_t h_kv;        /* KV heads: 1..16 for pages/append/dequant, 1..8 for decode */
   int32_t rank;        /* low-rank key rank R: 16 or 32 */
   int32_t n_q_groups;  /* query heads per KV head G, 1..16 */
 } bmx_k2b_geom;
@@ -108,8 +108,12 @@ typedef struct {
   int64_t tail_stride_h;
   int64_t tail_stride_t;
   const int32_t* tail_len;    /* device [batch] recent-window length (clamped to tail_cap) */
-  int32_t tail_cap;           /* host upper bound of tail_len, <= 1024 */
-  int32_t split_tokens;       /* tokens per split-KV work item; 0 = choose */
+  int32_t tail_cap;           /* host upper bound of tail_len, 0..4096 */
+  int32_t split_tokens;       /* 0 = one workgroup per CU, split over the batch (default);
+                                 > 0 (multiple of 64) = about (max_packed_len + tail_cap)
+                                 / split_tokens workgroups per sequence.  Work is dealt in
+                                 64-token units, balanced over the workgroups; the last
+                                 workgroup also owns the recent window. */
   void* workspace;            /* device scratch for split partials */
   size_t workspace_bytes;
   void* split_end_event;      /* optional hipEvent_t recorded on the stream between

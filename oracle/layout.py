@@ -8,17 +8,21 @@ can be checked exactly and decode-kernel inputs can be built on the CPU.
 
 Page of PT=16 tokens for one layer, head_dim 128, C = 128*h_kv channels,
 rank R.  Sections in order (all little-endian):
-  US     [16][R] fp16                      low-rank coefficients Us per token
-  VNORM  [h_kv][16] fp16                   value norm per (head, token)
-  KSCALE [C/4] fp16                        slot j = (page index mod 4) of the
-                                           page's 64-token scale group holds the
-                                           group scales of channels [jC/4,(j+1)C/4)
-  KRES   [h_kv][64 lanes][3 x u32]         3-bit two's-complement key residual
-         lane = 16q + n (token n, quarter q); code k=4b+i (b<8, i<4) is channel
-         16b + 4q + i of the head, at bits [3k, 3k+3) of the 96-bit lane string
-  VCODE  [h_kv][64 lanes][2 x u32]         2-bit value codes
-         lane = 16q + m; dword w holds channel 16b + m, b = 4w + bb (bb<4), for
-         token 4q + t (t<4) at bit 16*(t&1) + 4*bb + 2*(t>>1)
+  US     [4][16][R/4] fp16      US[q][n][i] = Us[token n][(R/4)*q + i]
+  VNORM  [h_kv][16] fp16        value norm per (head, token)
+  KSCALE [C/4] fp16             the 64-token group's C scales in pair order
+                                F[128h + 2j + e] = scale(channel 128h + j + 64e),
+                                j < 64, e < 2; page slot s (= page index mod 4)
+                                holds F[s*C/4, (s+1)*C/4)
+  KRES   [h_kv][64][3] u32      lane 16q+n = token n; pair p = 4b+i (b, i < 4)
+                                is channels (j, j+64), j = 16b + 4q + i, codes
+                                stored offset-binary (code + 4, 3 bits); pair
+                                p < 15: dword p // 5, low code at bit 3*(p % 5),
+                                high code at bit 16 + 3*(p % 5); pair 15: bit k
+                                of the low / high code at bit 15 / 31 of dword k
+  VCODE  [h_kv][64][2] u32      lane 16q+m; the code of channel 16b + m (b < 8),
+                                token 4q + t (t < 4) at dword b // 4, bit
+                                8*(b % 4) + 2*t
 """
 
 from __future__ import annotations
@@ -47,11 +51,24 @@ def page_bytes(h_kv: int, rank: int) -> int:
     return sections(h_kv, rank)["total"][1]
 
 
-def _kres_index(h_kv: int):
-    """channel index (within head) for [q, k] lane-string slots."""
+def kscale_flat_index(h_kv: int) -> np.ndarray:
+    """F position of each channel c (0..C-1) in the group's KSCALE order."""
+    c = np.arange(D * h_kv)
+    h, j = c // D, c % D
+    return D * h + 2 * (j % 64) + j // 64
+
+
+def kres_slots():
+    """(dword, bit) of the low code of pair p < 15 (the high code is at bit + 16)."""
+    p = np.arange(15)
+    return p // 5, 3 * (p % 5)
+
+
+def _pair_channels():
+    """channel j (< 64) of pair p for lane quarter q: (4, 16) array."""
     q = np.arange(4)[:, None]
-    k = np.arange(32)[None, :]
-    return 16 * (k // 4) + 4 * q + (k % 4)  # (4, 32)
+    p = np.arange(16)[None, :]
+    return 16 * (p // 4) + 4 * q + (p % 4)
 
 
 def pack_pages(us16, res, scale16, vidx, vnorm16, h_kv: int, rank: int) -> np.ndarray:
@@ -66,6 +83,7 @@ def pack_pages(us16, res, scale16, vidx, vnorm16, h_kv: int, rank: int) -> np.nd
     T = us16.shape[0]
     assert T % GROUP == 0
     C = D * h_kv
+    R = rank
     n_pages = T // PT
     sec = sections(h_kv, rank)
     out = np.zeros((n_pages, sec["total"][1]), dtype=np.uint8)
@@ -74,42 +92,45 @@ def pack_pages(us16, res, scale16, vidx, vnorm16, h_kv: int, rank: int) -> np.nd
     vidx = np.asarray(vidx).astype(np.int64)
     scale16 = np.asarray(scale16, dtype=np.float16)
     vnorm16 = np.asarray(vnorm16, dtype=np.float16)
-    chan = _kres_index(h_kv)  # (4, 32)
+    fpos = kscale_flat_index(h_kv)
+    chan = _pair_channels()                      # (4, 16)
+    dw, sh = kres_slots()
     for p in range(n_pages):
         t0 = p * PT
+        tok = t0 + np.arange(PT)
         o, s = sec["us"]
-        out[p, o:o + s] = us16[t0:t0 + PT].reshape(-1).view(np.uint8)
+        us = us16[t0:t0 + PT].reshape(PT, 4, R // 4).transpose(1, 0, 2)
+        out[p, o:o + s] = np.ascontiguousarray(us).reshape(-1).view(np.uint8)
         o, s = sec["vnorm"]
         out[p, o:o + s] = np.ascontiguousarray(vnorm16[t0:t0 + PT].T).reshape(-1).view(np.uint8)
         o, s = sec["kscale"]
         g, j = p // 4, p % 4
-        out[p, o:o + s] = np.ascontiguousarray(
-            scale16[j * C // 4:(j + 1) * C // 4, g]).view(np.uint8)
+        flat = np.zeros(C, dtype=np.float16)
+        flat[fpos] = scale16[:, g]
+        out[p, o:o + s] = np.ascontiguousarray(flat[j * C // 4:(j + 1) * C // 4]).view(np.uint8)
         # KRES
         o, s = sec["kres"]
         kres = np.zeros((h_kv, 4, PT, 3), dtype=np.uint64)
         for h in range(h_kv):
-            # codes[q, n, k] = res[h*128 + chan[q,k], t0+n]
-            codes = res[h * D + chan[:, None, :], t0 + np.arange(PT)[None, :, None]] & 7
-            for k in range(32):
-                bit = 3 * k
-                w, sh = bit // 32, bit % 32
-                val = codes[:, :, k].astype(np.uint64)
-                kres[h, :, :, w] |= (val << np.uint64(sh)) & np.uint64(0xFFFFFFFF)
-                if sh > 29:
-                    kres[h, :, :, w + 1] |= val >> np.uint64(32 - sh)
+            # lo[q, n, p] = code of channel chan[q, p], hi: channel + 64; offset-binary
+            lo = (res[h * D + chan[:, None, :], tok[None, :, None]] + 4).astype(np.uint64)
+            hi = (res[h * D + 64 + chan[:, None, :], tok[None, :, None]] + 4).astype(np.uint64)
+            for pp in range(15):
+                kres[h, :, :, dw[pp]] |= (lo[:, :, pp] << np.uint64(sh[pp])) | \
+                    (hi[:, :, pp] << np.uint64(16 + sh[pp]))
+            for k in range(3):
+                kres[h, :, :, k] |= (((lo[:, :, 15] >> np.uint64(k)) & np.uint64(1)) << np.uint64(15)) | \
+                    (((hi[:, :, 15] >> np.uint64(k)) & np.uint64(1)) << np.uint64(31))
         out[p, o:o + s] = kres.astype(np.uint32).reshape(-1).view(np.uint8)
         # VCODE
         o, s = sec["vcode"]
         vc = np.zeros((h_kv, 4, 16, 2), dtype=np.uint64)
         for h in range(h_kv):
             for b in range(8):
-                w, bb = b // 4, b % 4
-                # codes[q, t, m] of channel 16b+m, token t0 + 4q + t
+                # cm[q, t, m]: channel 16b + m, token t0 + 4q + t
                 cm = vidx[t0:t0 + PT, h * D + 16 * b + np.arange(16)].reshape(4, 4, 16)
                 for t in range(4):
-                    sh = 16 * (t & 1) + 4 * bb + 2 * (t >> 1)
-                    vc[h, :, :, w] |= cm[:, t, :].astype(np.uint64) << np.uint64(sh)
+                    vc[h, :, :, b // 4] |= cm[:, t, :].astype(np.uint64) << np.uint64(8 * (b % 4) + 2 * t)
         out[p, o:o + s] = vc.astype(np.uint32).reshape(-1).view(np.uint8)
     return out
 
@@ -120,42 +141,49 @@ def unpack_pages(pages: np.ndarray, h_kv: int, rank: int):
     n_pages = pages.shape[0]
     T = n_pages * PT
     C = D * h_kv
+    R = rank
     sec = sections(h_kv, rank)
     us16 = np.zeros((T, rank), dtype=np.float16)
     vnorm16 = np.zeros((T, h_kv), dtype=np.float16)
     scale16 = np.zeros((C, T // GROUP), dtype=np.float16)
     res = np.zeros((C, T), dtype=np.int8)
     vidx = np.zeros((T, C), dtype=np.int16)
-    chan = _kres_index(h_kv)
+    fpos = kscale_flat_index(h_kv)
+    chan = _pair_channels()
+    dw, sh = kres_slots()
     for p in range(n_pages):
         t0 = p * PT
+        tok = t0 + np.arange(PT)
         o, s = sec["us"]
-        us16[t0:t0 + PT] = pages[p, o:o + s].view(np.float16).reshape(PT, rank)
+        us16[t0:t0 + PT] = pages[p, o:o + s].view(np.float16).reshape(4, PT, R // 4) \
+            .transpose(1, 0, 2).reshape(PT, R)
         o, s = sec["vnorm"]
         vnorm16[t0:t0 + PT] = pages[p, o:o + s].view(np.float16).reshape(h_kv, PT).T
         o, s = sec["kscale"]
         g, j = p // 4, p % 4
         if g < scale16.shape[1]:
-            scale16[j * C // 4:(j + 1) * C // 4, g] = pages[p, o:o + s].view(np.float16)
+            sl = pages[p, o:o + s].view(np.float16)
+            sel = (fpos >= j * C // 4) & (fpos < (j + 1) * C // 4)
+            scale16[sel, g] = sl[fpos[sel] - j * C // 4]
         o, s = sec["kres"]
-        kres = pages[p, o:o + s].view(np.uint32).reshape(h_kv, 4, PT, 3).astype(np.uint64)
-        for k in range(32):
-            bit = 3 * k
-            w, sh = bit // 32, bit % 32
-            val = kres[..., w] >> np.uint64(sh)
-            if sh > 29:
-                val |= kres[..., w + 1] << np.uint64(32 - sh)
-            val = (val & np.uint64(7)).astype(np.int64)
-            val = np.where(val >= 4, val - 8, val)  # sign-extend 3 bits
-            for h in range(h_kv):
-                res[h * D + chan[:, k][:, None], t0 + np.arange(PT)[None, :]] = val[h]
+        kres = pages[p, o:o + s].view(np.uint32).reshape(h_kv, 4, PT, 3).astype(np.int64)
+        lo = np.zeros((h_kv, 4, PT, 16), dtype=np.int64)
+        hi = np.zeros_like(lo)
+        for pp in range(15):
+            lo[..., pp] = (kres[..., dw[pp]] >> sh[pp]) & 7
+            hi[..., pp] = (kres[..., dw[pp]] >> (16 + sh[pp])) & 7
+        for k in range(3):
+            lo[..., 15] |= ((kres[..., k] >> 15) & 1) << k
+            hi[..., 15] |= ((kres[..., k] >> 31) & 1) << k
+        for h in range(h_kv):
+            res[h * D + chan[:, None, :], tok[None, :, None]] = lo[h] - 4
+            res[h * D + 64 + chan[:, None, :], tok[None, :, None]] = hi[h] - 4
         o, s = sec["vcode"]
         vc = pages[p, o:o + s].view(np.uint32).reshape(h_kv, 4, 16, 2).astype(np.int64)
         for h in range(h_kv):
             for b in range(8):
-                w, bb = b // 4, b % 4
                 for t in range(4):
-                    sh = 16 * (t & 1) + 4 * bb + 2 * (t >> 1)
                     vidx[t0 + 4 * np.arange(4)[:, None] + t,
-                         h * D + 16 * b + np.arange(16)[None, :]] = (vc[h, :, :, w] >> sh) & 3
+                         h * D + 16 * b + np.arange(16)[None, :]] = \
+                        (vc[h, :, :, b // 4] >> (8 * (b % 4) + 2 * t)) & 3
     return us16, res, scale16, vidx, vnorm16

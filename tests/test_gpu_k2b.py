@@ -278,6 +278,70 @@ def test_64_decode_steps_zero_argmax_flips():
     assert flips == 0 and worst <= MAX_ABS
 
 
+@pytest.mark.parametrize("G", [1, 2, 8, 16])
+def test_decode_query_group_sizes(G):
+    """Query groups other than 4: the score tiles of 4, 2 or 1 pages share a
+    register after compaction (G <= 4, <= 8, <= 16)."""
+    gen = torch.Generator().manual_seed(20 + G)
+    h_kv, rank, S, T = 2, 32, 1024, 70
+    k_pre = synth.k2b_keys(h_kv, S + T, rank, gen)
+    v = synth.values(h_kv, S + T, gen)
+    svd = synth.first_page_svd(k_pre, rank)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    pool = synth.PagePool(S // 16, h_kv, rank, DEV, gen=gen)
+    seq = synth.encode_sequence(pool, k_pre[:, :S].to(DEV), v[:, :S].to(DEV), rank, consts, svd=svd)
+    inv = torch.tensor(consts.inv_freq)
+    cos, sin = A.rope_cos_sin(inv, torch.arange(S, S + T))
+    k_tail = A.apply_rope(k_pre[:, S:].float(), cos, sin).half()
+    v_tail = v[:, S:]
+    q = torch.randn(1, h_kv, G, 128, generator=gen)
+    out = _decode_one(seq, pool, q, consts, rank, k_tail, v_tail)
+    cache = _oracle_cache(k_pre[:, :S], v[:, :S], rank, svd)
+    ref = A.k2b_naive_attention(q.view(h_kv * G, 1, 128), cache, inv, k_tail, v_tail, G, 128 ** -0.5)
+    _close(out, ref.view(1, h_kv, G, 128), f"G {G}")
+
+
+def test_decode_window_only_and_long_window():
+    """No committed tokens (the fp16 window alone), and a 1100-token window
+    (three 512-token passes of the combine) over 1024 committed tokens."""
+    gen = torch.Generator().manual_seed(30)
+    h_kv, rank, G = 8, 32, 4
+    consts = k2b.CodecConsts.make(v_seed=0)
+    inv = torch.tensor(consts.inv_freq)
+    # window only
+    T = 300
+    k_pre = synth.k2b_keys(h_kv, T, rank, gen)
+    v = synth.values(h_kv, T, gen)
+    cos, sin = A.rope_cos_sin(inv, torch.arange(T))
+    k_tail = A.apply_rope(k_pre.float(), cos, sin).half()
+    pool = synth.PagePool(8, h_kv, rank, DEV, gen=gen)
+    q = torch.randn(1, h_kv, G, 128, generator=gen)
+    out = k2b.decode(q.to(DEV), pool.pages, torch.zeros(1, 1, dtype=torch.int32, device=DEV),
+                     torch.zeros(1, dtype=torch.int32, device=DEV), 0,
+                     torch.zeros(128 * h_kv, rank, dtype=torch.float16, device=DEV), consts,
+                     128 ** -0.5, rank=rank, k_tail=k_tail.unsqueeze(0).to(DEV),
+                     v_tail=v.unsqueeze(0).to(DEV).contiguous(),
+                     tail_len=torch.tensor([T], dtype=torch.int32, device=DEV), tail_cap=T)
+    torch.cuda.synchronize()
+    ref = A.naive_dense_attention(q.view(32, 1, 128), k_tail.float(), v.float(), G, 128 ** -0.5)
+    _close(out, ref.view(1, h_kv, G, 128), "window only")
+    # long window
+    S, T = 1024, 1100
+    k_pre = synth.k2b_keys(h_kv, S + T, rank, gen)
+    v = synth.values(h_kv, S + T, gen)
+    svd = synth.first_page_svd(k_pre, rank)
+    pool = synth.PagePool(S // 16, h_kv, rank, DEV, gen=gen)
+    seq = synth.encode_sequence(pool, k_pre[:, :S].to(DEV), v[:, :S].to(DEV), rank, consts, svd=svd)
+    cos, sin = A.rope_cos_sin(inv, torch.arange(S, S + T))
+    k_tail = A.apply_rope(k_pre[:, S:].float(), cos, sin).half()
+    v_tail = v[:, S:]
+    q = torch.randn(1, h_kv, G, 128, generator=gen)
+    out = _decode_one(seq, pool, q, consts, rank, k_tail, v_tail)
+    cache = _oracle_cache(k_pre[:, :S], v[:, :S], rank, svd)
+    ref = A.k2b_naive_attention(q.view(32, 1, 128), cache, inv, k_tail, v_tail, G, 128 ** -0.5)
+    _close(out, ref.view(1, h_kv, G, 128), "long window")
+
+
 # ------------------------------------------------------------------ dequant kernel
 
 
