@@ -8,18 +8,24 @@
  * BMX_E_* code, with a message from bmx_last_error().
  *
  * Packed page format (one layer, PT = 16 tokens, head_dim 128, C = 128*h_kv
- * channels, rank R; sections in this order, little-endian):
- *   US     [16][R]      fp16  low-rank key coefficients Us (per token)
+ * channels, rank R; sections in this order, little-endian).  "Lane 16q+n" is
+ * the MFMA lane that reads the bytes, so every lane's slice is contiguous.
+ *   US     [4][16][R/4] fp16  low-rank key coefficients: US[q][n][i] =
+ *                             Us[token n][(R/4)q + i]
  *   VNORM  [h_kv][16]   fp16  value norm per (head, token)
- *   KSCALE [C/4]        fp16  key-residual scales of the page's 64-token group:
- *                             slot j = (logical page index mod 4) holds channels
- *                             [j*C/4, (j+1)*C/4)
- *   KRES   [h_kv][64][3] u32  3-bit two's-complement key residual; lane
- *                             16q+n holds token n, channels 16b+4q+i (code k=4b+i
- *                             at bits [3k,3k+3) of the 96-bit lane string)
- *   VCODE  [h_kv][64][2] u32  2-bit Lloyd value codes; lane 16q+m, dword w holds
- *                             channel 16b+m (b = 4w+bb) for token 4q+t at bit
- *                             16*(t&1) + 4*bb + 2*(t>>1)
+ *   KSCALE [C/4]        fp16  key-residual scales of the page's 64-token group in
+ *                             pair order F[128h + 2j + e] = scale of channel
+ *                             128h + j + 64e (j < 64, e < 2); page slot s
+ *                             (= logical page index mod 4) holds F[sC/4, (s+1)C/4)
+ *   KRES   [h_kv][64][3] u32  3-bit key residual, offset binary (code + 4); lane
+ *                             16q+n holds token n; pair p = 4b+i (b, i < 4) is
+ *                             channels (j, j+64), j = 16b + 4q + i; pair p < 15:
+ *                             dword p/5, low code at bit 3(p%5), high code at bit
+ *                             16 + 3(p%5); pair 15: bit k of the low / high code
+ *                             at bit 15 / 31 of dword k
+ *   VCODE  [h_kv][64][2] u32  2-bit Lloyd value codes; lane 16q+m holds the code
+ *                             of channel 16b+m (b < 8), token 4q+t (t < 4) at
+ *                             dword b/4, bit 8(b%4) + 2t
  * Bytes per token = 2R + 86*h_kv  (752 at h_kv 8, R 32; 720 at R 16), i.e.
  * exactly the k2b bits-per-entry: 3 (residual) + 16/64 (scales) + 2 (V codes)
  * + 16*h_kv/C (norms) + 16R/C (Us).  The frozen basis V (C x R fp16) is stored
@@ -110,11 +116,11 @@ typedef struct {
   const int32_t* tail_len;    /* device [batch] recent-window length (clamped to tail_cap) */
   int32_t tail_cap;           /* host upper bound of tail_len, 0..4096 */
   int32_t split_tokens;       /* 0 = one workgroup per CU, split over the batch (default);
-                                 > 0 (multiple of 64) = about (max_packed_len + tail_cap)
-                                 / split_tokens workgroups per sequence.  Work is dealt in
-                                 64-token units, balanced over the workgroups; the last
-                                 workgroup also owns the recent window. */
-  void* workspace;            /* device scratch for split partials */
+                                 > 0 (multiple of 64) = about max_packed_len / split_tokens
+                                 workgroups per sequence.  Packed tokens are dealt in
+                                 64-token groups, balanced over the workgroups; the
+                                 recent window is attended by the merge kernel. */
+  void* workspace;            /* device scratch for the split partials (fp32) */
   size_t workspace_bytes;
   void* split_end_event;      /* optional hipEvent_t recorded on the stream between
                                  the split kernel and the combine kernel (timing) */
