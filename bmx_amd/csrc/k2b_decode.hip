@@ -29,13 +29,16 @@
 //   * P*norm is accumulated against the codebook levels on MFMA (V stays in
 //     the Hadamard-rotated domain); each level is an exact fp16 head+remainder
 //     pair, looked up four codes (one code byte, one MFMA operand) at a time in
-//     a 256-entry LDS table.
+//     a 256-entry LDS table;
+//   * at the end, the accumulator is half un-rotated in registers: the
+//     128-point Hadamard factors as H8 (over the 16-channel chunks) x H16
+//     (within a chunk), and the split kernel applies H8.
 //
-// k2b_combine_kernel: one workgroup per (query, head, sequence) attends the
-// fp16 recent window in fp32 (post-RoPE keys), merges the packed partials
-// (base-2 LSE), applies the one inverse Hadamard, the signs and the
-// normalisation, and joins the two; all of its first-round loads are issued
-// before any reduction.
+// k2b_combine_kernel: one workgroup per (16-channel chunk, query head,
+// sequence) merges the packed partials of its chunk (base-2 LSE), applies H16,
+// the signs and 1/128, and joins the fp16 recent window, attended in fp32
+// (post-RoPE keys); all of its first-round loads are issued before any
+// reduction.
 //
 // Reference semantics: cache/triton_dequant_attention.py:863-1115 (kernel),
 // 409-461 (merge), 324-360 (tail), 504-575 (finalize);
@@ -59,8 +62,8 @@ struct DecodeKArgs {
   int h_kv, G, max_splits, max_pages, max_packed_len, n_pool;
   int shared_bytes;    // page prefix read by every head: US, VNORM, KSCALE (multiple of 16)
   const float* q;
-  float* ws_acc;       // [B][max_splits][h_kv][G][128] rotated-domain accumulators
-  float* ws_ml;        // [B][max_splits][h_kv][G][2]   (running max, sum), base 2
+  float* ws_acc;       // [B][h_kv][G][8][max_splits][16] accumulators (H8 applied)
+  float* ws_ml;        // [B][h_kv][G][max_splits][2]     (running max, sum), base 2
   const uint8_t* pages;
   const int32_t* page_table;
   const int32_t* packed_len;
@@ -158,18 +161,34 @@ __device__ __forceinline__ half2_t rope2(half2_t p, uint32_t csu) {
   return __builtin_elementwise_fma(sw, sn, p * cc);
 }
 
-// Partial (acc, m, l) of this lane's query into the workspace row.
+// Partial (acc, m, l) of this lane's query into the workspace.  The rotated
+// accumulator is half un-rotated here: the 128-point Sylvester Hadamard of
+// channel c = 16bt + 4q + i factors as H8 (over bt) x H16 (over 4q + i); the
+// H8 butterflies run in registers, and the merge kernel, which holds whole
+// 16-channel chunks, applies H16, the signs and 1/128 after the merge (both
+// linear).  Lane 16q + n stores acc[bt] at offset 4q of chunk bt.  The workspace
+// row of a query is chunk-major ([chunk][split][16]), so a merge workgroup
+// reads one contiguous 64-byte record per split.
 __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int split, int h, int n,
-                                              int q, const float4_t acc[8], float m_run,
-                                              float l_run) {
+                                              int q, float4_t acc[8], float m_run, float l_run) {
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
-  if (n < a.G) {
-    const int64_t row = (((int64_t)b * a.max_splits + split) * a.h_kv + h) * a.G + n;
-    float* dst = a.ws_acc + row * kD;
 #pragma unroll
-    for (int bt = 0; bt < 8; ++bt) *reinterpret_cast<float4_t*>(dst + 16 * bt + 4 * q) = acc[bt];
-    if (q == 0) *reinterpret_cast<float2*>(a.ws_ml + row * 2) = make_float2(m_run, l_run);
+  for (int hb = 1; hb < 8; hb <<= 1)
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt)
+      if (!(bt & hb)) {
+        const float4_t u = acc[bt], w = acc[bt | hb];
+        acc[bt] = u + w;
+        acc[bt | hb] = u - w;
+      }
+  if (n < a.G) {
+    const int S = a.max_splits;
+    const int64_t row = ((int64_t)b * a.h_kv + h) * a.G + n;
+    float* dst = a.ws_acc + (row * 8 * S + split) * 16 + 4 * q;   // chunk bt at + bt * S * 16
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt) *reinterpret_cast<float4_t*>(dst + (int64_t)bt * S * 16) = acc[bt];
+    if (q == 0) *reinterpret_cast<float2*>(a.ws_ml + (row * S + split) * 2) = make_float2(m_run, l_run);
   }
 }
 
@@ -518,20 +537,22 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
 
 // ---------------------------------------------------------------------------
 // Combine: recent window + merge of the packed partials.  One workgroup per
-// (query, head, sequence); every load of the first partial block and the first
-// window block is issued before any reduction, so the kernel pays one memory
-// round trip, not one per phase.
+// (16-channel chunk, query row, sequence): the partials arrive already in the
+// output domain, so a chunk needs only its own 16 channels of every split
+// (contiguous, 64 B per split) plus every split's (max, sum).  The window
+// scores need whole keys; each chunk recomputes them (the window is small and
+// stays in L2).  Every load of the first block is issued before any reduction.
 // ---------------------------------------------------------------------------
-constexpr int kCmbThreads = 512;
+constexpr int kCmbThreads = 256;
 constexpr int kCmbWaves = kCmbThreads / 64;
-constexpr int kCmbStrides = kCmbThreads / 32;   // partial strides per channel quad
-constexpr int kCmbBatch = 16;                   // partials per thread per block
-constexpr int kCmbBlock = kCmbStrides * kCmbBatch;   // 256 partials per block
-constexpr int kWinBlock = kCmbThreads / 4;      // window tokens per block (4 threads each)
+constexpr int kChunk = 16;                  // channels per workgroup
+constexpr int kChunks = kD / kChunk;
+constexpr int kWinTok = kCmbThreads / 2;    // window tokens per block (two threads each)
+constexpr int kRedPad = kCmbThreads + 4;    // LDS row stride of the split reduction
 
 struct CombineKArgs {
   int h_kv, G, max_splits, tail_cap;
-  float qscale;        // sm_scale * log2(e) (window keys are already rotated and scaled)
+  float qscale;        // sm_scale * log2(e) (window keys are already rotated)
   float* out;
   const float* q;
   const float* ws_acc;
@@ -540,95 +561,85 @@ struct CombineKArgs {
   const uint16_t* v_tail;
   int64_t ts_b, ts_h, ts_t;
   const int32_t* tail_len;
-  uint32_t v_sign_bits[4];
+  uint32_t v_sign_bits[4];   // bit c set <=> value channel c carries Hadamard sign -1
 };
 
-// 128-point unnormalised Hadamard in one wave: lane holds channels 2l, 2l+1.
-__device__ __forceinline__ void wave_fwht128(float& x0, float& x1, int lane) {
-  const float y0 = x0 + x1, y1 = x0 - x1;
-  x0 = y0;
-  x1 = y1;
-#pragma unroll
-  for (int hb = 1; hb < 64; hb <<= 1) {
-    const float p0 = __shfl_xor(x0, hb), p1 = __shfl_xor(x1, hb);
-    const bool upper = (lane & hb) != 0;
-    x0 = upper ? (p0 - x0) : (x0 + p0);
-    x1 = upper ? (p1 - x1) : (x1 + p1);
-  }
+// Sum over the 16 lanes of a row (DPP-free butterfly; result in every lane).
+__device__ __forceinline__ float row_sum16(float x) {
+  x += __shfl_xor(x, 8);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 1);
+  return x;
 }
 
 __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineKArgs a) {
-  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int ch = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
+  const int h = r / a.G;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int S = a.max_splits;
-  const int T = min(max(a.tail_len[b], 0), a.tail_cap);
-  const int64_t row0 = ((int64_t)b * S * a.h_kv + h) * a.G + g;   // partial i at row0 + i*rstride
-  const int64_t rstride = (int64_t)a.h_kv * a.G;
+  const int64_t row = (int64_t)b * a.h_kv * a.G + r;   // (b, h, g) row
+  const float* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S * kChunk;
+  const float* mlb = a.ws_ml + row * S * 2;
   typedef float f2_t __attribute__((ext_vector_type(2)));
   __shared__ float s_red[2 * kCmbWaves];
-  __shared__ float s_w[kCmbBlock];
-  __shared__ float s_p[kWinBlock];
-  __shared__ float4_t s_x[kCmbThreads];
-  __shared__ f2_t s_v[kCmbThreads];
+  __shared__ float s_fin[2 * kChunk];
+  __shared__ float s_x[kChunk * kRedPad];
+  __shared__ float s_v[kChunk * (kWinTok + 4)];
 
-  // thread roles: partial (channel quad cq, stride ps); window score (token
-  // tk, channel quarter kq); window value (channel pair cp, token part)
-  const int cq = tid & 31, ps = tid >> 5;
-  const int tk = tid >> 2, kq = tid & 3;
-  const int cp = tid & 63, part = tid >> 6;
-  const uint16_t* kb = a.k_tail + b * a.ts_b + h * a.ts_h;
-  const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h;
-  const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + g) * kD + 32 * kq;
+  // thread roles: split i = block base + tid; window token tk (channel half kh)
+  const int tk = tid >> 1, kh = tid & 1;
+  const uint16_t* kb = a.k_tail + b * a.ts_b + h * a.ts_h + 64 * kh;
+  const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch + 8 * kh;
 
-  float4_t v[kCmbBatch];
-  f2_t ml = {-INFINITY, 0.f};   // raw (max, sum) of partial ib + tid; masked where used
-  uint4 kv[4];
-  uint32_t vv[kWinBlock / kCmbWaves];
-  auto load_block = [&](int k) {   // partial block k and window block k, no waits
-    const int ib = k * kCmbBlock, t0 = k * kWinBlock;
+  float4_t v[4];
+  f2_t ml = {-INFINITY, 0.f};
+  uint4 kv[8];
+  uint4 vv;
+  // partial block k and window block k, no waits; the first block's window
+  // rows are bounded by the host's tail_cap, so they do not wait for tail_len
+  auto load_block = [&](int k, int t_end) {
+    const int ib = k * kCmbThreads, t0 = k * kWinTok;
     if (ib < S) {
-      const int i = ib + (tid & (kCmbBlock - 1));
-      ml = *reinterpret_cast<const f2_t*>(a.ws_ml + (row0 + (int64_t)min(i, S - 1) * rstride) * 2);
+      const int i = min(ib + tid, S - 1);
+      ml = *reinterpret_cast<const f2_t*>(mlb + 2 * (int64_t)i);
 #pragma unroll
-      for (int u = 0; u < kCmbBatch; ++u) {
-        const int iu = min(ib + ps + kCmbStrides * u, S - 1);
-        v[u] = *reinterpret_cast<const float4_t*>(a.ws_acc + (row0 + (int64_t)iu * rstride) * kD + 4 * cq);
-      }
+      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4_t*>(accb + (int64_t)i * kChunk + 4 * u);
     }
-    if (t0 < T) {
-      const int t = min(t0 + tk, T - 1);
+    if (t0 < t_end) {
+      const int t = min(t0 + tk, t_end - 1);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        kv[u] = *reinterpret_cast<const uint4*>(kb + (int64_t)t * a.ts_t + 32 * kq + 8 * u);
-#pragma unroll
-      for (int k2 = 0; k2 < kWinBlock / kCmbWaves; ++k2) {
-        const int tv = min(t0 + part + kCmbWaves * k2, T - 1);
-        vv[k2] = *reinterpret_cast<const uint32_t*>(vb + (int64_t)tv * a.ts_t + 2 * cp);
-      }
+      for (int u = 0; u < 8; ++u) kv[u] = *reinterpret_cast<const uint4*>(kb + (int64_t)t * a.ts_t + 8 * u);
+      vv = *reinterpret_cast<const uint4*>(vb + (int64_t)t * a.ts_t);
     }
   };
-  load_block(0);
-  float4_t qf[8];
-  if (T > 0) {
+  load_block(0, a.tail_cap);
+  float4_t qf[16];
+  if (a.tail_cap > 0) {
+    const float* qrow = a.q + row * kD + 64 * kh;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) qf[u] = *reinterpret_cast<const float4_t*>(qrow + 4 * u);
+    for (int u = 0; u < 16; ++u) qf[u] = *reinterpret_cast<const float4_t*>(qrow + 4 * u);
   }
 
-  float4_t xp = {0.f, 0.f, 0.f, 0.f};
-  f2_t vacc = {0.f, 0.f};
+  const int T = min(max(a.tail_len[b], 0), a.tail_cap);
+  float4_t xp[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) xp[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float vacc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) vacc[e] = 0.f;
   float mp = -INFINITY, mt = -INFINITY, lp = 0.f, lt = 0.f;   // lp, lt: this thread's share
-  const int n_blk = max((S + kCmbBlock - 1) / kCmbBlock, (T + kWinBlock - 1) / kWinBlock);
+  const int n_blk = max((S + kCmbThreads - 1) / kCmbThreads, (T + kWinTok - 1) / kWinTok);
   for (int k = 0; k < n_blk; ++k) {   // uniform trip count
-    if (k != 0) load_block(k);
-    const int ib = k * kCmbBlock, t0 = k * kWinBlock;
-    const bool own_p = tid < kCmbBlock && ib + tid < S;
-    const bool own_t = t0 + tk < T;
+    if (k != 0) load_block(k, T);
+    const int ib = k * kCmbThreads, t0 = k * kWinTok;
+    const bool own_p = ib < S && ib + tid < S;
     const float mi = own_p ? ml[0] : -INFINITY;
     float s = -INFINITY;
     if (t0 < T) {
       float d = 0.f;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 8; ++u) {
         const uint32_t w[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
         const float4_t q0 = qf[2 * u], q1 = qf[2 * u + 1];
         d = __builtin_fmaf(half_bits_to_float(w[0] & 0xffff), q0[0], d);
@@ -641,8 +652,7 @@ __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineK
         d = __builtin_fmaf(half_bits_to_float(w[3] >> 16), q1[3], d);
       }
       d += __shfl_xor(d, 1);
-      d += __shfl_xor(d, 2);
-      s = own_t ? d * a.qscale : -INFINITY;
+      s = (t0 + tk < T) ? d * a.qscale : -INFINITY;
     }
     // one joint block max of (partial max, window score)
     float r0 = mi, r1 = s;
@@ -666,73 +676,76 @@ __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineK
     const float at = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - mt_new);
     const float wi = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - mp_new);
     const float pt = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mt_new);
-    if (tid < kCmbBlock) s_w[tid] = wi;
-    if (kq == 0) s_p[tk] = pt;
     lp = lp * ap + (own_p ? ml[1] * wi : 0.f);
-    lt = lt * at + (kq == 0 ? pt : 0.f);
-    xp *= ap;
-    vacc *= at;
-    __syncthreads();
-    if (ib < S) {
+    lt = lt * at + (kh == 0 ? pt : 0.f);
 #pragma unroll
-      for (int u = 0; u < kCmbBatch; ++u) xp += v[u] * s_w[ps + kCmbStrides * u];
-    }
+    for (int u = 0; u < 4; ++u) xp[u] = xp[u] * ap + (own_p ? v[u] * wi : float4_t{0.f, 0.f, 0.f, 0.f});
     if (t0 < T) {
+      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-      for (int k2 = 0; k2 < kWinBlock / kCmbWaves; ++k2) {
-        const float p2 = s_p[part + kCmbWaves * k2];
-        vacc[0] = __builtin_fmaf(p2, half_bits_to_float(vv[k2] & 0xffff), vacc[0]);
-        vacc[1] = __builtin_fmaf(p2, half_bits_to_float(vv[k2] >> 16), vacc[1]);
+      for (int e = 0; e < 4; ++e) {
+        vacc[2 * e] = __builtin_fmaf(pt, half_bits_to_float(w[e] & 0xffff), vacc[2 * e] * at);
+        vacc[2 * e + 1] = __builtin_fmaf(pt, half_bits_to_float(w[e] >> 16), vacc[2 * e + 1] * at);
       }
     }
     mp = mp_new;
     mt = mt_new;
-    __syncthreads();   // s_w, s_p, s_red are rewritten by the next block
+    __syncthreads();   // s_red is rewritten by the next block
   }
-  // ---- gather: strides, parts, denominators ----
+  // ---- gather: channel c of the packed sum over the splits (thread tid holds
+  // split tid's share), of the window sum over the tokens, and the denominators ----
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_x[(4 * u + e) * kRedPad + tid] = xp[u][e];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_v[(8 * kh + e) * (kWinTok + 4) + tk] = vacc[e];
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     lp += __shfl_xor(lp, o);
     lt += __shfl_xor(lt, o);
   }
-  s_x[tid] = xp;
-  s_v[tid] = vacc;
   if (lane == 0) {
     s_red[2 * wave] = lp;
     s_red[2 * wave + 1] = lt;
   }
   __syncthreads();
-  if (wave != 0) return;
   float lpt = 0.f, ltt = 0.f;
 #pragma unroll
   for (int w = 0; w < kCmbWaves; ++w) {
     lpt += s_red[2 * w];
     ltt += s_red[2 * w + 1];
   }
-  // lane holds channels 2l, 2l+1: quad l/2 of the packed sum, pair l of the window
-  const int c0 = 2 * lane, c1 = 2 * lane + 1;
-  float x0 = 0.f, x1 = 0.f, w0 = 0.f, w1 = 0.f;
+  // thread (c = tid / 16, part = tid % 16) sums splits part + 16j and tokens part + 16j
+  const int c = tid >> 4, part = tid & 15;
+  float x = 0.f, wv = 0.f;
 #pragma unroll
-  for (int k = 0; k < kCmbStrides; ++k) {
-    const float4_t u = s_x[32 * k + (lane >> 1)];
-    x0 += (lane & 1) ? u[2] : u[0];
-    x1 += (lane & 1) ? u[3] : u[1];
-  }
+  for (int j = 0; j < kCmbThreads / 16; ++j) x += s_x[c * kRedPad + part + 16 * j];
 #pragma unroll
-  for (int k = 0; k < kCmbWaves; ++k) {
-    const f2_t u = s_v[64 * k + lane];
-    w0 += u[0];
-    w1 += u[1];
+  for (int j = 0; j < kWinTok / 16; ++j) wv += s_v[c * (kWinTok + 4) + part + 16 * j];
+  x = row_sum16(x);
+  wv = row_sum16(wv);
+  if (part == 0) {
+    s_fin[c] = x;
+    s_fin[kChunk + c] = wv;
   }
-  wave_fwht128(x0, x1, lane);
-  x0 = (sign_neg(a.v_sign_bits, c0) ? -x0 : x0) * (1.0f / kD);
-  x1 = (sign_neg(a.v_sign_bits, c1) ? -x1 : x1) * (1.0f / kD);
-  const float M = fmaxf(mp, mt);
-  const float wp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
-  const float wt = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - M);
-  const float inv = 1.0f / (lpt * wp + ltt * wt);
-  float* dst = a.out + (((int64_t)b * a.h_kv + h) * a.G + g) * kD;
-  *reinterpret_cast<float2*>(dst + c0) = make_float2((x0 * wp + w0 * wt) * inv, (x1 * wp + w1 * wt) * inv);
+  __syncthreads();
+  if (tid < kChunk) {
+    // lane c: H16 over the chunk's channel bits 0-3, then sign and 1/128
+    float y = s_fin[tid];
+#pragma unroll
+    for (int hb = 1; hb < kChunk; hb <<= 1) {
+      const float p = __shfl_xor(y, hb);
+      y = (tid & hb) ? p - y : y + p;
+    }
+    const int cg = kChunk * ch + tid;
+    y = (sign_neg(a.v_sign_bits, cg) ? -y : y) * (1.0f / kD);
+    const float M = fmaxf(mp, mt);
+    const float wp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
+    const float wt = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - M);
+    const float inv = 1.0f / (lpt * wp + ltt * wt);
+    a.out[row * kD + cg] = (y * wp + s_fin[kChunk + tid] * wt) * inv;
+  }
 }
 
 }  // namespace bmx
@@ -766,8 +779,8 @@ static int choose_splits(const bmx_k2b_decode_args* a) {
   return S < 1 ? 1 : S;
 }
 
-// Workspace: split partials, accumulators [B][S][h_kv][G][128] then
-// (max, sum) [B][S][h_kv][G][2], fp32.
+// Workspace: split partials, accumulators [B][h_kv][G][8][S][16] then
+// (max, sum) [B][h_kv][G][S][2], fp32.
 static size_t ws_bytes(const bmx_k2b_decode_args* a, int splits) {
   const size_t rows = (size_t)a->batch * splits * a->geom.h_kv * a->geom.n_q_groups;
   return rows * (kD + 2) * sizeof(float);
@@ -882,7 +895,8 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
   c.tail_len = a->tail_len;
   for (int j = 0; j < 4; ++j) c.v_sign_bits[j] = a->v_sign_bits[j];
-  hipLaunchKernelGGL(k2b_combine_kernel, dim3(g.n_q_groups, g.h_kv, a->batch), dim3(kCmbThreads), 0, st, c);
+  hipLaunchKernelGGL(k2b_combine_kernel, dim3(kChunks, g.h_kv * g.n_q_groups, a->batch), dim3(kCmbThreads),
+                     0, st, c);
   e = hipGetLastError();
   if (e != hipSuccess)
     return fail(BMX_E_HIP, std::string("bmx_k2b_decode: combine kernel launch: ") + hipGetErrorString(e));
