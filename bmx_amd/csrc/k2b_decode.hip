@@ -26,10 +26,9 @@
 //     one register set with DPP row shifts, so the online softmax runs once per
 //     group on fully used lanes; the accumulator is rescaled only when a
 //     running max grows;
-//   * P*norm is accumulated against the codebook levels on MFMA (V stays in
-//     the Hadamard-rotated domain); each level is an exact fp16 head+remainder
-//     pair, looked up four codes (one code byte, one MFMA operand) at a time in
-//     a 256-entry LDS table;
+//   * P*norm is accumulated against the fp16 codebook levels on MFMA (V stays
+//     in the Hadamard-rotated domain), two pages per product; the levels are
+//     looked up four codes (one code byte) at a time in a 256-entry LDS table;
 //   * at the end, the accumulator is half un-rotated in registers: the
 //     128-point Hadamard factors as H8 (over the 16-channel chunks) x H16
 //     (within a chunk), and the split kernel applies H8.
@@ -45,6 +44,11 @@
 // cache/chunked_attention.py:398-530 (decode loop).
 
 #include "k2b_common.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
 
 namespace bmx {
 
@@ -76,7 +80,9 @@ struct DecodeKArgs {
   float step_s[64];
   float step8_c[64];   // cos / sin of 8 * inv_freq_j, between a thread's positions
   float step8_s[64];
-  float codebook[4];
+  uint32_t level_hi[4];   // fp16 bits of the value levels as used by the MFMA:
+                          // hi_c = kappa * codebook_c + mu (+ < 1e-6 relative)
+  float level_mu;         // mu (the merge divides by kappa)
 };
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
@@ -161,8 +167,9 @@ __device__ __forceinline__ half2_t rope2(half2_t p, uint32_t csu) {
   return __builtin_elementwise_fma(sw, sn, p * cc);
 }
 
-// Partial (acc, m, l) of this lane's query into the workspace.  The rotated
-// accumulator is half un-rotated here: the 128-point Sylvester Hadamard of
+// Partial (acc, m, l) of this lane's query into the workspace.  w_run is the
+// lane's sum of the fp16 P*norm operands, for the level correction.  The
+// rotated accumulator is half un-rotated here: the 128-point Sylvester Hadamard of
 // channel c = 16bt + 4q + i factors as H8 (over bt) x H16 (over 4q + i); the
 // H8 butterflies run in registers, and the merge kernel, which holds whole
 // 16-channel chunks, applies H16, the signs and 1/128 after the merge (both
@@ -170,9 +177,12 @@ __device__ __forceinline__ half2_t rope2(half2_t p, uint32_t csu) {
 // row of a query is chunk-major ([chunk][split][16]), so a merge workgroup
 // reads one contiguous 64-byte record per split.
 __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int split, int h, int n,
-                                              int q, float4_t acc[8], float m_run, float l_run) {
+                                              int q, float4_t acc[8], float m_run, float l_run,
+                                              float w_run) {
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
+  w_run += __shfl_xor(w_run, 16);
+  w_run += __shfl_xor(w_run, 32);
 #pragma unroll
   for (int hb = 1; hb < 8; hb <<= 1)
 #pragma unroll
@@ -182,6 +192,11 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
         acc[bt] = u + w;
         acc[bt | hb] = u - w;
       }
+  // the levels were hi = kappa * level + mu: remove mu * sum(P*norm) from every
+  // channel, which after H8 is 8 mu W on chunk 0 (the merge divides by kappa)
+  const float corr = 8.0f * a.level_mu * w_run;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[0][i] -= corr;
   if (n < a.G) {
     const int S = a.max_splits;
     const int64_t row = ((int64_t)b * a.h_kv + h) * a.G + n;
@@ -201,11 +216,10 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   constexpr int KQ = R / 4;                  // rank elements per lane in the K^T MFMA
   typedef _Float16 hvec_t __attribute__((ext_vector_type(KQ)));
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  // codebook levels of 4 codes (one VCODE byte) as exact fp16 head + remainder
-  // pairs: s_vlut[v] = {hr(c0), hr(c1), hr(c2), hr(c3)}, c_t = (v >> 2t) & 3 --
-  // the whole A operand of one P.V tile, read with one ds_read_b128 (static LDS:
-  // the byte index scales straight into the address)
-  __shared__ uint4 s_vlut[256];
+  // MFMA value levels (fp16 hi_c) of the 4 codes of one VCODE byte:
+  // s_vlut[v] = {lv(c0) | lv(c1) << 16, lv(c2) | lv(c3) << 16}, c_t = (v >> 2t) & 3
+  // (static LDS: the byte index scales straight into the address)
+  __shared__ uint2 s_vlut[256];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15;   // token within page (K side) / score column (softmax side)
@@ -253,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
       float4_t zero[8];
 #pragma unroll
       for (int bt = 0; bt < 8; ++bt) zero[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-      store_partial(a, b, split, h, n, q, zero, -INFINITY, 0.f);
+      store_partial(a, b, split, h, n, q, zero, -INFINITY, 0.f, 0.f);
     }
     return;
   }
@@ -307,11 +321,8 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   }
 
   if (tid < 256) {
-    auto hr = [&](int c) {
-      const _Float16 hd = (_Float16)a.codebook[c];
-      return half_bits(hd) | (half_bits((_Float16)(a.codebook[c] - (float)hd)) << 16);
-    };
-    s_vlut[tid] = make_uint4(hr(tid & 3), hr((tid >> 2) & 3), hr((tid >> 4) & 3), hr(tid >> 6));
+    auto lv = [&](int c) { return a.level_hi[c]; };
+    s_vlut[tid] = make_uint2(lv(tid & 3) | (lv((tid >> 2) & 3) << 16), lv((tid >> 4) & 3) | (lv(tid >> 6) << 16));
   }
 
   // ---- cos/sin recurrence state: this thread owns frequency j = tid & 63 at
@@ -360,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   float4_t acc[8];
 #pragma unroll
   for (int bt = 0; bt < 8; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f, w_run = 0.0f;
   const int my_slot = NSLOT > 1 ? n / SW : 0;   // page slot of this lane after compaction
   KresMasks km;
   km.init();
@@ -463,45 +474,54 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
         const float m_new = fmaxf(m_run, mx);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
+        w_run *= alpha;
 #pragma unroll
         for (int bt = 0; bt < 8; ++bt) acc[bt] *= alpha;
         m_run = m_new;
       }
-      // ---- P*norm as the B operand (tokens 4q..4q+3, each twice: head, remainder) ----
-      half8_t pd[NCR];
+      // ---- P*norm of the lane's page (its slot), tokens 4q..4q+3, fp16 ----
+      uint2 pd[NCR];
 #pragma unroll
       for (int r = 0; r < NCR; ++r) {
         const int pg = r * NSLOT + my_slot;
         const uint2 nr = *reinterpret_cast<const uint2*>(grp + pg * SHB + a.L.vnorm + h * 32 + q * 8);
         const float nv[4] = {half_bits_to_float(nr.x & 0xffff), half_bits_to_float(nr.x >> 16),
                              half_bits_to_float(nr.y & 0xffff), half_bits_to_float(nr.y >> 16)};
-        union { half2_t h2[4]; half8_t v; } pu;
+        float x[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float p = __builtin_amdgcn_exp2f(cr[r][i] - m_run);
           l_run += p;
-          const float x = p * nv[i];
-          pu.h2[i] = half2_t{(_Float16)x, (_Float16)x};
+          x[i] = p * nv[i];
         }
-        pd[r] = pu.v;
+        const half2_t h01 = {(_Float16)x[0], (_Float16)x[1]}, h23 = {(_Float16)x[2], (_Float16)x[3]};
+        const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
+        w_run = __builtin_amdgcn_fdot2(h23, one2, __builtin_amdgcn_fdot2(h01, one2, w_run, false), false);
+        pd[r] = make_uint2(as_u32(h01), as_u32(h23));
       }
-      // ---- P.V on MFMA, per page (B masked to the page's slot) ----
+      // ---- P.V on MFMA, two pages per product: K index 8q + j is token
+      // 4q + (j & 3) of page 2u + (j >> 2), so the A operand is the two pages'
+      // code bytes of the tile through the level table, and the B operand is the
+      // lane's own P*norm in the half of its page (zero for the other page) ----
 #pragma unroll
-      for (int pp = 0; pp < kGroupPages; ++pp) {
-        half8_t bp = pd[pp / NSLOT];
-        if constexpr (NSLOT > 1) {
-          if (my_slot != pp % NSLOT) bp = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-        const uint2 vc = vcd[pp];
-        union { uint4 e; half8_t v; } va[8];
+      for (int u = 0; u < kGroupPages / 2; ++u) {
+        const int pa = 2 * u, pb = 2 * u + 1;
+        const uint2 za = (NSLOT == 1 || my_slot == pa % NSLOT) ? pd[pa / NSLOT] : make_uint2(0u, 0u);
+        const uint2 zb = (NSLOT == 1 || my_slot == pb % NSLOT) ? pd[pb / NSLOT] : make_uint2(0u, 0u);
+        union { uint4 e; half8_t v; } bp;
+        bp.e = make_uint4(za.x, za.y, zb.x, zb.y);
+        const uint2 va_ = vcd[pa], vb_ = vcd[pb];
+        union { uint4 e; half8_t v; } av[8];
 #pragma unroll
         for (int bt = 0; bt < 8; ++bt) {
-          const uint32_t D = bt < 4 ? vc.x : vc.y;
-          va[bt].e = s_vlut[(D >> (8 * (bt & 3))) & 0xFFu];
+          const uint32_t Da = bt < 4 ? va_.x : va_.y, Db = bt < 4 ? vb_.x : vb_.y;
+          const uint2 la = s_vlut[(Da >> (8 * (bt & 3))) & 0xFFu];
+          const uint2 lb = s_vlut[(Db >> (8 * (bt & 3))) & 0xFFu];
+          av[bt].e = make_uint4(la.x, la.y, lb.x, lb.y);
         }
 #pragma unroll
         for (int bt = 0; bt < 8; ++bt)
-          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[bt].v, bp, acc[bt], 0, 0, 0);
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[bt].v, bp.v, acc[bt], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -523,6 +543,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[bt][i] += dpp_all<kRowRor + 4>(acc[bt][i]);
       l_run += dpp_all<kRowRor + 4>(l_run);
+      w_run += dpp_all<kRowRor + 4>(w_run);
     }
     if constexpr (NSLOT >= 2) {
 #pragma unroll
@@ -530,8 +551,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[bt][i] += dpp_all<kRowRor + 8>(acc[bt][i]);
       l_run += dpp_all<kRowRor + 8>(l_run);
+      w_run += dpp_all<kRowRor + 8>(w_run);
     }
-    store_partial(a, b, split, h, n, q, acc, m_run, l_run);
+    store_partial(a, b, split, h, n, q, acc, m_run, l_run, w_run);
   }
 }
 
@@ -562,6 +584,7 @@ struct CombineKArgs {
   int64_t ts_b, ts_h, ts_t;
   const int32_t* tail_len;
   uint32_t v_sign_bits[4];   // bit c set <=> value channel c carries Hadamard sign -1
+  float packed_scale;        // 1 / (128 kappa): Hadamard normalisation and the level scale
 };
 
 // Sum over the 16 lanes of a row (DPP-free butterfly; result in every lane).
@@ -731,7 +754,7 @@ __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineK
   }
   __syncthreads();
   if (tid < kChunk) {
-    // lane c: H16 over the chunk's channel bits 0-3, then sign and 1/128
+    // lane c: H16 over the chunk's channel bits 0-3, then sign and 1/(128 kappa)
     float y = s_fin[tid];
 #pragma unroll
     for (int hb = 1; hb < kChunk; hb <<= 1) {
@@ -739,7 +762,7 @@ __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineK
       y = (tid & hb) ? p - y : y + p;
     }
     const int cg = kChunk * ch + tid;
-    y = (sign_neg(a.v_sign_bits, cg) ? -y : y) * (1.0f / kD);
+    y = (sign_neg(a.v_sign_bits, cg) ? -y : y) * a.packed_scale;
     const float M = fmaxf(mp, mt);
     const float wp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
     const float wt = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - M);
@@ -789,6 +812,120 @@ static size_t ws_bytes(const bmx_k2b_decode_args* a, int splits) {
 extern "C" size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* a) {
   if (!a || a->batch < 1) return 0;
   return ws_bytes(a, choose_splits(a));
+}
+
+// ---------------------------------------------------------------------------
+// MFMA value levels.  The P.V product takes fp16 levels; plain rounding of the
+// codebook leaves a per-level error of up to 2^-11 relative that does not
+// average out over a long context.  Instead the levels are an affine image
+// hi_c = kappa * level_c + mu (kappa in [1/2, 2]) chosen so that all four are
+// fp16 numbers to within ~1e-6 relative: then sum_t w_t hi = kappa * (the exact
+// sum) + mu * sum_t w_t, and the kernels undo mu and kappa exactly.  The map is
+// found by a search over fp16 values for the two extreme levels (the two middle
+// levels follow) and cached per codebook.
+// ---------------------------------------------------------------------------
+struct LevelMap {
+  uint32_t hi[4];
+  float kappa, mu;
+  double err;   // max |hi_c - (kappa level_c + mu)| / max |kappa level|
+};
+
+static double round_half(double v) {   // nearest fp16 value (normal range), ties to even
+  return (double)(_Float16)v;
+}
+
+static uint32_t half_bits_host(double v) {
+  _Float16 h = (_Float16)v;
+  uint16_t u;
+  memcpy(&u, &h, 2);
+  return u;
+}
+
+static LevelMap search_level_map(const float cb[4]) {
+  LevelMap best{};
+  best.err = 1e30;
+  double L[4];
+  for (int c = 0; c < 4; ++c) L[c] = cb[c];
+  int ia = 0;
+  for (int c = 1; c < 4; ++c)
+    if (fabs(L[c]) > fabs(L[ia])) ia = c;
+  const int ib = (ia == 0) ? 3 : 0;   // the other extreme (levels ascend)
+  int io[2], k = 0;
+  for (int c = 0; c < 4; ++c)
+    if (c != ia && c != ib) io[k++] = c;
+  const double La = L[ia], Lb = L[ib], amax = fabs(La);
+  if (amax == 0.0 || La == Lb) {   // degenerate codebook: exact as it is
+    for (int c = 0; c < 4; ++c) best.hi[c] = half_bits_host(L[c]);
+    best.kappa = 1.f;
+    best.mu = 0.f;
+    best.err = 0.0;
+    return best;
+  }
+  const double mu_max = 0.25 * amax;
+  // g_a runs over the fp16 values of [amax/2, 2 amax] with the sign of La
+  const uint16_t lo_bits = (uint16_t)(half_bits_host(0.5 * amax) & 0x7fff);
+  const uint16_t hi_bits = (uint16_t)(half_bits_host(2.0 * amax) & 0x7fff);
+  for (uint32_t ub = lo_bits; ub <= hi_bits; ++ub) {
+    uint16_t u16 = (uint16_t)ub;
+    _Float16 hv;
+    memcpy(&hv, &u16, 2);
+    const double ga = La < 0 ? -(double)hv : (double)hv;
+    // mu = ga - kappa La within +-mu_max: kappa range, then the g_b range
+    double k0 = (ga - mu_max) / La, k1 = (ga + mu_max) / La;
+    if (k0 > k1) std::swap(k0, k1);
+    k0 = std::max(k0, 0.5);
+    k1 = std::min(k1, 2.0);
+    if (k0 > k1) continue;
+    double gb0 = ga + k0 * (Lb - La), gb1 = ga + k1 * (Lb - La);
+    if (gb0 > gb1) std::swap(gb0, gb1);
+    // walk the fp16 grid over [gb0, gb1]
+    double g = round_half(gb0);
+    for (int guard = 0; g <= gb1 && guard < 1 << 16; ++guard) {
+      const double kap = (g - ga) / (Lb - La), mu = ga - kap * La;
+      if (kap >= 0.5 && kap <= 2.0 && fabs(mu) <= mu_max && fabs(g) >= 6.2e-5) {
+        double e = 0.0;
+        for (int j = 0; j < 2; ++j) {
+          const double v = kap * L[io[j]] + mu;
+          e = std::max(e, fabs(v - round_half(v)));
+        }
+        e /= kap * amax;
+        if (e < best.err) {
+          best.err = e;
+          best.kappa = (float)kap;
+          best.mu = (float)mu;
+          for (int c = 0; c < 4; ++c) best.hi[c] = half_bits_host(kap * L[c] + mu);
+        }
+      }
+      // next fp16 value above g
+      _Float16 gh = (_Float16)g;
+      uint16_t gu;
+      memcpy(&gu, &gh, 2);
+      if (g >= 0) ++gu; else --gu;
+      if ((gu & 0x7fff) == 0 && g < 0) gu = 0;
+      memcpy(&gh, &gu, 2);
+      g = (double)gh;
+    }
+  }
+  return best;
+}
+
+static LevelMap level_map(const float cb[4]) {
+  struct Entry {
+    float cb[4];
+    LevelMap m;
+  };
+  static std::mutex mu;
+  static Entry cache[8];
+  static int n_cached = 0, next_slot = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_cached; ++i)
+    if (memcmp(cache[i].cb, cb, sizeof(cache[i].cb)) == 0) return cache[i].m;
+  Entry& e = cache[next_slot];
+  memcpy(e.cb, cb, sizeof(e.cb));
+  e.m = search_level_map(cb);
+  next_slot = (next_slot + 1) % 8;
+  n_cached = std::min(n_cached + 1, 8);
+  return e.m;
 }
 
 static int fail(int code, const std::string& msg) {
@@ -874,7 +1011,15 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
     k.step8_c[j] = (float)cos(step / 8.0);
     k.step8_s[j] = (float)sin(step / 8.0);
   }
-  for (int j = 0; j < 4; ++j) k.codebook[j] = a->codebook[j];
+  for (int j = 0; j < 4; ++j)
+    if (!(a->codebook[j] == a->codebook[j]) || (j > 0 && !(a->codebook[j] > a->codebook[j - 1])))
+      return fail(BMX_E_INVALID, "bmx_k2b_decode: codebook must be 4 finite ascending levels");
+  const LevelMap lm = level_map(a->codebook);
+  if (lm.err > 4e-6)
+    return fail(BMX_E_INVALID, "bmx_k2b_decode: no fp16 level map for this codebook (error " +
+                                   std::to_string(lm.err) + ")");
+  for (int j = 0; j < 4; ++j) k.level_hi[j] = lm.hi[j];
+  k.level_mu = lm.mu;
   const size_t smem = (size_t)2 * kCsBuf * 4 + (size_t)2 * kGroupPages * k.shared_bytes;
   dim3 grid(max_splits, a->batch);
   hipError_t e = g.rank == 32 ? launch_split<32>(k, grid, smem, st)
@@ -895,6 +1040,7 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
   c.tail_len = a->tail_len;
   for (int j = 0; j < 4; ++j) c.v_sign_bits[j] = a->v_sign_bits[j];
+  c.packed_scale = (float)(1.0 / (kD * (double)lm.kappa));
   hipLaunchKernelGGL(k2b_combine_kernel, dim3(kChunks, g.h_kv * g.n_q_groups, a->batch), dim3(kCmbThreads),
                      0, st, c);
   e = hipGetLastError();

@@ -301,6 +301,46 @@ def test_decode_query_group_sizes(G):
     _close(out, ref.view(1, h_kv, G, 128), f"G {G}")
 
 
+@pytest.mark.parametrize("levels", [(-1.5104, -0.4528, 0.4528, 1.5104),
+                                    (-1.9, -0.37, 0.52, 1.23)])
+def test_decode_other_codebooks(levels):
+    """The P.V product takes fp16 levels chosen as an affine image of the
+    codebook (exact to ~1e-7) and undoes the map; any ascending codebook must
+    match the fp32 oracle's dequantization cb[idx] (codecs.py:639-649).  The
+    first set is the analytic 2-bit Lloyd codebook, the second an asymmetric one."""
+    import dataclasses
+    import math
+    gen = torch.Generator().manual_seed(40)
+    h_kv, rank, S, T = 2, 32, 4096, 64
+    k_pre = synth.k2b_keys(h_kv, S + T, rank, gen)
+    v = synth.values(h_kv, S + T, gen)
+    svd = synth.first_page_svd(k_pre, rank)
+    consts = k2b.CodecConsts.make(v_seed=3)
+    pool = synth.PagePool(S // 16, h_kv, rank, DEV, gen=gen)
+    seq = synth.encode_sequence(pool, k_pre[:, :S].to(DEV), v[:, :S].to(DEV), rank, consts, svd=svd)
+    cache = _oracle_cache(k_pre[:, :S], v[:, :S], rank, svd, v_seed=3)
+    inv = torch.tensor(consts.inv_freq)
+    cos, sin = A.rope_cos_sin(inv, torch.arange(S))
+    K = A.apply_rope(cache.dense_k_pre(), cos, sin)
+    cb = torch.tensor(levels, dtype=torch.float32)
+    Vs = []
+    for (idx, norms), _, _ in cache.v_blocks:   # fwht(cb[idx]/sqrt(d)) * signs * norm
+        Mq = (cb[idx.long()] / math.sqrt(128)).reshape(-1, h_kv, 128)
+        rec = OC.unrotate(Mq.reshape(-1, 128), 3).reshape(-1, h_kv, 128)
+        Vs.append(OC.from_matrix((rec * norms[:, :, None]).reshape(-1, h_kv * 128), h_kv))
+    V = torch.cat(Vs, dim=1)
+    cos_t, sin_t = A.rope_cos_sin(inv, torch.arange(S, S + T))
+    k_tail = A.apply_rope(k_pre[:, S:].float(), cos_t, sin_t).half()
+    v_tail = v[:, S:]
+    K = torch.cat([K, k_tail.float()], dim=1)
+    V = torch.cat([V, v_tail.float()], dim=1)
+    q = torch.randn(1, h_kv, 4, 128, generator=gen)
+    out = _decode_one(seq, pool, q, dataclasses.replace(consts, codebook=tuple(levels)), rank,
+                      k_tail, v_tail)
+    ref = A.naive_dense_attention(q.view(h_kv * 4, 1, 128), K, V, 4, 128 ** -0.5)
+    _close(out, ref.view(1, h_kv, 4, 128), f"codebook {levels}")
+
+
 def test_decode_window_only_and_long_window():
     """No committed tokens (the fp16 window alone), and a 1100-token window
     (three 512-token passes of the combine) over 1024 committed tokens."""
