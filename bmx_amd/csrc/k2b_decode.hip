@@ -59,12 +59,14 @@ constexpr int kCsRow = 68;                  // dwords per position row of the co
                                             // (64 + 4: rows start 4 banks apart)
 constexpr int kCsBuf = kGroup * kCsRow;     // dwords per group table
 constexpr int kPidWindow = 64;              // page ids held per lane-vector
+constexpr int kCsMaxBufs = 8;               // RoPE table buffers at most (17 KB each)
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 struct DecodeKArgs {
   int h_kv, G, max_splits, max_pages, max_packed_len, n_pool;
   int shared_bytes;    // page prefix read by every head: US, VNORM, KSCALE (multiple of 16)
+  int cs_bufs;         // RoPE table buffers in LDS (groups produced in the prologue)
   const float* q;
   float* ws_acc;       // [B][h_kv][G][8][max_splits][16] accumulators (H8 applied)
   float* ws_ml;        // [B][h_kv][G][max_splits][2]     (running max, sum), base 2
@@ -103,22 +105,6 @@ constexpr int kRowRor = 0x120;  // + n: rotate within the row
 template <int CTRL>
 __device__ __forceinline__ float dpp_all(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
-}
-
-// Query fragments of the packed pages: chunk bb holds the RoPE pairs
-// B[8q + 2i + e][n] = q_n[16bb + 4q + i + 64e] (i < 4, e < 2), the order in
-// which the key pairs leave the rotation; column n is query n (zero if n >= G).
-__device__ __forceinline__ void load_query_pairs(const DecodeKArgs& a, int b, int h, int n, int q,
-                                                 half8_t qf[4]) {
-  const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
-  const float sc = (n < a.G) ? a.qscale_rope : 0.0f;
-#pragma unroll
-  for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      qf[bb][2 * i] = (_Float16)(qrow[16 * bb + 4 * q + i] * sc);
-      qf[bb][2 * i + 1] = (_Float16)(qrow[16 * bb + 4 * q + i + 64] * sc);
-    }
 }
 
 // The masks arrive in VGPRs (KresMasks) so each half pair is one v_and_or_b32.
@@ -228,19 +214,10 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const bool active = wave < a.h_kv;
   const int h = active ? wave : 0;
 
-  // ---- loads that depend on nothing: basis fragments, query ----
-  hvec_t vh[8];
-  const uint16_t* basis = a.basis + (int64_t)b * a.basis_stride;
-#pragma unroll
-  for (int bt = 0; bt < 8; ++bt)
-    vh[bt] = *reinterpret_cast<const hvec_t*>(basis + (int64_t)(h * kD + 16 * bt + n) * R + KQ * q);
-  half8_t qf[4];
-  load_query_pairs(a, b, h, n, q, qf);
-
-  // Balanced static partition of the sequence's 64-token groups over the
-  // max_splits workgroups.  The page-table read is issued for the host bound
-  // max_packed_len before the device length arrives, and redone in the rare
-  // case that the sequence is shorter.
+  // ---- every load that depends only on the arguments is issued first, the
+  // page-table read first of all, and nothing is used before the first group's
+  // page loads are in flight (a wait on one load waits on all earlier ones) ----
+  const int fj = tid & 63;   // RoPE frequency this thread produces
   const int S = a.max_splits;
   const int len_spec = a.max_packed_len & ~(kGroup - 1);
   auto range = [&](int L, int& r0, int& r1) {
@@ -251,15 +228,40 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   int g0, g1;
   range(len_spec, g0, g1);
   const int32_t* ptab_row = a.page_table + (int64_t)b * a.max_pages;
-  auto load_ids = [&](int first, int count) {   // ids of pages first .. first+63 of the range
-    if (count <= 0) return 0;                    // uniform: an empty range reads nothing
-    return (int)clamp_page(ptab_row[g0 * kGroupPages + min(first + lane, count - 1)], a.n_pool);
+  // Balanced static partition of the sequence's 64-token groups over the
+  // max_splits workgroups.  The page-table read is issued for the host bound
+  // max_packed_len before the device length arrives, and redone in the rare
+  // case that the sequence is shorter.
+  // ids of pages first .. first+63 of the range; an empty range reads the
+  // (valid) length word instead, so the load has no branch to wait in
+  auto load_ids_raw = [&](int first, int count) {
+    const int32_t* src = count > 0 ? ptab_row + g0 * kGroupPages + min(first + lane, count - 1)
+                                   : a.packed_len + b;
+    return (int)*src;
   };
-  int pidv = load_ids(0, (g1 - g0) * kGroupPages);
-  const int len = min(a.packed_len[b], a.max_packed_len) & ~(kGroup - 1);
+  const int pid_raw = load_ids_raw(0, (g1 - g0) * kGroupPages);
+  const int len_raw = a.packed_len[b];
+  const float fq = a.inv_freq[fj];
+  const float c8 = a.step8_c[fj], s8 = a.step8_s[fj];
+  const float stc = a.step_c[fj], sts = a.step_s[fj];
+  hvec_t vh[8];
+  const uint16_t* basis = a.basis + (int64_t)b * a.basis_stride;
+#pragma unroll
+  for (int bt = 0; bt < 8; ++bt)
+    vh[bt] = *reinterpret_cast<const hvec_t*>(basis + (int64_t)(h * kD + 16 * bt + n) * R + KQ * q);
+  float4_t qraw[8];   // q_n[16bb + 4q .. +3] (u = bb) and [.. + 64] (u = 4 + bb)
+  {
+    const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      qraw[u] = *reinterpret_cast<const float4_t*>(qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2));
+  }
+
+  int pidv = (int)clamp_page(pid_raw, a.n_pool);
+  const int len = min(len_raw, a.max_packed_len) & ~(kGroup - 1);
   if (len != len_spec) {
     range(len, g0, g1);
-    pidv = load_ids(0, (g1 - g0) * kGroupPages);
+    pidv = (int)clamp_page(load_ids_raw(0, (g1 - g0) * kGroupPages), a.n_pool);
   }
   const int n_groups = g1 - g0;
   if (n_groups == 0) {  // nothing packed here; an empty partial keeps the merge blind
@@ -271,6 +273,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     }
     return;
   }
+  auto load_ids = [&](int first, int count) { return (int)clamp_page(load_ids_raw(first, count), a.n_pool); };
   const int t_begin = g0 * kGroup;
   const int C = kD * a.h_kv;
   const int quarter = C / 4;
@@ -279,8 +282,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const int sh_chunks = SHB / 4;       // 16-byte chunks of the 4 pages' prefixes
   const int chunks_pp = SHB / 16;
   // dynamic LDS: the two cos/sin tables, then the prefix ring
-  uint32_t* cst = reinterpret_cast<uint32_t*>(smem);                            // [2][64][kCsRow]
-  uint8_t* ring = smem + 2 * kCsBuf * 4;                                        // [2][4][SHB]
+  const int cs_bufs = a.cs_bufs;
+  uint32_t* cst = reinterpret_cast<uint32_t*>(smem);                            // [cs_bufs][64][kCsRow]
+  uint8_t* ring = smem + cs_bufs * kCsBuf * 4;                                  // [2][4][SHB]
   const int n_pages = n_groups * kGroupPages;
 
   // page ids of the range, a window of 64 per lane-vector
@@ -289,13 +293,13 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     const int id = __builtin_amdgcn_readlane(pidv, gi * kGroupPages + pp - pid_base);
     return a.pages + (int64_t)id * pb;
   };
-  auto load_prefix = [&](int gi) -> uint4 {                   // thread tid's 16 B of the prefixes
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    const int pp = min(tid / chunks_pp, kGroupPages - 1);
+  // thread tid's 16 B of the prefixes (threads past the last chunk re-read the
+  // last one: an unconditional load leaves no branch to wait in)
+  auto load_prefix = [&](int gi) -> uint4 {
+    const int c = min(tid, sh_chunks - 1);
+    const int pp = c / chunks_pp;
     const int id = __shfl(pidv, gi * kGroupPages + pp - pid_base);
-    if (tid < sh_chunks)
-      v = *reinterpret_cast<const uint4*>(a.pages + (int64_t)id * pb + (tid - pp * chunks_pp) * 16);
-    return v;
+    return *reinterpret_cast<const uint4*>(a.pages + (int64_t)id * pb + (c - pp * chunks_pp) * 16);
   };
   auto store_prefix = [&](uint4 v, int slot) {
     if (tid < sh_chunks) *reinterpret_cast<uint4*>(ring + slot * kGroupPages * SHB + tid * 16) = v;
@@ -321,50 +325,63 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   }
 
   if (tid < 256) {
-    auto lv = [&](int c) { return a.level_hi[c]; };
+    const uint32_t l0 = a.level_hi[0], l1 = a.level_hi[1], l2 = a.level_hi[2], l3 = a.level_hi[3];
+    auto lv = [&](int c) { return c == 0 ? l0 : c == 1 ? l1 : c == 2 ? l2 : l3; };
     s_vlut[tid] = make_uint2(lv(tid & 3) | (lv((tid >> 2) & 3) << 16), lv((tid >> 4) & 3) | (lv(tid >> 6) << 16));
   }
 
-  // ---- cos/sin recurrence state: this thread owns frequency j = tid & 63 at
-  // group-local positions tl = wave + 8k, k < 8 ----
-  const int fj = tid & 63;
-  const float fq = a.inv_freq[fj];
-  float cc[8], ss[8];
+  // query fragments of the packed pages: chunk bb holds the RoPE pairs
+  // B[8q + 2i + e][n] = q_n[16bb + 4q + i + 64e] (i < 4, e < 2), the order in
+  // which the key pairs leave the rotation; column n is query n (zero if n >= G)
+  half8_t qf[4];
   {
-    // one exact-angle start per thread, then 8-position steps: the angle in
-    // revolutions (exact product, scaled in double), its fraction, and the
-    // hardware sin/cos of revolutions
-    const double rev = (double)fq * (double)(t_begin + wave) * 0.15915494309189535;
+    const float sc = (n < a.G) ? a.qscale_rope : 0.0f;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qf[bb][2 * i] = (_Float16)(qraw[bb][i] * sc);
+        qf[bb][2 * i + 1] = (_Float16)(qraw[4 + bb][i] * sc);
+      }
+  }
+
+  // ---- RoPE table: fp16 (cos, sin) of HF's angle fl(fq * pos) for 64
+  // positions per group, row = position, column = frequency, one LDS buffer per
+  // group for the first cs_bufs groups, all written here, where the wave would
+  // otherwise wait for the first pages.  This thread owns frequency j = tid & 63
+  // at group-local positions wave + 8k, k < 8.  Angles: one exact start (the
+  // angle in revolutions from the exact product, scaled in double; its
+  // fraction; the hardware sin/cos of revolutions), then 8-position and
+  // 64-position rotation steps, each value corrected to the fp32 angle ----
+  auto produce_groups = [&](int g_first, int count, int buf_first) {
+    float cc[8], ss[8];
+    const double rev = (double)fq * (double)(t_begin + g_first * kGroup + wave) * 0.15915494309189535;
     const float fr = (float)(rev - floor(rev));
     cc[0] = __builtin_amdgcn_cosf(fr);
     ss[0] = __builtin_amdgcn_sinf(fr);
-    const float c8 = a.step8_c[fj], s8 = a.step8_s[fj];
 #pragma unroll
     for (int k = 1; k < 8; ++k) {
       cc[k] = cc[k - 1] * c8 - ss[k - 1] * s8;
       ss[k] = ss[k - 1] * c8 + cc[k - 1] * s8;
     }
-  }
-  const float stc = a.step_c[fj], sts = a.step_s[fj];
-  // fp16 (cos, sin) of HF's angle fl(fq * pos) for the group's 64 positions,
-  // row = position, column = frequency; then step the state by 64 positions
-  auto produce_cs = [&](int gi, int buf) {
-    uint32_t* dst = cst + buf * kCsBuf;
+    for (int g = 0; g < count; ++g) {
+      uint32_t* dst = cst + ((buf_first + g) % cs_bufs) * kCsBuf;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int tl = wave + 8 * k;
-      const float tf = (float)(t_begin + gi * kGroup + tl);
-      const float ang = fq * tf;
-      const float e = __builtin_fmaf(fq, tf, -ang);  // exact: fq*tf - fl(fq*tf)
-      const half2_t v = {(_Float16)__builtin_fmaf(ss[k], e, cc[k]),
-                         (_Float16)__builtin_fmaf(-cc[k], e, ss[k])};
-      dst[tl * kCsRow + fj] = as_u32(v);
-      const float cn = cc[k] * stc - ss[k] * sts;
-      ss[k] = ss[k] * stc + cc[k] * sts;
-      cc[k] = cn;
+      for (int k = 0; k < 8; ++k) {
+        const int tl = wave + 8 * k;
+        const float tf = (float)(t_begin + (g_first + g) * kGroup + tl);
+        const float ang = fq * tf;
+        const float e = __builtin_fmaf(fq, tf, -ang);  // exact: fq*tf - fl(fq*tf)
+        const half2_t v = {(_Float16)__builtin_fmaf(ss[k], e, cc[k]),
+                           (_Float16)__builtin_fmaf(-cc[k], e, ss[k])};
+        dst[tl * kCsRow + fj] = as_u32(v);
+        const float cn = cc[k] * stc - ss[k] * sts;
+        ss[k] = ss[k] * stc + cc[k] * sts;
+        cc[k] = cn;
+      }
     }
   };
-  produce_cs(0, 0);
+  produce_groups(0, min(n_groups, cs_bufs), 0);
   store_prefix(pre, 0);
 
   // ---- per-wave state ----
@@ -376,6 +393,11 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   KresMasks km;
   km.init();
   __syncthreads();   // LUT, table 0 and prefix slot 0 are visible
+  // Group 0's codes must have landed before the loop: the compiler's wait
+  // tracking merges the loop entry with the back edge, and a load still pending
+  // on a current-group register at entry would make every group's key side wait
+  // on the next group's loads (issued at the top of the same group).
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
 
   for (int gi = 0; gi < n_groups; ++gi) {
     const int gn = min(gi + 1, n_groups - 1);   // group fetched during this one
@@ -394,11 +416,12 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
         vcd_n[pp] = load_vcode(gn, pp);
       }
     }
-    if (gi + 1 < n_groups) produce_cs(gi + 1, (gi + 1) & 1);
+    // groups past the prologue's tables: refill the buffer group gi-1 left
+    if (gi > 0 && gi - 1 + cs_bufs < n_groups) produce_groups(gi - 1 + cs_bufs, 1, gi - 1);
 
     if (active) {
       const uint8_t* grp = ring + (gi & 1) * kGroupPages * SHB;
-      const uint32_t* csb = cst + (gi & 1) * kCsBuf;
+      const uint32_t* csb = cst + (gi % cs_bufs) * kCsBuf;
       // key-residual scale pairs (s_j, s_{j+64}), j = 16bb + 4q + i: 16 bytes
       // per bb in the group's prefix (re-read per page: fewer live VGPRs)
       const uint8_t* scl[4];
@@ -1020,7 +1043,10 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
                                    std::to_string(lm.err) + ")");
   for (int j = 0; j < 4; ++j) k.level_hi[j] = lm.hi[j];
   k.level_mu = lm.mu;
-  const size_t smem = (size_t)2 * kCsBuf * 4 + (size_t)2 * kGroupPages * k.shared_bytes;
+  // RoPE tables for every group a workgroup owns, up to kCsMaxBufs
+  const int max_groups = ((a->max_packed_len / kGroup) + max_splits - 1) / max_splits;
+  k.cs_bufs = std::max(1, std::min(max_groups, kCsMaxBufs));
+  const size_t smem = (size_t)k.cs_bufs * kCsBuf * 4 + (size_t)2 * kGroupPages * k.shared_bytes;
   dim3 grid(max_splits, a->batch);
   hipError_t e = g.rank == 32 ? launch_split<32>(k, grid, smem, st)
                               : launch_split<16>(k, grid, smem, st);
