@@ -71,6 +71,7 @@ class AppendArgs(ct.Structure):
         ("pages", ct.c_void_p),
         ("n_pool_pages", ct.c_int32),
         ("page_ids", ct.c_void_p),
+        ("v_dtype", ct.c_int32),
     ]
 
 

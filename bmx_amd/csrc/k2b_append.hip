@@ -20,8 +20,9 @@ struct AppendKArgs {
   int h_kv, R, n_codec_pages, n_pool;
   const uint16_t* k_pre;
   int64_t ksh, kst;
-  const uint16_t* v;
+  const void* v;
   int64_t vsh, vst;
+  int v_dtype;         // BMX_K2B_F16 / F32 / BF16
   const float* basis32;
   const uint16_t* basis16;
   const float* us_first;
@@ -145,7 +146,15 @@ __global__ __launch_bounds__(256) void k2b_v_kernel(const AppendKArgs a) {
 
   for (int e = tid; e < kPT * kD; e += 256) {
     const int t = e / kD, c = e % kD;
-    x[t][c] = half_bits_to_float(a.v[h * a.vsh + (int64_t)(pg * kPT + t) * a.vst + c]);
+    const int64_t i = h * a.vsh + (int64_t)(pg * kPT + t) * a.vst + c;
+    float val;
+    if (a.v_dtype == BMX_K2B_F32)
+      val = static_cast<const float*>(a.v)[i];
+    else if (a.v_dtype == BMX_K2B_BF16)
+      val = __uint_as_float((uint32_t)static_cast<const uint16_t*>(a.v)[i] << 16);
+    else
+      val = half_bits_to_float(static_cast<const uint16_t*>(a.v)[i]);
+    x[t][c] = val;
   }
   __syncthreads();
   // norms: one thread per token, in the order torch's CPU 2-norm reduces a
@@ -231,7 +240,9 @@ extern "C" int bmx_k2b_append(const bmx_k2b_append_args* a, void* stream) {
   AppendKArgs k{};
   k.h_kv = g.h_kv; k.R = g.rank; k.n_codec_pages = a->n_codec_pages;
   k.k_pre = a->k_pre; k.ksh = a->k_stride_h; k.kst = a->k_stride_t;
-  k.v = a->v; k.vsh = a->v_stride_h; k.vst = a->v_stride_t;
+  if (a->v_dtype != BMX_K2B_F16 && a->v_dtype != BMX_K2B_F32 && a->v_dtype != BMX_K2B_BF16)
+    return afail(BMX_E_INVALID, "bmx_k2b_append: v_dtype must be BMX_K2B_F16, _F32 or _BF16");
+  k.v = a->v; k.vsh = a->v_stride_h; k.vst = a->v_stride_t; k.v_dtype = a->v_dtype;
   k.basis32 = a->basis32; k.basis16 = a->basis16; k.us_first = a->us_first;
   k.pages = a->pages; k.page_ids = a->page_ids; k.n_pool = a->n_pool_pages;
   k.L = PageLayout::make(g.h_kv, g.rank);

@@ -18,6 +18,7 @@ from . import codecs as K
 
 HEAD_DIM = 128
 PAGE_TOKENS = 16
+_V_DTYPES = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}   # BMX_K2B_F16 / F32 / BF16
 GROUP = 64
 CODEC_PAGE = 128
 
@@ -66,12 +67,14 @@ def page_bytes(h_kv: int, rank: int) -> int:
 def append(k_pre: torch.Tensor, v: torch.Tensor, basis32: torch.Tensor, basis16: torch.Tensor,
            pages: torch.Tensor, page_ids: torch.Tensor, consts: CodecConsts, *, rank: int,
            us_first: torch.Tensor | None = None) -> None:
-    """Encode n codec pages (k_pre/v: (h_kv, 128n, 128) fp16 views, last dim
+    """Encode n codec pages (k_pre: (h_kv, 128n, 128) fp16, v: same shape in fp16,
+    bf16 or fp32 -- values are encoded from their own precision; last dims
     contiguous) into the 8n physical pages listed in page_ids (int32, device)."""
     h_kv, T, d = k_pre.shape
     _need(d == HEAD_DIM and T % CODEC_PAGE == 0, "k_pre must be (h_kv, 128*n, 128)")
     _need(v.shape == k_pre.shape, "v must match k_pre")
-    _need(k_pre.dtype == torch.float16 and v.dtype == torch.float16, "k_pre/v must be fp16")
+    _need(k_pre.dtype == torch.float16, "k_pre must be fp16")
+    _need(v.dtype in _V_DTYPES, "v must be fp16, bf16 or fp32")
     _need(k_pre.stride(2) == 1 and v.stride(2) == 1, "k_pre/v last dim must be contiguous")
     n = T // CODEC_PAGE
     C = h_kv * HEAD_DIM
@@ -94,6 +97,7 @@ def append(k_pre: torch.Tensor, v: torch.Tensor, basis32: torch.Tensor, basis16:
     a.codebook[:] = consts.codebook
     a.v_sign_bits[:] = consts.sign_bits
     a.pages, a.page_ids, a.n_pool_pages = _ptr(pages), _ptr(page_ids), pages.shape[0]
+    a.v_dtype = _V_DTYPES[v.dtype]
     _lib.check(_lib.lib().bmx_k2b_append(ct.byref(a), _stream(pages.device)), "bmx_k2b_append")
 
 

@@ -1,0 +1,48 @@
+"""Codec specification and the recipe registry subset this path serves.
+
+Mirrors the reference's ``CacheCodecSpec`` (cache/specs.py:13-91) field for
+field where the k2b path reads them, and ``spec_pair`` (cache/recipes.py:13-42)
+for the ``k2b_ph`` recipe -- the one recipe the MI355X kernels implement (K:
+pre-RoPE ``lowrank_rtn_channel`` 3-bit residual, rank 16 or 32, 64-token scale
+groups; V: ``turboquant_mse_perhead`` 2-bit).  Every other recipe name raises,
+naming the recipe: there is no CPU or slow path to route it to.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+
+@dataclasses.dataclass
+class CacheCodecSpec:
+    """Codec specification for one side (K or V) of the KV cache
+    (cache/specs.py:13-91).  Only the fields the k2b path reads are kept."""
+
+    arm: str = "fp16"
+    bits: int = 3
+    rank: int = 0
+    group: int = 64
+    seed: int = 0
+    pre_rope: bool = False
+
+
+def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0):
+    """(k_spec, v_spec) for a named recipe (cache/recipes.py:13-42)."""
+    if arm != "k2b_ph":
+        raise NotImplementedError(
+            f"recipe {arm!r} has no MI355X kernels; this package implements 'k2b_ph' only")
+    return (CacheCodecSpec(arm="lowrank_rtn_channel", bits=3, rank=rank, group=group, seed=seed,
+                           pre_rope=True),
+            CacheCodecSpec(arm="turboquant_mse_perhead", bits=2, seed=seed))
+
+
+def check_k2b(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
+    """Raise unless (k_spec, v_spec) is a k2b pair the kernels implement."""
+    ok = (k_spec.arm == "lowrank_rtn_channel" and k_spec.bits == 3 and k_spec.group == 64
+          and k_spec.pre_rope and k_spec.rank in (16, 32)
+          and v_spec.arm == "turboquant_mse_perhead" and v_spec.bits == 2)
+    if not ok:
+        raise NotImplementedError(
+            f"the MI355X k2b path implements K=lowrank_rtn_channel (3 bits, group 64, "
+            f"pre-RoPE, rank 16|32) with V=turboquant_mse_perhead (2 bits); got "
+            f"K={k_spec} V={v_spec}")

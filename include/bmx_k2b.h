@@ -50,6 +50,10 @@ extern "C" {
 #define BMX_K2B_GROUP 64
 #define BMX_K2B_CODEC_PAGE 128
 
+#define BMX_K2B_F16 0
+#define BMX_K2B_F32 1
+#define BMX_K2B_BF16 2
+
 #define BMX_OK 0
 #define BMX_E_INVALID 1     /* bad argument (shape, pointer, unsupported geometry) */
 #define BMX_E_WORKSPACE 2   /* workspace missing or too small */
@@ -151,7 +155,7 @@ typedef struct {
                                  h*k_stride_h + t*k_stride_t + j, t in [0, 128*n) */
   int64_t k_stride_h;
   int64_t k_stride_t;
-  const uint16_t* v;          /* device fp16 values, same indexing */
+  const void* v;              /* device values, same indexing, element type v_dtype */
   int64_t v_stride_h;
   int64_t v_stride_t;
   const float* basis32;       /* device fp32 [C][R] frozen basis (projection) */
@@ -163,6 +167,9 @@ typedef struct {
   int32_t n_pool_pages;       /* pages in the pool (ids are clamped into range) */
   const int32_t* page_ids;    /* device [n_codec_pages*8] physical page of each
                                  16-token page, in token order */
+  int32_t v_dtype;            /* BMX_K2B_F16 (0), BMX_K2B_F32 or BMX_K2B_BF16: values are
+                                 encoded from the model's own precision, as the
+                                 reference's .float() of the value slab */
 } bmx_k2b_append_args;
 
 int bmx_k2b_append(const bmx_k2b_append_args* args, void* stream);

@@ -1,0 +1,79 @@
+"""CPU stand-in for the three kernels under the product cache's host logic
+(test infrastructure only).
+
+``OracleLayer`` subclasses bmx_amd.cache.PackedStreamingLayer and keeps its
+``update`` -- flush schedule, pre-RoPE stash and slab pruning, blended
+bits-per-entry -- while the encode, decode and prefill steps run the CPU oracle
+(the reference's codec and attention restated, oracle/): codes per committed
+codec page, keys dequantized and rotated with fp16-cast RoPE tables
+(packed_streaming.py:79-113, chunked_attention.py:148-189), one softmax over
+committed + recent tokens.  ``v_fp16`` encodes values from their fp16 rounding,
+as the product's write kernel does."""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from bmx_amd import cache as product
+from oracle import attention as A
+from oracle import codecs as OC
+
+
+class OracleLayer(product.PackedStreamingLayer):
+    v_fp16 = False
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        self._oc = A.K2bOracleCache(self._h_kv, self._d_head, self._rank, v_seed=self.v_spec.seed)
+
+    def _commit(self, k_pre, v):
+        for p in range(k_pre.shape[1] // product.PAGE):
+            sl = slice(p * product.PAGE, (p + 1) * product.PAGE)
+            vp = v[:, sl].half().float() if self.v_fp16 else v[:, sl].float()
+            self._oc.commit(k_pre[:, sl].cpu(), vp.cpu())
+
+    def _kv(self, dtype):
+        P = self._committed_S_q
+        ks, vs = [], []
+        if P:
+            cos, sin = product._rope_tables(self._inv_freq, self._rope_scaling, 0, P, "cpu")
+            ks.append(A.apply_rope(self._oc.dense_k_pre(), cos.float(), sin.float()).to(dtype))
+            vs.append(self._oc.dense_v().to(dtype))
+        if self.keys is not None and self.keys.numel():
+            ks.append(self.keys.squeeze(0).to(dtype))
+            vs.append(self.values.squeeze(0).to(dtype))
+        return torch.cat(ks, dim=1), torch.cat(vs, dim=1)
+
+    def attend(self, q, scaling, is_causal=False, attention_mask=None):
+        if q.device.type != "cpu":   # model on a GPU: the oracle attends on the host
+            keys, values = self.keys, self.values
+            self.keys, self.values = keys.cpu(), values.cpu()
+            try:
+                out = self.attend(q.cpu(), scaling, is_causal,
+                                  None if attention_mask is None else attention_mask.cpu())
+            finally:
+                self.keys, self.values = keys, values
+            return out.to(q.device)
+        n_heads, n_q, d = q.shape
+        G = n_heads // self._h_kv
+        Kd, Vd = self._kv(q.dtype)
+        if n_q == 1 and not is_causal:
+            return A.naive_dense_attention(q.float(), Kd, Vd, G, scaling).to(q.dtype)
+        Kx, Vx = Kd.repeat_interleave(G, dim=0), Vd.repeat_interleave(G, dim=0)
+        causal = is_causal and n_q > 1
+        return F.scaled_dot_product_attention(
+            q.unsqueeze(0), Kx.unsqueeze(0), Vx.unsqueeze(0), attn_mask=attention_mask,
+            is_causal=causal and attention_mask is None, scale=scaling).squeeze(0)
+
+
+class OracleCache(product.PackedStreamingCache):
+    def __init__(self, *args, v_fp16=False, **kwargs):
+        super().__init__(*args, **kwargs)
+
+        def _make_layer():
+            lay = OracleLayer(self.k_spec, self.v_spec, self.model_config, self.recent_window)
+            lay.v_fp16 = v_fp16
+            return lay
+
+        self._make_layer = _make_layer

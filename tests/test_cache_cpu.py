@@ -1,0 +1,123 @@
+"""Host side of the PackedStreamingCache mirror (no GPU): recipe specs, the
+bits-per-entry accounting against the reference's own end-to-end fixture,
+attach/detach bookkeeping, and the fail-loud rule (no CPU attention path)."""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from bmx_amd import codecs as K
+from bmx_amd.cache import ATTN_NAME, PackedStreamingCache, resolve_decoder_layers
+from bmx_amd.specs import CacheCodecSpec, check_k2b, spec_pair
+
+GOLD = Path(__file__).parent / "golden"
+
+
+def tiny_config():
+    from transformers import LlamaConfig
+
+    return LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                       num_attention_heads=4, num_key_value_heads=2, head_dim=128,
+                       max_position_embeddings=4096, rope_theta=500000.0, initializer_range=0.1)
+
+
+def test_spec_pair_k2b_ph_matches_reference_recipe():
+    """recipes.py:31-42: K lowrank_rtn_channel 3b group 64 pre-RoPE, V
+    turboquant_mse_perhead 2b."""
+    k, v = spec_pair("k2b_ph", rank=32)
+    assert (k.arm, k.bits, k.rank, k.group, k.pre_rope) == ("lowrank_rtn_channel", 3, 32, 64, True)
+    assert (v.arm, v.bits) == ("turboquant_mse_perhead", 2)
+    check_k2b(k, v)
+
+
+@pytest.mark.parametrize("bad", [dict(rank=8), dict(bits=4), dict(group=32), dict(pre_rope=False)])
+def test_unsupported_k_specs_raise(bad):
+    k, v = spec_pair("k2b_ph", rank=16)
+    k = CacheCodecSpec(**{**k.__dict__, **bad})
+    with pytest.raises(NotImplementedError):
+        check_k2b(k, v)
+
+
+def test_other_recipes_raise():
+    with pytest.raises(NotImplementedError, match="k2b_ph"):
+        spec_pair("kivi")
+
+
+@pytest.mark.parametrize("rank", [16, 32])
+def test_blended_bpe_reproduces_reference_fixture(rank):
+    """The reference's tiny-Llama run ends with 439 cached tokens (300 prompt +
+    139 fed back), 384 committed in 128-token pages and 55 fp16; its
+    bits_per_entry() must equal the per-page codec bpe blended with 16-bit tail
+    entries (packed_streaming.py:612-619, 713-725)."""
+    g = np.load(GOLD / "e2e_tiny_llama.npz")
+    C = 2 * 128
+    S = 300 + 139
+    P = K.compute_flush_schedule(S, 32, 128)
+    assert P == 384
+    bk = (P * K.bpe_k(rank, C) + (S - P) * 16.0) / S
+    bv = (P * K.bpe_v(2, C) + (S - P) * 16.0) / S
+    np.testing.assert_allclose([bk, bv], g[f"r{rank}_bpe"], rtol=1e-12)
+
+
+def test_attach_detach_and_no_cpu_path():
+    from transformers import LlamaForCausalLM
+
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(tiny_config()).eval()
+    saved = model.config._attn_implementation
+    cache = PackedStreamingCache(model.config, *spec_pair("k2b_ph", rank=16), recent_window=32)
+    with cache.attach(model):
+        assert model.config._attn_implementation == ATTN_NAME
+        assert len(cache.layers) == 2 and len(cache._handles) == 2
+        assert all(hasattr(l.self_attn, "_packed_layer") for l in resolve_decoder_layers(model))
+        ids = torch.randint(0, 256, (1, 40))
+        with pytest.raises(RuntimeError, match="HIP device"):
+            with torch.no_grad():
+                model(ids, past_key_values=cache, use_cache=True)
+    assert model.config._attn_implementation == saved
+    assert cache._handles == []
+    assert not any(hasattr(l.self_attn, "_packed_layer") for l in resolve_decoder_layers(model))
+
+
+def test_memory_report_uses_bpe():
+    cache = PackedStreamingCache(tiny_config(), *spec_pair("k2b_ph", rank=16))
+    rep = cache.memory_report(1000)   # nothing committed: 16 bits per entry both sides
+    assert rep["fp16_bytes"] == 2 * 2 * 2 * 1000 * 128 * 2
+    assert rep["compression"] == pytest.approx(1.0)
+
+
+@pytest.mark.parametrize("rank", [16, 32])
+def test_host_logic_reproduces_reference_run(rank):
+    """The product cache's host logic (flush schedule, pre-RoPE stash and slab
+    pruning, fp16 RoPE tables, prefill/decode split, bits-per-entry) with the
+    CPU oracle standing in for the three kernels, teacher-forced through the
+    reference's own 440-token run of the tiny Llama: every step's logits match
+    the reference's (to fp32 reduction order: the reference decodes with a
+    chunked online softmax, the stand-in with one softmax; 5e-4 against logits
+    of magnitude ~7), every greedy choice agrees, and bits_per_entry() is equal."""
+    import sys
+
+    sys.path.insert(0, str(Path(__file__).parent))
+    from oracle_cache import OracleCache
+    from transformers import LlamaForCausalLM
+
+    g = np.load(GOLD / "e2e_tiny_llama.npz")
+    tokens = torch.from_numpy(g[f"r{rank}_tokens"])
+    ref = torch.from_numpy(g[f"r{rank}_logits"]).double()
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(tiny_config()).eval()
+    cache = OracleCache(model.config, *spec_pair("k2b_ph", rank=rank), recent_window=32)
+    got = []
+    with cache.attach(model), torch.no_grad():
+        got.append(model(tokens[:, :300], past_key_values=cache, use_cache=True).logits[0, -1])
+        for i in range(1, ref.shape[0]):
+            out = model(tokens[:, 300 + i - 1: 300 + i], past_key_values=cache, use_cache=True)
+            got.append(out.logits[0, -1])
+    got = torch.stack(got).double()
+    err = (got - ref).abs().max().item()
+    print(f"r{rank}: oracle-backed cache vs reference run, logits max|err| {err:.3e}")
+    assert err <= 5e-4
+    assert bool((got.argmax(1) == ref.argmax(1)).all())
+    np.testing.assert_allclose(cache.bits_per_entry(), g[f"r{rank}_bpe"], rtol=1e-12)

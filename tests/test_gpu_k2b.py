@@ -124,6 +124,31 @@ def test_append_bit_exact_on_dyadic_inputs():
         np.testing.assert_array_equal(vn16[sl].astype(np.float32), norms.numpy())
 
 
+@pytest.mark.parametrize("vdtype", [torch.float32, torch.bfloat16])
+def test_append_values_in_model_precision(vdtype):
+    """Values are encoded from the model's own precision, as the reference
+    encodes values.float() (packed_streaming.py:544-580): fp32 and bf16 value
+    slabs give the oracle's codes and fp16 norms on the same values."""
+    gen = torch.Generator().manual_seed(7)
+    h_kv, rank, S = 4, 16, 256
+    C = 128 * h_kv
+    k_pre = (torch.randint(-24, 25, (h_kv, S, 128), generator=gen) / 8.0).half()
+    v = torch.randn(h_kv, S, 128, generator=gen).to(vdtype)
+    V = (torch.randint(-2, 3, (C, rank), generator=gen) / 4.0).float()
+    us0 = OC.to_matrix(k_pre[:, :128].float()) @ V
+    consts = k2b.CodecConsts.make(v_seed=2)
+    pool = synth.PagePool(32, h_kv, rank, DEV)
+    seq = synth.encode_sequence(pool, k_pre.to(DEV), v.to(DEV), rank, consts, svd=(us0, V))
+    torch.cuda.synchronize()
+    pages = pool.pages[torch.tensor(seq.page_ids, device=DEV)].cpu().numpy()
+    _, _, _, vidx, vn16 = OL.unpack_pages(pages, h_kv, rank)
+    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v.float()), bits=2, seed=2, h=h_kv)
+    mism = int((vidx != idx.numpy()).sum())
+    print(f"{vdtype}: value-code mismatches {mism}/{idx.numel()}", flush=True)
+    np.testing.assert_array_equal(vn16.astype(np.float32), norms.numpy())
+    assert mism == 0
+
+
 # ------------------------------------------------------------------ decode kernel
 
 
