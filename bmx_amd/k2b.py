@@ -104,8 +104,8 @@ def append(k_pre: torch.Tensor, v: torch.Tensor, basis32: torch.Tensor, basis16:
 class DecodeWorkspace:
     """Grow-only device scratch for split partials (reused across calls).
 
-    Zero-filled when (re)allocated: the merge counters at its head must start at
-    zero, and every completed call leaves them at zero again."""
+    Every call writes all the partials it reads; the buffer is zero-filled when
+    (re)allocated only so that its contents are defined."""
 
     def __init__(self):
         self.buf = None

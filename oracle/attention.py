@@ -142,6 +142,32 @@ def naive_dense_attention(q, K_post, V, n_q_groups: int, scale: float):
     return torch.softmax(s, dim=-1) @ Vx
 
 
+def grouped_dense_attention(q, K_post, V, n_q_groups: int, scale: float):
+    """``naive_dense_attention`` for several query positions without the GQA
+    copy of the keys: query head i reads KV head i // n_q_groups, the
+    repeat_interleave order.  q (n_q, n, d) -> (n_q, n, d) fp32, one softmax
+    over every key per (head, position)."""
+    h_kv, S, d = K_post.shape
+    n_q, n, _ = q.shape
+    qg = q.float().reshape(h_kv, n_q_groups * n, d)
+    s = (qg @ K_post.float().transpose(-1, -2)) * scale
+    return (torch.softmax(s, dim=-1) @ V.float()).reshape(n_q, n, d)
+
+
+def argmax_flip(r_out: torch.Tensor, r_ref: torch.Tensor) -> tuple:
+    """(flip, hard) for one step of the reference's teacher-forced argmax-flip
+    gate (scripts/profile_decode_ab.py:325-343, 388-395, 429-437): the step
+    flips when the argmaxes differ; the flip is hard -- a real divergence, not
+    accumulation-order drift -- when the reference's top-2 gap exceeds the
+    step's max-abs delta.  The gate fails on any hard flip or on more than
+    N // 8 flips over N steps.  r_out, r_ref: 1-D readouts of one step."""
+    flip = bool(r_out.argmax() != r_ref.argmax())
+    top2 = r_ref.topk(2).values
+    gap = (top2[0] - top2[1]).item()
+    delta = (r_out - r_ref).abs().max().item()
+    return flip, flip and gap > delta
+
+
 def k2b_dense_kv(cache: K2bOracleCache, inv_freq, k_tail=None, v_tail=None,
                  attention_scaling: float = 1.0):
     """Dequantize every committed page, RoPE the keys at read with fp32 tables,

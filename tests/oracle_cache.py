@@ -37,9 +37,13 @@ class OracleLayer(product.PackedStreamingLayer):
         P = self._committed_S_q
         ks, vs = [], []
         if P:
-            cos, sin = product._rope_tables(self._inv_freq, self._rope_scaling, 0, P, "cpu")
-            ks.append(A.apply_rope(self._oc.dense_k_pre(), cos.float(), sin.float()).to(dtype))
-            vs.append(self._oc.dense_v().to(dtype))
+            memo = getattr(self, "_kv_memo", None)   # the committed part changes only at a commit
+            if memo is None or memo[0] != (P, dtype):
+                cos, sin = product._rope_tables(self._inv_freq, self._rope_scaling, 0, P, "cpu")
+                kc = A.apply_rope(self._oc.dense_k_pre(), cos.float(), sin.float()).to(dtype)
+                memo = self._kv_memo = ((P, dtype), kc, self._oc.dense_v().to(dtype))
+            ks.append(memo[1])
+            vs.append(memo[2])
         if self.keys is not None and self.keys.numel():
             ks.append(self.keys.squeeze(0).to(dtype))
             vs.append(self.values.squeeze(0).to(dtype))
@@ -59,7 +63,7 @@ class OracleLayer(product.PackedStreamingLayer):
         G = n_heads // self._h_kv
         Kd, Vd = self._kv(q.dtype)
         if n_q == 1 and not is_causal:
-            return A.naive_dense_attention(q.float(), Kd, Vd, G, scaling).to(q.dtype)
+            return A.grouped_dense_attention(q.float(), Kd, Vd, G, scaling).to(q.dtype)
         Kx, Vx = Kd.repeat_interleave(G, dim=0), Vd.repeat_interleave(G, dim=0)
         causal = is_causal and n_q > 1
         return F.scaled_dot_product_attention(

@@ -92,3 +92,74 @@ def test_generate_runs_on_the_packed_path():
                              do_sample=False, pad_token_id=0)
     assert out.shape == (1, 240)
     assert cache.layers[0]._committed_S_q == 128 and cache.layers[0].get_seq_length() == 239
+
+
+def test_config5_qwen3_streaming_append_and_decode():
+    """Config 5: Qwen3-8B attention geometry (8 KV heads, G 4, d 128, RoPE theta
+    1e6), k2b rank 16, recent window 128.  An 8192-token seeded prefill is
+    committed once, then 512 steps each append one token -- the flush schedule
+    commits a codec page through bmx_k2b_append every 128 steps -- and
+    decode-attend through bmx_k2b_decode.  The product layer and the
+    oracle-backed layer run the same host logic on the same inputs: the pool
+    holds the oracle's codes packed (bit-exact up to fp32 reduction-order ties,
+    counted), every step is within the bars of the oracle, and a seeded
+    4096-way readout passes the reference's argmax-flip gate (no flip against a
+    top-2 gap wider than the step's delta, at most N // 8 near-tie flips)."""
+    from transformers import Qwen3Config
+
+    from bmx_amd import k2b, synth
+    from bmx_amd.cache import PackedStreamingLayer
+    from oracle import attention as A
+    from oracle import layout as OL
+    from oracle_cache import OracleLayer
+
+    cfg = Qwen3Config(hidden_size=4096, intermediate_size=12288, num_attention_heads=32,
+                      num_key_value_heads=8, head_dim=128, num_hidden_layers=36, rope_theta=1e6)
+    k_spec, v_spec = spec_pair("k2b_ph", rank=16)
+    h_kv, G, d, W = 8, 4, 128, 128
+    n_pre, n_steps = 8192, 512
+    prod = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=W)
+    orac = OracleLayer(k_spec, v_spec, cfg, recent_window=W)
+    gen = torch.Generator().manual_seed(55)
+    N = n_pre + n_steps
+    k_pre = synth.k2b_keys(h_kv, N, 16, gen)
+    v = synth.values(h_kv, N, gen).half()
+    cos, sin = A.rope_cos_sin(prod._inv_freq, torch.arange(N))
+    k_post = A.apply_rope(k_pre.float(), cos, sin).half()
+    W_read = torch.randn(h_kv * G * d, 4096, generator=gen)
+
+    def feed(lo, hi):
+        for lay, dev in ((prod, "cuda"), (orac, "cpu")):
+            lay.stash_pre_rope(k_pre[:, lo:hi].transpose(0, 1).unsqueeze(0).to(dev))
+            lay.update(k_post[:, lo:hi].unsqueeze(0).to(dev), v[:, lo:hi].unsqueeze(0).to(dev))
+
+    feed(0, n_pre)
+    worst, flips, hard = 0.0, 0, 0
+    for i in range(n_steps):
+        feed(n_pre + i, n_pre + i + 1)
+        q = torch.randn(h_kv * G, 1, d, generator=gen)
+        out = prod.attend(q.to("cuda"), d ** -0.5).double().cpu()
+        ref = orac.attend(q, d ** -0.5).double()
+        err = (out - ref).abs().max().item()
+        rel = ((out - ref).norm() / ref.norm()).item()
+        worst = max(worst, err)
+        assert err <= 2e-3 and rel <= 1e-2, f"step {i}: max_abs {err:.3e} rel {rel:.3e}"
+        f, hf = A.argmax_flip(out.float().reshape(-1) @ W_read, ref.float().reshape(-1) @ W_read)
+        flips, hard = flips + f, hard + hf
+    P = prod._committed_S_q
+    assert P == orac._committed_S_q == ((N - W) // 128) * 128
+    assert prod.bpe_k == orac.bpe_k and prod.bpe_v == orac.bpe_v
+    oc = orac._oc
+    us = torch.cat([kp["Us"] for kp, _, _ in oc.k_blocks]).numpy().astype(np.float16)
+    res = torch.cat([kp["res_Q_int"] for kp, _, _ in oc.k_blocks], dim=1).numpy()
+    sc = torch.cat([kp["res_scale"].squeeze(-1) for kp, _, _ in oc.k_blocks], dim=1)
+    vidx = torch.cat([idx for (idx, _), _, _ in oc.v_blocks]).numpy()
+    vn = torch.cat([n for (_, n), _, _ in oc.v_blocks]).numpy().astype(np.float16)
+    want = OL.pack_pages(us, res, sc.numpy().astype(np.float16), vidx, vn, h_kv, 16)
+    got = prod._pool[: P // k2b.PAGE_TOKENS].cpu().numpy()
+    bad = int((got != want).sum())
+    print(f"config 5 (Qwen3, rank 16, {n_pre} + {n_steps} steps): committed {P}, worst max_abs "
+          f"{worst:.3e}, argmax flips {flips} (hard {hard}), page bytes differing {bad}/{want.size}",
+          flush=True)
+    assert hard == 0 and flips <= n_steps // 8
+    assert bad <= want.size * 1e-4

@@ -7,13 +7,14 @@ counted and bounded below); attention output max-abs <= 2e-3 and
 flips over 64 decode steps.
 """
 
+import ctypes as ct
 from pathlib import Path
 
 import numpy as np
 import pytest
 import torch
 
-from bmx_amd import k2b, synth
+from bmx_amd import _lib, k2b, synth
 from oracle import attention as A
 from oracle import codecs as OC
 from oracle import layout as OL
@@ -276,10 +277,16 @@ def test_ragged_batch_shuffled_pages():
 
 
 def test_64_decode_steps_zero_argmax_flips():
-    """64 consecutive fixed-seed queries on one k2b cache: argmax of a seeded
-    readout of the attention output never differs from the fp32 oracle's."""
+    """Config 3: k2b rank 32, Llama-3.1-8B geometry, 131,072-token context =
+    130,944 committed tokens in 16-token pages + a 128-token fp16 window, split
+    KV over one workgroup per CU (>= 64 splits) with the LSE combine; 64
+    consecutive fixed-seed queries.  Every step is within the bars of the fp32
+    oracle, and a seeded 4096-way readout of the output passes the reference's
+    argmax-flip gate (no flip against a top-2 gap wider than the step's
+    delta, at most N // 8 near-tie flips); the flips are counted and printed."""
     gen = torch.Generator().manual_seed(10)
-    h_kv, rank, S, T = 8, 32, 16384, 160
+    h_kv, rank, G, T = 8, 32, 4, 128
+    S = 131072 - T
     k_pre = synth.k2b_keys(h_kv, S + T, rank, gen)
     v = synth.values(h_kv, S + T, gen)
     svd = synth.first_page_svd(k_pre, rank)
@@ -291,16 +298,37 @@ def test_64_decode_steps_zero_argmax_flips():
     k_tail = A.apply_rope(k_pre[:, S:].float(), cos, sin).half()
     v_tail = v[:, S:]
     K, V = A.k2b_dense_kv(_oracle_cache(k_pre[:, :S], v[:, :S], rank, svd), inv, k_tail, v_tail)
-    W_read = torch.randn(h_kv * 4 * 128, 4096, generator=gen)
-    flips, worst = 0, 0.0
+    del k_pre, v
+    W_read = torch.randn(h_kv * G * 128, 4096, generator=gen)
+    qs = torch.randn(64, 1, h_kv, G, 128, generator=gen)
+    q_dev = torch.empty(1, h_kv, G, 128, device=DEV)
+    plan = k2b.DecodePlan(q_dev, pool.pages, synth.page_table([seq], device=DEV),
+                          torch.tensor([S], dtype=torch.int32, device=DEV), S, seq.basis16, consts,
+                          128 ** -0.5, rank=rank, k_tail=k_tail.unsqueeze(0).to(DEV),
+                          v_tail=v_tail.unsqueeze(0).to(DEV),
+                          tail_len=torch.tensor([T], dtype=torch.int32, device=DEV), tail_cap=T)
+    splits = int(_lib.lib().bmx_k2b_decode_workspace_bytes(ct.byref(plan.args))) // (h_kv * G * 130 * 4)
+    outs = []
     for step in range(64):
-        q = torch.randn(1, h_kv, 4, 128, generator=gen)
-        out = _decode_one(seq, pool, q, consts, rank, k_tail, v_tail).cpu()
-        ref = A.naive_dense_attention(q.view(32, 1, 128), K, V, 4, 128 ** -0.5).view(1, h_kv, 4, 128)
-        worst = max(worst, (out.double() - ref.double()).abs().max().item())
-        flips += int((out.reshape(1, -1) @ W_read).argmax() != (ref.reshape(1, -1) @ W_read).argmax())
-    print(f"64 steps: argmax flips {flips}, worst max_abs {worst:.3e}", flush=True)
-    assert flips == 0 and worst <= MAX_ABS
+        q_dev.copy_(qs[step])
+        outs.append(plan.run().cpu().clone())
+    torch.cuda.synchronize()
+    flips, hard, worst = 0, 0, 0.0
+    for c0 in range(0, 64, 8):   # the oracle, 8 steps per batched softmax
+        qc = qs[c0:c0 + 8].reshape(8, h_kv * G, 128).transpose(0, 1)
+        ref = A.grouped_dense_attention(qc, K, V, G, 128 ** -0.5).transpose(0, 1)
+        for j in range(8):
+            out, r = outs[c0 + j].reshape(-1), ref[j].reshape(-1)
+            err = (out.double() - r.double()).abs().max().item()
+            rel = ((out.double() - r.double()).norm() / r.double().norm()).item()
+            assert err <= MAX_ABS and rel <= REL, f"step {c0 + j}: max_abs {err:.3e} rel {rel:.3e}"
+            worst = max(worst, err)
+            f, hf = A.argmax_flip(out @ W_read, r @ W_read)
+            flips, hard = flips + f, hard + hf
+    print(f"config 3 (131072 ctx, {splits} splits), 64 steps: argmax flips {flips} (hard {hard}), "
+          f"worst max_abs {worst:.3e}", flush=True)
+    assert splits >= 64
+    assert hard == 0 and flips <= 64 // 8
 
 
 @pytest.mark.parametrize("G", [1, 2, 8, 16])

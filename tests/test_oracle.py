@@ -235,6 +235,33 @@ def test_naive_oracle_equals_hand_softmax():
         np.testing.assert_allclose(out[h, 0].numpy(), want.numpy(), atol=1e-6)
 
 
+def test_grouped_oracle_equals_hand_softmax():
+    """The batched, copy-free form gives the hand softmax of every (head,
+    position) pair, query head h reading KV head h // G."""
+    torch.manual_seed(1)
+    q = torch.randn(6, 3, 8, dtype=torch.float64)
+    K = torch.randn(2, 10, 8, dtype=torch.float64)
+    V = torch.randn(2, 10, 8, dtype=torch.float64)
+    out = A.grouped_dense_attention(q, K, V, 3, 0.3).double()
+    for h in range(6):
+        for j in range(3):
+            s = [(q[h, j] @ K[h // 3, t]).item() * 0.3 for t in range(10)]
+            w = np.exp(np.array(s) - max(s))
+            w /= w.sum()
+            want = (torch.tensor(w)[:, None] * V[h // 3]).sum(0)
+            np.testing.assert_allclose(out[h, j].numpy(), want.numpy(), atol=1e-6)
+
+
+def test_argmax_flip_gate():
+    """No flip; a near-tie flip (top-2 gap 0.01 below the delta 0.02) is soft;
+    a flip against a top-2 gap of 1.0 with a delta of 0.7 is hard."""
+    ref = torch.tensor([0.0, 3.0, 2.99, -1.0])
+    assert A.argmax_flip(ref + 0.001, ref) == (False, False)
+    assert A.argmax_flip(torch.tensor([0.0, 2.99, 3.01, -1.0]), ref) == (True, False)
+    assert A.argmax_flip(torch.tensor([0.0, 2.6, 2.7, -1.0]), torch.tensor([0.0, 3.0, 2.0, -1.0])) \
+        == (True, True)
+
+
 def test_split_merge_equals_dense_union():
     """Merging per-split partials (plus a tail split) equals one softmax over the
     union (test_decode_finalize.py:165-220)."""
