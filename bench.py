@@ -61,6 +61,12 @@ def parse():
     ap.add_argument("--cpu-sample-tokens", type=int, default=16384)
     ap.add_argument("--cpu-reps", type=int, default=7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=["decode", "stream"], default="decode",
+                    help="decode: the headline 64k decode-attention step (default); stream: "
+                         "BASELINE config 5, Qwen3-8B geometry, rank 16, an 8192-token prefill "
+                         "then --stream-steps steps of one-token append + decode over 36 layers")
+    ap.add_argument("--stream-steps", type=int, default=512)
+    ap.add_argument("--stream-layers", type=int, default=36)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="run one untimed device copy of this many MiB first (a known-size "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -118,6 +124,127 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+STREAM_METRIC = ("append + decode-attn µs/step, k2b rank 16, Qwen3-8B geometry, "
+                 "8192-token prefill + 512 one-token steps, 1 MI355X")
+
+
+def gpu_sleep(torch):
+    """Queue a GPU sleep so that the host enqueues a region before it starts
+    and its kernels then run back to back (device time only)."""
+    try:
+        torch.cuda._sleep(int(2e8))
+    except Exception:  # pragma: no cover - sleep helper missing in this torch build
+        pass
+
+
+def run_stream(args, torch, k2b, synth, dev) -> dict:
+    """Qwen3-8B attention geometry (36 layers, 32q/8kv heads,
+    d 128, RoPE theta 1e6), k2b rank 16, recent window 128.  Per layer an
+    8192-token prefill is committed once (untimed), then each of the timed
+    steps appends one token to every layer's fp16 window and decodes; when the
+    flush schedule moves (every 128 steps) each layer commits one codec page
+    through bmx_k2b_append, its window drops those 128 tokens, and the layer's
+    decode plan is rebound to the new packed length.  Per step and layer the
+    device work is one window write (a copy of the token's post-RoPE key and
+    value), the decode call, and at commits the append and a window shift."""
+    L, W, rank, n_pre, n_steps = args.stream_layers, 128, 16, 8192, args.stream_steps
+    N = n_pre + n_steps
+    flush = lambda S: ((S - W) // 128) * 128 if S > W else 0   # noqa: E731
+    P0, P_end = flush(n_pre), flush(N)
+    cap = 2 * 128   # the window holds at most 255 tokens between commits
+    consts = k2b.CodecConsts.make(theta=1e6)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    ws = k2b.DecodeWorkspace()
+    tail_len = torch.tensor([n_pre - P0], dtype=torch.int32, device=dev)   # shared by the layers
+    packed_len = torch.tensor([P0], dtype=torch.int32, device=dev)
+    layers = []
+    for li in range(L):
+        k_pre = synth.k2b_keys(H_KV, N, rank, gen)
+        v = synth.values(H_KV, N, gen)
+        kv_post = torch.stack([synth.rope_keys(k_pre, 0, consts), v])   # (2, h_kv, N, d)
+        pool = synth.PagePool(P_end // 16, H_KV, rank, dev)
+        seq = synth.encode_sequence(pool, k_pre[:, :P0], v[:, :P0], rank, consts)
+        kvt = torch.zeros(2, 1, H_KV, cap, D, dtype=torch.float16, device=dev)
+        kvt[:, 0, :, : n_pre - P0] = kv_post[:, :, P0:n_pre]
+        lay = {"k_pre": k_pre, "v": v, "kv_post": kv_post, "pool": pool, "seq": seq, "kvt": kvt,
+               "q": torch.randn(1, H_KV, G, D, generator=gen, device=dev),
+               "out": torch.empty(1, H_KV, G, D, device=dev)}
+        layers.append(lay)
+    torch.cuda.synchronize()
+
+    def bind(lay, P):
+        pt = synth.page_table([lay["seq"]], max_pages=P_end // 16, device=dev)
+        lay["plan"] = k2b.DecodePlan(lay["q"], lay["pool"].pages, pt, packed_len, P, lay["seq"].basis16,
+                                     consts, D ** -0.5, rank=rank, k_tail=lay["kvt"][0],
+                                     v_tail=lay["kvt"][1], tail_len=tail_len, tail_cap=cap,
+                                     out=lay["out"], workspace=ws)
+
+    for lay in layers:
+        bind(lay, P0)
+    for _ in range(args.warmup):
+        for lay in layers:
+            lay["plan"].run()
+    torch.cuda.synchronize()
+
+    P, dev_ms, commits = P0, 0.0, 0
+    t_wall = time.perf_counter()
+    chunk = 16
+    for c0 in range(0, n_steps, chunk):
+        torch.cuda.synchronize()
+        gpu_sleep(torch)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for s in range(n_pre + c0, n_pre + min(n_steps, c0 + chunk)):
+            T = s - P
+            P_new = flush(s + 1)
+            for lay in layers:
+                lay["kvt"][:, 0, :, T] = lay["kv_post"][:, :, s]
+            tail_len.fill_(T + 1)
+            if P_new > P:   # commit one codec page per layer, drop it from the window
+                for lay in layers:
+                    ids = lay["pool"].alloc(8)
+                    lay["seq"].page_ids.extend(ids)
+                    k2b.append(lay["k_pre"][:, P:P_new], lay["v"][:, P:P_new], lay["seq"].basis32,
+                               lay["seq"].basis16, lay["pool"].pages,
+                               torch.tensor(ids, dtype=torch.int32, device=dev), consts, rank=rank)
+                    lay["kvt"][:, :, :, : T + 1 - 128] = lay["kvt"][:, :, :, 128: T + 1]
+                    bind(lay, P_new)
+                packed_len.fill_(P_new)
+                tail_len.fill_(T + 1 - 128)
+                P, commits = P_new, commits + 1
+            for lay in layers:
+                lay["plan"].run()
+        e1.record()
+        torch.cuda.synchronize()
+        dev_ms += e0.elapsed_time(e1)
+    t_wall = time.perf_counter() - t_wall
+    step_us = dev_ms * 1e3 / n_steps
+    return {
+        "metric": STREAM_METRIC,
+        "value": round(step_us, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": n_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_us / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"k2b rank-16 streaming append + decode, Qwen3-8B geometry ({L} layers, "
+                         f"32q/8kv heads, d 128, RoPE theta 1e6), batch 1, {n_pre}-token prefill "
+                         f"({P0} packed + {n_pre - P0} fp16 window) then {n_steps} one-token steps, "
+                         f"a codec page committed every 128 steps"),
+            "layers": L, "rank": rank, "prefill": n_pre, "packed_start": P0, "packed_end": P,
+            "commits_per_layer": commits,
+        },
+        "device_time": "HIP events around 16-step chunks queued behind a GPU sleep",
+        "wall_us_per_step": round(t_wall * 1e6 / n_steps, 1),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -133,6 +260,9 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.workload == "stream":
+        print(json.dumps(run_stream(args, torch, k2b, synth, dev)), flush=True)
+        return
     if args.copy_calib_mib > 0:
         n = args.copy_calib_mib << 20
         src = torch.ones(n, dtype=torch.uint8, device=dev)
@@ -196,18 +326,10 @@ def main():
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t_wall
 
-    def gpu_sleep():
-        # queue the region behind a GPU sleep so the host enqueues everything
-        # first and the kernels then run back to back (device time only)
-        try:
-            torch.cuda._sleep(int(2e8))
-        except Exception:  # pragma: no cover - sleep helper missing in this torch build
-            pass
-
     # timed pass (the reported value): K steps back to back, bracketed by events
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    gpu_sleep()
+    gpu_sleep(torch)
     start.record()
     for _ in range(args.steps):
         for lay in layers:
@@ -223,7 +345,7 @@ def main():
     n_calls = args.steps * args.layers
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_calls)]
     torch.cuda.synchronize()
-    gpu_sleep()
+    gpu_sleep(torch)
     i = 0
     for _ in range(args.steps):
         for lay in layers:

@@ -33,27 +33,60 @@ struct AppendKArgs {
   uint32_t v_sign_bits[4];
 };
 
-// grid (n_codec_pages * 8), block 256: 16 tokens x 16 rank lanes.
+// grid (n_codec_pages * 8), block 256 = 4 waves, one 16-token page slot each.
+// Us[t][r] = sum_c M[t][c] basis32[c][r] in fp32 (the reference's M @ V).  The
+// page's 16 key rows are staged in LDS (rows padded by one bank); wave w sums
+// channels [w C/4, (w+1) C/4) in order, lane (t = lane & 15, quad rq = lane >> 4)
+// owns ranks rq R/4 .. + R/4; the four partial sums are then added in wave
+// order.  The first codec page of a sequence takes its SVD factor instead.
+template <int R>
 __global__ __launch_bounds__(256) void k2b_us_kernel(const AppendKArgs a) {
-  const int pg = blockIdx.x;              // physical page slot (16 tokens)
+  constexpr int RQ = R / 4;
+  extern __shared__ uint16_t s_m[];          // [kPT][C + 2] fp16 key rows
+  __shared__ float s_part[4][kPT][R + 1];
+  const int pg = blockIdx.x;                  // physical page slot (16 tokens)
   const int cp = pg / 8, pl = pg % 8;
-  const int tl = threadIdx.x >> 4, rg = threadIdx.x & 15;
-  const int t = pg * kPT + tl;            // token index within the call
-  const int C = kD * a.h_kv;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int C = kD * a.h_kv, ld = C + 2;
   uint8_t* page = a.pages + clamp_page(a.page_ids[pg], a.n_pool) * a.L.bytes;
-  for (int r = rg; r < a.R; r += 16) {
-    float us;
-    if (a.us_first != nullptr && cp == 0) {
-      us = a.us_first[(pl * kPT + tl) * a.R + r];
-    } else {
-      float acc = 0.f;
-      for (int c = 0; c < C; ++c) {
-        const float m = half_bits_to_float(a.k_pre[(c / kD) * a.ksh + (int64_t)t * a.kst + (c % kD)]);
-        acc = __builtin_fmaf(m, a.basis32[(int64_t)c * a.R + r], acc);
-      }
-      us = acc;
+  if (a.us_first != nullptr && cp == 0) {
+    for (int e = tid; e < kPT * R; e += 256) {
+      const int t = e / R, r = e % R;
+      *reinterpret_cast<uint16_t*>(page + a.L.us + us_half(R, t, r) * 2) =
+          float_to_half_bits(a.us_first[(pl * kPT + t) * R + r]);
     }
-    *reinterpret_cast<uint16_t*>(page + a.L.us + us_half(a.R, tl, r) * 2) = float_to_half_bits(us);
+    return;
+  }
+  for (int e = tid; e < kPT * C; e += 256) {
+    const int t = e / C, c = e % C;
+    s_m[t * ld + c] = a.k_pre[(c / kD) * a.ksh + (int64_t)(pg * kPT + t) * a.kst + (c % kD)];
+  }
+  __syncthreads();
+  const int t = lane & 15, rq = lane >> 4;
+  float acc[RQ];
+#pragma unroll
+  for (int k = 0; k < RQ; ++k) acc[k] = 0.f;
+  const int c0 = wave * (C / 4), c1 = c0 + C / 4;
+#pragma unroll 4
+  for (int c = c0; c < c1; ++c) {
+    const float m = half_bits_to_float(s_m[t * ld + c]);
+    const float4* b = reinterpret_cast<const float4*>(a.basis32 + (int64_t)c * R + rq * RQ);
+#pragma unroll
+    for (int k4 = 0; k4 < RQ / 4; ++k4) {
+      const float4 bv = b[k4];
+      acc[4 * k4 + 0] = __builtin_fmaf(m, bv.x, acc[4 * k4 + 0]);
+      acc[4 * k4 + 1] = __builtin_fmaf(m, bv.y, acc[4 * k4 + 1]);
+      acc[4 * k4 + 2] = __builtin_fmaf(m, bv.z, acc[4 * k4 + 2]);
+      acc[4 * k4 + 3] = __builtin_fmaf(m, bv.w, acc[4 * k4 + 3]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < RQ; ++k) s_part[wave][t][rq * RQ + k] = acc[k];
+  __syncthreads();
+  for (int e = tid; e < kPT * R; e += 256) {
+    const int tt = e / R, r = e % R;
+    const float us = ((s_part[0][tt][r] + s_part[1][tt][r]) + s_part[2][tt][r]) + s_part[3][tt][r];
+    *reinterpret_cast<uint16_t*>(page + a.L.us + us_half(R, tt, r) * 2) = float_to_half_bits(us);
   }
 }
 
@@ -227,6 +260,21 @@ static int afail(int code, const std::string& msg) {
   return code;
 }
 
+// The Us kernel stages 16 key rows of C channels in LDS: above 64 KB (h_kv 16)
+// the launch needs the larger dynamic-LDS limit set once.
+template <int R>
+static hipError_t launch_us(const AppendKArgs& k, dim3 grid, size_t lds, hipStream_t st) {
+  static size_t attr_bytes = 0;
+  if (lds > 65536 && attr_bytes < lds) {
+    hipError_t e = hipFuncSetAttribute((const void*)k2b_us_kernel<R>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr_bytes = lds;
+  }
+  hipLaunchKernelGGL(k2b_us_kernel<R>, grid, dim3(256), lds, st, k);
+  return hipGetLastError();
+}
+
 extern "C" int bmx_k2b_append(const bmx_k2b_append_args* a, void* stream) {
   if (!a) return afail(BMX_E_INVALID, "bmx_k2b_append: args is NULL");
   const bmx_k2b_geom& g = a->geom;
@@ -237,6 +285,8 @@ extern "C" int bmx_k2b_append(const bmx_k2b_append_args* a, void* stream) {
   if (!a->k_pre || !a->v || !a->basis32 || !a->basis16 || !a->pages || !a->page_ids)
     return afail(BMX_E_INVALID, "bmx_k2b_append: null pointer argument");
   if (a->n_pool_pages < 1) return afail(BMX_E_INVALID, "bmx_k2b_append: n_pool_pages must be >= 1");
+  if (reinterpret_cast<uintptr_t>(a->basis32) % 16 != 0)
+    return afail(BMX_E_INVALID, "bmx_k2b_append: basis32 must be 16-byte aligned");
   AppendKArgs k{};
   k.h_kv = g.h_kv; k.R = g.rank; k.n_codec_pages = a->n_codec_pages;
   k.k_pre = a->k_pre; k.ksh = a->k_stride_h; k.kst = a->k_stride_t;
@@ -248,7 +298,10 @@ extern "C" int bmx_k2b_append(const bmx_k2b_append_args* a, void* stream) {
   k.L = PageLayout::make(g.h_kv, g.rank);
   for (int i = 0; i < 4; ++i) { k.codebook[i] = a->codebook[i]; k.v_sign_bits[i] = a->v_sign_bits[i]; }
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k2b_us_kernel, dim3(a->n_codec_pages * 8), dim3(256), 0, st, k);
+  const size_t us_lds = (size_t)kPT * (kD * g.h_kv + 2) * 2;
+  hipError_t le = g.rank == 32 ? launch_us<32>(k, dim3(a->n_codec_pages * 8), us_lds, st)
+                               : launch_us<16>(k, dim3(a->n_codec_pages * 8), us_lds, st);
+  if (le != hipSuccess) return afail(BMX_E_HIP, std::string("bmx_k2b_append: launch: ") + hipGetErrorString(le));
   hipLaunchKernelGGL(k2b_kres_kernel, dim3(a->n_codec_pages * 2, g.h_kv), dim3(256), 0, st, k);
   hipLaunchKernelGGL(k2b_v_kernel, dim3(a->n_codec_pages * 8, g.h_kv), dim3(256), 0, st, k);
   hipError_t e = hipGetLastError();

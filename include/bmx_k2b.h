@@ -158,7 +158,7 @@ typedef struct {
   const void* v;              /* device values, same indexing, element type v_dtype */
   int64_t v_stride_h;
   int64_t v_stride_t;
-  const float* basis32;       /* device fp32 [C][R] frozen basis (projection) */
+  const float* basis32;       /* device fp32 [C][R] frozen basis (projection), 16-byte aligned */
   const uint16_t* basis16;    /* device fp16 [C][R] (= fp16(basis32)) */
   const float* us_first;      /* device fp32 [128][R] or NULL: Us of codec page 0 */
   float codebook[4];

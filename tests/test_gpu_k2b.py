@@ -74,7 +74,7 @@ def test_append_codes_match_reference_golden(rank):
     torch.cuda.synchronize()
     pages = pool.pages[torch.tensor(seq.page_ids, device=DEV)].cpu().numpy()
     us16, res, sc16, vidx, vn16 = OL.unpack_pages(pages, 2, rank)
-    n_mis_res = n_mis_us = 0
+    n_mis_res = n_mis_us = n_mis_sc = 0
     for p in range(3):
         pre = f"k2b_r{rank}_p{p}_"
         sl = slice(p * 128, (p + 1) * 128)
@@ -82,23 +82,37 @@ def test_append_codes_match_reference_golden(rank):
         np.testing.assert_array_equal(vidx[sl], g[pre + "vidx"])
         np.testing.assert_array_equal(vn16[sl].astype(np.float32), g[pre + "vnorm"])
         # keys: Us16 of page 0 comes from the SVD input (exact); later pages are
-        # a length-C fp32 dot whose summation order differs from CPU BLAS.
+        # a length-C fp32 dot whose summation order differs from CPU BLAS, so a
+        # value next to an fp16 rounding boundary may round the other way: one
+        # fp16 ulp at most
         d_us = us16[sl].astype(np.float32) != g[pre + "us"]
         if p == 0:
             assert not d_us.any()
+        ulps = np.abs(us16[sl].view(np.int16).astype(np.int32)
+                      - g[pre + "us"].astype(np.float16).view(np.int16).astype(np.int32))
+        assert ulps.max() <= 1, f"page {p}: Us16 off by {ulps.max()} fp16 ulps"
         n_mis_us += int(d_us.sum())
         n_mis_res += int((res[:, sl] != g[pre + "res"]).sum())
-        np.testing.assert_array_equal(sc16[:, 2 * p:2 * p + 2],
-                                      g[pre + "scale"][..., 0].astype(np.float16))
+        # a group scale follows the group's largest residual, which moves with a
+        # flipped Us16 of its token: one fp16 ulp at most, counted
+        got_sc = sc16[:, 2 * p:2 * p + 2]
+        want_sc = g[pre + "scale"][..., 0].astype(np.float16)
+        sc_ulps = np.abs(got_sc.view(np.int16).astype(np.int32) - want_sc.view(np.int16).astype(np.int32))
+        assert sc_ulps.max() <= 1, f"page {p}: scale off by {sc_ulps.max()} fp16 ulps"
+        n_mis_sc += int((got_sc != want_sc).sum())
     print(f"rank {rank}: Us16 mismatches {n_mis_us}/{3 * 128 * rank}, "
-          f"residual-code mismatches {n_mis_res}/{3 * 256 * 128}", flush=True)
-    assert n_mis_us <= 4 and n_mis_res <= 8
+          f"residual-code mismatches {n_mis_res}/{3 * 256 * 128}, "
+          f"scale mismatches {n_mis_sc}/{3 * 256 * 2}", flush=True)
+    # <= 0.5% of Us16 values; their knock-on effects on codes and scales
+    assert n_mis_us <= 3 * 128 * rank // 200 and n_mis_res <= 8 and n_mis_sc <= 4
 
 
-def test_append_bit_exact_on_dyadic_inputs():
-    """Inputs whose every fp32 sum is exact in any order: codes must be identical."""
+@pytest.mark.parametrize("h_kv,rank", [(8, 32), (1, 16), (16, 32)])
+def test_append_bit_exact_on_dyadic_inputs(h_kv, rank):
+    """Inputs whose every fp32 sum is exact in any order: codes must be identical
+    (1 to 16 KV heads: 128 to 2048 key channels staged per page)."""
     gen = torch.Generator().manual_seed(4)
-    h_kv, rank, S = 8, 32, 256
+    S = 256
     C = 128 * h_kv
     k_pre = (torch.randint(-24, 25, (h_kv, S, 128), generator=gen) / 8.0).half()
     v = (torch.randint(-16, 17, (h_kv, S, 128), generator=gen) / 4.0).half()
