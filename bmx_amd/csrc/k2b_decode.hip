@@ -85,6 +85,12 @@ struct DecodeKArgs {
   uint32_t level_hi[4];   // fp16 bits of the value levels as used by the MFMA:
                           // hi_c = kappa * codebook_c + mu (+ < 1e-6 relative)
   float level_mu;         // mu (the merge divides by kappa)
+  // recent window: fp16 post-RoPE keys [b * ts_b + h * ts_h + t * ts_t][128]
+  const uint16_t* k_tail;
+  int64_t ts_b, ts_h, ts_t;
+  int tail_cap;
+  float win_rescale;      // 1 / rope_scaling: window keys carry the RoPE scaling
+  float* ws_win;          // [B][h_kv][G][tail_cap] window scores, base 2
 };
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
@@ -162,6 +168,68 @@ __device__ __forceinline__ half2_t rope2(half2_t p, uint32_t csu) {
 // linear).  Lane 16q + n stores acc[bt] at offset 4q of chunk bt.  The workspace
 // row of a query is chunk-major ([chunk][split][16]), so a merge workgroup
 // reads one contiguous 64-byte record per split.
+// ---------------------------------------------------------------------------
+// Recent-window scores.  Window tile j (tokens 16j .. 16j + 15 of the fp16
+// post-RoPE window) belongs to workgroup j mod max_splits and is scored on the
+// MFMA like a packed page: A = its 16 key rows (lane: token lane & 15, quarter
+// q = lane >> 4 holds channels 16bb + 4q + i and + 64, interleaved: the K order
+// of the query fragments), B = the query fragments split into fp16 high and low
+// parts (q = hi + lo to 2^-22 relative), so the scores carry the fp32 query.
+// Base-2 scores go to ws_win[b][h][g][t]; the merge does the window's softmax
+// and value sum.  Rows past tail_cap read row 0 of the head and are not stored.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void load_win_tile(const DecodeKArgs& a, int64_t tail_base, int j, int n, int q,
+                                              uint2 kw[8]) {
+  const int t = 16 * j + n;
+  const uint16_t* row = a.k_tail + tail_base + (int64_t)(t < a.tail_cap ? t : 0) * a.ts_t + 4 * q;
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    kw[2 * bb] = *reinterpret_cast<const uint2*>(row + 16 * bb);
+    kw[2 * bb + 1] = *reinterpret_cast<const uint2*>(row + 16 * bb + 64);
+  }
+}
+
+__device__ __forceinline__ void score_win_tile(const DecodeKArgs& a, int b, int h, int j, int n, int q,
+                                               const uint2 kw[8], const half8_t qh[4], const half8_t ql[4]) {
+  float4_t s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    const uint2 lo = kw[2 * bb], hi = kw[2 * bb + 1];   // channels +0..3 and +64..67
+    union { uint4 u; half8_t v; } ka;
+    ka.u = make_uint4(__builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u), __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u),
+                      __builtin_amdgcn_perm(hi.y, lo.y, 0x05040100u), __builtin_amdgcn_perm(hi.y, lo.y, 0x07060302u));
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, qh[bb], s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, ql[bb], s, 0, 0, 0);
+  }
+  // lane: query n, tokens 16j + 4q + i
+  if (n < a.G) {
+    float* dst = a.ws_win + (((int64_t)b * a.h_kv + h) * a.G + n) * a.tail_cap;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * j + 4 * q + i;
+      if (t < a.tail_cap) dst[t] = s[i] * a.win_rescale;
+    }
+  }
+}
+
+// query fragments of the packed pages, fp16 high and low parts: chunk bb holds
+// B[8q + 2i + e][n] = x_n[16bb + 4q + i + 64e] (i < 4, e < 2), the order in
+// which the key pairs leave the rotation, x = q * qscale_rope; column n is
+// query n (zero if n >= G)
+__device__ __forceinline__ void query_fragments(const float4_t qraw[8], float sc, half8_t qh[4], half8_t ql[4]) {
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float x = qraw[4 * e + bb][i] * sc;
+        const _Float16 xh = (_Float16)x;
+        qh[bb][2 * i + e] = xh;
+        ql[bb][2 * i + e] = (_Float16)(x - (float)xh);
+      }
+}
+
 __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int split, int h, int n,
                                               int q, float4_t acc[8], float m_run, float l_run,
                                               float w_run) {
@@ -191,6 +259,34 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
     for (int bt = 0; bt < 8; ++bt) *reinterpret_cast<float4_t*>(dst + (int64_t)bt * S * 16) = acc[bt];
     if (q == 0) *reinterpret_cast<float2*>(a.ws_ml + (row * S + split) * 2) = make_float2(m_run, l_run);
   }
+}
+
+// A workgroup with no packed tokens: its window tiles, then an empty partial
+// (max -inf) that the merge ignores.  Out of line, with the kernel argument
+// block passed by its kernarg-segment address: a second inlined copy of the
+// window code would disturb the group loop's register allocation.
+__device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, int split, int h, int n,
+                                                 int q) {
+  const int n_tiles = (a.tail_cap + 15) >> 4;
+  if (split < n_tiles) {
+    const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
+    float4_t qraw[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      qraw[u] = *reinterpret_cast<const float4_t*>(qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2));
+    half8_t qh[4], ql[4];
+    query_fragments(qraw, n < a.G ? a.qscale_rope : 0.0f, qh, ql);
+    const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
+    for (int j = split; j < n_tiles; j += a.max_splits) {
+      uint2 kw[8];
+      load_win_tile(a, tail_base, j, n, q, kw);
+      score_win_tile(a, b, h, j, n, q, kw, qh, ql);
+    }
+  }
+  float4_t zero[8];
+#pragma unroll
+  for (int bt = 0; bt < 8; ++bt) zero[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  store_partial(a, b, split, h, n, q, zero, -INFINITY, 0.f, 0.f);
 }
 
 // R: key rank (16 or 32).  SW: query slot width (G rounded up to 4, 8 or 16);
@@ -256,6 +352,8 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     for (int u = 0; u < 8; ++u)
       qraw[u] = *reinterpret_cast<const float4_t*>(qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2));
   }
+  const int n_win_tiles = (a.tail_cap + 15) >> 4;   // recent-window score tiles
+  const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
 
   int pidv = (int)clamp_page(pid_raw, a.n_pool);
   const int len = min(len_raw, a.max_packed_len) & ~(kGroup - 1);
@@ -264,13 +362,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     pidv = (int)clamp_page(load_ids_raw(0, (g1 - g0) * kGroupPages), a.n_pool);
   }
   const int n_groups = g1 - g0;
-  if (n_groups == 0) {  // nothing packed here; an empty partial keeps the merge blind
-    if (active) {
-      float4_t zero[8];
-#pragma unroll
-      for (int bt = 0; bt < 8; ++bt) zero[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-      store_partial(a, b, split, h, n, q, zero, -INFINITY, 0.f, 0.f);
-    }
+  if (n_groups == 0) {  // nothing packed here: the window tiles and an empty partial
+    if (active)
+      empty_range_partial(*(const DecodeKArgs*)__builtin_amdgcn_kernarg_segment_ptr(), b, split, h, n, q);
     return;
   }
   auto load_ids = [&](int first, int count) { return (int)clamp_page(load_ids_raw(first, count), a.n_pool); };
@@ -324,26 +418,21 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     vcd[pp] = load_vcode(0, pp);
   }
 
+  // the rows of this workgroup's first window tile, if it owns one: issued
+  // after the first group's pages, whose addresses wait for every load before
+  uint2 kw[8];
+  if (split < n_win_tiles) load_win_tile(a, tail_base, split, n, q, kw);
+
   if (tid < 256) {
     const uint32_t l0 = a.level_hi[0], l1 = a.level_hi[1], l2 = a.level_hi[2], l3 = a.level_hi[3];
     auto lv = [&](int c) { return c == 0 ? l0 : c == 1 ? l1 : c == 2 ? l2 : l3; };
     s_vlut[tid] = make_uint2(lv(tid & 3) | (lv((tid >> 2) & 3) << 16), lv((tid >> 4) & 3) | (lv(tid >> 6) << 16));
   }
 
-  // query fragments of the packed pages: chunk bb holds the RoPE pairs
-  // B[8q + 2i + e][n] = q_n[16bb + 4q + i + 64e] (i < 4, e < 2), the order in
-  // which the key pairs leave the rotation; column n is query n (zero if n >= G)
-  half8_t qf[4];
-  {
-    const float sc = (n < a.G) ? a.qscale_rope : 0.0f;
-#pragma unroll
-    for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qf[bb][2 * i] = (_Float16)(qraw[bb][i] * sc);
-        qf[bb][2 * i + 1] = (_Float16)(qraw[4 + bb][i] * sc);
-      }
-  }
+  // query fragments (qf: the MFMA B operand of the packed pages; qlo: the low
+  // parts, used by the window tiles only)
+  half8_t qf[4], qlo[4];
+  query_fragments(qraw, (n < a.G) ? a.qscale_rope : 0.0f, qf, qlo);
 
   // ---- RoPE table: fp16 (cos, sin) of HF's angle fl(fq * pos) for 64
   // positions per group, row = position, column = frequency, one LDS buffer per
@@ -382,6 +471,14 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     }
   };
   produce_groups(0, min(n_groups, cs_bufs), 0);
+  // recent-window tiles (the first one's rows are in flight)
+  if (active && split < n_win_tiles) {
+    score_win_tile(a, b, h, split, n, q, kw, qf, qlo);
+    for (int j = split + S; j < n_win_tiles; j += S) {
+      load_win_tile(a, tail_base, j, n, q, kw);
+      score_win_tile(a, b, h, j, n, q, kw, qf, qlo);
+    }
+  }
   store_prefix(pre, 0);
 
   // ---- per-wave state ----
@@ -581,28 +678,26 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
 }
 
 // ---------------------------------------------------------------------------
-// Combine: recent window + merge of the packed partials.  One workgroup per
-// (16-channel chunk, query row, sequence): the partials arrive already in the
-// output domain, so a chunk needs only its own 16 channels of every split
-// (contiguous, 64 B per split) plus every split's (max, sum).  The window
-// scores need whole keys; each chunk recomputes them (the window is small and
-// stays in L2).  Every load of the first block is issued before any reduction.
+// Combine: merge of the packed partials and the recent window.  One workgroup
+// per (16-channel chunk, query row, sequence): the partials arrive already in
+// the output domain, so a chunk needs only its own 16 channels of every split
+// (contiguous, 64 B per split) plus every split's (max, sum); the window needs
+// its scores (computed by the split kernel) and its 16 value channels of every
+// token.  Thread i takes split i and window token i of each 256-wide block;
+// every load of the first block is issued before any reduction.
 // ---------------------------------------------------------------------------
 constexpr int kCmbThreads = 256;
 constexpr int kCmbWaves = kCmbThreads / 64;
 constexpr int kChunk = 16;                  // channels per workgroup
 constexpr int kChunks = kD / kChunk;
-constexpr int kWinTok = kCmbThreads / 2;    // window tokens per block (two threads each)
-constexpr int kRedPad = kCmbThreads + 4;    // LDS row stride of the split reduction
+constexpr int kRedPad = kCmbThreads + 4;    // LDS row stride of the reductions
 
 struct CombineKArgs {
   int h_kv, G, max_splits, tail_cap;
-  float qscale;        // sm_scale * log2(e) (window keys are already rotated)
   float* out;
-  const float* q;
   const float* ws_acc;
   const float* ws_ml;
-  const uint16_t* k_tail;
+  const float* ws_win;
   const uint16_t* v_tail;
   int64_t ts_b, ts_h, ts_t;
   const int32_t* tail_len;
@@ -627,81 +722,54 @@ __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineK
   const int64_t row = (int64_t)b * a.h_kv * a.G + r;   // (b, h, g) row
   const float* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S * kChunk;
   const float* mlb = a.ws_ml + row * S * 2;
+  const float* swb = a.ws_win + row * a.tail_cap;
+  const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch;
   typedef float f2_t __attribute__((ext_vector_type(2)));
   __shared__ float s_red[2 * kCmbWaves];
   __shared__ float s_fin[2 * kChunk];
   __shared__ float s_x[kChunk * kRedPad];
-  __shared__ float s_v[kChunk * (kWinTok + 4)];
-
-  // thread roles: split i = block base + tid; window token tk (channel half kh)
-  const int tk = tid >> 1, kh = tid & 1;
-  const uint16_t* kb = a.k_tail + b * a.ts_b + h * a.ts_h + 64 * kh;
-  const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch + 8 * kh;
+  __shared__ float s_v[kChunk * kRedPad];
 
   float4_t v[4];
   f2_t ml = {-INFINITY, 0.f};
-  uint4 kv[8];
-  uint4 vv;
+  uint4 vv[2];
+  float sw = -INFINITY;
   // partial block k and window block k, no waits; the first block's window
   // rows are bounded by the host's tail_cap, so they do not wait for tail_len
   auto load_block = [&](int k, int t_end) {
-    const int ib = k * kCmbThreads, t0 = k * kWinTok;
-    if (ib < S) {
-      const int i = min(ib + tid, S - 1);
+    const int i0 = k * kCmbThreads;
+    if (i0 < S) {
+      const int i = min(i0 + tid, S - 1);
       ml = *reinterpret_cast<const f2_t*>(mlb + 2 * (int64_t)i);
 #pragma unroll
       for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4_t*>(accb + (int64_t)i * kChunk + 4 * u);
     }
-    if (t0 < t_end) {
-      const int t = min(t0 + tk, t_end - 1);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) kv[u] = *reinterpret_cast<const uint4*>(kb + (int64_t)t * a.ts_t + 8 * u);
-      vv = *reinterpret_cast<const uint4*>(vb + (int64_t)t * a.ts_t);
+    if (i0 < t_end) {
+      const int t = min(i0 + tid, t_end - 1);
+      sw = swb[t];
+      vv[0] = *reinterpret_cast<const uint4*>(vb + (int64_t)t * a.ts_t);
+      vv[1] = *reinterpret_cast<const uint4*>(vb + (int64_t)t * a.ts_t + 8);
     }
   };
   load_block(0, a.tail_cap);
-  float4_t qf[16];
-  if (a.tail_cap > 0) {
-    const float* qrow = a.q + row * kD + 64 * kh;
-#pragma unroll
-    for (int u = 0; u < 16; ++u) qf[u] = *reinterpret_cast<const float4_t*>(qrow + 4 * u);
-  }
 
   const int T = min(max(a.tail_len[b], 0), a.tail_cap);
   float4_t xp[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) xp[u] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float vacc[8];
+  float vacc[kChunk];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) vacc[e] = 0.f;
+  for (int e = 0; e < kChunk; ++e) vacc[e] = 0.f;
   float mp = -INFINITY, mt = -INFINITY, lp = 0.f, lt = 0.f;   // lp, lt: this thread's share
-  const int n_blk = max((S + kCmbThreads - 1) / kCmbThreads, (T + kWinTok - 1) / kWinTok);
+  const int n_blk = (max(S, T) + kCmbThreads - 1) / kCmbThreads;
   for (int k = 0; k < n_blk; ++k) {   // uniform trip count
     if (k != 0) load_block(k, T);
-    const int ib = k * kCmbThreads, t0 = k * kWinTok;
-    const bool own_p = ib < S && ib + tid < S;
+    const int i0 = k * kCmbThreads;
+    const bool own_p = i0 + tid < S;
     const float mi = own_p ? ml[0] : -INFINITY;
-    float s = -INFINITY;
-    if (t0 < T) {
-      float d = 0.f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const uint32_t w[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
-        const float4_t q0 = qf[2 * u], q1 = qf[2 * u + 1];
-        d = __builtin_fmaf(half_bits_to_float(w[0] & 0xffff), q0[0], d);
-        d = __builtin_fmaf(half_bits_to_float(w[0] >> 16), q0[1], d);
-        d = __builtin_fmaf(half_bits_to_float(w[1] & 0xffff), q0[2], d);
-        d = __builtin_fmaf(half_bits_to_float(w[1] >> 16), q0[3], d);
-        d = __builtin_fmaf(half_bits_to_float(w[2] & 0xffff), q1[0], d);
-        d = __builtin_fmaf(half_bits_to_float(w[2] >> 16), q1[1], d);
-        d = __builtin_fmaf(half_bits_to_float(w[3] & 0xffff), q1[2], d);
-        d = __builtin_fmaf(half_bits_to_float(w[3] >> 16), q1[3], d);
-      }
-      d += __shfl_xor(d, 1);
-      s = (t0 + tk < T) ? d * a.qscale : -INFINITY;
-    }
+    const float st = i0 + tid < T ? sw : -INFINITY;
     // one joint block max of (partial max, window score)
-    float r0 = mi, r1 = s;
+    float r0 = mi, r1 = st;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
       r0 = fmaxf(r0, __shfl_xor(r0, o));
@@ -721,17 +789,17 @@ __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineK
     const float ap = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mp_new);
     const float at = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - mt_new);
     const float wi = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - mp_new);
-    const float pt = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mt_new);
+    const float pt = st == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st - mt_new);
     lp = lp * ap + (own_p ? ml[1] * wi : 0.f);
-    lt = lt * at + (kh == 0 ? pt : 0.f);
+    lt = lt * at + pt;
 #pragma unroll
     for (int u = 0; u < 4; ++u) xp[u] = xp[u] * ap + (own_p ? v[u] * wi : float4_t{0.f, 0.f, 0.f, 0.f});
-    if (t0 < T) {
-      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+    if (i0 < T) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vacc[2 * e] = __builtin_fmaf(pt, half_bits_to_float(w[e] & 0xffff), vacc[2 * e] * at);
-        vacc[2 * e + 1] = __builtin_fmaf(pt, half_bits_to_float(w[e] >> 16), vacc[2 * e + 1] * at);
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = (e < 4 ? (&vv[0].x)[e] : (&vv[1].x)[e - 4]);
+        vacc[2 * e] = __builtin_fmaf(pt, half_bits_to_float(w & 0xffff), vacc[2 * e] * at);
+        vacc[2 * e + 1] = __builtin_fmaf(pt, half_bits_to_float(w >> 16), vacc[2 * e + 1] * at);
       }
     }
     mp = mp_new;
@@ -745,7 +813,7 @@ __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineK
 #pragma unroll
     for (int e = 0; e < 4; ++e) s_x[(4 * u + e) * kRedPad + tid] = xp[u][e];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s_v[(8 * kh + e) * (kWinTok + 4) + tk] = vacc[e];
+  for (int e = 0; e < kChunk; ++e) s_v[e * kRedPad + tid] = vacc[e];
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     lp += __shfl_xor(lp, o);
@@ -762,13 +830,14 @@ __global__ __launch_bounds__(kCmbThreads) void k2b_combine_kernel(const CombineK
     lpt += s_red[2 * w];
     ltt += s_red[2 * w + 1];
   }
-  // thread (c = tid / 16, part = tid % 16) sums splits part + 16j and tokens part + 16j
+  // thread (c = tid / 16, part = tid % 16) sums splits and tokens part + 16j
   const int c = tid >> 4, part = tid & 15;
   float x = 0.f, wv = 0.f;
 #pragma unroll
-  for (int j = 0; j < kCmbThreads / 16; ++j) x += s_x[c * kRedPad + part + 16 * j];
-#pragma unroll
-  for (int j = 0; j < kWinTok / 16; ++j) wv += s_v[c * (kWinTok + 4) + part + 16 * j];
+  for (int j = 0; j < kCmbThreads / 16; ++j) {
+    x += s_x[c * kRedPad + part + 16 * j];
+    wv += s_v[c * kRedPad + part + 16 * j];
+  }
   x = row_sum16(x);
   wv = row_sum16(wv);
   if (part == 0) {
@@ -813,23 +882,28 @@ static int device_cu_count() {
 
 // Workgroups per sequence: one wave of workgroups over the device's CUs (one
 // 8-wave workgroup per CU), or as many as split_tokens asks for; never more
-// than the sequence has 64-token groups.
+// than the sequence has 64-token groups, except that the recent window's
+// 16-token score tiles get a workgroup each, up to one per CU.
 static int choose_splits(const bmx_k2b_decode_args* a) {
   const int units = (a->max_packed_len + kGroup - 1) / kGroup;
+  const int per_seq = std::max(1, device_cu_count() / a->batch);
   int S;
   if (a->split_tokens > 0)
     S = (a->max_packed_len + a->split_tokens - 1) / a->split_tokens;
   else
-    S = device_cu_count() / a->batch;
+    S = per_seq;
   if (S > units) S = units;
+  const int tiles = (a->tail_cap + 15) / 16;
+  if (S < tiles) S = std::min(tiles, std::max(S, per_seq));
   return S < 1 ? 1 : S;
 }
 
 // Workspace: split partials, accumulators [B][h_kv][G][8][S][16] then
-// (max, sum) [B][h_kv][G][S][2], fp32.
+// (max, sum) [B][h_kv][G][S][2], then window scores [B][h_kv][G][tail_cap],
+// fp32.
 static size_t ws_bytes(const bmx_k2b_decode_args* a, int splits) {
-  const size_t rows = (size_t)a->batch * splits * a->geom.h_kv * a->geom.n_q_groups;
-  return rows * (kD + 2) * sizeof(float);
+  const size_t rows = (size_t)a->batch * a->geom.h_kv * a->geom.n_q_groups;
+  return rows * ((size_t)splits * (kD + 2) + (size_t)a->tail_cap) * sizeof(float);
 }
 
 extern "C" size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* a) {
@@ -990,6 +1064,8 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
     return fail(BMX_E_INVALID, "bmx_k2b_decode: max_pages*16 < max_packed_len");
   if (a->tail_cap < 0 || a->tail_cap > 4096)
     return fail(BMX_E_INVALID, "bmx_k2b_decode: tail_cap must be 0..4096");
+  if (!(a->rope_scaling > 0.0f) || !(a->rope_scaling < 1e30f))
+    return fail(BMX_E_INVALID, "bmx_k2b_decode: rope_scaling must be finite and > 0");
   if (a->split_tokens < 0 || a->split_tokens % kGroup != 0)
     return fail(BMX_E_INVALID, "bmx_k2b_decode: split_tokens must be a multiple of 64");
   if (!a->q || !a->out || !a->packed_len || !a->tail_len)
@@ -1014,6 +1090,7 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   const size_t rows = (size_t)a->batch * max_splits * g.h_kv * g.n_q_groups;
   float* ws_acc = (float*)a->workspace;
   float* ws_ml = ws_acc + rows * kD;
+  float* ws_win = ws_ml + rows * 2;
   const float qscale = a->sm_scale * 1.4426950408889634f;
 
   DecodeKArgs k{};
@@ -1026,6 +1103,11 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   k.pages = a->pages; k.page_table = a->page_table; k.packed_len = a->packed_len;
   k.basis = a->basis; k.basis_stride = a->basis_stride;
   k.qscale_rope = qscale * a->rope_scaling;
+  k.k_tail = a->k_tail;
+  k.ts_b = a->tail_stride_b; k.ts_h = a->tail_stride_h; k.ts_t = a->tail_stride_t;
+  k.tail_cap = a->tail_cap;
+  k.win_rescale = 1.0f / a->rope_scaling;
+  k.ws_win = ws_win;
   for (int j = 0; j < 64; ++j) {
     k.inv_freq[j] = a->inv_freq[j];
     const double step = 64.0 * (double)a->inv_freq[j];  // exact: 64 * fp32
@@ -1060,9 +1142,8 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   CombineKArgs c{};
   c.h_kv = g.h_kv; c.G = g.n_q_groups;
   c.max_splits = max_splits; c.tail_cap = a->tail_cap;
-  c.qscale = qscale;
-  c.out = a->out; c.q = a->q; c.ws_acc = ws_acc; c.ws_ml = ws_ml;
-  c.k_tail = a->k_tail; c.v_tail = a->v_tail;
+  c.out = a->out; c.ws_acc = ws_acc; c.ws_ml = ws_ml; c.ws_win = ws_win;
+  c.v_tail = a->v_tail;
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
   c.tail_len = a->tail_len;
   for (int j = 0; j < 4; ++j) c.v_sign_bits[j] = a->v_sign_bits[j];

@@ -124,7 +124,7 @@ typedef struct {
                                  workgroups per sequence.  Packed tokens are dealt in
                                  64-token groups, balanced over the workgroups; the
                                  recent window is attended by the merge kernel. */
-  void* workspace;            /* device scratch for the split partials (fp32) */
+  void* workspace;            /* device scratch: split partials and window scores (fp32) */
   size_t workspace_bytes;
   void* split_end_event;      /* optional hipEvent_t recorded on the stream between
                                  the split kernel and the combine kernel (timing) */
