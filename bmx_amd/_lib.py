@@ -1,4 +1,5 @@
-"""ctypes binding of libbmx_k2b.so (the C-ABI declared in include/bmx_k2b.h).
+"""ctypes binding of libbmx_k2b.so (the C-ABI declared in include/bmx_k2b.h and
+include/bmx_rtn.h).
 
 The library is the product path: there is no fallback.  ``lib()`` raises if the
 shared object was not built (python -m bmx_amd.build) and every wrapper raises
@@ -93,6 +94,67 @@ class DequantArgs(ct.Structure):
     ]
 
 
+class RtnGeom(ct.Structure):
+    _fields_ = [("h_kv", ct.c_int32), ("n_q_groups", ct.c_int32), ("k_bits", ct.c_int32),
+                ("v_bits", ct.c_int32), ("k_group", ct.c_int32), ("v_group", ct.c_int32)]
+
+
+class RtnAppendArgs(ct.Structure):
+    _fields_ = [
+        ("geom", RtnGeom),
+        ("n_codec_pages", ct.c_int32),
+        ("k", ct.c_void_p),
+        ("k_stride_h", ct.c_int64),
+        ("k_stride_t", ct.c_int64),
+        ("k_dtype", ct.c_int32),
+        ("v", ct.c_void_p),
+        ("v_stride_h", ct.c_int64),
+        ("v_stride_t", ct.c_int64),
+        ("v_dtype", ct.c_int32),
+        ("pages", ct.c_void_p),
+        ("page_ids", ct.c_void_p),
+        ("n_pool_pages", ct.c_int32),
+    ]
+
+
+class RtnDecodeArgs(ct.Structure):
+    _fields_ = [
+        ("geom", RtnGeom),
+        ("batch", ct.c_int32),
+        ("q", ct.c_void_p),
+        ("out", ct.c_void_p),
+        ("pages", ct.c_void_p),
+        ("n_pool_pages", ct.c_int32),
+        ("page_table", ct.c_void_p),
+        ("max_pages", ct.c_int32),
+        ("packed_len", ct.c_void_p),
+        ("max_packed_len", ct.c_int32),
+        ("sm_scale", ct.c_float),
+        ("k_tail", ct.c_void_p),
+        ("v_tail", ct.c_void_p),
+        ("tail_stride_b", ct.c_int64),
+        ("tail_stride_h", ct.c_int64),
+        ("tail_stride_t", ct.c_int64),
+        ("tail_len", ct.c_void_p),
+        ("tail_cap", ct.c_int32),
+        ("split_tokens", ct.c_int32),
+        ("workspace", ct.c_void_p),
+        ("workspace_bytes", ct.c_size_t),
+    ]
+
+
+class RtnDequantArgs(ct.Structure):
+    _fields_ = [
+        ("geom", RtnGeom),
+        ("pages", ct.c_void_p),
+        ("n_pool_pages", ct.c_int32),
+        ("page_ids", ct.c_void_p),
+        ("n_pages", ct.c_int32),
+        ("k_out", ct.c_void_p),
+        ("v_out", ct.c_void_p),
+    ]
+
+
 EXPORTS = {
     "bmx_last_error": (ct.c_char_p, []),
     "bmx_k2b_page_bytes": (ct.c_size_t, [ct.POINTER(Geom)]),
@@ -102,6 +164,11 @@ EXPORTS = {
     "bmx_k2b_decode": (ct.c_int, [ct.POINTER(DecodeArgs), ct.c_void_p]),
     "bmx_k2b_append": (ct.c_int, [ct.POINTER(AppendArgs), ct.c_void_p]),
     "bmx_k2b_dequant": (ct.c_int, [ct.POINTER(DequantArgs), ct.c_void_p]),
+    "bmx_rtn_page_bytes": (ct.c_size_t, [ct.POINTER(RtnGeom)]),
+    "bmx_rtn_append": (ct.c_int, [ct.POINTER(RtnAppendArgs), ct.c_void_p]),
+    "bmx_rtn_decode_workspace_bytes": (ct.c_size_t, [ct.POINTER(RtnDecodeArgs)]),
+    "bmx_rtn_decode": (ct.c_int, [ct.POINTER(RtnDecodeArgs), ct.c_void_p]),
+    "bmx_rtn_dequant": (ct.c_int, [ct.POINTER(RtnDequantArgs), ct.c_void_p]),
 }
 
 _LIB = None

@@ -1,4 +1,4 @@
-"""Build libbmx_k2b.so (gfx950) in-tree with hipcc.
+"""Build libbmx_k2b.so (gfx950: the k2b and RTN paths) in-tree with hipcc.
 
     python -m bmx_amd.build
 
@@ -34,6 +34,7 @@ SOURCES = {
     "k2b_decode.hip": ["-ffp-contract=fast"],
     "k2b_append.hip": ["-ffp-contract=off"],
     "k2b_dequant.hip": ["-ffp-contract=off"],
+    "rtn.hip": ["-ffp-contract=off"],
 }
 
 

@@ -16,6 +16,7 @@ constexpr int kD = 128;      // head_dim
 constexpr int kGroup = 64;   // tokens per key-scale group
 constexpr int kCodec = 128;  // tokens per codec page
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));

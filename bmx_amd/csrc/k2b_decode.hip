@@ -64,7 +64,6 @@ constexpr int kCsBuf = kGroup * kCsRow;     // dwords per group table
 constexpr int kPidWindow = 64;              // page ids held per lane-vector
 constexpr int kCsMaxBufs = 8;               // RoPE table buffers at most (17 KB each)
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 struct DecodeKArgs {
   int h_kv, G, max_splits, max_pages, max_packed_len, n_pool;

@@ -1,0 +1,138 @@
+/*
+ * bmx_rtn.h — C-ABI of the MI355X (gfx950) packed-KV RTN decode path.
+ *
+ * Drop-in boundary for pherber3/bmx's fused RTN path: rtn_token keys
+ * (post-RoPE) and rtn_token values, int codes times a per-(token, channel
+ * group) fp16 scale.  Same conventions as bmx_k2b.h (shared error channel
+ * bmx_last_error(), BMX_* codes, asynchronous calls that never allocate).
+ *
+ * Replaces, in cache/triton_dequant_attention.py:
+ *   fused_decode_attention_packed + _fused_decode_packed_kernel (:580-832)
+ *   build_kv_stacked_packed (:1390-1451): the device stacks become a page pool
+ *   _finalize_decode / _tail_partial / _fused_merge_kernel (:324-575)
+ * and at page commit quantize_packed("rtn_token") (cache/codecs.py:720-722,
+ * quant/rtn.py:23-44) for both keys and values.
+ *
+ * Page format "rtn" (PT = 16 tokens, head_dim 128, h_kv heads; little-endian;
+ * codes are 4-bit offset binary, code + 8, for 2..4-bit RTN; gk, gv = channel
+ * group of the key / value scales, 32, 64 or 128).  Sections, in this order:
+ *   KSCALE [h_kv][16 t][128/gk] fp16   key scale of (token t, group)
+ *   VSCALE [h_kv][4 q][128/gv][4 i] fp16  value scale of (token 4q + i, group)
+ *   KCODE  [h_kv][4 q][16 n][4 w] u32  token n, channels 32w + 8q .. +7, channel
+ *                                      32w + 8q + j in nibble j of the word
+ *   VCODE  [h_kv][4 q][16 c][8 b] u16  channel 16b + c, tokens 4q .. 4q + 3,
+ *                                      token 4q + j in nibble j
+ * ("lane 16q + n" of an MFMA reads each 16-byte code slice contiguously; the
+ * two scale sections come first so that a workgroup stages them with one
+ * cooperative copy.)  Bytes per token = h_kv * (128 + 2 * 128/gk + 2 * 128/gv):
+ * 1152 at h_kv 8, gk = gv = 32.
+ */
+#ifndef BMX_RTN_H
+#define BMX_RTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "bmx_k2b.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+  int32_t h_kv;        /* KV heads: 1..8 for decode, 1..16 for append/dequant */
+  int32_t n_q_groups;  /* query heads per KV head G, 1..16 */
+  int32_t k_bits;      /* RTN bits of the keys, 2..4 */
+  int32_t v_bits;      /* RTN bits of the values, 2..4 */
+  int32_t k_group;     /* key scale group along head_dim: 32, 64 or 128 */
+  int32_t v_group;     /* value scale group along head_dim: 32, 64 or 128 */
+} bmx_rtn_geom;
+
+/* Bytes of one 16-token page (0 if the geometry is unsupported). */
+size_t bmx_rtn_page_bytes(const bmx_rtn_geom* geom);
+
+/* ------------------------------------------------------------------------
+ * Quantize-on-append.  Replaces quantize_packed("rtn_token") of
+ * PackedStreamingLayer.update for both sides (cache/packed_streaming.py:
+ * 640-667 with K post-RoPE, 544-580): per (token, head, group) scale =
+ * max|x| (clamped to 1e-12) / qmax in fp32, code = clamp(round-half-even(x /
+ * scale), -qmax - 1, qmax), qmax = 2^(bits-1) - 1; the page keeps the scale
+ * in fp16, as build_kv_stacked_packed stacks it.  n_codec_pages pages of 128
+ * tokens become 8 * n_codec_pages physical pages listed in page_ids.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  bmx_rtn_geom geom;
+  int32_t n_codec_pages;
+  const void* k;              /* device [h_kv] x [128 * n_codec_pages] x [128] post-RoPE keys */
+  int64_t k_stride_h;         /* element strides (dim 128 contiguous) */
+  int64_t k_stride_t;
+  int32_t k_dtype;            /* BMX_K2B_F16 / _F32 / _BF16 */
+  const void* v;              /* device values, same shape */
+  int64_t v_stride_h;
+  int64_t v_stride_t;
+  int32_t v_dtype;
+  uint8_t* pages;             /* device page pool */
+  const int32_t* page_ids;    /* device [8 * n_codec_pages] physical page ids, in order */
+  int32_t n_pool_pages;
+} bmx_rtn_append_args;
+
+int bmx_rtn_append(const bmx_rtn_append_args* args, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decode attention.  Replaces fused_decode_attention_packed + _finalize_decode
+ * (cache/triton_dequant_attention.py:731-832, 504-575): one query step per
+ * sequence attends to its packed_len[b] committed tokens (keys and values
+ * dequantized in-kernel, code * fp16 scale) and to its tail_len[b] fp16
+ * recent-window tokens, one base-e softmax over their union.  The fields
+ * mean what they mean in bmx_k2b_decode_args.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  bmx_rtn_geom geom;
+  int32_t batch;
+  const float* q;             /* device [batch][h_kv][G][128] fp32, post-RoPE */
+  float* out;                 /* device [batch][h_kv][G][128] fp32 */
+  const uint8_t* pages;
+  int32_t n_pool_pages;
+  const int32_t* page_table;  /* device [batch][max_pages] */
+  int32_t max_pages;
+  const int32_t* packed_len;  /* device [batch], multiples of 128 */
+  int32_t max_packed_len;
+  float sm_scale;
+  const uint16_t* k_tail;     /* device fp16 post-RoPE recent-window keys */
+  const uint16_t* v_tail;
+  int64_t tail_stride_b;
+  int64_t tail_stride_h;
+  int64_t tail_stride_t;
+  const int32_t* tail_len;
+  int32_t tail_cap;           /* 0..4096 */
+  int32_t split_tokens;       /* 0 = one workgroup per CU (default) */
+  void* workspace;            /* device scratch: split partials and window scores */
+  size_t workspace_bytes;
+} bmx_rtn_decode_args;
+
+size_t bmx_rtn_decode_workspace_bytes(const bmx_rtn_decode_args* args);
+int bmx_rtn_decode(const bmx_rtn_decode_args* args, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dequantize pages to dense fp32 keys and values (prefill): the dequant half
+ * of chunked_attention._dense_kv (cache/chunked_attention.py:148-251) for the
+ * rtn_token arms (codes * fp16 scale).  k_out/v_out: device [h_kv][16 *
+ * n_pages][128] fp32.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  bmx_rtn_geom geom;
+  const uint8_t* pages;
+  int32_t n_pool_pages;
+  const int32_t* page_ids;    /* device [n_pages] */
+  int32_t n_pages;
+  float* k_out;
+  float* v_out;
+} bmx_rtn_dequant_args;
+
+int bmx_rtn_dequant(const bmx_rtn_dequant_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BMX_RTN_H */

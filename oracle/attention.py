@@ -226,3 +226,64 @@ def k2b_chunked_attention(q, cache: K2bOracleCache, inv_freq, k_tail, v_tail,
     if k_tail is not None and k_tail.shape[1] > 0:
         attend(k_tail.float(), v_tail.float())
     return acc / lse
+
+
+class RtnOracleCache:
+    """Committed rtn_token pages of one sequence -- post-RoPE keys and values,
+    each a quantize_packed("rtn_token") block dict (packed_streaming.py:640-667,
+    544-580; codecs.py:720-722; rtn.py:23-44) -- and their dequantization as
+    the reference's fused RTN path computes it: code times the fp16 scale of
+    its (token, channel group), the scale stacked in fp16 by
+    build_kv_stacked_packed (triton_dequant_attention.py:1436-1440), read in
+    fp32 by the kernel (:670-715)."""
+
+    def __init__(self, h_kv: int, *, k_bits: int, v_bits: int, k_group: int, v_group: int,
+                 page: int = 128):
+        self.h_kv, self.page = h_kv, page
+        self.k_bits, self.v_bits, self.k_group, self.v_group = k_bits, v_bits, k_group, v_group
+        self.k_blocks: list = []
+        self.v_blocks: list = []
+
+    @property
+    def n_tokens(self) -> int:
+        return len(self.k_blocks) * self.page
+
+    def commit(self, k_page: torch.Tensor, v_page: torch.Tensor):
+        """k_page, v_page: (h_kv, page, d) post-RoPE keys / values (any float dtype)."""
+        kp, _ = C.quantize_rtn_token(C.to_matrix(k_page.float()), self.k_bits, self.k_group)
+        vp, _ = C.quantize_rtn_token(C.to_matrix(v_page.float()), self.v_bits, self.v_group)
+        s = self.n_tokens
+        self.k_blocks.append((kp, s, s + self.page))
+        self.v_blocks.append((vp, s, s + self.page))
+
+    def _dense(self, blocks, group, fp16_scales):
+        out = []
+        for p, _, _ in blocks:
+            sc = p["scale"].half().float() if fp16_scales else p["scale"]
+            out.append(C.from_matrix(C.rtn_dequantize_packed(p["Q_int"], sc, group), self.h_kv))
+        return torch.cat(out, dim=1)
+
+    def dense_kv(self, fp16_scales: bool = True):
+        """(K (h_kv, S, d), V (h_kv, S, d)) fp32."""
+        return (self._dense(self.k_blocks, self.k_group, fp16_scales),
+                self._dense(self.v_blocks, self.v_group, fp16_scales))
+
+    def codes(self):
+        """(kq, ks, vq, vs): codes (h_kv, S, d) and fp32 scales (h_kv, S, d/group)."""
+        def per_head(blocks, group):
+            q = torch.cat([C.from_matrix(p["Q_int"], self.h_kv) for p, _, _ in blocks], dim=1)
+            s = torch.cat([C.from_matrix(p["scale"].squeeze(-1), self.h_kv) for p, _, _ in blocks], dim=1)
+            return q, s
+        kq, ks = per_head(self.k_blocks, self.k_group)
+        vq, vs = per_head(self.v_blocks, self.v_group)
+        return kq, ks, vq, vs
+
+
+def rtn_naive_attention(q, cache: RtnOracleCache, k_tail, v_tail, n_q_groups: int, scale: float):
+    """The fp32 oracle for one decode step over committed RTN pages plus the
+    fp16 tail: (n_q, 1, d)."""
+    K, V = cache.dense_kv()
+    if k_tail is not None and k_tail.shape[1] > 0:
+        K = torch.cat([K, k_tail.float()], dim=1)
+        V = torch.cat([V, v_tail.float()], dim=1)
+    return naive_dense_attention(q, K, V, n_q_groups, scale)

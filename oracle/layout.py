@@ -187,3 +187,87 @@ def unpack_pages(pages: np.ndarray, h_kv: int, rank: int):
                          h * D + 16 * b + np.arange(16)[None, :]] = \
                         (vc[h, :, :, b // 4] >> (8 * (b % 4) + 2 * t)) & 3
     return us16, res, scale16, vidx, vnorm16
+
+
+# ---------------------------------------------------------------------------
+# RTN pages (include/bmx_rtn.h): 16 tokens, per head 4-bit offset-binary codes
+# (code + 8) and fp16 scales of channel groups gk / gv (32, 64 or 128).
+#   KSCALE [h][16 t][128/gk] fp16
+#   VSCALE [h][4 q][128/gv][4 i] fp16        token 4q + i
+#   KCODE  [h][4 q][16 n][4 w] u32           channels 32w + 8q + j at nibble j
+#   VCODE  [h][4 q][16 c][8 b] u16           channel 16b + c, token 4q + j at nibble j
+# ---------------------------------------------------------------------------
+
+
+def rtn_sections(h_kv: int, gk: int, gv: int) -> dict:
+    ngk, ngv = 128 // gk, 128 // gv
+    off = 0
+    out = {}
+    for name, size in (("kscale", h_kv * 16 * ngk * 2), ("vscale", h_kv * 16 * ngv * 2),
+                       ("kcode", h_kv * 1024), ("vcode", h_kv * 1024)):
+        out[name] = (off, size)
+        off += size
+    return out
+
+
+def rtn_page_bytes(h_kv: int, gk: int, gv: int) -> int:
+    s = rtn_sections(h_kv, gk, gv)
+    return s["vcode"][0] + s["vcode"][1]
+
+
+def pack_rtn_pages(kq, ks16, vq, vs16, h_kv: int, gk: int, gv: int) -> np.ndarray:
+    """Codes and fp16 scales of T tokens (T multiple of 16) -> (T/16, page_bytes) u8.
+
+    kq, vq   (h_kv, T, 128) int in [-8, 7]
+    ks16     (h_kv, T, 128/gk) fp16;  vs16 (h_kv, T, 128/gv) fp16"""
+    kq, vq = np.asarray(kq, np.int64), np.asarray(vq, np.int64)
+    T = kq.shape[1]
+    P = T // 16
+    sec = rtn_sections(h_kv, gk, gv)
+    pages = np.zeros((P, rtn_page_bytes(h_kv, gk, gv)), np.uint8)
+    ngk, ngv = 128 // gk, 128 // gv
+    for p in range(P):
+        t0 = 16 * p
+        o, n = sec["kscale"]
+        pages[p, o:o + n] = np.ascontiguousarray(ks16[:, t0:t0 + 16].astype(np.float16)).view(np.uint8).ravel()
+        o, n = sec["vscale"]
+        vsc = vs16[:, t0:t0 + 16].astype(np.float16).reshape(h_kv, 4, 4, ngv).transpose(0, 1, 3, 2)
+        pages[p, o:o + n] = np.ascontiguousarray(vsc).view(np.uint8).ravel()
+        # keys: word (h, q, n, w) = channels 32w + 8q + j
+        kc = (kq[:, t0:t0 + 16] + 8).reshape(h_kv, 16, 4, 4, 8)           # [h][n][w][q][j]
+        words = (kc << (4 * np.arange(8))).sum(-1).astype(np.uint32)         # [h][n][w][q]
+        o, n = sec["kcode"]
+        pages[p, o:o + n] = np.ascontiguousarray(words.transpose(0, 3, 1, 2)).view(np.uint8).ravel()
+        # values: cell (h, q, c, b) = channel 16b + c, tokens 4q + j
+        vc = (vq[:, t0:t0 + 16] + 8).reshape(h_kv, 4, 4, 8, 16)           # [h][q][j][b][c]
+        cells = (vc << (4 * np.arange(4))[None, None, :, None, None]).sum(2).astype(np.uint16)  # [h][q][b][c]
+        o, n = sec["vcode"]
+        pages[p, o:o + n] = np.ascontiguousarray(cells.transpose(0, 1, 3, 2)).view(np.uint8).ravel()
+    return pages
+
+
+def unpack_rtn_pages(pages: np.ndarray, h_kv: int, gk: int, gv: int):
+    """Inverse of pack_rtn_pages: (kq, ks16, vq, vs16)."""
+    P = pages.shape[0]
+    sec = rtn_sections(h_kv, gk, gv)
+    ngk, ngv = 128 // gk, 128 // gv
+    kq = np.zeros((h_kv, 16 * P, 128), np.int64)
+    vq = np.zeros_like(kq)
+    ks = np.zeros((h_kv, 16 * P, ngk), np.float16)
+    vs = np.zeros((h_kv, 16 * P, ngv), np.float16)
+    for p in range(P):
+        t0 = 16 * p
+        o, n = sec["kscale"]
+        ks[:, t0:t0 + 16] = pages[p, o:o + n].view(np.float16).reshape(h_kv, 16, ngk)
+        o, n = sec["vscale"]
+        vs[:, t0:t0 + 16] = pages[p, o:o + n].view(np.float16).reshape(h_kv, 4, ngv, 4) \
+            .transpose(0, 1, 3, 2).reshape(h_kv, 16, ngv)
+        o, n = sec["kcode"]
+        words = pages[p, o:o + n].view(np.uint32).reshape(h_kv, 4, 16, 4).astype(np.int64)   # [h][q][n][w]
+        nib = (words[..., None] >> (4 * np.arange(8))) & 15                                 # [h][q][n][w][j]
+        kq[:, t0:t0 + 16] = nib.transpose(0, 2, 3, 1, 4).reshape(h_kv, 16, 128) - 8
+        o, n = sec["vcode"]
+        cells = pages[p, o:o + n].view(np.uint16).reshape(h_kv, 4, 16, 8).astype(np.int64)   # [h][q][c][b]
+        nib = (cells[..., None] >> (4 * np.arange(4))) & 15                                 # [h][q][c][b][j]
+        vq[:, t0:t0 + 16] = nib.transpose(0, 1, 4, 3, 2).reshape(h_kv, 16, 128) - 8
+    return kq, ks, vq, vs

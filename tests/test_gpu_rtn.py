@@ -1,0 +1,182 @@
+"""GPU parity of the HIP RTN path (rtn_token keys post-RoPE and values) against
+the CPU oracle, through the C-ABI (bmx_amd.rtn -> libbmx_k2b.so).
+
+Bars: codes and fp16 scales bit-exact (the codec is element-wise: max,
+divide, round half to even); dequantized pages bit-exact; attention output
+max-abs <= 2e-3 and ||err||/||ref|| <= 1e-2 against the fp32 oracle
+(code * fp16 scale, one softmax over packed + window tokens).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from bmx_amd import rtn
+from oracle import attention as A
+from oracle import layout as OL
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+MAX_ABS = 2e-3
+REL = 1e-2
+
+
+def _close(out, ref, what):
+    out, ref = out.double().cpu(), ref.double().cpu()
+    err = (out - ref).abs().max().item()
+    rel = ((out - ref).norm() / ref.norm()).item()
+    print(f"{what}: max_abs={err:.3e} rel={rel:.3e}", flush=True)
+    assert err <= MAX_ABS and rel <= REL, f"{what}: max_abs {err:.3e} rel {rel:.3e}"
+
+
+def _keys(h_kv, S, gen, outliers=True):
+    """Config-1 style keys: N(0,1) with 4 fixed channels x10."""
+    k = torch.randn(h_kv, S, 128, generator=gen)
+    if outliers:
+        k[:, :, [3, 40, 77, 101]] *= 10.0
+    return k
+
+
+def _encode(h_kv, k, v, codec, gen=None, n_pool=None):
+    """Append every codec page of (k, v) through the HIP write kernel; returns
+    (pool, page ids in logical order)."""
+    S = k.shape[1]
+    pool = rtn.PagePool(n_pool or S // 16, h_kv, DEV, gen=gen, **codec)
+    ids = pool.alloc(S // 16)
+    rtn.append(k.to(DEV), v.to(DEV), pool.pages, torch.tensor(ids, dtype=torch.int32, device=DEV), **codec)
+    return pool, ids
+
+
+def _oracle(h_kv, k, v, codec):
+    c = A.RtnOracleCache(h_kv, **codec)
+    for p in range(k.shape[1] // 128):
+        c.commit(k[:, p * 128:(p + 1) * 128], v[:, p * 128:(p + 1) * 128])
+    return c
+
+
+@pytest.mark.parametrize("h_kv,codec,dtype", [
+    (8, dict(k_bits=4, v_bits=4, k_group=32, v_group=32), torch.float16),
+    (2, dict(k_bits=2, v_bits=3, k_group=64, v_group=128), torch.bfloat16),
+    (16, dict(k_bits=4, v_bits=2, k_group=128, v_group=32), torch.float32),
+])
+def test_append_codes_bit_exact(h_kv, codec, dtype):
+    gen = torch.Generator().manual_seed(1)
+    S = 256
+    k, v = _keys(h_kv, S, gen).to(dtype), torch.randn(h_kv, S, 128, generator=gen).to(dtype)
+    pool, ids = _encode(h_kv, k, v, codec)
+    torch.cuda.synchronize()
+    pages = pool.pages[torch.tensor(ids, device=DEV)].cpu().numpy()
+    kq, ks, vq, vs = OL.unpack_rtn_pages(pages, h_kv, codec["k_group"], codec["v_group"])
+    ref = _oracle(h_kv, k, v, codec)
+    rkq, rks, rvq, rvs = ref.codes()
+    np.testing.assert_array_equal(kq, rkq.numpy())
+    np.testing.assert_array_equal(vq, rvq.numpy())
+    np.testing.assert_array_equal(ks, rks.numpy().astype(np.float16))
+    np.testing.assert_array_equal(vs, rvs.numpy().astype(np.float16))
+
+
+def test_dequant_bit_exact():
+    gen = torch.Generator().manual_seed(2)
+    h_kv, S = 8, 384
+    codec = dict(k_bits=4, v_bits=4, k_group=32, v_group=64)
+    k, v = _keys(h_kv, S, gen).half(), torch.randn(h_kv, S, 128, generator=gen).half()
+    pool, ids = _encode(h_kv, k, v, codec, gen=torch.Generator().manual_seed(5), n_pool=S // 16 + 7)
+    K, V = rtn.dequant(pool.pages, torch.tensor(ids, dtype=torch.int32, device=DEV), h_kv=h_kv, **codec)
+    rK, rV = _oracle(h_kv, k, v, codec).dense_kv()
+    assert torch.equal(K.cpu(), rK) and torch.equal(V.cpu(), rV)
+
+
+def _decode_case(h_kv, G, S, T, codec, gen, split_tokens=0, outliers=True):
+    k = _keys(h_kv, S + T, gen, outliers)
+    v = torch.randn(h_kv, S + T, 128, generator=gen)
+    k16, v16 = k.half(), v.half()
+    pool, ids = _encode(h_kv, k16[:, :S], v16[:, :S], codec, gen=torch.Generator().manual_seed(3),
+                        n_pool=S // 16 + 5) if S else (rtn.PagePool(1, h_kv, DEV, **codec), [0])
+    q = torch.randn(1, h_kv, G, 128, generator=gen)
+    out = rtn.decode(q.to(DEV), pool.pages, torch.tensor([ids], dtype=torch.int32, device=DEV),
+                     torch.tensor([S], dtype=torch.int32, device=DEV), S, 128 ** -0.5,
+                     k_tail=k16[:, S:].unsqueeze(0).to(DEV), v_tail=v16[:, S:].unsqueeze(0).to(DEV),
+                     tail_len=torch.tensor([T], dtype=torch.int32, device=DEV), tail_cap=T,
+                     split_tokens=split_tokens, **codec)
+    torch.cuda.synchronize()
+    cache = _oracle(h_kv, k16[:, :S], v16[:, :S], codec) if S else None
+    if cache is not None:
+        ref = A.rtn_naive_attention(q.view(h_kv * G, 1, 128), cache, k16[:, S:], v16[:, S:], G, 128 ** -0.5)
+    else:
+        ref = A.naive_dense_attention(q.view(h_kv * G, 1, 128), k16[:, S:].float(), v16[:, S:].float(),
+                                      G, 128 ** -0.5)
+    return out, ref.view(1, h_kv, G, 128)
+
+
+def test_decode_config1_geometry():
+    """Config 1 shape: 32 query / 8 KV heads, d 128, ctx 4096 = 3968 packed +
+    128 fp16 window tokens, 4-bit codes, groups of 32, keys with 4 outlier
+    channels x10, seed 0."""
+    gen = torch.Generator().manual_seed(0)
+    out, ref = _decode_case(8, 4, 3968, 128, dict(k_bits=4, v_bits=4, k_group=32, v_group=32), gen)
+    _close(out, ref, "config1 rtn_token 4b g32")
+
+
+@pytest.mark.parametrize("G", [1, 2, 8, 16])
+def test_decode_query_group_sizes(G):
+    gen = torch.Generator().manual_seed(30 + G)
+    out, ref = _decode_case(4, G, 2048, 100, dict(k_bits=4, v_bits=4, k_group=32, v_group=32), gen)
+    _close(out, ref, f"G {G}")
+
+
+@pytest.mark.parametrize("codec", [dict(k_bits=2, v_bits=2, k_group=64, v_group=64),
+                                   dict(k_bits=3, v_bits=4, k_group=128, v_group=32),
+                                   dict(k_bits=4, v_bits=3, k_group=32, v_group=128)])
+def test_decode_bits_and_groups(codec):
+    gen = torch.Generator().manual_seed(40)
+    out, ref = _decode_case(8, 4, 4096, 160, codec, gen, outliers=False)
+    _close(out, ref, f"bits {codec['k_bits']}/{codec['v_bits']} groups {codec['k_group']}/{codec['v_group']}")
+
+
+def test_decode_split_counts_window_only_and_no_window():
+    gen = torch.Generator().manual_seed(50)
+    codec = dict(k_bits=4, v_bits=4, k_group=32, v_group=32)
+    for st in (64, 512):
+        out, ref = _decode_case(8, 4, 2048, 128, codec, gen, split_tokens=st)
+        _close(out, ref, f"split_tokens {st}")
+    out, ref = _decode_case(8, 4, 1024, 0, codec, gen)
+    _close(out, ref, "no window")
+    out, ref = _decode_case(8, 4, 0, 300, codec, gen)
+    _close(out, ref, "window only")
+
+
+def test_ragged_batch_shuffled_pages():
+    """Batch of 4 sequences, ragged lengths and windows, shuffled physical pages."""
+    gen = torch.Generator().manual_seed(60)
+    h_kv, G = 8, 4
+    codec = dict(k_bits=4, v_bits=4, k_group=32, v_group=32)
+    lens = [128 * int(x) for x in torch.randint(2, 24, (4,), generator=gen)]
+    tails = [int(x) for x in torch.randint(1, 256, (4,), generator=gen)]
+    pool = rtn.PagePool(sum(lens) // 16 + 9, h_kv, DEV, gen=torch.Generator().manual_seed(4), **codec)
+    tables, caches, kts, vts = [], [], [], []
+    for S, T in zip(lens, tails):
+        k = _keys(h_kv, S + T, gen).half()
+        v = torch.randn(h_kv, S + T, 128, generator=gen).half()
+        ids = pool.alloc(S // 16)
+        rtn.append(k[:, :S].to(DEV), v[:, :S].to(DEV), pool.pages, torch.tensor(ids, dtype=torch.int32,
+                                                                                 device=DEV), **codec)
+        tables.append(ids)
+        caches.append(_oracle(h_kv, k[:, :S], v[:, :S], codec))
+        kts.append(k[:, S:])
+        vts.append(v[:, S:])
+    B, cap, mp = len(lens), max(tails), max(len(t) for t in tables)
+    table = torch.zeros(B, mp, dtype=torch.int32)
+    k_tail = torch.zeros(B, h_kv, cap, 128, dtype=torch.float16)
+    v_tail = torch.zeros_like(k_tail)
+    for i in range(B):
+        table[i, :len(tables[i])] = torch.tensor(tables[i])
+        k_tail[i, :, :tails[i]] = kts[i]
+        v_tail[i, :, :tails[i]] = vts[i]
+    q = torch.randn(B, h_kv, G, 128, generator=gen)
+    out = rtn.decode(q.to(DEV), pool.pages, table.to(DEV), torch.tensor(lens, dtype=torch.int32, device=DEV),
+                     max(lens), 128 ** -0.5, k_tail=k_tail.to(DEV), v_tail=v_tail.to(DEV),
+                     tail_len=torch.tensor(tails, dtype=torch.int32, device=DEV), tail_cap=cap, **codec)
+    torch.cuda.synchronize()
+    for i in range(B):
+        ref = A.rtn_naive_attention(q[i].reshape(h_kv * G, 1, 128), caches[i], kts[i], vts[i], G, 128 ** -0.5)
+        _close(out[i], ref.view(h_kv, G, 128), f"ragged seq {i} len {lens[i]} tail {tails[i]}")

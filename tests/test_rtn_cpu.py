@@ -1,0 +1,102 @@
+"""RTN path on the CPU: the page format (numpy packer vs the C-ABI's sizes, and
+its round trip), the RTN oracle cache against the reference's golden codec
+vectors, and host-side argument checks of the C-ABI (no GPU call)."""
+
+import ctypes as ct
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from bmx_amd import _lib, rtn
+from oracle import attention as A
+from oracle import codecs as OC
+from oracle import layout as OL
+
+GOLD = Path(__file__).parent / "golden"
+
+
+@pytest.mark.parametrize("h_kv,gk,gv", [(8, 32, 32), (8, 64, 128), (1, 128, 32), (16, 32, 64)])
+def test_page_bytes_match_numpy_layout(h_kv, gk, gv):
+    assert rtn.page_bytes(h_kv, k_group=gk, v_group=gv) == OL.rtn_page_bytes(h_kv, gk, gv)
+    # 4-bit codes + an fp16 scale per (token, group) for K and V
+    assert OL.rtn_page_bytes(h_kv, gk, gv) == 16 * h_kv * (128 + 2 * 128 // gk + 2 * 128 // gv)
+
+
+def test_headline_rtn_bytes_per_token():
+    assert rtn.page_bytes(8) == 16 * 1152
+
+
+@pytest.mark.parametrize("h_kv,gk,gv", [(8, 32, 32), (2, 64, 128)])
+def test_page_round_trip_and_layout(h_kv, gk, gv):
+    rng = np.random.default_rng(0)
+    T = 32
+    kq, vq = rng.integers(-8, 8, (h_kv, T, 128)), rng.integers(-8, 8, (h_kv, T, 128))
+    ks = rng.random((h_kv, T, 128 // gk)).astype(np.float16)
+    vs = rng.random((h_kv, T, 128 // gv)).astype(np.float16)
+    pages = OL.pack_rtn_pages(kq, ks, vq, vs, h_kv, gk, gv)
+    got = OL.unpack_rtn_pages(pages, h_kv, gk, gv)
+    for a, b in zip(got, (kq, ks, vq, vs)):
+        np.testing.assert_array_equal(a, b)
+    sec = OL.rtn_sections(h_kv, gk, gv)
+    # key word (q 1, token 3, w 2) holds channels 72..79 of token 3, head 0, page 0
+    o = sec["kcode"][0]
+    w = int(pages[0, o:o + 1024].view(np.uint32)[(1 * 16 + 3) * 4 + 2])
+    assert [((w >> (4 * j)) & 15) - 8 for j in range(8)] == list(kq[0, 3, 72:80])
+    # value cell (q 2, c 5, b 3) holds channel 53 of tokens 8..11
+    o = sec["vcode"][0]
+    c = int(pages[0, o:o + 1024].view(np.uint16)[(2 * 16 + 5) * 8 + 3])
+    assert [((c >> (4 * j)) & 15) - 8 for j in range(4)] == list(vq[0, 8:12, 53])
+    # value scale of token 4q + i, group g at [q][g][i]
+    o = sec["vscale"][0]
+    vsc = pages[0, o:o + sec["vscale"][1]].view(np.float16).reshape(h_kv, 4, 128 // gv, 4)
+    assert vsc[0, 2, 0, 1] == vs[0, 9, 0]
+
+
+def test_oracle_cache_matches_reference_golden():
+    """The RTN oracle cache codes a page with quantize_packed("rtn_token")
+    exactly as the reference (golden vectors of quant/rtn.py) and dequantizes
+    with the fp32 scale to the reference's own output."""
+    g = np.load(GOLD / "codecs.npz")
+    M = torch.from_numpy(g["rtn_v_in"])           # (128 tokens, 256 channels): h_kv 2
+    c = A.RtnOracleCache(2, k_bits=4, v_bits=4, k_group=32, v_group=32)
+    c.commit(OC.from_matrix(M, 2), OC.from_matrix(M, 2))
+    kq, ks, vq, vs = c.codes()
+    np.testing.assert_array_equal(OC.to_matrix(vq).numpy(), g["rtn_token_q"])
+    np.testing.assert_array_equal(OC.to_matrix(vs).numpy(), g["rtn_token_scale"][..., 0])
+    _, V32 = c.dense_kv(fp16_scales=False)
+    np.testing.assert_array_equal(OC.to_matrix(V32).numpy(), g["rtn_token_deq"])
+    # the fused path's fp16 scales: code * fp16(scale), exactly
+    _, V16 = c.dense_kv()
+    want = vq.float() * vs.half().float().repeat_interleave(32, dim=-1)
+    assert torch.equal(V16, want)
+
+
+def test_bad_rtn_arguments_are_rejected_with_message():
+    lib = _lib.lib()
+    with pytest.raises(NotImplementedError, match="2..4-bit"):
+        rtn.page_bytes(8, k_bits=8)
+    with pytest.raises(NotImplementedError):
+        rtn.page_bytes(8, k_group=16)
+    a = _lib.RtnDecodeArgs()
+    a.geom = rtn.geom(8, 32, k_bits=4, v_bits=4, k_group=32, v_group=32)   # G too large
+    a.batch = 1
+    assert lib.bmx_rtn_decode(ct.byref(a), None) != 0 and b"n_q_groups" in lib.bmx_last_error()
+    a.geom = rtn.geom(9, 4, k_bits=4, v_bits=4, k_group=32, v_group=32)    # decode takes 1..8 heads
+    assert lib.bmx_rtn_decode(ct.byref(a), None) != 0 and b"h_kv" in lib.bmx_last_error()
+    a.geom = rtn.geom(8, 4, k_bits=4, v_bits=4, k_group=32, v_group=32)
+    a.max_packed_len = 100
+    assert lib.bmx_rtn_decode(ct.byref(a), None) != 0 and b"multiple of 128" in lib.bmx_last_error()
+    ap = _lib.RtnAppendArgs()
+    ap.geom = rtn.geom(8, k_bits=4, v_bits=4, k_group=32, v_group=32)
+    ap.n_codec_pages = 1
+    assert lib.bmx_rtn_append(ct.byref(ap), None) != 0 and b"null pointer" in lib.bmx_last_error()
+
+
+def test_rtn_workspace_size_formula():
+    a = _lib.RtnDecodeArgs()
+    a.geom = rtn.geom(8, 4, k_bits=4, v_bits=4, k_group=32, v_group=32)
+    a.batch, a.max_packed_len, a.split_tokens, a.tail_cap = 2, 65536, 1024, 200
+    n = _lib.lib().bmx_rtn_decode_workspace_bytes(ct.byref(a))
+    assert n == 2 * 8 * 4 * (64 * 130 + 200) * 4   # split partials + window scores per query
