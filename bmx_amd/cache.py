@@ -1,6 +1,6 @@
-"""PackedStreamingCache over the MI355X k2b kernels, under HF ``generate()``.
+"""PackedStreamingCache over the MI355X packed kernels, under HF ``generate()``.
 
-The reference's Python API for the packed k2b path
+The reference's Python API for its fused packed paths
 (cache/packed_streaming.py:270-1222), kept name for name so that
 ``past_key_values=PackedStreamingCache(model.config, *spec_pair("k2b_ph"))``
 drops in:
@@ -32,6 +32,12 @@ What runs where:
   fp16 tail appended, then SDPA with HF's mask
   (``_prefill_dense_attention`` chunked_attention.py:320-395).
 
+The RTN pair (``rtn_token`` keys, post-RoPE, and values; the reference's
+other fused path, packed_streaming.py:904-950) takes the same host logic with
+the RTN kernels: each committed codec page's post-RoPE keys and values, taken
+from the slab, are encoded by ``bmx_rtn_append`` (no key stash, no basis);
+decode is ``bmx_rtn_decode``; prefill is ``bmx_rtn_dequant`` plus SDPA.
+
 There is no CPU path: attention on a tensor that is not on a HIP device raises.
 Values are encoded from the model's own precision (fp16, bf16 or fp32), as the
 reference encodes ``values.float()``; recent-window keys/values enter the
@@ -51,8 +57,8 @@ from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
 from . import codecs as K
-from . import k2b
-from .specs import CacheCodecSpec, check_k2b
+from . import k2b, rtn
+from .specs import CacheCodecSpec, packed_path
 
 ATTN_NAME = "bmx_k2b"
 PAGE = 128          # codec page (packed_streaming.py:438)
@@ -127,7 +133,7 @@ def packed_attention_forward(module, query, key, value, attention_mask, scaling,
     if not hasattr(module, "_packed_layer"):
         raise RuntimeError("PackedStreamingCache.attach(model) must be called before forward")
     if query.shape[0] != 1:
-        raise NotImplementedError("the packed k2b cache serves batch size 1")
+        raise NotImplementedError("the packed cache serves batch size 1")
     q = query.squeeze(0)
     n_q = q.shape[1]
     out = module._packed_layer.attend(q, scaling, is_causal=n_q > 1, attention_mask=attention_mask)
@@ -143,13 +149,16 @@ ALL_MASK_ATTENTION_FUNCTIONS.register(ATTN_NAME, sdpa_mask)
 
 
 class PackedStreamingLayer(DynamicLayer):
-    """Per-layer packed k2b cache: committed codec pages in a device page pool,
-    the frozen key basis, the pre-RoPE key stash and the fp16 recent window."""
+    """Per-layer packed cache: committed codec pages in a device page pool and
+    the fp16 recent window; for k2b also the frozen key basis and the pre-RoPE
+    key stash.  The spec pair picks the kernels: k2b, or RTN for rtn_token
+    keys (post-RoPE) and values (the reference's two fused pairs,
+    packed_streaming.py:904-975)."""
 
     def __init__(self, k_spec: CacheCodecSpec, v_spec: CacheCodecSpec, model_config,
                  recent_window: int = 32, pack_v: bool = True, pack_k: bool = True):
         super().__init__()
-        check_k2b(k_spec, v_spec)
+        self._path = packed_path(k_spec, v_spec)
         self.k_spec, self.v_spec = k_spec, v_spec
         self.model_config = model_config
         self.recent_window = recent_window
@@ -158,15 +167,19 @@ class PackedStreamingLayer(DynamicLayer):
         self._h_kv = getattr(tc, "num_key_value_heads", None) or tc.num_attention_heads
         self._d_head = getattr(tc, "head_dim", None) or tc.hidden_size // tc.num_attention_heads
         if self._d_head != k2b.HEAD_DIM:
-            raise NotImplementedError(f"head_dim {self._d_head}: the k2b kernels take head_dim 128")
+            raise NotImplementedError(f"head_dim {self._d_head}: the packed kernels take head_dim 128")
         if not 1 <= self._h_kv <= 8:
             raise NotImplementedError(f"{self._h_kv} KV heads: the decode kernel takes 1..8")
         self._rank = k_spec.rank
         self._page = PAGE
         inv, scaling = K.rope_inv_freq(tc)
         self._inv_freq, self._rope_scaling = inv, scaling
-        self._consts = k2b.CodecConsts.make(v_bits=2, v_seed=v_spec.seed, inv_freq=inv,
-                                            rope_scaling=scaling)
+        if self._path == "k2b":
+            self._consts = k2b.CodecConsts.make(v_bits=2, v_seed=v_spec.seed, inv_freq=inv,
+                                                rope_scaling=scaling)
+        else:
+            self._rtn = dict(k_bits=k_spec.bits, v_bits=v_spec.bits, k_group=k_spec.group,
+                             v_group=v_spec.group)
         # pre-RoPE key stash
         self._k_pre: torch.Tensor | None = None
         self._k_pre_offset = 0
@@ -189,7 +202,9 @@ class PackedStreamingLayer(DynamicLayer):
 
     def stash_pre_rope(self, out: torch.Tensor) -> None:
         """Append captured pre-RoPE keys: (1, S, h_kv*d) or (1, S, h_kv, d)
-        (packed_streaming.py:448-457)."""
+        (packed_streaming.py:448-457); post-RoPE codecs keep none."""
+        if not self.k_spec.pre_rope:
+            return
         block = reshape_heads(out, self._h_kv, self._d_head)
         self._k_pre = block if self._k_pre is None else torch.cat([self._k_pre, block], dim=1)
 
@@ -199,12 +214,28 @@ class PackedStreamingLayer(DynamicLayer):
         if n_pages <= cap:
             return
         new_cap = max(n_pages, 2 * cap, 64)
-        pb = k2b.page_bytes(self._h_kv, self._rank)
+        pb = self._page_bytes()
         pool = torch.zeros(new_cap, pb, dtype=torch.uint8, device=device)
         if self._pool is not None and self._n_pages:
             pool[: self._n_pages].copy_(self._pool[: self._n_pages])
         self._pool = pool
         self._table = torch.arange(new_cap, dtype=torch.int32, device=device).unsqueeze(0)
+
+    def _page_bytes(self) -> int:
+        if self._path == "k2b":
+            return k2b.page_bytes(self._h_kv, self._rank)
+        return rtn.page_bytes(self._h_kv, **self._rtn)
+
+    def _commit_rtn(self, k_post: torch.Tensor, v: torch.Tensor) -> None:
+        """Encode consecutive codec pages of post-RoPE keys and values
+        (h_kv, 128n, d) into the pool (quantize_packed("rtn_token") per side)."""
+        dev = v.device
+        n = k_post.shape[1] // PAGE
+        first = self._n_pages
+        self._reserve(first + PAGES_PER_CODEC * n, dev)
+        ids = self._table[0, first: first + PAGES_PER_CODEC * n]
+        rtn.append(k_post, v, self._pool, ids, **self._rtn)
+        self._n_pages = first + PAGES_PER_CODEC * n
 
     def _commit(self, k_pre: torch.Tensor, v: torch.Tensor) -> None:
         """Encode consecutive codec pages (h_kv, 128n, d) into the pool."""
@@ -235,20 +266,26 @@ class PackedStreamingLayer(DynamicLayer):
         new_S_q = K.compute_flush_schedule(S, W, self._page)
         if new_S_q > self._committed_S_q:
             start, end = self._committed_S_q, new_S_q
-            if self._k_pre is None:
-                raise RuntimeError("no pre-RoPE keys captured: call cache.attach(model) before prefill")
-            lo, hi = start - self._k_pre_offset, end - self._k_pre_offset
             v_new = values.squeeze(0)[:, : end - start, :]
-            self._commit(self._k_pre[:, lo:hi, :], v_new)
             n_cp = (end - start) // self._page
             page_entries = self._page * C
-            self._quant_bits_k += n_cp * K.bpe_k(self._rank, C) * page_entries
-            self._quant_bits_v += n_cp * K.bpe_v(self._h_kv, C) * page_entries
-            self._committed_S_q = end
-            if hi >= self._k_pre.shape[1]:
-                self._k_pre, self._k_pre_offset = None, end
-            elif hi > 0:
-                self._k_pre, self._k_pre_offset = self._k_pre[:, hi:, :].contiguous(), end
+            if self._path == "rtn":   # post-RoPE keys straight from the slab
+                self._commit_rtn(keys.squeeze(0)[:, : end - start, :], v_new)
+                self._quant_bits_k += n_cp * (self.k_spec.bits + 16.0 / self.k_spec.group) * page_entries
+                self._quant_bits_v += n_cp * (self.v_spec.bits + 16.0 / self.v_spec.group) * page_entries
+                self._committed_S_q = end
+            else:
+                if self._k_pre is None:
+                    raise RuntimeError("no pre-RoPE keys captured: call cache.attach(model) before prefill")
+                lo, hi = start - self._k_pre_offset, end - self._k_pre_offset
+                self._commit(self._k_pre[:, lo:hi, :], v_new)
+                self._quant_bits_k += n_cp * K.bpe_k(self._rank, C) * page_entries
+                self._quant_bits_v += n_cp * K.bpe_v(self._h_kv, C) * page_entries
+                self._committed_S_q = end
+                if hi >= self._k_pre.shape[1]:
+                    self._k_pre, self._k_pre_offset = None, end
+                elif hi > 0:
+                    self._k_pre, self._k_pre_offset = self._k_pre[:, hi:, :].contiguous(), end
             keys = keys[..., end - start:, :].contiguous()
             values = values[..., end - start:, :].contiguous()
             self._packed_len_dev = None
@@ -271,7 +308,7 @@ class PackedStreamingLayer(DynamicLayer):
                attention_mask: torch.Tensor | None = None) -> torch.Tensor:
         """q (n_q_heads, n_q, d) post-RoPE -> (n_q_heads, n_q, d)."""
         if q.device.type != "cuda":
-            raise RuntimeError("the packed k2b cache attends on a HIP device only (no CPU path)")
+            raise RuntimeError("the packed cache attends on a HIP device only (no CPU path)")
         n_heads, n_q, d = q.shape
         G = n_heads // self._h_kv
         if n_q == 1 and not is_causal:
@@ -286,6 +323,17 @@ class PackedStreamingLayer(DynamicLayer):
         k_tail = self.keys.half().contiguous()
         v_tail = self.values.half().contiguous()
         T = k_tail.shape[2]
+        if self._path == "rtn":
+            if P > 0:
+                pool, table = self._pool, self._table
+            else:
+                pool = torch.zeros(1, self._page_bytes(), dtype=torch.uint8, device=dev)
+                table = torch.zeros(1, 1, dtype=torch.int32, device=dev)
+            out = rtn.decode(
+                q.reshape(1, self._h_kv, G, self._d_head).float().contiguous(), pool, table,
+                self._packed_len_dev, P, scaling, k_tail=k_tail, v_tail=v_tail,
+                tail_len=torch.tensor([T], dtype=torch.int32, device=dev), tail_cap=T, **self._rtn)
+            return out.reshape(self._h_kv * G, 1, self._d_head)
         if P > 0:
             pool, table, basis16 = self._pool, self._table, self._basis16
         else:   # window only: the kernel reads no page
@@ -303,7 +351,12 @@ class PackedStreamingLayer(DynamicLayer):
         dev, dt = q.device, q.dtype
         P = self._committed_S_q
         parts_k, parts_v = [], []
-        if P > 0:
+        if P > 0 and self._path == "rtn":   # keys were committed post-RoPE
+            kp, vp = rtn.dequant(self._pool, self._table[0, : P // rtn.PAGE_TOKENS].contiguous(),
+                                 h_kv=self._h_kv, **self._rtn)
+            parts_k.append(kp.to(dt))
+            parts_v.append(vp.to(dt))
+        elif P > 0:
             kp, vp = k2b.dequant(self._pool, self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P,
                                  self._basis16, self._consts, h_kv=self._h_kv, rank=self._rank)
             cos, sin = _rope_tables(self._inv_freq, self._rope_scaling, 0, P, dev)
@@ -334,7 +387,7 @@ class PackedStreamingCache(Cache):
 
     def __init__(self, model_config, k_spec: CacheCodecSpec, v_spec: CacheCodecSpec,
                  recent_window: int = 32, pack_v: bool = True, pack_k: bool = True):
-        check_k2b(k_spec, v_spec)
+        packed_path(k_spec, v_spec)
         wself = weakref.proxy(self)   # no cache -> closure -> cache cycle
 
         def _make_layer():

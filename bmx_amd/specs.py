@@ -1,11 +1,18 @@
 """Codec specification and the recipe registry subset this path serves.
 
 Mirrors the reference's ``CacheCodecSpec`` (cache/specs.py:13-91) field for
-field where the k2b path reads them, and ``spec_pair`` (cache/recipes.py:13-42)
-for the ``k2b_ph`` recipe -- the one recipe the MI355X kernels implement (K:
-pre-RoPE ``lowrank_rtn_channel`` 3-bit residual, rank 16 or 32, 64-token scale
-groups; V: ``turboquant_mse_perhead`` 2-bit).  Every other recipe name raises,
-naming the recipe: there is no CPU or slow path to route it to.
+field where the packed paths read them, and ``spec_pair`` (cache/recipes.py:
+13-42) for the ``k2b_ph`` recipe.  The MI355X kernels implement the two arm
+pairs the reference's attend() sends to a fused kernel
+(cache/packed_streaming.py:904-975):
+
+* k2b: K pre-RoPE ``lowrank_rtn_channel`` 3-bit residual, rank 16 or 32,
+  64-token scale groups; V ``turboquant_mse_perhead`` 2-bit;
+* RTN: K and V ``rtn_token`` (K post-RoPE), 2..4 bits, channel groups of
+  32, 64 or 128.
+
+Every other pair raises, naming what it got: there is no CPU or slow path to
+route it to.
 """
 
 from __future__ import annotations
@@ -36,6 +43,22 @@ def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0):
             CacheCodecSpec(arm="turboquant_mse_perhead", bits=2, seed=seed))
 
 
+def is_rtn(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> bool:
+    """The fused RTN pair (packed_streaming.py:904-912: rtn_token keys, not
+    pre-RoPE, and rtn_token values) within the kernels' bit widths and groups."""
+    return (k_spec.arm == "rtn_token" and v_spec.arm == "rtn_token" and not k_spec.pre_rope
+            and 2 <= k_spec.bits <= 4 and 2 <= v_spec.bits <= 4
+            and k_spec.group in (32, 64, 128) and v_spec.group in (32, 64, 128))
+
+
+def packed_path(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> str:
+    """"k2b" or "rtn" for a spec pair the MI355X kernels implement; raise otherwise."""
+    if is_rtn(k_spec, v_spec):
+        return "rtn"
+    check_k2b(k_spec, v_spec)
+    return "k2b"
+
+
 def check_k2b(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
     """Raise unless (k_spec, v_spec) is a k2b pair the kernels implement."""
     ok = (k_spec.arm == "lowrank_rtn_channel" and k_spec.bits == 3 and k_spec.group == 64
@@ -43,6 +66,6 @@ def check_k2b(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
           and v_spec.arm == "turboquant_mse_perhead" and v_spec.bits == 2)
     if not ok:
         raise NotImplementedError(
-            f"the MI355X k2b path implements K=lowrank_rtn_channel (3 bits, group 64, "
-            f"pre-RoPE, rank 16|32) with V=turboquant_mse_perhead (2 bits); got "
-            f"K={k_spec} V={v_spec}")
+            f"the MI355X packed paths implement K=lowrank_rtn_channel (3 bits, group 64, "
+            f"pre-RoPE, rank 16|32) with V=turboquant_mse_perhead (2 bits), and K=V=rtn_token "
+            f"(2..4 bits, groups 32|64|128, K post-RoPE); got K={k_spec} V={v_spec}")

@@ -163,3 +163,67 @@ def test_config5_qwen3_streaming_append_and_decode():
           flush=True)
     assert hard == 0 and flips <= n_steps // 8
     assert bad <= want.size * 1e-4
+
+
+def test_rtn_layer_streaming_decode_and_prefill():
+    """The RTN pair (rtn_token keys post-RoPE and values, 4 bits, groups of 32)
+    through the cache layer: a 1000-token prefill attended causally through
+    bmx_rtn_dequant + SDPA, then 300 one-token steps, each committing on the
+    128-token grid through bmx_rtn_append and decoding through bmx_rtn_decode,
+    against the RTN oracle fed the same committed pages and windows."""
+    import torch.nn.functional as F
+    from transformers import LlamaConfig
+
+    from bmx_amd.cache import PackedStreamingLayer
+    from bmx_amd.specs import CacheCodecSpec
+    from oracle import attention as A
+
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                      num_hidden_layers=32, rope_theta=500000.0)
+    k_spec = CacheCodecSpec(arm="rtn_token", bits=4, group=32, pre_rope=False)
+    v_spec = CacheCodecSpec(arm="rtn_token", bits=4, group=32)
+    h_kv, G, d, W = 8, 4, 128, 128
+    lay = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=W)
+    gen = torch.Generator().manual_seed(77)
+    n_pre, n_steps = 1000, 300
+    N = n_pre + n_steps
+    k = torch.randn(h_kv, N, d, generator=gen)
+    k[:, :, [3, 40, 77, 101]] *= 10.0
+    k = k.half()
+    v = torch.randn(h_kv, N, d, generator=gen).half()
+    oc = A.RtnOracleCache(h_kv, k_bits=4, v_bits=4, k_group=32, v_group=32)
+
+    def sync_oracle():
+        while oc.n_tokens < lay._committed_S_q:
+            s = oc.n_tokens
+            oc.commit(k[:, s:s + 128], v[:, s:s + 128])
+
+    lay.update(k[:, :n_pre].unsqueeze(0).cuda(), v[:, :n_pre].unsqueeze(0).cuda())
+    sync_oracle()
+    P = lay._committed_S_q
+    assert P == ((n_pre - W) // 128) * 128
+    q = torch.randn(h_kv * G, n_pre, d, generator=gen)
+    out = lay.attend(q.cuda(), d ** -0.5, is_causal=True).float().cpu()
+    Kd, Vd = oc.dense_kv()
+    Kx = torch.cat([Kd, k[:, P:n_pre].float()], 1).repeat_interleave(G, 0)
+    Vx = torch.cat([Vd, v[:, P:n_pre].float()], 1).repeat_interleave(G, 0)
+    ref = F.scaled_dot_product_attention(q.unsqueeze(0), Kx.unsqueeze(0), Vx.unsqueeze(0), is_causal=True,
+                                         scale=d ** -0.5).squeeze(0)
+    err = (out - ref).abs().max().item()
+    print(f"rtn prefill {n_pre} tokens (causal): max_abs {err:.3e}", flush=True)
+    assert err <= 2e-3
+    worst = 0.0
+    for i in range(n_steps):
+        t = n_pre + i
+        lay.update(k[:, t:t + 1].unsqueeze(0).cuda(), v[:, t:t + 1].unsqueeze(0).cuda())
+        sync_oracle()
+        P = lay._committed_S_q
+        qs = torch.randn(h_kv * G, 1, d, generator=gen)
+        o = lay.attend(qs.cuda(), d ** -0.5).double().cpu()
+        r = A.rtn_naive_attention(qs, oc, k[:, P:t + 1], v[:, P:t + 1], G, d ** -0.5).double()
+        e = (o - r).abs().max().item()
+        worst = max(worst, e)
+        assert e <= 2e-3 and ((o - r).norm() / r.norm()).item() <= 1e-2, f"step {i}: {e:.3e}"
+    assert lay.bpe_k == pytest.approx((4.5 * P + 16 * (N - P)) / N)
+    print(f"rtn layer: {n_steps} decode steps, committed {P}, worst max_abs {worst:.3e}, "
+          f"bpe_k {lay.bpe_k:.4f}", flush=True)
