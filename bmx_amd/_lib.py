@@ -96,7 +96,8 @@ class DequantArgs(ct.Structure):
 
 class RtnGeom(ct.Structure):
     _fields_ = [("h_kv", ct.c_int32), ("n_q_groups", ct.c_int32), ("k_bits", ct.c_int32),
-                ("v_bits", ct.c_int32), ("k_group", ct.c_int32), ("v_group", ct.c_int32)]
+                ("v_bits", ct.c_int32), ("k_group", ct.c_int32), ("v_group", ct.c_int32),
+                ("k_arm", ct.c_int32)]
 
 
 class RtnAppendArgs(ct.Structure):

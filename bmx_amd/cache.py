@@ -32,8 +32,9 @@ What runs where:
   fp16 tail appended, then SDPA with HF's mask
   (``_prefill_dense_attention`` chunked_attention.py:320-395).
 
-The RTN pair (``rtn_token`` keys, post-RoPE, and values; the reference's
-other fused path, packed_streaming.py:904-950) takes the same host logic with
+The RTN pairs (``rtn_token`` or ``rtn_channel`` keys, post-RoPE, with
+``rtn_token`` values; the first is the reference's other fused path,
+packed_streaming.py:904-950) take the same host logic with
 the RTN kernels: each committed codec page's post-RoPE keys and values, taken
 from the slab, are encoded by ``bmx_rtn_append`` (no key stash, no basis);
 decode is ``bmx_rtn_decode``; prefill is ``bmx_rtn_dequant`` plus SDPA.
@@ -179,7 +180,8 @@ class PackedStreamingLayer(DynamicLayer):
                                                 rope_scaling=scaling)
         else:
             self._rtn = dict(k_bits=k_spec.bits, v_bits=v_spec.bits, k_group=k_spec.group,
-                             v_group=v_spec.group)
+                             v_group=v_spec.group,
+                             k_arm=rtn.CHANNEL if k_spec.arm == "rtn_channel" else rtn.TOKEN)
         # pre-RoPE key stash
         self._k_pre: torch.Tensor | None = None
         self._k_pre_offset = 0

@@ -43,18 +43,19 @@ constexpr int kRThreads = 64 * kRWaves;
 constexpr int kRGroupPages = 4;                  // 64-token groups, as for k2b
 constexpr int kRGroup = kRGroupPages * kPT;
 constexpr int kRPidWindow = 64;
-constexpr int kRMaxPrefix = 8 * kPT * (4 + 4) * 2;   // scale bytes of a page, h_kv 8, groups of 32
+constexpr int kRMaxPrefix = 8 * (kD + kPT * 4) * 2;  // scale bytes of a page at most: h_kv 8,
+                                                     // channel-arm keys, value groups of 32
 
 // Byte offsets of the four page sections (see include/bmx_rtn.h).
 struct RtnLayout {
   int32_t kscale, vscale, kcode, vcode, bytes;
-  int32_t ngk, ngv;   // scale groups per head and token
-  __host__ __device__ static RtnLayout make(int h_kv, int gk, int gv) {
+  int32_t ngk, ngv;   // scale groups per head and token (ngk: token-arm keys)
+  __host__ __device__ static RtnLayout make(int h_kv, int karm, int gk, int gv) {
     RtnLayout L;
     L.ngk = kD / gk;
     L.ngv = kD / gv;
     L.kscale = 0;
-    L.vscale = L.kscale + h_kv * kPT * L.ngk * 2;
+    L.vscale = L.kscale + h_kv * (karm == BMX_RTN_CHANNEL ? kD : kPT * L.ngk) * 2;
     L.kcode = L.vscale + h_kv * kPT * L.ngv * 2;
     L.vcode = L.kcode + h_kv * 1024;
     L.bytes = L.vcode + h_kv * 1024;
@@ -77,7 +78,7 @@ __device__ __forceinline__ float load_elem(const void* base, int64_t idx, int dt
 // even, clamp); this file is built without floating-point contraction.
 // ---------------------------------------------------------------------------
 struct RtnAppendKArgs {
-  int h_kv, kbits, vbits, gk, gv, n_pool;
+  int h_kv, kbits, vbits, gk, gv, n_pool, karm;
   const void* k;
   int64_t ksh, kst;
   int kdt;
@@ -113,17 +114,20 @@ __global__ __launch_bounds__(256) void rtn_append_kernel(const RtnAppendKArgs a)
   __shared__ int8_t s_v[kPT][kD];
   float x[8];
   int code[8];
-  // keys: word w = l / 4 of quarter q = l % 4 holds channels 32w + 8q .. +7 = 8l .. 8l + 7
+  float s;
+  if (a.karm == BMX_RTN_TOKEN) {   // channel-arm keys: rtn_append_kchan_kernel
+    // keys: word w = l / 4 of quarter q = l % 4 holds channels 32w + 8q .. +7 = 8l .. 8l + 7
 #pragma unroll
-  for (int j = 0; j < 8; ++j) x[j] = load_elem(a.k, h * a.ksh + T * a.kst + 8 * l + j, a.kdt);
-  float s = rtn_codes(x, a.gk, a.kbits, code);
-  uint32_t w = 0;
+    for (int j = 0; j < 8; ++j) x[j] = load_elem(a.k, h * a.ksh + T * a.kst + 8 * l + j, a.kdt);
+    s = rtn_codes(x, a.gk, a.kbits, code);
+    uint32_t w = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) w |= (uint32_t)(code[j] + 8) << (4 * j);
-  reinterpret_cast<uint32_t*>(page + a.L.kcode + h * 1024)[((l & 3) * kPT + tt) * 4 + (l >> 2)] = w;
-  if ((l & (a.gk / 8 - 1)) == 0)
-    reinterpret_cast<uint16_t*>(page + a.L.kscale)[(h * kPT + tt) * a.L.ngk + (8 * l) / a.gk] =
-        float_to_half_bits(s);
+    for (int j = 0; j < 8; ++j) w |= (uint32_t)(code[j] + 8) << (4 * j);
+    reinterpret_cast<uint32_t*>(page + a.L.kcode + h * 1024)[((l & 3) * kPT + tt) * 4 + (l >> 2)] = w;
+    if ((l & (a.gk / 8 - 1)) == 0)
+      reinterpret_cast<uint16_t*>(page + a.L.kscale)[(h * kPT + tt) * a.L.ngk + (8 * l) / a.gk] =
+          float_to_half_bits(s);
+  }
   // values: codes to LDS, then one 16-bit cell (4 tokens of a channel) per write
 #pragma unroll
   for (int j = 0; j < 8; ++j) x[j] = load_elem(a.v, h * a.vsh + T * a.vst + 8 * l + j, a.vdt);
@@ -144,11 +148,52 @@ __global__ __launch_bounds__(256) void rtn_append_kernel(const RtnAppendKArgs a)
   }
 }
 
+// position of channel c in a channel-arm KSCALE row: [4 b][4 q][8 j'], channel
+// 32b + 8q + p(j'), p = 0 4 1 5 2 6 3 7 (the pair order of nibble_pairs)
+__host__ __device__ __forceinline__ int kchan_slot(int c) {
+  const int j = c & 7;
+  return (c & ~7) + 2 * (j & 3) + (j >> 2);
+}
+
+// Channel-arm keys (quantize_packed("rtn_channel"), codecs.py:723-725: the
+// token axis grouped per channel).  grid (n_codec_pages * 128 / gk, h_kv),
+// block 128: thread c owns channel c of one gk-token group, spanning gk / 16
+// pages; codes go through LDS to be packed into the pages' code words, and
+// the group's fp16 scales are written into each of its pages.
+__global__ __launch_bounds__(128) void rtn_append_kchan_kernel(const RtnAppendKArgs a) {
+  const int grp = blockIdx.x, h = blockIdx.y, c = threadIdx.x;
+  const int64_t T0 = (int64_t)grp * a.gk;   // first token of the group within the call
+  __shared__ int8_t s_k[kCodec][kD];
+  float amax = 0.f;
+  for (int t = 0; t < a.gk; ++t) amax = fmaxf(amax, fabsf(load_elem(a.k, h * a.ksh + (T0 + t) * a.kst + c, a.kdt)));
+  const int qmax = (1 << (a.kbits - 1)) - 1;
+  const float scale = fmaxf(amax, 1e-12f) / (float)qmax;
+  for (int t = 0; t < a.gk; ++t) {
+    const float r = __builtin_rintf(load_elem(a.k, h * a.ksh + (T0 + t) * a.kst + c, a.kdt) / scale);
+    s_k[t][c] = (int8_t)fminf(fmaxf(r, (float)(-qmax - 1)), (float)qmax);
+  }
+  const int n_pg = a.gk / kPT;
+  const int pg0 = (int)(T0 / kPT);
+  for (int p = 0; p < n_pg; ++p) {
+    uint8_t* page = a.pages + clamp_page(a.page_ids[pg0 + p], a.n_pool) * a.L.bytes;
+    reinterpret_cast<uint16_t*>(page + a.L.kscale)[h * kD + kchan_slot(c)] = float_to_half_bits(scale);
+  }
+  __syncthreads();
+  for (int e = c; e < n_pg * 256; e += 128) {   // word (q, n, w): token n, channels 32w + 8q ..
+    const int p = e >> 8, qq = (e >> 6) & 3, n = (e >> 2) & 15, w = e & 3;
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) word |= (uint32_t)(s_k[p * kPT + n][32 * w + 8 * qq + j] + 8) << (4 * j);
+    uint8_t* page = a.pages + clamp_page(a.page_ids[pg0 + p], a.n_pool) * a.L.bytes;
+    reinterpret_cast<uint32_t*>(page + a.L.kcode + h * 1024)[e & 255] = word;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Dequantize: grid (n_pages, h_kv), block 256, thread (token tt, slice l).
 // ---------------------------------------------------------------------------
 struct RtnDequantKArgs {
-  int h_kv, n_pool;
+  int h_kv, n_pool, karm;
   const uint8_t* pages;
   const int32_t* page_ids;
   int64_t n_tok;
@@ -164,10 +209,13 @@ __global__ __launch_bounds__(256) void rtn_dequant_kernel(const RtnDequantKArgs 
   const uint8_t* page = a.pages + clamp_page(a.page_ids[p], a.n_pool) * a.L.bytes;
   const int64_t row = ((int64_t)h * a.n_tok + (int64_t)p * kPT + tt) * kD;
   const uint32_t w = reinterpret_cast<const uint32_t*>(page + a.L.kcode + h * 1024)[((l & 3) * kPT + tt) * 4 + (l >> 2)];
-  const float sk = half_bits_to_float(
-      reinterpret_cast<const uint16_t*>(page + a.L.kscale)[(h * kPT + tt) * a.L.ngk + (8 * l) / a.gk]);
+  const uint16_t* ksc = reinterpret_cast<const uint16_t*>(page + a.L.kscale);
+  const float sk = a.karm == BMX_RTN_TOKEN ? half_bits_to_float(ksc[(h * kPT + tt) * a.L.ngk + (8 * l) / a.gk]) : 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) a.k_out[row + 8 * l + j] = (float)((int)((w >> (4 * j)) & 15u) - 8) * sk;
+  for (int j = 0; j < 8; ++j) {
+    const float s = a.karm == BMX_RTN_TOKEN ? sk : half_bits_to_float(ksc[h * kD + kchan_slot(8 * l + j)]);
+    a.k_out[row + 8 * l + j] = (float)((int)((w >> (4 * j)) & 15u) - 8) * s;
+  }
   const uint16_t* vcode = reinterpret_cast<const uint16_t*>(page + a.L.vcode + h * 1024);
   const float sv = half_bits_to_float(reinterpret_cast<const uint16_t*>(page + a.L.vscale)
                                           [((h * 4 + (tt >> 2)) * a.L.ngv + (8 * l) / a.gv) * 4 + (tt & 3)]);
@@ -275,7 +323,7 @@ __device__ __noinline__ void rtn_empty_range(const RtnDecodeKArgs& a, int b, int
 
 // SW: query slot width (G rounded up to 4, 8 or 16); the 16 score columns of a
 // page hold 16 / SW pages after compaction.  NGK: key scale groups per token
-// (128 / k_group).
+// (128 / k_group) of token-arm keys, 0 for channel-arm keys.
 template <int SW, int NGK>
 __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDecodeKArgs a) {
   constexpr int NSLOT = 16 / SW;
@@ -338,16 +386,30 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
     const int id = __builtin_amdgcn_readlane(pidv, gi * kRGroupPages + pp - pid_base);
     return a.pages + (int64_t)id * pb;
   };
-  auto load_prefix = [&](int gi) -> uint4 {
-    const int c = min(tid, pre_chunks - 1);
+  // the 4 pages' scale sections, 16-byte chunk c (tid and tid + 512: the
+  // channel-arm key scales make them up to 768 chunks)
+  struct Pre { uint4 c0, c1; };
+  auto load_chunk = [&](int gi, int c) -> uint4 {
+    c = min(c, pre_chunks - 1);
     const int pp = c / chunks_pp;
     const int id = __shfl(pidv, gi * kRGroupPages + pp - pid_base);
     return *reinterpret_cast<const uint4*>(a.pages + (int64_t)id * pb + (c - pp * chunks_pp) * 16);
   };
-  auto store_prefix = [&](uint4 v, int slot) {
+  auto load_prefix = [&](int gi) -> Pre {
+    Pre r;
+    r.c0 = load_chunk(gi, tid);
+    r.c1 = pre_chunks > kRThreads ? load_chunk(gi, tid + kRThreads) : r.c0;
+    return r;
+  };
+  auto store_prefix = [&](const Pre& v, int slot) {
     if (tid < pre_chunks) {
       const int pp = tid / chunks_pp;
-      *reinterpret_cast<uint4*>(&ring[slot][pp][(tid - pp * chunks_pp) * 16]) = v;
+      *reinterpret_cast<uint4*>(&ring[slot][pp][(tid - pp * chunks_pp) * 16]) = v.c0;
+    }
+    const int c1 = tid + kRThreads;
+    if (c1 < pre_chunks) {
+      const int pp = c1 / chunks_pp;
+      *reinterpret_cast<uint4*>(&ring[slot][pp][(c1 - pp * chunks_pp) * 16]) = v.c1;
     }
   };
   const uint32_t kc_off = (uint32_t)(a.L.kcode + h * 1024 + lane * 16);
@@ -355,7 +417,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
   auto load_kc = [&](int gi, int pp) { return *reinterpret_cast<const uint4*>(page_ptr(gi, pp) + kc_off); };
   auto load_vc = [&](int gi, int pp) { return *reinterpret_cast<const uint4*>(page_ptr(gi, pp) + vc_off); };
 
-  uint4 pre = load_prefix(0);
+  Pre pre = load_prefix(0);
   uint4 kc[kRGroupPages], vc[kRGroupPages];
 #pragma unroll
   for (int pp = 0; pp < kRGroupPages; ++pp) {
@@ -404,7 +466,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
       pid_base = gi * kRGroupPages;
       pidv = load_ids(pid_base, n_pages);
     }
-    const uint4 pre_n = load_prefix(gn);
+    const Pre pre_n = load_prefix(gn);
     uint4 kc_n[kRGroupPages], vc_n[kRGroupPages];
     if (active) {
 #pragma unroll
@@ -420,6 +482,33 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
       float4_t sc[kRGroupPages];
 #pragma unroll
       for (int pp = 0; pp < kRGroupPages; ++pp) {
+        if constexpr (NGK == 0) {
+          // channel-arm keys: the scale varies along the MFMA's K axis, so it
+          // goes into the A operand, as an exact fp16 sum hi + lo of code *
+          // scale (lo = the rounding residual of hi, from one packed FMA)
+          const uint4* ksp = reinterpret_cast<const uint4*>(&ring[gi & 1][pp][a.L.kscale]) + h * 16 + q;
+          const uint32_t kw4[4] = {kc[pp].x, kc[pp].y, kc[pp].z, kc[pp].w};
+          float4_t s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) {
+            const uint4 sp = ksp[4 * bb];
+            const uint32_t s4[4] = {sp.x, sp.y, sp.z, sp.w};
+            uint32_t cp[4];
+            nibble_pairs(kw4[bb], cp);
+            union { uint32_t u[4]; half8_t v; } khi, klo;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+              const half2_t hi = as_h2r(cp[p]) * as_h2r(s4[p]);
+              khi.u[p] = as_u32r(hi);
+              klo.u[p] = as_u32r(__builtin_elementwise_fma(as_h2r(cp[p]), as_h2r(s4[p]), -hi));
+            }
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi.v, qh[bb], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi.v, ql[bb], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(klo.v, qh[bb], s, 0, 0, 0);
+          }
+          sc[pp] = s;
+          continue;
+        } else {
         // scales of the lane's score rows, tokens 4q .. 4q + 3: [4][NGK] fp16
         const uint16_t* ksp = reinterpret_cast<const uint16_t*>(&ring[gi & 1][pp][a.L.kscale]) +
                               (h * kPT + 4 * q) * NGK;
@@ -453,6 +542,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
           for (int i = 0; i < 4; ++i) s[i] = __builtin_fmaf(ksc[i][(bb * NGK) / 4], d[i], s[i]);
         }
         sc[pp] = s;
+        }
       }
       // ---- compaction: page r*NSLOT + s moves to columns [s*SW, (s+1)*SW) ----
       float4_t cr[NCR];
@@ -591,13 +681,17 @@ static bool rtn_geom_ok(const bmx_rtn_geom* g, int max_h, std::string& why) {
   }
   auto gok = [](int x) { return x == 32 || x == 64 || x == 128; };
   if (!gok(g->k_group) || !gok(g->v_group)) { why = "k_group and v_group must be 32, 64 or 128"; return false; }
+  if (g->k_arm != BMX_RTN_TOKEN && g->k_arm != BMX_RTN_CHANNEL) {
+    why = "k_arm must be BMX_RTN_TOKEN or BMX_RTN_CHANNEL";
+    return false;
+  }
   return true;
 }
 
 extern "C" size_t bmx_rtn_page_bytes(const bmx_rtn_geom* g) {
   std::string why;
   if (!rtn_geom_ok(g, 16, why)) return 0;
-  return (size_t)RtnLayout::make(g->h_kv, g->k_group, g->v_group).bytes;
+  return (size_t)RtnLayout::make(g->h_kv, g->k_arm, g->k_group, g->v_group).bytes;
 }
 
 extern "C" int bmx_rtn_append(const bmx_rtn_append_args* a, void* stream) {
@@ -618,8 +712,11 @@ extern "C" int bmx_rtn_append(const bmx_rtn_append_args* a, void* stream) {
   k.n_pool = a->n_pool_pages;
   k.k = a->k; k.ksh = a->k_stride_h; k.kst = a->k_stride_t; k.kdt = a->k_dtype;
   k.v = a->v; k.vsh = a->v_stride_h; k.vst = a->v_stride_t; k.vdt = a->v_dtype;
-  k.pages = a->pages; k.page_ids = a->page_ids;
-  k.L = RtnLayout::make(g.h_kv, g.k_group, g.v_group);
+  k.pages = a->pages; k.page_ids = a->page_ids; k.karm = g.k_arm;
+  k.L = RtnLayout::make(g.h_kv, g.k_arm, g.k_group, g.v_group);
+  if (g.k_arm == BMX_RTN_CHANNEL)
+    hipLaunchKernelGGL(rtn_append_kchan_kernel, dim3(a->n_codec_pages * (kCodec / g.k_group), g.h_kv), dim3(kD),
+                       0, (hipStream_t)stream, k);
   hipLaunchKernelGGL(rtn_append_kernel, dim3(a->n_codec_pages * (kCodec / kPT), g.h_kv), dim3(256), 0,
                      (hipStream_t)stream, k);
   hipError_t e = hipGetLastError();
@@ -639,8 +736,8 @@ extern "C" int bmx_rtn_dequant(const bmx_rtn_dequant_args* a, void* stream) {
   const bmx_rtn_geom& g = a->geom;
   k.h_kv = g.h_kv; k.n_pool = a->n_pool_pages; k.pages = a->pages; k.page_ids = a->page_ids;
   k.n_tok = (int64_t)a->n_pages * kPT; k.k_out = a->k_out; k.v_out = a->v_out;
-  k.gk = g.k_group; k.gv = g.v_group;
-  k.L = RtnLayout::make(g.h_kv, g.k_group, g.v_group);
+  k.gk = g.k_group; k.gv = g.v_group; k.karm = g.k_arm;
+  k.L = RtnLayout::make(g.h_kv, g.k_arm, g.k_group, g.v_group);
   hipLaunchKernelGGL(rtn_dequant_kernel, dim3(a->n_pages, g.h_kv), dim3(256), 0, (hipStream_t)stream, k);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return rfail(BMX_E_HIP, std::string("bmx_rtn_dequant: launch: ") + hipGetErrorString(e));
@@ -685,7 +782,9 @@ extern "C" size_t bmx_rtn_decode_workspace_bytes(const bmx_rtn_decode_args* a) {
 
 template <int SW>
 static void launch_rtn_split(int ngk, dim3 grid, const RtnDecodeKArgs& k, hipStream_t st) {
-  if (ngk == 4)
+  if (ngk == 0)
+    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 0>), grid, dim3(kRThreads), 0, st, k);
+  else if (ngk == 4)
     hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 4>), grid, dim3(kRThreads), 0, st, k);
   else if (ngk == 2)
     hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 2>), grid, dim3(kRThreads), 0, st, k);
@@ -733,7 +832,7 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   k.h_kv = g.h_kv; k.G = g.n_q_groups; k.max_splits = S; k.max_pages = a->max_pages;
   k.max_packed_len = a->max_packed_len; k.n_pool = a->n_pool_pages > 0 ? a->n_pool_pages : 1;
   k.gk = g.k_group; k.gv = g.v_group;
-  k.L = RtnLayout::make(g.h_kv, g.k_group, g.v_group);
+  k.L = RtnLayout::make(g.h_kv, g.k_arm, g.k_group, g.v_group);
   k.prefix_bytes = k.L.kcode;
   k.q = a->q; k.ws_acc = ws_acc; k.ws_ml = ws_ml;
   k.pages = a->pages; k.page_table = a->page_table; k.packed_len = a->packed_len;
@@ -741,7 +840,7 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   k.k_tail = a->k_tail; k.ts_b = a->tail_stride_b; k.ts_h = a->tail_stride_h; k.ts_t = a->tail_stride_t;
   k.tail_cap = a->tail_cap; k.win_rescale = 1.0f; k.ws_win = ws_win;
   dim3 grid(S, a->batch);
-  const int ngk = kD / g.k_group;
+  const int ngk = g.k_arm == BMX_RTN_CHANNEL ? 0 : kD / g.k_group;
   if (g.n_q_groups <= 4)
     launch_rtn_split<4>(ngk, grid, k, st);
   else if (g.n_q_groups <= 8)

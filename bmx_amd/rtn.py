@@ -1,6 +1,7 @@
 """Host wrappers of the MI355X RTN path (include/bmx_rtn.h): rtn_token keys
 (post-RoPE) and values, 2..4-bit codes times a per-(token, channel group) fp16
-scale, in 16-token pages of a device pool.
+scale, in 16-token pages of a device pool; keys may instead be rtn_channel
+(k_arm=CHANNEL: a scale per (channel, group of k_group tokens)).
 
 Mirrors the reference's fused RTN path (cache/triton_dequant_attention.py:
 580-832 and 1390-1451, called from PackedStreamingLayer.attend,
@@ -21,19 +22,21 @@ from .k2b import DecodeWorkspace, _need, _ptr, _stream, _V_DTYPES
 HEAD_DIM = 128
 PAGE_TOKENS = 16
 CODEC_PAGE = 128
+TOKEN, CHANNEL = 0, 1   # key arms: rtn_token, rtn_channel (BMX_RTN_TOKEN / BMX_RTN_CHANNEL)
 
 
-def geom(h_kv: int, G: int = 1, *, k_bits: int, v_bits: int, k_group: int, v_group: int):
-    return _lib.RtnGeom(h_kv, G, k_bits, v_bits, k_group, v_group)
+def geom(h_kv: int, G: int = 1, *, k_bits: int, v_bits: int, k_group: int, v_group: int, k_arm: int = TOKEN):
+    return _lib.RtnGeom(h_kv, G, k_bits, v_bits, k_group, v_group, k_arm)
 
 
-def page_bytes(h_kv: int, *, k_bits: int = 4, v_bits: int = 4, k_group: int = 32, v_group: int = 32) -> int:
-    g = geom(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group)
+def page_bytes(h_kv: int, *, k_bits: int = 4, v_bits: int = 4, k_group: int = 32, v_group: int = 32,
+               k_arm: int = TOKEN) -> int:
+    g = geom(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     n = _lib.lib().bmx_rtn_page_bytes(ct.byref(g))
     if n == 0:
         raise NotImplementedError(
-            f"RTN pages take 2..4-bit codes, channel groups of 32, 64 or 128 and 1..16 KV heads "
-            f"(got h_kv {h_kv}, bits {k_bits}/{v_bits}, groups {k_group}/{v_group})")
+            f"RTN pages take 2..4-bit codes, groups of 32, 64 or 128 and 1..16 KV heads "
+            f"(got h_kv {h_kv}, bits {k_bits}/{v_bits}, groups {k_group}/{v_group}, key arm {k_arm})")
     return int(n)
 
 
@@ -54,7 +57,7 @@ class PagePool:
 
 
 def append(k: torch.Tensor, v: torch.Tensor, pages: torch.Tensor, page_ids: torch.Tensor, *,
-           k_bits: int, v_bits: int, k_group: int, v_group: int) -> None:
+           k_bits: int, v_bits: int, k_group: int, v_group: int, k_arm: int = TOKEN) -> None:
     """Quantize n codec pages (k: (h_kv, 128n, 128) post-RoPE keys, v: same
     shape; fp16, bf16 or fp32, last dim contiguous) into the 8n pages listed in
     page_ids (int32, device)."""
@@ -65,11 +68,11 @@ def append(k: torch.Tensor, v: torch.Tensor, pages: torch.Tensor, page_ids: torc
     _need(k.stride(2) == 1 and v.stride(2) == 1, "k/v last dim must be contiguous")
     n = T // CODEC_PAGE
     _need(page_ids.dtype == torch.int32 and page_ids.numel() == 8 * n, "page_ids must be int32[8n]")
-    pb = page_bytes(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group)
+    pb = page_bytes(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     _need(pages.dtype == torch.uint8 and pages.dim() == 2 and pages.shape[1] == pb and pages.is_contiguous(),
           "pages must be a contiguous uint8 (n_pages, page_bytes) pool")
     a = _lib.RtnAppendArgs()
-    a.geom = geom(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group)
+    a.geom = geom(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     a.n_codec_pages = n
     a.k, a.k_stride_h, a.k_stride_t, a.k_dtype = _ptr(k), k.stride(0), k.stride(1), _V_DTYPES[k.dtype]
     a.v, a.v_stride_h, a.v_stride_t, a.v_dtype = _ptr(v), v.stride(0), v.stride(1), _V_DTYPES[v.dtype]
@@ -79,7 +82,7 @@ def append(k: torch.Tensor, v: torch.Tensor, pages: torch.Tensor, page_ids: torc
 
 def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packed_len: torch.Tensor,
            max_packed_len: int, sm_scale: float, *, k_bits: int, v_bits: int, k_group: int, v_group: int,
-           k_tail: torch.Tensor | None = None, v_tail: torch.Tensor | None = None,
+           k_arm: int = TOKEN, k_tail: torch.Tensor | None = None, v_tail: torch.Tensor | None = None,
            tail_len: torch.Tensor | None = None, tail_cap: int = 0, out: torch.Tensor | None = None,
            split_tokens: int = 0, workspace: DecodeWorkspace | None = None, _capture=None) -> torch.Tensor:
     """One decode step.  q (B, h_kv, G, 128) fp32 post-RoPE -> (B, h_kv, G, 128) fp32;
@@ -89,7 +92,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
     dev = q.device
     _need(d == HEAD_DIM and q.dtype == torch.float32 and q.is_contiguous(),
           "q must be contiguous fp32 (B, h_kv, G, 128)")
-    pb = page_bytes(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group)
+    pb = page_bytes(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     _need(pages.dtype == torch.uint8 and pages.shape[1] == pb, "pages must be (n_pages, page_bytes) uint8")
     _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B
           and page_table.is_contiguous(), "page_table must be contiguous int32 (B, max_pages)")
@@ -100,7 +103,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
     if tail_len is None:
         tail_len = torch.zeros(B, dtype=torch.int32, device=dev)
     a = _lib.RtnDecodeArgs()
-    a.geom = geom(h_kv, G, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group)
+    a.geom = geom(h_kv, G, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     a.batch = B
     a.q, a.out = _ptr(q), _ptr(out)
     a.pages, a.n_pool_pages = _ptr(pages), pages.shape[0]
@@ -137,7 +140,7 @@ class DecodePlan:
     (the bound tensors must stay alive and keep their storage)."""
 
     def __init__(self, q, pages, page_table, packed_len, max_packed_len, sm_scale, *, k_bits, v_bits,
-                 k_group, v_group, k_tail=None, v_tail=None, tail_len=None, tail_cap=0, out=None,
+                 k_group, v_group, k_arm=TOKEN, k_tail=None, v_tail=None, tail_len=None, tail_cap=0, out=None,
                  split_tokens=0, workspace: DecodeWorkspace | None = None):
         self.out = torch.empty_like(q) if out is None else out
         if tail_len is None:
@@ -146,7 +149,7 @@ class DecodePlan:
         self.ws = workspace or DecodeWorkspace()
         captured = {}
         decode(q, pages, page_table, packed_len, max_packed_len, sm_scale, k_bits=k_bits, v_bits=v_bits,
-               k_group=k_group, v_group=v_group, k_tail=k_tail, v_tail=v_tail, tail_len=tail_len,
+               k_group=k_group, v_group=v_group, k_arm=k_arm, k_tail=k_tail, v_tail=v_tail, tail_len=tail_len,
                tail_cap=tail_cap, out=self.out, split_tokens=split_tokens, workspace=self.ws,
                _capture=lambda a: captured.setdefault("a", a))
         self.args = captured["a"]
@@ -161,14 +164,14 @@ class DecodePlan:
 
 
 def dequant(pages: torch.Tensor, page_ids: torch.Tensor, *, h_kv: int, k_bits: int, v_bits: int,
-            k_group: int, v_group: int):
+            k_group: int, v_group: int, k_arm: int = TOKEN):
     """Pages (in order) -> dense fp32 (K (h_kv, 16n, 128), V (h_kv, 16n, 128))."""
     n = page_ids.numel()
     _need(page_ids.dtype == torch.int32 and page_ids.is_contiguous(), "page_ids must be contiguous int32")
     k_out = torch.empty(h_kv, n * PAGE_TOKENS, HEAD_DIM, dtype=torch.float32, device=pages.device)
     v_out = torch.empty_like(k_out)
     a = _lib.RtnDequantArgs()
-    a.geom = geom(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group)
+    a.geom = geom(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     a.pages, a.n_pool_pages = _ptr(pages), pages.shape[0]
     a.page_ids, a.n_pages = _ptr(page_ids), n
     a.k_out, a.v_out = _ptr(k_out), _ptr(v_out)

@@ -3,8 +3,11 @@
  *
  * Drop-in boundary for pherber3/bmx's fused RTN path: rtn_token keys
  * (post-RoPE) and rtn_token values, int codes times a per-(token, channel
- * group) fp16 scale.  Same conventions as bmx_k2b.h (shared error channel
- * bmx_last_error(), BMX_* codes, asynchronous calls that never allocate).
+ * group) fp16 scale.  Keys may also be rtn_channel (a per-(channel, token
+ * group) scale: config 1 and KIVI, which the reference runs on its chunked
+ * path only, cache/codecs.py:723-725).  Same conventions as bmx_k2b.h (shared
+ * error channel bmx_last_error(), BMX_* codes, asynchronous calls that never
+ * allocate).
  *
  * Replaces, in cache/triton_dequant_attention.py:
  *   fused_decode_attention_packed + _fused_decode_packed_kernel (:580-832)
@@ -14,9 +17,13 @@
  * quant/rtn.py:23-44) for both keys and values.
  *
  * Page format "rtn" (PT = 16 tokens, head_dim 128, h_kv heads; little-endian;
- * codes are 4-bit offset binary, code + 8, for 2..4-bit RTN; gk, gv = channel
- * group of the key / value scales, 32, 64 or 128).  Sections, in this order:
- *   KSCALE [h_kv][16 t][128/gk] fp16   key scale of (token t, group)
+ * codes are 4-bit offset binary, code + 8, for 2..4-bit RTN; gk, gv = group
+ * of the key / value scales, 32, 64 or 128: channels, or tokens for
+ * rtn_channel keys).  Sections, in this order:
+ *   KSCALE [h_kv][16 t][128/gk] fp16   rtn_token: key scale of (token t, group)
+ *          [h_kv][4 b][4 q][8 j] fp16  rtn_channel: scale of channel 32b + 8q +
+ *                                      p(j), p = 0 4 1 5 2 6 3 7, for the token
+ *                                      group that holds the page
  *   VSCALE [h_kv][4 q][128/gv][4 i] fp16  value scale of (token 4q + i, group)
  *   KCODE  [h_kv][4 q][16 n][4 w] u32  token n, channels 32w + 8q .. +7, channel
  *                                      32w + 8q + j in nibble j of the word
@@ -24,8 +31,10 @@
  *                                      token 4q + j in nibble j
  * ("lane 16q + n" of an MFMA reads each 16-byte code slice contiguously; the
  * two scale sections come first so that a workgroup stages them with one
- * cooperative copy.)  Bytes per token = h_kv * (128 + 2 * 128/gk + 2 * 128/gv):
- * 1152 at h_kv 8, gk = gv = 32.
+ * cooperative copy.)  Bytes per token = h_kv * (128 + 2 * 128/gk + 2 * 128/gv)
+ * for rtn_token keys (1152 at h_kv 8, gk = gv = 32), h_kv * (144 + 2 * 128/gv)
+ * for rtn_channel keys (the group's channel scales repeated in each of its
+ * pages).
  */
 #ifndef BMX_RTN_H
 #define BMX_RTN_H
@@ -39,13 +48,17 @@
 extern "C" {
 #endif
 
+#define BMX_RTN_TOKEN 0     /* scale per (token, group of k_group channels) */
+#define BMX_RTN_CHANNEL 1   /* scale per (channel, group of k_group tokens) */
+
 typedef struct {
   int32_t h_kv;        /* KV heads: 1..8 for decode, 1..16 for append/dequant */
   int32_t n_q_groups;  /* query heads per KV head G, 1..16 */
   int32_t k_bits;      /* RTN bits of the keys, 2..4 */
   int32_t v_bits;      /* RTN bits of the values, 2..4 */
-  int32_t k_group;     /* key scale group along head_dim: 32, 64 or 128 */
+  int32_t k_group;     /* key scale group: 32, 64 or 128 channels (token arm) or tokens (channel arm) */
   int32_t v_group;     /* value scale group along head_dim: 32, 64 or 128 */
+  int32_t k_arm;       /* BMX_RTN_TOKEN or BMX_RTN_CHANNEL */
 } bmx_rtn_geom;
 
 /* Bytes of one 16-token page (0 if the geometry is unsupported). */
@@ -54,11 +67,13 @@ size_t bmx_rtn_page_bytes(const bmx_rtn_geom* geom);
 /* ------------------------------------------------------------------------
  * Quantize-on-append.  Replaces quantize_packed("rtn_token") of
  * PackedStreamingLayer.update for both sides (cache/packed_streaming.py:
- * 640-667 with K post-RoPE, 544-580): per (token, head, group) scale =
- * max|x| (clamped to 1e-12) / qmax in fp32, code = clamp(round-half-even(x /
- * scale), -qmax - 1, qmax), qmax = 2^(bits-1) - 1; the page keeps the scale
- * in fp16, as build_kv_stacked_packed stacks it.  n_codec_pages pages of 128
- * tokens become 8 * n_codec_pages physical pages listed in page_ids.
+ * 640-667 with K post-RoPE, 544-580), or quantize_packed("rtn_channel") for
+ * the keys (codecs.py:723-725: groups of k_group tokens per channel): per
+ * group scale = max|x| (clamped to 1e-12) / qmax in fp32, code =
+ * clamp(round-half-even(x / scale), -qmax - 1, qmax), qmax = 2^(bits-1) - 1;
+ * the page keeps the scale in fp16, as build_kv_stacked_packed stacks it.
+ * n_codec_pages pages of 128 tokens become 8 * n_codec_pages physical pages
+ * listed in page_ids.
  * ---------------------------------------------------------------------- */
 typedef struct {
   bmx_rtn_geom geom;
@@ -116,7 +131,7 @@ int bmx_rtn_decode(const bmx_rtn_decode_args* args, void* stream);
 /* ------------------------------------------------------------------------
  * Dequantize pages to dense fp32 keys and values (prefill): the dequant half
  * of chunked_attention._dense_kv (cache/chunked_attention.py:148-251) for the
- * rtn_token arms (codes * fp16 scale).  k_out/v_out: device [h_kv][16 *
+ * RTN arms (codes * fp16 scale).  k_out/v_out: device [h_kv][16 *
  * n_pages][128] fp32.
  * ---------------------------------------------------------------------- */
 typedef struct {

@@ -229,17 +229,18 @@ def k2b_chunked_attention(q, cache: K2bOracleCache, inv_freq, k_tail, v_tail,
 
 
 class RtnOracleCache:
-    """Committed rtn_token pages of one sequence -- post-RoPE keys and values,
-    each a quantize_packed("rtn_token") block dict (packed_streaming.py:640-667,
-    544-580; codecs.py:720-722; rtn.py:23-44) -- and their dequantization as
-    the reference's fused RTN path computes it: code times the fp16 scale of
-    its (token, channel group), the scale stacked in fp16 by
-    build_kv_stacked_packed (triton_dequant_attention.py:1436-1440), read in
-    fp32 by the kernel (:670-715)."""
+    """Committed RTN pages of one sequence -- post-RoPE keys and values, each a
+    quantize_packed block dict (packed_streaming.py:640-667, 544-580):
+    "rtn_token" values, and "rtn_token" or (k_arm 1) "rtn_channel" keys
+    (codecs.py:720-725; rtn.py:23-44) -- and their dequantization as the
+    reference's fused RTN path computes it: code times the fp16 scale of its
+    group, the scale stacked in fp16 by build_kv_stacked_packed
+    (triton_dequant_attention.py:1436-1440), read in fp32 by the kernel
+    (:670-715)."""
 
     def __init__(self, h_kv: int, *, k_bits: int, v_bits: int, k_group: int, v_group: int,
-                 page: int = 128):
-        self.h_kv, self.page = h_kv, page
+                 k_arm: int = 0, page: int = 128):
+        self.h_kv, self.page, self.k_arm = h_kv, page, k_arm
         self.k_bits, self.v_bits, self.k_group, self.v_group = k_bits, v_bits, k_group, v_group
         self.k_blocks: list = []
         self.v_blocks: list = []
@@ -250,32 +251,37 @@ class RtnOracleCache:
 
     def commit(self, k_page: torch.Tensor, v_page: torch.Tensor):
         """k_page, v_page: (h_kv, page, d) post-RoPE keys / values (any float dtype)."""
-        kp, _ = C.quantize_rtn_token(C.to_matrix(k_page.float()), self.k_bits, self.k_group)
+        quant_k = C.quantize_rtn_channel if self.k_arm == 1 else C.quantize_rtn_token
+        kp, _ = quant_k(C.to_matrix(k_page.float()), self.k_bits, self.k_group)
         vp, _ = C.quantize_rtn_token(C.to_matrix(v_page.float()), self.v_bits, self.v_group)
         s = self.n_tokens
         self.k_blocks.append((kp, s, s + self.page))
         self.v_blocks.append((vp, s, s + self.page))
 
-    def _dense(self, blocks, group, fp16_scales):
+    def _dense(self, blocks, group, fp16_scales, channel=False):
         out = []
         for p, _, _ in blocks:
             sc = p["scale"].half().float() if fp16_scales else p["scale"]
-            out.append(C.from_matrix(C.rtn_dequantize_packed(p["Q_int"], sc, group), self.h_kv))
+            M = C.rtn_dequantize_packed(p["Q_int"], sc, group)   # (C, S) for the channel arm
+            out.append(C.from_matrix(M.mT if channel else M, self.h_kv))
         return torch.cat(out, dim=1)
 
     def dense_kv(self, fp16_scales: bool = True):
         """(K (h_kv, S, d), V (h_kv, S, d)) fp32."""
-        return (self._dense(self.k_blocks, self.k_group, fp16_scales),
+        return (self._dense(self.k_blocks, self.k_group, fp16_scales, self.k_arm == 1),
                 self._dense(self.v_blocks, self.v_group, fp16_scales))
 
     def codes(self):
-        """(kq, ks, vq, vs): codes (h_kv, S, d) and fp32 scales (h_kv, S, d/group)."""
-        def per_head(blocks, group):
-            q = torch.cat([C.from_matrix(p["Q_int"], self.h_kv) for p, _, _ in blocks], dim=1)
-            s = torch.cat([C.from_matrix(p["scale"].squeeze(-1), self.h_kv) for p, _, _ in blocks], dim=1)
+        """(kq, ks, vq, vs): codes (h_kv, S, d) and fp32 scales -- (h_kv, S,
+        d/group) per (token, channel group), or for channel-arm keys (h_kv,
+        S/group, d) per (token group, channel)."""
+        def per_head(blocks, channel=False):
+            tr = (lambda x: x.mT) if channel else (lambda x: x)
+            q = torch.cat([C.from_matrix(tr(p["Q_int"]), self.h_kv) for p, _, _ in blocks], dim=1)
+            s = torch.cat([C.from_matrix(tr(p["scale"].squeeze(-1)), self.h_kv) for p, _, _ in blocks], dim=1)
             return q, s
-        kq, ks = per_head(self.k_blocks, self.k_group)
-        vq, vs = per_head(self.v_blocks, self.v_group)
+        kq, ks = per_head(self.k_blocks, self.k_arm == 1)
+        vq, vs = per_head(self.v_blocks)
         return kq, ks, vq, vs
 
 

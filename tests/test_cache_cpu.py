@@ -42,7 +42,26 @@ def test_unsupported_k_specs_raise(bad):
 
 def test_other_recipes_raise():
     with pytest.raises(NotImplementedError, match="k2b_ph"):
-        spec_pair("kivi")
+        spec_pair("turboquant_mse")
+
+
+def test_kivi_recipe_and_rtn_pairs():
+    """kivi = rtn_channel keys with rtn_token values, 2 bits (recipes.py:173-177);
+    the RTN kernels take it and the reference's fused rtn_token pair; anything
+    outside their bit widths and groups raises."""
+    from bmx_amd.specs import packed_path
+
+    k, v = spec_pair("kivi", group=64)
+    assert (k.arm, k.bits, k.group, v.arm, v.bits, v.group) == ("rtn_channel", 2, 64, "rtn_token", 2, 64)
+    assert packed_path(k, v) == "rtn"
+    tok = CacheCodecSpec(arm="rtn_token", bits=4, group=32)
+    assert packed_path(tok, tok) == "rtn"
+    with pytest.raises(NotImplementedError):
+        packed_path(CacheCodecSpec(arm="rtn_token", bits=8, group=32), tok)
+    with pytest.raises(NotImplementedError):
+        packed_path(CacheCodecSpec(arm="rtn_token", bits=4, group=8), tok)
+    with pytest.raises(NotImplementedError):
+        packed_path(CacheCodecSpec(arm="rtn_token", bits=4, group=32, pre_rope=True), tok)
 
 
 @pytest.mark.parametrize("rank", [16, 32])

@@ -165,12 +165,15 @@ def test_config5_qwen3_streaming_append_and_decode():
     assert bad <= want.size * 1e-4
 
 
-def test_rtn_layer_streaming_decode_and_prefill():
-    """The RTN pair (rtn_token keys post-RoPE and values, 4 bits, groups of 32)
-    through the cache layer: a 1000-token prefill attended causally through
-    bmx_rtn_dequant + SDPA, then 300 one-token steps, each committing on the
-    128-token grid through bmx_rtn_append and decoding through bmx_rtn_decode,
-    against the RTN oracle fed the same committed pages and windows."""
+@pytest.mark.parametrize("recipe", ["rtn_token_4b", "kivi"])
+def test_rtn_layer_streaming_decode_and_prefill(recipe):
+    """The RTN pairs through the cache layer -- the reference's fused pair
+    (rtn_token keys post-RoPE and values, 4 bits, groups of 32) and the kivi
+    recipe (rtn_channel keys, 2 bits, groups of 64): a 1000-token prefill
+    attended causally through bmx_rtn_dequant + SDPA, then 300 one-token steps,
+    each committing on the 128-token grid through bmx_rtn_append and decoding
+    through bmx_rtn_decode, against the RTN oracle fed the same committed pages
+    and windows."""
     import torch.nn.functional as F
     from transformers import LlamaConfig
 
@@ -180,8 +183,11 @@ def test_rtn_layer_streaming_decode_and_prefill():
 
     cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8, head_dim=128,
                       num_hidden_layers=32, rope_theta=500000.0)
-    k_spec = CacheCodecSpec(arm="rtn_token", bits=4, group=32, pre_rope=False)
-    v_spec = CacheCodecSpec(arm="rtn_token", bits=4, group=32)
+    if recipe == "kivi":
+        k_spec, v_spec = spec_pair("kivi", group=64)
+    else:
+        k_spec = CacheCodecSpec(arm="rtn_token", bits=4, group=32, pre_rope=False)
+        v_spec = CacheCodecSpec(arm="rtn_token", bits=4, group=32)
     h_kv, G, d, W = 8, 4, 128, 128
     lay = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=W)
     gen = torch.Generator().manual_seed(77)
@@ -191,7 +197,8 @@ def test_rtn_layer_streaming_decode_and_prefill():
     k[:, :, [3, 40, 77, 101]] *= 10.0
     k = k.half()
     v = torch.randn(h_kv, N, d, generator=gen).half()
-    oc = A.RtnOracleCache(h_kv, k_bits=4, v_bits=4, k_group=32, v_group=32)
+    oc = A.RtnOracleCache(h_kv, k_bits=k_spec.bits, v_bits=v_spec.bits, k_group=k_spec.group,
+                          v_group=v_spec.group, k_arm=1 if k_spec.arm == "rtn_channel" else 0)
 
     def sync_oracle():
         while oc.n_tokens < lay._committed_S_q:
@@ -210,7 +217,7 @@ def test_rtn_layer_streaming_decode_and_prefill():
     ref = F.scaled_dot_product_attention(q.unsqueeze(0), Kx.unsqueeze(0), Vx.unsqueeze(0), is_causal=True,
                                          scale=d ** -0.5).squeeze(0)
     err = (out - ref).abs().max().item()
-    print(f"rtn prefill {n_pre} tokens (causal): max_abs {err:.3e}", flush=True)
+    print(f"{recipe} prefill {n_pre} tokens (causal): max_abs {err:.3e}", flush=True)
     assert err <= 2e-3
     worst = 0.0
     for i in range(n_steps):
@@ -224,6 +231,7 @@ def test_rtn_layer_streaming_decode_and_prefill():
         e = (o - r).abs().max().item()
         worst = max(worst, e)
         assert e <= 2e-3 and ((o - r).norm() / r.norm()).item() <= 1e-2, f"step {i}: {e:.3e}"
-    assert lay.bpe_k == pytest.approx((4.5 * P + 16 * (N - P)) / N)
-    print(f"rtn layer: {n_steps} decode steps, committed {P}, worst max_abs {worst:.3e}, "
+    bpe_page = k_spec.bits + 16.0 / k_spec.group
+    assert lay.bpe_k == pytest.approx((bpe_page * P + 16 * (N - P)) / N)
+    print(f"{recipe} layer: {n_steps} decode steps, committed {P}, worst max_abs {worst:.3e}, "
           f"bpe_k {lay.bpe_k:.4f}", flush=True)

@@ -75,12 +75,39 @@ def test_append_codes_bit_exact(h_kv, codec, dtype):
     np.testing.assert_array_equal(vs, rvs.numpy().astype(np.float16))
 
 
+@pytest.mark.parametrize("h_kv,codec", [
+    (8, dict(k_bits=4, v_bits=4, k_group=32, v_group=32, k_arm=rtn.CHANNEL)),
+    (2, dict(k_bits=2, v_bits=2, k_group=64, v_group=64, k_arm=rtn.CHANNEL)),
+    (16, dict(k_bits=3, v_bits=4, k_group=128, v_group=32, k_arm=rtn.CHANNEL)),
+])
+def test_append_channel_arm_codes_bit_exact(h_kv, codec):
+    """rtn_channel keys (quantize_packed("rtn_channel"): a scale per channel
+    and group of k_group tokens), written into every page of the group."""
+    gen = torch.Generator().manual_seed(11)
+    S = 256
+    k, v = _keys(h_kv, S, gen).half(), torch.randn(h_kv, S, 128, generator=gen).half()
+    pool, ids = _encode(h_kv, k, v, codec)
+    torch.cuda.synchronize()
+    pages = pool.pages[torch.tensor(ids, device=DEV)].cpu().numpy()
+    kq, ks, vq, vs = OL.unpack_rtn_pages(pages, h_kv, codec["k_group"], codec["v_group"], k_arm=1)
+    rkq, rks, rvq, rvs = _oracle(h_kv, k, v, codec).codes()
+    np.testing.assert_array_equal(kq, rkq.numpy())
+    np.testing.assert_array_equal(ks, np.repeat(rks.numpy().astype(np.float16), codec["k_group"] // 16, axis=1))
+    np.testing.assert_array_equal(vq, rvq.numpy())
+    np.testing.assert_array_equal(vs, rvs.numpy().astype(np.float16))
+
+
 def test_dequant_bit_exact():
     gen = torch.Generator().manual_seed(2)
     h_kv, S = 8, 384
     codec = dict(k_bits=4, v_bits=4, k_group=32, v_group=64)
     k, v = _keys(h_kv, S, gen).half(), torch.randn(h_kv, S, 128, generator=gen).half()
     pool, ids = _encode(h_kv, k, v, codec, gen=torch.Generator().manual_seed(5), n_pool=S // 16 + 7)
+    K, V = rtn.dequant(pool.pages, torch.tensor(ids, dtype=torch.int32, device=DEV), h_kv=h_kv, **codec)
+    rK, rV = _oracle(h_kv, k, v, codec).dense_kv()
+    assert torch.equal(K.cpu(), rK) and torch.equal(V.cpu(), rV)
+    codec = dict(codec, k_arm=rtn.CHANNEL)
+    pool, ids = _encode(h_kv, k, v, codec, gen=torch.Generator().manual_seed(6), n_pool=S // 16 + 3)
     K, V = rtn.dequant(pool.pages, torch.tensor(ids, dtype=torch.int32, device=DEV), h_kv=h_kv, **codec)
     rK, rV = _oracle(h_kv, k, v, codec).dense_kv()
     assert torch.equal(K.cpu(), rK) and torch.equal(V.cpu(), rV)
@@ -108,13 +135,32 @@ def _decode_case(h_kv, G, S, T, codec, gen, split_tokens=0, outliers=True):
     return out, ref.view(1, h_kv, G, 128)
 
 
-def test_decode_config1_geometry():
-    """Config 1 shape: 32 query / 8 KV heads, d 128, ctx 4096 = 3968 packed +
-    128 fp16 window tokens, 4-bit codes, groups of 32, keys with 4 outlier
-    channels x10, seed 0."""
+def test_decode_config1():
+    """Config 1: 32 query / 8 KV heads, d 128, ctx 4096 = 3968 packed + 128
+    fp16 window tokens; keys rtn_channel 4-bit (groups of 32 tokens) with 4
+    outlier channels x10, values rtn_token 4-bit (groups of 32 channels);
+    seed 0.  The reference runs this pair on its chunked path only."""
+    gen = torch.Generator().manual_seed(0)
+    out, ref = _decode_case(8, 4, 3968, 128,
+                            dict(k_bits=4, v_bits=4, k_group=32, v_group=32, k_arm=rtn.CHANNEL), gen)
+    _close(out, ref, "config1 rtn_channel K / rtn_token V, 4b g32")
+
+
+def test_decode_config1_geometry_fused_pair():
+    """The reference's fused pair (rtn_token keys and values) at config 1's
+    geometry."""
     gen = torch.Generator().manual_seed(0)
     out, ref = _decode_case(8, 4, 3968, 128, dict(k_bits=4, v_bits=4, k_group=32, v_group=32), gen)
-    _close(out, ref, "config1 rtn_token 4b g32")
+    _close(out, ref, "config1 geometry rtn_token K / rtn_token V, 4b g32")
+
+
+def test_decode_kivi():
+    """kivi recipe (recipes.py:173-177): rtn_channel keys and rtn_token values
+    at 2 bits, groups of 64."""
+    gen = torch.Generator().manual_seed(8)
+    out, ref = _decode_case(8, 4, 8192, 200,
+                            dict(k_bits=2, v_bits=2, k_group=64, v_group=64, k_arm=rtn.CHANNEL), gen)
+    _close(out, ref, "kivi 2b g64")
 
 
 @pytest.mark.parametrize("G", [1, 2, 8, 16])
@@ -126,7 +172,8 @@ def test_decode_query_group_sizes(G):
 
 @pytest.mark.parametrize("codec", [dict(k_bits=2, v_bits=2, k_group=64, v_group=64),
                                    dict(k_bits=3, v_bits=4, k_group=128, v_group=32),
-                                   dict(k_bits=4, v_bits=3, k_group=32, v_group=128)])
+                                   dict(k_bits=4, v_bits=3, k_group=32, v_group=128),
+                                   dict(k_bits=3, v_bits=3, k_group=128, v_group=64, k_arm=rtn.CHANNEL)])
 def test_decode_bits_and_groups(codec):
     gen = torch.Generator().manual_seed(40)
     out, ref = _decode_case(8, 4, 4096, 160, codec, gen, outliers=False)

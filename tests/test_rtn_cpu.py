@@ -26,6 +26,25 @@ def test_page_bytes_match_numpy_layout(h_kv, gk, gv):
 
 def test_headline_rtn_bytes_per_token():
     assert rtn.page_bytes(8) == 16 * 1152
+    # channel-arm keys: 128 channel scales per head and page
+    assert rtn.page_bytes(8, k_arm=rtn.CHANNEL) == OL.rtn_page_bytes(8, 32, 32, 1) == 16 * 1216
+
+
+def test_channel_arm_page_round_trip():
+    rng = np.random.default_rng(2)
+    h_kv, gk, gv, T = 4, 64, 32, 128
+    kq, vq = rng.integers(-8, 8, (h_kv, T, 128)), rng.integers(-8, 8, (h_kv, T, 128))
+    ks = rng.random((h_kv, T // gk, 128)).astype(np.float16)
+    vs = rng.random((h_kv, T, 128 // gv)).astype(np.float16)
+    pages = OL.pack_rtn_pages(kq, ks, vq, vs, h_kv, gk, gv, k_arm=1)
+    a, b, c, d = OL.unpack_rtn_pages(pages, h_kv, gk, gv, k_arm=1)
+    np.testing.assert_array_equal(a, kq)
+    np.testing.assert_array_equal(b, np.repeat(ks, gk // 16, axis=1))
+    np.testing.assert_array_equal(c, vq)
+    np.testing.assert_array_equal(d, vs)
+    # channel 13 = 32*0 + 8*1 + 5 sits at slot 8 + 2*1 + 1 of its row
+    o = OL.rtn_sections(h_kv, gk, gv, 1)["kscale"][0]
+    assert pages[0, o:o + 256].view(np.float16)[8 + 3] == ks[0, 0, 13]
 
 
 @pytest.mark.parametrize("h_kv,gk,gv", [(8, 32, 32), (2, 64, 128)])
@@ -71,6 +90,20 @@ def test_oracle_cache_matches_reference_golden():
     _, V16 = c.dense_kv()
     want = vq.float() * vs.half().float().repeat_interleave(32, dim=-1)
     assert torch.equal(V16, want)
+
+
+def test_channel_arm_oracle_matches_reference_golden():
+    """rtn_channel keys through the RTN oracle cache: the reference's golden
+    codes, scales and dequantization of quantize_packed("rtn_channel")."""
+    g = np.load(GOLD / "codecs.npz")
+    M = torch.from_numpy(g["rtn_k_in"])            # (128 tokens, 256 channels): h_kv 2
+    c = A.RtnOracleCache(2, k_bits=4, v_bits=4, k_group=32, v_group=32, k_arm=1)
+    c.commit(OC.from_matrix(M, 2), OC.from_matrix(M, 2))
+    kq, ks, _, _ = c.codes()
+    np.testing.assert_array_equal(OC.to_matrix(kq).numpy().T, g["rtn_channel_q"])
+    np.testing.assert_array_equal(OC.to_matrix(ks).numpy().T, g["rtn_channel_scale"][..., 0])
+    K32, _ = c.dense_kv(fp16_scales=False)
+    np.testing.assert_array_equal(OC.to_matrix(K32).numpy(), g["rtn_channel_deq"])
 
 
 def test_bad_rtn_arguments_are_rejected_with_message():
