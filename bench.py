@@ -11,7 +11,7 @@ the 256 MB MALL.  Inputs are resident in HBM before timing starts.
 
 A "step" is one decode-attention call per layer for all 32 layers (the
 attention part of one generated token).  A call is two kernels back to back
-(k2b_decode_split_kernel, then k2b_combine_kernel).  Printed: one JSON line with
+(k2b_decode_split_kernel, then combine_kernel<true>).  Printed: one JSON line with
 the step time; the roofline of a decode call (its algorithmic bytes over the
 average call duration, from HIP events around the back-to-back timed region on
 the library's stream), with the measured HBM traffic per call when a rocprofv3
@@ -61,10 +61,14 @@ def parse():
     ap.add_argument("--cpu-sample-tokens", type=int, default=16384)
     ap.add_argument("--cpu-reps", type=int, default=7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["decode", "stream"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "stream", "rtn"], default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
                          "BASELINE config 5, Qwen3-8B geometry, rank 16, an 8192-token prefill "
-                         "then --stream-steps steps of one-token append + decode over 36 layers")
+                         "then --stream-steps steps of one-token append + decode over 36 layers; "
+                         "rtn: BASELINE config 1, RTN 4-bit per-channel keys / per-token values, "
+                         "ctx --rtn-ctx, --rtn-layers layers")
+    ap.add_argument("--rtn-ctx", type=int, default=4096)
+    ap.add_argument("--rtn-layers", type=int, default=1)
     ap.add_argument("--stream-steps", type=int, default=512)
     ap.add_argument("--stream-layers", type=int, default=36)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -245,6 +249,102 @@ def run_stream(args, torch, k2b, synth, dev) -> dict:
     }
 
 
+RTN_METRIC = ("decode-attn µs/call + % HBM roofline, RTN 4-bit (rtn_channel keys g32, rtn_token "
+              "values g32), 1 MI355X")
+
+
+def run_rtn(args, torch, dev) -> dict:
+    """one layer, batch 1, 32 query / 8 KV heads, d 128,
+    ctx 4096 = 3968 packed + 128 fp16 window tokens; keys N(0,1) with 4 fixed
+    channels x10 coded rtn_channel 4-bit (groups of 32 tokens), values N(0,1)
+    coded rtn_token 4-bit (groups of 32 channels); seed 0.  A call is the RTN
+    split kernel and the merge kernel.  With one layer the 4.8 MB working set
+    stays in the 256 MB MALL between calls (the roofline against HBM peak is
+    nominal there); --rtn-layers rotates over that many layer caches."""
+    from bmx_amd import k2b, rtn
+    from oracle import attention as A
+
+    ctx, L, W = args.rtn_ctx, args.rtn_layers, 128
+    P = ((ctx - W) // 128) * 128
+    T = ctx - P
+    codec = dict(k_bits=4, v_bits=4, k_group=32, v_group=32, k_arm=rtn.CHANNEL)
+    gen = torch.Generator().manual_seed(0)
+    ws = k2b.DecodeWorkspace()
+    layers, cpu_case = [], None
+    for li in range(L):
+        k = torch.randn(H_KV, ctx, D, generator=gen)
+        k[:, :, [3, 40, 77, 101]] *= 10.0
+        k, v = k.half(), torch.randn(H_KV, ctx, D, generator=gen).half()
+        q = torch.randn(1, H_KV, G, D, generator=gen)
+        pool = rtn.PagePool(P // 16, H_KV, dev, **codec)
+        ids = pool.alloc(P // 16)
+        rtn.append(k[:, :P].to(dev), v[:, :P].to(dev), pool.pages,
+                   torch.tensor(ids, dtype=torch.int32, device=dev), **codec)
+        lay = {"pool": pool, "q": q.to(dev), "kt": k[:, P:].unsqueeze(0).to(dev),
+               "vt": v[:, P:].unsqueeze(0).to(dev), "table": torch.tensor([ids], dtype=torch.int32, device=dev),
+               "len": torch.tensor([P], dtype=torch.int32, device=dev),
+               "tl": torch.tensor([T], dtype=torch.int32, device=dev)}
+        lay["plan"] = rtn.DecodePlan(lay["q"], pool.pages, lay["table"], lay["len"], P, D ** -0.5,
+                                     k_tail=lay["kt"], v_tail=lay["vt"], tail_len=lay["tl"], tail_cap=T,
+                                     workspace=ws, **codec)
+        layers.append(lay)
+        if li == 0:
+            cpu_case = (k, v, q)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        for lay in layers:
+            lay["plan"].run()
+    calls = max(args.steps, 1) * 50
+    torch.cuda.synchronize()
+    gpu_sleep(torch)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(calls):
+        layers[i % L]["plan"].run()
+    e1.record()
+    torch.cuda.synchronize()
+    call_us = e0.elapsed_time(e1) * 1e3 / calls
+    page_bytes = rtn.page_bytes(H_KV, **codec)
+    C = H_KV * D
+    bytes_call = P * page_bytes // 16 + T * C * 2 * 2 + 2 * H_KV * G * D * 4
+    achieved = bytes_call / (call_us * 1e-6) / 1e9
+    res = {
+        "metric": RTN_METRIC, "value": round(call_us, 3), "unit": "us/call", "n_gpus": 1,
+        "steps": calls, "warmup": args.warmup, "ms_per_step": round(call_us / 1e3, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": (f"BASELINE config 1: {L} layer(s), batch 1, 32q/8kv heads, d 128, ctx {ctx} "
+                                f"= {P} packed + {T} fp16 window, rtn_channel 4b g32 keys (4 outlier "
+                                f"channels x10), rtn_token 4b g32 values, seed 0"),
+                   "ctx": ctx, "layers": L, "bytes_per_token_layer": page_bytes // 16},
+        "roofline": {"bound": "hbm", "kernel": "RTN decode call (rtn_decode_split_kernel + combine_kernel<false>)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": bytes_call, "avg_launch_us": round(call_us, 3),
+                     "note": ("working set in the 256 MB MALL" if L * bytes_call < 200e6 else "streams from HBM")},
+    }
+    if not args.no_cpu_baseline:
+        k, v, q = cpu_case
+        c = A.RtnOracleCache(H_KV, **codec)
+        for p in range(P // 128):
+            c.commit(k[:, p * 128:(p + 1) * 128], v[:, p * 128:(p + 1) * 128])
+        threads = min(os.cpu_count() or 1, 16)
+        torch.set_num_threads(threads)
+        qq = q.reshape(H_KV * G, 1, D)
+        A.rtn_chunked_attention(qq, c, k[:, P:], v[:, P:], G, D ** -0.5)
+        times = []
+        for _ in range(args.cpu_reps):
+            t0 = time.perf_counter()
+            A.rtn_chunked_attention(qq, c, k[:, P:], v[:, P:], G, D ** -0.5)
+            times.append(time.perf_counter() - t0)
+        t = statistics.median(times)
+        res["cpu_baseline"] = {"value": round(t * 1e6, 1), "unit": "us/call", "cores": threads, "kind": "port",
+                               "sample": (f"the whole config-1 call ({P} packed + {T} tail tokens), median of "
+                                          f"{args.cpu_reps} after 1 warm-up"),
+                               "cpu_model": _cpu_model()}
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -262,6 +362,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "stream":
         print(json.dumps(run_stream(args, torch, k2b, synth, dev)), flush=True)
+        return
+    if args.workload == "rtn":
+        print(json.dumps(run_rtn(args, torch, dev)), flush=True)
         return
     if args.copy_calib_mib > 0:
         n = args.copy_calib_mib << 20
@@ -393,7 +496,7 @@ def main():
         "per_layer_us": round(call_us, 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k2b decode call (k2b_decode_split_kernel + k2b_combine_kernel)",
+            "kernel": "k2b decode call (k2b_decode_split_kernel + combine_kernel<true>)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

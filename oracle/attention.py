@@ -285,6 +285,41 @@ class RtnOracleCache:
         return kq, ks, vq, vs
 
 
+def rtn_chunked_attention(q, cache: RtnOracleCache, k_tail, v_tail, n_q_groups: int, scale: float):
+    """Chunked dequant-attention for one decode step over RTN pages
+    (chunked_attention.py:398-530 with dequant_packed of the RTN arms,
+    codecs.py:819-822, fp32 scales): per committed page dequantize K and V,
+    grouped online softmax, the fp16 tail folded in last.  The reference's CPU
+    path for these arms and the cpu_baseline of the RTN benchmark."""
+    n_q, n, d = q.shape
+    h_kv = n_q // n_q_groups
+    qf = q.float()
+    acc = torch.zeros(n_q, n, d)
+    m = torch.full((n_q, n, 1), float("-inf"))
+    lse = torch.zeros(n_q, n, 1)
+
+    def attend(K_kv, V_kv):
+        nonlocal acc, m, lse
+        qg = qf.view(h_kv, n_q_groups, n, d)
+        s = torch.einsum("gpnd,gbd->gpnb", qg, K_kv) * scale
+        s = s.reshape(n_q, n, K_kv.shape[1])
+        m_new = torch.maximum(m, s.amax(dim=-1, keepdim=True))
+        corr = torch.exp(m - m_new)
+        p = torch.exp(s - m_new)
+        lse = lse * corr + p.sum(dim=-1, keepdim=True)
+        av = torch.einsum("gpnb,gbd->gpnd", p.view(h_kv, n_q_groups, n, -1), V_kv)
+        acc = acc * corr + av.reshape(n_q, n, d)
+        m = m_new
+
+    dq_k = C.dequant_rtn_channel if cache.k_arm == 1 else C.dequant_rtn_token
+    for (kp, _, _), (vp, _, _) in zip(cache.k_blocks, cache.v_blocks):
+        attend(C.from_matrix(dq_k(kp, cache.k_group), h_kv),
+               C.from_matrix(C.dequant_rtn_token(vp, cache.v_group), h_kv))
+    if k_tail is not None and k_tail.shape[1] > 0:
+        attend(k_tail.float(), v_tail.float())
+    return acc / lse
+
+
 def rtn_naive_attention(q, cache: RtnOracleCache, k_tail, v_tail, n_q_groups: int, scale: float):
     """The fp32 oracle for one decode step over committed RTN pages plus the
     fp16 tail: (n_q, 1, d)."""

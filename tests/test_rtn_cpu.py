@@ -106,6 +106,24 @@ def test_channel_arm_oracle_matches_reference_golden():
     np.testing.assert_array_equal(OC.to_matrix(K32).numpy(), g["rtn_channel_deq"])
 
 
+@pytest.mark.parametrize("k_arm", [0, 1])
+def test_chunked_rtn_oracle_equals_one_softmax(k_arm):
+    """The chunked restatement (per page, online softmax, fp32 scales) equals
+    one softmax over the same dequantized keys and values."""
+    gen = torch.Generator().manual_seed(3)
+    h_kv, G = 2, 4
+    c = A.RtnOracleCache(h_kv, k_bits=4, v_bits=4, k_group=32, v_group=64, k_arm=k_arm)
+    for _ in range(3):
+        c.commit(torch.randn(h_kv, 128, 128, generator=gen), torch.randn(h_kv, 128, 128, generator=gen))
+    kt, vt = torch.randn(h_kv, 37, 128, generator=gen).half(), torch.randn(h_kv, 37, 128, generator=gen).half()
+    q = torch.randn(h_kv * G, 1, 128, generator=gen)
+    got = A.rtn_chunked_attention(q, c, kt, vt, G, 128 ** -0.5)
+    K, V = c.dense_kv(fp16_scales=False)
+    want = A.naive_dense_attention(q, torch.cat([K, kt.float()], 1), torch.cat([V, vt.float()], 1), G,
+                                   128 ** -0.5)
+    assert (got - want).abs().max().item() < 1e-5
+
+
 def test_bad_rtn_arguments_are_rejected_with_message():
     lib = _lib.lib()
     with pytest.raises(NotImplementedError, match="2..4-bit"):
