@@ -123,7 +123,9 @@ typedef struct {
                                  > 0 (multiple of 64) = about max_packed_len / split_tokens
                                  workgroups per sequence.  Packed tokens are dealt in
                                  64-token groups, balanced over the workgroups; the
-                                 recent window is attended by the merge kernel. */
+                                 recent window is scored by the split kernel in
+                                 16-token tiles (at least one workgroup per tile, up
+                                 to one per CU) and summed by the merge kernel. */
   void* workspace;            /* device scratch: split partials and window scores (fp32) */
   size_t workspace_bytes;
   void* split_end_event;      /* optional hipEvent_t recorded on the stream between
