@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--cpu-sample-tokens", type=int, default=16384)
     ap.add_argument("--cpu-reps", type=int, default=7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fp16-comparator", action="store_true",
+                    help="skip timing the dense fp16 decode at the same context")
     ap.add_argument("--workload", choices=["decode", "stream", "rtn"], default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
                          "BASELINE config 5, Qwen3-8B geometry, rank 16, an 8192-token prefill "
@@ -108,13 +110,85 @@ def cpu_baseline(args, packed: int, tail: int) -> dict:
         A.k2b_chunked_attention(q, cache, inv, k_tail, v[:, S:], G, D ** -0.5)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
+    # the same on one thread (fewer repetitions: each call takes seconds)
+    torch.set_num_threads(1)
+    times1 = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        A.k2b_chunked_attention(q, cache, inv, k_tail, v[:, S:], G, D ** -0.5)
+        times1.append(time.perf_counter() - t0)
+    torch.set_num_threads(threads)
+    t1 = statistics.median(times1)
     scale = (packed + tail) / (S + tail) * args.layers
     return {"value": round(t * scale * 1e6, 1), "unit": "us/step", "cores": threads,
             "kind": "port",
             "sample": (f"1 layer of {S} packed + {tail} tail tokens (h_kv 8, G 4, rank {args.rank}), "
                        f"median of {args.cpu_reps} after 1 warm-up = {t * 1e3:.1f} ms/layer-call, "
                        f"scaled x{(packed + tail) / (S + tail):.2f} tokens x {args.layers} layers"),
+            "value_1_thread": round(t1 * scale * 1e6, 1),
+            "sample_1_thread": f"median of 3 = {t1 * 1e3:.1f} ms/layer-call, same scaling",
             "cpu_model": _cpu_model()}
+
+
+def fp16_comparator(args, torch, dev, ctx: int, our_us: float) -> dict:
+    """The measured fp16 decode at the same context, the bar the packed path
+    must beat: dense fp16 K/V of all ctx tokens per layer (8 KV heads, d 128),
+    one query step of 32 heads, over args.layers distinct layers (8.6 GB at
+    64k and 32 layers, past the MALL).  Two forms, the faster reported: torch
+    SDPA with grouped heads (ROCm's own attention), and grouped bmm ->
+    softmax -> bmm with the keys stored transposed (two skinny GEMMs that read
+    K and V once each)."""
+    import torch.nn.functional as F
+
+    gen = torch.Generator(device=dev).manual_seed(99)
+    n_l = args.layers
+    Ks = [torch.randn(1, H_KV, ctx, D, generator=gen, device=dev, dtype=torch.float16) for _ in range(n_l)]
+    Vs = [torch.randn(1, H_KV, ctx, D, generator=gen, device=dev, dtype=torch.float16) for _ in range(n_l)]
+    KTs = [k[0].transpose(1, 2).contiguous() for k in Ks]   # (8, 128, ctx): no transposed bmm operand
+    q = torch.randn(1, H_KV * G, 1, D, generator=gen, device=dev, dtype=torch.float16)
+    qg = q.view(H_KV, G, D)
+    scale = D ** -0.5
+
+    def sdpa(i):
+        return F.scaled_dot_product_attention(q, Ks[i], Vs[i], enable_gqa=True, scale=scale)
+
+    def bmm(i):
+        p = torch.softmax(torch.bmm(qg, KTs[i]).float() * scale, dim=-1).half()
+        return torch.bmm(p, Vs[i][0])
+
+    def timed(fn, reps=10):
+        for _ in range(3):
+            for i in range(n_l):
+                fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            for i in range(n_l):
+                fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * n_l)
+
+    res = {}
+    ref = bmm(0).float().view(-1)
+    try:
+        d = (sdpa(0).float().view(-1) - ref).abs().max().item()
+        res["sdpa_us_per_call"] = round(timed(sdpa), 3)
+        res["sdpa_vs_bmm_max_abs"] = d
+    except RuntimeError as e:   # a backend without grouped heads: the bmm form stands
+        res["sdpa_error"] = str(e)[:200]
+    res["bmm_us_per_call"] = round(timed(bmm), 3)
+    best = min(v for k, v in res.items() if k.endswith("_us_per_call"))
+    nbytes = ctx * H_KV * D * 2 * 2
+    res.update({"kind": "dense fp16 K/V decode on the same GPU (faster of the two forms)",
+                "us_per_call": best, "bytes_per_call": nbytes,
+                "achieved_GBs": round(nbytes / (best * 1e-6) / 1e9, 1),
+                "packed_speedup": round(best / our_us, 3),
+                "fp16_roofline_us": round(nbytes / HBM_PEAK_GBS / 1e3, 3)})
+    del Ks, Vs, KTs
+    torch.cuda.empty_cache()
+    return res
 
 
 def _cpu_model() -> str:
@@ -513,6 +587,11 @@ def main():
         },
         "build_s": round(t_build, 1),
     }
+    if not args.no_fp16_comparator:
+        del layers, pool
+        torch.cuda.empty_cache()
+        print("bench: timing the fp16 comparator", file=sys.stderr, flush=True)
+        res["fp16_comparator"] = fp16_comparator(args, torch, dev, args.ctx, call_us)
     if not args.no_cpu_baseline:
         print(f"bench: GPU timing done ({step_us:.1f} us/step); timing the CPU baseline",
               file=sys.stderr, flush=True)

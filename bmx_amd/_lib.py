@@ -91,6 +91,7 @@ class DequantArgs(ct.Structure):
         ("v_sign_bits", ct.c_uint32 * 4),
         ("k_out", ct.c_void_p),
         ("v_out", ct.c_void_p),
+        ("out_dtype", ct.c_int32),
     ]
 
 
@@ -153,6 +154,7 @@ class RtnDequantArgs(ct.Structure):
         ("n_pages", ct.c_int32),
         ("k_out", ct.c_void_p),
         ("v_out", ct.c_void_p),
+        ("out_dtype", ct.c_int32),
     ]
 
 

@@ -118,12 +118,6 @@ def _rope_tables(inv_freq: torch.Tensor, scaling: float, start: int, n: int, dev
     return (emb.cos() * scaling).half(), (emb.sin() * scaling).half()
 
 
-def _apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    d = x.shape[-1]
-    rot = torch.cat((-x[..., d // 2:], x[..., : d // 2]), dim=-1)
-    return x * cos.unsqueeze(0) + rot * sin.unsqueeze(0)
-
-
 # ------------------------------------------------------------------ attention
 
 
@@ -350,28 +344,40 @@ class PackedStreamingLayer(DynamicLayer):
         return out.reshape(self._h_kv * G, 1, self._d_head)
 
     def _dense(self, q, scaling, G, causal, attention_mask):
+        """Prefill (n_q > 1): _prefill_dense_attention (chunked_attention.py:
+        320-395).  The page kernel dequantizes the committed pages straight to
+        the model dtype (k2b keys rotated in the same pass with the fp16 RoPE
+        tables, as _dense_kv does), the fp16 window follows, and one flash SDPA
+        attends over the grouped heads (no G-fold copy of K and V).  With no
+        mask from the model and fewer queries than keys, the queries are the
+        last n_q positions: the mask is causal from the bottom right."""
         dev, dt = q.device, q.dtype
         P = self._committed_S_q
         parts_k, parts_v = [], []
         if P > 0 and self._path == "rtn":   # keys were committed post-RoPE
             kp, vp = rtn.dequant(self._pool, self._table[0, : P // rtn.PAGE_TOKENS].contiguous(),
-                                 h_kv=self._h_kv, **self._rtn)
-            parts_k.append(kp.to(dt))
-            parts_v.append(vp.to(dt))
+                                 h_kv=self._h_kv, dtype=dt, **self._rtn)
+            parts_k.append(kp)
+            parts_v.append(vp)
         elif P > 0:
             kp, vp = k2b.dequant(self._pool, self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P,
-                                 self._basis16, self._consts, h_kv=self._h_kv, rank=self._rank)
-            cos, sin = _rope_tables(self._inv_freq, self._rope_scaling, 0, P, dev)
-            parts_k.append(_apply_rope(kp, cos.float(), sin.float()).to(dt))
-            parts_v.append(vp.to(dt))
+                                 self._basis16, self._consts, h_kv=self._h_kv, rank=self._rank,
+                                 apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt)
+            parts_k.append(kp)
+            parts_v.append(vp)
         if self.keys is not None and self.keys.numel():
             parts_k.append(self.keys.squeeze(0).to(dt))
             parts_v.append(self.values.squeeze(0).to(dt))
-        Kd = torch.cat(parts_k, dim=1).repeat_interleave(G, dim=0)
-        Vd = torch.cat(parts_v, dim=1).repeat_interleave(G, dim=0)
+        Kd = torch.cat(parts_k, dim=1) if len(parts_k) > 1 else parts_k[0]
+        Vd = torch.cat(parts_v, dim=1) if len(parts_v) > 1 else parts_v[0]
+        n_q, n_kv = q.shape[1], Kd.shape[1]
+        if causal and attention_mask is None and n_q != n_kv:
+            i = torch.arange(n_q, device=dev)[:, None]
+            j = torch.arange(n_kv, device=dev)[None, :]
+            attention_mask = (j <= i + (n_kv - n_q))[None, None]
         out = F.scaled_dot_product_attention(
             q.unsqueeze(0), Kd.unsqueeze(0), Vd.unsqueeze(0), attn_mask=attention_mask,
-            is_causal=causal and attention_mask is None, scale=scaling)
+            is_causal=causal and attention_mask is None, scale=scaling, enable_gqa=G > 1)
         return out.squeeze(0)
 
 

@@ -56,6 +56,20 @@ __device__ __forceinline__ uint32_t half_bits(_Float16 v) {
   return h;
 }
 
+// Element idx of a dense output in dtype BMX_K2B_F32 / _F16 / _BF16 (fp16 and
+// bf16 round to nearest even, as torch's casts do).
+__device__ __forceinline__ void store_elem(void* base, int64_t idx, float v, int dtype) {
+  if (dtype == 1) {   // BMX_K2B_F32
+    reinterpret_cast<float*>(base)[idx] = v;
+  } else if (dtype == 2) {   // BMX_K2B_BF16
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = (u & 0x7fffffffu) > 0x7f800000u ? (u | 0x00400000u) : u + 0x7fffu + ((u >> 16) & 1u);
+    reinterpret_cast<uint16_t*>(base)[idx] = (uint16_t)(u >> 16);
+  } else {
+    reinterpret_cast<uint16_t*>(base)[idx] = float_to_half_bits(v);
+  }
+}
+
 // Physical page id clamped into the pool: a corrupt table entry cannot fault.
 __device__ __forceinline__ int64_t clamp_page(int32_t pid, int32_t n_pool) {
   return (int64_t)min(max(pid, 0), n_pool - 1);

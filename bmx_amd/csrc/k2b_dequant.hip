@@ -7,7 +7,7 @@
 namespace bmx {
 
 struct DequantKArgs {
-  int h_kv, R, n_tokens, apply_rope, n_pool;
+  int h_kv, R, n_tokens, apply_rope, n_pool, out_dtype;
   const uint8_t* pages;
   const int32_t* page_table;
   const uint16_t* basis;
@@ -16,8 +16,8 @@ struct DequantKArgs {
   float inv_freq[64];
   float codebook[4];
   uint32_t v_sign_bits[4];
-  float* k_out;
-  float* v_out;
+  void* k_out;
+  void* v_out;
 };
 
 // grid (n_tokens/16, h_kv), block 256
@@ -54,18 +54,23 @@ __global__ __launch_bounds__(256) void k2b_dequant_kernel(const DequantKArgs a) 
       kv[s] = acc + scale * (float)code;
     }
     const int64_t base = ((int64_t)h * a.n_tokens + lp * kPT + t) * kD;
+    float k0 = kv[0], k1 = kv[1];
     if (a.apply_rope) {
-      const float ang = a.inv_freq[j0] * (float)(lp * kPT + t);
+      const float ang = a.inv_freq[j0] * (float)(lp * kPT + t);   // HF's fp32 angle
       float sn, cn;
       sincosf(ang, &sn, &cn);
       cn *= a.rope_scaling;
       sn *= a.rope_scaling;
-      a.k_out[base + j0] = kv[0] * cn - kv[1] * sn;
-      a.k_out[base + j0 + 64] = kv[1] * cn + kv[0] * sn;
-    } else {
-      a.k_out[base + j0] = kv[0];
-      a.k_out[base + j0 + 64] = kv[1];
+      if (a.apply_rope == 2) {   // the reference's fp16 tables
+        cn = half_bits_to_float(float_to_half_bits(cn));
+        sn = half_bits_to_float(float_to_half_bits(sn));
+      }
+      // x*cos + rotate_half(x)*sin, rounded per operation as torch does
+      k0 = __fmul_rn(kv[0], cn) - __fmul_rn(kv[1], sn);
+      k1 = __fmul_rn(kv[1], cn) + __fmul_rn(kv[0], sn);
     }
+    store_elem(a.k_out, base + j0, k0, a.out_dtype);
+    store_elem(a.k_out, base + j0 + 64, k1, a.out_dtype);
   }
 
   // values: codebook level per (token, channel), FWHT, signs, norm
@@ -92,7 +97,8 @@ __global__ __launch_bounds__(256) void k2b_dequant_kernel(const DequantKArgs a) 
     const int t = e / kD, c = e % kD;
     const float nrm = half_bits_to_float(*reinterpret_cast<const uint16_t*>(page + a.L.vnorm + (h * kPT + t) * 2));
     const float v = x[t][c] / (float)kD;
-    a.v_out[((int64_t)h * a.n_tokens + lp * kPT + t) * kD + c] = (sign_neg(a.v_sign_bits, c) ? -v : v) * nrm;
+    store_elem(a.v_out, ((int64_t)h * a.n_tokens + lp * kPT + t) * kD + c, (sign_neg(a.v_sign_bits, c) ? -v : v) * nrm,
+               a.out_dtype);
   }
 }
 
@@ -117,7 +123,16 @@ extern "C" int bmx_k2b_dequant(const bmx_k2b_dequant_args* a, void* stream) {
     return BMX_E_INVALID;
   }
   DequantKArgs k{};
+  if (a->apply_rope < 0 || a->apply_rope > 2) {
+    bmx_set_error("bmx_k2b_dequant: apply_rope must be 0, 1 or 2");
+    return BMX_E_INVALID;
+  }
+  if (a->out_dtype < BMX_K2B_F16 || a->out_dtype > BMX_K2B_BF16) {
+    bmx_set_error("bmx_k2b_dequant: out_dtype must be BMX_K2B_F16, _F32 or _BF16");
+    return BMX_E_INVALID;
+  }
   k.h_kv = g.h_kv; k.R = g.rank; k.n_tokens = a->n_tokens; k.apply_rope = a->apply_rope;
+  k.out_dtype = a->out_dtype;
   k.pages = a->pages; k.page_table = a->page_table; k.basis = a->basis; k.n_pool = a->n_pool_pages;
   k.L = PageLayout::make(g.h_kv, g.rank);
   k.rope_scaling = a->rope_scaling;

@@ -197,8 +197,9 @@ struct RtnDequantKArgs {
   const uint8_t* pages;
   const int32_t* page_ids;
   int64_t n_tok;
-  float* k_out;
-  float* v_out;
+  void* k_out;
+  void* v_out;
+  int out_dtype;
   int gk, gv;
   RtnLayout L;
 };
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(256) void rtn_dequant_kernel(const RtnDequantKArgs 
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float s = a.karm == BMX_RTN_TOKEN ? sk : half_bits_to_float(ksc[h * kD + kchan_slot(8 * l + j)]);
-    a.k_out[row + 8 * l + j] = (float)((int)((w >> (4 * j)) & 15u) - 8) * s;
+    store_elem(a.k_out, row + 8 * l + j, (float)((int)((w >> (4 * j)) & 15u) - 8) * s, a.out_dtype);
   }
   const uint16_t* vcode = reinterpret_cast<const uint16_t*>(page + a.L.vcode + h * 1024);
   const float sv = half_bits_to_float(reinterpret_cast<const uint16_t*>(page + a.L.vscale)
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(256) void rtn_dequant_kernel(const RtnDequantKArgs 
   for (int j = 0; j < 8; ++j) {
     const int c = 8 * l + j;
     const uint32_t cell = vcode[((tt >> 2) * 16 + (c & 15)) * 8 + (c >> 4)];
-    a.v_out[row + c] = (float)((int)((cell >> (4 * (tt & 3))) & 15u) - 8) * sv;
+    store_elem(a.v_out, row + c, (float)((int)((cell >> (4 * (tt & 3))) & 15u) - 8) * sv, a.out_dtype);
   }
 }
 
@@ -732,10 +733,12 @@ extern "C" int bmx_rtn_dequant(const bmx_rtn_dequant_args* a, void* stream) {
   if (a->n_pages == 0) return BMX_OK;
   if (!a->pages || !a->page_ids || !a->k_out || !a->v_out || a->n_pool_pages < 1)
     return rfail(BMX_E_INVALID, "bmx_rtn_dequant: null pointer argument or empty pool");
+  if (a->out_dtype < BMX_K2B_F16 || a->out_dtype > BMX_K2B_BF16)
+    return rfail(BMX_E_INVALID, "bmx_rtn_dequant: out_dtype must be BMX_K2B_F16, _F32 or _BF16");
   RtnDequantKArgs k{};
   const bmx_rtn_geom& g = a->geom;
   k.h_kv = g.h_kv; k.n_pool = a->n_pool_pages; k.pages = a->pages; k.page_ids = a->page_ids;
-  k.n_tok = (int64_t)a->n_pages * kPT; k.k_out = a->k_out; k.v_out = a->v_out;
+  k.n_tok = (int64_t)a->n_pages * kPT; k.k_out = a->k_out; k.v_out = a->v_out; k.out_dtype = a->out_dtype;
   k.gk = g.k_group; k.gv = g.v_group; k.karm = g.k_arm;
   k.L = RtnLayout::make(g.h_kv, g.k_arm, g.k_group, g.v_group);
   hipLaunchKernelGGL(rtn_dequant_kernel, dim3(a->n_pages, g.h_kv), dim3(256), 0, (hipStream_t)stream, k);

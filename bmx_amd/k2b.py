@@ -230,11 +230,19 @@ class DecodePlan:
         return self.out
 
 
+ROPE_NONE, ROPE_EXACT, ROPE_FP16_TABLES = 0, 1, 2
+
+
 def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis16: torch.Tensor,
-            consts: CodecConsts, *, h_kv: int, rank: int, apply_rope: bool = False):
-    """Committed pages of one sequence -> dense fp32 (K (h_kv, n, 128), V (h_kv, n, 128))."""
+            consts: CodecConsts, *, h_kv: int, rank: int, apply_rope: int = ROPE_NONE,
+            dtype: torch.dtype = torch.float32):
+    """Committed pages of one sequence -> dense (K (h_kv, n, 128), V (h_kv, n, 128))
+    in dtype.  apply_rope: ROPE_NONE (pre-RoPE keys), ROPE_EXACT (fp32 cos/sin)
+    or ROPE_FP16_TABLES (the reference's prefill: fp16-rounded cos/sin)."""
     dev = pages.device
-    k = torch.empty(h_kv, n_tokens, HEAD_DIM, dtype=torch.float32, device=dev)
+    _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
+    _need(int(apply_rope) in (ROPE_NONE, ROPE_EXACT, ROPE_FP16_TABLES), "apply_rope must be 0, 1 or 2")
+    k = torch.empty(h_kv, n_tokens, HEAD_DIM, dtype=dtype, device=dev)
     v = torch.empty_like(k)
     _need(page_table.dtype == torch.int32 and page_table.numel() >= n_tokens // PAGE_TOKENS,
           "page_table must hold n_tokens/16 int32 page ids")
@@ -245,9 +253,10 @@ def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis1
     a.basis = _ptr(basis16)
     a.inv_freq[:] = consts.inv_freq
     a.rope_scaling = consts.rope_scaling
-    a.apply_rope = int(bool(apply_rope))
+    a.apply_rope = int(apply_rope)
     a.codebook[:] = consts.codebook
     a.v_sign_bits[:] = consts.sign_bits
     a.k_out, a.v_out = _ptr(k), _ptr(v)
+    a.out_dtype = _V_DTYPES[dtype]
     _lib.check(_lib.lib().bmx_k2b_dequant(ct.byref(a), _stream(dev)), "bmx_k2b_dequant")
     return k, v

@@ -177,9 +177,15 @@ typedef struct {
 int bmx_k2b_append(const bmx_k2b_append_args* args, void* stream);
 
 /* ------------------------------------------------------------------------
- * Dequantize committed pages of one sequence to dense fp32 (prefill path and
- * checks).  Replaces _dequant_block / _dense_kv (cache/chunked_attention.py:
- * 52-194): keys are returned pre-RoPE unless apply_rope != 0.
+ * Dequantize committed pages of one sequence to dense keys and values
+ * (prefill path and checks).  Replaces _dequant_block / _dense_kv and the
+ * dtype cast of _assemble_dense_kv (cache/chunked_attention.py:52-251).
+ * apply_rope: 0 = keys pre-RoPE; 1 = RoPE with fp32 cos/sin of the exact
+ * angle; 2 = RoPE as the reference's prefill applies it (cache/
+ * packed_streaming.py:79-113, chunked_attention.py:148-194): HF's fp32 angle
+ * fl(inv_freq_j * pos), cos/sin times rope_scaling rounded to fp16, the
+ * rotation x*cos + rotate_half(x)*sin in fp32.  The result is rounded once
+ * to out_dtype.
  * ---------------------------------------------------------------------- */
 typedef struct {
   bmx_k2b_geom geom;
@@ -193,8 +199,9 @@ typedef struct {
   int32_t apply_rope;
   float codebook[4];
   uint32_t v_sign_bits[4];
-  float* k_out;               /* device fp32 [h_kv][n_tokens][128] */
-  float* v_out;               /* device fp32 [h_kv][n_tokens][128] */
+  void* k_out;                /* device [h_kv][n_tokens][128] of out_dtype */
+  void* v_out;                /* device [h_kv][n_tokens][128] of out_dtype */
+  int32_t out_dtype;          /* BMX_K2B_F16 (0), BMX_K2B_F32 or BMX_K2B_BF16 */
 } bmx_k2b_dequant_args;
 
 int bmx_k2b_dequant(const bmx_k2b_dequant_args* args, void* stream);

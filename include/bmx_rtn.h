@@ -129,10 +129,10 @@ size_t bmx_rtn_decode_workspace_bytes(const bmx_rtn_decode_args* args);
 int bmx_rtn_decode(const bmx_rtn_decode_args* args, void* stream);
 
 /* ------------------------------------------------------------------------
- * Dequantize pages to dense fp32 keys and values (prefill): the dequant half
- * of chunked_attention._dense_kv (cache/chunked_attention.py:148-251) for the
- * RTN arms (codes * fp16 scale).  k_out/v_out: device [h_kv][16 *
- * n_pages][128] fp32.
+ * Dequantize pages to dense keys and values (prefill): the dequant half of
+ * chunked_attention._dense_kv and the dtype cast of _assemble_dense_kv
+ * (cache/chunked_attention.py:148-251) for the RTN arms (code * fp16 scale,
+ * rounded once to out_dtype).  k_out/v_out: device [h_kv][16 * n_pages][128].
  * ---------------------------------------------------------------------- */
 typedef struct {
   bmx_rtn_geom geom;
@@ -140,8 +140,9 @@ typedef struct {
   int32_t n_pool_pages;
   const int32_t* page_ids;    /* device [n_pages] */
   int32_t n_pages;
-  float* k_out;
-  float* v_out;
+  void* k_out;
+  void* v_out;
+  int32_t out_dtype;          /* BMX_K2B_F16 (0), BMX_K2B_F32 or BMX_K2B_BF16 */
 } bmx_rtn_dequant_args;
 
 int bmx_rtn_dequant(const bmx_rtn_dequant_args* args, void* stream);

@@ -235,3 +235,115 @@ def test_rtn_layer_streaming_decode_and_prefill(recipe):
     assert lay.bpe_k == pytest.approx((bpe_page * P + 16 * (N - P)) / N)
     print(f"{recipe} layer: {n_steps} decode steps, committed {P}, worst max_abs {worst:.3e}, "
           f"bpe_k {lay.bpe_k:.4f}", flush=True)
+
+
+def _explicit_attention(q, K, V, G, scale, offset):
+    """fp32 attention of q (H, n_q, d) over K, V (h_kv, n_kv, d): query i sits at
+    position offset + i and sees keys 0 .. offset + i."""
+    n_q, n_kv = q.shape[1], K.shape[1]
+    Kx, Vx = K.float().repeat_interleave(G, 0), V.float().repeat_interleave(G, 0)
+    s = (q.float() @ Kx.transpose(1, 2).contiguous()) * scale
+    i = torch.arange(n_q)[:, None]
+    j = torch.arange(n_kv)[None, :]
+    s = s.masked_fill(~(j <= i + offset), float("-inf"))
+    return torch.softmax(s, dim=-1) @ Vx
+
+
+@pytest.mark.parametrize("path,dtype", [("k2b", torch.float16), ("k2b", torch.float32),
+                                        ("rtn", torch.float16)])
+def test_two_block_prefill_mask_contract(path, dtype):
+    """The cached two-block prefill (test_packed_streaming.py:100-153): a first
+    forward of 600 tokens, then a second of 300 -- queries at positions
+    600..899 over 900 keys, fewer queries than keys, so a top-left causal mask
+    would be wrong.  The second block through the layer (committed pages
+    dequantized by the page kernel in the model dtype, k2b keys rotated with
+    the fp16 RoPE tables in the same pass, one SDPA over grouped heads), with
+    no mask from the model and with the model's own boolean mask, equals an
+    explicit bottom-right-masked fp32 attention over the oracle's dequantized
+    pages and the fp16 window; the top-left result is far from it."""
+    from transformers import LlamaConfig
+
+    from bmx_amd import synth
+    from bmx_amd.cache import PackedStreamingLayer
+    from bmx_amd.specs import CacheCodecSpec
+    from oracle import attention as A
+    from oracle_cache import OracleLayer
+
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                      num_hidden_layers=32, rope_theta=500000.0)
+    h_kv, G, d, W = 8, 4, 128, 128
+    n1, n2 = 600, 300
+    N = n1 + n2
+    gen = torch.Generator().manual_seed(91)
+    if path == "k2b":
+        k_spec, v_spec = spec_pair("k2b_ph", rank=16)
+        prod = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=W)
+        orac = OracleLayer(k_spec, v_spec, cfg, recent_window=W)
+        orac.v_fp16 = True
+        k_pre = synth.k2b_keys(h_kv, N, 16, gen)
+        cos, sin = A.rope_cos_sin(prod._inv_freq, torch.arange(N))
+        k_post = A.apply_rope(k_pre.float(), cos, sin).half()
+    else:
+        k_spec = CacheCodecSpec(arm="rtn_token", bits=4, group=32, pre_rope=False)
+        v_spec = CacheCodecSpec(arm="rtn_token", bits=4, group=32)
+        prod = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=W)
+        oc = A.RtnOracleCache(h_kv, k_bits=4, v_bits=4, k_group=32, v_group=32)
+        k_post = torch.randn(h_kv, N, d, generator=gen).half()
+    v = synth.values(h_kv, N, gen).half()
+
+    def feed(lo, hi):
+        if path == "k2b":
+            for lay, dev in ((prod, "cuda"), (orac, "cpu")):
+                lay.stash_pre_rope(k_pre[:, lo:hi].transpose(0, 1).unsqueeze(0).to(dev))
+                lay.update(k_post[:, lo:hi].unsqueeze(0).to(dev), v[:, lo:hi].unsqueeze(0).to(dev))
+        else:
+            prod.update(k_post[:, lo:hi].unsqueeze(0).cuda(), v[:, lo:hi].unsqueeze(0).cuda())
+            while oc.n_tokens < prod._committed_S_q:
+                s = oc.n_tokens
+                oc.commit(k_post[:, s:s + 128], v[:, s:s + 128])
+
+    feed(0, n1)
+    feed(n1, N)
+    P = prod._committed_S_q
+    assert P == ((N - W) // 128) * 128 and prod.get_seq_length() == N
+    if path == "k2b":
+        K, V = orac._kv(torch.float32)
+    else:
+        Kd, Vd = oc.dense_kv()
+        K, V = torch.cat([Kd, k_post[:, P:].float()], 1), torch.cat([Vd, v[:, P:].float()], 1)
+    q = torch.randn(h_kv * G, n2, d, generator=gen).to(dtype)
+    ref = _explicit_attention(q, K, V, G, d ** -0.5, n1)
+    wrong = _explicit_attention(q, K, V, G, d ** -0.5, 0)
+    mask = (torch.arange(N)[None, :] <= torch.arange(n2)[:, None] + n1)[None, None].cuda()
+    tol = 2e-3 if dtype == torch.float32 else 4e-3
+    for what, m in (("no mask", None), ("model mask", mask)):
+        out = prod.attend(q.cuda(), d ** -0.5, is_causal=True, attention_mask=m)
+        assert out.dtype == dtype
+        err = (out.float().cpu() - ref).abs().max().item()
+        off = (out.float().cpu() - wrong).abs().max().item()
+        print(f"{path} {dtype} two-block prefill ({what}): max_abs {err:.3e} vs the bottom-right "
+              f"oracle, {off:.3e} vs top-left", flush=True)
+        assert err <= tol and off > 50 * tol
+
+
+def test_two_block_prefill_through_the_model():
+    """HF threads its mask into the packed attention: the tiny Llama's cached
+    two-block prefill (200 tokens, then 200 more) through the product cache
+    and through the oracle-backed cache agree at every position of the second
+    block."""
+    g = np.load(GOLD / "e2e_tiny_llama.npz")
+    tokens = torch.from_numpy(g["r16_tokens"]).cuda()
+    model = _tiny_model()
+
+    def run(cache):
+        with cache.attach(model), torch.no_grad():
+            model(tokens[:, :200], past_key_values=cache, use_cache=True)
+            return model(tokens[:, 200:400], past_key_values=cache, use_cache=True).logits[0].double().cpu()
+
+    got = run(PackedStreamingCache(model.config, *spec_pair("k2b_ph", rank=16), recent_window=32))
+    ref = run(OracleCache(model.config, *spec_pair("k2b_ph", rank=16), recent_window=32))
+    err = (got - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    print(f"tiny Llama two-block prefill: logits max|err| {err:.3e} of max|logit| {scale:.3f}", flush=True)
+    assert err <= 2e-3 * max(scale, 1.0)
+    assert bool((got.argmax(-1) == ref.argmax(-1)).all())

@@ -471,3 +471,20 @@ def test_dequant_matches_oracle():
     assert (Kp.cpu() - K_or).abs().max().item() < 2e-3
     assert (Kr.cpu() - A.apply_rope(K_or, cos, sin)).abs().max().item() < 2e-3
     assert (Vd.cpu() - V_or).abs().max().item() < 1e-4
+    # the prefill form (chunked_attention.py:148-251): RoPE with the fp16-rounded
+    # tables applied in fp32, as torch applies them to the pre-RoPE keys, then one
+    # rounding to the model's dtype
+    from bmx_amd.cache import _rope_tables
+
+    Kt, _ = k2b.dequant(pool.pages, pt, S, seq.basis16, consts, h_kv=h_kv, rank=rank,
+                        apply_rope=k2b.ROPE_FP16_TABLES)
+    c16, s16 = _rope_tables(torch.tensor(consts.inv_freq), consts.rope_scaling, 0, S, DEV)
+    rot = torch.cat((-Kp[..., 64:], Kp[..., :64]), dim=-1)
+    want = Kp * c16.float().unsqueeze(0) + rot * s16.float().unsqueeze(0)
+    d = (Kt - want).abs().max().item()
+    print(f"fp16-table RoPE in the dequant pass vs torch: max_abs {d:.3e}", flush=True)
+    assert d <= 1e-6 * Kp.abs().max().item()
+    for dt in (torch.float16, torch.bfloat16):
+        Kh, Vh = k2b.dequant(pool.pages, pt, S, seq.basis16, consts, h_kv=h_kv, rank=rank,
+                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt)
+        assert Kh.dtype == dt and torch.equal(Kh, Kt.to(dt)) and torch.equal(Vh, Vd.to(dt))

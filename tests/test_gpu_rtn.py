@@ -111,6 +111,11 @@ def test_dequant_bit_exact():
     K, V = rtn.dequant(pool.pages, torch.tensor(ids, dtype=torch.int32, device=DEV), h_kv=h_kv, **codec)
     rK, rV = _oracle(h_kv, k, v, codec).dense_kv()
     assert torch.equal(K.cpu(), rK) and torch.equal(V.cpu(), rV)
+    # in the model's dtype (the prefill form): the same values rounded once
+    for dt in (torch.float16, torch.bfloat16):
+        Kh, Vh = rtn.dequant(pool.pages, torch.tensor(ids, dtype=torch.int32, device=DEV), h_kv=h_kv, dtype=dt,
+                             **codec)
+        assert Kh.dtype == dt and torch.equal(Kh, K.to(dt)) and torch.equal(Vh, V.to(dt))
 
 
 def _decode_case(h_kv, G, S, T, codec, gen, split_tokens=0, outliers=True):
