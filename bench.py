@@ -63,12 +63,15 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fp16-comparator", action="store_true",
                     help="skip timing the dense fp16 decode at the same context")
-    ap.add_argument("--workload", choices=["decode", "stream", "rtn"], default="decode",
+    ap.add_argument("--prefill-ctx", type=int, default=8192)
+    ap.add_argument("--prefill-chunk", type=int, default=512)
+    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill"], default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
                          "BASELINE config 5, Qwen3-8B geometry, rank 16, an 8192-token prefill "
                          "then --stream-steps steps of one-token append + decode over 36 layers; "
                          "rtn: BASELINE config 1, RTN 4-bit per-channel keys / per-token values, "
-                         "ctx --rtn-ctx, --rtn-layers layers")
+                         "ctx --rtn-ctx, --rtn-layers layers; prefill: the second block of a cached "
+                         "two-block prefill, --prefill-chunk queries over --prefill-ctx + chunk keys")
     ap.add_argument("--rtn-ctx", type=int, default=4096)
     ap.add_argument("--rtn-layers", type=int, default=1)
     ap.add_argument("--stream-steps", type=int, default=512)
@@ -419,6 +422,98 @@ def run_rtn(args, torch, dev) -> dict:
     return res
 
 
+PREFILL_METRIC = ("prefill-attn µs/layer-call (second block of a cached two-block prefill), k2b rank 32, "
+                  "Llama-3.1-8B geometry, 1 MI355X")
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+
+
+def run_prefill(args, torch, dev) -> dict:
+    """The prefill row: the second forward of a cached two-block prefill, the
+    case where the packed cache serves queries of a prompt chunk -- n_q =
+    --prefill-chunk new tokens at positions ctx .. ctx + n_q - 1 over ctx + n_q
+    keys, the model's boolean mask, one layer of Llama-3.1-8B geometry (32
+    query / 8 KV heads, d 128), k2b rank 32, recent window 128, fp16.  A call
+    is PackedStreamingLayer.attend: the page dequant kernel (keys rotated in
+    the pass, fp16 out), the window appended, one SDPA.  Beside it: the dequant
+    kernel alone (HBM-bound: pages in, dense fp16 K and V out) and the same
+    SDPA over the same dense fp16 K/V alone (what a dense fp16 cache pays)."""
+    import torch.nn.functional as F
+    from transformers import LlamaConfig
+
+    from bmx_amd import k2b, synth
+    from bmx_amd.cache import PackedStreamingLayer
+    from bmx_amd.specs import spec_pair
+    from oracle import attention as A
+
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                      num_hidden_layers=32, rope_theta=500000.0)
+    ctx, nq, W = args.prefill_ctx, args.prefill_chunk, 128
+    N = ctx + nq
+    k_spec, v_spec = spec_pair("k2b_ph", rank=args.rank)
+    lay = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=W)
+    gen = torch.Generator().manual_seed(5)
+    k_pre = synth.k2b_keys(H_KV, N, args.rank, gen)
+    v = synth.values(H_KV, N, gen).half()
+    cos, sin = A.rope_cos_sin(lay._inv_freq, torch.arange(N))
+    k_post = A.apply_rope(k_pre.float(), cos, sin).half()
+    for lo, hi in ((0, ctx), (ctx, N)):
+        lay.stash_pre_rope(k_pre[:, lo:hi].transpose(0, 1).unsqueeze(0).to(dev))
+        lay.update(k_post[:, lo:hi].unsqueeze(0).to(dev), v[:, lo:hi].unsqueeze(0).to(dev))
+    P = lay._committed_S_q
+    q = torch.randn(H_KV * G, nq, D, generator=gen).half().to(dev)
+    mask = (torch.arange(N, device=dev)[None, :] <= torch.arange(nq, device=dev)[:, None] + ctx)[None, None]
+    scale = D ** -0.5
+    Kd, Vd = k2b.dequant(lay._pool, lay._table[0, : P // 16].contiguous(), P, lay._basis16, lay._consts,
+                         h_kv=H_KV, rank=args.rank, apply_rope=k2b.ROPE_FP16_TABLES, dtype=torch.float16)
+    Kf = torch.cat([Kd, lay.keys.squeeze(0).half()], 1).repeat_interleave(G, 0).unsqueeze(0)
+    Vf = torch.cat([Vd, lay.values.squeeze(0).half()], 1).repeat_interleave(G, 0).unsqueeze(0)
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    reps = max(args.steps, 1)
+    call_us = timed(lambda: lay.attend(q, scale, is_causal=True, attention_mask=mask), reps)
+    deq_us = timed(lambda: k2b.dequant(lay._pool, lay._table[0, : P // 16].contiguous(), P, lay._basis16,
+                                       lay._consts, h_kv=H_KV, rank=args.rank,
+                                       apply_rope=k2b.ROPE_FP16_TABLES, dtype=torch.float16), reps)
+    sdpa_us = timed(lambda: F.scaled_dot_product_attention(q.unsqueeze(0), Kf, Vf, attn_mask=mask, scale=scale),
+                    reps)
+    out = lay.attend(q, scale, is_causal=True, attention_mask=mask).float()
+    ref = F.scaled_dot_product_attention(q.unsqueeze(0).float(), Kf.float(), Vf.float(), attn_mask=mask,
+                                         scale=scale).squeeze(0)
+    page_bytes = k2b.page_bytes(H_KV, args.rank)
+    deq_bytes = P * page_bytes // 16 + H_KV * D * args.rank * 2 + 2 * P * H_KV * D * 2
+    flops = 4.0 * H_KV * G * D * (nq * ctx + nq * (nq + 1) / 2)   # QK^T and PV over the visible keys
+    return {
+        "metric": PREFILL_METRIC, "value": round(call_us, 2), "unit": "us/layer-call", "n_gpus": 1,
+        "steps": reps, "warmup": 3, "ms_per_step": round(call_us / 1e3, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": (f"cached two-block prefill, second block: {nq} queries at positions "
+                                f"{ctx}..{N - 1} over {N} keys ({P} packed + {N - P} fp16 window), "
+                                f"k2b rank {args.rank}, 32q/8kv heads, d 128, model mask"),
+                   "ctx": ctx, "chunk": nq, "packed_tokens": P, "rank": args.rank},
+        "roofline": {"bound": "hbm", "kernel": "k2b_dequant_kernel (pages -> dense fp16 K, V)",
+                     "achieved": round(deq_bytes / (deq_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(deq_bytes / (deq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": deq_bytes, "avg_launch_us": round(deq_us, 3)},
+        "prefill_call": {"dequant_us": round(deq_us, 2), "sdpa_dense_fp16_us": round(sdpa_us, 2),
+                         "sdpa_tflops": round(flops / (sdpa_us * 1e-6) / 1e12, 1),
+                         "sdpa_frac_of_fp16_mfma_peak": round(flops / (sdpa_us * 1e-6) / 1e12
+                                                              / MFMA_FP16_PEAK_TFLOPS, 4),
+                         "packed_over_dense_fp16": round(call_us / sdpa_us, 3),
+                         "max_abs_vs_fp32_sdpa": (out - ref).abs().max().item()},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -439,6 +534,9 @@ def main():
         return
     if args.workload == "rtn":
         print(json.dumps(run_rtn(args, torch, dev)), flush=True)
+        return
+    if args.workload == "prefill":
+        print(json.dumps(run_prefill(args, torch, dev)), flush=True)
         return
     if args.copy_calib_mib > 0:
         n = args.copy_calib_mib << 20

@@ -347,10 +347,12 @@ class PackedStreamingLayer(DynamicLayer):
         """Prefill (n_q > 1): _prefill_dense_attention (chunked_attention.py:
         320-395).  The page kernel dequantizes the committed pages straight to
         the model dtype (k2b keys rotated in the same pass with the fp16 RoPE
-        tables, as _dense_kv does), the fp16 window follows, and one flash SDPA
-        attends over the grouped heads (no G-fold copy of K and V).  With no
-        mask from the model and fewer queries than keys, the queries are the
-        last n_q positions: the mask is causal from the bottom right."""
+        tables, as _dense_kv does), the fp16 window follows, and one SDPA
+        attends: flash attention over the grouped heads (no G-fold copy of K
+        and V) when no mask is needed, the memory-efficient kernel over expanded
+        heads with one.  With no mask from the model and fewer queries than
+        keys, the queries are the last n_q positions: the mask is causal from
+        the bottom right."""
         dev, dt = q.device, q.dtype
         P = self._committed_S_q
         parts_k, parts_v = [], []
@@ -375,9 +377,16 @@ class PackedStreamingLayer(DynamicLayer):
             i = torch.arange(n_q, device=dev)[:, None]
             j = torch.arange(n_kv, device=dev)[None, :]
             attention_mask = (j <= i + (n_kv - n_q))[None, None]
-        out = F.scaled_dot_product_attention(
-            q.unsqueeze(0), Kd.unsqueeze(0), Vd.unsqueeze(0), attn_mask=attention_mask,
-            is_causal=causal and attention_mask is None, scale=scaling, enable_gqa=G > 1)
+        if attention_mask is None:
+            # no mask: ROCm's flash attention takes the grouped heads as they are
+            out = F.scaled_dot_product_attention(q.unsqueeze(0), Kd.unsqueeze(0), Vd.unsqueeze(0),
+                                                 is_causal=causal, scale=scaling, enable_gqa=G > 1)
+        else:
+            # with a mask only the memory-efficient kernel serves (the grouped-head
+            # form would fall back to the math path, several times slower): expand
+            out = F.scaled_dot_product_attention(
+                q.unsqueeze(0), Kd.repeat_interleave(G, dim=0).unsqueeze(0),
+                Vd.repeat_interleave(G, dim=0).unsqueeze(0), attn_mask=attention_mask, scale=scaling)
         return out.squeeze(0)
 
 
