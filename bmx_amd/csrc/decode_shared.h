@@ -74,19 +74,22 @@ __device__ __forceinline__ void query_fragments(const float4_t qraw[8], float sc
 }
 
 // ---------------------------------------------------------------------------
-// Combine: merge of the packed partials and the recent window.  One workgroup
-// per (16-channel chunk, query row, sequence): the partials arrive already in
-// the output domain, so a chunk needs only its own 16 channels of every split
+// Combine: merge of the packed partials and the recent window.  One wave per
+// (16-channel chunk, query row, sequence): the partials arrive already in the
+// output domain, so a chunk needs only its own 16 channels of every split
 // (contiguous, 64 B per split) plus every split's (max, sum); the window needs
 // its scores (computed by the split kernel) and its 16 value channels of every
-// token.  Thread i takes split i and window token i of each 256-wide block;
-// every load of the first block is issued before any reduction.
+// token.  Lane (phase p = lane & 15, quarter c4 = lane >> 4) takes channels
+// 4c4 .. 4c4 + 3 of splits p, p + 16, ... and of window tokens p, p + 16, ...;
+// every row of 16 lanes sees every split and token, so the maxima and sums
+// are row reductions (DPP, no LDS, no barrier) and only the final Hadamard
+// crosses rows.  All loads of the first pass are issued before any use.
 // ---------------------------------------------------------------------------
-constexpr int kCmbThreads = 256;
-constexpr int kCmbWaves = kCmbThreads / 64;
-constexpr int kChunk = 16;                  // channels per workgroup
+constexpr int kCmbThreads = 64;
+constexpr int kChunk = 16;                  // channels per merge unit
 constexpr int kChunks = kD / kChunk;
-constexpr int kRedPad = kCmbThreads + 4;    // LDS row stride of the reductions
+constexpr int kCmbSplits = 16;              // splits per lane per pass
+constexpr int kCmbTokens = 8;               // window tokens per lane per pass
 
 struct CombineKArgs {
   int h_kv, G, max_splits, tail_cap;
@@ -102,12 +105,27 @@ struct CombineKArgs {
                              // level scale; 1 otherwise
 };
 
-// Sum over the 16 lanes of a row (DPP-free butterfly; result in every lane).
-__device__ __forceinline__ float row_sum16(float x) {
-  x += __shfl_xor(x, 8);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 1);
+// v from another lane of the same 16-lane row (DPP control CTRL), every lane written.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// All-reduce over the 16 lanes of a row with DPP (quad xor 1, quad xor 2,
+// half-row mirror, row mirror): every lane gets the same value.
+template <bool kMax>
+__device__ __forceinline__ float row_reduce16(float x) {
+  if constexpr (kMax) {
+    x = fmaxf(x, dpp_row<0xB1>(x));    // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp_row<0x4E>(x));    // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp_row<0x141>(x));   // row_half_mirror
+    x = fmaxf(x, dpp_row<0x140>(x));   // row_mirror
+  } else {
+    x += dpp_row<0xB1>(x);
+    x += dpp_row<0x4E>(x);
+    x += dpp_row<0x141>(x);
+    x += dpp_row<0x140>(x);
+  }
   return x;
 }
 
@@ -118,151 +136,130 @@ template <bool kRotated>
 __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs a) {
   const int ch = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
   const int h = r / a.G;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lane = threadIdx.x, p = lane & 15, c4 = lane >> 4;
   const int S = a.max_splits;
   const int64_t row = (int64_t)b * a.h_kv * a.G + r;   // (b, h, g) row
-  const float* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S * kChunk;
+  const float* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S * kChunk + 4 * c4;
   const float* mlb = a.ws_ml + row * S * 2;
   const float* swb = a.ws_win + row * a.tail_cap;
-  const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch;
+  const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch + 4 * c4;
   typedef float f2_t __attribute__((ext_vector_type(2)));
-  __shared__ float s_red[2 * kCmbWaves];
-  __shared__ float s_fin[2 * kChunk];
-  __shared__ float s_x[kChunk * kRedPad];
-  __shared__ float s_v[kChunk * kRedPad];
 
-  float4_t v[4];
-  f2_t ml = {-INFINITY, 0.f};
-  uint4 vv[2];
-  float sw = -INFINITY;
-  // partial block k and window block k, no waits; the first block's window
-  // rows are bounded by the host's tail_cap, so they do not wait for tail_len
-  auto load_block = [&](int k, int t_end) {
-    const int i0 = k * kCmbThreads;
-    if (i0 < S) {
-      const int i = min(i0 + tid, S - 1);
-      ml = *reinterpret_cast<const f2_t*>(mlb + 2 * (int64_t)i);
+  f2_t ml[kCmbSplits];
+  float4_t pv[kCmbSplits];
+  float ws[kCmbTokens];
+  uint2 wv[kCmbTokens];
+  auto load_splits = [&](int j0) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4_t*>(accb + (int64_t)i * kChunk + 4 * u);
-    }
-    if (i0 < t_end) {
-      const int t = min(i0 + tid, t_end - 1);
-      sw = swb[t];
-      vv[0] = *reinterpret_cast<const uint4*>(vb + (int64_t)t * a.ts_t);
-      vv[1] = *reinterpret_cast<const uint4*>(vb + (int64_t)t * a.ts_t + 8);
+    for (int u = 0; u < kCmbSplits; ++u) {
+      const int i = min(j0 + p + 16 * u, S - 1);
+      ml[u] = *reinterpret_cast<const f2_t*>(mlb + 2 * (int64_t)i);
+      pv[u] = *reinterpret_cast<const float4_t*>(accb + (int64_t)i * kChunk);
     }
   };
-  load_block(0, a.tail_cap);
-
+  auto load_tokens = [&](int t0, int t_end) {   // t_end >= 1
+#pragma unroll
+    for (int u = 0; u < kCmbTokens; ++u) {
+      const int t = min(t0 + p + 16 * u, t_end - 1);
+      ws[u] = swb[t];
+      wv[u] = *reinterpret_cast<const uint2*>(vb + (int64_t)t * a.ts_t);
+    }
+  };
+  // first pass of both, bounded by the host's S and tail_cap (no wait on tail_len)
+  load_splits(0);
+  if (a.tail_cap > 0) load_tokens(0, a.tail_cap);
   const int T = min(max(a.tail_len[b], 0), a.tail_cap);
-  float4_t xp[4];
+
+  // ---- packed partials: online over passes of 16 splits per lane ----
+  float mp = -INFINITY, lp = 0.f;
+  float4_t xp = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < S; j0 += 16 * kCmbSplits) {
+    if (j0 != 0) load_splits(j0);
+    float mloc = -INFINITY;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) xp[u] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float vacc[kChunk];
+    for (int u = 0; u < kCmbSplits; ++u)
+      if (j0 + p + 16 * u < S) mloc = fmaxf(mloc, ml[u][0]);
+    const float mnew = fmaxf(mp, row_reduce16<true>(mloc));
+    if (mnew != -INFINITY) {
+      const float sc = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mnew);
+      xp *= sc;
+      lp *= sc;
 #pragma unroll
-  for (int e = 0; e < kChunk; ++e) vacc[e] = 0.f;
-  float mp = -INFINITY, mt = -INFINITY, lp = 0.f, lt = 0.f;   // lp, lt: this thread's share
-  const int n_blk = (max(S, T) + kCmbThreads - 1) / kCmbThreads;
-  for (int k = 0; k < n_blk; ++k) {   // uniform trip count
-    if (k != 0) load_block(k, T);
-    const int i0 = k * kCmbThreads;
-    const bool own_p = i0 + tid < S;
-    const float mi = own_p ? ml[0] : -INFINITY;
-    const float st = i0 + tid < T ? sw : -INFINITY;
-    // one joint block max of (partial max, window score)
-    float r0 = mi, r1 = st;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      r0 = fmaxf(r0, __shfl_xor(r0, o));
-      r1 = fmaxf(r1, __shfl_xor(r1, o));
-    }
-    if (lane == 0) {
-      s_red[2 * wave] = r0;
-      s_red[2 * wave + 1] = r1;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int w = 0; w < kCmbWaves; ++w) {
-      r0 = fmaxf(r0, s_red[2 * w]);
-      r1 = fmaxf(r1, s_red[2 * w + 1]);
-    }
-    const float mp_new = fmaxf(mp, r0), mt_new = fmaxf(mt, r1);
-    const float ap = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mp_new);
-    const float at = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - mt_new);
-    const float wi = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - mp_new);
-    const float pt = st == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st - mt_new);
-    lp = lp * ap + (own_p ? ml[1] * wi : 0.f);
-    lt = lt * at + pt;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) xp[u] = xp[u] * ap + (own_p ? v[u] * wi : float4_t{0.f, 0.f, 0.f, 0.f});
-    if (i0 < T) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t w = (e < 4 ? (&vv[0].x)[e] : (&vv[1].x)[e - 4]);
-        vacc[2 * e] = __builtin_fmaf(pt, half_bits_to_float(w & 0xffff), vacc[2 * e] * at);
-        vacc[2 * e + 1] = __builtin_fmaf(pt, half_bits_to_float(w >> 16), vacc[2 * e + 1] * at);
+      for (int u = 0; u < kCmbSplits; ++u) {
+        const bool ok = j0 + p + 16 * u < S && ml[u][0] != -INFINITY;
+        const float w = ok ? __builtin_amdgcn_exp2f(ml[u][0] - mnew) : 0.f;
+        xp += w * pv[u];
+        lp = __builtin_fmaf(w, ml[u][1], lp);
       }
+      mp = mnew;
     }
-    mp = mp_new;
-    mt = mt_new;
-    __syncthreads();   // s_red is rewritten by the next block
   }
-  // ---- gather: channel c of the packed sum over the splits (thread tid holds
-  // split tid's share), of the window sum over the tokens, and the denominators ----
+  // ---- window: online over passes of 8 tokens per lane ----
+  float mt = -INFINITY, lt = 0.f;
+  float4_t xt = {0.f, 0.f, 0.f, 0.f};
+  for (int t0 = 0; t0 < T; t0 += 16 * kCmbTokens) {
+    if (t0 != 0) load_tokens(t0, T);
+    float mloc = -INFINITY;
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < kCmbTokens; ++u)
+      if (t0 + p + 16 * u < T) mloc = fmaxf(mloc, ws[u]);
+    const float mnew = fmaxf(mt, row_reduce16<true>(mloc));
+    const float sc = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - mnew);
+    xt *= sc;
+    lt *= sc;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s_x[(4 * u + e) * kRedPad + tid] = xp[u][e];
-#pragma unroll
-  for (int e = 0; e < kChunk; ++e) s_v[e * kRedPad + tid] = vacc[e];
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    lp += __shfl_xor(lp, o);
-    lt += __shfl_xor(lt, o);
+    for (int u = 0; u < kCmbTokens; ++u) {
+      const float w = t0 + p + 16 * u < T ? __builtin_amdgcn_exp2f(ws[u] - mnew) : 0.f;
+      const float4_t vf = {half_bits_to_float(wv[u].x & 0xffff), half_bits_to_float(wv[u].x >> 16),
+                           half_bits_to_float(wv[u].y & 0xffff), half_bits_to_float(wv[u].y >> 16)};
+      xt += w * vf;
+      lt += w;
+    }
+    mt = mnew;
   }
-  if (lane == 0) {
-    s_red[2 * wave] = lp;
-    s_red[2 * wave + 1] = lt;
-  }
-  __syncthreads();
-  float lpt = 0.f, ltt = 0.f;
+  // ---- row sums (every row holds all splits and tokens, for its 4 channels) ----
+  float y[4], z[4];
 #pragma unroll
-  for (int w = 0; w < kCmbWaves; ++w) {
-    lpt += s_red[2 * w];
-    ltt += s_red[2 * w + 1];
+  for (int i = 0; i < 4; ++i) {
+    y[i] = row_reduce16<false>(xp[i]);
+    z[i] = row_reduce16<false>(xt[i]);
   }
-  // thread (c = tid / 16, part = tid % 16) sums splits and tokens part + 16j
-  const int c = tid >> 4, part = tid & 15;
-  float x = 0.f, wv = 0.f;
+  lp = row_reduce16<false>(lp);
+  lt = row_reduce16<false>(lt);
+  if constexpr (kRotated) {
+    // H16 over the chunk's channel c = 4 c4 + i: bits 0-1 in registers, bits 2-3
+    // across rows; then sign and 1/(128 kappa)
 #pragma unroll
-  for (int j = 0; j < kCmbThreads / 16; ++j) {
-    x += s_x[c * kRedPad + part + 16 * j];
-    wv += s_v[c * kRedPad + part + 16 * j];
-  }
-  x = row_sum16(x);
-  wv = row_sum16(wv);
-  if (part == 0) {
-    s_fin[c] = x;
-    s_fin[kChunk + c] = wv;
-  }
-  __syncthreads();
-  if (tid < kChunk) {
-    float y = s_fin[tid];
-    const int cg = kChunk * ch + tid;
-    if constexpr (kRotated) {
-      // lane c: H16 over the chunk's channel bits 0-3, then sign and 1/(128 kappa)
+    for (int hb = 1; hb < 4; hb <<= 1)
 #pragma unroll
-      for (int hb = 1; hb < kChunk; hb <<= 1) {
-        const float p = __shfl_xor(y, hb);
-        y = (tid & hb) ? p - y : y + p;
+      for (int i = 0; i < 4; ++i)
+        if (!(i & hb)) {
+          const float u = y[i], w = y[i | hb];
+          y[i] = u + w;
+          y[i | hb] = u - w;
+        }
+#pragma unroll
+    for (int rb = 1; rb < 4; rb <<= 1)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float o = __shfl_xor(y[i], 16 * rb);
+        y[i] = (c4 & rb) ? o - y[i] : y[i] + o;
       }
-      y = (sign_neg(a.v_sign_bits, cg) ? -y : y) * a.packed_scale;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cg = kChunk * ch + 4 * c4 + i;
+      y[i] = (sign_neg(a.v_sign_bits, cg) ? -y[i] : y[i]) * a.packed_scale;
     }
+  }
+  if (p == 0) {
     const float M = fmaxf(mp, mt);
     const float wp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
     const float wt = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - M);
-    const float inv = 1.0f / (lpt * wp + ltt * wt);
-    a.out[row * kD + cg] = (y * wp + s_fin[kChunk + tid] * wt) * inv;
+    const float inv = 1.0f / (lp * wp + lt * wt);
+    float4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (y[i] * wp + z[i] * wt) * inv;
+    *reinterpret_cast<float4_t*>(a.out + row * kD + kChunk * ch + 4 * c4) = o;
   }
 }
 

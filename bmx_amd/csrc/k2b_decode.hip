@@ -10,7 +10,10 @@
 //     straight into VGPRs: all loads of the next group are issued at the top
 //     of a group and first waited on at its end;
 //   * the page prefix every head reads (Us, value norms, key scales) is loaded
-//     cooperatively one group ahead and staged in a two-slot LDS ring;
+//     cooperatively two groups ahead and staged in a three-slot LDS ring; when
+//     the prologue made every group's RoPE table, the waves hand the ring on
+//     with LDS counters instead of a barrier per group, so a wave may run a
+//     group ahead of the slowest;
 //   * the RoPE cos/sin of the group's 64 positions is produced once per
 //     workgroup, one group ahead (angle-addition recurrence from an exact start,
 //     corrected to HF's fp32 angle fl(inv_freq * pos)), as fp16 pairs in LDS
@@ -35,7 +38,7 @@
 //   * the workgroups that own a 16-token tile of the fp16 recent window score
 //     it on MFMA (decode_shared.h).
 //
-// combine_kernel<true> (decode_shared.h): one workgroup per (16-channel chunk,
+// combine_kernel<true> (decode_shared.h): one wave per (16-channel chunk,
 // query head, sequence) merges the packed partials of its chunk (base-2 LSE),
 // applies H16, the signs and 1/128, and joins the recent window from its
 // scores and fp16 values; all of its first-round loads are issued before any
@@ -63,6 +66,8 @@ constexpr int kCsRow = 68;                  // dwords per position row of the co
 constexpr int kCsBuf = kGroup * kCsRow;     // dwords per group table
 constexpr int kPidWindow = 64;              // page ids held per lane-vector
 constexpr int kCsMaxBufs = 8;               // RoPE table buffers at most (17 KB each)
+constexpr int kRingSlots = 3;               // prefix ring: group g in slot g % 3
+constexpr int kSyncPolls = 1 << 22;         // bound of a wave's wait on another wave's slot
 
 
 struct DecodeKArgs {
@@ -94,6 +99,22 @@ struct DecodeKArgs {
   float win_rescale;      // 1 / rope_scaling: window keys carry the RoPE scaling
   float* ws_win;          // [B][h_kv][G][tail_cap] window scores, base 2
 };
+
+// Wait until the workgroup counter *c reaches target (LDS, acquire at
+// workgroup scope); bounded, so a wave can never wait for ever.
+__device__ __forceinline__ void wait_count(uint32_t* c, uint32_t target) {
+  for (int it = 0; it < kSyncPolls; ++it) {
+    if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// One wave's arrival at the workgroup counter *c (release at workgroup scope:
+// the wave's earlier LDS reads and writes are complete).
+__device__ __forceinline__ void count_wave(uint32_t* c) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): every lane's LDS access has completed
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
@@ -242,6 +263,11 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   // s_vlut[v] = {lv(c0) | lv(c1) << 16, lv(c2) | lv(c3) << 16}, c_t = (v >> 2t) & 3
   // (static LDS: the byte index scales straight into the address)
   __shared__ uint2 s_vlut[256];
+  // hand-off of the prefix ring between waves, no workgroup barrier per group:
+  // s_sync[s] counts the waves that have stored a group's prefix into ring slot
+  // s, s_sync[3 + s] the waves done reading a group from slot s (monotonic:
+  // slot s serves groups s, s + 3, ...)
+  __shared__ uint32_t s_sync[2 * kRingSlots];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15;   // token within page (K side) / score column (softmax side)
@@ -315,10 +341,10 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const int SHB = a.shared_bytes;
   const int sh_chunks = SHB / 4;       // 16-byte chunks of the 4 pages' prefixes
   const int chunks_pp = SHB / 16;
-  // dynamic LDS: the two cos/sin tables, then the prefix ring
+  // dynamic LDS: the cos/sin tables, then the prefix ring
   const int cs_bufs = a.cs_bufs;
   uint32_t* cst = reinterpret_cast<uint32_t*>(smem);                            // [cs_bufs][64][kCsRow]
-  uint8_t* ring = smem + cs_bufs * kCsBuf * 4;                                  // [2][4][SHB]
+  uint8_t* ring = smem + cs_bufs * kCsBuf * 4;                                  // [3][4][SHB]
   const int n_pages = n_groups * kGroupPages;
 
   // page ids of the range, a window of 64 per lane-vector
@@ -350,6 +376,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
 
   // ---- first group in flight ----
   uint4 pre = load_prefix(0);
+  const uint4 pre1 = load_prefix(min(1, n_groups - 1));
   uint3 kres[kGroupPages];   // this group's codes (the next group's are fetched
   uint2 vcd[kGroupPages];    // into separate registers at the top of the group)
 #pragma unroll
@@ -420,6 +447,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     }
   }
   store_prefix(pre, 0);
+  store_prefix(pre1, 1);
+  // slots 0 and 1 hold groups 0 and 1 (visible at the barrier)
+  if (tid < 2 * kRingSlots) s_sync[tid] = tid < 2 ? kWaves : 0;
 
   // ---- per-wave state ----
   float4_t acc[8];
@@ -436,14 +466,19 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   // on the next group's loads (issued at the top of the same group).
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
 
+  // every RoPE table was made in the prologue: waves hand the prefix ring on
+  // through s_sync and may drift apart by up to a group
+  const bool lockstep = n_groups > cs_bufs;
   for (int gi = 0; gi < n_groups; ++gi) {
-    const int gn = min(gi + 1, n_groups - 1);   // group fetched during this one
-    if ((gn + 1) * kGroupPages - pid_base > kPidWindow) {   // slide the page-id window
-      pid_base = gi * kGroupPages;
+    const int gn = min(gi + 1, n_groups - 1);   // group whose codes are fetched during this one
+    const int gp = min(gi + 2, n_groups - 1);   // group whose prefix is fetched during this one
+    if ((gp + 1) * kGroupPages - pid_base > kPidWindow) {   // slide the page-id window
+      pid_base = gn * kGroupPages;
       pidv = load_ids(pid_base, n_pages);
     }
-    // every load of group gn is issued here, a whole group before its first use
-    const uint4 pre_n = load_prefix(gn);
+    // every load of group gn is issued here, a whole group before its first
+    // use, and the prefix of group gn + 1 with them
+    const uint4 pre_n = load_prefix(gp);
     uint3 kres_n[kGroupPages];
     uint2 vcd_n[kGroupPages];
     if (active) {
@@ -455,9 +490,12 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     }
     // groups past the prologue's tables: refill the buffer group gi-1 left
     if (gi > 0 && gi - 1 + cs_bufs < n_groups) produce_groups(gi - 1 + cs_bufs, 1, gi - 1);
+    // every wave has stored this group's prefix (use gi / 3 of slot gi % 3)
+    const int slot = gi % kRingSlots;
+    if (!lockstep) wait_count(&s_sync[slot], kWaves * (gi / kRingSlots + 1));
 
     if (active) {
-      const uint8_t* grp = ring + (gi & 1) * kGroupPages * SHB;
+      const uint8_t* grp = ring + slot * kGroupPages * SHB;
       const uint32_t* csb = cst + (gi % cs_bufs) * kCsBuf;
       // key-residual scale pairs (s_j, s_{j+64}), j = 16bb + 4q + i: 16 bytes
       // per bb in the group's prefix (re-read per page: fewer live VGPRs)
@@ -585,7 +623,18 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (gi + 1 < n_groups) store_prefix(pre_n, (gi + 1) & 1);   // slot last read by group gi-1
+    // the prefix of group gi + 2 goes to slot (gi + 2) % 3, last read by group gi - 1
+    const int slot2 = (gi + 2) % kRingSlots;
+    if (lockstep) {
+      if (gi + 2 < n_groups) store_prefix(pre_n, slot2);
+    } else {
+      count_wave(&s_sync[kRingSlots + slot]);   // done reading group gi
+      if (gi + 2 < n_groups) {
+        if (gi >= 1) wait_count(&s_sync[kRingSlots + slot2], kWaves * ((gi - 1) / kRingSlots + 1));
+        store_prefix(pre_n, slot2);
+        count_wave(&s_sync[slot2]);
+      }
+    }
     if (active) {
 #pragma unroll
       for (int pp = 0; pp < kGroupPages; ++pp) {
@@ -593,7 +642,8 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
         vcd[pp] = vcd_n[pp];
       }
     }
-    __syncthreads();   // table and prefix of group gi+1 visible; group gi's slots free
+    // with tables to refill in the loop, all waves move group by group
+    if (lockstep) __syncthreads();   // table of group gi+1 visible; group gi's slots free
   }
   if (active) {
     // fold the page slots: column s*SW + g -> g
@@ -882,7 +932,7 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   // RoPE tables for every group a workgroup owns, up to kCsMaxBufs
   const int max_groups = ((a->max_packed_len / kGroup) + max_splits - 1) / max_splits;
   k.cs_bufs = std::max(1, std::min(max_groups, kCsMaxBufs));
-  const size_t smem = (size_t)k.cs_bufs * kCsBuf * 4 + (size_t)2 * kGroupPages * k.shared_bytes;
+  const size_t smem = (size_t)k.cs_bufs * kCsBuf * 4 + (size_t)kRingSlots * kGroupPages * k.shared_bytes;
   dim3 grid(max_splits, a->batch);
   hipError_t e = g.rank == 32 ? launch_split<32>(k, grid, smem, st)
                               : launch_split<16>(k, grid, smem, st);
