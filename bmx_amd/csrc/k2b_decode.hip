@@ -116,9 +116,6 @@ __device__ __forceinline__ void count_wave(uint32_t* c) {
   if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
-__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
-
 // v_mov_b32_dpp: lanes enabled by BANK (4-lane banks of each 16-lane row) take
 // src from the DPP-selected lane, the others keep old.
 template <int CTRL, int BANK = 0xF>
@@ -134,42 +131,6 @@ constexpr int kRowRor = 0x120;  // + n: rotate within the row
 template <int CTRL>
 __device__ __forceinline__ float dpp_all(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
-}
-
-// The masks arrive in VGPRs (KresMasks) so each half pair is one v_and_or_b32.
-struct KresMasks {
-  uint32_t m0, m1, m2;   // code bits of slots 0, 3, 6 (both halves)
-  uint32_t e0, e1, e2;   // exponent fields 25, 22, 19 (both halves)
-  __device__ __forceinline__ void init() {
-    m0 = 0x00070007u; m1 = 0x00380038u; m2 = 0x01C001C0u;
-    e0 = 0x64006400u; e1 = 0x58005800u; e2 = 0x4C004C00u;
-    // opaque to the optimiser: keeps them in registers, out of literal operands
-    asm volatile("" : "+v"(m0), "+v"(m1), "+v"(m2));
-    asm volatile("" : "+s"(e0), "+s"(e1), "+s"(e2));
-  }
-};
-
-// The lane's 16 key-residual pairs (channels j, j+64) as exact fp16 integers.
-// An offset-binary 3-bit code c' at mantissa bits [s, s+3) under exponent field
-// 25 - s reads as 2^(10-s) + c'; one AND-OR builds two such halves and one
-// packed add removes 2^(10-s) + 4, leaving code = c' - 4.
-__device__ __forceinline__ void kres_pairs(const KresMasks& km, uint32_t w0, uint32_t w1, uint32_t w2,
-                                           half2_t c[16]) {
-  const half2_t b0 = {(_Float16)-1028.0f, (_Float16)-1028.0f};
-  const half2_t b1 = {(_Float16)-132.0f, (_Float16)-132.0f};
-  const half2_t b2 = {(_Float16)-20.0f, (_Float16)-20.0f};
-  const uint32_t w[3] = {w0, w1, w2};
-#pragma unroll
-  for (int d = 0; d < 3; ++d) {
-    const uint32_t x = w[d], y = x >> 9;
-    c[5 * d + 0] = as_h2((x & km.m0) | km.e0) + b0;
-    c[5 * d + 1] = as_h2((x & km.m1) | km.e1) + b1;
-    c[5 * d + 2] = as_h2((x & km.m2) | km.e2) + b2;
-    c[5 * d + 3] = as_h2((y & km.m0) | km.e0) + b0;
-    c[5 * d + 4] = as_h2((y & km.m1) | km.e1) + b1;
-  }
-  c[15] = as_h2(((w0 >> 15) & 0x00010001u) | ((w1 >> 14) & 0x00020002u) |
-                ((w2 >> 13) & 0x00040004u) | km.e0) + b0;
 }
 
 // RoPE of one packed pair (k_j, k_{j+64}) by the packed (cos, sin):

@@ -20,86 +20,185 @@ struct DequantKArgs {
   void* v_out;
 };
 
-// grid (n_tokens/16, h_kv), block 256
-__global__ __launch_bounds__(256) void k2b_dequant_kernel(const DequantKArgs a) {
-  const int lp = blockIdx.x, h = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int C = kD * a.h_kv;
-  const int R = a.R;
-  const uint8_t* page = a.pages + clamp_page(a.page_table[lp], a.n_pool) * a.L.bytes;
-  __shared__ float s_us[kPT][33];
-  __shared__ float x[kPT][kD];
-  for (int e = tid; e < kPT * R; e += 256)
-    s_us[e / R][e % R] = half_bits_to_float(
-        *reinterpret_cast<const uint16_t*>(page + a.L.us + us_half(R, e / R, e % R) * 2));
-  __syncthreads();
+// One wave per (16-token page, head), four heads per workgroup; grid
+// (n_tokens / 16, ceil(h_kv / 4)), block 256.  The wave does a decode
+// kernel's page work once, in fp32:
+//   keys: K^T = basis_h * Us^T on MFMA (lane 16q + n: token n, channels
+//   j = 16bb + 4q + i and j + 64), plus code * scale (the 3-bit codes as exact
+//   fp16 integers), then RoPE from the page's cos/sin table, shared by the
+//   workgroup's heads;
+//   values: the lane's code bytes (channel 16b + n, tokens 4q .. 4q + 3) give
+//   codebook levels, H8 over b in registers and H16 over n across the row's
+//   lanes make the 128-point Hadamard, then 1/128, signs and the norm;
+// each tile goes through a per-wave LDS staging tile so that the dense rows
+// are written with 16-byte coalesced stores, rounded once to the output type.
+constexpr int kDqWaves = 4;
+constexpr int kDqPad = kD + 4;   // staging row stride (floats)
 
-  // keys: thread handles (token t, channel pair j, j+64) for 4 pairs
-  const int grp = lp / 4;
-  for (int e = tid; e < kPT * 64; e += 256) {
-    const int t = e / 64, j0 = e % 64;
-    float kv[2];
-    for (int s = 0; s < 2; ++s) {
-      const int j = j0 + 64 * s;
-      const int c = h * kD + j;
-      float acc = 0.f;
-      for (int r = 0; r < R; ++r)
-        acc = __builtin_fmaf(s_us[t][r], half_bits_to_float(a.basis[(int64_t)c * R + r]), acc);
-      const int f = kscale_flat(c), quarter = C / 4, slot = f / quarter, off = f % quarter;
-      const uint8_t* sp = a.pages + clamp_page(a.page_table[grp * 4 + slot], a.n_pool) * a.L.bytes + a.L.kscale;
-      const float scale = half_bits_to_float(*reinterpret_cast<const uint16_t*>(sp + off * 2));
-      const int b = j0 / 16, q = (j0 % 16) / 4, i = j0 % 4;
-      const uint32_t* kr = reinterpret_cast<const uint32_t*>(page + a.L.kres + h * 768 + (16 * q + t) * 12);
-      const int code = kres_pair_code(kr[0], kr[1], kr[2], 4 * b + i, s);
-      kv[s] = acc + scale * (float)code;
+struct DqTile {
+  float v[kPT][kDqPad];
+};
+
+// row t = lane / 4, columns 32 (lane % 4) .. + 31 of the wave's staging tile
+// to out rows base + t (elements of dtype)
+__device__ __forceinline__ void dq_store_tile(const DqTile& tl, void* out, int64_t row0, int dtype) {
+  const int lane = threadIdx.x & 63, t = lane >> 2, c0 = 32 * (lane & 3);
+  const float* src = &tl.v[t][c0];
+  const int64_t e0 = (row0 + t) * kD + c0;
+  if (dtype == 1) {   // BMX_K2B_F32
+    float4_t* dst = reinterpret_cast<float4_t*>(reinterpret_cast<float*>(out) + e0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) dst[u] = *reinterpret_cast<const float4_t*>(src + 4 * u);
+  } else {
+    uint4* dst = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + e0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint16_t hbits[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint16_t tmp[1];
+        store_elem(tmp, 0, src[8 * u + e], dtype);
+        hbits[e] = tmp[0];
+      }
+      dst[u] = make_uint4(hbits[0] | (uint32_t)hbits[1] << 16, hbits[2] | (uint32_t)hbits[3] << 16,
+                          hbits[4] | (uint32_t)hbits[5] << 16, hbits[6] | (uint32_t)hbits[7] << 16);
     }
-    const int64_t base = ((int64_t)h * a.n_tokens + lp * kPT + t) * kD;
-    float k0 = kv[0], k1 = kv[1];
-    if (a.apply_rope) {
-      const float ang = a.inv_freq[j0] * (float)(lp * kPT + t);   // HF's fp32 angle
+  }
+}
+
+template <int R>
+__global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const DequantKArgs a) {
+  constexpr int KQ = R / 4;
+  typedef _Float16 hvec_t __attribute__((ext_vector_type(KQ)));
+  const int lp = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
+  const int h_raw = blockIdx.y * kDqWaves + wave;
+  const bool active = h_raw < a.h_kv;
+  const int h = active ? h_raw : 0;
+  const int C = kD * a.h_kv, quarter = C / 4;
+  __shared__ float s_cs[2][kPT][64];
+  __shared__ DqTile s_tile[kDqWaves];
+
+  // ---- every load first ----
+  const uint8_t* page = a.pages + clamp_page(a.page_table[lp], a.n_pool) * a.L.bytes;
+  const hvec_t us = *reinterpret_cast<const hvec_t*>(page + a.L.us + lane * (2 * KQ));
+  const uint3 kres = *reinterpret_cast<const uint3*>(page + a.L.kres + h * 768 + lane * 12);
+  const uint2 vcd = *reinterpret_cast<const uint2*>(page + a.L.vcode + h * 512 + lane * 8);
+  const uint2 nrm = *reinterpret_cast<const uint2*>(page + a.L.vnorm + (h * kPT + 4 * q) * 2);
+  uint4 scl[4];   // key-scale pairs (s_j, s_{j+64}), j = 16bb + 4q + i, in the group's pages
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    const int f = h * kD + 2 * (16 * bb + 4 * q);
+    const int slot = f / quarter, off = f - slot * quarter;
+    const uint8_t* sp = a.pages + clamp_page(a.page_table[(lp & ~3) + slot], a.n_pool) * a.L.bytes;
+    scl[bb] = *reinterpret_cast<const uint4*>(sp + a.L.kscale + 2 * off);
+  }
+  hvec_t vh[8];
+#pragma unroll
+  for (int bt = 0; bt < 8; ++bt)
+    vh[bt] = *reinterpret_cast<const hvec_t*>(a.basis + (int64_t)(h * kD + 16 * bt + n) * R + KQ * q);
+
+  // ---- the page's cos/sin: HF's fp32 angle fl(inv_freq_j * pos) ----
+  if (a.apply_rope) {
+#pragma unroll
+    for (int k = 0; k < kPT * 64 / (64 * kDqWaves); ++k) {
+      const int e = tid + 64 * kDqWaves * k, t = e >> 6, j = e & 63;
       float sn, cn;
-      sincosf(ang, &sn, &cn);
+      sincosf(a.inv_freq[j] * (float)(lp * kPT + t), &sn, &cn);
       cn *= a.rope_scaling;
       sn *= a.rope_scaling;
       if (a.apply_rope == 2) {   // the reference's fp16 tables
         cn = half_bits_to_float(float_to_half_bits(cn));
         sn = half_bits_to_float(float_to_half_bits(sn));
       }
-      // x*cos + rotate_half(x)*sin, rounded per operation as torch does
-      k0 = __fmul_rn(kv[0], cn) - __fmul_rn(kv[1], sn);
-      k1 = __fmul_rn(kv[1], cn) + __fmul_rn(kv[0], sn);
+      s_cs[0][t][j] = cn;
+      s_cs[1][t][j] = sn;
     }
-    store_elem(a.k_out, base + j0, k0, a.out_dtype);
-    store_elem(a.k_out, base + j0 + 64, k1, a.out_dtype);
   }
 
-  // values: codebook level per (token, channel), FWHT, signs, norm
-  for (int e = tid; e < kPT * kD; e += 256) {
-    const int t = e / kD, c = e % kD;
-    const int b = c / 16, m = c % 16, q = t / 4, tt = t % 4;
-    const uint32_t* vc = reinterpret_cast<const uint32_t*>(page + a.L.vcode + h * 512 + (16 * q + m) * 8);
-    const uint32_t D = vc[b / 4];
-    const int idx = (D >> (8 * (b % 4) + 2 * tt)) & 3;
-    x[t][c] = a.codebook[idx];
+  // ---- keys ----
+  float4_t kt[8];
+#pragma unroll
+  for (int bt = 0; bt < 8; ++bt) {
+    const float4_t z = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (R == 32)
+      kt[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[bt], us, z, 0, 0, 0);
+    else
+      kt[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh[bt], us, z, 0, 0, 0);
+  }
+  KresMasks km;
+  km.init();
+  half2_t cp[16];
+  kres_pairs(km, kres.x, kres.y, kres.z, cp);
+  __syncthreads();   // s_cs
+  DqTile& tl = s_tile[wave];
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    const uint32_t sv[4] = {scl[bb].x, scl[bb].y, scl[bb].z, scl[bb].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 16 * bb + 4 * q + i;
+      const half2_t s2 = as_h2(sv[i]);
+      // L + code * scale in fp32 (the product is exact)
+      float k0 = kt[bb][i] + (float)cp[4 * bb + i][0] * (float)s2[0];
+      float k1 = kt[bb + 4][i] + (float)cp[4 * bb + i][1] * (float)s2[1];
+      if (a.apply_rope) {
+        const float c = s_cs[0][n][j], sn = s_cs[1][n][j];
+        // x*cos + rotate_half(x)*sin, rounded per operation as torch does
+        const float r0 = __fmul_rn(k0, c) - __fmul_rn(k1, sn);
+        k1 = __fmul_rn(k1, c) + __fmul_rn(k0, sn);
+        k0 = r0;
+      }
+      tl.v[n][j] = k0;
+      tl.v[n][j + 64] = k1;
+    }
   }
   __syncthreads();
-  for (int hb = 1; hb < kD; hb <<= 1) {
-    for (int e = tid; e < kPT * kD / 2; e += 256) {
-      const int t = e / (kD / 2), pidx = e % (kD / 2);
-      const int i0 = (pidx / hb) * 2 * hb + (pidx % hb);
-      const float u = x[t][i0], w = x[t][i0 + hb];
-      x[t][i0] = u + w;
-      x[t][i0 + hb] = u - w;
+  const int64_t row0 = (int64_t)h * a.n_tokens + (int64_t)lp * kPT;
+  if (active) dq_store_tile(tl, a.k_out, row0, a.out_dtype);
+  __syncthreads();   // the staging tile is reused for the values
+
+  // ---- values: y = H128 (codebook level), channel 16b + n, token 4q + tt ----
+  float y[4][8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const uint32_t D = b < 4 ? vcd.x : vcd.y;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) y[tt][b] = a.codebook[(D >> (8 * (b & 3) + 2 * tt)) & 3];
+  }
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+    for (int hb = 1; hb < 8; hb <<= 1)   // H8 over b
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        if (!(b & hb)) {
+          const float u = y[tt][b], w = y[tt][b | hb];
+          y[tt][b] = u + w;
+          y[tt][b | hb] = u - w;
+        }
+#pragma unroll
+    for (int hb = 1; hb < 16; hb <<= 1)   // H16 over n, across the row
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const float o = __shfl_xor(y[tt][b], hb);
+        y[tt][b] = (n & hb) ? o - y[tt][b] : y[tt][b] + o;
+      }
+  }
+  const float nv[4] = {half_bits_to_float(nrm.x & 0xffff), half_bits_to_float(nrm.x >> 16),
+                       half_bits_to_float(nrm.y & 0xffff), half_bits_to_float(nrm.y >> 16)};
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const int c = 16 * b + n;
+    const bool neg = sign_neg(a.v_sign_bits, c);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const float v = y[tt][b] / (float)kD;
+      tl.v[4 * q + tt][c] = (neg ? -v : v) * nv[tt];
     }
-    __syncthreads();
   }
-  for (int e = tid; e < kPT * kD; e += 256) {
-    const int t = e / kD, c = e % kD;
-    const float nrm = half_bits_to_float(*reinterpret_cast<const uint16_t*>(page + a.L.vnorm + (h * kPT + t) * 2));
-    const float v = x[t][c] / (float)kD;
-    store_elem(a.v_out, ((int64_t)h * a.n_tokens + lp * kPT + t) * kD + c, (sign_neg(a.v_sign_bits, c) ? -v : v) * nrm,
-               a.out_dtype);
-  }
+  __syncthreads();
+  if (active) dq_store_tile(tl, a.v_out, row0, a.out_dtype);
 }
 
 }  // namespace bmx
@@ -139,8 +238,11 @@ extern "C" int bmx_k2b_dequant(const bmx_k2b_dequant_args* a, void* stream) {
   for (int j = 0; j < 64; ++j) k.inv_freq[j] = a->inv_freq[j];
   for (int j = 0; j < 4; ++j) { k.codebook[j] = a->codebook[j]; k.v_sign_bits[j] = a->v_sign_bits[j]; }
   k.k_out = a->k_out; k.v_out = a->v_out;
-  hipLaunchKernelGGL(k2b_dequant_kernel, dim3(a->n_tokens / kPT, g.h_kv), dim3(256), 0,
-                     (hipStream_t)stream, k);
+  const dim3 grid(a->n_tokens / kPT, (g.h_kv + kDqWaves - 1) / kDqWaves);
+  if (g.rank == 32)
+    hipLaunchKernelGGL(k2b_dequant_kernel<32>, grid, dim3(64 * kDqWaves), 0, (hipStream_t)stream, k);
+  else
+    hipLaunchKernelGGL(k2b_dequant_kernel<16>, grid, dim3(64 * kDqWaves), 0, (hipStream_t)stream, k);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     bmx_set_error(std::string("bmx_k2b_dequant: launch: ") + hipGetErrorString(e));

@@ -452,9 +452,10 @@ def test_decode_window_only_and_long_window():
 # ------------------------------------------------------------------ dequant kernel
 
 
-def test_dequant_matches_oracle():
+@pytest.mark.parametrize("h_kv,rank", [(8, 16), (8, 32), (3, 32)])
+def test_dequant_matches_oracle(h_kv, rank):
     gen = torch.Generator().manual_seed(11)
-    h_kv, rank, S = 8, 16, 512
+    S = 512
     k_pre, v = synth.k2b_keys(h_kv, S, rank, gen), synth.values(h_kv, S, gen)
     svd = synth.first_page_svd(k_pre, rank)
     consts = k2b.CodecConsts.make(v_seed=0)
