@@ -7,6 +7,24 @@
 
 namespace bmx {
 
+constexpr int kSyncPolls = 1 << 22;   // bound of a wave's wait on another wave's ring slot
+
+// Wait until the workgroup counter *c reaches target (LDS, acquire at
+// workgroup scope); bounded, so a wave can never wait for ever.
+__device__ __forceinline__ void wait_count(uint32_t* c, uint32_t target) {
+  for (int it = 0; it < kSyncPolls; ++it) {
+    if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// One wave's arrival at the workgroup counter *c (release at workgroup scope:
+// the wave's earlier LDS reads and writes are complete).
+__device__ __forceinline__ void count_wave(uint32_t* c) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): every lane's LDS access has completed
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // ---------------------------------------------------------------------------
 // Recent-window scores (any decode kernel whose arguments carry k_tail, ts_b,
 // ts_h, ts_t, tail_cap, win_rescale, ws_win, h_kv, G).  Window tile j (tokens

@@ -67,7 +67,6 @@ constexpr int kCsBuf = kGroup * kCsRow;     // dwords per group table
 constexpr int kPidWindow = 64;              // page ids held per lane-vector
 constexpr int kCsMaxBufs = 8;               // RoPE table buffers at most (17 KB each)
 constexpr int kRingSlots = 3;               // prefix ring: group g in slot g % 3
-constexpr int kSyncPolls = 1 << 22;         // bound of a wave's wait on another wave's slot
 
 
 struct DecodeKArgs {
@@ -99,22 +98,6 @@ struct DecodeKArgs {
   float win_rescale;      // 1 / rope_scaling: window keys carry the RoPE scaling
   float* ws_win;          // [B][h_kv][G][tail_cap] window scores, base 2
 };
-
-// Wait until the workgroup counter *c reaches target (LDS, acquire at
-// workgroup scope); bounded, so a wave can never wait for ever.
-__device__ __forceinline__ void wait_count(uint32_t* c, uint32_t target) {
-  for (int it = 0; it < kSyncPolls; ++it) {
-    if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
-// One wave's arrival at the workgroup counter *c (release at workgroup scope:
-// the wave's earlier LDS reads and writes are complete).
-__device__ __forceinline__ void count_wave(uint32_t* c) {
-  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): every lane's LDS access has completed
-  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
 
 // v_mov_b32_dpp: lanes enabled by BANK (4-lane banks of each 16-lane row) take
 // src from the DPP-selected lane, the others keep old.

@@ -8,7 +8,9 @@
 //                     (4 pages) of the split's balanced share:
 //   * each lane streams its 16-byte key-code and value-code slices of every
 //     page straight into VGPRs, a whole group ahead; the scale sections of the
-//     group's pages are staged cooperatively in a two-slot LDS ring;
+//     group's pages are staged cooperatively two groups ahead in a three-slot
+//     LDS ring that the waves hand on with LDS counters (no barrier per
+//     group), so a wave may run a group ahead of the slowest;
 //   * keys: the lane's 8 channels of a word become 4 fp16 pairs of exact
 //     integer codes with one and-or each (code + 8 in the mantissa of 1024)
 //     and a packed subtract; the G query heads are scored on MFMA against the
@@ -329,7 +331,11 @@ template <int SW, int NGK>
 __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDecodeKArgs a) {
   constexpr int NSLOT = 16 / SW;
   constexpr int NCR = kRGroupPages / NSLOT;
-  __shared__ __attribute__((aligned(16))) uint8_t ring[2][kRGroupPages][kRMaxPrefix];
+  constexpr int kSlots = 3;   // group g's scales in ring slot g % 3
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kSlots][kRGroupPages][kRMaxPrefix];
+  // s_sync[s]: waves that have stored a group's scales into slot s;
+  // s_sync[kSlots + s]: waves done reading a group from slot s (monotonic)
+  __shared__ uint32_t s_sync[2 * kSlots];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15, q = lane >> 4;
@@ -419,6 +425,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
   auto load_vc = [&](int gi, int pp) { return *reinterpret_cast<const uint4*>(page_ptr(gi, pp) + vc_off); };
 
   Pre pre = load_prefix(0);
+  const Pre pre1 = load_prefix(min(1, n_groups - 1));
   uint4 kc[kRGroupPages], vc[kRGroupPages];
 #pragma unroll
   for (int pp = 0; pp < kRGroupPages; ++pp) {
@@ -452,6 +459,8 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
     }
   }
   store_prefix(pre, 0);
+  store_prefix(pre1, 1);
+  if (tid < 2 * kSlots) s_sync[tid] = tid < 2 ? kRWaves : 0;   // slots 0, 1: groups 0, 1 (barrier below)
 
   float4_t acc[8];
 #pragma unroll
@@ -462,12 +471,13 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): group 0 has landed
 
   for (int gi = 0; gi < n_groups; ++gi) {
-    const int gn = min(gi + 1, n_groups - 1);
-    if ((gn + 1) * kRGroupPages - pid_base > kRPidWindow) {
-      pid_base = gi * kRGroupPages;
+    const int gn = min(gi + 1, n_groups - 1);   // group whose codes are fetched during this one
+    const int gp = min(gi + 2, n_groups - 1);   // group whose scales are fetched during this one
+    if ((gp + 1) * kRGroupPages - pid_base > kRPidWindow) {
+      pid_base = gn * kRGroupPages;
       pidv = load_ids(pid_base, n_pages);
     }
-    const Pre pre_n = load_prefix(gn);
+    const Pre pre_n = load_prefix(gp);
     uint4 kc_n[kRGroupPages], vc_n[kRGroupPages];
     if (active) {
 #pragma unroll
@@ -476,6 +486,9 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
         vc_n[pp] = load_vc(gn, pp);
       }
     }
+    // every wave has stored this group's scales (use gi / 3 of slot gi % 3)
+    const int slot = gi % kSlots;
+    wait_count(&s_sync[slot], kRWaves * (gi / kSlots + 1));
     if (active) {
       // ---- keys: scores of the 4 pages.  MFMA bb spans channels 32bb .. +31,
       // inside one scale group: the exact integer codes meet the query, and the
@@ -487,7 +500,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
           // channel-arm keys: the scale varies along the MFMA's K axis, so it
           // goes into the A operand, as an exact fp16 sum hi + lo of code *
           // scale (lo = the rounding residual of hi, from one packed FMA)
-          const uint4* ksp = reinterpret_cast<const uint4*>(&ring[gi & 1][pp][a.L.kscale]) + h * 16 + q;
+          const uint4* ksp = reinterpret_cast<const uint4*>(&ring[slot][pp][a.L.kscale]) + h * 16 + q;
           const uint32_t kw4[4] = {kc[pp].x, kc[pp].y, kc[pp].z, kc[pp].w};
           float4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -511,7 +524,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
           continue;
         } else {
         // scales of the lane's score rows, tokens 4q .. 4q + 3: [4][NGK] fp16
-        const uint16_t* ksp = reinterpret_cast<const uint16_t*>(&ring[gi & 1][pp][a.L.kscale]) +
+        const uint16_t* ksp = reinterpret_cast<const uint16_t*>(&ring[slot][pp][a.L.kscale]) +
                               (h * kPT + 4 * q) * NGK;
         float ksc[4][NGK];
         if constexpr (NGK == 4) {
@@ -607,9 +620,9 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
                                  __builtin_amdgcn_perm(zb.y, za.y, 0x07060302u)};
         const uint32_t va4[4] = {vc[pa].x, vc[pa].y, vc[pa].z, vc[pa].w};
         const uint32_t vb4[4] = {vc[pbb].x, vc[pbb].y, vc[pbb].z, vc[pbb].w};
-        const uint16_t* vsa = reinterpret_cast<const uint16_t*>(&ring[gi & 1][pa][a.L.vscale]) +
+        const uint16_t* vsa = reinterpret_cast<const uint16_t*>(&ring[slot][pa][a.L.vscale]) +
                               (h * 4 + q) * a.L.ngv * 4;
-        const uint16_t* vsb = reinterpret_cast<const uint16_t*>(&ring[gi & 1][pbb][a.L.vscale]) +
+        const uint16_t* vsb = reinterpret_cast<const uint16_t*>(&ring[slot][pbb][a.L.vscale]) +
                               (h * 4 + q) * a.L.ngv * 4;
         union { uint32_t u[4]; half8_t v; } bp;
         int g_cur = -1;
@@ -635,7 +648,14 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
         }
       }
     }
-    if (gi + 1 < n_groups) store_prefix(pre_n, (gi + 1) & 1);
+    // the scales of group gi + 2 go to slot (gi + 2) % 3, last read by group gi - 1
+    count_wave(&s_sync[kSlots + slot]);   // done reading group gi
+    if (gi + 2 < n_groups) {
+      const int slot2 = (gi + 2) % kSlots;
+      if (gi >= 1) wait_count(&s_sync[kSlots + slot2], kRWaves * ((gi - 1) / kSlots + 1));
+      store_prefix(pre_n, slot2);
+      count_wave(&s_sync[slot2]);
+    }
     if (active) {
 #pragma unroll
       for (int pp = 0; pp < kRGroupPages; ++pp) {
@@ -643,7 +663,6 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
         vc[pp] = vc_n[pp];
       }
     }
-    __syncthreads();
   }
   if (active) {
     if constexpr (NSLOT == 4) {
