@@ -245,11 +245,13 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
                                    : a.packed_len + b;
     return (int)*src;
   };
-  const int pid_raw = load_ids_raw(0, (g1 - g0) * kGroupPages);
-  const int len_raw = a.packed_len[b];
+  // the RoPE table constants first: the table production below waits for them
+  // alone (loads complete in issue order), not for the page table
   const float fq = a.inv_freq[fj];
   const float c8 = a.step8_c[fj], s8 = a.step8_s[fj];
   const float stc = a.step_c[fj], sts = a.step_s[fj];
+  const int pid_raw = load_ids_raw(0, (g1 - g0) * kGroupPages);
+  const int len_raw = a.packed_len[b];
   hvec_t vh[8];
   const uint16_t* basis = a.basis + (int64_t)b * a.basis_stride;
 #pragma unroll
@@ -264,12 +266,57 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   }
   const int n_win_tiles = (a.tail_cap + 15) >> 4;   // recent-window score tiles
   const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
+  // dynamic LDS: the cos/sin tables, then the prefix ring
+  const int cs_bufs = a.cs_bufs;
+  uint32_t* cst = reinterpret_cast<uint32_t*>(smem);                            // [cs_bufs][64][kCsRow]
+  int t_begin = g0 * kGroup;
+  // ---- RoPE table: fp16 (cos, sin) of HF's angle fl(fq * pos) for 64
+  // positions per group, row = position, column = frequency, one LDS buffer per
+  // group for the first cs_bufs groups, all written here, while the page table
+  // and then the first pages are in flight.  This thread owns frequency j = tid & 63
+  // at group-local positions wave + 8k, k < 8.  Angles: one exact start (the
+  // angle in revolutions from the exact product, scaled in double; its
+  // fraction; the hardware sin/cos of revolutions), then 8-position and
+  // 64-position rotation steps, each value corrected to the fp32 angle ----
+  auto produce_groups = [&](int g_first, int count, int buf_first) {
+    float cc[8], ss[8];
+    const double rev = (double)fq * (double)(t_begin + g_first * kGroup + wave) * 0.15915494309189535;
+    const float fr = (float)(rev - floor(rev));
+    cc[0] = __builtin_amdgcn_cosf(fr);
+    ss[0] = __builtin_amdgcn_sinf(fr);
+#pragma unroll
+    for (int k = 1; k < 8; ++k) {
+      cc[k] = cc[k - 1] * c8 - ss[k - 1] * s8;
+      ss[k] = ss[k - 1] * c8 + cc[k - 1] * s8;
+    }
+    for (int g = 0; g < count; ++g) {
+      uint32_t* dst = cst + ((buf_first + g) % cs_bufs) * kCsBuf;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int tl = wave + 8 * k;
+        const float tf = (float)(t_begin + (g_first + g) * kGroup + tl);
+        const float ang = fq * tf;
+        const float e = __builtin_fmaf(fq, tf, -ang);  // exact: fq*tf - fl(fq*tf)
+        const half2_t v = {(_Float16)__builtin_fmaf(ss[k], e, cc[k]),
+                           (_Float16)__builtin_fmaf(-cc[k], e, ss[k])};
+        dst[tl * kCsRow + fj] = as_u32(v);
+        const float cn = cc[k] * stc - ss[k] * sts;
+        ss[k] = ss[k] * stc + cc[k] * sts;
+        cc[k] = cn;
+      }
+    }
+  };
+  // the tables of the range for the host bound, made while the page table is
+  // in flight; remade below in the rare case that the sequence is shorter
+  produce_groups(0, min(g1 - g0, cs_bufs), 0);
 
   int pidv = (int)clamp_page(pid_raw, a.n_pool);
   const int len = min(len_raw, a.max_packed_len) & ~(kGroup - 1);
   if (len != len_spec) {
     range(len, g0, g1);
     pidv = (int)clamp_page(load_ids_raw(0, (g1 - g0) * kGroupPages), a.n_pool);
+    t_begin = g0 * kGroup;
+    produce_groups(0, min(g1 - g0, cs_bufs), 0);
   }
   const int n_groups = g1 - g0;
   if (n_groups == 0) {  // nothing packed here: the window tiles and an empty partial
@@ -278,16 +325,12 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     return;
   }
   auto load_ids = [&](int first, int count) { return (int)clamp_page(load_ids_raw(first, count), a.n_pool); };
-  const int t_begin = g0 * kGroup;
   const int C = kD * a.h_kv;
   const int quarter = C / 4;
   const int pb = a.L.bytes;
   const int SHB = a.shared_bytes;
   const int sh_chunks = SHB / 4;       // 16-byte chunks of the 4 pages' prefixes
   const int chunks_pp = SHB / 16;
-  // dynamic LDS: the cos/sin tables, then the prefix ring
-  const int cs_bufs = a.cs_bufs;
-  uint32_t* cst = reinterpret_cast<uint32_t*>(smem);                            // [cs_bufs][64][kCsRow]
   uint8_t* ring = smem + cs_bufs * kCsBuf * 4;                                  // [3][4][SHB]
   const int n_pages = n_groups * kGroupPages;
 
@@ -345,43 +388,6 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   half8_t qf[4], qlo[4];
   query_fragments(qraw, (n < a.G) ? a.qscale_rope : 0.0f, qf, qlo);
 
-  // ---- RoPE table: fp16 (cos, sin) of HF's angle fl(fq * pos) for 64
-  // positions per group, row = position, column = frequency, one LDS buffer per
-  // group for the first cs_bufs groups, all written here, where the wave would
-  // otherwise wait for the first pages.  This thread owns frequency j = tid & 63
-  // at group-local positions wave + 8k, k < 8.  Angles: one exact start (the
-  // angle in revolutions from the exact product, scaled in double; its
-  // fraction; the hardware sin/cos of revolutions), then 8-position and
-  // 64-position rotation steps, each value corrected to the fp32 angle ----
-  auto produce_groups = [&](int g_first, int count, int buf_first) {
-    float cc[8], ss[8];
-    const double rev = (double)fq * (double)(t_begin + g_first * kGroup + wave) * 0.15915494309189535;
-    const float fr = (float)(rev - floor(rev));
-    cc[0] = __builtin_amdgcn_cosf(fr);
-    ss[0] = __builtin_amdgcn_sinf(fr);
-#pragma unroll
-    for (int k = 1; k < 8; ++k) {
-      cc[k] = cc[k - 1] * c8 - ss[k - 1] * s8;
-      ss[k] = ss[k - 1] * c8 + cc[k - 1] * s8;
-    }
-    for (int g = 0; g < count; ++g) {
-      uint32_t* dst = cst + ((buf_first + g) % cs_bufs) * kCsBuf;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int tl = wave + 8 * k;
-        const float tf = (float)(t_begin + (g_first + g) * kGroup + tl);
-        const float ang = fq * tf;
-        const float e = __builtin_fmaf(fq, tf, -ang);  // exact: fq*tf - fl(fq*tf)
-        const half2_t v = {(_Float16)__builtin_fmaf(ss[k], e, cc[k]),
-                           (_Float16)__builtin_fmaf(-cc[k], e, ss[k])};
-        dst[tl * kCsRow + fj] = as_u32(v);
-        const float cn = cc[k] * stc - ss[k] * sts;
-        ss[k] = ss[k] * stc + cc[k] * sts;
-        cc[k] = cn;
-      }
-    }
-  };
-  produce_groups(0, min(n_groups, cs_bufs), 0);
   // recent-window tiles (the first one's rows are in flight)
   if (active && split < n_win_tiles) {
     score_win_tile(a, b, h, split, n, q, kw, qf, qlo);

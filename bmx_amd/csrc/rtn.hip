@@ -24,7 +24,7 @@
 //     the value scales multiply P in the B operand (one B per channel group);
 //   * the window's 16-token score tiles and the merge are the shared ones
 //     (decode_shared.h); the partials are plain channel sums.
-// rtn_dequant_kernel  pages -> dense fp32 keys and values (prefill)
+// rtn_dequant_kernel  pages -> dense keys and values in fp32, fp16 or bf16 (prefill)
 //
 // Reference semantics: cache/triton_dequant_attention.py:580-728 (kernel),
 // 731-832 (launcher), 1390-1451 (stacks: fp16 scales), 504-575 / 409-461 /
