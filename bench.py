@@ -65,13 +65,14 @@ def parse():
                     help="skip timing the dense fp16 decode at the same context")
     ap.add_argument("--prefill-ctx", type=int, default=8192)
     ap.add_argument("--prefill-chunk", type=int, default=512)
-    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch"], default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
                          "BASELINE config 5, Qwen3-8B geometry, rank 16, an 8192-token prefill "
                          "then --stream-steps steps of one-token append + decode over 36 layers; "
                          "rtn: BASELINE config 1, RTN 4-bit per-channel keys / per-token values, "
                          "ctx --rtn-ctx, --rtn-layers layers; prefill: the second block of a cached "
-                         "two-block prefill, --prefill-chunk queries over --prefill-ctx + chunk keys")
+                         "two-block prefill, --prefill-chunk queries over --prefill-ctx + chunk keys; "
+                         "batch: BASELINE config 4, 16 ragged sequences of 4k-16k")
     ap.add_argument("--rtn-ctx", type=int, default=4096)
     ap.add_argument("--rtn-layers", type=int, default=1)
     ap.add_argument("--stream-steps", type=int, default=512)
@@ -421,6 +422,85 @@ def run_rtn(args, torch, dev) -> dict:
     return res
 
 
+BATCH_METRIC = "decode-attn µs/step, k2b rank 32, batch 16 ragged 4k-16k ctx, Llama-3.1-8B geometry, 1 MI355X"
+
+
+def run_batch(args, torch, dev) -> dict:
+    """batched decode, 16 sequences with contexts drawn
+    uniformly from 4096..16384 (seeded), k2b rank 32, Llama-3.1-8B geometry
+    (32 layers, 32q/8kv heads, d 128), each sequence its own frozen key basis
+    and a 128-token fp16 window, 16-token pages shuffled over the pool.  A
+    step is one decode call per layer for the whole batch (two kernels: the
+    split kernel over 16 workgroups per sequence, the merge)."""
+    from bmx_amd import k2b, synth
+
+    B, W = 16, 128
+    gen_h = torch.Generator().manual_seed(44)
+    ctxs = [int(x) for x in torch.randint(4096, 16385, (B,), generator=gen_h)]
+    packed = [((c - W) // 128) * 128 for c in ctxs]
+    tails = [c - p for c, p in zip(ctxs, packed)]
+    cap = max(tails)
+    consts = k2b.CodecConsts.make()
+    gen = torch.Generator(device=dev).manual_seed(45)
+    pool = synth.PagePool(sum(packed) // 16 * args.layers, H_KV, args.rank, dev,
+                          gen=torch.Generator().manual_seed(46))
+    ws = k2b.DecodeWorkspace()
+    plans = []
+    for li in range(args.layers):
+        seqs = []
+        k_tail = torch.zeros(B, H_KV, cap, D, dtype=torch.float16, device=dev)
+        v_tail = torch.zeros_like(k_tail)
+        for i in range(B):
+            k_pre = synth.k2b_keys(H_KV, ctxs[i], args.rank, gen)
+            v = synth.values(H_KV, ctxs[i], gen)
+            seqs.append(synth.encode_sequence(pool, k_pre[:, :packed[i]], v[:, :packed[i]], args.rank, consts))
+            k_tail[i, :, :tails[i]] = synth.rope_keys(k_pre[:, packed[i]:], packed[i], consts)
+            v_tail[i, :, :tails[i]] = v[:, packed[i]:]
+            del k_pre, v
+        basis = torch.stack([sq.basis16 for sq in seqs])
+        q = torch.randn(B, H_KV, G, D, generator=gen, device=dev)
+        pt = synth.page_table(seqs, device=dev)
+        lens = torch.tensor(packed, dtype=torch.int32, device=dev)
+        tl = torch.tensor(tails, dtype=torch.int32, device=dev)
+        plans.append(k2b.DecodePlan(q, pool.pages, pt, lens, max(packed), basis, consts, D ** -0.5,
+                                    rank=args.rank, k_tail=k_tail, v_tail=v_tail, tail_len=tl, tail_cap=cap,
+                                    workspace=ws))
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        for pl in plans:
+            pl.run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()   # no sleep kernel ahead: the host enqueues faster than a call runs
+    for _ in range(args.steps):
+        for pl in plans:
+            pl.run()
+    e1.record()
+    torch.cuda.synchronize()
+    step_us = e0.elapsed_time(e1) * 1e3 / args.steps
+    call_us = step_us / args.layers
+    C = H_KV * D
+    page_bytes = k2b.page_bytes(H_KV, args.rank)
+    bytes_call = (sum(packed) * page_bytes // 16 + B * C * args.rank * 2 + sum(tails) * C * 2 * 2
+                  + 2 * B * H_KV * G * D * 4)
+    achieved = bytes_call / (call_us * 1e-6) / 1e9
+    return {
+        "metric": BATCH_METRIC, "value": round(step_us, 2), "unit": "us/step", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_us / 1e3, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": (f"BASELINE config 4: batch {B}, ctx uniform 4096..16384 (seeded: mean "
+                                f"{sum(ctxs) / B:.0f}), k2b rank {args.rank}, {args.layers} layers, 32q/8kv heads, "
+                                f"d 128, 16-token pages shuffled, per-sequence basis, 128-token fp16 windows"),
+                   "batch": B, "ctx": ctxs, "layers": args.layers, "rank": args.rank},
+        "per_layer_us": round(call_us, 3),
+        "tokens_per_s": round(B / (step_us * 1e-6), 1),
+        "roofline": {"bound": "hbm", "kernel": "k2b decode call, batch 16 (k2b_decode_split_kernel + combine_kernel<true>)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": bytes_call,
+                     "avg_launch_us": round(call_us, 3)},
+    }
+
+
 PREFILL_METRIC = ("prefill-attn µs/layer-call (second block of a cached two-block prefill), k2b rank 32, "
                   "Llama-3.1-8B geometry, 1 MI355X")
 MFMA_FP16_PEAK_TFLOPS = 2500.0
@@ -536,6 +616,9 @@ def main():
         return
     if args.workload == "prefill":
         print(json.dumps(run_prefill(args, torch, dev)), flush=True)
+        return
+    if args.workload == "batch":
+        print(json.dumps(run_batch(args, torch, dev)), flush=True)
         return
     if args.copy_calib_mib > 0:
         n = args.copy_calib_mib << 20

@@ -26,6 +26,34 @@ __device__ __forceinline__ void count_wave(uint32_t* c) {
 }
 
 // ---------------------------------------------------------------------------
+// Balanced split of a ragged batch.  Sequence b of n_seq (at most 64) gets
+// 1 + floor((n_wg - n_seq) * groups_b / total) of the n_wg split workgroups,
+// groups_b = its committed 64-token groups (packed_len clamped to max_len),
+// and its workgroups follow those of sequences 0 .. b - 1.  Every lane of a
+// wave computes the same shares; lane i returns sequence i's share, first
+// workgroup and length (lanes >= n_seq: share 0).
+// ---------------------------------------------------------------------------
+constexpr int kMaxBalancedBatch = 64;
+
+__device__ __forceinline__ void batch_shares(const int32_t* packed_len, int max_len, int n_seq, int n_wg,
+                                             int& share, int& first, int& len) {
+  const int lane = threadIdx.x & 63;
+  len = lane < n_seq ? min(max(packed_len[lane], 0), max_len) & ~63 : 0;
+  const int groups = len >> 6;
+  int total = groups;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) total += __shfl_xor(total, o);
+  share = lane < n_seq ? 1 + (int)(((int64_t)(n_wg - n_seq) * groups) / max(total, 1)) : 0;
+  int incl = share;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  first = incl - share;
+}
+
+// ---------------------------------------------------------------------------
 // Recent-window scores (any decode kernel whose arguments carry k_tail, ts_b,
 // ts_h, ts_t, tail_cap, win_rescale, ws_win, h_kv, G).  Window tile j (tokens
 // 16j .. 16j + 15 of the fp16 post-RoPE window) belongs to workgroup j mod
@@ -110,7 +138,10 @@ constexpr int kCmbSplits = 16;              // splits per lane per pass
 constexpr int kCmbTokens = 8;               // window tokens per lane per pass
 
 struct CombineKArgs {
-  int h_kv, G, max_splits, tail_cap;
+  int h_kv, G, max_splits, tail_cap;   // max_splits: partial slots per row
+  int balanced, n_wg;                  // balanced: sequence b has its batch_shares() share of n_wg
+  const int32_t* packed_len;
+  int max_packed_len;
   float* out;
   const float* ws_acc;
   const float* ws_ml;
@@ -155,10 +186,10 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   const int ch = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
   const int h = r / a.G;
   const int lane = threadIdx.x, p = lane & 15, c4 = lane >> 4;
-  const int S = a.max_splits;
+  const int S_slots = a.max_splits;
   const int64_t row = (int64_t)b * a.h_kv * a.G + r;   // (b, h, g) row
-  const float* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S * kChunk + 4 * c4;
-  const float* mlb = a.ws_ml + row * S * 2;
+  const float* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S_slots * kChunk + 4 * c4;
+  const float* mlb = a.ws_ml + row * S_slots * 2;
   const float* swb = a.ws_win + row * a.tail_cap;
   const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch + 4 * c4;
   typedef float f2_t __attribute__((ext_vector_type(2)));
@@ -167,6 +198,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   float4_t pv[kCmbSplits];
   float ws[kCmbTokens];
   uint2 wv[kCmbTokens];
+  int S = S_slots;   // the sequence's splits
   auto load_splits = [&](int j0) {
 #pragma unroll
     for (int u = 0; u < kCmbSplits; ++u) {
@@ -183,9 +215,16 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
       wv[u] = *reinterpret_cast<const uint2*>(vb + (int64_t)t * a.ts_t);
     }
   };
-  // first pass of both, bounded by the host's S and tail_cap (no wait on tail_len)
-  load_splits(0);
+  // first pass of both: the window rows bounded by the host's tail_cap (no
+  // wait on tail_len), the partials by the sequence's split count (a ragged
+  // batch reads it from the lengths, after the window loads are in flight)
   if (a.tail_cap > 0) load_tokens(0, a.tail_cap);
+  if (a.balanced) {
+    int share, first, len;
+    batch_shares(a.packed_len, a.max_packed_len, gridDim.z, a.n_wg, share, first, len);
+    S = __shfl(share, b);
+  }
+  load_splits(0);
   const int T = min(max(a.tail_len[b], 0), a.tail_cap);
 
   // ---- packed partials: online over passes of 16 splits per lane ----
@@ -204,10 +243,11 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
       lp *= sc;
 #pragma unroll
       for (int u = 0; u < kCmbSplits; ++u) {
+        // lanes past the sequence's splits re-read its last: select, not weight by 0
         const bool ok = j0 + p + 16 * u < S && ml[u][0] != -INFINITY;
         const float w = ok ? __builtin_amdgcn_exp2f(ml[u][0] - mnew) : 0.f;
-        xp += w * pv[u];
-        lp = __builtin_fmaf(w, ml[u][1], lp);
+        xp += ok ? w * pv[u] : float4_t{0.f, 0.f, 0.f, 0.f};
+        lp = ok ? __builtin_fmaf(w, ml[u][1], lp) : lp;
       }
       mp = mnew;
     }

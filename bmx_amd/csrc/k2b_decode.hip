@@ -97,6 +97,9 @@ struct DecodeKArgs {
   int tail_cap;
   float win_rescale;      // 1 / rope_scaling: window keys carry the RoPE scaling
   float* ws_win;          // [B][h_kv][G][tail_cap] window scores, base 2
+  int balanced;           // a ragged batch: workgroup w of the flat grid serves the
+                          // sequence batch_shares() gives it (max_splits = the slots per row)
+  int n_seq;
 };
 
 // v_mov_b32_dpp: lanes enabled by BANK (4-lane banks of each 16-lane row) take
@@ -170,7 +173,7 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
 // (max -inf) that the merge ignores.  Out of line, with the kernel argument
 // block passed by its kernarg-segment address: a second inlined copy of the
 // window code would disturb the group loop's register allocation.
-__device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, int split, int h, int n,
+__device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, int split, int S, int h, int n,
                                                  int q) {
   const int n_tiles = (a.tail_cap + 15) >> 4;
   if (split < n_tiles) {
@@ -182,7 +185,7 @@ __device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, in
     half8_t qh[4], ql[4];
     query_fragments(qraw, n < a.G ? a.qscale_rope : 0.0f, qh, ql);
     const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
-    for (int j = split; j < n_tiles; j += a.max_splits) {
+    for (int j = split; j < n_tiles; j += S) {
       uint2 kw[8];
       load_win_tile(a, tail_base, j, n, q, kw);
       score_win_tile(a, b, h, j, n, q, kw, qh, ql);
@@ -216,16 +219,29 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15;   // token within page (K side) / score column (softmax side)
   const int q = lane >> 4;   // quarter
-  const int split = blockIdx.x, b = blockIdx.y;
   const bool active = wave < a.h_kv;
   const int h = active ? wave : 0;
+  // this workgroup's sequence b, split and the sequence's split count S: the
+  // grid's (x, y), or, for a ragged batch, the workgroup's place in the
+  // length-proportional shares of the flat grid (read from the lengths)
+  int split = blockIdx.x, b = blockIdx.y, S = a.max_splits;
+  int len_known = -1;
+  if (a.balanced) {
+    int share, first, len_l;
+    batch_shares(a.packed_len, a.max_packed_len, a.n_seq, gridDim.x, share, first, len_l);
+    const uint64_t mine = __ballot(share > 0 && (int)blockIdx.x >= first && (int)blockIdx.x < first + share);
+    if (mine == 0) return;   // a workgroup past every share: nothing to do
+    b = __builtin_ctzll(mine);
+    split = blockIdx.x - __shfl(first, b);
+    S = __shfl(share, b);
+    len_known = __shfl(len_l, b);
+  }
 
   // ---- every load that depends only on the arguments is issued first, the
   // page-table read first of all, and nothing is used before the first group's
   // page loads are in flight (a wait on one load waits on all earlier ones) ----
   const int fj = tid & 63;   // RoPE frequency this thread produces
-  const int S = a.max_splits;
-  const int len_spec = a.max_packed_len & ~(kGroup - 1);
+  const int len_spec = len_known >= 0 ? len_known : a.max_packed_len & ~(kGroup - 1);
   auto range = [&](int L, int& r0, int& r1) {
     const int NG = L / kGroup;
     r0 = (int)(((int64_t)split * NG) / S);
@@ -321,7 +337,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const int n_groups = g1 - g0;
   if (n_groups == 0) {  // nothing packed here: the window tiles and an empty partial
     if (active)
-      empty_range_partial(*(const DecodeKArgs*)__builtin_amdgcn_kernarg_segment_ptr(), b, split, h, n, q);
+      empty_range_partial(*(const DecodeKArgs*)__builtin_amdgcn_kernarg_segment_ptr(), b, split, S, h, n, q);
     return;
   }
   auto load_ids = [&](int first, int count) { return (int)clamp_page(load_ids_raw(first, count), a.n_pool); };
@@ -638,7 +654,18 @@ static int device_cu_count() {
 // 8-wave workgroup per CU), or as many as split_tokens asks for; never more
 // than the sequence has 64-token groups, except that the recent window's
 // 16-token score tiles get a workgroup each, up to one per CU.
+// A ragged batch (2..64 sequences, no split_tokens, two CUs or more per
+// sequence) runs balanced: one flat wave of workgroups over the CUs, each
+// sequence a share proportional to its length (batch_shares); the partial
+// slots per row are then the largest share, CUs - batch + 1.
+static bool balanced_batch(const bmx_k2b_decode_args* a) {
+  return a->batch > 1 && a->batch <= kMaxBalancedBatch && a->split_tokens == 0 &&
+         device_cu_count() >= 2 * a->batch;
+}
+
+// Partial slots per row (the split count of a sequence, at most).
 static int choose_splits(const bmx_k2b_decode_args* a) {
+  if (balanced_batch(a)) return device_cu_count() - a->batch + 1;
   const int units = (a->max_packed_len + kGroup - 1) / kGroup;
   const int per_seq = std::max(1, device_cu_count() / a->batch);
   int S;
@@ -879,11 +906,17 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
                                    std::to_string(lm.err) + ")");
   for (int j = 0; j < 4; ++j) k.level_hi[j] = lm.hi[j];
   k.level_mu = lm.mu;
-  // RoPE tables for every group a workgroup owns, up to kCsMaxBufs
-  const int max_groups = ((a->max_packed_len / kGroup) + max_splits - 1) / max_splits;
+  // RoPE tables for every group a workgroup owns, up to kCsMaxBufs (balanced:
+  // the longest sequence gets at least 1 + (CUs - B) / B workgroups)
+  const bool balanced = balanced_batch(a);
+  const int n_wg = balanced ? device_cu_count() : max_splits * a->batch;
+  const int least_share = balanced ? 1 + (n_wg - a->batch) / a->batch : max_splits;
+  const int max_groups = ((a->max_packed_len / kGroup) + least_share - 1) / least_share;
   k.cs_bufs = std::max(1, std::min(max_groups, kCsMaxBufs));
+  k.balanced = balanced ? 1 : 0;
+  k.n_seq = a->batch;
   const size_t smem = (size_t)k.cs_bufs * kCsBuf * 4 + (size_t)kRingSlots * kGroupPages * k.shared_bytes;
-  dim3 grid(max_splits, a->batch);
+  const dim3 grid = balanced ? dim3(n_wg, 1) : dim3(max_splits, a->batch);
   hipError_t e = g.rank == 32 ? launch_split<32>(k, grid, smem, st)
                               : launch_split<16>(k, grid, smem, st);
   if (e != hipSuccess)
@@ -902,6 +935,8 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   c.tail_len = a->tail_len;
   for (int j = 0; j < 4; ++j) c.v_sign_bits[j] = a->v_sign_bits[j];
   c.packed_scale = (float)(1.0 / (kD * (double)lm.kappa));
+  c.balanced = k.balanced; c.n_wg = n_wg;
+  c.packed_len = a->packed_len; c.max_packed_len = a->max_packed_len;
   hipLaunchKernelGGL(combine_kernel<true>, dim3(kChunks, g.h_kv * g.n_q_groups, a->batch), dim3(kCmbThreads),
                      0, st, c);
   e = hipGetLastError();

@@ -290,6 +290,69 @@ def test_ragged_batch_shuffled_pages():
         _close(out[i], ref.view(h_kv, G, 128), f"ragged seq {i} len {lens[i]}")
 
 
+def test_balanced_batch_matches_static_split():
+    """A ragged batch runs balanced (each sequence a share of the CUs
+    proportional to its length, read from the device lengths); the same batch
+    with a static split (split_tokens) must give the same output, and both the
+    oracle's.  One sequence has no packed tokens (its one workgroup scores all
+    of its window tiles) and the windows are ragged."""
+    gen = torch.Generator().manual_seed(17)
+    h_kv, rank, G = 8, 32, 4
+    lens, tails = [0, 512, 4096, 1024, 2048], [64, 128, 200, 17, 255]
+    consts = k2b.CodecConsts.make(v_seed=0)
+    inv = torch.tensor(consts.inv_freq)
+    pool = synth.PagePool(sum(lens) // 16 + 8, h_kv, rank, DEV, gen=gen)
+    seqs, caches, kts, vts = [], [], [], []
+    for S, T in zip(lens, tails):
+        k_pre = synth.k2b_keys(h_kv, S + T, rank, gen)
+        v = synth.values(h_kv, S + T, gen)
+        if S:
+            svd = synth.first_page_svd(k_pre, rank)
+            seqs.append(synth.encode_sequence(pool, k_pre[:, :S].to(DEV), v[:, :S].to(DEV), rank, consts,
+                                              svd=svd))
+            caches.append(_oracle_cache(k_pre[:, :S], v[:, :S], rank, svd))
+        else:
+            seqs.append(None)
+            caches.append(None)
+        cos, sin = A.rope_cos_sin(inv, torch.arange(S, S + T))
+        kts.append(A.apply_rope(k_pre[:, S:].float(), cos, sin).half())
+        vts.append(v[:, S:])
+    basis0 = next(s_.basis16 for s_ in seqs if s_ is not None)
+    seqs = [s_ if s_ is not None else synth.PackedSeq(page_ids=[], packed_len=0, basis16=basis0) for s_ in seqs]
+    B, cap = len(lens), max(tails)
+    k_tail = torch.zeros(B, h_kv, cap, 128, dtype=torch.float16)
+    v_tail = torch.zeros_like(k_tail)
+    for i in range(B):
+        k_tail[i, :, :tails[i]] = kts[i]
+        v_tail[i, :, :tails[i]] = vts[i]
+    q = torch.randn(B, h_kv, G, 128, generator=gen)
+
+    def run(split_tokens):
+        out = k2b.decode(q.to(DEV), pool.pages, synth.page_table(seqs, device=DEV),
+                         torch.tensor(lens, dtype=torch.int32, device=DEV), max(lens),
+                         torch.stack([s_.basis16 for s_ in seqs]), consts, 128 ** -0.5, rank=rank,
+                         k_tail=k_tail.to(DEV), v_tail=v_tail.to(DEV),
+                         tail_len=torch.tensor(tails, dtype=torch.int32, device=DEV), tail_cap=cap,
+                         split_tokens=split_tokens)
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    bal, sta = run(0), run(512)
+    d = (bal - sta).abs().max().item()
+    print(f"balanced vs static split: max_abs {d:.3e}", flush=True)
+    # P*norm enters the P.V product rounded to fp16 against each split's running
+    # max, so any other partition rounds differently (as across split counts)
+    assert d < 1e-4
+    for i in range(B):
+        if caches[i] is None:
+            ref = A.naive_dense_attention(q[i].reshape(32, 1, 128), kts[i].float(), vts[i].float(), G,
+                                          128 ** -0.5)
+        else:
+            ref = A.k2b_naive_attention(q[i].reshape(32, 1, 128), caches[i], inv, kts[i], vts[i], G,
+                                        128 ** -0.5)
+        _close(bal[i], ref.view(h_kv, G, 128), f"balanced seq {i} len {lens[i]}")
+
+
 def test_64_decode_steps_zero_argmax_flips():
     """Config 3: k2b rank 32, Llama-3.1-8B geometry, 131,072-token context =
     130,944 committed tokens in 16-token pages + a 128-token fp16 window, split
