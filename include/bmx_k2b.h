@@ -119,7 +119,10 @@ typedef struct {
   int64_t tail_stride_t;
   const int32_t* tail_len;    /* device [batch] recent-window length (clamped to tail_cap) */
   int32_t tail_cap;           /* host upper bound of tail_len, 0..4096 */
-  int32_t split_tokens;       /* 0 = one workgroup per CU, split over the batch (default);
+  int32_t split_tokens;       /* 0 = one workgroup per CU, split over the batch (default):
+                                 a batch of 2..64 sequences shares them in proportion
+                                 to the sequences' device lengths (the workspace then
+                                 holds CU count - batch + 1 partial slots per row);
                                  > 0 (multiple of 64) = about max_packed_len / split_tokens
                                  workgroups per sequence.  Packed tokens are dealt in
                                  64-token groups, balanced over the workgroups; the
