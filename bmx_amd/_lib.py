@@ -1,5 +1,5 @@
-"""ctypes binding of libbmx_k2b.so (the C-ABI declared in include/bmx_k2b.h and
-include/bmx_rtn.h).
+"""ctypes binding of libbmx_k2b.so (the C-ABI declared in include/bmx_k2b.h,
+include/bmx_rtn.h and include/bmx_spectral.h).
 
 The library is the product path: there is no fallback.  ``lib()`` raises if the
 shared object was not built (python -m bmx_amd.build) and every wrapper raises
@@ -158,6 +158,57 @@ class RtnDequantArgs(ct.Structure):
     ]
 
 
+class SpectralLayout(ct.Structure):
+    _fields_ = [("h_kv", ct.c_int32), ("c_pad", ct.c_int32), ("k_page_bytes", ct.c_int32),
+                ("slice_tab", ct.c_void_p)]
+
+
+class SpectralAppendArgs(ct.Structure):
+    _fields_ = [
+        ("L", SpectralLayout),
+        ("n_groups", ct.c_int32),
+        ("k_pre", ct.c_void_p),
+        ("k_dtype", ct.c_int32),
+        ("k_sh", ct.c_int64),
+        ("k_st", ct.c_int64),
+        ("v", ct.c_void_p),
+        ("v_dtype", ct.c_int32),
+        ("v_sh", ct.c_int64),
+        ("v_st", ct.c_int64),
+        ("enc_perm", ct.c_void_p),
+        ("k_pages", ct.c_void_p),
+        ("k_page_ids", ct.c_void_p),
+        ("n_k_pool", ct.c_int32),
+        ("v_pages", ct.c_void_p),
+        ("v_page_ids", ct.c_void_p),
+        ("n_v_pool", ct.c_int32),
+        ("v_codebook", ct.c_float * 4),
+        ("v_sign_bits", ct.c_uint32 * 4),
+    ]
+
+
+class SpectralDequantArgs(ct.Structure):
+    _fields_ = [
+        ("L", SpectralLayout),
+        ("n_tokens", ct.c_int32),
+        ("k_pages", ct.c_void_p),
+        ("k_page_table", ct.c_void_p),
+        ("n_k_pool", ct.c_int32),
+        ("v_pages", ct.c_void_p),
+        ("v_page_table", ct.c_void_p),
+        ("n_v_pool", ct.c_int32),
+        ("dec_perm", ct.c_void_p),
+        ("apply_rope", ct.c_int32),
+        ("rope_scaling", ct.c_float),
+        ("inv_freq", ct.c_float * 64),
+        ("v_codebook", ct.c_float * 4),
+        ("v_sign_bits", ct.c_uint32 * 4),
+        ("out_dtype", ct.c_int32),
+        ("k_out", ct.c_void_p),
+        ("v_out", ct.c_void_p),
+    ]
+
+
 EXPORTS = {
     "bmx_last_error": (ct.c_char_p, []),
     "bmx_k2b_page_bytes": (ct.c_size_t, [ct.POINTER(Geom)]),
@@ -172,6 +223,9 @@ EXPORTS = {
     "bmx_rtn_decode_workspace_bytes": (ct.c_size_t, [ct.POINTER(RtnDecodeArgs)]),
     "bmx_rtn_decode": (ct.c_int, [ct.POINTER(RtnDecodeArgs), ct.c_void_p]),
     "bmx_rtn_dequant": (ct.c_int, [ct.POINTER(RtnDequantArgs), ct.c_void_p]),
+    "bmx_spectral_v_page_bytes": (ct.c_int64, [ct.c_int32]),
+    "bmx_spectral_append": (ct.c_int32, [ct.POINTER(SpectralAppendArgs), ct.c_void_p]),
+    "bmx_spectral_dequant": (ct.c_int32, [ct.POINTER(SpectralDequantArgs), ct.c_void_p]),
 }
 
 _LIB = None

@@ -1,4 +1,4 @@
-"""Build libbmx_k2b.so (gfx950: the k2b and RTN paths) in-tree with hipcc.
+"""Build libbmx_k2b.so (gfx950: the k2b, RTN and spectral paths) in-tree with hipcc.
 
     python -m bmx_amd.build
 
@@ -35,6 +35,7 @@ SOURCES = {
     "k2b_append.hip": ["-ffp-contract=off"],
     "k2b_dequant.hip": ["-ffp-contract=off"],
     "rtn.hip": ["-ffp-contract=off"],
+    "spectral.hip": ["-ffp-contract=off"],
 }
 
 

@@ -16,23 +16,6 @@
 
 namespace bmx {
 
-struct AppendKArgs {
-  int h_kv, R, n_codec_pages, n_pool;
-  const uint16_t* k_pre;
-  int64_t ksh, kst;
-  const void* v;
-  int64_t vsh, vst;
-  int v_dtype;         // BMX_K2B_F16 / F32 / BF16
-  const float* basis32;
-  const uint16_t* basis16;
-  const float* us_first;
-  uint8_t* pages;
-  const int32_t* page_ids;
-  PageLayout L;
-  float codebook[4];
-  uint32_t v_sign_bits[4];
-};
-
 // grid (n_codec_pages * 8), block 256 = 4 waves, one 16-token page slot each.
 // Us[t][r] = sum_c M[t][c] basis32[c][r] in fp32 (the reference's M @ V).  The
 // page's 16 key rows are staged in LDS (rows padded by one bank); wave w sums
@@ -249,6 +232,13 @@ __global__ __launch_bounds__(256) void k2b_v_kernel(const AppendKArgs a) {
     }
     *reinterpret_cast<uint32_t*>(page + a.L.vcode + h * 512 + lane * 8 + w * 4) = dword;
   }
+}
+
+// The value kernel alone, for pages whose layout has value sections only
+// (the spectral key path keeps its keys in pages of its own).
+hipError_t launch_k2b_values(const AppendKArgs& a, int n_pages16, int h_kv, hipStream_t st) {
+  hipLaunchKernelGGL(k2b_v_kernel, dim3(n_pages16, h_kv), dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 }  // namespace bmx

@@ -147,6 +147,107 @@ __device__ __forceinline__ int kres_pair_code(uint32_t w0, uint32_t w1, uint32_t
   return (int)v - 4;
 }
 
+constexpr int kDqPad = kD + 4;   // staging row stride (floats)
+
+struct DqTile {
+  float v[kPT][kDqPad];
+};
+
+// row t = lane / 4, columns 32 (lane % 4) .. + 31 of the wave's staging tile
+// to out rows base + t (elements of dtype)
+__device__ __forceinline__ void dq_store_tile(const DqTile& tl, void* out, int64_t row0, int dtype) {
+  const int lane = threadIdx.x & 63, t = lane >> 2, c0 = 32 * (lane & 3);
+  const float* src = &tl.v[t][c0];
+  const int64_t e0 = (row0 + t) * kD + c0;
+  if (dtype == 1) {   // BMX_K2B_F32
+    float4_t* dst = reinterpret_cast<float4_t*>(reinterpret_cast<float*>(out) + e0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) dst[u] = *reinterpret_cast<const float4_t*>(src + 4 * u);
+  } else {
+    uint4* dst = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + e0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint16_t hbits[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint16_t tmp[1];
+        store_elem(tmp, 0, src[8 * u + e], dtype);
+        hbits[e] = tmp[0];
+      }
+      dst[u] = make_uint4(hbits[0] | (uint32_t)hbits[1] << 16, hbits[2] | (uint32_t)hbits[3] << 16,
+                          hbits[4] | (uint32_t)hbits[5] << 16, hbits[6] | (uint32_t)hbits[7] << 16);
+    }
+  }
+}
+
+// Arguments of the k2b write kernels (k2b_append.hip).
+struct AppendKArgs {
+  int h_kv, R, n_codec_pages, n_pool;
+  const uint16_t* k_pre;
+  int64_t ksh, kst;
+  const void* v;
+  int64_t vsh, vst;
+  int v_dtype;         // BMX_K2B_F16 / F32 / BF16
+  const float* basis32;
+  const uint16_t* basis16;
+  const float* us_first;
+  uint8_t* pages;
+  const int32_t* page_ids;
+  PageLayout L;
+  float codebook[4];
+  uint32_t v_sign_bits[4];
+};
+
+// k2b_v_kernel over n_pages16 16-token pages of h_kv heads: norms and codes
+// into the VNORM and VCODE sections of a.L (k2b_append.hip).
+hipError_t launch_k2b_values(const AppendKArgs& a, int n_pages16, int h_kv, hipStream_t st);
+
+// Values of one 16-token page of one head into the wave's staging tile: the
+// lane's code bytes (channel 16b + n, tokens 4q .. 4q + 3) give codebook
+// levels, H8 over b in registers and H16 over n across the row's lanes make
+// the 128-point Hadamard, then 1/128, the signs and the token's norm.
+__device__ __forceinline__ void dq_value_tile(uint2 vcd, uint2 nrm, const float codebook[4],
+                                              const uint32_t sign_bits[4], int n, int q, DqTile& tl) {
+  float y[4][8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const uint32_t D = b < 4 ? vcd.x : vcd.y;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) y[tt][b] = codebook[(D >> (8 * (b & 3) + 2 * tt)) & 3];
+  }
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+    for (int hb = 1; hb < 8; hb <<= 1)   // H8 over b
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        if (!(b & hb)) {
+          const float u = y[tt][b], w = y[tt][b | hb];
+          y[tt][b] = u + w;
+          y[tt][b | hb] = u - w;
+        }
+#pragma unroll
+    for (int hb = 1; hb < 16; hb <<= 1)   // H16 over n, across the row
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const float o = __shfl_xor(y[tt][b], hb);
+        y[tt][b] = (n & hb) ? o - y[tt][b] : y[tt][b] + o;
+      }
+  }
+  const float nv[4] = {half_bits_to_float(nrm.x & 0xffff), half_bits_to_float(nrm.x >> 16),
+                       half_bits_to_float(nrm.y & 0xffff), half_bits_to_float(nrm.y >> 16)};
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const int c = 16 * b + n;
+    const bool neg = sign_neg(sign_bits, c);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const float v = y[tt][b] / (float)kD;
+      tl.v[4 * q + tt][c] = (neg ? -v : v) * nv[tt];
+    }
+  }
+}
+
 }  // namespace bmx
 
 // Error channel shared by every C-ABI entry point (defined in k2b_api.cpp).

@@ -33,38 +33,6 @@ struct DequantKArgs {
 // each tile goes through a per-wave LDS staging tile so that the dense rows
 // are written with 16-byte coalesced stores, rounded once to the output type.
 constexpr int kDqWaves = 4;
-constexpr int kDqPad = kD + 4;   // staging row stride (floats)
-
-struct DqTile {
-  float v[kPT][kDqPad];
-};
-
-// row t = lane / 4, columns 32 (lane % 4) .. + 31 of the wave's staging tile
-// to out rows base + t (elements of dtype)
-__device__ __forceinline__ void dq_store_tile(const DqTile& tl, void* out, int64_t row0, int dtype) {
-  const int lane = threadIdx.x & 63, t = lane >> 2, c0 = 32 * (lane & 3);
-  const float* src = &tl.v[t][c0];
-  const int64_t e0 = (row0 + t) * kD + c0;
-  if (dtype == 1) {   // BMX_K2B_F32
-    float4_t* dst = reinterpret_cast<float4_t*>(reinterpret_cast<float*>(out) + e0);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) dst[u] = *reinterpret_cast<const float4_t*>(src + 4 * u);
-  } else {
-    uint4* dst = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + e0);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      uint16_t hbits[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        uint16_t tmp[1];
-        store_elem(tmp, 0, src[8 * u + e], dtype);
-        hbits[e] = tmp[0];
-      }
-      dst[u] = make_uint4(hbits[0] | (uint32_t)hbits[1] << 16, hbits[2] | (uint32_t)hbits[3] << 16,
-                          hbits[4] | (uint32_t)hbits[5] << 16, hbits[6] | (uint32_t)hbits[7] << 16);
-    }
-  }
-}
 
 template <int R>
 __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const DequantKArgs a) {
@@ -158,45 +126,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
   if (active) dq_store_tile(tl, a.k_out, row0, a.out_dtype);
   __syncthreads();   // the staging tile is reused for the values
 
-  // ---- values: y = H128 (codebook level), channel 16b + n, token 4q + tt ----
-  float y[4][8];
-#pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    const uint32_t D = b < 4 ? vcd.x : vcd.y;
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) y[tt][b] = a.codebook[(D >> (8 * (b & 3) + 2 * tt)) & 3];
-  }
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-#pragma unroll
-    for (int hb = 1; hb < 8; hb <<= 1)   // H8 over b
-#pragma unroll
-      for (int b = 0; b < 8; ++b)
-        if (!(b & hb)) {
-          const float u = y[tt][b], w = y[tt][b | hb];
-          y[tt][b] = u + w;
-          y[tt][b | hb] = u - w;
-        }
-#pragma unroll
-    for (int hb = 1; hb < 16; hb <<= 1)   // H16 over n, across the row
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const float o = __shfl_xor(y[tt][b], hb);
-        y[tt][b] = (n & hb) ? o - y[tt][b] : y[tt][b] + o;
-      }
-  }
-  const float nv[4] = {half_bits_to_float(nrm.x & 0xffff), half_bits_to_float(nrm.x >> 16),
-                       half_bits_to_float(nrm.y & 0xffff), half_bits_to_float(nrm.y >> 16)};
-#pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    const int c = 16 * b + n;
-    const bool neg = sign_neg(a.v_sign_bits, c);
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const float v = y[tt][b] / (float)kD;
-      tl.v[4 * q + tt][c] = (neg ? -v : v) * nv[tt];
-    }
-  }
+  dq_value_tile(vcd, nrm, a.codebook, a.v_sign_bits, n, q, tl);
   __syncthreads();
   if (active) dq_store_tile(tl, a.v_out, row0, a.out_dtype);
 }

@@ -1,0 +1,230 @@
+"""Spectral (K4) key path: host side of the C-ABI in include/bmx_spectral.h.
+
+A corpus-fitted pack per layer (cache/spectral.py:175-215, ``SpectralPack``:
+enc, dec (C x C fp32), lam, bits per direction on the tier grid, group 64)
+codes the pre-RoPE keys; the values use the k2b value codec in value-only
+pages.  ``DevicePack`` holds what the kernels read: the page layout of the
+pack's bits, enc's columns and dec's rows in page order.  ``append`` writes
+64-token groups; ``dequant`` reads them back dense (the reference's spectral
+read path: chunked_attention.py:106-116, then RoPE).
+
+Pack files: the reference's format (spectral.py:1081-1170, save_pack_file /
+load_packs), a safetensors file of ``layer{i}.enc / .dec / .lam /
+.bits_b{budget:g}`` and a JSON sidecar ``<path>.json`` with tiers, group and
+budgets.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+import json
+import math
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _lib
+from .k2b import _V_DTYPES, HEAD_DIM, ROPE_NONE, CodecConsts, _need, _ptr, _stream
+
+TIERS = (0, 2, 3, 4, 5, 6, 8)
+GROUP = 64
+_CONTAINER = {2: 2, 3: 4, 4: 4, 5: 8, 6: 8, 8: 8}
+MAX_CPAD = 1072
+
+
+@dataclass
+class SpectralPack:
+    """One layer's pack (spectral.py:175-215): Y = M enc, M_hat = Y_hat dec^T."""
+
+    enc: torch.Tensor
+    dec: torch.Tensor
+    lam: torch.Tensor
+    bits: torch.Tensor
+    group: int = GROUP
+    tiers: tuple = TIERS
+    budget: float = float("nan")
+
+    @property
+    def c_used(self) -> int:
+        return int((self.bits != 0).sum())
+
+
+def allocate_bits(var, budget: float, tiers=TIERS, n_search: int = 40) -> torch.Tensor:
+    """Reverse water-filling of a per-direction variance onto the tier grid,
+    midpoint rounding (allocate_bits_from_variance, selection "round",
+    codecs.py:203-287): bisect log(kappa) for the smallest kappa whose mean
+    rounded rate 0.5 log2(var / kappa) stays within the budget."""
+    var = np.maximum(np.asarray(torch.as_tensor(var, dtype=torch.float64)), 1e-30)
+    grid = np.array(sorted(tiers), dtype=np.float64)
+
+    def rounded(kappa):
+        b = np.maximum(0.5 * np.log2(var / kappa), 0.0)
+        return grid[np.abs(b[:, None] - grid[None, :]).argmin(axis=1)]
+
+    lo_k, hi_k = float(var.min()) * 1e-6, float(var.max()) * 1e6
+    lo, hi = math.log(lo_k), math.log(hi_k)
+    best = rounded(hi_k)
+    for _ in range(n_search):
+        mid = 0.5 * (lo + hi)
+        b = rounded(math.exp(mid))
+        if b.mean() <= budget + 1e-12:
+            best, hi = b, mid
+        else:
+            lo = mid
+    return torch.from_numpy(best.astype(np.int64))
+
+
+def payload_bpe(bits: torch.Tensor, group: int = GROUP) -> float:
+    """Model-level payload bits per entry: mean(bits) + (16 / group) c_used / C
+    (spectral_payload_bpe, spectral.py:602-615)."""
+    C = bits.shape[0]
+    return float(bits.float().mean()) + 16.0 / group * int((bits != 0).sum()) / C
+
+
+def load_packs(path, budget: float) -> dict:
+    """{layer: SpectralPack} of one budget from a pack file (load_packs,
+    spectral.py:1137-1170); KeyError names the budgets the file holds."""
+    from safetensors.torch import load_file
+
+    side = json.loads(Path(str(path) + ".json").read_text())
+    if budget not in side["budgets"]:
+        raise KeyError(f"budget {budget} not in pack file; available: {side['budgets']}")
+    t = load_file(str(path))
+    layers = sorted({int(k.split(".")[0].removeprefix("layer")) for k in t if "." in k})
+    return {i: SpectralPack(enc=t[f"layer{i}.enc"], dec=t[f"layer{i}.dec"], lam=t[f"layer{i}.lam"],
+                            bits=t[f"layer{i}.bits_b{budget:g}"], group=int(side["group"]),
+                            tiers=tuple(side["tiers"]), budget=float(budget))
+            for i in layers}
+
+
+def save_packs(path, layers: dict, budgets, *, tiers=TIERS, group: int = GROUP) -> None:
+    """Write {layer: (enc, dec, lam, {budget: bits})} in the pack-file format."""
+    from safetensors.torch import save_file
+
+    t = {}
+    for i, (enc, dec, lam, bits) in layers.items():
+        t[f"layer{i}.enc"], t[f"layer{i}.dec"], t[f"layer{i}.lam"] = enc, dec, lam
+        for b in budgets:
+            t[f"layer{i}.bits_b{b:g}"] = bits[b]
+    save_file({k: v.contiguous() for k, v in t.items()}, str(path))
+    Path(str(path) + ".json").write_text(json.dumps({"tiers": list(tiers), "group": group,
+                                                     "budgets": list(budgets)}))
+
+
+class DevicePack:
+    """A pack's page layout and kernel operands on one device.
+
+    Columns: the coded directions in tier order (tier ascending, direction
+    ascending: tier_columns, spectral.py:631-645), each tier padded with zero
+    directions to a multiple of 8 (c_pad columns).  Slice s (8 columns) of
+    tier b has a w-bit container, w = 2 / 4 / 8 (tiers 2 / 3-4 / 5-8), 64 w
+    bytes per page at off[s] after the fp16 scales."""
+
+    def __init__(self, pack: SpectralPack, h_kv: int, device):
+        if pack.group != GROUP:
+            raise NotImplementedError(f"pack group {pack.group}: the spectral kernels take 64-token groups")
+        bits = pack.bits.to(torch.int64).cpu()
+        C = HEAD_DIM * h_kv
+        _need(tuple(pack.enc.shape) == (C, C) and tuple(pack.dec.shape) == (C, C) and bits.shape[0] == C,
+              f"pack shapes must be ({C}, {C}) with {C} bits for h_kv {h_kv}")
+        bad = set(bits.tolist()) - set(TIERS)
+        if bad:
+            raise NotImplementedError(f"tiers {sorted(bad)}: the kernels take tiers {TIERS}")
+        perm, slice_bits = [], []
+        for b in sorted(set(bits.tolist()) - {0}):
+            cols = torch.nonzero(bits == b).flatten().tolist()
+            n_pad = -(-len(cols) // 8) * 8
+            perm += cols + [-1] * (n_pad - len(cols))
+            slice_bits += [b] * (n_pad // 8)
+        _need(len(perm) > 0, "the pack codes no direction")
+        self.h_kv, self.C, self.c_pad = h_kv, C, len(perm)
+        if self.c_pad > MAX_CPAD:
+            raise NotImplementedError(f"c_pad {self.c_pad} above {MAX_CPAD}")
+        self.c_pad32 = -(-self.c_pad // 32) * 32
+        widths = [_CONTAINER[b] for b in slice_bits]
+        off, o = [], 2 * self.c_pad
+        for w in widths:
+            off.append(o)
+            o += GROUP * w
+        self.k_page_bytes = o + 16
+        self.v_page_bytes = int(_lib.lib().bmx_spectral_v_page_bytes(h_kv))
+        self.perm = torch.tensor(perm, dtype=torch.int64)
+        self.slice_bits = slice_bits
+        tab = [x | (b << 24) for x, b in zip(off, slice_bits)]
+        self.slice_tab = torch.tensor(tab, dtype=torch.int32, device=device)
+        keep = self.perm >= 0
+        encp = torch.zeros(C, self.c_pad, dtype=torch.float32)
+        encp[:, keep] = pack.enc.float().cpu()[:, self.perm[keep]]
+        decp = torch.zeros(C, self.c_pad32, dtype=torch.float32)
+        decp[:, : self.c_pad][:, keep] = pack.dec.float().cpu()[:, self.perm[keep]]
+        self.enc_perm = encp.to(device).contiguous()
+        self.dec_perm = decp.half().to(device).contiguous()
+        self.bpe = payload_bpe(bits, pack.group)
+
+    def layout(self) -> _lib.SpectralLayout:
+        return _lib.SpectralLayout(self.h_kv, self.c_pad, self.k_page_bytes, _ptr(self.slice_tab))
+
+
+def append(k_pre: torch.Tensor, v: torch.Tensor, dp: DevicePack, k_pages: torch.Tensor,
+           k_ids: torch.Tensor, v_pages: torch.Tensor, v_ids: torch.Tensor, consts: CodecConsts) -> None:
+    """Write 64n tokens: k_pre, v (h_kv, 64n, 128) on the device (fp16, bf16 or
+    fp32; innermost stride 1) into key pages k_ids (n) and value pages v_ids (4n)."""
+    dev = v.device
+    h_kv, S, d = k_pre.shape
+    _need(d == HEAD_DIM and h_kv == dp.h_kv and tuple(v.shape) == (h_kv, S, d), "k_pre, v must be (h_kv, S, 128)")
+    _need(S % GROUP == 0, "S must be a multiple of 64")
+    _need(k_pre.stride(2) == 1 and v.stride(2) == 1, "innermost stride must be 1")
+    _need(k_pre.dtype in _V_DTYPES and v.dtype in _V_DTYPES, "keys and values must be fp16, bf16 or fp32")
+    n = S // GROUP
+    _need(k_ids.dtype == torch.int32 and k_ids.numel() >= n and v_ids.dtype == torch.int32
+          and v_ids.numel() >= 4 * n, "k_ids (n) and v_ids (4n) must be int32")
+    _need(k_pages.shape[1] == dp.k_page_bytes and v_pages.shape[1] == dp.v_page_bytes, "pool page sizes")
+    a = _lib.SpectralAppendArgs()
+    a.L = dp.layout()
+    a.n_groups = n
+    a.k_pre, a.k_dtype, a.k_sh, a.k_st = _ptr(k_pre), _V_DTYPES[k_pre.dtype], k_pre.stride(0), k_pre.stride(1)
+    a.v, a.v_dtype, a.v_sh, a.v_st = _ptr(v), _V_DTYPES[v.dtype], v.stride(0), v.stride(1)
+    a.enc_perm = _ptr(dp.enc_perm)
+    a.k_pages, a.k_page_ids, a.n_k_pool = _ptr(k_pages), _ptr(k_ids), k_pages.shape[0]
+    a.v_pages, a.v_page_ids, a.n_v_pool = _ptr(v_pages), _ptr(v_ids), v_pages.shape[0]
+    a.v_codebook[:] = consts.codebook
+    a.v_sign_bits[:] = consts.sign_bits
+    _lib.check(_lib.lib().bmx_spectral_append(ct.byref(a), _stream(dev)), "bmx_spectral_append")
+
+
+def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_pages: torch.Tensor,
+            v_table: torch.Tensor, n_tokens: int, consts: CodecConsts, *, apply_rope: int = ROPE_NONE,
+            dtype: torch.dtype = torch.float32, out: tuple | None = None):
+    """Pages of one sequence -> dense (K, V), each (h_kv, n_tokens, 128) in
+    dtype; keys pre-RoPE (ROPE_NONE) or rotated at read (ROPE_EXACT: fp32
+    cos/sin, ROPE_FP16_TABLES: the reference's fp16 tables).  ``out`` takes
+    preallocated (K, V) of that shape and dtype."""
+    dev = k_pages.device
+    _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
+    _need(n_tokens % GROUP == 0, "n_tokens must be a multiple of 64")
+    _need(k_table.dtype == torch.int32 and k_table.numel() >= n_tokens // GROUP and v_table.dtype == torch.int32
+          and v_table.numel() >= n_tokens // 16, "k_table (n/64) and v_table (n/16) must be int32")
+    if out is None:
+        k = torch.empty(dp.h_kv, n_tokens, HEAD_DIM, dtype=dtype, device=dev)
+        v = torch.empty_like(k)
+    else:
+        k, v = out
+        _need(k.dtype == dtype and tuple(k.shape) == (dp.h_kv, n_tokens, HEAD_DIM) and k.is_contiguous()
+              and v.dtype == dtype and v.shape == k.shape and v.is_contiguous(), "out tensors")
+    a = _lib.SpectralDequantArgs()
+    a.L = dp.layout()
+    a.n_tokens = int(n_tokens)
+    a.k_pages, a.k_page_table, a.n_k_pool = _ptr(k_pages), _ptr(k_table), k_pages.shape[0]
+    a.v_pages, a.v_page_table, a.n_v_pool = _ptr(v_pages), _ptr(v_table), v_pages.shape[0]
+    a.dec_perm = _ptr(dp.dec_perm)
+    a.apply_rope = int(apply_rope)
+    a.rope_scaling = consts.rope_scaling
+    a.inv_freq[:] = consts.inv_freq
+    a.v_codebook[:] = consts.codebook
+    a.v_sign_bits[:] = consts.sign_bits
+    a.out_dtype = _V_DTYPES[dtype]
+    a.k_out, a.v_out = _ptr(k), _ptr(v)
+    _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
+    return k, v

@@ -1,0 +1,108 @@
+/* C-ABI of the spectral (K4) key path on gfx950: the write kernels and the
+ * dense dequantization a decode or prefill step attends over.
+ *
+ * Keys: a corpus-fitted spectral pack (enc, dec: C x C fp32; bits per
+ * direction from the tier grid {0, 2, 3, 4, 5, 6, 8}; group 64 tokens) codes
+ * the pre-RoPE keys as Y = M enc, RTN per direction over 64-token groups with
+ * the MSE-refined step, and reads them back as Y_hat dec^T with RoPE applied
+ * at read.  Reference: src/bmx/cache/spectral.py:763-841
+ * (spectral_quantize_packed / spectral_dequant_packed), quant/rtn.py:10-53,
+ * the write call in cache/packed_streaming.py:491-511 and the read in
+ * cache/chunked_attention.py:106-116 (_dequant_block, arm "spectral"), whose
+ * decode is the reference's chunked path (packed_streaming.py:1016-1032).
+ * Values: the k2b value codec (2-bit Lloyd codes of the Hadamard-rotated
+ * values and an fp16 norm per head and token, include/bmx_k2b.h) in value-only
+ * pages of 16 tokens: VNORM [h_kv][16] fp16 at byte 0, VCODE [h_kv][64][2] u32
+ * at byte 32 h_kv, bmx_spectral_v_page_bytes(h_kv) bytes per page.
+ *
+ * Key page: one per 64-token group.  Columns are the pack's coded directions
+ * in tier order (tier ascending, direction ascending), each tier padded with
+ * zero directions to a multiple of 8: c_pad columns.  SCALE [c_pad] fp16 at
+ * byte 0 holds the group's step of each column; then slices of 8 columns,
+ * slice s at byte offset off[s] = slice_tab[s] & 0xFFFFFF with tier
+ * b = slice_tab[s] >> 24, container width w = 2 (b = 2), 4 (b = 3, 4) or
+ * 8 (b = 5, 6, 8) bits: token t's 8 codes in the w bytes at off[s] + t w,
+ * column k at bits [k w, (k + 1) w), stored as code + 2^(b - 1).  16 bytes of
+ * padding end the page.  Codes and steps are computed in fp32 in a fixed
+ * order: Y[t][j] = sum over c ascending of M[t][c] enc[c][j] and the step's
+ * sums over the group's tokens left to right, no fused multiply-add.
+ *
+ * Every entry point returns BMX_OK (0) or a BMX_E_* code with a message from
+ * bmx_last_error() (include/bmx_k2b.h). */
+#ifndef BMX_SPECTRAL_H
+#define BMX_SPECTRAL_H
+
+#include <stdint.h>
+
+#include "bmx_k2b.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BMX_SPECTRAL_MAX_CPAD 1072   /* 1024 directions + padding of 6 tiers */
+
+typedef struct bmx_spectral_layout {
+  int32_t h_kv;                /* key heads, 1..8; C = 128 h_kv */
+  int32_t c_pad;               /* coded columns with padding: multiple of 8, 8..C + 48 */
+  int32_t k_page_bytes;        /* bytes per key page (SCALE + slices + 16) */
+  const int32_t* slice_tab;    /* device, c_pad / 8 entries: off | tier << 24 */
+} bmx_spectral_layout;
+
+/* Replaces the spectral branch of PackedStreamingLayer._pack_k_block
+ * (packed_streaming.py:491-511: spectral_quantize_packed on the block's
+ * pre-RoPE keys) and its _pack_v_block for the paired turboquant_mse values
+ * (packed_streaming.py:544-580), for n_groups 64-token groups at once. */
+typedef struct bmx_spectral_append_args {
+  bmx_spectral_layout L;
+  int32_t n_groups;            /* 64-token groups to write */
+  const void* k_pre;           /* pre-RoPE keys, element [h][t][d] at h k_sh + t k_st + d */
+  int32_t k_dtype;             /* BMX_K2B_F16, _F32 or _BF16 (converted to fp32) */
+  int64_t k_sh, k_st;
+  const void* v;               /* values, element [h][t][d] at h v_sh + t v_st + d */
+  int32_t v_dtype;
+  int64_t v_sh, v_st;
+  const float* enc_perm;       /* device [C][c_pad] fp32: enc's columns in page order, zero padding */
+  uint8_t* k_pages;            /* key page pool */
+  const int32_t* k_page_ids;   /* n_groups ids */
+  int32_t n_k_pool;
+  uint8_t* v_pages;            /* value page pool */
+  const int32_t* v_page_ids;   /* 4 n_groups ids (16 tokens each) */
+  int32_t n_v_pool;
+  float v_codebook[4];         /* 2-bit Lloyd levels (gaussian_codebook(2)) */
+  uint32_t v_sign_bits[4];     /* Hadamard signs of the 128 channels (1 = negative) */
+} bmx_spectral_append_args;
+
+/* Replaces _dequant_block(arm "spectral") + apply_rope for the keys and
+ * _dequant_block(arm "turboquant_mse") for the values (chunked_attention.py:
+ * 52-194), n_tokens tokens of one sequence into dense [h_kv][n_tokens][128]. */
+typedef struct bmx_spectral_dequant_args {
+  bmx_spectral_layout L;
+  int32_t n_tokens;            /* multiple of 64 */
+  const uint8_t* k_pages;
+  const int32_t* k_page_table; /* n_tokens / 64 key page ids */
+  int32_t n_k_pool;
+  const uint8_t* v_pages;
+  const int32_t* v_page_table; /* n_tokens / 16 value page ids */
+  int32_t n_v_pool;
+  const uint16_t* dec_perm;    /* device fp16 [h_kv][128][c_pad rounded up to 32]: dec's
+                                  rows of each head, columns in page order, zero padding */
+  int32_t apply_rope;          /* 0 none, 1 fp32 cos/sin, 2 cos/sin rounded to fp16 */
+  float rope_scaling;
+  float inv_freq[64];
+  float v_codebook[4];
+  uint32_t v_sign_bits[4];
+  int32_t out_dtype;           /* BMX_K2B_F16, _F32 or _BF16 */
+  void* k_out;
+  void* v_out;
+} bmx_spectral_dequant_args;
+
+int64_t bmx_spectral_v_page_bytes(int32_t h_kv);
+int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* stream);
+int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BMX_SPECTRAL_H */

@@ -29,6 +29,15 @@ Functions covered (reference file:line, paths under ``src/bmx``):
   * _tail_partial + merge math   cache/triton_dequant_attention.py:324-360, 409-461
   * PackedStreamingCache under HF generate (tiny Llama, head_dim 128)
                                  cache/packed_streaming.py:1067-1222
+  * spectral K codec: fit_spectral_basis, pack_from_basis,
+    allocate_bits_from_variance ("round"), tier_columns,
+    spectral_quantize_packed / spectral_dequant_packed (rtn quantizer,
+    mse_scale)                   cache/spectral.py:238-254, 421-485, 631-645,
+                                 763-841; cache/codecs.py:203-287;
+                                 quant/rtn.py:10-53
+
+``python tests/golden/make_golden.py SRC spectral`` rewrites only the named
+fixture files (codecs, attention, e2e_tiny_llama, spectral).
 """
 
 from __future__ import annotations
@@ -270,13 +279,60 @@ def e2e_fixtures():
     return out
 
 
+def spectral_fixtures():
+    """A spectral pack fitted by the reference on seeded synthetic keys with a
+    non-identity weighting (enc != dec), h_kv 2 (C 256), group 64, and the
+    packed codes, scales and dequantization of 4 groups of keys."""
+    from bmx.cache import codecs
+    from bmx.cache.spectral import (
+        _unpack_tier_codes,
+        fit_spectral_basis,
+        pack_from_basis,
+        spectral_dequant_packed,
+        spectral_quantize_packed,
+        tier_columns,
+    )
+
+    g = torch.Generator().manual_seed(23)
+    C, S = 256, 256
+    lam_true = 40.0 * torch.arange(1, C + 1, dtype=torch.float64) ** -1.3
+    Q, _ = torch.linalg.qr(torch.randn(C, C, generator=g, dtype=torch.float64))
+    mix = (Q * lam_true.sqrt()).mT            # rows of keys: z @ mix
+    M_fit = (torch.randn(1024, C, generator=g, dtype=torch.float64) @ mix).float()
+    w = 0.5 + torch.rand(C, generator=g, dtype=torch.float64)
+    Wh, Wh_inv = torch.diag(w.sqrt()), torch.diag(w.rsqrt())
+    basis = fit_spectral_basis(M_fit, Wh, Wh_inv)
+    out = {"enc": basis.enc.numpy(), "dec": basis.dec.numpy(), "lam64": basis.lam64.numpy()}
+    for budget in (2.0, 2.5, 3.0):
+        b = codecs.allocate_bits_from_variance(basis.lam64, budget, (0, 2, 3, 4, 5, 6, 8))
+        out[f"bits_b{budget}"] = b.numpy()
+    pack = pack_from_basis(basis, 2.5, group=64)
+    assert np.array_equal(pack.bits.numpy(), out["bits_b2.5"])
+    M = (torch.randn(S, C, generator=g, dtype=torch.float64) @ mix).float()
+    out["M"] = M.numpy()
+    out["Y"] = (M @ pack.enc).numpy()
+    cols = tier_columns(pack.bits)
+    packed, bpe = spectral_quantize_packed(M, pack, mse_scale=True, cols_by_tier=cols)
+    out["bpe"] = np.float64(bpe)
+    for b, c in cols.items():
+        out[f"cols_t{b}"] = c.numpy()
+        out[f"codes_t{b}"] = _unpack_tier_codes(packed[f"t{b}_codes"], b, S).numpy()
+        out[f"scale_t{b}"] = packed[f"t{b}_scale"].numpy()
+    out["M_hat"] = spectral_dequant_packed(packed, pack, cols_by_tier=cols).numpy()
+    return out
+
+
+FIXTURES = {"codecs": codec_fixtures, "attention": attention_fixtures,
+            "e2e_tiny_llama": e2e_fixtures, "spectral": spectral_fixtures}
+
+
 def main():
     src = sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src"
+    names = sys.argv[2:] or list(FIXTURES)
     torch.set_num_threads(min(8, os.cpu_count() or 1))
     _import_reference(src)
-    np.savez_compressed(HERE / "codecs.npz", **codec_fixtures())
-    np.savez_compressed(HERE / "attention.npz", **attention_fixtures())
-    np.savez_compressed(HERE / "e2e_tiny_llama.npz", **e2e_fixtures())
+    for name in names:
+        np.savez_compressed(HERE / f"{name}.npz", **FIXTURES[name]())
     for f in sorted(HERE.glob("*.npz")):
         print(f.name, f.stat().st_size)
 

@@ -1,0 +1,160 @@
+"""Spectral (K4) key path on the GPU against the CPU oracle (oracle/spectral.py,
+pinned to the reference's golden vectors): the write kernel's pages byte for
+byte, the dequant kernel's keys (fp16 MFMA reconstruction: bounded by the
+inputs' fp16 rounding) and values, and attention over the dequantized cache."""
+
+import numpy as np
+import pytest
+import torch
+
+from bmx_amd import k2b, spectral
+from oracle import attention as A
+from oracle import codecs as OC
+from oracle import layout as OL
+from oracle import spectral as O
+
+from tests.spectral_util import golden_pack, synthetic_pack, synthetic_keys
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _values_of(vpages: np.ndarray, h_kv: int):
+    """(codes, fp16 norms) of value-only pages through the k2b page reader."""
+    sec = OL.sections(h_kv, 16)
+    full = np.zeros((vpages.shape[0], sec["total"][1]), np.uint8)
+    nv, nc = h_kv * 32, h_kv * 512
+    full[:, sec["vnorm"][0]: sec["vnorm"][0] + nv] = vpages[:, :nv]
+    full[:, sec["vcode"][0]: sec["vcode"][0] + nc] = vpages[:, nv: nv + nc]
+    _, _, _, vidx, vn16 = OL.unpack_pages(full, h_kv, 16)
+    return vidx, vn16
+
+
+def _write(pack, h_kv, M, v, consts, shuffle_seed=None):
+    """Append keys M (S, C) and values v (h_kv, S, 128) through the C-ABI into
+    pools with (optionally shuffled) page ids; returns (dp, kp, vp, k_ids, v_ids)."""
+    S = M.shape[0]
+    dp = spectral.DevicePack(pack, h_kv, DEV)
+    ng = S // 64
+    k_ids = torch.arange(ng, dtype=torch.int32)
+    v_ids = torch.arange(4 * ng, dtype=torch.int32)
+    if shuffle_seed is not None:
+        g = torch.Generator().manual_seed(shuffle_seed)
+        k_ids = k_ids[torch.randperm(ng, generator=g)].to(torch.int32)
+        v_ids = v_ids[torch.randperm(4 * ng, generator=g)].to(torch.int32)
+    kp = torch.zeros(ng, dp.k_page_bytes, dtype=torch.uint8, device=DEV)
+    vp = torch.zeros(4 * ng, dp.v_page_bytes, dtype=torch.uint8, device=DEV)
+    k_pre = OC.from_matrix(torch.from_numpy(M).float(), h_kv)
+    spectral.append(k_pre.to(DEV), v.to(DEV), dp, kp, k_ids.to(DEV), vp, v_ids.to(DEV), consts)
+    torch.cuda.synchronize()
+    return dp, kp, vp, k_ids.to(DEV), v_ids.to(DEV)
+
+
+CASES = ["golden_h2", "synthetic_h8", "synthetic_h8_b3"]
+
+
+def _case(name):
+    if name == "golden_h2":
+        pack, M = golden_pack()
+        return pack, 2, M
+    budget = 3.0 if name.endswith("b3") else 2.5
+    pack = synthetic_pack(8, budget, seed=5)
+    return pack, 8, synthetic_keys(pack, 512, seed=6)
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_append_pages_match_oracle(name):
+    """Every key page byte equals the oracle's page (encode in the fixed order,
+    MSE-refined RTN, container packing), and the value pages hold the k2b
+    value codec's codes and fp16 norms."""
+    pack, h_kv, M = _case(name)
+    print(f"case {name}: h_kv {h_kv}, S {M.shape[0]}", flush=True)
+    gen = torch.Generator().manual_seed(3)
+    v = torch.randn(h_kv, M.shape[0], 128, generator=gen)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=1)
+    L = O.Layout(pack.bits.numpy())
+    assert (L.c_pad, L.page_bytes) == (dp.c_pad, dp.k_page_bytes)
+    assert np.array_equal(L.slice_table(), dp.slice_tab.cpu().numpy())
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
+    want = O.pack_pages(codes, scales, L)
+    got = kp[k_ids.long()].cpu().numpy()
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    print(f"key pages differing: {len(bad)}/{len(want)}; c_pad {L.c_pad}, tiers "
+          f"{sorted(set(L.slice_bits.tolist()))}", flush=True)
+    assert len(bad) == 0
+    vidx, vn16 = _values_of(vp[v_ids.long()].cpu().numpy(), h_kv)
+    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v), bits=2, seed=0, h=h_kv)
+    np.testing.assert_array_equal(vn16.astype(np.float32), norms.numpy())
+    assert int((vidx != idx.numpy()).sum()) == 0
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_dequant_matches_oracle(name):
+    """Keys: Y_hat dec^T from the pages (fp16 steps, as stored) within the
+    fp16 rounding of the MFMA inputs (code * step and dec), pre-RoPE and
+    rotated (fp32 and fp16 tables); values as the k2b value codec; dtypes
+    rounded once from the fp32 result."""
+    pack, h_kv, M = _case(name)
+    S = M.shape[0]
+    gen = torch.Generator().manual_seed(4)
+    v = torch.randn(h_kv, S, 128, generator=gen)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=2)
+    L = O.Layout(pack.bits.numpy())
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)), h_kv)
+    Kp, Vd = spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts)
+    kmax = K_or.abs().max().item()
+    err = (Kp.cpu().double() - K_or).abs().max().item()
+    print(f"{name}: pre-RoPE keys max_abs {err:.3e} (max|K| {kmax:.3f}, rel {err / kmax:.2e})", flush=True)
+    assert err <= 1.5e-3 * kmax
+    inv = torch.tensor(consts.inv_freq)
+    cos, sin = A.rope_cos_sin(inv, torch.arange(S))
+    Kr, _ = spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=k2b.ROPE_EXACT)
+    err_r = (Kr.cpu().double() - A.apply_rope(K_or.float(), cos, sin).double()).abs().max().item()
+    assert err_r <= 1.5e-3 * kmax
+    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v), bits=2, seed=0, h=h_kv)
+    V_or = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=h_kv), h_kv)
+    assert (Vd.cpu() - V_or).abs().max().item() < 1e-4
+    Kt, _ = spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=k2b.ROPE_FP16_TABLES)
+    for dt in (torch.float16, torch.bfloat16):
+        Kh, Vh = spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=k2b.ROPE_FP16_TABLES,
+                                  dtype=dt)
+        assert Kh.dtype == dt and torch.equal(Kh, Kt.to(dt)) and torch.equal(Vh, Vd.to(dt))
+
+
+def test_attention_over_dequantized_pages():
+    """Grouped decode attention over the dequantized cache (RoPE'd keys and
+    the fp16 window) against the oracle's dense attention over the same
+    codes: the spectral decode step's numerics, at the decode bar."""
+    pack = synthetic_pack(8, 2.5, seed=8)
+    S, T, G = 1024, 40, 4
+    M = synthetic_keys(pack, S, seed=9)
+    gen = torch.Generator().manual_seed(10)
+    v = torch.randn(8, S, 128, generator=gen)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    dp, kp, vp, k_ids, v_ids = _write(pack, 8, M, v, consts)
+    Kd, Vd = spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=k2b.ROPE_EXACT,
+                              dtype=torch.float16)
+    kt = torch.randn(8, T, 128, generator=gen).half()
+    vt = torch.randn(8, T, 128, generator=gen).half()
+    q = torch.randn(8 * G, 1, 128, generator=gen)
+    scale = 128 ** -0.5
+    K = torch.cat([Kd, kt.to(DEV)], 1)
+    V = torch.cat([Vd, vt.to(DEV)], 1)
+    out = torch.nn.functional.scaled_dot_product_attention(
+        q.half().to(DEV).unsqueeze(0), K.unsqueeze(0), V.unsqueeze(0), scale=scale, enable_gqa=True)[0]
+    L = O.Layout(pack.bits.numpy())
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)).float(), 8)
+    cos, sin = A.rope_cos_sin(torch.tensor(consts.inv_freq), torch.arange(S))
+    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v), bits=2, seed=0, h=8)
+    V_or = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=8), 8)
+    ref = A.naive_dense_attention(q.half().float(), torch.cat([A.apply_rope(K_or, cos, sin), kt.float()], 1),
+                                  torch.cat([V_or, vt.float()], 1), G, scale)
+    o = out.float().cpu().double()
+    err = (o - ref.double()).abs().max().item()
+    rel = ((o - ref.double()).norm() / ref.double().norm()).item()
+    print(f"attention over spectral pages: max_abs {err:.3e} rel {rel:.3e}", flush=True)
+    assert err <= 2e-3 and rel <= 1e-2
