@@ -58,7 +58,7 @@ from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
 from . import codecs as K
-from . import k2b, rtn
+from . import k2b, rtn, spectral
 from .specs import CacheCodecSpec, packed_path
 
 ATTN_NAME = "bmx_k2b"
@@ -151,7 +151,8 @@ class PackedStreamingLayer(DynamicLayer):
     packed_streaming.py:904-975)."""
 
     def __init__(self, k_spec: CacheCodecSpec, v_spec: CacheCodecSpec, model_config,
-                 recent_window: int = 32, pack_v: bool = True, pack_k: bool = True):
+                 recent_window: int = 32, pack_v: bool = True, pack_k: bool = True,
+                 pack: "spectral.SpectralPack | None" = None):
         super().__init__()
         self._path = packed_path(k_spec, v_spec)
         self.k_spec, self.v_spec = k_spec, v_spec
@@ -169,7 +170,7 @@ class PackedStreamingLayer(DynamicLayer):
         self._page = PAGE
         inv, scaling = K.rope_inv_freq(tc)
         self._inv_freq, self._rope_scaling = inv, scaling
-        if self._path == "k2b":
+        if self._path in ("k2b", "spectral"):
             self._consts = k2b.CodecConsts.make(v_bits=2, v_seed=v_spec.seed, inv_freq=inv,
                                                 rope_scaling=scaling)
         else:
@@ -193,6 +194,15 @@ class PackedStreamingLayer(DynamicLayer):
         self._table: torch.Tensor | None = None   # (1, capacity) int32: 0, 1, 2, ...
         self._n_pages = 0
         self._packed_len_dev: torch.Tensor | None = None
+        # spectral keys: the layer's pack, its device operands, the key pages
+        # (one per 64-token group; the pool above holds the value pages)
+        if self._path == "spectral" and pack is None:
+            raise ValueError("the spectral path needs the layer's pack")
+        self._pack = pack
+        self._dp: spectral.DevicePack | None = None
+        self._kpool: torch.Tensor | None = None
+        self._ktable: torch.Tensor | None = None
+        self._n_kpages = 0
 
     # -------------------------------------------------------------- write side
 
@@ -220,7 +230,32 @@ class PackedStreamingLayer(DynamicLayer):
     def _page_bytes(self) -> int:
         if self._path == "k2b":
             return k2b.page_bytes(self._h_kv, self._rank)
+        if self._path == "spectral":
+            return int(_lib_v_page_bytes(self._h_kv))
         return rtn.page_bytes(self._h_kv, **self._rtn)
+
+    def _commit_spectral(self, k_pre: torch.Tensor, v: torch.Tensor) -> None:
+        """Encode consecutive codec pages (h_kv, 128n, d): the spectral branch
+        of _pack_k_block (packed_streaming.py:491-511) and the paired value
+        pages, 2n key pages of 64 tokens and 8n value pages of 16."""
+        dev = v.device
+        if self._dp is None:
+            self._dp = spectral.DevicePack(self._pack, self._h_kv, dev)
+        n_grp = k_pre.shape[1] // spectral.GROUP
+        kf, vf = self._n_kpages, self._n_pages
+        cap = 0 if self._kpool is None else self._kpool.shape[0]
+        if kf + n_grp > cap:
+            new_cap = max(kf + n_grp, 2 * cap, 16)
+            pool = torch.zeros(new_cap, self._dp.k_page_bytes, dtype=torch.uint8, device=dev)
+            if self._kpool is not None and kf:
+                pool[:kf].copy_(self._kpool[:kf])
+            self._kpool = pool
+            self._ktable = torch.arange(new_cap, dtype=torch.int32, device=dev)
+        self._reserve(vf + 4 * n_grp, dev)
+        spectral.append(k_pre.to(dev), v, self._dp, self._kpool, self._ktable[kf: kf + n_grp], self._pool,
+                        self._table[0, vf: vf + 4 * n_grp], self._consts)
+        self._n_kpages = kf + n_grp
+        self._n_pages = vf + 4 * n_grp
 
     def _commit_rtn(self, k_post: torch.Tensor, v: torch.Tensor) -> None:
         """Encode consecutive codec pages of post-RoPE keys and values
@@ -274,8 +309,13 @@ class PackedStreamingLayer(DynamicLayer):
                 if self._k_pre is None:
                     raise RuntimeError("no pre-RoPE keys captured: call cache.attach(model) before prefill")
                 lo, hi = start - self._k_pre_offset, end - self._k_pre_offset
-                self._commit(self._k_pre[:, lo:hi, :], v_new)
-                self._quant_bits_k += n_cp * K.bpe_k(self._rank, C) * page_entries
+                if self._path == "spectral":
+                    self._commit_spectral(self._k_pre[:, lo:hi, :], v_new)
+                    self._quant_bits_k += n_cp * spectral.payload_bpe(self._pack.bits, self._pack.group) \
+                        * page_entries
+                else:
+                    self._commit(self._k_pre[:, lo:hi, :], v_new)
+                    self._quant_bits_k += n_cp * K.bpe_k(self._rank, C) * page_entries
                 self._quant_bits_v += n_cp * K.bpe_v(self._h_kv, C) * page_entries
                 self._committed_S_q = end
                 if hi >= self._k_pre.shape[1]:
@@ -307,7 +347,7 @@ class PackedStreamingLayer(DynamicLayer):
             raise RuntimeError("the packed cache attends on a HIP device only (no CPU path)")
         n_heads, n_q, d = q.shape
         G = n_heads // self._h_kv
-        if n_q == 1 and not is_causal:
+        if n_q == 1 and not is_causal and self._path != "spectral":
             return self._decode(q, scaling, G)
         return self._dense(q, scaling, G, is_causal and n_q > 1, attention_mask)
 
@@ -361,6 +401,12 @@ class PackedStreamingLayer(DynamicLayer):
                                  h_kv=self._h_kv, dtype=dt, **self._rtn)
             parts_k.append(kp)
             parts_v.append(vp)
+        elif P > 0 and self._path == "spectral":   # keys rotated at read, fp16 tables
+            kp, vp = spectral.dequant(self._dp, self._kpool, self._ktable[: P // spectral.GROUP], self._pool,
+                                      self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._consts,
+                                      apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt)
+            parts_k.append(kp)
+            parts_v.append(vp)
         elif P > 0:
             kp, vp = k2b.dequant(self._pool, self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P,
                                  self._basis16, self._consts, h_kv=self._h_kv, rank=self._rank,
@@ -390,6 +436,11 @@ class PackedStreamingLayer(DynamicLayer):
         return out.squeeze(0)
 
 
+def _lib_v_page_bytes(h_kv: int) -> int:
+    from . import _lib
+    return _lib.lib().bmx_spectral_v_page_bytes(h_kv)
+
+
 # ------------------------------------------------------------------ cache
 
 
@@ -404,12 +455,21 @@ class PackedStreamingCache(Cache):
 
     def __init__(self, model_config, k_spec: CacheCodecSpec, v_spec: CacheCodecSpec,
                  recent_window: int = 32, pack_v: bool = True, pack_k: bool = True):
-        packed_path(k_spec, v_spec)
+        path = packed_path(k_spec, v_spec)
+        # spectral: every layer's pack, loaded once (packed_streaming.py:1094-1147)
+        self._packs = spectral.load_packs(k_spec.pack_path, k_spec.budget) if path == "spectral" else {}
         wself = weakref.proxy(self)   # no cache -> closure -> cache cycle
 
         def _make_layer():
+            i = len(wself.layers)    # layers are made in order, layer i when len(layers) == i
+            pack = None
+            if path == "spectral":
+                if i not in wself._packs:
+                    raise KeyError(f"spectral pack file missing layer {i}")
+                pack = wself._packs[i]
             return PackedStreamingLayer(wself.k_spec, wself.v_spec, wself.model_config,
-                                        wself.recent_window, pack_v=wself.pack_v, pack_k=wself.pack_k)
+                                        wself.recent_window, pack_v=wself.pack_v, pack_k=wself.pack_k,
+                                        pack=pack)
 
         self._make_layer = _make_layer
         super().__init__(layer_class_to_replicate=_make_layer)

@@ -11,7 +11,11 @@ pairs the reference's attend() sends to a fused kernel
 * RTN: K and V ``rtn_token`` (K post-RoPE), 2..4 bits, channel groups of
   32, 64 or 128; the keys may also be ``rtn_channel`` (token groups of 32,
   64 or 128 per channel: config 1 and the ``kivi`` recipe, which the
-  reference runs on its chunked path only).
+  reference runs on its chunked path only);
+* spectral (K4): K ``spectral`` pre-RoPE from a pack file (rtn payload,
+  fp32 decoder, 64-token groups), V ``turboquant_mse_perhead`` 2-bit, the
+  value codec of the other pre-RoPE pair (the reference's ``k4_b*`` recipe
+  pairs the full-C ``turboquant_mse``, which no MI355X kernel reads).
 
 Every other pair raises, naming what it got: there is no CPU or slow path to
 route it to.
@@ -33,16 +37,30 @@ class CacheCodecSpec:
     group: int = 64
     seed: int = 0
     pre_rope: bool = False
+    pack_path: str | None = None      # spectral: the pack file (spectral.py:1081-1170)
+    budget: float | None = None       # spectral: the pack's budget label
+    dec_quant: str = "fp32"           # spectral: decoder storage (only "fp32" here)
+    payload_quant: str = "rtn"        # spectral: payload quantizer (only "rtn" here)
 
 
-def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0):
-    """(k_spec, v_spec) for a named recipe (cache/recipes.py:13-42, 173-177)."""
+def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0, pack_path: str | None = None):
+    """(k_spec, v_spec) for a named recipe (cache/recipes.py:13-42, 88-143, 173-177)."""
+    if arm.startswith("k4_b"):
+        if not pack_path:
+            raise ValueError("k4 arms require --pack-path (a fitted spectral pack file)")
+        budget_str = arm[len("k4_b"):]
+        if "_dec8" in budget_str or "_lq" in budget_str:
+            raise NotImplementedError(
+                f"recipe {arm!r}: the int8 decoder and Lloyd payload variants have no MI355X kernels")
+        return (CacheCodecSpec(arm="spectral", pre_rope=True, group=group, pack_path=pack_path,
+                               budget=float(budget_str), seed=seed),
+                CacheCodecSpec(arm="turboquant_mse_perhead", bits=2, seed=seed))
     if arm == "kivi":
         return (CacheCodecSpec(arm="rtn_channel", bits=2, group=group, seed=seed),
                 CacheCodecSpec(arm="rtn_token", bits=2, group=group, seed=seed))
     if arm != "k2b_ph":
         raise NotImplementedError(
-            f"recipe {arm!r} has no MI355X kernels; this package implements 'k2b_ph' and 'kivi'")
+            f"recipe {arm!r} has no MI355X kernels; this package implements 'k2b_ph', 'kivi' and 'k4_b<budget>'")
     return (CacheCodecSpec(arm="lowrank_rtn_channel", bits=3, rank=rank, group=group, seed=seed,
                            pre_rope=True),
             CacheCodecSpec(arm="turboquant_mse_perhead", bits=2, seed=seed))
@@ -58,9 +76,13 @@ def is_rtn(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> bool:
 
 
 def packed_path(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> str:
-    """"k2b" or "rtn" for a spec pair the MI355X kernels implement; raise otherwise."""
+    """"k2b", "rtn" or "spectral" for a spec pair the MI355X kernels implement;
+    raise otherwise."""
     if is_rtn(k_spec, v_spec):
         return "rtn"
+    if k_spec.arm == "spectral":
+        check_spectral(k_spec, v_spec)
+        return "spectral"
     check_k2b(k_spec, v_spec)
     return "k2b"
 
@@ -76,3 +98,18 @@ def check_k2b(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
             f"pre-RoPE, rank 16|32) with V=turboquant_mse_perhead (2 bits), and K=rtn_token|"
             f"rtn_channel with V=rtn_token (2..4 bits, groups 32|64|128, K post-RoPE); got "
             f"K={k_spec} V={v_spec}")
+
+
+def check_spectral(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
+    """The construction-time guards of the spectral arm (packed_streaming.py:
+    336-360: pre-RoPE keys and a pack file, asserted), then the variants the
+    kernels implement."""
+    assert k_spec.pre_rope, "spectral K requires pre_rope=True (RoPE is applied at read)"
+    assert k_spec.pack_path, "spectral K requires pack_path (a fitted spectral pack file)"
+    if k_spec.dec_quant != "fp32" or k_spec.payload_quant != "rtn":
+        raise NotImplementedError(
+            f"spectral dec_quant={k_spec.dec_quant!r} payload_quant={k_spec.payload_quant!r}: the MI355X "
+            f"kernels implement the fp32 decoder and the rtn payload")
+    if not (v_spec.arm == "turboquant_mse_perhead" and v_spec.bits == 2):
+        raise NotImplementedError(
+            f"spectral K pairs with V=turboquant_mse_perhead (2 bits) on the MI355X path; got V={v_spec}")

@@ -18,6 +18,34 @@ import torch.nn.functional as F
 from bmx_amd import cache as product
 from oracle import attention as A
 from oracle import codecs as OC
+from oracle import spectral as OS
+
+
+class SpectralOracleStore:
+    """Committed spectral codec pages on the CPU: codes by oracle/spectral
+    (fixed-order encode, MSE-refined RTN, fp16 steps as stored), keys
+    dequantized pre-RoPE, values by the per-head value codec."""
+
+    def __init__(self, pack, h_kv, v_seed, v_fp16):
+        self.pack, self.h_kv, self.v_seed, self.v_fp16 = pack, h_kv, v_seed, v_fp16
+        self.L = OS.Layout(pack.bits.numpy())
+        self.k, self.v = [], []
+
+    def commit(self, k_pre, v):
+        M = OC.to_matrix(k_pre.float().cpu()).numpy()
+        codes, scales = OS.quantize(OS.encode(M, self.pack.enc.numpy(), self.L), self.L)
+        K = OS.dequant(codes, scales, self.pack.dec.numpy(), self.L)
+        self.k.append(OC.from_matrix(torch.from_numpy(K).float(), self.h_kv))
+        vp = v.half().float() if self.v_fp16 else v.float()
+        idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(vp.cpu()), bits=2, seed=self.v_seed, h=self.h_kv)
+        self.v.append(OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=self.v_seed,
+                                                          h=self.h_kv), self.h_kv))
+
+    def dense_k_pre(self):
+        return torch.cat(self.k, dim=1)
+
+    def dense_v(self):
+        return torch.cat(self.v, dim=1)
 
 
 class OracleLayer(product.PackedStreamingLayer):
@@ -25,7 +53,14 @@ class OracleLayer(product.PackedStreamingLayer):
 
     def __init__(self, *args, **kwargs):
         super().__init__(*args, **kwargs)
-        self._oc = A.K2bOracleCache(self._h_kv, self._d_head, self._rank, v_seed=self.v_spec.seed)
+        if self._path == "spectral":
+            self._oc = SpectralOracleStore(self._pack, self._h_kv, self.v_spec.seed, self.v_fp16)
+        else:
+            self._oc = A.K2bOracleCache(self._h_kv, self._d_head, self._rank, v_seed=self.v_spec.seed)
+
+    def _commit_spectral(self, k_pre, v):
+        self._oc.v_fp16 = self.v_fp16
+        self._oc.commit(k_pre, v)
 
     def _commit(self, k_pre, v):
         for p in range(k_pre.shape[1] // product.PAGE):
@@ -76,7 +111,8 @@ class OracleCache(product.PackedStreamingCache):
         super().__init__(*args, **kwargs)
 
         def _make_layer():
-            lay = OracleLayer(self.k_spec, self.v_spec, self.model_config, self.recent_window)
+            pack = self._packs.get(len(self.layers)) if self._packs else None
+            lay = OracleLayer(self.k_spec, self.v_spec, self.model_config, self.recent_window, pack=pack)
             lay.v_fp16 = v_fp16
             return lay
 

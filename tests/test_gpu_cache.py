@@ -32,10 +32,10 @@ pytestmark = pytest.mark.gpu
 GOLD = Path(__file__).parent / "golden"
 
 
-def _tiny_model():
+def _tiny_model(n_layers=2):
     from transformers import LlamaConfig, LlamaForCausalLM
 
-    cfg = LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+    cfg = LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=n_layers,
                       num_attention_heads=4, num_key_value_heads=2, head_dim=128,
                       max_position_embeddings=4096, rope_theta=500000.0, initializer_range=0.1)
     torch.manual_seed(0)
@@ -80,6 +80,64 @@ def test_product_cache_matches_oracle_backed_cache(rank):
     assert prod.layers[0]._committed_S_q == 384
     assert err.max().item() <= 2e-3 * max(scale, 1.0)
     assert agree == 1.0
+
+
+def _spectral_pack_file(tmp_path, n_layers):
+    from bmx_amd import spectral
+    from tests.spectral_util import synthetic_pack
+
+    layers = {}
+    for i in range(n_layers):
+        p25, p3 = synthetic_pack(2, 2.5, seed=40 + i), synthetic_pack(2, 3.0, seed=40 + i)
+        layers[i] = (p25.enc, p25.dec, p25.lam, {2.5: p25.bits, 3.0: p3.bits})
+    path = tmp_path / "packs.safetensors"
+    spectral.save_packs(path, layers, (2.5, 3.0))
+    return str(path)
+
+
+@pytest.mark.parametrize("budget", [2.5, 3.0])
+def test_spectral_cache_matches_oracle_backed_cache(tmp_path, budget):
+    """The k4 recipe through the model: every commit through
+    bmx_spectral_append, every step (decode and prefill) through
+    bmx_spectral_dequant + SDPA, against the same host logic with the CPU
+    oracle's codes (one layer: both caches encode the same keys, so the
+    logits differ by the kernels' numerics only), teacher-forced."""
+    from bmx_amd import spectral
+
+    g = np.load(GOLD / "e2e_tiny_llama.npz")
+    tokens = torch.from_numpy(g["r16_tokens"]).cuda()
+    model = _tiny_model(n_layers=1)
+    path = _spectral_pack_file(tmp_path, 1)
+    specs = spec_pair(f"k4_b{budget:g}", pack_path=path)
+    prod = PackedStreamingCache(model.config, *specs, recent_window=32)
+    got = _run(prod, model, tokens, 140)
+    orc = OracleCache(model.config, *specs, recent_window=32)
+    ref = _run(orc, model, tokens, 140)
+    err = (got - ref).abs().max(dim=1).values
+    scale = ref.abs().max().item()
+    agree = (got.argmax(1) == ref.argmax(1)).float().mean().item()
+    lay = prod.layers[0]
+    print(f"k4_b{budget:g}: logits max|err| {err.max():.3e} of max|logit| {scale:.3f}; argmax "
+          f"agreement {agree:.4f}; committed {lay._committed_S_q}; c_pad {lay._dp.c_pad}", flush=True)
+    assert lay._committed_S_q == 384 and lay._n_kpages == 6 and lay._n_pages == 24
+    bpe = spectral.payload_bpe(spectral.load_packs(path, budget)[0].bits)
+    S = lay.get_seq_length()
+    assert abs(prod.bits_per_entry()[0] - (384 * bpe + (S - 384) * 16.0) / S) < 1e-9
+    assert err.max().item() <= 2e-3 * max(scale, 1.0)
+    assert agree == 1.0
+
+
+def test_spectral_generate_runs(tmp_path):
+    """HF generate() on the k4 recipe, two layers."""
+    model = _tiny_model()
+    ids = torch.randint(0, 256, (1, 200), generator=torch.Generator().manual_seed(9)).cuda()
+    cache = PackedStreamingCache(model.config, *spec_pair("k4_b2.5", pack_path=_spectral_pack_file(tmp_path, 2)),
+                                 recent_window=32)
+    with cache.attach(model), torch.no_grad():
+        out = model.generate(ids, past_key_values=cache, max_new_tokens=40, min_new_tokens=40,
+                             do_sample=False, pad_token_id=0)
+    assert out.shape == (1, 240)
+    assert cache.layers[1]._committed_S_q == 128 and cache.layers[1].get_seq_length() == 239
 
 
 def test_generate_runs_on_the_packed_path():

@@ -154,3 +154,37 @@ def test_bad_spectral_arguments_are_rejected_with_message():
     d.n_tokens, d.apply_rope = 64, 3
     assert lib.bmx_spectral_dequant(ct.byref(d), None) != 0 and b"apply_rope" in lib.bmx_last_error()
     assert lib.bmx_spectral_v_page_bytes(8) == 4352 and lib.bmx_spectral_v_page_bytes(0) == -1
+
+
+def test_recipe_and_construction_guards(tmp_path):
+    """spec_pair("k4_b<budget>") needs a pack path; the cache asserts pre-RoPE
+    keys and a pack file at construction (packed_streaming.py:336-360), loads
+    every layer's pack once, and refuses the variants without kernels."""
+    from transformers import LlamaConfig
+
+    from bmx_amd.cache import PackedStreamingCache
+    from bmx_amd.specs import CacheCodecSpec, spec_pair
+
+    cfg = LlamaConfig(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=1,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=128)
+    p = synthetic_pack(2, 2.5, seed=1)
+    path = tmp_path / "packs.safetensors"
+    spectral.save_packs(path, {0: (p.enc, p.dec, p.lam, {2.5: p.bits})}, (2.5,))
+    with pytest.raises(ValueError, match="pack-path"):
+        spec_pair("k4_b2.5")
+    for arm in ("k4_b2.5_lq", "k4_b2.5_dec8tl"):
+        with pytest.raises(NotImplementedError, match="no MI355X kernels"):
+            spec_pair(arm, pack_path=str(path))
+    k, v = spec_pair("k4_b2.5", pack_path=str(path))
+    assert (k.arm, k.pre_rope, k.budget, v.arm, v.bits) == ("spectral", True, 2.5, "turboquant_mse_perhead", 2)
+    with pytest.raises(AssertionError, match="pre_rope"):
+        PackedStreamingCache(cfg, CacheCodecSpec(arm="spectral", pack_path=str(path), budget=2.5), v)
+    with pytest.raises(AssertionError, match="pack_path"):
+        PackedStreamingCache(cfg, CacheCodecSpec(arm="spectral", pre_rope=True), v)
+    with pytest.raises(NotImplementedError, match="turboquant_mse_perhead"):
+        PackedStreamingCache(cfg, k, CacheCodecSpec(arm="turboquant_mse", bits=2))
+    cache = PackedStreamingCache(cfg, k, v)
+    assert torch.equal(cache._packs[0].bits, p.bits)
+    with pytest.raises(KeyError, match="available"):
+        PackedStreamingCache(cfg, CacheCodecSpec(arm="spectral", pre_rope=True, pack_path=str(path),
+                                                 budget=3.0), v)
