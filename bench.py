@@ -65,14 +65,18 @@ def parse():
                     help="skip timing the dense fp16 decode at the same context")
     ap.add_argument("--prefill-ctx", type=int, default=8192)
     ap.add_argument("--prefill-chunk", type=int, default=512)
-    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch"], default="decode",
+    ap.add_argument("--spectral-budget", type=float, default=2.5)
+    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch", "spectral"],
+                    default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
                          "BASELINE config 5, Qwen3-8B geometry, rank 16, an 8192-token prefill "
                          "then --stream-steps steps of one-token append + decode over 36 layers; "
                          "rtn: BASELINE config 1, RTN 4-bit per-channel keys / per-token values, "
                          "ctx --rtn-ctx, --rtn-layers layers; prefill: the second block of a cached "
                          "two-block prefill, --prefill-chunk queries over --prefill-ctx + chunk keys; "
-                         "batch: BASELINE config 4, 16 ragged sequences of 4k-16k")
+                         "batch: BASELINE config 4, 16 ragged sequences of 4k-16k; spectral: the "
+                         "k4 recipe's decode step (spectral keys at --spectral-budget, one layer "
+                         "of Llama-3.1-8B geometry, --ctx tokens)")
     ap.add_argument("--rtn-ctx", type=int, default=4096)
     ap.add_argument("--rtn-layers", type=int, default=1)
     ap.add_argument("--stream-steps", type=int, default=512)
@@ -593,6 +597,152 @@ def run_prefill(args, torch, dev) -> dict:
     }
 
 
+SPECTRAL_METRIC = "decode-attn µs/layer-call, spectral (K4) keys, 64k ctx, 1 MI355X"
+MFMA_FP16_DENSE_TFLOPS = 2500.0
+
+
+def run_spectral(args, torch, dev) -> dict:
+    """The spectral (K4) row: one decode call of one layer of Llama-3.1-8B
+    attention geometry (32 query / 8 KV heads, d 128) at --ctx tokens, window
+    --window, fp16 model, the k4 recipe at --spectral-budget on a synthetic
+    pack of the reference's form (orthonormal basis under a positive diagonal
+    weighting, power-law spectrum, bits by the reference's allocator), keys
+    drawn with that spectrum.  A call is PackedStreamingLayer.attend as the
+    reference runs a spectral step (its chunked path, packed_streaming.py:
+    1016-1032): the dequant kernel (tier codes -> Y_hat, Y_hat dec^T on MFMA,
+    RoPE, values; fp16 rows with the window after them), then one SDPA.
+    Beside it: the dequant kernel alone (its MFMA work over the coded
+    directions is the bound) and the dense fp16 decode of the same context."""
+    import math
+
+    from transformers import LlamaConfig
+
+    from bmx_amd import k2b, spectral
+    from bmx_amd.cache import PackedStreamingLayer
+    from bmx_amd.specs import spec_pair
+
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                      num_hidden_layers=32, rope_theta=500000.0)
+    C = H_KV * D
+    gen = torch.Generator().manual_seed(5)
+    E, _ = torch.linalg.qr(torch.randn(C, C, generator=gen, dtype=torch.float64))
+    w = 0.5 + torch.rand(C, generator=gen, dtype=torch.float64)
+    lam = torch.arange(1, C + 1, dtype=torch.float64) ** -2.0
+    lam *= C / lam.sum()
+    pack = spectral.SpectralPack(enc=(w.sqrt()[:, None] * E).float(), dec=(w.rsqrt()[:, None] * E).float(),
+                                 lam=lam.float(), bits=spectral.allocate_bits(lam, args.spectral_budget),
+                                 budget=args.spectral_budget)
+    k_spec, v_spec = spec_pair(f"k4_b{args.spectral_budget:g}", pack_path="synthetic")
+    lay = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=args.window, pack=pack)
+    N = args.ctx
+    dec = pack.dec.to(dev)
+    lam_d = lam.float().sqrt().to(dev)
+    g2 = torch.Generator(device=dev).manual_seed(6)
+    for lo in range(0, N, 8192):      # keys with the pack's spectrum, values random, in chunks
+        n = min(8192, N - lo)
+        z = torch.randn(n, C, generator=g2, device=dev) * lam_d
+        kp = (z @ dec.T).reshape(n, H_KV, D).half()
+        vv = torch.randn(1, H_KV, n, D, generator=g2, device=dev).half()
+        lay.stash_pre_rope(kp.unsqueeze(0))
+        lay.update(kp.transpose(0, 1).unsqueeze(0), vv)
+    torch.cuda.synchronize()
+    P = lay._committed_S_q
+    dp = lay._dp
+    q = torch.randn(H_KV * G, 1, D, generator=gen).half().to(dev)
+    scale = D ** -0.5
+    kt = lay._ktable[: P // 64]
+    vt = lay._table[0, : P // 16].contiguous()
+    Kb = torch.empty(H_KV, P, D, dtype=torch.float16, device=dev)
+    Vb = torch.empty_like(Kb)
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    reps = max(args.steps, 1)
+    call_us = timed(lambda: lay.attend(q, scale), reps)
+    deq_us = timed(lambda: spectral.dequant(dp, lay._kpool, kt, lay._pool, vt, P, lay._consts,
+                                            apply_rope=k2b.ROPE_FP16_TABLES, dtype=torch.float16,
+                                            out=(Kb, Vb)), reps)
+    c_used = pack.c_used
+    flops = 2.0 * P * c_used * C                            # Y_hat dec^T over the coded directions
+    page_bytes = P // 64 * dp.k_page_bytes + P // 16 * dp.v_page_bytes
+    out_bytes = 2 * P * C * 2
+    comp = {} if args.no_fp16_comparator else fp16_comparator(args, torch, dev, N, call_us)
+    # CPU: the oracle's restatement of the reference's chunked spectral step on
+    # a bounded sample (dequant of the sample's keys and values, RoPE, one
+    # softmax), scaled to the context
+    cpu = None
+    if not args.no_cpu_baseline:
+        import numpy as np
+
+        from oracle import attention as A
+        from oracle import codecs as OC
+        from oracle import spectral as O
+
+        S = 4096
+        L = O.Layout(pack.bits.numpy())
+        rng = np.random.default_rng(0)
+        codes = np.zeros((S // 64, 64, L.c_pad), np.int64)
+        for b in set(L.slice_bits.tolist()):
+            k = L.col_bits == b
+            codes[:, :, k] = rng.integers(-(1 << (b - 1)), 1 << (b - 1), (S // 64, 64, int(k.sum())))
+        steps = rng.random((S // 64, L.c_pad)).astype(np.float32) * 0.1
+        idx = torch.randint(0, 4, (S, C), dtype=torch.int16)
+        norms = torch.rand(S, H_KV) + 0.5
+        qf = q.float().cpu()
+        cos, sin = A.rope_cos_sin(torch.tensor(lay._consts.inv_freq), torch.arange(S))
+        threads = min(os.cpu_count() or 1, 16)
+        torch.set_num_threads(threads)
+
+        def cpu_step():
+            Kc = OC.from_matrix(torch.from_numpy(O.dequant(codes, steps, pack.dec.numpy(), L)).float(), H_KV)
+            Vc = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=H_KV), H_KV)
+            return A.naive_dense_attention(qf, A.apply_rope(Kc, cos, sin), Vc, G, scale)
+
+        cpu_step()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            cpu_step()
+            times.append(time.perf_counter() - t0)
+        t = statistics.median(times)
+        cpu = {"value": round(t * (P + args.window) / S * 1e6, 1), "unit": "us/layer-call", "cores": threads,
+               "kind": "port",
+               "sample": (f"1 layer, {S} committed tokens (h_kv 8, G 4, c_pad {L.c_pad}): the oracle's "
+                          f"spectral dequant (float64 Y_hat dec^T), value dequant, RoPE and one softmax, "
+                          f"median of 3 = {t * 1e3:.1f} ms, scaled x{(P + args.window) / S:.1f} tokens"),
+               "cpu_model": _cpu_model()}
+    return {
+        "metric": SPECTRAL_METRIC, "value": round(call_us, 2), "unit": "us/layer-call", "n_gpus": 1,
+        "steps": reps, "warmup": 3, "ms_per_step": round(call_us / 1e3, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": (f"k4_b{args.spectral_budget:g} decode call: {P} packed + "
+                                f"{N - P} fp16 window tokens, 32q/8kv heads, d 128, synthetic pack "
+                                f"(c_used {c_used} of {C}, c_pad {dp.c_pad}, {spectral.payload_bpe(pack.bits):.3f} "
+                                f"payload bpe keys)"),
+                   "ctx": N, "packed_tokens": P, "budget": args.spectral_budget, "c_used": c_used,
+                   "c_pad": dp.c_pad, "key_page_bytes": dp.k_page_bytes},
+        "roofline": {"bound": "mfma", "kernel": "spectral_dequant_kernel (pages -> dense fp16 K, V)",
+                     "achieved": round(flops / (deq_us * 1e-6) / 1e12, 1), "peak": MFMA_FP16_DENSE_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flops / (deq_us * 1e-6) / 1e12 / MFMA_FP16_DENSE_TFLOPS, 4),
+                     "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(deq_us, 3),
+                     "hbm_bytes_per_launch": page_bytes + out_bytes,
+                     "hbm_frac": round((page_bytes + out_bytes) / (deq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+        "spectral_call": {"dequant_us": round(deq_us, 2), "sdpa_and_window_us": round(call_us - deq_us, 2),
+                          "fp16_comparator": comp},
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -619,6 +769,9 @@ def main():
         return
     if args.workload == "batch":
         print(json.dumps(run_batch(args, torch, dev)), flush=True)
+        return
+    if args.workload == "spectral":
+        print(json.dumps(run_spectral(args, torch, dev)), flush=True)
         return
     if args.copy_calib_mib > 0:
         n = args.copy_calib_mib << 20

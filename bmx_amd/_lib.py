@@ -206,6 +206,7 @@ class SpectralDequantArgs(ct.Structure):
         ("out_dtype", ct.c_int32),
         ("k_out", ct.c_void_p),
         ("v_out", ct.c_void_p),
+        ("out_rows", ct.c_int32),
     ]
 
 

@@ -401,24 +401,40 @@ class PackedStreamingLayer(DynamicLayer):
                                  h_kv=self._h_kv, dtype=dt, **self._rtn)
             parts_k.append(kp)
             parts_v.append(vp)
-        elif P > 0 and self._path == "spectral":   # keys rotated at read, fp16 tables
-            kp, vp = spectral.dequant(self._dp, self._kpool, self._ktable[: P // spectral.GROUP], self._pool,
-                                      self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._consts,
-                                      apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt)
-            parts_k.append(kp)
-            parts_v.append(vp)
+        elif P > 0 and self._path == "spectral":
+            # keys rotated at read with the fp16 tables, written with room for
+            # the window after them (no second copy of the dequantized rows)
+            T = 0 if self.keys is None else self.keys.shape[2]
+            Kd = torch.empty(self._h_kv, P + T, self._d_head, dtype=dt, device=dev)
+            Vd = torch.empty_like(Kd)
+            spectral.dequant(self._dp, self._kpool, self._ktable[: P // spectral.GROUP], self._pool,
+                             self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._consts,
+                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt, out=(Kd, Vd))
+            if T:
+                Kd[:, P:].copy_(self.keys.squeeze(0))
+                Vd[:, P:].copy_(self.values.squeeze(0))
+            parts_k, parts_v = [Kd], [Vd]
         elif P > 0:
             kp, vp = k2b.dequant(self._pool, self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P,
                                  self._basis16, self._consts, h_kv=self._h_kv, rank=self._rank,
                                  apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt)
             parts_k.append(kp)
             parts_v.append(vp)
-        if self.keys is not None and self.keys.numel():
+        if self.keys is not None and self.keys.numel() and not (P > 0 and self._path == "spectral"):
             parts_k.append(self.keys.squeeze(0).to(dt))
             parts_v.append(self.values.squeeze(0).to(dt))
         Kd = torch.cat(parts_k, dim=1) if len(parts_k) > 1 else parts_k[0]
         Vd = torch.cat(parts_v, dim=1) if len(parts_v) > 1 else parts_v[0]
         n_q, n_kv = q.shape[1], Kd.shape[1]
+        if self._path == "spectral" and n_q == 1 and not causal and attention_mask is None:
+            # one query per head: two grouped products with fp32 outputs and one
+            # softmax (no G-fold copy of K and V; ROCm's grouped SDPA takes its
+            # slow path for a single query)
+            qt = q.reshape(self._h_kv, G, self._d_head).transpose(1, 2).contiguous()
+            s = torch.bmm(Kd, qt, out_dtype=torch.float32).transpose(1, 2).contiguous()   # (h_kv, G, n_kv)
+            p = torch.softmax(s * scaling, dim=-1).to(dt)
+            out = torch.bmm(p, Vd, out_dtype=torch.float32)                    # (h_kv, G, d)
+            return out.to(dt).reshape(self._h_kv * G, 1, self._d_head)
         if causal and attention_mask is None and n_q != n_kv:
             i = torch.arange(n_q, device=dev)[:, None]
             j = torch.arange(n_kv, device=dev)[None, :]

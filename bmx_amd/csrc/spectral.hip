@@ -108,7 +108,7 @@ __global__ __launch_bounds__(64) void spectral_encode_kernel(const SpEncodeKArgs
 }
 
 struct SpDequantKArgs {
-  int h_kv, c_pad, c_pad32, n_tokens, apply_rope, n_k_pool, n_v_pool, out_dtype, k_page_bytes;
+  int h_kv, c_pad, c_pad32, n_tokens, out_rows, apply_rope, n_k_pool, n_v_pool, out_dtype, k_page_bytes;
   const uint8_t* k_pages;
   const int32_t* k_table;
   const uint8_t* v_pages;
@@ -124,122 +124,175 @@ struct SpDequantKArgs {
   void* v_out;
 };
 
-// grid (n_tokens / 64, h_kv), block 256: the group's keys and values of one
-// head.  Wave w computes K^T rows 16w .. 16w + 15 and their RoPE partners
-// 64 + 16w .. (two 16-row tiles) for the group's 4 token tiles: per 32-column
-// step, A = dec rows (fp16, lane 16q + n: row n, columns 8q .. 8q + 7) and
-// B = Y_hat^T (lane 16q + n: token n of the tile, the 8 columns of slice
-// 4 step + q, code times step rounded to fp16), accumulated in fp32.  Then
-// RoPE on the lane's pairs (j, j + 64) and LDS-staged dense rows; the wave
-// then dequantizes value page 4 group + w.
-__global__ __launch_bounds__(256) void spectral_dequant_kernel(const SpDequantKArgs a) {
-  const int g = blockIdx.x, h = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
-  __shared__ uint32_t s_tab[kSpMaxSlices];
-  __shared__ DqTile s_tile[4];
-  const int n_sl = a.c_pad >> 3;
-  for (int i = tid; i < n_sl; i += 256) s_tab[i] = (uint32_t)a.slice_tab[i];
-  const uint8_t* page = a.k_pages + clamp_page(a.k_table[g], a.n_k_pool) * (int64_t)a.k_page_bytes;
-  const uint8_t* vpage = a.v_pages + clamp_page(a.v_table[4 * g + wave], a.n_v_pool) * (int64_t)a.VL.bytes;
-  const uint2 vcd = *reinterpret_cast<const uint2*>(vpage + a.VL.vcode + h * 512 + lane * 8);
-  const uint2 nrm = *reinterpret_cast<const uint2*>(vpage + a.VL.vnorm + (h * kPT + 4 * q) * 2);
-  __syncthreads();
+constexpr int kSpBRow = 40;   // halves per token row of the staged Y_hat tile (32 + 8 pad)
 
-  const uint16_t* dec0 = a.dec + ((int64_t)h * kD + 16 * wave + n) * a.c_pad32 + 8 * q;
-  const uint16_t* dec1 = dec0 + (int64_t)64 * a.c_pad32;
-  float4_t acc[2][4];
+// Workgroup barrier over LDS only: this wave's LDS accesses complete, then
+// s_barrier.  Global loads in flight stay in flight (__syncthreads would wait
+// for them too, and with them for the next step's prefetched dec rows).
+__device__ __forceinline__ void wave_lds_order() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// grid (n_tokens / 64), block 512: one 64-token group, wave w = head w.  Per
+// 32-column step the group's Y_hat^T tile (code times step, fp16) is decoded
+// once, by all 512 threads (4 codes each), into one of two LDS buffers; every
+// head's wave reads its B fragments from there (lane 16q + n: token n of the
+// tile, columns 8q .. 8q + 7) and multiplies with its dec rows (A, lane 16q + n:
+// row n of the tile, columns 8q ..; loaded a step ahead), 8 row tiles x 4 token
+// tiles in fp32.  The group's RoPE table is made once for all heads.  Then each
+// wave rotates its pairs (channels j, j + 64 in row tiles bb, bb + 4), stages
+// 16 rows at a time in LDS and writes them coalesced, and dequantizes its
+// head's 4 value pages.
+__global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKArgs a) {
+  const int g = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
+  const int h = wave;
+  const bool head_ok = h < a.h_kv;
+  __shared__ uint32_t s_tab[kSpMaxSlices];
+  __shared__ __align__(16) _Float16 s_b[2][kGroup][kSpBRow];
+  __shared__ float s_cs[2][kGroup][64];
+  __shared__ DqTile s_tile[8];
+  const int n_sl = a.c_pad >> 3;
+  for (int i = tid; i < n_sl; i += 512) s_tab[i] = (uint32_t)a.slice_tab[i];
+  const uint8_t* page = a.k_pages + clamp_page(a.k_table[g], a.n_k_pool) * (int64_t)a.k_page_bytes;
+  uint2 vcd[4], nrm[4];
+  if (head_ok) {
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) acc[r][tt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  const int n_steps = a.c_pad32 / 32;
-  for (int ks = 0; ks < n_steps; ++ks) {
-    const half8_t A0 = *reinterpret_cast<const half8_t*>(dec0 + 32 * ks);
-    const half8_t A1 = *reinterpret_cast<const half8_t*>(dec1 + 32 * ks);
-    const int s = 4 * ks + q;
-    half8_t B[4];
+    for (int pg = 0; pg < 4; ++pg) {
+      const uint8_t* vp = a.v_pages + clamp_page(a.v_table[4 * g + pg], a.n_v_pool) * (int64_t)a.VL.bytes;
+      vcd[pg] = *reinterpret_cast<const uint2*>(vp + a.VL.vcode + h * 512 + lane * 8);
+      nrm[pg] = *reinterpret_cast<const uint2*>(vp + a.VL.vnorm + (h * kPT + 4 * q) * 2);
+    }
+  }
+  if (a.apply_rope) {   // HF's fp32 angle fl(inv_freq_j * pos) of the group's 64 positions
+    for (int e = tid; e < kGroup * 64; e += 512) {
+      const int t = e >> 6, j = e & 63;
+      float sn, cn;
+      sincosf(a.inv_freq[j] * (float)(g * kGroup + t), &sn, &cn);
+      cn *= a.rope_scaling;
+      sn *= a.rope_scaling;
+      if (a.apply_rope == 2) {
+        cn = half_bits_to_float(float_to_half_bits(cn));
+        sn = half_bits_to_float(float_to_half_bits(sn));
+      }
+      s_cs[0][t][j] = cn;
+      s_cs[1][t][j] = sn;
+    }
+  }
+  __syncthreads();   // s_tab
+
+  // thread tid decodes codes 4 hf .. 4 hf + 3 of slice 4 step + sq, token t
+  const int dt = tid >> 3, dsq = (tid >> 1) & 3, dhf = tid & 1;
+  auto decode_b = [&](int ks, int buf) {
+    const int s = 4 * ks + dsq;
+    half4_t v = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
     if (s < n_sl) {
       const uint32_t tab = s_tab[s];
       const int b = (int)(tab >> 24), off = (int)(tab & 0xFFFFFFu), w = sp_width(b);
-      const uint4 sc = *reinterpret_cast<const uint4*>(page + 16 * s);
-      const uint32_t sw[4] = {sc.x, sc.y, sc.z, sc.w};
-      float scl[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        scl[2 * e] = half_bits_to_float(sw[e] & 0xffffu);
-        scl[2 * e + 1] = half_bits_to_float(sw[e] >> 16);
-      }
+      const uint2 sc = *reinterpret_cast<const uint2*>(page + 16 * s + 8 * dhf);
+      const int p = off + dt * w;
+      const uint2 cw = *reinterpret_cast<const uint2*>(page + (p & ~7));
+      const uint64_t word = ((((uint64_t)cw.y << 32) | cw.x) >> (8 * (p & 7))) >> (4 * dhf * w);
+      const uint64_t mask = (1ull << w) - 1ull;
       const float bias = (float)(1 << (b - 1));
-      const uint32_t mask = (1u << w) - 1u;
+      const float scl[4] = {half_bits_to_float(sc.x & 0xffffu), half_bits_to_float(sc.x >> 16),
+                            half_bits_to_float(sc.y & 0xffffu), half_bits_to_float(sc.y >> 16)};
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const uint8_t* p = page + off + (16 * tt + n) * w;
-        uint32_t lo, hi = 0u;
-        if (w == 8) {
-          const uint2 v = *reinterpret_cast<const uint2*>(p);
-          lo = v.x;
-          hi = v.y;
-        } else if (w == 4) {
-          lo = *reinterpret_cast<const uint32_t*>(p);
-        } else {
-          lo = *reinterpret_cast<const uint16_t*>(p);
-        }
+      for (int e = 0; e < 4; ++e)
+        v[e] = (_Float16)(((float)(uint32_t)((word >> (e * w)) & mask) - bias) * scl[e]);
+    }
+    *reinterpret_cast<half4_t*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) = v;
+  };
+
+  const uint16_t* decb = a.dec + ((int64_t)(head_ok ? h : 0) * kD + n) * a.c_pad32 + 8 * q;
+  const int64_t tile_stride = (int64_t)16 * a.c_pad32;
+  float4_t acc[8][4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          uint32_t code;
-          if (w == 8)
-            code = ((e < 4 ? lo : hi) >> (8 * (e & 3))) & 0xFFu;
-          else
-            code = (lo >> (e * w)) & mask;
-          B[tt][e] = (_Float16)(((float)code - bias) * scl[e]);
-        }
+  for (int bt = 0; bt < 8; ++bt)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) acc[bt][tt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  const int n_steps = a.c_pad32 / 32;
+  half8_t An[8];
+  if (head_ok) {
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt) An[bt] = *reinterpret_cast<const half8_t*>(decb + bt * tile_stride);
+  }
+  decode_b(0, 0);
+  __syncthreads();
+  for (int ks = 0; ks < n_steps; ++ks) {
+    const int buf = ks & 1;
+    if (ks + 1 < n_steps) decode_b(ks + 1, buf ^ 1);   // that buffer was last read in step ks - 1
+    if (head_ok) {
+      half8_t A[8];
+#pragma unroll
+      for (int bt = 0; bt < 8; ++bt) A[bt] = An[bt];
+      if (ks + 1 < n_steps) {
+#pragma unroll
+        for (int bt = 0; bt < 8; ++bt)
+          An[bt] = *reinterpret_cast<const half8_t*>(decb + bt * tile_stride + 32 * (ks + 1));
       }
-    } else {
+      half8_t B[4];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int tt = 0; tt < 4; ++tt) B[tt] = *reinterpret_cast<const half8_t*>(&s_b[buf][16 * tt + n][8 * q]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) B[tt][e] = (_Float16)0.f;
+      for (int bt = 0; bt < 8; ++bt)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          acc[bt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[bt], B[tt], acc[bt][tt], 0, 0, 0);
     }
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      acc[0][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B[tt], acc[0][tt], 0, 0, 0);
-      acc[1][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B[tt], acc[1][tt], 0, 0, 0);
-    }
+    lds_barrier();   // buffer buf ^ 1 written, buffer buf read by every wave
   }
 
-  // RoPE of the lane's pairs: channel j = 16w + 4q + i and j + 64, token
-  // 16tt + n, HF's fp32 angle fl(inv_freq_j * pos)
-  const int pos0 = g * kGroup;
+  // keys: RoPE of the lane's pairs, channel j = 16bb + 4q + i and j + 64, token
+  // 16tt + n; 16 rows staged per token tile.  Each wave stages through its own
+  // tile only: no workgroup barrier from here on (a wave's LDS accesses take
+  // effect in program order; wave_lds_order keeps the compiler from moving
+  // them and waits for them)
+  DqTile& tl = s_tile[wave];
+  const int64_t row_h = (int64_t)(head_ok ? h : 0) * a.out_rows + g * kGroup;
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
+    if (head_ok) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 16 * wave + 4 * q + i;
-      float k0 = acc[0][tt][i], k1 = acc[1][tt][i];
-      if (a.apply_rope) {
-        float sn, cn;
-        sincosf(a.inv_freq[j] * (float)(pos0 + 16 * tt + n), &sn, &cn);
-        cn *= a.rope_scaling;
-        sn *= a.rope_scaling;
-        if (a.apply_rope == 2) {
-          cn = half_bits_to_float(float_to_half_bits(cn));
-          sn = half_bits_to_float(float_to_half_bits(sn));
+      for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = 16 * bb + 4 * q + i;
+          float k0 = acc[bb][tt][i], k1 = acc[bb + 4][tt][i];
+          if (a.apply_rope) {
+            const float cn = s_cs[0][16 * tt + n][j], sn = s_cs[1][16 * tt + n][j];
+            const float r0 = __fmul_rn(k0, cn) - __fmul_rn(k1, sn);
+            k1 = __fmul_rn(k1, cn) + __fmul_rn(k0, sn);
+            k0 = r0;
+          }
+          tl.v[n][j] = k0;
+          tl.v[n][j + 64] = k1;
         }
-        const float r0 = __fmul_rn(k0, cn) - __fmul_rn(k1, sn);
-        k1 = __fmul_rn(k1, cn) + __fmul_rn(k0, sn);
-        k0 = r0;
-      }
-      s_tile[tt].v[n][j] = k0;
-      s_tile[tt].v[n][j + 64] = k1;
+      wave_lds_order();
+      dq_store_tile(tl, a.k_out, row_h + 16 * tt, a.out_dtype);
+      wave_lds_order();
     }
   }
-  __syncthreads();
-  const int64_t row0 = (int64_t)h * a.n_tokens + pos0 + 16 * wave;
-  dq_store_tile(s_tile[wave], a.k_out, row0, a.out_dtype);
-  __syncthreads();   // the staging tiles are reused for the values
-  dq_value_tile(vcd, nrm, a.codebook, a.v_sign_bits, n, q, s_tile[wave]);
-  __syncthreads();
-  dq_store_tile(s_tile[wave], a.v_out, row0, a.out_dtype);
+  // values: the head's 4 pages of the group
+  if (head_ok) {
+#pragma unroll
+    for (int pg = 0; pg < 4; ++pg) {
+      dq_value_tile(vcd[pg], nrm[pg], a.codebook, a.v_sign_bits, n, q, tl);
+      wave_lds_order();
+      dq_store_tile(tl, a.v_out, row_h + 16 * pg, a.out_dtype);
+      wave_lds_order();
+    }
+  }
 }
 
 static PageLayout value_layout(int h_kv) {
@@ -324,12 +377,14 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   if (a->n_tokens == 0) return BMX_OK;
   if (a->apply_rope < 0 || a->apply_rope > 2) return sp_fail(fn, "apply_rope must be 0, 1 or 2");
   if (!dtype_ok(a->out_dtype)) return sp_fail(fn, "out_dtype must be BMX_K2B_F16, _F32 or _BF16");
+  if (a->out_rows != 0 && a->out_rows < a->n_tokens) return sp_fail(fn, "out_rows must be 0 or >= n_tokens");
   if (!a->k_pages || !a->k_page_table || !a->v_pages || !a->v_page_table || !a->dec_perm || !a->k_out ||
       !a->v_out || a->n_k_pool < 1 || a->n_v_pool < 1)
     return sp_fail(fn, "null pointer argument or empty pool");
   SpDequantKArgs k{};
   k.h_kv = a->L.h_kv; k.c_pad = a->L.c_pad; k.c_pad32 = (a->L.c_pad + 31) / 32 * 32;
-  k.n_tokens = a->n_tokens; k.apply_rope = a->apply_rope; k.n_k_pool = a->n_k_pool; k.n_v_pool = a->n_v_pool;
+  k.n_tokens = a->n_tokens; k.out_rows = a->out_rows ? a->out_rows : a->n_tokens;
+  k.apply_rope = a->apply_rope; k.n_k_pool = a->n_k_pool; k.n_v_pool = a->n_v_pool;
   k.out_dtype = a->out_dtype; k.k_page_bytes = a->L.k_page_bytes;
   k.k_pages = a->k_pages; k.k_table = a->k_page_table; k.v_pages = a->v_pages; k.v_table = a->v_page_table;
   k.slice_tab = a->L.slice_tab; k.dec = a->dec_perm; k.VL = value_layout(a->L.h_kv);
@@ -337,8 +392,7 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   for (int j = 0; j < 64; ++j) k.inv_freq[j] = a->inv_freq[j];
   for (int i = 0; i < 4; ++i) { k.codebook[i] = a->v_codebook[i]; k.v_sign_bits[i] = a->v_sign_bits[i]; }
   k.k_out = a->k_out; k.v_out = a->v_out;
-  hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup, a->L.h_kv), dim3(256), 0,
-                     (hipStream_t)stream, k);
+  hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512), 0, (hipStream_t)stream, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     bmx_set_error(std::string(fn) + ": launch: " + hipGetErrorString(e));

@@ -200,7 +200,9 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     """Pages of one sequence -> dense (K, V), each (h_kv, n_tokens, 128) in
     dtype; keys pre-RoPE (ROPE_NONE) or rotated at read (ROPE_EXACT: fp32
     cos/sin, ROPE_FP16_TABLES: the reference's fp16 tables).  ``out`` takes
-    preallocated (K, V) of that shape and dtype."""
+    preallocated contiguous (K, V) of shape (h_kv, R, 128), R >= n_tokens, in
+    dtype: rows 0 .. n_tokens - 1 of each head are written, the rest left to
+    the caller (the recent window of a decode step)."""
     dev = k_pages.device
     _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
     _need(n_tokens % GROUP == 0, "n_tokens must be a multiple of 64")
@@ -211,8 +213,9 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
         v = torch.empty_like(k)
     else:
         k, v = out
-        _need(k.dtype == dtype and tuple(k.shape) == (dp.h_kv, n_tokens, HEAD_DIM) and k.is_contiguous()
-              and v.dtype == dtype and v.shape == k.shape and v.is_contiguous(), "out tensors")
+        _need(k.dtype == dtype and k.shape[0] == dp.h_kv and k.shape[1] >= n_tokens and k.shape[2] == HEAD_DIM
+              and k.is_contiguous() and v.dtype == dtype and v.shape == k.shape and v.is_contiguous(),
+              "out tensors: contiguous (h_kv, >= n_tokens, 128) in dtype")
     a = _lib.SpectralDequantArgs()
     a.L = dp.layout()
     a.n_tokens = int(n_tokens)
@@ -226,5 +229,6 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     a.v_sign_bits[:] = consts.sign_bits
     a.out_dtype = _V_DTYPES[dtype]
     a.k_out, a.v_out = _ptr(k), _ptr(v)
+    a.out_rows = k.shape[1]
     _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
     return k, v

@@ -93,8 +93,10 @@ typedef struct bmx_spectral_dequant_args {
   float v_codebook[4];
   uint32_t v_sign_bits[4];
   int32_t out_dtype;           /* BMX_K2B_F16, _F32 or _BF16 */
-  void* k_out;
+  void* k_out;                 /* [h_kv][out_rows][128]: rows 0 .. n_tokens - 1 of each head written */
   void* v_out;
+  int32_t out_rows;            /* rows per head in k_out / v_out, >= n_tokens (0: n_tokens); the
+                                  rows after n_tokens are left for the caller (the recent window) */
 } bmx_spectral_dequant_args;
 
 int64_t bmx_spectral_v_page_bytes(int32_t h_kv);
