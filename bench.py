@@ -609,8 +609,10 @@ def run_spectral(args, torch, dev) -> dict:
     weighting, power-law spectrum, bits by the reference's allocator), keys
     drawn with that spectrum.  A call is PackedStreamingLayer.attend as the
     reference runs a spectral step (its chunked path, packed_streaming.py:
-    1016-1032): the dequant kernel (tier codes -> Y_hat, Y_hat dec^T on MFMA,
-    RoPE, values; fp16 rows with the window after them), then one SDPA.
+    1016-1032, every page dequantized): the dequant kernel's decode form (tier
+    codes -> Y_hat, Y_hat dec^T on MFMA, RoPE, the scores against the step's
+    queries on MFMA, dense fp16 values with the window after them), the
+    window's scores, one softmax and the value product.
     Beside it: the dequant kernel alone (its MFMA work over the coded
     directions is the bound) and the dense fp16 decode of the same context."""
     import math
@@ -652,8 +654,9 @@ def run_spectral(args, torch, dev) -> dict:
     scale = D ** -0.5
     kt = lay._ktable[: P // 64]
     vt = lay._table[0, : P // 16].contiguous()
-    Kb = torch.empty(H_KV, P, D, dtype=torch.float16, device=dev)
-    Vb = torch.empty_like(Kb)
+    Vb = torch.empty(H_KV, P, D, dtype=torch.float16, device=dev)
+    Sb = torch.empty(H_KV, G, P, dtype=torch.float32, device=dev)
+    qg = q.reshape(H_KV, G, D).contiguous()
 
     def timed(fn, reps):
         for _ in range(3):
@@ -671,11 +674,11 @@ def run_spectral(args, torch, dev) -> dict:
     call_us = timed(lambda: lay.attend(q, scale), reps)
     deq_us = timed(lambda: spectral.dequant(dp, lay._kpool, kt, lay._pool, vt, P, lay._consts,
                                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=torch.float16,
-                                            out=(Kb, Vb)), reps)
+                                            out=(None, Vb), q=qg, scores=Sb), reps)
     c_used = pack.c_used
     flops = 2.0 * P * c_used * C                            # Y_hat dec^T over the coded directions
     page_bytes = P // 64 * dp.k_page_bytes + P // 16 * dp.v_page_bytes
-    out_bytes = 2 * P * C * 2
+    out_bytes = P * C * 2 + H_KV * G * P * 4          # dense fp16 values and fp32 scores
     comp = {} if args.no_fp16_comparator else fp16_comparator(args, torch, dev, N, call_us)
     # CPU: the oracle's restatement of the reference's chunked spectral step on
     # a bounded sample (dequant of the sample's keys and values, RoPE, one
@@ -731,7 +734,7 @@ def run_spectral(args, torch, dev) -> dict:
                                 f"payload bpe keys)"),
                    "ctx": N, "packed_tokens": P, "budget": args.spectral_budget, "c_used": c_used,
                    "c_pad": dp.c_pad, "key_page_bytes": dp.k_page_bytes},
-        "roofline": {"bound": "mfma", "kernel": "spectral_dequant_kernel (pages -> dense fp16 K, V)",
+        "roofline": {"bound": "mfma", "kernel": "spectral_dequant_kernel, decode form (pages -> scores, dense fp16 V)",
                      "achieved": round(flops / (deq_us * 1e-6) / 1e12, 1), "peak": MFMA_FP16_DENSE_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (deq_us * 1e-6) / 1e12 / MFMA_FP16_DENSE_TFLOPS, 4),
                      "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(deq_us, 3),

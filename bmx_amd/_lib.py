@@ -207,6 +207,10 @@ class SpectralDequantArgs(ct.Structure):
         ("k_out", ct.c_void_p),
         ("v_out", ct.c_void_p),
         ("out_rows", ct.c_int32),
+        ("q", ct.c_void_p),
+        ("q_dtype", ct.c_int32),
+        ("n_q_groups", ct.c_int32),
+        ("scores", ct.c_void_p),
     ]
 
 

@@ -347,7 +347,9 @@ class PackedStreamingLayer(DynamicLayer):
             raise RuntimeError("the packed cache attends on a HIP device only (no CPU path)")
         n_heads, n_q, d = q.shape
         G = n_heads // self._h_kv
-        if n_q == 1 and not is_causal and self._path != "spectral":
+        if n_q == 1 and not is_causal:
+            if self._path == "spectral":
+                return self._decode_spectral(q, scaling, G)
             return self._decode(q, scaling, G)
         return self._dense(q, scaling, G, is_causal and n_q > 1, attention_mask)
 
@@ -382,6 +384,32 @@ class PackedStreamingLayer(DynamicLayer):
             k_tail=k_tail, v_tail=v_tail,
             tail_len=torch.tensor([T], dtype=torch.int32, device=dev), tail_cap=T)
         return out.reshape(self._h_kv * G, 1, self._d_head)
+
+    def _decode_spectral(self, q: torch.Tensor, scaling: float, G: int) -> torch.Tensor:
+        """One decode step of the spectral arm: the reference's chunked step
+        (every committed page dequantized, packed_streaming.py:1016-1032) with
+        the scores taken in the dequant kernel from the rotated keys (no dense
+        keys written), the window's scores from one grouped product, one
+        softmax and the value product with fp32 outputs (ROCm's grouped SDPA
+        takes a slow path for a single query)."""
+        dev, dt = q.device, q.dtype
+        h, d = self._h_kv, self._d_head
+        P = self._committed_S_q
+        T = 0 if self.keys is None else self.keys.shape[2]
+        qg = q.reshape(h, G, d).contiguous()
+        S = torch.empty(h, G, P + T, dtype=torch.float32, device=dev)
+        Vd = torch.empty(h, P + T, d, dtype=dt, device=dev)
+        if P > 0:
+            spectral.dequant(self._dp, self._kpool, self._ktable[: P // spectral.GROUP], self._pool,
+                             self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._consts,
+                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt, out=(None, Vd), q=qg, scores=S)
+        if T:
+            kw = self.keys.squeeze(0).to(dt)
+            S[:, :, P:] = torch.bmm(kw, qg.transpose(1, 2).contiguous(), out_dtype=torch.float32).transpose(1, 2)
+            Vd[:, P:].copy_(self.values.squeeze(0))
+        p = torch.softmax(S * scaling, dim=-1).to(dt)
+        out = torch.bmm(p, Vd, out_dtype=torch.float32)
+        return out.to(dt).reshape(h * G, 1, d)
 
     def _dense(self, q, scaling, G, causal, attention_mask):
         """Prefill (n_q > 1): _prefill_dense_attention (chunked_attention.py:
@@ -426,15 +454,6 @@ class PackedStreamingLayer(DynamicLayer):
         Kd = torch.cat(parts_k, dim=1) if len(parts_k) > 1 else parts_k[0]
         Vd = torch.cat(parts_v, dim=1) if len(parts_v) > 1 else parts_v[0]
         n_q, n_kv = q.shape[1], Kd.shape[1]
-        if self._path == "spectral" and n_q == 1 and not causal and attention_mask is None:
-            # one query per head: two grouped products with fp32 outputs and one
-            # softmax (no G-fold copy of K and V; ROCm's grouped SDPA takes its
-            # slow path for a single query)
-            qt = q.reshape(self._h_kv, G, self._d_head).transpose(1, 2).contiguous()
-            s = torch.bmm(Kd, qt, out_dtype=torch.float32).transpose(1, 2).contiguous()   # (h_kv, G, n_kv)
-            p = torch.softmax(s * scaling, dim=-1).to(dt)
-            out = torch.bmm(p, Vd, out_dtype=torch.float32)                    # (h_kv, G, d)
-            return out.to(dt).reshape(self._h_kv * G, 1, self._d_head)
         if causal and attention_mask is None and n_q != n_kv:
             i = torch.arange(n_q, device=dev)[:, None]
             j = torch.arange(n_kv, device=dev)[None, :]

@@ -122,6 +122,9 @@ struct SpDequantKArgs {
   uint32_t v_sign_bits[4];
   void* k_out;
   void* v_out;
+  const void* q;
+  int q_dtype, n_q_groups;
+  float* scores;
 };
 
 constexpr int kSpBRow = 40;   // halves per token row of the staged Y_hat tile (32 + 8 pad)
@@ -253,6 +256,22 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     lds_barrier();   // buffer buf ^ 1 written, buffer buf read by every wave
   }
 
+  // query fragments (decode form), loaded after the main loop: the MFMA B operand of the scores, lane
+  // 16q + n: query n, K index 8q + 2i + e = channel 16bb + 4q + i + 64e
+  half8_t qf[4];
+  const bool scoring = a.q != nullptr;
+  if (scoring && head_ok) {
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int c = 16 * bb + 4 * q + i + 64 * e;
+          const float v = n < a.n_q_groups ? sp_load(a.q, ((int64_t)h * a.n_q_groups + n) * kD + c, a.q_dtype) : 0.f;
+          qf[bb][2 * i + e] = (_Float16)v;
+        }
+  }
   // keys: RoPE of the lane's pairs, channel j = 16bb + 4q + i and j + 64, token
   // 16tt + n; 16 rows staged per token tile.  Each wave stages through its own
   // tile only: no workgroup barrier from here on (a wave's LDS accesses take
@@ -263,8 +282,10 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
     if (head_ok) {
+      float4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int bb = 0; bb < 4; ++bb)
+      for (int bb = 0; bb < 4; ++bb) {
+        half8_t ka;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int j = 16 * bb + 4 * q + i;
@@ -277,10 +298,22 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
           }
           tl.v[n][j] = k0;
           tl.v[n][j + 64] = k1;
+          ka[2 * i] = (_Float16)k0;
+          ka[2 * i + 1] = (_Float16)k1;
         }
-      wave_lds_order();
-      dq_store_tile(tl, a.k_out, row_h + 16 * tt, a.out_dtype);
-      wave_lds_order();
+        // scores: A = the tile's rotated keys (token n, K index 8q + 2i + e)
+        if (scoring) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[bb], sc, 0, 0, 0);
+      }
+      if (scoring && n < a.n_q_groups) {   // lane 16q + n: tokens 4q .. 4q + 3, query n
+        float* dst = a.scores + ((int64_t)h * a.n_q_groups + n) * a.out_rows + g * kGroup + 16 * tt + 4 * q;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = sc[i];
+      }
+      if (a.k_out) {
+        wave_lds_order();
+        dq_store_tile(tl, a.k_out, row_h + 16 * tt, a.out_dtype);
+        wave_lds_order();
+      }
     }
   }
   // values: the head's 4 pages of the group
@@ -378,9 +411,11 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   if (a->apply_rope < 0 || a->apply_rope > 2) return sp_fail(fn, "apply_rope must be 0, 1 or 2");
   if (!dtype_ok(a->out_dtype)) return sp_fail(fn, "out_dtype must be BMX_K2B_F16, _F32 or _BF16");
   if (a->out_rows != 0 && a->out_rows < a->n_tokens) return sp_fail(fn, "out_rows must be 0 or >= n_tokens");
-  if (!a->k_pages || !a->k_page_table || !a->v_pages || !a->v_page_table || !a->dec_perm || !a->k_out ||
-      !a->v_out || a->n_k_pool < 1 || a->n_v_pool < 1)
+  if (!a->k_pages || !a->k_page_table || !a->v_pages || !a->v_page_table || !a->dec_perm || !a->v_out ||
+      (!a->k_out && !a->q) || a->n_k_pool < 1 || a->n_v_pool < 1)
     return sp_fail(fn, "null pointer argument or empty pool");
+  if (a->q && (!a->scores || a->n_q_groups < 1 || a->n_q_groups > 16 || !dtype_ok(a->q_dtype) || !a->apply_rope))
+    return sp_fail(fn, "the decode form needs scores, n_q_groups 1..16, a q_dtype and apply_rope");
   SpDequantKArgs k{};
   k.h_kv = a->L.h_kv; k.c_pad = a->L.c_pad; k.c_pad32 = (a->L.c_pad + 31) / 32 * 32;
   k.n_tokens = a->n_tokens; k.out_rows = a->out_rows ? a->out_rows : a->n_tokens;
@@ -392,6 +427,7 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   for (int j = 0; j < 64; ++j) k.inv_freq[j] = a->inv_freq[j];
   for (int i = 0; i < 4; ++i) { k.codebook[i] = a->v_codebook[i]; k.v_sign_bits[i] = a->v_sign_bits[i]; }
   k.k_out = a->k_out; k.v_out = a->v_out;
+  k.q = a->q; k.q_dtype = a->q_dtype; k.n_q_groups = a->n_q_groups; k.scores = a->scores;
   hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512), 0, (hipStream_t)stream, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -196,13 +196,19 @@ def append(k_pre: torch.Tensor, v: torch.Tensor, dp: DevicePack, k_pages: torch.
 
 def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_pages: torch.Tensor,
             v_table: torch.Tensor, n_tokens: int, consts: CodecConsts, *, apply_rope: int = ROPE_NONE,
-            dtype: torch.dtype = torch.float32, out: tuple | None = None):
+            dtype: torch.dtype = torch.float32, out: tuple | None = None, q: torch.Tensor | None = None,
+            scores: torch.Tensor | None = None):
     """Pages of one sequence -> dense (K, V), each (h_kv, n_tokens, 128) in
     dtype; keys pre-RoPE (ROPE_NONE) or rotated at read (ROPE_EXACT: fp32
     cos/sin, ROPE_FP16_TABLES: the reference's fp16 tables).  ``out`` takes
     preallocated contiguous (K, V) of shape (h_kv, R, 128), R >= n_tokens, in
     dtype: rows 0 .. n_tokens - 1 of each head are written, the rest left to
-    the caller (the recent window of a decode step)."""
+    the caller (the recent window of a decode step).
+
+    Decode form: with q (h_kv, G, 128) the kernel also writes scores
+    (h_kv, G, R) fp32, q . k of the rotated keys for rows 0 .. n_tokens - 1
+    (no softmax scale); out may then be (None, V) and no dense keys are
+    written."""
     dev = k_pages.device
     _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
     _need(n_tokens % GROUP == 0, "n_tokens must be a multiple of 64")
@@ -213,9 +219,16 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
         v = torch.empty_like(k)
     else:
         k, v = out
-        _need(k.dtype == dtype and k.shape[0] == dp.h_kv and k.shape[1] >= n_tokens and k.shape[2] == HEAD_DIM
-              and k.is_contiguous() and v.dtype == dtype and v.shape == k.shape and v.is_contiguous(),
+        _need(v.dtype == dtype and v.shape[0] == dp.h_kv and v.shape[1] >= n_tokens and v.shape[2] == HEAD_DIM
+              and v.is_contiguous() and (k is None or (k.shape == v.shape and k.dtype == dtype and k.is_contiguous())),
               "out tensors: contiguous (h_kv, >= n_tokens, 128) in dtype")
+        _need(k is not None or q is not None, "keys may be left out only in the decode form (q given)")
+    if q is not None:
+        _need(q.dim() == 3 and q.shape[0] == dp.h_kv and q.shape[2] == HEAD_DIM and 1 <= q.shape[1] <= 16
+              and q.is_contiguous() and q.dtype in _V_DTYPES, "q must be contiguous (h_kv, 1..16, 128)")
+        _need(scores is not None and scores.dtype == torch.float32 and scores.is_contiguous()
+              and tuple(scores.shape) == (dp.h_kv, q.shape[1], v.shape[1]), "scores must be fp32 (h_kv, G, rows)")
+        _need(int(apply_rope) != ROPE_NONE, "the decode form scores rotated keys")
     a = _lib.SpectralDequantArgs()
     a.L = dp.layout()
     a.n_tokens = int(n_tokens)
@@ -229,6 +242,8 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     a.v_sign_bits[:] = consts.sign_bits
     a.out_dtype = _V_DTYPES[dtype]
     a.k_out, a.v_out = _ptr(k), _ptr(v)
-    a.out_rows = k.shape[1]
+    a.out_rows = v.shape[1]
+    if q is not None:
+        a.q, a.q_dtype, a.n_q_groups, a.scores = _ptr(q), _V_DTYPES[q.dtype], q.shape[1], _ptr(scores)
     _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
     return k, v

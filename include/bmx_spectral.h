@@ -95,8 +95,17 @@ typedef struct bmx_spectral_dequant_args {
   int32_t out_dtype;           /* BMX_K2B_F16, _F32 or _BF16 */
   void* k_out;                 /* [h_kv][out_rows][128]: rows 0 .. n_tokens - 1 of each head written */
   void* v_out;
-  int32_t out_rows;            /* rows per head in k_out / v_out, >= n_tokens (0: n_tokens); the
-                                  rows after n_tokens are left for the caller (the recent window) */
+  int32_t out_rows;            /* rows per head in k_out / v_out / scores, >= n_tokens (0: n_tokens);
+                                  the rows after n_tokens are left for the caller (the recent window) */
+  /* Decode form: with q set, the kernel also scores the rotated keys against
+   * the step's queries, scores[h][g][t] = q[h][g] . k_rot[h][t] (fp32
+   * accumulation of fp16 keys and queries, no softmax scale), for rows
+   * 0 .. n_tokens - 1; k_out may then be NULL (no dense keys written).
+   * Requires apply_rope != 0. */
+  const void* q;               /* [h_kv][n_q_groups][128], dtype q_dtype, or NULL */
+  int32_t q_dtype;             /* BMX_K2B_F16, _F32 or _BF16 */
+  int32_t n_q_groups;          /* 1..16 */
+  float* scores;               /* [h_kv][n_q_groups][out_rows] fp32 */
 } bmx_spectral_dequant_args;
 
 int64_t bmx_spectral_v_page_bytes(int32_t h_kv);

@@ -158,3 +158,40 @@ def test_attention_over_dequantized_pages():
     rel = ((o - ref.double()).norm() / ref.double().norm()).item()
     print(f"attention over spectral pages: max_abs {err:.3e} rel {rel:.3e}", flush=True)
     assert err <= 2e-3 and rel <= 1e-2
+
+
+def test_decode_form_scores_match_keys():
+    """The decode form's scores equal q . k of the kernel's own rotated keys
+    (fp16 keys and queries, fp32 accumulation) and of the oracle's keys, for
+    G 1 and 4 and a buffer with rows left for a window; its values equal the
+    keys-and-values form's."""
+    pack = synthetic_pack(8, 2.5, seed=11)
+    S, extra = 512, 24
+    M = synthetic_keys(pack, S, seed=12)
+    gen = torch.Generator().manual_seed(13)
+    v = torch.randn(8, S, 128, generator=gen)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    dp, kp, vp, k_ids, v_ids = _write(pack, 8, M, v, consts, shuffle_seed=3)
+    K, V = spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=k2b.ROPE_FP16_TABLES,
+                            dtype=torch.float16)
+    L = O.Layout(pack.bits.numpy())
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)).float(), 8)
+    from bmx_amd.cache import _rope_tables
+
+    c16, s16 = _rope_tables(torch.tensor(consts.inv_freq), consts.rope_scaling, 0, S, "cpu")
+    K_or = K_or * c16.float() + torch.cat((-K_or[..., 64:], K_or[..., :64]), -1) * s16.float()
+    for G in (1, 4):
+        q = torch.randn(8, G, 128, generator=gen).half()
+        Vb = torch.zeros(8, S + extra, 128, dtype=torch.float16, device=DEV)
+        Sb = torch.zeros(8, G, S + extra, dtype=torch.float32, device=DEV)
+        spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=k2b.ROPE_FP16_TABLES,
+                         dtype=torch.float16, out=(None, Vb), q=q.to(DEV), scores=Sb)
+        own = torch.bmm(q.float().to(DEV), K.float().transpose(1, 2).contiguous())
+        d_own = (Sb[:, :, :S] - own).abs().max().item()
+        want = q.float() @ K_or.transpose(1, 2)
+        d_or = (Sb[:, :, :S].cpu() - want).abs().max().item()
+        smax = want.abs().max().item()
+        print(f"G {G}: scores vs own keys {d_own:.3e}, vs oracle keys {d_or:.3e} (max {smax:.2f})", flush=True)
+        assert d_own <= 1e-5 * smax and d_or <= 3e-3 * smax
+        assert torch.equal(Vb[:, :S], V) and not Vb[:, S:].any() and not Sb[:, :, S:].any()
