@@ -34,13 +34,14 @@ METRIC = "decode-attn µs/step + % HBM roofline, k2b 3.0 bpe, 64k ctx, 1 MI355X"
 HBM_PEAK_GBS = 8000.0
 H_KV, G, D = 8, 4, 128
 TRAFFIC_FILE = Path(__file__).resolve().parent / "profiles" / "k2b_decode_traffic.json"
+SPECTRAL_TRAFFIC_FILE = Path(__file__).resolve().parent / "profiles" / "spectral_dequant_traffic.json"
 
 
-def measured_traffic(workload: dict):
+def measured_traffic(workload: dict, path: Path = TRAFFIC_FILE):
     """HBM bytes per decode call from the committed rocprofv3 PMC summary, if it
     was taken on this exact workload (else None)."""
     try:
-        rec = json.loads(TRAFFIC_FILE.read_text())
+        rec = json.loads(path.read_text())
     except (OSError, ValueError):
         return None
     if rec.get("workload") != workload:
@@ -737,7 +738,9 @@ def run_spectral(args, torch, dev) -> dict:
         "roofline": {"bound": "mfma", "kernel": "spectral_dequant_kernel, decode form (pages -> scores, dense fp16 V)",
                      "achieved": round(flops / (deq_us * 1e-6) / 1e12, 1), "peak": MFMA_FP16_DENSE_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (deq_us * 1e-6) / 1e12 / MFMA_FP16_DENSE_TFLOPS, 4),
-                     "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(deq_us, 3),
+                     "traffic": measured_traffic({"ctx": N, "window": args.window, "budget": args.spectral_budget,
+                                                  "c_pad": dp.c_pad}, SPECTRAL_TRAFFIC_FILE),
+                     "flops_per_launch": flops, "avg_launch_us": round(deq_us, 3),
                      "hbm_bytes_per_launch": page_bytes + out_bytes,
                      "hbm_frac": round((page_bytes + out_bytes) / (deq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
         "spectral_call": {"dequant_us": round(deq_us, 2), "sdpa_and_window_us": round(call_us - deq_us, 2),
@@ -761,6 +764,13 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.copy_calib_mib > 0:
+        n = args.copy_calib_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.workload == "stream":
         print(json.dumps(run_stream(args, torch, k2b, synth, dev)), flush=True)
         return
@@ -776,13 +786,6 @@ def main():
     if args.workload == "spectral":
         print(json.dumps(run_spectral(args, torch, dev)), flush=True)
         return
-    if args.copy_calib_mib > 0:
-        n = args.copy_calib_mib << 20
-        src = torch.ones(n, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     W = args.window
     packed = ((args.ctx - W) // 128) * 128
     tail = args.ctx - packed
