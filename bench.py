@@ -610,10 +610,10 @@ def run_spectral(args, torch, dev) -> dict:
     weighting, power-law spectrum, bits by the reference's allocator), keys
     drawn with that spectrum.  A call is PackedStreamingLayer.attend as the
     reference runs a spectral step (its chunked path, packed_streaming.py:
-    1016-1032, every page dequantized): the dequant kernel's decode form (tier
+    1016-1032, every page dequantized): the dequant kernel's partial form (tier
     codes -> Y_hat, Y_hat dec^T on MFMA, RoPE, the scores against the step's
-    queries on MFMA, dense fp16 values with the window after them), the
-    window's scores, one softmax and the value product.
+    queries and the weights times the dequantized values on MFMA, one softmax
+    partial per 64-token group), the window's partial and the merge.
     Beside it: the dequant kernel alone (its MFMA work over the coded
     directions is the bound) and the dense fp16 decode of the same context."""
     import math
@@ -673,13 +673,14 @@ def run_spectral(args, torch, dev) -> dict:
 
     reps = max(args.steps, 1)
     call_us = timed(lambda: lay.attend(q, scale), reps)
+    Pb = torch.empty(H_KV, G, P // 64, 130, dtype=torch.float32, device=dev)
     deq_us = timed(lambda: spectral.dequant(dp, lay._kpool, kt, lay._pool, vt, P, lay._consts,
                                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=torch.float16,
-                                            out=(None, Vb), q=qg, scores=Sb), reps)
+                                            q=qg, partials=Pb, sm_scale=scale), reps)
     c_used = pack.c_used
     flops = 2.0 * P * c_used * C                            # Y_hat dec^T over the coded directions
     page_bytes = P // 64 * dp.k_page_bytes + P // 16 * dp.v_page_bytes
-    out_bytes = P * C * 2 + H_KV * G * P * 4          # dense fp16 values and fp32 scores
+    out_bytes = H_KV * G * (P // 64) * 130 * 4        # the groups' softmax partials
     comp = {} if args.no_fp16_comparator else fp16_comparator(args, torch, dev, N, call_us)
     # CPU: the oracle's restatement of the reference's chunked spectral step on
     # a bounded sample (dequant of the sample's keys and values, RoPE, one
@@ -735,15 +736,15 @@ def run_spectral(args, torch, dev) -> dict:
                                 f"payload bpe keys)"),
                    "ctx": N, "packed_tokens": P, "budget": args.spectral_budget, "c_used": c_used,
                    "c_pad": dp.c_pad, "key_page_bytes": dp.k_page_bytes},
-        "roofline": {"bound": "mfma", "kernel": "spectral_dequant_kernel, decode form (pages -> scores, dense fp16 V)",
+        "roofline": {"bound": "mfma", "kernel": "spectral_dequant_kernel, partial form (pages -> per-group softmax partials)",
                      "achieved": round(flops / (deq_us * 1e-6) / 1e12, 1), "peak": MFMA_FP16_DENSE_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (deq_us * 1e-6) / 1e12 / MFMA_FP16_DENSE_TFLOPS, 4),
                      "traffic": measured_traffic({"ctx": N, "window": args.window, "budget": args.spectral_budget,
-                                                  "c_pad": dp.c_pad}, SPECTRAL_TRAFFIC_FILE),
+                                                  "c_pad": dp.c_pad, "form": "partials"}, SPECTRAL_TRAFFIC_FILE),
                      "flops_per_launch": flops, "avg_launch_us": round(deq_us, 3),
                      "hbm_bytes_per_launch": page_bytes + out_bytes,
                      "hbm_frac": round((page_bytes + out_bytes) / (deq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
-        "spectral_call": {"dequant_us": round(deq_us, 2), "sdpa_and_window_us": round(call_us - deq_us, 2),
+        "spectral_call": {"dequant_us": round(deq_us, 2), "window_and_merge_us": round(call_us - deq_us, 2),
                           "fp16_comparator": comp},
         "cpu_baseline": cpu,
     }

@@ -211,6 +211,8 @@ class SpectralDequantArgs(ct.Structure):
         ("q_dtype", ct.c_int32),
         ("n_q_groups", ct.c_int32),
         ("scores", ct.c_void_p),
+        ("partials", ct.c_void_p),
+        ("sm_scale", ct.c_float),
     ]
 
 

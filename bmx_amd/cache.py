@@ -388,28 +388,20 @@ class PackedStreamingLayer(DynamicLayer):
     def _decode_spectral(self, q: torch.Tensor, scaling: float, G: int) -> torch.Tensor:
         """One decode step of the spectral arm: the reference's chunked step
         (every committed page dequantized, packed_streaming.py:1016-1032) with
-        the scores taken in the dequant kernel from the rotated keys (no dense
-        keys written), the window's scores from one grouped product, one
-        softmax and the value product with fp32 outputs (ROCm's grouped SDPA
-        takes a slow path for a single query)."""
-        dev, dt = q.device, q.dtype
+        the keys rebuilt, scored, weighted and applied to the values inside the
+        dequant kernel (one softmax partial per 64-token group, no dense rows
+        written), merged with the fp16 window's partial."""
         h, d = self._h_kv, self._d_head
         P = self._committed_S_q
-        T = 0 if self.keys is None else self.keys.shape[2]
         qg = q.reshape(h, G, d).contiguous()
-        S = torch.empty(h, G, P + T, dtype=torch.float32, device=dev)
-        Vd = torch.empty(h, P + T, d, dtype=dt, device=dev)
-        if P > 0:
-            spectral.dequant(self._dp, self._kpool, self._ktable[: P // spectral.GROUP], self._pool,
-                             self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._consts,
-                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt, out=(None, Vd), q=qg, scores=S)
-        if T:
-            kw = self.keys.squeeze(0).to(dt)
-            S[:, :, P:] = torch.bmm(kw, qg.transpose(1, 2).contiguous(), out_dtype=torch.float32).transpose(1, 2)
-            Vd[:, P:].copy_(self.values.squeeze(0))
-        p = torch.softmax(S * scaling, dim=-1).to(dt)
-        out = torch.bmm(p, Vd, out_dtype=torch.float32)
-        return out.to(dt).reshape(h * G, 1, d)
+        kw = vw = None
+        if self.keys is not None and self.keys.numel():
+            kw, vw = self.keys.squeeze(0).half(), self.values.squeeze(0).half()
+        kt = self._ktable[: P // spectral.GROUP] if P else None
+        vt = self._table[0, : P // k2b.PAGE_TOKENS].contiguous() if P else None
+        out = spectral.decode_attention(self._dp, self._kpool, kt, self._pool, vt, P, self._consts, qg, scaling,
+                                        k_win=kw, v_win=vw, apply_rope=k2b.ROPE_FP16_TABLES)
+        return out.to(q.dtype).reshape(h * G, 1, d)
 
     def _dense(self, q, scaling, G, causal, attention_mask):
         """Prefill (n_q > 1): _prefill_dense_attention (chunked_attention.py:

@@ -125,6 +125,8 @@ struct SpDequantKArgs {
   const void* q;
   int q_dtype, n_q_groups;
   float* scores;
+  float* partials;
+  float sm_scale;
 };
 
 constexpr int kSpBRow = 40;   // halves per token row of the staged Y_hat tile (32 + 8 pad)
@@ -279,6 +281,7 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   // them and waits for them)
   DqTile& tl = s_tile[wave];
   const int64_t row_h = (int64_t)(head_ok ? h : 0) * a.out_rows + g * kGroup;
+  float4_t sct[4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
     if (head_ok) {
@@ -304,7 +307,8 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
         // scores: A = the tile's rotated keys (token n, K index 8q + 2i + e)
         if (scoring) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[bb], sc, 0, 0, 0);
       }
-      if (scoring && n < a.n_q_groups) {   // lane 16q + n: tokens 4q .. 4q + 3, query n
+      sct[tt] = sc;
+      if (scoring && !a.partials && n < a.n_q_groups) {   // lane 16q + n: tokens 4q .. 4q + 3, query n
         float* dst = a.scores + ((int64_t)h * a.n_q_groups + n) * a.out_rows + g * kGroup + 16 * tt + 4 * q;
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = sc[i];
@@ -315,6 +319,66 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
         wave_lds_order();
       }
     }
+  }
+  if (a.partials) {   // partial form: the group's softmax partial per query, no dense values
+    if (head_ok) {
+      // lane 16q + n holds query n's scores of tokens 16tt + 4q + i
+      float m = -INFINITY;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, sct[tt][i] * a.sm_scale);
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      const bool qok = n < a.n_q_groups;
+      half4_t pw[4];
+      float l = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const _Float16 p = qok ? (_Float16)__expf(sct[tt][i] * a.sm_scale - m) : (_Float16)0.f;
+          pw[tt][i] = p;
+          l += (float)p;
+        }
+      l += __shfl_xor(l, 16);
+      l += __shfl_xor(l, 32);
+      // P.V on MFMA per value page (= token tile): A = the weights (query n,
+      // tokens 4q ..), B = the page's values (tokens 4q .., channel 16ct + n)
+      float4_t pv[8];
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) pv[ct] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int pg = 0; pg < 4; ++pg) {
+        dq_value_tile(vcd[pg], nrm[pg], a.codebook, a.v_sign_bits, n, q, tl);
+        wave_lds_order();
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+          half4_t vb;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vb[i] = (_Float16)tl.v[4 * q + i][16 * ct + n];
+          pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(pw[pg], vb, pv[ct], 0, 0, 0);
+        }
+        wave_lds_order();
+      }
+      // lane n (q = 0) holds queries i = 0..3, channel 16ct + n; queries 4.. in lanes q >= 1
+      const int n_grp = a.n_tokens / kGroup;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qi = 4 * q + i;
+        if (qi < a.n_q_groups) {
+          float* dst = a.partials + (((int64_t)h * a.n_q_groups + qi) * n_grp + g) * 130;
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) dst[2 + 16 * ct + n] = pv[ct][i];
+        }
+      }
+      if (q == 0 && qok) {
+        float* dst = a.partials + (((int64_t)h * a.n_q_groups + n) * n_grp + g) * 130;
+        dst[0] = m;
+        dst[1] = l;
+      }
+    }
+    return;
   }
   // values: the head's 4 pages of the group
   if (head_ok) {
@@ -411,11 +475,13 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   if (a->apply_rope < 0 || a->apply_rope > 2) return sp_fail(fn, "apply_rope must be 0, 1 or 2");
   if (!dtype_ok(a->out_dtype)) return sp_fail(fn, "out_dtype must be BMX_K2B_F16, _F32 or _BF16");
   if (a->out_rows != 0 && a->out_rows < a->n_tokens) return sp_fail(fn, "out_rows must be 0 or >= n_tokens");
-  if (!a->k_pages || !a->k_page_table || !a->v_pages || !a->v_page_table || !a->dec_perm || !a->v_out ||
-      (!a->k_out && !a->q) || a->n_k_pool < 1 || a->n_v_pool < 1)
+  if (!a->k_pages || !a->k_page_table || !a->v_pages || !a->v_page_table || !a->dec_perm ||
+      (!a->v_out && !a->partials) || (!a->k_out && !a->q) || a->n_k_pool < 1 || a->n_v_pool < 1)
     return sp_fail(fn, "null pointer argument or empty pool");
-  if (a->q && (!a->scores || a->n_q_groups < 1 || a->n_q_groups > 16 || !dtype_ok(a->q_dtype) || !a->apply_rope))
-    return sp_fail(fn, "the decode form needs scores, n_q_groups 1..16, a q_dtype and apply_rope");
+  if (a->q && ((!a->scores && !a->partials) || a->n_q_groups < 1 || a->n_q_groups > 16 || !dtype_ok(a->q_dtype) ||
+               !a->apply_rope))
+    return sp_fail(fn, "the decode form needs scores or partials, n_q_groups 1..16, a q_dtype and apply_rope");
+  if (a->partials && !a->q) return sp_fail(fn, "the partial form needs q");
   SpDequantKArgs k{};
   k.h_kv = a->L.h_kv; k.c_pad = a->L.c_pad; k.c_pad32 = (a->L.c_pad + 31) / 32 * 32;
   k.n_tokens = a->n_tokens; k.out_rows = a->out_rows ? a->out_rows : a->n_tokens;
@@ -428,6 +494,7 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   for (int i = 0; i < 4; ++i) { k.codebook[i] = a->v_codebook[i]; k.v_sign_bits[i] = a->v_sign_bits[i]; }
   k.k_out = a->k_out; k.v_out = a->v_out;
   k.q = a->q; k.q_dtype = a->q_dtype; k.n_q_groups = a->n_q_groups; k.scores = a->scores;
+  k.partials = a->partials; k.sm_scale = a->sm_scale;
   hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512), 0, (hipStream_t)stream, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -197,7 +197,7 @@ def append(k_pre: torch.Tensor, v: torch.Tensor, dp: DevicePack, k_pages: torch.
 def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_pages: torch.Tensor,
             v_table: torch.Tensor, n_tokens: int, consts: CodecConsts, *, apply_rope: int = ROPE_NONE,
             dtype: torch.dtype = torch.float32, out: tuple | None = None, q: torch.Tensor | None = None,
-            scores: torch.Tensor | None = None):
+            scores: torch.Tensor | None = None, partials: torch.Tensor | None = None, sm_scale: float = 1.0):
     """Pages of one sequence -> dense (K, V), each (h_kv, n_tokens, 128) in
     dtype; keys pre-RoPE (ROPE_NONE) or rotated at read (ROPE_EXACT: fp32
     cos/sin, ROPE_FP16_TABLES: the reference's fp16 tables).  ``out`` takes
@@ -208,8 +208,34 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     Decode form: with q (h_kv, G, 128) the kernel also writes scores
     (h_kv, G, R) fp32, q . k of the rotated keys for rows 0 .. n_tokens - 1
     (no softmax scale); out may then be (None, V) and no dense keys are
-    written."""
+    written.  Partial form: with q and partials (h_kv, G, n_tokens / 64, 130)
+    fp32 the kernel writes each 64-token group's softmax partial of the
+    scaled scores (m, l, P.V; see include/bmx_spectral.h) and no dense rows;
+    out is then unused."""
     dev = k_pages.device
+    if partials is not None:
+        _need(q is not None and partials.dtype == torch.float32 and partials.is_contiguous()
+              and tuple(partials.shape) == (dp.h_kv, q.shape[1], n_tokens // GROUP, 130),
+              "partials must be fp32 (h_kv, G, n_tokens / 64, 130), with q")
+        _need(q.dim() == 3 and q.shape[0] == dp.h_kv and q.shape[2] == HEAD_DIM and 1 <= q.shape[1] <= 16
+              and q.is_contiguous() and q.dtype in _V_DTYPES, "q must be contiguous (h_kv, 1..16, 128)")
+        _need(int(apply_rope) != ROPE_NONE, "the decode form scores rotated keys")
+        a = _lib.SpectralDequantArgs()
+        a.L = dp.layout()
+        a.n_tokens = int(n_tokens)
+        a.k_pages, a.k_page_table, a.n_k_pool = _ptr(k_pages), _ptr(k_table), k_pages.shape[0]
+        a.v_pages, a.v_page_table, a.n_v_pool = _ptr(v_pages), _ptr(v_table), v_pages.shape[0]
+        a.dec_perm = _ptr(dp.dec_perm)
+        a.apply_rope = int(apply_rope)
+        a.rope_scaling = consts.rope_scaling
+        a.inv_freq[:] = consts.inv_freq
+        a.v_codebook[:] = consts.codebook
+        a.v_sign_bits[:] = consts.sign_bits
+        a.out_dtype = _V_DTYPES[dtype]
+        a.q, a.q_dtype, a.n_q_groups = _ptr(q), _V_DTYPES[q.dtype], q.shape[1]
+        a.partials, a.sm_scale = _ptr(partials), float(sm_scale)
+        _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
+        return partials
     _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
     _need(n_tokens % GROUP == 0, "n_tokens must be a multiple of 64")
     _need(k_table.dtype == torch.int32 and k_table.numel() >= n_tokens // GROUP and v_table.dtype == torch.int32
@@ -247,3 +273,41 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
         a.q, a.q_dtype, a.n_q_groups, a.scores = _ptr(q), _V_DTYPES[q.dtype], q.shape[1], _ptr(scores)
     _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
     return k, v
+
+
+def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_pages: torch.Tensor,
+                     v_table: torch.Tensor, n_tokens: int, consts: CodecConsts, q: torch.Tensor, sm_scale: float,
+                     k_win: torch.Tensor | None = None, v_win: torch.Tensor | None = None,
+                     apply_rope: int = 2) -> torch.Tensor:
+    """One decode step over n_tokens committed tokens and the fp16 window:
+    q (h_kv, G, 128) post-RoPE -> (h_kv, G, 128) fp32.  The dequant kernel's
+    partial form gives every 64-token group's (m, l, P.V); the window's
+    partial comes from two small grouped products; the merge is the split
+    softmax's (m = max m_i, weights e^(m_i - m))."""
+    h, G, d = q.shape
+    ms, ls, accs = [], [], []      # (h, G, n) maxima and sums, (h, G, n, d) value sums, one entry per source
+    if n_tokens > 0:
+        pt = torch.empty(h, G, n_tokens // GROUP, 130, dtype=torch.float32, device=q.device)
+        dequant(dp, k_pages, k_table, v_pages, v_table, n_tokens, consts, apply_rope=apply_rope,
+                dtype=torch.float16, q=q, partials=pt, sm_scale=sm_scale)
+        ms.append(pt[..., 0])
+        ls.append(pt[..., 1])
+        accs.append(pt[..., 2:])
+    if k_win is not None and k_win.shape[1] > 0:
+        s = torch.bmm(k_win, q.to(k_win.dtype).transpose(1, 2).contiguous(),
+                      out_dtype=torch.float32).transpose(1, 2) * sm_scale          # (h, G, T)
+        mw = s.amax(dim=-1, keepdim=True)
+        pw = torch.exp(s - mw)
+        ms.append(mw)
+        ls.append(pw.sum(dim=-1, keepdim=True))
+        accs.append(torch.bmm(pw.to(v_win.dtype), v_win, out_dtype=torch.float32).unsqueeze(2))
+    M = torch.stack([m.amax(dim=-1) for m in ms], dim=-1).amax(dim=-1, keepdim=True)   # (h, G, 1)
+    L = None
+    A = None
+    for m, l, acc in zip(ms, ls, accs):
+        w = torch.exp(m - M)                                                       # (h, G, n)
+        lw = (w * l).sum(dim=-1)
+        aw = torch.matmul(w.unsqueeze(-2), acc).squeeze(-2)                        # one pass over acc
+        L = lw if L is None else L + lw
+        A = aw if A is None else A + aw
+    return A / L.unsqueeze(-1)

@@ -106,6 +106,16 @@ typedef struct bmx_spectral_dequant_args {
   int32_t q_dtype;             /* BMX_K2B_F16, _F32 or _BF16 */
   int32_t n_q_groups;          /* 1..16 */
   float* scores;               /* [h_kv][n_q_groups][out_rows] fp32 */
+  /* Partial form (with q): instead of scores and values, each 64-token group's
+   * softmax partial per (head, query): partials[((h G + g) n_groups + grp) 130 + e],
+   * e = 0: m = max of the scaled scores, 1: l = sum of exp(s - m) (the fp16
+   * weights), 2 + c: sum of the weights times value channel c (fp32
+   * accumulation of fp16 weights and values); n_groups = n_tokens / 64.  The
+   * caller merges the groups' partials (m = max m_i, l = sum l_i e^(m_i - m),
+   * out = sum acc_i e^(m_i - m) / l) with the window's.  v_out and scores may
+   * then be NULL. */
+  float* partials;
+  float sm_scale;
 } bmx_spectral_dequant_args;
 
 int64_t bmx_spectral_v_page_bytes(int32_t h_kv);

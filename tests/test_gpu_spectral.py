@@ -195,3 +195,48 @@ def test_decode_form_scores_match_keys():
         print(f"G {G}: scores vs own keys {d_own:.3e}, vs oracle keys {d_or:.3e} (max {smax:.2f})", flush=True)
         assert d_own <= 1e-5 * smax and d_or <= 3e-3 * smax
         assert torch.equal(Vb[:, :S], V) and not Vb[:, S:].any() and not Sb[:, :, S:].any()
+
+
+@pytest.mark.parametrize("G,T", [(4, 40), (1, 0), (8, 7)])
+def test_partial_form_decode_matches_oracle(G, T):
+    """The decode step through the kernel's partial form (per-group softmax
+    partials) and the merge with the window: against the oracle's one-softmax
+    attention over the same codes, and against the scores form + softmax."""
+    pack = synthetic_pack(8, 2.5, seed=14)
+    S = 1024
+    M = synthetic_keys(pack, S, seed=15)
+    gen = torch.Generator().manual_seed(16)
+    v = torch.randn(8, S, 128, generator=gen)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    dp, kp, vp, k_ids, v_ids = _write(pack, 8, M, v, consts, shuffle_seed=4)
+    kt = torch.randn(8, T, 128, generator=gen).half()
+    vt = torch.randn(8, T, 128, generator=gen).half()
+    q = torch.randn(8, G, 128, generator=gen).half()
+    scale = 128 ** -0.5
+    out = spectral.decode_attention(dp, kp, k_ids, vp, v_ids, S, consts, q.to(DEV), scale,
+                                    k_win=kt.to(DEV) if T else None, v_win=vt.to(DEV) if T else None,
+                                    apply_rope=k2b.ROPE_EXACT)
+    L = O.Layout(pack.bits.numpy())
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)).float(), 8)
+    cos, sin = A.rope_cos_sin(torch.tensor(consts.inv_freq), torch.arange(S))
+    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v), bits=2, seed=0, h=8)
+    V_or = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=8), 8)
+    ref = A.naive_dense_attention(q.reshape(8 * G, 1, 128).float(),
+                                  torch.cat([A.apply_rope(K_or, cos, sin), kt.float()], 1),
+                                  torch.cat([V_or, vt.float()], 1), G, scale).reshape(8, G, 128)
+    o = out.cpu().double()
+    err = (o - ref.double()).abs().max().item()
+    rel = ((o - ref.double()).norm() / ref.double().norm()).item()
+    # the scores form + one softmax + value product, same kernel inputs
+    Vb = torch.empty(8, S, 128, dtype=torch.float16, device=DEV)
+    Sb = torch.empty(8, G, S, dtype=torch.float32, device=DEV)
+    spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=k2b.ROPE_EXACT, dtype=torch.float16,
+                     out=(None, Vb), q=q.to(DEV), scores=Sb)
+    sw = torch.cat([Sb, (q.float() @ kt.float().transpose(1, 2)).to(DEV)], -1) * scale
+    Vw = torch.cat([Vb.float(), vt.float().to(DEV)], 1)
+    alt = (torch.softmax(sw, -1) @ Vw).cpu().double()
+    d_alt = (o - alt).abs().max().item()
+    print(f"G {G} T {T}: partial-form decode vs oracle max_abs {err:.3e} rel {rel:.3e}; vs scores form {d_alt:.3e}",
+          flush=True)
+    assert err <= 2e-3 and rel <= 1e-2 and d_alt <= 2e-3
