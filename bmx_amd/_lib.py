@@ -216,6 +216,13 @@ class SpectralDequantArgs(ct.Structure):
     ]
 
 
+class SpectralMergeArgs(ct.Structure):
+    _fields_ = [("h_kv", ct.c_int32), ("n_q_groups", ct.c_int32), ("n_groups", ct.c_int32),
+                ("partials", ct.c_void_p), ("q", ct.c_void_p), ("q_dtype", ct.c_int32),
+                ("k_win", ct.c_void_p), ("v_win", ct.c_void_p), ("win_len", ct.c_int32),
+                ("sm_scale", ct.c_float), ("out", ct.c_void_p), ("out_dtype", ct.c_int32)]
+
+
 EXPORTS = {
     "bmx_last_error": (ct.c_char_p, []),
     "bmx_k2b_page_bytes": (ct.c_size_t, [ct.POINTER(Geom)]),
@@ -233,6 +240,7 @@ EXPORTS = {
     "bmx_spectral_v_page_bytes": (ct.c_int64, [ct.c_int32]),
     "bmx_spectral_append": (ct.c_int32, [ct.POINTER(SpectralAppendArgs), ct.c_void_p]),
     "bmx_spectral_dequant": (ct.c_int32, [ct.POINTER(SpectralDequantArgs), ct.c_void_p]),
+    "bmx_spectral_merge": (ct.c_int32, [ct.POINTER(SpectralMergeArgs), ct.c_void_p]),
 }
 
 _LIB = None

@@ -396,12 +396,12 @@ class PackedStreamingLayer(DynamicLayer):
         qg = q.reshape(h, G, d).contiguous()
         kw = vw = None
         if self.keys is not None and self.keys.numel():
-            kw, vw = self.keys.squeeze(0).half(), self.values.squeeze(0).half()
+            kw, vw = self.keys.squeeze(0).half().contiguous(), self.values.squeeze(0).half().contiguous()
         kt = self._ktable[: P // spectral.GROUP] if P else None
         vt = self._table[0, : P // k2b.PAGE_TOKENS].contiguous() if P else None
         out = spectral.decode_attention(self._dp, self._kpool, kt, self._pool, vt, P, self._consts, qg, scaling,
                                         k_win=kw, v_win=vw, apply_rope=k2b.ROPE_FP16_TABLES)
-        return out.to(q.dtype).reshape(h * G, 1, d)
+        return out.reshape(h * G, 1, d)
 
     def _dense(self, q, scaling, G, causal, attention_mask):
         """Prefill (n_q > 1): _prefill_dense_attention (chunked_attention.py:

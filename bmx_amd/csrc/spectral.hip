@@ -392,6 +392,99 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   }
 }
 
+constexpr int kSpMaxWin = 4096;
+
+struct SpMergeKArgs {
+  int h_kv, G, n_groups, q_dtype, win_len, out_dtype;
+  const float* partials;
+  const void* q;
+  const uint16_t* k_win;
+  const uint16_t* v_win;
+  float sm_scale;
+  void* out;
+};
+
+constexpr int kSpMergeMaxGroups = 16384;   // 1M committed tokens
+constexpr int kSpMergeThreads = 1024;      // 8 slices x 128 channels
+
+// Sum (or max) of one value per thread over the 1024-thread block.
+template <bool kMax>
+__device__ __forceinline__ float block_reduce(float v, float* s_red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float u = __shfl_xor(v, o);
+    v = kMax ? fmaxf(v, u) : v + u;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();   // s_red free from any earlier reduction
+  if (lane == 0) s_red[wave] = v;
+  __syncthreads();
+  v = s_red[lane & 15];
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) {
+    const float u = __shfl_xor(v, o);
+    v = kMax ? fmaxf(v, u) : v + u;
+  }
+  return v;
+}
+
+// grid (G, h_kv), block 1024: one query (h, blockIdx.x).  The window's scaled
+// scores and the groups' weights e^(m_i - M) go to LDS (thread t takes tokens
+// and groups t, t + 1024, ..), M and the weight sum come from block
+// reductions, then thread (s, c) sums weight times channel c over the groups
+// and window tokens of slice s (index mod 8), and the 8 slices are added in LDS.
+__global__ __launch_bounds__(kSpMergeThreads) void spectral_merge_kernel(const SpMergeKArgs a) {
+  const int g = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 127, sl = tid >> 7;
+  __shared__ float s_q[kD];
+  __shared__ float s_s[kSpMaxWin];
+  __shared__ float s_w[kSpMergeMaxGroups];
+  __shared__ float s_red[16];
+  __shared__ float s_acc[8][kD];
+  const int64_t row = (int64_t)h * a.G + g;
+  if (tid < kD) s_q[tid] = sp_load(a.q, row * kD + tid, a.q_dtype);
+  __syncthreads();
+  const float* pt = a.partials + row * (int64_t)a.n_groups * 130;
+  float mx = -INFINITY;
+  for (int t = tid; t < a.win_len; t += kSpMergeThreads) {
+    const uint16_t* kr = a.k_win + ((int64_t)h * a.win_len + t) * kD;
+    float acc = 0.f;
+    for (int d = 0; d < kD; d += 2) {
+      const uint32_t kk = *reinterpret_cast<const uint32_t*>(kr + d);
+      acc = fmaf(s_q[d], half_bits_to_float(kk & 0xffffu), acc);
+      acc = fmaf(s_q[d + 1], half_bits_to_float(kk >> 16), acc);
+    }
+    s_s[t] = acc * a.sm_scale;
+    mx = fmaxf(mx, s_s[t]);
+  }
+  for (int i = tid; i < a.n_groups; i += kSpMergeThreads) mx = fmaxf(mx, pt[(int64_t)i * 130]);
+  const float M = block_reduce<true>(mx, s_red);
+  float lsum = 0.f;
+  for (int i = tid; i < a.n_groups; i += kSpMergeThreads) {
+    const float w = __expf(pt[(int64_t)i * 130] - M);
+    s_w[i] = w;
+    lsum = fmaf(w, pt[(int64_t)i * 130 + 1], lsum);
+  }
+  for (int t = tid; t < a.win_len; t += kSpMergeThreads) {
+    const float w = __expf(s_s[t] - M);
+    s_s[t] = w;
+    lsum += w;
+  }
+  const float L = block_reduce<false>(lsum, s_red);   // its barriers also publish s_w and s_s
+  float A = 0.f;
+#pragma unroll 8
+  for (int i = sl; i < a.n_groups; i += 8) A = fmaf(s_w[i], pt[(int64_t)i * 130 + 2 + c], A);
+  for (int t = sl; t < a.win_len; t += 8)
+    A = fmaf(s_s[t], half_bits_to_float(a.v_win[((int64_t)h * a.win_len + t) * kD + c]), A);
+  s_acc[sl][c] = A;
+  __syncthreads();
+  if (sl == 0) {
+    float tot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tot += s_acc[j][c];
+    store_elem(a.out, row * kD + c, tot / L, a.out_dtype);
+  }
+}
+
 static PageLayout value_layout(int h_kv) {
   PageLayout L{};
   L.vnorm = 0;
@@ -496,6 +589,31 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   k.q = a->q; k.q_dtype = a->q_dtype; k.n_q_groups = a->n_q_groups; k.scores = a->scores;
   k.partials = a->partials; k.sm_scale = a->sm_scale;
   hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512), 0, (hipStream_t)stream, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    bmx_set_error(std::string(fn) + ": launch: " + hipGetErrorString(e));
+    return BMX_E_HIP;
+  }
+  return BMX_OK;
+}
+
+extern "C" int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* stream) {
+  const char* fn = "bmx_spectral_merge";
+  if (!a) return sp_fail(fn, "args is NULL");
+  if (a->h_kv < 1 || a->h_kv > 8 || a->n_q_groups < 1 || a->n_q_groups > 16)
+    return sp_fail(fn, "h_kv must be 1..8 and n_q_groups 1..16");
+  if (a->n_groups < 0 || a->n_groups > kSpMergeMaxGroups || a->win_len < 0 || a->win_len > kSpMaxWin ||
+      a->n_groups + a->win_len == 0)
+    return sp_fail(fn, "n_groups 0..16384, win_len 0..4096, and at least one token");
+  if (!dtype_ok(a->q_dtype) || !dtype_ok(a->out_dtype)) return sp_fail(fn, "q_dtype / out_dtype");
+  if (!a->q || !a->out || (a->n_groups && !a->partials) || (a->win_len && (!a->k_win || !a->v_win)))
+    return sp_fail(fn, "null pointer argument");
+  SpMergeKArgs k{};
+  k.h_kv = a->h_kv; k.G = a->n_q_groups; k.n_groups = a->n_groups; k.q_dtype = a->q_dtype;
+  k.win_len = a->win_len; k.out_dtype = a->out_dtype; k.partials = a->partials; k.q = a->q;
+  k.k_win = a->k_win; k.v_win = a->v_win; k.sm_scale = a->sm_scale; k.out = a->out;
+  hipLaunchKernelGGL(spectral_merge_kernel, dim3(a->n_q_groups, a->h_kv), dim3(kSpMergeThreads), 0,
+                     (hipStream_t)stream, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     bmx_set_error(std::string(fn) + ": launch: " + hipGetErrorString(e));

@@ -278,36 +278,31 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
 def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_pages: torch.Tensor,
                      v_table: torch.Tensor, n_tokens: int, consts: CodecConsts, q: torch.Tensor, sm_scale: float,
                      k_win: torch.Tensor | None = None, v_win: torch.Tensor | None = None,
-                     apply_rope: int = 2) -> torch.Tensor:
+                     apply_rope: int = 2, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """One decode step over n_tokens committed tokens and the fp16 window:
-    q (h_kv, G, 128) post-RoPE -> (h_kv, G, 128) fp32.  The dequant kernel's
-    partial form gives every 64-token group's (m, l, P.V); the window's
-    partial comes from two small grouped products; the merge is the split
-    softmax's (m = max m_i, weights e^(m_i - m))."""
+    q (h_kv, G, 128) post-RoPE -> (h_kv, G, 128) in out_dtype (q's by default).  The dequant
+    kernel's partial form gives every 64-token group's (m, l, P.V); the merge
+    kernel scores the window and folds everything by the split softmax's
+    weights (m = max m_i, weights e^(m_i - m))."""
     h, G, d = q.shape
-    ms, ls, accs = [], [], []      # (h, G, n) maxima and sums, (h, G, n, d) value sums, one entry per source
+    _need(q.is_contiguous() and q.dtype in _V_DTYPES and d == HEAD_DIM and h == dp.h_kv, "q (h_kv, G, 128)")
+    pt = None
     if n_tokens > 0:
         pt = torch.empty(h, G, n_tokens // GROUP, 130, dtype=torch.float32, device=q.device)
         dequant(dp, k_pages, k_table, v_pages, v_table, n_tokens, consts, apply_rope=apply_rope,
                 dtype=torch.float16, q=q, partials=pt, sm_scale=sm_scale)
-        ms.append(pt[..., 0])
-        ls.append(pt[..., 1])
-        accs.append(pt[..., 2:])
-    if k_win is not None and k_win.shape[1] > 0:
-        s = torch.bmm(k_win, q.to(k_win.dtype).transpose(1, 2).contiguous(),
-                      out_dtype=torch.float32).transpose(1, 2) * sm_scale          # (h, G, T)
-        mw = s.amax(dim=-1, keepdim=True)
-        pw = torch.exp(s - mw)
-        ms.append(mw)
-        ls.append(pw.sum(dim=-1, keepdim=True))
-        accs.append(torch.bmm(pw.to(v_win.dtype), v_win, out_dtype=torch.float32).unsqueeze(2))
-    M = torch.stack([m.amax(dim=-1) for m in ms], dim=-1).amax(dim=-1, keepdim=True)   # (h, G, 1)
-    L = None
-    A = None
-    for m, l, acc in zip(ms, ls, accs):
-        w = torch.exp(m - M)                                                       # (h, G, n)
-        lw = (w * l).sum(dim=-1)
-        aw = torch.matmul(w.unsqueeze(-2), acc).squeeze(-2)                        # one pass over acc
-        L = lw if L is None else L + lw
-        A = aw if A is None else A + aw
-    return A / L.unsqueeze(-1)
+    T = 0 if k_win is None else k_win.shape[1]
+    if T:
+        _need(k_win.dtype == torch.float16 and v_win.dtype == torch.float16 and k_win.is_contiguous()
+              and v_win.is_contiguous() and tuple(k_win.shape) == (h, T, d) and v_win.shape == k_win.shape,
+              "window keys and values: contiguous fp16 (h_kv, T, 128)")
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    _need(out_dtype in _V_DTYPES, "out_dtype must be fp16, bf16 or fp32")
+    out = torch.empty(h, G, d, dtype=out_dtype, device=q.device)
+    a = _lib.SpectralMergeArgs()
+    a.h_kv, a.n_q_groups, a.n_groups = h, G, n_tokens // GROUP
+    a.partials, a.q, a.q_dtype = _ptr(pt), _ptr(q), _V_DTYPES[q.dtype]
+    a.k_win, a.v_win, a.win_len = (_ptr(k_win), _ptr(v_win), T) if T else (None, None, 0)
+    a.sm_scale, a.out, a.out_dtype = float(sm_scale), _ptr(out), _V_DTYPES[out_dtype]
+    _lib.check(_lib.lib().bmx_spectral_merge(ct.byref(a), _stream(q.device)), "bmx_spectral_merge")
+    return out

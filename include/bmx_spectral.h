@@ -118,7 +118,28 @@ typedef struct bmx_spectral_dequant_args {
   float sm_scale;
 } bmx_spectral_dequant_args;
 
+/* The decode step's merge: the groups' softmax partials (the partial form
+ * above) and the fp16 recent window's tokens, scored here, folded by the split
+ * softmax's weights (m = max, weights e^(m_i - m)) into the attention output.
+ * Replaces the online-softmax reassembly of chunked_dequant_attention
+ * (chunked_attention.py:398-530) and the merge of _finalize_decode
+ * (triton_dequant_attention.py:504-575) for the spectral step. */
+typedef struct bmx_spectral_merge_args {
+  int32_t h_kv, n_q_groups;    /* 1..8, 1..16 */
+  int32_t n_groups;            /* groups in partials, 0..16384 (0: window only) */
+  const float* partials;       /* [h_kv][n_q_groups][n_groups][130] fp32 */
+  const void* q;               /* [h_kv][n_q_groups][128] post-RoPE, dtype q_dtype */
+  int32_t q_dtype;
+  const uint16_t* k_win;       /* fp16 [h_kv][win_len][128] post-RoPE window keys */
+  const uint16_t* v_win;       /* fp16 [h_kv][win_len][128] window values */
+  int32_t win_len;             /* 0..4096 */
+  float sm_scale;
+  void* out;                   /* [h_kv][n_q_groups][128], dtype out_dtype */
+  int32_t out_dtype;
+} bmx_spectral_merge_args;
+
 int64_t bmx_spectral_v_page_bytes(int32_t h_kv);
+int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* stream);
 int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* stream);
 int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void* stream);
 

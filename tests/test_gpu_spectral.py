@@ -215,7 +215,7 @@ def test_partial_form_decode_matches_oracle(G, T):
     scale = 128 ** -0.5
     out = spectral.decode_attention(dp, kp, k_ids, vp, v_ids, S, consts, q.to(DEV), scale,
                                     k_win=kt.to(DEV) if T else None, v_win=vt.to(DEV) if T else None,
-                                    apply_rope=k2b.ROPE_EXACT)
+                                    apply_rope=k2b.ROPE_EXACT, out_dtype=torch.float32)
     L = O.Layout(pack.bits.numpy())
     codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
     K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)).float(), 8)
