@@ -188,3 +188,16 @@ def test_recipe_and_construction_guards(tmp_path):
     with pytest.raises(KeyError, match="available"):
         PackedStreamingCache(cfg, CacheCodecSpec(arm="spectral", pre_rope=True, pack_path=str(path),
                                                  budget=3.0), v)
+
+
+def test_bad_merge_arguments_are_rejected_with_message():
+    lib = _lib.lib()
+    m = _lib.SpectralMergeArgs()
+    m.h_kv, m.n_q_groups = 9, 4
+    assert lib.bmx_spectral_merge(ct.byref(m), None) != 0 and b"h_kv" in lib.bmx_last_error()
+    m.h_kv, m.n_groups, m.win_len = 8, 0, 0
+    assert lib.bmx_spectral_merge(ct.byref(m), None) != 0 and b"at least one token" in lib.bmx_last_error()
+    m.n_groups = 16385
+    assert lib.bmx_spectral_merge(ct.byref(m), None) != 0 and b"16384" in lib.bmx_last_error()
+    m.n_groups = 4
+    assert lib.bmx_spectral_merge(ct.byref(m), None) != 0 and b"null pointer" in lib.bmx_last_error()
