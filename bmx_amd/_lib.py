@@ -220,7 +220,8 @@ class SpectralMergeArgs(ct.Structure):
     _fields_ = [("h_kv", ct.c_int32), ("n_q_groups", ct.c_int32), ("n_groups", ct.c_int32),
                 ("partials", ct.c_void_p), ("q", ct.c_void_p), ("q_dtype", ct.c_int32),
                 ("k_win", ct.c_void_p), ("v_win", ct.c_void_p), ("win_len", ct.c_int32),
-                ("sm_scale", ct.c_float), ("out", ct.c_void_p), ("out_dtype", ct.c_int32)]
+                ("sm_scale", ct.c_float), ("out", ct.c_void_p), ("out_dtype", ct.c_int32),
+                ("v_sign_bits", ct.c_uint32 * 4)]
 
 
 EXPORTS = {

@@ -299,8 +299,10 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
             k1 = __fmul_rn(k1, cn) + __fmul_rn(k0, sn);
             k0 = r0;
           }
-          tl.v[n][j] = k0;
-          tl.v[n][j + 64] = k1;
+          if (a.k_out) {
+            tl.v[n][j] = k0;
+            tl.v[n][j + 64] = k1;
+          }
           ka[2 * i] = (_Float16)k0;
           ka[2 * i + 1] = (_Float16)k1;
         }
@@ -343,23 +345,29 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
         }
       l += __shfl_xor(l, 16);
       l += __shfl_xor(l, 32);
-      // P.V on MFMA per value page (= token tile): A = the weights (query n,
-      // tokens 4q ..), B = the page's values (tokens 4q .., channel 16ct + n)
+      // P.V in the rotated value domain, per value page (= token tile): A = the
+      // weights times the token norms (query n, tokens 4q .. 4q + 3), B = the
+      // codebook levels of rotated channel 16ct + n, tokens 4q .. 4q + 3: byte
+      // ct of the lane's own code pair.  The inverse Hadamard, the signs and
+      // 1/128 are linear and left to the merge.
       float4_t pv[8];
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct) pv[ct] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int pg = 0; pg < 4; ++pg) {
-        dq_value_tile(vcd[pg], nrm[pg], a.codebook, a.v_sign_bits, n, q, tl);
-        wave_lds_order();
+        const float nv[4] = {half_bits_to_float(nrm[pg].x & 0xffffu), half_bits_to_float(nrm[pg].x >> 16),
+                             half_bits_to_float(nrm[pg].y & 0xffffu), half_bits_to_float(nrm[pg].y >> 16)};
+        half4_t aw;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[pg][i] * nv[i]);
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct) {
+          const uint32_t byte = ((ct < 4 ? vcd[pg].x : vcd[pg].y) >> (8 * (ct & 3))) & 0xFFu;
           half4_t vb;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) vb[i] = (_Float16)tl.v[4 * q + i][16 * ct + n];
-          pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(pw[pg], vb, pv[ct], 0, 0, 0);
+          for (int i = 0; i < 4; ++i) vb[i] = (_Float16)a.codebook[(byte >> (2 * i)) & 3u];
+          pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[ct], 0, 0, 0);
         }
-        wave_lds_order();
       }
       // lane n (q = 0) holds queries i = 0..3, channel 16ct + n; queries 4.. in lanes q >= 1
       const int n_grp = a.n_tokens / kGroup;
@@ -402,6 +410,7 @@ struct SpMergeKArgs {
   const uint16_t* v_win;
   float sm_scale;
   void* out;
+  uint32_t v_sign_bits[4];
 };
 
 constexpr int kSpMergeMaxGroups = 16384;   // 1M committed tokens
@@ -440,6 +449,8 @@ __global__ __launch_bounds__(kSpMergeThreads) void spectral_merge_kernel(const S
   __shared__ float s_w[kSpMergeMaxGroups];
   __shared__ float s_red[16];
   __shared__ float s_acc[8][kD];
+  __shared__ float s_accw[8][kD];
+  __shared__ float s_h[kD];
   const int64_t row = (int64_t)h * a.G + g;
   if (tid < kD) s_q[tid] = sp_load(a.q, row * kD + tid, a.q_dtype);
   __syncthreads();
@@ -470,18 +481,39 @@ __global__ __launch_bounds__(kSpMergeThreads) void spectral_merge_kernel(const S
     lsum += w;
   }
   const float L = block_reduce<false>(lsum, s_red);   // its barriers also publish s_w and s_s
-  float A = 0.f;
+  float A = 0.f, Aw = 0.f;
 #pragma unroll 8
   for (int i = sl; i < a.n_groups; i += 8) A = fmaf(s_w[i], pt[(int64_t)i * 130 + 2 + c], A);
   for (int t = sl; t < a.win_len; t += 8)
-    A = fmaf(s_s[t], half_bits_to_float(a.v_win[((int64_t)h * a.win_len + t) * kD + c]), A);
+    Aw = fmaf(s_s[t], half_bits_to_float(a.v_win[((int64_t)h * a.win_len + t) * kD + c]), Aw);
   s_acc[sl][c] = A;
+  s_accw[sl][c] = Aw;
   __syncthreads();
-  if (sl == 0) {
-    float tot = 0.f;
+  // the groups' sums are in the rotated value domain: H128 over the channel
+  // index, then the signs and 1/128 (the value codec's inverse)
+  if (tid < kD) {
+    float x = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) tot += s_acc[j][c];
-    store_elem(a.out, row * kD + c, tot / L, a.out_dtype);
+    for (int j = 0; j < 8; ++j) x += s_acc[j][c];
+    s_h[c] = x;
+  }
+  for (int hb = 1; hb < kD; hb <<= 1) {
+    __syncthreads();
+    float x = 0.f, o = 0.f;
+    if (tid < kD) {
+      x = s_h[c];
+      o = s_h[c ^ hb];
+    }
+    __syncthreads();
+    if (tid < kD) s_h[c] = (c & hb) ? o - x : x + o;
+  }
+  __syncthreads();
+  if (tid < kD) {
+    float w = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w += s_accw[j][c];
+    const float v = s_h[c] / (float)kD;
+    store_elem(a.out, row * kD + c, ((sign_neg(a.v_sign_bits, c) ? -v : v) + w) / L, a.out_dtype);
   }
 }
 
@@ -612,6 +644,7 @@ extern "C" int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* st
   k.h_kv = a->h_kv; k.G = a->n_q_groups; k.n_groups = a->n_groups; k.q_dtype = a->q_dtype;
   k.win_len = a->win_len; k.out_dtype = a->out_dtype; k.partials = a->partials; k.q = a->q;
   k.k_win = a->k_win; k.v_win = a->v_win; k.sm_scale = a->sm_scale; k.out = a->out;
+  for (int i = 0; i < 4; ++i) k.v_sign_bits[i] = a->v_sign_bits[i];
   hipLaunchKernelGGL(spectral_merge_kernel, dim3(a->n_q_groups, a->h_kv), dim3(kSpMergeThreads), 0,
                      (hipStream_t)stream, k);
   const hipError_t e = hipGetLastError();

@@ -304,5 +304,6 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
     a.partials, a.q, a.q_dtype = _ptr(pt), _ptr(q), _V_DTYPES[q.dtype]
     a.k_win, a.v_win, a.win_len = (_ptr(k_win), _ptr(v_win), T) if T else (None, None, 0)
     a.sm_scale, a.out, a.out_dtype = float(sm_scale), _ptr(out), _V_DTYPES[out_dtype]
+    a.v_sign_bits[:] = consts.sign_bits
     _lib.check(_lib.lib().bmx_spectral_merge(ct.byref(a), _stream(q.device)), "bmx_spectral_merge")
     return out

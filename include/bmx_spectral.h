@@ -109,8 +109,10 @@ typedef struct bmx_spectral_dequant_args {
   /* Partial form (with q): instead of scores and values, each 64-token group's
    * softmax partial per (head, query): partials[((h G + g) n_groups + grp) 130 + e],
    * e = 0: m = max of the scaled scores, 1: l = sum of exp(s - m) (the fp16
-   * weights), 2 + c: sum of the weights times value channel c (fp32
-   * accumulation of fp16 weights and values); n_groups = n_tokens / 64.  The
+   * weights), 2 + c: in the rotated value domain, the sum of the weights
+   * times the token norms times the codebook levels of rotated channel c
+   * (fp32 accumulation of fp16 operands; the values are that sum's inverse
+   * Hadamard, signs and 1/128); n_groups = n_tokens / 64.  The
    * caller merges the groups' partials (m = max m_i, l = sum l_i e^(m_i - m),
    * out = sum acc_i e^(m_i - m) / l) with the window's.  v_out and scores may
    * then be NULL. */
@@ -136,6 +138,7 @@ typedef struct bmx_spectral_merge_args {
   float sm_scale;
   void* out;                   /* [h_kv][n_q_groups][128], dtype out_dtype */
   int32_t out_dtype;
+  uint32_t v_sign_bits[4];     /* the value codec's Hadamard signs (the partials are rotated) */
 } bmx_spectral_merge_args;
 
 int64_t bmx_spectral_v_page_bytes(int32_t h_kv);
