@@ -110,7 +110,7 @@ def cpu_baseline(args, packed: int, tail: int) -> dict:
     inv = torch.tensor(consts.inv_freq)
     k_tail = synth.rope_keys(k_pre[:, S:], S, consts)
     q = torch.randn(H_KV * G, 1, D, generator=gen)
-    threads = min(os.cpu_count() or 1, 16)
+    threads, host = cpu_threads()
     torch.set_num_threads(threads)
     A.k2b_chunked_attention(q, cache, inv, k_tail, v[:, S:], G, D ** -0.5)  # warm-up
     times = []
@@ -136,7 +136,7 @@ def cpu_baseline(args, packed: int, tail: int) -> dict:
                        f"scaled x{(packed + tail) / (S + tail):.2f} tokens x {args.layers} layers"),
             "value_1_thread": round(t1 * scale * 1e6, 1),
             "sample_1_thread": f"median of 3 = {t1 * 1e3:.1f} ms/layer-call, same scaling",
-            "cpu_model": _cpu_model()}
+            **host}
 
 
 def fp16_comparator(args, torch, dev, ctx: int, our_us: float) -> dict:
@@ -201,6 +201,16 @@ def fp16_comparator(args, torch, dev, ctx: int, our_us: float) -> dict:
 
 
 def _cpu_model() -> str:
+    """The host CPU's model name, as lscpu reports it (else /proc/cpuinfo)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -209,6 +219,25 @@ def _cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def cpu_threads() -> tuple:
+    """(threads, host fields) for the CPU baseline.  The threads are every CPU
+    this process may run on (its affinity mask), capped by OMP_NUM_THREADS
+    when the environment sets it (the GPU box gives one GPU's job a 16-CPU
+    share of a larger host); the fields report the host's logical CPU count,
+    the affinity count, the threads used and the CPU model separately."""
+    host = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = host
+    threads = avail
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        threads = min(threads, int(env))
+    return threads, {"host_logical_cpus": host, "affinity_cpus": avail, "threads": threads,
+                     "omp_num_threads": env or None, "cpu_model": _cpu_model()}
 
 
 STREAM_METRIC = ("append + decode-attn µs/step, k2b rank 16, Qwen3-8B geometry, "
@@ -410,7 +439,7 @@ def run_rtn(args, torch, dev) -> dict:
         c = A.RtnOracleCache(H_KV, **codec)
         for p in range(P // 128):
             c.commit(k[:, p * 128:(p + 1) * 128], v[:, p * 128:(p + 1) * 128])
-        threads = min(os.cpu_count() or 1, 16)
+        threads, host = cpu_threads()
         torch.set_num_threads(threads)
         qq = q.reshape(H_KV * G, 1, D)
         A.rtn_chunked_attention(qq, c, k[:, P:], v[:, P:], G, D ** -0.5)
@@ -423,7 +452,7 @@ def run_rtn(args, torch, dev) -> dict:
         res["cpu_baseline"] = {"value": round(t * 1e6, 1), "unit": "us/call", "cores": threads, "kind": "port",
                                "sample": (f"the whole config-1 call ({P} packed + {T} tail tokens), median of "
                                           f"{args.cpu_reps} after 1 warm-up"),
-                               "cpu_model": _cpu_model()}
+                               **host}
     return res
 
 
@@ -635,7 +664,7 @@ def run_spectral(args, torch, dev) -> dict:
     pack = spectral.SpectralPack(enc=(w.sqrt()[:, None] * E).float(), dec=(w.rsqrt()[:, None] * E).float(),
                                  lam=lam.float(), bits=spectral.allocate_bits(lam, args.spectral_budget),
                                  budget=args.spectral_budget)
-    k_spec, v_spec = spec_pair(f"k4_b{args.spectral_budget:g}", pack_path="synthetic")
+    k_spec, v_spec = spec_pair(f"k4ph_b{args.spectral_budget:g}", pack_path="synthetic")
     lay = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=args.window, pack=pack)
     N = args.ctx
     dec = pack.dec.to(dev)
@@ -705,7 +734,7 @@ def run_spectral(args, torch, dev) -> dict:
         norms = torch.rand(S, H_KV) + 0.5
         qf = q.float().cpu()
         cos, sin = A.rope_cos_sin(torch.tensor(lay._consts.inv_freq), torch.arange(S))
-        threads = min(os.cpu_count() or 1, 16)
+        threads, host = cpu_threads()
         torch.set_num_threads(threads)
 
         def cpu_step():
@@ -725,12 +754,12 @@ def run_spectral(args, torch, dev) -> dict:
                "sample": (f"1 layer, {S} committed tokens (h_kv 8, G 4, c_pad {L.c_pad}): the oracle's "
                           f"spectral dequant (float64 Y_hat dec^T), value dequant, RoPE and one softmax, "
                           f"median of 3 = {t * 1e3:.1f} ms, scaled x{(P + args.window) / S:.1f} tokens"),
-               "cpu_model": _cpu_model()}
+               **host}
     return {
         "metric": SPECTRAL_METRIC, "value": round(call_us, 2), "unit": "us/layer-call", "n_gpus": 1,
         "steps": reps, "warmup": 3, "ms_per_step": round(call_us / 1e3, 4), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
-        "config": {"workload": (f"k4_b{args.spectral_budget:g} decode call: {P} packed + "
+        "config": {"workload": (f"k4ph_b{args.spectral_budget:g} decode call: {P} packed + "
                                 f"{N - P} fp16 window tokens, 32q/8kv heads, d 128, synthetic pack "
                                 f"(c_used {c_used} of {C}, c_pad {dp.c_pad}, {spectral.payload_bpe(pack.bits):.3f} "
                                 f"payload bpe keys)"),

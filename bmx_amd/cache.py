@@ -393,6 +393,8 @@ class PackedStreamingLayer(DynamicLayer):
         written), merged with the fp16 window's partial."""
         h, d = self._h_kv, self._d_head
         P = self._committed_S_q
+        if self._dp is None:   # a step before the first commit: the window alone
+            self._dp = spectral.DevicePack(self._pack, self._h_kv, q.device)
         qg = q.reshape(h, G, d).contiguous()
         kw = vw = None
         if self.keys is not None and self.keys.numel():

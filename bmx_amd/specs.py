@@ -14,8 +14,11 @@ pairs the reference's attend() sends to a fused kernel
   reference runs on its chunked path only);
 * spectral (K4): K ``spectral`` pre-RoPE from a pack file (rtn payload,
   fp32 decoder, 64-token groups), V ``turboquant_mse_perhead`` 2-bit, the
-  value codec of the other pre-RoPE pair (the reference's ``k4_b*`` recipe
-  pairs the full-C ``turboquant_mse``, which no MI355X kernel reads).
+  value codec of the other pre-RoPE pair, under the recipe name
+  ``k4ph_b<budget>``.  The reference's own ``k4_b<budget>`` recipe pairs the
+  spectral keys with the full-C ``turboquant_mse`` values (one 1024-point
+  rotation and one norm per token, recipes.py:138-143), which no MI355X
+  kernel reads: that name raises rather than answer with another codec.
 
 Every other pair raises, naming what it got: there is no CPU or slow path to
 route it to.
@@ -46,9 +49,15 @@ class CacheCodecSpec:
 def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0, pack_path: str | None = None):
     """(k_spec, v_spec) for a named recipe (cache/recipes.py:13-42, 88-143, 173-177)."""
     if arm.startswith("k4_b"):
+        # the reference's k4 recipe: spectral keys with full-C turboquant_mse values
+        raise NotImplementedError(
+            f"recipe {arm!r} pairs spectral keys with full-C turboquant_mse values (one 1024-point "
+            f"rotation per token), which have no MI355X kernels; 'k4ph_b<budget>' pairs the same keys "
+            f"with the per-head value codec (turboquant_mse_perhead)")
+    if arm.startswith("k4ph_b"):
         if not pack_path:
             raise ValueError("k4 arms require --pack-path (a fitted spectral pack file)")
-        budget_str = arm[len("k4_b"):]
+        budget_str = arm[len("k4ph_b"):]
         if "_dec8" in budget_str or "_lq" in budget_str:
             raise NotImplementedError(
                 f"recipe {arm!r}: the int8 decoder and Lloyd payload variants have no MI355X kernels")
@@ -60,7 +69,7 @@ def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0, pack_
                 CacheCodecSpec(arm="rtn_token", bits=2, group=group, seed=seed))
     if arm != "k2b_ph":
         raise NotImplementedError(
-            f"recipe {arm!r} has no MI355X kernels; this package implements 'k2b_ph', 'kivi' and 'k4_b<budget>'")
+            f"recipe {arm!r} has no MI355X kernels; this package implements 'k2b_ph', 'kivi' and 'k4ph_b<budget>'")
     return (CacheCodecSpec(arm="lowrank_rtn_channel", bits=3, rank=rank, group=group, seed=seed,
                            pre_rope=True),
             CacheCodecSpec(arm="turboquant_mse_perhead", bits=2, seed=seed))

@@ -213,6 +213,14 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     scaled scores (m, l, P.V; see include/bmx_spectral.h) and no dense rows;
     out is then unused."""
     dev = k_pages.device
+    # the C-ABI carries no table lengths: a short or wrongly typed table would
+    # be read past its end on the device, so every form checks them here
+    _need(n_tokens % GROUP == 0, "n_tokens must be a multiple of 64")
+    _need(k_table is not None and v_table is not None and k_table.dtype == torch.int32
+          and k_table.numel() >= n_tokens // GROUP and v_table.dtype == torch.int32
+          and v_table.numel() >= n_tokens // 16, "k_table (n/64) and v_table (n/16) must be int32")
+    _need(k_table.device == dev and v_table.device == dev and k_table.is_contiguous()
+          and v_table.is_contiguous(), "k_table and v_table must be contiguous on the pages' device")
     if partials is not None:
         _need(q is not None and partials.dtype == torch.float32 and partials.is_contiguous()
               and tuple(partials.shape) == (dp.h_kv, q.shape[1], n_tokens // GROUP, 130),
@@ -237,9 +245,6 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
         _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
         return partials
     _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
-    _need(n_tokens % GROUP == 0, "n_tokens must be a multiple of 64")
-    _need(k_table.dtype == torch.int32 and k_table.numel() >= n_tokens // GROUP and v_table.dtype == torch.int32
-          and v_table.numel() >= n_tokens // 16, "k_table (n/64) and v_table (n/16) must be int32")
     if out is None:
         k = torch.empty(dp.h_kv, n_tokens, HEAD_DIM, dtype=dtype, device=dev)
         v = torch.empty_like(k)
@@ -285,7 +290,11 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
     kernel scores the window and folds everything by the split softmax's
     weights (m = max m_i, weights e^(m_i - m))."""
     h, G, d = q.shape
-    _need(q.is_contiguous() and q.dtype in _V_DTYPES and d == HEAD_DIM and h == dp.h_kv, "q (h_kv, G, 128)")
+    _need(q.is_contiguous() and q.dtype in _V_DTYPES and d == HEAD_DIM, "q (h_kv, G, 128)")
+    # no committed token: only the window is read, and a layer that has not
+    # committed yet may have no device pack
+    _need(n_tokens >= 0 and (n_tokens == 0 or (dp is not None and h == dp.h_kv)),
+          "q (h_kv, G, 128) with h_kv of the pack")
     pt = None
     if n_tokens > 0:
         pt = torch.empty(h, G, n_tokens // GROUP, 130, dtype=torch.float32, device=q.device)

@@ -108,7 +108,7 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, budget):
     tokens = torch.from_numpy(g["r16_tokens"]).cuda()
     model = _tiny_model(n_layers=1)
     path = _spectral_pack_file(tmp_path, 1)
-    specs = spec_pair(f"k4_b{budget:g}", pack_path=path)
+    specs = spec_pair(f"k4ph_b{budget:g}", pack_path=path)
     prod = PackedStreamingCache(model.config, *specs, recent_window=32)
     got = _run(prod, model, tokens, 140)
     orc = OracleCache(model.config, *specs, recent_window=32)
@@ -117,7 +117,7 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, budget):
     scale = ref.abs().max().item()
     agree = (got.argmax(1) == ref.argmax(1)).float().mean().item()
     lay = prod.layers[0]
-    print(f"k4_b{budget:g}: logits max|err| {err.max():.3e} of max|logit| {scale:.3f}; argmax "
+    print(f"k4ph_b{budget:g}: logits max|err| {err.max():.3e} of max|logit| {scale:.3f}; argmax "
           f"agreement {agree:.4f}; committed {lay._committed_S_q}; c_pad {lay._dp.c_pad}", flush=True)
     assert lay._committed_S_q == 384 and lay._n_kpages == 6 and lay._n_pages == 24
     bpe = spectral.payload_bpe(spectral.load_packs(path, budget)[0].bits)
@@ -127,11 +127,41 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, budget):
     assert agree == 1.0
 
 
+def test_spectral_short_prompt_decodes_across_first_commit(tmp_path):
+    """A 100-token prompt on k4ph_b2.5 with a 32-token window: the first decode
+    steps run before any commit (the window alone, no device pack built yet),
+    the flush at 160 tokens commits the first codec page mid-stream.  Teacher
+    forced against the oracle-backed cache, step by step."""
+    g = np.load(GOLD / "e2e_tiny_llama.npz")
+    tokens = torch.from_numpy(g["r16_tokens"]).cuda()
+    model = _tiny_model(n_layers=1)
+    specs = spec_pair("k4ph_b2.5", pack_path=_spectral_pack_file(tmp_path, 1))
+
+    def run(cache):
+        got = []
+        with cache.attach(model), torch.no_grad():
+            got.append(model(tokens[:, :100], past_key_values=cache, use_cache=True).logits[0, -1])
+            for i in range(100, 200):
+                got.append(model(tokens[:, i:i + 1], past_key_values=cache, use_cache=True).logits[0, -1])
+        return torch.stack(got).double().cpu()
+
+    prod = PackedStreamingCache(model.config, *specs, recent_window=32)
+    got = run(prod)
+    ref = run(OracleCache(model.config, *specs, recent_window=32))
+    err = (got - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    agree = (got.argmax(1) == ref.argmax(1)).float().mean().item()
+    print(f"k4ph_b2.5 short prompt: logits max|err| {err:.3e} of {scale:.3f}, argmax agreement {agree:.4f}, "
+          f"committed {prod.layers[0]._committed_S_q}", flush=True)
+    assert prod.layers[0]._committed_S_q == 128
+    assert err <= 2e-3 * max(scale, 1.0) and agree == 1.0
+
+
 def test_spectral_generate_runs(tmp_path):
     """HF generate() on the k4 recipe, two layers."""
     model = _tiny_model()
     ids = torch.randint(0, 256, (1, 200), generator=torch.Generator().manual_seed(9)).cuda()
-    cache = PackedStreamingCache(model.config, *spec_pair("k4_b2.5", pack_path=_spectral_pack_file(tmp_path, 2)),
+    cache = PackedStreamingCache(model.config, *spec_pair("k4ph_b2.5", pack_path=_spectral_pack_file(tmp_path, 2)),
                                  recent_window=32)
     with cache.attach(model), torch.no_grad():
         out = model.generate(ids, past_key_values=cache, max_new_tokens=40, min_new_tokens=40,

@@ -118,7 +118,7 @@ def test_dequant_bit_exact():
         assert Kh.dtype == dt and torch.equal(Kh, K.to(dt)) and torch.equal(Vh, V.to(dt))
 
 
-def _decode_case(h_kv, G, S, T, codec, gen, split_tokens=0, outliers=True):
+def _decode_case(h_kv, G, S, T, codec, gen, split_tokens=0, outliers=True, with_chunked=False):
     k = _keys(h_kv, S + T, gen, outliers)
     v = torch.randn(h_kv, S + T, 128, generator=gen)
     k16, v16 = k.half(), v.half()
@@ -137,6 +137,11 @@ def _decode_case(h_kv, G, S, T, codec, gen, split_tokens=0, outliers=True):
     else:
         ref = A.naive_dense_attention(q.view(h_kv * G, 1, 128), k16[:, S:].float(), v16[:, S:].float(),
                                       G, 128 ** -0.5)
+    if with_chunked:
+        # the reference's own chunked path with fp32 scales (codecs.py:819-822)
+        chunked = A.rtn_chunked_attention(q.view(h_kv * G, 1, 128), cache, k16[:, S:], v16[:, S:], G,
+                                          128 ** -0.5)
+        return out, ref.view(1, h_kv, G, 128), chunked.view(1, h_kv, G, 128)
     return out, ref.view(1, h_kv, G, 128)
 
 
@@ -146,9 +151,13 @@ def test_decode_config1():
     outlier channels x10, values rtn_token 4-bit (groups of 32 channels);
     seed 0.  The reference runs this pair on its chunked path only."""
     gen = torch.Generator().manual_seed(0)
-    out, ref = _decode_case(8, 4, 3968, 128,
-                            dict(k_bits=4, v_bits=4, k_group=32, v_group=32, k_arm=rtn.CHANNEL), gen)
-    _close(out, ref, "config1 rtn_channel K / rtn_token V, 4b g32")
+    out, ref, chunked = _decode_case(8, 4, 3968, 128,
+                                     dict(k_bits=4, v_bits=4, k_group=32, v_group=32, k_arm=rtn.CHANNEL), gen,
+                                     with_chunked=True)
+    _close(out, ref, "config1 rtn_channel K / rtn_token V, 4b g32 (fp16-scale oracle)")
+    # the path the reference executes for this pair: chunked dequant-attention
+    # with the fp32 scales of dequant_packed
+    _close(out, chunked, "config1 vs the reference's chunked path (fp32 scales)")
 
 
 def test_decode_config1_geometry_fused_pair():

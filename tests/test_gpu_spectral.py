@@ -197,7 +197,7 @@ def test_decode_form_scores_match_keys():
         assert torch.equal(Vb[:, :S], V) and not Vb[:, S:].any() and not Sb[:, :, S:].any()
 
 
-@pytest.mark.parametrize("G,T", [(4, 40), (1, 0), (8, 7)])
+@pytest.mark.parametrize("G,T", [(4, 40), (1, 0), (8, 7), (16, 40)])
 def test_partial_form_decode_matches_oracle(G, T):
     """The decode step through the kernel's partial form (per-group softmax
     partials) and the merge with the window: against the oracle's one-softmax
@@ -240,3 +240,25 @@ def test_partial_form_decode_matches_oracle(G, T):
     print(f"G {G} T {T}: partial-form decode vs oracle max_abs {err:.3e} rel {rel:.3e}; vs scores form {d_alt:.3e}",
           flush=True)
     assert err <= 2e-3 and rel <= 1e-2 and d_alt <= 2e-3
+
+
+@pytest.mark.parametrize("G", [4, 16])
+def test_window_only_decode_step(G):
+    """A decode step with no committed token (a layer before its first
+    commit): only the merge runs, over the fp16 window; the layer may have no
+    device pack yet."""
+    gen = torch.Generator().manual_seed(21)
+    T = 45
+    kt = torch.randn(8, T, 128, generator=gen).half()
+    vt = torch.randn(8, T, 128, generator=gen).half()
+    q = torch.randn(8, G, 128, generator=gen).half()
+    consts = k2b.CodecConsts.make(v_seed=0)
+    scale = 128 ** -0.5
+    ref = A.naive_dense_attention(q.reshape(8 * G, 1, 128).float(), kt.float(), vt.float(), G,
+                                  scale).reshape(8, G, 128)
+    for dp in (None, spectral.DevicePack(synthetic_pack(8, 2.5, seed=14), 8, DEV)):
+        out = spectral.decode_attention(dp, None, None, None, None, 0, consts, q.to(DEV), scale,
+                                        k_win=kt.to(DEV), v_win=vt.to(DEV), out_dtype=torch.float32)
+        err = (out.cpu().double() - ref.double()).abs().max().item()
+        print(f"window only G {G} (pack {'given' if dp is not None else 'absent'}): max_abs {err:.3e}", flush=True)
+        assert err <= 2e-3

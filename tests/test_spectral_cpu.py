@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from bmx_amd import _lib, spectral
+from bmx_amd import _lib, k2b, spectral
 from oracle import spectral as O
 from tests.spectral_util import GOLD, golden_pack, synthetic_pack
 
@@ -157,7 +157,7 @@ def test_bad_spectral_arguments_are_rejected_with_message():
 
 
 def test_recipe_and_construction_guards(tmp_path):
-    """spec_pair("k4_b<budget>") needs a pack path; the cache asserts pre-RoPE
+    """spec_pair("k4ph_b<budget>") needs a pack path; the cache asserts pre-RoPE
     keys and a pack file at construction (packed_streaming.py:336-360), loads
     every layer's pack once, and refuses the variants without kernels."""
     from transformers import LlamaConfig
@@ -170,12 +170,17 @@ def test_recipe_and_construction_guards(tmp_path):
     p = synthetic_pack(2, 2.5, seed=1)
     path = tmp_path / "packs.safetensors"
     spectral.save_packs(path, {0: (p.enc, p.dec, p.lam, {2.5: p.bits})}, (2.5,))
+    # the reference's k4 name pairs full-C turboquant_mse values: it must not
+    # answer with another value codec
+    for arm in ("k4_b2.5", "k4_b3"):
+        with pytest.raises(NotImplementedError, match="full-C turboquant_mse"):
+            spec_pair(arm, pack_path=str(path))
     with pytest.raises(ValueError, match="pack-path"):
-        spec_pair("k4_b2.5")
-    for arm in ("k4_b2.5_lq", "k4_b2.5_dec8tl"):
+        spec_pair("k4ph_b2.5")
+    for arm in ("k4ph_b2.5_lq", "k4ph_b2.5_dec8tl"):
         with pytest.raises(NotImplementedError, match="no MI355X kernels"):
             spec_pair(arm, pack_path=str(path))
-    k, v = spec_pair("k4_b2.5", pack_path=str(path))
+    k, v = spec_pair("k4ph_b2.5", pack_path=str(path))
     assert (k.arm, k.pre_rope, k.budget, v.arm, v.bits) == ("spectral", True, 2.5, "turboquant_mse_perhead", 2)
     with pytest.raises(AssertionError, match="pre_rope"):
         PackedStreamingCache(cfg, CacheCodecSpec(arm="spectral", pack_path=str(path), budget=2.5), v)
@@ -201,3 +206,25 @@ def test_bad_merge_arguments_are_rejected_with_message():
     assert lib.bmx_spectral_merge(ct.byref(m), None) != 0 and b"16384" in lib.bmx_last_error()
     m.n_groups = 4
     assert lib.bmx_spectral_merge(ct.byref(m), None) != 0 and b"null pointer" in lib.bmx_last_error()
+
+
+def test_dequant_table_checks_precede_every_form():
+    """The C-ABI carries no table lengths: short or int64 tables, and token
+    counts off the 64-token grid, are refused on the host for the partial form
+    too (no device call is made)."""
+    pack = synthetic_pack(2, 2.5, seed=1)
+    dp = spectral.DevicePack(pack, 2, "cpu")
+    consts = k2b.CodecConsts.make()
+    S = 256
+    kp = torch.zeros(S // 64, dp.k_page_bytes, dtype=torch.uint8)
+    vp = torch.zeros(S // 16, dp.v_page_bytes, dtype=torch.uint8)
+    kt, vt = torch.arange(S // 64, dtype=torch.int32), torch.arange(S // 16, dtype=torch.int32)
+    q = torch.zeros(2, 4, 128)
+    part = torch.zeros(2, 4, S // 64, 130)
+    bad = [(kt[:-1], vt, S), (kt, vt[:-1], S), (kt.long(), vt, S), (kt, vt.long(), S), (kt, vt, S - 32)]
+    for k_t, v_t, n in bad:
+        with pytest.raises(ValueError, match="k_table|multiple of 64"):
+            spectral.dequant(dp, kp, k_t, vp, v_t, n, consts, apply_rope=k2b.ROPE_EXACT, q=q,
+                             partials=part if n == S else torch.zeros(2, 4, n // 64, 130))
+        with pytest.raises(ValueError, match="k_table|multiple of 64"):
+            spectral.dequant(dp, kp, k_t, vp, v_t, n, consts)
