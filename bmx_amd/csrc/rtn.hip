@@ -45,7 +45,7 @@ constexpr int kRThreads = 64 * kRWaves;
 constexpr int kRGroupPages = 4;                  // 64-token groups, as for k2b
 constexpr int kRGroup = kRGroupPages * kPT;
 constexpr int kRPidWindow = 64;
-constexpr int kRMaxPrefix = 8 * (kD + kPT * 4) * 2;  // scale bytes of a page at most: h_kv 8,
+constexpr int kRMaxPrefix = 8 * (2 * kD + kPT * 4) * 2;  // scale bytes of a page at most: h_kv 8,
                                                      // channel-arm keys, value groups of 32
 
 // Byte offsets of the four page sections (see include/bmx_rtn.h).
@@ -57,7 +57,8 @@ struct RtnLayout {
     L.ngk = kD / gk;
     L.ngv = kD / gv;
     L.kscale = 0;
-    L.vscale = L.kscale + h_kv * (karm == BMX_RTN_CHANNEL ? kD : kPT * L.ngk) * 2;
+    // channel-arm keys: the fp32 scale as an fp16 pair, hi for every head, then lo
+    L.vscale = L.kscale + h_kv * (karm == BMX_RTN_CHANNEL ? 2 * kD : kPT * L.ngk) * 2;
     L.kcode = L.vscale + h_kv * kPT * L.ngv * 2;
     L.vcode = L.kcode + h_kv * 1024;
     L.bytes = L.vcode + h_kv * 1024;
@@ -176,9 +177,15 @@ __global__ __launch_bounds__(128) void rtn_append_kchan_kernel(const RtnAppendKA
   }
   const int n_pg = a.gk / kPT;
   const int pg0 = (int)(T0 / kPT);
+  // the fp32 scale as hi = fp16(scale) and lo = fp16(scale - hi): hi + lo is
+  // the scale to 2^-22 relative (the reference dequantizes with the fp32 scale)
+  const uint16_t s_hi = float_to_half_bits(scale);
+  const uint16_t s_lo = float_to_half_bits(scale - half_bits_to_float(s_hi));
   for (int p = 0; p < n_pg; ++p) {
     uint8_t* page = a.pages + clamp_page(a.page_ids[pg0 + p], a.n_pool) * a.L.bytes;
-    reinterpret_cast<uint16_t*>(page + a.L.kscale)[h * kD + kchan_slot(c)] = float_to_half_bits(scale);
+    uint16_t* ks = reinterpret_cast<uint16_t*>(page + a.L.kscale);
+    ks[h * kD + kchan_slot(c)] = s_hi;
+    ks[(a.h_kv + h) * kD + kchan_slot(c)] = s_lo;
   }
   __syncthreads();
   for (int e = c; e < n_pg * 256; e += 128) {   // word (q, n, w): token n, channels 32w + 8q ..
@@ -216,7 +223,10 @@ __global__ __launch_bounds__(256) void rtn_dequant_kernel(const RtnDequantKArgs 
   const float sk = a.karm == BMX_RTN_TOKEN ? half_bits_to_float(ksc[(h * kPT + tt) * a.L.ngk + (8 * l) / a.gk]) : 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float s = a.karm == BMX_RTN_TOKEN ? sk : half_bits_to_float(ksc[h * kD + kchan_slot(8 * l + j)]);
+    const float s = a.karm == BMX_RTN_TOKEN
+                        ? sk
+                        : half_bits_to_float(ksc[h * kD + kchan_slot(8 * l + j)]) +
+                              half_bits_to_float(ksc[(a.h_kv + h) * kD + kchan_slot(8 * l + j)]);
     store_elem(a.k_out, row + 8 * l + j, (float)((int)((w >> (4 * j)) & 15u) - 8) * s, a.out_dtype);
   }
   const uint16_t* vcode = reinterpret_cast<const uint16_t*>(page + a.L.vcode + h * 1024);
@@ -393,9 +403,9 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
     const int id = __builtin_amdgcn_readlane(pidv, gi * kRGroupPages + pp - pid_base);
     return a.pages + (int64_t)id * pb;
   };
-  // the 4 pages' scale sections, 16-byte chunk c (tid and tid + 512: the
-  // channel-arm key scales make them up to 768 chunks)
-  struct Pre { uint4 c0, c1; };
+  // the 4 pages' scale sections, 16-byte chunk c (tid, tid + 512 and tid +
+  // 1024: the channel-arm key scales, hi and lo, make them up to 1280 chunks)
+  struct Pre { uint4 c0, c1, c2; };
   auto load_chunk = [&](int gi, int c) -> uint4 {
     c = min(c, pre_chunks - 1);
     const int pp = c / chunks_pp;
@@ -406,6 +416,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
     Pre r;
     r.c0 = load_chunk(gi, tid);
     r.c1 = pre_chunks > kRThreads ? load_chunk(gi, tid + kRThreads) : r.c0;
+    r.c2 = pre_chunks > 2 * kRThreads ? load_chunk(gi, tid + 2 * kRThreads) : r.c0;
     return r;
   };
   auto store_prefix = [&](const Pre& v, int slot) {
@@ -417,6 +428,11 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
     if (c1 < pre_chunks) {
       const int pp = c1 / chunks_pp;
       *reinterpret_cast<uint4*>(&ring[slot][pp][(c1 - pp * chunks_pp) * 16]) = v.c1;
+    }
+    const int c2 = tid + 2 * kRThreads;
+    if (c2 < pre_chunks) {
+      const int pp = c2 / chunks_pp;
+      *reinterpret_cast<uint4*>(&ring[slot][pp][(c2 - pp * chunks_pp) * 16]) = v.c2;
     }
   };
   const uint32_t kc_off = (uint32_t)(a.L.kcode + h * 1024 + lane * 16);
@@ -498,15 +514,18 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
       for (int pp = 0; pp < kRGroupPages; ++pp) {
         if constexpr (NGK == 0) {
           // channel-arm keys: the scale varies along the MFMA's K axis, so it
-          // goes into the A operand, as an exact fp16 sum hi + lo of code *
-          // scale (lo = the rounding residual of hi, from one packed FMA)
+          // goes into the A operand, as an fp16 sum hi + lo of code * scale:
+          // hi = fp16(code * s_hi), lo = its rounding residual (one packed
+          // FMA) plus code * s_lo, the fp32 scale being s_hi + s_lo
           const uint4* ksp = reinterpret_cast<const uint4*>(&ring[slot][pp][a.L.kscale]) + h * 16 + q;
+          const uint4* ksl = ksp + a.h_kv * 16;
           const uint32_t kw4[4] = {kc[pp].x, kc[pp].y, kc[pp].z, kc[pp].w};
           float4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int bb = 0; bb < 4; ++bb) {
-            const uint4 sp = ksp[4 * bb];
+            const uint4 sp = ksp[4 * bb], sl = ksl[4 * bb];
             const uint32_t s4[4] = {sp.x, sp.y, sp.z, sp.w};
+            const uint32_t l4[4] = {sl.x, sl.y, sl.z, sl.w};
             uint32_t cp[4];
             nibble_pairs(kw4[bb], cp);
             union { uint32_t u[4]; half8_t v; } khi, klo;
@@ -514,7 +533,8 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
             for (int p = 0; p < 4; ++p) {
               const half2_t hi = as_h2r(cp[p]) * as_h2r(s4[p]);
               khi.u[p] = as_u32r(hi);
-              klo.u[p] = as_u32r(__builtin_elementwise_fma(as_h2r(cp[p]), as_h2r(s4[p]), -hi));
+              const half2_t res = __builtin_elementwise_fma(as_h2r(cp[p]), as_h2r(s4[p]), -hi);
+              klo.u[p] = as_u32r(__builtin_elementwise_fma(as_h2r(cp[p]), as_h2r(l4[p]), res));
             }
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi.v, qh[bb], s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi.v, ql[bb], s, 0, 0, 0);

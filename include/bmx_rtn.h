@@ -21,9 +21,12 @@
  * of the key / value scales, 32, 64 or 128: channels, or tokens for
  * rtn_channel keys).  Sections, in this order:
  *   KSCALE [h_kv][16 t][128/gk] fp16   rtn_token: key scale of (token t, group)
- *          [h_kv][4 b][4 q][8 j] fp16  rtn_channel: scale of channel 32b + 8q +
+ *          [2][h_kv][4 b][4 q][8 j] fp16  rtn_channel: scale of channel 32b + 8q +
  *                                      p(j), p = 0 4 1 5 2 6 3 7, for the token
- *                                      group that holds the page
+ *                                      group that holds the page, as the pair
+ *                                      hi = fp16(s) ([0]), lo = fp16(s - hi) ([1]):
+ *                                      hi + lo is the fp32 scale to 2^-21
+ *                                      relative (scales of 1/8 and up)
  *   VSCALE [h_kv][4 q][128/gv][4 i] fp16  value scale of (token 4q + i, group)
  *   KCODE  [h_kv][4 q][16 n][4 w] u32  token n, channels 32w + 8q .. +7, channel
  *                                      32w + 8q + j in nibble j of the word
@@ -32,9 +35,9 @@
  * ("lane 16q + n" of an MFMA reads each 16-byte code slice contiguously; the
  * two scale sections come first so that a workgroup stages them with one
  * cooperative copy.)  Bytes per token = h_kv * (128 + 2 * 128/gk + 2 * 128/gv)
- * for rtn_token keys (1152 at h_kv 8, gk = gv = 32), h_kv * (144 + 2 * 128/gv)
- * for rtn_channel keys (the group's channel scales repeated in each of its
- * pages).
+ * for rtn_token keys (1152 at h_kv 8, gk = gv = 32), h_kv * (160 + 2 * 128/gv)
+ * for rtn_channel keys (1344; the group's channel scale pairs repeated in each
+ * of its pages).
  */
 #ifndef BMX_RTN_H
 #define BMX_RTN_H
@@ -71,7 +74,10 @@ size_t bmx_rtn_page_bytes(const bmx_rtn_geom* geom);
  * the keys (codecs.py:723-725: groups of k_group tokens per channel): per
  * group scale = max|x| (clamped to 1e-12) / qmax in fp32, code =
  * clamp(round-half-even(x / scale), -qmax - 1, qmax), qmax = 2^(bits-1) - 1;
- * the page keeps the scale in fp16, as build_kv_stacked_packed stacks it.
+ * the page keeps a token-arm scale in fp16, as build_kv_stacked_packed stacks
+ * it for the reference's fused pair, and a channel-arm scale as an fp16 (hi,
+ * lo) pair, since the reference reads that arm with its fp32 scale
+ * (dequant_packed, codecs.py:819-822).
  * n_codec_pages pages of 128 tokens become 8 * n_codec_pages physical pages
  * listed in page_ids.
  * ---------------------------------------------------------------------- */
@@ -97,7 +103,7 @@ int bmx_rtn_append(const bmx_rtn_append_args* args, void* stream);
  * Decode attention.  Replaces fused_decode_attention_packed + _finalize_decode
  * (cache/triton_dequant_attention.py:731-832, 504-575): one query step per
  * sequence attends to its packed_len[b] committed tokens (keys and values
- * dequantized in-kernel, code * fp16 scale) and to its tail_len[b] fp16
+ * dequantized in-kernel, code * the page's scale) and to its tail_len[b] fp16
  * recent-window tokens, one base-e softmax over their union.  The fields
  * mean what they mean in bmx_k2b_decode_args.
  * ---------------------------------------------------------------------- */
@@ -131,7 +137,7 @@ int bmx_rtn_decode(const bmx_rtn_decode_args* args, void* stream);
 /* ------------------------------------------------------------------------
  * Dequantize pages to dense keys and values (prefill): the dequant half of
  * chunked_attention._dense_kv and the dtype cast of _assemble_dense_kv
- * (cache/chunked_attention.py:148-251) for the RTN arms (code * fp16 scale,
+ * (cache/chunked_attention.py:148-251) for the RTN arms (code * the page's scale,
  * rounded once to out_dtype).  k_out/v_out: device [h_kv][16 * n_pages][128].
  * ---------------------------------------------------------------------- */
 typedef struct {

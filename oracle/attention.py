@@ -236,7 +236,10 @@ class RtnOracleCache:
     reference's fused RTN path computes it: code times the fp16 scale of its
     group, the scale stacked in fp16 by build_kv_stacked_packed
     (triton_dequant_attention.py:1436-1440), read in fp32 by the kernel
-    (:670-715)."""
+    (:670-715).  Channel-arm keys have no fused path in the reference, whose
+    chunked path reads them with the fp32 scale (codecs.py:819-822); the
+    pages carry that scale as the fp16 pair hi + lo (layout.scale_pair), so
+    their page scale is float32(hi) + float32(lo)."""
 
     def __init__(self, h_kv: int, *, k_bits: int, v_bits: int, k_group: int, v_group: int,
                  k_arm: int = 0, page: int = 128):
@@ -261,13 +264,21 @@ class RtnOracleCache:
     def _dense(self, blocks, group, fp16_scales, channel=False):
         out = []
         for p, _, _ in blocks:
-            sc = p["scale"].half().float() if fp16_scales else p["scale"]
+            if not fp16_scales:
+                sc = p["scale"]
+            elif channel:   # the page's hi + lo pair of the fp32 scale
+                hi = p["scale"].half().float()
+                sc = hi + (p["scale"] - hi).half().float()
+            else:
+                sc = p["scale"].half().float()
             M = C.rtn_dequantize_packed(p["Q_int"], sc, group)   # (C, S) for the channel arm
             out.append(C.from_matrix(M.mT if channel else M, self.h_kv))
         return torch.cat(out, dim=1)
 
     def dense_kv(self, fp16_scales: bool = True):
-        """(K (h_kv, S, d), V (h_kv, S, d)) fp32."""
+        """(K (h_kv, S, d), V (h_kv, S, d)) fp32; fp16_scales: with the scales
+        the pages hold (fp16, or the hi + lo pair for channel-arm keys), else
+        with the codec's fp32 scales."""
         return (self._dense(self.k_blocks, self.k_group, fp16_scales, self.k_arm == 1),
                 self._dense(self.v_blocks, self.v_group, fp16_scales))
 

@@ -193,8 +193,9 @@ def unpack_pages(pages: np.ndarray, h_kv: int, rank: int):
 # RTN pages (include/bmx_rtn.h): 16 tokens, per head 4-bit offset-binary codes
 # (code + 8) and fp16 scales of channel groups gk / gv (32, 64 or 128).
 #   KSCALE [h][16 t][128/gk] fp16            token-arm keys
-#          [h][4 b][4 q][8 j'] fp16          channel-arm keys: channel 32b + 8q + p(j'),
-#                                            p = 0 4 1 5 2 6 3 7, scale of the page's token group
+#          [2][h][4 b][4 q][8 j'] fp16       channel-arm keys: channel 32b + 8q + p(j'),
+#                                            p = 0 4 1 5 2 6 3 7, scale of the page's token
+#                                            group as hi = fp16(s) then lo = fp16(s - hi)
 #   VSCALE [h][4 q][128/gv][4 i] fp16        token 4q + i
 #   KCODE  [h][4 q][16 n][4 w] u32           channels 32w + 8q + j at nibble j
 #   VCODE  [h][4 q][16 c][8 b] u16           channel 16b + c, token 4q + j at nibble j
@@ -207,11 +208,19 @@ def kchan_slot(c):
     return (c & ~7) + 2 * (j & 3) + (j >> 2)
 
 
+def scale_pair(s):
+    """fp32 scales -> (hi, lo) fp16 with hi = fp16(s), lo = fp16(s - hi)."""
+    s = np.asarray(s, np.float32)
+    hi = s.astype(np.float16)
+    lo = (s - hi.astype(np.float32)).astype(np.float16)
+    return hi, lo
+
+
 def rtn_sections(h_kv: int, gk: int, gv: int, k_arm: int = 0) -> dict:
     ngk, ngv = 128 // gk, 128 // gv
     off = 0
     out = {}
-    ksize = h_kv * 128 * 2 if k_arm == 1 else h_kv * 16 * ngk * 2
+    ksize = h_kv * 128 * 2 * 2 if k_arm == 1 else h_kv * 16 * ngk * 2
     for name, size in (("kscale", ksize), ("vscale", h_kv * 16 * ngv * 2),
                        ("kcode", h_kv * 1024), ("vcode", h_kv * 1024)):
         out[name] = (off, size)
@@ -225,10 +234,11 @@ def rtn_page_bytes(h_kv: int, gk: int, gv: int, k_arm: int = 0) -> int:
 
 
 def pack_rtn_pages(kq, ks16, vq, vs16, h_kv: int, gk: int, gv: int, k_arm: int = 0) -> np.ndarray:
-    """Codes and fp16 scales of T tokens (T multiple of 16) -> (T/16, page_bytes) u8.
+    """Codes and scales of T tokens (T multiple of 16) -> (T/16, page_bytes) u8.
 
     kq, vq   (h_kv, T, 128) int in [-8, 7]
-    ks16     (h_kv, T, 128/gk) fp16, or (h_kv, T/gk, 128) for channel-arm keys
+    ks16     (h_kv, T, 128/gk) fp16, or for channel-arm keys (h_kv, T/gk, 128)
+             fp32, stored as the pair scale_pair()
     vs16     (h_kv, T, 128/gv) fp16"""
     kq, vq = np.asarray(kq, np.int64), np.asarray(vq, np.int64)
     T = kq.shape[1]
@@ -241,8 +251,8 @@ def pack_rtn_pages(kq, ks16, vq, vs16, h_kv: int, gk: int, gv: int, k_arm: int =
         t0 = 16 * p
         o, n = sec["kscale"]
         if k_arm == 1:
-            row = np.zeros((h_kv, 128), np.float16)
-            row[:, slots] = ks16[:, t0 // gk].astype(np.float16)
+            row = np.zeros((2, h_kv, 128), np.float16)
+            row[0][:, slots], row[1][:, slots] = scale_pair(ks16[:, t0 // gk])
             pages[p, o:o + n] = row.view(np.uint8).ravel()
         else:
             pages[p, o:o + n] = np.ascontiguousarray(ks16[:, t0:t0 + 16].astype(np.float16)).view(np.uint8).ravel()
@@ -264,20 +274,21 @@ def pack_rtn_pages(kq, ks16, vq, vs16, h_kv: int, gk: int, gv: int, k_arm: int =
 
 def unpack_rtn_pages(pages: np.ndarray, h_kv: int, gk: int, gv: int, k_arm: int = 0):
     """Inverse of pack_rtn_pages: (kq, ks16, vq, vs16); channel-arm key scales
-    come back per page, (h_kv, P, 128)."""
+    come back per page as float32 hi + lo, (h_kv, P, 128)."""
     P = pages.shape[0]
     sec = rtn_sections(h_kv, gk, gv, k_arm)
     ngk, ngv = 128 // gk, 128 // gv
     kq = np.zeros((h_kv, 16 * P, 128), np.int64)
     vq = np.zeros_like(kq)
-    ks = np.zeros((h_kv, P, 128) if k_arm == 1 else (h_kv, 16 * P, ngk), np.float16)
+    ks = np.zeros((h_kv, P, 128), np.float32) if k_arm == 1 else np.zeros((h_kv, 16 * P, ngk), np.float16)
     vs = np.zeros((h_kv, 16 * P, ngv), np.float16)
     slots = np.array([kchan_slot(c) for c in range(128)])
     for p in range(P):
         t0 = 16 * p
         o, n = sec["kscale"]
         if k_arm == 1:
-            ks[:, p] = pages[p, o:o + n].view(np.float16).reshape(h_kv, 128)[:, slots]
+            pair = pages[p, o:o + n].view(np.float16).reshape(2, h_kv, 128)[:, :, slots].astype(np.float32)
+            ks[:, p] = pair[0] + pair[1]
         else:
             ks[:, t0:t0 + 16] = pages[p, o:o + n].view(np.float16).reshape(h_kv, 16, ngk)
         o, n = sec["vscale"]

@@ -92,7 +92,9 @@ def test_append_channel_arm_codes_bit_exact(h_kv, codec):
     kq, ks, vq, vs = OL.unpack_rtn_pages(pages, h_kv, codec["k_group"], codec["v_group"], k_arm=1)
     rkq, rks, rvq, rvs = _oracle(h_kv, k, v, codec).codes()
     np.testing.assert_array_equal(kq, rkq.numpy())
-    np.testing.assert_array_equal(ks, np.repeat(rks.numpy().astype(np.float16), codec["k_group"] // 16, axis=1))
+    hi, lo = OL.scale_pair(rks.numpy())   # the fp32 scale as the page's fp16 pair
+    np.testing.assert_array_equal(ks, np.repeat(hi.astype(np.float32) + lo.astype(np.float32),
+                                                codec["k_group"] // 16, axis=1))
     np.testing.assert_array_equal(vq, rvq.numpy())
     np.testing.assert_array_equal(vs, rvs.numpy().astype(np.float16))
 

@@ -27,24 +27,33 @@ def test_page_bytes_match_numpy_layout(h_kv, gk, gv):
 def test_headline_rtn_bytes_per_token():
     assert rtn.page_bytes(8) == 16 * 1152
     # channel-arm keys: 128 channel scales per head and page
-    assert rtn.page_bytes(8, k_arm=rtn.CHANNEL) == OL.rtn_page_bytes(8, 32, 32, 1) == 16 * 1216
+    assert rtn.page_bytes(8, k_arm=rtn.CHANNEL) == OL.rtn_page_bytes(8, 32, 32, 1) == 16 * 1344
 
 
 def test_channel_arm_page_round_trip():
     rng = np.random.default_rng(2)
     h_kv, gk, gv, T = 4, 64, 32, 128
     kq, vq = rng.integers(-8, 8, (h_kv, T, 128)), rng.integers(-8, 8, (h_kv, T, 128))
-    ks = rng.random((h_kv, T // gk, 128)).astype(np.float16)
+    ks = (0.01 + rng.random((h_kv, T // gk, 128))).astype(np.float32)   # normal fp16 range
     vs = rng.random((h_kv, T, 128 // gv)).astype(np.float16)
     pages = OL.pack_rtn_pages(kq, ks, vq, vs, h_kv, gk, gv, k_arm=1)
     a, b, c, d = OL.unpack_rtn_pages(pages, h_kv, gk, gv, k_arm=1)
     np.testing.assert_array_equal(a, kq)
-    np.testing.assert_array_equal(b, np.repeat(ks, gk // 16, axis=1))
+    hi, lo = OL.scale_pair(ks)
+    np.testing.assert_array_equal(b, np.repeat(hi.astype(np.float32) + lo.astype(np.float32), gk // 16, axis=1))
+    # hi + lo carries the fp32 scale to ~2^-22 relative (2^-21 with the fp32
+    # sum's own rounding, while lo is a normal fp16: scales of 1/8 and up;
+    # below, lo's subnormal step 2^-24 sets the bound); hi alone to 2^-12
+    rel = np.abs(b[:, ::gk // 16] / ks - 1)
+    assert rel[ks >= 0.125].max() <= 2 ** -21 and rel.max() <= 2 ** -17
+    assert np.abs(hi.astype(np.float32) / ks - 1).max() > 2 ** -16
     np.testing.assert_array_equal(c, vq)
     np.testing.assert_array_equal(d, vs)
-    # channel 13 = 32*0 + 8*1 + 5 sits at slot 8 + 2*1 + 1 of its row
+    # channel 13 = 32*0 + 8*1 + 5 sits at slot 8 + 2*1 + 1 of its row; head 0's
+    # lo row follows every head's hi row
     o = OL.rtn_sections(h_kv, gk, gv, 1)["kscale"][0]
-    assert pages[0, o:o + 256].view(np.float16)[8 + 3] == ks[0, 0, 13]
+    assert pages[0, o:o + 256].view(np.float16)[8 + 3] == hi[0, 0, 13]
+    assert pages[0, o + 256 * h_kv:o + 256 * h_kv + 256].view(np.float16)[8 + 3] == lo[0, 0, 13]
 
 
 @pytest.mark.parametrize("h_kv,gk,gv", [(8, 32, 32), (2, 64, 128)])
