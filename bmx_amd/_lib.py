@@ -14,6 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libbmx_k2b.so"
 
 BMX_OK = 0
+DECODE_SCRATCH_BYTES = 32 << 20   # BMX_K2B_DECODE_SCRATCH_BYTES (include/bmx_k2b.h)
 SECTIONS = ("us", "vnorm", "kscale", "kres", "vcode")
 
 
@@ -231,6 +232,7 @@ EXPORTS = {
                                         ct.POINTER(ct.c_size_t)]),
     "bmx_k2b_decode_workspace_bytes": (ct.c_size_t, [ct.POINTER(DecodeArgs)]),
     "bmx_k2b_decode": (ct.c_int, [ct.POINTER(DecodeArgs), ct.c_void_p]),
+    "bmx_k2b_decode_noalloc": (ct.c_int, [ct.POINTER(DecodeArgs), ct.c_void_p]),
     "bmx_k2b_append": (ct.c_int, [ct.POINTER(AppendArgs), ct.c_void_p]),
     "bmx_k2b_dequant": (ct.c_int, [ct.POINTER(DequantArgs), ct.c_void_p]),
     "bmx_rtn_page_bytes": (ct.c_size_t, [ct.POINTER(RtnGeom)]),

@@ -831,45 +831,108 @@ static hipError_t launch_split(const DecodeKArgs& k, dim3 grid, size_t smem, hip
   return launch_split_sw<R, 16>(k, grid, smem, st);
 }
 
+// The split and merge launches of one decode call over the workspace ws
+// (ws_cap bytes usable); name prefixes every error message.
+static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, size_t ws_cap,
+                         const std::string& name);
+
 extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   if (!a) return fail(BMX_E_INVALID, "bmx_k2b_decode: args is NULL");
+  return decode_launch(a, stream, a->workspace, a->workspace_bytes, "bmx_k2b_decode");
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode.  The partials live in a file-scope device array of
+// BMX_K2B_DECODE_SCRATCH_BYTES (every GPU the library runs on holds its own
+// copy until the process ends).  In host code the array's name is only a
+// host-side stand-in: its device address is fetched once per device with
+// hipGetSymbolAddress, with that device current, and only that address is
+// ever passed to a kernel.  All calls on one GPU share the array: calls that
+// overlap on one GPU (two streams, two threads) race.  Nothing needs clearing:
+// a call writes every partial and window score it reads.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[BMX_K2B_DECODE_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];
+
+static int scratch_address(void** out, std::string& err) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    err = std::string("no current HIP device in range: ") + hipGetErrorString(e);
+    return BMX_E_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+      return BMX_E_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return BMX_OK;
+}
+
+extern "C" int bmx_k2b_decode_noalloc(const bmx_k2b_decode_args* a, void* stream) {
+  if (!a) return fail(BMX_E_INVALID, "bmx_k2b_decode_noalloc: args is NULL");
+  if (a->batch < 1) return fail(BMX_E_INVALID, "bmx_k2b_decode_noalloc: batch must be >= 1");
+  const size_t need = bmx_k2b_decode_workspace_bytes(a);
+  if (need > (size_t)BMX_K2B_DECODE_SCRATCH_BYTES)
+    return fail(BMX_E_WORKSPACE, "bmx_k2b_decode_noalloc: this call needs " + std::to_string(need) +
+                                     " bytes of partials, above the static scratch's " +
+                                     std::to_string((size_t)BMX_K2B_DECODE_SCRATCH_BYTES) +
+                                     " (use bmx_k2b_decode with a workspace)");
+  void* ptr = nullptr;
+  std::string err;
+  const int rc = scratch_address(&ptr, err);
+  if (rc != BMX_OK) return fail(rc, "bmx_k2b_decode_noalloc: " + err);
+  return decode_launch(a, stream, ptr, (size_t)BMX_K2B_DECODE_SCRATCH_BYTES, "bmx_k2b_decode_noalloc");
+}
+
+static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, size_t ws_cap,
+                         const std::string& name) {
   const bmx_k2b_geom& g = a->geom;
-  if (g.h_kv < 1 || g.h_kv > kWaves) return fail(BMX_E_INVALID, "bmx_k2b_decode: h_kv must be 1..8");
-  if (g.rank != 16 && g.rank != 32) return fail(BMX_E_INVALID, "bmx_k2b_decode: rank must be 16 or 32");
+  if (g.h_kv < 1 || g.h_kv > kWaves) return fail(BMX_E_INVALID, name + ": h_kv must be 1..8");
+  if (g.rank != 16 && g.rank != 32) return fail(BMX_E_INVALID, name + ": rank must be 16 or 32");
   if (g.n_q_groups < 1 || g.n_q_groups > 16)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: n_q_groups must be 1..16");
-  if (a->batch < 1) return fail(BMX_E_INVALID, "bmx_k2b_decode: batch must be >= 1");
+    return fail(BMX_E_INVALID, name + ": n_q_groups must be 1..16");
+  if (a->batch < 1) return fail(BMX_E_INVALID, name + ": batch must be >= 1");
   if (a->max_packed_len < 0 || a->max_packed_len % kCodec != 0)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: max_packed_len must be a multiple of 128");
+    return fail(BMX_E_INVALID, name + ": max_packed_len must be a multiple of 128");
   if (a->max_packed_len > 0 && a->max_pages * kPT < a->max_packed_len)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: max_pages*16 < max_packed_len");
+    return fail(BMX_E_INVALID, name + ": max_pages*16 < max_packed_len");
   if (a->tail_cap < 0 || a->tail_cap > 4096)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: tail_cap must be 0..4096");
+    return fail(BMX_E_INVALID, name + ": tail_cap must be 0..4096");
   if (!(a->rope_scaling > 0.0f) || !(a->rope_scaling < 1e30f))
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: rope_scaling must be finite and > 0");
+    return fail(BMX_E_INVALID, name + ": rope_scaling must be finite and > 0");
   if (a->split_tokens < 0 || a->split_tokens % kGroup != 0)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: split_tokens must be a multiple of 64");
+    return fail(BMX_E_INVALID, name + ": split_tokens must be a multiple of 64");
   if (!a->q || !a->out || !a->packed_len || !a->tail_len)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: q/out/packed_len/tail_len must be non-NULL");
+    return fail(BMX_E_INVALID, name + ": q/out/packed_len/tail_len must be non-NULL");
   if (a->max_packed_len > 0 && (!a->pages || !a->page_table || !a->basis))
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: pages/page_table/basis must be non-NULL");
+    return fail(BMX_E_INVALID, name + ": pages/page_table/basis must be non-NULL");
   if (a->max_packed_len > 0 && a->n_pool_pages < 1)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: n_pool_pages must be >= 1");
+    return fail(BMX_E_INVALID, name + ": n_pool_pages must be >= 1");
   if (a->tail_cap > 0 && (!a->k_tail || !a->v_tail))
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: k_tail/v_tail must be non-NULL when tail_cap > 0");
+    return fail(BMX_E_INVALID, name + ": k_tail/v_tail must be non-NULL when tail_cap > 0");
   if (a->tail_cap > 0 && (a->tail_stride_t % 8 != 0 || a->tail_stride_h % 8 != 0 ||
                           a->tail_stride_b % 8 != 0))
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: tail strides must be multiples of 8 elements");
+    return fail(BMX_E_INVALID, name + ": tail strides must be multiples of 8 elements");
   const int max_splits = choose_splits(a);
   const size_t need = ws_bytes(a, max_splits);
   if (max_splits > 8192)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: more than 8192 splits; use a larger split_tokens");
-  if (!a->workspace || a->workspace_bytes < need)
-    return fail(BMX_E_WORKSPACE, "bmx_k2b_decode: workspace missing or smaller than "
+    return fail(BMX_E_INVALID, name + ": more than 8192 splits; use a larger split_tokens");
+  if (!ws || ws_cap < need)
+    return fail(BMX_E_WORKSPACE, name + ": workspace missing or smaller than "
                                  "bmx_k2b_decode_workspace_bytes()");
   hipStream_t st = (hipStream_t)stream;
   const size_t rows = (size_t)a->batch * max_splits * g.h_kv * g.n_q_groups;
-  float* ws_acc = (float*)a->workspace;
+  float* ws_acc = (float*)ws;
   float* ws_ml = ws_acc + rows * kD;
   float* ws_win = ws_ml + rows * 2;
   const float qscale = a->sm_scale * 1.4426950408889634f;
@@ -899,10 +962,10 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   }
   for (int j = 0; j < 4; ++j)
     if (!(a->codebook[j] == a->codebook[j]) || (j > 0 && !(a->codebook[j] > a->codebook[j - 1])))
-      return fail(BMX_E_INVALID, "bmx_k2b_decode: codebook must be 4 finite ascending levels");
+      return fail(BMX_E_INVALID, name + ": codebook must be 4 finite ascending levels");
   const LevelMap lm = level_map(a->codebook);
   if (lm.err > 4e-6)
-    return fail(BMX_E_INVALID, "bmx_k2b_decode: no fp16 level map for this codebook (error " +
+    return fail(BMX_E_INVALID, name + ": no fp16 level map for this codebook (error " +
                                    std::to_string(lm.err) + ")");
   for (int j = 0; j < 4; ++j) k.level_hi[j] = lm.hi[j];
   k.level_mu = lm.mu;
@@ -920,11 +983,11 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
   hipError_t e = g.rank == 32 ? launch_split<32>(k, grid, smem, st)
                               : launch_split<16>(k, grid, smem, st);
   if (e != hipSuccess)
-    return fail(BMX_E_HIP, std::string("bmx_k2b_decode: split kernel launch: ") + hipGetErrorString(e));
+    return fail(BMX_E_HIP, name + std::string(": split kernel launch: ") + hipGetErrorString(e));
   if (a->split_end_event) {
     e = hipEventRecord((hipEvent_t)a->split_end_event, st);
     if (e != hipSuccess)
-      return fail(BMX_E_HIP, std::string("bmx_k2b_decode: hipEventRecord: ") + hipGetErrorString(e));
+      return fail(BMX_E_HIP, name + std::string(": hipEventRecord: ") + hipGetErrorString(e));
   }
   CombineKArgs c{};
   c.h_kv = g.h_kv; c.G = g.n_q_groups;
@@ -941,6 +1004,6 @@ extern "C" int bmx_k2b_decode(const bmx_k2b_decode_args* a, void* stream) {
                      0, st, c);
   e = hipGetLastError();
   if (e != hipSuccess)
-    return fail(BMX_E_HIP, std::string("bmx_k2b_decode: combine kernel launch: ") + hipGetErrorString(e));
+    return fail(BMX_E_HIP, name + std::string(": combine kernel launch: ") + hipGetErrorString(e));
   return BMX_OK;
 }

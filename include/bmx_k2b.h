@@ -138,6 +138,19 @@ typedef struct {
 size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* args);
 int bmx_k2b_decode(const bmx_k2b_decode_args* args, void* stream);
 
+/* Allocation-free decode: no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * bmx_k2b_decode, except that workspace / workspace_bytes are ignored: the
+ * split partials live in a static device array of
+ * BMX_K2B_DECODE_SCRATCH_BYTES that every GPU the library runs on holds until
+ * the process ends.  A call whose bmx_k2b_decode_workspace_bytes() exceeds it
+ * fails with BMX_E_WORKSPACE.  All calls on one GPU share that array: calls
+ * that overlap on one GPU (other streams, other threads) race and must be
+ * serialized by the caller.  Calls no hipMalloc/hipFree. */
+#define BMX_K2B_DECODE_SCRATCH_BYTES (32u << 20)
+int bmx_k2b_decode_noalloc(const bmx_k2b_decode_args* args, void* stream);
+
 /* ------------------------------------------------------------------------
  * Quantize-on-append (page commit).  Replaces the write path of
  * PackedStreamingLayer.update (cache/packed_streaming.py:582-730):
