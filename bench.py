@@ -59,6 +59,10 @@ def parse():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--window", type=int, default=128)
     ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--layout", choices=["contig", "paged"], default="contig",
+                    help="contig: each layer's pages in order in its own pool, no page table (the "
+                         "layout PackedStreamingCache allocates); paged: one shuffled pool read "
+                         "through a page table")
     ap.add_argument("--cpu-sample-tokens", type=int, default=16384)
     ap.add_argument("--cpu-reps", type=int, default=7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -828,14 +832,18 @@ def main():
     gen = torch.Generator(device=dev).manual_seed(2024)
     layers = []
     pool = synth.PagePool(n_pages * args.layers, H_KV, args.rank, dev,
-                          gen=torch.Generator().manual_seed(7))
+                          gen=torch.Generator().manual_seed(7) if args.layout == "paged" else None)
     for li in range(args.layers):
         k_pre = synth.k2b_keys(H_KV, args.ctx, args.rank, gen)
         v = synth.values(H_KV, args.ctx, gen)
         seq = synth.encode_sequence(pool, k_pre[:, :packed], v[:, :packed], args.rank, consts)
+        if args.layout == "contig":   # the layer's own run of pages, read with no table
+            base = seq.page_ids[0]
+            assert seq.page_ids == list(range(base, base + n_pages))
         lay = {
             "seq": seq,
-            "pt": synth.page_table([seq], device=dev),
+            "pt": synth.page_table([seq], device=dev) if args.layout == "paged" else None,
+            "pages": pool.pages if args.layout == "paged" else pool.pages[seq.page_ids[0]: seq.page_ids[0] + n_pages],
             "len": torch.tensor([packed], dtype=torch.int32, device=dev),
             "k_tail": synth.rope_keys(k_pre[:, packed:], packed, consts).unsqueeze(0).contiguous(),
             "v_tail": v[:, packed:].unsqueeze(0).contiguous(),
@@ -854,7 +862,7 @@ def main():
     ws = k2b.DecodeWorkspace()
     for lay in layers:
         lay["plan"] = k2b.DecodePlan(
-            lay["q"], pool.pages, lay["pt"], lay["len"], packed, lay["seq"].basis16, consts,
+            lay["q"], lay["pages"], lay["pt"], lay["len"], packed, lay["seq"].basis16, consts,
             D ** -0.5, rank=args.rank, k_tail=lay["k_tail"], v_tail=lay["v_tail"],
             tail_len=lay["tail_len"], tail_cap=tail, out=lay["out"],
             split_tokens=args.split_tokens, workspace=ws)
@@ -915,7 +923,7 @@ def main():
     call_us = step_us / args.layers                                          # back-to-back calls
     achieved = bytes_call / (call_us * 1e-6) / 1e9
     bpe = page_bytes * 8 / 16 / (2 * C)
-    workload_key = {"ctx": args.ctx, "window": W, "rank": args.rank, "h_kv": H_KV, "G": G}
+    workload_key = {"ctx": args.ctx, "window": W, "rank": args.rank, "h_kv": H_KV, "G": G, "layout": args.layout}
     res = {
         "metric": METRIC,
         "value": round(step_us, 2),
@@ -932,7 +940,11 @@ def main():
         "config": {
             "workload": (f"k2b rank-{args.rank} decode attention, Llama-3.1-8B geometry "
                          f"({args.layers} layers, 32q/8kv heads, d 128), batch 1, ctx {args.ctx} "
-                         f"= {packed} packed + {tail} fp16 tail, 16-token pages, RoPE 5e5 at read"),
+                         f"= {packed} packed + {tail} fp16 tail, 16-token pages "
+                         + ("in order per layer, no page table (the cache's layout)" if args.layout == "contig"
+                            else "shuffled over one pool, read through a page table")
+                         + ", RoPE 5e5 at read"),
+            "layout": args.layout,
             "ctx": args.ctx, "packed_tokens": packed, "tail_tokens": tail, "layers": args.layers,
             "batch": 1, "rank": args.rank, "bits_per_entry_kv_avg": round(bpe, 4),
             "bytes_per_token_layer": page_bytes // 16,

@@ -373,13 +373,13 @@ class PackedStreamingLayer(DynamicLayer):
                 tail_len=torch.tensor([T], dtype=torch.int32, device=dev), tail_cap=T, **self._rtn)
             return out.reshape(self._h_kv * G, 1, self._d_head)
         if P > 0:
-            pool, table, basis16 = self._pool, self._table, self._basis16
+            # the pool holds this sequence's pages in order: no table to read
+            pool, basis16 = self._pool, self._basis16
         else:   # window only: the kernel reads no page
             pool = torch.zeros(1, k2b.page_bytes(self._h_kv, self._rank), dtype=torch.uint8, device=dev)
-            table = torch.zeros(1, 1, dtype=torch.int32, device=dev)
             basis16 = torch.zeros(self._h_kv * self._d_head, self._rank, dtype=torch.float16, device=dev)
         out = k2b.decode(
-            q.reshape(1, self._h_kv, G, self._d_head).float().contiguous(), pool, table,
+            q.reshape(1, self._h_kv, G, self._d_head).float().contiguous(), pool, None,
             self._packed_len_dev, P, basis16, self._consts, scaling, rank=self._rank,
             k_tail=k_tail, v_tail=v_tail,
             tail_len=torch.tensor([T], dtype=torch.int32, device=dev), tail_cap=T)

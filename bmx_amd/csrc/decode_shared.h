@@ -56,8 +56,8 @@ __device__ __forceinline__ void batch_shares(const int32_t* packed_len, int max_
 // ---------------------------------------------------------------------------
 // Recent-window scores (any decode kernel whose arguments carry k_tail, ts_b,
 // ts_h, ts_t, tail_cap, win_rescale, ws_win, h_kv, G).  Window tile j (tokens
-// 16j .. 16j + 15 of the fp16 post-RoPE window) belongs to workgroup j mod
-// max_splits and is scored on the MFMA like a packed page: A = its 16 key rows (lane: token lane & 15, quarter
+// 16j .. 16j + 15 of the fp16 post-RoPE window), scored by the workgroup the
+// decode kernel deals it to, goes on the MFMA like a packed page: A = its 16 key rows (lane: token lane & 15, quarter
 // q = lane >> 4 holds channels 16bb + 4q + i and + 64, interleaved: the K order
 // of the query fragments), B = the query fragments split into fp16 high and low
 // parts (q = hi + lo to 2^-22 relative), so the scores carry the fp32 query.
@@ -120,22 +120,26 @@ __device__ __forceinline__ void query_fragments(const float4_t qraw[8], float sc
 }
 
 // ---------------------------------------------------------------------------
-// Combine: merge of the packed partials and the recent window.  One wave per
-// (16-channel chunk, query row, sequence): the partials arrive already in the
-// output domain, so a chunk needs only its own 16 channels of every split
-// (contiguous, 64 B per split) plus every split's (max, sum); the window needs
-// its scores (computed by the split kernel) and its 16 value channels of every
-// token.  Lane (phase p = lane & 15, quarter c4 = lane >> 4) takes channels
-// 4c4 .. 4c4 + 3 of splits p, p + 16, ... and of window tokens p, p + 16, ...;
-// every row of 16 lanes sees every split and token, so the maxima and sums
-// are row reductions (DPP, no LDS, no barrier) and only the final Hadamard
-// crosses rows.  All loads of the first pass are issued before any use.
+// Combine: merge of the packed partials and the recent window.  One workgroup
+// of kCmbWaves waves per (16-channel chunk, query row, sequence): the partials
+// arrive already in the output domain, so a chunk needs only its own 16
+// channels of every split (contiguous, 64 B per split) plus every split's
+// (max, sum); the window needs its scores (computed by the split kernel) and
+// its 16 value channels of every token.  Splits and window tokens are dealt
+// in blocks of 16: wave w takes blocks w, w + kCmbWaves, ...; lane (phase
+// p = lane & 15, quarter c4 = lane >> 4) takes channels 4c4 .. 4c4 + 3 of
+// element p of each of its blocks.  Every row of 16 lanes sees all of its
+// wave's elements, so a wave's maxima and sums are row reductions (DPP);
+// the waves' (max, sum, channel sums) then meet once in LDS, and only the
+// final Hadamard crosses rows.  All loads of a wave's first pass are issued
+// before any use.
 // ---------------------------------------------------------------------------
-constexpr int kCmbThreads = 64;
+constexpr int kCmbWaves = 4;
+constexpr int kCmbThreads = 64 * kCmbWaves;
 constexpr int kChunk = 16;                  // channels per merge unit
 constexpr int kChunks = kD / kChunk;
-constexpr int kCmbSplits = 16;              // splits per lane per pass
-constexpr int kCmbTokens = 8;               // window tokens per lane per pass
+constexpr int kCmbSplits = 4;               // split blocks per wave per pass
+constexpr int kCmbTokens = 2;               // window-token blocks per wave per pass
 
 struct CombineKArgs {
   int h_kv, G, max_splits, tail_cap;   // max_splits: partial slots per row
@@ -178,6 +182,11 @@ __device__ __forceinline__ float row_reduce16(float x) {
   return x;
 }
 
+// weight e^(m_i - M) of a part with running max m_i (0 for an empty part)
+__device__ __forceinline__ float part_weight(float mi, float M) {
+  return mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - M);
+}
+
 // kRotated: the packed partials are sums of k2b's rotated value levels with
 // the H8 half of the inverse Hadamard applied (the merge applies H16, the
 // signs and packed_scale); otherwise they are plain channel sums.
@@ -185,7 +194,7 @@ template <bool kRotated>
 __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs a) {
   const int ch = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
   const int h = r / a.G;
-  const int lane = threadIdx.x, p = lane & 15, c4 = lane >> 4;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, p = lane & 15, c4 = lane >> 4;
   const int S_slots = a.max_splits;
   const int64_t row = (int64_t)b * a.h_kv * a.G + r;   // (b, h, g) row
   const float* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S_slots * kChunk + 4 * c4;
@@ -193,6 +202,10 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   const float* swb = a.ws_win + row * a.tail_cap;
   const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch + 4 * c4;
   typedef float f2_t __attribute__((ext_vector_type(2)));
+  // element e of this lane in pass j0: p + 16 (wave + kCmbWaves u) + j0
+  auto elem = [&](int j0, int u) { return j0 + p + 16 * (wave + kCmbWaves * u); };
+  constexpr int kSplitPass = 16 * kCmbWaves * kCmbSplits;   // splits per pass of the workgroup
+  constexpr int kTokenPass = 16 * kCmbWaves * kCmbTokens;   // window tokens per pass
 
   f2_t ml[kCmbSplits];
   float4_t pv[kCmbSplits];
@@ -202,7 +215,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   auto load_splits = [&](int j0) {
 #pragma unroll
     for (int u = 0; u < kCmbSplits; ++u) {
-      const int i = min(j0 + p + 16 * u, S - 1);
+      const int i = min(elem(j0, u), S - 1);
       ml[u] = *reinterpret_cast<const f2_t*>(mlb + 2 * (int64_t)i);
       pv[u] = *reinterpret_cast<const float4_t*>(accb + (int64_t)i * kChunk);
     }
@@ -210,7 +223,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   auto load_tokens = [&](int t0, int t_end) {   // t_end >= 1
 #pragma unroll
     for (int u = 0; u < kCmbTokens; ++u) {
-      const int t = min(t0 + p + 16 * u, t_end - 1);
+      const int t = min(elem(t0, u), t_end - 1);
       ws[u] = swb[t];
       wv[u] = *reinterpret_cast<const uint2*>(vb + (int64_t)t * a.ts_t);
     }
@@ -227,24 +240,24 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   load_splits(0);
   const int T = min(max(a.tail_len[b], 0), a.tail_cap);
 
-  // ---- packed partials: online over passes of 16 splits per lane ----
+  // ---- packed partials: online over passes ----
   float mp = -INFINITY, lp = 0.f;
   float4_t xp = {0.f, 0.f, 0.f, 0.f};
-  for (int j0 = 0; j0 < S; j0 += 16 * kCmbSplits) {
+  for (int j0 = 0; j0 < S; j0 += kSplitPass) {
     if (j0 != 0) load_splits(j0);
     float mloc = -INFINITY;
 #pragma unroll
     for (int u = 0; u < kCmbSplits; ++u)
-      if (j0 + p + 16 * u < S) mloc = fmaxf(mloc, ml[u][0]);
+      if (elem(j0, u) < S) mloc = fmaxf(mloc, ml[u][0]);
     const float mnew = fmaxf(mp, row_reduce16<true>(mloc));
     if (mnew != -INFINITY) {
-      const float sc = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - mnew);
+      const float sc = part_weight(mp, mnew);
       xp *= sc;
       lp *= sc;
 #pragma unroll
       for (int u = 0; u < kCmbSplits; ++u) {
         // lanes past the sequence's splits re-read its last: select, not weight by 0
-        const bool ok = j0 + p + 16 * u < S && ml[u][0] != -INFINITY;
+        const bool ok = elem(j0, u) < S && ml[u][0] != -INFINITY;
         const float w = ok ? __builtin_amdgcn_exp2f(ml[u][0] - mnew) : 0.f;
         xp += ok ? w * pv[u] : float4_t{0.f, 0.f, 0.f, 0.f};
         lp = ok ? __builtin_fmaf(w, ml[u][1], lp) : lp;
@@ -252,31 +265,37 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
       mp = mnew;
     }
   }
-  // ---- window: online over passes of 8 tokens per lane ----
+  // ---- window: online over passes ----
   float mt = -INFINITY, lt = 0.f;
   float4_t xt = {0.f, 0.f, 0.f, 0.f};
-  for (int t0 = 0; t0 < T; t0 += 16 * kCmbTokens) {
+  for (int t0 = 0; t0 < T; t0 += kTokenPass) {
     if (t0 != 0) load_tokens(t0, T);
     float mloc = -INFINITY;
 #pragma unroll
     for (int u = 0; u < kCmbTokens; ++u)
-      if (t0 + p + 16 * u < T) mloc = fmaxf(mloc, ws[u]);
+      if (elem(t0, u) < T) mloc = fmaxf(mloc, ws[u]);
     const float mnew = fmaxf(mt, row_reduce16<true>(mloc));
-    const float sc = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - mnew);
-    xt *= sc;
-    lt *= sc;
+    if (mnew != -INFINITY) {
+      const float sc = part_weight(mt, mnew);
+      xt *= sc;
+      lt *= sc;
 #pragma unroll
-    for (int u = 0; u < kCmbTokens; ++u) {
-      const float w = t0 + p + 16 * u < T ? __builtin_amdgcn_exp2f(ws[u] - mnew) : 0.f;
-      const float4_t vf = {half_bits_to_float(wv[u].x & 0xffff), half_bits_to_float(wv[u].x >> 16),
-                           half_bits_to_float(wv[u].y & 0xffff), half_bits_to_float(wv[u].y >> 16)};
-      xt += w * vf;
-      lt += w;
+      for (int u = 0; u < kCmbTokens; ++u) {
+        const float w = elem(t0, u) < T ? __builtin_amdgcn_exp2f(ws[u] - mnew) : 0.f;
+        const float4_t vf = {half_bits_to_float(wv[u].x & 0xffff), half_bits_to_float(wv[u].x >> 16),
+                             half_bits_to_float(wv[u].y & 0xffff), half_bits_to_float(wv[u].y >> 16)};
+        xt += w * vf;
+        lt += w;
+      }
+      mt = mnew;
     }
-    mt = mnew;
   }
-  // ---- row sums (every row holds all splits and tokens, for its 4 channels) ----
-  float y[4], z[4];
+  // ---- row sums (every row holds all of the wave's splits and tokens, for
+  // its 4 channels), then the waves meet in LDS: per wave (mp, lp, mt, lt)
+  // and the 16 channels' packed and window sums ----
+  __shared__ float s_m[kCmbWaves][4];
+  __shared__ float4_t s_y[kCmbWaves][4], s_z[kCmbWaves][4];
+  float4_t y, z;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     y[i] = row_reduce16<false>(xp[i]);
@@ -284,6 +303,34 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   }
   lp = row_reduce16<false>(lp);
   lt = row_reduce16<false>(lt);
+  if (p == 0) {
+    s_y[wave][c4] = y;
+    s_z[wave][c4] = z;
+    if (c4 == 0) {
+      s_m[wave][0] = mp;
+      s_m[wave][1] = lp;
+      s_m[wave][2] = mt;
+      s_m[wave][3] = lt;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float Mp = -INFINITY, Mt = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kCmbWaves; ++w) {
+    Mp = fmaxf(Mp, s_m[w][0]);
+    Mt = fmaxf(Mt, s_m[w][2]);
+  }
+  lp = lt = 0.f;
+  y = z = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kCmbWaves; ++w) {
+    const float wp = part_weight(s_m[w][0], Mp), wt = part_weight(s_m[w][2], Mt);
+    lp = __builtin_fmaf(wp, s_m[w][1], lp);
+    lt = __builtin_fmaf(wt, s_m[w][3], lt);
+    y += wp * s_y[w][c4];
+    z += wt * s_z[w][c4];
+  }
   if constexpr (kRotated) {
     // H16 over the chunk's channel c = 4 c4 + i: bits 0-1 in registers, bits 2-3
     // across rows; then sign and 1/(128 kappa)
@@ -310,9 +357,8 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
     }
   }
   if (p == 0) {
-    const float M = fmaxf(mp, mt);
-    const float wp = mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp - M);
-    const float wt = mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mt - M);
+    const float M = fmaxf(Mp, Mt);
+    const float wp = part_weight(Mp, M), wt = part_weight(Mt, M);
     const float inv = 1.0f / (lp * wp + lt * wt);
     float4_t o;
 #pragma unroll

@@ -109,6 +109,26 @@ __device__ __forceinline__ void kres_pairs(const KresMasks& km, uint32_t w0, uin
                 ((w2 >> 13) & 0x00040004u) | km.e0) + b0;
 }
 
+// Pair P (0..15) of kres_pairs alone, for a caller that decodes the pairs
+// just before it uses them.
+template <int P>
+__device__ __forceinline__ half2_t kres_pair(const KresMasks& km, uint32_t w0, uint32_t w1, uint32_t w2) {
+  const half2_t b0 = {(_Float16)-1028.0f, (_Float16)-1028.0f};
+  const half2_t b1 = {(_Float16)-132.0f, (_Float16)-132.0f};
+  const half2_t b2 = {(_Float16)-20.0f, (_Float16)-20.0f};
+  if constexpr (P == 15) {
+    return as_h2(((w0 >> 15) & 0x00010001u) | ((w1 >> 14) & 0x00020002u) | ((w2 >> 13) & 0x00040004u) | km.e0) + b0;
+  } else {
+    constexpr int d = P / 5, k = P % 5;
+    const uint32_t x = d == 0 ? w0 : d == 1 ? w1 : w2;
+    if constexpr (k == 0) return as_h2((x & km.m0) | km.e0) + b0;
+    if constexpr (k == 1) return as_h2((x & km.m1) | km.e1) + b1;
+    if constexpr (k == 2) return as_h2((x & km.m2) | km.e2) + b2;
+    if constexpr (k == 3) return as_h2(((x >> 9) & km.m0) | km.e0) + b0;
+    return as_h2(((x >> 9) & km.m1) | km.e1) + b1;
+  }
+}
+
 // Physical page id clamped into the pool: a corrupt table entry cannot fault.
 __device__ __forceinline__ int64_t clamp_page(int32_t pid, int32_t n_pool) {
   return (int64_t)min(max(pid, 0), n_pool - 1);

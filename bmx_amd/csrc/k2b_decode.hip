@@ -52,6 +52,7 @@
 #include "decode_shared.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -169,6 +170,15 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
   }
 }
 
+// Window tiles of split `split` of S: tiles split, split + S, ... (a tile's
+// rows are one memory round trip; dealing several to the splits that own
+// one group less made those splits the last to finish).  Returns the first
+// tile and the stride between the split's tiles.
+__device__ __forceinline__ int first_win_tile(int split, int S, int& stride) {
+  stride = S;
+  return split;
+}
+
 // A workgroup with no packed tokens: its window tiles, then an empty partial
 // (max -inf) that the merge ignores.  Out of line, with the kernel argument
 // block passed by its kernarg-segment address: a second inlined copy of the
@@ -176,7 +186,9 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
 __device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, int split, int S, int h, int n,
                                                  int q) {
   const int n_tiles = (a.tail_cap + 15) >> 4;
-  if (split < n_tiles) {
+  int stride;
+  const int j0 = first_win_tile(split, S, stride);
+  if (j0 < n_tiles) {
     const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
     float4_t qraw[8];
 #pragma unroll
@@ -185,7 +197,7 @@ __device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, in
     half8_t qh[4], ql[4];
     query_fragments(qraw, n < a.G ? a.qscale_rope : 0.0f, qh, ql);
     const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
-    for (int j = split; j < n_tiles; j += S) {
+    for (int j = j0; j < n_tiles; j += stride) {
       uint2 kw[8];
       load_win_tile(a, tail_base, j, n, q, kw);
       score_win_tile(a, b, h, j, n, q, kw, qh, ql);
@@ -199,7 +211,7 @@ __device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, in
 
 // R: key rank (16 or 32).  SW: query slot width (G rounded up to 4, 8 or 16);
 // the 16 score columns of a page hold 16/SW pages after compaction.
-template <int R, int SW>
+template <int R, int SW, bool CONTIG>
 __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const DecodeKArgs a) {
   constexpr int NSLOT = 16 / SW;             // pages per compacted score register
   constexpr int NCR = kGroupPages / NSLOT;   // compacted registers per group
@@ -249,14 +261,21 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   };
   int g0, g1;
   range(len_spec, g0, g1);
-  const int32_t* ptab_row = a.page_table + (int64_t)b * a.max_pages;
+  // no page table: the sequence's pages are contiguous, logical page i of
+  // sequence b at physical page b * max_pages + i (the page ids are computed,
+  // so the first pages are requested at once, with no table round trip)
+  // (a template parameter: a guarded table load joined with another path
+  // would make the compiler wait on it right away)
+  constexpr bool contig = CONTIG;
+  const int32_t* ptab_row = contig ? nullptr : a.page_table + (int64_t)b * a.max_pages;
   // Balanced static partition of the sequence's 64-token groups over the
-  // max_splits workgroups.  The page-table read is issued for the host bound
-  // max_packed_len before the device length arrives, and redone in the rare
-  // case that the sequence is shorter.
+  // max_splits workgroups.  The page ids (a page-table read) are taken for the
+  // host bound max_packed_len before the device length arrives, and taken
+  // again in the rare case that the sequence is shorter.
   // ids of pages first .. first+63 of the range; an empty range reads the
   // (valid) length word instead, so the load has no branch to wait in
-  auto load_ids_raw = [&](int first, int count) {
+  auto load_ids_raw = [&](int first, int count) -> int {
+    if constexpr (contig) return b * a.max_pages + g0 * kGroupPages + min(first + lane, max(count - 1, 0));
     const int32_t* src = count > 0 ? ptab_row + g0 * kGroupPages + min(first + lane, count - 1)
                                    : a.packed_len + b;
     return (int)*src;
@@ -266,6 +285,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const float fq = a.inv_freq[fj];
   const float c8 = a.step8_c[fj], s8 = a.step8_s[fj];
   const float stc = a.step_c[fj], sts = a.step_s[fj];
+  // keep those loads ahead of every later one (loads complete in issue order,
+  // and the table production must not wait for the basis or the pages)
+  __builtin_amdgcn_sched_barrier(0);
   const int pid_raw = load_ids_raw(0, (g1 - g0) * kGroupPages);
   const int len_raw = a.packed_len[b];
   hvec_t vh[8];
@@ -322,24 +344,6 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
       }
     }
   };
-  // the tables of the range for the host bound, made while the page table is
-  // in flight; remade below in the rare case that the sequence is shorter
-  produce_groups(0, min(g1 - g0, cs_bufs), 0);
-
-  int pidv = (int)clamp_page(pid_raw, a.n_pool);
-  const int len = min(len_raw, a.max_packed_len) & ~(kGroup - 1);
-  if (len != len_spec) {
-    range(len, g0, g1);
-    pidv = (int)clamp_page(load_ids_raw(0, (g1 - g0) * kGroupPages), a.n_pool);
-    t_begin = g0 * kGroup;
-    produce_groups(0, min(g1 - g0, cs_bufs), 0);
-  }
-  const int n_groups = g1 - g0;
-  if (n_groups == 0) {  // nothing packed here: the window tiles and an empty partial
-    if (active)
-      empty_range_partial(*(const DecodeKArgs*)__builtin_amdgcn_kernarg_segment_ptr(), b, split, S, h, n, q);
-    return;
-  }
   auto load_ids = [&](int first, int count) { return (int)clamp_page(load_ids_raw(first, count), a.n_pool); };
   const int C = kD * a.h_kv;
   const int quarter = C / 4;
@@ -348,9 +352,8 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const int sh_chunks = SHB / 4;       // 16-byte chunks of the 4 pages' prefixes
   const int chunks_pp = SHB / 16;
   uint8_t* ring = smem + cs_bufs * kCsBuf * 4;                                  // [3][4][SHB]
-  const int n_pages = n_groups * kGroupPages;
-
   // page ids of the range, a window of 64 per lane-vector
+  int pidv = contig ? load_ids(0, (g1 - g0) * kGroupPages) : 0;
   int pid_base = 0;
   auto page_ptr = [&](int gi, int pp) -> const uint8_t* {   // uniform (gi, pp)
     const int id = __builtin_amdgcn_readlane(pidv, gi * kGroupPages + pp - pid_base);
@@ -377,21 +380,51 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     return *reinterpret_cast<const uint2*>(page_ptr(gi, pp) + vcode_off);
   };
 
-  // ---- first group in flight ----
-  uint4 pre = load_prefix(0);
-  const uint4 pre1 = load_prefix(min(1, n_groups - 1));
+  // ---- first group in flight: at once for contiguous pages (for the host
+  // bound, before the tables are made), else after the page-table read ----
+  uint4 pre, pre1;
   uint3 kres[kGroupPages];   // this group's codes (the next group's are fetched
   uint2 vcd[kGroupPages];    // into separate registers at the top of the group)
+  auto issue_first = [&](int ng) {
+    pre = load_prefix(0);
+    pre1 = load_prefix(min(1, ng - 1));
 #pragma unroll
-  for (int pp = 0; pp < kGroupPages; ++pp) {
-    kres[pp] = load_kres(0, pp);
-    vcd[pp] = load_vcode(0, pp);
+    for (int pp = 0; pp < kGroupPages; ++pp) {
+      kres[pp] = load_kres(0, pp);
+      vcd[pp] = load_vcode(0, pp);
+    }
+  };
+  if (contig && g1 > g0) issue_first(g1 - g0);
+
+  // the tables of the range for the host bound, made while the page table (or
+  // the first pages) are in flight; remade below in the rare case that the
+  // sequence is shorter
+  produce_groups(0, min(g1 - g0, cs_bufs), 0);
+
+  if (!contig) pidv = (int)clamp_page(pid_raw, a.n_pool);
+  const int len = min(len_raw, a.max_packed_len) & ~(kGroup - 1);
+  if (len != len_spec) {
+    range(len, g0, g1);
+    pidv = load_ids(0, (g1 - g0) * kGroupPages);
+    t_begin = g0 * kGroup;
+    produce_groups(0, min(g1 - g0, cs_bufs), 0);
+    if (contig && g1 > g0) issue_first(g1 - g0);
   }
+  const int n_groups = g1 - g0;
+  if (n_groups == 0) {  // nothing packed here: the window tiles and an empty partial
+    if (active)
+      empty_range_partial(*(const DecodeKArgs*)__builtin_amdgcn_kernarg_segment_ptr(), b, split, S, h, n, q);
+    return;
+  }
+  if (!contig) issue_first(n_groups);
+  const int n_pages = n_groups * kGroupPages;
 
   // the rows of this workgroup's first window tile, if it owns one: issued
   // after the first group's pages, whose addresses wait for every load before
+  int win_stride;
+  const int win_j0 = first_win_tile(split, S, win_stride);
   uint2 kw[8];
-  if (split < n_win_tiles) load_win_tile(a, tail_base, split, n, q, kw);
+  if (win_j0 < n_win_tiles) load_win_tile(a, tail_base, win_j0, n, q, kw);
 
   if (tid < 256) {
     const uint32_t l0 = a.level_hi[0], l1 = a.level_hi[1], l2 = a.level_hi[2], l3 = a.level_hi[3];
@@ -405,9 +438,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   query_fragments(qraw, (n < a.G) ? a.qscale_rope : 0.0f, qf, qlo);
 
   // recent-window tiles (the first one's rows are in flight)
-  if (active && split < n_win_tiles) {
-    score_win_tile(a, b, h, split, n, q, kw, qf, qlo);
-    for (int j = split + S; j < n_win_tiles; j += S) {
+  if (active && win_j0 < n_win_tiles) {
+    score_win_tile(a, b, h, win_j0, n, q, kw, qf, qlo);
+    for (int j = win_j0 + win_stride; j < n_win_tiles; j += win_stride) {
       load_win_tile(a, tail_base, j, n, q, kw);
       score_win_tile(a, b, h, j, n, q, kw, qf, qlo);
     }
@@ -464,47 +497,52 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
       const uint8_t* grp = ring + slot * kGroupPages * SHB;
       const uint32_t* csb = cst + (gi % cs_bufs) * kCsBuf;
       // key-residual scale pairs (s_j, s_{j+64}), j = 16bb + 4q + i: 16 bytes
-      // per bb in the group's prefix (re-read per page: fewer live VGPRs)
-      const uint8_t* scl[4];
+      // per bb in the group's prefix, read once per group
+      uint32_t sv[4][4];
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb) {
         const int f = h * kD + 2 * (16 * bb + 4 * q);
         const int slot = f / quarter, off = f - slot * quarter;
-        scl[bb] = grp + slot * SHB + a.L.kscale + 2 * off;
+        const uint4 s4 = *reinterpret_cast<const uint4*>(grp + slot * SHB + a.L.kscale + 2 * off);
+        sv[bb][0] = s4.x; sv[bb][1] = s4.y; sv[bb][2] = s4.z; sv[bb][3] = s4.w;
       }
-      // ---- K side: scores of the 4 pages ----
+      // ---- K side: scores of the 4 pages, a (j, j + 64) slice at a time:
+      // the slice's two key tiles, its 4 residual pairs, RoPE, one score MFMA ----
       float4_t sc[kGroupPages];
 #pragma unroll
       for (int pp = 0; pp < kGroupPages; ++pp) {
         const uint8_t* pre_p = grp + pp * SHB;
         const hvec_t us = *reinterpret_cast<const hvec_t*>(pre_p + a.L.us + lane * (2 * KQ));
-        float4_t kt[8];
-#pragma unroll
-        for (int bt = 0; bt < 8; ++bt) {
-          const float4_t z = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (R == 32)
-            kt[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[bt], us, z, 0, 0, 0);
-          else
-            kt[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh[bt], us, z, 0, 0, 0);
-        }
-        half2_t cp[16];
-        kres_pairs(km, kres[pp].x, kres[pp].y, kres[pp].z, cp);
+        const uint32_t w0 = kres[pp].x, w1 = kres[pp].y, w2 = kres[pp].z;
         float4_t s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
+        auto slice = [&](auto bbc) {
+          constexpr int bb = decltype(bbc)::value;
+          const float4_t z = {0.f, 0.f, 0.f, 0.f};
+          float4_t klo, khi;
+          if constexpr (R == 32) {
+            klo = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[bb], us, z, 0, 0, 0);
+            khi = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[bb + 4], us, z, 0, 0, 0);
+          } else {
+            klo = __builtin_amdgcn_mfma_f32_16x16x16f16(vh[bb], us, z, 0, 0, 0);
+            khi = __builtin_amdgcn_mfma_f32_16x16x16f16(vh[bb + 4], us, z, 0, 0, 0);
+          }
           const uint4 c4 = *reinterpret_cast<const uint4*>(csb + (pp * kPT + n) * kCsRow + 16 * bb + 4 * q);
-          const uint4 s4 = *reinterpret_cast<const uint4*>(scl[bb]);
           const uint32_t cv[4] = {c4.x, c4.y, c4.z, c4.w};
-          const uint32_t sv[4] = {s4.x, s4.y, s4.z, s4.w};
+          const half2_t cp[4] = {kres_pair<4 * bb + 0>(km, w0, w1, w2), kres_pair<4 * bb + 1>(km, w0, w1, w2),
+                                 kres_pair<4 * bb + 2>(km, w0, w1, w2), kres_pair<4 * bb + 3>(km, w0, w1, w2)};
           union { half2_t h2[4]; half8_t v; } ka;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            half2_t pr = {(_Float16)kt[bb][i], (_Float16)kt[bb + 4][i]};
-            pr = __builtin_elementwise_fma(cp[4 * bb + i], as_h2(sv[i]), pr);
+            half2_t pr = {(_Float16)klo[i], (_Float16)khi[i]};
+            pr = __builtin_elementwise_fma(cp[i], as_h2(sv[bb][i]), pr);
             ka.h2[i] = rope2(pr, cv[i]);
           }
           s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, qf[bb], s, 0, 0, 0);
-        }
+        };
+        slice(std::integral_constant<int, 0>{});
+        slice(std::integral_constant<int, 1>{});
+        slice(std::integral_constant<int, 2>{});
+        slice(std::integral_constant<int, 3>{});
         sc[pp] = s;
         __builtin_amdgcn_sched_barrier(0);   // bound the cross-page overlap (VGPR budget)
       }
@@ -811,24 +849,29 @@ static int fail(int code, const std::string& msg) {
   return code;
 }
 
-template <int R, int SW>
+template <int R, int SW, bool CONTIG>
 static hipError_t launch_split_sw(const DecodeKArgs& k, dim3 grid, size_t smem, hipStream_t st) {
   static size_t attr_bytes = 0;
   if (attr_bytes < smem) {
-    hipError_t e = hipFuncSetAttribute((const void*)k2b_decode_split_kernel<R, SW>,
+    hipError_t e = hipFuncSetAttribute((const void*)k2b_decode_split_kernel<R, SW, CONTIG>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) return e;
     attr_bytes = smem;
   }
-  hipLaunchKernelGGL((k2b_decode_split_kernel<R, SW>), grid, dim3(kThreads), smem, st, k);
+  hipLaunchKernelGGL((k2b_decode_split_kernel<R, SW, CONTIG>), grid, dim3(kThreads), smem, st, k);
   return hipGetLastError();
+}
+
+template <int R, bool CONTIG>
+static hipError_t launch_split_c(const DecodeKArgs& k, dim3 grid, size_t smem, hipStream_t st) {
+  if (k.G <= 4) return launch_split_sw<R, 4, CONTIG>(k, grid, smem, st);
+  if (k.G <= 8) return launch_split_sw<R, 8, CONTIG>(k, grid, smem, st);
+  return launch_split_sw<R, 16, CONTIG>(k, grid, smem, st);
 }
 
 template <int R>
 static hipError_t launch_split(const DecodeKArgs& k, dim3 grid, size_t smem, hipStream_t st) {
-  if (k.G <= 4) return launch_split_sw<R, 4>(k, grid, smem, st);
-  if (k.G <= 8) return launch_split_sw<R, 8>(k, grid, smem, st);
-  return launch_split_sw<R, 16>(k, grid, smem, st);
+  return k.page_table ? launch_split_c<R, false>(k, grid, smem, st) : launch_split_c<R, true>(k, grid, smem, st);
 }
 
 // The split and merge launches of one decode call over the workspace ws
@@ -914,8 +957,8 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
     return fail(BMX_E_INVALID, name + ": split_tokens must be a multiple of 64");
   if (!a->q || !a->out || !a->packed_len || !a->tail_len)
     return fail(BMX_E_INVALID, name + ": q/out/packed_len/tail_len must be non-NULL");
-  if (a->max_packed_len > 0 && (!a->pages || !a->page_table || !a->basis))
-    return fail(BMX_E_INVALID, name + ": pages/page_table/basis must be non-NULL");
+  if (a->max_packed_len > 0 && (!a->pages || !a->basis))
+    return fail(BMX_E_INVALID, name + ": pages/basis must be non-NULL");
   if (a->max_packed_len > 0 && a->n_pool_pages < 1)
     return fail(BMX_E_INVALID, name + ": n_pool_pages must be >= 1");
   if (a->tail_cap > 0 && (!a->k_tail || !a->v_tail))

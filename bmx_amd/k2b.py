@@ -119,18 +119,20 @@ class DecodeWorkspace:
 _DEFAULT_WS: dict = {}
 
 
-def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor,
+def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None,
            packed_len: torch.Tensor, max_packed_len: int, basis16: torch.Tensor,
            consts: CodecConsts, sm_scale: float, *, rank: int,
            k_tail: torch.Tensor | None = None, v_tail: torch.Tensor | None = None,
            tail_len: torch.Tensor | None = None, tail_cap: int = 0,
            out: torch.Tensor | None = None, split_tokens: int = 0,
-           workspace: DecodeWorkspace | None = None,
+           workspace: DecodeWorkspace | None = None, page_stride: int | None = None,
            split_end_event: torch.cuda.Event | None = None, _capture=None) -> torch.Tensor:
     """One decode step.  q (B, h_kv, G, 128) fp32 post-RoPE -> (B, h_kv, G, 128) fp32.
 
-    page_table (B, max_pages) int32; packed_len (B,) int32 committed tokens
-    (multiples of 128, <= max_packed_len); basis16 (B, C, rank) or (C, rank) fp16;
+    page_table (B, max_pages) int32, or None for contiguous pages: logical page
+    i of sequence b at pool page b * page_stride + i (page_stride defaults to
+    max_packed_len / 16); packed_len (B,) int32 committed tokens (multiples of
+    128, <= max_packed_len); basis16 (B, C, rank) or (C, rank) fp16;
     k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 post-RoPE recent window with
     tail_len (B,) int32 valid rows."""
     B, h_kv, G, d = q.shape
@@ -139,8 +141,16 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor,
           "q must be contiguous fp32 (B, h_kv, G, 128)")
     _need(pages.dtype == torch.uint8 and pages.shape[1] == page_bytes(h_kv, rank),
           "pages must be (n_pages, page_bytes) uint8")
-    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B
-          and page_table.is_contiguous(), "page_table must be contiguous int32 (B, max_pages)")
+    if page_table is None:
+        stride = page_stride if page_stride is not None else max(1, -(-max_packed_len // PAGE_TOKENS))
+        _need(stride * PAGE_TOKENS >= max_packed_len and (B == 1 or page_stride is not None),
+              "contiguous pages: page_stride * 16 must cover max_packed_len (and is required for B > 1)")
+        _need(max_packed_len == 0 or (B - 1) * stride + -(-max_packed_len // PAGE_TOKENS) <= pages.shape[0],
+              "contiguous pages: the pool holds fewer pages than the batch's sequences need")
+    else:
+        _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B
+              and page_table.is_contiguous(), "page_table must be contiguous int32 (B, max_pages)")
+        stride = page_table.shape[1]
     _need(packed_len.dtype == torch.int32 and packed_len.numel() == B, "packed_len must be int32[B]")
     C = h_kv * HEAD_DIM
     if basis16.dim() == 2:
@@ -159,9 +169,9 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor,
     a.geom = _lib.Geom(h_kv, rank, G)
     a.batch = B
     a.q, a.out = _ptr(q), _ptr(out)
-    a.pages, a.page_table, a.max_pages = _ptr(pages), _ptr(page_table), page_table.shape[1]
+    a.pages, a.page_table, a.max_pages = _ptr(pages), _ptr(page_table), stride
     a.n_pool_pages = pages.shape[0]
-    _need(page_table.shape[1] * PAGE_TOKENS >= max_packed_len, "page_table too narrow for max_packed_len")
+    _need(stride * PAGE_TOKENS >= max_packed_len, "page_table too narrow for max_packed_len")
     a.packed_len, a.max_packed_len = _ptr(packed_len), int(max_packed_len)
     a.basis, a.basis_stride = _ptr(basis16), bstride
     a.inv_freq[:] = consts.inv_freq
@@ -204,7 +214,8 @@ class DecodePlan:
 
     def __init__(self, q, pages, page_table, packed_len, max_packed_len, basis16, consts,
                  sm_scale, *, rank, k_tail=None, v_tail=None, tail_len=None, tail_cap=0,
-                 out=None, split_tokens=0, workspace: DecodeWorkspace | None = None):
+                 out=None, split_tokens=0, workspace: DecodeWorkspace | None = None,
+                 page_stride: int | None = None):
         self.out = torch.empty_like(q) if out is None else out
         self._keep = (q, pages, page_table, packed_len, basis16, k_tail, v_tail, tail_len)
         if tail_len is None:
@@ -217,7 +228,8 @@ class DecodePlan:
             captured["a"] = a
         decode(q, pages, page_table, packed_len, max_packed_len, basis16, consts, sm_scale,
                rank=rank, k_tail=k_tail, v_tail=v_tail, tail_len=tail_len, tail_cap=tail_cap,
-               out=self.out, split_tokens=split_tokens, workspace=self.ws, _capture=capture)
+               out=self.out, split_tokens=split_tokens, workspace=self.ws, page_stride=page_stride,
+               _capture=capture)
         self.args = captured["a"]
         self.stream = _stream(q.device)
         self._fn = _lib.lib().bmx_k2b_decode

@@ -100,8 +100,12 @@ typedef struct {
   const uint8_t* pages;       /* device page pool; page i at pages + i*page_bytes */
   int32_t n_pool_pages;       /* pages in the pool; table entries are clamped into
                                  [0, n_pool_pages) so a bad entry cannot fault */
-  const int32_t* page_table;  /* device [batch][max_pages] logical -> physical page */
-  int32_t max_pages;          /* row stride of page_table */
+  const int32_t* page_table;  /* device [batch][max_pages] logical -> physical page, or
+                                 NULL: contiguous pages, logical page i of sequence b
+                                 at physical page b * max_pages + i (the kernel then
+                                 requests the first pages at once, without a table
+                                 read: the layout PackedStreamingLayer allocates) */
+  int32_t max_pages;          /* row stride of page_table (of the pool when NULL) */
   const int32_t* packed_len;  /* device [batch] committed tokens, multiple of 128;
                                  clamped to max_packed_len on the device */
   int32_t max_packed_len;     /* host upper bound of packed_len (sizes the grid) */

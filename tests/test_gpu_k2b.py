@@ -290,6 +290,55 @@ def test_ragged_batch_shuffled_pages():
         _close(out[i], ref.view(h_kv, G, 128), f"ragged seq {i} len {lens[i]}")
 
 
+def test_contiguous_pages_without_table():
+    """No page table (contiguous pages: logical page i of sequence b at pool
+    page b * page_stride + i, the layout the cache allocates): identical output
+    to the same pages read through an identity table, at batch 1 and for a
+    ragged batch of 3 (balanced split) with a stride between sequences."""
+    gen = torch.Generator().manual_seed(19)
+    h_kv, rank, G = 8, 32, 4
+    consts = k2b.CodecConsts.make(v_seed=0)
+    inv = torch.tensor(consts.inv_freq)
+    lens, tails = [4096, 1024, 2560], [130, 77, 200]
+    stride = max(lens) // 16 + 3
+    pool = synth.PagePool(stride * len(lens), h_kv, rank, DEV)
+    seqs, refs, kts, vts = [], [], [], []
+    q = torch.randn(len(lens), h_kv, G, 128, generator=gen)
+    for i, (S, T) in enumerate(zip(lens, tails)):
+        pool.free = list(range(stride * (i + 1) - 1, stride * i - 1, -1))   # pages b*stride, b*stride+1, ...
+        k_pre = synth.k2b_keys(h_kv, S + T, rank, gen)
+        v = synth.values(h_kv, S + T, gen)
+        svd = synth.first_page_svd(k_pre, rank)
+        seqs.append(synth.encode_sequence(pool, k_pre[:, :S].to(DEV), v[:, :S].to(DEV), rank, consts, svd=svd))
+        assert seqs[-1].page_ids == list(range(stride * i, stride * i + S // 16))
+        cos, sin = A.rope_cos_sin(inv, torch.arange(S, S + T))
+        kts.append(A.apply_rope(k_pre[:, S:].float(), cos, sin).half())
+        vts.append(v[:, S:])
+        refs.append(A.k2b_naive_attention(q[i].reshape(h_kv * G, 1, 128), _oracle_cache(k_pre[:, :S], v[:, :S], rank,
+                                                                                        svd),
+                                          inv, kts[-1], vts[-1], G, 128 ** -0.5).view(h_kv, G, 128))
+    for B in (1, 3):
+        cap = max(tails[:B])
+        k_tail = torch.zeros(B, h_kv, cap, 128, dtype=torch.float16)
+        v_tail = torch.zeros_like(k_tail)
+        for i in range(B):
+            k_tail[i, :, :tails[i]], v_tail[i, :, :tails[i]] = kts[i], vts[i]
+        common = dict(rank=rank, k_tail=k_tail.to(DEV), v_tail=v_tail.to(DEV),
+                      tail_len=torch.tensor(tails[:B], dtype=torch.int32, device=DEV), tail_cap=cap)
+        basis = torch.stack([s_.basis16 for s_ in seqs[:B]]) if B > 1 else seqs[0].basis16
+        ln = torch.tensor(lens[:B], dtype=torch.int32, device=DEV)
+        ident = torch.stack([torch.arange(stride * i, stride * (i + 1), dtype=torch.int32) for i in range(B)]).to(DEV)
+        with_table = k2b.decode(q[:B].to(DEV), pool.pages, ident, ln, max(lens[:B]), basis, consts, 128 ** -0.5,
+                                **common)
+        without = k2b.decode(q[:B].to(DEV), pool.pages, None, ln, max(lens[:B]), basis, consts, 128 ** -0.5,
+                             page_stride=stride, **common)
+        torch.cuda.synchronize()
+        print(f"batch {B}: contiguous == identity table: {torch.equal(with_table, without)}", flush=True)
+        assert torch.equal(with_table, without)
+        for i in range(B):
+            _close(without[i], refs[i], f"contiguous batch {B} seq {i}")
+
+
 def test_balanced_batch_matches_static_split():
     """A ragged batch runs balanced (each sequence a share of the CUs
     proportional to its length, read from the device lengths); the same batch
