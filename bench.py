@@ -265,8 +265,10 @@ def run_stream(args, torch, k2b, synth, dev) -> dict:
     flush schedule moves (every 128 steps) each layer commits one codec page
     through bmx_k2b_append, its window drops those 128 tokens, and the layer's
     decode plan is rebound to the new packed length.  Per step and layer the
-    device work is one window write (a copy of the token's post-RoPE key and
-    value), the decode call, and at commits the append and a window shift."""
+    device work is the decode call alone: the token's post-RoPE key and value
+    are given to it apart (new_kv, with the window length from the host), and
+    it stores them into the window; at commits the append and a window shift
+    come on top."""
     L, W, rank, n_pre, n_steps = args.stream_layers, 128, 16, 8192, args.stream_steps
     N = n_pre + n_steps
     flush = lambda S: ((S - W) // 128) * 128 if S > W else 0   # noqa: E731
@@ -275,32 +277,38 @@ def run_stream(args, torch, k2b, synth, dev) -> dict:
     consts = k2b.CodecConsts.make(theta=1e6)
     gen = torch.Generator(device=dev).manual_seed(5)
     ws = k2b.DecodeWorkspace()
-    tail_len = torch.tensor([n_pre - P0], dtype=torch.int32, device=dev)   # shared by the layers
     packed_len = torch.tensor([P0], dtype=torch.int32, device=dev)
     layers = []
     for li in range(L):
         k_pre = synth.k2b_keys(H_KV, N, rank, gen)
         v = synth.values(H_KV, N, gen)
         kv_post = torch.stack([synth.rope_keys(k_pre, 0, consts), v])   # (2, h_kv, N, d)
-        pool = synth.PagePool(P_end // 16, H_KV, rank, dev)
+        pool = synth.PagePool(P_end // 16, H_KV, rank, dev,
+                              gen=torch.Generator().manual_seed(li) if args.layout == "paged" else None)
         seq = synth.encode_sequence(pool, k_pre[:, :P0], v[:, :P0], rank, consts)
         kvt = torch.zeros(2, 1, H_KV, cap, D, dtype=torch.float16, device=dev)
         kvt[:, 0, :, : n_pre - P0] = kv_post[:, :, P0:n_pre]
         lay = {"k_pre": k_pre, "v": v, "kv_post": kv_post, "pool": pool, "seq": seq, "kvt": kvt,
+               "k_new": kv_post[0].unsqueeze(0), "v_new": kv_post[1].unsqueeze(0),
                "q": torch.randn(1, H_KV, G, D, generator=gen, device=dev),
                "out": torch.empty(1, H_KV, G, D, device=dev)}
         layers.append(lay)
     torch.cuda.synchronize()
 
-    def bind(lay, P):
-        pt = synth.page_table([lay["seq"]], max_pages=P_end // 16, device=dev)
-        lay["plan"] = k2b.DecodePlan(lay["q"], lay["pool"].pages, pt, packed_len, P, lay["seq"].basis16,
+    def bind(lay, P, T):
+        if args.layout == "contig":   # the layer's pages in order (asserted), read with no table
+            ids = lay["seq"].page_ids
+            assert ids == list(range(ids[0], ids[0] + len(ids)))
+            pages, pt = lay["pool"].pages[ids[0]:], None
+        else:
+            pages, pt = lay["pool"].pages, synth.page_table([lay["seq"]], max_pages=P_end // 16, device=dev)
+        lay["plan"] = k2b.DecodePlan(lay["q"], pages, pt, packed_len, P, lay["seq"].basis16,
                                      consts, D ** -0.5, rank=rank, k_tail=lay["kvt"][0],
-                                     v_tail=lay["kvt"][1], tail_len=tail_len, tail_cap=cap,
+                                     v_tail=lay["kvt"][1], tail_len=T, tail_cap=cap,
                                      out=lay["out"], workspace=ws)
 
     for lay in layers:
-        bind(lay, P0)
+        bind(lay, P0, n_pre - P0)
     for _ in range(args.warmup):
         for lay in layers:
             lay["plan"].run()
@@ -315,11 +323,8 @@ def run_stream(args, torch, k2b, synth, dev) -> dict:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for s in range(n_pre + c0, n_pre + min(n_steps, c0 + chunk)):
-            T = s - P
+            T = s - P   # the window's rows before token s
             P_new = flush(s + 1)
-            for lay in layers:
-                lay["kvt"][:, 0, :, T] = lay["kv_post"][:, :, s]
-            tail_len.fill_(T + 1)
             if P_new > P:   # commit one codec page per layer, drop it from the window
                 for lay in layers:
                     ids = lay["pool"].alloc(8)
@@ -327,13 +332,12 @@ def run_stream(args, torch, k2b, synth, dev) -> dict:
                     k2b.append(lay["k_pre"][:, P:P_new], lay["v"][:, P:P_new], lay["seq"].basis32,
                                lay["seq"].basis16, lay["pool"].pages,
                                torch.tensor(ids, dtype=torch.int32, device=dev), consts, rank=rank)
-                    lay["kvt"][:, :, :, : T + 1 - 128] = lay["kvt"][:, :, :, 128: T + 1]
-                    bind(lay, P_new)
+                    lay["kvt"][:, :, :, : T - 128] = lay["kvt"][:, :, :, 128:T]
+                    bind(lay, P_new, T - 128)
                 packed_len.fill_(P_new)
-                tail_len.fill_(T + 1 - 128)
-                P, commits = P_new, commits + 1
-            for lay in layers:
-                lay["plan"].run()
+                P, commits, T = P_new, commits + 1, T - 128
+            for lay in layers:   # token s is window row T, given apart
+                lay["plan"].run(tail_len=T + 1, new_kv=(lay["k_new"][:, :, s:s + 1], lay["v_new"][:, :, s:s + 1]))
         e1.record()
         torch.cuda.synchronize()
         dev_ms += e0.elapsed_time(e1)
@@ -358,6 +362,7 @@ def run_stream(args, torch, k2b, synth, dev) -> dict:
                          f"({P0} packed + {n_pre - P0} fp16 window) then {n_steps} one-token steps, "
                          f"a codec page committed every 128 steps"),
             "layers": L, "rank": rank, "prefill": n_pre, "packed_start": P0, "packed_end": P,
+            "layout": args.layout,
             "commits_per_layer": commits,
         },
         "device_time": "HIP events around 16-step chunks queued behind a GPU sleep",

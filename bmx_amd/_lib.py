@@ -52,6 +52,13 @@ class DecodeArgs(ct.Structure):
         ("workspace", ct.c_void_p),
         ("workspace_bytes", ct.c_size_t),
         ("split_end_event", ct.c_void_p),
+        ("tail_len_value", ct.c_int32),
+        ("new_k", ct.c_void_p),
+        ("new_v", ct.c_void_p),
+        ("new_stride_b", ct.c_int64),
+        ("new_stride_h", ct.c_int64),
+        ("new_stride_t", ct.c_int64),
+        ("n_new", ct.c_int32),
     ]
 
 
@@ -143,6 +150,13 @@ class RtnDecodeArgs(ct.Structure):
         ("split_tokens", ct.c_int32),
         ("workspace", ct.c_void_p),
         ("workspace_bytes", ct.c_size_t),
+        ("tail_len_value", ct.c_int32),
+        ("new_k", ct.c_void_p),
+        ("new_v", ct.c_void_p),
+        ("new_stride_b", ct.c_int64),
+        ("new_stride_h", ct.c_int64),
+        ("new_stride_t", ct.c_int64),
+        ("n_new", ct.c_int32),
     ]
 
 

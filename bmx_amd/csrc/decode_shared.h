@@ -54,6 +54,30 @@ __device__ __forceinline__ void batch_shares(const int32_t* packed_len, int max_
 }
 
 // ---------------------------------------------------------------------------
+// The newest rows of the recent window, given apart (a decode step's own
+// token): rows [T - n, T) of every sequence's window (T = the window length,
+// a host value) come from k / v instead of the window buffers, and are
+// copied into the buffers (k_dst / v_dst, the window's own pointers) for
+// the calls that follow: the keys by the split kernel that scores them, the
+// values by the merge that reads them.
+// ---------------------------------------------------------------------------
+struct WinNew {
+  const uint16_t* k;   // fp16 post-RoPE keys, row i of (b, h) at b * sb + h * sh + i * st
+  const uint16_t* v;   // fp16 values, same indexing
+  int64_t sb, sh, st;
+  int n;               // rows given apart (0: none)
+  int T;               // window length when given by the host (tail_len NULL), else -1
+  uint16_t* k_dst;     // = k_tail
+  uint16_t* v_dst;     // = v_tail
+};
+
+// row t of the window is one of the rows given apart: its index among them, else -1
+__device__ __forceinline__ int fresh_row(const WinNew& w, int t) {
+  const int i = t - (w.T - w.n);
+  return (w.n > 0 && i >= 0 && t < w.T) ? i : -1;
+}
+
+// ---------------------------------------------------------------------------
 // Recent-window scores (any decode kernel whose arguments carry k_tail, ts_b,
 // ts_h, ts_t, tail_cap, win_rescale, ws_win, h_kv, G).  Window tile j (tokens
 // 16j .. 16j + 15 of the fp16 post-RoPE window), scored by the workgroup the
@@ -66,9 +90,11 @@ __device__ __forceinline__ void batch_shares(const int32_t* packed_len, int max_
 // ---------------------------------------------------------------------------
 template <class A>
 __device__ __forceinline__ void load_win_tile(const A& a, int64_t tail_base, int j, int n, int q,
-                                              uint2 kw[8]) {
+                                              uint2 kw[8], int64_t new_base) {
   const int t = 16 * j + n;
-  const uint16_t* row = a.k_tail + tail_base + (int64_t)(t < a.tail_cap ? t : 0) * a.ts_t + 4 * q;
+  const int i_new = fresh_row(a.nw, t);
+  const uint16_t* row = i_new >= 0 ? a.nw.k + new_base + (int64_t)i_new * a.nw.st + 4 * q
+                                   : a.k_tail + tail_base + (int64_t)(t < a.tail_cap ? t : 0) * a.ts_t + 4 * q;
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
     kw[2 * bb] = *reinterpret_cast<const uint2*>(row + 16 * bb);
@@ -78,7 +104,16 @@ __device__ __forceinline__ void load_win_tile(const A& a, int64_t tail_base, int
 
 template <class A>
 __device__ __forceinline__ void score_win_tile(const A& a, int b, int h, int j, int n, int q,
-                                               const uint2 kw[8], const half8_t qh[4], const half8_t ql[4]) {
+                                               const uint2 kw[8], const half8_t qh[4], const half8_t ql[4],
+                                               int64_t tail_base) {
+  if (fresh_row(a.nw, 16 * j + n) >= 0) {   // a row given apart: into the window buffer
+    uint16_t* dst = a.nw.k_dst + tail_base + (int64_t)(16 * j + n) * a.ts_t + 4 * q;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      *reinterpret_cast<uint2*>(dst + 16 * bb) = kw[2 * bb];
+      *reinterpret_cast<uint2*>(dst + 16 * bb + 64) = kw[2 * bb + 1];
+    }
+  }
   float4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
@@ -152,7 +187,8 @@ struct CombineKArgs {
   const float* ws_win;
   const uint16_t* v_tail;
   int64_t ts_b, ts_h, ts_t;
-  const int32_t* tail_len;
+  const int32_t* tail_len;   // NULL: every sequence's window holds nw.T rows
+  WinNew nw;
   uint32_t v_sign_bits[4];   // rotated: bit c set <=> value channel c carries Hadamard sign -1
   float packed_scale;        // rotated: 1 / (128 kappa), the Hadamard normalisation and the
                              // level scale; 1 otherwise
@@ -201,6 +237,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   const float* mlb = a.ws_ml + row * S_slots * 2;
   const float* swb = a.ws_win + row * a.tail_cap;
   const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch + 4 * c4;
+  const int64_t new_base = b * a.nw.sb + h * a.nw.sh + kChunk * ch + 4 * c4;
   typedef float f2_t __attribute__((ext_vector_type(2)));
   // element e of this lane in pass j0: p + 16 (wave + kCmbWaves u) + j0
   auto elem = [&](int j0, int u) { return j0 + p + 16 * (wave + kCmbWaves * u); };
@@ -225,7 +262,9 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
     for (int u = 0; u < kCmbTokens; ++u) {
       const int t = min(elem(t0, u), t_end - 1);
       ws[u] = swb[t];
-      wv[u] = *reinterpret_cast<const uint2*>(vb + (int64_t)t * a.ts_t);
+      const int i_new = fresh_row(a.nw, t);
+      wv[u] = *reinterpret_cast<const uint2*>(i_new >= 0 ? a.nw.v + new_base + (int64_t)i_new * a.nw.st
+                                                         : vb + (int64_t)t * a.ts_t);
     }
   };
   // first pass of both: the window rows bounded by the host's tail_cap (no
@@ -238,7 +277,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
     S = __shfl(share, b);
   }
   load_splits(0);
-  const int T = min(max(a.tail_len[b], 0), a.tail_cap);
+  const int T = a.tail_len ? min(max(a.tail_len[b], 0), a.tail_cap) : a.nw.T;
 
   // ---- packed partials: online over passes ----
   float mp = -INFINITY, lp = 0.f;
@@ -281,6 +320,9 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
       lt *= sc;
 #pragma unroll
       for (int u = 0; u < kCmbTokens; ++u) {
+        // a row given apart goes into the window buffer (once: by query 0's merge)
+        if (r % a.G == 0 && elem(t0, u) < T && fresh_row(a.nw, elem(t0, u)) >= 0)
+          *reinterpret_cast<uint2*>(a.nw.v_dst + (vb - a.v_tail) + (int64_t)elem(t0, u) * a.ts_t) = wv[u];
         const float w = elem(t0, u) < T ? __builtin_amdgcn_exp2f(ws[u] - mnew) : 0.f;
         const float4_t vf = {half_bits_to_float(wv[u].x & 0xffff), half_bits_to_float(wv[u].x >> 16),
                              half_bits_to_float(wv[u].y & 0xffff), half_bits_to_float(wv[u].y >> 16)};

@@ -95,6 +95,7 @@ struct DecodeKArgs {
   // recent window: fp16 post-RoPE keys [b * ts_b + h * ts_h + t * ts_t][128]
   const uint16_t* k_tail;
   int64_t ts_b, ts_h, ts_t;
+  WinNew nw;           // the window's newest rows given apart (decode_shared.h)
   int tail_cap;
   float win_rescale;      // 1 / rope_scaling: window keys carry the RoPE scaling
   float* ws_win;          // [B][h_kv][G][tail_cap] window scores, base 2
@@ -199,8 +200,8 @@ __device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, in
     const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
     for (int j = j0; j < n_tiles; j += stride) {
       uint2 kw[8];
-      load_win_tile(a, tail_base, j, n, q, kw);
-      score_win_tile(a, b, h, j, n, q, kw, qh, ql);
+      load_win_tile(a, tail_base, j, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh);
+      score_win_tile(a, b, h, j, n, q, kw, qh, ql, tail_base);
     }
   }
   float4_t zero[8];
@@ -424,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   int win_stride;
   const int win_j0 = first_win_tile(split, S, win_stride);
   uint2 kw[8];
-  if (win_j0 < n_win_tiles) load_win_tile(a, tail_base, win_j0, n, q, kw);
+  if (win_j0 < n_win_tiles) load_win_tile(a, tail_base, win_j0, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh);
 
   if (tid < 256) {
     const uint32_t l0 = a.level_hi[0], l1 = a.level_hi[1], l2 = a.level_hi[2], l3 = a.level_hi[3];
@@ -439,10 +440,10 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
 
   // recent-window tiles (the first one's rows are in flight)
   if (active && win_j0 < n_win_tiles) {
-    score_win_tile(a, b, h, win_j0, n, q, kw, qf, qlo);
+    score_win_tile(a, b, h, win_j0, n, q, kw, qf, qlo, tail_base);
     for (int j = win_j0 + win_stride; j < n_win_tiles; j += win_stride) {
-      load_win_tile(a, tail_base, j, n, q, kw);
-      score_win_tile(a, b, h, j, n, q, kw, qf, qlo);
+      load_win_tile(a, tail_base, j, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh);
+      score_win_tile(a, b, h, j, n, q, kw, qf, qlo, tail_base);
     }
   }
   store_prefix(pre, 0);
@@ -955,8 +956,16 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
     return fail(BMX_E_INVALID, name + ": rope_scaling must be finite and > 0");
   if (a->split_tokens < 0 || a->split_tokens % kGroup != 0)
     return fail(BMX_E_INVALID, name + ": split_tokens must be a multiple of 64");
-  if (!a->q || !a->out || !a->packed_len || !a->tail_len)
-    return fail(BMX_E_INVALID, name + ": q/out/packed_len/tail_len must be non-NULL");
+  if (!a->q || !a->out || !a->packed_len)
+    return fail(BMX_E_INVALID, name + ": q/out/packed_len must be non-NULL");
+  if (!a->tail_len && (a->tail_len_value < 0 || a->tail_len_value > a->tail_cap))
+    return fail(BMX_E_INVALID, name + ": with tail_len NULL, tail_len_value must be 0..tail_cap");
+  if (a->n_new < 0 || (a->n_new > 0 && (a->tail_len || a->n_new > a->tail_len_value || !a->new_k ||
+                                        !a->new_v)))
+    return fail(BMX_E_INVALID, name + ": n_new rows given apart need tail_len NULL, "
+                                      "n_new <= tail_len_value and new_k/new_v non-NULL");
+  if (a->n_new > 0 && (a->new_stride_b % 8 != 0 || a->new_stride_h % 8 != 0 || a->new_stride_t % 8 != 0))
+    return fail(BMX_E_INVALID, name + ": new_k/new_v strides must be multiples of 8 elements");
   if (a->max_packed_len > 0 && (!a->pages || !a->basis))
     return fail(BMX_E_INVALID, name + ": pages/basis must be non-NULL");
   if (a->max_packed_len > 0 && a->n_pool_pages < 1)
@@ -995,6 +1004,12 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   k.tail_cap = a->tail_cap;
   k.win_rescale = 1.0f / a->rope_scaling;
   k.ws_win = ws_win;
+  k.nw.k = a->new_k; k.nw.v = a->new_v;
+  k.nw.sb = a->new_stride_b; k.nw.sh = a->new_stride_h; k.nw.st = a->new_stride_t;
+  k.nw.n = a->n_new;
+  k.nw.T = a->tail_len ? -1 : a->tail_len_value;
+  k.nw.k_dst = const_cast<uint16_t*>(a->k_tail);
+  k.nw.v_dst = const_cast<uint16_t*>(a->v_tail);
   for (int j = 0; j < 64; ++j) {
     k.inv_freq[j] = a->inv_freq[j];
     const double step = 64.0 * (double)a->inv_freq[j];  // exact: 64 * fp32
@@ -1039,6 +1054,7 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   c.v_tail = a->v_tail;
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
   c.tail_len = a->tail_len;
+  c.nw = k.nw;
   for (int j = 0; j < 4; ++j) c.v_sign_bits[j] = a->v_sign_bits[j];
   c.packed_scale = (float)(1.0 / (kD * (double)lm.kappa));
   c.balanced = k.balanced; c.n_wg = n_wg;

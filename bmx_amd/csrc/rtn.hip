@@ -258,6 +258,7 @@ struct RtnDecodeKArgs {
   // recent window (decode_shared.h)
   const uint16_t* k_tail;
   int64_t ts_b, ts_h, ts_t;
+  WinNew nw;           // the window's newest rows given apart (decode_shared.h)
   int tail_cap;
   float win_rescale;   // 1: the window keys are scored with qscale
   float* ws_win;
@@ -324,8 +325,8 @@ __device__ __noinline__ void rtn_empty_range(const RtnDecodeKArgs& a, int b, int
     const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
     for (int j = split; j < n_tiles; j += a.max_splits) {
       uint2 kw[8];
-      load_win_tile(a, tail_base, j, n, q, kw);
-      score_win_tile(a, b, h, j, n, q, kw, qh, ql);
+      load_win_tile(a, tail_base, j, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh);
+      score_win_tile(a, b, h, j, n, q, kw, qh, ql, tail_base);
     }
   }
   float4_t zero[8];
@@ -470,8 +471,8 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
     rtn_window_fragments(a, b, h, n, q, wh, wl);
     for (int j = split; j < n_win_tiles; j += S) {
       uint2 kw[8];
-      load_win_tile(a, tail_base, j, n, q, kw);
-      score_win_tile(a, b, h, j, n, q, kw, wh, wl);
+      load_win_tile(a, tail_base, j, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh);
+      score_win_tile(a, b, h, j, n, q, kw, wh, wl, tail_base);
     }
   }
   store_prefix(pre, 0);
@@ -850,8 +851,16 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: tail_cap must be 0..4096");
   if (a->split_tokens < 0 || a->split_tokens % kRGroup != 0)
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: split_tokens must be a multiple of 64");
-  if (!a->q || !a->out || !a->packed_len || !a->tail_len)
-    return rfail(BMX_E_INVALID, "bmx_rtn_decode: q/out/packed_len/tail_len must be non-NULL");
+  if (!a->q || !a->out || !a->packed_len)
+    return rfail(BMX_E_INVALID, "bmx_rtn_decode: q/out/packed_len must be non-NULL");
+  if (!a->tail_len && (a->tail_len_value < 0 || a->tail_len_value > a->tail_cap))
+    return rfail(BMX_E_INVALID, "bmx_rtn_decode: with tail_len NULL, tail_len_value must be 0..tail_cap");
+  if (a->n_new < 0 || (a->n_new > 0 && (a->tail_len || a->n_new > a->tail_len_value || !a->new_k ||
+                                        !a->new_v)))
+    return rfail(BMX_E_INVALID, "bmx_rtn_decode: n_new rows given apart need tail_len NULL, "
+                                "n_new <= tail_len_value and new_k/new_v non-NULL");
+  if (a->n_new > 0 && (a->new_stride_b % 8 != 0 || a->new_stride_h % 8 != 0 || a->new_stride_t % 8 != 0))
+    return rfail(BMX_E_INVALID, "bmx_rtn_decode: new_k/new_v strides must be multiples of 8 elements");
   if (a->max_packed_len > 0 && (!a->pages || !a->page_table || a->n_pool_pages < 1))
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: pages/page_table must be non-NULL and the pool non-empty");
   if (a->tail_cap > 0 && (!a->k_tail || !a->v_tail))
@@ -881,6 +890,12 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   k.qscale = a->sm_scale * 1.4426950408889634f;
   k.k_tail = a->k_tail; k.ts_b = a->tail_stride_b; k.ts_h = a->tail_stride_h; k.ts_t = a->tail_stride_t;
   k.tail_cap = a->tail_cap; k.win_rescale = 1.0f; k.ws_win = ws_win;
+  k.nw.k = a->new_k; k.nw.v = a->new_v;
+  k.nw.sb = a->new_stride_b; k.nw.sh = a->new_stride_h; k.nw.st = a->new_stride_t;
+  k.nw.n = a->n_new;
+  k.nw.T = a->tail_len ? -1 : a->tail_len_value;
+  k.nw.k_dst = const_cast<uint16_t*>(a->k_tail);
+  k.nw.v_dst = const_cast<uint16_t*>(a->v_tail);
   dim3 grid(S, a->batch);
   const int ngk = g.k_arm == BMX_RTN_CHANNEL ? 0 : kD / g.k_group;
   if (g.n_q_groups <= 4)
@@ -898,6 +913,7 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   c.v_tail = a->v_tail;
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
   c.tail_len = a->tail_len;
+  c.nw = k.nw;
   c.packed_scale = 1.0f;
   hipLaunchKernelGGL(combine_kernel<false>, dim3(kChunks, g.h_kv * g.n_q_groups, a->batch), dim3(kCmbThreads),
                      0, st, c);

@@ -60,6 +60,38 @@ def _need(cond: bool, msg: str):
         raise ValueError(msg)
 
 
+def set_window_rows(a, B: int, h_kv: int, tail_len, tail_cap: int, new_kv=None) -> None:
+    """Fill the window-length and new-row fields of decode args a (k2b or RTN).
+
+    tail_len: a device int32 (B,) tensor, or a host int (every sequence's window
+    length, no device read), or None (0).  new_kv: (k, v) fp16 (B, h_kv, n, 128)
+    post-RoPE keys and values of the window's newest n rows (rows tail_len - n
+    .. tail_len - 1), attended from there and copied into the window buffers by
+    the decode call; needs a host tail_len."""
+    if isinstance(tail_len, torch.Tensor):
+        _need(tail_len.dtype == torch.int32 and tail_len.numel() == B and tail_len.is_cuda,
+              "tail_len must be a device int32[B] tensor or a host int")
+        a.tail_len, a.tail_len_value = tail_len.data_ptr(), 0
+    else:
+        T = 0 if tail_len is None else int(tail_len)
+        _need(0 <= T <= tail_cap, "tail_len must be within 0..tail_cap")
+        a.tail_len, a.tail_len_value = None, T
+    if new_kv is None:
+        a.new_k = a.new_v = None
+        a.n_new = 0
+        return
+    k, v = new_kv
+    _need(not isinstance(tail_len, torch.Tensor), "rows given apart need a host tail_len")
+    _need(k.dtype == torch.float16 and v.dtype == torch.float16 and k.shape == v.shape and k.stride() == v.stride()
+          and k.dim() == 4 and k.shape[0] == B and k.shape[1] == h_kv and k.shape[3] == HEAD_DIM
+          and k.stride(3) == 1, "new_kv: fp16 (B, h_kv, n, 128) keys and values with the same strides")
+    _need(all(st % 8 == 0 for st in k.stride()[:3]), "new_kv strides must be multiples of 8 elements")
+    a.new_k, a.new_v = k.data_ptr(), v.data_ptr()
+    a.new_stride_b, a.new_stride_h, a.new_stride_t = k.stride(0), k.stride(1), k.stride(2)
+    a.n_new = k.shape[2]
+    _need(a.n_new <= a.tail_len_value, "new_kv holds more rows than the window")
+
+
 def page_bytes(h_kv: int, rank: int) -> int:
     return _lib.page_bytes(h_kv, rank)
 
@@ -126,7 +158,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
            tail_len: torch.Tensor | None = None, tail_cap: int = 0,
            out: torch.Tensor | None = None, split_tokens: int = 0,
            workspace: DecodeWorkspace | None = None, page_stride: int | None = None,
-           split_end_event: torch.cuda.Event | None = None, _capture=None) -> torch.Tensor:
+           new_kv=None, split_end_event: torch.cuda.Event | None = None, _capture=None) -> torch.Tensor:
     """One decode step.  q (B, h_kv, G, 128) fp32 post-RoPE -> (B, h_kv, G, 128) fp32.
 
     page_table (B, max_pages) int32, or None for contiguous pages: logical page
@@ -134,7 +166,8 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
     max_packed_len / 16); packed_len (B,) int32 committed tokens (multiples of
     128, <= max_packed_len); basis16 (B, C, rank) or (C, rank) fp16;
     k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 post-RoPE recent window with
-    tail_len (B,) int32 valid rows."""
+    tail_len valid rows (a device int32 (B,) tensor or a host int); new_kv as in
+    set_window_rows."""
     B, h_kv, G, d = q.shape
     dev = q.device
     _need(d == HEAD_DIM and q.dtype == torch.float32 and q.is_contiguous(),
@@ -163,8 +196,6 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
           "basis16 rows must be contiguous fp16")
     if out is None:
         out = torch.empty_like(q)
-    if tail_len is None:
-        tail_len = torch.zeros(B, dtype=torch.int32, device=dev)
     a = _lib.DecodeArgs()
     a.geom = _lib.Geom(h_kv, rank, G)
     a.batch = B
@@ -187,7 +218,8 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
               "k_tail must be fp16 (B, h_kv, >=tail_cap, 128) with contiguous last dim")
         a.k_tail, a.v_tail = _ptr(k_tail), _ptr(v_tail)
         a.tail_stride_b, a.tail_stride_h, a.tail_stride_t = k_tail.stride(0), k_tail.stride(1), k_tail.stride(2)
-    a.tail_len, a.tail_cap = _ptr(tail_len), int(tail_cap)
+    a.tail_cap = int(tail_cap)
+    set_window_rows(a, B, h_kv, tail_len, tail_cap, new_kv)
     a.split_tokens = int(split_tokens)
     lib = _lib.lib()
     need = int(lib.bmx_k2b_decode_workspace_bytes(ct.byref(a)))
@@ -218,9 +250,6 @@ class DecodePlan:
                  page_stride: int | None = None):
         self.out = torch.empty_like(q) if out is None else out
         self._keep = (q, pages, page_table, packed_len, basis16, k_tail, v_tail, tail_len)
-        if tail_len is None:
-            tail_len = torch.zeros(q.shape[0], dtype=torch.int32, device=q.device)
-            self._keep = self._keep + (tail_len,)
         self.ws = workspace or DecodeWorkspace()
         captured = {}
 
@@ -234,9 +263,21 @@ class DecodePlan:
         self.stream = _stream(q.device)
         self._fn = _lib.lib().bmx_k2b_decode
 
-    def run(self, split_end_event: torch.cuda.Event | None = None) -> torch.Tensor:
-        self.args.split_end_event = None if split_end_event is None else split_end_event.cuda_event
-        rc = self._fn(ct.byref(self.args), self.stream)
+    def run(self, split_end_event: torch.cuda.Event | None = None, *, q: torch.Tensor | None = None,
+            tail_len: int | None = None, new_kv=None) -> torch.Tensor:
+        """One call.  q: a new query tensor of the bound one's shape, dtype and
+        contiguity (its pointer replaces the bound one); tail_len / new_kv: the
+        host window length and the rows given apart for this call (the plan must
+        have been bound with a host tail_len)."""
+        a = self.args
+        a.split_end_event = None if split_end_event is None else split_end_event.cuda_event
+        if q is not None:
+            a.q = q.data_ptr()
+        if tail_len is not None or new_kv is not None:
+            _need(not a.tail_len, "the plan was bound with a device tail_len")
+            set_window_rows(a, q.shape[0] if q is not None else self.out.shape[0], self.out.shape[1],
+                            a.tail_len_value if tail_len is None else tail_len, a.tail_cap, new_kv)
+        rc = self._fn(ct.byref(a), self.stream)
         if rc != 0:
             _lib.check(rc, "bmx_k2b_decode")
         return self.out

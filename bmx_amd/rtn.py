@@ -17,7 +17,7 @@ import ctypes as ct
 import torch
 
 from . import _lib
-from .k2b import DecodeWorkspace, _need, _ptr, _stream, _V_DTYPES
+from .k2b import DecodeWorkspace, _need, _ptr, _stream, _V_DTYPES, set_window_rows
 
 HEAD_DIM = 128
 PAGE_TOKENS = 16
@@ -84,10 +84,12 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
            max_packed_len: int, sm_scale: float, *, k_bits: int, v_bits: int, k_group: int, v_group: int,
            k_arm: int = TOKEN, k_tail: torch.Tensor | None = None, v_tail: torch.Tensor | None = None,
            tail_len: torch.Tensor | None = None, tail_cap: int = 0, out: torch.Tensor | None = None,
-           split_tokens: int = 0, workspace: DecodeWorkspace | None = None, _capture=None) -> torch.Tensor:
+           split_tokens: int = 0, workspace: DecodeWorkspace | None = None, new_kv=None,
+           _capture=None) -> torch.Tensor:
     """One decode step.  q (B, h_kv, G, 128) fp32 post-RoPE -> (B, h_kv, G, 128) fp32;
     page_table (B, max_pages) int32; packed_len (B,) int32 (multiples of 128);
-    k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 with tail_len (B,) int32."""
+    k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 with tail_len valid rows (a
+    device int32 (B,) tensor or a host int); new_kv as in k2b.set_window_rows."""
     B, h_kv, G, d = q.shape
     dev = q.device
     _need(d == HEAD_DIM and q.dtype == torch.float32 and q.is_contiguous(),
@@ -100,8 +102,6 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
     _need(page_table.shape[1] * PAGE_TOKENS >= max_packed_len, "page_table too narrow for max_packed_len")
     if out is None:
         out = torch.empty_like(q)
-    if tail_len is None:
-        tail_len = torch.zeros(B, dtype=torch.int32, device=dev)
     a = _lib.RtnDecodeArgs()
     a.geom = geom(h_kv, G, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     a.batch = B
@@ -118,7 +118,8 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
               "k_tail must be fp16 (B, h_kv, >=tail_cap, 128) with contiguous last dim")
         a.k_tail, a.v_tail = _ptr(k_tail), _ptr(v_tail)
         a.tail_stride_b, a.tail_stride_h, a.tail_stride_t = k_tail.stride(0), k_tail.stride(1), k_tail.stride(2)
-    a.tail_len, a.tail_cap = _ptr(tail_len), int(tail_cap)
+    a.tail_cap = int(tail_cap)
+    set_window_rows(a, B, h_kv, tail_len, tail_cap, new_kv)
     a.split_tokens = int(split_tokens)
     lib = _lib.lib()
     need = int(lib.bmx_rtn_decode_workspace_bytes(ct.byref(a)))
@@ -143,8 +144,6 @@ class DecodePlan:
                  k_group, v_group, k_arm=TOKEN, k_tail=None, v_tail=None, tail_len=None, tail_cap=0, out=None,
                  split_tokens=0, workspace: DecodeWorkspace | None = None):
         self.out = torch.empty_like(q) if out is None else out
-        if tail_len is None:
-            tail_len = torch.zeros(q.shape[0], dtype=torch.int32, device=q.device)
         self._keep = (q, pages, page_table, packed_len, k_tail, v_tail, tail_len)
         self.ws = workspace or DecodeWorkspace()
         captured = {}
@@ -156,8 +155,16 @@ class DecodePlan:
         self.stream = _stream(q.device)
         self._fn = _lib.lib().bmx_rtn_decode
 
-    def run(self) -> torch.Tensor:
-        rc = self._fn(ct.byref(self.args), self.stream)
+    def run(self, *, q: torch.Tensor | None = None, tail_len: int | None = None, new_kv=None) -> torch.Tensor:
+        """One call; q, tail_len and new_kv as in k2b.DecodePlan.run."""
+        a = self.args
+        if q is not None:
+            a.q = q.data_ptr()
+        if tail_len is not None or new_kv is not None:
+            _need(not a.tail_len, "the plan was bound with a device tail_len")
+            set_window_rows(a, self.out.shape[0], self.out.shape[1],
+                            a.tail_len_value if tail_len is None else tail_len, a.tail_cap, new_kv)
+        rc = self._fn(ct.byref(a), self.stream)
         if rc != 0:
             _lib.check(rc, "bmx_rtn_decode")
         return self.out

@@ -121,7 +121,8 @@ typedef struct {
   int64_t tail_stride_b;      /* element strides of k_tail/v_tail (dim 128 contiguous) */
   int64_t tail_stride_h;
   int64_t tail_stride_t;
-  const int32_t* tail_len;    /* device [batch] recent-window length (clamped to tail_cap) */
+  const int32_t* tail_len;    /* device [batch] recent-window length (clamped to tail_cap), or
+                                 NULL: every sequence's window holds tail_len_value rows */
   int32_t tail_cap;           /* host upper bound of tail_len, 0..4096 */
   int32_t split_tokens;       /* 0 = one workgroup per CU, split over the batch (default):
                                  a batch of 2..64 sequences shares them in proportion
@@ -137,6 +138,20 @@ typedef struct {
   size_t workspace_bytes;
   void* split_end_event;      /* optional hipEvent_t recorded on the stream between
                                  the split kernel and the combine kernel (timing) */
+  int32_t tail_len_value;     /* window length of every sequence when tail_len is NULL
+                                 (0..tail_cap): a host value, no device read */
+  const uint16_t* new_k;      /* with tail_len NULL, optionally the window's newest n_new
+                                 rows (the step's own token) given apart: device fp16
+                                 post-RoPE keys, row i of (b, h) at b*new_stride_b +
+                                 h*new_stride_h + i*new_stride_t, rows tail_len_value -
+                                 n_new .. tail_len_value - 1 of the window.  They are
+                                 attended from here and copied into k_tail / v_tail, so
+                                 the caller writes no window row for a decode step */
+  const uint16_t* new_v;      /* device fp16 values of the same rows, same strides */
+  int64_t new_stride_b;
+  int64_t new_stride_h;
+  int64_t new_stride_t;
+  int32_t n_new;              /* rows given apart, 0..tail_len_value (0 = none) */
 } bmx_k2b_decode_args;
 
 size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* args);

@@ -124,11 +124,18 @@ typedef struct {
   int64_t tail_stride_b;
   int64_t tail_stride_h;
   int64_t tail_stride_t;
-  const int32_t* tail_len;
+  const int32_t* tail_len;    /* device [batch], or NULL: tail_len_value for every sequence */
   int32_t tail_cap;           /* 0..4096 */
   int32_t split_tokens;       /* 0 = one workgroup per CU (default) */
   void* workspace;            /* device scratch: split partials and window scores */
   size_t workspace_bytes;
+  int32_t tail_len_value;     /* as in bmx_k2b_decode_args: the host window length, and */
+  const uint16_t* new_k;      /* the window's newest n_new rows given apart, attended */
+  const uint16_t* new_v;      /* from here and copied into k_tail / v_tail */
+  int64_t new_stride_b;
+  int64_t new_stride_h;
+  int64_t new_stride_t;
+  int32_t n_new;
 } bmx_rtn_decode_args;
 
 size_t bmx_rtn_decode_workspace_bytes(const bmx_rtn_decode_args* args);

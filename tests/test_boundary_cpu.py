@@ -67,6 +67,48 @@ def test_bad_geometry_is_rejected_with_message():
     assert rc != 0 and b"null pointer" in _lib.lib().bmx_last_error()
 
 
+def test_window_rows_given_apart_rejected_on_the_host():
+    """The host window length and the rows given apart are checked before any
+    device work: tail_len_value within 0..tail_cap, rows given apart only with
+    tail_len NULL and n_new <= tail_len_value, 8-element strides."""
+    from bmx_amd import k2b
+    lib = _lib.lib()
+    fake = 1 << 20   # never dereferenced: every call below fails validation
+    for args_t, fn, geom in ((_lib.DecodeArgs, lib.bmx_k2b_decode, _lib.Geom(8, 32, 4)),
+                             (_lib.RtnDecodeArgs, lib.bmx_rtn_decode, None)):
+        a = args_t()
+        if geom is not None:
+            a.geom = geom
+            a.rope_scaling = 1.0
+        else:
+            from bmx_amd import rtn
+            a.geom = rtn.geom(8, 4, k_bits=4, v_bits=4, k_group=32, v_group=32)
+        a.batch = 1
+        a.q = a.out = a.packed_len = fake
+        a.tail_cap = 128
+        a.tail_len_value = 129
+        assert fn(ct.byref(a), None) != 0 and b"tail_len_value" in lib.bmx_last_error()
+        a.tail_len_value = 4
+        a.n_new, a.new_k, a.new_v = 5, fake, fake
+        assert fn(ct.byref(a), None) != 0 and b"n_new" in lib.bmx_last_error()
+        a.n_new, a.tail_len = 1, fake
+        assert fn(ct.byref(a), None) != 0 and b"n_new" in lib.bmx_last_error()
+        a.tail_len, a.new_stride_t = None, 12
+        assert fn(ct.byref(a), None) != 0 and b"multiples of 8" in lib.bmx_last_error()
+    # the Python wrapper's own checks
+    a = _lib.DecodeArgs()
+    a.tail_cap = 128
+    with pytest.raises(ValueError, match="within 0..tail_cap"):
+        k2b.set_window_rows(a, 1, 8, 200, 128)
+    k = torch.zeros(1, 8, 2, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="more rows than the window"):
+        k2b.set_window_rows(a, 1, 8, 1, 128, (k, k))
+    with pytest.raises(ValueError, match="fp16"):
+        k2b.set_window_rows(a, 1, 8, 4, 128, (k.float(), k.float()))
+    k2b.set_window_rows(a, 1, 8, 4, 128, (k, k))
+    assert a.tail_len is None and a.tail_len_value == 4 and a.n_new == 2 and a.new_stride_t == 128
+
+
 def test_decode_workspace_size_formula():
     a = _lib.DecodeArgs()
     a.geom = _lib.Geom(8, 32, 4)

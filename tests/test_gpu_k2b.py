@@ -657,6 +657,82 @@ def test_decode_window_only_and_long_window():
     _close(out, ref.view(1, h_kv, G, 128), "long window")
 
 
+def test_rows_given_apart_fold_the_window_write():
+    """The window's newest rows given apart (new_kv, host tail_len): the output
+    equals, bit for bit, the call over a window that already holds them, and
+    after the call the window buffers hold them (rows past the window keep their
+    contents).  Batch 2 through a page table and batch 1 contiguous; windows of
+    133 and 700 rows (the second merge pass); 1 and 3 rows given apart, from a
+    strided view; a plan stepped through two calls with run(q, tail_len, new_kv)."""
+    gen = torch.Generator().manual_seed(41)
+    h_kv, rank, G = 8, 32, 4
+    consts = k2b.CodecConsts.make(v_seed=0)
+    inv = torch.tensor(consts.inv_freq)
+    lens = [2048, 1024]
+    pool = synth.PagePool(sum(lens) // 16, h_kv, rank, DEV)
+    seqs, k_pres, vs = [], [], []
+    Tmax = 702
+    for i, S in enumerate(lens):
+        pool.free = list(range(sum(lens[:i + 1]) // 16 - 1, sum(lens[:i]) // 16 - 1, -1))
+        k_pre = synth.k2b_keys(h_kv, S + Tmax, rank, gen)
+        v = synth.values(h_kv, S + Tmax, gen)
+        seqs.append(synth.encode_sequence(pool, k_pre[:, :S].to(DEV), v[:, :S].to(DEV), rank, consts,
+                                          svd=synth.first_page_svd(k_pre, rank)))
+        k_pres.append(k_pre)
+        vs.append(v)
+    for B, T, n in ((2, 133, 1), (2, 700, 3), (1, 700, 1)):
+        cap = T + 2
+        k_full = torch.full((B, h_kv, cap, 128), 7.0, dtype=torch.float16)   # rows past T: sentinel
+        v_full = torch.full_like(k_full, -3.0)
+        for i in range(B):
+            S = lens[i]
+            cos, sin = A.rope_cos_sin(inv, torch.arange(S, S + T))
+            k_full[i, :, :T] = A.apply_rope(k_pres[i][:, S:S + T].float(), cos, sin).half()
+            v_full[i, :, :T] = vs[i][:, S:S + T]
+        k_full, v_full = k_full.to(DEV), v_full.to(DEV)
+        # the rows given apart, as a strided view of a wider buffer
+        wide_k = torch.randn(B, h_kv, n + 5, 128, generator=gen).half().to(DEV)
+        wide_v = torch.randn(B, h_kv, n + 5, 128, generator=gen).half().to(DEV)
+        wide_k[:, :, 2:2 + n] = k_full[:, :, T - n:T]
+        wide_v[:, :, 2:2 + n] = v_full[:, :, T - n:T]
+        new_kv = (wide_k[:, :, 2:2 + n], wide_v[:, :, 2:2 + n])
+        k_stale, v_stale = k_full.clone(), v_full.clone()
+        k_stale[:, :, T - n:T] = 0.5
+        v_stale[:, :, T - n:T] = -0.25
+        q = torch.randn(B, h_kv, G, 128, generator=gen).to(DEV)
+        ln = torch.tensor(lens[:B], dtype=torch.int32, device=DEV)
+        basis = torch.stack([s_.basis16 for s_ in seqs[:B]]) if B > 1 else seqs[0].basis16
+        table = synth.page_table(seqs[:B], device=DEV) if B > 1 else None
+        common = dict(rank=rank, tail_cap=cap)
+        ref = k2b.decode(q, pool.pages, table, ln, max(lens[:B]), basis, consts, 128 ** -0.5,
+                         k_tail=k_full, v_tail=v_full,
+                         tail_len=torch.full((B,), T, dtype=torch.int32, device=DEV), **common)
+        out = k2b.decode(q, pool.pages, table, ln, max(lens[:B]), basis, consts, 128 ** -0.5,
+                         k_tail=k_stale, v_tail=v_stale, tail_len=T, new_kv=new_kv, **common)
+        torch.cuda.synchronize()
+        same = torch.equal(out, ref)
+        print(f"B {B} T {T} n {n}: folded == written {same}; window rows "
+              f"{torch.equal(k_stale, k_full)} {torch.equal(v_stale, v_full)}", flush=True)
+        assert same and torch.equal(k_stale, k_full) and torch.equal(v_stale, v_full)
+    # a plan over two steps: T = 699 then 700, one row given apart each
+    k_buf, v_buf = k_full.clone(), v_full.clone()
+    k_buf[:, :, 698:] = 1.0
+    v_buf[:, :, 698:] = 1.0
+    plan = k2b.DecodePlan(q, pool.pages, None, ln, lens[0], basis, consts, 128 ** -0.5, rank=rank,
+                          k_tail=k_buf, v_tail=v_buf, tail_len=0, tail_cap=cap)
+    for T in (699, 700):
+        q2 = torch.randn(1, h_kv, G, 128, generator=gen).to(DEV)
+        out = plan.run(q=q2, tail_len=T, new_kv=(k_full[:, :, T - 1:T], v_full[:, :, T - 1:T])).clone()
+        ref = k2b.decode(q2, pool.pages, None, ln, lens[0], basis, consts, 128 ** -0.5, k_tail=k_full,
+                         v_tail=v_full, tail_len=torch.full((1,), T, dtype=torch.int32, device=DEV),
+                         rank=rank, tail_cap=cap)
+        torch.cuda.synchronize()
+        print(f"plan step T {T}: {torch.equal(out, ref)}", flush=True)
+        assert torch.equal(out, ref)
+    assert torch.equal(k_buf[:, :, :700], k_full[:, :, :700]) and torch.equal(v_buf[:, :, :700], v_full[:, :, :700])
+    assert bool((k_buf[:, :, 700:] == 1.0).all())
+
+
 # ------------------------------------------------------------------ dequant kernel
 
 

@@ -243,3 +243,37 @@ def test_ragged_batch_shuffled_pages():
     for i in range(B):
         ref = A.rtn_naive_attention(q[i].reshape(h_kv * G, 1, 128), caches[i], kts[i], vts[i], G, 128 ** -0.5)
         _close(out[i], ref.view(h_kv, G, 128), f"ragged seq {i} len {lens[i]} tail {tails[i]}")
+
+
+def test_rows_given_apart_fold_the_window_write():
+    """As for k2b: the window's newest rows given apart (host tail_len) give the
+    output of the call over a window that already holds them, bit for bit, and
+    land in the window buffers; token and channel key arms."""
+    gen = torch.Generator().manual_seed(71)
+    h_kv, G, S = 8, 4, 1024
+    for codec, T, n in ((dict(k_bits=4, v_bits=4, k_group=32, v_group=32), 300, 2),
+                        (dict(k_bits=2, v_bits=2, k_group=128, v_group=32, k_arm=rtn.CHANNEL), 600, 1)):
+        k = _keys(h_kv, S + T, gen).half()
+        v = torch.randn(h_kv, S + T, 128, generator=gen).half()
+        pool, ids = _encode(h_kv, k[:, :S], v[:, :S], codec, gen=torch.Generator().manual_seed(5),
+                            n_pool=S // 16 + 3)
+        cap = T + 3
+        k_full = torch.full((1, h_kv, cap, 128), 2.0, dtype=torch.float16)
+        v_full = torch.full_like(k_full, -1.0)
+        k_full[0, :, :T], v_full[0, :, :T] = k[:, S:], v[:, S:]
+        k_full, v_full = k_full.to(DEV), v_full.to(DEV)
+        k_stale, v_stale = k_full.clone(), v_full.clone()
+        k_stale[:, :, T - n:T] = 0.0
+        v_stale[:, :, T - n:T] = 0.0
+        q = torch.randn(1, h_kv, G, 128, generator=gen).to(DEV)
+        table = torch.tensor([ids], dtype=torch.int32, device=DEV)
+        ln = torch.tensor([S], dtype=torch.int32, device=DEV)
+        ref = rtn.decode(q, pool.pages, table, ln, S, 128 ** -0.5, k_tail=k_full, v_tail=v_full,
+                         tail_len=torch.tensor([T], dtype=torch.int32, device=DEV), tail_cap=cap, **codec)
+        out = rtn.decode(q, pool.pages, table, ln, S, 128 ** -0.5, k_tail=k_stale, v_tail=v_stale, tail_len=T,
+                         tail_cap=cap, new_kv=(k_full[:, :, T - n:T], v_full[:, :, T - n:T]), **codec)
+        torch.cuda.synchronize()
+        ok = torch.equal(out, ref) and torch.equal(k_stale, k_full) and torch.equal(v_stale, v_full)
+        print(f"rtn arm {codec.get('k_arm', 0)} T {T} n {n}: folded == written and window rows stored: {ok}",
+              flush=True)
+        assert ok
