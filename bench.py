@@ -71,7 +71,7 @@ def parse():
     ap.add_argument("--prefill-ctx", type=int, default=8192)
     ap.add_argument("--prefill-chunk", type=int, default=512)
     ap.add_argument("--spectral-budget", type=float, default=2.5)
-    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch", "spectral"],
+    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch", "spectral", "e2e"],
                     default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
                          "BASELINE config 5, Qwen3-8B geometry, rank 16, an 8192-token prefill "
@@ -81,7 +81,15 @@ def parse():
                          "two-block prefill, --prefill-chunk queries over --prefill-ctx + chunk keys; "
                          "batch: BASELINE config 4, 16 ragged sequences of 4k-16k; spectral: the "
                          "k4 recipe's decode step (spectral keys at --spectral-budget, one layer "
-                         "of Llama-3.1-8B geometry, --ctx tokens)")
+                         "of Llama-3.1-8B geometry, --ctx tokens); e2e: ms per decode token under "
+                         "HF generate() on a random-init Llama-3.1-8B-geometry fp16 model, dense "
+                         "DynamicCache vs the streaming twin vs the packed cache (k2b_ph rank 16)")
+    ap.add_argument("--e2e-ctx", default="4096,16384,65536")
+    ap.add_argument("--e2e-decode", type=int, default=64, help="decode tokens per timed generate")
+    ap.add_argument("--e2e-kinds", default="dense,streaming,packed")
+    ap.add_argument("--e2e-layers", type=int, default=32)
+    ap.add_argument("--e2e-parity", type=int, default=32,
+                    help="greedy tokens compared between the streaming twin and the packed cache")
     ap.add_argument("--rtn-ctx", type=int, default=4096)
     ap.add_argument("--rtn-layers", type=int, default=1)
     ap.add_argument("--stream-steps", type=int, default=512)
@@ -788,6 +796,120 @@ def run_spectral(args, torch, dev) -> dict:
     }
 
 
+E2E_METRIC = ("ms per decode token under HF generate(), Llama-3.1-8B geometry (random init, fp16), "
+              "k2b_ph rank 16, 1 MI355X")
+
+
+def run_e2e(args, torch, dev) -> dict:
+    """End-to-end decode latency, the reference's Mode A
+    (scripts/profile_decode_ab.py:113-141, 248-279): per context and cache kind,
+    one warm 1-token generate, then generate(1) and generate(1 + n) timed on the
+    host around device synchronisation; ms/token = (t_n - t_1) / n, which
+    cancels the prefill and counts every host-side cost of a step.  The model is
+    Llama-3.1-8B's geometry (32 layers, 4096 hidden, 32/8 heads, d 128, 14336
+    MLP, 128256 vocabulary, llama3 RoPE scaling) with random weights in fp16
+    (no checkpoint is available offline); the prompt is random token ids.
+    Before timing, greedy generate through the streaming twin and through the
+    packed cache are compared token for token at the smallest context (the
+    reference's parity gate; reported, since random weights leave near-ties)."""
+    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
+
+    from bmx_amd.cache import PackedStreamingCache, StreamingQuantizedCache
+    from bmx_amd.specs import spec_pair
+
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336,
+                      num_hidden_layers=args.e2e_layers, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, max_position_embeddings=131072, rope_theta=500000.0,
+                      rope_scaling={"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                                    "high_freq_factor": 4.0, "original_max_position_embeddings": 8192},
+                      rms_norm_eps=1e-5, tie_word_embeddings=False)
+    t0 = time.perf_counter()
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(dev):
+            model = LlamaForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    print(f"e2e: model built in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    k_spec, v_spec = spec_pair("k2b_ph", rank=16)
+    kinds = [k for k in args.e2e_kinds.split(",") if k]
+    ctxs = [int(c) for c in args.e2e_ctx.split(",") if c]
+
+    def fresh(kind):
+        if kind == "dense":
+            return DynamicCache()
+        cls = StreamingQuantizedCache if kind == "streaming" else PackedStreamingCache
+        return cls(model.config, k_spec, v_spec)
+
+    def generate(kind, ids, n):
+        cache = fresh(kind)
+        attach = getattr(cache, "attach", None)
+        if attach is not None:
+            attach(model)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        with torch.no_grad():
+            out = model.generate(ids, max_new_tokens=n, min_new_tokens=n, do_sample=False, use_cache=True,
+                                 past_key_values=cache, pad_token_id=0)
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t
+        if attach is not None:
+            cache.detach()
+        return out, t
+
+    def prompt(ctx):
+        g = torch.Generator().manual_seed(1234)
+        return torch.randint(10, cfg.vocab_size - 10, (1, ctx), generator=g).to(dev)
+
+    parity = None
+    if "streaming" in kinds and "packed" in kinds and args.e2e_parity > 0:
+        ids = prompt(min(ctxs))
+        a, _ = generate("streaming", ids, args.e2e_parity)
+        b, _ = generate("packed", ids, args.e2e_parity)
+        new_a, new_b = a[0, ids.shape[1]:], b[0, ids.shape[1]:]
+        agree = int((new_a == new_b).cumprod(0).sum().item())
+        parity = {"ctx": min(ctxs), "tokens": args.e2e_parity, "equal": bool(torch.equal(a, b)),
+                  "leading_tokens_equal": agree}
+        print(f"e2e: parity {parity}", file=sys.stderr, flush=True)
+    rows = []
+    for ctx in ctxs:
+        ids = prompt(ctx)
+        for kind in kinds:
+            generate(kind, ids, 1)
+            _, t1 = generate(kind, ids, 1)
+            out, tn = generate(kind, ids, 1 + args.e2e_decode)
+            row = {"cache": kind, "ctx": ctx,
+                   "ms_per_decode_token": round((tn - t1) * 1e3 / args.e2e_decode, 3),
+                   "prefill_plus1_s": round(t1, 3),
+                   "peak_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 2)}
+            torch.cuda.reset_peak_memory_stats()
+            rows.append(row)
+            print(f"e2e: {row}", file=sys.stderr, flush=True)
+    packed = [r for r in rows if r["cache"] == "packed"]
+    head = max(packed, key=lambda r: r["ctx"]) if packed else rows[-1]
+    return {
+        "metric": E2E_METRIC,
+        "value": head["ms_per_decode_token"],
+        "unit": "ms/token",
+        "n_gpus": 1,
+        "steps": args.e2e_decode,
+        "warmup": 1,
+        "ms_per_step": head["ms_per_decode_token"],
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (random weights, random prompt ids)",
+        "config": {"workload": f"HF generate(), Llama-3.1-8B geometry ({args.e2e_layers} layers), batch 1, "
+                               f"greedy, {args.e2e_decode} decode tokens per timed run, recent window 32",
+                   "value_is": f"{head['cache']} at ctx {head['ctx']}", "recipe": "k2b_ph rank 16"},
+        "rows": rows,
+        "parity": parity,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -824,6 +946,9 @@ def main():
         return
     if args.workload == "spectral":
         print(json.dumps(run_spectral(args, torch, dev)), flush=True)
+        return
+    if args.workload == "e2e":
+        print(json.dumps(run_e2e(args, torch, dev)), flush=True)
         return
     W = args.window
     packed = ((args.ctx - W) // 128) * 128

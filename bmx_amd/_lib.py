@@ -100,6 +100,8 @@ class DequantArgs(ct.Structure):
         ("k_out", ct.c_void_p),
         ("v_out", ct.c_void_p),
         ("out_dtype", ct.c_int32),
+        ("pos0", ct.c_int32),
+        ("out_rows", ct.c_int64),
     ]
 
 
@@ -170,6 +172,7 @@ class RtnDequantArgs(ct.Structure):
         ("k_out", ct.c_void_p),
         ("v_out", ct.c_void_p),
         ("out_dtype", ct.c_int32),
+        ("out_rows", ct.c_int64),
     ]
 
 

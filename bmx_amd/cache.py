@@ -25,7 +25,12 @@ What runs where:
   encoded by ``bmx_k2b_append`` straight into this layer's device page pool
   (8 physical 16-token pages per codec page, logical order = table order);
 * decode (one query step): ``bmx_k2b_decode`` over the pool and the fp16
-  recent-window slab;
+  recent window, through a plan bound once per layer and rebound only at a
+  commit.  The window lives in a fixed per-layer buffer of recent_window + 128
+  rows; a step's new key and value are not copied into it by the host: the
+  decode call is given them apart (with the window length from the host) and
+  stores them itself, so a step costs the decode call alone (no slab
+  concatenation, no host-to-device copy, no length upload);
 * prefill (several query steps): ``bmx_k2b_dequant`` to dense pre-RoPE keys and
   values, RoPE with the fp16 tables the reference casts to
   (``_shared_rope`` :79-113, ``_dense_kv`` chunked_attention.py:148-189), the
@@ -177,9 +182,23 @@ class PackedStreamingLayer(DynamicLayer):
             self._rtn = dict(k_bits=k_spec.bits, v_bits=v_spec.bits, k_group=k_spec.group,
                              v_group=v_spec.group,
                              k_arm=rtn.CHANNEL if k_spec.arm == "rtn_channel" else rtn.TOKEN)
-        # pre-RoPE key stash
-        self._k_pre: torch.Tensor | None = None
+        # pre-RoPE key stash: the captured blocks as the hook gave them (kept by
+        # reference, no copy per step), rows from absolute position _k_pre_offset
+        self._k_pre_parts: list = []
+        self._k_pre_rows = 0
         self._k_pre_offset = 0
+        # recent window: rows [0, _T) of fixed buffers (1, h_kv, recent_window + 128, d),
+        # fp16 for fp16/bf16 models (the decode kernel's operand), else the model
+        # dtype; _pending: the newest row's (key, value) when the decode call has
+        # still to store it (the product decode path only)
+        self._win_k: torch.Tensor | None = None
+        self._win_v: torch.Tensor | None = None
+        self._T = 0
+        self._pending: tuple | None = None
+        self.n_rows_folded = 0    # newest rows the decode call stored (no copy of their own)
+        self._plan = None
+        self._plan_key = None
+        self._empty_pool: torch.Tensor | None = None
         # committed prefix
         self._committed_S_q = 0
         self._quant_bits_k = 0.0
@@ -208,11 +227,67 @@ class PackedStreamingLayer(DynamicLayer):
 
     def stash_pre_rope(self, out: torch.Tensor) -> None:
         """Append captured pre-RoPE keys: (1, S, h_kv*d) or (1, S, h_kv, d)
-        (packed_streaming.py:448-457); post-RoPE codecs keep none."""
+        (packed_streaming.py:448-457); post-RoPE codecs keep none.  The block is
+        kept as given (the projection's output, which the model does not write
+        again) until its codec page commits: no device work per step."""
         if not self.k_spec.pre_rope:
             return
-        block = reshape_heads(out, self._h_kv, self._d_head)
-        self._k_pre = block if self._k_pre is None else torch.cat([self._k_pre, block], dim=1)
+        self._k_pre_parts.append(out)
+        self._k_pre_rows += out.shape[1]
+
+    def _take_k_pre(self, start: int, end: int) -> torch.Tensor:
+        """Stashed pre-RoPE keys of absolute positions [start, end) as (h_kv, n, d)
+        fp16; the stash keeps what follows end."""
+        if not self._k_pre_parts:
+            raise RuntimeError("no pre-RoPE keys captured: call cache.attach(model) before prefill")
+        lo, hi = start - self._k_pre_offset, end - self._k_pre_offset
+        if lo < 0 or hi > self._k_pre_rows:
+            raise RuntimeError(f"pre-RoPE stash holds positions {self._k_pre_offset}.."
+                               f"{self._k_pre_offset + self._k_pre_rows}, commit needs {start}..{end}")
+        raw = torch.cat(self._k_pre_parts, dim=1) if len(self._k_pre_parts) > 1 else self._k_pre_parts[0]
+        block = reshape_heads(raw[:, lo:hi], self._h_kv, self._d_head)
+        rest = raw[:, hi:]
+        self._k_pre_parts = [rest.clone()] if rest.shape[1] else []
+        self._k_pre_rows -= hi
+        self._k_pre_offset = end
+        return block
+
+    # -------------------------------------------------------------- window
+
+    def _window_dtype(self) -> torch.dtype:
+        return torch.float16 if self.dtype in (torch.float16, torch.bfloat16) else self.dtype
+
+    def _ensure_window(self, device, committed_after: int) -> None:
+        """The window buffers, made on first use (committed_after: the committed
+        length this update ends with)."""
+        if self._win_k is None:
+            cap = self.recent_window + self._page
+            self._win_k = torch.zeros(1, self._h_kv, cap, self._d_head, dtype=self._window_dtype(),
+                                      device=device)
+            self._win_v = torch.zeros_like(self._win_k)
+            self._packed_len_dev = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def _land_pending(self) -> None:
+        """Store a pending newest row into the window buffers (a copy), for a
+        reader other than the decode call that would have stored it."""
+        if self._pending is not None:
+            k, v = self._pending
+            self._pending = None
+            self._win_k[:, :, self._T - 1: self._T].copy_(k)
+            self._win_v[:, :, self._T - 1: self._T].copy_(v)
+
+    def window(self) -> tuple:
+        """The recent window's (keys, values), (1, h_kv, T, d) views of the buffers."""
+        if self._win_k is None:
+            return None, None
+        self._land_pending()
+        return self._win_k[:, :, : self._T], self._win_v[:, :, : self._T]
+
+    def _fold_ok(self, key_states: torch.Tensor) -> bool:
+        """A one-token step may leave its row to the decode call: the product's
+        fused decode paths, an fp16 window, on a HIP device."""
+        return (self._path in ("k2b", "rtn") and key_states.is_cuda
+                and self._win_k.dtype == torch.float16)
 
     def _reserve(self, n_pages: int, device) -> None:
         """Grow the pool (doubling, contents kept) to hold n_pages pages."""
@@ -288,55 +363,89 @@ class PackedStreamingLayer(DynamicLayer):
         self._n_pages = first + PAGES_PER_CODEC * n
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
-        """Append new tokens; commit codec pages on schedule; keep only the fp16
-        tail in the slab (packed_streaming.py:582-730)."""
-        keys, values = super().update(key_states, value_states, *args, **kwargs)
-        S = self._committed_S_q + keys.shape[2]
+        """Append new tokens; commit codec pages on schedule; keep only the
+        recent tail in the window (packed_streaming.py:582-730).  Returns views
+        of the window; after a one-token step that commits nothing, its newest
+        row is stored by the decode call (or by the first other reader,
+        window())."""
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        n = key_states.shape[2]
+        T0 = self._T
+        S = self._committed_S_q + T0 + n
         W = self.recent_window
         C = self._h_kv * self._d_head
         new_S_q = K.compute_flush_schedule(S, W, self._page)
+        self._ensure_window(key_states.device, new_S_q)
+        self._land_pending()
+        if new_S_q == self._committed_S_q:   # nothing commits: the rows join the window
+            if n == 1 and self._fold_ok(key_states):
+                self._pending = (key_states.to(torch.float16), value_states.to(torch.float16))
+            else:
+                self._win_k[:, :, T0:T0 + n].copy_(key_states)
+                self._win_v[:, :, T0:T0 + n].copy_(value_states)
+            self._T = T0 + n
+            self._set_bpe(S)
+            self._publish()
+            return self.keys, self.values
+        wdt = self._win_k.dtype
+        if T0:
+            keys = torch.cat([self._win_k[:, :, :T0], key_states.to(wdt)], dim=2)
+            values = torch.cat([self._win_v[:, :, :T0], value_states.to(wdt)], dim=2)
+        else:
+            keys, values = key_states, value_states
         if new_S_q > self._committed_S_q:
             start, end = self._committed_S_q, new_S_q
             v_new = values.squeeze(0)[:, : end - start, :]
             n_cp = (end - start) // self._page
             page_entries = self._page * C
-            if self._path == "rtn":   # post-RoPE keys straight from the slab
+            if self._path == "rtn":   # post-RoPE keys straight from the window
                 self._commit_rtn(keys.squeeze(0)[:, : end - start, :], v_new)
                 self._quant_bits_k += n_cp * (self.k_spec.bits + 16.0 / self.k_spec.group) * page_entries
                 self._quant_bits_v += n_cp * (self.v_spec.bits + 16.0 / self.v_spec.group) * page_entries
                 self._committed_S_q = end
             else:
-                if self._k_pre is None:
-                    raise RuntimeError("no pre-RoPE keys captured: call cache.attach(model) before prefill")
-                lo, hi = start - self._k_pre_offset, end - self._k_pre_offset
+                k_pre = self._take_k_pre(start, end)
                 if self._path == "spectral":
-                    self._commit_spectral(self._k_pre[:, lo:hi, :], v_new)
+                    self._commit_spectral(k_pre, v_new)
                     self._quant_bits_k += n_cp * spectral.payload_bpe(self._pack.bits, self._pack.group) \
                         * page_entries
                 else:
-                    self._commit(self._k_pre[:, lo:hi, :], v_new)
+                    self._commit(k_pre, v_new)
                     self._quant_bits_k += n_cp * K.bpe_k(self._rank, C) * page_entries
                 self._quant_bits_v += n_cp * K.bpe_v(self._h_kv, C) * page_entries
                 self._committed_S_q = end
-                if hi >= self._k_pre.shape[1]:
-                    self._k_pre, self._k_pre_offset = None, end
-                elif hi > 0:
-                    self._k_pre, self._k_pre_offset = self._k_pre[:, hi:, :].contiguous(), end
-            keys = keys[..., end - start:, :].contiguous()
-            values = values[..., end - start:, :].contiguous()
-            self._packed_len_dev = None
+            keys = keys[..., end - start:, :]
+            values = values[..., end - start:, :]
+            self._packed_len_dev.fill_(end)
+            self._after_commit(start, end)
+        T = keys.shape[2]
+        if T > self._win_k.shape[2]:
+            raise RuntimeError(f"window of {T} rows exceeds its buffer ({self._win_k.shape[2]})")
+        self._win_k[:, :, :T].copy_(keys)
+        self._win_v[:, :, :T].copy_(values)
+        self._T = T
+        self._set_bpe(S)
+        self._publish()
+        return self.keys, self.values
+
+    def _after_commit(self, start: int, end: int) -> None:
+        """Hook: positions [start, end) were just committed."""
+
+    def _publish(self) -> None:
+        """What update() returns and the layer holds as keys/values: the window."""
+        self.keys, self.values = self._win_k[:, :, : self._T], self._win_v[:, :, : self._T]
+
+    def _set_bpe(self, S: int) -> None:
+        C = self._h_kv * self._d_head
         total = S * C
         if total > 0:
-            tail = keys.shape[2] * C * 16.0
+            tail = self._T * C * 16.0
             self.bpe_k = (self._quant_bits_k + tail) / total
             self.bpe_v = (self._quant_bits_v + tail) / total
-        self.keys, self.values = keys, values
-        return keys, values
 
     def get_seq_length(self) -> int:
-        if not self.is_initialized or self.keys is None or self.keys.numel() == 0:
-            return self._committed_S_q
-        return self._committed_S_q + self.keys.shape[-2]
+        return self._committed_S_q + self._T
 
     # -------------------------------------------------------------- read side
 
@@ -354,36 +463,57 @@ class PackedStreamingLayer(DynamicLayer):
         return self._dense(q, scaling, G, is_causal and n_q > 1, attention_mask)
 
     def _decode(self, q: torch.Tensor, scaling: float, G: int) -> torch.Tensor:
+        """One query step through the layer's bound decode plan: q, the window
+        length and the pending newest row are the only per-call arguments."""
         dev = q.device
-        P = self._committed_S_q
-        if self._packed_len_dev is None or self._packed_len_dev.device != dev:
-            self._packed_len_dev = torch.tensor([P], dtype=torch.int32, device=dev)
-        k_tail = self.keys.half().contiguous()
-        v_tail = self.values.half().contiguous()
-        T = k_tail.shape[2]
-        if self._path == "rtn":
-            if P > 0:
-                pool, table = self._pool, self._table
+        h, d = self._h_kv, self._d_head
+        P, T = self._committed_S_q, self._T
+        q32 = q.reshape(1, h, G, d).float()
+        if not q32.is_contiguous():
+            q32 = q32.contiguous()
+        if self._win_k.dtype != torch.float16:   # a model in fp32: the window goes in as fp16
+            self._land_pending()
+            kt = self._win_k[:, :, :T].half().contiguous()
+            vt = self._win_v[:, :, :T].half().contiguous()
+            pool, table, basis16 = self._decode_operands(dev)
+            if self._path == "rtn":
+                out = rtn.decode(q32, pool, table, self._packed_len_dev, P, scaling, k_tail=kt, v_tail=vt,
+                                 tail_len=T, tail_cap=T, **self._rtn)
             else:
-                pool = torch.zeros(1, self._page_bytes(), dtype=torch.uint8, device=dev)
-                table = torch.zeros(1, 1, dtype=torch.int32, device=dev)
-            out = rtn.decode(
-                q.reshape(1, self._h_kv, G, self._d_head).float().contiguous(), pool, table,
-                self._packed_len_dev, P, scaling, k_tail=k_tail, v_tail=v_tail,
-                tail_len=torch.tensor([T], dtype=torch.int32, device=dev), tail_cap=T, **self._rtn)
-            return out.reshape(self._h_kv * G, 1, self._d_head)
-        if P > 0:
-            # the pool holds this sequence's pages in order: no table to read
-            pool, basis16 = self._pool, self._basis16
-        else:   # window only: the kernel reads no page
-            pool = torch.zeros(1, k2b.page_bytes(self._h_kv, self._rank), dtype=torch.uint8, device=dev)
-            basis16 = torch.zeros(self._h_kv * self._d_head, self._rank, dtype=torch.float16, device=dev)
-        out = k2b.decode(
-            q.reshape(1, self._h_kv, G, self._d_head).float().contiguous(), pool, None,
-            self._packed_len_dev, P, basis16, self._consts, scaling, rank=self._rank,
-            k_tail=k_tail, v_tail=v_tail,
-            tail_len=torch.tensor([T], dtype=torch.int32, device=dev), tail_cap=T)
-        return out.reshape(self._h_kv * G, 1, self._d_head)
+                out = k2b.decode(q32, pool, None, self._packed_len_dev, P, basis16, self._consts, scaling,
+                                 rank=self._rank, k_tail=kt, v_tail=vt, tail_len=T, tail_cap=T)
+            return out.reshape(h * G, 1, d)
+        key = (P, G, float(scaling), None if self._pool is None else self._pool.data_ptr())
+        if self._plan is None or self._plan_key != key:
+            pool, table, basis16 = self._decode_operands(dev)
+            cap = self._win_k.shape[2]
+            common = dict(k_tail=self._win_k, v_tail=self._win_v, tail_len=T, tail_cap=cap,
+                          out=torch.empty_like(q32))
+            if self._path == "rtn":
+                self._plan = rtn.DecodePlan(q32, pool, table, self._packed_len_dev, P, scaling, **common,
+                                            **self._rtn)
+            else:
+                self._plan = k2b.DecodePlan(q32, pool, None, self._packed_len_dev, P, basis16, self._consts,
+                                            scaling, rank=self._rank, **common)
+            self._plan_key = key
+        pending, self._pending = self._pending, None
+        out = self._plan.run(q=q32, tail_len=T, new_kv=pending)
+        self.n_rows_folded += pending is not None
+        if q.dtype == torch.float32:   # the caller keeps the output as it is: a copy of the plan's buffer
+            out = out.clone()
+        return out.reshape(h * G, 1, d)
+
+    def _decode_operands(self, dev) -> tuple:
+        """(pool, page table, basis16) for a decode over the committed pages; with
+        none committed, stand-ins that the kernel does not read."""
+        if self._committed_S_q > 0:
+            return self._pool, self._table, self._basis16
+        if self._empty_pool is None:
+            self._empty_pool = (torch.zeros(1, self._page_bytes(), dtype=torch.uint8, device=dev),
+                                torch.zeros(1, 1, dtype=torch.int32, device=dev),
+                                torch.zeros(self._h_kv * self._d_head, max(self._rank or 16, 16),
+                                            dtype=torch.float16, device=dev))
+        return self._empty_pool
 
     def _decode_spectral(self, q: torch.Tensor, scaling: float, G: int) -> torch.Tensor:
         """One decode step of the spectral arm: the reference's chunked step
@@ -397,8 +527,9 @@ class PackedStreamingLayer(DynamicLayer):
             self._dp = spectral.DevicePack(self._pack, self._h_kv, q.device)
         qg = q.reshape(h, G, d).contiguous()
         kw = vw = None
-        if self.keys is not None and self.keys.numel():
-            kw, vw = self.keys.squeeze(0).half().contiguous(), self.values.squeeze(0).half().contiguous()
+        wk, wv = self.window()
+        if wk is not None and wk.shape[2]:
+            kw, vw = wk.squeeze(0).half().contiguous(), wv.squeeze(0).half().contiguous()
         kt = self._ktable[: P // spectral.GROUP] if P else None
         vt = self._table[0, : P // k2b.PAGE_TOKENS].contiguous() if P else None
         out = spectral.decode_attention(self._dp, self._kpool, kt, self._pool, vt, P, self._consts, qg, scaling,
@@ -417,6 +548,8 @@ class PackedStreamingLayer(DynamicLayer):
         the bottom right."""
         dev, dt = q.device, q.dtype
         P = self._committed_S_q
+        wk, wv = self.window()
+        T = 0 if wk is None else wk.shape[2]
         parts_k, parts_v = [], []
         if P > 0 and self._path == "rtn":   # keys were committed post-RoPE
             kp, vp = rtn.dequant(self._pool, self._table[0, : P // rtn.PAGE_TOKENS].contiguous(),
@@ -426,15 +559,14 @@ class PackedStreamingLayer(DynamicLayer):
         elif P > 0 and self._path == "spectral":
             # keys rotated at read with the fp16 tables, written with room for
             # the window after them (no second copy of the dequantized rows)
-            T = 0 if self.keys is None else self.keys.shape[2]
             Kd = torch.empty(self._h_kv, P + T, self._d_head, dtype=dt, device=dev)
             Vd = torch.empty_like(Kd)
             spectral.dequant(self._dp, self._kpool, self._ktable[: P // spectral.GROUP], self._pool,
                              self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._consts,
                              apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt, out=(Kd, Vd))
             if T:
-                Kd[:, P:].copy_(self.keys.squeeze(0))
-                Vd[:, P:].copy_(self.values.squeeze(0))
+                Kd[:, P:].copy_(wk.squeeze(0))
+                Vd[:, P:].copy_(wv.squeeze(0))
             parts_k, parts_v = [Kd], [Vd]
         elif P > 0:
             kp, vp = k2b.dequant(self._pool, self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P,
@@ -442,9 +574,9 @@ class PackedStreamingLayer(DynamicLayer):
                                  apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt)
             parts_k.append(kp)
             parts_v.append(vp)
-        if self.keys is not None and self.keys.numel() and not (P > 0 and self._path == "spectral"):
-            parts_k.append(self.keys.squeeze(0).to(dt))
-            parts_v.append(self.values.squeeze(0).to(dt))
+        if T and not (P > 0 and self._path == "spectral"):
+            parts_k.append(wk.squeeze(0).to(dt))
+            parts_v.append(wv.squeeze(0).to(dt))
         Kd = torch.cat(parts_k, dim=1) if len(parts_k) > 1 else parts_k[0]
         Vd = torch.cat(parts_v, dim=1) if len(parts_v) > 1 else parts_v[0]
         n_q, n_kv = q.shape[1], Kd.shape[1]
@@ -482,6 +614,8 @@ class PackedStreamingCache(Cache):
             out = model.generate(ids, past_key_values=cache, ...)
     """
 
+    _layer_cls = PackedStreamingLayer
+
     def __init__(self, model_config, k_spec: CacheCodecSpec, v_spec: CacheCodecSpec,
                  recent_window: int = 32, pack_v: bool = True, pack_k: bool = True):
         path = packed_path(k_spec, v_spec)
@@ -496,9 +630,9 @@ class PackedStreamingCache(Cache):
                 if i not in wself._packs:
                     raise KeyError(f"spectral pack file missing layer {i}")
                 pack = wself._packs[i]
-            return PackedStreamingLayer(wself.k_spec, wself.v_spec, wself.model_config,
-                                        wself.recent_window, pack_v=wself.pack_v, pack_k=wself.pack_k,
-                                        pack=pack)
+            return wself._layer_cls(wself.k_spec, wself.v_spec, wself.model_config,
+                                    wself.recent_window, pack_v=wself.pack_v, pack_k=wself.pack_k,
+                                    pack=pack)
 
         self._make_layer = _make_layer
         super().__init__(layer_class_to_replicate=_make_layer)
@@ -572,3 +706,118 @@ class PackedStreamingCache(Cache):
     def __exit__(self, *exc):
         self.detach()
         return False
+
+
+# ------------------------------------------------------------------ streaming twin
+
+
+class StreamingQuantizedLayer(PackedStreamingLayer):
+    """The reference's StreamingQuantizedLayer (cache/streaming.py:308-650) on
+    the packed kernels: the same flush schedule and codecs; each committed codec
+    page is encoded by the append kernel and then, once, dequantized by the
+    page kernel into a write-once dense prefix in the cache dtype (k2b keys
+    rotated at their true positions with fp32 cos/sin, as
+    _quantize_k_block_pre_rope does at :390-453).  The layer's keys/values are
+    that prefix followed by the pristine recent tail, and the model's own
+    attention (SDPA) reads them.  Prefix and tail share one slab
+    (1, h_kv, capacity, d) indexed by absolute position, the tail a sliding view
+    of it from the committed length on: a step appends one row, a commit moves
+    none, and the slab grows by doubling."""
+
+    def __init__(self, k_spec: CacheCodecSpec, v_spec: CacheCodecSpec, model_config,
+                 recent_window: int = 32, pack_v: bool = True, pack_k: bool = True,
+                 pack: "spectral.SpectralPack | None" = None):
+        super().__init__(k_spec, v_spec, model_config, recent_window, pack_v=pack_v, pack_k=pack_k, pack=pack)
+        self._slab_k: torch.Tensor | None = None
+        self._slab_v: torch.Tensor | None = None
+
+    def _window_dtype(self) -> torch.dtype:
+        return self.dtype   # prefix and tail in the cache dtype (streaming.py:583-646)
+
+    def _fold_ok(self, key_states: torch.Tensor) -> bool:
+        return False
+
+    def _ensure_window(self, device, committed_after: int) -> None:
+        need = committed_after + self.recent_window + self._page
+        have = 0 if self._slab_k is None else self._slab_k.shape[2]
+        if need > have:
+            rows = max(need, 2 * have, 1024)
+            k = torch.zeros(1, self._h_kv, rows, self._d_head, dtype=self._window_dtype(), device=device)
+            v = torch.zeros_like(k)
+            used = self._committed_S_q + self._T
+            if used:
+                k[:, :, :used].copy_(self._slab_k[:, :, :used])
+                v[:, :, :used].copy_(self._slab_v[:, :, :used])
+            self._slab_k, self._slab_v = k, v
+            if self._packed_len_dev is None:
+                self._packed_len_dev = torch.zeros(1, dtype=torch.int32, device=device)
+        self._point_window(self._committed_S_q)
+
+    def _point_window(self, P: int) -> None:
+        cap = self.recent_window + self._page
+        self._win_k = self._slab_k[:, :, P:P + cap]
+        self._win_v = self._slab_v[:, :, P:P + cap]
+
+    def _after_commit(self, start: int, end: int) -> None:
+        """Dequantize the pages of positions [start, end) into slab rows [start, end)."""
+        dt = self._slab_k.dtype
+        out = (self._slab_k[0, :, start:], self._slab_v[0, :, start:])
+        p0, p1 = start // k2b.PAGE_TOKENS, end // k2b.PAGE_TOKENS
+        if self._path == "rtn":
+            rtn.dequant(self._pool, self._table[0, p0:p1].contiguous(), h_kv=self._h_kv, dtype=dt, out=out,
+                        **self._rtn)
+        elif self._path == "spectral":
+            # the spectral page kernel writes from position 0: the whole prefix again
+            spectral.dequant(self._dp, self._kpool, self._ktable[: end // spectral.GROUP], self._pool,
+                             self._table[0, :p1].contiguous(), end, self._consts, apply_rope=k2b.ROPE_EXACT,
+                             dtype=dt, out=(self._slab_k[0], self._slab_v[0]))
+        else:
+            k2b.dequant(self._pool, self._table[0, p0:p1].contiguous(), end - start, self._basis16, self._consts,
+                        h_kv=self._h_kv, rank=self._rank, apply_rope=k2b.ROPE_EXACT, dtype=dt, pos0=start,
+                        out=out)
+        self._point_window(end)
+
+    def _publish(self) -> None:
+        S = self._committed_S_q + self._T
+        self.keys, self.values = self._slab_k[:, :, :S], self._slab_v[:, :, :S]
+
+    def attend(self, q, scaling, is_causal=False, attention_mask=None):
+        raise RuntimeError("StreamingQuantizedLayer is read by the model's own attention")
+
+
+class StreamingQuantizedCache(PackedStreamingCache):
+    """Drop-in ``past_key_values=`` twin of PackedStreamingCache
+    (cache/streaming.py:653-815): the same specs and flush schedule, the
+    committed prefix resident dequantized, attention by the model's own
+    implementation.  ``attach(model)`` only registers the pre-RoPE key capture
+    (a no-op for post-RoPE key codecs)."""
+
+    _layer_cls = StreamingQuantizedLayer
+
+    def __init__(self, model_config, k_spec: CacheCodecSpec, v_spec: CacheCodecSpec,
+                 recent_window: int = 32):
+        super().__init__(model_config, k_spec, v_spec, recent_window)
+
+    def attach(self, model) -> "StreamingQuantizedCache":
+        self.detach()
+        if not self.k_spec.pre_rope:
+            return self
+        self._model = model
+        decoder = resolve_decoder_layers(model)
+        while len(self.layers) < len(decoder):
+            self.layers.append(self._make_layer())
+        for i, mlayer in enumerate(decoder):
+            layer_ref = weakref.proxy(self.layers[i])
+
+            def k_hook(module, inp, out, layer=layer_ref):
+                layer.stash_pre_rope(out)
+
+            self._handles.append(resolve_k_capture_module(mlayer.self_attn).register_forward_hook(k_hook))
+        return self
+
+    def reconstruct_layer(self, layer_idx: int) -> tuple:
+        """(keys, values) as the layer holds them, (1, h_kv, S, d): RoPE'd keys,
+        dequantized prefix then the fp16 tail (streaming.py:780-786)."""
+        layer = self.layers[layer_idx]
+        return layer.keys, layer.values
+

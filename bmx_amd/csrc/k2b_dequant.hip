@@ -8,6 +8,8 @@ namespace bmx {
 
 struct DequantKArgs {
   int h_kv, R, n_tokens, apply_rope, n_pool, out_dtype;
+  int pos0;          // position of the first listed token
+  int64_t out_rows;  // rows between consecutive heads in k_out / v_out
   const uint8_t* pages;
   const int32_t* page_table;
   const uint16_t* basis;
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
     for (int k = 0; k < kPT * 64 / (64 * kDqWaves); ++k) {
       const int e = tid + 64 * kDqWaves * k, t = e >> 6, j = e & 63;
       float sn, cn;
-      sincosf(a.inv_freq[j] * (float)(lp * kPT + t), &sn, &cn);
+      sincosf(a.inv_freq[j] * (float)(a.pos0 + lp * kPT + t), &sn, &cn);
       cn *= a.rope_scaling;
       sn *= a.rope_scaling;
       if (a.apply_rope == 2) {   // the reference's fp16 tables
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
     }
   }
   __syncthreads();
-  const int64_t row0 = (int64_t)h * a.n_tokens + (int64_t)lp * kPT;
+  const int64_t row0 = (int64_t)h * a.out_rows + (int64_t)lp * kPT;
   if (active) dq_store_tile(tl, a.k_out, row0, a.out_dtype);
   __syncthreads();   // the staging tile is reused for the values
 
@@ -160,6 +162,10 @@ extern "C" int bmx_k2b_dequant(const bmx_k2b_dequant_args* a, void* stream) {
     bmx_set_error("bmx_k2b_dequant: out_dtype must be BMX_K2B_F16, _F32 or _BF16");
     return BMX_E_INVALID;
   }
+  if (a->pos0 < 0 || (a->out_rows != 0 && a->out_rows < a->n_tokens)) {
+    bmx_set_error("bmx_k2b_dequant: pos0 must be >= 0 and out_rows 0 or >= n_tokens");
+    return BMX_E_INVALID;
+  }
   k.h_kv = g.h_kv; k.R = g.rank; k.n_tokens = a->n_tokens; k.apply_rope = a->apply_rope;
   k.out_dtype = a->out_dtype;
   k.pages = a->pages; k.page_table = a->page_table; k.basis = a->basis; k.n_pool = a->n_pool_pages;
@@ -168,6 +174,8 @@ extern "C" int bmx_k2b_dequant(const bmx_k2b_dequant_args* a, void* stream) {
   for (int j = 0; j < 64; ++j) k.inv_freq[j] = a->inv_freq[j];
   for (int j = 0; j < 4; ++j) { k.codebook[j] = a->codebook[j]; k.v_sign_bits[j] = a->v_sign_bits[j]; }
   k.k_out = a->k_out; k.v_out = a->v_out;
+  k.pos0 = a->pos0;
+  k.out_rows = a->out_rows ? a->out_rows : a->n_tokens;
   const dim3 grid(a->n_tokens / kPT, (g.h_kv + kDqWaves - 1) / kDqWaves);
   if (g.rank == 32)
     hipLaunchKernelGGL(k2b_dequant_kernel<32>, grid, dim3(64 * kDqWaves), 0, (hipStream_t)stream, k);

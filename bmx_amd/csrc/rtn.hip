@@ -205,7 +205,7 @@ struct RtnDequantKArgs {
   int h_kv, n_pool, karm;
   const uint8_t* pages;
   const int32_t* page_ids;
-  int64_t n_tok;
+  int64_t n_tok;       // rows between consecutive heads in k_out / v_out
   void* k_out;
   void* v_out;
   int out_dtype;
@@ -775,10 +775,12 @@ extern "C" int bmx_rtn_dequant(const bmx_rtn_dequant_args* a, void* stream) {
     return rfail(BMX_E_INVALID, "bmx_rtn_dequant: null pointer argument or empty pool");
   if (a->out_dtype < BMX_K2B_F16 || a->out_dtype > BMX_K2B_BF16)
     return rfail(BMX_E_INVALID, "bmx_rtn_dequant: out_dtype must be BMX_K2B_F16, _F32 or _BF16");
+  if (a->out_rows != 0 && a->out_rows < (int64_t)a->n_pages * kPT)
+    return rfail(BMX_E_INVALID, "bmx_rtn_dequant: out_rows must be 0 or >= 16 * n_pages");
   RtnDequantKArgs k{};
   const bmx_rtn_geom& g = a->geom;
   k.h_kv = g.h_kv; k.n_pool = a->n_pool_pages; k.pages = a->pages; k.page_ids = a->page_ids;
-  k.n_tok = (int64_t)a->n_pages * kPT; k.k_out = a->k_out; k.v_out = a->v_out; k.out_dtype = a->out_dtype;
+  k.n_tok = a->out_rows ? a->out_rows : (int64_t)a->n_pages * kPT; k.k_out = a->k_out; k.v_out = a->v_out; k.out_dtype = a->out_dtype;
   k.gk = g.k_group; k.gv = g.v_group; k.karm = g.k_arm;
   k.L = RtnLayout::make(g.h_kv, g.k_arm, g.k_group, g.v_group);
   hipLaunchKernelGGL(rtn_dequant_kernel, dim3(a->n_pages, g.h_kv), dim3(256), 0, (hipStream_t)stream, k);

@@ -82,12 +82,17 @@ def set_window_rows(a, B: int, h_kv: int, tail_len, tail_cap: int, new_kv=None) 
         return
     k, v = new_kv
     _need(not isinstance(tail_len, torch.Tensor), "rows given apart need a host tail_len")
-    _need(k.dtype == torch.float16 and v.dtype == torch.float16 and k.shape == v.shape and k.stride() == v.stride()
-          and k.dim() == 4 and k.shape[0] == B and k.shape[1] == h_kv and k.shape[3] == HEAD_DIM
-          and k.stride(3) == 1, "new_kv: fp16 (B, h_kv, n, 128) keys and values with the same strides")
-    _need(all(st % 8 == 0 for st in k.stride()[:3]), "new_kv strides must be multiples of 8 elements")
+    _need(k.dim() == 4 and k.shape == v.shape and k.dtype == torch.float16 and v.dtype == torch.float16
+          and k.shape[0] == B and k.shape[1] == h_kv and k.shape[3] == HEAD_DIM,
+          "new_kv: fp16 (B, h_kv, n, 128) keys and values")
+    # strides of size-1 dimensions are never used: taken as 0
+    sk = tuple(0 if n == 1 else st for n, st in zip(k.shape[:3], k.stride()[:3]))
+    sv = tuple(0 if n == 1 else st for n, st in zip(v.shape[:3], v.stride()[:3]))
+    _need(sk == sv and k.stride(3) == 1 and v.stride(3) == 1,
+          "new_kv: keys and values with the same strides, channels contiguous")
+    _need(all(st % 8 == 0 for st in sk), "new_kv strides must be multiples of 8 elements")
     a.new_k, a.new_v = k.data_ptr(), v.data_ptr()
-    a.new_stride_b, a.new_stride_h, a.new_stride_t = k.stride(0), k.stride(1), k.stride(2)
+    a.new_stride_b, a.new_stride_h, a.new_stride_t = sk
     a.n_new = k.shape[2]
     _need(a.n_new <= a.tail_len_value, "new_kv holds more rows than the window")
 
@@ -286,17 +291,34 @@ class DecodePlan:
 ROPE_NONE, ROPE_EXACT, ROPE_FP16_TABLES = 0, 1, 2
 
 
+def _dense_out(out, h_kv: int, n_rows: int, dtype, dev):
+    """(K, V) destinations of a dequant: new (h_kv, n_rows, 128) tensors, or the
+    caller's (h_kv, >= n_rows, 128) views with contiguous rows; -> (K, V, rows
+    between heads)."""
+    if out is None:
+        k = torch.empty(h_kv, n_rows, HEAD_DIM, dtype=dtype, device=dev)
+        return k, torch.empty_like(k), n_rows
+    k, v = out
+    _need(k.dtype == dtype and v.dtype == dtype and k.shape == v.shape and k.stride() == v.stride()
+          and k.dim() == 3 and k.shape[0] == h_kv and k.shape[1] >= n_rows and k.shape[2] == HEAD_DIM
+          and k.stride(2) == 1 and k.stride(1) == HEAD_DIM and k.stride(0) % HEAD_DIM == 0
+          and k.device == dev, "out must be (K, V) of shape (h_kv, >= n, 128) in dtype with contiguous rows")
+    return k, v, k.stride(0) // HEAD_DIM
+
+
 def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis16: torch.Tensor,
             consts: CodecConsts, *, h_kv: int, rank: int, apply_rope: int = ROPE_NONE,
-            dtype: torch.dtype = torch.float32):
+            dtype: torch.dtype = torch.float32, pos0: int = 0, out: tuple | None = None):
     """Committed pages of one sequence -> dense (K (h_kv, n, 128), V (h_kv, n, 128))
     in dtype.  apply_rope: ROPE_NONE (pre-RoPE keys), ROPE_EXACT (fp32 cos/sin)
-    or ROPE_FP16_TABLES (the reference's prefill: fp16-rounded cos/sin)."""
+    or ROPE_FP16_TABLES (the reference's prefill: fp16-rounded cos/sin); pos0:
+    the position of the first listed token; out: (K, V) views to write into (see
+    _dense_out)."""
     dev = pages.device
     _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
     _need(int(apply_rope) in (ROPE_NONE, ROPE_EXACT, ROPE_FP16_TABLES), "apply_rope must be 0, 1 or 2")
-    k = torch.empty(h_kv, n_tokens, HEAD_DIM, dtype=dtype, device=dev)
-    v = torch.empty_like(k)
+    _need(pos0 >= 0, "pos0 must be >= 0")
+    k, v, rows = _dense_out(out, h_kv, n_tokens, dtype, dev)
     _need(page_table.dtype == torch.int32 and page_table.numel() >= n_tokens // PAGE_TOKENS,
           "page_table must hold n_tokens/16 int32 page ids")
     a = _lib.DequantArgs()
@@ -311,5 +333,6 @@ def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis1
     a.v_sign_bits[:] = consts.sign_bits
     a.k_out, a.v_out = _ptr(k), _ptr(v)
     a.out_dtype = _V_DTYPES[dtype]
+    a.pos0, a.out_rows = int(pos0), rows
     _lib.check(_lib.lib().bmx_k2b_dequant(ct.byref(a), _stream(dev)), "bmx_k2b_dequant")
     return k, v

@@ -17,7 +17,7 @@ import ctypes as ct
 import torch
 
 from . import _lib
-from .k2b import DecodeWorkspace, _need, _ptr, _stream, _V_DTYPES, set_window_rows
+from .k2b import DecodeWorkspace, _dense_out, _need, _ptr, _stream, _V_DTYPES, set_window_rows
 
 HEAD_DIM = 128
 PAGE_TOKENS = 16
@@ -171,18 +171,20 @@ class DecodePlan:
 
 
 def dequant(pages: torch.Tensor, page_ids: torch.Tensor, *, h_kv: int, k_bits: int, v_bits: int,
-            k_group: int, v_group: int, k_arm: int = TOKEN, dtype: torch.dtype = torch.float32):
-    """Pages (in order) -> dense (K (h_kv, 16n, 128), V (h_kv, 16n, 128)) in dtype."""
+            k_group: int, v_group: int, k_arm: int = TOKEN, dtype: torch.dtype = torch.float32,
+            out: tuple | None = None):
+    """Pages (in order) -> dense (K (h_kv, 16n, 128), V (h_kv, 16n, 128)) in dtype;
+    out: (K, V) views to write into, as for k2b.dequant."""
     n = page_ids.numel()
     _need(page_ids.dtype == torch.int32 and page_ids.is_contiguous(), "page_ids must be contiguous int32")
     _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
-    k_out = torch.empty(h_kv, n * PAGE_TOKENS, HEAD_DIM, dtype=dtype, device=pages.device)
-    v_out = torch.empty_like(k_out)
+    k_out, v_out, rows = _dense_out(out, h_kv, n * PAGE_TOKENS, dtype, pages.device)
     a = _lib.RtnDequantArgs()
     a.geom = geom(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     a.pages, a.n_pool_pages = _ptr(pages), pages.shape[0]
     a.page_ids, a.n_pages = _ptr(page_ids), n
     a.k_out, a.v_out = _ptr(k_out), _ptr(v_out)
     a.out_dtype = _V_DTYPES[dtype]
+    a.out_rows = rows
     _lib.check(_lib.lib().bmx_rtn_dequant(ct.byref(a), _stream(pages.device)), "bmx_rtn_dequant")
     return k_out, v_out

@@ -234,9 +234,11 @@ typedef struct {
   int32_t apply_rope;
   float codebook[4];
   uint32_t v_sign_bits[4];
-  void* k_out;                /* device [h_kv][n_tokens][128] of out_dtype */
-  void* v_out;                /* device [h_kv][n_tokens][128] of out_dtype */
+  void* k_out;                /* device [h_kv][out_rows][128] of out_dtype: rows 0 .. n_tokens - 1 */
+  void* v_out;                /* of each head written */
   int32_t out_dtype;          /* BMX_K2B_F16 (0), BMX_K2B_F32 or BMX_K2B_BF16 */
+  int32_t pos0;               /* RoPE position of the first listed token (0: the sequence's start) */
+  int64_t out_rows;           /* rows per head in k_out / v_out, >= n_tokens (0: n_tokens) */
 } bmx_k2b_dequant_args;
 
 int bmx_k2b_dequant(const bmx_k2b_dequant_args* args, void* stream);

@@ -145,7 +145,8 @@ int bmx_rtn_decode(const bmx_rtn_decode_args* args, void* stream);
  * Dequantize pages to dense keys and values (prefill): the dequant half of
  * chunked_attention._dense_kv and the dtype cast of _assemble_dense_kv
  * (cache/chunked_attention.py:148-251) for the RTN arms (code * the page's scale,
- * rounded once to out_dtype).  k_out/v_out: device [h_kv][16 * n_pages][128].
+ * rounded once to out_dtype).  k_out/v_out: device [h_kv][out_rows][128],
+ * rows 0 .. 16 * n_pages - 1 of each head written.
  * ---------------------------------------------------------------------- */
 typedef struct {
   bmx_rtn_geom geom;
@@ -156,6 +157,7 @@ typedef struct {
   void* k_out;
   void* v_out;
   int32_t out_dtype;          /* BMX_K2B_F16 (0), BMX_K2B_F32 or BMX_K2B_BF16 */
+  int64_t out_rows;           /* rows per head in k_out / v_out, >= 16 * n_pages (0: 16 * n_pages) */
 } bmx_rtn_dequant_args;
 
 int bmx_rtn_dequant(const bmx_rtn_dequant_args* args, void* stream);

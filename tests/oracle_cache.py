@@ -79,31 +79,26 @@ class OracleLayer(product.PackedStreamingLayer):
                 memo = self._kv_memo = ((P, dtype), kc, self._oc.dense_v().to(dtype))
             ks.append(memo[1])
             vs.append(memo[2])
-        if self.keys is not None and self.keys.numel():
-            ks.append(self.keys.squeeze(0).to(dtype))
-            vs.append(self.values.squeeze(0).to(dtype))
+        kw, vw = self.window()   # the product layer's window (its newest row stored)
+        if kw is not None and kw.shape[2]:
+            ks.append(kw.squeeze(0).cpu().to(dtype))
+            vs.append(vw.squeeze(0).cpu().to(dtype))
         return torch.cat(ks, dim=1), torch.cat(vs, dim=1)
 
     def attend(self, q, scaling, is_causal=False, attention_mask=None):
         if q.device.type != "cpu":   # model on a GPU: the oracle attends on the host
-            keys, values = self.keys, self.values
-            self.keys, self.values = keys.cpu(), values.cpu()
-            try:
-                out = self.attend(q.cpu(), scaling, is_causal,
-                                  None if attention_mask is None else attention_mask.cpu())
-            finally:
-                self.keys, self.values = keys, values
+            out = self.attend(q.cpu(), scaling, is_causal, None if attention_mask is None else attention_mask.cpu())
             return out.to(q.device)
         n_heads, n_q, d = q.shape
         G = n_heads // self._h_kv
-        Kd, Vd = self._kv(q.dtype)
+        Kd, Vd = self._kv(q.dtype)   # rounded to the model dtype, as the product's are
         if n_q == 1 and not is_causal:
             return A.grouped_dense_attention(q.float(), Kd, Vd, G, scaling).to(q.dtype)
-        Kx, Vx = Kd.repeat_interleave(G, dim=0), Vd.repeat_interleave(G, dim=0)
+        Kx, Vx = Kd.float().repeat_interleave(G, dim=0), Vd.float().repeat_interleave(G, dim=0)
         causal = is_causal and n_q > 1
         return F.scaled_dot_product_attention(
-            q.unsqueeze(0), Kx.unsqueeze(0), Vx.unsqueeze(0), attn_mask=attention_mask,
-            is_causal=causal and attention_mask is None, scale=scaling).squeeze(0)
+            q.float().unsqueeze(0), Kx.unsqueeze(0), Vx.unsqueeze(0), attn_mask=attention_mask,
+            is_causal=causal and attention_mask is None, scale=scaling).squeeze(0).to(q.dtype)
 
 
 class OracleCache(product.PackedStreamingCache):

@@ -105,8 +105,15 @@ def test_window_rows_given_apart_rejected_on_the_host():
         k2b.set_window_rows(a, 1, 8, 1, 128, (k, k))
     with pytest.raises(ValueError, match="fp16"):
         k2b.set_window_rows(a, 1, 8, 4, 128, (k.float(), k.float()))
+    with pytest.raises(ValueError, match="same strides"):
+        k2b.set_window_rows(a, 1, 8, 4, 128, (k, k.transpose(1, 2).contiguous().transpose(1, 2)))
     k2b.set_window_rows(a, 1, 8, 4, 128, (k, k))
     assert a.tail_len is None and a.tail_len_value == 4 and a.n_new == 2 and a.new_stride_t == 128
+    assert a.new_stride_b == 0 and a.new_stride_h == 256   # size-1 batch: stride unused
+    # one row: its time stride is unused (any layout of the (1, h, 1, d) row)
+    r = torch.zeros(1, 1, 8, 128, dtype=torch.float16).transpose(1, 2)
+    k2b.set_window_rows(a, 1, 8, 4, 128, (r, torch.zeros(1, 8, 1, 128, dtype=torch.float16)))
+    assert a.n_new == 1 and a.new_stride_h == 128 and a.new_stride_t == 0
 
 
 def test_decode_workspace_size_formula():

@@ -82,6 +82,44 @@ def test_product_cache_matches_oracle_backed_cache(rank):
     assert agree == 1.0
 
 
+def test_fp16_model_folds_the_window_write():
+    """An fp16 model: each one-token step that commits nothing leaves its new
+    key and value to the decode call, which stores them into the window.  The
+    logits equal, bit for bit, those of the same cache with every row written
+    by a copy first (the fold turned off); against the oracle-backed cache they
+    agree to fp16 model arithmetic (the two attention outputs round to fp16
+    apart and the difference propagates through the fp16 layers): max |logit
+    delta| <= 5e-3 of the largest logit, argmax agreement >= 0.97."""
+    from bmx_amd.cache import PackedStreamingLayer
+
+    g = np.load(GOLD / "e2e_tiny_llama.npz")
+    tokens = torch.from_numpy(g["r16_tokens"]).cuda()
+    n = 140
+    model = _tiny_model().half()
+    specs = spec_pair("k2b_ph", rank=16)
+    prod = PackedStreamingCache(model.config, *specs, recent_window=32)
+    got = _run(prod, model, tokens, n)
+    folded = prod.layers[0].n_rows_folded
+    orig = PackedStreamingLayer._fold_ok
+    PackedStreamingLayer._fold_ok = lambda self, k: False
+    try:
+        plain = PackedStreamingCache(model.config, *specs, recent_window=32)
+        ref_plain = _run(plain, model, tokens, n)
+    finally:
+        PackedStreamingLayer._fold_ok = orig
+    orc = OracleCache(model.config, *specs, recent_window=32)
+    ref = _run(orc, model, tokens, n)
+    err = (got - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    agree = (got.argmax(1) == ref.argmax(1)).float().mean().item()
+    print(f"fp16: rows folded {folded}, folded == copied {torch.equal(got, ref_plain)}; vs oracle-backed "
+          f"max|err| {err:.3e} of {scale:.3f}, argmax agreement {agree:.4f}", flush=True)
+    assert folded == n - 1 - 1 and plain.layers[0].n_rows_folded == 0   # one step commits
+    assert torch.equal(got, ref_plain)
+    assert torch.equal(prod.layers[0]._pool[:24], plain.layers[0]._pool[:24])
+    assert err <= 5e-3 * max(scale, 1.0) and agree >= 0.97
+
+
 def _spectral_pack_file(tmp_path, n_layers):
     from bmx_amd import spectral
     from tests.spectral_util import synthetic_pack
@@ -180,6 +218,101 @@ def test_generate_runs_on_the_packed_path():
                              do_sample=False, pad_token_id=0)
     assert out.shape == (1, 240)
     assert cache.layers[0]._committed_S_q == 128 and cache.layers[0].get_seq_length() == 239
+
+
+def _generate(cache, model, ids, n):
+    with cache.attach(model), torch.no_grad():
+        return model.generate(ids, past_key_values=cache, max_new_tokens=n, min_new_tokens=n, do_sample=False,
+                              pad_token_id=0)
+
+
+@pytest.mark.parametrize("recipe,seq,dtype", [("k2b_ph", 12, torch.float32), ("k2b_ph", 200, torch.float32),
+                                              ("k2b_ph", 200, torch.float16), ("rtn_token_4b", 200, torch.float32),
+                                              ("kivi", 200, torch.float32)])
+def test_packed_generate_matches_streaming(recipe, seq, dtype):
+    """The reference's parity invariant (tests/test_packed_streaming.py:23-97):
+    greedy generate through PackedStreamingCache equals generate through its
+    StreamingQuantizedCache twin -- the same codes, read by the fused decode
+    kernel on one side and dequantized once into a dense prefix for the model's
+    own SDPA on the other.  A 12-token prompt (no commit before decode) and a
+    200-token prompt (a codec page commits during prefill); the packed layer's
+    resident window stays within recent_window + 128 rows."""
+    from bmx_amd.cache import StreamingQuantizedCache
+    from bmx_amd.specs import CacheCodecSpec
+
+    if recipe == "rtn_token_4b":
+        specs = (CacheCodecSpec(arm="rtn_token", bits=4, group=32, pre_rope=False),
+                 CacheCodecSpec(arm="rtn_token", bits=4, group=32))
+    elif recipe == "kivi":
+        specs = spec_pair("kivi", group=64)
+    else:
+        specs = spec_pair("k2b_ph", rank=16)
+    model = _tiny_model().to(dtype)
+    ids = torch.randint(0, 256, (1, seq), generator=torch.Generator().manual_seed(11)).cuda()
+    ref_cache = StreamingQuantizedCache(model.config, *specs)
+    ref = _generate(ref_cache, model, ids, 20)
+    packed = PackedStreamingCache(model.config, *specs)
+    out = _generate(packed, model, ids, 20)
+    lay = packed.layers[0]
+    print(f"{recipe} seq {seq} {dtype}: packed == streaming {torch.equal(out, ref)}; committed "
+          f"{lay._committed_S_q} (twin {ref_cache.layers[0]._committed_S_q}); window {lay.keys.shape[2]} rows",
+          flush=True)
+    assert lay._committed_S_q == ref_cache.layers[0]._committed_S_q == (128 if seq == 200 else 0)
+    assert lay.keys.shape[2] <= lay.recent_window + lay._page + 1
+    assert ref_cache.reconstruct_layer(0)[0].shape[2] == seq + 19
+    assert torch.equal(out, ref)
+
+
+def test_packed_vs_streaming_logit_probe_16k():
+    """The reference's teacher-forced packed-vs-streaming logit probe
+    (scripts/profile_decode_ab.py:316-439) at 16384 tokens: both caches
+    prefilled on the same prompt, then 32 steps each fed the streaming cache's
+    greedy token; per step the max |logit delta| is recorded and the flip gate
+    applied (no flip with the streaming top-2 gap above that step's delta, at
+    most N // 8 flips).  Model: fp16, Llama geometry at reduced width (2 layers,
+    8 query / 2 KV heads, d 128), key projections rank 8 plus 1% noise."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from bmx_amd.cache import StreamingQuantizedCache
+    from oracle import attention as A
+
+    ctx, N = 16384, 32
+    cfg = LlamaConfig(vocab_size=4096, hidden_size=1024, intermediate_size=2048, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+                      max_position_embeddings=32768, rope_theta=500000.0, initializer_range=0.1)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).eval()
+    gen = torch.Generator().manual_seed(4)
+    with torch.no_grad():
+        for layer in model.model.layers:
+            W = layer.self_attn.k_proj.weight
+            U, s_, Vh = torch.linalg.svd(W, full_matrices=False)
+            W.copy_((U[:, :8] * s_[:8]) @ Vh[:8] + 0.01 * W.abs().mean() * torch.randn(W.shape, generator=gen))
+    model = model.half().cuda()
+    ids = torch.randint(10, 4086, (1, ctx), generator=torch.Generator().manual_seed(1234)).cuda()
+    specs = spec_pair("k2b_ph", rank=16)
+    caches = {"streaming": StreamingQuantizedCache(model.config, *specs),
+              "packed": PackedStreamingCache(model.config, *specs)}
+    logits = {}
+    for kind, c in caches.items():
+        with c.attach(model), torch.no_grad():
+            logits[kind] = model(ids, past_key_values=c, use_cache=True, logits_to_keep=1).logits[:, -1].float()
+    flips = hard = 0
+    envelope = 0.0
+    for step in range(N):
+        tok = logits["streaming"].argmax(dim=-1, keepdim=True)
+        pos = torch.tensor([ctx + step], device="cuda")
+        for kind, c in caches.items():
+            with c.attach(model), torch.no_grad():
+                logits[kind] = model(tok, past_key_values=c, use_cache=True,
+                                     cache_position=pos).logits[:, -1].float()
+        f, h = A.argmax_flip(logits["packed"][0].cpu(), logits["streaming"][0].cpu())
+        envelope = max(envelope, (logits["packed"] - logits["streaming"]).abs().max().item())
+        flips, hard = flips + f, hard + h
+    print(f"logit probe ctx {ctx} N {N}: flips {flips} (hard {hard}), max_abs envelope {envelope:.4f}, "
+          f"committed {caches['packed'].layers[0]._committed_S_q}", flush=True)
+    assert caches["packed"].layers[0]._committed_S_q == caches["streaming"].layers[0]._committed_S_q
+    assert hard == 0 and flips <= N // 8
 
 
 def test_config5_qwen3_streaming_append_and_decode():

@@ -773,3 +773,13 @@ def test_dequant_matches_oracle(h_kv, rank):
         Kh, Vh = k2b.dequant(pool.pages, pt, S, seq.basis16, consts, h_kv=h_kv, rank=rank,
                              apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt)
         assert Kh.dtype == dt and torch.equal(Kh, Kt.to(dt)) and torch.equal(Vh, Vd.to(dt))
+    # a sub-range of pages at its true positions, written into rows of a wider
+    # buffer (the streaming twin's commit): the same rows as the full pass
+    buf_k = torch.full((h_kv, S + 40, 128), 9.0, device=DEV)
+    buf_v = torch.full_like(buf_k, 9.0)
+    p0, p1 = 8, 24   # tokens 128 .. 383
+    k2b.dequant(pool.pages, pt[p0:p1].contiguous(), 16 * (p1 - p0), seq.basis16, consts, h_kv=h_kv, rank=rank,
+                apply_rope=k2b.ROPE_EXACT, pos0=16 * p0, out=(buf_k[:, 16 * p0:], buf_v[:, 16 * p0:]))
+    assert torch.equal(buf_k[:, 16 * p0:16 * p1], Kr[:, 16 * p0:16 * p1])
+    assert torch.equal(buf_v[:, 16 * p0:16 * p1], Vd[:, 16 * p0:16 * p1])
+    assert bool((buf_k[:, :16 * p0] == 9.0).all() and (buf_k[:, 16 * p1:] == 9.0).all())

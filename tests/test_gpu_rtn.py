@@ -118,6 +118,14 @@ def test_dequant_bit_exact():
         Kh, Vh = rtn.dequant(pool.pages, torch.tensor(ids, dtype=torch.int32, device=DEV), h_kv=h_kv, dtype=dt,
                              **codec)
         assert Kh.dtype == dt and torch.equal(Kh, K.to(dt)) and torch.equal(Vh, V.to(dt))
+    # pages 4 .. 15 into rows 64 .. 255 of a wider buffer
+    buf = torch.full((2, h_kv, S + 16, 128), 5.0, dtype=torch.float16, device=DEV)
+    ids_t = torch.tensor(ids, dtype=torch.int32, device=DEV)
+    rtn.dequant(pool.pages, ids_t[4:16].contiguous(), h_kv=h_kv, dtype=torch.float16,
+                out=(buf[0, :, 64:], buf[1, :, 64:]), **codec)
+    Kh, Vh = rtn.dequant(pool.pages, ids_t, h_kv=h_kv, dtype=torch.float16, **codec)
+    assert torch.equal(buf[0, :, 64:256], Kh[:, 64:256]) and torch.equal(buf[1, :, 64:256], Vh[:, 64:256])
+    assert bool((buf[:, :, :64] == 5.0).all() and (buf[:, :, 256:] == 5.0).all())
 
 
 def _decode_case(h_kv, G, S, T, codec, gen, split_tokens=0, outliers=True, with_chunked=False):
