@@ -528,8 +528,10 @@ class PackedStreamingLayer(DynamicLayer):
         qg = q.reshape(h, G, d).contiguous()
         kw = vw = None
         wk, wv = self.window()
-        if wk is not None and wk.shape[2]:
-            kw, vw = wk.squeeze(0).half().contiguous(), wv.squeeze(0).half().contiguous()
+        if wk is not None and wk.shape[2]:   # fp16 buffers are read in place (rows contiguous)
+            kw, vw = wk.squeeze(0), wv.squeeze(0)
+            if kw.dtype != torch.float16:
+                kw, vw = kw.half().contiguous(), vw.half().contiguous()
         kt = self._ktable[: P // spectral.GROUP] if P else None
         vt = self._table[0, : P // k2b.PAGE_TOKENS].contiguous() if P else None
         out = spectral.decode_attention(self._dp, self._kpool, kt, self._pool, vt, P, self._consts, qg, scaling,

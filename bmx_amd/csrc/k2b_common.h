@@ -168,6 +168,7 @@ __device__ __forceinline__ int kres_pair_code(uint32_t w0, uint32_t w1, uint32_t
 }
 
 constexpr int kDqPad = kD + 4;   // staging row stride (floats)
+constexpr int kCsPad = 68;       // cos/sin table row stride (floats): 16-byte reads of 16 rows hit distinct banks
 
 struct DqTile {
   float v[kPT][kDqPad];
@@ -226,14 +227,22 @@ hipError_t launch_k2b_values(const AppendKArgs& a, int n_pages16, int h_kv, hipS
 // lane's code bytes (channel 16b + n, tokens 4q .. 4q + 3) give codebook
 // levels, H8 over b in registers and H16 over n across the row's lanes make
 // the 128-point Hadamard, then 1/128, the signs and the token's norm.
+// level c (0..3) of four held in registers: a select chain, no indexed load
+// (an array indexed by a lane-varying code would be read from memory)
+__device__ __forceinline__ float level4(uint32_t c, float l0, float l1, float l2, float l3) {
+  const float lo = (c & 1u) ? l1 : l0, hi = (c & 1u) ? l3 : l2;
+  return (c & 2u) ? hi : lo;
+}
+
 __device__ __forceinline__ void dq_value_tile(uint2 vcd, uint2 nrm, const float codebook[4],
                                               const uint32_t sign_bits[4], int n, int q, DqTile& tl) {
+  const float l0 = codebook[0], l1 = codebook[1], l2 = codebook[2], l3 = codebook[3];
   float y[4][8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) {
     const uint32_t D = b < 4 ? vcd.x : vcd.y;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) y[tt][b] = codebook[(D >> (8 * (b & 3) + 2 * tt)) & 3];
+    for (int tt = 0; tt < 4; ++tt) y[tt][b] = level4((D >> (8 * (b & 3) + 2 * tt)) & 3u, l0, l1, l2, l3);
   }
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {

@@ -46,7 +46,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
   const bool active = h_raw < a.h_kv;
   const int h = active ? h_raw : 0;
   const int C = kD * a.h_kv, quarter = C / 4;
-  __shared__ float s_cs[2][kPT][64];
+  __shared__ __align__(16) float s_cs[2][kPT][kCsPad];   // rows padded: conflict-free 16-byte reads
   __shared__ DqTile s_tile[kDqWaves];
 
   // ---- every load first ----
@@ -105,6 +105,8 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
     const uint32_t sv[4] = {scl[bb].x, scl[bb].y, scl[bb].z, scl[bb].w};
+    const float4_t c4 = *reinterpret_cast<const float4_t*>(&s_cs[0][n][16 * bb + 4 * q]);
+    const float4_t s4 = *reinterpret_cast<const float4_t*>(&s_cs[1][n][16 * bb + 4 * q]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 16 * bb + 4 * q + i;
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
       float k0 = kt[bb][i] + (float)cp[4 * bb + i][0] * (float)s2[0];
       float k1 = kt[bb + 4][i] + (float)cp[4 * bb + i][1] * (float)s2[1];
       if (a.apply_rope) {
-        const float c = s_cs[0][n][j], sn = s_cs[1][n][j];
+        const float c = c4[i], sn = s4[i];
         // x*cos + rotate_half(x)*sin, rounded per operation as torch does
         const float r0 = __fmul_rn(k0, c) - __fmul_rn(k1, sn);
         k1 = __fmul_rn(k1, c) + __fmul_rn(k0, sn);

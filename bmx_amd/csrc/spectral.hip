@@ -16,6 +16,33 @@ constexpr int kSpMaxSlices = BMX_SPECTRAL_MAX_CPAD / 8;
 
 __device__ __forceinline__ int sp_width(int b) { return b == 2 ? 2 : (b <= 4 ? 4 : 8); }
 
+// sin and cos of an fp32 angle x (|x| < 2^40): x - k pi/2 in double (pi/2 in
+// two parts, the first with 33 significant bits so that k times it is exact),
+// rounded once to fp32 (|r| <= pi/4: within 3e-8 of the exact reduced angle),
+// then the fp32 sin/cos of r on its short path and the quadrant's swap and
+// signs.  The library's sincosf takes a long reduction for large arguments
+// (positions times frequencies reach 1e5 at long context).
+// (cos, sin) of x - e from those of x, |e| <= 2^-7 (half an fp32 ulp at 2^17):
+// cos e and sin e to second and third order (the next terms are below 1e-10)
+__device__ __forceinline__ void rotate_back(float c, float s, float e, float* cn, float* sn) {
+  const float e2 = e * e;
+  const float ce = __builtin_fmaf(-0.5f, e2, 1.0f), se = e * __builtin_fmaf(-e2, 1.0f / 6.0f, 1.0f);
+  *cn = __builtin_fmaf(c, ce, s * se);
+  *sn = __builtin_fmaf(s, ce, -(c * se));
+}
+
+__device__ __forceinline__ void sincos_reduced(float x, float* sn, float* cn) {
+  const double xd = x;
+  const double k = rint(xd * 0.63661977236758134308);   // 2/pi
+  double rd = __builtin_fma(-k, 1.5707963267341256142, xd);     // pi/2, high part
+  rd = __builtin_fma(-k, 6.0771005065061922e-11, rd);            // pi/2 - high part
+  float sr, cr;
+  sincosf((float)rd, &sr, &cr);
+  const int qd = (int)(int64_t)k & 3;
+  *sn = qd == 0 ? sr : qd == 1 ? cr : qd == 2 ? -sr : -cr;
+  *cn = qd == 0 ? cr : qd == 1 ? -sr : qd == 2 ? -cr : sr;
+}
+
 __device__ __forceinline__ float sp_load(const void* base, int64_t i, int dtype) {
   if (dtype == BMX_K2B_F32) return static_cast<const float*>(base)[i];
   const uint16_t u = static_cast<const uint16_t*>(base)[i];
@@ -130,6 +157,13 @@ struct SpDequantKArgs {
 };
 
 constexpr int kSpBRow = 40;   // halves per token row of the staged Y_hat tile (32 + 8 pad)
+constexpr int kSpMaxKPage = 72 * 1024;   // key page bytes staged in LDS at most (c_pad 1072, 8 bits: 70768)
+constexpr int kSpPageLoads = kSpMaxKPage / (16 * 512);   // 16-byte loads per thread at most
+// dynamic LDS of the dequant kernel: the group's key page while the main loop
+// decodes it, then the waves' staging tiles
+constexpr size_t sp_dyn_bytes(int k_page_bytes) {
+  return (size_t)k_page_bytes > 8 * sizeof(DqTile) ? (size_t)k_page_bytes : 8 * sizeof(DqTile);
+}
 
 // Workgroup barrier over LDS only: this wave's LDS accesses complete, then
 // s_barrier.  Global loads in flight stay in flight (__syncthreads would wait
@@ -148,8 +182,10 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// grid (n_tokens / 64), block 512: one 64-token group, wave w = head w.  Per
-// 32-column step the group's Y_hat^T tile (code times step, fp16) is decoded
+// grid (n_tokens / 64), block 512: one 64-token group, wave w = head w.  The
+// group's key page is copied to LDS first (one round trip for the whole page,
+// issued with every other load of the prologue).  Per 32-column step the
+// group's Y_hat^T tile (code times step, fp16) is decoded from there
 // once, by all 512 threads (4 codes each), into one of two LDS buffers; every
 // head's wave reads its B fragments from there (lane 16q + n: token n of the
 // tile, columns 8q .. 8q + 7) and multiplies with its dec rows (A, lane 16q + n:
@@ -164,37 +200,94 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   const int h = wave;
   const bool head_ok = h < a.h_kv;
   __shared__ uint32_t s_tab[kSpMaxSlices];
-  __shared__ __align__(16) _Float16 s_b[2][kGroup][kSpBRow];
-  __shared__ float s_cs[2][kGroup][64];
-  __shared__ DqTile s_tile[8];
+  __shared__ __align__(16) _Float16 s_b[4][kGroup][kSpBRow];
+  __shared__ __align__(16) float s_cs[2][kGroup][kCsPad];   // rows padded: conflict-free 16-byte reads
+  // fp16 codebook levels of the 4 codes of one value-code byte (the P.V B operand)
+  __shared__ uint2 s_cbl[256];
+  extern __shared__ __align__(16) uint8_t sp_dyn[];
+  uint8_t* kp = sp_dyn;                                 // the key page, until the main loop ends
+  DqTile* s_tile = reinterpret_cast<DqTile*>(sp_dyn);   // then the staging tiles
   const int n_sl = a.c_pad >> 3;
-  for (int i = tid; i < n_sl; i += 512) s_tab[i] = (uint32_t)a.slice_tab[i];
+  const int hh = head_ok ? h : 0;   // waves past the heads load head 0's operands (unused)
+  // ---- every global load of the prologue is issued first, the RoPE
+  // frequency first of all: the table below waits for it alone (loads
+  // complete in issue order), not for the page ----
+  const int fj = tid & 63;
+  const float fq = a.inv_freq[fj];   // every table entry of this thread has frequency fj
+  __builtin_amdgcn_sched_barrier(0);
   const uint8_t* page = a.k_pages + clamp_page(a.k_table[g], a.n_k_pool) * (int64_t)a.k_page_bytes;
-  uint2 vcd[4], nrm[4];
-  if (head_ok) {
+  // the key page's 16-byte chunks (threads past the last chunk re-read it: no
+  // branch around the loads)
+  const int n16 = a.k_page_bytes >> 4;
+  uint4 kpw[kSpPageLoads];
 #pragma unroll
-    for (int pg = 0; pg < 4; ++pg) {
-      const uint8_t* vp = a.v_pages + clamp_page(a.v_table[4 * g + pg], a.n_v_pool) * (int64_t)a.VL.bytes;
-      vcd[pg] = *reinterpret_cast<const uint2*>(vp + a.VL.vcode + h * 512 + lane * 8);
-      nrm[pg] = *reinterpret_cast<const uint2*>(vp + a.VL.vnorm + (h * kPT + 4 * q) * 2);
-    }
+  for (int i = 0; i < kSpPageLoads; ++i)
+    kpw[i] = reinterpret_cast<const uint4*>(page)[min(tid + 512 * i, n16 - 1)];
+  const uint32_t tabv = (uint32_t)a.slice_tab[min(tid, n_sl - 1)];   // n_sl <= 134 < 512
+  uint2 vcd[4], nrm[4];
+#pragma unroll
+  for (int pg = 0; pg < 4; ++pg) {
+    const uint8_t* vp = a.v_pages + clamp_page(a.v_table[4 * g + pg], a.n_v_pool) * (int64_t)a.VL.bytes;
+    vcd[pg] = *reinterpret_cast<const uint2*>(vp + a.VL.vcode + hh * 512 + lane * 8);
+    nrm[pg] = *reinterpret_cast<const uint2*>(vp + a.VL.vnorm + (hh * kPT + 4 * q) * 2);
   }
-  if (a.apply_rope) {   // HF's fp32 angle fl(inv_freq_j * pos) of the group's 64 positions
-    for (int e = tid; e < kGroup * 64; e += 512) {
-      const int t = e >> 6, j = e & 63;
-      float sn, cn;
-      sincosf(a.inv_freq[j] * (float)(g * kGroup + t), &sn, &cn);
+  // dec tiled: [h][c_pad32 / 32 steps][8 row tiles][16 rows][32 columns], a
+  // contiguous KB per (step, row tile): lane 16q + n reads row n, columns 8q ..
+  const uint16_t* decb = a.dec + (int64_t)hh * kD * a.c_pad32 + n * 32 + 8 * q;
+  constexpr int tile_stride = 512, step_stride = 4096;
+  half8_t An[8];
+#pragma unroll
+  for (int bt = 0; bt < 8; ++bt) An[bt] = *reinterpret_cast<const half8_t*>(decb + bt * tile_stride);
+  if (tid < 256) {
+    const float l0 = a.codebook[0], l1 = a.codebook[1], l2 = a.codebook[2], l3 = a.codebook[3];
+    half4_t lv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lv[i] = (_Float16)level4(((uint32_t)tid >> (2 * i)) & 3u, l0, l1, l2, l3);
+    s_cbl[tid] = *reinterpret_cast<const uint2*>(&lv);
+  }
+  if (a.apply_rope) {
+    // HF's fp32 angle fl(inv_freq_j * pos) of the group's 64 positions: this
+    // thread has frequency fj at positions p0 + 8k (k < 8).  cos/sin of the exact
+    // product fq * pos from one accurate start and a rotation by 8 fq per step,
+    // then corrected to the fp32 angle: cos(ang) = cos(x - e) with the rounding
+    // error e = fq * pos - fl(fq * pos) (exact by FMA)
+    const int t0 = tid >> 6, p0 = g * kGroup + t0;
+    float ss, cc, s8, c8;
+    sincos_reduced(fq * (float)p0, &ss, &cc);   // fq * p0 rounded: corrected below like the rest
+    {   // the exact product's: rotate forward by the rounding error e0
+      const float a0 = fq * (float)p0, e0 = __builtin_fmaf(fq, (float)p0, -a0);
+      float cx, sx;
+      rotate_back(cc, ss, -e0, &cx, &sx);
+      cc = cx;
+      ss = sx;
+    }
+    sincos_reduced(8.0f * fq, &s8, &c8);   // 8 fq: exact in fp32
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int t = t0 + 8 * k;
+      const float tf = (float)(p0 + 8 * k);
+      const float ang = fq * tf;
+      const float e = __builtin_fmaf(fq, tf, -ang);
+      float cn, sn;
+      rotate_back(cc, ss, e, &cn, &sn);
       cn *= a.rope_scaling;
       sn *= a.rope_scaling;
       if (a.apply_rope == 2) {
         cn = half_bits_to_float(float_to_half_bits(cn));
         sn = half_bits_to_float(float_to_half_bits(sn));
       }
-      s_cs[0][t][j] = cn;
-      s_cs[1][t][j] = sn;
+      s_cs[0][t][fj] = cn;
+      s_cs[1][t][fj] = sn;
+      const float cnx = cc * c8 - ss * s8;
+      ss = ss * c8 + cc * s8;
+      cc = cnx;
     }
   }
-  __syncthreads();   // s_tab
+  if (tid < n_sl) s_tab[tid] = tabv;
+#pragma unroll
+  for (int i = 0; i < kSpPageLoads; ++i)
+    if (tid + 512 * i < n16) reinterpret_cast<uint4*>(kp)[tid + 512 * i] = kpw[i];
+  __syncthreads();   // s_tab, s_cbl, the RoPE table, the key page
 
   // thread tid decodes codes 4 hf .. 4 hf + 3 of slice 4 step + sq, token t
   const int dt = tid >> 3, dsq = (tid >> 1) & 3, dhf = tid & 1;
@@ -204,9 +297,9 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     if (s < n_sl) {
       const uint32_t tab = s_tab[s];
       const int b = (int)(tab >> 24), off = (int)(tab & 0xFFFFFFu), w = sp_width(b);
-      const uint2 sc = *reinterpret_cast<const uint2*>(page + 16 * s + 8 * dhf);
+      const uint2 sc = *reinterpret_cast<const uint2*>(kp + 16 * s + 8 * dhf);
       const int p = off + dt * w;
-      const uint2 cw = *reinterpret_cast<const uint2*>(page + (p & ~7));
+      const uint2 cw = *reinterpret_cast<const uint2*>(kp + (p & ~7));
       const uint64_t word = ((((uint64_t)cw.y << 32) | cw.x) >> (8 * (p & 7))) >> (4 * dhf * w);
       const uint64_t mask = (1ull << w) - 1ull;
       const float bias = (float)(1 << (b - 1));
@@ -219,43 +312,59 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     *reinterpret_cast<half4_t*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) = v;
   };
 
-  const uint16_t* decb = a.dec + ((int64_t)(head_ok ? h : 0) * kD + n) * a.c_pad32 + 8 * q;
-  const int64_t tile_stride = (int64_t)16 * a.c_pad32;
   float4_t acc[8][4];
 #pragma unroll
   for (int bt = 0; bt < 8; ++bt)
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) acc[bt][tt] = (float4_t){0.f, 0.f, 0.f, 0.f};
   const int n_steps = a.c_pad32 / 32;
-  half8_t An[8];
-  if (head_ok) {
-#pragma unroll
-    for (int bt = 0; bt < 8; ++bt) An[bt] = *reinterpret_cast<const half8_t*>(decb + bt * tile_stride);
-  }
+  // Two steps per workgroup barrier: buffers 2p and 2p + 1 hold steps ks and
+  // ks + 1 while the next two are decoded into the other pair; each step's
+  // MFMAs are interleaved with the next pair's decode (VALU and LDS reads).
   decode_b(0, 0);
+  if (n_steps > 1) decode_b(1, 1);
   __syncthreads();
-  for (int ks = 0; ks < n_steps; ++ks) {
-    const int buf = ks & 1;
-    if (ks + 1 < n_steps) decode_b(ks + 1, buf ^ 1);   // that buffer was last read in step ks - 1
+  auto mfma_step = [&](int ks, int buf) {
+    half8_t A[8];
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt) A[bt] = An[bt];
+    const int kn = min(ks + 1, n_steps - 1);   // the last step re-reads its own rows: no branch
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt)
+      An[bt] = *reinterpret_cast<const half8_t*>(decb + bt * tile_stride + step_stride * kn);
+    half8_t B[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) B[tt] = *reinterpret_cast<const half8_t*>(&s_b[buf][16 * tt + n][8 * q]);
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        acc[bt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[bt], B[tt], acc[bt][tt], 0, 0, 0);
+  };
+  for (int ks = 0; ks < n_steps; ks += 2) {
+    const int pb = (ks >> 1) & 1;
     if (head_ok) {
-      half8_t A[8];
+      mfma_step(ks, 2 * pb);
+      if (ks + 2 < n_steps) decode_b(ks + 2, 2 * (pb ^ 1));
 #pragma unroll
-      for (int bt = 0; bt < 8; ++bt) A[bt] = An[bt];
-      if (ks + 1 < n_steps) {
-#pragma unroll
-        for (int bt = 0; bt < 8; ++bt)
-          An[bt] = *reinterpret_cast<const half8_t*>(decb + bt * tile_stride + 32 * (ks + 1));
+      for (int r = 0; r < 16; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // 3 VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // 1 LDS read
       }
-      half8_t B[4];
+      if (ks + 1 < n_steps) mfma_step(ks + 1, 2 * pb + 1);
+      if (ks + 3 < n_steps) decode_b(ks + 3, 2 * (pb ^ 1) + 1);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) B[tt] = *reinterpret_cast<const half8_t*>(&s_b[buf][16 * tt + n][8 * q]);
-#pragma unroll
-      for (int bt = 0; bt < 8; ++bt)
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          acc[bt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[bt], B[tt], acc[bt][tt], 0, 0, 0);
+      for (int r = 0; r < 16; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      }
+    } else {
+      if (ks + 2 < n_steps) decode_b(ks + 2, 2 * (pb ^ 1));
+      if (ks + 3 < n_steps) decode_b(ks + 3, 2 * (pb ^ 1) + 1);
     }
-    lds_barrier();   // buffer buf ^ 1 written, buffer buf read by every wave
+    lds_barrier();   // the next pair decoded, this pair read by every wave
   }
 
   // query fragments (decode form), loaded after the main loop: the MFMA B operand of the scores, lane
@@ -263,16 +372,38 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   half8_t qf[4];
   const bool scoring = a.q != nullptr;
   if (scoring && head_ok) {
+    // the lane's 8 runs of 4 channels (16bb + 4q .. + 3, and + 64), all loads issued first
+    float qv[8][4];
+    const int64_t qrow = ((int64_t)h * a.n_q_groups + (n < a.n_q_groups ? n : 0)) * kD + 4 * q;
+    if (a.q_dtype == BMX_K2B_F32) {
+      float4_t r[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        r[u] = *reinterpret_cast<const float4_t*>(static_cast<const float*>(a.q) + qrow + 16 * (u & 3) + 64 * (u >> 2));
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[u][i] = r[u][i];
+    } else {
+      uint2 r[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        r[u] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.q) + qrow + 16 * (u & 3) + 64 * (u >> 2));
+      const bool bf = a.q_dtype == BMX_K2B_BF16;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t w[4] = {r[u].x & 0xffffu, r[u].x >> 16, r[u].y & 0xffffu, r[u].y >> 16};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[u][i] = bf ? __uint_as_float(w[i] << 16) : half_bits_to_float(w[i]);
+      }
+    }
+    const bool qok = n < a.n_q_groups;
 #pragma unroll
     for (int bb = 0; bb < 4; ++bb)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int c = 16 * bb + 4 * q + i + 64 * e;
-          const float v = n < a.n_q_groups ? sp_load(a.q, ((int64_t)h * a.n_q_groups + n) * kD + c, a.q_dtype) : 0.f;
-          qf[bb][2 * i + e] = (_Float16)v;
-        }
+        for (int e = 0; e < 2; ++e) qf[bb][2 * i + e] = (_Float16)(qok ? qv[bb + 4 * e][i] : 0.f);
   }
   // keys: RoPE of the lane's pairs, channel j = 16bb + 4q + i and j + 64, token
   // 16tt + n; 16 rows staged per token tile.  Each wave stages through its own
@@ -289,12 +420,14 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb) {
         half8_t ka;
+        const float4_t c4 = *reinterpret_cast<const float4_t*>(&s_cs[0][16 * tt + n][16 * bb + 4 * q]);
+        const float4_t s4 = *reinterpret_cast<const float4_t*>(&s_cs[1][16 * tt + n][16 * bb + 4 * q]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int j = 16 * bb + 4 * q + i;
           float k0 = acc[bb][tt][i], k1 = acc[bb + 4][tt][i];
           if (a.apply_rope) {
-            const float cn = s_cs[0][16 * tt + n][j], sn = s_cs[1][16 * tt + n][j];
+            const float cn = c4[i], sn = s4[i];
             const float r0 = __fmul_rn(k0, cn) - __fmul_rn(k1, sn);
             k1 = __fmul_rn(k1, cn) + __fmul_rn(k0, sn);
             k0 = r0;
@@ -363,9 +496,8 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct) {
           const uint32_t byte = ((ct < 4 ? vcd[pg].x : vcd[pg].y) >> (8 * (ct & 3))) & 0xFFu;
-          half4_t vb;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) vb[i] = (_Float16)a.codebook[(byte >> (2 * i)) & 3u];
+          const uint2 lvb = s_cbl[byte];
+          const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
           pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[ct], 0, 0, 0);
         }
       }
@@ -404,6 +536,7 @@ constexpr int kSpMaxWin = 4096;
 
 struct SpMergeKArgs {
   int h_kv, G, n_groups, q_dtype, win_len, out_dtype;
+  int64_t win_sh;   // elements between heads in k_win / v_win
   const float* partials;
   const void* q;
   const uint16_t* k_win;
@@ -456,16 +589,28 @@ __global__ __launch_bounds__(kSpMergeThreads) void spectral_merge_kernel(const S
   __syncthreads();
   const float* pt = a.partials + row * (int64_t)a.n_groups * 130;
   float mx = -INFINITY;
-  for (int t = tid; t < a.win_len; t += kSpMergeThreads) {
-    const uint16_t* kr = a.k_win + ((int64_t)h * a.win_len + t) * kD;
+  // window scores: 8 threads per token, 16 channels each (two 16-byte loads,
+  // issued together), summed across the 8 lanes
+  const int sub = tid & 7;
+  for (int t0 = 0; t0 < a.win_len; t0 += kSpMergeThreads / 8) {
+    const int t = t0 + (tid >> 3);
+    const uint16_t* kr = a.k_win + (int64_t)h * a.win_sh + (int64_t)min(t, a.win_len - 1) * kD + 16 * sub;
+    const uint4 k0 = *reinterpret_cast<const uint4*>(kr), k1 = *reinterpret_cast<const uint4*>(kr + 8);
+    const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
     float acc = 0.f;
-    for (int d = 0; d < kD; d += 2) {
-      const uint32_t kk = *reinterpret_cast<const uint32_t*>(kr + d);
-      acc = fmaf(s_q[d], half_bits_to_float(kk & 0xffffu), acc);
-      acc = fmaf(s_q[d + 1], half_bits_to_float(kk >> 16), acc);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      acc = fmaf(s_q[16 * sub + 2 * i], half_bits_to_float(kw[i] & 0xffffu), acc);
+      acc = fmaf(s_q[16 * sub + 2 * i + 1], half_bits_to_float(kw[i] >> 16), acc);
     }
-    s_s[t] = acc * a.sm_scale;
-    mx = fmaxf(mx, s_s[t]);
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 4);
+    if (t < a.win_len) {
+      const float sc = acc * a.sm_scale;
+      if (sub == 0) s_s[t] = sc;
+      mx = fmaxf(mx, sc);
+    }
   }
   for (int i = tid; i < a.n_groups; i += kSpMergeThreads) mx = fmaxf(mx, pt[(int64_t)i * 130]);
   const float M = block_reduce<true>(mx, s_red);
@@ -484,37 +629,92 @@ __global__ __launch_bounds__(kSpMergeThreads) void spectral_merge_kernel(const S
   float A = 0.f, Aw = 0.f;
 #pragma unroll 8
   for (int i = sl; i < a.n_groups; i += 8) A = fmaf(s_w[i], pt[(int64_t)i * 130 + 2 + c], A);
-  for (int t = sl; t < a.win_len; t += 8)
-    Aw = fmaf(s_s[t], half_bits_to_float(a.v_win[((int64_t)h * a.win_len + t) * kD + c]), Aw);
+  const uint16_t* vw = a.v_win + (int64_t)h * a.win_sh + c;
+  for (int t0 = sl; t0 < a.win_len; t0 += 64) {   // 8 tokens per slice per pass, loads first
+    float vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) vv[u] = half_bits_to_float(vw[(int64_t)min(t0 + 8 * u, a.win_len - 1) * kD]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (t0 + 8 * u < a.win_len) Aw = fmaf(s_s[t0 + 8 * u], vv[u], Aw);
+  }
   s_acc[sl][c] = A;
   s_accw[sl][c] = Aw;
   __syncthreads();
   // the groups' sums are in the rotated value domain: H128 over the channel
-  // index, then the signs and 1/128 (the value codec's inverse)
+  // index (bits 0..5 within a wave by lane exchange, bit 6 across the two
+  // waves through LDS), then the signs and 1/128 (the value codec's inverse)
+  float x = 0.f;
   if (tid < kD) {
-    float x = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) x += s_acc[j][c];
-    s_h[c] = x;
-  }
-  for (int hb = 1; hb < kD; hb <<= 1) {
-    __syncthreads();
-    float x = 0.f, o = 0.f;
-    if (tid < kD) {
-      x = s_h[c];
-      o = s_h[c ^ hb];
+#pragma unroll
+    for (int hb = 1; hb < 64; hb <<= 1) {
+      const float o = __shfl_xor(x, hb);
+      x = (c & hb) ? o - x : x + o;
     }
-    __syncthreads();
-    if (tid < kD) s_h[c] = (c & hb) ? o - x : x + o;
+    s_h[c] = x;
   }
   __syncthreads();
   if (tid < kD) {
+    const float o = s_h[c ^ 64];
+    x = (c & 64) ? o - x : x + o;
     float w = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) w += s_accw[j][c];
-    const float v = s_h[c] / (float)kD;
+    const float v = x / (float)kD;
     store_elem(a.out, row * kD + c, ((sign_neg(a.v_sign_bits, c) ? -v : v) + w) / L, a.out_dtype);
   }
+}
+
+// First stage of the merge for many groups: grid (n_runs, G, h_kv), block 256
+// (2 slices x 128 channels).  Workgroup r folds the partials of groups
+// [64 r, 64 r + 64) of one (head, query) into one partial of the same form
+// (m = their max, l and the channel sums weighted by e^(m_i - m)), written to
+// run r of the scratch rows; the per-query kernel above then merges the runs.
+constexpr int kSpRun = 64;
+constexpr int kSpMaxRuns = kSpMergeMaxGroups / kSpRun;
+
+struct SpFoldKArgs {
+  int G, n_groups, n_runs;
+  const float* partials;
+  float* runs;   // [h_kv][G][n_runs][130]
+};
+
+__global__ __launch_bounds__(256) void spectral_fold_kernel(const SpFoldKArgs a) {
+  const int r = blockIdx.x, g = blockIdx.y, h = blockIdx.z, tid = threadIdx.x, c = tid & 127, sl = tid >> 7;
+  __shared__ float s_w[kSpRun];
+  __shared__ float s_ml[2];
+  __shared__ float s_acc[kD];
+  const int64_t row = (int64_t)h * a.G + g;
+  const float* pt = a.partials + (row * a.n_groups + (int64_t)r * kSpRun) * 130;
+  const int n = min(kSpRun, a.n_groups - r * kSpRun);
+  // the run's channel sums, every load issued before any is used
+  float v[kSpRun / 2];
+#pragma unroll
+  for (int k = 0; k < kSpRun / 2; ++k) v[k] = pt[(int64_t)min(2 * k + sl, n - 1) * 130 + 2 + c];
+  if (tid < 64) {   // one wave: the weights and the run's (m, l)
+    const float m = tid < n ? pt[(int64_t)tid * 130] : -INFINITY;
+    const float l = tid < n ? pt[(int64_t)tid * 130 + 1] : 0.f;
+    float M = m;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    const float w = tid < n ? __expf(m - M) : 0.f;
+    float L = w * l;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
+    s_w[tid] = w;
+    if (tid == 0) { s_ml[0] = M; s_ml[1] = L; }
+  }
+  __syncthreads();
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < kSpRun / 2; ++k) acc = fmaf(s_w[2 * k + sl], v[k], acc);   // weight 0 past n
+  if (sl == 1) s_acc[c] = acc;
+  __syncthreads();
+  float* dst = a.runs + (row * a.n_runs + r) * 130;
+  if (sl == 0) dst[2 + c] = acc + s_acc[c];
+  if (tid < 2) dst[tid] = s_ml[tid];
 }
 
 static PageLayout value_layout(int h_kv) {
@@ -600,6 +800,7 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   if (a->apply_rope < 0 || a->apply_rope > 2) return sp_fail(fn, "apply_rope must be 0, 1 or 2");
   if (!dtype_ok(a->out_dtype)) return sp_fail(fn, "out_dtype must be BMX_K2B_F16, _F32 or _BF16");
   if (a->out_rows != 0 && a->out_rows < a->n_tokens) return sp_fail(fn, "out_rows must be 0 or >= n_tokens");
+  if (a->L.k_page_bytes > kSpMaxKPage) return sp_fail(fn, "k_page_bytes above 73728 (the LDS-staged page)");
   if (!a->k_pages || !a->k_page_table || !a->v_pages || !a->v_page_table || !a->dec_perm ||
       (!a->v_out && !a->partials) || (!a->k_out && !a->q) || a->n_k_pool < 1 || a->n_v_pool < 1)
     return sp_fail(fn, "null pointer argument or empty pool");
@@ -620,7 +821,8 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   k.k_out = a->k_out; k.v_out = a->v_out;
   k.q = a->q; k.q_dtype = a->q_dtype; k.n_q_groups = a->n_q_groups; k.scores = a->scores;
   k.partials = a->partials; k.sm_scale = a->sm_scale;
-  hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512), 0, (hipStream_t)stream, k);
+  hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512),
+                     sp_dyn_bytes(a->L.k_page_bytes), (hipStream_t)stream, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     bmx_set_error(std::string(fn) + ": launch: " + hipGetErrorString(e));
@@ -640,10 +842,23 @@ extern "C" int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* st
   if (!dtype_ok(a->q_dtype) || !dtype_ok(a->out_dtype)) return sp_fail(fn, "q_dtype / out_dtype");
   if (!a->q || !a->out || (a->n_groups && !a->partials) || (a->win_len && (!a->k_win || !a->v_win)))
     return sp_fail(fn, "null pointer argument");
+  if (a->win_len && (((uintptr_t)a->k_win & 15) != 0 || a->win_stride_h % 8 != 0 ||
+                     (a->win_stride_h != 0 && a->win_stride_h < (int64_t)a->win_len * kD)))
+    return sp_fail(fn, "k_win must be 16-byte aligned and win_stride_h 0 or a multiple of 8 >= 128 win_len");
   SpMergeKArgs k{};
   k.h_kv = a->h_kv; k.G = a->n_q_groups; k.n_groups = a->n_groups; k.q_dtype = a->q_dtype;
   k.win_len = a->win_len; k.out_dtype = a->out_dtype; k.partials = a->partials; k.q = a->q;
+  if (a->scratch && a->n_groups > 2 * kSpRun) {   // fold runs of 64 groups first, on many CUs
+    SpFoldKArgs f{};
+    f.G = a->n_q_groups; f.n_groups = a->n_groups; f.n_runs = (a->n_groups + kSpRun - 1) / kSpRun;
+    f.partials = a->partials; f.runs = a->scratch;
+    hipLaunchKernelGGL(spectral_fold_kernel, dim3(f.n_runs, a->n_q_groups, a->h_kv), dim3(256), 0,
+                       (hipStream_t)stream, f);
+    k.partials = a->scratch;
+    k.n_groups = f.n_runs;
+  }
   k.k_win = a->k_win; k.v_win = a->v_win; k.sm_scale = a->sm_scale; k.out = a->out;
+  k.win_sh = a->win_stride_h ? a->win_stride_h : (int64_t)a->win_len * kD;
   for (int i = 0; i < 4; ++i) k.v_sign_bits[i] = a->v_sign_bits[i];
   hipLaunchKernelGGL(spectral_merge_kernel, dim3(a->n_q_groups, a->h_kv), dim3(kSpMergeThreads), 0,
                      (hipStream_t)stream, k);

@@ -160,7 +160,10 @@ class DevicePack:
         decp = torch.zeros(C, self.c_pad32, dtype=torch.float32)
         decp[:, : self.c_pad][:, keep] = pack.dec.float().cpu()[:, self.perm[keep]]
         self.enc_perm = encp.to(device).contiguous()
-        self.dec_perm = decp.half().to(device).contiguous()
+        # tiled for the dequant kernel: [h][c_pad32 / 32][8][16][32], one contiguous
+        # (16 rows x 32 columns) tile per (head, 32-column step, 16-row tile)
+        self.dec_perm = (decp.half().view(h_kv, 8, 16, self.c_pad32 // 32, 32).permute(0, 3, 1, 2, 4)
+                         .contiguous().to(device))
         self.bpe = payload_bpe(bits, pack.group)
 
     def layout(self) -> _lib.SpectralLayout:
@@ -302,9 +305,10 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
                 dtype=torch.float16, q=q, partials=pt, sm_scale=sm_scale)
     T = 0 if k_win is None else k_win.shape[1]
     if T:
-        _need(k_win.dtype == torch.float16 and v_win.dtype == torch.float16 and k_win.is_contiguous()
-              and v_win.is_contiguous() and tuple(k_win.shape) == (h, T, d) and v_win.shape == k_win.shape,
-              "window keys and values: contiguous fp16 (h_kv, T, 128)")
+        _need(k_win.dtype == torch.float16 and v_win.dtype == torch.float16 and tuple(k_win.shape) == (h, T, d)
+              and v_win.shape == k_win.shape and k_win.stride() == v_win.stride() and k_win.stride(2) == 1
+              and k_win.stride(1) == d and k_win.stride(0) % 8 == 0 and k_win.data_ptr() % 16 == 0,
+              "window keys and values: fp16 (h_kv, T, 128) with contiguous rows, 16-byte aligned")
     out_dtype = q.dtype if out_dtype is None else out_dtype
     _need(out_dtype in _V_DTYPES, "out_dtype must be fp16, bf16 or fp32")
     out = torch.empty(h, G, d, dtype=out_dtype, device=q.device)
@@ -312,7 +316,11 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
     a.h_kv, a.n_q_groups, a.n_groups = h, G, n_tokens // GROUP
     a.partials, a.q, a.q_dtype = _ptr(pt), _ptr(q), _V_DTYPES[q.dtype]
     a.k_win, a.v_win, a.win_len = (_ptr(k_win), _ptr(v_win), T) if T else (None, None, 0)
+    a.win_stride_h = k_win.stride(0) if T else 0
     a.sm_scale, a.out, a.out_dtype = float(sm_scale), _ptr(out), _V_DTYPES[out_dtype]
     a.v_sign_bits[:] = consts.sign_bits
+    n_runs = -(-(n_tokens // GROUP) // 64)
+    scratch = torch.empty(h, G, n_runs, 130, dtype=torch.float32, device=q.device) if n_runs else None
+    a.scratch = _ptr(scratch)
     _lib.check(_lib.lib().bmx_spectral_merge(ct.byref(a), _stream(q.device)), "bmx_spectral_merge")
     return out

@@ -85,8 +85,11 @@ typedef struct bmx_spectral_dequant_args {
   const uint8_t* v_pages;
   const int32_t* v_page_table; /* n_tokens / 16 value page ids */
   int32_t n_v_pool;
-  const uint16_t* dec_perm;    /* device fp16 [h_kv][128][c_pad rounded up to 32]: dec's
-                                  rows of each head, columns in page order, zero padding */
+  const uint16_t* dec_perm;    /* device fp16 dec, rows of each head, columns in page order
+                                  with zero padding to c_pad32 = c_pad rounded up to 32,
+                                  tiled [h_kv][c_pad32 / 32][8][16][32]: element (row
+                                  16 i + r, column 32 k + c) of head h at
+                                  (((h c_pad32 / 32 + k) 8 + i) 16 + r) 32 + c */
   int32_t apply_rope;          /* 0 none, 1 fp32 cos/sin, 2 cos/sin rounded to fp16 */
   float rope_scaling;
   float inv_freq[64];
@@ -132,13 +135,18 @@ typedef struct bmx_spectral_merge_args {
   const float* partials;       /* [h_kv][n_q_groups][n_groups][130] fp32 */
   const void* q;               /* [h_kv][n_q_groups][128] post-RoPE, dtype q_dtype */
   int32_t q_dtype;
-  const uint16_t* k_win;       /* fp16 [h_kv][win_len][128] post-RoPE window keys */
-  const uint16_t* v_win;       /* fp16 [h_kv][win_len][128] window values */
+  const uint16_t* k_win;       /* fp16 post-RoPE window keys, row t of head h at h win_stride_h + 128 t,
+                                  16-byte aligned */
+  const uint16_t* v_win;       /* fp16 window values, same indexing */
   int32_t win_len;             /* 0..4096 */
   float sm_scale;
   void* out;                   /* [h_kv][n_q_groups][128], dtype out_dtype */
   int32_t out_dtype;
   uint32_t v_sign_bits[4];     /* the value codec's Hadamard signs (the partials are rotated) */
+  float* scratch;              /* NULL, or device [h_kv][n_q_groups][ceil(n_groups / 64)][130] fp32:
+                                  above 128 groups the partials are first folded in runs of 64
+                                  groups there, on many workgroups, then merged */
+  int64_t win_stride_h;        /* elements between heads in k_win / v_win (0: 128 win_len) */
 } bmx_spectral_merge_args;
 
 int64_t bmx_spectral_v_page_bytes(int32_t h_kv);

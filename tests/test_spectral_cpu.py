@@ -103,9 +103,12 @@ def test_host_layout_matches_oracle(h_kv, budget):
     np.testing.assert_array_equal(dp.slice_tab.numpy(), L.slice_table())
     np.testing.assert_array_equal(dp.perm.numpy(), L.perm)
     np.testing.assert_array_equal(dp.enc_perm.numpy(), L.permute_cols(pack.enc.numpy()))
-    assert dp.dec_perm.shape == (128 * h_kv, -(-L.c_pad // 32) * 32)
-    np.testing.assert_array_equal(dp.dec_perm[:, : L.c_pad].numpy(),
+    c32 = -(-L.c_pad // 32) * 32
+    assert dp.dec_perm.shape == (h_kv, c32 // 32, 8, 16, 32)
+    rows = dp.dec_perm.permute(0, 2, 3, 1, 4).reshape(128 * h_kv, c32)   # untile
+    np.testing.assert_array_equal(rows[:, : L.c_pad].numpy(),
                                   L.permute_cols(pack.dec.numpy()).astype(np.float16))
+    assert not rows[:, L.c_pad:].any()
     assert dp.v_page_bytes == 544 * h_kv
 
 
