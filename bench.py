@@ -719,14 +719,15 @@ def run_spectral(args, torch, dev) -> dict:
 
     reps = max(args.steps, 1)
     call_us = timed(lambda: lay.attend(q, scale), reps)
-    Pb = torch.empty(H_KV, G, P // 64, 130, dtype=torch.float32, device=dev)
+    n_parts = spectral.partial_count(dp, P, qg, k2b.ROPE_FP16_TABLES)
+    Pb = torch.empty(H_KV, G, n_parts, 130, dtype=torch.float32, device=dev)
     deq_us = timed(lambda: spectral.dequant(dp, lay._kpool, kt, lay._pool, vt, P, lay._consts,
                                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=torch.float16,
                                             q=qg, partials=Pb, sm_scale=scale), reps)
     c_used = pack.c_used
     flops = 2.0 * P * c_used * C                            # Y_hat dec^T over the coded directions
     page_bytes = P // 64 * dp.k_page_bytes + P // 16 * dp.v_page_bytes
-    out_bytes = H_KV * G * (P // 64) * 130 * 4        # the groups' softmax partials
+    out_bytes = H_KV * G * n_parts * 130 * 4          # the blocks' softmax partials
     comp = {} if args.no_fp16_comparator else fp16_comparator(args, torch, dev, N, call_us)
     # CPU: the oracle's restatement of the reference's chunked spectral step on
     # a bounded sample (dequant of the sample's keys and values, RoPE, one
@@ -782,7 +783,9 @@ def run_spectral(args, torch, dev) -> dict:
                                 f"payload bpe keys)"),
                    "ctx": N, "packed_tokens": P, "budget": args.spectral_budget, "c_used": c_used,
                    "c_pad": dp.c_pad, "key_page_bytes": dp.k_page_bytes},
-        "roofline": {"bound": "mfma", "kernel": "spectral_dequant_kernel, partial form (pages -> per-group softmax partials)",
+        "roofline": {"bound": "mfma", "kernel": (("spectral_partial128_kernel (pages -> per-128-token-block softmax partials)"
+                                                if n_parts == P // 128 else
+                                                "spectral_dequant_kernel, partial form (pages -> per-group softmax partials)")),
                      "achieved": round(flops / (deq_us * 1e-6) / 1e12, 1), "peak": MFMA_FP16_DENSE_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (deq_us * 1e-6) / 1e12 / MFMA_FP16_DENSE_TFLOPS, 4),
                      "traffic": measured_traffic({"ctx": N, "window": args.window, "budget": args.spectral_budget,

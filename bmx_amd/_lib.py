@@ -261,6 +261,7 @@ EXPORTS = {
     "bmx_spectral_append": (ct.c_int32, [ct.POINTER(SpectralAppendArgs), ct.c_void_p]),
     "bmx_spectral_dequant": (ct.c_int32, [ct.POINTER(SpectralDequantArgs), ct.c_void_p]),
     "bmx_spectral_merge": (ct.c_int32, [ct.POINTER(SpectralMergeArgs), ct.c_void_p]),
+    "bmx_spectral_partial_count": (ct.c_int32, [ct.POINTER(SpectralDequantArgs)]),
 }
 
 _LIB = None

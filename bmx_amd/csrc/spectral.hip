@@ -6,6 +6,8 @@
 // include/bmx_spectral.h.  Built without floating-point contraction: every
 // product and sum of the write kernel is rounded on its own, in a fixed order.
 
+#include <type_traits>
+
 #include "bmx_spectral.h"
 #include "k2b_common.h"
 
@@ -156,7 +158,7 @@ struct SpDequantKArgs {
   float sm_scale;
 };
 
-constexpr int kSpBRow = 40;   // halves per token row of the staged Y_hat tile (32 + 8 pad)
+constexpr int kSpBRow = 40;   // halves per token row of the staged code tile (32 + 8 pad)
 constexpr int kSpMaxKPage = 72 * 1024;   // key page bytes staged in LDS at most (c_pad 1072, 8 bits: 70768)
 constexpr int kSpPageLoads = kSpMaxKPage / (16 * 512);   // 16-byte loads per thread at most
 // dynamic LDS of the dequant kernel: the group's key page while the main loop
@@ -182,15 +184,70 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The MFMA operands of Y_hat dec^T.  Below tier kSpWideTier the B side holds
+// fp16(code * step) (exact for 2-bit codes, one rounding for 3 and 4 bits);
+// from it on, where the codes are wide and the directions the ones of
+// largest variance, the B side holds the code itself (exact) and the A side
+// the dec rows times the step (one rounding of an exact product), so that no
+// wide product is rounded: in fp16 that rounding of the leading directions
+// was the largest error of the keys.  Tiers ascend in the page, so the narrow
+// slices lead; the steps made of them alone skip the A-side products.
+constexpr uint32_t kSpWideTier = 5;
+// Codes 0 .. 255 of width w from the low bits of word, 4 of them as fp16
+// (1024 + c, from the bits, minus 1024 + 2^(b-1)).
+__device__ __forceinline__ uint2 sp_codes4(uint64_t word, int w, int b) {
+  const uint32_t mask = (1u << w) - 1u;
+  uint32_t c[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) c[e] = ((uint32_t)(word >> (e * w)) & mask) | 0x6400u;
+  const _Float16 off = (_Float16)(float)(1024 + (1 << (b - 1)));
+  const half2_t o2 = {off, off};
+  return make_uint2(as_u32(as_h2(c[0] | (c[1] << 16)) - o2), as_u32(as_h2(c[2] | (c[3] << 16)) - o2));
+}
+
+__device__ __forceinline__ uint32_t sp_hmul2(uint32_t x, uint32_t y) { return as_u32(as_h2(x) * as_h2(y)); }
+
+constexpr uint32_t kHalfOnes = 0x3C003C00u;   // fp16 (1, 1)
+
+// The B-side factor of slice s's 8 columns (the fp16 steps of a narrow tier,
+// else 1) and the A-side one (1 for a narrow tier, else the steps; 0 past the
+// last slice, whose codes are stored as 0 too), from the key page in LDS.
+__device__ __forceinline__ uint4 sp_b_factor(const uint8_t* kp, int s_clamped, int b) {
+  const uint4 r = *reinterpret_cast<const uint4*>(kp + 16 * s_clamped);
+  return (uint32_t)b < kSpWideTier ? r : make_uint4(kHalfOnes, kHalfOnes, kHalfOnes, kHalfOnes);
+}
+
+__device__ __forceinline__ half8_t sp_a_factor(const uint8_t* kp, const uint32_t* s_tab, int s, int n_sl) {
+  const int sc = min(s, n_sl - 1);
+  const uint4 r = *reinterpret_cast<const uint4*>(kp + 16 * sc);
+  const bool narrow = (s_tab[sc] >> 24) < kSpWideTier, ok = s < n_sl;
+  const uint32_t f[4] = {r.x, r.y, r.z, r.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = ok ? (narrow ? kHalfOnes : f[i]) : 0u;
+  return __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+// Leading 32-column steps made of narrow slices only (their A side is the dec
+// rows as they are).  tabv: this thread's slice_tab entry (slice min(tid,
+// n_sl - 1)); every thread of the block calls this, in place of a barrier.
+__device__ __forceinline__ int sp_narrow_steps(uint32_t tabv, int tid, int n_sl, int n_steps) {
+  const int nn = __syncthreads_count(tid < n_sl && (tabv >> 24) < kSpWideTier);
+  // the count is the narrow prefix only if no wide slice comes before slice nn
+  const int out_of_order = __syncthreads_count(tid < nn && (tabv >> 24) >= kSpWideTier);
+  if (out_of_order) return 0;
+  return nn == n_sl ? n_steps : nn >> 2;
+}
+
 // grid (n_tokens / 64), block 512: one 64-token group, wave w = head w.  The
 // group's key page is copied to LDS first (one round trip for the whole page,
 // issued with every other load of the prologue).  Per 32-column step the
-// group's Y_hat^T tile (code times step, fp16) is decoded from there
+// group's code tile (exact fp16 integers) is decoded from there
 // once, by all 512 threads (4 codes each), into one of two LDS buffers; every
 // head's wave reads its B fragments from there (lane 16q + n: token n of the
-// tile, columns 8q .. 8q + 7) and multiplies with its dec rows (A, lane 16q + n:
-// row n of the tile, columns 8q ..; loaded a step ahead), 8 row tiles x 4 token
-// tiles in fp32.  The group's RoPE table is made once for all heads.  Then each
+// tile, columns 8q .. 8q + 7) and multiplies with its dec rows times the
+// columns' steps (A, lane 16q + n: row n of the tile, columns 8q ..; rows
+// loaded a step ahead), 8 row tiles x 4 token tiles in fp32.  The group's RoPE table is made once for all heads.  Then each
 // wave rotates its pairs (channels j, j + 64 in row tiles bb, bb + 4), stages
 // 16 rows at a time in LDS and writes them coalesced, and dequantizes its
 // head's 4 value pages.
@@ -287,29 +344,26 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 #pragma unroll
   for (int i = 0; i < kSpPageLoads; ++i)
     if (tid + 512 * i < n16) reinterpret_cast<uint4*>(kp)[tid + 512 * i] = kpw[i];
-  __syncthreads();   // s_tab, s_cbl, the RoPE table, the key page
+  const int n_steps = a.c_pad32 / 32;
+  // a barrier: s_tab, s_cbl, the RoPE table, the key page
+  const int n_narrow = sp_narrow_steps(tabv, tid, n_sl, n_steps);
 
   // thread tid decodes codes 4 hf .. 4 hf + 3 of slice 4 step + sq, token t
   const int dt = tid >> 3, dsq = (tid >> 1) & 3, dhf = tid & 1;
   auto decode_b = [&](int ks, int buf) {
-    const int s = 4 * ks + dsq;
-    half4_t v = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
-    if (s < n_sl) {
-      const uint32_t tab = s_tab[s];
-      const int b = (int)(tab >> 24), off = (int)(tab & 0xFFFFFFu), w = sp_width(b);
-      const uint2 sc = *reinterpret_cast<const uint2*>(kp + 16 * s + 8 * dhf);
-      const int p = off + dt * w;
-      const uint2 cw = *reinterpret_cast<const uint2*>(kp + (p & ~7));
-      const uint64_t word = ((((uint64_t)cw.y << 32) | cw.x) >> (8 * (p & 7))) >> (4 * dhf * w);
-      const uint64_t mask = (1ull << w) - 1ull;
-      const float bias = (float)(1 << (b - 1));
-      const float scl[4] = {half_bits_to_float(sc.x & 0xffffu), half_bits_to_float(sc.x >> 16),
-                            half_bits_to_float(sc.y & 0xffffu), half_bits_to_float(sc.y >> 16)};
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[e] = (_Float16)(((float)(uint32_t)((word >> (e * w)) & mask) - bias) * scl[e]);
-    }
-    *reinterpret_cast<half4_t*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) = v;
+    // no branch: slices past the last decode the last slice and store zeros
+    const int s = 4 * ks + dsq, sc = min(s, n_sl - 1);
+    const uint32_t tab = s_tab[sc];
+    const int b = (int)(tab >> 24), off = (int)(tab & 0xFFFFFFu), w = sp_width(b);
+    const int p = off + dt * w;
+    const uint2 cw = *reinterpret_cast<const uint2*>(kp + (p & ~7));
+    const uint4 f = sp_b_factor(kp, sc, b);
+    const uint64_t word = ((((uint64_t)cw.y << 32) | cw.x) >> (8 * (p & 7))) >> (4 * dhf * w);
+    const uint2 c = sp_codes4(word, w, b);
+    const bool ok = s < n_sl;
+    const uint32_t f0 = dhf ? f.z : f.x, f1 = dhf ? f.w : f.y;
+    *reinterpret_cast<uint2*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) =
+        make_uint2(ok ? sp_hmul2(c.x, f0) : 0u, ok ? sp_hmul2(c.y, f1) : 0u);
   };
 
   float4_t acc[8][4];
@@ -317,17 +371,24 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   for (int bt = 0; bt < 8; ++bt)
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) acc[bt][tt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  const int n_steps = a.c_pad32 / 32;
   // Two steps per workgroup barrier: buffers 2p and 2p + 1 hold steps ks and
   // ks + 1 while the next two are decoded into the other pair; each step's
   // MFMAs are interleaved with the next pair's decode (VALU and LDS reads).
   decode_b(0, 0);
-  if (n_steps > 1) decode_b(1, 1);
+  decode_b(1, 1);
   __syncthreads();
-  auto mfma_step = [&](int ks, int buf) {
+  auto mfma_step = [&](int ks, int buf, auto wide) {
+    // A = the dec rows, times the group's steps of the lane's 8 columns in a
+    // step with wider tiers
     half8_t A[8];
+    if constexpr (decltype(wide)::value) {
+      const half8_t f = sp_a_factor(kp, s_tab, 4 * ks + q, n_sl);
 #pragma unroll
-    for (int bt = 0; bt < 8; ++bt) A[bt] = An[bt];
+      for (int bt = 0; bt < 8; ++bt) A[bt] = An[bt] * f;
+    } else {
+#pragma unroll
+      for (int bt = 0; bt < 8; ++bt) A[bt] = An[bt];
+    }
     const int kn = min(ks + 1, n_steps - 1);   // the last step re-reads its own rows: no branch
 #pragma unroll
     for (int bt = 0; bt < 8; ++bt)
@@ -341,31 +402,28 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
       for (int tt = 0; tt < 4; ++tt)
         acc[bt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[bt], B[tt], acc[bt][tt], 0, 0, 0);
   };
-  for (int ks = 0; ks < n_steps; ks += 2) {
-    const int pb = (ks >> 1) & 1;
+  // whole pairs of steps in one basic block each (decodes past the last step
+  // store zeros into buffers nobody reads), then an odd last step; the
+  // compiler's own interleave measured faster than a fixed MFMA/VALU/LDS
+  // pattern
+  const int n_pairs = n_steps >> 1, n_narrow_pairs = n_narrow >> 1;
+  auto pair = [&](int kq, auto wide) {
+    const int ks = 2 * kq, pb = kq & 1;
     if (head_ok) {
-      mfma_step(ks, 2 * pb);
-      if (ks + 2 < n_steps) decode_b(ks + 2, 2 * (pb ^ 1));
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // 3 VALU
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // 1 LDS read
-      }
-      if (ks + 1 < n_steps) mfma_step(ks + 1, 2 * pb + 1);
-      if (ks + 3 < n_steps) decode_b(ks + 3, 2 * (pb ^ 1) + 1);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-      }
+      mfma_step(ks, 2 * pb, wide);
+      decode_b(ks + 2, 2 * (pb ^ 1));
+      mfma_step(ks + 1, 2 * pb + 1, wide);
+      decode_b(ks + 3, 2 * (pb ^ 1) + 1);
     } else {
-      if (ks + 2 < n_steps) decode_b(ks + 2, 2 * (pb ^ 1));
-      if (ks + 3 < n_steps) decode_b(ks + 3, 2 * (pb ^ 1) + 1);
+      decode_b(ks + 2, 2 * (pb ^ 1));
+      decode_b(ks + 3, 2 * (pb ^ 1) + 1);
     }
     lds_barrier();   // the next pair decoded, this pair read by every wave
-  }
+  };
+  int kq = 0;
+  for (; kq < n_narrow_pairs; ++kq) pair(kq, std::false_type{});
+  for (; kq < n_pairs; ++kq) pair(kq, std::true_type{});
+  if ((n_steps & 1) && head_ok) mfma_step(n_steps - 1, 2 * (n_pairs & 1), std::true_type{});
 
   // query fragments (decode form), loaded after the main loop: the MFMA B operand of the scores, lane
   // 16q + n: query n, K index 8q + 2i + e = channel 16bb + 4q + i + 64e
@@ -528,6 +586,338 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
       wave_lds_order();
       dq_store_tile(tl, a.v_out, row_h + 16 * pg, a.out_dtype);
       wave_lds_order();
+    }
+  }
+}
+
+// Partial form over 128-token blocks (two key pages), four heads per
+// workgroup: grid (n_tokens / 128, ceil(h_kv / 4)), block 512.  Wave w serves
+// head 4 blockIdx.y + (w >> 1) and half r = w & 1 of its rows: row tiles 2r,
+// 2r + 1 and their RoPE partners 2r + 4, 2r + 5 (channels 32r .. 32r + 31 and
+// + 64), times the block's 8 token tiles.  Against the 64-token form, each
+// dec row read from L2 feeds twice the MFMAs (the main loop's second cost
+// after the MFMAs); the block's code tile is decoded once for 4 heads
+// instead of 8.  Each token tile takes the A operand of its page (the dec
+// rows times that page's steps).  The two halves of a head add their partial
+// scores through LDS, then each takes 4 of the head's 8 rotated value-channel
+// blocks.  The
+// RoPE table is the fp16-rounded one (apply_rope 2), kept as fp16 pairs.
+constexpr int kSpBlk = 128;
+constexpr int kSpBlkMaxPages = 56 * 1024;   // two key pages staged in LDS at most
+
+__global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequantKArgs a, int kpb) {
+  const int blk = blockIdx.x, hq = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
+  const int hl = wave >> 1, r2 = wave & 1;
+  const int h = 4 * hq + hl;
+  const bool head_ok = h < a.h_kv;
+  const int hh = head_ok ? h : 0;
+  __shared__ uint32_t s_tab[kSpMaxSlices];
+  __shared__ __align__(16) _Float16 s_b[4][kSpBlk][kSpBRow];
+  __shared__ __align__(16) uint32_t s_cs[kSpBlk][kCsPad];   // (cos, sin) fp16 of (position, frequency)
+  __shared__ uint2 s_cbl[256];
+  __shared__ uint2 s_vcd[4][8][64];   // (local head, value page, lane)
+  __shared__ uint2 s_nrm[4][8][4];    // (local head, value page, quarter)
+  extern __shared__ __align__(16) uint8_t sp_dyn[];   // the two key pages; after the loop, the score exchange
+  const int n_sl = a.c_pad >> 3;
+  const int fj = tid & 63;
+  const float fq = a.inv_freq[fj];
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- every global load first: the two key pages (kpb bytes apart in LDS),
+  // the slice table, the value codes and norms of the 8 value pages, dec rows
+  const int n16 = kpb >> 4;            // 16-byte chunks per page in LDS
+  const int p16 = a.k_page_bytes >> 4; // 16-byte chunks per page read
+  const uint8_t* pg0 = a.k_pages + clamp_page(a.k_table[2 * blk], a.n_k_pool) * (int64_t)a.k_page_bytes;
+  const uint8_t* pg1 = a.k_pages + clamp_page(a.k_table[2 * blk + 1], a.n_k_pool) * (int64_t)a.k_page_bytes;
+  constexpr int kLoads = (kSpBlkMaxPages / 2 + 16 * 512 - 1) / (16 * 512);   // per page per thread
+  uint4 kw0[kLoads], kw1[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int c = min(tid + 512 * i, p16 - 1);
+    kw0[i] = reinterpret_cast<const uint4*>(pg0)[c];
+    kw1[i] = reinterpret_cast<const uint4*>(pg1)[c];
+  }
+  const uint32_t tabv = (uint32_t)a.slice_tab[min(tid, n_sl - 1)];
+  // value pages: thread (local head tid >> 7, page (tid >> 6) & 1 + 2 k, lane)
+  uint2 vcw[4], nrw[4];
+  const int vh = min(4 * hq + (tid >> 7), a.h_kv - 1), vl = tid & 63;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int vp_i = ((tid >> 6) & 1) + 2 * k;
+    const uint8_t* vp = a.v_pages + clamp_page(a.v_table[8 * blk + vp_i], a.n_v_pool) * (int64_t)a.VL.bytes;
+    vcw[k] = *reinterpret_cast<const uint2*>(vp + a.VL.vcode + vh * 512 + vl * 8);
+    nrw[k] = *reinterpret_cast<const uint2*>(vp + a.VL.vnorm + (vh * kPT + 4 * (vl >> 4)) * 2);
+  }
+  // dec rows of this wave's 4 row tiles: rt(i) = 2 r2 + (i & 1) + 4 (i >> 1)
+  const uint16_t* decb = a.dec + (int64_t)hh * kD * a.c_pad32 + n * 32 + 8 * q;
+  constexpr int tile_stride = 512, step_stride = 4096;
+  auto rt = [&](int i) { return 2 * r2 + (i & 1) + 4 * (i >> 1); };
+  half8_t An[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) An[i] = *reinterpret_cast<const half8_t*>(decb + rt(i) * tile_stride);
+  if (tid < 256) {
+    const float l0 = a.codebook[0], l1 = a.codebook[1], l2 = a.codebook[2], l3 = a.codebook[3];
+    half4_t lv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lv[i] = (_Float16)level4(((uint32_t)tid >> (2 * i)) & 3u, l0, l1, l2, l3);
+    s_cbl[tid] = *reinterpret_cast<const uint2*>(&lv);
+  }
+  {   // RoPE table, fp16 (cos, sin): frequency fj at positions p0 + 8k, k < 16
+    const int t0 = tid >> 6, p0 = blk * kSpBlk + t0;
+    float ss, cc, s8, c8;
+    sincos_reduced(fq * (float)p0, &ss, &cc);
+    {
+      const float a0 = fq * (float)p0, e0 = __builtin_fmaf(fq, (float)p0, -a0);
+      float cx, sx;
+      rotate_back(cc, ss, -e0, &cx, &sx);
+      cc = cx;
+      ss = sx;
+    }
+    sincos_reduced(8.0f * fq, &s8, &c8);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int t = t0 + 8 * k;
+      const float tf = (float)(p0 + 8 * k);
+      const float ang = fq * tf;
+      const float e = __builtin_fmaf(fq, tf, -ang);
+      float cn, sn;
+      rotate_back(cc, ss, e, &cn, &sn);
+      const half2_t cs = {(_Float16)(cn * a.rope_scaling), (_Float16)(sn * a.rope_scaling)};
+      s_cs[t][fj] = as_u32(cs);
+      const float cnx = cc * c8 - ss * s8;
+      ss = ss * c8 + cc * s8;
+      cc = cnx;
+    }
+  }
+  if (tid < n_sl) s_tab[tid] = tabv;
+  uint8_t* kp0 = sp_dyn;
+  uint8_t* kp1 = sp_dyn + kpb;
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i)
+    if (tid + 512 * i < n16) {
+      reinterpret_cast<uint4*>(kp0)[tid + 512 * i] = kw0[i];
+      reinterpret_cast<uint4*>(kp1)[tid + 512 * i] = kw1[i];
+    }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int vp_i = ((tid >> 6) & 1) + 2 * k;
+    s_vcd[tid >> 7][vp_i][vl] = vcw[k];
+    if ((vl & 15) == 0) s_nrm[tid >> 7][vp_i][vl >> 4] = nrw[k];
+  }
+  const int n_steps = a.c_pad32 / 32;
+  // a barrier: s_tab, s_cbl, s_cs, the key pages, the value codes
+  const int n_narrow = sp_narrow_steps(tabv, tid, n_sl, n_steps);
+
+  // thread tid decodes the 8 codes of slice 4 step + (tid & 3), token tid >> 2
+  const int dt = tid >> 2, dsq = tid & 3;
+  const uint8_t* kpt = dt < kGroup ? kp0 : kp1;
+  const int dtp = dt & (kGroup - 1);
+  auto decode_b = [&](int ks, int buf) {
+    // no branch: slices past the last (the padding of the last step, or a
+    // step past the last) decode the last slice and store zeros
+    const int s = 4 * ks + dsq, sc = min(s, n_sl - 1);
+    const uint32_t tab = s_tab[sc];
+    const int b = (int)(tab >> 24), off = (int)(tab & 0xFFFFFFu), w = sp_width(b);
+    const int pp = off + dtp * w;
+    const uint2 cw = *reinterpret_cast<const uint2*>(kpt + (pp & ~7));
+    const uint4 f = sp_b_factor(kpt, sc, b);
+    const uint64_t word = (((uint64_t)cw.y << 32) | cw.x) >> (8 * (pp & 7));
+    const uint2 lo = sp_codes4(word, w, b), hi = sp_codes4(word >> (4 * w), w, b);
+    const bool ok = s < n_sl;
+    const uint4 v = make_uint4(ok ? sp_hmul2(lo.x, f.x) : 0u, ok ? sp_hmul2(lo.y, f.y) : 0u,
+                               ok ? sp_hmul2(hi.x, f.z) : 0u, ok ? sp_hmul2(hi.y, f.w) : 0u);
+    *reinterpret_cast<uint4*>(&s_b[buf][dt][8 * dsq]) = v;
+  };
+
+  float4_t acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) acc[i][tt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  decode_b(0, 0);
+  decode_b(1, 1);
+  __syncthreads();
+  auto mfma_step = [&](int ks, int buf, auto wide) {
+    // A = the dec rows, times each page's steps of the lane's 8 columns in a
+    // step with wider tiers
+    half8_t A[2][4];
+    if constexpr (decltype(wide)::value) {
+      const half8_t f0 = sp_a_factor(kp0, s_tab, 4 * ks + q, n_sl), f1 = sp_a_factor(kp1, s_tab, 4 * ks + q, n_sl);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        A[0][i] = An[i] * f0;
+        A[1][i] = An[i] * f1;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) A[0][i] = A[1][i] = An[i];
+    }
+    const int kn = min(ks + 1, n_steps - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      An[i] = *reinterpret_cast<const half8_t*>(decb + rt(i) * tile_stride + step_stride * kn);
+    half8_t B[8];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) B[tt] = *reinterpret_cast<const half8_t*>(&s_b[buf][16 * tt + n][8 * q]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt)
+        acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[tt >> 2][i], B[tt], acc[i][tt], 0, 0, 0);
+  };
+  // whole pairs of steps in one basic block each (decodes past the last step
+  // store zeros into buffers nobody reads), then an odd last step; the
+  // compiler's own interleave of the MFMAs, the decode and the dec loads
+  // measured faster here than a fixed MFMA/VALU/LDS pattern
+  const int n_pairs = n_steps >> 1, n_narrow_pairs = n_narrow >> 1;
+  auto pair = [&](int kp, auto wide) {
+    const int ks = 2 * kp, pb = kp & 1;
+    mfma_step(ks, 2 * pb, wide);
+    decode_b(ks + 2, 2 * (pb ^ 1));
+    mfma_step(ks + 1, 2 * pb + 1, wide);
+    decode_b(ks + 3, 2 * (pb ^ 1) + 1);
+    lds_barrier();
+  };
+  int kp = 0;
+  for (; kp < n_narrow_pairs; ++kp) pair(kp, std::false_type{});
+  for (; kp < n_pairs; ++kp) pair(kp, std::true_type{});
+  if (n_steps & 1) mfma_step(n_steps - 1, 2 * (n_pairs & 1), std::true_type{});
+
+  // ---- query fragments of this wave's channels: bb = 2 r2 + bl ----
+  half8_t qf[2];
+  {
+    float qv[4][4];   // runs (bl, e): channels 16 bb + 4q .. + 3 + 64 e
+    const int64_t qrow = ((int64_t)hh * a.n_q_groups + (n < a.n_q_groups ? n : 0)) * kD + 4 * q;
+    if (a.q_dtype == BMX_K2B_F32) {
+      float4_t r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        r[u] = *reinterpret_cast<const float4_t*>(static_cast<const float*>(a.q) + qrow + 16 * (2 * r2 + (u & 1)) +
+                                                  64 * (u >> 1));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[u][i] = r[u][i];
+    } else {
+      uint2 r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        r[u] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.q) + qrow + 16 * (2 * r2 + (u & 1)) +
+                                               64 * (u >> 1));
+      const bool bf = a.q_dtype == BMX_K2B_BF16;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t w[4] = {r[u].x & 0xffffu, r[u].x >> 16, r[u].y & 0xffffu, r[u].y >> 16};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[u][i] = bf ? __uint_as_float(w[i] << 16) : half_bits_to_float(w[i]);
+      }
+    }
+    const bool qok = n < a.n_q_groups;
+#pragma unroll
+    for (int bl = 0; bl < 2; ++bl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) qf[bl][2 * i + e] = (_Float16)(qok ? qv[bl + 2 * e][i] : 0.f);
+  }
+  // ---- the wave's partial scores: RoPE of its pairs, fp16 keys, MFMA ----
+  float4_t sct[8];
+#pragma unroll
+  for (int tt = 0; tt < 8; ++tt) {
+    float4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int bl = 0; bl < 2; ++bl) {
+      const int bb = 2 * r2 + bl;
+      const uint4 cs4 = *reinterpret_cast<const uint4*>(&s_cs[16 * tt + n][16 * bb + 4 * q]);
+      const uint32_t csw[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+      half8_t ka;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half2_t cs = as_h2(csw[i]);
+        const float cn = (float)cs[0], sn = (float)cs[1];
+        const float k0 = acc[bl][tt][i], k1 = acc[bl + 2][tt][i];
+        const float r0 = __fmul_rn(k0, cn) - __fmul_rn(k1, sn);
+        const float r1 = __fmul_rn(k1, cn) + __fmul_rn(k0, sn);
+        ka[2 * i] = (_Float16)r0;
+        ka[2 * i + 1] = (_Float16)r1;
+      }
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[bl], sc, 0, 0, 0);
+    }
+    sct[tt] = sc;
+  }
+  // ---- the two halves of a head add their scores: through LDS (the pages'
+  // space, free after the loop), token tiles 0..3 then 4..7 ----
+  float4_t* xch = reinterpret_cast<float4_t*>(sp_dyn);   // [8 waves][4 tiles][64 lanes]
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xch[(wave * 4 + k) * 64 + lane] = sct[4 * half + k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4_t o = xch[((wave ^ 1) * 4 + k) * 64 + lane];
+      // the same sum in both waves: the lower half's value first
+      sct[4 * half + k] = r2 == 0 ? sct[4 * half + k] + o : o + sct[4 * half + k];
+    }
+    __syncthreads();
+  }
+  if (head_ok) {
+    // lane 16q + n holds query n's scores of tokens 16tt + 4q + i
+    float m = -INFINITY;
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = fmaxf(m, sct[tt][i] * a.sm_scale);
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    const bool qok = n < a.n_q_groups;
+    half4_t pw[8];
+    float l = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const _Float16 pr = qok ? (_Float16)__expf(sct[tt][i] * a.sm_scale - m) : (_Float16)0.f;
+        pw[tt][i] = pr;
+        l += (float)pr;
+      }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    // P.V in the rotated value domain, value page tt (= token tile tt), this
+    // wave's channel blocks ct = 4 r2 + c
+    float4_t pv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) pv[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) {
+      const uint2 nr = s_nrm[hl][tt][q];
+      const uint32_t vc = r2 == 0 ? s_vcd[hl][tt][lane].x : s_vcd[hl][tt][lane].y;
+      const float nv[4] = {half_bits_to_float(nr.x & 0xffffu), half_bits_to_float(nr.x >> 16),
+                           half_bits_to_float(nr.y & 0xffffu), half_bits_to_float(nr.y >> 16)};
+      half4_t aw;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[tt][i] * nv[i]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
+        const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
+        pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[c], 0, 0, 0);
+      }
+    }
+    const int n_parts = a.n_tokens / kSpBlk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qi = 4 * q + i;
+      if (qi < a.n_q_groups) {
+        float* dst = a.partials + (((int64_t)h * a.n_q_groups + qi) * n_parts + blk) * 130;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dst[2 + 16 * (4 * r2 + c) + n] = pv[c][i];
+      }
+    }
+    if (r2 == 0 && q == 0 && qok) {
+      float* dst = a.partials + (((int64_t)h * a.n_q_groups + n) * n_parts + blk) * 130;
+      dst[0] = m;
+      dst[1] = l;
     }
   }
 }
@@ -748,6 +1138,18 @@ static bool sp_layout_ok(const bmx_spectral_layout& L, std::string& why) {
 
 static bool dtype_ok(int d) { return d == BMX_K2B_F16 || d == BMX_K2B_F32 || d == BMX_K2B_BF16; }
 
+// The 128-token partial form serves a decode step whose two key pages fit in
+// LDS together, with the fp16-rounded RoPE table and 128-token multiples.
+// The partial form runs on 128-token blocks when both key pages of a block
+// fit in LDS together; the partials pointer itself is not consulted, so the
+// count below can be asked before the buffer exists.
+static bool sp_block_shape(const bmx_spectral_dequant_args* a) {
+  return a->q && !a->k_out && a->apply_rope == 2 && a->n_tokens % kSpBlk == 0 &&
+         2 * (int64_t)a->L.k_page_bytes <= kSpBlkMaxPages;
+}
+
+static bool sp_blocked(const bmx_spectral_dequant_args* a) { return a->partials && sp_block_shape(a); }
+
 }  // namespace bmx
 
 using namespace bmx;
@@ -821,14 +1223,26 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   k.k_out = a->k_out; k.v_out = a->v_out;
   k.q = a->q; k.q_dtype = a->q_dtype; k.n_q_groups = a->n_q_groups; k.scores = a->scores;
   k.partials = a->partials; k.sm_scale = a->sm_scale;
-  hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512),
-                     sp_dyn_bytes(a->L.k_page_bytes), (hipStream_t)stream, k);
+  if (sp_blocked(a)) {
+    const int kpb = a->L.k_page_bytes;
+    const size_t dyn = std::max<size_t>(2 * (size_t)kpb, (size_t)8 * 4 * 64 * 16);   // pages, then the exchange
+    hipLaunchKernelGGL(spectral_partial128_kernel, dim3(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4), dim3(512),
+                       dyn, (hipStream_t)stream, k, kpb);
+  } else {
+    hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512),
+                       sp_dyn_bytes(a->L.k_page_bytes), (hipStream_t)stream, k);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     bmx_set_error(std::string(fn) + ": launch: " + hipGetErrorString(e));
     return BMX_E_HIP;
   }
   return BMX_OK;
+}
+
+extern "C" int32_t bmx_spectral_partial_count(const bmx_spectral_dequant_args* a) {
+  if (!a || a->n_tokens < 0 || a->n_tokens % kGroup != 0) return -1;
+  return sp_block_shape(a) ? a->n_tokens / kSpBlk : a->n_tokens / kGroup;
 }
 
 extern "C" int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* stream) {

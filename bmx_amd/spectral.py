@@ -197,6 +197,42 @@ def append(k_pre: torch.Tensor, v: torch.Tensor, dp: DevicePack, k_pages: torch.
     _lib.check(_lib.lib().bmx_spectral_append(ct.byref(a), _stream(dev)), "bmx_spectral_append")
 
 
+def _partial_args(dp: DevicePack, k_pages, k_table, v_pages, v_table, n_tokens: int, consts: CodecConsts,
+                  q: torch.Tensor, apply_rope: int, sm_scale: float):
+    """Arguments of the dequant kernel's partial form, partials not yet set."""
+    _need(q.dim() == 3 and q.shape[0] == dp.h_kv and q.shape[2] == HEAD_DIM and 1 <= q.shape[1] <= 16
+          and q.is_contiguous() and q.dtype in _V_DTYPES, "q must be contiguous (h_kv, 1..16, 128)")
+    _need(int(apply_rope) != ROPE_NONE, "the decode form scores rotated keys")
+    a = _lib.SpectralDequantArgs()
+    a.L = dp.layout()
+    a.n_tokens = int(n_tokens)
+    a.k_pages, a.k_page_table, a.n_k_pool = _ptr(k_pages), _ptr(k_table), k_pages.shape[0]
+    a.v_pages, a.v_page_table, a.n_v_pool = _ptr(v_pages), _ptr(v_table), v_pages.shape[0]
+    a.dec_perm = _ptr(dp.dec_perm)
+    a.apply_rope = int(apply_rope)
+    a.rope_scaling = consts.rope_scaling
+    a.inv_freq[:] = consts.inv_freq
+    a.v_codebook[:] = consts.codebook
+    a.v_sign_bits[:] = consts.sign_bits
+    a.out_dtype = _V_DTYPES[torch.float16]
+    a.q, a.q_dtype, a.n_q_groups = _ptr(q), _V_DTYPES[q.dtype], q.shape[1]
+    a.sm_scale = float(sm_scale)
+    return a
+
+
+def partial_count(dp: DevicePack, n_tokens: int, q: torch.Tensor, apply_rope: int = 2) -> int:
+    """Softmax partials per (head, query) row that dequant's partial form
+    writes for n_tokens committed tokens: one per 128-token block when the
+    kernel's blocked form applies (see include/bmx_spectral.h), else one per
+    64-token group."""
+    a = _lib.SpectralDequantArgs()
+    a.L = dp.layout()
+    a.n_tokens, a.q, a.apply_rope = int(n_tokens), _ptr(q), int(apply_rope)
+    n = _lib.lib().bmx_spectral_partial_count(ct.byref(a))
+    _need(n >= 0, "n_tokens must be a non-negative multiple of 64")
+    return n
+
+
 def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_pages: torch.Tensor,
             v_table: torch.Tensor, n_tokens: int, consts: CodecConsts, *, apply_rope: int = ROPE_NONE,
             dtype: torch.dtype = torch.float32, out: tuple | None = None, q: torch.Tensor | None = None,
@@ -211,9 +247,9 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     Decode form: with q (h_kv, G, 128) the kernel also writes scores
     (h_kv, G, R) fp32, q . k of the rotated keys for rows 0 .. n_tokens - 1
     (no softmax scale); out may then be (None, V) and no dense keys are
-    written.  Partial form: with q and partials (h_kv, G, n_tokens / 64, 130)
-    fp32 the kernel writes each 64-token group's softmax partial of the
-    scaled scores (m, l, P.V; see include/bmx_spectral.h) and no dense rows;
+    written.  Partial form: with q and partials (h_kv, G, partial_count(), 130)
+    fp32 the kernel writes each 128-token block's (or 64-token group's)
+    softmax partial of the scaled scores (m, l, P.V; see include/bmx_spectral.h) and no dense rows;
     out is then unused."""
     dev = k_pages.device
     # the C-ABI carries no table lengths: a short or wrongly typed table would
@@ -225,26 +261,13 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     _need(k_table.device == dev and v_table.device == dev and k_table.is_contiguous()
           and v_table.is_contiguous(), "k_table and v_table must be contiguous on the pages' device")
     if partials is not None:
-        _need(q is not None and partials.dtype == torch.float32 and partials.is_contiguous()
-              and tuple(partials.shape) == (dp.h_kv, q.shape[1], n_tokens // GROUP, 130),
-              "partials must be fp32 (h_kv, G, n_tokens / 64, 130), with q")
-        _need(q.dim() == 3 and q.shape[0] == dp.h_kv and q.shape[2] == HEAD_DIM and 1 <= q.shape[1] <= 16
-              and q.is_contiguous() and q.dtype in _V_DTYPES, "q must be contiguous (h_kv, 1..16, 128)")
-        _need(int(apply_rope) != ROPE_NONE, "the decode form scores rotated keys")
-        a = _lib.SpectralDequantArgs()
-        a.L = dp.layout()
-        a.n_tokens = int(n_tokens)
-        a.k_pages, a.k_page_table, a.n_k_pool = _ptr(k_pages), _ptr(k_table), k_pages.shape[0]
-        a.v_pages, a.v_page_table, a.n_v_pool = _ptr(v_pages), _ptr(v_table), v_pages.shape[0]
-        a.dec_perm = _ptr(dp.dec_perm)
-        a.apply_rope = int(apply_rope)
-        a.rope_scaling = consts.rope_scaling
-        a.inv_freq[:] = consts.inv_freq
-        a.v_codebook[:] = consts.codebook
-        a.v_sign_bits[:] = consts.sign_bits
-        a.out_dtype = _V_DTYPES[dtype]
-        a.q, a.q_dtype, a.n_q_groups = _ptr(q), _V_DTYPES[q.dtype], q.shape[1]
-        a.partials, a.sm_scale = _ptr(partials), float(sm_scale)
+        _need(q is not None, "partials need q")
+        a = _partial_args(dp, k_pages, k_table, v_pages, v_table, n_tokens, consts, q, apply_rope, sm_scale)
+        n_parts = _lib.lib().bmx_spectral_partial_count(ct.byref(a))
+        _need(partials.dtype == torch.float32 and partials.is_contiguous()
+              and tuple(partials.shape) == (dp.h_kv, q.shape[1], n_parts, 130),
+              f"partials must be fp32 (h_kv, G, {n_parts}, 130): partial_count() per row")
+        a.partials = _ptr(partials)
         _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
         return partials
     _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
@@ -289,7 +312,7 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
                      apply_rope: int = 2, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """One decode step over n_tokens committed tokens and the fp16 window:
     q (h_kv, G, 128) post-RoPE -> (h_kv, G, 128) in out_dtype (q's by default).  The dequant
-    kernel's partial form gives every 64-token group's (m, l, P.V); the merge
+    kernel's partial form gives every 128-token block's (m, l, P.V); the merge
     kernel scores the window and folds everything by the split softmax's
     weights (m = max m_i, weights e^(m_i - m))."""
     h, G, d = q.shape
@@ -300,7 +323,8 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
           "q (h_kv, G, 128) with h_kv of the pack")
     pt = None
     if n_tokens > 0:
-        pt = torch.empty(h, G, n_tokens // GROUP, 130, dtype=torch.float32, device=q.device)
+        pt = torch.empty(h, G, partial_count(dp, n_tokens, q, apply_rope), 130, dtype=torch.float32,
+                         device=q.device)
         dequant(dp, k_pages, k_table, v_pages, v_table, n_tokens, consts, apply_rope=apply_rope,
                 dtype=torch.float16, q=q, partials=pt, sm_scale=sm_scale)
     T = 0 if k_win is None else k_win.shape[1]
@@ -313,13 +337,14 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
     _need(out_dtype in _V_DTYPES, "out_dtype must be fp16, bf16 or fp32")
     out = torch.empty(h, G, d, dtype=out_dtype, device=q.device)
     a = _lib.SpectralMergeArgs()
-    a.h_kv, a.n_q_groups, a.n_groups = h, G, n_tokens // GROUP
+    n_parts = 0 if pt is None else pt.shape[2]
+    a.h_kv, a.n_q_groups, a.n_groups = h, G, n_parts
     a.partials, a.q, a.q_dtype = _ptr(pt), _ptr(q), _V_DTYPES[q.dtype]
     a.k_win, a.v_win, a.win_len = (_ptr(k_win), _ptr(v_win), T) if T else (None, None, 0)
     a.win_stride_h = k_win.stride(0) if T else 0
     a.sm_scale, a.out, a.out_dtype = float(sm_scale), _ptr(out), _V_DTYPES[out_dtype]
     a.v_sign_bits[:] = consts.sign_bits
-    n_runs = -(-(n_tokens // GROUP) // 64)
+    n_runs = -(-n_parts // 64)
     scratch = torch.empty(h, G, n_runs, 130, dtype=torch.float32, device=q.device) if n_runs else None
     a.scratch = _ptr(scratch)
     _lib.check(_lib.lib().bmx_spectral_merge(ct.byref(a), _stream(q.device)), "bmx_spectral_merge")

@@ -110,12 +110,15 @@ typedef struct bmx_spectral_dequant_args {
   int32_t n_q_groups;          /* 1..16 */
   float* scores;               /* [h_kv][n_q_groups][out_rows] fp32 */
   /* Partial form (with q): instead of scores and values, each 64-token group's
-   * softmax partial per (head, query): partials[((h G + g) n_groups + grp) 130 + e],
+   * softmax partial per (head, query): partials[((h G + g) n_parts + grp) 130 + e],
    * e = 0: m = max of the scaled scores, 1: l = sum of exp(s - m) (the fp16
    * weights), 2 + c: in the rotated value domain, the sum of the weights
    * times the token norms times the codebook levels of rotated channel c
    * (fp32 accumulation of fp16 operands; the values are that sum's inverse
-   * Hadamard, signs and 1/128); n_groups = n_tokens / 64.  The
+   * Hadamard, signs and 1/128); n_parts = bmx_spectral_partial_count(args):
+   * one partial per 128-token block when the two key pages of a block fit
+   * in LDS together (2 k_page_bytes <= 57344), apply_rope is 2 and n_tokens
+   * a multiple of 128, else one per 64-token group.  The
    * caller merges the groups' partials (m = max m_i, l = sum l_i e^(m_i - m),
    * out = sum acc_i e^(m_i - m) / l) with the window's.  v_out and scores may
    * then be NULL. */
@@ -153,6 +156,9 @@ int64_t bmx_spectral_v_page_bytes(int32_t h_kv);
 int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* stream);
 int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* stream);
 int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void* stream);
+/* Partials per (head, query) row that the partial form of these arguments
+ * writes, or -1; partials itself may still be NULL when this is asked. */
+int32_t bmx_spectral_partial_count(const bmx_spectral_dequant_args* a);
 
 #ifdef __cplusplus
 }

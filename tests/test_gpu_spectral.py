@@ -197,48 +197,66 @@ def test_decode_form_scores_match_keys():
         assert torch.equal(Vb[:, :S], V) and not Vb[:, S:].any() and not Sb[:, :, S:].any()
 
 
-@pytest.mark.parametrize("G,T", [(4, 40), (1, 0), (8, 7), (16, 40)])
-def test_partial_form_decode_matches_oracle(G, T):
-    """The decode step through the kernel's partial form (per-group softmax
+PARTIAL_CASES = [
+    # (h_kv, G, T, rope, S): the exact-RoPE form runs on 64-token groups; the
+    # fp16-table form on 128-token blocks of 4 heads when S is a multiple of
+    # 128 (ragged head counts leave waves of the last workgroup idle), else on
+    # 64-token groups
+    (8, 4, 40, k2b.ROPE_EXACT, 1024), (8, 1, 0, k2b.ROPE_EXACT, 1024), (8, 8, 7, k2b.ROPE_EXACT, 1024),
+    (8, 16, 40, k2b.ROPE_EXACT, 1024),
+    (8, 4, 40, k2b.ROPE_FP16_TABLES, 1024), (8, 16, 7, k2b.ROPE_FP16_TABLES, 2048),
+    (8, 1, 0, k2b.ROPE_FP16_TABLES, 1088), (3, 8, 40, k2b.ROPE_FP16_TABLES, 512),
+    (2, 5, 3, k2b.ROPE_FP16_TABLES, 256),
+]
+
+
+@pytest.mark.parametrize("h_kv,G,T,rope,S", PARTIAL_CASES)
+def test_partial_form_decode_matches_oracle(h_kv, G, T, rope, S):
+    """The decode step through the kernel's partial form (per-block softmax
     partials) and the merge with the window: against the oracle's one-softmax
-    attention over the same codes, and against the scores form + softmax."""
-    pack = synthetic_pack(8, 2.5, seed=14)
-    S = 1024
+    attention over the same codes (RoPE by fp32 tables, or by the fp16-rounded
+    tables of an fp16 model), and against the scores form + softmax."""
+    pack = synthetic_pack(h_kv, 2.5, seed=14)
     M = synthetic_keys(pack, S, seed=15)
     gen = torch.Generator().manual_seed(16)
-    v = torch.randn(8, S, 128, generator=gen)
+    v = torch.randn(h_kv, S, 128, generator=gen)
     consts = k2b.CodecConsts.make(v_seed=0)
-    dp, kp, vp, k_ids, v_ids = _write(pack, 8, M, v, consts, shuffle_seed=4)
-    kt = torch.randn(8, T, 128, generator=gen).half()
-    vt = torch.randn(8, T, 128, generator=gen).half()
-    q = torch.randn(8, G, 128, generator=gen).half()
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=4)
+    kt = torch.randn(h_kv, T, 128, generator=gen).half()
+    vt = torch.randn(h_kv, T, 128, generator=gen).half()
+    q = torch.randn(h_kv, G, 128, generator=gen).half()
     scale = 128 ** -0.5
+    n_parts = spectral.partial_count(dp, S, q.to(DEV), rope)
+    blocked = rope == k2b.ROPE_FP16_TABLES and S % 128 == 0 and 2 * dp.k_page_bytes <= 57344
+    assert n_parts == (S // 128 if blocked else S // 64)
     out = spectral.decode_attention(dp, kp, k_ids, vp, v_ids, S, consts, q.to(DEV), scale,
                                     k_win=kt.to(DEV) if T else None, v_win=vt.to(DEV) if T else None,
-                                    apply_rope=k2b.ROPE_EXACT, out_dtype=torch.float32)
+                                    apply_rope=rope, out_dtype=torch.float32)
     L = O.Layout(pack.bits.numpy())
     codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
-    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)).float(), 8)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)).float(), h_kv)
     cos, sin = A.rope_cos_sin(torch.tensor(consts.inv_freq), torch.arange(S))
-    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v), bits=2, seed=0, h=8)
-    V_or = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=8), 8)
-    ref = A.naive_dense_attention(q.reshape(8 * G, 1, 128).float(),
+    if rope == k2b.ROPE_FP16_TABLES:
+        cos, sin = cos.half().float(), sin.half().float()
+    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v), bits=2, seed=0, h=h_kv)
+    V_or = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=h_kv), h_kv)
+    ref = A.naive_dense_attention(q.reshape(h_kv * G, 1, 128).float(),
                                   torch.cat([A.apply_rope(K_or, cos, sin), kt.float()], 1),
-                                  torch.cat([V_or, vt.float()], 1), G, scale).reshape(8, G, 128)
+                                  torch.cat([V_or, vt.float()], 1), G, scale).reshape(h_kv, G, 128)
     o = out.cpu().double()
     err = (o - ref.double()).abs().max().item()
     rel = ((o - ref.double()).norm() / ref.double().norm()).item()
     # the scores form + one softmax + value product, same kernel inputs
-    Vb = torch.empty(8, S, 128, dtype=torch.float16, device=DEV)
-    Sb = torch.empty(8, G, S, dtype=torch.float32, device=DEV)
-    spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=k2b.ROPE_EXACT, dtype=torch.float16,
+    Vb = torch.empty(h_kv, S, 128, dtype=torch.float16, device=DEV)
+    Sb = torch.empty(h_kv, G, S, dtype=torch.float32, device=DEV)
+    spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=rope, dtype=torch.float16,
                      out=(None, Vb), q=q.to(DEV), scores=Sb)
     sw = torch.cat([Sb, (q.float() @ kt.float().transpose(1, 2)).to(DEV)], -1) * scale
     Vw = torch.cat([Vb.float(), vt.float().to(DEV)], 1)
     alt = (torch.softmax(sw, -1) @ Vw).cpu().double()
     d_alt = (o - alt).abs().max().item()
-    print(f"G {G} T {T}: partial-form decode vs oracle max_abs {err:.3e} rel {rel:.3e}; vs scores form {d_alt:.3e}",
-          flush=True)
+    print(f"h_kv {h_kv} G {G} T {T} rope {rope} S {S} ({n_parts} partials): partial-form decode vs oracle "
+          f"max_abs {err:.3e} rel {rel:.3e}; vs scores form {d_alt:.3e}", flush=True)
     assert err <= 2e-3 and rel <= 1e-2 and d_alt <= 2e-3
 
 
