@@ -720,7 +720,7 @@ def run_spectral(args, torch, dev) -> dict:
     reps = max(args.steps, 1)
     call_us = timed(lambda: lay.attend(q, scale), reps)
     n_parts = spectral.partial_count(dp, P, qg, k2b.ROPE_FP16_TABLES)
-    Pb = torch.empty(H_KV, G, n_parts, 130, dtype=torch.float32, device=dev)
+    Pb = torch.empty(H_KV, G, 130 * n_parts, dtype=torch.float32, device=dev)
     deq_us = timed(lambda: spectral.dequant(dp, lay._kpool, kt, lay._pool, vt, P, lay._consts,
                                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=torch.float16,
                                             q=qg, partials=Pb, sm_scale=scale), reps)

@@ -239,7 +239,7 @@ class SpectralMergeArgs(ct.Structure):
                 ("partials", ct.c_void_p), ("q", ct.c_void_p), ("q_dtype", ct.c_int32),
                 ("k_win", ct.c_void_p), ("v_win", ct.c_void_p), ("win_len", ct.c_int32),
                 ("sm_scale", ct.c_float), ("out", ct.c_void_p), ("out_dtype", ct.c_int32),
-                ("v_sign_bits", ct.c_uint32 * 4), ("scratch", ct.c_void_p), ("win_stride_h", ct.c_int64)]
+                ("v_sign_bits", ct.c_uint32 * 4), ("win_stride_h", ct.c_int64)]
 
 
 EXPORTS = {

@@ -205,6 +205,42 @@ __device__ __forceinline__ uint2 sp_codes4(uint64_t word, int w, int b) {
   return make_uint2(as_u32(as_h2(c[0] | (c[1] << 16)) - o2), as_u32(as_h2(c[2] | (c[3] << 16)) - o2));
 }
 
+// Partial records, per (head, query) row r of n_parts partials: (m, l) of
+// partial p at row base + 2p, its channels 16k .. 16k + 15 at row base +
+// 2 n_parts + 16 (k n_parts + p): a merge workgroup of one 16-channel chunk
+// reads contiguous records.
+__device__ __forceinline__ float* sp_part_ml(float* partials, int64_t r, int n_parts, int p) {
+  return partials + r * 130 * (int64_t)n_parts + 2 * p;
+}
+__device__ __forceinline__ float* sp_part_ch(float* partials, int64_t r, int n_parts, int chunk, int p) {
+  return partials + r * 130 * (int64_t)n_parts + 2 * (int64_t)n_parts + 16 * ((int64_t)chunk * n_parts + p);
+}
+
+// The 128-point Hadamard (unnormalized; pairs (a, b) -> (a + b, a - b)) of
+// the channel sums, channel 16 ct + n: H8 over ct = H over the channel's
+// bits 4..6, applied to each partial by the dequant kernels; H16 over n (bits
+// 0..3, within a 16-channel chunk), applied by the merge to the merged sums
+// of its chunk, held by the lanes n of one 16-lane row.
+// The partner lanes come by DPP within the 16-lane row (no LDS crossbar):
+// lane ^ 1 and ^ 2 by quad permutes, ^ 4 by a quad reversal then the
+// half-row mirror (i ^ 3 ^ 7), ^ 8 by a row rotation of 8.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kCtrl, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float h16_lanes(float x, int n) {
+  float o = dpp_f<0xB1>(x);                 // quad_perm [1, 0, 3, 2]
+  x = (n & 1) ? o - x : x + o;
+  o = dpp_f<0x4E>(x);                       // quad_perm [2, 3, 0, 1]
+  x = (n & 2) ? o - x : x + o;
+  o = dpp_f<0x141>(dpp_f<0x1B>(x));         // quad_perm [3, 2, 1, 0], row_half_mirror
+  x = (n & 4) ? o - x : x + o;
+  o = dpp_f<0x128>(x);                      // row_ror:8
+  x = (n & 8) ? o - x : x + o;
+  return x;
+}
+
 __device__ __forceinline__ uint32_t sp_hmul2(uint32_t x, uint32_t y) { return as_u32(as_h2(x) * as_h2(y)); }
 
 constexpr uint32_t kHalfOnes = 0x3C003C00u;   // fp16 (1, 1)
@@ -559,19 +595,31 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
           pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[ct], 0, 0, 0);
         }
       }
-      // lane n (q = 0) holds queries i = 0..3, channel 16ct + n; queries 4.. in lanes q >= 1
+      // lane 16q + n holds queries 4q + i, channel 16ct + n: H8 over ct in
+      // registers (the merge applies H16 over n to its chunk's merged sums)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int sb = 1; sb < 8; sb <<= 1)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+            if (!(ct & sb)) {
+              const float u = pv[ct][i], w = pv[ct | sb][i];
+              pv[ct][i] = u + w;
+              pv[ct | sb][i] = u - w;
+            }
       const int n_grp = a.n_tokens / kGroup;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int qi = 4 * q + i;
         if (qi < a.n_q_groups) {
-          float* dst = a.partials + (((int64_t)h * a.n_q_groups + qi) * n_grp + g) * 130;
+          const int64_t r = (int64_t)h * a.n_q_groups + qi;
 #pragma unroll
-          for (int ct = 0; ct < 8; ++ct) dst[2 + 16 * ct + n] = pv[ct][i];
+          for (int ct = 0; ct < 8; ++ct) sp_part_ch(a.partials, r, n_grp, ct, g)[n] = pv[ct][i];
         }
       }
       if (q == 0 && qok) {
-        float* dst = a.partials + (((int64_t)h * a.n_q_groups + n) * n_grp + g) * 130;
+        float* dst = sp_part_ml(a.partials, (int64_t)h * a.n_q_groups + n, n_grp, g);
         dst[0] = m;
         dst[1] = l;
       }
@@ -861,64 +909,87 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     }
     __syncthreads();
   }
-  if (head_ok) {
-    // lane 16q + n holds query n's scores of tokens 16tt + 4q + i
-    float m = -INFINITY;
+  // lane 16q + n holds query n's scores of tokens 16tt + 4q + i
+  float m = -INFINITY;
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt)
+  for (int tt = 0; tt < 8; ++tt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) m = fmaxf(m, sct[tt][i] * a.sm_scale);
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
-    const bool qok = n < a.n_q_groups;
-    half4_t pw[8];
-    float l = 0.f;
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, sct[tt][i] * a.sm_scale);
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
+  const bool qok = n < a.n_q_groups;
+  half4_t pw[8];
+  float l = 0.f;
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const _Float16 pr = qok ? (_Float16)__expf(sct[tt][i] * a.sm_scale - m) : (_Float16)0.f;
-        pw[tt][i] = pr;
-        l += (float)pr;
-      }
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    // P.V in the rotated value domain, value page tt (= token tile tt), this
-    // wave's channel blocks ct = 4 r2 + c
-    float4_t pv[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) pv[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      const uint2 nr = s_nrm[hl][tt][q];
-      const uint32_t vc = r2 == 0 ? s_vcd[hl][tt][lane].x : s_vcd[hl][tt][lane].y;
-      const float nv[4] = {half_bits_to_float(nr.x & 0xffffu), half_bits_to_float(nr.x >> 16),
-                           half_bits_to_float(nr.y & 0xffffu), half_bits_to_float(nr.y >> 16)};
-      half4_t aw;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[tt][i] * nv[i]);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
-        const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
-        pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[c], 0, 0, 0);
-      }
-    }
-    const int n_parts = a.n_tokens / kSpBlk;
+  for (int tt = 0; tt < 8; ++tt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int qi = 4 * q + i;
-      if (qi < a.n_q_groups) {
-        float* dst = a.partials + (((int64_t)h * a.n_q_groups + qi) * n_parts + blk) * 130;
+      const _Float16 pr = qok ? (_Float16)__expf(sct[tt][i] * a.sm_scale - m) : (_Float16)0.f;
+      pw[tt][i] = pr;
+      l += (float)pr;
+    }
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  // P.V in the rotated value domain, value page tt (= token tile tt), this
+  // wave's channel blocks ct = 4 r2 + c (waves past the heads compute head 0's)
+  float4_t pv[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dst[2 + 16 * (4 * r2 + c) + n] = pv[c][i];
-      }
+  for (int c = 0; c < 4; ++c) pv[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int tt = 0; tt < 8; ++tt) {
+    const uint2 nr = s_nrm[hl][tt][q];
+    const uint32_t vc = r2 == 0 ? s_vcd[hl][tt][lane].x : s_vcd[hl][tt][lane].y;
+    const float nv[4] = {half_bits_to_float(nr.x & 0xffffu), half_bits_to_float(nr.x >> 16),
+                         half_bits_to_float(nr.y & 0xffffu), half_bits_to_float(nr.y >> 16)};
+    half4_t aw;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[tt][i] * nv[i]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
+      const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
+      pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[c], 0, 0, 0);
     }
-    if (r2 == 0 && q == 0 && qok) {
-      float* dst = a.partials + (((int64_t)h * a.n_q_groups + n) * n_parts + blk) * 130;
-      dst[0] = m;
-      dst[1] = l;
+  }
+  // H8 over the block index ct = 4 r2 + c: c in registers, r2 (the
+  // channel's bit 6) with the head's other wave through LDS (the exchange's
+  // space, read out above); the merge applies H16 over n
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int sb = 1; sb < 4; sb <<= 1)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (!(c & sb)) {
+          const float u = pv[c][i], w = pv[c | sb][i];
+          pv[c][i] = u + w;
+          pv[c | sb][i] = u - w;
+        }
+  float4_t* xv = reinterpret_cast<float4_t*>(sp_dyn);   // [8 waves][4 blocks][64 lanes]
+#pragma unroll
+  for (int c = 0; c < 4; ++c) xv[(wave * 4 + c) * 64 + lane] = pv[c];
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float4_t o = xv[((wave ^ 1) * 4 + c) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pv[c][i] = r2 == 0 ? pv[c][i] + o[i] : o[i] - pv[c][i];
+  }
+  if (!head_ok) return;
+  const int n_parts = a.n_tokens / kSpBlk;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int qi = 4 * q + i;
+    if (qi < a.n_q_groups) {
+      const int64_t r = (int64_t)h * a.n_q_groups + qi;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sp_part_ch(a.partials, r, n_parts, 4 * r2 + c, blk)[n] = pv[c][i];
     }
+  }
+  if (r2 == 0 && q == 0 && qok) {
+    float* dst = sp_part_ml(a.partials, (int64_t)h * a.n_q_groups + n, n_parts, blk);
+    dst[0] = m;
+    dst[1] = l;
   }
 }
 
@@ -937,174 +1008,175 @@ struct SpMergeKArgs {
 };
 
 constexpr int kSpMergeMaxGroups = 16384;   // 1M committed tokens
-constexpr int kSpMergeThreads = 1024;      // 8 slices x 128 channels
+constexpr int kSpMergeBatch = 8;           // parts per thread whose loads are in flight together
 
-// Sum (or max) of one value per thread over the 1024-thread block.
+// Max or sum of one value per thread over a 256-thread block (the result in
+// every thread); s_red holds 4 floats.
 template <bool kMax>
-__device__ __forceinline__ float block_reduce(float v, float* s_red) {
+__device__ __forceinline__ float reduce256(float v, float* s_red) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     const float u = __shfl_xor(v, o);
     v = kMax ? fmaxf(v, u) : v + u;
   }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   __syncthreads();   // s_red free from any earlier reduction
-  if (lane == 0) s_red[wave] = v;
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
   __syncthreads();
-  v = s_red[lane & 15];
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) {
-    const float u = __shfl_xor(v, o);
-    v = kMax ? fmaxf(v, u) : v + u;
-  }
-  return v;
+  return kMax ? fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]))
+              : (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
 }
 
-// grid (G, h_kv), block 1024: one query (h, blockIdx.x).  The window's scaled
-// scores and the groups' weights e^(m_i - M) go to LDS (thread t takes tokens
-// and groups t, t + 1024, ..), M and the weight sum come from block
-// reductions, then thread (s, c) sums weight times channel c over the groups
-// and window tokens of slice s (index mod 8), and the 8 slices are added in LDS.
-__global__ __launch_bounds__(kSpMergeThreads) void spectral_merge_kernel(const SpMergeKArgs a) {
-  const int g = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 127, sl = tid >> 7;
+__device__ __forceinline__ float4_t f4_fma(float w, float4_t x, float4_t acc) {
+  return (float4_t){fmaf(w, x[0], acc[0]), fmaf(w, x[1], acc[1]), fmaf(w, x[2], acc[2]), fmaf(w, x[3], acc[3])};
+}
+
+// grid (8 chunks, G, h_kv), block 256: channels 16 chunk .. 16 chunk + 15 of
+// query row (h, g).  The partials come in the value domain up to the codec's
+// signs and 1/128 (the dequant kernels apply the 128-point Hadamard to each),
+// so a chunk needs only its 16 channels of every partial, the partials'
+// (m, l) and the window; the 256 workgroups do the merge in one pass.
+// Thread (slot s = tid >> 2, quad c4 = tid & 3) takes the partials and window
+// rows s + 64k and channels 16 chunk + 4 c4 .. + 3; for the window scores,
+// thread tid takes token tid >> 1 of each 128-token pass and half tid & 1 of
+// the dims.  Every load of the first batch of partials and of the first pass
+// of the window is issued before anything waits.
+__global__ __launch_bounds__(256) void spectral_merge_kernel(const SpMergeKArgs a) {
+  const int chunk = blockIdx.x, g = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
+  const int slot = tid >> 2, c4 = tid & 3, c0 = 16 * chunk + 4 * c4;
+  const int tw = tid >> 1, half = tid & 1;
   __shared__ float s_q[kD];
   __shared__ float s_s[kSpMaxWin];
-  __shared__ float s_w[kSpMergeMaxGroups];
-  __shared__ float s_red[16];
-  __shared__ float s_acc[8][kD];
-  __shared__ float s_accw[8][kD];
-  __shared__ float s_h[kD];
+  __shared__ float s_red[4];
+  __shared__ float4_t s_sum[4][4], s_sumw[4][4];
   const int64_t row = (int64_t)h * a.G + g;
-  if (tid < kD) s_q[tid] = sp_load(a.q, row * kD + tid, a.q_dtype);
+  const float* pml = a.partials + row * 130 * (int64_t)a.n_groups;          // (m, l) of partial p at 2p
+  const float* pch = pml + 2 * (int64_t)a.n_groups + 16 * (int64_t)chunk * a.n_groups + 4 * c4;   // + 16p
+  const int P = a.n_groups, T = a.win_len;
+  const uint16_t* kbase = a.k_win + (int64_t)h * a.win_sh;
+  const uint16_t* vbase = a.v_win + (int64_t)h * a.win_sh;
+  // ---- loads: the query, the first batch of partials, the first window pass
+  float qv = 0.f;
+  if (tid < kD) qv = sp_load(a.q, row * kD + tid, a.q_dtype);
+  float2 ml[kSpMergeBatch];
+  float4_t y[kSpMergeBatch];
+  auto load_part = [&](int p, float2& m_l, float4_t& yy) {   // p clamped by the caller
+    m_l = *reinterpret_cast<const float2*>(pml + 2 * (int64_t)p);
+    const float* r = pch + 16 * (int64_t)p;   // 8-byte aligned: two 8-byte loads
+    const float2 lo = *reinterpret_cast<const float2*>(r), hi = *reinterpret_cast<const float2*>(r + 2);
+    yy = (float4_t){lo.x, lo.y, hi.x, hi.y};
+  };
+  if (P > 0) {
+#pragma unroll
+    for (int k = 0; k < kSpMergeBatch; ++k) load_part(min(slot + 64 * k, P - 1), ml[k], y[k]);
+  }
+  uint4 kr[8];
+  uint2 vr[2];
+  if (T > 0) {
+    const uint16_t* kp = kbase + (int64_t)min(tw, T - 1) * kD + 64 * half;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = reinterpret_cast<const uint4*>(kp)[i];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      vr[k] = *reinterpret_cast<const uint2*>(vbase + (int64_t)min(slot + 64 * k, T - 1) * kD + c0);
+  }
+  if (tid < kD) s_q[tid] = qv;
   __syncthreads();
-  const float* pt = a.partials + row * (int64_t)a.n_groups * 130;
+  // ---- the window's scaled scores, 128 tokens a pass, into s_s
   float mx = -INFINITY;
-  // window scores: 8 threads per token, 16 channels each (two 16-byte loads,
-  // issued together), summed across the 8 lanes
-  const int sub = tid & 7;
-  for (int t0 = 0; t0 < a.win_len; t0 += kSpMergeThreads / 8) {
-    const int t = t0 + (tid >> 3);
-    const uint16_t* kr = a.k_win + (int64_t)h * a.win_sh + (int64_t)min(t, a.win_len - 1) * kD + 16 * sub;
-    const uint4 k0 = *reinterpret_cast<const uint4*>(kr), k1 = *reinterpret_cast<const uint4*>(kr + 8);
-    const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+  for (int t0 = 0; t0 < T; t0 += 128) {
+    const int t = t0 + tw;
+    if (t0 > 0) {
+      const uint16_t* kp = kbase + (int64_t)min(t, T - 1) * kD + 64 * half;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kr[i] = reinterpret_cast<const uint4*>(kp)[i];
+    }
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      acc = fmaf(s_q[16 * sub + 2 * i], half_bits_to_float(kw[i] & 0xffffu), acc);
-      acc = fmaf(s_q[16 * sub + 2 * i + 1], half_bits_to_float(kw[i] >> 16), acc);
+      const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = 64 * half + 8 * i + 2 * e;
+        acc = fmaf(s_q[d], half_bits_to_float(w4[e] & 0xffffu), acc);
+        acc = fmaf(s_q[d + 1], half_bits_to_float(w4[e] >> 16), acc);
+      }
     }
     acc += __shfl_xor(acc, 1);
-    acc += __shfl_xor(acc, 2);
-    acc += __shfl_xor(acc, 4);
-    if (t < a.win_len) {
+    if (t < T) {
       const float sc = acc * a.sm_scale;
-      if (sub == 0) s_s[t] = sc;
+      if (half == 0) s_s[t] = sc;
       mx = fmaxf(mx, sc);
     }
   }
-  for (int i = tid; i < a.n_groups; i += kSpMergeThreads) mx = fmaxf(mx, pt[(int64_t)i * 130]);
-  const float M = block_reduce<true>(mx, s_red);
-  float lsum = 0.f;
-  for (int i = tid; i < a.n_groups; i += kSpMergeThreads) {
-    const float w = __expf(pt[(int64_t)i * 130] - M);
-    s_w[i] = w;
-    lsum = fmaf(w, pt[(int64_t)i * 130 + 1], lsum);
-  }
-  for (int t = tid; t < a.win_len; t += kSpMergeThreads) {
-    const float w = __expf(s_s[t] - M);
-    s_s[t] = w;
-    lsum += w;
-  }
-  const float L = block_reduce<false>(lsum, s_red);   // its barriers also publish s_w and s_s
-  float A = 0.f, Aw = 0.f;
-#pragma unroll 8
-  for (int i = sl; i < a.n_groups; i += 8) A = fmaf(s_w[i], pt[(int64_t)i * 130 + 2 + c], A);
-  const uint16_t* vw = a.v_win + (int64_t)h * a.win_sh + c;
-  for (int t0 = sl; t0 < a.win_len; t0 += 64) {   // 8 tokens per slice per pass, loads first
-    float vv[8];
+  // ---- the partials' maxima (later batches: the maxima alone)
 #pragma unroll
-    for (int u = 0; u < 8; ++u) vv[u] = half_bits_to_float(vw[(int64_t)min(t0 + 8 * u, a.win_len - 1) * kD]);
+  for (int k = 0; k < kSpMergeBatch; ++k)
+    if (slot + 64 * k < P) mx = fmaxf(mx, ml[k].x);
+  for (int p0 = 64 * kSpMergeBatch; p0 < P; p0 += 64)
+    if (p0 + slot < P) mx = fmaxf(mx, pml[2 * (int64_t)(p0 + slot)]);
+  const float M = reduce256<true>(mx, s_red);   // its barriers also publish s_s
+  // ---- weights and sums: L counts each partial and token once (quad 0)
+  float L = 0.f;
+  float4_t A = {0.f, 0.f, 0.f, 0.f}, W = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (t0 + 8 * u < a.win_len) Aw = fmaf(s_s[t0 + 8 * u], vv[u], Aw);
-  }
-  s_acc[sl][c] = A;
-  s_accw[sl][c] = Aw;
-  __syncthreads();
-  // the groups' sums are in the rotated value domain: H128 over the channel
-  // index (bits 0..5 within a wave by lane exchange, bit 6 across the two
-  // waves through LDS), then the signs and 1/128 (the value codec's inverse)
-  float x = 0.f;
-  if (tid < kD) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x += s_acc[j][c];
-#pragma unroll
-    for (int hb = 1; hb < 64; hb <<= 1) {
-      const float o = __shfl_xor(x, hb);
-      x = (c & hb) ? o - x : x + o;
+  for (int k = 0; k < kSpMergeBatch; ++k)
+    if (slot + 64 * k < P) {
+      const float w = __expf(ml[k].x - M);
+      if (c4 == 0) L = fmaf(w, ml[k].y, L);
+      A = f4_fma(w, y[k], A);
     }
-    s_h[c] = x;
+  for (int p0 = 64 * kSpMergeBatch; p0 < P; p0 += 64 * kSpMergeBatch) {
+#pragma unroll
+    for (int k = 0; k < kSpMergeBatch; ++k) load_part(min(p0 + slot + 64 * k, P - 1), ml[k], y[k]);
+#pragma unroll
+    for (int k = 0; k < kSpMergeBatch; ++k)
+      if (p0 + slot + 64 * k < P) {
+        const float w = __expf(ml[k].x - M);
+        if (c4 == 0) L = fmaf(w, ml[k].y, L);
+        A = f4_fma(w, y[k], A);
+      }
+  }
+  for (int t0 = 0; t0 < T; t0 += 128) {
+    if (t0 > 0) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        vr[k] = *reinterpret_cast<const uint2*>(vbase + (int64_t)min(t0 + slot + 64 * k, T - 1) * kD + c0);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int t = t0 + slot + 64 * k;
+      if (t < T) {
+        const float w = __expf(s_s[t] - M);
+        if (c4 == 0) L += w;
+        const float4_t v = {half_bits_to_float(vr[k].x & 0xffffu), half_bits_to_float(vr[k].x >> 16),
+                            half_bits_to_float(vr[k].y & 0xffffu), half_bits_to_float(vr[k].y >> 16)};
+        W = f4_fma(w, v, W);
+      }
+    }
+  }
+  // ---- sums over the slots: the lanes of a wave with this quad, then the waves
+#pragma unroll
+  for (int o = 4; o <= 32; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      A[e] += __shfl_xor(A[e], o);
+      W[e] += __shfl_xor(W[e], o);
+    }
+  const float Ls = reduce256<false>(L, s_red);
+  if ((tid & 63) < 4) {
+    s_sum[tid >> 6][c4] = A;
+    s_sumw[tid >> 6][c4] = W;
   }
   __syncthreads();
-  if (tid < kD) {
-    const float o = s_h[c ^ 64];
-    x = (c & 64) ? o - x : x + o;
-    float w = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) w += s_accw[j][c];
-    const float v = x / (float)kD;
-    store_elem(a.out, row * kD + c, ((sign_neg(a.v_sign_bits, c) ? -v : v) + w) / L, a.out_dtype);
+  if (tid < 64) {   // wave 0; lanes 0..15 hold the chunk's channels
+    const int cc = tid & 15, q4 = cc >> 2, e = cc & 3;
+    float x = (s_sum[0][q4][e] + s_sum[1][q4][e]) + (s_sum[2][q4][e] + s_sum[3][q4][e]);
+    const float w = (s_sumw[0][q4][e] + s_sumw[1][q4][e]) + (s_sumw[2][q4][e] + s_sumw[3][q4][e]);
+    x = h16_lanes(x, cc);   // the Hadamard's bits 0..3, then the codec's signs and 1/128
+    const int c = 16 * chunk + cc;
+    if (tid < 16) store_elem(a.out, row * kD + c, ((sign_neg(a.v_sign_bits, c) ? -x : x) * (1.0f / kD) + w) / Ls,
+                             a.out_dtype);
   }
-}
-
-// First stage of the merge for many groups: grid (n_runs, G, h_kv), block 256
-// (2 slices x 128 channels).  Workgroup r folds the partials of groups
-// [64 r, 64 r + 64) of one (head, query) into one partial of the same form
-// (m = their max, l and the channel sums weighted by e^(m_i - m)), written to
-// run r of the scratch rows; the per-query kernel above then merges the runs.
-constexpr int kSpRun = 64;
-constexpr int kSpMaxRuns = kSpMergeMaxGroups / kSpRun;
-
-struct SpFoldKArgs {
-  int G, n_groups, n_runs;
-  const float* partials;
-  float* runs;   // [h_kv][G][n_runs][130]
-};
-
-__global__ __launch_bounds__(256) void spectral_fold_kernel(const SpFoldKArgs a) {
-  const int r = blockIdx.x, g = blockIdx.y, h = blockIdx.z, tid = threadIdx.x, c = tid & 127, sl = tid >> 7;
-  __shared__ float s_w[kSpRun];
-  __shared__ float s_ml[2];
-  __shared__ float s_acc[kD];
-  const int64_t row = (int64_t)h * a.G + g;
-  const float* pt = a.partials + (row * a.n_groups + (int64_t)r * kSpRun) * 130;
-  const int n = min(kSpRun, a.n_groups - r * kSpRun);
-  // the run's channel sums, every load issued before any is used
-  float v[kSpRun / 2];
-#pragma unroll
-  for (int k = 0; k < kSpRun / 2; ++k) v[k] = pt[(int64_t)min(2 * k + sl, n - 1) * 130 + 2 + c];
-  if (tid < 64) {   // one wave: the weights and the run's (m, l)
-    const float m = tid < n ? pt[(int64_t)tid * 130] : -INFINITY;
-    const float l = tid < n ? pt[(int64_t)tid * 130 + 1] : 0.f;
-    float M = m;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    const float w = tid < n ? __expf(m - M) : 0.f;
-    float L = w * l;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o);
-    s_w[tid] = w;
-    if (tid == 0) { s_ml[0] = M; s_ml[1] = L; }
-  }
-  __syncthreads();
-  float acc = 0.f;
-#pragma unroll
-  for (int k = 0; k < kSpRun / 2; ++k) acc = fmaf(s_w[2 * k + sl], v[k], acc);   // weight 0 past n
-  if (sl == 1) s_acc[c] = acc;
-  __syncthreads();
-  float* dst = a.runs + (row * a.n_runs + r) * 130;
-  if (sl == 0) dst[2 + c] = acc + s_acc[c];
-  if (tid < 2) dst[tid] = s_ml[tid];
 }
 
 static PageLayout value_layout(int h_kv) {
@@ -1262,20 +1334,11 @@ extern "C" int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* st
   SpMergeKArgs k{};
   k.h_kv = a->h_kv; k.G = a->n_q_groups; k.n_groups = a->n_groups; k.q_dtype = a->q_dtype;
   k.win_len = a->win_len; k.out_dtype = a->out_dtype; k.partials = a->partials; k.q = a->q;
-  if (a->scratch && a->n_groups > 2 * kSpRun) {   // fold runs of 64 groups first, on many CUs
-    SpFoldKArgs f{};
-    f.G = a->n_q_groups; f.n_groups = a->n_groups; f.n_runs = (a->n_groups + kSpRun - 1) / kSpRun;
-    f.partials = a->partials; f.runs = a->scratch;
-    hipLaunchKernelGGL(spectral_fold_kernel, dim3(f.n_runs, a->n_q_groups, a->h_kv), dim3(256), 0,
-                       (hipStream_t)stream, f);
-    k.partials = a->scratch;
-    k.n_groups = f.n_runs;
-  }
   k.k_win = a->k_win; k.v_win = a->v_win; k.sm_scale = a->sm_scale; k.out = a->out;
   k.win_sh = a->win_stride_h ? a->win_stride_h : (int64_t)a->win_len * kD;
   for (int i = 0; i < 4; ++i) k.v_sign_bits[i] = a->v_sign_bits[i];
-  hipLaunchKernelGGL(spectral_merge_kernel, dim3(a->n_q_groups, a->h_kv), dim3(kSpMergeThreads), 0,
-                     (hipStream_t)stream, k);
+  hipLaunchKernelGGL(spectral_merge_kernel, dim3(kD / 16, a->n_q_groups, a->h_kv), dim3(256), 0, (hipStream_t)stream,
+                     k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     bmx_set_error(std::string(fn) + ": launch: " + hipGetErrorString(e));

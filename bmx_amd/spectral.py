@@ -247,7 +247,7 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     Decode form: with q (h_kv, G, 128) the kernel also writes scores
     (h_kv, G, R) fp32, q . k of the rotated keys for rows 0 .. n_tokens - 1
     (no softmax scale); out may then be (None, V) and no dense keys are
-    written.  Partial form: with q and partials (h_kv, G, partial_count(), 130)
+    written.  Partial form: with q and partials (h_kv, G, 130 * partial_count())
     fp32 the kernel writes each 128-token block's (or 64-token group's)
     softmax partial of the scaled scores (m, l, P.V; see include/bmx_spectral.h) and no dense rows;
     out is then unused."""
@@ -265,8 +265,8 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
         a = _partial_args(dp, k_pages, k_table, v_pages, v_table, n_tokens, consts, q, apply_rope, sm_scale)
         n_parts = _lib.lib().bmx_spectral_partial_count(ct.byref(a))
         _need(partials.dtype == torch.float32 and partials.is_contiguous()
-              and tuple(partials.shape) == (dp.h_kv, q.shape[1], n_parts, 130),
-              f"partials must be fp32 (h_kv, G, {n_parts}, 130): partial_count() per row")
+              and tuple(partials.shape) == (dp.h_kv, q.shape[1], 130 * n_parts),
+              f"partials must be fp32 (h_kv, G, 130 * {n_parts}): partial_count() per row")
         a.partials = _ptr(partials)
         _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
         return partials
@@ -323,7 +323,7 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
           "q (h_kv, G, 128) with h_kv of the pack")
     pt = None
     if n_tokens > 0:
-        pt = torch.empty(h, G, partial_count(dp, n_tokens, q, apply_rope), 130, dtype=torch.float32,
+        pt = torch.empty(h, G, 130 * partial_count(dp, n_tokens, q, apply_rope), dtype=torch.float32,
                          device=q.device)
         dequant(dp, k_pages, k_table, v_pages, v_table, n_tokens, consts, apply_rope=apply_rope,
                 dtype=torch.float16, q=q, partials=pt, sm_scale=sm_scale)
@@ -337,15 +337,12 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
     _need(out_dtype in _V_DTYPES, "out_dtype must be fp16, bf16 or fp32")
     out = torch.empty(h, G, d, dtype=out_dtype, device=q.device)
     a = _lib.SpectralMergeArgs()
-    n_parts = 0 if pt is None else pt.shape[2]
+    n_parts = 0 if pt is None else pt.shape[2] // 130
     a.h_kv, a.n_q_groups, a.n_groups = h, G, n_parts
     a.partials, a.q, a.q_dtype = _ptr(pt), _ptr(q), _V_DTYPES[q.dtype]
     a.k_win, a.v_win, a.win_len = (_ptr(k_win), _ptr(v_win), T) if T else (None, None, 0)
     a.win_stride_h = k_win.stride(0) if T else 0
     a.sm_scale, a.out, a.out_dtype = float(sm_scale), _ptr(out), _V_DTYPES[out_dtype]
     a.v_sign_bits[:] = consts.sign_bits
-    n_runs = -(-n_parts // 64)
-    scratch = torch.empty(h, G, n_runs, 130, dtype=torch.float32, device=q.device) if n_runs else None
-    a.scratch = _ptr(scratch)
     _lib.check(_lib.lib().bmx_spectral_merge(ct.byref(a), _stream(q.device)), "bmx_spectral_merge")
     return out

@@ -110,18 +110,23 @@ typedef struct bmx_spectral_dequant_args {
   int32_t n_q_groups;          /* 1..16 */
   float* scores;               /* [h_kv][n_q_groups][out_rows] fp32 */
   /* Partial form (with q): instead of scores and values, each 64-token group's
-   * softmax partial per (head, query): partials[((h G + g) n_parts + grp) 130 + e],
-   * e = 0: m = max of the scaled scores, 1: l = sum of exp(s - m) (the fp16
-   * weights), 2 + c: in the rotated value domain, the sum of the weights
-   * times the token norms times the codebook levels of rotated channel c
-   * (fp32 accumulation of fp16 operands; the values are that sum's inverse
-   * Hadamard, signs and 1/128); n_parts = bmx_spectral_partial_count(args):
-   * one partial per 128-token block when the two key pages of a block fit
-   * in LDS together (2 k_page_bytes <= 57344), apply_rope is 2 and n_tokens
-   * a multiple of 128, else one per 64-token group.  The
-   * caller merges the groups' partials (m = max m_i, l = sum l_i e^(m_i - m),
-   * out = sum acc_i e^(m_i - m) / l) with the window's.  v_out and scores may
-   * then be NULL. */
+   * or 128-token block's softmax partial per (head, query), in the rows
+   * r = h G + g of 130 n_parts floats each: at r 130 n_parts + 2p, partial
+   * p's m = max of the scaled scores and l = sum of exp(s - m) (the fp16
+   * weights); at r 130 n_parts + 2 n_parts + 16 (k n_parts + p) + j, its
+   * channel c = 16k + j: channel c of the Hadamard over the channel index's
+   * bits 4..6 (unnormalized, pairs (a, b) -> (a + b, a - b); H8 over k) of
+   * the rotated-domain sums of the weights times the token norms times the
+   * codebook levels (fp32 accumulation of fp16 operands): the values are the
+   * merged sums' Hadamard over bits 0..3 (H16 over j), the codec's signs and
+   * 1/128;
+   * n_parts = bmx_spectral_partial_count(args): one partial per 128-token
+   * block when the two key pages of a block fit in LDS together
+   * (2 k_page_bytes <= 57344), apply_rope is 2 and n_tokens a multiple of
+   * 128, else one per 64-token group.  The caller merges the partials
+   * (m = max m_i, l = sum l_i e^(m_i - m), out = signs * H16(sum acc_i
+   * e^(m_i - m)) / (128 l)) with the window's.  v_out and scores may then be
+   * NULL. */
   float* partials;
   float sm_scale;
 } bmx_spectral_dequant_args;
@@ -145,10 +150,7 @@ typedef struct bmx_spectral_merge_args {
   float sm_scale;
   void* out;                   /* [h_kv][n_q_groups][128], dtype out_dtype */
   int32_t out_dtype;
-  uint32_t v_sign_bits[4];     /* the value codec's Hadamard signs (the partials are rotated) */
-  float* scratch;              /* NULL, or device [h_kv][n_q_groups][ceil(n_groups / 64)][130] fp32:
-                                  above 128 groups the partials are first folded in runs of 64
-                                  groups there, on many workgroups, then merged */
+  uint32_t v_sign_bits[4];     /* the value codec's signs, applied to the partials' sums */
   int64_t win_stride_h;        /* elements between heads in k_win / v_win (0: 128 win_len) */
 } bmx_spectral_merge_args;
 

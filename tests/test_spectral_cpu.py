@@ -223,11 +223,11 @@ def test_dequant_table_checks_precede_every_form():
     vp = torch.zeros(S // 16, dp.v_page_bytes, dtype=torch.uint8)
     kt, vt = torch.arange(S // 64, dtype=torch.int32), torch.arange(S // 16, dtype=torch.int32)
     q = torch.zeros(2, 4, 128)
-    part = torch.zeros(2, 4, S // 64, 130)
+    part = torch.zeros(2, 4, 130 * (S // 64))
     bad = [(kt[:-1], vt, S), (kt, vt[:-1], S), (kt.long(), vt, S), (kt, vt.long(), S), (kt, vt, S - 32)]
     for k_t, v_t, n in bad:
         with pytest.raises(ValueError, match="k_table|multiple of 64"):
             spectral.dequant(dp, kp, k_t, vp, v_t, n, consts, apply_rope=k2b.ROPE_EXACT, q=q,
-                             partials=part if n == S else torch.zeros(2, 4, n // 64, 130))
+                             partials=part if n == S else torch.zeros(2, 4, 130 * (n // 64)))
         with pytest.raises(ValueError, match="k_table|multiple of 64"):
             spectral.dequant(dp, kp, k_t, vp, v_t, n, consts)
