@@ -460,6 +460,9 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   for (; kq < n_narrow_pairs; ++kq) pair(kq, std::false_type{});
   for (; kq < n_pairs; ++kq) pair(kq, std::true_type{});
   if ((n_steps & 1) && head_ok) mfma_step(n_steps - 1, 2 * (n_pairs & 1), std::true_type{});
+  // the last step's A factors read the key page, whose space takes the
+  // staging tiles below
+  if (n_steps & 1) __syncthreads();
 
   // query fragments (decode form), loaded after the main loop: the MFMA B operand of the scores, lane
   // 16q + n: query n, K index 8q + 2i + e = channel 16bb + 4q + i + 64e
@@ -893,21 +896,24 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     }
     sct[tt] = sc;
   }
-  // ---- the two halves of a head add their scores: through LDS (the pages'
-  // space, free after the loop), token tiles 0..3 then 4..7 ----
-  float4_t* xch = reinterpret_cast<float4_t*>(sp_dyn);   // [8 waves][4 tiles][64 lanes]
+  // ---- the two halves of a head add their scores through LDS, in one
+  // round: token tiles 0..3 in the pages' space, 4..7 in the code tiles'
+  // (both free after the loop) ----
+  float4_t* xch0 = reinterpret_cast<float4_t*>(sp_dyn);        // [8 waves][4 tiles][64 lanes]
+  float4_t* xch1 = reinterpret_cast<float4_t*>(&s_b[0][0][0]);
+  __syncthreads();   // every wave is past the last step (whose A factors read the pages)
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int k = 0; k < 4; ++k) {
+    xch0[(wave * 4 + k) * 64 + lane] = sct[k];
+    xch1[(wave * 4 + k) * 64 + lane] = sct[4 + k];
+  }
+  __syncthreads();   // also: every wave's scores read s_cs, which takes the H8 exchange below
 #pragma unroll
-    for (int k = 0; k < 4; ++k) xch[(wave * 4 + k) * 64 + lane] = sct[4 * half + k];
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float4_t o = xch[((wave ^ 1) * 4 + k) * 64 + lane];
-      // the same sum in both waves: the lower half's value first
-      sct[4 * half + k] = r2 == 0 ? sct[4 * half + k] + o : o + sct[4 * half + k];
-    }
-    __syncthreads();
+  for (int k = 0; k < 4; ++k) {
+    const float4_t o0 = xch0[((wave ^ 1) * 4 + k) * 64 + lane], o1 = xch1[((wave ^ 1) * 4 + k) * 64 + lane];
+    // the same sum in both waves: the lower half's value first
+    sct[k] = r2 == 0 ? sct[k] + o0 : o0 + sct[k];
+    sct[4 + k] = r2 == 0 ? sct[4 + k] + o1 : o1 + sct[4 + k];
   }
   // lane 16q + n holds query n's scores of tokens 16tt + 4q + i
   float m = -INFINITY;
@@ -952,8 +958,9 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     }
   }
   // H8 over the block index ct = 4 r2 + c: c in registers, r2 (the
-  // channel's bit 6) with the head's other wave through LDS (the exchange's
-  // space, read out above); the merge applies H16 over n
+  // channel's bit 6) with the head's other wave through LDS (the RoPE
+  // table's space, read before the barrier above); the merge applies H16
+  // over n
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -965,7 +972,7 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
           pv[c][i] = u + w;
           pv[c | sb][i] = u - w;
         }
-  float4_t* xv = reinterpret_cast<float4_t*>(sp_dyn);   // [8 waves][4 blocks][64 lanes]
+  float4_t* xv = reinterpret_cast<float4_t*>(&s_cs[0][0]);   // [8 waves][4 blocks][64 lanes]: 32 KB
 #pragma unroll
   for (int c = 0; c < 4; ++c) xv[(wave * 4 + c) * 64 + lane] = pv[c];
   __syncthreads();
