@@ -312,10 +312,10 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   // the key page's 16-byte chunks (threads past the last chunk re-read it: no
   // branch around the loads)
   const int n16 = a.k_page_bytes >> 4;
-  uint4 kpw[kSpPageLoads];
+  u32x4_t kpw[kSpPageLoads];   // a native vector type: an array of uint4 stays in scratch
 #pragma unroll
   for (int i = 0; i < kSpPageLoads; ++i)
-    kpw[i] = reinterpret_cast<const uint4*>(page)[min(tid + 512 * i, n16 - 1)];
+    kpw[i] = reinterpret_cast<const u32x4_t*>(page)[min(tid + 512 * i, n16 - 1)];
   const uint32_t tabv = (uint32_t)a.slice_tab[min(tid, n_sl - 1)];   // n_sl <= 134 < 512
   uint2 vcd[4], nrm[4];
 #pragma unroll
@@ -379,7 +379,7 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   if (tid < n_sl) s_tab[tid] = tabv;
 #pragma unroll
   for (int i = 0; i < kSpPageLoads; ++i)
-    if (tid + 512 * i < n16) reinterpret_cast<uint4*>(kp)[tid + 512 * i] = kpw[i];
+    if (tid + 512 * i < n16) reinterpret_cast<u32x4_t*>(kp)[tid + 512 * i] = kpw[i];
   const int n_steps = a.c_pad32 / 32;
   // a barrier: s_tab, s_cbl, the RoPE table, the key page
   const int n_narrow = sp_narrow_steps(tabv, tid, n_sl, n_steps);
@@ -681,12 +681,12 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
   const uint8_t* pg0 = a.k_pages + clamp_page(a.k_table[2 * blk], a.n_k_pool) * (int64_t)a.k_page_bytes;
   const uint8_t* pg1 = a.k_pages + clamp_page(a.k_table[2 * blk + 1], a.n_k_pool) * (int64_t)a.k_page_bytes;
   constexpr int kLoads = (kSpBlkMaxPages / 2 + 16 * 512 - 1) / (16 * 512);   // per page per thread
-  uint4 kw0[kLoads], kw1[kLoads];
+  u32x4_t kw0[kLoads], kw1[kLoads];   // a native vector type: an array of uint4 stays in scratch
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) {
     const int c = min(tid + 512 * i, p16 - 1);
-    kw0[i] = reinterpret_cast<const uint4*>(pg0)[c];
-    kw1[i] = reinterpret_cast<const uint4*>(pg1)[c];
+    kw0[i] = reinterpret_cast<const u32x4_t*>(pg0)[c];
+    kw1[i] = reinterpret_cast<const u32x4_t*>(pg1)[c];
   }
   const uint32_t tabv = (uint32_t)a.slice_tab[min(tid, n_sl - 1)];
   // value pages: thread (local head tid >> 7, page (tid >> 6) & 1 + 2 k, lane)
@@ -746,8 +746,8 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
 #pragma unroll
   for (int i = 0; i < kLoads; ++i)
     if (tid + 512 * i < n16) {
-      reinterpret_cast<uint4*>(kp0)[tid + 512 * i] = kw0[i];
-      reinterpret_cast<uint4*>(kp1)[tid + 512 * i] = kw1[i];
+      reinterpret_cast<u32x4_t*>(kp0)[tid + 512 * i] = kw0[i];
+      reinterpret_cast<u32x4_t*>(kp1)[tid + 512 * i] = kw1[i];
     }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
