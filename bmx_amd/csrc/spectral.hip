@@ -200,8 +200,8 @@ __device__ __forceinline__ uint2 sp_codes4(uint64_t word, int w, int b) {
   uint32_t c[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) c[e] = ((uint32_t)(word >> (e * w)) & mask) | 0x6400u;
-  const _Float16 off = (_Float16)(float)(1024 + (1 << (b - 1)));
-  const half2_t o2 = {off, off};
+  const uint32_t off = 0x6400u | (1u << (b - 1));   // fp16 1024 + 2^(b-1): spacing 1 in [1024, 2048)
+  const half2_t o2 = as_h2(off | (off << 16));
   return make_uint2(as_u32(as_h2(c[0] | (c[1] << 16)) - o2), as_u32(as_h2(c[2] | (c[3] << 16)) - o2));
 }
 
@@ -249,8 +249,11 @@ constexpr uint32_t kHalfOnes = 0x3C003C00u;   // fp16 (1, 1)
 // else 1) and the A-side one (1 for a narrow tier, else the steps; 0 past the
 // last slice, whose codes are stored as 0 too), from the key page in LDS.
 __device__ __forceinline__ uint4 sp_b_factor(const uint8_t* kp, int s_clamped, int b) {
+  // read always, chosen by a mask: a select of the load became a branch
+  // around it, splitting the main loop's basic block
   const uint4 r = *reinterpret_cast<const uint4*>(kp + 16 * s_clamped);
-  return (uint32_t)b < kSpWideTier ? r : make_uint4(kHalfOnes, kHalfOnes, kHalfOnes, kHalfOnes);
+  const uint32_t keep = (uint32_t)b < kSpWideTier ? 0xFFFFFFFFu : 0u, ones = kHalfOnes & ~keep;
+  return make_uint4((r.x & keep) | ones, (r.y & keep) | ones, (r.z & keep) | ones, (r.w & keep) | ones);
 }
 
 __device__ __forceinline__ half8_t sp_a_factor(const uint8_t* kp, const uint32_t* s_tab, int s, int n_sl) {
