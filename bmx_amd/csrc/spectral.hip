@@ -62,50 +62,59 @@ struct SpEncodeKArgs {
   const int32_t* page_ids;
 };
 
-// grid (ceil(c_pad / 64), n_groups), block 64: thread j of block x codes page
-// column 64x + j of group y.  Y[t][j] for the group's 64 tokens accumulates in
-// registers over the C channels, staged 64 at a time through LDS (every lane
-// reads the same key element: a broadcast); then the column's step (max|Y| /
-// qmax and 10 rounds of <Y, Q> / <Q, Q>), its codes, and the block's 8 slices
-// assembled in LDS and written with dword stores.
-__global__ __launch_bounds__(64) void spectral_encode_kernel(const SpEncodeKArgs a) {
-  __shared__ float s_m[kGroup][kSpCh + 1];
+// grid (ceil(c_pad / 64), n_groups), block 512: wave w of block x
+// accumulates Y[t][j] for tokens 8w .. 8w + 7 of group y and page column
+// 64x + j (lane j) over the C channels, staged 64 at a time through LDS with
+// the chunk's enc rows (every product and sum rounded on its own, channels in
+// order); then wave 0's lane j takes column 64x + j's 64 values from LDS for
+// the step (max|Y| / qmax and 10 rounds of <Y, Q> / <Q, Q>) and its codes,
+// and the block's 8 slices are assembled in LDS and written with dword stores.
+__global__ __launch_bounds__(512) void spectral_encode_kernel(const SpEncodeKArgs a) {
+  __shared__ float s_m[kGroup][kSpCh + 1];   // the chunk's keys: [token][channel]
+  __shared__ float s_e[kSpCh][64];           // the chunk's enc rows: [channel][column]
+  __shared__ float s_y[kGroup][65];          // Y: [token][column]
   __shared__ uint32_t s_code[8 * kGroup * 8 / 4];   // 8 slices of at most 512 bytes
-  const int lane = threadIdx.x, j = blockIdx.x * 64 + lane, g = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = blockIdx.x * 64 + lane, g = blockIdx.y;
   const bool active = j < a.c_pad;
-  float y[kGroup];
+  float y[8];
 #pragma unroll
-  for (int t = 0; t < kGroup; ++t) y[t] = 0.f;
+  for (int t = 0; t < 8; ++t) y[t] = 0.f;
   for (int c0 = 0; c0 < a.C; c0 += kSpCh) {
-    __syncthreads();
+    __syncthreads();   // the previous chunk read
     const int c = c0 + lane, h = c >> 7, d = c & (kD - 1);
-    for (int t = 0; t < kGroup; ++t)
-      s_m[t][lane] = sp_load(a.k, h * a.ksh + (int64_t)(g * kGroup + t) * a.kst + d, a.k_dtype);
-    __syncthreads();
-    if (active) {
-      for (int cc = 0; cc < kSpCh; ++cc) {
-        const float e = a.encp[(int64_t)(c0 + cc) * a.c_pad + j];
 #pragma unroll
-        for (int t = 0; t < kGroup; ++t) y[t] = __fadd_rn(y[t], __fmul_rn(s_m[t][cc], e));
-      }
+    for (int t = 0; t < 8; ++t)
+      s_m[8 * wave + t][lane] = sp_load(a.k, h * a.ksh + (int64_t)(g * kGroup + 8 * wave + t) * a.kst + d, a.k_dtype);
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      s_e[8 * wave + r][lane] = active ? a.encp[(int64_t)(c0 + 8 * wave + r) * a.c_pad + j] : 0.f;
+    __syncthreads();
+#pragma unroll 4
+    for (int cc = 0; cc < kSpCh; ++cc) {
+      const float e = s_e[cc][lane];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) y[t] = __fadd_rn(y[t], __fmul_rn(s_m[8 * wave + t][cc], e));
     }
   }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) s_y[8 * wave + t][lane] = y[t];
+  __syncthreads();
   const int s = j >> 3, k = j & 7;
   const uint32_t tab = active ? (uint32_t)a.slice_tab[s] : 0u;
   const int b = active ? (int)(tab >> 24) : 2, w = sp_width(b);
   const float qmax = (float)((1 << (b - 1)) - 1);
   float scale = 1e-12f;
-  if (active) {
+  if (active && wave == 0) {
     float amax = 0.f;
-#pragma unroll
-    for (int t = 0; t < kGroup; ++t) amax = fmaxf(amax, fabsf(y[t]));
+    for (int t = 0; t < kGroup; ++t) amax = fmaxf(amax, fabsf(s_y[t][lane]));
     scale = fmaxf(amax, 1e-12f) / qmax;
     for (int it = 0; it < 10; ++it) {
       float num = 0.f, den = 0.f;
-#pragma unroll
       for (int t = 0; t < kGroup; ++t) {
-        const float qv = fminf(fmaxf(rintf(y[t] / scale), -qmax - 1.f), qmax);
-        num = __fadd_rn(num, __fmul_rn(y[t], qv));
+        const float yv = s_y[t][lane];
+        const float qv = fminf(fmaxf(rintf(yv / scale), -qmax - 1.f), qmax);
+        num = __fadd_rn(num, __fmul_rn(yv, qv));
         den = __fadd_rn(den, __fmul_rn(qv, qv));
       }
       scale = fmaxf(num / fmaxf(den, 1e-12f), 1e-12f);
@@ -116,14 +125,13 @@ __global__ __launch_bounds__(64) void spectral_encode_kernel(const SpEncodeKArgs
   const uint32_t tab0 = (uint32_t)a.slice_tab[s_first], tabl = (uint32_t)a.slice_tab[s_last];
   const int base = (int)(tab0 & 0xFFFFFFu);
   const int n_words = ((int)(tabl & 0xFFFFFFu) + kGroup * sp_width((int)(tabl >> 24)) - base) >> 2;
-  for (int i = lane; i < n_words; i += 64) s_code[i] = 0u;
+  for (int i = tid; i < n_words; i += 512) s_code[i] = 0u;
   __syncthreads();
-  if (active) {
+  if (active && wave == 0) {
     const int bit0 = ((int)(tab & 0xFFFFFFu) - base) * 8 + k * w;
     const uint32_t bias = 1u << (b - 1);
-#pragma unroll
     for (int t = 0; t < kGroup; ++t) {
-      const float qv = fminf(fmaxf(rintf(y[t] / scale), -qmax - 1.f), qmax);
+      const float qv = fminf(fmaxf(rintf(s_y[t][lane] / scale), -qmax - 1.f), qmax);
       const uint32_t stored = (uint32_t)((int)qv + (int)bias);
       const int bit = bit0 + t * w * 8;
       atomicOr(&s_code[bit >> 5], stored << (bit & 31));
@@ -132,8 +140,8 @@ __global__ __launch_bounds__(64) void spectral_encode_kernel(const SpEncodeKArgs
   __syncthreads();
   uint8_t* page = a.pages + clamp_page(a.page_ids[g], a.n_pool) * (int64_t)a.page_bytes;
   uint32_t* dst = reinterpret_cast<uint32_t*>(page + base);
-  for (int i = lane; i < n_words; i += 64) dst[i] = s_code[i];
-  if (active) reinterpret_cast<uint16_t*>(page)[j] = float_to_half_bits(scale);
+  for (int i = tid; i < n_words; i += 512) dst[i] = s_code[i];
+  if (active && wave == 0) reinterpret_cast<uint16_t*>(page)[j] = float_to_half_bits(scale);
 }
 
 struct SpDequantKArgs {
@@ -1257,7 +1265,7 @@ extern "C" int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* 
   k.page_bytes = a->L.k_page_bytes;
   k.k = a->k_pre; k.ksh = a->k_sh; k.kst = a->k_st;
   k.encp = a->enc_perm; k.slice_tab = a->L.slice_tab; k.pages = a->k_pages; k.page_ids = a->k_page_ids;
-  hipLaunchKernelGGL(spectral_encode_kernel, dim3((a->L.c_pad + 63) / 64, a->n_groups), dim3(64), 0, st, k);
+  hipLaunchKernelGGL(spectral_encode_kernel, dim3((a->L.c_pad + 63) / 64, a->n_groups), dim3(512), 0, st, k);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) {
     AppendKArgs v{};
