@@ -395,8 +395,10 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   // a barrier: s_tab, s_cbl, the RoPE table, the key page
   const int n_narrow = sp_narrow_steps(tabv, tid, n_sl, n_steps);
 
-  // thread tid decodes codes 4 hf .. 4 hf + 3 of slice 4 step + sq, token t
-  const int dt = tid >> 3, dsq = (tid >> 1) & 3, dhf = tid & 1;
+  // lane (sq, hf, t) of wave w decodes codes 4 hf .. 4 hf + 3 of slice 4 step + sq, token 8w + t
+  // (a row of 16 lanes shares one slice, so that its code-word reads fall in
+  // distinct banks: lanes on 4 slices 128 B apart hit the same banks)
+  const int dsq = (lane >> 4) & 3, dhf = (lane >> 3) & 1, dt = 8 * wave + (lane & 7);
   auto decode_b = [&](int ks, int buf) {
     // no branch: slices past the last decode the last slice and store zeros
     const int s = 4 * ks + dsq, sc = min(s, n_sl - 1);
@@ -770,8 +772,10 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
   // a barrier: s_tab, s_cbl, s_cs, the key pages, the value codes
   const int n_narrow = sp_narrow_steps(tabv, tid, n_sl, n_steps);
 
-  // thread tid decodes the 8 codes of slice 4 step + (tid & 3), token tid >> 2
-  const int dt = tid >> 2, dsq = tid & 3;
+  // lane (sq, t) of wave w decodes the 8 codes of slice 4 step + sq, token 16w + t
+  // (a row of 16 lanes shares one slice, so that its code-word reads fall in
+  // distinct banks: lanes on 4 slices 128 B apart hit the same banks)
+  const int dsq = (lane >> 4) & 3, dt = 16 * wave + (lane & 15);
   const uint8_t* kpt = dt < kGroup ? kp0 : kp1;
   const int dtp = dt & (kGroup - 1);
   auto decode_b = [&](int ks, int buf) {
