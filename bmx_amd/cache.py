@@ -622,7 +622,8 @@ class PackedStreamingCache(Cache):
                  recent_window: int = 32, pack_v: bool = True, pack_k: bool = True):
         path = packed_path(k_spec, v_spec)
         # spectral: every layer's pack, loaded once (packed_streaming.py:1094-1147)
-        self._packs = spectral.load_packs(k_spec.pack_path, k_spec.budget) if path == "spectral" else {}
+        # decoder variants (dec_quant) applied here, once (spectral.py:1254-1326)
+        self._packs = spectral.load_packs_for_spec(k_spec) if path == "spectral" else {}
         wself = weakref.proxy(self)   # no cache -> closure -> cache cycle
 
         def _make_layer():
@@ -648,11 +649,23 @@ class PackedStreamingCache(Cache):
 
     def bits_per_entry(self) -> tuple:
         """(bpe_k, bpe_v): blended payload bits per entry, averaged across layers
-        (streaming.py:154-260)."""
+        (cache_bits_per_entry, streaming.py:154-260).  Spectral keys, once a
+        layer has committed, also pay the decoder and tier map over the whole
+        sequence at the layer-mean coded and int8 column counts (the charge
+        is linear in both), the int8 count read from each pack's dec_tier."""
         layers = list(self.layers)
         if not layers:
             return float("nan"), float("nan")
-        return (sum(l.bpe_k for l in layers) / len(layers), sum(l.bpe_v for l in layers) / len(layers))
+        bpe_k = sum(l.bpe_k for l in layers) / len(layers)
+        bpe_v = sum(l.bpe_v for l in layers) / len(layers)
+        last = layers[-1]
+        if self.k_spec.arm == "spectral" and last._committed_S_q > 0:
+            c_used = sum(l._pack.c_used for l in layers) / len(layers)
+            c_int8 = sum(0 if l._pack.dec_tier is None else l._pack.c_int8(l._pack.dec_tier)
+                         for l in layers) / len(layers)
+            bpe_k += spectral.mixed_dec_charge(last._h_kv * last._d_head, last.get_seq_length(),
+                                               last._pack.tiers, c_used, c_int8)
+        return bpe_k, bpe_v
 
     def memory_report(self, seq_len: int) -> dict:
         """Dense fp16 bytes vs packed (bpe-derived) bytes (streaming.py:263-305)."""

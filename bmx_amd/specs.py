@@ -15,7 +15,9 @@ pairs the reference's attend() sends to a fused kernel
 * spectral (K4): K ``spectral`` pre-RoPE from a pack file (rtn payload,
   fp32 decoder, 64-token groups), V ``turboquant_mse_perhead`` 2-bit, the
   value codec of the other pre-RoPE pair, under the recipe name
-  ``k4ph_b<budget>``.  The reference's own ``k4_b<budget>`` recipe pairs the
+  ``k4ph_b<budget>``, with the reference's decoder suffixes ``_dec8``,
+  ``_dec8t<T>`` and ``_dec8tl`` (an int8 roundtrip of the decoder when the
+  packs load).  The reference's own ``k4_b<budget>`` recipe pairs the
   spectral keys with the full-C ``turboquant_mse`` values (one 1024-point
   rotation and one norm per token, recipes.py:138-143), which no MI355X
   kernel reads: that name raises rather than answer with another codec.
@@ -27,6 +29,7 @@ route it to.
 from __future__ import annotations
 
 import dataclasses
+import re
 
 
 @dataclasses.dataclass
@@ -42,7 +45,7 @@ class CacheCodecSpec:
     pre_rope: bool = False
     pack_path: str | None = None      # spectral: the pack file (spectral.py:1081-1170)
     budget: float | None = None       # spectral: the pack's budget label
-    dec_quant: str = "fp32"           # spectral: decoder storage (only "fp32" here)
+    dec_quant: str = "fp32"           # spectral: decoder storage: fp32 | int8 | int8_t<T> | int8_tl
     payload_quant: str = "rtn"        # spectral: payload quantizer (only "rtn" here)
 
 
@@ -57,12 +60,9 @@ def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0, pack_
     if arm.startswith("k4ph_b"):
         if not pack_path:
             raise ValueError("k4 arms require --pack-path (a fitted spectral pack file)")
-        budget_str = arm[len("k4ph_b"):]
-        if "_dec8" in budget_str or "_lq" in budget_str:
-            raise NotImplementedError(
-                f"recipe {arm!r}: the int8 decoder and Lloyd payload variants have no MI355X kernels")
+        budget, payload_quant, dec_quant = _k4_variant(arm, "k4ph_b")
         return (CacheCodecSpec(arm="spectral", pre_rope=True, group=group, pack_path=pack_path,
-                               budget=float(budget_str), seed=seed),
+                               budget=budget, seed=seed, dec_quant=dec_quant, payload_quant=payload_quant),
                 CacheCodecSpec(arm="turboquant_mse_perhead", bits=2, seed=seed))
     if arm == "kivi":
         return (CacheCodecSpec(arm="rtn_channel", bits=2, group=group, seed=seed),
@@ -73,6 +73,27 @@ def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0, pack_
     return (CacheCodecSpec(arm="lowrank_rtn_channel", bits=3, rank=rank, group=group, seed=seed,
                            pre_rope=True),
             CacheCodecSpec(arm="turboquant_mse_perhead", bits=2, seed=seed))
+
+
+_K4_SUFFIX = re.compile(r"(?P<budget>.+?)(?P<lq>_lq)?(?P<dec>_dec8(?:tl|t[^_]*)?)?")
+
+
+def _k4_variant(arm: str, prefix: str) -> tuple:
+    """(budget, payload_quant, dec_quant) of a k4 recipe name
+    ``<prefix><budget>[_lq][_dec8 | _dec8t<T> | _dec8tl]`` (recipes.py:
+    100-150): "_lq" selects the Lloyd payload and sits between the budget and
+    the decoder suffix; "_dec8" stores every coded decoder column int8,
+    "_dec8t<T>" those of tiers <= T, "_dec8tl" a certificate-derived
+    threshold per layer."""
+    m = _K4_SUFFIX.fullmatch(arm[len(prefix):])
+    dec = m.group("dec") or ""
+    dec_quant = {"": "fp32", "_dec8": "int8", "_dec8tl": "int8_tl"}.get(dec, "int8_t" + dec[len("_dec8t"):])
+    if "_lq" in m.group("budget") or "_dec8" in m.group("budget"):
+        raise ValueError(f"malformed k4 arm {arm!r}: the form is '{prefix}<budget>[_lq][_dec8|_dec8t<T>|_dec8tl]', "
+                         f"e.g. '{prefix}2.5_lq_dec8tl'")
+    from .spectral import dec_quant_threshold
+    dec_quant_threshold(dec_quant)   # raises on a threshold outside 2..8
+    return float(m.group("budget")), ("lloyd" if m.group("lq") else "rtn"), dec_quant
 
 
 def is_rtn(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> bool:
@@ -115,10 +136,11 @@ def check_spectral(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
     kernels implement."""
     assert k_spec.pre_rope, "spectral K requires pre_rope=True (RoPE is applied at read)"
     assert k_spec.pack_path, "spectral K requires pack_path (a fitted spectral pack file)"
-    if k_spec.dec_quant != "fp32" or k_spec.payload_quant != "rtn":
+    from .spectral import dec_quant_threshold
+    dec_quant_threshold(k_spec.dec_quant)
+    if k_spec.payload_quant != "rtn":
         raise NotImplementedError(
-            f"spectral dec_quant={k_spec.dec_quant!r} payload_quant={k_spec.payload_quant!r}: the MI355X "
-            f"kernels implement the fp32 decoder and the rtn payload")
+            f"spectral payload_quant={k_spec.payload_quant!r}: the MI355X kernels implement the rtn payload")
     if not (v_spec.arm == "turboquant_mse_perhead" and v_spec.bits == 2):
         raise NotImplementedError(
             f"spectral K pairs with V=turboquant_mse_perhead (2 bits) on the MI355X path; got V={v_spec}")

@@ -17,6 +17,7 @@ budgets.
 from __future__ import annotations
 
 import ctypes as ct
+import dataclasses
 import json
 import math
 from dataclasses import dataclass
@@ -45,10 +46,16 @@ class SpectralPack:
     group: int = GROUP
     tiers: tuple = TIERS
     budget: float = float("nan")
+    dec_tier: int | None = None       # the int8 threshold dec was roundtripped at (None: fp32 as loaded)
 
     @property
     def c_used(self) -> int:
         return int((self.bits != 0).sum())
+
+    def c_int8(self, tier_threshold: int) -> int:
+        """Coded directions whose tier is at most tier_threshold: the decoder
+        columns an int8 decoder at that threshold stores (spectral.py:213-220)."""
+        return int(((self.bits > 0) & (self.bits <= tier_threshold)).sum())
 
 
 def allocate_bits(var, budget: float, tiers=TIERS, n_search: int = 40) -> torch.Tensor:
@@ -81,6 +88,109 @@ def payload_bpe(bits: torch.Tensor, group: int = GROUP) -> float:
     (spectral_payload_bpe, spectral.py:602-615)."""
     C = bits.shape[0]
     return float(bits.float().mean()) + 16.0 / group * int((bits != 0).sum()) / C
+
+
+TIER_THRESHOLD_GRID = (2, 3, 4, 5, 6, 8)
+PER_LAYER_TIER = -1   # dec_quant "int8_tl": a threshold per layer, from each pack's certificate
+
+
+def dec_quant_threshold(dec_quant: str) -> int | None:
+    """The int8 tier threshold a ``dec_quant`` string names (spectral.py:
+    1213-1250): "fp32" -> None (no int8 decoder), "int8" -> 8 (every coded
+    column), "int8_t{T}" -> T for 2 <= T <= 8, "int8_tl" -> PER_LAYER_TIER."""
+    if dec_quant == "fp32":
+        return None
+    if dec_quant == "int8":
+        return 8
+    if dec_quant == "int8_tl":
+        return PER_LAYER_TIER
+    t = dec_quant[len("int8_t"):] if dec_quant.startswith("int8_t") else ""
+    if not t.isdigit() or not 2 <= int(t) <= 8:
+        raise ValueError(f"dec_quant must be 'fp32', 'int8', 'int8_tl' or 'int8_t<T>' with 2 <= T <= 8; "
+                         f"got {dec_quant!r}")
+    return int(t)
+
+
+def int8_decoder_roundtrip(dec: torch.Tensor, bits: torch.Tensor, tier_threshold: int | None = None) -> torch.Tensor:
+    """The decoder as an int8 store would give it back (spectral.py:913-944):
+    each selected column c (bits[c] != 0, and bits[c] <= tier_threshold when
+    one is given) becomes q * s with s = fp16(max|dec[:, c]| / 127, floored at
+    1e-12) and q = round-half-even(dec[:, c] / s) clamped to [-127, 127], all
+    in fp32; the other columns are returned unchanged."""
+    dec = dec.float()
+    bits = bits.to(device=dec.device)
+    sel = bits != 0
+    if tier_threshold is not None:
+        sel = sel & (bits <= tier_threshold)
+    out = dec.clone()
+    cols = dec[:, sel]
+    s = (cols.abs().amax(dim=0) / 127.0).clamp_min(1e-12).half().float()
+    out[:, sel] = torch.round(cols / s).clamp(-127.0, 127.0) * s
+    return out
+
+
+def int8_certificate(pack: SpectralPack, tier_threshold: int) -> dict:
+    """Closed-form weighted distortion an int8 decoder at tier_threshold adds
+    (spectral.py:947-960, 1004-1033), in float64: with D = dec_int8 - dec,
+    added = sum_c lam_c |enc^T D[:, c]|^2, payload = sum_c lam_c 4^-bits_c,
+    implied_rel_degradation = added / (payload + added)."""
+    D = int8_decoder_roundtrip(pack.dec, pack.bits, tier_threshold).double() - pack.dec.double()
+    lam = pack.lam.double().clamp_min(0.0)
+    added = float((lam * ((pack.enc.double().T @ D) ** 2).sum(dim=0)).sum())
+    payload = float((lam * torch.pow(4.0, -pack.bits.double())).sum())
+    return {"tier_threshold": int(tier_threshold), "c_used": pack.c_used, "c_int8": pack.c_int8(tier_threshold),
+            "added": added, "payload": payload, "noise_to_signal": added / max(payload, 1e-300),
+            "implied_rel_degradation": added / max(payload + added, 1e-300)}
+
+
+def per_layer_tier_thresholds(packs: dict, bar: float = 0.05) -> dict:
+    """{layer: T}: the last threshold of TIER_THRESHOLD_GRID (scanned in
+    ascending order) whose certificate keeps implied_rel_degradation <= bar,
+    0 when none does (spectral.py:1176-1210).  Pass the packs as loaded: a
+    decoder already roundtripped certifies almost anything."""
+    out = {}
+    for i, pack in packs.items():
+        out[i] = 0
+        for t in TIER_THRESHOLD_GRID:
+            if int8_certificate(pack, t)["implied_rel_degradation"] <= bar:
+                out[i] = t
+    return out
+
+
+def tier_bits(tiers, S: int) -> float:
+    """The tier map's charge per entry: ceil(log2(n_tiers)) bits per channel
+    over S rows (codecs.py:94-96)."""
+    return math.ceil(math.log2(len(tiers))) / S
+
+
+def mixed_dec_charge(C: int, S: int, tiers, c_used: float, c_int8: float) -> float:
+    """Per-entry charge of the decoder and tier map over S rows with c_int8
+    of the c_used coded columns stored int8 (8 bits per entry and one fp16
+    scale per column) and the rest fp16 (spectral.py:1036-1064)."""
+    if not 0 <= c_int8 <= c_used <= C:
+        raise ValueError(f"need 0 <= c_int8 <= c_used <= C; got {c_int8}, {c_used}, {C}")
+    return 8.0 * c_int8 / S + 16.0 * c_int8 / (S * C) + 16.0 * (c_used - c_int8) / S + tier_bits(tiers, S)
+
+
+def load_packs_for_spec(k_spec) -> dict:
+    """{layer: SpectralPack} a cache holds for a spectral key spec
+    (spectral.py:1254-1326): the pack file's layers at the spec's budget,
+    with each decoder int8-roundtripped once here when dec_quant asks for it
+    and dec_tier set to the threshold applied.  "int8_tl" takes each layer's
+    threshold from per_layer_tier_thresholds of the packs as loaded; a layer
+    whose threshold is 0 keeps its fp32 decoder.  Other arms: {}."""
+    thr = dec_quant_threshold(k_spec.dec_quant)
+    if k_spec.arm != "spectral":
+        return {}
+    if not k_spec.pre_rope or not k_spec.pack_path:
+        raise ValueError("a spectral key spec needs pre_rope=True and a pack_path")
+    packs = load_packs(k_spec.pack_path, k_spec.budget)
+    if thr is None:
+        return packs
+    t_map = per_layer_tier_thresholds(packs) if thr == PER_LAYER_TIER else {i: thr for i in packs}
+    return {i: p if t_map[i] == 0 else
+            dataclasses.replace(p, dec=int8_decoder_roundtrip(p.dec, p.bits, t_map[i]), dec_tier=t_map[i])
+            for i, p in packs.items()}
 
 
 def load_packs(path, budget: float) -> dict:

@@ -12,10 +12,17 @@ Reference algorithm (paths under src/bmx):
                                                       cache/spectral.py:763-815,
                                                       quant/rtn.py:10-44
   * spectral_dequant_packed: Y_hat @ dec^T            cache/spectral.py:818-841
+  * int8_decoder_roundtrip, the tiered int8 certificate and the per-layer
+    thresholds it picks                               cache/spectral.py:913-1033,
+                                                      1176-1210
 Pinned by tests/test_spectral_cpu.py against the reference's own outputs
 (tests/golden/spectral.npz): the allocation at three budgets, the tier
 columns, every code and scale of four groups given the reference's Y, and
 the dequantized keys; the encode order below against a float64 product.
+The int8 decoder functions against tests/golden/spectral_variants.npz (the
+roundtrip bit for bit at three thresholds, the certificate at every
+threshold, the per-layer thresholds at three bars), and the certificate
+against a Monte-Carlo estimate of the distortion it states in closed form.
 
 The device restatement fixes two orders the reference leaves to torch:
   * encode: Y[t, j] = sum over c = 0, 1, ... of M[t, c] * enc[c, j], each
@@ -213,3 +220,46 @@ def unpack_pages(pages, layout: Layout):
             codes[:, :, 8 * s + k] = ((word >> np.uint64(k * w)) & np.uint64((1 << w) - 1)).astype(np.int64) \
                 - (1 << (b - 1))
     return codes, scales
+
+
+TIER_THRESHOLD_GRID = (2, 3, 4, 5, 6, 8)
+
+
+def int8_decoder_roundtrip(dec, bits, tier_threshold=None) -> np.ndarray:
+    """fp32 decoder whose columns with 0 < bits (<= tier_threshold if given)
+    are stored int8 with one fp16 absmax scale per column and read back
+    (spectral.py:913-944); round half to even, codes in [-127, 127]."""
+    dec = np.asarray(dec, dtype=np.float32)
+    bits = np.asarray(bits)
+    sel = bits != 0
+    if tier_threshold is not None:
+        sel &= bits <= tier_threshold
+    out = dec.copy()
+    if sel.any():
+        c = dec[:, sel]
+        s = np.maximum(np.abs(c).max(axis=0) / np.float32(127.0), np.float32(1e-12))
+        s = s.astype(np.float16).astype(np.float32)
+        out[:, sel] = np.clip(np.rint(c / s), -127.0, 127.0).astype(np.float32) * s
+    return out
+
+
+def int8_certificate(enc, dec, lam, bits, tier_threshold) -> tuple:
+    """(added, payload, implied_rel_degradation) in float64
+    (spectral.py:947-960): the expected weighted distortion the int8 decoder
+    adds for codes of second moment diag(lam), against the payload's."""
+    D = int8_decoder_roundtrip(dec, bits, tier_threshold).astype(np.float64) - np.asarray(dec, np.float64)
+    lam = np.maximum(np.asarray(lam, np.float64), 0.0)
+    proj = np.asarray(enc, np.float64).T @ D
+    added = float((lam * (proj ** 2).sum(axis=0)).sum())
+    payload = float((lam * 4.0 ** -np.asarray(bits, np.float64)).sum())
+    return added, payload, added / max(payload + added, 1e-300)
+
+
+def per_layer_tier_thresholds(layers: dict, bar: float = 0.05) -> dict:
+    """{layer: largest T of the grid whose certificate stays <= bar, else 0}
+    for layers {i: (enc, dec, lam, bits)} (spectral.py:1176-1210)."""
+    out = {}
+    for i, (enc, dec, lam, bits) in layers.items():
+        ok = [t for t in TIER_THRESHOLD_GRID if int8_certificate(enc, dec, lam, bits, t)[2] <= bar]
+        out[i] = ok[-1] if ok else 0
+    return out

@@ -36,8 +36,15 @@ Functions covered (reference file:line, paths under ``src/bmx``):
                                  763-841; cache/codecs.py:203-287;
                                  quant/rtn.py:10-53
 
+  * k4 variants: int8_decoder_roundtrip, int8_decoder_certificate_tiered,
+    per_layer_tier_thresholds, the Lloyd payload (_lloyd_quantize_packed /
+    _lloyd_dequantize_packed through spectral_quantize_packed /
+    spectral_dequant_packed with quantizer="lloyd")
+                                 cache/spectral.py:648-700, 763-841, 913-1027,
+                                 1176-1210
+
 ``python tests/golden/make_golden.py SRC spectral`` rewrites only the named
-fixture files (codecs, attention, e2e_tiny_llama, spectral).
+fixture files (codecs, attention, e2e_tiny_llama, spectral, spectral_variants).
 """
 
 from __future__ import annotations
@@ -322,8 +329,62 @@ def spectral_fixtures():
     return out
 
 
+def spectral_variant_fixtures():
+    """The k4 recipe variants on spectral.npz's pack (refitted from the same
+    seeds): the int8 decoder roundtrip (blanket and tier-gated), the tiered
+    int8 certificate and the per-layer thresholds it picks, and the Lloyd
+    payload (Gaussian Lloyd-Max codebooks per tier, codes, scales and the
+    dequantized keys of spectral.npz's keys)."""
+    from bmx.cache import codecs
+    from bmx.cache.spectral import (
+        TIER_THRESHOLD_GRID,
+        _unpack_tier_codes,
+        fit_spectral_basis,
+        int8_decoder_certificate_tiered,
+        int8_decoder_roundtrip,
+        pack_from_basis,
+        per_layer_tier_thresholds,
+        spectral_dequant_packed,
+        spectral_quantize_packed,
+        tier_columns,
+    )
+
+    g = torch.Generator().manual_seed(23)
+    C, S = 256, 256
+    lam_true = 40.0 * torch.arange(1, C + 1, dtype=torch.float64) ** -1.3
+    Q, _ = torch.linalg.qr(torch.randn(C, C, generator=g, dtype=torch.float64))
+    mix = (Q * lam_true.sqrt()).mT
+    M_fit = (torch.randn(1024, C, generator=g, dtype=torch.float64) @ mix).float()
+    w = 0.5 + torch.rand(C, generator=g, dtype=torch.float64)
+    Wh, Wh_inv = torch.diag(w.sqrt()), torch.diag(w.rsqrt())
+    basis = fit_spectral_basis(M_fit, Wh, Wh_inv)
+    pack = pack_from_basis(basis, 2.5, group=64)
+    pack3 = pack_from_basis(basis, 3.0, group=64)
+    M = (torch.randn(S, C, generator=g, dtype=torch.float64) @ mix).float()
+    out = {"M": M.numpy(), "dec": pack.dec.numpy(), "enc": pack.enc.numpy(), "lam": pack.lam.numpy(),
+           "bits_b2.5": pack.bits.numpy(), "bits_b3.0": pack3.bits.numpy()}
+    for t in (None, 3, 5):
+        out[f"dec8_t{t or 'all'}"] = int8_decoder_roundtrip(pack.dec, pack.bits, tier_threshold=t).numpy()
+    for t in TIER_THRESHOLD_GRID:
+        cert = int8_decoder_certificate_tiered(pack, t)
+        out[f"cert_b2.5_t{t}"] = np.array([cert["added"], cert["payload"], cert["implied_rel_degradation"]])
+    for bar in (0.05, 0.001, 1e-5):
+        thr = per_layer_tier_thresholds({0: pack, 1: pack3}, bar=bar)
+        out[f"layer_thr_bar{bar:g}"] = np.array([thr[0], thr[1]], dtype=np.int64)
+    for b in (2, 3, 4, 5, 6, 8):
+        out[f"codebook_{b}"] = codecs.gaussian_codebook(b).numpy()
+    cols = tier_columns(pack.bits)
+    packed, _ = spectral_quantize_packed(M, pack, cols_by_tier=cols, quantizer="lloyd")
+    for b, c in cols.items():
+        out[f"lq_codes_t{b}"] = _unpack_tier_codes(packed[f"t{b}_codes"], b, S, quantizer="lloyd").numpy()
+        out[f"lq_scale_t{b}"] = packed[f"t{b}_scale"].numpy()
+    out["lq_M_hat"] = spectral_dequant_packed(packed, pack, cols_by_tier=cols, quantizer="lloyd").numpy()
+    return out
+
+
 FIXTURES = {"codecs": codec_fixtures, "attention": attention_fixtures,
-            "e2e_tiny_llama": e2e_fixtures, "spectral": spectral_fixtures}
+            "e2e_tiny_llama": e2e_fixtures, "spectral": spectral_fixtures,
+            "spectral_variants": spectral_variant_fixtures}
 
 
 def main():

@@ -133,20 +133,23 @@ def _spectral_pack_file(tmp_path, n_layers):
     return str(path)
 
 
-@pytest.mark.parametrize("budget", [2.5, 3.0])
-def test_spectral_cache_matches_oracle_backed_cache(tmp_path, budget):
+@pytest.mark.parametrize("arm", ["k4ph_b2.5", "k4ph_b3", "k4ph_b2.5_dec8t4"])
+def test_spectral_cache_matches_oracle_backed_cache(tmp_path, arm):
     """The k4 recipe through the model: every commit through
     bmx_spectral_append, every step (decode and prefill) through
     bmx_spectral_dequant + SDPA, against the same host logic with the CPU
     oracle's codes (one layer: both caches encode the same keys, so the
-    logits differ by the kernels' numerics only), teacher-forced."""
+    logits differ by the kernels' numerics only), teacher-forced.  The
+    _dec8t4 arm decodes with the int8-roundtripped decoder and pays the
+    int8 decoder charge in bits_per_entry."""
     from bmx_amd import spectral
 
     g = np.load(GOLD / "e2e_tiny_llama.npz")
     tokens = torch.from_numpy(g["r16_tokens"]).cuda()
     model = _tiny_model(n_layers=1)
     path = _spectral_pack_file(tmp_path, 1)
-    specs = spec_pair(f"k4ph_b{budget:g}", pack_path=path)
+    specs = spec_pair(arm, pack_path=path)
+    budget = specs[0].budget
     prod = PackedStreamingCache(model.config, *specs, recent_window=32)
     got = _run(prod, model, tokens, 140)
     orc = OracleCache(model.config, *specs, recent_window=32)
@@ -155,12 +158,17 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, budget):
     scale = ref.abs().max().item()
     agree = (got.argmax(1) == ref.argmax(1)).float().mean().item()
     lay = prod.layers[0]
-    print(f"k4ph_b{budget:g}: logits max|err| {err.max():.3e} of max|logit| {scale:.3f}; argmax "
+    print(f"{arm}: logits max|err| {err.max():.3e} of max|logit| {scale:.3f}; argmax "
           f"agreement {agree:.4f}; committed {lay._committed_S_q}; c_pad {lay._dp.c_pad}", flush=True)
     assert lay._committed_S_q == 384 and lay._n_kpages == 6 and lay._n_pages == 24
-    bpe = spectral.payload_bpe(spectral.load_packs(path, budget)[0].bits)
+    pack = spectral.load_packs(path, budget)[0]
+    if arm.endswith("_dec8t4"):
+        assert lay._pack.dec_tier == 4 and not torch.equal(lay._pack.dec, pack.dec)
+    bpe = spectral.payload_bpe(pack.bits)
     S = lay.get_seq_length()
-    assert abs(prod.bits_per_entry()[0] - (384 * bpe + (S - 384) * 16.0) / S) < 1e-9
+    c_int8 = pack.c_int8(4) if arm.endswith("_dec8t4") else 0
+    charge = 8.0 * c_int8 / S + 16.0 * c_int8 / (S * 256) + 16.0 * (pack.c_used - c_int8) / S + 3.0 / S
+    assert abs(prod.bits_per_entry()[0] - ((384 * bpe + (S - 384) * 16.0) / S + charge)) < 1e-9
     assert err.max().item() <= 2e-3 * max(scale, 1.0)
     assert agree == 1.0
 

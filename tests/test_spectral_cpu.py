@@ -19,6 +19,17 @@ def gold():
     return np.load(GOLD / "spectral.npz")
 
 
+@pytest.fixture(scope="module")
+def variants():
+    return np.load(GOLD / "spectral_variants.npz")
+
+
+def _variant_pack(variants, budget=2.5):
+    return spectral.SpectralPack(enc=torch.from_numpy(variants["enc"]), dec=torch.from_numpy(variants["dec"]),
+                                 lam=torch.from_numpy(variants["lam"]),
+                                 bits=torch.from_numpy(variants[f"bits_b{budget}"]))
+
+
 @pytest.mark.parametrize("budget", [2.0, 2.5, 3.0])
 def test_allocation_matches_reference(gold, budget):
     """Both restatements of allocate_bits_from_variance ("round") give the
@@ -180,9 +191,8 @@ def test_recipe_and_construction_guards(tmp_path):
             spec_pair(arm, pack_path=str(path))
     with pytest.raises(ValueError, match="pack-path"):
         spec_pair("k4ph_b2.5")
-    for arm in ("k4ph_b2.5_lq", "k4ph_b2.5_dec8tl"):
-        with pytest.raises(NotImplementedError, match="no MI355X kernels"):
-            spec_pair(arm, pack_path=str(path))
+    with pytest.raises(NotImplementedError, match="rtn payload"):
+        PackedStreamingCache(cfg, *spec_pair("k4ph_b2.5_lq", pack_path=str(path)))
     k, v = spec_pair("k4ph_b2.5", pack_path=str(path))
     assert (k.arm, k.pre_rope, k.budget, v.arm, v.bits) == ("spectral", True, 2.5, "turboquant_mse_perhead", 2)
     with pytest.raises(AssertionError, match="pre_rope"):
@@ -231,3 +241,126 @@ def test_dequant_table_checks_precede_every_form():
                              partials=part if n == S else torch.zeros(2, 4, 130 * (n // 64)))
         with pytest.raises(ValueError, match="k_table|multiple of 64"):
             spectral.dequant(dp, kp, k_t, vp, v_t, n, consts)
+
+
+@pytest.mark.parametrize("thr", [None, 3, 5])
+def test_int8_decoder_roundtrip_matches_reference(variants, thr):
+    """Both restatements of int8_decoder_roundtrip give the reference's
+    decoder bit for bit; columns outside the threshold (and uncoded ones)
+    are untouched."""
+    dec, bits = variants["dec"], variants["bits_b2.5"]
+    want = variants[f"dec8_t{thr or 'all'}"]
+    got_o = O.int8_decoder_roundtrip(dec, bits, thr)
+    got_p = spectral.int8_decoder_roundtrip(torch.from_numpy(dec), torch.from_numpy(bits), thr).numpy()
+    assert np.array_equal(got_o.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(got_p.view(np.uint32), want.view(np.uint32))
+    keep = (bits == 0) | ((bits > thr) if thr is not None else False)
+    assert np.array_equal(want[:, keep], dec[:, keep]) and not np.array_equal(want[:, ~keep], dec[:, ~keep])
+
+
+def test_int8_certificate_matches_reference(variants):
+    """The certificate's three numbers at every grid threshold, both
+    restatements, against the reference's (float64, matmul order aside)."""
+    pack = _variant_pack(variants)
+    for t in spectral.TIER_THRESHOLD_GRID:
+        want = variants[f"cert_b2.5_t{t}"]
+        c = spectral.int8_certificate(pack, t)
+        np.testing.assert_allclose([c["added"], c["payload"], c["implied_rel_degradation"]], want, rtol=1e-12)
+        np.testing.assert_allclose(O.int8_certificate(variants["enc"], variants["dec"], variants["lam"],
+                                                      variants["bits_b2.5"], t), want, rtol=1e-12)
+        assert c["c_int8"] == int(((variants["bits_b2.5"] > 0) & (variants["bits_b2.5"] <= t)).sum())
+
+
+def test_int8_certificate_is_the_expected_weighted_distortion(variants):
+    """What the closed form states, estimated: for codes y ~ N(0, diag(lam))
+    the weighted error |enc^T (dec_int8 - dec) y|^2 averages to `added`
+    (a column/row swap of the perturbation or a dropped lam misses by far
+    more than the 3% allowed); below the lowest coded tier nothing is
+    stored int8 and `added` is exactly 0; `payload` is sum lam 4^-bits."""
+    enc, dec, lam, bits = (variants[k].astype(np.float64) for k in ("enc", "dec", "lam", "bits_b2.5"))
+    D = O.int8_decoder_roundtrip(variants["dec"], variants["bits_b2.5"], 5).astype(np.float64) - dec
+    y = np.random.default_rng(5).standard_normal((40000, lam.size)) * np.sqrt(lam)
+    est = float(((y @ D.T @ enc) ** 2).sum(axis=1).mean())
+    added, payload, rel = O.int8_certificate(variants["enc"], variants["dec"], variants["lam"], variants["bits_b2.5"], 5)
+    assert abs(est / added - 1) < 0.03
+    assert payload == pytest.approx(float((lam * 4.0 ** -bits).sum()), rel=1e-12)
+    assert rel == pytest.approx(added / (added + payload), rel=1e-12)
+    low = int(bits[bits > 0].min()) - 1
+    assert O.int8_certificate(variants["enc"], variants["dec"], variants["lam"], variants["bits_b2.5"], low)[0] == 0.0
+
+
+@pytest.mark.parametrize("bar", [0.05, 0.001, 1e-5])
+def test_per_layer_tier_thresholds_match_reference(variants, bar):
+    p25, p3 = _variant_pack(variants, 2.5), _variant_pack(variants, 3.0)
+    want = variants[f"layer_thr_bar{bar:g}"].tolist()
+    got = spectral.per_layer_tier_thresholds({0: p25, 1: p3}, bar=bar)
+    assert [got[0], got[1]] == want
+    layers = {i: (variants["enc"], variants["dec"], variants["lam"], p.bits.numpy()) for i, p in enumerate((p25, p3))}
+    assert list(O.per_layer_tier_thresholds(layers, bar).values()) == want
+
+
+def test_k4_recipe_suffixes():
+    """recipes.py:100-150: '_lq' between the budget and the decoder suffix,
+    '_dec8' | '_dec8t<T>' | '_dec8tl'; a misplaced '_lq' and a threshold
+    outside 2..8 raise."""
+    from bmx_amd.specs import spec_pair
+
+    want = {"k4ph_b2.5": (2.5, "rtn", "fp32"), "k4ph_b2.5_dec8": (2.5, "rtn", "int8"),
+            "k4ph_b3_dec8t5": (3.0, "rtn", "int8_t5"), "k4ph_b2.5_dec8tl": (2.5, "rtn", "int8_tl"),
+            "k4ph_b2.5_lq": (2.5, "lloyd", "fp32"), "k4ph_b2.5_lq_dec8t3": (2.5, "lloyd", "int8_t3")}
+    for arm, (b, pq, dq) in want.items():
+        k, _ = spec_pair(arm, pack_path="p")
+        assert (k.budget, k.payload_quant, k.dec_quant) == (b, pq, dq), arm
+    for arm in ("k4ph_b2.5_dec8tl_lq", "k4ph_b2.5_dec8_lq"):
+        with pytest.raises(ValueError, match="malformed"):
+            spec_pair(arm, pack_path="p")
+    for arm in ("k4ph_b2.5_dec8t9", "k4ph_b2.5_dec8t1", "k4ph_b2.5_dec8t"):
+        with pytest.raises(ValueError, match="int8_t<T>"):
+            spec_pair(arm, pack_path="p")
+    assert [spectral.dec_quant_threshold(d) for d in ("fp32", "int8", "int8_t4", "int8_tl")] == \
+        [None, 8, 4, spectral.PER_LAYER_TIER]
+
+
+def test_int8_decoder_packs_load_once_with_their_threshold(tmp_path):
+    """load_packs_for_spec (spectral.py:1254-1326): dec8t<T> roundtrips every
+    layer at T, dec8tl at each layer's certified threshold, from the packs
+    as loaded; enc, lam and bits are untouched and dec_tier records T; the
+    cache holds exactly these packs."""
+    from transformers import LlamaConfig
+
+    from bmx_amd.cache import PackedStreamingCache
+    from bmx_amd.specs import spec_pair
+
+    layers = {i: synthetic_pack(2, 2.5, seed=60 + i) for i in range(2)}
+    path = tmp_path / "packs.safetensors"
+    spectral.save_packs(path, {i: (p.enc, p.dec, p.lam, {2.5: p.bits}) for i, p in layers.items()}, (2.5,))
+    t_map = spectral.per_layer_tier_thresholds(layers)
+    for arm, thr in (("k4ph_b2.5_dec8t4", {0: 4, 1: 4}), ("k4ph_b2.5_dec8", {0: 8, 1: 8}),
+                     ("k4ph_b2.5_dec8tl", t_map), ("k4ph_b2.5", {0: None, 1: None})):
+        k, _ = spec_pair(arm, pack_path=str(path))
+        packs = spectral.load_packs_for_spec(k)
+        for i, p in layers.items():
+            q = packs[i]
+            assert q.dec_tier == thr[i] and torch.equal(q.enc, p.enc) and torch.equal(q.bits, p.bits)
+            want = p.dec if thr[i] is None else O.int8_decoder_roundtrip(p.dec.numpy(), p.bits.numpy(), thr[i])
+            assert np.array_equal(np.asarray(q.dec), np.asarray(want))
+    cfg = LlamaConfig(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=128)
+    cache = PackedStreamingCache(cfg, *spec_pair("k4ph_b2.5_dec8t4", pack_path=str(path)))
+    assert cache._packs[1].dec_tier == 4
+
+
+def test_mixed_decoder_charge():
+    """mixed_dec_charge (spectral.py:1036-1064) at its two ends: all fp16
+    columns 16 c_used / S, all int8 8 c_used / S + 16 c_used / (S C), plus
+    the tier map's ceil(log2 7) / S; linear in between."""
+    C, S, tiers = 256, 1000, spectral.TIERS
+    tb = 3 / S
+    assert spectral.mixed_dec_charge(C, S, tiers, 100, 0) == pytest.approx(16 * 100 / S + tb, rel=1e-15)
+    assert spectral.mixed_dec_charge(C, S, tiers, 100, 100) == pytest.approx(8 * 100 / S + 1600 / (S * C) + tb,
+                                                                            rel=1e-15)
+    mid = spectral.mixed_dec_charge(C, S, tiers, 100, 50)
+    assert mid == pytest.approx(0.5 * (spectral.mixed_dec_charge(C, S, tiers, 100, 0)
+                                       + spectral.mixed_dec_charge(C, S, tiers, 100, 100)), rel=1e-14)
+    with pytest.raises(ValueError):
+        spectral.mixed_dec_charge(C, S, tiers, 100, 101)
