@@ -178,7 +178,7 @@ class RtnDequantArgs(ct.Structure):
 
 class SpectralLayout(ct.Structure):
     _fields_ = [("h_kv", ct.c_int32), ("c_pad", ct.c_int32), ("k_page_bytes", ct.c_int32),
-                ("slice_tab", ct.c_void_p)]
+                ("slice_tab", ct.c_void_p), ("lloyd_levels", ct.c_void_p)]
 
 
 class SpectralAppendArgs(ct.Structure):

@@ -315,7 +315,7 @@ class PackedStreamingLayer(DynamicLayer):
         pages, 2n key pages of 64 tokens and 8n value pages of 16."""
         dev = v.device
         if self._dp is None:
-            self._dp = spectral.DevicePack(self._pack, self._h_kv, dev)
+            self._dp = spectral.DevicePack(self._pack, self._h_kv, dev, self.k_spec.payload_quant)
         n_grp = k_pre.shape[1] // spectral.GROUP
         kf, vf = self._n_kpages, self._n_pages
         cap = 0 if self._kpool is None else self._kpool.shape[0]
@@ -524,7 +524,7 @@ class PackedStreamingLayer(DynamicLayer):
         h, d = self._h_kv, self._d_head
         P = self._committed_S_q
         if self._dp is None:   # a step before the first commit: the window alone
-            self._dp = spectral.DevicePack(self._pack, self._h_kv, q.device)
+            self._dp = spectral.DevicePack(self._pack, self._h_kv, q.device, self.k_spec.payload_quant)
         qg = q.reshape(h, G, d).contiguous()
         kw = vw = None
         wk, wv = self.window()

@@ -18,6 +18,19 @@ constexpr int kSpMaxSlices = BMX_SPECTRAL_MAX_CPAD / 8;
 
 __device__ __forceinline__ int sp_width(int b) { return b == 2 ? 2 : (b <= 4 ? 4 : 8); }
 
+// The Lloyd payload's level table: tier b's 2^b levels at lq_off(b)
+constexpr int kLqLevels = BMX_SPECTRAL_LLOYD_LEVELS;
+__device__ __forceinline__ int lq_off(int b) { return b == 8 ? 124 : (1 << b) - 4; }
+
+// Index of the level nearest to x among tier b's sorted levels: the number of
+// the 2^b - 1 midpoints mid[0 ..] below x (torch.bucketize, right=False)
+__device__ __forceinline__ int lq_index(const float* mid, int b, float x) {
+  int i = 0;
+  for (int k = b - 1; k >= 0; --k)
+    if (mid[i + (1 << k) - 1] < x) i += 1 << k;
+  return i;
+}
+
 // sin and cos of an fp32 angle x (|x| < 2^40): x - k pi/2 in double (pi/2 in
 // two parts, the first with 33 significant bits so that k times it is exact),
 // rounded once to fp32 (|r| <= pi/4: within 3e-8 of the exact reduced angle),
@@ -60,6 +73,7 @@ struct SpEncodeKArgs {
   const int32_t* slice_tab;
   uint8_t* pages;
   const int32_t* page_ids;
+  const float* lq;   // the Lloyd levels, or nullptr (rtn payload)
 };
 
 // grid (ceil(c_pad / 64), n_groups), block 512: wave w of block x
@@ -67,16 +81,23 @@ struct SpEncodeKArgs {
 // 64x + j (lane j) over the C channels, staged 64 at a time through LDS with
 // the chunk's enc rows (every product and sum rounded on its own, channels in
 // order); then wave 0's lane j takes column 64x + j's 64 values from LDS for
-// the step (max|Y| / qmax and 10 rounds of <Y, Q> / <Q, Q>) and its codes,
-// and the block's 8 slices are assembled in LDS and written with dword stores.
+// the step (max|Y| / qmax and 10 rounds of <Y, Q> / <Q, Q>; for the Lloyd
+// payload the sample deviation and 3 rounds of <Y, l> / <l, l>) and its
+// codes, and the block's 8 slices are assembled in LDS and written with dword
+// stores.
+template <bool kLloyd>
 __global__ __launch_bounds__(512) void spectral_encode_kernel(const SpEncodeKArgs a) {
   __shared__ float s_m[kGroup][kSpCh + 1];   // the chunk's keys: [token][channel]
   __shared__ float s_e[kSpCh][64];           // the chunk's enc rows: [channel][column]
   __shared__ float s_y[kGroup][65];          // Y: [token][column]
   __shared__ uint32_t s_code[8 * kGroup * 8 / 4];   // 8 slices of at most 512 bytes
+  __shared__ float s_lv[kLloyd ? kLqLevels : 1], s_mid[kLloyd ? kLqLevels : 1];   // levels, midpoints
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = blockIdx.x * 64 + lane, g = blockIdx.y;
   const bool active = j < a.c_pad;
+  constexpr bool lloyd = kLloyd;
+  if (lloyd)
+    for (int i = tid; i < kLqLevels; i += 512) s_lv[i] = a.lq[i];
   float y[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) y[t] = 0.f;
@@ -99,13 +120,39 @@ __global__ __launch_bounds__(512) void spectral_encode_kernel(const SpEncodeKArg
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t) s_y[8 * wave + t][lane] = y[t];
+  // midpoints (l_i + l_{i+1}) / 2 within each tier (the slot after a tier's
+  // last level is never read); s_lv was written before the chunk loop's barriers
+  if (lloyd)
+    for (int i = tid; i + 1 < kLqLevels; i += 512) s_mid[i] = (s_lv[i] + s_lv[i + 1]) * 0.5f;
   __syncthreads();
   const int s = j >> 3, k = j & 7;
   const uint32_t tab = active ? (uint32_t)a.slice_tab[s] : 0u;
   const int b = active ? (int)(tab >> 24) : 2, w = sp_width(b);
   const float qmax = (float)((1 << (b - 1)) - 1);
+  const float* lv = s_lv + (kLloyd ? lq_off(b) : 0);
+  const float* mid = s_mid + (kLloyd ? lq_off(b) : 0);
   float scale = 1e-12f;
-  if (active && wave == 0) {
+  if (active && wave == 0 && lloyd) {
+    double sum = 0.0;
+    for (int t = 0; t < kGroup; ++t) sum += (double)s_y[t][lane];
+    const double mean = sum / 64.0;
+    double ss = 0.0;
+    for (int t = 0; t < kGroup; ++t) {
+      const double d = (double)s_y[t][lane] - mean;
+      ss += d * d;
+    }
+    scale = fmaxf((float)__dsqrt_rn(ss / 63.0), 1e-12f);
+    for (int it = 0; it < 3; ++it) {
+      float num = 0.f, den = 0.f;
+      for (int t = 0; t < kGroup; ++t) {
+        const float yv = s_y[t][lane];
+        const float l = lv[lq_index(mid, b, yv / scale)];
+        num = __fadd_rn(num, __fmul_rn(yv, l));
+        den = __fadd_rn(den, __fmul_rn(l, l));
+      }
+      scale = fmaxf(num / fmaxf(den, 1e-12f), 1e-12f);
+    }
+  } else if (active && wave == 0) {
     float amax = 0.f;
     for (int t = 0; t < kGroup; ++t) amax = fmaxf(amax, fabsf(s_y[t][lane]));
     scale = fmaxf(amax, 1e-12f) / qmax;
@@ -132,7 +179,8 @@ __global__ __launch_bounds__(512) void spectral_encode_kernel(const SpEncodeKArg
     const uint32_t bias = 1u << (b - 1);
     for (int t = 0; t < kGroup; ++t) {
       const float qv = fminf(fmaxf(rintf(s_y[t][lane] / scale), -qmax - 1.f), qmax);
-      const uint32_t stored = (uint32_t)((int)qv + (int)bias);
+      const uint32_t stored = lloyd ? (uint32_t)lq_index(mid, b, s_y[t][lane] / scale)
+                                    : (uint32_t)((int)qv + (int)bias);
       const int bit = bit0 + t * w * 8;
       atomicOr(&s_code[bit >> 5], stored << (bit & 31));
     }
@@ -164,6 +212,7 @@ struct SpDequantKArgs {
   float* scores;
   float* partials;
   float sm_scale;
+  const float* lq;   // the Lloyd levels, or nullptr (rtn payload)
 };
 
 constexpr int kSpBRow = 40;   // halves per token row of the staged code tile (32 + 8 pad)
@@ -298,6 +347,16 @@ __device__ __forceinline__ int sp_narrow_steps(uint32_t tabv, int tid, int n_sl,
 // wave rotates its pairs (channels j, j + 64 in row tiles bb, bb + 4), stages
 // 16 rows at a time in LDS and writes them coalesced, and dequantizes its
 // head's 4 value pages.
+//
+// kLloyd (the Lloyd payload): a code is a level index, read through the
+// levels in LDS; the B side holds v = level * the column's B factor (its step
+// in a narrow slice, else 1).  The leading narrow steps (an even number) take
+// fp16(v); every later step runs twice on one A operand, with B = fp16(v) and
+// then B = fp16(v - fp16(v)), so that the pair of halves carries v to 2^-22:
+// a single fp16 level of the wide tiers was the keys' largest error, as the
+// product code * step was in the rtn payload (levels are no integers, so no
+// exact fp16 form exists).
+template <bool kLloyd>
 __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKArgs a) {
   const int g = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
@@ -308,6 +367,7 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   __shared__ __align__(16) float s_cs[2][kGroup][kCsPad];   // rows padded: conflict-free 16-byte reads
   // fp16 codebook levels of the 4 codes of one value-code byte (the P.V B operand)
   __shared__ uint2 s_cbl[256];
+  __shared__ float s_lq[kLloyd ? kLqLevels : 1];   // the key payload's Lloyd levels
   extern __shared__ __align__(16) uint8_t sp_dyn[];
   uint8_t* kp = sp_dyn;                                 // the key page, until the main loop ends
   DqTile* s_tile = reinterpret_cast<DqTile*>(sp_dyn);   // then the staging tiles
@@ -328,6 +388,8 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   for (int i = 0; i < kSpPageLoads; ++i)
     kpw[i] = reinterpret_cast<const u32x4_t*>(page)[min(tid + 512 * i, n16 - 1)];
   const uint32_t tabv = (uint32_t)a.slice_tab[min(tid, n_sl - 1)];   // n_sl <= 134 < 512
+  float lqv = 0.f;
+  if constexpr (kLloyd) lqv = a.lq[min(tid, kLqLevels - 1)];
   uint2 vcd[4], nrm[4];
 #pragma unroll
   for (int pg = 0; pg < 4; ++pg) {
@@ -388,12 +450,20 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     }
   }
   if (tid < n_sl) s_tab[tid] = tabv;
+  if constexpr (kLloyd) {
+    if (tid < kLqLevels) s_lq[tid] = lqv;
+  }
 #pragma unroll
   for (int i = 0; i < kSpPageLoads; ++i)
     if (tid + 512 * i < n16) reinterpret_cast<u32x4_t*>(kp)[tid + 512 * i] = kpw[i];
   const int n_steps = a.c_pad32 / 32;
-  // a barrier: s_tab, s_cbl, the RoPE table, the key page
+  // a barrier: s_tab, s_cbl, s_lq, the RoPE table, the key page
   const int n_narrow = sp_narrow_steps(tabv, tid, n_sl, n_steps);
+  // Lloyd: steps 0 .. nn - 1 once each, the others as (fp16(v), remainder)
+  // halves: virtual step u < nn is step u, else step nn + (u - nn) / 2, half
+  // (u - nn) & 1; nn is even, so every barrier pair of the later steps holds
+  // one step's two halves
+  const int nn = kLloyd ? (n_narrow & ~1) : n_steps;
 
   // lane (sq, hf, t) of wave w decodes codes 4 hf .. 4 hf + 3 of slice 4 step + sq, token 8w + t
   // (a row of 16 lanes shares one slice, so that its code-word reads fall in
@@ -414,6 +484,36 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     *reinterpret_cast<uint2*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) =
         make_uint2(ok ? sp_hmul2(c.x, f0) : 0u, ok ? sp_hmul2(c.y, f1) : 0u);
   };
+  // Lloyd: virtual step u's B tile (see nn above)
+  auto decode_lq = [&](int u, int buf) {
+    const int ks = u < nn ? u : nn + ((u - nn) >> 1);
+    const bool rem = u >= nn && ((u - nn) & 1);
+    const int s = 4 * ks + dsq, sc = min(s, n_sl - 1);
+    const uint32_t tab = s_tab[sc];
+    const int b = (int)(tab >> 24), off = (int)(tab & 0xFFFFFFu), w = sp_width(b);
+    const int p = off + dt * w;
+    const uint2 cw = *reinterpret_cast<const uint2*>(kp + (p & ~7));
+    const uint4 f = sp_b_factor(kp, sc, b);
+    const uint64_t word = ((((uint64_t)cw.y << 32) | cw.x) >> (8 * (p & 7))) >> (4 * dhf * w);
+    const half2_t f01 = as_h2(dhf ? f.z : f.x), f23 = as_h2(dhf ? f.w : f.y);
+    const float fe[4] = {(float)f01[0], (float)f01[1], (float)f23[0], (float)f23[1]};
+    const float* lv = s_lq + lq_off(b);
+    const uint32_t mask = (1u << w) - 1u;
+    const bool ok = s < n_sl;
+    _Float16 o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v = lv[(uint32_t)(word >> (e * w)) & mask] * fe[e];
+      const _Float16 hi = (_Float16)v;
+      o[e] = ok ? (rem ? (_Float16)(v - (float)hi) : hi) : (_Float16)0.f;
+    }
+    *reinterpret_cast<uint2*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) =
+        make_uint2(as_u32(half2_t{o[0], o[1]}), as_u32(half2_t{o[2], o[3]}));
+  };
+  auto decode = [&](int u, int buf) {
+    if constexpr (kLloyd) decode_lq(u, buf);
+    else decode_b(u, buf);
+  };
 
   float4_t acc[8][4];
 #pragma unroll
@@ -423,13 +523,13 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   // Two steps per workgroup barrier: buffers 2p and 2p + 1 hold steps ks and
   // ks + 1 while the next two are decoded into the other pair; each step's
   // MFMAs are interleaved with the next pair's decode (VALU and LDS reads).
-  decode_b(0, 0);
-  decode_b(1, 1);
+  decode(0, 0);
+  decode(1, 1);
   __syncthreads();
-  auto mfma_step = [&](int ks, int buf, auto wide) {
-    // A = the dec rows, times the group's steps of the lane's 8 columns in a
-    // step with wider tiers
-    half8_t A[8];
+  half8_t A[8];
+  // A = the dec rows, times the group's steps of the lane's 8 columns in a
+  // step with wider tiers; then the next step's rows are loaded
+  auto a_operand = [&](int ks, auto wide) {
     if constexpr (decltype(wide)::value) {
       const half8_t f = sp_a_factor(kp, s_tab, 4 * ks + q, n_sl);
 #pragma unroll
@@ -442,6 +542,8 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 #pragma unroll
     for (int bt = 0; bt < 8; ++bt)
       An[bt] = *reinterpret_cast<const half8_t*>(decb + bt * tile_stride + step_stride * kn);
+  };
+  auto mfma_b = [&](int buf) {
     half8_t B[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) B[tt] = *reinterpret_cast<const half8_t*>(&s_b[buf][16 * tt + n][8 * q]);
@@ -450,6 +552,10 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
         acc[bt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[bt], B[tt], acc[bt][tt], 0, 0, 0);
+  };
+  auto mfma_step = [&](int ks, int buf, auto wide) {
+    a_operand(ks, wide);
+    mfma_b(buf);
   };
   // whole pairs of steps in one basic block each (decodes past the last step
   // store zeros into buffers nobody reads), then an odd last step; the
@@ -460,22 +566,41 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     const int ks = 2 * kq, pb = kq & 1;
     if (head_ok) {
       mfma_step(ks, 2 * pb, wide);
-      decode_b(ks + 2, 2 * (pb ^ 1));
+      decode(ks + 2, 2 * (pb ^ 1));
       mfma_step(ks + 1, 2 * pb + 1, wide);
-      decode_b(ks + 3, 2 * (pb ^ 1) + 1);
+      decode(ks + 3, 2 * (pb ^ 1) + 1);
     } else {
-      decode_b(ks + 2, 2 * (pb ^ 1));
-      decode_b(ks + 3, 2 * (pb ^ 1) + 1);
+      decode(ks + 2, 2 * (pb ^ 1));
+      decode(ks + 3, 2 * (pb ^ 1) + 1);
     }
     lds_barrier();   // the next pair decoded, this pair read by every wave
   };
   int kq = 0;
-  for (; kq < n_narrow_pairs; ++kq) pair(kq, std::false_type{});
-  for (; kq < n_pairs; ++kq) pair(kq, std::true_type{});
-  if ((n_steps & 1) && head_ok) mfma_step(n_steps - 1, 2 * (n_pairs & 1), std::true_type{});
-  // the last step's A factors read the key page, whose space takes the
-  // staging tiles below
-  if (n_steps & 1) __syncthreads();
+  if constexpr (kLloyd) {
+    // the narrow pairs, then one step per pair: its two halves on one A operand
+    for (; kq < (nn >> 1); ++kq) pair(kq, std::false_type{});
+    for (; kq < (nn >> 1) + n_steps - nn; ++kq) {
+      const int u = 2 * kq, pb = kq & 1;
+      if (head_ok) {
+        a_operand(nn + kq - (nn >> 1), std::true_type{});
+        mfma_b(2 * pb);
+        decode(u + 2, 2 * (pb ^ 1));
+        mfma_b(2 * pb + 1);
+        decode(u + 3, 2 * (pb ^ 1) + 1);
+      } else {
+        decode(u + 2, 2 * (pb ^ 1));
+        decode(u + 3, 2 * (pb ^ 1) + 1);
+      }
+      lds_barrier();
+    }
+  } else {
+    for (; kq < n_narrow_pairs; ++kq) pair(kq, std::false_type{});
+    for (; kq < n_pairs; ++kq) pair(kq, std::true_type{});
+    if ((n_steps & 1) && head_ok) mfma_step(n_steps - 1, 2 * (n_pairs & 1), std::true_type{});
+    // the last step's A factors read the key page, whose space takes the
+    // staging tiles below
+    if (n_steps & 1) __syncthreads();
+  }
 
   // query fragments (decode form), loaded after the main loop: the MFMA B operand of the scores, lane
   // 16q + n: query n, K index 8q + 2i + e = channel 16bb + 4q + i + 64e
@@ -1238,7 +1363,7 @@ static bool dtype_ok(int d) { return d == BMX_K2B_F16 || d == BMX_K2B_F32 || d =
 // fit in LDS together; the partials pointer itself is not consulted, so the
 // count below can be asked before the buffer exists.
 static bool sp_block_shape(const bmx_spectral_dequant_args* a) {
-  return a->q && !a->k_out && a->apply_rope == 2 && a->n_tokens % kSpBlk == 0 &&
+  return a->q && !a->k_out && !a->L.lloyd_levels && a->apply_rope == 2 && a->n_tokens % kSpBlk == 0 &&
          2 * (int64_t)a->L.k_page_bytes <= kSpBlkMaxPages;
 }
 
@@ -1269,7 +1394,11 @@ extern "C" int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* 
   k.page_bytes = a->L.k_page_bytes;
   k.k = a->k_pre; k.ksh = a->k_sh; k.kst = a->k_st;
   k.encp = a->enc_perm; k.slice_tab = a->L.slice_tab; k.pages = a->k_pages; k.page_ids = a->k_page_ids;
-  hipLaunchKernelGGL(spectral_encode_kernel, dim3((a->L.c_pad + 63) / 64, a->n_groups), dim3(512), 0, st, k);
+  k.lq = a->L.lloyd_levels;
+  if (k.lq)
+    hipLaunchKernelGGL(spectral_encode_kernel<true>, dim3((a->L.c_pad + 63) / 64, a->n_groups), dim3(512), 0, st, k);
+  else
+    hipLaunchKernelGGL(spectral_encode_kernel<false>, dim3((a->L.c_pad + 63) / 64, a->n_groups), dim3(512), 0, st, k);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) {
     AppendKArgs v{};
@@ -1316,14 +1445,17 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   for (int i = 0; i < 4; ++i) { k.codebook[i] = a->v_codebook[i]; k.v_sign_bits[i] = a->v_sign_bits[i]; }
   k.k_out = a->k_out; k.v_out = a->v_out;
   k.q = a->q; k.q_dtype = a->q_dtype; k.n_q_groups = a->n_q_groups; k.scores = a->scores;
-  k.partials = a->partials; k.sm_scale = a->sm_scale;
+  k.partials = a->partials; k.sm_scale = a->sm_scale; k.lq = a->L.lloyd_levels;
   if (sp_blocked(a)) {
     const int kpb = a->L.k_page_bytes;
     const size_t dyn = std::max<size_t>(2 * (size_t)kpb, (size_t)8 * 4 * 64 * 16);   // pages, then the exchange
     hipLaunchKernelGGL(spectral_partial128_kernel, dim3(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4), dim3(512),
                        dyn, (hipStream_t)stream, k, kpb);
+  } else if (k.lq) {
+    hipLaunchKernelGGL(spectral_dequant_kernel<true>, dim3(a->n_tokens / kGroup), dim3(512),
+                       sp_dyn_bytes(a->L.k_page_bytes), (hipStream_t)stream, k);
   } else {
-    hipLaunchKernelGGL(spectral_dequant_kernel, dim3(a->n_tokens / kGroup), dim3(512),
+    hipLaunchKernelGGL(spectral_dequant_kernel<false>, dim3(a->n_tokens / kGroup), dim3(512),
                        sp_dyn_bytes(a->L.k_page_bytes), (hipStream_t)stream, k);
   }
   const hipError_t e = hipGetLastError();

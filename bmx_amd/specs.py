@@ -15,9 +15,9 @@ pairs the reference's attend() sends to a fused kernel
 * spectral (K4): K ``spectral`` pre-RoPE from a pack file (rtn payload,
   fp32 decoder, 64-token groups), V ``turboquant_mse_perhead`` 2-bit, the
   value codec of the other pre-RoPE pair, under the recipe name
-  ``k4ph_b<budget>``, with the reference's decoder suffixes ``_dec8``,
-  ``_dec8t<T>`` and ``_dec8tl`` (an int8 roundtrip of the decoder when the
-  packs load).  The reference's own ``k4_b<budget>`` recipe pairs the
+  ``k4ph_b<budget>``, with the reference's suffixes ``_lq`` (the Lloyd
+  payload) and ``_dec8``, ``_dec8t<T>``, ``_dec8tl`` (an int8 roundtrip of
+  the decoder when the packs load).  The reference's own ``k4_b<budget>`` recipe pairs the
   spectral keys with the full-C ``turboquant_mse`` values (one 1024-point
   rotation and one norm per token, recipes.py:138-143), which no MI355X
   kernel reads: that name raises rather than answer with another codec.
@@ -46,7 +46,7 @@ class CacheCodecSpec:
     pack_path: str | None = None      # spectral: the pack file (spectral.py:1081-1170)
     budget: float | None = None       # spectral: the pack's budget label
     dec_quant: str = "fp32"           # spectral: decoder storage: fp32 | int8 | int8_t<T> | int8_tl
-    payload_quant: str = "rtn"        # spectral: payload quantizer (only "rtn" here)
+    payload_quant: str = "rtn"        # spectral: payload quantizer: rtn | lloyd
 
 
 def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0, pack_path: str | None = None):
@@ -138,9 +138,10 @@ def check_spectral(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
     assert k_spec.pack_path, "spectral K requires pack_path (a fitted spectral pack file)"
     from .spectral import dec_quant_threshold
     dec_quant_threshold(k_spec.dec_quant)
-    if k_spec.payload_quant != "rtn":
+    if k_spec.payload_quant not in ("rtn", "lloyd"):
         raise NotImplementedError(
-            f"spectral payload_quant={k_spec.payload_quant!r}: the MI355X kernels implement the rtn payload")
+            f"spectral payload_quant={k_spec.payload_quant!r}: the MI355X kernels implement the rtn and lloyd "
+            f"payloads")
     if not (v_spec.arm == "turboquant_mse_perhead" and v_spec.bits == 2):
         raise NotImplementedError(
             f"spectral K pairs with V=turboquant_mse_perhead (2 bits) on the MI355X path; got V={v_spec}")

@@ -223,6 +223,21 @@ def save_packs(path, layers: dict, budgets, *, tiers=TIERS, group: int = GROUP) 
                                                      "budgets": list(budgets)}))
 
 
+LLOYD_TIERS = (2, 3, 4, 5, 6, 8)
+
+
+def lloyd_levels(device) -> torch.Tensor:
+    """The Lloyd payload's level table (include/bmx_spectral.h): the sorted
+    levels of gaussian_codebook(b) for b = 2, 3, 4, 5, 6, 8 back to back, fp32
+    (the codebook the reference's _lloyd_quantize_packed codes against,
+    spectral.py:648-684)."""
+    from .codecs import gaussian_codebook
+
+    t = torch.tensor([v for b in LLOYD_TIERS for v in gaussian_codebook(b)], dtype=torch.float32)
+    assert t.numel() == 380
+    return t.to(device)
+
+
 class DevicePack:
     """A pack's page layout and kernel operands on one device.
 
@@ -232,7 +247,9 @@ class DevicePack:
     tier b has a w-bit container, w = 2 / 4 / 8 (tiers 2 / 3-4 / 5-8), 64 w
     bytes per page at off[s] after the fp16 scales."""
 
-    def __init__(self, pack: SpectralPack, h_kv: int, device):
+    def __init__(self, pack: SpectralPack, h_kv: int, device, payload: str = "rtn"):
+        if payload not in ("rtn", "lloyd"):
+            raise ValueError(f"payload must be 'rtn' or 'lloyd'; got {payload!r}")
         if pack.group != GROUP:
             raise NotImplementedError(f"pack group {pack.group}: the spectral kernels take 64-token groups")
         bits = pack.bits.to(torch.int64).cpu()
@@ -275,9 +292,12 @@ class DevicePack:
         self.dec_perm = (decp.half().view(h_kv, 8, 16, self.c_pad32 // 32, 32).permute(0, 3, 1, 2, 4)
                          .contiguous().to(device))
         self.bpe = payload_bpe(bits, pack.group)
+        self.payload = payload
+        self.lloyd_levels = lloyd_levels(device) if payload == "lloyd" else None
 
     def layout(self) -> _lib.SpectralLayout:
-        return _lib.SpectralLayout(self.h_kv, self.c_pad, self.k_page_bytes, _ptr(self.slice_tab))
+        return _lib.SpectralLayout(self.h_kv, self.c_pad, self.k_page_bytes, _ptr(self.slice_tab),
+                                   _ptr(self.lloyd_levels) if self.lloyd_levels is not None else None)
 
 
 def append(k_pre: torch.Tensor, v: torch.Tensor, dp: DevicePack, k_pages: torch.Tensor,

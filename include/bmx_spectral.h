@@ -27,6 +27,18 @@
  * order: Y[t][j] = sum over c ascending of M[t][c] enc[c][j] and the step's
  * sums over the group's tokens left to right, no fused multiply-add.
  *
+ * Lloyd payload (the reference's payload_quant "lloyd", recipe suffix "_lq":
+ * spectral.py:648-700 _lloyd_quantize_packed / _lloyd_dequantize_packed):
+ * with L.lloyd_levels set, a column of tier b codes its group against the
+ * 2^b sorted levels of gaussian_codebook(b): the step starts at the sample
+ * standard deviation of the group's 64 values (mean and squared deviations
+ * summed left to right in fp64, divided by 64 and 63, square root, rounded to
+ * fp32; at least 1e-12), the code of a value is the number of midpoints
+ * (l_i + l_{i+1}) / 2 below value / step, and 3 rounds of step = <Y, l_code>
+ * / <l_code, l_code> (fp32, left to right, both at least 1e-12) refit it
+ * before the final codes.  The stored value is the level index itself
+ * (0 .. 2^b - 1, no offset) and the key reads back as level * step.
+ *
  * Every entry point returns BMX_OK (0) or a BMX_E_* code with a message from
  * bmx_last_error() (include/bmx_k2b.h). */
 #ifndef BMX_SPECTRAL_H
@@ -41,12 +53,16 @@ extern "C" {
 #endif
 
 #define BMX_SPECTRAL_MAX_CPAD 1072   /* 1024 directions + padding of 6 tiers */
+#define BMX_SPECTRAL_LLOYD_LEVELS 380 /* levels of tiers 2, 3, 4, 5, 6, 8 back to back */
 
 typedef struct bmx_spectral_layout {
   int32_t h_kv;                /* key heads, 1..8; C = 128 h_kv */
   int32_t c_pad;               /* coded columns with padding: multiple of 8, 8..C + 48 */
   int32_t k_page_bytes;        /* bytes per key page (SCALE + slices + 16) */
   const int32_t* slice_tab;    /* device, c_pad / 8 entries: off | tier << 24 */
+  const float* lloyd_levels;   /* NULL: the rtn payload.  Else the Lloyd payload's levels,
+                                  device fp32 [BMX_SPECTRAL_LLOYD_LEVELS]: gaussian_codebook(b)
+                                  of tier b at offset 2^b - 4 (b <= 6) and 124 (b = 8) */
 } bmx_spectral_layout;
 
 /* Replaces the spectral branch of PackedStreamingLayer._pack_k_block

@@ -15,11 +15,16 @@ Reference algorithm (paths under src/bmx):
   * int8_decoder_roundtrip, the tiered int8 certificate and the per-layer
     thresholds it picks                               cache/spectral.py:913-1033,
                                                       1176-1210
+  * the Lloyd payload (quantizer "lloyd"): _lloyd_quantize_packed /
+    _lloyd_dequantize_packed                          cache/spectral.py:648-700
 Pinned by tests/test_spectral_cpu.py against the reference's own outputs
 (tests/golden/spectral.npz): the allocation at three budgets, the tier
 columns, every code and scale of four groups given the reference's Y, and
 the dequantized keys; the encode order below against a float64 product.
-The int8 decoder functions against tests/golden/spectral_variants.npz (the
+The Lloyd payload against the same file: the reference's level indices for
+every column of every tier given the reference's Y, its steps, its
+dequantized keys; and every code against the nearest-level rule it
+implements.  The int8 decoder functions against tests/golden/spectral_variants.npz (the
 roundtrip bit for bit at three thresholds, the certificate at every
 threshold, the per-layer thresholds at three bars), and the certificate
 against a Monte-Carlo estimate of the distortion it states in closed form.
@@ -32,6 +37,12 @@ The device restatement fixes two orders the reference leaves to torch:
 Scales are stored as fp16 on the device page (the reference's accounting
 charge, scale_bits = 16 / group); dequant(fp16_scales=True) is what the
 device pages hold.
+
+The Lloyd payload fixes its orders the same way: the initial step is the
+sample deviation with the mean and the squared deviations summed left to
+right in float64 (torch's float64 Welford gives the same fp32 value on
+every group of the golden file), then the refits' sums left to right in
+fp32.  The page stores the level index itself.
 
 Page format (one page per 64-token group of one layer; tokens of the group
 are the page's rows):
@@ -120,6 +131,44 @@ def quantize_groups(G: np.ndarray, b: int, n_iter: int = 10):
     return codes(scale).astype(np.int64), scale.astype(np.float32)
 
 
+def lloyd_quantize_groups(G: np.ndarray, levels, n_iter: int = 3):
+    """The Lloyd payload over each row of G (n, 64), fp32 (spectral.py:
+    648-684): step = the sample deviation (at least 1e-12), code = the number
+    of midpoints (l_i + l_{i+1}) / 2 below value / step, then n_iter rounds of
+    step = <G, l_code> / <l_code, l_code> and new codes.  Returns (level
+    indices int, fp32 steps (n,))."""
+    G = np.asarray(G, dtype=np.float32)
+    f32 = np.float32
+    cb = np.asarray(levels, dtype=np.float32)
+    mid = ((cb[:-1] + cb[1:]) * f32(0.5)).astype(np.float32)
+    tiny = f32(1e-12)
+    g64 = G.astype(np.float64)
+    tot = np.zeros(G.shape[0])
+    for t in range(G.shape[1]):
+        tot = tot + g64[:, t]
+    mean = tot / 64.0
+    ss = np.zeros(G.shape[0])
+    for t in range(G.shape[1]):
+        d = g64[:, t] - mean
+        ss = ss + d * d
+    scale = np.maximum(np.sqrt(ss / 63.0).astype(np.float32), tiny)
+
+    def codes(s):
+        return np.searchsorted(mid, G / s[:, None], side="left")
+
+    q = codes(scale)
+    for _ in range(n_iter):
+        lv = cb[q]
+        num = np.zeros(G.shape[0], np.float32)
+        den = np.zeros(G.shape[0], np.float32)
+        for t in range(G.shape[1]):
+            num = num + G[:, t] * lv[:, t]
+            den = den + lv[:, t] * lv[:, t]
+        scale = np.maximum(num / np.maximum(den, tiny), tiny)
+        q = codes(scale)
+    return q.astype(np.int64), scale.astype(np.float32)
+
+
 class Layout:
     """The page layout of a pack's bit allocation (module docstring)."""
 
@@ -162,9 +211,10 @@ def encode(M: np.ndarray, enc: np.ndarray, layout: Layout) -> np.ndarray:
     return Y
 
 
-def quantize(Y: np.ndarray, layout: Layout):
+def quantize(Y: np.ndarray, layout: Layout, lloyd: dict | None = None):
     """Codes (n_groups, 64, c_pad) int and fp32 scales (n_groups, c_pad) of Y
-    in page column order."""
+    in page column order; with lloyd ({tier: levels}) the Lloyd payload's
+    level indices."""
     S = Y.shape[0]
     assert S % GROUP == 0
     ng = S // GROUP
@@ -173,29 +223,43 @@ def quantize(Y: np.ndarray, layout: Layout):
     for b in sorted(set(layout.slice_bits.tolist())):
         k = np.nonzero(layout.col_bits == b)[0]
         G = Y[:, k].T.reshape(len(k), ng, GROUP).transpose(1, 0, 2).reshape(ng * len(k), GROUP)
-        q, s = quantize_groups(G, b)
+        q, s = lloyd_quantize_groups(G, lloyd[b]) if lloyd is not None else quantize_groups(G, b)
         codes[:, :, k] = q.reshape(ng, len(k), GROUP).transpose(0, 2, 1)
         scales[:, k] = s.reshape(ng, len(k))
     return codes, scales
 
 
-def dequant(codes, scales, dec, layout: Layout, fp16_scales: bool = True) -> np.ndarray:
-    """Pre-RoPE keys (S, C) float64 = Y_hat @ dec^T, Y_hat = code * scale."""
+def code_values(codes, layout: Layout, lloyd: dict | None = None) -> np.ndarray:
+    """The codes' values before the step: the signed code, or the Lloyd
+    level of the index (fp32 levels; padding columns 0)."""
+    if lloyd is None:
+        return codes.astype(np.float64)
+    out = np.zeros(codes.shape, np.float64)
+    for b in sorted(set(layout.slice_bits.tolist())):
+        k = layout.col_bits == b
+        out[..., k] = np.asarray(lloyd[b], np.float32).astype(np.float64)[codes[..., k]]
+    out[..., layout.perm < 0] = 0.0
+    return out
+
+
+def dequant(codes, scales, dec, layout: Layout, fp16_scales: bool = True, lloyd: dict | None = None) -> np.ndarray:
+    """Pre-RoPE keys (S, C) float64 = Y_hat @ dec^T, Y_hat = code * scale
+    (the Lloyd payload: level * scale)."""
     s = scales.astype(np.float16).astype(np.float64) if fp16_scales else scales.astype(np.float64)
-    Yh = (codes.astype(np.float64) * s[:, None, :]).reshape(-1, layout.c_pad)
+    Yh = (code_values(codes, layout, lloyd) * s[:, None, :]).reshape(-1, layout.c_pad)
     decp = layout.permute_cols(np.asarray(dec, dtype=np.float64))
     return Yh @ decp.T
 
 
-def pack_pages(codes, scales, layout: Layout) -> np.ndarray:
+def pack_pages(codes, scales, layout: Layout, lloyd: bool = False) -> np.ndarray:
     """(n_groups, page_bytes) uint8 pages of codes (n_groups, 64, c_pad) and
-    fp32 scales (stored as fp16)."""
+    fp32 scales (stored as fp16); Lloyd level indices are stored as they are."""
     ng = codes.shape[0]
     pages = np.zeros((ng, layout.page_bytes), np.uint8)
     pages[:, : 2 * layout.c_pad] = scales.astype(np.float16).view(np.uint8).reshape(ng, -1)
     for s in range(len(layout.width)):
         w, b = int(layout.width[s]), int(layout.slice_bits[s])
-        stored = (codes[:, :, 8 * s: 8 * s + 8] + (1 << (b - 1))).astype(np.uint64)
+        stored = (codes[:, :, 8 * s: 8 * s + 8] + (0 if lloyd else 1 << (b - 1))).astype(np.uint64)
         word = np.zeros((ng, GROUP), np.uint64)
         for k in range(8):
             word |= stored[:, :, k] << np.uint64(k * w)
@@ -205,7 +269,7 @@ def pack_pages(codes, scales, layout: Layout) -> np.ndarray:
     return pages
 
 
-def unpack_pages(pages, layout: Layout):
+def unpack_pages(pages, layout: Layout, lloyd: bool = False):
     """Inverse of pack_pages: (codes, fp16 scales as fp32)."""
     ng = pages.shape[0]
     scales = pages[:, : 2 * layout.c_pad].copy().view(np.float16).astype(np.float32)
@@ -218,7 +282,7 @@ def unpack_pages(pages, layout: Layout):
         word = raw.view("<u8")[..., 0]
         for k in range(8):
             codes[:, :, 8 * s + k] = ((word >> np.uint64(k * w)) & np.uint64((1 << w) - 1)).astype(np.int64) \
-                - (1 << (b - 1))
+                - (0 if lloyd else 1 << (b - 1))
     return codes, scales
 
 

@@ -361,7 +361,8 @@ def spectral_variant_fixtures():
     pack = pack_from_basis(basis, 2.5, group=64)
     pack3 = pack_from_basis(basis, 3.0, group=64)
     M = (torch.randn(S, C, generator=g, dtype=torch.float64) @ mix).float()
-    out = {"M": M.numpy(), "dec": pack.dec.numpy(), "enc": pack.enc.numpy(), "lam": pack.lam.numpy(),
+    out = {"M": M.numpy(), "Y": (M @ pack.enc.to(M.dtype)).numpy(),
+           "dec": pack.dec.numpy(), "enc": pack.enc.numpy(), "lam": pack.lam.numpy(),
            "bits_b2.5": pack.bits.numpy(), "bits_b3.0": pack3.bits.numpy()}
     for t in (None, 3, 5):
         out[f"dec8_t{t or 'all'}"] = int8_decoder_roundtrip(pack.dec, pack.bits, tier_threshold=t).numpy()

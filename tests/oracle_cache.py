@@ -26,15 +26,17 @@ class SpectralOracleStore:
     (fixed-order encode, MSE-refined RTN, fp16 steps as stored), keys
     dequantized pre-RoPE, values by the per-head value codec."""
 
-    def __init__(self, pack, h_kv, v_seed, v_fp16):
+    def __init__(self, pack, h_kv, v_seed, v_fp16, payload="rtn"):
         self.pack, self.h_kv, self.v_seed, self.v_fp16 = pack, h_kv, v_seed, v_fp16
         self.L = OS.Layout(pack.bits.numpy())
+        self.lloyd = ({b: OC.gaussian_codebook(b).numpy() for b in set(self.L.slice_bits.tolist())}
+                      if payload == "lloyd" else None)
         self.k, self.v = [], []
 
     def commit(self, k_pre, v):
         M = OC.to_matrix(k_pre.float().cpu()).numpy()
-        codes, scales = OS.quantize(OS.encode(M, self.pack.enc.numpy(), self.L), self.L)
-        K = OS.dequant(codes, scales, self.pack.dec.numpy(), self.L)
+        codes, scales = OS.quantize(OS.encode(M, self.pack.enc.numpy(), self.L), self.L, self.lloyd)
+        K = OS.dequant(codes, scales, self.pack.dec.numpy(), self.L, lloyd=self.lloyd)
         self.k.append(OC.from_matrix(torch.from_numpy(K).float(), self.h_kv))
         vp = v.half().float() if self.v_fp16 else v.float()
         idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(vp.cpu()), bits=2, seed=self.v_seed, h=self.h_kv)
@@ -54,7 +56,8 @@ class OracleLayer(product.PackedStreamingLayer):
     def __init__(self, *args, **kwargs):
         super().__init__(*args, **kwargs)
         if self._path == "spectral":
-            self._oc = SpectralOracleStore(self._pack, self._h_kv, self.v_spec.seed, self.v_fp16)
+            self._oc = SpectralOracleStore(self._pack, self._h_kv, self.v_spec.seed, self.v_fp16,
+                                           self.k_spec.payload_quant)
         else:
             self._oc = A.K2bOracleCache(self._h_kv, self._d_head, self._rank, v_seed=self.v_spec.seed)
 

@@ -133,7 +133,7 @@ def _spectral_pack_file(tmp_path, n_layers):
     return str(path)
 
 
-@pytest.mark.parametrize("arm", ["k4ph_b2.5", "k4ph_b3", "k4ph_b2.5_dec8t4"])
+@pytest.mark.parametrize("arm", ["k4ph_b2.5", "k4ph_b3", "k4ph_b2.5_dec8t4", "k4ph_b2.5_lq_dec8tl"])
 def test_spectral_cache_matches_oracle_backed_cache(tmp_path, arm):
     """The k4 recipe through the model: every commit through
     bmx_spectral_append, every step (decode and prefill) through
@@ -141,7 +141,8 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, arm):
     oracle's codes (one layer: both caches encode the same keys, so the
     logits differ by the kernels' numerics only), teacher-forced.  The
     _dec8t4 arm decodes with the int8-roundtripped decoder and pays the
-    int8 decoder charge in bits_per_entry."""
+    int8 decoder charge in bits_per_entry; the _lq arm codes the Lloyd
+    payload (both caches: its level indices, read back through the levels)."""
     from bmx_amd import spectral
 
     g = np.load(GOLD / "e2e_tiny_llama.npz")
@@ -162,11 +163,12 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, arm):
           f"agreement {agree:.4f}; committed {lay._committed_S_q}; c_pad {lay._dp.c_pad}", flush=True)
     assert lay._committed_S_q == 384 and lay._n_kpages == 6 and lay._n_pages == 24
     pack = spectral.load_packs(path, budget)[0]
-    if arm.endswith("_dec8t4"):
-        assert lay._pack.dec_tier == 4 and not torch.equal(lay._pack.dec, pack.dec)
+    if "_dec8" in arm:
+        assert lay._pack.dec_tier is not None and not torch.equal(lay._pack.dec, pack.dec)
+    assert (lay._dp.lloyd_levels is not None) == ("_lq" in arm)
     bpe = spectral.payload_bpe(pack.bits)
     S = lay.get_seq_length()
-    c_int8 = pack.c_int8(4) if arm.endswith("_dec8t4") else 0
+    c_int8 = pack.c_int8(lay._pack.dec_tier) if "_dec8" in arm else 0
     charge = 8.0 * c_int8 / S + 16.0 * c_int8 / (S * 256) + 16.0 * (pack.c_used - c_int8) / S + 3.0 / S
     assert abs(prod.bits_per_entry()[0] - ((384 * bpe + (S - 384) * 16.0) / S + charge)) < 1e-9
     assert err.max().item() <= 2e-3 * max(scale, 1.0)

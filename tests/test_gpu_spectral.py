@@ -13,7 +13,7 @@ from oracle import codecs as OC
 from oracle import layout as OL
 from oracle import spectral as O
 
-from tests.spectral_util import golden_pack, synthetic_pack, synthetic_keys
+from tests.spectral_util import GOLD, golden_pack, synthetic_pack, synthetic_keys
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -30,11 +30,20 @@ def _values_of(vpages: np.ndarray, h_kv: int):
     return vidx, vn16
 
 
-def _write(pack, h_kv, M, v, consts, shuffle_seed=None):
+def _lloyd(payload):
+    """The oracle's Lloyd levels per tier (the reference's codebooks, from the
+    golden file), or None for the rtn payload."""
+    if payload == "rtn":
+        return None
+    z = np.load(GOLD / "spectral_variants.npz")
+    return {b: z[f"codebook_{b}"] for b in (2, 3, 4, 5, 6, 8)}
+
+
+def _write(pack, h_kv, M, v, consts, shuffle_seed=None, payload="rtn"):
     """Append keys M (S, C) and values v (h_kv, S, 128) through the C-ABI into
     pools with (optionally shuffled) page ids; returns (dp, kp, vp, k_ids, v_ids)."""
     S = M.shape[0]
-    dp = spectral.DevicePack(pack, h_kv, DEV)
+    dp = spectral.DevicePack(pack, h_kv, DEV, payload)
     ng = S // 64
     k_ids = torch.arange(ng, dtype=torch.int32)
     v_ids = torch.arange(4 * ng, dtype=torch.int32)
@@ -62,22 +71,24 @@ def _case(name):
     return pack, 8, synthetic_keys(pack, 512, seed=6)
 
 
+@pytest.mark.parametrize("payload", ["rtn", "lloyd"])
 @pytest.mark.parametrize("name", CASES)
-def test_append_pages_match_oracle(name):
+def test_append_pages_match_oracle(name, payload):
     """Every key page byte equals the oracle's page (encode in the fixed order,
-    MSE-refined RTN, container packing), and the value pages hold the k2b
-    value codec's codes and fp16 norms."""
+    MSE-refined RTN or the Lloyd payload, container packing), and the value
+    pages hold the k2b value codec's codes and fp16 norms."""
     pack, h_kv, M = _case(name)
-    print(f"case {name}: h_kv {h_kv}, S {M.shape[0]}", flush=True)
+    print(f"case {name} {payload}: h_kv {h_kv}, S {M.shape[0]}", flush=True)
     gen = torch.Generator().manual_seed(3)
     v = torch.randn(h_kv, M.shape[0], 128, generator=gen)
     consts = k2b.CodecConsts.make(v_seed=0)
-    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=1)
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=1, payload=payload)
     L = O.Layout(pack.bits.numpy())
     assert (L.c_pad, L.page_bytes) == (dp.c_pad, dp.k_page_bytes)
     assert np.array_equal(L.slice_table(), dp.slice_tab.cpu().numpy())
-    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
-    want = O.pack_pages(codes, scales, L)
+    lloyd = _lloyd(payload)
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L, lloyd)
+    want = O.pack_pages(codes, scales, L, lloyd=lloyd is not None)
     got = kp[k_ids.long()].cpu().numpy()
     bad = np.nonzero((got != want).any(axis=1))[0]
     print(f"key pages differing: {len(bad)}/{len(want)}; c_pad {L.c_pad}, tiers "
@@ -89,25 +100,28 @@ def test_append_pages_match_oracle(name):
     assert int((vidx != idx.numpy()).sum()) == 0
 
 
+@pytest.mark.parametrize("payload", ["rtn", "lloyd"])
 @pytest.mark.parametrize("name", CASES)
-def test_dequant_matches_oracle(name):
+def test_dequant_matches_oracle(name, payload):
     """Keys: Y_hat dec^T from the pages (fp16 steps, as stored) within the
-    fp16 rounding of the MFMA inputs (code * step and dec), pre-RoPE and
-    rotated (fp32 and fp16 tables); values as the k2b value codec; dtypes
-    rounded once from the fp32 result."""
+    fp16 rounding of the MFMA inputs (code or level times step, and dec),
+    pre-RoPE and rotated (fp32 and fp16 tables); values as the k2b value
+    codec; dtypes rounded once from the fp32 result."""
     pack, h_kv, M = _case(name)
     S = M.shape[0]
     gen = torch.Generator().manual_seed(4)
     v = torch.randn(h_kv, S, 128, generator=gen)
     consts = k2b.CodecConsts.make(v_seed=0)
-    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=2)
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=2, payload=payload)
     L = O.Layout(pack.bits.numpy())
-    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
-    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)), h_kv)
+    lloyd = _lloyd(payload)
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L, lloyd)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L, lloyd=lloyd)), h_kv)
     Kp, Vd = spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts)
     kmax = K_or.abs().max().item()
     err = (Kp.cpu().double() - K_or).abs().max().item()
-    print(f"{name}: pre-RoPE keys max_abs {err:.3e} (max|K| {kmax:.3f}, rel {err / kmax:.2e})", flush=True)
+    print(f"{name} {payload}: pre-RoPE keys max_abs {err:.3e} (max|K| {kmax:.3f}, rel {err / kmax:.2e})",
+          flush=True)
     assert err <= 1.5e-3 * kmax
     inv = torch.tensor(consts.inv_freq)
     cos, sin = A.rope_cos_sin(inv, torch.arange(S))
@@ -210,31 +224,35 @@ PARTIAL_CASES = [
 ]
 
 
+@pytest.mark.parametrize("payload", ["rtn", "lloyd"])
 @pytest.mark.parametrize("h_kv,G,T,rope,S", PARTIAL_CASES)
-def test_partial_form_decode_matches_oracle(h_kv, G, T, rope, S):
+def test_partial_form_decode_matches_oracle(h_kv, G, T, rope, S, payload):
     """The decode step through the kernel's partial form (per-block softmax
     partials) and the merge with the window: against the oracle's one-softmax
     attention over the same codes (RoPE by fp32 tables, or by the fp16-rounded
-    tables of an fp16 model), and against the scores form + softmax."""
+    tables of an fp16 model), and against the scores form + softmax.  The
+    Lloyd payload runs on 64-token groups."""
     pack = synthetic_pack(h_kv, 2.5, seed=14)
     M = synthetic_keys(pack, S, seed=15)
     gen = torch.Generator().manual_seed(16)
     v = torch.randn(h_kv, S, 128, generator=gen)
     consts = k2b.CodecConsts.make(v_seed=0)
-    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=4)
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=4, payload=payload)
+    lloyd = _lloyd(payload)
     kt = torch.randn(h_kv, T, 128, generator=gen).half()
     vt = torch.randn(h_kv, T, 128, generator=gen).half()
     q = torch.randn(h_kv, G, 128, generator=gen).half()
     scale = 128 ** -0.5
     n_parts = spectral.partial_count(dp, S, q.to(DEV), rope)
-    blocked = rope == k2b.ROPE_FP16_TABLES and S % 128 == 0 and 2 * dp.k_page_bytes <= 57344
+    blocked = rope == k2b.ROPE_FP16_TABLES and S % 128 == 0 and 2 * dp.k_page_bytes <= 57344 and not lloyd
     assert n_parts == (S // 128 if blocked else S // 64)
     out = spectral.decode_attention(dp, kp, k_ids, vp, v_ids, S, consts, q.to(DEV), scale,
                                     k_win=kt.to(DEV) if T else None, v_win=vt.to(DEV) if T else None,
                                     apply_rope=rope, out_dtype=torch.float32)
     L = O.Layout(pack.bits.numpy())
-    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
-    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L)).float(), h_kv)
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L, lloyd)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L, lloyd=lloyd)).float(),
+                          h_kv)
     cos, sin = A.rope_cos_sin(torch.tensor(consts.inv_freq), torch.arange(S))
     if rope == k2b.ROPE_FP16_TABLES:
         cos, sin = cos.half().float(), sin.half().float()
@@ -255,7 +273,7 @@ def test_partial_form_decode_matches_oracle(h_kv, G, T, rope, S):
     Vw = torch.cat([Vb.float(), vt.float().to(DEV)], 1)
     alt = (torch.softmax(sw, -1) @ Vw).cpu().double()
     d_alt = (o - alt).abs().max().item()
-    print(f"h_kv {h_kv} G {G} T {T} rope {rope} S {S} ({n_parts} partials): partial-form decode vs oracle "
+    print(f"{payload} h_kv {h_kv} G {G} T {T} rope {rope} S {S} ({n_parts} partials): partial-form decode vs oracle "
           f"max_abs {err:.3e} rel {rel:.3e}; vs scores form {d_alt:.3e}", flush=True)
     assert err <= 2e-3 and rel <= 1e-2 and d_alt <= 2e-3
 

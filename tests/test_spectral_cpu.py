@@ -191,8 +191,11 @@ def test_recipe_and_construction_guards(tmp_path):
             spec_pair(arm, pack_path=str(path))
     with pytest.raises(ValueError, match="pack-path"):
         spec_pair("k4ph_b2.5")
-    with pytest.raises(NotImplementedError, match="rtn payload"):
-        PackedStreamingCache(cfg, *spec_pair("k4ph_b2.5_lq", pack_path=str(path)))
+    kl, vl = spec_pair("k4ph_b2.5_lq", pack_path=str(path))
+    assert PackedStreamingCache(cfg, kl, vl).k_spec.payload_quant == "lloyd"
+    with pytest.raises(NotImplementedError, match="lloyd payloads"):
+        PackedStreamingCache(cfg, CacheCodecSpec(arm="spectral", pre_rope=True, pack_path=str(path), budget=2.5,
+                                                 payload_quant="nf4"), vl)
     k, v = spec_pair("k4ph_b2.5", pack_path=str(path))
     assert (k.arm, k.pre_rope, k.budget, v.arm, v.bits) == ("spectral", True, 2.5, "turboquant_mse_perhead", 2)
     with pytest.raises(AssertionError, match="pre_rope"):
@@ -364,3 +367,59 @@ def test_mixed_decoder_charge():
                                        + spectral.mixed_dec_charge(C, S, tiers, 100, 100)), rel=1e-14)
     with pytest.raises(ValueError):
         spectral.mixed_dec_charge(C, S, tiers, 100, 101)
+
+
+def _lloyd_levels(variants):
+    return {b: variants[f"codebook_{b}"] for b in (2, 3, 4, 5, 6, 8)}
+
+
+def test_lloyd_payload_matches_reference(variants):
+    """The oracle's Lloyd payload on the reference's Y: every level index of
+    every tier equal, the steps within 2e-6 (the refits' fp32 sums run in a
+    fixed order here), the dequantized keys (fp32 steps) within 1e-5; pages
+    round-trip the indices."""
+    bits = variants["bits_b2.5"]
+    L = O.Layout(bits)
+    lloyd = _lloyd_levels(variants)
+    codes, scales = O.quantize(L.permute_cols(variants["Y"]), L, lloyd)
+    for b, c in O.tier_columns(bits).items():
+        k = np.array([np.nonzero(L.perm == x)[0][0] for x in c])
+        mine = codes[:, :, k].transpose(2, 0, 1).reshape(len(c), -1)
+        np.testing.assert_array_equal(mine, variants[f"lq_codes_t{b}"])
+        assert np.abs(scales[:, k].T / variants[f"lq_scale_t{b}"][..., 0] - 1).max() < 2e-6
+    Mh = O.dequant(codes, scales, variants["dec"], L, fp16_scales=False, lloyd=lloyd)
+    assert np.abs(Mh - variants["lq_M_hat"]).max() < 1e-5
+    c2, s2 = O.unpack_pages(O.pack_pages(codes, scales, L, lloyd=True), L, lloyd=True)
+    assert np.array_equal(c2, codes) and np.array_equal(s2, scales.astype(np.float16).astype(np.float32))
+    assert codes.min() >= 0 and all(codes[:, :, L.col_bits == b].max() < 2 ** b for b in set(L.slice_bits.tolist()))
+
+
+def test_lloyd_codes_are_nearest_levels_and_refits_matter(variants):
+    """What the payload is, checked without its formulas: each index names
+    the level nearest to value / step (a midpoint off by one level, or codes
+    bucketized against the levels instead of the midpoints, fails it), and
+    the step is the least-squares one for the final indices up to their
+    last reassignment; without the 3 refits the indices change."""
+    cb = variants["codebook_3"]
+    G = variants["Y"][:, :40].T.reshape(-1, 64)[:160].astype(np.float32)
+    q, s = O.lloyd_quantize_groups(G, cb)
+    x = G / s[:, None]
+    dist = np.abs(x[..., None] - cb[None, None, :].astype(np.float64))
+    assert np.all(dist[np.arange(G.shape[0])[:, None], np.arange(64)[None, :], q] <= dist.min(axis=2) + 1e-12)
+    q0, _ = O.lloyd_quantize_groups(G, cb, n_iter=0)
+    assert (q0 != q).any()
+    lv = cb[q].astype(np.float64)
+    ls = (G * lv).sum(1) / (lv * lv).sum(1)
+    assert np.median(np.abs(ls / s - 1)) < 1e-3
+
+
+def test_lloyd_level_table_is_the_reference_codebook(variants):
+    """The device table the kernels read: gaussian_codebook(b) of b = 2, 3,
+    4, 5, 6, 8 at offsets 2^b - 4 and 124, equal to the reference's."""
+    t = spectral.lloyd_levels("cpu").numpy()
+    for b in (2, 3, 4, 5, 6, 8):
+        off = 124 if b == 8 else 2 ** b - 4
+        assert np.array_equal(t[off: off + 2 ** b], variants[f"codebook_{b}"])
+    dp = spectral.DevicePack(synthetic_pack(2, 2.5, seed=1), 2, "cpu", "lloyd")
+    assert dp.layout().lloyd_levels == dp.lloyd_levels.data_ptr()
+    assert spectral.DevicePack(synthetic_pack(2, 2.5, seed=1), 2, "cpu").layout().lloyd_levels is None
