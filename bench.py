@@ -71,6 +71,8 @@ def parse():
     ap.add_argument("--prefill-ctx", type=int, default=8192)
     ap.add_argument("--prefill-chunk", type=int, default=512)
     ap.add_argument("--spectral-budget", type=float, default=2.5)
+    ap.add_argument("--spectral-payload", choices=["rtn", "lloyd"], default="rtn",
+                    help="spectral workload: the key payload (lloyd: the recipe's _lq suffix)")
     ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch", "spectral", "e2e"],
                     default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
@@ -681,7 +683,8 @@ def run_spectral(args, torch, dev) -> dict:
     pack = spectral.SpectralPack(enc=(w.sqrt()[:, None] * E).float(), dec=(w.rsqrt()[:, None] * E).float(),
                                  lam=lam.float(), bits=spectral.allocate_bits(lam, args.spectral_budget),
                                  budget=args.spectral_budget)
-    k_spec, v_spec = spec_pair(f"k4ph_b{args.spectral_budget:g}", pack_path="synthetic")
+    recipe = f"k4ph_b{args.spectral_budget:g}" + ("_lq" if args.spectral_payload == "lloyd" else "")
+    k_spec, v_spec = spec_pair(recipe, pack_path="synthetic")
     lay = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=args.window, pack=pack)
     N = args.ctx
     dec = pack.dec.to(dev)
@@ -744,9 +747,13 @@ def run_spectral(args, torch, dev) -> dict:
         L = O.Layout(pack.bits.numpy())
         rng = np.random.default_rng(0)
         codes = np.zeros((S // 64, 64, L.c_pad), np.int64)
+        lloyd = None
+        if args.spectral_payload == "lloyd":
+            lloyd = {b: OC.gaussian_codebook(b).numpy() for b in set(L.slice_bits.tolist())}
         for b in set(L.slice_bits.tolist()):
             k = L.col_bits == b
-            codes[:, :, k] = rng.integers(-(1 << (b - 1)), 1 << (b - 1), (S // 64, 64, int(k.sum())))
+            lo = 0 if lloyd else -(1 << (b - 1))
+            codes[:, :, k] = rng.integers(lo, lo + (1 << b), (S // 64, 64, int(k.sum())))
         steps = rng.random((S // 64, L.c_pad)).astype(np.float32) * 0.1
         idx = torch.randint(0, 4, (S, C), dtype=torch.int16)
         norms = torch.rand(S, H_KV) + 0.5
@@ -756,7 +763,8 @@ def run_spectral(args, torch, dev) -> dict:
         torch.set_num_threads(threads)
 
         def cpu_step():
-            Kc = OC.from_matrix(torch.from_numpy(O.dequant(codes, steps, pack.dec.numpy(), L)).float(), H_KV)
+            Kc = OC.from_matrix(torch.from_numpy(O.dequant(codes, steps, pack.dec.numpy(), L, lloyd=lloyd)).float(),
+                                H_KV)
             Vc = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=H_KV), H_KV)
             return A.naive_dense_attention(qf, A.apply_rope(Kc, cos, sin), Vc, G, scale)
 
@@ -777,11 +785,12 @@ def run_spectral(args, torch, dev) -> dict:
         "metric": SPECTRAL_METRIC, "value": round(call_us, 2), "unit": "us/layer-call", "n_gpus": 1,
         "steps": reps, "warmup": 3, "ms_per_step": round(call_us / 1e3, 4), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
-        "config": {"workload": (f"k4ph_b{args.spectral_budget:g} decode call: {P} packed + "
+        "config": {"workload": (f"{recipe} decode call: {P} packed + "
                                 f"{N - P} fp16 window tokens, 32q/8kv heads, d 128, synthetic pack "
                                 f"(c_used {c_used} of {C}, c_pad {dp.c_pad}, {spectral.payload_bpe(pack.bits):.3f} "
                                 f"payload bpe keys)"),
-                   "ctx": N, "packed_tokens": P, "budget": args.spectral_budget, "c_used": c_used,
+                   "ctx": N, "packed_tokens": P, "budget": args.spectral_budget, "payload": args.spectral_payload,
+                   "c_used": c_used,
                    "c_pad": dp.c_pad, "key_page_bytes": dp.k_page_bytes},
         "roofline": {"bound": "mfma", "kernel": (("spectral_partial128_kernel (pages -> per-128-token-block softmax partials)"
                                                 if n_parts == P // 128 else
@@ -789,7 +798,9 @@ def run_spectral(args, torch, dev) -> dict:
                      "achieved": round(flops / (deq_us * 1e-6) / 1e12, 1), "peak": MFMA_FP16_DENSE_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (deq_us * 1e-6) / 1e12 / MFMA_FP16_DENSE_TFLOPS, 4),
                      "traffic": measured_traffic({"ctx": N, "window": args.window, "budget": args.spectral_budget,
-                                                  "c_pad": dp.c_pad, "form": "partials"}, SPECTRAL_TRAFFIC_FILE),
+                                                  "c_pad": dp.c_pad, "form": "partials",
+                                                  **({"payload": "lloyd"} if args.spectral_payload == "lloyd" else {})},
+                                                 SPECTRAL_TRAFFIC_FILE),
                      "flops_per_launch": flops, "avg_launch_us": round(deq_us, 3),
                      "hbm_bytes_per_launch": page_bytes + out_bytes,
                      "hbm_frac": round((page_bytes + out_bytes) / (deq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},

@@ -22,6 +22,20 @@ __device__ __forceinline__ int sp_width(int b) { return b == 2 ? 2 : (b <= 4 ? 4
 constexpr int kLqLevels = BMX_SPECTRAL_LLOYD_LEVELS;
 __device__ __forceinline__ int lq_off(int b) { return b == 8 ? 124 : (1 << b) - 4; }
 
+// Pair tables of the narrow Lloyd tiers (2, 3, 4): entry key of tier b holds
+// the fp16 levels of the two codes in the key's 2w bits (w the container
+// width), low code first; 16 entries for tier 2, 256 each for tiers 3 and 4.
+constexpr int kLqPairs = 16 + 256 + 256;
+__device__ __forceinline__ int lq_pair_base(int b) { return b == 2 ? 0 : (b == 3 ? 16 : 272); }
+
+// Entry i of the pair tables from the fp32 levels lq (kLqLevels)
+__device__ __forceinline__ uint32_t lq_pair_entry(const float* lq, int i) {
+  const int b = i < 16 ? 2 : (i < 272 ? 3 : 4), key = i - lq_pair_base(b);
+  const int w = sp_width(b), m = (1 << b) - 1;
+  const half2_t h = {(_Float16)lq[lq_off(b) + (key & m)], (_Float16)lq[lq_off(b) + ((key >> w) & m)]};
+  return as_u32(h);
+}
+
 // Index of the level nearest to x among tier b's sorted levels: the number of
 // the 2^b - 1 midpoints mid[0 ..] below x (torch.bucketize, right=False)
 __device__ __forceinline__ int lq_index(const float* mid, int b, float x) {
@@ -368,6 +382,7 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   // fp16 codebook levels of the 4 codes of one value-code byte (the P.V B operand)
   __shared__ uint2 s_cbl[256];
   __shared__ float s_lq[kLloyd ? kLqLevels : 1];   // the key payload's Lloyd levels
+  __shared__ uint32_t s_lqp[kLloyd ? kLqPairs : 1];   // and their fp16 pair tables
   extern __shared__ __align__(16) uint8_t sp_dyn[];
   uint8_t* kp = sp_dyn;                                 // the key page, until the main loop ends
   DqTile* s_tile = reinterpret_cast<DqTile*>(sp_dyn);   // then the staging tiles
@@ -389,7 +404,12 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     kpw[i] = reinterpret_cast<const u32x4_t*>(page)[min(tid + 512 * i, n16 - 1)];
   const uint32_t tabv = (uint32_t)a.slice_tab[min(tid, n_sl - 1)];   // n_sl <= 134 < 512
   float lqv = 0.f;
-  if constexpr (kLloyd) lqv = a.lq[min(tid, kLqLevels - 1)];
+  uint32_t lqp0 = 0u, lqp1 = 0u;
+  if constexpr (kLloyd) {
+    lqv = a.lq[min(tid, kLqLevels - 1)];
+    lqp0 = lq_pair_entry(a.lq, tid);
+    lqp1 = lq_pair_entry(a.lq, min(tid + 512, kLqPairs - 1));
+  }
   uint2 vcd[4], nrm[4];
 #pragma unroll
   for (int pg = 0; pg < 4; ++pg) {
@@ -452,6 +472,8 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   if (tid < n_sl) s_tab[tid] = tabv;
   if constexpr (kLloyd) {
     if (tid < kLqLevels) s_lq[tid] = lqv;
+    s_lqp[tid] = lqp0;
+    if (tid + 512 < kLqPairs) s_lqp[tid + 512] = lqp1;
   }
 #pragma unroll
   for (int i = 0; i < kSpPageLoads; ++i)
@@ -484,10 +506,14 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     *reinterpret_cast<uint2*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) =
         make_uint2(ok ? sp_hmul2(c.x, f0) : 0u, ok ? sp_hmul2(c.y, f1) : 0u);
   };
-  // Lloyd: virtual step u's B tile (see nn above)
-  auto decode_lq = [&](int u, int buf) {
-    const int ks = u < nn ? u : nn + ((u - nn) >> 1);
-    const bool rem = u >= nn && ((u - nn) & 1);
+  // Lloyd: virtual step u's B tile (see nn above).  A step taken once holds
+  // narrow slices only: fp16 level pairs from the pair tables times the fp16
+  // steps (two roundings, against the exact product: within the bound of the
+  // keys); a split step the fp32 level times the B factor, in two halves.
+  auto decode_lq = [&](int u, int buf, auto split_t) {
+    constexpr bool split = decltype(split_t)::value;   // u >= nn, known where it is called
+    const int ks = split ? nn + ((u - nn) >> 1) : u;
+    const bool rem = split && ((u - nn) & 1);
     const int s = 4 * ks + dsq, sc = min(s, n_sl - 1);
     const uint32_t tab = s_tab[sc];
     const int b = (int)(tab >> 24), off = (int)(tab & 0xFFFFFFu), w = sp_width(b);
@@ -495,23 +521,35 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     const uint2 cw = *reinterpret_cast<const uint2*>(kp + (p & ~7));
     const uint4 f = sp_b_factor(kp, sc, b);
     const uint64_t word = ((((uint64_t)cw.y << 32) | cw.x) >> (8 * (p & 7))) >> (4 * dhf * w);
-    const half2_t f01 = as_h2(dhf ? f.z : f.x), f23 = as_h2(dhf ? f.w : f.y);
-    const float fe[4] = {(float)f01[0], (float)f01[1], (float)f23[0], (float)f23[1]};
-    const float* lv = s_lq + lq_off(b);
-    const uint32_t mask = (1u << w) - 1u;
-    const bool ok = s < n_sl;
-    _Float16 o[4];
+    const uint32_t f0 = dhf ? f.z : f.x, f1 = dhf ? f.w : f.y;
+    // every load unconditional and the result masked: a select of an LDS
+    // load becomes a branch around it, which splits the loop's basic block
+    const uint32_t okm = s < n_sl ? 0xFFFFFFFFu : 0u;
+    uint2 o;
+    if constexpr (!split) {
+      const int base = lq_pair_base(b);
+      const uint32_t km = ((1u << (2 * w)) - 1u) & 0xFFu;   // narrow: w <= 4
+      o.x = sp_hmul2(s_lqp[base + ((uint32_t)word & km)], f0) & okm;
+      o.y = sp_hmul2(s_lqp[base + ((uint32_t)(word >> (2 * w)) & km)], f1) & okm;
+    } else {
+      const half2_t f01 = as_h2(f0), f23 = as_h2(f1);
+      const float fe[4] = {(float)f01[0], (float)f01[1], (float)f23[0], (float)f23[1]};
+      const float* lv = s_lq + lq_off(b);
+      const uint32_t mask = (1u << w) - 1u;
+      _Float16 h[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v = lv[(uint32_t)(word >> (e * w)) & mask] * fe[e];
-      const _Float16 hi = (_Float16)v;
-      o[e] = ok ? (rem ? (_Float16)(v - (float)hi) : hi) : (_Float16)0.f;
+      for (int e = 0; e < 4; ++e) {
+        const float v = lv[(uint32_t)(word >> (e * w)) & mask] * fe[e];
+        const _Float16 hv = (_Float16)v;
+        h[e] = rem ? (_Float16)(v - (float)hv) : hv;
+      }
+      o = make_uint2(as_u32(half2_t{h[0], h[1]}) & okm, as_u32(half2_t{h[2], h[3]}) & okm);
     }
-    *reinterpret_cast<uint2*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) =
-        make_uint2(as_u32(half2_t{o[0], o[1]}), as_u32(half2_t{o[2], o[3]}));
+    *reinterpret_cast<uint2*>(&s_b[buf][dt][8 * dsq + 4 * dhf]) = o;
   };
-  auto decode = [&](int u, int buf) {
-    if constexpr (kLloyd) decode_lq(u, buf);
+  // decode(u, buf, split): split tells a Lloyd decode that u >= nn
+  auto decode = [&](int u, int buf, auto split_t) {
+    if constexpr (kLloyd) decode_lq(u, buf, split_t);
     else decode_b(u, buf);
   };
 
@@ -523,8 +561,13 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   // Two steps per workgroup barrier: buffers 2p and 2p + 1 hold steps ks and
   // ks + 1 while the next two are decoded into the other pair; each step's
   // MFMAs are interleaved with the next pair's decode (VALU and LDS reads).
-  decode(0, 0);
-  decode(1, 1);
+  if (nn >= 2) {
+    decode(0, 0, std::false_type{});
+    decode(1, 1, std::false_type{});
+  } else {
+    decode(0, 0, std::true_type{});
+    decode(1, 1, std::true_type{});
+  }
   __syncthreads();
   half8_t A[8];
   // A = the dec rows, times the group's steps of the lane's 8 columns in a
@@ -562,40 +605,42 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   // compiler's own interleave measured faster than a fixed MFMA/VALU/LDS
   // pattern
   const int n_pairs = n_steps >> 1, n_narrow_pairs = n_narrow >> 1;
-  auto pair = [&](int kq, auto wide) {
+  auto pair = [&](int kq, auto wide, auto split_t) {
     const int ks = 2 * kq, pb = kq & 1;
     if (head_ok) {
       mfma_step(ks, 2 * pb, wide);
-      decode(ks + 2, 2 * (pb ^ 1));
+      decode(ks + 2, 2 * (pb ^ 1), split_t);
       mfma_step(ks + 1, 2 * pb + 1, wide);
-      decode(ks + 3, 2 * (pb ^ 1) + 1);
+      decode(ks + 3, 2 * (pb ^ 1) + 1, split_t);
     } else {
-      decode(ks + 2, 2 * (pb ^ 1));
-      decode(ks + 3, 2 * (pb ^ 1) + 1);
+      decode(ks + 2, 2 * (pb ^ 1), split_t);
+      decode(ks + 3, 2 * (pb ^ 1) + 1, split_t);
     }
     lds_barrier();   // the next pair decoded, this pair read by every wave
   };
   int kq = 0;
   if constexpr (kLloyd) {
-    // the narrow pairs, then one step per pair: its two halves on one A operand
-    for (; kq < (nn >> 1); ++kq) pair(kq, std::false_type{});
+    // the narrow pairs (the last of them decodes the first split step), then
+    // one step per pair: its two halves on one A operand
+    for (; kq + 1 < (nn >> 1); ++kq) pair(kq, std::false_type{}, std::false_type{});
+    if (kq < (nn >> 1)) pair(kq++, std::false_type{}, std::true_type{});
     for (; kq < (nn >> 1) + n_steps - nn; ++kq) {
       const int u = 2 * kq, pb = kq & 1;
       if (head_ok) {
         a_operand(nn + kq - (nn >> 1), std::true_type{});
         mfma_b(2 * pb);
-        decode(u + 2, 2 * (pb ^ 1));
+        decode(u + 2, 2 * (pb ^ 1), std::true_type{});
         mfma_b(2 * pb + 1);
-        decode(u + 3, 2 * (pb ^ 1) + 1);
+        decode(u + 3, 2 * (pb ^ 1) + 1, std::true_type{});
       } else {
-        decode(u + 2, 2 * (pb ^ 1));
-        decode(u + 3, 2 * (pb ^ 1) + 1);
+        decode(u + 2, 2 * (pb ^ 1), std::true_type{});
+        decode(u + 3, 2 * (pb ^ 1) + 1, std::true_type{});
       }
       lds_barrier();
     }
   } else {
-    for (; kq < n_narrow_pairs; ++kq) pair(kq, std::false_type{});
-    for (; kq < n_pairs; ++kq) pair(kq, std::true_type{});
+    for (; kq < n_narrow_pairs; ++kq) pair(kq, std::false_type{}, std::false_type{});
+    for (; kq < n_pairs; ++kq) pair(kq, std::true_type{}, std::false_type{});
     if ((n_steps & 1) && head_ok) mfma_step(n_steps - 1, 2 * (n_pairs & 1), std::true_type{});
     // the last step's A factors read the key page, whose space takes the
     // staging tiles below
@@ -791,9 +836,11 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 // scores through LDS, then each takes 4 of the head's 8 rotated value-channel
 // blocks.  The
 // RoPE table is the fp16-rounded one (apply_rope 2), kept as fp16 pairs.
+// kLloyd: the Lloyd payload, decoded as in spectral_dequant_kernel<true>.
 constexpr int kSpBlk = 128;
 constexpr int kSpBlkMaxPages = 56 * 1024;   // two key pages staged in LDS at most
 
+template <bool kLloyd>
 __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequantKArgs a, int kpb) {
   const int blk = blockIdx.x, hq = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
@@ -807,6 +854,8 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
   __shared__ uint2 s_cbl[256];
   __shared__ uint2 s_vcd[4][8][64];   // (local head, value page, lane)
   __shared__ uint2 s_nrm[4][8][4];    // (local head, value page, quarter)
+  __shared__ float s_lq[kLloyd ? kLqLevels : 1];   // the key payload's Lloyd levels
+  __shared__ uint32_t s_lqp[kLloyd ? kLqPairs : 1];   // and their fp16 pair tables
   extern __shared__ __align__(16) uint8_t sp_dyn[];   // the two key pages; after the loop, the score exchange
   const int n_sl = a.c_pad >> 3;
   const int fj = tid & 63;
@@ -827,6 +876,13 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     kw1[i] = reinterpret_cast<const u32x4_t*>(pg1)[c];
   }
   const uint32_t tabv = (uint32_t)a.slice_tab[min(tid, n_sl - 1)];
+  float lqv = 0.f;
+  uint32_t lqp0 = 0u, lqp1 = 0u;
+  if constexpr (kLloyd) {
+    lqv = a.lq[min(tid, kLqLevels - 1)];
+    lqp0 = lq_pair_entry(a.lq, tid);
+    lqp1 = lq_pair_entry(a.lq, min(tid + 512, kLqPairs - 1));
+  }
   // value pages: thread (local head tid >> 7, page (tid >> 6) & 1 + 2 k, lane)
   uint2 vcw[4], nrw[4];
   const int vh = min(4 * hq + (tid >> 7), a.h_kv - 1), vl = tid & 63;
@@ -879,6 +935,11 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     }
   }
   if (tid < n_sl) s_tab[tid] = tabv;
+  if constexpr (kLloyd) {
+    if (tid < kLqLevels) s_lq[tid] = lqv;
+    s_lqp[tid] = lqp0;
+    if (tid + 512 < kLqPairs) s_lqp[tid + 512] = lqp1;
+  }
   uint8_t* kp0 = sp_dyn;
   uint8_t* kp1 = sp_dyn + kpb;
 #pragma unroll
@@ -894,8 +955,10 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     if ((vl & 15) == 0) s_nrm[tid >> 7][vp_i][vl >> 4] = nrw[k];
   }
   const int n_steps = a.c_pad32 / 32;
-  // a barrier: s_tab, s_cbl, s_cs, the key pages, the value codes
+  // a barrier: s_tab, s_cbl, s_cs, s_lq, the key pages, the value codes
   const int n_narrow = sp_narrow_steps(tabv, tid, n_sl, n_steps);
+  // Lloyd: virtual steps as in spectral_dequant_kernel<true>
+  const int nn = kLloyd ? (n_narrow & ~1) : n_steps;
 
   // lane (sq, t) of wave w decodes the 8 codes of slice 4 step + sq, token 16w + t
   // (a row of 16 lanes shares one slice, so that its code-word reads fall in
@@ -919,19 +982,67 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
                                ok ? sp_hmul2(hi.x, f.z) : 0u, ok ? sp_hmul2(hi.y, f.w) : 0u);
     *reinterpret_cast<uint4*>(&s_b[buf][dt][8 * dsq]) = v;
   };
+  auto decode_lq = [&](int u, int buf, auto split_t) {
+    constexpr bool split = decltype(split_t)::value;   // u >= nn, known where it is called
+    const int ks = split ? nn + ((u - nn) >> 1) : u;
+    const bool rem = split && ((u - nn) & 1);
+    const int s = 4 * ks + dsq, sc = min(s, n_sl - 1);
+    const uint32_t tab = s_tab[sc];
+    const int b = (int)(tab >> 24), off = (int)(tab & 0xFFFFFFu), w = sp_width(b);
+    const int pp = off + dtp * w;
+    const uint2 cw = *reinterpret_cast<const uint2*>(kpt + (pp & ~7));
+    const uint4 f = sp_b_factor(kpt, sc, b);
+    const uint64_t word = (((uint64_t)cw.y << 32) | cw.x) >> (8 * (pp & 7));
+    const uint32_t fw[4] = {f.x, f.y, f.z, f.w};
+    const uint32_t okm = s < n_sl ? 0xFFFFFFFFu : 0u;   // loads unconditional, results masked
+    uint32_t o[4];
+    if constexpr (!split) {
+      const int base = lq_pair_base(b);
+      const uint32_t km = ((1u << (2 * w)) - 1u) & 0xFFu;   // narrow: w <= 4
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2)
+        o[e2] = sp_hmul2(s_lqp[base + ((uint32_t)(word >> (2 * e2 * w)) & km)], fw[e2]) & okm;
+    } else {
+      const float* lv = s_lq + lq_off(b);
+      const uint32_t mask = (1u << w) - 1u;
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const half2_t fe = as_h2(fw[e2]);
+        half2_t r;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const float v = lv[(uint32_t)(word >> ((2 * e2 + i) * w)) & mask] * (float)fe[i];
+          const _Float16 h16 = (_Float16)v;
+          r[i] = rem ? (_Float16)(v - (float)h16) : h16;
+        }
+        o[e2] = as_u32(r) & okm;
+      }
+    }
+    *reinterpret_cast<uint4*>(&s_b[buf][dt][8 * dsq]) = make_uint4(o[0], o[1], o[2], o[3]);
+  };
+  // decode(u, buf, split): split tells a Lloyd decode that u >= nn
+  auto decode = [&](int u, int buf, auto split_t) {
+    if constexpr (kLloyd) decode_lq(u, buf, split_t);
+    else decode_b(u, buf);
+  };
 
   float4_t acc[4][8];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int tt = 0; tt < 8; ++tt) acc[i][tt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  decode_b(0, 0);
-  decode_b(1, 1);
+  if (nn >= 2) {
+    decode(0, 0, std::false_type{});
+    decode(1, 1, std::false_type{});
+  } else {
+    decode(0, 0, std::true_type{});
+    decode(1, 1, std::true_type{});
+  }
   __syncthreads();
-  auto mfma_step = [&](int ks, int buf, auto wide) {
-    // A = the dec rows, times each page's steps of the lane's 8 columns in a
-    // step with wider tiers
-    half8_t A[2][4];
+  half8_t A[2][4];
+  // A = the dec rows, times each page's steps of the lane's 8 columns in a
+  // step with wider tiers; then the next step's rows are loaded
+  auto a_operand = [&](int ks, auto wide) {
     if constexpr (decltype(wide)::value) {
       const half8_t f0 = sp_a_factor(kp0, s_tab, 4 * ks + q, n_sl), f1 = sp_a_factor(kp1, s_tab, 4 * ks + q, n_sl);
 #pragma unroll
@@ -947,6 +1058,8 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       An[i] = *reinterpret_cast<const half8_t*>(decb + rt(i) * tile_stride + step_stride * kn);
+  };
+  auto mfma_b = [&](int buf) {
     half8_t B[8];
 #pragma unroll
     for (int tt = 0; tt < 8; ++tt) B[tt] = *reinterpret_cast<const half8_t*>(&s_b[buf][16 * tt + n][8 * q]);
@@ -956,23 +1069,43 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
       for (int tt = 0; tt < 8; ++tt)
         acc[i][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[tt >> 2][i], B[tt], acc[i][tt], 0, 0, 0);
   };
+  auto mfma_step = [&](int ks, int buf, auto wide) {
+    a_operand(ks, wide);
+    mfma_b(buf);
+  };
   // whole pairs of steps in one basic block each (decodes past the last step
   // store zeros into buffers nobody reads), then an odd last step; the
   // compiler's own interleave of the MFMAs, the decode and the dec loads
   // measured faster here than a fixed MFMA/VALU/LDS pattern
   const int n_pairs = n_steps >> 1, n_narrow_pairs = n_narrow >> 1;
-  auto pair = [&](int kp, auto wide) {
+  auto pair = [&](int kp, auto wide, auto split_t) {
     const int ks = 2 * kp, pb = kp & 1;
     mfma_step(ks, 2 * pb, wide);
-    decode_b(ks + 2, 2 * (pb ^ 1));
+    decode(ks + 2, 2 * (pb ^ 1), split_t);
     mfma_step(ks + 1, 2 * pb + 1, wide);
-    decode_b(ks + 3, 2 * (pb ^ 1) + 1);
+    decode(ks + 3, 2 * (pb ^ 1) + 1, split_t);
     lds_barrier();
   };
   int kp = 0;
-  for (; kp < n_narrow_pairs; ++kp) pair(kp, std::false_type{});
-  for (; kp < n_pairs; ++kp) pair(kp, std::true_type{});
-  if (n_steps & 1) mfma_step(n_steps - 1, 2 * (n_pairs & 1), std::true_type{});
+  if constexpr (kLloyd) {
+    // the narrow pairs (the last of them decodes the first split step), then
+    // one step per pair: its two halves on one A operand
+    for (; kp + 1 < (nn >> 1); ++kp) pair(kp, std::false_type{}, std::false_type{});
+    if (kp < (nn >> 1)) pair(kp++, std::false_type{}, std::true_type{});
+    for (; kp < (nn >> 1) + n_steps - nn; ++kp) {
+      const int u = 2 * kp, pb = kp & 1;
+      a_operand(nn + kp - (nn >> 1), std::true_type{});
+      mfma_b(2 * pb);
+      decode(u + 2, 2 * (pb ^ 1), std::true_type{});
+      mfma_b(2 * pb + 1);
+      decode(u + 3, 2 * (pb ^ 1) + 1, std::true_type{});
+      lds_barrier();
+    }
+  } else {
+    for (; kp < n_narrow_pairs; ++kp) pair(kp, std::false_type{}, std::false_type{});
+    for (; kp < n_pairs; ++kp) pair(kp, std::true_type{}, std::false_type{});
+    if (n_steps & 1) mfma_step(n_steps - 1, 2 * (n_pairs & 1), std::true_type{});
+  }
 
   // ---- query fragments of this wave's channels: bb = 2 r2 + bl ----
   half8_t qf[2];
@@ -1363,7 +1496,7 @@ static bool dtype_ok(int d) { return d == BMX_K2B_F16 || d == BMX_K2B_F32 || d =
 // fit in LDS together; the partials pointer itself is not consulted, so the
 // count below can be asked before the buffer exists.
 static bool sp_block_shape(const bmx_spectral_dequant_args* a) {
-  return a->q && !a->k_out && !a->L.lloyd_levels && a->apply_rope == 2 && a->n_tokens % kSpBlk == 0 &&
+  return a->q && !a->k_out && a->apply_rope == 2 && a->n_tokens % kSpBlk == 0 &&
          2 * (int64_t)a->L.k_page_bytes <= kSpBlkMaxPages;
 }
 
@@ -1449,8 +1582,12 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   if (sp_blocked(a)) {
     const int kpb = a->L.k_page_bytes;
     const size_t dyn = std::max<size_t>(2 * (size_t)kpb, (size_t)8 * 4 * 64 * 16);   // pages, then the exchange
-    hipLaunchKernelGGL(spectral_partial128_kernel, dim3(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4), dim3(512),
-                       dyn, (hipStream_t)stream, k, kpb);
+    if (k.lq)
+      hipLaunchKernelGGL(spectral_partial128_kernel<true>, dim3(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4),
+                         dim3(512), dyn, (hipStream_t)stream, k, kpb);
+    else
+      hipLaunchKernelGGL(spectral_partial128_kernel<false>, dim3(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4),
+                         dim3(512), dyn, (hipStream_t)stream, k, kpb);
   } else if (k.lq) {
     hipLaunchKernelGGL(spectral_dequant_kernel<true>, dim3(a->n_tokens / kGroup), dim3(512),
                        sp_dyn_bytes(a->L.k_page_bytes), (hipStream_t)stream, k);

@@ -230,8 +230,7 @@ def test_partial_form_decode_matches_oracle(h_kv, G, T, rope, S, payload):
     """The decode step through the kernel's partial form (per-block softmax
     partials) and the merge with the window: against the oracle's one-softmax
     attention over the same codes (RoPE by fp32 tables, or by the fp16-rounded
-    tables of an fp16 model), and against the scores form + softmax.  The
-    Lloyd payload runs on 64-token groups."""
+    tables of an fp16 model), and against the scores form + softmax."""
     pack = synthetic_pack(h_kv, 2.5, seed=14)
     M = synthetic_keys(pack, S, seed=15)
     gen = torch.Generator().manual_seed(16)
@@ -244,7 +243,7 @@ def test_partial_form_decode_matches_oracle(h_kv, G, T, rope, S, payload):
     q = torch.randn(h_kv, G, 128, generator=gen).half()
     scale = 128 ** -0.5
     n_parts = spectral.partial_count(dp, S, q.to(DEV), rope)
-    blocked = rope == k2b.ROPE_FP16_TABLES and S % 128 == 0 and 2 * dp.k_page_bytes <= 57344 and not lloyd
+    blocked = rope == k2b.ROPE_FP16_TABLES and S % 128 == 0 and 2 * dp.k_page_bytes <= 57344
     assert n_parts == (S // 128 if blocked else S // 64)
     out = spectral.decode_attention(dp, kp, k_ids, vp, v_ids, S, consts, q.to(DEV), scale,
                                     k_win=kt.to(DEV) if T else None, v_win=vt.to(DEV) if T else None,
