@@ -202,6 +202,8 @@ class SpectralAppendArgs(ct.Structure):
         ("n_v_pool", ct.c_int32),
         ("v_codebook", ct.c_float * 4),
         ("v_sign_bits", ct.c_uint32 * 4),
+        ("v_codec", ct.c_int32),
+        ("v_sign_bits_c", ct.c_uint32 * 32),
     ]
 
 
@@ -231,6 +233,8 @@ class SpectralDequantArgs(ct.Structure):
         ("scores", ct.c_void_p),
         ("partials", ct.c_void_p),
         ("sm_scale", ct.c_float),
+        ("v_codec", ct.c_int32),
+        ("v_sign_bits_c", ct.c_uint32 * 32),
     ]
 
 
@@ -239,7 +243,8 @@ class SpectralMergeArgs(ct.Structure):
                 ("partials", ct.c_void_p), ("q", ct.c_void_p), ("q_dtype", ct.c_int32),
                 ("k_win", ct.c_void_p), ("v_win", ct.c_void_p), ("win_len", ct.c_int32),
                 ("sm_scale", ct.c_float), ("out", ct.c_void_p), ("out_dtype", ct.c_int32),
-                ("v_sign_bits", ct.c_uint32 * 4), ("win_stride_h", ct.c_int64)]
+                ("v_sign_bits", ct.c_uint32 * 4), ("win_stride_h", ct.c_int64),
+                ("v_codec", ct.c_int32), ("v_sign_bits_c", ct.c_uint32 * 32)]
 
 
 EXPORTS = {
@@ -258,6 +263,7 @@ EXPORTS = {
     "bmx_rtn_decode": (ct.c_int, [ct.POINTER(RtnDecodeArgs), ct.c_void_p]),
     "bmx_rtn_dequant": (ct.c_int, [ct.POINTER(RtnDequantArgs), ct.c_void_p]),
     "bmx_spectral_v_page_bytes": (ct.c_int64, [ct.c_int32]),
+    "bmx_spectral_v_page_bytes_codec": (ct.c_int64, [ct.c_int32, ct.c_int32]),
     "bmx_spectral_append": (ct.c_int32, [ct.POINTER(SpectralAppendArgs), ct.c_void_p]),
     "bmx_spectral_dequant": (ct.c_int32, [ct.POINTER(SpectralDequantArgs), ct.c_void_p]),
     "bmx_spectral_merge": (ct.c_int32, [ct.POINTER(SpectralMergeArgs), ct.c_void_p]),

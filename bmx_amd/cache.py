@@ -217,6 +217,12 @@ class PackedStreamingLayer(DynamicLayer):
         # (one per 64-token group; the pool above holds the value pages)
         if self._path == "spectral" and pack is None:
             raise ValueError("the spectral path needs the layer's pack")
+        # spectral values: the per-head codec, or the full-C turboquant_mse of the reference's k4 recipe
+        self._v_codec = "full" if v_spec.arm == "turboquant_mse" else "perhead"
+        if self._path == "spectral" and self._v_codec == "full" and self._h_kv not in (1, 2, 4, 8):
+            raise NotImplementedError(f"full-C turboquant_mse values need C = 128 h_kv a power of two "
+                                      f"(the reference rotates other C with a random orthogonal matrix); "
+                                      f"h_kv {self._h_kv}")
         self._pack = pack
         self._dp: spectral.DevicePack | None = None
         self._kpool: torch.Tensor | None = None
@@ -306,7 +312,7 @@ class PackedStreamingLayer(DynamicLayer):
         if self._path == "k2b":
             return k2b.page_bytes(self._h_kv, self._rank)
         if self._path == "spectral":
-            return int(_lib_v_page_bytes(self._h_kv))
+            return spectral.v_page_bytes(self._h_kv, self._v_codec)
         return rtn.page_bytes(self._h_kv, **self._rtn)
 
     def _commit_spectral(self, k_pre: torch.Tensor, v: torch.Tensor) -> None:
@@ -315,7 +321,8 @@ class PackedStreamingLayer(DynamicLayer):
         pages, 2n key pages of 64 tokens and 8n value pages of 16."""
         dev = v.device
         if self._dp is None:
-            self._dp = spectral.DevicePack(self._pack, self._h_kv, dev, self.k_spec.payload_quant)
+            self._dp = spectral.DevicePack(self._pack, self._h_kv, dev, self.k_spec.payload_quant, self._v_codec,
+                                             self.v_spec.seed)
         n_grp = k_pre.shape[1] // spectral.GROUP
         kf, vf = self._n_kpages, self._n_pages
         cap = 0 if self._kpool is None else self._kpool.shape[0]
@@ -413,7 +420,7 @@ class PackedStreamingLayer(DynamicLayer):
                 else:
                     self._commit(k_pre, v_new)
                     self._quant_bits_k += n_cp * K.bpe_k(self._rank, C) * page_entries
-                self._quant_bits_v += n_cp * K.bpe_v(self._h_kv, C) * page_entries
+                self._quant_bits_v += n_cp * K.bpe_v(1 if self._v_codec == "full" else self._h_kv, C) * page_entries
                 self._committed_S_q = end
             keys = keys[..., end - start:, :]
             values = values[..., end - start:, :]
@@ -524,7 +531,8 @@ class PackedStreamingLayer(DynamicLayer):
         h, d = self._h_kv, self._d_head
         P = self._committed_S_q
         if self._dp is None:   # a step before the first commit: the window alone
-            self._dp = spectral.DevicePack(self._pack, self._h_kv, q.device, self.k_spec.payload_quant)
+            self._dp = spectral.DevicePack(self._pack, self._h_kv, q.device, self.k_spec.payload_quant,
+                                             self._v_codec, self.v_spec.seed)
         qg = q.reshape(h, G, d).contiguous()
         kw = vw = None
         wk, wv = self.window()
@@ -597,11 +605,6 @@ class PackedStreamingLayer(DynamicLayer):
                 q.unsqueeze(0), Kd.repeat_interleave(G, dim=0).unsqueeze(0),
                 Vd.repeat_interleave(G, dim=0).unsqueeze(0), attn_mask=attention_mask, scale=scaling)
         return out.squeeze(0)
-
-
-def _lib_v_page_bytes(h_kv: int) -> int:
-    from . import _lib
-    return _lib.lib().bmx_spectral_v_page_bytes(h_kv)
 
 
 # ------------------------------------------------------------------ cache

@@ -43,8 +43,9 @@ def hadamard_signs(d: int, seed: int) -> tuple:
 
 
 def sign_bits(signs) -> list:
-    """+-1 vector of length 128 -> four uint32 words, bit c set where sign is -1."""
-    words = [0, 0, 0, 0]
+    """+-1 vector -> uint32 words (at least 4), bit c of word c // 32 set where
+    the sign is -1."""
+    words = [0] * max(4, -(-len(signs) // 32))
     for c, s in enumerate(signs):
         if s < 0:
             words[c >> 5] |= 1 << (c & 31)

@@ -21,6 +21,7 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Byte offsets of the five page sections (see include/bmx_k2b.h).
 struct PageLayout {
@@ -235,16 +236,12 @@ __device__ __forceinline__ float level4(uint32_t c, float l0, float l1, float l2
   return (c & 2u) ? hi : lo;
 }
 
-__device__ __forceinline__ void dq_value_tile(uint2 vcd, uint2 nrm, const float codebook[4],
-                                              const uint32_t sign_bits[4], int n, int q, DqTile& tl) {
-  const float l0 = codebook[0], l1 = codebook[1], l2 = codebook[2], l3 = codebook[3];
-  float y[4][8];
-#pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    const uint32_t D = b < 4 ? vcd.x : vcd.y;
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) y[tt][b] = level4((D >> (8 * (b & 3) + 2 * tt)) & 3u, l0, l1, l2, l3);
-  }
+// The rotated-domain values y of one 16-token value tile back to channels:
+// lane 16q + n holds y[tt][b] of token 4q + tt, rotated channel 16b + n; H128
+// (H8 over b, H16 over n across the row), times inv_d and the signs, times
+// the token norms, into tl.v[token][channel].
+__device__ __forceinline__ void dq_value_tile_rot(float (&y)[4][8], uint2 nrm, const uint32_t sign_bits[4],
+                                                  float inv_d, int n, int q, DqTile& tl) {
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
@@ -272,10 +269,23 @@ __device__ __forceinline__ void dq_value_tile(uint2 vcd, uint2 nrm, const float 
     const bool neg = sign_neg(sign_bits, c);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      const float v = y[tt][b] / (float)kD;
+      const float v = y[tt][b] * inv_d;   // inv_d a power of two: exact
       tl.v[4 * q + tt][c] = (neg ? -v : v) * nv[tt];
     }
   }
+}
+
+__device__ __forceinline__ void dq_value_tile(uint2 vcd, uint2 nrm, const float codebook[4],
+                                              const uint32_t sign_bits[4], int n, int q, DqTile& tl) {
+  const float l0 = codebook[0], l1 = codebook[1], l2 = codebook[2], l3 = codebook[3];
+  float y[4][8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const uint32_t D = b < 4 ? vcd.x : vcd.y;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) y[tt][b] = level4((D >> (8 * (b & 3) + 2 * tt)) & 3u, l0, l1, l2, l3);
+  }
+  dq_value_tile_rot(y, nrm, sign_bits, 1.0f / (float)kD, n, q, tl);
 }
 
 }  // namespace bmx

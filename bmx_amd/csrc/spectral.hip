@@ -206,6 +206,97 @@ __global__ __launch_bounds__(512) void spectral_encode_kernel(const SpEncodeKArg
   if (active && wave == 0) reinterpret_cast<uint16_t*>(page)[j] = float_to_half_bits(scale);
 }
 
+struct SpVFullKArgs {
+  int h_kv, n_pool, v_dtype;
+  const void* v;
+  int64_t vsh, vst;
+  uint8_t* pages;
+  const int32_t* page_ids;
+  PageLayout L;
+  float codebook[4];
+  uint32_t sign_c[32];
+};
+
+constexpr int kSpMaxC = 1024;
+
+// The full-C value codec (codecs.py:616-636 at h = 1): grid (16-token pages),
+// block 256.  Per token the fp16 norm of all C channels (squares in 8
+// strided fp32 FMA accumulators, then those left to right: torch's CPU
+// order), the unit row times the C signs, a C-point FWHT in LDS (stages as
+// quant/hadamard.py:19-25), / sqrt(C) * sqrt(C) in fp32, then the 2-bit
+// codes against the codebook's midpoints, packed per 128-channel slice in
+// the per-head VCODE layout.
+__global__ __launch_bounds__(256) void spectral_vfull_kernel(const SpVFullKArgs a) {
+  const int pg = blockIdx.x, tid = threadIdx.x;
+  const int C = kD * a.h_kv;
+  __shared__ float x[kPT][kSpMaxC];
+  __shared__ float s_acc[kPT][8];
+  __shared__ float s_norm[kPT];
+  __shared__ uint8_t code[kPT][kSpMaxC];
+  uint8_t* page = a.pages + clamp_page(a.page_ids[pg], a.n_pool) * (int64_t)a.L.bytes;
+  for (int e = tid; e < kPT * C; e += 256) {
+    const int t = e / C, c = e % C;
+    x[t][c] = sp_load(a.v, (c >> 7) * a.vsh + (int64_t)(pg * kPT + t) * a.vst + (c & (kD - 1)), a.v_dtype);
+  }
+  __syncthreads();
+  if (tid < kPT * 8) {
+    const int t = tid >> 3, j = tid & 7;
+    float acc = 0.f;
+    for (int i = j; i < C; i += 8) acc = __builtin_fmaf(x[t][i], x[t][i], acc);
+    s_acc[t][j] = acc;
+  }
+  __syncthreads();
+  if (tid < kPT) {
+    float ss = s_acc[tid][0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) ss = ss + s_acc[tid][j];
+    const float nrm = fmaxf(__builtin_sqrtf(ss), 1e-12f);
+    const uint16_t nb = float_to_half_bits(nrm);
+    s_norm[tid] = half_bits_to_float(nb);
+    reinterpret_cast<uint16_t*>(page + a.L.vnorm)[tid] = nb;
+  }
+  __syncthreads();
+  for (int e = tid; e < kPT * C; e += 256) {
+    const int t = e / C, c = e % C;
+    const float u = x[t][c] / s_norm[t];
+    x[t][c] = ((a.sign_c[c >> 5] >> (c & 31)) & 1u) ? -u : u;
+  }
+  __syncthreads();
+  for (int hb = 1; hb < C; hb <<= 1) {
+    for (int e = tid; e < kPT * C / 2; e += 256) {
+      const int t = e / (C / 2), pidx = e % (C / 2);
+      const int i0 = (pidx / hb) * 2 * hb + (pidx % hb);
+      const float u = x[t][i0], w = x[t][i0 + hb];
+      x[t][i0] = u + w;
+      x[t][i0 + hb] = u - w;
+    }
+    __syncthreads();
+  }
+  // fl32(sqrt(C)), applied as / then *, as the reference does
+  const float sqrt_c = C == 128 ? 11.313708498984761f : C == 256 ? 16.f : C == 512 ? 22.627416997969522f : 32.f;
+  const float mid0 = (a.codebook[0] + a.codebook[1]) / 2.0f;
+  const float mid1 = (a.codebook[1] + a.codebook[2]) / 2.0f;
+  const float mid2 = (a.codebook[2] + a.codebook[3]) / 2.0f;
+  for (int e = tid; e < kPT * C; e += 256) {
+    const int t = e / C, c = e % C;
+    const float r = (x[t][c] / sqrt_c) * sqrt_c;
+    code[t][c] = (uint8_t)((r > mid0) + (r > mid1) + (r > mid2));
+  }
+  __syncthreads();
+  // slice sl, lane 16q + m, dword w: channel 128 sl + 16 (4w + bb) + m, token 4q + t at bit 8bb + 2t
+  for (int i = tid; i < a.h_kv * 128; i += 256) {
+    const int sl = i >> 7, lane = (i >> 1) & 63, w = i & 1, q = lane >> 4, m = lane & 15;
+    uint32_t dword = 0;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      const int c = 128 * sl + 16 * (4 * w + bb) + m;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dword |= (uint32_t)code[4 * q + t][c] << (8 * bb + 2 * t);
+    }
+    *reinterpret_cast<uint32_t*>(page + a.L.vcode + sl * 512 + lane * 8 + w * 4) = dword;
+  }
+}
+
 struct SpDequantKArgs {
   int h_kv, c_pad, c_pad32, n_tokens, out_rows, apply_rope, n_k_pool, n_v_pool, out_dtype, k_page_bytes;
   const uint8_t* k_pages;
@@ -227,7 +318,43 @@ struct SpDequantKArgs {
   float* partials;
   float sm_scale;
   const float* lq;   // the Lloyd levels, or nullptr (rtn payload)
+  int v_full;        // values: the full-C codec (one norm per token, C-wide codes)
+  uint32_t v_sign_c[32];
 };
+
+// Full-C values, one 16-token page: lane (q, n)'s 2-bit codes of every slice
+// (slice sl at VCODE + 512 sl), and the H_{C/128} row h sign of slice sl
+__device__ __forceinline__ bool vfull_neg(int h, int sl) { return __builtin_popcount((unsigned)(h & sl)) & 1; }
+
+// Rotated-domain values of head h for the lane's 4 tokens x 8 channel
+// blocks: y[tt][b] = sum over slices sl of (-1)^popcount(h & sl) times the
+// level of slice sl's code (then H128 over the slice's channels gives head
+// h's channels, the Kronecker form of the C-point Hadamard)
+__device__ __forceinline__ void vfull_y(const uint8_t* vp, int vcode, int h_kv, int h, int lane, const float cb[4],
+                                        float (&y)[4][8]) {
+  u32x2_t cs[8];
+#pragma unroll
+  for (int sl = 0; sl < 8; ++sl)
+    cs[sl] = *reinterpret_cast<const u32x2_t*>(vp + vcode + min(sl, h_kv - 1) * 512 + lane * 8);
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) y[tt][b] = 0.f;
+#pragma unroll
+  for (int sl = 0; sl < 8; ++sl) {
+    if (sl >= h_kv) break;
+    const bool neg = vfull_neg(h, sl);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const uint32_t D = b < 4 ? cs[sl].x : cs[sl].y;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const float l = level4((D >> (8 * (b & 3) + 2 * tt)) & 3u, cb[0], cb[1], cb[2], cb[3]);
+        y[tt][b] = neg ? y[tt][b] - l : y[tt][b] + l;
+      }
+    }
+  }
+}
 
 constexpr int kSpBRow = 40;   // halves per token row of the staged code tile (32 + 8 pad)
 constexpr int kSpMaxKPage = 72 * 1024;   // key page bytes staged in LDS at most (c_pad 1072, 8 bits: 70768)
@@ -410,12 +537,12 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
     lqp0 = lq_pair_entry(a.lq, tid);
     lqp1 = lq_pair_entry(a.lq, min(tid + 512, kLqPairs - 1));
   }
-  uint2 vcd[4], nrm[4];
+  u32x2_t vcd[4], nrm[4];   // native vectors: an array of uint2 stays in scratch
 #pragma unroll
   for (int pg = 0; pg < 4; ++pg) {
     const uint8_t* vp = a.v_pages + clamp_page(a.v_table[4 * g + pg], a.n_v_pool) * (int64_t)a.VL.bytes;
-    vcd[pg] = *reinterpret_cast<const uint2*>(vp + a.VL.vcode + hh * 512 + lane * 8);
-    nrm[pg] = *reinterpret_cast<const uint2*>(vp + a.VL.vnorm + (hh * kPT + 4 * q) * 2);
+    vcd[pg] = *reinterpret_cast<const u32x2_t*>(vp + a.VL.vcode + hh * 512 + lane * 8);
+    nrm[pg] = *reinterpret_cast<const u32x2_t*>(vp + a.VL.vnorm + ((a.v_full ? 0 : hh * kPT) + 4 * q) * 2);
   }
   // dec tiled: [h][c_pad32 / 32 steps][8 row tiles][16 rows][32 columns], a
   // contiguous KB per (step, row tile): lane 16q + n reads row n, columns 8q ..
@@ -773,12 +900,33 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
         half4_t aw;
 #pragma unroll
         for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[pg][i] * nv[i]);
+        if (a.v_full) {
+          // every slice's codes, A = the weights times H_{C/128}[h][slice]
+          const uint8_t* vp = a.v_pages + clamp_page(a.v_table[4 * g + pg], a.n_v_pool) * (int64_t)a.VL.bytes;
+          u32x2_t cs[8];
 #pragma unroll
-        for (int ct = 0; ct < 8; ++ct) {
-          const uint32_t byte = ((ct < 4 ? vcd[pg].x : vcd[pg].y) >> (8 * (ct & 3))) & 0xFFu;
-          const uint2 lvb = s_cbl[byte];
-          const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
-          pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[ct], 0, 0, 0);
+          for (int sl = 0; sl < 8; ++sl)
+            cs[sl] = *reinterpret_cast<const u32x2_t*>(vp + a.VL.vcode + min(sl, a.h_kv - 1) * 512 + lane * 8);
+#pragma unroll
+          for (int sl = 0; sl < 8; ++sl) {
+            if (sl >= a.h_kv) break;
+            const half4_t as = vfull_neg(h, sl) ? -aw : aw;
+#pragma unroll
+            for (int ct = 0; ct < 8; ++ct) {
+              const uint32_t byte = ((ct < 4 ? cs[sl].x : cs[sl].y) >> (8 * (ct & 3))) & 0xFFu;
+              const uint2 lvb = s_cbl[byte];
+              const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
+              pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(as, vb, pv[ct], 0, 0, 0);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) {
+            const uint32_t byte = ((ct < 4 ? vcd[pg].x : vcd[pg].y) >> (8 * (ct & 3))) & 0xFFu;
+            const uint2 lvb = s_cbl[byte];
+            const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
+            pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[ct], 0, 0, 0);
+          }
         }
       }
       // lane 16q + n holds queries 4q + i, channel 16ct + n: H8 over ct in
@@ -816,7 +964,16 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
   if (head_ok) {
 #pragma unroll
     for (int pg = 0; pg < 4; ++pg) {
-      dq_value_tile(vcd[pg], nrm[pg], a.codebook, a.v_sign_bits, n, q, tl);
+      if (a.v_full) {
+        const uint8_t* vp = a.v_pages + clamp_page(a.v_table[4 * g + pg], a.n_v_pool) * (int64_t)a.VL.bytes;
+        float y[4][8];
+        vfull_y(vp, a.VL.vcode, a.h_kv, h, lane, a.codebook, y);
+        dq_value_tile_rot(y, make_uint2(nrm[pg].x, nrm[pg].y), a.v_sign_c + 4 * h, 1.0f / (float)(kD * a.h_kv), n,
+                          q, tl);
+      } else {
+        dq_value_tile(make_uint2(vcd[pg].x, vcd[pg].y), make_uint2(nrm[pg].x, nrm[pg].y), a.codebook,
+                      a.v_sign_bits, n, q, tl);
+      }
       wave_lds_order();
       dq_store_tile(tl, a.v_out, row_h + 16 * pg, a.out_dtype);
       wave_lds_order();
@@ -837,10 +994,13 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 // blocks.  The
 // RoPE table is the fp16-rounded one (apply_rope 2), kept as fp16 pairs.
 // kLloyd: the Lloyd payload, decoded as in spectral_dequant_kernel<true>.
+// kVFull: full-C values; each head's P.V runs over every slice's codes (read
+// from the value pages after the main loop: staged in LDS they would not fit
+// beside the key pages) with the weights signed by H_{C/128}[h][slice].
 constexpr int kSpBlk = 128;
 constexpr int kSpBlkMaxPages = 56 * 1024;   // two key pages staged in LDS at most
 
-template <bool kLloyd>
+template <bool kLloyd, bool kVFull>
 __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequantKArgs a, int kpb) {
   const int blk = blockIdx.x, hq = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
@@ -852,8 +1012,8 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
   __shared__ __align__(16) _Float16 s_b[4][kSpBlk][kSpBRow];
   __shared__ __align__(16) uint32_t s_cs[kSpBlk][kCsPad];   // (cos, sin) fp16 of (position, frequency)
   __shared__ uint2 s_cbl[256];
-  __shared__ uint2 s_vcd[4][8][64];   // (local head, value page, lane)
-  __shared__ uint2 s_nrm[4][8][4];    // (local head, value page, quarter)
+  __shared__ uint2 s_vcd[kVFull ? 1 : 4][8][64];   // (local head, value page, lane)
+  __shared__ uint2 s_nrm[kVFull ? 1 : 4][8][4];    // (local head, value page, quarter)
   __shared__ float s_lq[kLloyd ? kLqLevels : 1];   // the key payload's Lloyd levels
   __shared__ uint32_t s_lqp[kLloyd ? kLqPairs : 1];   // and their fp16 pair tables
   extern __shared__ __align__(16) uint8_t sp_dyn[];   // the two key pages; after the loop, the score exchange
@@ -886,12 +1046,20 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
   // value pages: thread (local head tid >> 7, page (tid >> 6) & 1 + 2 k, lane)
   uint2 vcw[4], nrw[4];
   const int vh = min(4 * hq + (tid >> 7), a.h_kv - 1), vl = tid & 63;
+  if constexpr (kVFull) {
+    {   // norms: thread tid < 32 takes page tid >> 2, tokens 4 (tid & 3) ..
+      const int vp_i = (tid >> 2) & 7;
+      const uint8_t* vp = a.v_pages + clamp_page(a.v_table[8 * blk + vp_i], a.n_v_pool) * (int64_t)a.VL.bytes;
+      nrw[0] = *reinterpret_cast<const uint2*>(vp + a.VL.vnorm + 4 * (tid & 3) * 2);
+    }
+  } else {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int vp_i = ((tid >> 6) & 1) + 2 * k;
-    const uint8_t* vp = a.v_pages + clamp_page(a.v_table[8 * blk + vp_i], a.n_v_pool) * (int64_t)a.VL.bytes;
-    vcw[k] = *reinterpret_cast<const uint2*>(vp + a.VL.vcode + vh * 512 + vl * 8);
-    nrw[k] = *reinterpret_cast<const uint2*>(vp + a.VL.vnorm + (vh * kPT + 4 * (vl >> 4)) * 2);
+    for (int k = 0; k < 4; ++k) {
+      const int vp_i = ((tid >> 6) & 1) + 2 * k;
+      const uint8_t* vp = a.v_pages + clamp_page(a.v_table[8 * blk + vp_i], a.n_v_pool) * (int64_t)a.VL.bytes;
+      vcw[k] = *reinterpret_cast<const uint2*>(vp + a.VL.vcode + vh * 512 + vl * 8);
+      nrw[k] = *reinterpret_cast<const uint2*>(vp + a.VL.vnorm + (vh * kPT + 4 * (vl >> 4)) * 2);
+    }
   }
   // dec rows of this wave's 4 row tiles: rt(i) = 2 r2 + (i & 1) + 4 (i >> 1)
   const uint16_t* decb = a.dec + (int64_t)hh * kD * a.c_pad32 + n * 32 + 8 * q;
@@ -948,11 +1116,15 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
       reinterpret_cast<u32x4_t*>(kp0)[tid + 512 * i] = kw0[i];
       reinterpret_cast<u32x4_t*>(kp1)[tid + 512 * i] = kw1[i];
     }
+  if constexpr (kVFull) {
+    if (tid < 32) s_nrm[0][tid >> 2][tid & 3] = nrw[0];
+  } else {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int vp_i = ((tid >> 6) & 1) + 2 * k;
-    s_vcd[tid >> 7][vp_i][vl] = vcw[k];
-    if ((vl & 15) == 0) s_nrm[tid >> 7][vp_i][vl >> 4] = nrw[k];
+    for (int k = 0; k < 4; ++k) {
+      const int vp_i = ((tid >> 6) & 1) + 2 * k;
+      s_vcd[tid >> 7][vp_i][vl] = vcw[k];
+      if ((vl & 15) == 0) s_nrm[tid >> 7][vp_i][vl >> 4] = nrw[k];
+    }
   }
   const int n_steps = a.c_pad32 / 32;
   // a barrier: s_tab, s_cbl, s_cs, s_lq, the key pages, the value codes
@@ -1216,18 +1388,39 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
   for (int c = 0; c < 4; ++c) pv[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int tt = 0; tt < 8; ++tt) {
-    const uint2 nr = s_nrm[hl][tt][q];
-    const uint32_t vc = r2 == 0 ? s_vcd[hl][tt][lane].x : s_vcd[hl][tt][lane].y;
+    const uint2 nr = s_nrm[kVFull ? 0 : hl][tt][q];
     const float nv[4] = {half_bits_to_float(nr.x & 0xffffu), half_bits_to_float(nr.x >> 16),
                          half_bits_to_float(nr.y & 0xffffu), half_bits_to_float(nr.y >> 16)};
     half4_t aw;
 #pragma unroll
     for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[tt][i] * nv[i]);
+    if constexpr (kVFull) {
+      // this wave's half (r2) of every slice's code pair of value page tt
+      const uint8_t* vp = a.v_pages + clamp_page(a.v_table[8 * blk + tt], a.n_v_pool) * (int64_t)a.VL.bytes;
+      uint32_t vcs[8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
-      const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
-      pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[c], 0, 0, 0);
+      for (int sl = 0; sl < 8; ++sl)
+        vcs[sl] = *reinterpret_cast<const uint32_t*>(vp + a.VL.vcode + min(sl, a.h_kv - 1) * 512 + lane * 8 + 4 * r2);
+#pragma unroll
+      for (int sl = 0; sl < 8; ++sl) {
+        if (sl >= a.h_kv) break;
+        const half4_t as = vfull_neg(hh, sl) ? -aw : aw;
+        const uint32_t vc = vcs[sl];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
+          const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
+          pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(as, vb, pv[c], 0, 0, 0);
+        }
+      }
+    } else {
+      const uint32_t vc = r2 == 0 ? s_vcd[hl][tt][lane].x : s_vcd[hl][tt][lane].y;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
+        const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
+        pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[c], 0, 0, 0);
+      }
     }
   }
   // H8 over the block index ct = 4 r2 + c: c in registers, r2 (the
@@ -1284,7 +1477,8 @@ struct SpMergeKArgs {
   const uint16_t* v_win;
   float sm_scale;
   void* out;
-  uint32_t v_sign_bits[4];
+  uint32_t sign_h[8][4];   // the value codec's signs of head h's 128 channels
+  float v_scale;           // 1/128 (per-head codec) or 1/C (full-C codec)
 };
 
 constexpr int kSpMergeMaxGroups = 16384;   // 1M committed tokens
@@ -1452,19 +1646,25 @@ __global__ __launch_bounds__(256) void spectral_merge_kernel(const SpMergeKArgs 
     const int cc = tid & 15, q4 = cc >> 2, e = cc & 3;
     float x = (s_sum[0][q4][e] + s_sum[1][q4][e]) + (s_sum[2][q4][e] + s_sum[3][q4][e]);
     const float w = (s_sumw[0][q4][e] + s_sumw[1][q4][e]) + (s_sumw[2][q4][e] + s_sumw[3][q4][e]);
-    x = h16_lanes(x, cc);   // the Hadamard's bits 0..3, then the codec's signs and 1/128
+    x = h16_lanes(x, cc);   // the Hadamard's bits 0..3, then the codec's signs and scale
     const int c = 16 * chunk + cc;
-    if (tid < 16) store_elem(a.out, row * kD + c, ((sign_neg(a.v_sign_bits, c) ? -x : x) * (1.0f / kD) + w) / Ls,
+    if (tid < 16) store_elem(a.out, row * kD + c, ((sign_neg(a.sign_h[h], c) ? -x : x) * a.v_scale + w) / Ls,
                              a.out_dtype);
   }
 }
 
-static PageLayout value_layout(int h_kv) {
+// Value-only pages: VNORM (h_kv x 16 fp16, or 16 for the full-C codec), then VCODE
+static PageLayout value_layout(int h_kv, bool full = false) {
   PageLayout L{};
   L.vnorm = 0;
-  L.vcode = h_kv * kPT * 2;
+  L.vcode = (full ? 1 : h_kv) * kPT * 2;
   L.bytes = L.vcode + h_kv * 64 * 8;
   return L;
+}
+
+static bool v_codec_ok(int v_codec, int h_kv) {
+  return v_codec == BMX_SPECTRAL_V_PERHEAD ||
+         (v_codec == BMX_SPECTRAL_V_FULL && (h_kv == 1 || h_kv == 2 || h_kv == 4 || h_kv == 8));
 }
 
 static int sp_fail(const char* fn, const std::string& msg) {
@@ -1502,12 +1702,27 @@ static bool sp_block_shape(const bmx_spectral_dequant_args* a) {
 
 static bool sp_blocked(const bmx_spectral_dequant_args* a) { return a->partials && sp_block_shape(a); }
 
+constexpr size_t kLdsBytes = 160 * 1024;   // per workgroup on gfx950
+
+// A launch whose static and dynamic LDS exceed the CU's is not a valid
+// allocation: refuse it on the host instead.
+static bool sp_lds_fits(const void* kernel, size_t dyn) {
+  hipFuncAttributes attr{};
+  if (hipFuncGetAttributes(&attr, kernel) != hipSuccess) return false;
+  return attr.sharedSizeBytes + dyn <= kLdsBytes;
+}
+
 }  // namespace bmx
 
 using namespace bmx;
 
 extern "C" int64_t bmx_spectral_v_page_bytes(int32_t h_kv) {
   return (h_kv < 1 || h_kv > 8) ? -1 : (int64_t)value_layout(h_kv).bytes;
+}
+
+extern "C" int64_t bmx_spectral_v_page_bytes_codec(int32_t h_kv, int32_t v_codec) {
+  if (h_kv < 1 || h_kv > 8 || !v_codec_ok(v_codec, h_kv)) return -1;
+  return (int64_t)value_layout(h_kv, v_codec == BMX_SPECTRAL_V_FULL).bytes;
 }
 
 extern "C" int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* stream) {
@@ -1521,6 +1736,8 @@ extern "C" int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* 
   if (!a->k_pre || !a->v || !a->enc_perm || !a->k_pages || !a->k_page_ids || !a->v_pages || !a->v_page_ids ||
       a->n_k_pool < 1 || a->n_v_pool < 1)
     return sp_fail(fn, "null pointer argument or empty pool");
+  if (!v_codec_ok(a->v_codec, a->L.h_kv))
+    return sp_fail(fn, "v_codec must be BMX_SPECTRAL_V_PERHEAD, or BMX_SPECTRAL_V_FULL with h_kv 1, 2, 4 or 8");
   hipStream_t st = (hipStream_t)stream;
   SpEncodeKArgs k{};
   k.C = kD * a->L.h_kv; k.c_pad = a->L.c_pad; k.n_pool = a->n_k_pool; k.k_dtype = a->k_dtype;
@@ -1533,7 +1750,16 @@ extern "C" int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* 
   else
     hipLaunchKernelGGL(spectral_encode_kernel<false>, dim3((a->L.c_pad + 63) / 64, a->n_groups), dim3(512), 0, st, k);
   hipError_t e = hipGetLastError();
-  if (e == hipSuccess) {
+  if (e == hipSuccess && a->v_codec == BMX_SPECTRAL_V_FULL) {
+    SpVFullKArgs v{};
+    v.h_kv = a->L.h_kv; v.n_pool = a->n_v_pool; v.v_dtype = a->v_dtype;
+    v.v = a->v; v.vsh = a->v_sh; v.vst = a->v_st;
+    v.pages = a->v_pages; v.page_ids = a->v_page_ids; v.L = value_layout(a->L.h_kv, true);
+    for (int i = 0; i < 4; ++i) v.codebook[i] = a->v_codebook[i];
+    for (int i = 0; i < 32; ++i) v.sign_c[i] = a->v_sign_bits_c[i];
+    hipLaunchKernelGGL(spectral_vfull_kernel, dim3(4 * a->n_groups), dim3(256), 0, st, v);
+    e = hipGetLastError();
+  } else if (e == hipSuccess) {
     AppendKArgs v{};
     v.h_kv = a->L.h_kv; v.n_pool = a->n_v_pool;
     v.v = a->v; v.vsh = a->v_sh; v.vst = a->v_st; v.v_dtype = a->v_dtype;
@@ -1566,13 +1792,18 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
                !a->apply_rope))
     return sp_fail(fn, "the decode form needs scores or partials, n_q_groups 1..16, a q_dtype and apply_rope");
   if (a->partials && !a->q) return sp_fail(fn, "the partial form needs q");
+  if (!v_codec_ok(a->v_codec, a->L.h_kv))
+    return sp_fail(fn, "v_codec must be BMX_SPECTRAL_V_PERHEAD, or BMX_SPECTRAL_V_FULL with h_kv 1, 2, 4 or 8");
   SpDequantKArgs k{};
   k.h_kv = a->L.h_kv; k.c_pad = a->L.c_pad; k.c_pad32 = (a->L.c_pad + 31) / 32 * 32;
   k.n_tokens = a->n_tokens; k.out_rows = a->out_rows ? a->out_rows : a->n_tokens;
   k.apply_rope = a->apply_rope; k.n_k_pool = a->n_k_pool; k.n_v_pool = a->n_v_pool;
   k.out_dtype = a->out_dtype; k.k_page_bytes = a->L.k_page_bytes;
   k.k_pages = a->k_pages; k.k_table = a->k_page_table; k.v_pages = a->v_pages; k.v_table = a->v_page_table;
-  k.slice_tab = a->L.slice_tab; k.dec = a->dec_perm; k.VL = value_layout(a->L.h_kv);
+  k.slice_tab = a->L.slice_tab; k.dec = a->dec_perm;
+  k.v_full = a->v_codec == BMX_SPECTRAL_V_FULL;
+  k.VL = value_layout(a->L.h_kv, k.v_full);
+  for (int i = 0; i < 32; ++i) k.v_sign_c[i] = a->v_sign_bits_c[i];
   k.rope_scaling = a->rope_scaling;
   for (int j = 0; j < 64; ++j) k.inv_freq[j] = a->inv_freq[j];
   for (int i = 0; i < 4; ++i) { k.codebook[i] = a->v_codebook[i]; k.v_sign_bits[i] = a->v_sign_bits[i]; }
@@ -1582,12 +1813,24 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   if (sp_blocked(a)) {
     const int kpb = a->L.k_page_bytes;
     const size_t dyn = std::max<size_t>(2 * (size_t)kpb, (size_t)8 * 4 * 64 * 16);   // pages, then the exchange
-    if (k.lq)
-      hipLaunchKernelGGL(spectral_partial128_kernel<true>, dim3(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4),
-                         dim3(512), dyn, (hipStream_t)stream, k, kpb);
+    const dim3 grid(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4);
+    const void* kern = k.lq ? (k.v_full ? (const void*)spectral_partial128_kernel<true, true>
+                                        : (const void*)spectral_partial128_kernel<true, false>)
+                            : (k.v_full ? (const void*)spectral_partial128_kernel<false, true>
+                                        : (const void*)spectral_partial128_kernel<false, false>);
+    if (!sp_lds_fits(kern, dyn)) return sp_fail(fn, "the 128-token kernel's LDS does not fit this key page size");
+    if (k.lq && k.v_full)
+      hipLaunchKernelGGL((spectral_partial128_kernel<true, true>), grid, dim3(512), dyn, (hipStream_t)stream, k, kpb);
+    else if (k.lq)
+      hipLaunchKernelGGL((spectral_partial128_kernel<true, false>), grid, dim3(512), dyn, (hipStream_t)stream, k, kpb);
+    else if (k.v_full)
+      hipLaunchKernelGGL((spectral_partial128_kernel<false, true>), grid, dim3(512), dyn, (hipStream_t)stream, k, kpb);
     else
-      hipLaunchKernelGGL(spectral_partial128_kernel<false>, dim3(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4),
-                         dim3(512), dyn, (hipStream_t)stream, k, kpb);
+      hipLaunchKernelGGL((spectral_partial128_kernel<false, false>), grid, dim3(512), dyn, (hipStream_t)stream, k,
+                         kpb);
+  } else if (!sp_lds_fits(k.lq ? (const void*)spectral_dequant_kernel<true> : (const void*)spectral_dequant_kernel<false>,
+                          sp_dyn_bytes(a->L.k_page_bytes))) {
+    return sp_fail(fn, "the 64-token kernel's LDS does not fit this key page size");
   } else if (k.lq) {
     hipLaunchKernelGGL(spectral_dequant_kernel<true>, dim3(a->n_tokens / kGroup), dim3(512),
                        sp_dyn_bytes(a->L.k_page_bytes), (hipStream_t)stream, k);
@@ -1622,12 +1865,17 @@ extern "C" int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* st
   if (a->win_len && (((uintptr_t)a->k_win & 15) != 0 || a->win_stride_h % 8 != 0 ||
                      (a->win_stride_h != 0 && a->win_stride_h < (int64_t)a->win_len * kD)))
     return sp_fail(fn, "k_win must be 16-byte aligned and win_stride_h 0 or a multiple of 8 >= 128 win_len");
+  if (!v_codec_ok(a->v_codec, a->h_kv))
+    return sp_fail(fn, "v_codec must be BMX_SPECTRAL_V_PERHEAD, or BMX_SPECTRAL_V_FULL with h_kv 1, 2, 4 or 8");
   SpMergeKArgs k{};
   k.h_kv = a->h_kv; k.G = a->n_q_groups; k.n_groups = a->n_groups; k.q_dtype = a->q_dtype;
   k.win_len = a->win_len; k.out_dtype = a->out_dtype; k.partials = a->partials; k.q = a->q;
   k.k_win = a->k_win; k.v_win = a->v_win; k.sm_scale = a->sm_scale; k.out = a->out;
   k.win_sh = a->win_stride_h ? a->win_stride_h : (int64_t)a->win_len * kD;
-  for (int i = 0; i < 4; ++i) k.v_sign_bits[i] = a->v_sign_bits[i];
+  const bool full = a->v_codec == BMX_SPECTRAL_V_FULL;
+  for (int h = 0; h < 8; ++h)
+    for (int i = 0; i < 4; ++i) k.sign_h[h][i] = full ? a->v_sign_bits_c[4 * h + i] : a->v_sign_bits[i];
+  k.v_scale = 1.0f / (float)(full ? kD * a->h_kv : kD);
   hipLaunchKernelGGL(spectral_merge_kernel, dim3(kD / 16, a->n_q_groups, a->h_kv), dim3(256), 0, (hipStream_t)stream,
                      k);
   const hipError_t e = hipGetLastError();

@@ -12,15 +12,14 @@ pairs the reference's attend() sends to a fused kernel
   32, 64 or 128; the keys may also be ``rtn_channel`` (token groups of 32,
   64 or 128 per channel: config 1 and the ``kivi`` recipe, which the
   reference runs on its chunked path only);
-* spectral (K4): K ``spectral`` pre-RoPE from a pack file (rtn payload,
-  fp32 decoder, 64-token groups), V ``turboquant_mse_perhead`` 2-bit, the
-  value codec of the other pre-RoPE pair, under the recipe name
-  ``k4ph_b<budget>``, with the reference's suffixes ``_lq`` (the Lloyd
-  payload) and ``_dec8``, ``_dec8t<T>``, ``_dec8tl`` (an int8 roundtrip of
-  the decoder when the packs load).  The reference's own ``k4_b<budget>`` recipe pairs the
-  spectral keys with the full-C ``turboquant_mse`` values (one 1024-point
-  rotation and one norm per token, recipes.py:138-143), which no MI355X
-  kernel reads: that name raises rather than answer with another codec.
+* spectral (K4): K ``spectral`` pre-RoPE from a pack file (64-token
+  groups) under the reference's recipe ``k4_b<budget>``, with its full-C
+  ``turboquant_mse`` 2-bit values (one C-point rotation and one norm per
+  token, recipes.py:138-143; C = 128 h_kv a power of two), and under
+  ``k4ph_b<budget>`` with the per-head value codec of the other pre-RoPE
+  pair; both with the reference's suffixes ``_lq`` (the Lloyd payload) and
+  ``_dec8``, ``_dec8t<T>``, ``_dec8tl`` (an int8 roundtrip of the decoder
+  when the packs load).
 
 Every other pair raises, naming what it got: there is no CPU or slow path to
 route it to.
@@ -51,19 +50,17 @@ class CacheCodecSpec:
 
 def spec_pair(arm: str, *, rank: int = 16, group: int = 64, seed: int = 0, pack_path: str | None = None):
     """(k_spec, v_spec) for a named recipe (cache/recipes.py:13-42, 88-143, 173-177)."""
-    if arm.startswith("k4_b"):
-        # the reference's k4 recipe: spectral keys with full-C turboquant_mse values
-        raise NotImplementedError(
-            f"recipe {arm!r} pairs spectral keys with full-C turboquant_mse values (one 1024-point "
-            f"rotation per token), which have no MI355X kernels; 'k4ph_b<budget>' pairs the same keys "
-            f"with the per-head value codec (turboquant_mse_perhead)")
-    if arm.startswith("k4ph_b"):
+    if arm.startswith("k4_b") or arm.startswith("k4ph_b"):
+        # k4_b: the reference's recipe, full-C turboquant_mse values (recipes.py:
+        # 138-143); k4ph_b: the same keys with the per-head value codec
         if not pack_path:
             raise ValueError("k4 arms require --pack-path (a fitted spectral pack file)")
-        budget, payload_quant, dec_quant = _k4_variant(arm, "k4ph_b")
+        prefix = "k4_b" if arm.startswith("k4_b") else "k4ph_b"
+        budget, payload_quant, dec_quant = _k4_variant(arm, prefix)
         return (CacheCodecSpec(arm="spectral", pre_rope=True, group=group, pack_path=pack_path,
                                budget=budget, seed=seed, dec_quant=dec_quant, payload_quant=payload_quant),
-                CacheCodecSpec(arm="turboquant_mse_perhead", bits=2, seed=seed))
+                CacheCodecSpec(arm="turboquant_mse" if prefix == "k4_b" else "turboquant_mse_perhead", bits=2,
+                               seed=seed))
     if arm == "kivi":
         return (CacheCodecSpec(arm="rtn_channel", bits=2, group=group, seed=seed),
                 CacheCodecSpec(arm="rtn_token", bits=2, group=group, seed=seed))
@@ -142,6 +139,7 @@ def check_spectral(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
         raise NotImplementedError(
             f"spectral payload_quant={k_spec.payload_quant!r}: the MI355X kernels implement the rtn and lloyd "
             f"payloads")
-    if not (v_spec.arm == "turboquant_mse_perhead" and v_spec.bits == 2):
+    if not (v_spec.arm in ("turboquant_mse_perhead", "turboquant_mse") and v_spec.bits == 2):
         raise NotImplementedError(
-            f"spectral K pairs with V=turboquant_mse_perhead (2 bits) on the MI355X path; got V={v_spec}")
+            f"spectral K pairs with V=turboquant_mse (full C) or turboquant_mse_perhead, 2 bits, on the MI355X "
+            f"path; got V={v_spec}")

@@ -3,8 +3,9 @@
 A corpus-fitted pack per layer (cache/spectral.py:175-215, ``SpectralPack``:
 enc, dec (C x C fp32), lam, bits per direction on the tier grid, group 64)
 codes the pre-RoPE keys; the values use the k2b value codec in value-only
-pages.  ``DevicePack`` holds what the kernels read: the page layout of the
-pack's bits, enc's columns and dec's rows in page order.  ``append`` writes
+pages (the per-head codec, or the full-C turboquant_mse of the reference's
+k4 recipe).  ``DevicePack`` holds what the kernels read: the page layout of
+the pack's bits, enc's columns and dec's rows in page order.  ``append`` writes
 64-token groups; ``dequant`` reads them back dense (the reference's spectral
 read path: chunked_attention.py:106-116, then RoPE).
 
@@ -223,6 +224,31 @@ def save_packs(path, layers: dict, budgets, *, tiers=TIERS, group: int = GROUP) 
                                                      "budgets": list(budgets)}))
 
 
+V_CODECS = {"perhead": 0, "full": 1}   # BMX_SPECTRAL_V_PERHEAD, BMX_SPECTRAL_V_FULL
+
+
+def v_page_bytes(h_kv: int, v_codec: str = "perhead") -> int:
+    """Bytes of a 16-token value page of the value codec: "perhead"
+    (turboquant_mse_perhead) or "full" (the full-C turboquant_mse)."""
+    n = int(_lib.lib().bmx_spectral_v_page_bytes_codec(h_kv, V_CODECS[v_codec]))
+    _need(n > 0, f"no {v_codec} value pages for h_kv {h_kv}")
+    return n
+
+
+def v_sign_bits_c(h_kv: int, seed: int) -> tuple:
+    """The full-C codec's Hadamard signs of the C = 128 h_kv channels as 32
+    uint32 words (_hadamard_signs(C, seed), codecs.py:114-124)."""
+    from .codecs import hadamard_signs, sign_bits
+
+    w = sign_bits(hadamard_signs(HEAD_DIM * h_kv, seed))
+    return tuple(w + [0] * (32 - len(w)))
+
+
+def _set_v_codec(a, dp) -> None:
+    a.v_codec = dp.v_codec
+    a.v_sign_bits_c[:] = dp.v_sign_c
+
+
 LLOYD_TIERS = (2, 3, 4, 5, 6, 8)
 
 
@@ -247,9 +273,16 @@ class DevicePack:
     tier b has a w-bit container, w = 2 / 4 / 8 (tiers 2 / 3-4 / 5-8), 64 w
     bytes per page at off[s] after the fp16 scales."""
 
-    def __init__(self, pack: SpectralPack, h_kv: int, device, payload: str = "rtn"):
+    def __init__(self, pack: SpectralPack, h_kv: int, device, payload: str = "rtn", v_codec: str = "perhead",
+                 v_seed: int = 0):
         if payload not in ("rtn", "lloyd"):
             raise ValueError(f"payload must be 'rtn' or 'lloyd'; got {payload!r}")
+        if v_codec not in V_CODECS:
+            raise ValueError(f"v_codec must be 'perhead' or 'full'; got {v_codec!r}")
+        if v_codec == "full" and h_kv not in (1, 2, 4, 8):
+            # the reference rotates a non-power-of-two C with a seeded random
+            # orthogonal matrix (codecs.py:104-111), which no kernel here reads
+            raise NotImplementedError(f"full-C turboquant_mse values need C = 128 h_kv a power of two; h_kv {h_kv}")
         if pack.group != GROUP:
             raise NotImplementedError(f"pack group {pack.group}: the spectral kernels take 64-token groups")
         bits = pack.bits.to(torch.int64).cpu()
@@ -276,7 +309,9 @@ class DevicePack:
             off.append(o)
             o += GROUP * w
         self.k_page_bytes = o + 16
-        self.v_page_bytes = int(_lib.lib().bmx_spectral_v_page_bytes(h_kv))
+        self.v_codec = V_CODECS[v_codec]
+        self.v_page_bytes = v_page_bytes(h_kv, v_codec)
+        self.v_sign_c = v_sign_bits_c(h_kv, v_seed) if v_codec == "full" else (0,) * 32
         self.perm = torch.tensor(perm, dtype=torch.int64)
         self.slice_bits = slice_bits
         tab = [x | (b << 24) for x, b in zip(off, slice_bits)]
@@ -324,6 +359,7 @@ def append(k_pre: torch.Tensor, v: torch.Tensor, dp: DevicePack, k_pages: torch.
     a.v_pages, a.v_page_ids, a.n_v_pool = _ptr(v_pages), _ptr(v_ids), v_pages.shape[0]
     a.v_codebook[:] = consts.codebook
     a.v_sign_bits[:] = consts.sign_bits
+    _set_v_codec(a, dp)
     _lib.check(_lib.lib().bmx_spectral_append(ct.byref(a), _stream(dev)), "bmx_spectral_append")
 
 
@@ -347,6 +383,7 @@ def _partial_args(dp: DevicePack, k_pages, k_table, v_pages, v_table, n_tokens: 
     a.out_dtype = _V_DTYPES[torch.float16]
     a.q, a.q_dtype, a.n_q_groups = _ptr(q), _V_DTYPES[q.dtype], q.shape[1]
     a.sm_scale = float(sm_scale)
+    _set_v_codec(a, dp)
     return a
 
 
@@ -358,6 +395,7 @@ def partial_count(dp: DevicePack, n_tokens: int, q: torch.Tensor, apply_rope: in
     a = _lib.SpectralDequantArgs()
     a.L = dp.layout()
     a.n_tokens, a.q, a.apply_rope = int(n_tokens), _ptr(q), int(apply_rope)
+    _set_v_codec(a, dp)
     n = _lib.lib().bmx_spectral_partial_count(ct.byref(a))
     _need(n >= 0, "n_tokens must be a non-negative multiple of 64")
     return n
@@ -430,6 +468,7 @@ def dequant(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tensor, v_page
     a.out_dtype = _V_DTYPES[dtype]
     a.k_out, a.v_out = _ptr(k), _ptr(v)
     a.out_rows = v.shape[1]
+    _set_v_codec(a, dp)
     if q is not None:
         a.q, a.q_dtype, a.n_q_groups, a.scores = _ptr(q), _V_DTYPES[q.dtype], q.shape[1], _ptr(scores)
     _lib.check(_lib.lib().bmx_spectral_dequant(ct.byref(a), _stream(dev)), "bmx_spectral_dequant")
@@ -474,5 +513,7 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
     a.win_stride_h = k_win.stride(0) if T else 0
     a.sm_scale, a.out, a.out_dtype = float(sm_scale), _ptr(out), _V_DTYPES[out_dtype]
     a.v_sign_bits[:] = consts.sign_bits
+    if dp is not None:
+        _set_v_codec(a, dp)
     _lib.check(_lib.lib().bmx_spectral_merge(ct.byref(a), _stream(q.device)), "bmx_spectral_merge")
     return out

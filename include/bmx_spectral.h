@@ -10,10 +10,20 @@
  * the write call in cache/packed_streaming.py:491-511 and the read in
  * cache/chunked_attention.py:106-116 (_dequant_block, arm "spectral"), whose
  * decode is the reference's chunked path (packed_streaming.py:1016-1032).
- * Values: the k2b value codec (2-bit Lloyd codes of the Hadamard-rotated
- * values and an fp16 norm per head and token, include/bmx_k2b.h) in value-only
+ * Values, v_codec BMX_SPECTRAL_V_PERHEAD: the k2b value codec (2-bit Lloyd
+ * codes of the Hadamard-rotated values and an fp16 norm per head and token,
+ * include/bmx_k2b.h, the reference's turboquant_mse_perhead) in value-only
  * pages of 16 tokens: VNORM [h_kv][16] fp16 at byte 0, VCODE [h_kv][64][2] u32
  * at byte 32 h_kv, bmx_spectral_v_page_bytes(h_kv) bytes per page.
+ * v_codec BMX_SPECTRAL_V_FULL: the reference's full-C turboquant_mse
+ * (codecs.py:616-675 at h = 1: one fp16 norm per token over all C channels,
+ * one C-point randomized Hadamard, 2-bit codes of the C rotated channels;
+ * C = 128 h_kv must be a power of two, h_kv 1, 2, 4 or 8): VNORM [16] fp16
+ * at byte 0, VCODE [C / 128][64][2] u32 at byte 32, slice s holding rotated
+ * channels 128 s .. 128 s + 127 in the per-head layout;
+ * bmx_spectral_v_page_bytes_codec(h_kv, v_codec) bytes per page.  The norm
+ * sums the squares in 8 strided fp32 FMA accumulators, then those left to
+ * right (torch's CPU order for these rows).
  *
  * Key page: one per 64-token group.  Columns are the pack's coded directions
  * in tier order (tier ascending, direction ascending), each tier padded with
@@ -54,6 +64,8 @@ extern "C" {
 
 #define BMX_SPECTRAL_MAX_CPAD 1072   /* 1024 directions + padding of 6 tiers */
 #define BMX_SPECTRAL_LLOYD_LEVELS 380 /* levels of tiers 2, 3, 4, 5, 6, 8 back to back */
+#define BMX_SPECTRAL_V_PERHEAD 0      /* values: turboquant_mse_perhead (one Hadamard per head) */
+#define BMX_SPECTRAL_V_FULL 1         /* values: turboquant_mse (one Hadamard over all C channels) */
 
 typedef struct bmx_spectral_layout {
   int32_t h_kv;                /* key heads, 1..8; C = 128 h_kv */
@@ -87,6 +99,8 @@ typedef struct bmx_spectral_append_args {
   int32_t n_v_pool;
   float v_codebook[4];         /* 2-bit Lloyd levels (gaussian_codebook(2)) */
   uint32_t v_sign_bits[4];     /* Hadamard signs of the 128 channels (1 = negative) */
+  int32_t v_codec;             /* BMX_SPECTRAL_V_PERHEAD or BMX_SPECTRAL_V_FULL */
+  uint32_t v_sign_bits_c[32];  /* V_FULL: signs of the C channels, bit c % 32 of word c / 32 */
 } bmx_spectral_append_args;
 
 /* Replaces _dequant_block(arm "spectral") + apply_rope for the keys and
@@ -145,6 +159,11 @@ typedef struct bmx_spectral_dequant_args {
    * NULL. */
   float* partials;
   float sm_scale;
+  int32_t v_codec;             /* BMX_SPECTRAL_V_PERHEAD or BMX_SPECTRAL_V_FULL: with V_FULL the
+                                  partials' sums are over the tokens' C-wide codes combined by
+                                  H_{C/128} (row h: sign (-1)^popcount(h & s) for slice s), so that
+                                  the merge's H16, signs and scale give head h's values */
+  uint32_t v_sign_bits_c[32];  /* V_FULL: signs of the C channels */
 } bmx_spectral_dequant_args;
 
 /* The decode step's merge: the groups' softmax partials (the partial form
@@ -168,9 +187,15 @@ typedef struct bmx_spectral_merge_args {
   int32_t out_dtype;
   uint32_t v_sign_bits[4];     /* the value codec's signs, applied to the partials' sums */
   int64_t win_stride_h;        /* elements between heads in k_win / v_win (0: 128 win_len) */
+  int32_t v_codec;             /* BMX_SPECTRAL_V_PERHEAD (signs v_sign_bits, scale 1/128) or
+                                  BMX_SPECTRAL_V_FULL (head h: signs 128 h .. of v_sign_bits_c,
+                                  scale 1/C) */
+  uint32_t v_sign_bits_c[32];
 } bmx_spectral_merge_args;
 
 int64_t bmx_spectral_v_page_bytes(int32_t h_kv);
+/* Value page bytes of either value codec, or -1 (V_FULL needs h_kv 1, 2, 4 or 8). */
+int64_t bmx_spectral_v_page_bytes_codec(int32_t h_kv, int32_t v_codec);
 int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* stream);
 int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* stream);
 int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void* stream);

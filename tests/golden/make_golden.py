@@ -43,8 +43,12 @@ Functions covered (reference file:line, paths under ``src/bmx``):
                                  cache/spectral.py:648-700, 763-841, 913-1027,
                                  1176-1210
 
+  * full-C turboquant_mse values (quantize_packed / dequant_packed, arm
+    "turboquant_mse")          cache/codecs.py:616-675, 729-735, 815-818
+
 ``python tests/golden/make_golden.py SRC spectral`` rewrites only the named
-fixture files (codecs, attention, e2e_tiny_llama, spectral, spectral_variants).
+fixture files (codecs, attention, e2e_tiny_llama, spectral, spectral_variants,
+tq_full).
 """
 
 from __future__ import annotations
@@ -383,9 +387,33 @@ def spectral_variant_fixtures():
     return out
 
 
+def tq_full_fixtures():
+    """The full-C turboquant_mse value codec (the k4 recipe's values): one
+    Hadamard over all C = 128 h_kv channels and one norm per token, at
+    h_kv 2 and 8, on fp16 values as the cache passes them; indices, norms,
+    the dequantized values and the C-wide signs."""
+    from bmx.cache import codecs
+    from bmx.cache.collect import to_matrix
+
+    out = {}
+    g = torch.Generator().manual_seed(31)
+    for h_kv in (2, 8):
+        C = 128 * h_kv
+        v = (torch.randn(h_kv, 96, 128, generator=g) * 1.5).half()
+        M = to_matrix(v.float())
+        packed, bpe = codecs.quantize_packed("turboquant_mse", M, bits=2, seed=0)
+        out[f"h{h_kv}_v"] = v.numpy()
+        out[f"h{h_kv}_idx"] = packed["indices"].numpy()
+        out[f"h{h_kv}_norms"] = packed["norms"].numpy()
+        out[f"h{h_kv}_bpe"] = np.float64(bpe)
+        out[f"h{h_kv}_deq"] = codecs.dequant_packed("turboquant_mse", packed, seed=0).numpy()
+        out[f"signs_d{C}_s0"] = codecs._hadamard_signs(C, 0).numpy().astype(np.int8)
+    return out
+
+
 FIXTURES = {"codecs": codec_fixtures, "attention": attention_fixtures,
             "e2e_tiny_llama": e2e_fixtures, "spectral": spectral_fixtures,
-            "spectral_variants": spectral_variant_fixtures}
+            "spectral_variants": spectral_variant_fixtures, "tq_full": tq_full_fixtures}
 
 
 def main():

@@ -26,8 +26,9 @@ class SpectralOracleStore:
     (fixed-order encode, MSE-refined RTN, fp16 steps as stored), keys
     dequantized pre-RoPE, values by the per-head value codec."""
 
-    def __init__(self, pack, h_kv, v_seed, v_fp16, payload="rtn"):
+    def __init__(self, pack, h_kv, v_seed, v_fp16, payload="rtn", v_full=False):
         self.pack, self.h_kv, self.v_seed, self.v_fp16 = pack, h_kv, v_seed, v_fp16
+        self.v_h = 1 if v_full else h_kv   # full-C turboquant_mse: the per-head codec at h = 1
         self.L = OS.Layout(pack.bits.numpy())
         self.lloyd = ({b: OC.gaussian_codebook(b).numpy() for b in set(self.L.slice_bits.tolist())}
                       if payload == "lloyd" else None)
@@ -39,9 +40,9 @@ class SpectralOracleStore:
         K = OS.dequant(codes, scales, self.pack.dec.numpy(), self.L, lloyd=self.lloyd)
         self.k.append(OC.from_matrix(torch.from_numpy(K).float(), self.h_kv))
         vp = v.half().float() if self.v_fp16 else v.float()
-        idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(vp.cpu()), bits=2, seed=self.v_seed, h=self.h_kv)
+        idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(vp.cpu()), bits=2, seed=self.v_seed, h=self.v_h)
         self.v.append(OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=self.v_seed,
-                                                          h=self.h_kv), self.h_kv))
+                                                          h=self.v_h), self.h_kv))
 
     def dense_k_pre(self):
         return torch.cat(self.k, dim=1)
@@ -57,7 +58,7 @@ class OracleLayer(product.PackedStreamingLayer):
         super().__init__(*args, **kwargs)
         if self._path == "spectral":
             self._oc = SpectralOracleStore(self._pack, self._h_kv, self.v_spec.seed, self.v_fp16,
-                                           self.k_spec.payload_quant)
+                                           self.k_spec.payload_quant, self.v_spec.arm == "turboquant_mse")
         else:
             self._oc = A.K2bOracleCache(self._h_kv, self._d_head, self._rank, v_seed=self.v_spec.seed)
 

@@ -133,7 +133,8 @@ def _spectral_pack_file(tmp_path, n_layers):
     return str(path)
 
 
-@pytest.mark.parametrize("arm", ["k4ph_b2.5", "k4ph_b3", "k4ph_b2.5_dec8t4", "k4ph_b2.5_lq_dec8tl"])
+@pytest.mark.parametrize("arm", ["k4ph_b2.5", "k4ph_b3", "k4ph_b2.5_dec8t4", "k4ph_b2.5_lq_dec8tl", "k4_b2.5",
+                                 "k4_b2.5_lq"])
 def test_spectral_cache_matches_oracle_backed_cache(tmp_path, arm):
     """The k4 recipe through the model: every commit through
     bmx_spectral_append, every step (decode and prefill) through
@@ -142,7 +143,9 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, arm):
     logits differ by the kernels' numerics only), teacher-forced.  The
     _dec8t4 arm decodes with the int8-roundtripped decoder and pays the
     int8 decoder charge in bits_per_entry; the _lq arm codes the Lloyd
-    payload (both caches: its level indices, read back through the levels)."""
+    payload (both caches: its level indices, read back through the levels);
+    k4_b is the reference's recipe, full-C turboquant_mse values (value bpe
+    2 + 16 / C)."""
     from bmx_amd import spectral
 
     g = np.load(GOLD / "e2e_tiny_llama.npz")
@@ -171,6 +174,8 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, arm):
     c_int8 = pack.c_int8(lay._pack.dec_tier) if "_dec8" in arm else 0
     charge = 8.0 * c_int8 / S + 16.0 * c_int8 / (S * 256) + 16.0 * (pack.c_used - c_int8) / S + 3.0 / S
     assert abs(prod.bits_per_entry()[0] - ((384 * bpe + (S - 384) * 16.0) / S + charge)) < 1e-9
+    bpe_v = 2 + 16.0 / 256 if arm.startswith("k4_b") else 2 + 16.0 * 2 / 256
+    assert abs(prod.bits_per_entry()[1] - (384 * bpe_v + (S - 384) * 16.0) / S) < 1e-9
     assert err.max().item() <= 2e-3 * max(scale, 1.0)
     assert agree == 1.0
 

@@ -39,11 +39,36 @@ def _lloyd(payload):
     return {b: z[f"codebook_{b}"] for b in (2, 3, 4, 5, 6, 8)}
 
 
-def _write(pack, h_kv, M, v, consts, shuffle_seed=None, payload="rtn"):
+def _values_full_of(vpages: np.ndarray, h_kv: int):
+    """(codes (16 n, C), fp16 norms (16 n,)) of n full-C value pages, in order
+    (the layout of include/bmx_spectral.h)."""
+    n, C = vpages.shape[0], 128 * h_kv
+    norms = vpages[:, :32].copy().view(np.float16).reshape(-1)
+    words = vpages[:, 32: 32 + 512 * h_kv].copy().view("<u4").reshape(n, h_kv, 64, 2)
+    codes = np.zeros((n, 16, C), np.int64)
+    for sl in range(h_kv):
+        for lane in range(64):
+            q, m = lane >> 4, lane & 15
+            for w in range(2):
+                dw = words[:, sl, lane, w].astype(np.int64)
+                for bb in range(4):
+                    for t in range(4):
+                        codes[:, 4 * q + t, 128 * sl + 16 * (4 * w + bb) + m] = (dw >> (8 * bb + 2 * t)) & 3
+    return codes.reshape(16 * n, C), norms
+
+
+def _values_oracle(v, h_kv, v_codec):
+    """The oracle's dequantized values (h_kv, S, 128) of either value codec."""
+    h = 1 if v_codec == "full" else h_kv
+    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v), bits=2, seed=0, h=h)
+    return OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=h), h_kv)
+
+
+def _write(pack, h_kv, M, v, consts, shuffle_seed=None, payload="rtn", v_codec="perhead"):
     """Append keys M (S, C) and values v (h_kv, S, 128) through the C-ABI into
     pools with (optionally shuffled) page ids; returns (dp, kp, vp, k_ids, v_ids)."""
     S = M.shape[0]
-    dp = spectral.DevicePack(pack, h_kv, DEV, payload)
+    dp = spectral.DevicePack(pack, h_kv, DEV, payload, v_codec)
     ng = S // 64
     k_ids = torch.arange(ng, dtype=torch.int32)
     v_ids = torch.arange(4 * ng, dtype=torch.int32)
@@ -297,3 +322,90 @@ def test_window_only_decode_step(G):
         err = (out.cpu().double() - ref.double()).abs().max().item()
         print(f"window only G {G} (pack {'given' if dp is not None else 'absent'}): max_abs {err:.3e}", flush=True)
         assert err <= 2e-3
+
+
+@pytest.mark.parametrize("h_kv", [1, 2, 4, 8])
+def test_full_c_values_pages_and_dequant(h_kv):
+    """The k4 recipe's full-C turboquant_mse values: every value page's codes
+    and fp16 norm equal the oracle's (the reference's codec at h = 1), on
+    shuffled pages; the dense values (the prefill form) within 1e-4 of the
+    oracle's, each head's channels from the Kronecker form of the C-point
+    inverse rotation; the keys as with the per-head values."""
+    pack = synthetic_pack(h_kv, 2.5, seed=21)
+    S = 256
+    M = synthetic_keys(pack, S, seed=22)
+    v = (torch.randn(h_kv, S, 128, generator=torch.Generator().manual_seed(23)) * 1.3).half().float()
+    consts = k2b.CodecConsts.make(v_seed=0)
+    print(f"full-C values h_kv {h_kv}", flush=True)
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=5, v_codec="full")
+    assert dp.v_page_bytes == 32 + 512 * h_kv
+    codes, n16 = _values_full_of(vp[v_ids.long()].cpu().numpy(), h_kv)
+    idx, norms, _ = OC.quantize_v_perhead(OC.to_matrix(v), bits=2, seed=0, h=1)
+    assert np.array_equal(n16.astype(np.float32), norms.numpy()[:, 0])
+    assert int((codes != idx.numpy()).sum()) == 0
+    V_or = _values_oracle(v, h_kv, "full")
+    Kp, Vd = spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts)
+    err = (Vd.cpu() - V_or).abs().max().item()
+    print(f"full-C values h_kv {h_kv}: dense values max_abs {err:.3e} (max {V_or.abs().max():.3f})", flush=True)
+    assert err < 1e-4
+    L = O.Layout(pack.bits.numpy())
+    codes_k, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes_k, scales, pack.dec.numpy(), L)), h_kv)
+    assert (Kp.cpu().double() - K_or).abs().max().item() <= 1.5e-3 * K_or.abs().max().item()
+
+
+FULL_CASES = [
+    # (h_kv, G, T, rope, S, payload)
+    (8, 4, 40, k2b.ROPE_FP16_TABLES, 1024, "rtn"), (8, 16, 7, k2b.ROPE_FP16_TABLES, 2048, "rtn"),
+    (8, 4, 40, k2b.ROPE_EXACT, 1024, "rtn"), (8, 16, 0, k2b.ROPE_EXACT, 512, "lloyd"),
+    (4, 8, 40, k2b.ROPE_FP16_TABLES, 512, "lloyd"), (2, 5, 3, k2b.ROPE_FP16_TABLES, 256, "rtn"),
+    (1, 8, 7, k2b.ROPE_FP16_TABLES, 256, "rtn"), (8, 1, 0, k2b.ROPE_FP16_TABLES, 1088, "rtn"),
+]
+
+
+@pytest.mark.parametrize("h_kv,G,T,rope,S,payload", FULL_CASES)
+def test_full_c_values_decode_matches_oracle(h_kv, G, T, rope, S, payload):
+    """The decode step with full-C values (both partial kernels: each head's
+    P.V over every slice with the weights signed by H_{C/128}, the merge's
+    H16, the head's C-wide signs and 1/C) against the oracle's one-softmax
+    attention over the same codes, and against the scores form + softmax."""
+    pack = synthetic_pack(h_kv, 2.5, seed=24)
+    M = synthetic_keys(pack, S, seed=25)
+    gen = torch.Generator().manual_seed(26)
+    v = torch.randn(h_kv, S, 128, generator=gen)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=6, payload=payload, v_codec="full")
+    kt = torch.randn(h_kv, T, 128, generator=gen).half()
+    vt = torch.randn(h_kv, T, 128, generator=gen).half()
+    q = torch.randn(h_kv, G, 128, generator=gen).half()
+    scale = 128 ** -0.5
+    n_parts = spectral.partial_count(dp, S, q.to(DEV), rope)
+    out = spectral.decode_attention(dp, kp, k_ids, vp, v_ids, S, consts, q.to(DEV), scale,
+                                    k_win=kt.to(DEV) if T else None, v_win=vt.to(DEV) if T else None,
+                                    apply_rope=rope, out_dtype=torch.float32)
+    lloyd = _lloyd(payload)
+    L = O.Layout(pack.bits.numpy())
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L, lloyd)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L, lloyd=lloyd)).float(),
+                          h_kv)
+    cos, sin = A.rope_cos_sin(torch.tensor(consts.inv_freq), torch.arange(S))
+    if rope == k2b.ROPE_FP16_TABLES:
+        cos, sin = cos.half().float(), sin.half().float()
+    V_or = _values_oracle(v, h_kv, "full")
+    ref = A.naive_dense_attention(q.reshape(h_kv * G, 1, 128).float(),
+                                  torch.cat([A.apply_rope(K_or, cos, sin), kt.float()], 1),
+                                  torch.cat([V_or, vt.float()], 1), G, scale).reshape(h_kv, G, 128)
+    o = out.cpu().double()
+    err = (o - ref.double()).abs().max().item()
+    rel = ((o - ref.double()).norm() / ref.double().norm()).item()
+    Vb = torch.empty(h_kv, S, 128, dtype=torch.float16, device=DEV)
+    Sb = torch.empty(h_kv, G, S, dtype=torch.float32, device=DEV)
+    spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=rope, dtype=torch.float16,
+                     out=(None, Vb), q=q.to(DEV), scores=Sb)
+    sw = torch.cat([Sb, (q.float() @ kt.float().transpose(1, 2)).to(DEV)], -1) * scale
+    Vw = torch.cat([Vb.float(), vt.float().to(DEV)], 1)
+    alt = (torch.softmax(sw, -1) @ Vw).cpu().double()
+    d_alt = (o - alt).abs().max().item()
+    print(f"full-C {payload} h_kv {h_kv} G {G} T {T} rope {rope} S {S} ({n_parts} partials): decode vs oracle "
+          f"max_abs {err:.3e} rel {rel:.3e}; vs scores form {d_alt:.3e}", flush=True)
+    assert err <= 2e-3 and rel <= 1e-2 and d_alt <= 2e-3

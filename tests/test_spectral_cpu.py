@@ -184,11 +184,18 @@ def test_recipe_and_construction_guards(tmp_path):
     p = synthetic_pack(2, 2.5, seed=1)
     path = tmp_path / "packs.safetensors"
     spectral.save_packs(path, {0: (p.enc, p.dec, p.lam, {2.5: p.bits})}, (2.5,))
-    # the reference's k4 name pairs full-C turboquant_mse values: it must not
-    # answer with another value codec
-    for arm in ("k4_b2.5", "k4_b3"):
-        with pytest.raises(NotImplementedError, match="full-C turboquant_mse"):
-            spec_pair(arm, pack_path=str(path))
+    # the reference's k4 name pairs full-C turboquant_mse values (recipes.py:138-143)
+    for arm, b in (("k4_b2.5", 2.5), ("k4_b3_lq_dec8tl", 3.0)):
+        k4, v4 = spec_pair(arm, pack_path=str(path))
+        assert (k4.arm, k4.budget, v4.arm, v4.bits) == ("spectral", b, "turboquant_mse", 2)
+    c4 = PackedStreamingCache(cfg, *spec_pair("k4_b2.5", pack_path=str(path)))
+    lay = c4._make_layer()
+    assert lay._v_codec == "full" and lay._page_bytes() == spectral.v_page_bytes(2, "full") == 32 + 2 * 512
+    cfg3 = LlamaConfig(vocab_size=64, hidden_size=384, intermediate_size=256, num_hidden_layers=1,
+                       num_attention_heads=6, num_key_value_heads=3, head_dim=128)
+    from bmx_amd.cache import PackedStreamingLayer
+    with pytest.raises(NotImplementedError, match="power of two"):
+        PackedStreamingLayer(*spec_pair("k4_b2.5", pack_path=str(path)), cfg3, pack=p)
     with pytest.raises(ValueError, match="pack-path"):
         spec_pair("k4ph_b2.5")
     kl, vl = spec_pair("k4ph_b2.5_lq", pack_path=str(path))
@@ -203,7 +210,7 @@ def test_recipe_and_construction_guards(tmp_path):
     with pytest.raises(AssertionError, match="pack_path"):
         PackedStreamingCache(cfg, CacheCodecSpec(arm="spectral", pre_rope=True), v)
     with pytest.raises(NotImplementedError, match="turboquant_mse_perhead"):
-        PackedStreamingCache(cfg, k, CacheCodecSpec(arm="turboquant_mse", bits=2))
+        PackedStreamingCache(cfg, k, CacheCodecSpec(arm="turboquant_mse", bits=3))
     cache = PackedStreamingCache(cfg, k, v)
     assert torch.equal(cache._packs[0].bits, p.bits)
     with pytest.raises(KeyError, match="available"):
@@ -423,3 +430,41 @@ def test_lloyd_level_table_is_the_reference_codebook(variants):
     dp = spectral.DevicePack(synthetic_pack(2, 2.5, seed=1), 2, "cpu", "lloyd")
     assert dp.layout().lloyd_levels == dp.lloyd_levels.data_ptr()
     assert spectral.DevicePack(synthetic_pack(2, 2.5, seed=1), 2, "cpu").layout().lloyd_levels is None
+
+
+@pytest.mark.parametrize("h_kv", [2, 8])
+def test_full_c_value_codec_matches_reference(h_kv):
+    """The oracle's value codec at h = 1 is the reference's full-C
+    turboquant_mse (tests/golden/tq_full.npz): every index and fp16 norm, the
+    dequantized values, the bpe; the C-wide signs the kernels take are the
+    reference's _hadamard_signs(C, 0)."""
+    from oracle import codecs as OC
+
+    z = np.load(GOLD / "tq_full.npz")
+    M = OC.to_matrix(torch.from_numpy(z[f"h{h_kv}_v"]).float())
+    idx, norms, bpe = OC.quantize_v_perhead(M, bits=2, seed=0, h=1)
+    assert np.array_equal(idx.numpy(), z[f"h{h_kv}_idx"]) and np.array_equal(norms.numpy(), z[f"h{h_kv}_norms"])
+    assert bpe == float(z[f"h{h_kv}_bpe"]) == 2 + 16 / (128 * h_kv)
+    deq = OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=1)
+    np.testing.assert_allclose(deq.numpy(), z[f"h{h_kv}_deq"], rtol=0, atol=1e-6)
+    signs = z[f"signs_d{128 * h_kv}_s0"]
+    words = spectral.v_sign_bits_c(h_kv, 0)
+    assert len(words) == 32
+    bits = np.array([(words[c >> 5] >> (c & 31)) & 1 for c in range(128 * h_kv)])
+    assert np.array_equal(bits, (signs < 0).astype(int)) and not any(words[4 * h_kv:])
+
+
+def test_full_c_value_rotation_is_the_kronecker_form():
+    """What the kernels use in place of a C-point FWHT per token: the
+    C-point Hadamard is H_{C/128} (x) H_128 in the index order (slice,
+    channel), so head h's values are H_128 of the slices' sum signed by
+    row h of H_{C/128}."""
+    from oracle import codecs as OC
+
+    h_kv = 8
+    z = np.random.default_rng(3).standard_normal((5, 128 * h_kv)).astype(np.float32)
+    full = OC.fwht(torch.from_numpy(z)).numpy() * np.sqrt(128 * h_kv)
+    for h in range(h_kv):
+        comb = sum((-1) ** bin(h & sl).count("1") * z[:, 128 * sl: 128 * (sl + 1)] for sl in range(h_kv))
+        mine = OC.fwht(torch.from_numpy(comb.astype(np.float32))).numpy() * np.sqrt(128)
+        np.testing.assert_allclose(mine, full[:, 128 * h: 128 * (h + 1)], rtol=1e-4, atol=1e-4)
