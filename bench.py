@@ -73,6 +73,9 @@ def parse():
     ap.add_argument("--spectral-budget", type=float, default=2.5)
     ap.add_argument("--spectral-payload", choices=["rtn", "lloyd"], default="rtn",
                     help="spectral workload: the key payload (lloyd: the recipe's _lq suffix)")
+    ap.add_argument("--spectral-values", choices=["perhead", "full"], default="perhead",
+                    help="spectral workload: the value codec (full: the reference's k4_b recipe, "
+                         "full-C turboquant_mse; perhead: k4ph_b, turboquant_mse_perhead)")
     ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch", "spectral", "e2e"],
                     default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
@@ -683,7 +686,8 @@ def run_spectral(args, torch, dev) -> dict:
     pack = spectral.SpectralPack(enc=(w.sqrt()[:, None] * E).float(), dec=(w.rsqrt()[:, None] * E).float(),
                                  lam=lam.float(), bits=spectral.allocate_bits(lam, args.spectral_budget),
                                  budget=args.spectral_budget)
-    recipe = f"k4ph_b{args.spectral_budget:g}" + ("_lq" if args.spectral_payload == "lloyd" else "")
+    recipe = (("k4_b" if args.spectral_values == "full" else "k4ph_b") + f"{args.spectral_budget:g}"
+              + ("_lq" if args.spectral_payload == "lloyd" else ""))
     k_spec, v_spec = spec_pair(recipe, pack_path="synthetic")
     lay = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=args.window, pack=pack)
     N = args.ctx
@@ -756,7 +760,8 @@ def run_spectral(args, torch, dev) -> dict:
             codes[:, :, k] = rng.integers(lo, lo + (1 << b), (S // 64, 64, int(k.sum())))
         steps = rng.random((S // 64, L.c_pad)).astype(np.float32) * 0.1
         idx = torch.randint(0, 4, (S, C), dtype=torch.int16)
-        norms = torch.rand(S, H_KV) + 0.5
+        v_h = 1 if args.spectral_values == "full" else H_KV
+        norms = torch.rand(S, v_h) + 0.5
         qf = q.float().cpu()
         cos, sin = A.rope_cos_sin(torch.tensor(lay._consts.inv_freq), torch.arange(S))
         threads, host = cpu_threads()
@@ -765,7 +770,7 @@ def run_spectral(args, torch, dev) -> dict:
         def cpu_step():
             Kc = OC.from_matrix(torch.from_numpy(O.dequant(codes, steps, pack.dec.numpy(), L, lloyd=lloyd)).float(),
                                 H_KV)
-            Vc = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=H_KV), H_KV)
+            Vc = OC.from_matrix(OC.dequant_v_perhead(idx, norms, bits=2, seed=0, h=v_h), H_KV)
             return A.naive_dense_attention(qf, A.apply_rope(Kc, cos, sin), Vc, G, scale)
 
         cpu_step()
@@ -790,6 +795,7 @@ def run_spectral(args, torch, dev) -> dict:
                                 f"(c_used {c_used} of {C}, c_pad {dp.c_pad}, {spectral.payload_bpe(pack.bits):.3f} "
                                 f"payload bpe keys)"),
                    "ctx": N, "packed_tokens": P, "budget": args.spectral_budget, "payload": args.spectral_payload,
+                   "values": args.spectral_values,
                    "c_used": c_used,
                    "c_pad": dp.c_pad, "key_page_bytes": dp.k_page_bytes},
         "roofline": {"bound": "mfma", "kernel": (("spectral_partial128_kernel (pages -> per-128-token-block softmax partials)"
@@ -799,7 +805,8 @@ def run_spectral(args, torch, dev) -> dict:
                      "unit": "TFLOP/s", "frac": round(flops / (deq_us * 1e-6) / 1e12 / MFMA_FP16_DENSE_TFLOPS, 4),
                      "traffic": measured_traffic({"ctx": N, "window": args.window, "budget": args.spectral_budget,
                                                   "c_pad": dp.c_pad, "form": "partials",
-                                                  **({"payload": "lloyd"} if args.spectral_payload == "lloyd" else {})},
+                                                  **({"payload": "lloyd"} if args.spectral_payload == "lloyd" else {}),
+                                                  **({"values": "full"} if args.spectral_values == "full" else {})},
                                                  SPECTRAL_TRAFFIC_FILE),
                      "flops_per_launch": flops, "avg_launch_us": round(deq_us, 3),
                      "hbm_bytes_per_launch": page_bytes + out_bytes,

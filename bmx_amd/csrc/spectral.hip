@@ -907,16 +907,22 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 #pragma unroll
           for (int sl = 0; sl < 8; ++sl)
             cs[sl] = *reinterpret_cast<const u32x2_t*>(vp + a.VL.vcode + min(sl, a.h_kv - 1) * 512 + lane * 8);
+          // two slices per 32-deep MFMA (K index 8q + i: tokens 4q + i of
+          // slice 2sp for i < 4, of slice 2sp + 1 after)
 #pragma unroll
-          for (int sl = 0; sl < 8; ++sl) {
-            if (sl >= a.h_kv) break;
-            const half4_t as = vfull_neg(h, sl) ? -aw : aw;
+          for (int sp = 0; sp < 4; ++sp) {
+            if (2 * sp >= a.h_kv) break;
+            const half4_t z4 = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
+            const half4_t a0 = vfull_neg(h, 2 * sp) ? -aw : aw;
+            const half4_t a1 = 2 * sp + 1 < a.h_kv ? (vfull_neg(h, 2 * sp + 1) ? -aw : aw) : z4;
+            const half8_t A8 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            const u32x2_t c0 = cs[2 * sp], c1 = cs[2 * sp + 1];
 #pragma unroll
             for (int ct = 0; ct < 8; ++ct) {
-              const uint32_t byte = ((ct < 4 ? cs[sl].x : cs[sl].y) >> (8 * (ct & 3))) & 0xFFu;
-              const uint2 lvb = s_cbl[byte];
-              const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
-              pv[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(as, vb, pv[ct], 0, 0, 0);
+              const uint2 l0 = s_cbl[((ct < 4 ? c0.x : c0.y) >> (8 * (ct & 3))) & 0xFFu];
+              const uint2 l1 = s_cbl[((ct < 4 ? c1.x : c1.y) >> (8 * (ct & 3))) & 0xFFu];
+              const half8_t B8 = __builtin_bit_cast(half8_t, make_uint4(l0.x, l0.y, l1.x, l1.y));
+              pv[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A8, B8, pv[ct], 0, 0, 0);
             }
           }
         } else {
@@ -1341,6 +1347,19 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     }
     sct[tt] = sc;
   }
+  // full-C values: the block's value codes (8 pages x h_kv slices x 512 B),
+  // loaded now in 16-byte chunks and staged in the RoPE table's space once
+  // the scores have read it
+  u32x4_t vfc[4];
+  const int vf_chunks = 32 * a.h_kv;   // 16-byte chunks of one page's VCODE
+  if constexpr (kVFull) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = min(tid + 512 * i, 8 * vf_chunks - 1), pgi = c / vf_chunks;
+      const uint8_t* vp = a.v_pages + clamp_page(a.v_table[8 * blk + pgi], a.n_v_pool) * (int64_t)a.VL.bytes;
+      vfc[i] = *reinterpret_cast<const u32x4_t*>(vp + a.VL.vcode + (c - pgi * vf_chunks) * 16);
+    }
+  }
   // ---- the two halves of a head add their scores through LDS, in one
   // round: token tiles 0..3 in the pages' space, 4..7 in the code tiles'
   // (both free after the loop) ----
@@ -1359,6 +1378,13 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     // the same sum in both waves: the lower half's value first
     sct[k] = r2 == 0 ? sct[k] + o0 : o0 + sct[k];
     sct[4 + k] = r2 == 0 ? sct[4 + k] + o1 : o1 + sct[4 + k];
+  }
+  uint8_t* vcl = reinterpret_cast<uint8_t*>(&s_cs[0][0]);   // full-C: [page][slice][lane][2] u32
+  if constexpr (kVFull) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (tid + 512 * i < 8 * vf_chunks) reinterpret_cast<u32x4_t*>(vcl)[tid + 512 * i] = vfc[i];
+    __syncthreads();   // the codes staged; every wave is past its reads of the exchange above
   }
   // lane 16q + n holds query n's scores of tokens 16tt + 4q + i
   float m = -INFINITY;
@@ -1395,22 +1421,24 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
 #pragma unroll
     for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[tt][i] * nv[i]);
     if constexpr (kVFull) {
-      // this wave's half (r2) of every slice's code pair of value page tt
-      const uint8_t* vp = a.v_pages + clamp_page(a.v_table[8 * blk + tt], a.n_v_pool) * (int64_t)a.VL.bytes;
-      uint32_t vcs[8];
+      // this wave's half (r2) of every slice's code pair of value page tt, two
+      // slices per 32-deep MFMA (K index 8q + i: tokens 4q + i of slice 2sp
+      // for i < 4, of slice 2sp + 1 after)
 #pragma unroll
-      for (int sl = 0; sl < 8; ++sl)
-        vcs[sl] = *reinterpret_cast<const uint32_t*>(vp + a.VL.vcode + min(sl, a.h_kv - 1) * 512 + lane * 8 + 4 * r2);
-#pragma unroll
-      for (int sl = 0; sl < 8; ++sl) {
-        if (sl >= a.h_kv) break;
-        const half4_t as = vfull_neg(hh, sl) ? -aw : aw;
-        const uint32_t vc = vcs[sl];
+      for (int sp = 0; sp < 4; ++sp) {
+        const int s0 = 2 * sp, s1 = min(2 * sp + 1, a.h_kv - 1);
+        if (s0 >= a.h_kv) break;
+        const half4_t z4 = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
+        const half4_t a0 = vfull_neg(hh, s0) ? -aw : aw;
+        const half4_t a1 = 2 * sp + 1 < a.h_kv ? (vfull_neg(hh, s1) ? -aw : aw) : z4;
+        const half8_t A8 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        const uint32_t vc0 = *reinterpret_cast<const uint32_t*>(vcl + (tt * a.h_kv + s0) * 512 + lane * 8 + 4 * r2);
+        const uint32_t vc1 = *reinterpret_cast<const uint32_t*>(vcl + (tt * a.h_kv + s1) * 512 + lane * 8 + 4 * r2);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
-          const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
-          pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(as, vb, pv[c], 0, 0, 0);
+          const uint2 l0 = s_cbl[(vc0 >> (8 * c)) & 0xFFu], l1 = s_cbl[(vc1 >> (8 * c)) & 0xFFu];
+          const half8_t B8 = __builtin_bit_cast(half8_t, make_uint4(l0.x, l0.y, l1.x, l1.y));
+          pv[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A8, B8, pv[c], 0, 0, 0);
         }
       }
     } else {
@@ -1438,7 +1466,9 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
           pv[c][i] = u + w;
           pv[c | sb][i] = u - w;
         }
-  float4_t* xv = reinterpret_cast<float4_t*>(&s_cs[0][0]);   // [8 waves][4 blocks][64 lanes]: 32 KB
+  // [8 waves][4 blocks][64 lanes]: 32 KB, in the RoPE table's space (full-C:
+  // the pages', whose exchange every wave has read before the codes' barrier)
+  float4_t* xv = reinterpret_cast<float4_t*>(kVFull ? (void*)sp_dyn : (void*)&s_cs[0][0]);
 #pragma unroll
   for (int c = 0; c < 4; ++c) xv[(wave * 4 + c) * 64 + lane] = pv[c];
   __syncthreads();
