@@ -106,6 +106,9 @@ __global__ __launch_bounds__(512) void spectral_encode_kernel(const SpEncodeKArg
   __shared__ float s_y[kGroup][65];          // Y: [token][column]
   __shared__ uint32_t s_code[8 * kGroup * 8 / 4];   // 8 slices of at most 512 bytes
   __shared__ float s_lv[kLloyd ? kLqLevels : 1], s_mid[kLloyd ? kLqLevels : 1];   // levels, midpoints
+  __shared__ float s_l[kLloyd ? kGroup : 1][65];      // Lloyd: the level of each (token, column)
+  __shared__ uint8_t s_cd[kLloyd ? kGroup : 1][64];   // Lloyd: the final level indices
+  __shared__ float s_sc[64];                          // Lloyd: each column's current step
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = blockIdx.x * 64 + lane, g = blockIdx.y;
   const bool active = j < a.c_pad;
@@ -146,26 +149,42 @@ __global__ __launch_bounds__(512) void spectral_encode_kernel(const SpEncodeKArg
   const float* lv = s_lv + (kLloyd ? lq_off(b) : 0);
   const float* mid = s_mid + (kLloyd ? lq_off(b) : 0);
   float scale = 1e-12f;
-  if (active && wave == 0 && lloyd) {
-    double sum = 0.0;
-    for (int t = 0; t < kGroup; ++t) sum += (double)s_y[t][lane];
-    const double mean = sum / 64.0;
-    double ss = 0.0;
-    for (int t = 0; t < kGroup; ++t) {
-      const double d = (double)s_y[t][lane] - mean;
-      ss += d * d;
-    }
-    scale = fmaxf((float)__dsqrt_rn(ss / 63.0), 1e-12f);
-    for (int it = 0; it < 3; ++it) {
-      float num = 0.f, den = 0.f;
+  if constexpr (kLloyd) {
+    // the starting step in wave 0 (lane = column), then 4 rounds: every wave
+    // finds the level indices of 8 tokens (binary searches in parallel), and
+    // for the 3 refits wave 0 sums <Y, l> and <l, l> left to right
+    if (wave == 0) {
+      double sum = 0.0;
+      for (int t = 0; t < kGroup; ++t) sum += (double)s_y[t][lane];
+      const double mean = sum / 64.0;
+      double ss = 0.0;
       for (int t = 0; t < kGroup; ++t) {
-        const float yv = s_y[t][lane];
-        const float l = lv[lq_index(mid, b, yv / scale)];
-        num = __fadd_rn(num, __fmul_rn(yv, l));
-        den = __fadd_rn(den, __fmul_rn(l, l));
+        const double d = (double)s_y[t][lane] - mean;
+        ss += d * d;
       }
-      scale = fmaxf(num / fmaxf(den, 1e-12f), 1e-12f);
+      s_sc[lane] = fmaxf((float)__dsqrt_rn(ss / 63.0), 1e-12f);
     }
+    for (int r = 0; r <= 3; ++r) {
+      __syncthreads();   // the step written; the previous round's levels read
+      const float sc = s_sc[lane];
+      for (int t = wave; t < kGroup; t += 8) {
+        const int c = lq_index(mid, b, s_y[t][lane] / sc);
+        if (r < 3) s_l[t][lane] = lv[c];
+        else s_cd[t][lane] = (uint8_t)c;
+      }
+      if (r == 3) break;
+      __syncthreads();
+      if (wave == 0) {
+        float num = 0.f, den = 0.f;
+        for (int t = 0; t < kGroup; ++t) {
+          const float yv = s_y[t][lane], l = s_l[t][lane];
+          num = __fadd_rn(num, __fmul_rn(yv, l));
+          den = __fadd_rn(den, __fmul_rn(l, l));
+        }
+        s_sc[lane] = fmaxf(num / fmaxf(den, 1e-12f), 1e-12f);
+      }
+    }
+    scale = s_sc[lane];
   } else if (active && wave == 0) {
     float amax = 0.f;
     for (int t = 0; t < kGroup; ++t) amax = fmaxf(amax, fabsf(s_y[t][lane]));
@@ -193,8 +212,7 @@ __global__ __launch_bounds__(512) void spectral_encode_kernel(const SpEncodeKArg
     const uint32_t bias = 1u << (b - 1);
     for (int t = 0; t < kGroup; ++t) {
       const float qv = fminf(fmaxf(rintf(s_y[t][lane] / scale), -qmax - 1.f), qmax);
-      const uint32_t stored = lloyd ? (uint32_t)lq_index(mid, b, s_y[t][lane] / scale)
-                                    : (uint32_t)((int)qv + (int)bias);
+      const uint32_t stored = lloyd ? (uint32_t)s_cd[kLloyd ? t : 0][lane] : (uint32_t)((int)qv + (int)bias);
       const int bit = bit0 + t * w * 8;
       atomicOr(&s_code[bit >> 5], stored << (bit & 31));
     }
@@ -219,53 +237,58 @@ struct SpVFullKArgs {
 
 constexpr int kSpMaxC = 1024;
 
-// The full-C value codec (codecs.py:616-636 at h = 1): grid (16-token pages),
-// block 256.  Per token the fp16 norm of all C channels (squares in 8
-// strided fp32 FMA accumulators, then those left to right: torch's CPU
-// order), the unit row times the C signs, a C-point FWHT in LDS (stages as
-// quant/hadamard.py:19-25), / sqrt(C) * sqrt(C) in fp32, then the 2-bit
-// codes against the codebook's midpoints, packed per 128-channel slice in
-// the per-head VCODE layout.
+// The full-C value codec (codecs.py:616-636 at h = 1): grid (16-token pages x
+// 4), block 256, one quarter q of a page (tokens 4q .. 4q + 3: the tokens of
+// one VCODE dword) per workgroup.  Per token the fp16 norm of all C channels
+// (squares in 8 strided fp32 FMA accumulators, then those left to right:
+// torch's CPU order), the unit row times the C signs, a C-point FWHT in LDS
+// (stages as quant/hadamard.py:19-25), / sqrt(C) * sqrt(C) in fp32, then the
+// 2-bit codes against the codebook's midpoints, packed per 128-channel slice
+// in the per-head VCODE layout.
+constexpr int kVfTok = 4;   // tokens per workgroup
 __global__ __launch_bounds__(256) void spectral_vfull_kernel(const SpVFullKArgs a) {
-  const int pg = blockIdx.x, tid = threadIdx.x;
-  const int C = kD * a.h_kv;
-  __shared__ float x[kPT][kSpMaxC];
-  __shared__ float s_acc[kPT][8];
-  __shared__ float s_norm[kPT];
-  __shared__ uint8_t code[kPT][kSpMaxC];
+  const int pg = blockIdx.x >> 2, qt = blockIdx.x & 3, tid = threadIdx.x;
+  const int C = kD * a.h_kv, lc = 7 + __builtin_ctz((unsigned)a.h_kv);   // C = 2^lc (h_kv a power of two)
+  __shared__ float x[kVfTok][kSpMaxC];
+  __shared__ float s_acc[kVfTok][8];
+  __shared__ float s_norm[kVfTok];
+  __shared__ uint8_t code[kVfTok][kSpMaxC];
   uint8_t* page = a.pages + clamp_page(a.page_ids[pg], a.n_pool) * (int64_t)a.L.bytes;
-  for (int e = tid; e < kPT * C; e += 256) {
-    const int t = e / C, c = e % C;
-    x[t][c] = sp_load(a.v, (c >> 7) * a.vsh + (int64_t)(pg * kPT + t) * a.vst + (c & (kD - 1)), a.v_dtype);
+  const int tok0 = pg * kPT + kVfTok * qt;
+  for (int e = tid; e < kVfTok * C; e += 256) {
+    const int t = e >> lc, c = e & (C - 1);
+    x[t][c] = sp_load(a.v, (c >> 7) * a.vsh + (int64_t)(tok0 + t) * a.vst + (c & (kD - 1)), a.v_dtype);
   }
   __syncthreads();
-  if (tid < kPT * 8) {
+  if (tid < kVfTok * 8) {
     const int t = tid >> 3, j = tid & 7;
     float acc = 0.f;
+#pragma unroll 16
     for (int i = j; i < C; i += 8) acc = __builtin_fmaf(x[t][i], x[t][i], acc);
     s_acc[t][j] = acc;
   }
   __syncthreads();
-  if (tid < kPT) {
+  if (tid < kVfTok) {
     float ss = s_acc[tid][0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) ss = ss + s_acc[tid][j];
     const float nrm = fmaxf(__builtin_sqrtf(ss), 1e-12f);
     const uint16_t nb = float_to_half_bits(nrm);
     s_norm[tid] = half_bits_to_float(nb);
-    reinterpret_cast<uint16_t*>(page + a.L.vnorm)[tid] = nb;
+    reinterpret_cast<uint16_t*>(page + a.L.vnorm)[kVfTok * qt + tid] = nb;
   }
   __syncthreads();
-  for (int e = tid; e < kPT * C; e += 256) {
-    const int t = e / C, c = e % C;
+  for (int e = tid; e < kVfTok * C; e += 256) {
+    const int t = e >> lc, c = e & (C - 1);
     const float u = x[t][c] / s_norm[t];
     x[t][c] = ((a.sign_c[c >> 5] >> (c & 31)) & 1u) ? -u : u;
   }
   __syncthreads();
-  for (int hb = 1; hb < C; hb <<= 1) {
-    for (int e = tid; e < kPT * C / 2; e += 256) {
-      const int t = e / (C / 2), pidx = e % (C / 2);
-      const int i0 = (pidx / hb) * 2 * hb + (pidx % hb);
+  for (int lh = 0; lh < lc; ++lh) {   // butterflies (i, i + hb), hb = 2^lh, as the reference's stages
+    const int hb = 1 << lh;
+    for (int e = tid; e < kVfTok * C / 2; e += 256) {
+      const int t = e >> (lc - 1), pidx = e & (C / 2 - 1);
+      const int i0 = ((pidx >> lh) << (lh + 1)) | (pidx & (hb - 1));
       const float u = x[t][i0], w = x[t][i0 + hb];
       x[t][i0] = u + w;
       x[t][i0 + hb] = u - w;
@@ -277,21 +300,21 @@ __global__ __launch_bounds__(256) void spectral_vfull_kernel(const SpVFullKArgs 
   const float mid0 = (a.codebook[0] + a.codebook[1]) / 2.0f;
   const float mid1 = (a.codebook[1] + a.codebook[2]) / 2.0f;
   const float mid2 = (a.codebook[2] + a.codebook[3]) / 2.0f;
-  for (int e = tid; e < kPT * C; e += 256) {
-    const int t = e / C, c = e % C;
+  for (int e = tid; e < kVfTok * C; e += 256) {
+    const int t = e >> lc, c = e & (C - 1);
     const float r = (x[t][c] / sqrt_c) * sqrt_c;
     code[t][c] = (uint8_t)((r > mid0) + (r > mid1) + (r > mid2));
   }
   __syncthreads();
-  // slice sl, lane 16q + m, dword w: channel 128 sl + 16 (4w + bb) + m, token 4q + t at bit 8bb + 2t
-  for (int i = tid; i < a.h_kv * 128; i += 256) {
-    const int sl = i >> 7, lane = (i >> 1) & 63, w = i & 1, q = lane >> 4, m = lane & 15;
+  // slice sl, lane 16 qt + m, dword w: channel 128 sl + 16 (4w + bb) + m, token 4 qt + t at bit 8bb + 2t
+  if (tid < a.h_kv * 32) {
+    const int sl = tid >> 5, m = (tid >> 1) & 15, w = tid & 1, lane = 16 * qt + m;
     uint32_t dword = 0;
 #pragma unroll
     for (int bb = 0; bb < 4; ++bb) {
       const int c = 128 * sl + 16 * (4 * w + bb) + m;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) dword |= (uint32_t)code[4 * q + t][c] << (8 * bb + 2 * t);
+      for (int t = 0; t < kVfTok; ++t) dword |= (uint32_t)code[t][c] << (8 * bb + 2 * t);
     }
     *reinterpret_cast<uint32_t*>(page + a.L.vcode + sl * 512 + lane * 8 + w * 4) = dword;
   }
@@ -1787,7 +1810,7 @@ extern "C" int32_t bmx_spectral_append(const bmx_spectral_append_args* a, void* 
     v.pages = a->v_pages; v.page_ids = a->v_page_ids; v.L = value_layout(a->L.h_kv, true);
     for (int i = 0; i < 4; ++i) v.codebook[i] = a->v_codebook[i];
     for (int i = 0; i < 32; ++i) v.sign_c[i] = a->v_sign_bits_c[i];
-    hipLaunchKernelGGL(spectral_vfull_kernel, dim3(4 * a->n_groups), dim3(256), 0, st, v);
+    hipLaunchKernelGGL(spectral_vfull_kernel, dim3(4 * 4 * a->n_groups), dim3(256), 0, st, v);
     e = hipGetLastError();
   } else if (e == hipSuccess) {
     AppendKArgs v{};

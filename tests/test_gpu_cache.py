@@ -243,8 +243,9 @@ def _generate(cache, model, ids, n):
 
 @pytest.mark.parametrize("recipe,seq,dtype", [("k2b_ph", 12, torch.float32), ("k2b_ph", 200, torch.float32),
                                               ("k2b_ph", 200, torch.float16), ("rtn_token_4b", 200, torch.float32),
-                                              ("kivi", 200, torch.float32)])
-def test_packed_generate_matches_streaming(recipe, seq, dtype):
+                                              ("kivi", 200, torch.float32), ("k4_b2.5", 200, torch.float32),
+                                              ("k4ph_b2.5_lq_dec8tl", 200, torch.float16)])
+def test_packed_generate_matches_streaming(recipe, seq, dtype, tmp_path):
     """The reference's parity invariant (tests/test_packed_streaming.py:23-97):
     greedy generate through PackedStreamingCache equals generate through its
     StreamingQuantizedCache twin -- the same codes, read by the fused decode
@@ -260,6 +261,8 @@ def test_packed_generate_matches_streaming(recipe, seq, dtype):
                  CacheCodecSpec(arm="rtn_token", bits=4, group=32))
     elif recipe == "kivi":
         specs = spec_pair("kivi", group=64)
+    elif recipe.startswith("k4"):
+        specs = spec_pair(recipe, pack_path=_spectral_pack_file(tmp_path, 2))
     else:
         specs = spec_pair("k2b_ph", rank=16)
     model = _tiny_model().to(dtype)
