@@ -622,6 +622,14 @@ def run_prefill(args, torch, dev) -> dict:
                                        apply_rope=k2b.ROPE_FP16_TABLES, dtype=torch.float16), reps)
     sdpa_us = timed(lambda: F.scaled_dot_product_attention(q.unsqueeze(0), Kf, Vf, attn_mask=mask, scale=scale),
                     reps)
+    # the same dense fp16 K/V through the bottom-right causal bias the packed
+    # layer uses for this mask (grouped heads)
+    from torch.nn.attention.bias import causal_lower_right
+
+    Kg, Vg = Kf[:, ::G].contiguous(), Vf[:, ::G].contiguous()
+    sdpa_lr_us = timed(lambda: F.scaled_dot_product_attention(q.unsqueeze(0), Kg, Vg,
+                                                              attn_mask=causal_lower_right(nq, N), scale=scale,
+                                                              enable_gqa=True), reps)
     out = lay.attend(q, scale, is_causal=True, attention_mask=mask).float()
     ref = F.scaled_dot_product_attention(q.unsqueeze(0).float(), Kf.float(), Vf.float(), attn_mask=mask,
                                          scale=scale).squeeze(0)
@@ -645,6 +653,8 @@ def run_prefill(args, torch, dev) -> dict:
                          "sdpa_frac_of_fp16_mfma_peak": round(flops / (sdpa_us * 1e-6) / 1e12
                                                               / MFMA_FP16_PEAK_TFLOPS, 4),
                          "packed_over_dense_fp16": round(call_us / sdpa_us, 3),
+                         "sdpa_dense_fp16_lower_right_us": round(sdpa_lr_us, 2),
+                         "packed_over_dense_fp16_lower_right": round(call_us / sdpa_lr_us, 3),
                          "max_abs_vs_fp32_sdpa": (out - ref).abs().max().item()},
     }
 

@@ -58,6 +58,7 @@ import weakref
 
 import torch
 import torch.nn.functional as F
+from torch.nn.attention.bias import causal_lower_right
 from transformers.cache_utils import Cache, DynamicLayer
 from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
@@ -552,48 +553,46 @@ class PackedStreamingLayer(DynamicLayer):
         the model dtype (k2b keys rotated in the same pass with the fp16 RoPE
         tables, as _dense_kv does), the fp16 window follows, and one SDPA
         attends: flash attention over the grouped heads (no G-fold copy of K
-        and V) when no mask is needed, the memory-efficient kernel over expanded
-        heads with one.  With no mask from the model and fewer queries than
-        keys, the queries are the last n_q positions: the mask is causal from
-        the bottom right."""
+        and V) when no mask is needed; with fewer queries than keys and no
+        mask, or the model's mask equal to it, the queries are the last n_q
+        positions and the bottom-right causal bias serves the grouped heads;
+        any other mask takes the memory-efficient kernel over expanded heads."""
         dev, dt = q.device, q.dtype
         P = self._committed_S_q
         wk, wv = self.window()
         T = 0 if wk is None else wk.shape[2]
-        parts_k, parts_v = [], []
-        if P > 0 and self._path == "rtn":   # keys were committed post-RoPE
-            kp, vp = rtn.dequant(self._pool, self._table[0, : P // rtn.PAGE_TOKENS].contiguous(),
-                                 h_kv=self._h_kv, dtype=dt, **self._rtn)
-            parts_k.append(kp)
-            parts_v.append(vp)
-        elif P > 0 and self._path == "spectral":
-            # keys rotated at read with the fp16 tables, written with room for
-            # the window after them (no second copy of the dequantized rows)
+        if P > 0:
+            # the committed rows dequantized straight into one buffer with the
+            # window after them: no concatenation of the dense prefix
             Kd = torch.empty(self._h_kv, P + T, self._d_head, dtype=dt, device=dev)
             Vd = torch.empty_like(Kd)
-            spectral.dequant(self._dp, self._kpool, self._ktable[: P // spectral.GROUP], self._pool,
-                             self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._consts,
-                             apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt, out=(Kd, Vd))
+            if self._path == "rtn":   # keys were committed post-RoPE
+                rtn.dequant(self._pool, self._table[0, : P // rtn.PAGE_TOKENS].contiguous(), h_kv=self._h_kv,
+                            dtype=dt, out=(Kd, Vd), **self._rtn)
+            elif self._path == "spectral":   # keys rotated at read with the fp16 tables
+                spectral.dequant(self._dp, self._kpool, self._ktable[: P // spectral.GROUP], self._pool,
+                                 self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._consts,
+                                 apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt, out=(Kd, Vd))
+            else:
+                k2b.dequant(self._pool, self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._basis16,
+                            self._consts, h_kv=self._h_kv, rank=self._rank, apply_rope=k2b.ROPE_FP16_TABLES,
+                            dtype=dt, out=(Kd, Vd))
             if T:
                 Kd[:, P:].copy_(wk.squeeze(0))
                 Vd[:, P:].copy_(wv.squeeze(0))
-            parts_k, parts_v = [Kd], [Vd]
-        elif P > 0:
-            kp, vp = k2b.dequant(self._pool, self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P,
-                                 self._basis16, self._consts, h_kv=self._h_kv, rank=self._rank,
-                                 apply_rope=k2b.ROPE_FP16_TABLES, dtype=dt)
-            parts_k.append(kp)
-            parts_v.append(vp)
-        if T and not (P > 0 and self._path == "spectral"):
-            parts_k.append(wk.squeeze(0).to(dt))
-            parts_v.append(wv.squeeze(0).to(dt))
-        Kd = torch.cat(parts_k, dim=1) if len(parts_k) > 1 else parts_k[0]
-        Vd = torch.cat(parts_v, dim=1) if len(parts_v) > 1 else parts_v[0]
+        else:
+            Kd, Vd = wk.squeeze(0).to(dt), wv.squeeze(0).to(dt)
         n_q, n_kv = q.shape[1], Kd.shape[1]
-        if causal and attention_mask is None and n_q != n_kv:
-            i = torch.arange(n_q, device=dev)[:, None]
-            j = torch.arange(n_kv, device=dev)[None, :]
-            attention_mask = (j <= i + (n_kv - n_q))[None, None]
+        if n_q != n_kv and ((causal and attention_mask is None)
+                            or _is_lower_right_causal(attention_mask, n_q, n_kv)):
+            # the queries are the last n_q positions: causal from the bottom
+            # right, which ROCm's kernels take as a bias of their own (grouped
+            # heads, no mask tensor: ~1.5x the memory-efficient kernel's speed
+            # with the equal boolean mask)
+            out = F.scaled_dot_product_attention(q.unsqueeze(0), Kd.unsqueeze(0), Vd.unsqueeze(0),
+                                                 attn_mask=causal_lower_right(n_q, n_kv), scale=scaling,
+                                                 enable_gqa=G > 1)
+            return out.squeeze(0)
         if attention_mask is None:
             # no mask: ROCm's flash attention takes the grouped heads as they are
             out = F.scaled_dot_product_attention(q.unsqueeze(0), Kd.unsqueeze(0), Vd.unsqueeze(0),
@@ -605,6 +604,26 @@ class PackedStreamingLayer(DynamicLayer):
                 q.unsqueeze(0), Kd.repeat_interleave(G, dim=0).unsqueeze(0),
                 Vd.repeat_interleave(G, dim=0).unsqueeze(0), attn_mask=attention_mask, scale=scaling)
         return out.squeeze(0)
+
+
+_MASK_SEEN: list = [None, -1, False]   # (weak reference to the mask, its version, the answer)
+
+
+def _is_lower_right_causal(mask, n_q: int, n_kv: int) -> bool:
+    """Whether a model's boolean mask (1, 1, n_q, n_kv) is exactly the causal
+    mask of the last n_q positions over n_kv keys.  One device compare (the
+    host waits for it) per mask: the model hands every layer the same mask
+    tensor, so the answer is kept for it while it lives unmodified."""
+    if mask is None or mask.dtype != torch.bool or mask.dim() != 4 or tuple(mask.shape) != (1, 1, n_q, n_kv):
+        return False
+    ref, version, answer = _MASK_SEEN
+    if ref is not None and ref() is mask and version == mask._version:
+        return answer
+    i = torch.arange(n_q, device=mask.device)[:, None]
+    j = torch.arange(n_kv, device=mask.device)[None, :]
+    answer = bool(torch.equal(mask[0, 0], j <= i + (n_kv - n_q)))
+    _MASK_SEEN[:] = [weakref.ref(mask), mask._version, answer]
+    return answer
 
 
 # ------------------------------------------------------------------ cache
