@@ -180,15 +180,17 @@ def test_spectral_cache_matches_oracle_backed_cache(tmp_path, arm):
     assert agree == 1.0
 
 
-def test_spectral_short_prompt_decodes_across_first_commit(tmp_path):
-    """A 100-token prompt on k4ph_b2.5 with a 32-token window: the first decode
-    steps run before any commit (the window alone, no device pack built yet),
-    the flush at 160 tokens commits the first codec page mid-stream.  Teacher
-    forced against the oracle-backed cache, step by step."""
+@pytest.mark.parametrize("arm", ["k4ph_b2.5", "k4_b2.5"])
+def test_spectral_short_prompt_decodes_across_first_commit(tmp_path, arm):
+    """A 100-token prompt with a 32-token window: the first decode steps run
+    before any commit (the window alone, no device pack built yet), the flush
+    at 160 tokens commits the first codec page mid-stream.  Teacher forced
+    against the oracle-backed cache, step by step; per-head and full-C
+    values."""
     g = np.load(GOLD / "e2e_tiny_llama.npz")
     tokens = torch.from_numpy(g["r16_tokens"]).cuda()
     model = _tiny_model(n_layers=1)
-    specs = spec_pair("k4ph_b2.5", pack_path=_spectral_pack_file(tmp_path, 1))
+    specs = spec_pair(arm, pack_path=_spectral_pack_file(tmp_path, 1))
 
     def run(cache):
         got = []
@@ -204,7 +206,7 @@ def test_spectral_short_prompt_decodes_across_first_commit(tmp_path):
     err = (got - ref).abs().max().item()
     scale = ref.abs().max().item()
     agree = (got.argmax(1) == ref.argmax(1)).float().mean().item()
-    print(f"k4ph_b2.5 short prompt: logits max|err| {err:.3e} of {scale:.3f}, argmax agreement {agree:.4f}, "
+    print(f"{arm} short prompt: logits max|err| {err:.3e} of {scale:.3f}, argmax agreement {agree:.4f}, "
           f"committed {prod.layers[0]._committed_S_q}", flush=True)
     assert prod.layers[0]._committed_S_q == 128
     assert err <= 2e-3 * max(scale, 1.0) and agree == 1.0
