@@ -6,6 +6,7 @@
 // include/bmx_spectral.h.  Built without floating-point contraction: every
 // product and sum of the write kernel is rounded on its own, in a fixed order.
 
+#include <mutex>
 #include <type_traits>
 
 #include "bmx_spectral.h"
@@ -1758,11 +1759,30 @@ static bool sp_blocked(const bmx_spectral_dequant_args* a) { return a->partials 
 constexpr size_t kLdsBytes = 160 * 1024;   // per workgroup on gfx950
 
 // A launch whose static and dynamic LDS exceed the CU's is not a valid
-// allocation: refuse it on the host instead.
+// allocation: refuse it on the host instead.  The kernels' static sizes are
+// asked once each (a few kernels: a small table under a lock).
 static bool sp_lds_fits(const void* kernel, size_t dyn) {
-  hipFuncAttributes attr{};
-  if (hipFuncGetAttributes(&attr, kernel) != hipSuccess) return false;
-  return attr.sharedSizeBytes + dyn <= kLdsBytes;
+  static std::mutex mu;
+  static const void* keys[16];
+  static size_t vals[16];
+  static int n = 0;
+  size_t stat = (size_t)-1;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n; ++i)
+      if (keys[i] == kernel) stat = vals[i];
+  }
+  if (stat == (size_t)-1) {
+    hipFuncAttributes attr{};
+    if (hipFuncGetAttributes(&attr, kernel) != hipSuccess) return false;
+    stat = attr.sharedSizeBytes;
+    std::lock_guard<std::mutex> lock(mu);
+    if (n < 16) {
+      keys[n] = kernel;
+      vals[n++] = stat;
+    }
+  }
+  return stat + dyn <= kLdsBytes;
 }
 
 }  // namespace bmx

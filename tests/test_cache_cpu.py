@@ -140,3 +140,24 @@ def test_host_logic_reproduces_reference_run(rank):
     assert err <= 5e-4
     assert bool((got.argmax(1) == ref.argmax(1)).all())
     np.testing.assert_allclose(cache.bits_per_entry(), g[f"r{rank}_bpe"], rtol=1e-12)
+
+
+def test_lower_right_causal_mask_detection():
+    """The prefill's bias choice: a boolean (1, 1, n_q, n_kv) mask equal to the
+    causal mask of the last n_q positions is recognised (and the answer kept
+    for that tensor while it is unmodified); a padded, top-left, float or
+    mis-shaped mask is not."""
+    from bmx_amd.cache import _is_lower_right_causal
+
+    n_q, n_kv = 5, 12
+    i = torch.arange(n_q)[:, None]
+    j = torch.arange(n_kv)[None, :]
+    m = (j <= i + (n_kv - n_q))[None, None].clone()
+    assert _is_lower_right_causal(m, n_q, n_kv)
+    assert _is_lower_right_causal(m, n_q, n_kv)          # kept for the same tensor
+    m[0, 0, 2, 0] = False                                 # in place: the version moves, asked again
+    assert not _is_lower_right_causal(m, n_q, n_kv)
+    assert not _is_lower_right_causal((j <= i)[None, None], n_q, n_kv)   # top-left causal
+    assert not _is_lower_right_causal((j <= i + (n_kv - n_q))[None, None].float(), n_q, n_kv)
+    assert not _is_lower_right_causal((j <= i + (n_kv - n_q))[None, None].expand(2, 1, n_q, n_kv), n_q, n_kv)
+    assert not _is_lower_right_causal(None, n_q, n_kv)
