@@ -1443,6 +1443,96 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     }
   l += __shfl_xor(l, 16);
   l += __shfl_xor(l, 32);
+  if constexpr (kVFull) {
+    // Full-C values: every head of the block reads the same slice codes, so
+    // the 4 heads' weights share the A rows, (local head, query) = divmod(r,
+    // G) for row r, each signed by H_{C/128}[h][slice], and wave w takes the
+    // 16-channel block ct = w of all of them: G <= 4 fills one 16-row tile.
+    if (r2 == 0 && q == 0 && qok && head_ok) {
+      float* dst = sp_part_ml(a.partials, (int64_t)h * a.n_q_groups + n, a.n_tokens / kSpBlk, blk);
+      dst[0] = m;
+      dst[1] = l;
+    }
+    // the weights times the token norms, [local head][value page][q][query]
+    // half4, in the code tiles' space (free since the codes' barrier)
+    u32x2_t* s_aw = reinterpret_cast<u32x2_t*>(&s_b[0][0][0]);
+    if (r2 == 0) {
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt) {
+        const uint2 nr = s_nrm[0][tt][q];
+        const float nv[4] = {half_bits_to_float(nr.x & 0xffffu), half_bits_to_float(nr.x >> 16),
+                             half_bits_to_float(nr.y & 0xffffu), half_bits_to_float(nr.y >> 16)};
+        half4_t aw;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[tt][i] * nv[i]);
+        s_aw[((hl * 8 + tt) * 4 + q) * 16 + n] = __builtin_bit_cast(u32x2_t, aw);
+      }
+    }
+    __syncthreads();
+    const int G = a.n_q_groups, nrg = (4 * G + 15) >> 4;
+    float4_t* xv = reinterpret_cast<float4_t*>(sp_dyn);   // [8 blocks][4 row groups][64 lanes]
+    for (int rg = 0; rg < nrg; ++rg) {
+      const int r = 16 * rg + n, hr = r / G, qr = r - hr * G;
+      const uint32_t amsk = hr < 4 ? 0xffffffffu : 0u;
+      const int hg = 4 * hq + hr;
+      const u32x2_t* ap = s_aw + (min(hr, 3) * 32 + q) * 16 + qr;
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt) {
+        const u32x2_t aw = ap[tt * 64] & amsk;
+        // two slices per 32-deep MFMA: K index 8q + i is token 4q + i of
+        // slice 2sp for i < 4, of slice 2sp + 1 after
+#pragma unroll
+        for (int sp = 0; sp < 4; ++sp) {
+          const int s0 = 2 * sp;
+          if (s0 >= a.h_kv) break;
+          const bool has1 = s0 + 1 < a.h_kv;
+          const int s1 = has1 ? s0 + 1 : s0;
+          const uint32_t n0 = vfull_neg(hg, s0) ? 0x80008000u : 0u;
+          const uint32_t n1 = vfull_neg(hg, s0 + 1) ? 0x80008000u : 0u;
+          const uint32_t m1 = has1 ? 0xffffffffu : 0u;
+          const u32x4_t A4 = {aw[0] ^ n0, aw[1] ^ n0, (aw[0] ^ n1) & m1, (aw[1] ^ n1) & m1};
+          const uint32_t b0 = vcl[(tt * a.h_kv + s0) * 512 + lane * 8 + wave];
+          const uint32_t b1 = vcl[(tt * a.h_kv + s1) * 512 + lane * 8 + wave];
+          const uint2 l0 = s_cbl[b0], l1 = s_cbl[b1];
+          const u32x4_t B4 = {l0.x, l0.y, l1.x, l1.y};
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A4),
+                                                       __builtin_bit_cast(half8_t, B4), acc, 0, 0, 0);
+        }
+      }
+      xv[(wave * 4 + rg) * 64 + lane] = acc;
+    }
+    __syncthreads();
+    // H8 over the block index ct (bits 0, 1, 2 in turn), then the stores:
+    // thread (rg, lane) takes rows 16 rg + 4 (lane >> 4) + i, channel
+    // lane & 15 of every block; the merge applies H16 over that channel
+    if (tid < nrg * 64) {
+      const int rg = tid >> 6, ln = tid & 63;
+      float4_t y[8];
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) y[ct] = xv[(ct * 4 + rg) * 64 + ln];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int sb = 1; sb < 8; sb <<= 1)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+            if (!(ct & sb)) {
+              const float u = y[ct][i], w = y[ct | sb][i];
+              y[ct][i] = u + w;
+              y[ct | sb][i] = u - w;
+            }
+      const int n_parts = a.n_tokens / kSpBlk;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rg + 4 * (ln >> 4) + i, hr = r / G, qr = r - hr * G, hg = 4 * hq + hr;
+        if (hr < 4 && hg < a.h_kv) {
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) sp_part_ch(a.partials, (int64_t)hg * G + qr, n_parts, ct, blk)[ln & 15] = y[ct][i];
+        }
+      }
+    }
+  } else {
   // P.V in the rotated value domain, value page tt (= token tile tt), this
   // wave's channel blocks ct = 4 r2 + c (waves past the heads compute head 0's)
   float4_t pv[4];
@@ -1450,41 +1540,18 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
   for (int c = 0; c < 4; ++c) pv[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int tt = 0; tt < 8; ++tt) {
-    const uint2 nr = s_nrm[kVFull ? 0 : hl][tt][q];
+    const uint2 nr = s_nrm[hl][tt][q];
     const float nv[4] = {half_bits_to_float(nr.x & 0xffffu), half_bits_to_float(nr.x >> 16),
                          half_bits_to_float(nr.y & 0xffffu), half_bits_to_float(nr.y >> 16)};
     half4_t aw;
 #pragma unroll
     for (int i = 0; i < 4; ++i) aw[i] = (_Float16)((float)pw[tt][i] * nv[i]);
-    if constexpr (kVFull) {
-      // this wave's half (r2) of every slice's code pair of value page tt, two
-      // slices per 32-deep MFMA (K index 8q + i: tokens 4q + i of slice 2sp
-      // for i < 4, of slice 2sp + 1 after)
+    const uint32_t vc = r2 == 0 ? s_vcd[hl][tt][lane].x : s_vcd[hl][tt][lane].y;
 #pragma unroll
-      for (int sp = 0; sp < 4; ++sp) {
-        const int s0 = 2 * sp, s1 = min(2 * sp + 1, a.h_kv - 1);
-        if (s0 >= a.h_kv) break;
-        const half4_t z4 = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
-        const half4_t a0 = vfull_neg(hh, s0) ? -aw : aw;
-        const half4_t a1 = 2 * sp + 1 < a.h_kv ? (vfull_neg(hh, s1) ? -aw : aw) : z4;
-        const half8_t A8 = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        const uint32_t vc0 = *reinterpret_cast<const uint32_t*>(vcl + (tt * a.h_kv + s0) * 512 + lane * 8 + 4 * r2);
-        const uint32_t vc1 = *reinterpret_cast<const uint32_t*>(vcl + (tt * a.h_kv + s1) * 512 + lane * 8 + 4 * r2);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint2 l0 = s_cbl[(vc0 >> (8 * c)) & 0xFFu], l1 = s_cbl[(vc1 >> (8 * c)) & 0xFFu];
-          const half8_t B8 = __builtin_bit_cast(half8_t, make_uint4(l0.x, l0.y, l1.x, l1.y));
-          pv[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A8, B8, pv[c], 0, 0, 0);
-        }
-      }
-    } else {
-      const uint32_t vc = r2 == 0 ? s_vcd[hl][tt][lane].x : s_vcd[hl][tt][lane].y;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
-        const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
-        pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[c], 0, 0, 0);
-      }
+    for (int c = 0; c < 4; ++c) {
+      const uint2 lvb = s_cbl[(vc >> (8 * c)) & 0xFFu];
+      const half4_t vb = *reinterpret_cast<const half4_t*>(&lvb);
+      pv[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw, vb, pv[c], 0, 0, 0);
     }
   }
   // H8 over the block index ct = 4 r2 + c: c in registers, r2 (the
@@ -1502,9 +1569,8 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
           pv[c][i] = u + w;
           pv[c | sb][i] = u - w;
         }
-  // [8 waves][4 blocks][64 lanes]: 32 KB, in the RoPE table's space (full-C:
-  // the pages', whose exchange every wave has read before the codes' barrier)
-  float4_t* xv = reinterpret_cast<float4_t*>(kVFull ? (void*)sp_dyn : (void*)&s_cs[0][0]);
+  // [8 waves][4 blocks][64 lanes]: 32 KB, in the RoPE table's space
+  float4_t* xv = reinterpret_cast<float4_t*>(&s_cs[0][0]);
 #pragma unroll
   for (int c = 0; c < 4; ++c) xv[(wave * 4 + c) * 64 + lane] = pv[c];
   __syncthreads();
@@ -1529,6 +1595,7 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     float* dst = sp_part_ml(a.partials, (int64_t)h * a.n_q_groups + n, n_parts, blk);
     dst[0] = m;
     dst[1] = l;
+  }
   }
 }
 
