@@ -1040,6 +1040,7 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 // from the value pages after the main loop: staged in LDS they would not fit
 // beside the key pages) with the weights signed by H_{C/128}[h][slice].
 constexpr int kSpBlk = 128;
+constexpr int kSpVfAwOff = 8 * 4 * 64 * 16;   // full-C: the weight table's offset in the dynamic LDS
 constexpr int kSpBlkMaxPages = 56 * 1024;   // two key pages staged in LDS at most
 
 template <bool kLloyd, bool kVFull>
@@ -1415,13 +1416,6 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
     sct[k] = r2 == 0 ? sct[k] + o0 : o0 + sct[k];
     sct[4 + k] = r2 == 0 ? sct[4 + k] + o1 : o1 + sct[4 + k];
   }
-  uint8_t* vcl = reinterpret_cast<uint8_t*>(&s_cs[0][0]);   // full-C: [page][slice][lane][2] u32
-  if constexpr (kVFull) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (tid + 512 * i < 8 * vf_chunks) reinterpret_cast<u32x4_t*>(vcl)[tid + 512 * i] = vfc[i];
-    __syncthreads();   // the codes staged; every wave is past its reads of the exchange above
-  }
   // lane 16q + n holds query n's scores of tokens 16tt + 4q + i
   float m = -INFINITY;
 #pragma unroll
@@ -1454,8 +1448,14 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
       dst[1] = l;
     }
     // the weights times the token norms, [local head][value page][q][query]
-    // half4, in the code tiles' space (free since the codes' barrier)
-    u32x2_t* s_aw = reinterpret_cast<u32x2_t*>(&s_b[0][0][0]);
+    // half4, in the pages' space past the score exchange (dynamic LDS of 48
+    // KB at least), and the codes, [page][slice][lane][2] u32, in the RoPE
+    // table's (every wave's scores have read it): one barrier for both
+    uint8_t* vcl = reinterpret_cast<uint8_t*>(&s_cs[0][0]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (tid + 512 * i < 8 * vf_chunks) reinterpret_cast<u32x4_t*>(vcl)[tid + 512 * i] = vfc[i];
+    u32x2_t* s_aw = reinterpret_cast<u32x2_t*>(sp_dyn + kSpVfAwOff);
     if (r2 == 0) {
 #pragma unroll
       for (int tt = 0; tt < 8; ++tt) {
@@ -1503,14 +1503,14 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
       xv[(wave * 4 + rg) * 64 + lane] = acc;
     }
     __syncthreads();
-    // H8 over the block index ct (bits 0, 1, 2 in turn), then the stores:
-    // thread (rg, lane) takes rows 16 rg + 4 (lane >> 4) + i, channel
-    // lane & 15 of every block; the merge applies H16 over that channel
-    if (tid < nrg * 64) {
-      const int rg = tid >> 6, ln = tid & 63;
+    // H8 over the block index ct (bits 0, 1, 2 in turn) in every wave; wave
+    // w stores block w: rows 16 rg + 4q + i, channel n (the merge applies
+    // H16 over that channel)
+    const int n_parts = a.n_tokens / kSpBlk;
+    for (int rg = 0; rg < nrg; ++rg) {
       float4_t y[8];
 #pragma unroll
-      for (int ct = 0; ct < 8; ++ct) y[ct] = xv[(ct * 4 + rg) * 64 + ln];
+      for (int ct = 0; ct < 8; ++ct) y[ct] = xv[(ct * 4 + rg) * 64 + lane];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1522,14 +1522,14 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
               y[ct][i] = u + w;
               y[ct | sb][i] = u - w;
             }
-      const int n_parts = a.n_tokens / kSpBlk;
+      float4_t o = y[0];
+#pragma unroll
+      for (int ct = 1; ct < 8; ++ct)
+        if (wave == ct) o = y[ct];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rg + 4 * (ln >> 4) + i, hr = r / G, qr = r - hr * G, hg = 4 * hq + hr;
-        if (hr < 4 && hg < a.h_kv) {
-#pragma unroll
-          for (int ct = 0; ct < 8; ++ct) sp_part_ch(a.partials, (int64_t)hg * G + qr, n_parts, ct, blk)[ln & 15] = y[ct][i];
-        }
+        const int r = 16 * rg + 4 * q + i, hr = r / G, qr = r - hr * G, hg = 4 * hq + hr;
+        if (hr < 4 && hg < a.h_kv) sp_part_ch(a.partials, (int64_t)hg * G + qr, n_parts, wave, blk)[n] = o[i];
       }
     }
   } else {
@@ -1964,7 +1964,8 @@ extern "C" int32_t bmx_spectral_dequant(const bmx_spectral_dequant_args* a, void
   k.partials = a->partials; k.sm_scale = a->sm_scale; k.lq = a->L.lloyd_levels;
   if (sp_blocked(a)) {
     const int kpb = a->L.k_page_bytes;
-    const size_t dyn = std::max<size_t>(2 * (size_t)kpb, (size_t)8 * 4 * 64 * 16);   // pages, then the exchange
+    // the two pages, then the score exchange (and, full-C, the weight table)
+    const size_t dyn = std::max<size_t>(2 * (size_t)kpb, (size_t)kSpVfAwOff + (k.v_full ? 4 * 8 * 4 * 16 * 8 : 0));
     const dim3 grid(a->n_tokens / kSpBlk, (a->L.h_kv + 3) / 4);
     const void* kern = k.lq ? (k.v_full ? (const void*)spectral_partial128_kernel<true, true>
                                         : (const void*)spectral_partial128_kernel<true, false>)
