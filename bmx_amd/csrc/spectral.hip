@@ -1036,9 +1036,10 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
 // blocks.  The
 // RoPE table is the fp16-rounded one (apply_rope 2), kept as fp16 pairs.
 // kLloyd: the Lloyd payload, decoded as in spectral_dequant_kernel<true>.
-// kVFull: full-C values; each head's P.V runs over every slice's codes (read
-// from the value pages after the main loop: staged in LDS they would not fit
-// beside the key pages) with the weights signed by H_{C/128}[h][slice].
+// kVFull: full-C values; the P.V runs over every slice's codes (read from
+// the value pages after the main loop: staged in LDS they would not fit
+// beside the key pages), the block's 4 heads sharing the MFMA rows, each
+// row's weights signed by H_{C/128}[h][slice].
 constexpr int kSpBlk = 128;
 constexpr int kSpVfAwOff = 8 * 4 * 64 * 16;   // full-C: the weight table's offset in the dynamic LDS
 constexpr int kSpBlkMaxPages = 56 * 1024;   // two key pages staged in LDS at most
