@@ -8,7 +8,9 @@
 //   * each wave streams its head's slice of every page (3-bit key residual and
 //     2-bit value codes, 20 bytes per lane per page, 83% of the page bytes)
 //     straight into VGPRs: all loads of the next group are issued at the top
-//     of a group and first waited on at its end;
+//     of a group and first waited on at its end; page bytes are read once, so
+//     every page load is non-temporal (streamed past the L2, which keeps the
+//     kernel's code, arguments, basis and tables: ~1.7 us per 64k call);
 //   * the page prefix every head reads (Us, value norms, key scales) is loaded
 //     cooperatively two groups ahead and staged in a three-slot LDS ring; when
 //     the prologue made every group's RoPE table, the waves hand the ring on
@@ -36,7 +38,11 @@
 //     128-point Hadamard factors as H8 (over the 16-channel chunks) x H16
 //     (within a chunk), and the split kernel applies H8;
 //   * the workgroups that own a 16-token tile of the fp16 recent window score
-//     it on MFMA (decode_shared.h).
+//     it on MFMA (decode_shared.h) after their group loop, on waves 0-3: of
+//     the two waves of a SIMD (w, w + 4) the older wins issue arbitration and
+//     ends its groups ~2 us before the younger, so the tiles fill that slack
+//     instead of delaying the workgroup's first group; the two waves of a
+//     SIMD also take turns at the higher issue priority page by page.
 //
 // combine_kernel<true> (decode_shared.h): one wave per (16-channel chunk,
 // query head, sequence) merges the packed partials of its chunk (base-2 LSE),
@@ -102,6 +108,10 @@ struct DecodeKArgs {
   int balanced;           // a ragged batch: workgroup w of the flat grid serves the
                           // sequence batch_shares() gives it (max_splits = the slots per row)
   int n_seq;
+  // floor(n / max_splits) for n < 2^32 as (t + ((n - t) >> div_sh1)) >> div_sh2,
+  // t = mulhi(n, div_magic) (Granlund-Montgomery); div_ok: split * groups < 2^32
+  uint32_t div_magic;
+  int div_sh1, div_sh2, div_ok;
 };
 
 // v_mov_b32_dpp: lanes enabled by BANK (4-lane banks of each 16-lane row) take
@@ -257,8 +267,20 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const int len_spec = len_known >= 0 ? len_known : a.max_packed_len & ~(kGroup - 1);
   auto range = [&](int L, int& r0, int& r1) {
     const int NG = L / kGroup;
-    r0 = (int)(((int64_t)split * NG) / S);
-    r1 = (int)(((int64_t)(split + 1) * NG) / S);
+    if (!a.balanced && a.div_ok) {
+      // uniform operands in scalar registers: no 64-bit divide on the vector unit
+      const uint32_t ng = (uint32_t)__builtin_amdgcn_readfirstlane(NG);
+      const uint32_t sp = (uint32_t)__builtin_amdgcn_readfirstlane(split);
+      auto div = [&](uint32_t n) -> int {
+        const uint32_t t = __umulhi(n, a.div_magic);
+        return (int)((t + ((n - t) >> a.div_sh1)) >> a.div_sh2);
+      };
+      r0 = div(sp * ng);
+      r1 = div((sp + 1) * ng);
+    } else {
+      r0 = (int)(((int64_t)split * NG) / S);
+      r1 = (int)(((int64_t)(split + 1) * NG) / S);
+    }
   };
   int g0, g1;
   range(len_spec, g0, g1);
@@ -319,7 +341,8 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   // 64-position rotation steps, each value corrected to the fp32 angle ----
   auto produce_groups = [&](int g_first, int count, int buf_first) {
     float cc[8], ss[8];
-    const double rev = (double)fq * (double)(t_begin + g_first * kGroup + wave) * 0.15915494309189535;
+    const int t_first = t_begin + g_first * kGroup + wave;
+    const double rev = (double)fq * (double)t_first * 0.15915494309189535;
     const float fr = (float)(rev - floor(rev));
     cc[0] = __builtin_amdgcn_cosf(fr);
     ss[0] = __builtin_amdgcn_sinf(fr);
@@ -328,21 +351,24 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
       cc[k] = cc[k - 1] * c8 - ss[k - 1] * s8;
       ss[k] = ss[k - 1] * c8 + cc[k - 1] * s8;
     }
+    float tf0 = (float)t_first;   // positions below 2^24: every step exact
+    int buf = buf_first % cs_bufs;
     for (int g = 0; g < count; ++g) {
-      uint32_t* dst = cst + ((buf_first + g) % cs_bufs) * kCsBuf;
+      uint32_t* dst = cst + buf * kCsBuf + wave * kCsRow + fj;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const int tl = wave + 8 * k;
-        const float tf = (float)(t_begin + (g_first + g) * kGroup + tl);
+        const float tf = tf0 + (float)(8 * k);
         const float ang = fq * tf;
         const float e = __builtin_fmaf(fq, tf, -ang);  // exact: fq*tf - fl(fq*tf)
         const half2_t v = {(_Float16)__builtin_fmaf(ss[k], e, cc[k]),
                            (_Float16)__builtin_fmaf(-cc[k], e, ss[k])};
-        dst[tl * kCsRow + fj] = as_u32(v);
+        dst[8 * k * kCsRow] = as_u32(v);
         const float cn = cc[k] * stc - ss[k] * sts;
         ss[k] = ss[k] * stc + cc[k] * sts;
         cc[k] = cn;
       }
+      tf0 += (float)kGroup;
+      buf = buf + 1 == cs_bufs ? 0 : buf + 1;
     }
   };
   auto load_ids = [&](int first, int count) { return (int)clamp_page(load_ids_raw(first, count), a.n_pool); };
@@ -366,7 +392,8 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     const int c = min(tid, sh_chunks - 1);
     const int pp = c / chunks_pp;
     const int id = __shfl(pidv, gi * kGroupPages + pp - pid_base);
-    return *reinterpret_cast<const uint4*>(a.pages + (int64_t)id * pb + (c - pp * chunks_pp) * 16);
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(a.pages + (int64_t)id * pb + (c - pp * chunks_pp) * 16));
+    return make_uint4(v[0], v[1], v[2], v[3]);
   };
   auto store_prefix = [&](uint4 v, int slot) {
     if (tid < sh_chunks) *reinterpret_cast<uint4*>(ring + slot * kGroupPages * SHB + tid * 16) = v;
@@ -374,11 +401,14 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   // uniform page base + 32-bit lane offset: the scalar-base load form
   const uint32_t kres_off = (uint32_t)(a.L.kres + h * 768 + lane * 12);
   const uint32_t vcode_off = (uint32_t)(a.L.vcode + h * 512 + lane * 8);
+  typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
   auto load_kres = [&](int gi, int pp) -> uint3 {
-    return *reinterpret_cast<const uint3*>(page_ptr(gi, pp) + kres_off);
+    const u32x3_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x3_t*>(page_ptr(gi, pp) + kres_off));
+    return make_uint3(v[0], v[1], v[2]);
   };
   auto load_vcode = [&](int gi, int pp) -> uint2 {
-    return *reinterpret_cast<const uint2*>(page_ptr(gi, pp) + vcode_off);
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(page_ptr(gi, pp) + vcode_off));
+    return make_uint2(v[0], v[1]);
   };
 
   // ---- first group in flight: at once for contiguous pages (for the host
@@ -420,12 +450,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   if (!contig) issue_first(n_groups);
   const int n_pages = n_groups * kGroupPages;
 
-  // the rows of this workgroup's first window tile, if it owns one: issued
-  // after the first group's pages, whose addresses wait for every load before
+  // the recent-window tiles this workgroup owns (scored after the group loop)
   int win_stride;
   const int win_j0 = first_win_tile(split, S, win_stride);
-  uint2 kw[8];
-  if (win_j0 < n_win_tiles) load_win_tile(a, tail_base, win_j0, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh);
 
   if (tid < 256) {
     const uint32_t l0 = a.level_hi[0], l1 = a.level_hi[1], l2 = a.level_hi[2], l3 = a.level_hi[3];
@@ -433,19 +460,11 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     s_vlut[tid] = make_uint2(lv(tid & 3) | (lv((tid >> 2) & 3) << 16), lv((tid >> 4) & 3) | (lv(tid >> 6) << 16));
   }
 
-  // query fragments (qf: the MFMA B operand of the packed pages; qlo: the low
-  // parts, used by the window tiles only)
+  // query fragments (qf: the MFMA B operand of the packed pages; the low parts
+  // are unused here: the window tiles remake both after the loop)
   half8_t qf[4], qlo[4];
   query_fragments(qraw, (n < a.G) ? a.qscale_rope : 0.0f, qf, qlo);
 
-  // recent-window tiles (the first one's rows are in flight)
-  if (active && win_j0 < n_win_tiles) {
-    score_win_tile(a, b, h, win_j0, n, q, kw, qf, qlo, tail_base);
-    for (int j = win_j0 + win_stride; j < n_win_tiles; j += win_stride) {
-      load_win_tile(a, tail_base, j, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh);
-      score_win_tile(a, b, h, j, n, q, kw, qf, qlo, tail_base);
-    }
-  }
   store_prefix(pre, 0);
   store_prefix(pre1, 1);
   // slots 0 and 1 hold groups 0 and 1 (visible at the barrier)
@@ -545,6 +564,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
         slice(std::integral_constant<int, 2>{});
         slice(std::integral_constant<int, 3>{});
         sc[pp] = s;
+        // the two waves of a SIMD (w, w + 4) take turns at the higher issue priority
+        if (((pp + (wave >> 2)) & 1) != 0) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);   // bound the cross-page overlap (VGPR budget)
       }
       // ---- compaction: page r*NSLOT + s moves to columns [s*SW, (s+1)*SW) ----
@@ -649,6 +671,28 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     }
     // with tables to refill in the loop, all waves move group by group
     if (lockstep) __syncthreads();   // table of group gi+1 visible; group gi's slots free
+  }
+  if (wave < 4 && win_j0 < n_win_tiles) {
+    // the window tiles, scored after the group loop by waves 0-3: of the two
+    // waves of a SIMD these finish their groups first, so the tiles take no
+    // time on the workgroup's critical path; wave w takes heads w and w + 4
+    for (int hh = wave; hh < a.h_kv; hh += 4) {
+      const float* qrow = a.q + (((int64_t)b * a.h_kv + hh) * a.G + (n < a.G ? n : 0)) * kD;
+      const int64_t tb = (int64_t)b * a.ts_b + (int64_t)hh * a.ts_h;
+      const int64_t nb = (int64_t)b * a.nw.sb + (int64_t)hh * a.nw.sh;
+      float4_t qraw2[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) qraw2[u] = *reinterpret_cast<const float4_t*>(qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2));
+      uint2 kw[8];
+      load_win_tile(a, tb, win_j0, n, q, kw, nb);
+      half8_t qh2[4], ql2[4];
+      query_fragments(qraw2, (n < a.G) ? a.qscale_rope : 0.0f, qh2, ql2);
+      score_win_tile(a, b, hh, win_j0, n, q, kw, qh2, ql2, tb);
+      for (int j = win_j0 + win_stride; j < n_win_tiles; j += win_stride) {
+        load_win_tile(a, tb, j, n, q, kw, nb);
+        score_win_tile(a, b, hh, j, n, q, kw, qh2, ql2, tb);
+      }
+    }
   }
   if (active) {
     // fold the page slots: column s*SW + g -> g
@@ -1036,6 +1080,17 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   k.cs_bufs = std::max(1, std::min(max_groups, kCsMaxBufs));
   k.balanced = balanced ? 1 : 0;
   k.n_seq = a->batch;
+  {
+    // magic division by max_splits (Granlund-Montgomery, all 32-bit numerators)
+    const uint32_t d = (uint32_t)max_splits;
+    int l = 0;
+    while ((1ull << l) < d) ++l;
+    k.div_magic = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    k.div_sh1 = l < 1 ? l : 1;
+    k.div_sh2 = l > 1 ? l - 1 : 0;
+    const uint64_t groups = (uint64_t)(a->max_packed_len / kGroup);
+    k.div_ok = (uint64_t)d * (groups + 1) < (1ull << 32) ? 1 : 0;
+  }
   const size_t smem = (size_t)k.cs_bufs * kCsBuf * 4 + (size_t)kRingSlots * kGroupPages * k.shared_bytes;
   const dim3 grid = balanced ? dim3(n_wg, 1) : dim3(max_splits, a->batch);
   hipError_t e = g.rank == 32 ? launch_split<32>(k, grid, smem, st)
