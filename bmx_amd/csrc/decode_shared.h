@@ -155,6 +155,33 @@ __device__ __forceinline__ void query_fragments(const float4_t qraw[8], float sc
 }
 
 // ---------------------------------------------------------------------------
+// Split partial records.  A (row, split) partial is its 128 channel sums
+// divided by its softmax sum l, in fp16 (a weighted mean of value-sized
+// numbers: 2^-12 relative rounding, half the bytes of fp32), chunk-major so a
+// merge workgroup reads one 32-byte record per split: acc16[row][chunk][S][16];
+// (m, l) stay fp32 in ml[row][S][2].  The merge weighs record s by
+// l_s 2^(m_s - M).  An empty split (l = 0, m = -inf) stores zeros.
+// Lane 16q + n (n < G: query n) writes channels 4q..4q+3 of each chunk.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_partial_record(uint16_t* acc16, float* ml, int64_t row, int S, int split,
+                                                     int q, const float4_t acc[8], float m_run, float l_run) {
+  const float inv_l = l_run > 0.f ? 1.0f / l_run : 0.f;
+  uint16_t* dst = acc16 + (row * 8 * S + split) * 16 + 4 * q;   // chunk bt at + bt * S * 16
+#pragma unroll
+  for (int bt = 0; bt < 8; ++bt) {
+    const half2_t lo = {(_Float16)(acc[bt][0] * inv_l), (_Float16)(acc[bt][1] * inv_l)};
+    const half2_t hi = {(_Float16)(acc[bt][2] * inv_l), (_Float16)(acc[bt][3] * inv_l)};
+    *reinterpret_cast<uint2*>(dst + (int64_t)bt * S * 16) = make_uint2(as_u32(lo), as_u32(hi));
+  }
+  if (q == 0) *reinterpret_cast<float2*>(ml + (row * S + split) * 2) = make_float2(m_run, l_run);
+}
+
+// Bytes of the partial records and (m, l) of rows x splits (the window scores follow).
+__host__ __device__ __forceinline__ size_t partial_bytes(size_t rows, size_t splits) {
+  return rows * splits * (kD * 2 + 2 * 4);
+}
+
+// ---------------------------------------------------------------------------
 // Combine: merge of the packed partials and the recent window.  One workgroup
 // of kCmbWaves waves per (16-channel chunk, query row, sequence): the partials
 // arrive already in the output domain, so a chunk needs only its own 16
@@ -182,7 +209,7 @@ struct CombineKArgs {
   const int32_t* packed_len;
   int max_packed_len;
   float* out;
-  const float* ws_acc;
+  const uint16_t* ws_acc;   // partial records (store_partial_record)
   const float* ws_ml;
   const float* ws_win;
   const uint16_t* v_tail;
@@ -233,7 +260,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, p = lane & 15, c4 = lane >> 4;
   const int S_slots = a.max_splits;
   const int64_t row = (int64_t)b * a.h_kv * a.G + r;   // (b, h, g) row
-  const float* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S_slots * kChunk + 4 * c4;
+  const uint16_t* accb = a.ws_acc + (row * kChunks + ch) * (int64_t)S_slots * kChunk + 4 * c4;
   const float* mlb = a.ws_ml + row * S_slots * 2;
   const float* swb = a.ws_win + row * a.tail_cap;
   const uint16_t* vb = a.v_tail + b * a.ts_b + h * a.ts_h + kChunk * ch + 4 * c4;
@@ -254,7 +281,9 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
     for (int u = 0; u < kCmbSplits; ++u) {
       const int i = min(elem(j0, u), S - 1);
       ml[u] = *reinterpret_cast<const f2_t*>(mlb + 2 * (int64_t)i);
-      pv[u] = *reinterpret_cast<const float4_t*>(accb + (int64_t)i * kChunk);
+      const uint2 r = *reinterpret_cast<const uint2*>(accb + (int64_t)i * kChunk);
+      const half2_t lo = as_h2(r.x), hi = as_h2(r.y);
+      pv[u] = float4_t{(float)lo[0], (float)lo[1], (float)hi[0], (float)hi[1]};
     }
   };
   auto load_tokens = [&](int t0, int t_end) {   // t_end >= 1
@@ -295,11 +324,12 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
       lp *= sc;
 #pragma unroll
       for (int u = 0; u < kCmbSplits; ++u) {
-        // lanes past the sequence's splits re-read its last: select, not weight by 0
+        // lanes past the sequence's splits re-read its last: select, not weight by 0;
+        // a record is a mean over its split: weight l 2^(m - M)
         const bool ok = elem(j0, u) < S && ml[u][0] != -INFINITY;
-        const float w = ok ? __builtin_amdgcn_exp2f(ml[u][0] - mnew) : 0.f;
+        const float w = ok ? __builtin_amdgcn_exp2f(ml[u][0] - mnew) * ml[u][1] : 0.f;
         xp += ok ? w * pv[u] : float4_t{0.f, 0.f, 0.f, 0.f};
-        lp = ok ? __builtin_fmaf(w, ml[u][1], lp) : lp;
+        lp = ok ? lp + w : lp;
       }
       mp = mnew;
     }

@@ -81,7 +81,7 @@ struct DecodeKArgs {
   int shared_bytes;    // page prefix read by every head: US, VNORM, KSCALE (multiple of 16)
   int cs_bufs;         // RoPE table buffers in LDS (groups produced in the prologue)
   const float* q;
-  float* ws_acc;       // [B][h_kv][G][8][max_splits][16] accumulators (H8 applied)
+  uint16_t* ws_acc;    // [B][h_kv][G][8][max_splits][16] partial records (H8 applied; decode_shared.h)
   float* ws_ml;        // [B][h_kv][G][max_splits][2]     (running max, sum), base 2
   const uint8_t* pages;
   const int32_t* page_table;
@@ -171,14 +171,9 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
   const float corr = 8.0f * a.level_mu * w_run;
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[0][i] -= corr;
-  if (n < a.G) {
-    const int S = a.max_splits;
-    const int64_t row = ((int64_t)b * a.h_kv + h) * a.G + n;
-    float* dst = a.ws_acc + (row * 8 * S + split) * 16 + 4 * q;   // chunk bt at + bt * S * 16
-#pragma unroll
-    for (int bt = 0; bt < 8; ++bt) *reinterpret_cast<float4_t*>(dst + (int64_t)bt * S * 16) = acc[bt];
-    if (q == 0) *reinterpret_cast<float2*>(a.ws_ml + (row * S + split) * 2) = make_float2(m_run, l_run);
-  }
+  if (n < a.G)
+    store_partial_record(a.ws_acc, a.ws_ml, ((int64_t)b * a.h_kv + h) * a.G + n, a.max_splits, split, q, acc,
+                         m_run, l_run);
 }
 
 // Window tiles of split `split` of S: tiles split, split + S, ... (a tile's
@@ -762,12 +757,11 @@ static int choose_splits(const bmx_k2b_decode_args* a) {
   return S < 1 ? 1 : S;
 }
 
-// Workspace: split partials, accumulators [B][h_kv][G][8][S][16] then
-// (max, sum) [B][h_kv][G][S][2], then window scores [B][h_kv][G][tail_cap],
-// fp32.
+// Workspace: split partial records [B][h_kv][G][8][S][16] fp16, then (max,
+// sum) [B][h_kv][G][S][2] fp32, then window scores [B][h_kv][G][tail_cap] fp32.
 static size_t ws_bytes(const bmx_k2b_decode_args* a, int splits) {
   const size_t rows = (size_t)a->batch * a->geom.h_kv * a->geom.n_q_groups;
-  return rows * ((size_t)splits * (kD + 2) + (size_t)a->tail_cap) * sizeof(float);
+  return partial_bytes(rows, (size_t)splits) + rows * (size_t)a->tail_cap * sizeof(float);
 }
 
 extern "C" size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* a) {
@@ -1028,8 +1022,8 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
                                  "bmx_k2b_decode_workspace_bytes()");
   hipStream_t st = (hipStream_t)stream;
   const size_t rows = (size_t)a->batch * max_splits * g.h_kv * g.n_q_groups;
-  float* ws_acc = (float*)ws;
-  float* ws_ml = ws_acc + rows * kD;
+  uint16_t* ws_acc = (uint16_t*)ws;
+  float* ws_ml = (float*)(ws_acc + rows * kD);
   float* ws_win = ws_ml + rows * 2;
   const float qscale = a->sm_scale * 1.4426950408889634f;
 

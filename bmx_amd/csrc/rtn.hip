@@ -248,7 +248,7 @@ struct RtnDecodeKArgs {
   int gk, gv;
   int prefix_bytes;    // scale bytes of one page (KSCALE + VSCALE), multiple of 16
   const float* q;
-  float* ws_acc;       // [B][h_kv][G][8][max_splits][16] channel sums
+  uint16_t* ws_acc;    // [B][h_kv][G][8][max_splits][16] partial records of the channel sums (decode_shared.h)
   float* ws_ml;        // [B][h_kv][G][max_splits][2] (running max, sum), base 2
   const uint8_t* pages;
   const int32_t* page_table;
@@ -295,14 +295,9 @@ __device__ __forceinline__ void rtn_store_partial(const RtnDecodeKArgs& a, int b
                                                   int q, const float4_t acc[8], float m_run, float l_run) {
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
-  if (n < a.G) {
-    const int S = a.max_splits;
-    const int64_t row = ((int64_t)b * a.h_kv + h) * a.G + n;
-    float* dst = a.ws_acc + (row * 8 * S + split) * 16 + 4 * q;
-#pragma unroll
-    for (int bt = 0; bt < 8; ++bt) *reinterpret_cast<float4_t*>(dst + (int64_t)bt * S * 16) = acc[bt];
-    if (q == 0) *reinterpret_cast<float2*>(a.ws_ml + (row * S + split) * 2) = make_float2(m_run, l_run);
-  }
+  if (n < a.G)
+    store_partial_record(a.ws_acc, a.ws_ml, ((int64_t)b * a.h_kv + h) * a.G + n, a.max_splits, split, q, acc,
+                         m_run, l_run);
 }
 
 // the lane's query in the RoPE pair order of the window tiles (decode_shared.h)
@@ -817,7 +812,7 @@ static int rtn_choose_splits(const bmx_rtn_decode_args* a) {
 
 static size_t rtn_ws_bytes(const bmx_rtn_decode_args* a, int splits) {
   const size_t rows = (size_t)a->batch * a->geom.h_kv * a->geom.n_q_groups;
-  return rows * ((size_t)splits * (kD + 2) + (size_t)a->tail_cap) * sizeof(float);
+  return partial_bytes(rows, (size_t)splits) + rows * (size_t)a->tail_cap * sizeof(float);
 }
 
 extern "C" size_t bmx_rtn_decode_workspace_bytes(const bmx_rtn_decode_args* a) {
@@ -876,8 +871,8 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
     return rfail(BMX_E_WORKSPACE, "bmx_rtn_decode: workspace missing or smaller than "
                                   "bmx_rtn_decode_workspace_bytes()");
   const size_t rows = (size_t)a->batch * S * g.h_kv * g.n_q_groups;
-  float* ws_acc = (float*)a->workspace;
-  float* ws_ml = ws_acc + rows * kD;
+  uint16_t* ws_acc = (uint16_t*)a->workspace;
+  float* ws_ml = (float*)(ws_acc + rows * kD);
   float* ws_win = ws_ml + rows * 2;
   hipStream_t st = (hipStream_t)stream;
 
