@@ -123,7 +123,8 @@ def test_decode_workspace_size_formula():
     a.max_packed_len = 65536
     a.split_tokens = 1024
     n = _lib.lib().bmx_k2b_decode_workspace_bytes(ct.byref(a))
-    assert n == 2 * 64 * 8 * 4 * 130 * 4  # 64 split partials of (128 acc + max + sum) per query
+    # 64 split partials per query: a record of 128 fp16 channel means, then fp32 (max, sum)
+    assert n == 2 * 64 * 8 * 4 * (128 * 2 + 2 * 4)
 
 
 def test_product_codec_constants_match_reference():
