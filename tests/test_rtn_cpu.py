@@ -159,4 +159,5 @@ def test_rtn_workspace_size_formula():
     a.geom = rtn.geom(8, 4, k_bits=4, v_bits=4, k_group=32, v_group=32)
     a.batch, a.max_packed_len, a.split_tokens, a.tail_cap = 2, 65536, 1024, 200
     n = _lib.lib().bmx_rtn_decode_workspace_bytes(ct.byref(a))
-    assert n == 2 * 8 * 4 * (64 * 130 + 200) * 4   # split partials + window scores per query
+    # per query: 64 split records (128 fp16 channel means, fp32 max and sum), then 200 fp32 window scores
+    assert n == 2 * 8 * 4 * (64 * (128 * 2 + 2 * 4) + 200 * 4)
