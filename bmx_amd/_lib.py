@@ -59,6 +59,7 @@ class DecodeArgs(ct.Structure):
         ("new_stride_h", ct.c_int64),
         ("new_stride_t", ct.c_int64),
         ("n_new", ct.c_int32),
+        ("io_dtype", ct.c_int32),
     ]
 
 
@@ -159,6 +160,7 @@ class RtnDecodeArgs(ct.Structure):
         ("new_stride_h", ct.c_int64),
         ("new_stride_t", ct.c_int64),
         ("n_new", ct.c_int32),
+        ("io_dtype", ct.c_int32),
     ]
 
 

@@ -67,7 +67,8 @@ from . import codecs as K
 from . import k2b, rtn, spectral
 from .specs import CacheCodecSpec, packed_path
 
-ATTN_NAME = "bmx_k2b"
+ATTN_NAME = "chunked_dequant"   # the reference's name (packed_streaming.py:54), set on attach
+ATTN_ALIASES = ("bmx_k2b",)      # the name earlier versions of this package registered
 PAGE = 128          # codec page (packed_streaming.py:438)
 PAGES_PER_CODEC = PAGE // k2b.PAGE_TOKENS
 
@@ -142,8 +143,9 @@ def packed_attention_forward(module, query, key, value, attention_mask, scaling,
     return out.transpose(0, 1).reshape(1, n_q, n_h * d).to(query.dtype), None
 
 
-ALL_ATTENTION_FUNCTIONS.register(ATTN_NAME, packed_attention_forward)
-ALL_MASK_ATTENTION_FUNCTIONS.register(ATTN_NAME, sdpa_mask)
+for _name in (ATTN_NAME, *ATTN_ALIASES):
+    ALL_ATTENTION_FUNCTIONS.register(_name, packed_attention_forward)
+    ALL_MASK_ATTENTION_FUNCTIONS.register(_name, sdpa_mask)
 
 
 # ------------------------------------------------------------------ layer
@@ -476,39 +478,41 @@ class PackedStreamingLayer(DynamicLayer):
         dev = q.device
         h, d = self._h_kv, self._d_head
         P, T = self._committed_S_q, self._T
-        q32 = q.reshape(1, h, G, d).float()
-        if not q32.is_contiguous():
-            q32 = q32.contiguous()
+        # the query goes in as the model gives it (fp32, fp16 or bf16; the kernels
+        # convert on load), and the output comes back in the same dtype
+        qm = q.reshape(1, h, G, d)
+        if not qm.is_contiguous():
+            qm = qm.contiguous()
         if self._win_k.dtype != torch.float16:   # a model in fp32: the window goes in as fp16
             self._land_pending()
             kt = self._win_k[:, :, :T].half().contiguous()
             vt = self._win_v[:, :, :T].half().contiguous()
             pool, table, basis16 = self._decode_operands(dev)
             if self._path == "rtn":
-                out = rtn.decode(q32, pool, table, self._packed_len_dev, P, scaling, k_tail=kt, v_tail=vt,
+                out = rtn.decode(qm, pool, table, self._packed_len_dev, P, scaling, k_tail=kt, v_tail=vt,
                                  tail_len=T, tail_cap=T, **self._rtn)
             else:
-                out = k2b.decode(q32, pool, None, self._packed_len_dev, P, basis16, self._consts, scaling,
+                out = k2b.decode(qm, pool, None, self._packed_len_dev, P, basis16, self._consts, scaling,
                                  rank=self._rank, k_tail=kt, v_tail=vt, tail_len=T, tail_cap=T)
             return out.reshape(h * G, 1, d)
-        key = (P, G, float(scaling), None if self._pool is None else self._pool.data_ptr())
+        key = (P, G, float(scaling), qm.dtype, None if self._pool is None else self._pool.data_ptr())
         if self._plan is None or self._plan_key != key:
             pool, table, basis16 = self._decode_operands(dev)
             cap = self._win_k.shape[2]
             common = dict(k_tail=self._win_k, v_tail=self._win_v, tail_len=T, tail_cap=cap,
-                          out=torch.empty_like(q32))
+                          out=torch.empty_like(qm))
             if self._path == "rtn":
-                self._plan = rtn.DecodePlan(q32, pool, table, self._packed_len_dev, P, scaling, **common,
+                self._plan = rtn.DecodePlan(qm, pool, table, self._packed_len_dev, P, scaling, **common,
                                             **self._rtn)
             else:
-                self._plan = k2b.DecodePlan(q32, pool, None, self._packed_len_dev, P, basis16, self._consts,
+                self._plan = k2b.DecodePlan(qm, pool, None, self._packed_len_dev, P, basis16, self._consts,
                                             scaling, rank=self._rank, **common)
             self._plan_key = key
         pending, self._pending = self._pending, None
-        out = self._plan.run(q=q32, tail_len=T, new_kv=pending)
+        # a fresh output tensor per call (an allocation, no kernel): the caller
+        # may keep it past the layer's next step
+        out = self._plan.run(q=qm, tail_len=T, new_kv=pending, out=torch.empty_like(qm))
         self.n_rows_folded += pending is not None
-        if q.dtype == torch.float32:   # the caller keeps the output as it is: a copy of the plan's buffer
-            out = out.clone()
         return out.reshape(h * G, 1, d)
 
     def _decode_operands(self, dev) -> tuple:

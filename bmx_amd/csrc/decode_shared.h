@@ -135,6 +135,43 @@ __device__ __forceinline__ void score_win_tile(const A& a, int b, int h, int j, 
   }
 }
 
+// Query and output elements of a decode call in its I/O dtype: 0 = fp32,
+// 1 = fp16, 2 = bf16 (BMX_K2B_IO_*; the model's own dtype, so a decode step
+// needs no conversion kernel).  Four consecutive elements from element idx.
+constexpr int kIoF32 = 0, kIoF16 = 1, kIoBF16 = 2;
+
+__device__ __forceinline__ float4_t load_q4(const void* base, int64_t idx, int io) {
+  if (io == kIoF32) return *reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(base) + idx);
+  const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(base) + idx);
+  if (io == kIoF16) {
+    const half2_t lo = as_h2(r.x), hi = as_h2(r.y);
+    return float4_t{(float)lo[0], (float)lo[1], (float)hi[0], (float)hi[1]};
+  }
+  return float4_t{__builtin_bit_cast(float, r.x << 16), __builtin_bit_cast(float, r.x & 0xffff0000u),
+                  __builtin_bit_cast(float, r.y << 16), __builtin_bit_cast(float, r.y & 0xffff0000u)};
+}
+
+__device__ __forceinline__ uint32_t bf16_bits(float v) {   // round to nearest even, NaN kept
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  u = (u & 0x7fffffffu) > 0x7f800000u ? (u | 0x00400000u) : u + 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ void store_o4(void* base, int64_t idx, float4_t v, int io) {
+  if (io == kIoF32) {
+    *reinterpret_cast<float4_t*>(reinterpret_cast<float*>(base) + idx) = v;
+    return;
+  }
+  uint2 w;
+  if (io == kIoF16) {
+    const half2_t lo = {(_Float16)v[0], (_Float16)v[1]}, hi = {(_Float16)v[2], (_Float16)v[3]};
+    w = make_uint2(as_u32(lo), as_u32(hi));
+  } else {
+    w = make_uint2(bf16_bits(v[0]) | (bf16_bits(v[1]) << 16), bf16_bits(v[2]) | (bf16_bits(v[3]) << 16));
+  }
+  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(base) + idx) = w;
+}
+
 // Query fragments in the RoPE pair order, fp16 high and low parts: chunk bb
 // holds B[8q + 2i + e][n] = x_n[16bb + 4q + i + 64e] (i < 4, e < 2), the order
 // in which k2b's key pairs leave the rotation and the window tiles' K order;
@@ -208,7 +245,8 @@ struct CombineKArgs {
   int balanced, n_wg;                  // balanced: sequence b has its batch_shares() share of n_wg
   const int32_t* packed_len;
   int max_packed_len;
-  float* out;
+  void* out;               // [B][h_kv][G][128] in io_dtype
+  int io_dtype;
   const uint16_t* ws_acc;   // partial records (store_partial_record)
   const float* ws_ml;
   const float* ws_win;
@@ -435,7 +473,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
     float4_t o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = (y[i] * wp + z[i] * wt) * inv;
-    *reinterpret_cast<float4_t*>(a.out + row * kD + kChunk * ch + 4 * c4) = o;
+    store_o4(a.out, row * kD + kChunk * ch + 4 * c4, o, a.io_dtype);
   }
 }
 

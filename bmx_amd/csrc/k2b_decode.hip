@@ -80,7 +80,8 @@ struct DecodeKArgs {
   int h_kv, G, max_splits, max_pages, max_packed_len, n_pool;
   int shared_bytes;    // page prefix read by every head: US, VNORM, KSCALE (multiple of 16)
   int cs_bufs;         // RoPE table buffers in LDS (groups produced in the prologue)
-  const float* q;
+  const void* q;       // [B][h_kv][G][128] in io_dtype
+  int io_dtype;
   uint16_t* ws_acc;    // [B][h_kv][G][8][max_splits][16] partial records (H8 applied; decode_shared.h)
   float* ws_ml;        // [B][h_kv][G][max_splits][2]     (running max, sum), base 2
   const uint8_t* pages;
@@ -195,11 +196,10 @@ __device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, in
   int stride;
   const int j0 = first_win_tile(split, S, stride);
   if (j0 < n_tiles) {
-    const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
+    const int64_t qrow = (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
     float4_t qraw[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      qraw[u] = *reinterpret_cast<const float4_t*>(qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2));
+    for (int u = 0; u < 8; ++u) qraw[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
     half8_t qh[4], ql[4];
     query_fragments(qraw, n < a.G ? a.qscale_rope : 0.0f, qh, ql);
     const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
@@ -315,10 +315,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     vh[bt] = *reinterpret_cast<const hvec_t*>(basis + (int64_t)(h * kD + 16 * bt + n) * R + KQ * q);
   float4_t qraw[8];   // q_n[16bb + 4q .. +3] (u = bb) and [.. + 64] (u = 4 + bb)
   {
-    const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
+    const int64_t qrow = (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      qraw[u] = *reinterpret_cast<const float4_t*>(qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2));
+    for (int u = 0; u < 8; ++u) qraw[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
   }
   const int n_win_tiles = (a.tail_cap + 15) >> 4;   // recent-window score tiles
   const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
@@ -672,12 +671,12 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     // waves of a SIMD these finish their groups first, so the tiles take no
     // time on the workgroup's critical path; wave w takes heads w and w + 4
     for (int hh = wave; hh < a.h_kv; hh += 4) {
-      const float* qrow = a.q + (((int64_t)b * a.h_kv + hh) * a.G + (n < a.G ? n : 0)) * kD;
+      const int64_t qrow = (((int64_t)b * a.h_kv + hh) * a.G + (n < a.G ? n : 0)) * kD;
       const int64_t tb = (int64_t)b * a.ts_b + (int64_t)hh * a.ts_h;
       const int64_t nb = (int64_t)b * a.nw.sb + (int64_t)hh * a.nw.sh;
       float4_t qraw2[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) qraw2[u] = *reinterpret_cast<const float4_t*>(qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2));
+      for (int u = 0; u < 8; ++u) qraw2[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
       uint2 kw[8];
       load_win_tile(a, tb, win_j0, n, q, kw, nb);
       half8_t qh2[4], ql2[4];
@@ -996,6 +995,8 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
     return fail(BMX_E_INVALID, name + ": split_tokens must be a multiple of 64");
   if (!a->q || !a->out || !a->packed_len)
     return fail(BMX_E_INVALID, name + ": q/out/packed_len must be non-NULL");
+  if (a->io_dtype < BMX_K2B_IO_F32 || a->io_dtype > BMX_K2B_IO_BF16)
+    return fail(BMX_E_INVALID, name + ": io_dtype must be BMX_K2B_IO_F32, _F16 or _BF16");
   if (!a->tail_len && (a->tail_len_value < 0 || a->tail_len_value > a->tail_cap))
     return fail(BMX_E_INVALID, name + ": with tail_len NULL, tail_len_value must be 0..tail_cap");
   if (a->n_new < 0 || (a->n_new > 0 && (a->tail_len || a->n_new > a->tail_len_value || !a->new_k ||
@@ -1033,7 +1034,7 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   k.max_packed_len = a->max_packed_len; k.n_pool = a->n_pool_pages > 0 ? a->n_pool_pages : 1;
   k.L = PageLayout::make(g.h_kv, g.rank);
   k.shared_bytes = k.L.kres;   // US, VNORM, KSCALE precede KRES
-  k.q = a->q; k.ws_acc = ws_acc; k.ws_ml = ws_ml;
+  k.q = a->q; k.io_dtype = a->io_dtype; k.ws_acc = ws_acc; k.ws_ml = ws_ml;
   k.pages = a->pages; k.page_table = a->page_table; k.packed_len = a->packed_len;
   k.basis = a->basis; k.basis_stride = a->basis_stride;
   k.qscale_rope = qscale * a->rope_scaling;
@@ -1099,7 +1100,7 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   CombineKArgs c{};
   c.h_kv = g.h_kv; c.G = g.n_q_groups;
   c.max_splits = max_splits; c.tail_cap = a->tail_cap;
-  c.out = a->out; c.ws_acc = ws_acc; c.ws_ml = ws_ml; c.ws_win = ws_win;
+  c.out = a->out; c.io_dtype = a->io_dtype; c.ws_acc = ws_acc; c.ws_ml = ws_ml; c.ws_win = ws_win;
   c.v_tail = a->v_tail;
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
   c.tail_len = a->tail_len;

@@ -247,7 +247,8 @@ struct RtnDecodeKArgs {
   int h_kv, G, max_splits, max_pages, max_packed_len, n_pool;
   int gk, gv;
   int prefix_bytes;    // scale bytes of one page (KSCALE + VSCALE), multiple of 16
-  const float* q;
+  const void* q;       // [B][h_kv][G][128] in io_dtype
+  int io_dtype;
   uint16_t* ws_acc;    // [B][h_kv][G][8][max_splits][16] partial records of the channel sums (decode_shared.h)
   float* ws_ml;        // [B][h_kv][G][max_splits][2] (running max, sum), base 2
   const uint8_t* pages;
@@ -303,11 +304,10 @@ __device__ __forceinline__ void rtn_store_partial(const RtnDecodeKArgs& a, int b
 // the lane's query in the RoPE pair order of the window tiles (decode_shared.h)
 __device__ __forceinline__ void rtn_window_fragments(const RtnDecodeKArgs& a, int b, int h, int n, int q,
                                                      half8_t qh[4], half8_t ql[4]) {
-  const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
+  const int64_t qrow = (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
   float4_t qraw[8];
 #pragma unroll
-  for (int u = 0; u < 8; ++u)
-    qraw[u] = *reinterpret_cast<const float4_t*>(qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2));
+  for (int u = 0; u < 8; ++u) qraw[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
   query_fragments(qraw, n < a.G ? a.qscale : 0.0f, qh, ql);
 }
 
@@ -368,10 +368,9 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
   // the lane's query: channels 32bb + 8q + j (bb < 4, j < 8) of query n
   float4_t qraw[8];
   {
-    const float* qrow = a.q + (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
+    const int64_t qrow = (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      qraw[u] = *reinterpret_cast<const float4_t*>(qrow + 32 * (u >> 1) + 8 * q + 4 * (u & 1));
+    for (int u = 0; u < 8; ++u) qraw[u] = load_q4(a.q, qrow + 32 * (u >> 1) + 8 * q + 4 * (u & 1), a.io_dtype);
   }
   const int n_win_tiles = (a.tail_cap + 15) >> 4;
   const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
@@ -850,6 +849,8 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: split_tokens must be a multiple of 64");
   if (!a->q || !a->out || !a->packed_len)
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: q/out/packed_len must be non-NULL");
+  if (a->io_dtype < BMX_K2B_IO_F32 || a->io_dtype > BMX_K2B_IO_BF16)
+    return rfail(BMX_E_INVALID, "bmx_rtn_decode: io_dtype must be BMX_K2B_IO_F32, _F16 or _BF16");
   if (!a->tail_len && (a->tail_len_value < 0 || a->tail_len_value > a->tail_cap))
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: with tail_len NULL, tail_len_value must be 0..tail_cap");
   if (a->n_new < 0 || (a->n_new > 0 && (a->tail_len || a->n_new > a->tail_len_value || !a->new_k ||
@@ -882,7 +883,7 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   k.gk = g.k_group; k.gv = g.v_group;
   k.L = RtnLayout::make(g.h_kv, g.k_arm, g.k_group, g.v_group);
   k.prefix_bytes = k.L.kcode;
-  k.q = a->q; k.ws_acc = ws_acc; k.ws_ml = ws_ml;
+  k.q = a->q; k.io_dtype = a->io_dtype; k.ws_acc = ws_acc; k.ws_ml = ws_ml;
   k.pages = a->pages; k.page_table = a->page_table; k.packed_len = a->packed_len;
   k.qscale = a->sm_scale * 1.4426950408889634f;
   k.k_tail = a->k_tail; k.ts_b = a->tail_stride_b; k.ts_h = a->tail_stride_h; k.ts_t = a->tail_stride_t;
@@ -906,7 +907,7 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
     return rfail(BMX_E_HIP, std::string("bmx_rtn_decode: split kernel launch: ") + hipGetErrorString(e));
   CombineKArgs c{};
   c.h_kv = g.h_kv; c.G = g.n_q_groups; c.max_splits = S; c.tail_cap = a->tail_cap;
-  c.out = a->out; c.ws_acc = ws_acc; c.ws_ml = ws_ml; c.ws_win = ws_win;
+  c.out = a->out; c.io_dtype = a->io_dtype; c.ws_acc = ws_acc; c.ws_ml = ws_ml; c.ws_win = ws_win;
   c.v_tail = a->v_tail;
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
   c.tail_len = a->tail_len;

@@ -19,6 +19,7 @@ from . import codecs as K
 HEAD_DIM = 128
 PAGE_TOKENS = 16
 _V_DTYPES = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}   # BMX_K2B_F16 / F32 / BF16
+_IO_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}  # BMX_K2B_IO_F32 / F16 / BF16
 GROUP = 64
 CODEC_PAGE = 128
 
@@ -164,7 +165,8 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
            out: torch.Tensor | None = None, split_tokens: int = 0,
            workspace: DecodeWorkspace | None = None, page_stride: int | None = None,
            new_kv=None, split_end_event: torch.cuda.Event | None = None, _capture=None) -> torch.Tensor:
-    """One decode step.  q (B, h_kv, G, 128) fp32 post-RoPE -> (B, h_kv, G, 128) fp32.
+    """One decode step.  q (B, h_kv, G, 128) post-RoPE in fp32, fp16 or bf16 (the
+    model's dtype) -> (B, h_kv, G, 128) in q's dtype.
 
     page_table (B, max_pages) int32, or None for contiguous pages: logical page
     i of sequence b at pool page b * page_stride + i (page_stride defaults to
@@ -175,8 +177,8 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
     set_window_rows."""
     B, h_kv, G, d = q.shape
     dev = q.device
-    _need(d == HEAD_DIM and q.dtype == torch.float32 and q.is_contiguous(),
-          "q must be contiguous fp32 (B, h_kv, G, 128)")
+    _need(d == HEAD_DIM and q.dtype in _IO_DTYPES and q.is_contiguous(),
+          "q must be contiguous fp32, fp16 or bf16 (B, h_kv, G, 128)")
     _need(pages.dtype == torch.uint8 and pages.shape[1] == page_bytes(h_kv, rank),
           "pages must be (n_pages, page_bytes) uint8")
     if page_table is None:
@@ -201,10 +203,13 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
           "basis16 rows must be contiguous fp16")
     if out is None:
         out = torch.empty_like(q)
+    _need(out.dtype == q.dtype and out.shape == q.shape and out.is_contiguous(),
+          "out must be contiguous and of q's shape and dtype")
     a = _lib.DecodeArgs()
     a.geom = _lib.Geom(h_kv, rank, G)
     a.batch = B
     a.q, a.out = _ptr(q), _ptr(out)
+    a.io_dtype = _IO_DTYPES[q.dtype]
     a.pages, a.page_table, a.max_pages = _ptr(pages), _ptr(page_table), stride
     a.n_pool_pages = pages.shape[0]
     _need(stride * PAGE_TOKENS >= max_packed_len, "page_table too narrow for max_packed_len")
@@ -269,14 +274,21 @@ class DecodePlan:
         self._fn = _lib.lib().bmx_k2b_decode
 
     def run(self, split_end_event: torch.cuda.Event | None = None, *, q: torch.Tensor | None = None,
-            tail_len: int | None = None, new_kv=None) -> torch.Tensor:
+            tail_len: int | None = None, new_kv=None, out: torch.Tensor | None = None) -> torch.Tensor:
         """One call.  q: a new query tensor of the bound one's shape, dtype and
-        contiguity (its pointer replaces the bound one); tail_len / new_kv: the
-        host window length and the rows given apart for this call (the plan must
-        have been bound with a host tail_len)."""
+        contiguity (its pointer replaces the bound one); out: likewise, the
+        tensor this call writes (default: the plan's own output buffer);
+        tail_len / new_kv: the host window length and the rows given apart for
+        this call (the plan must have been bound with a host tail_len)."""
         a = self.args
+        if out is not None:
+            _need(out.dtype == self.out.dtype and out.shape == self.out.shape and out.is_contiguous(),
+                  "out must match the bound output's shape, dtype and contiguity")
+        res = self.out if out is None else out
+        a.out = res.data_ptr()
         a.split_end_event = None if split_end_event is None else split_end_event.cuda_event
         if q is not None:
+            _need(q.dtype == self.out.dtype, "q must keep the bound query's dtype")
             a.q = q.data_ptr()
         if tail_len is not None or new_kv is not None:
             _need(not a.tail_len, "the plan was bound with a device tail_len")
@@ -285,7 +297,7 @@ class DecodePlan:
         rc = self._fn(ct.byref(a), self.stream)
         if rc != 0:
             _lib.check(rc, "bmx_k2b_decode")
-        return self.out
+        return res
 
 
 ROPE_NONE, ROPE_EXACT, ROPE_FP16_TABLES = 0, 1, 2

@@ -17,7 +17,7 @@ import ctypes as ct
 import torch
 
 from . import _lib
-from .k2b import DecodeWorkspace, _dense_out, _need, _ptr, _stream, _V_DTYPES, set_window_rows
+from .k2b import DecodeWorkspace, _dense_out, _IO_DTYPES, _need, _ptr, _stream, _V_DTYPES, set_window_rows
 
 HEAD_DIM = 128
 PAGE_TOKENS = 16
@@ -86,14 +86,15 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
            tail_len: torch.Tensor | None = None, tail_cap: int = 0, out: torch.Tensor | None = None,
            split_tokens: int = 0, workspace: DecodeWorkspace | None = None, new_kv=None,
            _capture=None) -> torch.Tensor:
-    """One decode step.  q (B, h_kv, G, 128) fp32 post-RoPE -> (B, h_kv, G, 128) fp32;
+    """One decode step.  q (B, h_kv, G, 128) post-RoPE in fp32, fp16 or bf16 ->
+    (B, h_kv, G, 128) in q's dtype;
     page_table (B, max_pages) int32; packed_len (B,) int32 (multiples of 128);
     k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 with tail_len valid rows (a
     device int32 (B,) tensor or a host int); new_kv as in k2b.set_window_rows."""
     B, h_kv, G, d = q.shape
     dev = q.device
-    _need(d == HEAD_DIM and q.dtype == torch.float32 and q.is_contiguous(),
-          "q must be contiguous fp32 (B, h_kv, G, 128)")
+    _need(d == HEAD_DIM and q.dtype in _IO_DTYPES and q.is_contiguous(),
+          "q must be contiguous fp32, fp16 or bf16 (B, h_kv, G, 128)")
     pb = page_bytes(h_kv, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     _need(pages.dtype == torch.uint8 and pages.shape[1] == pb, "pages must be (n_pages, page_bytes) uint8")
     _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B
@@ -102,10 +103,13 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
     _need(page_table.shape[1] * PAGE_TOKENS >= max_packed_len, "page_table too narrow for max_packed_len")
     if out is None:
         out = torch.empty_like(q)
+    _need(out.dtype == q.dtype and out.shape == q.shape and out.is_contiguous(),
+          "out must be contiguous and of q's shape and dtype")
     a = _lib.RtnDecodeArgs()
     a.geom = geom(h_kv, G, k_bits=k_bits, v_bits=v_bits, k_group=k_group, v_group=v_group, k_arm=k_arm)
     a.batch = B
     a.q, a.out = _ptr(q), _ptr(out)
+    a.io_dtype = _IO_DTYPES[q.dtype]
     a.pages, a.n_pool_pages = _ptr(pages), pages.shape[0]
     a.page_table, a.max_pages = _ptr(page_table), page_table.shape[1]
     a.packed_len, a.max_packed_len = _ptr(packed_len), int(max_packed_len)
@@ -155,10 +159,17 @@ class DecodePlan:
         self.stream = _stream(q.device)
         self._fn = _lib.lib().bmx_rtn_decode
 
-    def run(self, *, q: torch.Tensor | None = None, tail_len: int | None = None, new_kv=None) -> torch.Tensor:
-        """One call; q, tail_len and new_kv as in k2b.DecodePlan.run."""
+    def run(self, *, q: torch.Tensor | None = None, tail_len: int | None = None, new_kv=None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+        """One call; q, tail_len, new_kv and out as in k2b.DecodePlan.run."""
         a = self.args
+        if out is not None:
+            _need(out.dtype == self.out.dtype and out.shape == self.out.shape and out.is_contiguous(),
+                  "out must match the bound output's shape, dtype and contiguity")
+        res = self.out if out is None else out
+        a.out = res.data_ptr()
         if q is not None:
+            _need(q.dtype == self.out.dtype, "q must keep the bound query's dtype")
             a.q = q.data_ptr()
         if tail_len is not None or new_kv is not None:
             _need(not a.tail_len, "the plan was bound with a device tail_len")
@@ -167,7 +178,7 @@ class DecodePlan:
         rc = self._fn(ct.byref(a), self.stream)
         if rc != 0:
             _lib.check(rc, "bmx_rtn_decode")
-        return self.out
+        return res
 
 
 def dequant(pages: torch.Tensor, page_ids: torch.Tensor, *, h_kv: int, k_bits: int, v_bits: int,

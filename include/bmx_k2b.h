@@ -54,6 +54,12 @@ extern "C" {
 #define BMX_K2B_F32 1
 #define BMX_K2B_BF16 2
 
+/* Decode query / output dtype (bmx_k2b_decode_args.io_dtype and
+ * bmx_rtn_decode_args.io_dtype): zero keeps fp32. */
+#define BMX_K2B_IO_F32 0
+#define BMX_K2B_IO_F16 1
+#define BMX_K2B_IO_BF16 2
+
 #define BMX_OK 0
 #define BMX_E_INVALID 1     /* bad argument (shape, pointer, unsupported geometry) */
 #define BMX_E_WORKSPACE 2   /* workspace missing or too small */
@@ -95,8 +101,8 @@ int bmx_k2b_page_section(const bmx_k2b_geom* geom, int section, size_t* offset,
 typedef struct {
   bmx_k2b_geom geom;
   int32_t batch;
-  const float* q;             /* device [batch][h_kv][G][128] fp32, post-RoPE */
-  float* out;                 /* device [batch][h_kv][G][128] fp32 */
+  const void* q;              /* device [batch][h_kv][G][128] post-RoPE, in io_dtype */
+  void* out;                  /* device [batch][h_kv][G][128] in io_dtype */
   const uint8_t* pages;       /* device page pool; page i at pages + i*page_bytes */
   int32_t n_pool_pages;       /* pages in the pool; table entries are clamped into
                                  [0, n_pool_pages) so a bad entry cannot fault */
@@ -134,7 +140,8 @@ typedef struct {
                                  recent window is scored by the split kernel in
                                  16-token tiles (at least one workgroup per tile, up
                                  to one per CU) and summed by the merge kernel. */
-  void* workspace;            /* device scratch: split partials and window scores (fp32) */
+  void* workspace;            /* device scratch: split partials (fp16 records, fp32 max
+                                 and sum) and window scores (fp32) */
   size_t workspace_bytes;
   void* split_end_event;      /* optional hipEvent_t recorded on the stream between
                                  the split kernel and the combine kernel (timing) */
@@ -152,6 +159,9 @@ typedef struct {
   int64_t new_stride_h;
   int64_t new_stride_t;
   int32_t n_new;              /* rows given apart, 0..tail_len_value (0 = none) */
+  int32_t io_dtype;           /* BMX_K2B_IO_F32 (0), _F16 or _BF16: the dtype of q and out
+                                 (the model's: fused_decode_attention_k2b takes q in the
+                                 model dtype, triton_dequant_attention.py:1232-1246) */
 } bmx_k2b_decode_args;
 
 size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* args);

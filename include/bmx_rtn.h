@@ -110,8 +110,8 @@ int bmx_rtn_append(const bmx_rtn_append_args* args, void* stream);
 typedef struct {
   bmx_rtn_geom geom;
   int32_t batch;
-  const float* q;             /* device [batch][h_kv][G][128] fp32, post-RoPE */
-  float* out;                 /* device [batch][h_kv][G][128] fp32 */
+  const void* q;              /* device [batch][h_kv][G][128] post-RoPE, in io_dtype */
+  void* out;                  /* device [batch][h_kv][G][128] in io_dtype */
   const uint8_t* pages;
   int32_t n_pool_pages;
   const int32_t* page_table;  /* device [batch][max_pages] */
@@ -136,6 +136,7 @@ typedef struct {
   int64_t new_stride_h;
   int64_t new_stride_t;
   int32_t n_new;
+  int32_t io_dtype;           /* BMX_K2B_IO_F32 (0), _F16 or _BF16: the dtype of q and out */
 } bmx_rtn_decode_args;
 
 size_t bmx_rtn_decode_workspace_bytes(const bmx_rtn_decode_args* args);
