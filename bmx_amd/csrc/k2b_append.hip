@@ -254,12 +254,9 @@ static int afail(int code, const std::string& msg) {
 // the launch needs the larger dynamic-LDS limit set once.
 template <int R>
 static hipError_t launch_us(const AppendKArgs& k, dim3 grid, size_t lds, hipStream_t st) {
-  static size_t attr_bytes = 0;
-  if (lds > 65536 && attr_bytes < lds) {
-    hipError_t e = hipFuncSetAttribute((const void*)k2b_us_kernel<R>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (lds > 65536) {
+    const hipError_t e = bmx_ensure_dynamic_lds((const void*)k2b_us_kernel<R>, lds);
     if (e != hipSuccess) return e;
-    attr_bytes = lds;
   }
   hipLaunchKernelGGL(k2b_us_kernel<R>, grid, dim3(256), lds, st, k);
   return hipGetLastError();

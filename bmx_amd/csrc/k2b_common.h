@@ -290,5 +290,12 @@ __device__ __forceinline__ void dq_value_tile(uint2 vcd, uint2 nrm, const float 
 
 }  // namespace bmx
 
-// Error channel shared by every C-ABI entry point (defined in k2b_api.cpp).
+// Error channel shared by every C-ABI entry point (defined in k2b_api.hip).
 void bmx_set_error(const std::string& msg);
+
+// Per-device host state of the launchers (k2b_api.hip; thread-safe): the
+// current device's CU count (cached per device; 256, MI355X's, if the query
+// fails), and the dynamic-LDS limit of a kernel raised to at least bytes on
+// the current device (hipFuncSetAttribute once per device, kernel and size).
+int bmx_device_cu_count();
+hipError_t bmx_ensure_dynamic_lds(const void* kernel, size_t bytes);

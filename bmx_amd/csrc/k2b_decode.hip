@@ -714,18 +714,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
 
 using namespace bmx;
 
-static int device_cu_count() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-      n = cus;
-    else
-      n = 256;  // MI355X
-  }
-  return n;
-}
+static int device_cu_count() { return bmx_device_cu_count(); }
 
 // Workgroups per sequence: one wave of workgroups over the device's CUs (one
 // 8-wave workgroup per CU), or as many as split_tokens asks for; never more
@@ -889,13 +878,8 @@ static int fail(int code, const std::string& msg) {
 
 template <int R, int SW, bool CONTIG>
 static hipError_t launch_split_sw(const DecodeKArgs& k, dim3 grid, size_t smem, hipStream_t st) {
-  static size_t attr_bytes = 0;
-  if (attr_bytes < smem) {
-    hipError_t e = hipFuncSetAttribute((const void*)k2b_decode_split_kernel<R, SW, CONTIG>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    if (e != hipSuccess) return e;
-    attr_bytes = smem;
-  }
+  const hipError_t e = bmx_ensure_dynamic_lds((const void*)k2b_decode_split_kernel<R, SW, CONTIG>, smem);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k2b_decode_split_kernel<R, SW, CONTIG>), grid, dim3(kThreads), smem, st, k);
   return hipGetLastError();
 }
@@ -911,6 +895,8 @@ template <int R>
 static hipError_t launch_split(const DecodeKArgs& k, dim3 grid, size_t smem, hipStream_t st) {
   return k.page_table ? launch_split_c<R, false>(k, grid, smem, st) : launch_split_c<R, true>(k, grid, smem, st);
 }
+
+static int check_decode_args(const bmx_k2b_decode_args* a, const std::string& name);
 
 // The split and merge launches of one decode call over the workspace ws
 // (ws_cap bytes usable); name prefixes every error message.
@@ -961,7 +947,8 @@ static int scratch_address(void** out, std::string& err) {
 
 extern "C" int bmx_k2b_decode_noalloc(const bmx_k2b_decode_args* a, void* stream) {
   if (!a) return fail(BMX_E_INVALID, "bmx_k2b_decode_noalloc: args is NULL");
-  if (a->batch < 1) return fail(BMX_E_INVALID, "bmx_k2b_decode_noalloc: batch must be >= 1");
+  // the arguments first: an invalid geometry must not size the scratch
+  if (const int rc = check_decode_args(a, "bmx_k2b_decode_noalloc")) return rc;
   const size_t need = bmx_k2b_decode_workspace_bytes(a);
   if (need > (size_t)BMX_K2B_DECODE_SCRATCH_BYTES)
     return fail(BMX_E_WORKSPACE, "bmx_k2b_decode_noalloc: this call needs " + std::to_string(need) +
@@ -975,8 +962,9 @@ extern "C" int bmx_k2b_decode_noalloc(const bmx_k2b_decode_args* a, void* stream
   return decode_launch(a, stream, ptr, (size_t)BMX_K2B_DECODE_SCRATCH_BYTES, "bmx_k2b_decode_noalloc");
 }
 
-static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, size_t ws_cap,
-                         const std::string& name) {
+// The argument checks of a decode call (before any sizing or launch); 0 or a
+// BMX_E_INVALID code with the message set.
+static int check_decode_args(const bmx_k2b_decode_args* a, const std::string& name) {
   const bmx_k2b_geom& g = a->geom;
   if (g.h_kv < 1 || g.h_kv > kWaves) return fail(BMX_E_INVALID, name + ": h_kv must be 1..8");
   if (g.rank != 16 && g.rank != 32) return fail(BMX_E_INVALID, name + ": rank must be 16 or 32");
@@ -1014,6 +1002,13 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   if (a->tail_cap > 0 && (a->tail_stride_t % 8 != 0 || a->tail_stride_h % 8 != 0 ||
                           a->tail_stride_b % 8 != 0))
     return fail(BMX_E_INVALID, name + ": tail strides must be multiples of 8 elements");
+  return BMX_OK;
+}
+
+static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, size_t ws_cap,
+                         const std::string& name) {
+  const bmx_k2b_geom& g = a->geom;
+  if (const int rc = check_decode_args(a, name)) return rc;
   const int max_splits = choose_splits(a);
   const size_t need = ws_bytes(a, max_splits);
   if (max_splits > 8192)

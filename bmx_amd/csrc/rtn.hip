@@ -783,18 +783,7 @@ extern "C" int bmx_rtn_dequant(const bmx_rtn_dequant_args* a, void* stream) {
   return BMX_OK;
 }
 
-static int rtn_cu_count() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-      n = cus;
-    else
-      n = 256;
-  }
-  return n;
-}
+static int rtn_cu_count() { return bmx_device_cu_count(); }
 
 // as for k2b: one workgroup per CU over the batch (or split_tokens), never more
 // than the 64-token groups, and at least one per 16-token window tile (up to

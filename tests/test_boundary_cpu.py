@@ -67,6 +67,36 @@ def test_bad_geometry_is_rejected_with_message():
     assert rc != 0 and b"null pointer" in _lib.lib().bmx_last_error()
 
 
+def test_noalloc_checks_arguments_before_the_scratch_size():
+    """An invalid geometry reaches bmx_k2b_decode_noalloc's argument checks
+    (BMX_E_INVALID, the field named), not its scratch-size check, which a
+    wrapped size would fail with BMX_E_WORKSPACE; a valid call too large for
+    the static scratch is the BMX_E_WORKSPACE case (no launch in either)."""
+    E_INVALID, E_WORKSPACE = 1, 2
+    L = _lib.lib()
+    a = _lib.DecodeArgs()
+    a.geom = _lib.Geom(-1, 32, 4)
+    a.batch = 1
+    assert L.bmx_k2b_decode_noalloc(ct.byref(a), None) == E_INVALID
+    assert b"h_kv" in L.bmx_last_error()
+    a.geom = _lib.Geom(8, 32, -3)
+    assert L.bmx_k2b_decode_noalloc(ct.byref(a), None) == E_INVALID
+    assert b"n_q_groups" in L.bmx_last_error()
+    a.geom = _lib.Geom(8, 32, 4)
+    a.rope_scaling = 1.0
+    a.io_dtype = 7
+    a.q = a.out = a.packed_len = 16   # non-NULL stand-ins: the call stops at the checks
+    assert L.bmx_k2b_decode_noalloc(ct.byref(a), None) == E_INVALID
+    assert b"io_dtype" in L.bmx_last_error()
+    a.io_dtype = 0
+    a.pages = a.basis = 16
+    a.n_pool_pages = 1
+    a.batch, a.max_packed_len, a.split_tokens = 64, 1 << 20, 128   # 8192 splits of 2048 rows: 4.4 GB
+    a.max_pages = (1 << 20) // 16
+    assert L.bmx_k2b_decode_noalloc(ct.byref(a), None) == E_WORKSPACE
+    assert b"static scratch" in L.bmx_last_error()
+
+
 def test_window_rows_given_apart_rejected_on_the_host():
     """The host window length and the rows given apart are checked before any
     device work: tail_len_value within 0..tail_cap, rows given apart only with

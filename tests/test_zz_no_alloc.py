@@ -90,9 +90,53 @@ def test_noalloc_refuses_calls_above_the_scratch():
     a.batch = 64
     a.max_packed_len = 1 << 20
     a.tail_cap = 4096
+    # valid stand-ins for every pointer and size the argument checks look at
+    # (the call must be refused on the scratch size, never launched)
+    a.rope_scaling = 1.0
+    a.q = a.out = a.packed_len = a.pages = a.basis = a.k_tail = a.v_tail = 1 << 20
+    a.n_pool_pages, a.max_pages = 1, (1 << 20) // 16
+    a.tail_len = 1 << 20
     need = int(_lib.lib().bmx_k2b_decode_workspace_bytes(ct.byref(a)))
     assert need > _lib.DECODE_SCRATCH_BYTES
     rc = _lib.lib().bmx_k2b_decode_noalloc(ct.byref(a), None)
     msg = _lib.lib().bmx_last_error().decode()
     print(f"refused: status {rc}: {msg}", flush=True)
     assert rc == 2 and "static scratch" in msg   # BMX_E_WORKSPACE, before any launch
+
+
+def test_noalloc_under_graph_capture():
+    """One noalloc call captured in a HIP graph, after a warm-up call outside
+    the capture (it fetches the scratch's device address and raises the split
+    kernel's LDS limit); nothing in the call records a memset.  Each replay,
+    with a new query written eagerly and the device synchronised between
+    replays, equals the workspace entry point on the same query bit for bit."""
+    args, _, pool = _case(4096, 40, 63, 4096 // 16 + 8)
+    q = args["q"]
+    out = torch.full_like(q, float("nan"))
+    captured = {}
+    k2b.decode(**args, out=out, _capture=lambda a: captured.setdefault("a", a))
+    a = captured["a"]
+    a.workspace, a.workspace_bytes = None, 0
+    lib = _lib.lib()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        _lib.check(lib.bmx_k2b_decode_noalloc(ct.byref(a), ct.c_void_p(side.cuda_stream)), "warm-up")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = torch.cuda.current_stream()
+        _lib.check(lib.bmx_k2b_decode_noalloc(ct.byref(a), ct.c_void_p(st.cuda_stream)), "captured call")
+    torch.cuda.synchronize()
+    gen = torch.Generator().manual_seed(64)
+    for rep in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen).to(DEV))
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = k2b.decode(**args)
+        torch.cuda.synchronize()
+        same = torch.equal(out, want)
+        print(f"replay {rep}: identical to bmx_k2b_decode: {same}", flush=True)
+        assert same
+    del graph, pool
