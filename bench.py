@@ -63,8 +63,9 @@ def parse():
                     help="contig: each layer's pages in order in its own pool, no page table (the "
                          "layout PackedStreamingCache allocates); paged: one shuffled pool read "
                          "through a page table")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=16384)
-    ap.add_argument("--cpu-reps", type=int, default=7)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=0,
+                    help="committed tokens of the CPU baseline's layer call (0: the workload's own)")
+    ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fp16-comparator", action="store_true",
                     help="skip timing the dense fp16 decode at the same context")
@@ -107,15 +108,17 @@ def parse():
 
 def cpu_baseline(args, packed: int, tail: int) -> dict:
     """Time the CPU chunked path (oracle restatement of chunked_dequant_attention,
-    fp32 torch) on one layer of cpu_sample_tokens committed + tail tokens and
-    scale linearly (the chunked path is per-page work) to the full step."""
+    fp32 torch) on one layer call: by default the workload's own (all of its
+    committed tokens + its tail), so only the layer count scales it to a step;
+    with --cpu-sample-tokens, that many committed tokens, scaled linearly (the
+    chunked path is per-page work)."""
     import torch
 
     from bmx_amd import k2b, synth
     from oracle import attention as A
 
     gen = torch.Generator().manual_seed(1234)
-    S = args.cpu_sample_tokens
+    S = args.cpu_sample_tokens or packed
     k_pre = synth.k2b_keys(H_KV, S + tail, args.rank, gen)
     v = synth.values(H_KV, S + tail, gen)
     cache = A.K2bOracleCache(H_KV, D, args.rank)
@@ -145,12 +148,15 @@ def cpu_baseline(args, packed: int, tail: int) -> dict:
         times1.append(time.perf_counter() - t0)
     torch.set_num_threads(threads)
     t1 = statistics.median(times1)
-    scale = (packed + tail) / (S + tail) * args.layers
+    tok = (packed + tail) / (S + tail)
+    scale = tok * args.layers
+    what = (f"the headline layer call ({S} packed + {tail} tail tokens, h_kv 8, G 4, rank {args.rank})"
+            if S == packed else f"1 layer of {S} packed + {tail} tail tokens (h_kv 8, G 4, rank {args.rank})")
+    scaled = f"x {args.layers} layers" if S == packed else f"scaled x{tok:.2f} tokens x {args.layers} layers"
     return {"value": round(t * scale * 1e6, 1), "unit": "us/step", "cores": threads,
             "kind": "port",
-            "sample": (f"1 layer of {S} packed + {tail} tail tokens (h_kv 8, G 4, rank {args.rank}), "
-                       f"median of {args.cpu_reps} after 1 warm-up = {t * 1e3:.1f} ms/layer-call, "
-                       f"scaled x{(packed + tail) / (S + tail):.2f} tokens x {args.layers} layers"),
+            "sample": (f"{what}, median of {args.cpu_reps} after 1 warm-up = {t * 1e3:.1f} ms/layer-call, "
+                       f"{scaled}"),
             "value_1_thread": round(t1 * scale * 1e6, 1),
             "sample_1_thread": f"median of 3 = {t1 * 1e3:.1f} ms/layer-call, same scaling",
             **host}
@@ -218,24 +224,31 @@ def fp16_comparator(args, torch, dev, ctx: int, our_us: float) -> dict:
 
 
 def _cpu_model() -> str:
-    """The host CPU's model name, as lscpu reports it (else /proc/cpuinfo)."""
+    """The host CPU as lscpu reports it: every model-name field it prints
+    (a virtual machine's "Model name" can be a bare family, the "BIOS Model
+    name" the full part), the vendor and the family / model / stepping; else
+    /proc/cpuinfo's model name."""
     import subprocess
 
+    fields = {}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
         for line in out.splitlines():
-            if line.startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key in ("Model name", "BIOS Model name", "Vendor ID", "CPU family", "Model", "Stepping") and val:
+                fields.setdefault(key, val)
     except (OSError, subprocess.SubprocessError):
         pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                    fields.setdefault("cpuinfo model name", line.split(":", 1)[1].strip())
+                    break
     except OSError:
         pass
-    return "unknown"
+    return "; ".join(f"{k}: {v}" for k, v in fields.items()) or "unknown"
 
 
 def cpu_threads() -> tuple:
