@@ -409,3 +409,53 @@ def test_full_c_values_decode_matches_oracle(h_kv, G, T, rope, S, payload):
     print(f"full-C {payload} h_kv {h_kv} G {G} T {T} rope {rope} S {S} ({n_parts} partials): decode vs oracle "
           f"max_abs {err:.3e} rel {rel:.3e}; vs scores form {d_alt:.3e}", flush=True)
     assert err <= 2e-3 and rel <= 1e-2 and d_alt <= 2e-3
+
+
+@pytest.mark.parametrize("payload", ["rtn", "lloyd"])
+def test_full_c_values_decode_long_context(payload):
+    """The reference's k4_b2.5 recipe (rtn payload) and its Lloyd-payload
+    variant k4_b2.5_lq at 32,768 committed tokens + a 128-token fp16 window
+    (h_kv 8, G 4, the fp16 RoPE tables of an fp16 model): a bias of the
+    kernels' fp16 levels or scales that is invisible over a few thousand
+    tokens accumulates here.  Against the oracle's one-softmax attention over
+    the same codes at the north-star bar, and against the scores form."""
+    h_kv, G, T, S = 8, 4, 128, 32768
+    rope = k2b.ROPE_FP16_TABLES
+    pack = synthetic_pack(h_kv, 2.5, seed=34)
+    M = synthetic_keys(pack, S, seed=35)
+    gen = torch.Generator().manual_seed(36)
+    v = torch.randn(h_kv, S, 128, generator=gen)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    dp, kp, vp, k_ids, v_ids = _write(pack, h_kv, M, v, consts, shuffle_seed=7, payload=payload, v_codec="full")
+    kt = torch.randn(h_kv, T, 128, generator=gen).half()
+    vt = torch.randn(h_kv, T, 128, generator=gen).half()
+    q = torch.randn(h_kv, G, 128, generator=gen).half()
+    scale = 128 ** -0.5
+    out = spectral.decode_attention(dp, kp, k_ids, vp, v_ids, S, consts, q.to(DEV), scale,
+                                    k_win=kt.to(DEV), v_win=vt.to(DEV), apply_rope=rope, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    lloyd = _lloyd(payload)
+    L = O.Layout(pack.bits.numpy())
+    codes, scales = O.quantize(O.encode(M, pack.enc.numpy(), L), L, lloyd)
+    K_or = OC.from_matrix(torch.from_numpy(O.dequant(codes, scales, pack.dec.numpy(), L, lloyd=lloyd)).float(),
+                          h_kv)
+    cos, sin = A.rope_cos_sin(torch.tensor(consts.inv_freq), torch.arange(S))
+    cos, sin = cos.half().float(), sin.half().float()
+    V_or = _values_oracle(v, h_kv, "full")
+    ref = A.naive_dense_attention(q.reshape(h_kv * G, 1, 128).float(),
+                                  torch.cat([A.apply_rope(K_or, cos, sin), kt.float()], 1),
+                                  torch.cat([V_or, vt.float()], 1), G, scale).reshape(h_kv, G, 128)
+    o = out.cpu().double()
+    err = (o - ref.double()).abs().max().item()
+    rel = ((o - ref.double()).norm() / ref.double().norm()).item()
+    Vb = torch.empty(h_kv, S, 128, dtype=torch.float16, device=DEV)
+    Sb = torch.empty(h_kv, G, S, dtype=torch.float32, device=DEV)
+    spectral.dequant(dp, kp, k_ids, vp, v_ids, S, consts, apply_rope=rope, dtype=torch.float16,
+                     out=(None, Vb), q=q.to(DEV), scores=Sb)
+    sw = torch.cat([Sb, (q.float() @ kt.float().transpose(1, 2)).to(DEV)], -1) * scale
+    Vw = torch.cat([Vb.float(), vt.float().to(DEV)], 1)
+    alt = (torch.softmax(sw, -1) @ Vw).cpu().double()
+    d_alt = (o - alt).abs().max().item()
+    print(f"long full-C {payload} S {S} T {T}: decode vs oracle max_abs {err:.3e} rel {rel:.3e}; "
+          f"vs scores form {d_alt:.3e}", flush=True)
+    assert err <= 2e-3 and rel <= 1e-2 and d_alt <= 2e-3
