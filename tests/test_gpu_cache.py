@@ -283,23 +283,24 @@ def test_packed_generate_matches_streaming(recipe, seq, dtype, tmp_path):
     assert torch.equal(out, ref)
 
 
-def test_packed_vs_streaming_logit_probe_16k():
+@pytest.mark.parametrize("ctx,N", [(16384, 32), (65536, 64)])
+def test_packed_vs_streaming_logit_probe(ctx, N):
     """The reference's teacher-forced packed-vs-streaming logit probe
-    (scripts/profile_decode_ab.py:316-439) at 16384 tokens: both caches
-    prefilled on the same prompt, then 32 steps each fed the streaming cache's
-    greedy token; per step the max |logit delta| is recorded and the flip gate
-    applied (no flip with the streaming top-2 gap above that step's delta, at
-    most N // 8 flips).  Model: fp16, Llama geometry at reduced width (2 layers,
-    8 query / 2 KV heads, d 128), key projections rank 8 plus 1% noise."""
+    (scripts/profile_decode_ab.py:316-439), at 16384 tokens for 32 steps and at
+    the acceptance run's 65536 tokens for 64 steps: both caches prefilled on
+    the same prompt, then N steps each fed the streaming cache's greedy token;
+    per step the max |logit delta| is recorded and the flip gate applied (no
+    flip with the streaming top-2 gap above that step's delta, at most N // 8
+    flips).  Model: fp16, Llama geometry at reduced width (2 layers, 8 query /
+    2 KV heads, d 128), key projections rank 8 plus 1% noise."""
     from transformers import LlamaConfig, LlamaForCausalLM
 
     from bmx_amd.cache import StreamingQuantizedCache
     from oracle import attention as A
 
-    ctx, N = 16384, 32
     cfg = LlamaConfig(vocab_size=4096, hidden_size=1024, intermediate_size=2048, num_hidden_layers=2,
                       num_attention_heads=8, num_key_value_heads=2, head_dim=128,
-                      max_position_embeddings=32768, rope_theta=500000.0, initializer_range=0.1)
+                      max_position_embeddings=2 * ctx, rope_theta=500000.0, initializer_range=0.1)
     torch.manual_seed(0)
     model = LlamaForCausalLM(cfg).eval()
     gen = torch.Generator().manual_seed(4)
@@ -317,6 +318,7 @@ def test_packed_vs_streaming_logit_probe_16k():
     for kind, c in caches.items():
         with c.attach(model), torch.no_grad():
             logits[kind] = model(ids, past_key_values=c, use_cache=True, logits_to_keep=1).logits[:, -1].float()
+        print(f"  {kind} cache prefilled with {ctx} tokens", flush=True)
     flips = hard = 0
     envelope = 0.0
     for step in range(N):
@@ -329,6 +331,8 @@ def test_packed_vs_streaming_logit_probe_16k():
         f, h = A.argmax_flip(logits["packed"][0].cpu(), logits["streaming"][0].cpu())
         envelope = max(envelope, (logits["packed"] - logits["streaming"]).abs().max().item())
         flips, hard = flips + f, hard + h
+        if step % 16 == 15:
+            print(f"  step {step + 1}/{N}: flips {flips} (hard {hard}), envelope {envelope:.4f}", flush=True)
     print(f"logit probe ctx {ctx} N {N}: flips {flips} (hard {hard}), max_abs envelope {envelope:.4f}, "
           f"committed {caches['packed'].layers[0]._committed_S_q}", flush=True)
     assert caches["packed"].layers[0]._committed_S_q == caches["streaming"].layers[0]._committed_S_q
