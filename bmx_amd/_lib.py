@@ -60,6 +60,7 @@ class DecodeArgs(ct.Structure):
         ("new_stride_t", ct.c_int64),
         ("n_new", ct.c_int32),
         ("io_dtype", ct.c_int32),
+        ("tail_dtype", ct.c_int32),
     ]
 
 
@@ -161,6 +162,7 @@ class RtnDecodeArgs(ct.Structure):
         ("new_stride_t", ct.c_int64),
         ("n_new", ct.c_int32),
         ("io_dtype", ct.c_int32),
+        ("tail_dtype", ct.c_int32),
     ]
 
 
@@ -246,7 +248,7 @@ class SpectralMergeArgs(ct.Structure):
                 ("k_win", ct.c_void_p), ("v_win", ct.c_void_p), ("win_len", ct.c_int32),
                 ("sm_scale", ct.c_float), ("out", ct.c_void_p), ("out_dtype", ct.c_int32),
                 ("v_sign_bits", ct.c_uint32 * 4), ("win_stride_h", ct.c_int64),
-                ("v_codec", ct.c_int32), ("v_sign_bits_c", ct.c_uint32 * 32)]
+                ("v_codec", ct.c_int32), ("v_sign_bits_c", ct.c_uint32 * 32), ("win_dtype", ct.c_int32)]
 
 
 EXPORTS = {

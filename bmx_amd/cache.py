@@ -190,10 +190,11 @@ class PackedStreamingLayer(DynamicLayer):
         self._k_pre_parts: list = []
         self._k_pre_rows = 0
         self._k_pre_offset = 0
-        # recent window: rows [0, _T) of fixed buffers (1, h_kv, recent_window + 128, d),
-        # fp16 for fp16/bf16 models (the decode kernel's operand), else the model
-        # dtype; _pending: the newest row's (key, value) when the decode call has
-        # still to store it (the product decode path only)
+        # recent window: rows [0, _T) of fixed buffers (1, h_kv, recent_window + 128, d)
+        # in the model dtype (fp16 and bf16 windows are the decode kernels' operands
+        # as they are; an fp32 window goes in converted); _pending: the newest row's
+        # (key, value) when the decode call has still to store it (the product
+        # decode path only)
         self._win_k: torch.Tensor | None = None
         self._win_v: torch.Tensor | None = None
         self._T = 0
@@ -264,7 +265,7 @@ class PackedStreamingLayer(DynamicLayer):
     # -------------------------------------------------------------- window
 
     def _window_dtype(self) -> torch.dtype:
-        return torch.float16 if self.dtype in (torch.float16, torch.bfloat16) else self.dtype
+        return self.dtype   # the tail in the model dtype (packed_streaming.py:849)
 
     def _ensure_window(self, device, committed_after: int) -> None:
         """The window buffers, made on first use (committed_after: the committed
@@ -294,9 +295,9 @@ class PackedStreamingLayer(DynamicLayer):
 
     def _fold_ok(self, key_states: torch.Tensor) -> bool:
         """A one-token step may leave its row to the decode call: the product's
-        fused decode paths, an fp16 window, on a HIP device."""
+        fused decode paths, an fp16 or bf16 window, on a HIP device."""
         return (self._path in ("k2b", "rtn") and key_states.is_cuda
-                and self._win_k.dtype == torch.float16)
+                and self._win_k.dtype in (torch.float16, torch.bfloat16))
 
     def _reserve(self, n_pages: int, device) -> None:
         """Grow the pool (doubling, contents kept) to hold n_pages pages."""
@@ -390,7 +391,8 @@ class PackedStreamingLayer(DynamicLayer):
         self._land_pending()
         if new_S_q == self._committed_S_q:   # nothing commits: the rows join the window
             if n == 1 and self._fold_ok(key_states):
-                self._pending = (key_states.to(torch.float16), value_states.to(torch.float16))
+                wdt = self._win_k.dtype   # the model's rows as they are (no conversion kernel)
+                self._pending = (key_states.to(wdt), value_states.to(wdt))
             else:
                 self._win_k[:, :, T0:T0 + n].copy_(key_states)
                 self._win_v[:, :, T0:T0 + n].copy_(value_states)
@@ -483,7 +485,7 @@ class PackedStreamingLayer(DynamicLayer):
         qm = q.reshape(1, h, G, d)
         if not qm.is_contiguous():
             qm = qm.contiguous()
-        if self._win_k.dtype != torch.float16:   # a model in fp32: the window goes in as fp16
+        if self._win_k.dtype not in (torch.float16, torch.bfloat16):   # an fp32 model: the window goes in as fp16
             self._land_pending()
             kt = self._win_k[:, :, :T].half().contiguous()
             vt = self._win_v[:, :, :T].half().contiguous()
@@ -541,9 +543,9 @@ class PackedStreamingLayer(DynamicLayer):
         qg = q.reshape(h, G, d).contiguous()
         kw = vw = None
         wk, wv = self.window()
-        if wk is not None and wk.shape[2]:   # fp16 buffers are read in place (rows contiguous)
+        if wk is not None and wk.shape[2]:   # fp16 / bf16 buffers are read in place (rows contiguous)
             kw, vw = wk.squeeze(0), wv.squeeze(0)
-            if kw.dtype != torch.float16:
+            if kw.dtype not in (torch.float16, torch.bfloat16):
                 kw, vw = kw.half().contiguous(), vw.half().contiguous()
         kt = self._ktable[: P // spectral.GROUP] if P else None
         vt = self._table[0, : P // k2b.PAGE_TOKENS].contiguous() if P else None
@@ -771,9 +773,6 @@ class StreamingQuantizedLayer(PackedStreamingLayer):
         super().__init__(k_spec, v_spec, model_config, recent_window, pack_v=pack_v, pack_k=pack_k, pack=pack)
         self._slab_k: torch.Tensor | None = None
         self._slab_v: torch.Tensor | None = None
-
-    def _window_dtype(self) -> torch.dtype:
-        return self.dtype   # prefix and tail in the cache dtype (streaming.py:583-646)
 
     def _fold_ok(self, key_states: torch.Tensor) -> bool:
         return False

@@ -85,6 +85,8 @@ __device__ __forceinline__ int fresh_row(const WinNew& w, int t) {
 // q = lane >> 4 holds channels 16bb + 4q + i and + 64, interleaved: the K order
 // of the query fragments), B = the query fragments split into fp16 high and low
 // parts (q = hi + lo to 2^-22 relative), so the scores carry the fp32 query.
+// A bf16 window (tail_bf16: a bf16 model's rows as the model made them) goes
+// on the bf16 MFMA, its query split into bf16 high and low parts (2^-17).
 // Base-2 scores go to ws_win[b][h][g][t]; the merge does the window's softmax
 // and value sum.  Rows past tail_cap read row 0 of the head and are not stored.
 // ---------------------------------------------------------------------------
@@ -114,6 +116,11 @@ __device__ __forceinline__ void score_win_tile(const A& a, int b, int h, int j, 
       *reinterpret_cast<uint2*>(dst + 16 * bb + 64) = kw[2 * bb + 1];
     }
   }
+  // the window dtype as a wave-uniform (scalar) value: a branch on it is a
+  // scalar branch.  Read through a pointer it would be a vector value, and the
+  // two MFMA forms would be selected by the exec mask, where the form not
+  // taken still writes its result (an MFMA runs whatever the exec mask).
+  const bool bf16 = __builtin_amdgcn_readfirstlane(a.tail_bf16) != 0;
   float4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
@@ -121,8 +128,15 @@ __device__ __forceinline__ void score_win_tile(const A& a, int b, int h, int j, 
     union { uint4 u; half8_t v; } ka;
     ka.u = make_uint4(__builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u), __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u),
                       __builtin_amdgcn_perm(hi.y, lo.y, 0x05040100u), __builtin_amdgcn_perm(hi.y, lo.y, 0x07060302u));
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, qh[bb], s, 0, 0, 0);
-    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, ql[bb], s, 0, 0, 0);
+    if (bf16) {
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka.v),
+                                                  __builtin_bit_cast(bf16x8_t, qh[bb]), s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka.v),
+                                                  __builtin_bit_cast(bf16x8_t, ql[bb]), s, 0, 0, 0);
+    } else {
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, qh[bb], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, ql[bb], s, 0, 0, 0);
+    }
   }
   // lane: query n, tokens 16j + 4q + i
   if (n < a.G) {
@@ -191,6 +205,27 @@ __device__ __forceinline__ void query_fragments(const float4_t qraw[8], float sc
       }
 }
 
+// The same fragments for the window tiles: fp16 high and low parts, or bf16
+// ones (bit patterns in the half8_t registers) for a bf16 window.
+__device__ __forceinline__ void window_fragments(const float4_t qraw[8], float sc, bool bf16, half8_t qh[4],
+                                                 half8_t ql[4]) {
+  if (!bf16) {
+    query_fragments(qraw, sc, qh, ql);
+    return;
+  }
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float x = qraw[4 * e + bb][i] * sc;
+        const uint32_t hb = bf16_bits(x);
+        qh[bb][2 * i + e] = __builtin_bit_cast(_Float16, (uint16_t)hb);
+        ql[bb][2 * i + e] = __builtin_bit_cast(_Float16, (uint16_t)bf16_bits(x - __uint_as_float(hb << 16)));
+      }
+}
+
 // ---------------------------------------------------------------------------
 // Split partial records.  A (row, split) partial is its 128 channel sums
 // divided by its softmax sum l, in fp16 (a weighted mean of value-sized
@@ -252,6 +287,7 @@ struct CombineKArgs {
   const float* ws_win;
   const uint16_t* v_tail;
   int64_t ts_b, ts_h, ts_t;
+  int tail_bf16;             // window (and rows given apart) in bf16, else fp16
   const int32_t* tail_len;   // NULL: every sequence's window holds nw.T rows
   WinNew nw;
   uint32_t v_sign_bits[4];   // rotated: bit c set <=> value channel c carries Hadamard sign -1
@@ -392,8 +428,11 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
         if (r % a.G == 0 && elem(t0, u) < T && fresh_row(a.nw, elem(t0, u)) >= 0)
           *reinterpret_cast<uint2*>(a.nw.v_dst + (vb - a.v_tail) + (int64_t)elem(t0, u) * a.ts_t) = wv[u];
         const float w = elem(t0, u) < T ? __builtin_amdgcn_exp2f(ws[u] - mnew) : 0.f;
-        const float4_t vf = {half_bits_to_float(wv[u].x & 0xffff), half_bits_to_float(wv[u].x >> 16),
-                             half_bits_to_float(wv[u].y & 0xffff), half_bits_to_float(wv[u].y >> 16)};
+        const float4_t vf = a.tail_bf16
+            ? float4_t{__uint_as_float(wv[u].x << 16), __uint_as_float(wv[u].x & 0xffff0000u),
+                       __uint_as_float(wv[u].y << 16), __uint_as_float(wv[u].y & 0xffff0000u)}
+            : float4_t{half_bits_to_float(wv[u].x & 0xffff), half_bits_to_float(wv[u].x >> 16),
+                       half_bits_to_float(wv[u].y & 0xffff), half_bits_to_float(wv[u].y >> 16)};
         xt += w * vf;
         lt += w;
       }

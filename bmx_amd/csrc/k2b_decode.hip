@@ -99,9 +99,10 @@ struct DecodeKArgs {
   uint32_t level_hi[4];   // fp16 bits of the value levels as used by the MFMA:
                           // hi_c = kappa * codebook_c + mu (+ < 1e-6 relative)
   float level_mu;         // mu (the merge divides by kappa)
-  // recent window: fp16 post-RoPE keys [b * ts_b + h * ts_h + t * ts_t][128]
+  // recent window: fp16 (or bf16: tail_bf16) post-RoPE keys [b * ts_b + h * ts_h + t * ts_t][128]
   const uint16_t* k_tail;
   int64_t ts_b, ts_h, ts_t;
+  int tail_bf16;
   WinNew nw;           // the window's newest rows given apart (decode_shared.h)
   int tail_cap;
   float win_rescale;      // 1 / rope_scaling: window keys carry the RoPE scaling
@@ -201,7 +202,7 @@ __device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, in
 #pragma unroll
     for (int u = 0; u < 8; ++u) qraw[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
     half8_t qh[4], ql[4];
-    query_fragments(qraw, n < a.G ? a.qscale_rope : 0.0f, qh, ql);
+    window_fragments(qraw, n < a.G ? a.qscale_rope : 0.0f, a.tail_bf16, qh, ql);
     const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
     for (int j = j0; j < n_tiles; j += stride) {
       uint2 kw[8];
@@ -680,7 +681,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
       uint2 kw[8];
       load_win_tile(a, tb, win_j0, n, q, kw, nb);
       half8_t qh2[4], ql2[4];
-      query_fragments(qraw2, (n < a.G) ? a.qscale_rope : 0.0f, qh2, ql2);
+      window_fragments(qraw2, (n < a.G) ? a.qscale_rope : 0.0f, a.tail_bf16, qh2, ql2);
       score_win_tile(a, b, hh, win_j0, n, q, kw, qh2, ql2, tb);
       for (int j = win_j0 + win_stride; j < n_win_tiles; j += win_stride) {
         load_win_tile(a, tb, j, n, q, kw, nb);
@@ -985,6 +986,8 @@ static int check_decode_args(const bmx_k2b_decode_args* a, const std::string& na
     return fail(BMX_E_INVALID, name + ": q/out/packed_len must be non-NULL");
   if (a->io_dtype < BMX_K2B_IO_F32 || a->io_dtype > BMX_K2B_IO_BF16)
     return fail(BMX_E_INVALID, name + ": io_dtype must be BMX_K2B_IO_F32, _F16 or _BF16");
+  if (a->tail_dtype != BMX_K2B_TAIL_F16 && a->tail_dtype != BMX_K2B_TAIL_BF16)
+    return fail(BMX_E_INVALID, name + ": tail_dtype must be BMX_K2B_TAIL_F16 or _BF16");
   if (!a->tail_len && (a->tail_len_value < 0 || a->tail_len_value > a->tail_cap))
     return fail(BMX_E_INVALID, name + ": with tail_len NULL, tail_len_value must be 0..tail_cap");
   if (a->n_new < 0 || (a->n_new > 0 && (a->tail_len || a->n_new > a->tail_len_value || !a->new_k ||
@@ -1035,6 +1038,7 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   k.qscale_rope = qscale * a->rope_scaling;
   k.k_tail = a->k_tail;
   k.ts_b = a->tail_stride_b; k.ts_h = a->tail_stride_h; k.ts_t = a->tail_stride_t;
+  k.tail_bf16 = a->tail_dtype == BMX_K2B_TAIL_BF16;
   k.tail_cap = a->tail_cap;
   k.win_rescale = 1.0f / a->rope_scaling;
   k.ws_win = ws_win;
@@ -1098,6 +1102,7 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   c.out = a->out; c.io_dtype = a->io_dtype; c.ws_acc = ws_acc; c.ws_ml = ws_ml; c.ws_win = ws_win;
   c.v_tail = a->v_tail;
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
+  c.tail_bf16 = k.tail_bf16;
   c.tail_len = a->tail_len;
   c.nw = k.nw;
   for (int j = 0; j < 4; ++j) c.v_sign_bits[j] = a->v_sign_bits[j];

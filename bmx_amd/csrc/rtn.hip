@@ -256,9 +256,10 @@ struct RtnDecodeKArgs {
   const int32_t* packed_len;
   RtnLayout L;
   float qscale;        // sm_scale * log2(e)
-  // recent window (decode_shared.h)
+  // recent window (decode_shared.h), fp16 or bf16 (tail_bf16)
   const uint16_t* k_tail;
   int64_t ts_b, ts_h, ts_t;
+  int tail_bf16;
   WinNew nw;           // the window's newest rows given apart (decode_shared.h)
   int tail_cap;
   float win_rescale;   // 1: the window keys are scored with qscale
@@ -308,7 +309,7 @@ __device__ __forceinline__ void rtn_window_fragments(const RtnDecodeKArgs& a, in
   float4_t qraw[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) qraw[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
-  query_fragments(qraw, n < a.G ? a.qscale : 0.0f, qh, ql);
+  window_fragments(qraw, n < a.G ? a.qscale : 0.0f, a.tail_bf16, qh, ql);
 }
 
 // A workgroup with no packed tokens: its window tiles and an empty partial.
@@ -840,6 +841,8 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: q/out/packed_len must be non-NULL");
   if (a->io_dtype < BMX_K2B_IO_F32 || a->io_dtype > BMX_K2B_IO_BF16)
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: io_dtype must be BMX_K2B_IO_F32, _F16 or _BF16");
+  if (a->tail_dtype != BMX_K2B_TAIL_F16 && a->tail_dtype != BMX_K2B_TAIL_BF16)
+    return rfail(BMX_E_INVALID, "bmx_rtn_decode: tail_dtype must be BMX_K2B_TAIL_F16 or _BF16");
   if (!a->tail_len && (a->tail_len_value < 0 || a->tail_len_value > a->tail_cap))
     return rfail(BMX_E_INVALID, "bmx_rtn_decode: with tail_len NULL, tail_len_value must be 0..tail_cap");
   if (a->n_new < 0 || (a->n_new > 0 && (a->tail_len || a->n_new > a->tail_len_value || !a->new_k ||
@@ -876,6 +879,7 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   k.pages = a->pages; k.page_table = a->page_table; k.packed_len = a->packed_len;
   k.qscale = a->sm_scale * 1.4426950408889634f;
   k.k_tail = a->k_tail; k.ts_b = a->tail_stride_b; k.ts_h = a->tail_stride_h; k.ts_t = a->tail_stride_t;
+  k.tail_bf16 = a->tail_dtype == BMX_K2B_TAIL_BF16;
   k.tail_cap = a->tail_cap; k.win_rescale = 1.0f; k.ws_win = ws_win;
   k.nw.k = a->new_k; k.nw.v = a->new_v;
   k.nw.sb = a->new_stride_b; k.nw.sh = a->new_stride_h; k.nw.st = a->new_stride_t;
@@ -899,6 +903,7 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   c.out = a->out; c.io_dtype = a->io_dtype; c.ws_acc = ws_acc; c.ws_ml = ws_ml; c.ws_win = ws_win;
   c.v_tail = a->v_tail;
   c.ts_b = a->tail_stride_b; c.ts_h = a->tail_stride_h; c.ts_t = a->tail_stride_t;
+  c.tail_bf16 = k.tail_bf16;
   c.tail_len = a->tail_len;
   c.nw = k.nw;
   c.packed_scale = 1.0f;

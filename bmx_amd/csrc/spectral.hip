@@ -1604,6 +1604,7 @@ constexpr int kSpMaxWin = 4096;
 
 struct SpMergeKArgs {
   int h_kv, G, n_groups, q_dtype, win_len, out_dtype;
+  int win_bf16;     // k_win / v_win in bf16, else fp16
   int64_t win_sh;   // elements between heads in k_win / v_win
   const float* partials;
   const void* q;
@@ -1662,6 +1663,10 @@ __global__ __launch_bounds__(256) void spectral_merge_kernel(const SpMergeKArgs 
   const int P = a.n_groups, T = a.win_len;
   const uint16_t* kbase = a.k_win + (int64_t)h * a.win_sh;
   const uint16_t* vbase = a.v_win + (int64_t)h * a.win_sh;
+  const bool wbf = a.win_bf16;
+  auto wcvt = [wbf](uint32_t bits) {   // a window element's 16 low bits as fp32
+    return wbf ? __uint_as_float(bits << 16) : half_bits_to_float(bits & 0xffffu);
+  };
   // ---- loads: the query, the first batch of partials, the first window pass
   float qv = 0.f;
   if (tid < kD) qv = sp_load(a.q, row * kD + tid, a.q_dtype);
@@ -1705,8 +1710,8 @@ __global__ __launch_bounds__(256) void spectral_merge_kernel(const SpMergeKArgs 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int d = 64 * half + 8 * i + 2 * e;
-        acc = fmaf(s_q[d], half_bits_to_float(w4[e] & 0xffffu), acc);
-        acc = fmaf(s_q[d + 1], half_bits_to_float(w4[e] >> 16), acc);
+        acc = fmaf(s_q[d], wcvt(w4[e] & 0xffffu), acc);
+        acc = fmaf(s_q[d + 1], wcvt(w4[e] >> 16), acc);
       }
     }
     acc += __shfl_xor(acc, 1);
@@ -1756,8 +1761,8 @@ __global__ __launch_bounds__(256) void spectral_merge_kernel(const SpMergeKArgs 
       if (t < T) {
         const float w = __expf(s_s[t] - M);
         if (c4 == 0) L += w;
-        const float4_t v = {half_bits_to_float(vr[k].x & 0xffffu), half_bits_to_float(vr[k].x >> 16),
-                            half_bits_to_float(vr[k].y & 0xffffu), half_bits_to_float(vr[k].y >> 16)};
+        const float4_t v = {wcvt(vr[k].x & 0xffffu), wcvt(vr[k].x >> 16), wcvt(vr[k].y & 0xffffu),
+                            wcvt(vr[k].y >> 16)};
         W = f4_fma(w, v, W);
       }
     }
@@ -2021,7 +2026,10 @@ extern "C" int32_t bmx_spectral_merge(const bmx_spectral_merge_args* a, void* st
     return sp_fail(fn, "k_win must be 16-byte aligned and win_stride_h 0 or a multiple of 8 >= 128 win_len");
   if (!v_codec_ok(a->v_codec, a->h_kv))
     return sp_fail(fn, "v_codec must be BMX_SPECTRAL_V_PERHEAD, or BMX_SPECTRAL_V_FULL with h_kv 1, 2, 4 or 8");
+  if (a->win_dtype != BMX_K2B_TAIL_F16 && a->win_dtype != BMX_K2B_TAIL_BF16)
+    return sp_fail(fn, "win_dtype must be BMX_K2B_TAIL_F16 or _BF16");
   SpMergeKArgs k{};
+  k.win_bf16 = a->win_dtype == BMX_K2B_TAIL_BF16;
   k.h_kv = a->h_kv; k.G = a->n_q_groups; k.n_groups = a->n_groups; k.q_dtype = a->q_dtype;
   k.win_len = a->win_len; k.out_dtype = a->out_dtype; k.partials = a->partials; k.q = a->q;
   k.k_win = a->k_win; k.v_win = a->v_win; k.sm_scale = a->sm_scale; k.out = a->out;

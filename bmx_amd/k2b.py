@@ -20,6 +20,7 @@ HEAD_DIM = 128
 PAGE_TOKENS = 16
 _V_DTYPES = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}   # BMX_K2B_F16 / F32 / BF16
 _IO_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}  # BMX_K2B_IO_F32 / F16 / BF16
+_TAIL_DTYPES = {torch.float16: 0, torch.bfloat16: 1}                   # BMX_K2B_TAIL_F16 / BF16
 GROUP = 64
 CODEC_PAGE = 128
 
@@ -65,10 +66,11 @@ def set_window_rows(a, B: int, h_kv: int, tail_len, tail_cap: int, new_kv=None) 
     """Fill the window-length and new-row fields of decode args a (k2b or RTN).
 
     tail_len: a device int32 (B,) tensor, or a host int (every sequence's window
-    length, no device read), or None (0).  new_kv: (k, v) fp16 (B, h_kv, n, 128)
+    length, no device read), or None (0).  new_kv: (k, v) (B, h_kv, n, 128)
     post-RoPE keys and values of the window's newest n rows (rows tail_len - n
-    .. tail_len - 1), attended from there and copied into the window buffers by
-    the decode call; needs a host tail_len."""
+    .. tail_len - 1) in the window's dtype (a.tail_dtype), attended from there
+    and copied into the window buffers by the decode call; needs a host
+    tail_len."""
     if isinstance(tail_len, torch.Tensor):
         _need(tail_len.dtype == torch.int32 and tail_len.numel() == B and tail_len.is_cuda,
               "tail_len must be a device int32[B] tensor or a host int")
@@ -83,9 +85,10 @@ def set_window_rows(a, B: int, h_kv: int, tail_len, tail_cap: int, new_kv=None) 
         return
     k, v = new_kv
     _need(not isinstance(tail_len, torch.Tensor), "rows given apart need a host tail_len")
-    _need(k.dim() == 4 and k.shape == v.shape and k.dtype == torch.float16 and v.dtype == torch.float16
+    wdt = torch.bfloat16 if a.tail_dtype == _TAIL_DTYPES[torch.bfloat16] else torch.float16
+    _need(k.dim() == 4 and k.shape == v.shape and k.dtype == wdt and v.dtype == wdt
           and k.shape[0] == B and k.shape[1] == h_kv and k.shape[3] == HEAD_DIM,
-          "new_kv: fp16 (B, h_kv, n, 128) keys and values")
+          f"new_kv: (B, h_kv, n, 128) keys and values in the window's dtype ({wdt})")
     # strides of size-1 dimensions are never used: taken as 0
     sk = tuple(0 if n == 1 else st for n, st in zip(k.shape[:3], k.stride()[:3]))
     sv = tuple(0 if n == 1 else st for n, st in zip(v.shape[:3], v.stride()[:3]))
@@ -172,7 +175,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
     i of sequence b at pool page b * page_stride + i (page_stride defaults to
     max_packed_len / 16); packed_len (B,) int32 committed tokens (multiples of
     128, <= max_packed_len); basis16 (B, C, rank) or (C, rank) fp16;
-    k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 post-RoPE recent window with
+    k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 or bf16 post-RoPE recent window with
     tail_len valid rows (a device int32 (B,) tensor or a host int); new_kv as in
     set_window_rows."""
     B, h_kv, G, d = q.shape
@@ -223,10 +226,12 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
     if tail_cap > 0:
         _need(k_tail is not None and v_tail is not None and k_tail.shape == v_tail.shape
               and k_tail.stride() == v_tail.stride(), "k_tail/v_tail must share shape and strides")
-        _need(k_tail.dtype == torch.float16 and k_tail.dim() == 4 and k_tail.shape[0] == B
-              and k_tail.shape[1] == h_kv and k_tail.shape[2] >= tail_cap and k_tail.stride(3) == 1,
-              "k_tail must be fp16 (B, h_kv, >=tail_cap, 128) with contiguous last dim")
+        _need(k_tail.dtype in _TAIL_DTYPES and v_tail.dtype == k_tail.dtype and k_tail.dim() == 4
+              and k_tail.shape[0] == B and k_tail.shape[1] == h_kv and k_tail.shape[2] >= tail_cap
+              and k_tail.stride(3) == 1,
+              "k_tail/v_tail must be fp16 or bf16 (B, h_kv, >=tail_cap, 128) with contiguous last dim")
         a.k_tail, a.v_tail = _ptr(k_tail), _ptr(v_tail)
+        a.tail_dtype = _TAIL_DTYPES[k_tail.dtype]
         a.tail_stride_b, a.tail_stride_h, a.tail_stride_t = k_tail.stride(0), k_tail.stride(1), k_tail.stride(2)
     a.tail_cap = int(tail_cap)
     set_window_rows(a, B, h_kv, tail_len, tail_cap, new_kv)

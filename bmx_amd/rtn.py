@@ -17,7 +17,8 @@ import ctypes as ct
 import torch
 
 from . import _lib
-from .k2b import DecodeWorkspace, _dense_out, _IO_DTYPES, _need, _ptr, _stream, _V_DTYPES, set_window_rows
+from .k2b import (DecodeWorkspace, _dense_out, _IO_DTYPES, _need, _ptr, _stream, _TAIL_DTYPES, _V_DTYPES,
+                  set_window_rows)
 
 HEAD_DIM = 128
 PAGE_TOKENS = 16
@@ -89,7 +90,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
     """One decode step.  q (B, h_kv, G, 128) post-RoPE in fp32, fp16 or bf16 ->
     (B, h_kv, G, 128) in q's dtype;
     page_table (B, max_pages) int32; packed_len (B,) int32 (multiples of 128);
-    k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 with tail_len valid rows (a
+    k_tail/v_tail (B, h_kv, >=tail_cap, 128) fp16 or bf16 with tail_len valid rows (a
     device int32 (B,) tensor or a host int); new_kv as in k2b.set_window_rows."""
     B, h_kv, G, d = q.shape
     dev = q.device
@@ -117,10 +118,12 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor, packe
     if tail_cap > 0:
         _need(k_tail is not None and v_tail is not None and k_tail.shape == v_tail.shape
               and k_tail.stride() == v_tail.stride(), "k_tail/v_tail must share shape and strides")
-        _need(k_tail.dtype == torch.float16 and k_tail.dim() == 4 and k_tail.shape[0] == B
-              and k_tail.shape[1] == h_kv and k_tail.shape[2] >= tail_cap and k_tail.stride(3) == 1,
-              "k_tail must be fp16 (B, h_kv, >=tail_cap, 128) with contiguous last dim")
+        _need(k_tail.dtype in _TAIL_DTYPES and v_tail.dtype == k_tail.dtype and k_tail.dim() == 4
+              and k_tail.shape[0] == B and k_tail.shape[1] == h_kv and k_tail.shape[2] >= tail_cap
+              and k_tail.stride(3) == 1,
+              "k_tail/v_tail must be fp16 or bf16 (B, h_kv, >=tail_cap, 128) with contiguous last dim")
         a.k_tail, a.v_tail = _ptr(k_tail), _ptr(v_tail)
+        a.tail_dtype = _TAIL_DTYPES[k_tail.dtype]
         a.tail_stride_b, a.tail_stride_h, a.tail_stride_t = k_tail.stride(0), k_tail.stride(1), k_tail.stride(2)
     a.tail_cap = int(tail_cap)
     set_window_rows(a, B, h_kv, tail_len, tail_cap, new_kv)

@@ -479,7 +479,7 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
                      v_table: torch.Tensor, n_tokens: int, consts: CodecConsts, q: torch.Tensor, sm_scale: float,
                      k_win: torch.Tensor | None = None, v_win: torch.Tensor | None = None,
                      apply_rope: int = 2, out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """One decode step over n_tokens committed tokens and the fp16 window:
+    """One decode step over n_tokens committed tokens and the fp16 (or bf16) window:
     q (h_kv, G, 128) post-RoPE -> (h_kv, G, 128) in out_dtype (q's by default).  The dequant
     kernel's partial form gives every 128-token block's (m, l, P.V); the merge
     kernel scores the window and folds everything by the split softmax's
@@ -498,10 +498,11 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
                 dtype=torch.float16, q=q, partials=pt, sm_scale=sm_scale)
     T = 0 if k_win is None else k_win.shape[1]
     if T:
-        _need(k_win.dtype == torch.float16 and v_win.dtype == torch.float16 and tuple(k_win.shape) == (h, T, d)
+        _need(k_win.dtype in (torch.float16, torch.bfloat16) and v_win.dtype == k_win.dtype
+              and tuple(k_win.shape) == (h, T, d)
               and v_win.shape == k_win.shape and k_win.stride() == v_win.stride() and k_win.stride(2) == 1
               and k_win.stride(1) == d and k_win.stride(0) % 8 == 0 and k_win.data_ptr() % 16 == 0,
-              "window keys and values: fp16 (h_kv, T, 128) with contiguous rows, 16-byte aligned")
+              "window keys and values: fp16 or bf16 (h_kv, T, 128) with contiguous rows, 16-byte aligned")
     out_dtype = q.dtype if out_dtype is None else out_dtype
     _need(out_dtype in _V_DTYPES, "out_dtype must be fp16, bf16 or fp32")
     out = torch.empty(h, G, d, dtype=out_dtype, device=q.device)
@@ -511,6 +512,7 @@ def decode_attention(dp: DevicePack, k_pages: torch.Tensor, k_table: torch.Tenso
     a.partials, a.q, a.q_dtype = _ptr(pt), _ptr(q), _V_DTYPES[q.dtype]
     a.k_win, a.v_win, a.win_len = (_ptr(k_win), _ptr(v_win), T) if T else (None, None, 0)
     a.win_stride_h = k_win.stride(0) if T else 0
+    a.win_dtype = 1 if T and k_win.dtype == torch.bfloat16 else 0   # BMX_K2B_TAIL_BF16 / _F16
     a.sm_scale, a.out, a.out_dtype = float(sm_scale), _ptr(out), _V_DTYPES[out_dtype]
     a.v_sign_bits[:] = consts.sign_bits
     if dp is not None:

@@ -60,6 +60,13 @@ extern "C" {
 #define BMX_K2B_IO_F16 1
 #define BMX_K2B_IO_BF16 2
 
+/* Recent-window dtype (bmx_k2b_decode_args.tail_dtype and
+ * bmx_rtn_decode_args.tail_dtype), for k_tail, v_tail, new_k and new_v: zero
+ * keeps fp16; bf16 holds a bf16 model's rows as the model made them (the
+ * reference keeps the tail in the model dtype, packed_streaming.py:849). */
+#define BMX_K2B_TAIL_F16 0
+#define BMX_K2B_TAIL_BF16 1
+
 #define BMX_OK 0
 #define BMX_E_INVALID 1     /* bad argument (shape, pointer, unsupported geometry) */
 #define BMX_E_WORKSPACE 2   /* workspace missing or too small */
@@ -122,8 +129,8 @@ typedef struct {
   float sm_scale;             /* softmax scale (HF module.scaling) */
   float codebook[4];          /* 2-bit Lloyd levels, ascending */
   uint32_t v_sign_bits[4];    /* bit c set <=> V Hadamard sign of channel c is -1 */
-  const uint16_t* k_tail;     /* device fp16 post-RoPE recent-window keys */
-  const uint16_t* v_tail;     /* device fp16 recent-window values */
+  const uint16_t* k_tail;     /* device fp16 (tail_dtype) post-RoPE recent-window keys */
+  const uint16_t* v_tail;     /* device fp16 (tail_dtype) recent-window values */
   int64_t tail_stride_b;      /* element strides of k_tail/v_tail (dim 128 contiguous) */
   int64_t tail_stride_h;
   int64_t tail_stride_t;
@@ -162,6 +169,8 @@ typedef struct {
   int32_t io_dtype;           /* BMX_K2B_IO_F32 (0), _F16 or _BF16: the dtype of q and out
                                  (the model's: fused_decode_attention_k2b takes q in the
                                  model dtype, triton_dequant_attention.py:1232-1246) */
+  int32_t tail_dtype;         /* BMX_K2B_TAIL_F16 (0) or _BF16: the dtype of the window
+                                 rows (k_tail, v_tail, new_k, new_v) */
 } bmx_k2b_decode_args;
 
 size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* args);

@@ -119,7 +119,7 @@ typedef struct {
   const int32_t* packed_len;  /* device [batch], multiples of 128 */
   int32_t max_packed_len;
   float sm_scale;
-  const uint16_t* k_tail;     /* device fp16 post-RoPE recent-window keys */
+  const uint16_t* k_tail;     /* device fp16 (tail_dtype) post-RoPE recent-window keys */
   const uint16_t* v_tail;
   int64_t tail_stride_b;
   int64_t tail_stride_h;
@@ -137,6 +137,7 @@ typedef struct {
   int64_t new_stride_t;
   int32_t n_new;
   int32_t io_dtype;           /* BMX_K2B_IO_F32 (0), _F16 or _BF16: the dtype of q and out */
+  int32_t tail_dtype;         /* BMX_K2B_TAIL_F16 (0) or _BF16: the window rows' dtype */
 } bmx_rtn_decode_args;
 
 size_t bmx_rtn_decode_workspace_bytes(const bmx_rtn_decode_args* args);

@@ -178,9 +178,9 @@ typedef struct bmx_spectral_merge_args {
   const float* partials;       /* [h_kv][n_q_groups][n_groups][130] fp32 */
   const void* q;               /* [h_kv][n_q_groups][128] post-RoPE, dtype q_dtype */
   int32_t q_dtype;
-  const uint16_t* k_win;       /* fp16 post-RoPE window keys, row t of head h at h win_stride_h + 128 t,
+  const uint16_t* k_win;       /* fp16 (win_dtype) post-RoPE window keys, row t of head h at h win_stride_h + 128 t,
                                   16-byte aligned */
-  const uint16_t* v_win;       /* fp16 window values, same indexing */
+  const uint16_t* v_win;       /* fp16 (win_dtype) window values, same indexing */
   int32_t win_len;             /* 0..4096 */
   float sm_scale;
   void* out;                   /* [h_kv][n_q_groups][128], dtype out_dtype */
@@ -191,6 +191,7 @@ typedef struct bmx_spectral_merge_args {
                                   BMX_SPECTRAL_V_FULL (head h: signs 128 h .. of v_sign_bits_c,
                                   scale 1/C) */
   uint32_t v_sign_bits_c[32];
+  int32_t win_dtype;           /* BMX_K2B_TAIL_F16 (0) or _BF16: the dtype of k_win and v_win */
 } bmx_spectral_merge_args;
 
 int64_t bmx_spectral_v_page_bytes(int32_t h_kv);

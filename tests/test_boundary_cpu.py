@@ -125,6 +125,8 @@ def test_window_rows_given_apart_rejected_on_the_host():
         assert fn(ct.byref(a), None) != 0 and b"n_new" in lib.bmx_last_error()
         a.tail_len, a.new_stride_t = None, 12
         assert fn(ct.byref(a), None) != 0 and b"multiples of 8" in lib.bmx_last_error()
+        a.new_stride_t, a.tail_dtype = 128, 2
+        assert fn(ct.byref(a), None) != 0 and b"tail_dtype" in lib.bmx_last_error()
     # the Python wrapper's own checks
     a = _lib.DecodeArgs()
     a.tail_cap = 128
@@ -133,8 +135,14 @@ def test_window_rows_given_apart_rejected_on_the_host():
     k = torch.zeros(1, 8, 2, 128, dtype=torch.float16)
     with pytest.raises(ValueError, match="more rows than the window"):
         k2b.set_window_rows(a, 1, 8, 1, 128, (k, k))
-    with pytest.raises(ValueError, match="fp16"):
+    with pytest.raises(ValueError, match="window's dtype"):
         k2b.set_window_rows(a, 1, 8, 4, 128, (k.float(), k.float()))
+    a.tail_dtype = 1   # a bf16 window takes bf16 rows only
+    with pytest.raises(ValueError, match="window's dtype"):
+        k2b.set_window_rows(a, 1, 8, 4, 128, (k, k))
+    k2b.set_window_rows(a, 1, 8, 4, 128, (k.bfloat16(), k.bfloat16()))
+    assert a.n_new == 2
+    a.tail_dtype = 0
     with pytest.raises(ValueError, match="same strides"):
         k2b.set_window_rows(a, 1, 8, 4, 128, (k, k.transpose(1, 2).contiguous().transpose(1, 2)))
     k2b.set_window_rows(a, 1, 8, 4, 128, (k, k))

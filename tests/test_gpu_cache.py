@@ -592,3 +592,71 @@ def test_two_block_prefill_through_the_model():
     print(f"tiny Llama two-block prefill: logits max|err| {err:.3e} of max|logit| {scale:.3f}", flush=True)
     assert err <= 2e-3 * max(scale, 1.0)
     assert bool((got.argmax(-1) == ref.argmax(-1)).all())
+
+
+def test_bf16_window_keeps_the_model_rows():
+    """A bf16 model's recent window stays in bf16 (the reference keeps the
+    tail in the model dtype, packed_streaming.py:849, and its decode reads it
+    as fp32, triton_dequant_attention.py:353): window rows beyond fp16's range
+    reach the prefill's dense keys and the decode kernels as the model made
+    them.  600 tokens whose last 100 key and value rows are scaled by 2^17
+    (|x| up to ~6e5), a causal prefill over them, then two decode steps with
+    large newest rows (each folded into the decode call), all against explicit
+    fp32 attention over the oracle's pages and the bf16 rows."""
+    from transformers import LlamaConfig
+
+    from bmx_amd import synth
+    from bmx_amd.cache import PackedStreamingLayer
+    from oracle import attention as A
+    from oracle_cache import OracleLayer
+
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                      num_hidden_layers=32, rope_theta=500000.0)
+    h_kv, G, d, W, N = 8, 4, 128, 128, 600
+    gen = torch.Generator().manual_seed(92)
+    k_spec, v_spec = spec_pair("k2b_ph", rank=16)
+    prod = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=W)
+    orac = OracleLayer(k_spec, v_spec, cfg, recent_window=W)
+    orac.v_fp16 = True
+    k_pre = synth.k2b_keys(h_kv, N + 2, 16, gen)
+    cos, sin = A.rope_cos_sin(prod._inv_freq, torch.arange(N + 2))
+    k_post = A.apply_rope(k_pre.float(), cos, sin)
+    v = synth.values(h_kv, N + 2, gen).float()
+    k_post[:, N - 100:] *= 2.0 ** 17
+    v[:, N - 100:] *= 2.0 ** 17
+    k_post, v = k_post.bfloat16(), v.bfloat16()
+    assert k_post.float().abs().max() > 65504 and v.float().abs().max() > 65504
+
+    def feed(lo, hi):
+        for lay, dev in ((prod, "cuda"), (orac, "cpu")):
+            lay.stash_pre_rope(k_pre[:, lo:hi].transpose(0, 1).unsqueeze(0).to(dev))
+            lay.update(k_post[:, lo:hi].unsqueeze(0).to(dev), v[:, lo:hi].unsqueeze(0).to(dev))
+
+    feed(0, N)
+    P = prod._committed_S_q
+    assert P > 0 and prod._win_k.dtype == torch.bfloat16
+    q = (1e-5 * torch.randn(h_kv * G, N, d, generator=gen)).bfloat16()
+    K, V = orac._kv(torch.float32)
+    assert torch.equal(K[:, P:], k_post[:, P:N].float()) and torch.equal(V[:, P:], v[:, P:N].float())
+    ref = _explicit_attention(q, K, V, G, d ** -0.5, 0)
+    out = prod.attend(q.cuda(), d ** -0.5, is_causal=True)
+    torch.cuda.synchronize()
+    err = (out.float().cpu() - ref).abs().max().item()
+    top = ref.abs().max().item()
+    print(f"bf16 prefill over rows up to {k_post.float().abs().max().item():.3g}: max_abs {err:.3e} "
+          f"(max |out| {top:.3g})", flush=True)
+    assert torch.isfinite(out).all() and err <= 1e-2 * top
+    for step in range(2):
+        feed(N + step, N + step + 1)
+        K, V = orac._kv(torch.float32)
+        qd = (1e-5 * torch.randn(h_kv * G, 1, d, generator=gen)).bfloat16()
+        ref = _explicit_attention(qd, K, V, G, d ** -0.5, N + step)
+        out = prod.attend(qd.cuda(), d ** -0.5)
+        torch.cuda.synchronize()
+        err = (out.float().cpu() - ref).abs().max().item()
+        top = ref.abs().max().item()
+        print(f"bf16 decode step {step}: max_abs {err:.3e} (max |out| {top:.3g}), rows folded "
+              f"{prod.n_rows_folded}", flush=True)
+        assert out.dtype == torch.bfloat16 and torch.isfinite(out).all() and err <= 1e-2 * top
+    assert prod.n_rows_folded == 2
+    assert torch.equal(prod.window()[0].cpu(), orac.window()[0])

@@ -101,3 +101,81 @@ def test_rtn_decode_model_dtype_query(dt):
     torch.cuda.synchronize()
     assert out_d.dtype == dt
     assert torch.equal(out_d, out_f.to(dt)), f"{dt}: max |diff| {(out_d.float() - out_f).abs().max().item():.3e}"
+
+
+def _bf16_exact(x):
+    """Rows exactly representable in both bf16 and fp16 (bf16's 8 bits of
+    mantissa, fp16's range)."""
+    return x.float().bfloat16().half()
+
+
+@pytest.mark.parametrize("S,T", [(1024, 40), (128, 100)])
+@pytest.mark.parametrize("fold", [False, True])
+def test_k2b_bf16_window_equals_fp16_window(fold, S, T):
+    """The same window rows given as bf16 (tail_dtype BF16: bf16 MFMA with a
+    bf16 hi/lo query, bf16 values in the merge) and as fp16: the outputs agree
+    to the query split's precision; rows given apart land in the window
+    buffer bit for bit.  128 packed tokens and 100 window rows: most window
+    tiles are scored by workgroups with no packed tokens (a separate code
+    path, whose dtype branch must be a scalar one)."""
+    gen = torch.Generator().manual_seed(24)
+    h_kv, rank, G = 8, 32, 4
+    _, _, _, consts, pool, seq, kt, vt, table = _k2b_case(gen, h_kv, rank, S, T)
+    kt, vt = _bf16_exact(kt), _bf16_exact(vt)
+    q = torch.randn(1, h_kv, G, 128, generator=gen).to(DEV)
+    ln = torch.tensor([S], dtype=torch.int32, device=DEV)
+    outs = {}
+    for dt in (torch.float16, torch.bfloat16):
+        k_w, v_w = kt.to(dt).clone(), vt.to(dt).clone()
+        new_kv = None
+        if fold:   # the newest 2 rows given apart, their buffer rows zeroed
+            new_kv = (k_w[:, :, T - 2:].clone(), v_w[:, :, T - 2:].clone())
+            k_w[:, :, T - 2:] = 0
+            v_w[:, :, T - 2:] = 0
+        outs[dt] = k2b.decode(q, pool.pages, table, ln, S, seq.basis16, consts, 128 ** -0.5, rank=rank,
+                              k_tail=k_w, v_tail=v_w, tail_len=T, tail_cap=T, new_kv=new_kv)
+        torch.cuda.synchronize()
+        assert torch.equal(k_w.float(), kt.float()) and torch.equal(v_w.float(), vt.float())
+    err = (outs[torch.bfloat16] - outs[torch.float16]).abs().max().item()
+    assert err <= 2e-5 * outs[torch.float16].abs().max().item(), err
+
+
+@pytest.mark.parametrize("S,T", [(512, 40), (128, 100)])
+def test_rtn_bf16_window_equals_fp16_window(S, T):
+    gen = torch.Generator().manual_seed(25)
+    h_kv, G = 8, 4
+    codec = dict(k_bits=4, v_bits=4, k_group=32, v_group=32)
+    k = torch.randn(h_kv, S + T, 128, generator=gen).half()
+    v = torch.randn(h_kv, S + T, 128, generator=gen).half()
+    pool = rtn.PagePool(S // 16 + 2, h_kv, DEV, **codec)
+    ids = pool.alloc(S // 16)
+    rtn.append(k[:, :S].to(DEV), v[:, :S].to(DEV), pool.pages, torch.tensor(ids, dtype=torch.int32, device=DEV),
+               **codec)
+    table = torch.tensor([ids], dtype=torch.int32, device=DEV)
+    ln = torch.tensor([S], dtype=torch.int32, device=DEV)
+    kt = _bf16_exact(k[:, S:]).unsqueeze(0).to(DEV).contiguous()
+    vt = _bf16_exact(v[:, S:]).unsqueeze(0).to(DEV).contiguous()
+    q = torch.randn(1, h_kv, G, 128, generator=gen).to(DEV)
+    outs = [rtn.decode(q, pool.pages, table, ln, S, 128 ** -0.5, k_tail=kt.to(dt), v_tail=vt.to(dt), tail_len=T,
+                       tail_cap=T, **codec) for dt in (torch.float16, torch.bfloat16)]
+    torch.cuda.synchronize()
+    assert (outs[1] - outs[0]).abs().max().item() <= 2e-5 * outs[0].abs().max().item()
+
+
+def test_spectral_merge_bf16_window_equals_fp16_window():
+    """The spectral decode's merge reads a bf16 window (win_dtype BF16) as the
+    fp16 one: the window alone (no committed token), the same rows in both."""
+    from bmx_amd import spectral
+    gen = torch.Generator().manual_seed(26)
+    h_kv, G, T = 8, 4, 100
+    kw = _bf16_exact(torch.randn(h_kv, T, 128, generator=gen)).to(DEV)
+    vw = _bf16_exact(torch.randn(h_kv, T, 128, generator=gen)).to(DEV)
+    q = torch.randn(h_kv, G, 128, generator=gen).half().to(DEV)
+    consts = k2b.CodecConsts.make(v_seed=0)
+    outs = [spectral.decode_attention(None, None, None, None, None, 0, consts, q, 128 ** -0.5, k_win=kw.to(dt),
+                                      v_win=vw.to(dt), out_dtype=torch.float32)
+            for dt in (torch.float16, torch.bfloat16)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    ref = torch.softmax((q.float() @ kw.float().transpose(1, 2)) * 128 ** -0.5, -1) @ vw.float()
+    assert (outs[0] - ref).abs().max().item() <= 1e-5
