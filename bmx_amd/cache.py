@@ -200,6 +200,10 @@ class PackedStreamingLayer(DynamicLayer):
         self._T = 0
         self._pending: tuple | None = None
         self.n_rows_folded = 0    # newest rows the decode call stored (no copy of their own)
+        # set while PackedStreamingCache.attach has the packed attention read this
+        # layer: the one reader that takes a newest row given apart (any other
+        # reader of the window lands it first, window())
+        self.packed_reader = False
         self._plan = None
         self._plan_key = None
         self._empty_pool: torch.Tensor | None = None
@@ -295,8 +299,10 @@ class PackedStreamingLayer(DynamicLayer):
 
     def _fold_ok(self, key_states: torch.Tensor) -> bool:
         """A one-token step may leave its row to the decode call: the product's
-        fused decode paths, an fp16 or bf16 window, on a HIP device."""
-        return (self._path in ("k2b", "rtn") and key_states.is_cuda
+        fused decode paths, an fp16 or bf16 window, on a HIP device, with the
+        packed attention as the layer's reader (the tensors update() returns
+        are then read by nothing else)."""
+        return (self.packed_reader and self._path in ("k2b", "rtn") and key_states.is_cuda
                 and self._win_k.dtype in (torch.float16, torch.bfloat16))
 
     def _reserve(self, n_pages: int, device) -> None:
@@ -458,6 +464,61 @@ class PackedStreamingLayer(DynamicLayer):
 
     def get_seq_length(self) -> int:
         return self._committed_S_q + self._T
+
+    # -------------------------------------------------------------- DynamicLayer mutators
+    # DynamicLayer's own versions slice self.keys / self.values, which here are
+    # views of the window alone: they would leave the committed pages, the
+    # window length and the pre-RoPE stash out of step.
+
+    def crop(self, tokens_to_remove: int) -> None:
+        """Drop the newest tokens (DynamicLayer.crop: a negative count removes
+        that many, a positive one is the length to keep).  Only window rows can
+        go: committed codec pages are not taken back."""
+        n = self.get_seq_length()
+        drop = -tokens_to_remove if tokens_to_remove <= 0 else max(n - tokens_to_remove, 0)
+        if drop == 0:
+            return
+        if drop > self._T:
+            raise NotImplementedError(f"crop of {drop} tokens reaches into the committed codec pages "
+                                      f"({self._T} window rows)")
+        self._land_pending()
+        keep = n - drop
+        if self._k_pre_rows > keep - self._k_pre_offset:   # stashed pre-RoPE rows past the new end
+            raw = torch.cat(self._k_pre_parts, dim=1) if len(self._k_pre_parts) > 1 else self._k_pre_parts[0]
+            raw = raw[:, : max(keep - self._k_pre_offset, 0)]
+            self._k_pre_parts = [raw] if raw.shape[1] else []
+            self._k_pre_rows = raw.shape[1]
+        self._T -= drop
+        self._set_bpe(keep)
+        self._publish()
+
+    def _one_sequence(self, what: str, ok: bool) -> None:
+        if not ok:
+            raise NotImplementedError(f"{what}: the packed cache serves batch size 1")
+
+    def reorder_cache(self, beam_idx: torch.LongTensor) -> None:
+        self._one_sequence("reorder_cache", beam_idx.numel() == 1 and int(beam_idx.reshape(-1)[0]) == 0)
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        idx = torch.as_tensor(indices).reshape(-1)
+        self._one_sequence("batch_select_indices", idx.numel() == 1 and int(idx[0]) == 0)
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        self._one_sequence("batch_repeat_interleave", repeats == 1)
+
+    def offload(self):
+        raise NotImplementedError("the packed cache's page pool stays on the device")
+
+    def prefetch(self):
+        raise NotImplementedError("the packed cache's page pool stays on the device")
+
+    def reset(self) -> None:
+        """Forget every token (the layer object stays, as DynamicLayer.reset
+        keeps it): pages, window and stash are released."""
+        reader = self.packed_reader
+        self.__init__(self.k_spec, self.v_spec, self.model_config, recent_window=self.recent_window,
+                      pack=self._pack)
+        self.packed_reader = reader
 
     # -------------------------------------------------------------- read side
 
@@ -721,6 +782,7 @@ class PackedStreamingCache(Cache):
             self.layers.append(self._make_layer())
         for i, mlayer in enumerate(decoder):
             mlayer.self_attn._packed_layer = self.layers[i]
+            self.layers[i].packed_reader = True
             layer_ref = weakref.proxy(self.layers[i])
 
             def k_hook(module, inp, out, layer=layer_ref):
@@ -733,6 +795,11 @@ class PackedStreamingCache(Cache):
         for h in self._handles:
             h.remove()
         self._handles = []
+        for layer in self.layers:
+            if isinstance(layer, PackedStreamingLayer):
+                layer.packed_reader = False
+                if layer._win_k is not None:
+                    layer._land_pending()
         if self._model is not None:
             for mlayer in resolve_decoder_layers(self._model):
                 if hasattr(mlayer.self_attn, "_packed_layer"):

@@ -161,3 +161,81 @@ def test_lower_right_causal_mask_detection():
     assert not _is_lower_right_causal((j <= i + (n_kv - n_q))[None, None].float(), n_q, n_kv)
     assert not _is_lower_right_causal((j <= i + (n_kv - n_q))[None, None].expand(2, 1, n_q, n_kv), n_q, n_kv)
     assert not _is_lower_right_causal(None, n_q, n_kv)
+
+
+def test_attach_marks_the_packed_reader():
+    """Only an attached layer leaves a step's newest row to the decode call:
+    attach() marks its layers as read by the packed attention, detach() clears
+    the mark (a detached layer's update() writes every row itself)."""
+    from transformers import LlamaForCausalLM
+
+    model = LlamaForCausalLM(tiny_config()).eval()
+    cache = PackedStreamingCache(model.config, *spec_pair("k2b_ph", rank=16), recent_window=32)
+    cache.attach(model)
+    assert all(layer.packed_reader for layer in cache.layers)
+    cache.detach()
+    assert not any(layer.packed_reader for layer in cache.layers)
+
+
+def _window_layer(n_rows, recent_window=64):
+    """A k2b layer on the CPU fed n_rows tokens (fewer than its first commit
+    needs: the rows stay in the window, no kernel runs)."""
+    from bmx_amd.cache import PackedStreamingLayer
+
+    cfg = tiny_config()
+    layer = PackedStreamingLayer(*spec_pair("k2b_ph", rank=16), cfg, recent_window=recent_window)
+    gen = torch.Generator().manual_seed(3)
+    k = torch.randn(1, 2, n_rows, 128, generator=gen)
+    v = torch.randn(1, 2, n_rows, 128, generator=gen)
+    layer.stash_pre_rope(torch.randn(1, n_rows, 2 * 128, generator=gen))
+    layer.update(k, v)
+    return layer, k, v
+
+
+def test_crop_drops_window_rows_and_their_stash():
+    """DynamicLayer.crop semantics on the packed layer: -n drops the newest n
+    rows, a positive count is the length to keep; the window length, the
+    returned keys/values, the bits-per-entry and the pre-RoPE stash follow."""
+    layer, k, v = _window_layer(100)
+    assert layer.get_seq_length() == 100 and layer._committed_S_q == 0
+    layer.crop(-10)
+    assert layer.get_seq_length() == 90 and layer._k_pre_rows == 90
+    assert torch.equal(layer.keys, k[:, :, :90]) and torch.equal(layer.values, v[:, :, :90])
+    layer.crop(80)
+    assert layer.get_seq_length() == 80 and layer._k_pre_rows == 80 and layer.keys.shape[2] == 80
+    layer.crop(200)   # longer than the cache: nothing to drop
+    layer.crop(0)
+    assert layer.get_seq_length() == 80
+    # new rows continue from the cropped length
+    k2 = torch.randn(1, 2, 5, 128)
+    layer.update(k2, k2)
+    assert layer.get_seq_length() == 85 and torch.equal(layer.keys[:, :, 80:], k2)
+
+
+def test_crop_into_committed_pages_and_batch_mutators_refused():
+    layer, _, _ = _window_layer(100)
+    layer._committed_S_q, layer._T = 128, 100   # as if a codec page had committed
+    with pytest.raises(NotImplementedError, match="committed"):
+        layer.crop(-101)
+    for call in (lambda: layer.reorder_cache(torch.tensor([1, 0])),
+                 lambda: layer.batch_select_indices(torch.tensor([0, 1])),
+                 lambda: layer.batch_repeat_interleave(2)):
+        with pytest.raises(NotImplementedError, match="batch size 1"):
+            call()
+    layer.reorder_cache(torch.tensor([0]))   # the one sequence in place: nothing to do
+    layer.batch_select_indices(torch.tensor([0]))
+    layer.batch_repeat_interleave(1)
+    with pytest.raises(NotImplementedError, match="device"):
+        layer.offload()
+
+
+def test_reset_forgets_every_token():
+    layer, _, _ = _window_layer(40)
+    layer.packed_reader = True
+    layer.reset()
+    assert layer.get_seq_length() == 0 and layer._k_pre_rows == 0 and layer._win_k is None
+    assert layer.packed_reader and not layer.is_initialized
+    k = torch.randn(1, 2, 3, 128)
+    layer.stash_pre_rope(torch.randn(1, 3, 256))
+    layer.update(k, k)
+    assert layer.get_seq_length() == 3

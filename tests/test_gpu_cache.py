@@ -616,6 +616,7 @@ def test_bf16_window_keeps_the_model_rows():
     gen = torch.Generator().manual_seed(92)
     k_spec, v_spec = spec_pair("k2b_ph", rank=16)
     prod = PackedStreamingLayer(k_spec, v_spec, cfg, recent_window=W)
+    prod.packed_reader = True   # as attach() sets it: the decode call takes the newest row
     orac = OracleLayer(k_spec, v_spec, cfg, recent_window=W)
     orac.v_fp16 = True
     k_pre = synth.k2b_keys(h_kv, N + 2, 16, gen)
