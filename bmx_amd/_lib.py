@@ -19,7 +19,9 @@ SECTIONS = ("us", "vnorm", "kscale", "kres", "vcode")
 
 
 class Geom(ct.Structure):
-    _fields_ = [("h_kv", ct.c_int32), ("rank", ct.c_int32), ("n_q_groups", ct.c_int32)]
+    # head_dim / k_group / k_bits 0: the recipe's 128 / 64 / 3
+    _fields_ = [("h_kv", ct.c_int32), ("rank", ct.c_int32), ("n_q_groups", ct.c_int32),
+                ("head_dim", ct.c_int32), ("k_group", ct.c_int32), ("k_bits", ct.c_int32)]
 
 
 class DecodeArgs(ct.Structure):
@@ -300,16 +302,16 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed (status {rc}): {msg}")
 
 
-def page_bytes(h_kv: int, rank: int) -> int:
-    g = Geom(h_kv, rank, 1)
+def page_bytes(h_kv: int, rank: int, *, head_dim: int = 128, group: int = 64, k_bits: int = 3) -> int:
+    g = Geom(h_kv, rank, 1, head_dim, group, k_bits)
     n = lib().bmx_k2b_page_bytes(ct.byref(g))
     if n == 0:
         raise RuntimeError(lib().bmx_last_error().decode())
     return int(n)
 
 
-def page_sections(h_kv: int, rank: int) -> dict:
-    g = Geom(h_kv, rank, 1)
+def page_sections(h_kv: int, rank: int, *, head_dim: int = 128, group: int = 64, k_bits: int = 3) -> dict:
+    g = Geom(h_kv, rank, 1, head_dim, group, k_bits)
     out = {}
     for i, name in enumerate(SECTIONS):
         off, sz = ct.c_size_t(), ct.c_size_t()

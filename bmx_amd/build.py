@@ -36,6 +36,7 @@ SOURCES = {
     "k2b_dequant.hip": ["-ffp-contract=off"],
     "rtn.hip": ["-ffp-contract=off"],
     "spectral.hip": ["-ffp-contract=off"],
+    "k2b_general.hip": ["-ffp-contract=off"],
 }
 
 

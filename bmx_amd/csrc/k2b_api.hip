@@ -2,6 +2,7 @@
 // page geometry queries.
 
 #include "k2b_common.h"
+#include "k2b_general.h"
 
 #include <mutex>
 
@@ -58,31 +59,52 @@ hipError_t bmx_ensure_dynamic_lds(const void* kernel, size_t bytes) {
   return hipSuccess;
 }
 
-static bool geom_ok(const bmx_k2b_geom* g) {
-  return g && g->h_kv >= 1 && g->h_kv <= 16 && (g->rank == 16 || g->rank == 32);
+// The geometry's page sections: (offset, size) of US, VNORM, KSCALE, KRES,
+// VCODE and the page size; an error message when the geometry is not taken.
+static std::string page_sections(const bmx_k2b_geom* g, int32_t starts[6], int32_t sizes[5]) {
+  if (!g) return "geometry is NULL";
+  const bmx::Geo geo = bmx::Geo::from(*g);
+  const std::string why = geo.check();
+  if (!why.empty()) return why;
+  if (!geo.general) {
+    const bmx::PageLayout L = bmx::PageLayout::make(geo.h, geo.R);
+    const int32_t st[6] = {L.us, L.vnorm, L.kscale, L.kres, L.vcode, L.bytes};
+    for (int i = 0; i < 6; ++i) starts[i] = st[i];
+    for (int i = 0; i < 5; ++i) sizes[i] = st[i + 1] - st[i];
+    return "";
+  }
+  const bmx::GenLayout L = bmx::GenLayout::of(geo);
+  const int32_t st[6] = {L.us, L.vnorm, L.kscale, L.kres, L.vcode, L.bytes};
+  const int32_t sz[5] = {bmx::kPT * geo.R * 2, geo.h * bmx::kPT * 2, L.per_slot * 2,
+                         geo.h * bmx::kPT * (geo.d / 2), geo.h * 4 * geo.d};
+  for (int i = 0; i < 6; ++i) starts[i] = st[i];
+  for (int i = 0; i < 5; ++i) sizes[i] = sz[i];
+  return "";
 }
 
 extern "C" size_t bmx_k2b_page_bytes(const bmx_k2b_geom* g) {
-  if (!geom_ok(g)) {
-    bmx_set_error("bmx_k2b_page_bytes: unsupported geometry (h_kv 1..16, rank 16|32)");
+  int32_t starts[6], sizes[5];
+  const std::string why = page_sections(g, starts, sizes);
+  if (!why.empty()) {
+    bmx_set_error("bmx_k2b_page_bytes: unsupported geometry: " + why);
     return 0;
   }
-  return (size_t)bmx::PageLayout::make(g->h_kv, g->rank).bytes;
+  return (size_t)starts[5];
 }
 
 extern "C" int bmx_k2b_page_section(const bmx_k2b_geom* g, int section, size_t* offset,
                                     size_t* bytes) {
-  if (!geom_ok(g) || !offset || !bytes) {
-    bmx_set_error("bmx_k2b_page_section: bad geometry or NULL output");
+  int32_t starts[6], sizes[5];
+  const std::string why = page_sections(g, starts, sizes);
+  if (!why.empty() || !offset || !bytes) {
+    bmx_set_error("bmx_k2b_page_section: " + (why.empty() ? std::string("NULL output") : why));
     return BMX_E_INVALID;
   }
-  const bmx::PageLayout L = bmx::PageLayout::make(g->h_kv, g->rank);
-  const int32_t starts[6] = {L.us, L.vnorm, L.kscale, L.kres, L.vcode, L.bytes};
   if (section < 0 || section > 4) {
     bmx_set_error("bmx_k2b_page_section: section must be 0..4");
     return BMX_E_INVALID;
   }
   *offset = (size_t)starts[section];
-  *bytes = (size_t)(starts[section + 1] - starts[section]);
+  *bytes = (size_t)sizes[section];
   return BMX_OK;
 }

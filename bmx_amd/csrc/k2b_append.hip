@@ -13,6 +13,7 @@
 // to the reference's whenever the reduction results (Us, the norm) agree.
 
 #include "k2b_common.h"
+#include "k2b_general.h"
 
 namespace bmx {
 
@@ -265,8 +266,11 @@ static hipError_t launch_us(const AppendKArgs& k, dim3 grid, size_t lds, hipStre
 extern "C" int bmx_k2b_append(const bmx_k2b_append_args* a, void* stream) {
   if (!a) return afail(BMX_E_INVALID, "bmx_k2b_append: args is NULL");
   const bmx_k2b_geom& g = a->geom;
+  const Geo geo = Geo::from(g);
   if (g.h_kv < 1 || g.h_kv > 16) return afail(BMX_E_INVALID, "bmx_k2b_append: h_kv must be 1..16");
-  if (g.rank != 16 && g.rank != 32) return afail(BMX_E_INVALID, "bmx_k2b_append: rank must be 16 or 32");
+  if (!geo.general && g.rank != 16 && g.rank != 32)
+    return afail(BMX_E_INVALID, "bmx_k2b_append: rank must be 16 or 32");
+  if (geo.general && !geo.check().empty()) return afail(BMX_E_INVALID, "bmx_k2b_append: " + geo.check());
   if (a->n_codec_pages < 0) return afail(BMX_E_INVALID, "bmx_k2b_append: n_codec_pages < 0");
   if (a->n_codec_pages == 0) return BMX_OK;
   if (!a->k_pre || !a->v || !a->basis32 || !a->basis16 || !a->pages || !a->page_ids)
@@ -274,11 +278,12 @@ extern "C" int bmx_k2b_append(const bmx_k2b_append_args* a, void* stream) {
   if (a->n_pool_pages < 1) return afail(BMX_E_INVALID, "bmx_k2b_append: n_pool_pages must be >= 1");
   if (reinterpret_cast<uintptr_t>(a->basis32) % 16 != 0)
     return afail(BMX_E_INVALID, "bmx_k2b_append: basis32 must be 16-byte aligned");
+  if (a->v_dtype != BMX_K2B_F16 && a->v_dtype != BMX_K2B_F32 && a->v_dtype != BMX_K2B_BF16)
+    return afail(BMX_E_INVALID, "bmx_k2b_append: v_dtype must be BMX_K2B_F16, _F32 or _BF16");
+  if (geo.general) return gen_append(a, (hipStream_t)stream);
   AppendKArgs k{};
   k.h_kv = g.h_kv; k.R = g.rank; k.n_codec_pages = a->n_codec_pages;
   k.k_pre = a->k_pre; k.ksh = a->k_stride_h; k.kst = a->k_stride_t;
-  if (a->v_dtype != BMX_K2B_F16 && a->v_dtype != BMX_K2B_F32 && a->v_dtype != BMX_K2B_BF16)
-    return afail(BMX_E_INVALID, "bmx_k2b_append: v_dtype must be BMX_K2B_F16, _F32 or _BF16");
   k.v = a->v; k.vsh = a->v_stride_h; k.vst = a->v_stride_t; k.v_dtype = a->v_dtype;
   k.basis32 = a->basis32; k.basis16 = a->basis16; k.us_first = a->us_first;
   k.pages = a->pages; k.page_ids = a->page_ids; k.n_pool = a->n_pool_pages;

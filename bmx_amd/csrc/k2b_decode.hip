@@ -56,6 +56,7 @@
 
 #include "k2b_common.h"
 #include "decode_shared.h"
+#include "k2b_general.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -755,6 +756,7 @@ static size_t ws_bytes(const bmx_k2b_decode_args* a, int splits) {
 
 extern "C" size_t bmx_k2b_decode_workspace_bytes(const bmx_k2b_decode_args* a) {
   if (!a || a->batch < 1) return 0;
+  if (Geo::from(a->geom).general) return gen_decode_workspace(a);
   return ws_bytes(a, choose_splits(a));
 }
 
@@ -967,8 +969,13 @@ extern "C" int bmx_k2b_decode_noalloc(const bmx_k2b_decode_args* a, void* stream
 // BMX_E_INVALID code with the message set.
 static int check_decode_args(const bmx_k2b_decode_args* a, const std::string& name) {
   const bmx_k2b_geom& g = a->geom;
-  if (g.h_kv < 1 || g.h_kv > kWaves) return fail(BMX_E_INVALID, name + ": h_kv must be 1..8");
-  if (g.rank != 16 && g.rank != 32) return fail(BMX_E_INVALID, name + ": rank must be 16 or 32");
+  if (Geo::from(g).general) {   // the general page: its own geometry limits
+    const std::string why = gen_decode_check(a);
+    if (!why.empty()) return fail(BMX_E_INVALID, name + ": " + why);
+  } else {
+    if (g.h_kv < 1 || g.h_kv > kWaves) return fail(BMX_E_INVALID, name + ": h_kv must be 1..8");
+    if (g.rank != 16 && g.rank != 32) return fail(BMX_E_INVALID, name + ": rank must be 16 or 32");
+  }
   if (g.n_q_groups < 1 || g.n_q_groups > 16)
     return fail(BMX_E_INVALID, name + ": n_q_groups must be 1..16");
   if (a->batch < 1) return fail(BMX_E_INVALID, name + ": batch must be >= 1");
@@ -1012,6 +1019,7 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
                          const std::string& name) {
   const bmx_k2b_geom& g = a->geom;
   if (const int rc = check_decode_args(a, name)) return rc;
+  if (Geo::from(g).general) return gen_decode(a, (hipStream_t)stream, ws, ws_cap, name);
   const int max_splits = choose_splits(a);
   const size_t need = ws_bytes(a, max_splits);
   if (max_splits > 8192)

@@ -3,6 +3,7 @@
 // _dense_kv), cache/codecs.py:639-649, 839-842 (dequant_packed).
 
 #include "k2b_common.h"
+#include "k2b_general.h"
 
 namespace bmx {
 
@@ -142,12 +143,17 @@ using namespace bmx;
 extern "C" int bmx_k2b_dequant(const bmx_k2b_dequant_args* a, void* stream) {
   if (!a) { bmx_set_error("bmx_k2b_dequant: args is NULL"); return BMX_E_INVALID; }
   const bmx_k2b_geom& g = a->geom;
-  if (g.h_kv < 1 || g.h_kv > 16 || (g.rank != 16 && g.rank != 32)) {
+  const Geo geo = Geo::from(g);
+  if (g.h_kv < 1 || g.h_kv > 16 || (!geo.general && g.rank != 16 && g.rank != 32)) {
     bmx_set_error("bmx_k2b_dequant: unsupported geometry (h_kv 1..16, rank 16|32)");
     return BMX_E_INVALID;
   }
-  if (a->n_tokens < 0 || a->n_tokens % kGroup != 0) {
-    bmx_set_error("bmx_k2b_dequant: n_tokens must be a non-negative multiple of 64");
+  if (geo.general && !geo.check().empty()) {
+    bmx_set_error("bmx_k2b_dequant: " + geo.check());
+    return BMX_E_INVALID;
+  }
+  if (a->n_tokens < 0 || a->n_tokens % geo.group != 0) {
+    bmx_set_error("bmx_k2b_dequant: n_tokens must be a non-negative multiple of the residual group");
     return BMX_E_INVALID;
   }
   if (a->n_tokens == 0) return BMX_OK;
@@ -168,6 +174,7 @@ extern "C" int bmx_k2b_dequant(const bmx_k2b_dequant_args* a, void* stream) {
     bmx_set_error("bmx_k2b_dequant: pos0 must be >= 0 and out_rows 0 or >= n_tokens");
     return BMX_E_INVALID;
   }
+  if (geo.general) return gen_dequant(a, (hipStream_t)stream);
   k.h_kv = g.h_kv; k.R = g.rank; k.n_tokens = a->n_tokens; k.apply_rope = a->apply_rope;
   k.out_dtype = a->out_dtype;
   k.pages = a->pages; k.page_table = a->page_table; k.basis = a->basis; k.n_pool = a->n_pool_pages;

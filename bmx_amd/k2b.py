@@ -17,6 +17,7 @@ from . import _lib
 from . import codecs as K
 
 HEAD_DIM = 128
+HEAD_DIMS = (32, 64, 128)   # 128: the recipe's page; 32 and 64 (and other ranks, groups, key bits): the general page
 PAGE_TOKENS = 16
 _V_DTYPES = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}   # BMX_K2B_F16 / F32 / BF16
 _IO_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}  # BMX_K2B_IO_F32 / F16 / BF16
@@ -36,17 +37,27 @@ class CodecConsts:
 
     @staticmethod
     def make(*, v_bits: int = 2, v_seed: int = 0, inv_freq=None, rope_scaling: float = 1.0,
-             theta: float = 500000.0):
+             theta: float = 500000.0, head_dim: int = HEAD_DIM):
         if v_bits != 2:
             raise ValueError("the k2b kernels implement 2-bit V codes only")
+        if head_dim not in HEAD_DIMS:
+            raise ValueError(f"head_dim must be one of {HEAD_DIMS}")
         if inv_freq is None:
-            inv_freq, rope_scaling = K.rope_inv_freq(head_dim=HEAD_DIM, theta=theta)
+            inv_freq, rope_scaling = K.rope_inv_freq(head_dim=head_dim, theta=theta)
         inv = tuple(float(x) for x in torch.as_tensor(inv_freq, dtype=torch.float32).tolist())
-        if len(inv) != HEAD_DIM // 2:
-            raise ValueError(f"inv_freq must have {HEAD_DIM // 2} entries")
+        if len(inv) != head_dim // 2:
+            raise ValueError(f"inv_freq must have {head_dim // 2} entries")
         return CodecConsts(K.gaussian_codebook(v_bits),
-                           tuple(K.sign_bits(K.hadamard_signs(HEAD_DIM, v_seed))),
+                           tuple(K.sign_bits(K.hadamard_signs(head_dim, v_seed))),
                            inv, float(rope_scaling))
+
+    @property
+    def head_dim(self) -> int:
+        return 2 * len(self.inv_freq)
+
+    def inv_freq64(self) -> tuple:
+        """inv_freq padded to the 64 entries of the argument structs."""
+        return tuple(self.inv_freq) + (0.0,) * (64 - len(self.inv_freq))
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -87,8 +98,8 @@ def set_window_rows(a, B: int, h_kv: int, tail_len, tail_cap: int, new_kv=None) 
     _need(not isinstance(tail_len, torch.Tensor), "rows given apart need a host tail_len")
     wdt = torch.bfloat16 if a.tail_dtype == _TAIL_DTYPES[torch.bfloat16] else torch.float16
     _need(k.dim() == 4 and k.shape == v.shape and k.dtype == wdt and v.dtype == wdt
-          and k.shape[0] == B and k.shape[1] == h_kv and k.shape[3] == HEAD_DIM,
-          f"new_kv: (B, h_kv, n, 128) keys and values in the window's dtype ({wdt})")
+          and k.shape[0] == B and k.shape[1] == h_kv and k.shape[3] in HEAD_DIMS,
+          f"new_kv: (B, h_kv, n, head_dim) keys and values in the window's dtype ({wdt})")
     # strides of size-1 dimensions are never used: taken as 0
     sk = tuple(0 if n == 1 else st for n, st in zip(k.shape[:3], k.stride()[:3]))
     sv = tuple(0 if n == 1 else st for n, st in zip(v.shape[:3], v.stride()[:3]))
@@ -101,36 +112,44 @@ def set_window_rows(a, B: int, h_kv: int, tail_len, tail_cap: int, new_kv=None) 
     _need(a.n_new <= a.tail_len_value, "new_kv holds more rows than the window")
 
 
-def page_bytes(h_kv: int, rank: int) -> int:
-    return _lib.page_bytes(h_kv, rank)
+def page_bytes(h_kv: int, rank: int, *, head_dim: int = HEAD_DIM, group: int = GROUP, k_bits: int = 3) -> int:
+    return _lib.page_bytes(h_kv, rank, head_dim=head_dim, group=group, k_bits=k_bits)
+
+
+def geom(h_kv: int, rank: int, n_q_groups: int = 1, *, head_dim: int = HEAD_DIM, group: int = GROUP,
+         k_bits: int = 3) -> "_lib.Geom":
+    return _lib.Geom(h_kv, rank, n_q_groups, head_dim, group, k_bits)
 
 
 def append(k_pre: torch.Tensor, v: torch.Tensor, basis32: torch.Tensor, basis16: torch.Tensor,
            pages: torch.Tensor, page_ids: torch.Tensor, consts: CodecConsts, *, rank: int,
-           us_first: torch.Tensor | None = None) -> None:
-    """Encode n codec pages (k_pre: (h_kv, 128n, 128) fp16, v: same shape in fp16,
-    bf16 or fp32 -- values are encoded from their own precision; last dims
-    contiguous) into the 8n physical pages listed in page_ids (int32, device)."""
+           us_first: torch.Tensor | None = None, group: int = GROUP, k_bits: int = 3) -> None:
+    """Encode n codec pages (k_pre: (h_kv, 128n, head_dim) fp16, v: same shape in
+    fp16, bf16 or fp32 -- values are encoded from their own precision; last dims
+    contiguous) into the 8n physical pages listed in page_ids (int32, device).
+    group / k_bits: the residual's scale group and bits (64 / 3: the recipe)."""
     h_kv, T, d = k_pre.shape
-    _need(d == HEAD_DIM and T % CODEC_PAGE == 0, "k_pre must be (h_kv, 128*n, 128)")
+    _need(d in HEAD_DIMS and T % CODEC_PAGE == 0, "k_pre must be (h_kv, 128*n, head_dim)")
+    _need(consts.head_dim == d, "consts were made for another head_dim")
     _need(v.shape == k_pre.shape, "v must match k_pre")
     _need(k_pre.dtype == torch.float16, "k_pre must be fp16")
     _need(v.dtype in _V_DTYPES, "v must be fp16, bf16 or fp32")
     _need(k_pre.stride(2) == 1 and v.stride(2) == 1, "k_pre/v last dim must be contiguous")
     n = T // CODEC_PAGE
-    C = h_kv * HEAD_DIM
+    C = h_kv * d
     _need(basis32.shape == (C, rank) and basis32.dtype == torch.float32 and basis32.is_contiguous(),
           "basis32 must be contiguous fp32 (C, rank)")
     _need(basis16.shape == (C, rank) and basis16.dtype == torch.float16 and basis16.is_contiguous(),
           "basis16 must be contiguous fp16 (C, rank)")
     _need(page_ids.dtype == torch.int32 and page_ids.numel() == 8 * n, "page_ids must be int32[8n]")
-    _need(pages.dtype == torch.uint8 and pages.dim() == 2 and pages.shape[1] == page_bytes(h_kv, rank)
+    pb = page_bytes(h_kv, rank, head_dim=d, group=group, k_bits=k_bits)
+    _need(pages.dtype == torch.uint8 and pages.dim() == 2 and pages.shape[1] == pb
           and pages.is_contiguous(), "pages must be a contiguous uint8 (n_pages, page_bytes) pool")
     if us_first is not None:
         _need(us_first.shape == (CODEC_PAGE, rank) and us_first.dtype == torch.float32
               and us_first.is_contiguous(), "us_first must be contiguous fp32 (128, rank)")
     a = _lib.AppendArgs()
-    a.geom = _lib.Geom(h_kv, rank, 1)
+    a.geom = geom(h_kv, rank, 1, head_dim=d, group=group, k_bits=k_bits)
     a.n_codec_pages = n
     a.k_pre, a.k_stride_h, a.k_stride_t = _ptr(k_pre), k_pre.stride(0), k_pre.stride(1)
     a.v, a.v_stride_h, a.v_stride_t = _ptr(v), v.stride(0), v.stride(1)
@@ -167,9 +186,11 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
            tail_len: torch.Tensor | None = None, tail_cap: int = 0,
            out: torch.Tensor | None = None, split_tokens: int = 0,
            workspace: DecodeWorkspace | None = None, page_stride: int | None = None,
-           new_kv=None, split_end_event: torch.cuda.Event | None = None, _capture=None) -> torch.Tensor:
-    """One decode step.  q (B, h_kv, G, 128) post-RoPE in fp32, fp16 or bf16 (the
-    model's dtype) -> (B, h_kv, G, 128) in q's dtype.
+           new_kv=None, split_end_event: torch.cuda.Event | None = None, group: int = GROUP,
+           k_bits: int = 3, _capture=None) -> torch.Tensor:
+    """One decode step.  q (B, h_kv, G, head_dim) post-RoPE in fp32, fp16 or bf16
+    (the model's dtype) -> (B, h_kv, G, head_dim) in q's dtype; group / k_bits
+    as in append.
 
     page_table (B, max_pages) int32, or None for contiguous pages: logical page
     i of sequence b at pool page b * page_stride + i (page_stride defaults to
@@ -180,9 +201,11 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
     set_window_rows."""
     B, h_kv, G, d = q.shape
     dev = q.device
-    _need(d == HEAD_DIM and q.dtype in _IO_DTYPES and q.is_contiguous(),
-          "q must be contiguous fp32, fp16 or bf16 (B, h_kv, G, 128)")
-    _need(pages.dtype == torch.uint8 and pages.shape[1] == page_bytes(h_kv, rank),
+    _need(d in HEAD_DIMS and q.dtype in _IO_DTYPES and q.is_contiguous(),
+          "q must be contiguous fp32, fp16 or bf16 (B, h_kv, G, head_dim)")
+    _need(consts.head_dim == d, "consts were made for another head_dim")
+    _need(pages.dtype == torch.uint8
+          and pages.shape[1] == page_bytes(h_kv, rank, head_dim=d, group=group, k_bits=k_bits),
           "pages must be (n_pages, page_bytes) uint8")
     if page_table is None:
         stride = page_stride if page_stride is not None else max(1, -(-max_packed_len // PAGE_TOKENS))
@@ -195,7 +218,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
               and page_table.is_contiguous(), "page_table must be contiguous int32 (B, max_pages)")
         stride = page_table.shape[1]
     _need(packed_len.dtype == torch.int32 and packed_len.numel() == B, "packed_len must be int32[B]")
-    C = h_kv * HEAD_DIM
+    C = h_kv * d
     if basis16.dim() == 2:
         _need(basis16.shape == (C, rank), "basis16 must be (C, rank)")
         bstride = 0
@@ -209,7 +232,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
     _need(out.dtype == q.dtype and out.shape == q.shape and out.is_contiguous(),
           "out must be contiguous and of q's shape and dtype")
     a = _lib.DecodeArgs()
-    a.geom = _lib.Geom(h_kv, rank, G)
+    a.geom = geom(h_kv, rank, G, head_dim=d, group=group, k_bits=k_bits)
     a.batch = B
     a.q, a.out = _ptr(q), _ptr(out)
     a.io_dtype = _IO_DTYPES[q.dtype]
@@ -218,7 +241,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
     _need(stride * PAGE_TOKENS >= max_packed_len, "page_table too narrow for max_packed_len")
     a.packed_len, a.max_packed_len = _ptr(packed_len), int(max_packed_len)
     a.basis, a.basis_stride = _ptr(basis16), bstride
-    a.inv_freq[:] = consts.inv_freq
+    a.inv_freq[:] = consts.inv_freq64()
     a.rope_scaling = consts.rope_scaling
     a.sm_scale = float(sm_scale)
     a.codebook[:] = consts.codebook
@@ -229,7 +252,7 @@ def decode(q: torch.Tensor, pages: torch.Tensor, page_table: torch.Tensor | None
         _need(k_tail.dtype in _TAIL_DTYPES and v_tail.dtype == k_tail.dtype and k_tail.dim() == 4
               and k_tail.shape[0] == B and k_tail.shape[1] == h_kv and k_tail.shape[2] >= tail_cap
               and k_tail.stride(3) == 1,
-              "k_tail/v_tail must be fp16 or bf16 (B, h_kv, >=tail_cap, 128) with contiguous last dim")
+              "k_tail/v_tail must be fp16 or bf16 (B, h_kv, >=tail_cap, head_dim) with contiguous last dim")
         a.k_tail, a.v_tail = _ptr(k_tail), _ptr(v_tail)
         a.tail_dtype = _TAIL_DTYPES[k_tail.dtype]
         a.tail_stride_b, a.tail_stride_h, a.tail_stride_t = k_tail.stride(0), k_tail.stride(1), k_tail.stride(2)
@@ -262,7 +285,7 @@ class DecodePlan:
     def __init__(self, q, pages, page_table, packed_len, max_packed_len, basis16, consts,
                  sm_scale, *, rank, k_tail=None, v_tail=None, tail_len=None, tail_cap=0,
                  out=None, split_tokens=0, workspace: DecodeWorkspace | None = None,
-                 page_stride: int | None = None):
+                 page_stride: int | None = None, group: int = GROUP, k_bits: int = 3):
         self.out = torch.empty_like(q) if out is None else out
         self._keep = (q, pages, page_table, packed_len, basis16, k_tail, v_tail, tail_len)
         self.ws = workspace or DecodeWorkspace()
@@ -273,7 +296,7 @@ class DecodePlan:
         decode(q, pages, page_table, packed_len, max_packed_len, basis16, consts, sm_scale,
                rank=rank, k_tail=k_tail, v_tail=v_tail, tail_len=tail_len, tail_cap=tail_cap,
                out=self.out, split_tokens=split_tokens, workspace=self.ws, page_stride=page_stride,
-               _capture=capture)
+               group=group, k_bits=k_bits, _capture=capture)
         self.args = captured["a"]
         self.stream = _stream(q.device)
         self._fn = _lib.lib().bmx_k2b_decode
@@ -308,26 +331,27 @@ class DecodePlan:
 ROPE_NONE, ROPE_EXACT, ROPE_FP16_TABLES = 0, 1, 2
 
 
-def _dense_out(out, h_kv: int, n_rows: int, dtype, dev):
-    """(K, V) destinations of a dequant: new (h_kv, n_rows, 128) tensors, or the
-    caller's (h_kv, >= n_rows, 128) views with contiguous rows; -> (K, V, rows
+def _dense_out(out, h_kv: int, n_rows: int, dtype, dev, d: int = HEAD_DIM):
+    """(K, V) destinations of a dequant: new (h_kv, n_rows, d) tensors, or the
+    caller's (h_kv, >= n_rows, d) views with contiguous rows; -> (K, V, rows
     between heads)."""
     if out is None:
-        k = torch.empty(h_kv, n_rows, HEAD_DIM, dtype=dtype, device=dev)
+        k = torch.empty(h_kv, n_rows, d, dtype=dtype, device=dev)
         return k, torch.empty_like(k), n_rows
     k, v = out
     _need(k.dtype == dtype and v.dtype == dtype and k.shape == v.shape and k.stride() == v.stride()
-          and k.dim() == 3 and k.shape[0] == h_kv and k.shape[1] >= n_rows and k.shape[2] == HEAD_DIM
-          and k.stride(2) == 1 and k.stride(1) == HEAD_DIM and k.stride(0) % HEAD_DIM == 0
-          and k.device == dev, "out must be (K, V) of shape (h_kv, >= n, 128) in dtype with contiguous rows")
-    return k, v, k.stride(0) // HEAD_DIM
+          and k.dim() == 3 and k.shape[0] == h_kv and k.shape[1] >= n_rows and k.shape[2] == d
+          and k.stride(2) == 1 and k.stride(1) == d and k.stride(0) % d == 0
+          and k.device == dev, f"out must be (K, V) of shape (h_kv, >= n, {d}) in dtype with contiguous rows")
+    return k, v, k.stride(0) // d
 
 
 def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis16: torch.Tensor,
             consts: CodecConsts, *, h_kv: int, rank: int, apply_rope: int = ROPE_NONE,
-            dtype: torch.dtype = torch.float32, pos0: int = 0, out: tuple | None = None):
-    """Committed pages of one sequence -> dense (K (h_kv, n, 128), V (h_kv, n, 128))
-    in dtype.  apply_rope: ROPE_NONE (pre-RoPE keys), ROPE_EXACT (fp32 cos/sin)
+            dtype: torch.dtype = torch.float32, pos0: int = 0, out: tuple | None = None,
+            group: int = GROUP, k_bits: int = 3):
+    """Committed pages of one sequence -> dense (K (h_kv, n, d), V (h_kv, n, d))
+    in dtype (d = consts.head_dim; group / k_bits as in append).  apply_rope: ROPE_NONE (pre-RoPE keys), ROPE_EXACT (fp32 cos/sin)
     or ROPE_FP16_TABLES (the reference's prefill: fp16-rounded cos/sin); pos0:
     the position of the first listed token; out: (K, V) views to write into (see
     _dense_out)."""
@@ -335,15 +359,16 @@ def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis1
     _need(dtype in _V_DTYPES, "dtype must be fp16, bf16 or fp32")
     _need(int(apply_rope) in (ROPE_NONE, ROPE_EXACT, ROPE_FP16_TABLES), "apply_rope must be 0, 1 or 2")
     _need(pos0 >= 0, "pos0 must be >= 0")
-    k, v, rows = _dense_out(out, h_kv, n_tokens, dtype, dev)
+    d = consts.head_dim
+    k, v, rows = _dense_out(out, h_kv, n_tokens, dtype, dev, d)
     _need(page_table.dtype == torch.int32 and page_table.numel() >= n_tokens // PAGE_TOKENS,
           "page_table must hold n_tokens/16 int32 page ids")
     a = _lib.DequantArgs()
-    a.geom = _lib.Geom(h_kv, rank, 1)
+    a.geom = geom(h_kv, rank, 1, head_dim=d, group=group, k_bits=k_bits)
     a.pages, a.page_table, a.n_tokens = _ptr(pages), _ptr(page_table), int(n_tokens)
     a.n_pool_pages = pages.shape[0]
     a.basis = _ptr(basis16)
-    a.inv_freq[:] = consts.inv_freq
+    a.inv_freq[:] = consts.inv_freq64()
     a.rope_scaling = consts.rope_scaling
     a.apply_rope = int(apply_rope)
     a.codebook[:] = consts.codebook

@@ -19,25 +19,25 @@ D = 128
 
 
 def k2b_keys(h_kv: int, S: int, rank: int, gen: torch.Generator, *, res_std: float = 0.05,
-             basis_rank: int | None = None) -> torch.Tensor:
-    """(h_kv, S, 128) fp16 pre-RoPE keys of rank-``basis_rank`` structure + noise,
-    on the generator's device."""
-    br = basis_rank or rank
+             basis_rank: int | None = None, head_dim: int = D) -> torch.Tensor:
+    """(h_kv, S, head_dim) fp16 pre-RoPE keys of rank-``basis_rank`` structure +
+    noise (at most head_dim directions per head), on the generator's device."""
+    br = min(basis_rank or rank, head_dim)
     dev = gen.device
-    out = torch.empty(h_kv, S, D, dtype=torch.float16, device=dev)
+    out = torch.empty(h_kv, S, head_dim, dtype=torch.float16, device=dev)
     std = (torch.arange(1, br + 1, dtype=torch.float32) ** (-0.35)).to(dev)
     for h in range(h_kv):
-        Q, R = torch.linalg.qr(torch.randn(D, br, generator=gen, device=dev).cpu())
+        Q, R = torch.linalg.qr(torch.randn(head_dim, br, generator=gen, device=dev).cpu())
         sgn = torch.sign(torch.diagonal(R))
         sgn[sgn == 0] = 1
         U = (Q * sgn).to(dev)
         c = torch.randn(S, br, generator=gen, device=dev) * std
-        out[h] = (c @ U.T + res_std * torch.randn(S, D, generator=gen, device=dev)).half()
+        out[h] = (c @ U.T + res_std * torch.randn(S, head_dim, generator=gen, device=dev)).half()
     return out
 
 
-def values(h_kv: int, S: int, gen: torch.Generator) -> torch.Tensor:
-    return torch.randn(h_kv, S, D, generator=gen, device=gen.device).half()
+def values(h_kv: int, S: int, gen: torch.Generator, head_dim: int = D) -> torch.Tensor:
+    return torch.randn(h_kv, S, head_dim, generator=gen, device=gen.device).half()
 
 
 def rope_keys(k_pre: torch.Tensor, start: int, consts: k2b.CodecConsts) -> torch.Tensor:
@@ -50,7 +50,8 @@ def rope_keys(k_pre: torch.Tensor, start: int, consts: k2b.CodecConsts) -> torch
     emb = torch.cat((ang, ang), dim=-1)
     cos, sin = emb.cos() * consts.rope_scaling, emb.sin() * consts.rope_scaling
     x = k_pre.float()
-    rot = torch.cat((-x[..., D // 2:], x[..., :D // 2]), dim=-1)
+    d = x.shape[-1]
+    rot = torch.cat((-x[..., d // 2:], x[..., :d // 2]), dim=-1)
     return (x * cos + rot * sin).half()
 
 
@@ -59,7 +60,7 @@ def first_page_svd(k_pre: torch.Tensor, rank: int):
     PackedStreamingLayer._pack_k_block does (packed_streaming.py:513-516):
     (Us (128, r) fp32, V (C, r) fp32) of the truncated SVD of M = to_matrix."""
     h_kv = k_pre.shape[0]
-    M = k_pre[:, :128].float().permute(1, 0, 2).reshape(128, h_kv * D).cpu()
+    M = k_pre[:, :128].float().permute(1, 0, 2).reshape(128, h_kv * k_pre.shape[2]).cpu()
     U, s, Vh = torch.linalg.svd(M, full_matrices=False)
     return U[:, :rank] * s[:rank], Vh[:rank, :].mT.contiguous()
 
@@ -67,9 +68,11 @@ def first_page_svd(k_pre: torch.Tensor, rank: int):
 class PagePool:
     """Fixed-capacity device pool of physical pages with a host free list."""
 
-    def __init__(self, n_pages: int, h_kv: int, rank: int, device, *, gen: torch.Generator | None = None):
+    def __init__(self, n_pages: int, h_kv: int, rank: int, device, *, gen: torch.Generator | None = None,
+                 head_dim: int = D, group: int = 64, k_bits: int = 3):
         self.h_kv, self.rank = h_kv, rank
-        self.page_bytes = k2b.page_bytes(h_kv, rank)
+        self.head_dim, self.group, self.k_bits = head_dim, group, k_bits
+        self.page_bytes = k2b.page_bytes(h_kv, rank, head_dim=head_dim, group=group, k_bits=k_bits)
         self.pages = torch.zeros(n_pages, self.page_bytes, dtype=torch.uint8, device=device)
         order = torch.randperm(n_pages, generator=gen) if gen is not None else torch.arange(n_pages)
         self.free = order.tolist()[::-1]
@@ -96,7 +99,7 @@ class PackedSeq:
 def encode_sequence(pool: PagePool, k_pre: torch.Tensor, v: torch.Tensor, rank: int,
                     consts: k2b.CodecConsts, svd=None, *, chunk_pages: int = 256) -> PackedSeq:
     """Quantize-on-append every full 128-token codec page of (k_pre, v) (device fp16,
-    (h_kv, S, 128)) with the HIP write kernel.  ``svd`` = (Us, V) of the first page;
+    (h_kv, S, head_dim)) with the HIP write kernel, in the pool's geometry.  ``svd`` = (Us, V) of the first page;
     computed from k_pre when omitted."""
     dev = pool.pages.device
     h_kv, S, _ = k_pre.shape
@@ -112,7 +115,8 @@ def encode_sequence(pool: PagePool, k_pre: torch.Tensor, v: torch.Tensor, rank: 
         seq.page_ids.extend(ids)
         k2b.append(k_pre[:, c0 * 128:c1 * 128], v[:, c0 * 128:c1 * 128], seq.basis32, seq.basis16,
                    pool.pages, torch.tensor(ids, dtype=torch.int32, device=dev), consts, rank=rank,
-                   us_first=us0.to(dev).float().contiguous() if c0 == 0 else None)
+                   us_first=us0.to(dev).float().contiguous() if c0 == 0 else None, group=pool.group,
+                   k_bits=pool.k_bits)
     seq.packed_len = n_cp * 128
     return seq
 

@@ -31,9 +31,31 @@
  * + 16*h_kv/C (norms) + 16R/C (Us).  The frozen basis V (C x R fp16) is stored
  * once per sequence and layer, outside the pages.
  *
- * Codec geometry fixed by the reference recipe: codec page 128 tokens
+ * Codec geometry of the reference recipe: codec page 128 tokens
  * (packed_streaming.py:438), key-scale group 64 tokens (recipes.py:31-42),
  * 3-bit keys / 2-bit values.
+ *
+ * General geometry.  The reference's fused path takes any power-of-two
+ * head_dim and rank and the recipe's residual group (packed_streaming.py:
+ * 957-975, recipes.py:31-56).  Every other geometry this library takes --
+ * head_dim d in {32, 64, 128}, rank R in {16, 32, 64, 128} (R <= C), residual
+ * group in {16, 32, 64, 128} tokens, 2..4-bit keys -- uses the general page
+ * (same 16 tokens, C = d*h_kv; sections in this order, each starting on a
+ * 16-byte boundary):
+ *   US     [16][R]          fp16  Us[token][r]
+ *   VNORM  [h_kv][16]       fp16  value norm per (head, token)
+ *   KSCALE [C*16/group]     fp16  the group's C scales (channel c = d*h + j
+ *                                 at c); page slot s (= logical page index
+ *                                 mod group/16) holds scales
+ *                                 [s*C*16/group, (s+1)*C*16/group)
+ *   KRES   [h_kv][16][d/2]  u8    residual codes, offset binary (code +
+ *                                 2^(bits-1)), channel j of (head, token) in
+ *                                 the low (j even) / high nibble of byte j/2
+ *   VCODE  [h_kv][4][d]     u8    2-bit value codes: byte (head, a, j) holds
+ *                                 tokens 4a .. 4a+3 of channel j, token 4a+t
+ *                                 at bits 2t
+ * The 4-bit residual container is the reference's own packed form
+ * (pack_signed_codes, triton_dequant_attention.py:49-165).
  */
 #ifndef BMX_K2B_H
 #define BMX_K2B_H
@@ -82,8 +104,11 @@ enum bmx_k2b_section {
 
 typedef struct {
   int32_t h_kv;        /* KV heads: 1..16 for pages/append/dequant, 1..8 for decode */
-  int32_t rank;        /* low-rank key rank R: 16 or 32 */
+  int32_t rank;        /* low-rank key rank R: 16 or 32 (any of 16..128: general page) */
   int32_t n_q_groups;  /* query heads per KV head G, 1..16 */
+  int32_t head_dim;    /* 0 or 128; 32 or 64: general page */
+  int32_t k_group;     /* residual scale group in tokens: 0 or 64; 16, 32 or 128: general page */
+  int32_t k_bits;      /* residual bits: 0 or 3; 2 or 4: general page */
 } bmx_k2b_geom;
 
 /* Message of the last failed call on this thread ("" if none). */

@@ -190,6 +190,106 @@ def unpack_pages(pages: np.ndarray, h_kv: int, rank: int):
 
 
 # ---------------------------------------------------------------------------
+# The general k2b page (include/bmx_k2b.h, "General geometry"): head_dim d,
+# rank R, residual group NG, key bits b; sections 16-byte aligned:
+#   US [16][R] fp16, VNORM [h][16] fp16, KSCALE [C*16/NG] fp16 (slot s = page
+#   mod NG/16 holds scales [s C 16/NG, (s+1) C 16/NG)), KRES [h][16][d/2] u8
+#   (offset-binary nibbles, even channel low), VCODE [h][4][d] u8 (byte (a, j):
+#   tokens 4a..4a+3 of channel j at bits 2t).
+# ---------------------------------------------------------------------------
+
+
+def _a16(x: int) -> int:
+    return (x + 15) & ~15
+
+
+def general_sections(h_kv: int, rank: int, d: int, group: int) -> dict:
+    C = d * h_kv
+    per_slot = C // (group // PT)
+    sizes = [("us", PT * rank * 2), ("vnorm", h_kv * PT * 2), ("kscale", per_slot * 2),
+             ("kres", h_kv * PT * (d // 2)), ("vcode", h_kv * 4 * d)]
+    off, out = 0, {}
+    for name, sz in sizes:
+        out[name] = (off, sz)
+        off = _a16(off + sz)
+    out["total"] = (0, off)
+    return out
+
+
+def pack_general(us16, res, scale16, vidx, vnorm16, h_kv: int, rank: int, d: int, group: int,
+                 bits: int) -> np.ndarray:
+    """Logical codec outputs of T tokens (T multiple of group) -> (T/16,
+    page_bytes) u8 general pages; arguments as pack_pages (scale16 (C, T/group))."""
+    T = us16.shape[0]
+    assert T % group == 0
+    C = d * h_kv
+    slots = group // PT
+    per = C // slots
+    sec = general_sections(h_kv, rank, d, group)
+    out = np.zeros((T // PT, sec["total"][1]), dtype=np.uint8)
+    res = np.asarray(res).astype(np.int64) + (1 << (bits - 1))
+    vidx = np.asarray(vidx).astype(np.int64)
+    for p in range(T // PT):
+        t0 = p * PT
+        o, s = sec["us"]
+        out[p, o:o + s] = np.ascontiguousarray(np.asarray(us16[t0:t0 + PT], np.float16)).reshape(-1).view(np.uint8)
+        o, s = sec["vnorm"]
+        out[p, o:o + s] = np.ascontiguousarray(np.asarray(vnorm16[t0:t0 + PT], np.float16).T).view(np.uint8).reshape(-1)
+        o, s = sec["kscale"]
+        slot = p % slots
+        sc = np.asarray(scale16[:, t0 // group], np.float16)[slot * per:(slot + 1) * per]
+        out[p, o:o + s] = np.ascontiguousarray(sc).view(np.uint8)
+        o, s = sec["kres"]
+        cr = res[:, t0:t0 + PT].T.reshape(PT, h_kv, d // 2, 2)          # (t, h, byte, nibble)
+        by = (cr[..., 0] | (cr[..., 1] << 4)).transpose(1, 0, 2)        # (h, t, byte)
+        out[p, o:o + s] = by.astype(np.uint8).reshape(-1)
+        o, s = sec["vcode"]
+        cv = vidx[t0:t0 + PT].reshape(4, 4, h_kv, d)                     # (a, t, h, j)
+        vb = np.zeros((h_kv, 4, d), dtype=np.int64)
+        for t in range(4):
+            vb |= cv[:, t].transpose(1, 0, 2) << (2 * t)
+        out[p, o:o + s] = vb.astype(np.uint8).reshape(-1)
+    return out
+
+
+def unpack_general(pages: np.ndarray, h_kv: int, rank: int, d: int, group: int, bits: int):
+    """Inverse of pack_general for a run of consecutive pages (count a multiple
+    of group / 16): (us16 (T, R), res (C, T), scale16 (C, T/group), vidx (T, C),
+    vnorm16 (T, h))."""
+    pages = np.asarray(pages, dtype=np.uint8)
+    T = pages.shape[0] * PT
+    C = d * h_kv
+    slots = group // PT
+    per = C // slots
+    sec = general_sections(h_kv, rank, d, group)
+    us16 = np.zeros((T, rank), dtype=np.float16)
+    vnorm16 = np.zeros((T, h_kv), dtype=np.float16)
+    scale16 = np.zeros((C, T // group), dtype=np.float16)
+    res = np.zeros((C, T), dtype=np.int8)
+    vidx = np.zeros((T, C), dtype=np.int16)
+    for p in range(pages.shape[0]):
+        t0 = p * PT
+        o, s = sec["us"]
+        us16[t0:t0 + PT] = pages[p, o:o + s].view(np.float16).reshape(PT, rank)
+        o, s = sec["vnorm"]
+        vnorm16[t0:t0 + PT] = pages[p, o:o + s].view(np.float16).reshape(h_kv, PT).T
+        o, s = sec["kscale"]
+        slot = p % slots
+        scale16[slot * per:(slot + 1) * per, t0 // group] = pages[p, o:o + s].view(np.float16)
+        o, s = sec["kres"]
+        by = pages[p, o:o + s].reshape(h_kv, PT, d // 2).astype(np.int64)
+        nib = np.stack([by & 15, by >> 4], axis=-1).reshape(h_kv, PT, d)   # (h, t, j)
+        res[:, t0:t0 + PT] = (nib - (1 << (bits - 1))).transpose(0, 2, 1).reshape(C, PT)
+        o, s = sec["vcode"]
+        vb = pages[p, o:o + s].reshape(h_kv, 4, d).astype(np.int64)
+        for t in range(4):
+            vidx[t0 + 4 * np.arange(4)[:, None, None] + t, (np.arange(h_kv)[None, :, None] * d
+                                                            + np.arange(d)[None, None, :])] = \
+                ((vb >> (2 * t)) & 3).transpose(1, 0, 2)
+    return us16, res, scale16, vidx, vnorm16
+
+
+# ---------------------------------------------------------------------------
 # RTN pages (include/bmx_rtn.h): 16 tokens, per head 4-bit offset-binary codes
 # (code + 8) and fp16 scales of channel groups gk / gv (32, 64 or 128).
 #   KSCALE [h][16 t][128/gk] fp16            token-arm keys

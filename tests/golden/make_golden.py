@@ -46,9 +46,14 @@ Functions covered (reference file:line, paths under ``src/bmx``):
   * full-C turboquant_mse values (quantize_packed / dequant_packed, arm
     "turboquant_mse")          cache/codecs.py:616-675, 729-735, 815-818
 
+  * k2b codecs at other geometries (head_dim 32/64, rank 64, groups 16/32/128,
+    2- and 4-bit keys) and PackedStreamingCache on a head_dim-64 tiny Llama
+                               cache/codecs.py:616-649, 677-695, 786-796;
+                               cache/packed_streaming.py:1067-1222
+
 ``python tests/golden/make_golden.py SRC spectral`` rewrites only the named
 fixture files (codecs, attention, e2e_tiny_llama, spectral, spectral_variants,
-tq_full).
+tq_full, k2b_geom, e2e_tiny_llama_d64).
 """
 
 from __future__ import annotations
@@ -411,9 +416,98 @@ def tq_full_fixtures():
     return out
 
 
+# name, h_kv, head_dim, rank, residual group, key bits, value seed
+GEOM_CASES = [
+    ("d64_r16_g32", 2, 64, 16, 32, 3, 7),        # the reference's k2b test geometry (n_q 8, G 4)
+    ("d128_r64_g64", 2, 128, 64, 64, 3, 0),      # spec_pair("k2b_ph", rank=64)
+    ("d32_r16_g16_b2", 4, 32, 16, 16, 2, 3),
+    ("d128_r32_g128_b4", 2, 128, 32, 128, 4, 0),
+]
+
+
+def k2b_geometry_fixtures():
+    """The k2b codecs at geometries other than head_dim 128 / group 64 / 3 bits
+    / rank 16|32: three 128-token codec pages per case, frozen basis from the
+    first (packed_streaming.py:513-520), quantize_packed for keys and values
+    (codecs.py:616-636, 677-695, 786-796)."""
+    from bmx.cache import codecs
+    from bmx.cache.collect import to_matrix
+    from bmx.decomp.lrs import truncated_svd
+
+    out = {}
+    S, PAGE = 384, 128
+    for name, h_kv, d, rank, group, bits, vseed in GEOM_CASES:
+        kpre = synthetic_k2b_keys(h_kv, S, d, min(rank, d), seed=300 + d + rank)
+        gv = torch.Generator().manual_seed(400 + d + rank)
+        v = torch.randn(h_kv, S, d, generator=gv).half()
+        out[f"{name}_kpre"] = kpre.numpy()
+        out[f"{name}_v"] = v.numpy()
+        out[f"{name}_signs"] = codecs._hadamard_signs(d, vseed).numpy().astype(np.int8)
+        frozen = None
+        for p in range(S // PAGE):
+            M = to_matrix(kpre[:, p * PAGE:(p + 1) * PAGE].float())
+            if frozen is None:
+                Us, V = truncated_svd(M, rank)
+                frozen = (Us, V)
+                out[f"{name}_svd_us_fp32"] = Us.numpy()
+                out[f"{name}_svd_v_fp32"] = V.numpy()
+            else:
+                Us = M @ frozen[1]
+            kp, bpe_k = codecs.quantize_packed(
+                "lowrank_rtn_channel", M, bits=bits, group=group, rank=rank,
+                svd_factors=(Us, frozen[1]), seed=0)
+            pre = f"{name}_p{p}_"
+            out[pre + "us"] = kp["Us"].numpy()
+            out[pre + "res"] = kp["res_Q_int"].numpy()
+            out[pre + "scale"] = kp["res_scale"].numpy()
+            out[pre + "bpe_k"] = np.float64(bpe_k)
+            Mv = to_matrix(v[:, p * PAGE:(p + 1) * PAGE].float())
+            vp, bpe_v = codecs.quantize_packed("turboquant_mse_perhead", Mv, bits=2, seed=vseed, h_heads=h_kv)
+            out[pre + "vidx"] = vp["indices"].numpy()
+            out[pre + "vnorm"] = vp["norms"].numpy()
+            out[pre + "bpe_v"] = np.float64(bpe_v)
+            if p == 0:
+                out[pre + "kdeq"] = codecs.dequant_packed("lowrank_rtn_channel", kp, group=group).numpy()
+                out[pre + "vdeq"] = codecs.dequant_packed("turboquant_mse_perhead", vp, seed=vseed).numpy()
+    return out
+
+
+def e2e_d64_fixtures():
+    """The reference's PackedStreamingCache under HF generate on a tiny Llama
+    with head_dim 64, k2b_ph at rank 16 and residual group 32
+    (packed_streaming.py:1067-1222, recipes.py:31-42)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from bmx.cache.packed_streaming import PackedStreamingCache
+    from bmx.cache.recipes import spec_pair
+
+    cfg = LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=64,
+                      max_position_embeddings=4096, rope_theta=500000.0, initializer_range=0.1)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).eval()
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, cfg.vocab_size, (1, 300), generator=g)
+    out = {"prompt": ids.numpy()}
+    k_spec, v_spec = spec_pair("k2b_ph", rank=16, group=32)
+    cache = PackedStreamingCache(cfg, k_spec, v_spec, recent_window=32)
+    cache.attach(model)
+    with torch.no_grad():
+        res = model.generate(ids, past_key_values=cache, max_new_tokens=140, min_new_tokens=140,
+                             do_sample=False, output_logits=True,
+                             return_dict_in_generate=True, pad_token_id=0)
+    bpe = cache.bits_per_entry()
+    cache.detach()
+    out["tokens"] = res.sequences.numpy()
+    out["logits"] = torch.stack(res.logits, 0).squeeze(1).numpy()
+    out["bpe"] = np.array(bpe, dtype=np.float64)
+    return out
+
+
 FIXTURES = {"codecs": codec_fixtures, "attention": attention_fixtures,
             "e2e_tiny_llama": e2e_fixtures, "spectral": spectral_fixtures,
-            "spectral_variants": spectral_variant_fixtures, "tq_full": tq_full_fixtures}
+            "spectral_variants": spectral_variant_fixtures, "tq_full": tq_full_fixtures,
+            "k2b_geom": k2b_geometry_fixtures, "e2e_tiny_llama_d64": e2e_d64_fixtures}
 
 
 def main():

@@ -105,3 +105,41 @@ def test_pack_unpack_round_trip(h_kv, rank):
     u2, r2, s2, v2, n2 = OL.unpack_pages(pages, h_kv, rank)
     assert np.array_equal(u2, us) and np.array_equal(r2, res) and np.array_equal(s2, sc)
     assert np.array_equal(v2, vidx) and np.array_equal(n2, vn)
+
+
+@pytest.mark.parametrize("h,R,d,g,b", [(2, 16, 64, 32, 3), (8, 64, 128, 64, 3), (4, 32, 32, 16, 2),
+                                       (1, 128, 128, 128, 4), (16, 16, 32, 32, 3)])
+def test_general_page_layout_round_trip_and_library_geometry(h, R, d, g, b):
+    """The general page's numpy restatement packs and unpacks every field, and
+    its sections sit where the library says (include/bmx_k2b.h)."""
+    from bmx_amd import _lib
+
+    rng = np.random.default_rng(h * 1000 + R + d + g + b)
+    C, T = h * d, 256
+    us = rng.standard_normal((T, R)).astype(np.float16)
+    res = rng.integers(-(1 << (b - 1)), 1 << (b - 1), (C, T))
+    sc = rng.random((C, T // g)).astype(np.float16)
+    vi = rng.integers(0, 4, (T, C))
+    vn = rng.random((T, h)).astype(np.float16)
+    pages = OL.pack_general(us, res, sc, vi, vn, h, R, d, g, b)
+    got = OL.unpack_general(pages, h, R, d, g, b)
+    for a_, w in zip(got, (us, res, sc, vi, vn)):
+        np.testing.assert_array_equal(a_, w)
+    sec = OL.general_sections(h, R, d, g)
+    assert pages.shape[1] == sec["total"][1] == _lib.page_bytes(h, R, head_dim=d, group=g, k_bits=b)
+    lib = _lib.page_sections(h, R, head_dim=d, group=g, k_bits=b)
+    for name in _lib.SECTIONS:
+        assert lib[name] == sec[name] and lib[name][0] % 16 == 0
+    # one residual code lands where the format says: head hh, channel 3, token 17
+    # -> page 1, row (hh, token 1), byte 1, high nibble, offset binary
+    hh = h - 1
+    res2 = np.zeros_like(res)
+    res2[hh * d + 3, 17] = 1
+    p2 = OL.pack_general(us, res2, sc, vi, vn, h, R, d, g, b)
+    o = sec["kres"][0] + (hh * 16 + 1) * (d // 2) + 1
+    assert p2[1, o] >> 4 == 1 + (1 << (b - 1)) and p2[1, o] & 15 == 1 << (b - 1)
+    # one value code: token 6 of channel 5, head hh -> byte (hh, a 1, 5), bits 4..5
+    vi2 = np.zeros_like(vi)
+    vi2[6, hh * d + 5] = 3
+    p3 = OL.pack_general(us, res, sc, vi2, vn, h, R, d, g, b)
+    assert p3[0, sec["vcode"][0] + (hh * 4 + 1) * d + 5] == 3 << 4

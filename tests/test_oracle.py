@@ -308,3 +308,52 @@ def test_oracle_catches_a_wrong_v_seed(ga):
     vt = torch.from_numpy(ga[pre + "v"])[:, 384:]
     o = A.k2b_naive_attention(q, cache, A.default_inv_freq(128, 5e5), kt, vt, 4, 128 ** -0.5)
     assert (o.numpy() - ga[pre + "naive"]).__abs__().max() > 0.05
+
+
+# ---------------------------------------------------------------- k2b at other geometries
+
+# name, h_kv, head_dim, rank, residual group, key bits, value seed (tests/golden/make_golden.py)
+GEOM_CASES = [
+    ("d64_r16_g32", 2, 64, 16, 32, 3, 7),
+    ("d128_r64_g64", 2, 128, 64, 64, 3, 0),
+    ("d32_r16_g16_b2", 4, 32, 16, 16, 2, 3),
+    ("d128_r32_g128_b4", 2, 128, 32, 128, 4, 0),
+]
+
+
+@pytest.mark.parametrize("case", GEOM_CASES, ids=[c[0] for c in GEOM_CASES])
+def test_k2b_codecs_at_other_geometries_match_reference(case):
+    """The oracle's key and value codecs at head_dim 32/64, rank 64, residual
+    groups 16/32/128 and 2- or 4-bit keys reproduce the reference's own
+    quantize_packed outputs bit for bit (the first page's SVD is an input)."""
+    name, h, d, rank, group, bits, vseed = case
+    g = np.load(GOLD / "k2b_geom.npz")
+    np.testing.assert_array_equal(C.hadamard_signs(d, vseed).numpy(), g[f"{name}_signs"])
+    kpre = torch.from_numpy(g[f"{name}_kpre"])
+    v = torch.from_numpy(g[f"{name}_v"])
+    enc = C.FrozenSubspaceKeyEncoder(rank, bits, group)
+    us0 = torch.from_numpy(g[f"{name}_svd_us_fp32"])
+    v0 = torch.from_numpy(g[f"{name}_svd_v_fp32"])
+    for p in range(3):
+        M = C.to_matrix(kpre[:, p * 128:(p + 1) * 128].float())
+        kp, bpe = enc.encode(M, us_override=(us0, v0) if p == 0 else None)
+        pre = f"{name}_p{p}_"
+        np.testing.assert_array_equal(kp["Us"].numpy(), g[pre + "us"])
+        np.testing.assert_array_equal(kp["res_Q_int"].numpy(), g[pre + "res"])
+        np.testing.assert_array_equal(kp["res_scale"].numpy(), g[pre + "scale"])
+        assert bpe == float(g[pre + "bpe_k"]) == pytest.approx(
+            bits + 16 / group + 16 * rank * (128 + h * d) / (128 * h * d))
+        idx, norms, bpe_v = C.quantize_v_perhead(C.to_matrix(v[:, p * 128:(p + 1) * 128].float()), bits=2,
+                                                 seed=vseed, h=h)
+        np.testing.assert_array_equal(idx.numpy(), g[pre + "vidx"])
+        np.testing.assert_array_equal(norms.numpy(), g[pre + "vnorm"])
+        assert bpe_v == float(g[pre + "bpe_v"])
+        if p == 0:
+            np.testing.assert_array_equal(C.dequant_k2b_key(kp, group).numpy(), g[pre + "kdeq"])
+            np.testing.assert_array_equal(
+                C.dequant_v_perhead(idx, norms, bits=2, seed=vseed, h=h).numpy(), g[pre + "vdeq"])
+    # the residual's range is the key bits': a 3-bit restatement of a 2-bit case fails
+    if bits != 3:
+        kp3, _ = C.FrozenSubspaceKeyEncoder(rank, 3, group).encode(
+            C.to_matrix(kpre[:, :128].float()), us_override=(us0, v0))
+        assert not np.array_equal(kp3["res_Q_int"].numpy(), g[f"{name}_p0_res"])
