@@ -170,17 +170,26 @@ class PackedStreamingLayer(DynamicLayer):
         tc = resolve_text_config(model_config)
         self._h_kv = getattr(tc, "num_key_value_heads", None) or tc.num_attention_heads
         self._d_head = getattr(tc, "head_dim", None) or tc.hidden_size // tc.num_attention_heads
-        if self._d_head != k2b.HEAD_DIM:
-            raise NotImplementedError(f"head_dim {self._d_head}: the packed kernels take head_dim 128")
-        if not 1 <= self._h_kv <= 8:
-            raise NotImplementedError(f"{self._h_kv} KV heads: the decode kernel takes 1..8")
+        # the k2b kernels take head_dim 32, 64 or 128 (the general page below 128,
+        # or at another rank, residual group or key width); RTN and spectral 128
+        dims = k2b.HEAD_DIMS if self._path == "k2b" else (k2b.HEAD_DIM,)
+        if self._d_head not in dims:
+            raise NotImplementedError(f"head_dim {self._d_head}: the {self._path} kernels take head_dim "
+                                      f"{' or '.join(str(x) for x in dims)}")
+        recipe_page = (self._path == "k2b" and self._d_head == k2b.HEAD_DIM and k_spec.group == k2b.GROUP
+                       and k_spec.bits == 3 and k_spec.rank in (16, 32))
+        max_h = 16 if self._path == "k2b" and not recipe_page else 8
+        if not 1 <= self._h_kv <= max_h:
+            raise NotImplementedError(f"{self._h_kv} KV heads: the decode kernel takes 1..{max_h}")
         self._rank = k_spec.rank
         self._page = PAGE
+        # the k2b key geometry beyond rank: residual scale group and bits
+        self._kgeom = dict(group=k_spec.group, k_bits=k_spec.bits) if self._path == "k2b" else {}
         inv, scaling = K.rope_inv_freq(tc)
         self._inv_freq, self._rope_scaling = inv, scaling
         if self._path in ("k2b", "spectral"):
             self._consts = k2b.CodecConsts.make(v_bits=2, v_seed=v_spec.seed, inv_freq=inv,
-                                                rope_scaling=scaling)
+                                                rope_scaling=scaling, head_dim=self._d_head)
         else:
             self._rtn = dict(k_bits=k_spec.bits, v_bits=v_spec.bits, k_group=k_spec.group,
                              v_group=v_spec.group,
@@ -320,7 +329,7 @@ class PackedStreamingLayer(DynamicLayer):
 
     def _page_bytes(self) -> int:
         if self._path == "k2b":
-            return k2b.page_bytes(self._h_kv, self._rank)
+            return k2b.page_bytes(self._h_kv, self._rank, head_dim=self._d_head, **self._kgeom)
         if self._path == "spectral":
             return spectral.v_page_bytes(self._h_kv, self._v_codec)
         return rtn.page_bytes(self._h_kv, **self._rtn)
@@ -376,7 +385,7 @@ class PackedStreamingLayer(DynamicLayer):
         self._reserve(first + PAGES_PER_CODEC * n, dev)
         ids = self._table[0, first: first + PAGES_PER_CODEC * n]
         k2b.append(k_pre.to(dev).half(), v, self._basis32, self._basis16, self._pool, ids,
-                   self._consts, rank=self._rank, us_first=us_first)
+                   self._consts, rank=self._rank, us_first=us_first, **self._kgeom)
         self._n_pages = first + PAGES_PER_CODEC * n
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
@@ -430,7 +439,8 @@ class PackedStreamingLayer(DynamicLayer):
                         * page_entries
                 else:
                     self._commit(k_pre, v_new)
-                    self._quant_bits_k += n_cp * K.bpe_k(self._rank, C) * page_entries
+                    self._quant_bits_k += n_cp * K.bpe_k(self._rank, C, bits=self.k_spec.bits,
+                                                         group=self.k_spec.group) * page_entries
                 self._quant_bits_v += n_cp * K.bpe_v(1 if self._v_codec == "full" else self._h_kv, C) * page_entries
                 self._committed_S_q = end
             keys = keys[..., end - start:, :]
@@ -556,7 +566,7 @@ class PackedStreamingLayer(DynamicLayer):
                                  tail_len=T, tail_cap=T, **self._rtn)
             else:
                 out = k2b.decode(qm, pool, None, self._packed_len_dev, P, basis16, self._consts, scaling,
-                                 rank=self._rank, k_tail=kt, v_tail=vt, tail_len=T, tail_cap=T)
+                                 rank=self._rank, k_tail=kt, v_tail=vt, tail_len=T, tail_cap=T, **self._kgeom)
             return out.reshape(h * G, 1, d)
         key = (P, G, float(scaling), qm.dtype, None if self._pool is None else self._pool.data_ptr())
         if self._plan is None or self._plan_key != key:
@@ -569,7 +579,7 @@ class PackedStreamingLayer(DynamicLayer):
                                             **self._rtn)
             else:
                 self._plan = k2b.DecodePlan(qm, pool, None, self._packed_len_dev, P, basis16, self._consts,
-                                            scaling, rank=self._rank, **common)
+                                            scaling, rank=self._rank, **common, **self._kgeom)
             self._plan_key = key
         pending, self._pending = self._pending, None
         # a fresh output tensor per call (an allocation, no kernel): the caller
@@ -643,7 +653,7 @@ class PackedStreamingLayer(DynamicLayer):
             else:
                 k2b.dequant(self._pool, self._table[0, : P // k2b.PAGE_TOKENS].contiguous(), P, self._basis16,
                             self._consts, h_kv=self._h_kv, rank=self._rank, apply_rope=k2b.ROPE_FP16_TABLES,
-                            dtype=dt, out=(Kd, Vd))
+                            dtype=dt, out=(Kd, Vd), **self._kgeom)
             if T:
                 Kd[:, P:].copy_(wk.squeeze(0))
                 Vd[:, P:].copy_(wv.squeeze(0))
@@ -881,7 +891,7 @@ class StreamingQuantizedLayer(PackedStreamingLayer):
         else:
             k2b.dequant(self._pool, self._table[0, p0:p1].contiguous(), end - start, self._basis16, self._consts,
                         h_kv=self._h_kv, rank=self._rank, apply_rope=k2b.ROPE_EXACT, dtype=dt, pos0=start,
-                        out=out)
+                        out=out, **self._kgeom)
         self._point_window(end)
 
     def _publish(self) -> None:

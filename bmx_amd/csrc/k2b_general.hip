@@ -8,7 +8,9 @@
 // Read:
 //   gen_split_kernel one workgroup per (split, head, sequence): every 16-token
 //                    page of the split rebuilt on MFMA (K^T = basis * Us^T),
-//                    residual and RoPE in registers, scores K^T Q^T on MFMA,
+//                    residual and RoPE in registers (cos and sin of HF's fp32
+//                    angle times rope_scaling, rounded to fp16: the
+//                    reference's shared tables), scores K^T Q^T on MFMA,
 //                    online softmax, P V on MFMA in the rotated value domain
 //   gen_merge_kernel one workgroup per (query, head, sequence): the splits'
 //                    partials, the inverse Hadamard, the recent window
@@ -260,11 +262,12 @@ __global__ __launch_bounds__(256) void gen_v_kernel(const GenAppendArgs a) {
 // A[n][4qd .. 4qd+3], B holds B[4qd .. 4qd+3][n], the result D[4qd + e][n].
 //   K^T tile rt (channels 16rt ..): A = basis rows 16rt + n, ranks 16ks + 4qd ..
 //     (LDS), B = Us[token n][16ks + 4qd ..] -> lane: K[16rt + 4qd + e][token n]
-//   S^T = K^T Q^T: A = that tile as fp16 (token n, channels 16rt + 4qd + e),
-//     B = query n's channels 16rt + 4qd + e (fp16 high and low parts)
+//   S^T = K^T Q^T: A = that tile (token n, channels 16rt + 4qd + e), B = query
+//     n's channels 16rt + 4qd + e, both as fp16 high and low parts
 //     -> lane: score of token 4qd + e for query n
 //   O = P V: A = those weights (query n, tokens 4qd + e), B = value level times
-//     norm of token 4qd + e, channel n + 16ct -> lane: O[query 4qd + e][n + 16ct]
+//     norm of token 4qd + e, channel n + 16ct (both high + low parts)
+//     -> lane: O[query 4qd + e][n + 16ct]
 // RoPE pairs channels j and j + d/2: tiles rt and rt + d/32 of the same lane.
 // ---------------------------------------------------------------------------
 struct GenReadArgs {
@@ -413,13 +416,17 @@ __global__ __launch_bounds__(256) void gen_split_kernel(const GenDecodeArgs a) {
     for (int ct = 0; ct < NT; ++ct) vc[ct] = pg[L.vcode + (h * 4 + qd) * D + n + 16 * ct];
     float4_t kt[NT];
     gen_keys<D, R>(a.r, pg, s_B, b, p, h, n, qd, kt);
-    gen_rope<D>(a.r, kt, p * kPT + n, qd, 1);
+    gen_rope<D>(a.r, kt, p * kPT + n, qd, 2);   // the reference's shared fp16 tables
+    // keys and queries as fp16 high + low parts: the three products that
+    // matter carry both to about 2^-22
     float4_t st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < NT; ++ks) {
       const half4_t kh = gen_h4(kt[ks]);
+      const half4_t kl = gen_h4(kt[ks] - float4_t{(float)kh[0], (float)kh[1], (float)kh[2], (float)kh[3]});
       st = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, qh[ks], st, 0, 0, 0);
       st = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, ql[ks], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, qh[ks], st, 0, 0, 0);
     }
     // online softmax of query n over the page's 16 tokens (4 per lane)
     float mloc = fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3]));
@@ -440,12 +447,17 @@ __global__ __launch_bounds__(256) void gen_split_kernel(const GenDecodeArgs a) {
     const half4_t pl = gen_h4(pw - float4_t{(float)ph[0], (float)ph[1], (float)ph[2], (float)ph[3]});
 #pragma unroll
     for (int ct = 0; ct < NT; ++ct) {
-      half4_t vb;
+      half4_t vh, vl;   // norm times level, fp16 high + low parts
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vb[e] = (_Float16)((float)vn[e] * a.r.level[(vc[ct] >> (2 * e)) & 3u]);
+      for (int e = 0; e < 4; ++e) {
+        const float x = (float)vn[e] * a.r.level[(vc[ct] >> (2 * e)) & 3u];
+        vh[e] = (_Float16)x;
+        vl[e] = (_Float16)(x - (float)vh[e]);
+      }
       o[ct] *= al;
-      o[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, o[ct], 0, 0, 0);
-      o[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vb, o[ct], 0, 0, 0);
+      o[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vh, o[ct], 0, 0, 0);
+      o[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vh, o[ct], 0, 0, 0);
+      o[ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vl, o[ct], 0, 0, 0);
     }
   }
   l_part += __shfl_xor(l_part, 16);

@@ -116,13 +116,13 @@ def packed_path(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> str:
 
 def check_k2b(k_spec: CacheCodecSpec, v_spec: CacheCodecSpec) -> None:
     """Raise unless (k_spec, v_spec) is a k2b pair the kernels implement."""
-    ok = (k_spec.arm == "lowrank_rtn_channel" and k_spec.bits == 3 and k_spec.group == 64
-          and k_spec.pre_rope and k_spec.rank in (16, 32)
+    ok = (k_spec.arm == "lowrank_rtn_channel" and k_spec.bits in (2, 3, 4) and k_spec.group in (16, 32, 64, 128)
+          and k_spec.pre_rope and k_spec.rank in (16, 32, 64, 128)
           and v_spec.arm == "turboquant_mse_perhead" and v_spec.bits == 2)
     if not ok:
         raise NotImplementedError(
-            f"the MI355X packed paths implement K=lowrank_rtn_channel (3 bits, group 64, "
-            f"pre-RoPE, rank 16|32) with V=turboquant_mse_perhead (2 bits), and K=rtn_token|"
+            f"the MI355X packed paths implement K=lowrank_rtn_channel (2..4 bits, groups 16|32|64|128, "
+            f"pre-RoPE, rank 16|32|64|128) with V=turboquant_mse_perhead (2 bits), and K=rtn_token|"
             f"rtn_channel with V=rtn_token (2..4 bits, groups 32|64|128, K post-RoPE); got "
             f"K={k_spec} V={v_spec}")
 

@@ -60,7 +60,8 @@ class OracleLayer(product.PackedStreamingLayer):
             self._oc = SpectralOracleStore(self._pack, self._h_kv, self.v_spec.seed, self.v_fp16,
                                            self.k_spec.payload_quant, self.v_spec.arm == "turboquant_mse")
         else:
-            self._oc = A.K2bOracleCache(self._h_kv, self._d_head, self._rank, v_seed=self.v_spec.seed)
+            self._oc = A.K2bOracleCache(self._h_kv, self._d_head, self._rank, group=self.k_spec.group,
+                                        k_bits=self.k_spec.bits, v_seed=self.v_spec.seed)
 
     def _commit_spectral(self, k_pre, v):
         self._oc.v_fp16 = self.v_fp16

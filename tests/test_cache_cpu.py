@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from bmx_amd import codecs as K
+from bmx_amd import k2b as K2B
 from bmx_amd.cache import ATTN_NAME, PackedStreamingCache, resolve_decoder_layers
 from bmx_amd.specs import CacheCodecSpec, check_k2b, spec_pair
 
@@ -32,12 +33,40 @@ def test_spec_pair_k2b_ph_matches_reference_recipe():
     check_k2b(k, v)
 
 
-@pytest.mark.parametrize("bad", [dict(rank=8), dict(bits=4), dict(group=32), dict(pre_rope=False)])
+@pytest.mark.parametrize("bad", [dict(rank=8), dict(rank=48), dict(bits=5), dict(bits=1), dict(group=8),
+                                 dict(group=256), dict(pre_rope=False)])
 def test_unsupported_k_specs_raise(bad):
     k, v = spec_pair("k2b_ph", rank=16)
     k = CacheCodecSpec(**{**k.__dict__, **bad})
     with pytest.raises(NotImplementedError):
         check_k2b(k, v)
+
+
+@pytest.mark.parametrize("good", [dict(rank=64), dict(rank=128), dict(bits=2), dict(bits=4), dict(group=32),
+                                  dict(group=16), dict(group=128)])
+def test_general_k_specs_taken(good):
+    """The fused path's geometry (packed_streaming.py:957-975): rank, residual
+    group and key bits beyond the recipe's default run on the general page."""
+    k, v = spec_pair("k2b_ph", rank=16)
+    check_k2b(CacheCodecSpec(**{**k.__dict__, **good}), v)
+
+
+@pytest.mark.parametrize("head_dim,ok", [(64, True), (32, True), (96, False), (256, False)])
+def test_k2b_layer_head_dims(head_dim, ok):
+    from transformers import LlamaConfig
+
+    from bmx_amd.cache import PackedStreamingLayer
+
+    cfg = LlamaConfig(vocab_size=256, hidden_size=512, intermediate_size=512, num_hidden_layers=1,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=head_dim)
+    k, v = spec_pair("k2b_ph", rank=16, group=32)
+    if ok:
+        lay = PackedStreamingLayer(k, v, cfg)
+        assert lay._consts.head_dim == head_dim and lay._kgeom == dict(group=32, k_bits=3)
+        assert lay._page_bytes() == K2B.page_bytes(2, 16, head_dim=head_dim, group=32)
+    else:
+        with pytest.raises(NotImplementedError, match="head_dim"):
+            PackedStreamingLayer(k, v, cfg)
 
 
 def test_other_recipes_raise():
@@ -140,6 +169,40 @@ def test_host_logic_reproduces_reference_run(rank):
     assert err <= 5e-4
     assert bool((got.argmax(1) == ref.argmax(1)).all())
     np.testing.assert_allclose(cache.bits_per_entry(), g[f"r{rank}_bpe"], rtol=1e-12)
+
+
+def test_host_logic_reproduces_reference_run_head_dim_64():
+    """The same teacher-forced check at a geometry off the recipe's page: a
+    tiny Llama with head_dim 64 (8 query / 2 KV heads) and k2b_ph at rank 16,
+    residual group 32 -- the reference's fused-kernel test geometry -- against
+    the reference's own 440-token run (tests/golden/e2e_tiny_llama_d64.npz)."""
+    import sys
+
+    sys.path.insert(0, str(Path(__file__).parent))
+    from oracle_cache import OracleCache
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    g = np.load(GOLD / "e2e_tiny_llama_d64.npz")
+    tokens = torch.from_numpy(g["tokens"])
+    ref = torch.from_numpy(g["logits"]).double()
+    cfg = LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=64,
+                      max_position_embeddings=4096, rope_theta=500000.0, initializer_range=0.1)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).eval()
+    cache = OracleCache(model.config, *spec_pair("k2b_ph", rank=16, group=32), recent_window=32)
+    got = []
+    with cache.attach(model), torch.no_grad():
+        got.append(model(tokens[:, :300], past_key_values=cache, use_cache=True).logits[0, -1])
+        for i in range(1, ref.shape[0]):
+            out = model(tokens[:, 300 + i - 1: 300 + i], past_key_values=cache, use_cache=True)
+            got.append(out.logits[0, -1])
+    got = torch.stack(got).double()
+    err = (got - ref).abs().max().item()
+    print(f"head_dim 64, group 32: oracle-backed cache vs reference run, logits max|err| {err:.3e}")
+    assert err <= 5e-4
+    assert bool((got.argmax(1) == ref.argmax(1)).all())
+    np.testing.assert_allclose(cache.bits_per_entry(), g["bpe"], rtol=1e-12)
 
 
 def test_lower_right_causal_mask_detection():

@@ -22,6 +22,7 @@ import numpy as np
 import pytest
 import torch
 
+from bmx_amd import k2b
 from bmx_amd.cache import PackedStreamingCache
 from bmx_amd.specs import spec_pair
 
@@ -661,3 +662,76 @@ def test_bf16_window_keeps_the_model_rows():
         assert out.dtype == torch.bfloat16 and torch.isfinite(out).all() and err <= 1e-2 * top
     assert prod.n_rows_folded == 2
     assert torch.equal(prod.window()[0].cpu(), orac.window()[0])
+
+
+def _tiny_model_d(head_dim, n_heads, n_kv, n_layers=2):
+    """_tiny_model at another head_dim: key projections rank 8 plus 1% noise
+    (with full-rank random keys the fp16 storage of the key scales and the fp16
+    key operand of the score product, in the recipe's kernels as in these,
+    move the random model's logits by ~0.1 against the fp32 oracle)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=256, hidden_size=256, intermediate_size=512, num_hidden_layers=n_layers,
+                      num_attention_heads=n_heads, num_key_value_heads=n_kv, head_dim=head_dim,
+                      max_position_embeddings=4096, rope_theta=500000.0, initializer_range=0.1)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).eval()
+    gen = torch.Generator().manual_seed(3)
+    with torch.no_grad():
+        for layer in model.model.layers:
+            W = layer.self_attn.k_proj.weight
+            U, s, Vh = torch.linalg.svd(W, full_matrices=False)
+            W.copy_((U[:, :8] * s[:8]) @ Vh[:8] + 0.01 * W.abs().mean() * torch.randn(W.shape, generator=gen))
+    return model.to("cuda")
+
+
+@pytest.mark.parametrize("head_dim,n_heads,rank,group,dtype", [
+    (64, 8, 16, 32, torch.float32), (64, 8, 16, 32, torch.float16), (128, 4, 64, 64, torch.float32),
+    (32, 8, 16, 16, torch.float32)])
+def test_general_geometry_cache_matches_oracle_backed_cache(head_dim, n_heads, rank, group, dtype):
+    """Models off the recipe's page through the product cache (the general
+    page's append, decode and prefill kernels): head_dim 64 with group 32 (the
+    reference's k2b test geometry; the oracle-backed cache reproduces the
+    reference's own run of this geometry on the CPU), rank 64 at head_dim 128
+    (spec_pair("k2b_ph", rank=64)), head_dim 32 with group 16.  140
+    teacher-forced steps: logits within 2e-3 of the largest (1e-2 for the fp16
+    model, whose own arithmetic rounds every layer to fp16; the newest rows go
+    through the decode call there), and the reference's flip gate on the greedy
+    choices (no flip whose top-2 gap exceeds the step's logit delta, at most
+    N // 8 flips; scripts/profile_decode_ab.py:325-343)."""
+    from oracle import attention as A
+
+    g = np.load(GOLD / "e2e_tiny_llama_d64.npz")
+    tokens = torch.from_numpy(g["tokens"]).cuda()
+    n = 140
+    model = _tiny_model_d(head_dim, n_heads, 2).to(dtype)
+    specs = spec_pair("k2b_ph", rank=rank, group=group)
+    prod = PackedStreamingCache(model.config, *specs, recent_window=32)
+    got = _run(prod, model, tokens, n)
+    orc = OracleCache(model.config, *specs, recent_window=32)
+    ref = _run(orc, model, tokens, n)
+    err = (got - ref).abs().max(dim=1).values
+    scale = ref.abs().max().item()
+    gate = [A.argmax_flip(got[i], ref[i]) for i in range(n)]
+    flips, hard = sum(f for f, _ in gate), sum(h for _, h in gate)
+    folded = prod.layers[0].n_rows_folded
+    print(f"head_dim {head_dim} rank {rank} group {group} {dtype}: product vs oracle-backed cache, logits "
+          f"max|err| {err.max():.3e} of {scale:.3f}; flips {flips} (hard {hard}); rows folded {folded}; "
+          f"committed {prod.layers[0]._committed_S_q}", flush=True)
+    assert prod.layers[0]._committed_S_q == 384
+    assert (folded > 100) == (dtype == torch.float16)
+    np.testing.assert_allclose(prod.bits_per_entry(), orc.bits_per_entry(), rtol=1e-12)
+    assert err.max().item() <= (2e-3 if dtype == torch.float32 else 1e-2) * max(scale, 1.0)
+    assert hard == 0 and flips <= n // 8
+
+
+def test_rank_64_generate_runs():
+    """spec_pair("k2b_ph", rank=64) under HF generate on the packed path, fp16."""
+    model = _tiny_model().half()
+    ids = torch.randint(0, 256, (1, 300), generator=torch.Generator().manual_seed(12)).cuda()
+    cache = PackedStreamingCache(model.config, *spec_pair("k2b_ph", rank=64), recent_window=32)
+    with cache.attach(model), torch.no_grad():
+        out = model.generate(ids, past_key_values=cache, max_new_tokens=40, min_new_tokens=40, do_sample=False,
+                             pad_token_id=0)
+    assert out.shape == (1, 340) and cache.layers[0]._committed_S_q >= 256
+    assert cache.layers[0]._page_bytes() == k2b.page_bytes(2, 64)

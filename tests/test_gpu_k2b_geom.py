@@ -8,7 +8,7 @@ packed_streaming.py:957-975; its own k2b test runs head_dim 64, group 32, rank
     (tests/golden/k2b_geom.npz, written by make_golden.py from quantize_packed),
     and bit for bit against the oracle on dyadic inputs;
   * decode against the oracle's one-softmax attention over the same codes
-    (RoPE at the exact fp32 angle), at the north-star bar 2e-3, with and
+    (RoPE with the reference's fp16 tables), at the north-star bar 2e-3, with and
     without a recent window, rows given apart, bf16 windows, ragged batches;
   * dequant (the prefill path) against the oracle's dense keys and values.
 """
@@ -121,6 +121,19 @@ def _case_pages(gen, h, d, rank, group, bits, S, vseed=0, pool_pages=None):
     return k_pre, v, svd, consts, pool, seq
 
 
+def _attention_ref(q, cache, consts, kt, vt, G, d):
+    """The oracle's one-softmax attention, keys rotated with the reference's
+    shared fp16 RoPE tables (HF's fp32 angle, cos/sin rounded to fp16, the
+    rotation in fp32), as its decode reads them (packed_streaming.py:79-113)."""
+    K = cache.dense_k_pre()
+    cos, sin = A.rope_cos_sin(torch.tensor(consts.inv_freq), torch.arange(K.shape[1]))
+    K = A.apply_rope(K, cos.half().float(), sin.half().float())
+    V = cache.dense_v()
+    if kt is not None:
+        K, V = torch.cat([K, kt.float()], 1), torch.cat([V, vt.float()], 1)
+    return A.naive_dense_attention(q, K, V, G, d ** -0.5)
+
+
 def _oracle(k_pre, v, svd, consts, h, d, rank, group, bits, vseed, S):
     cache = A.K2bOracleCache(h, d, rank, group=group, k_bits=bits, v_seed=vseed)
     for p in range(S // 128):
@@ -155,9 +168,8 @@ def test_decode_matches_oracle(h, d, rank, group, bits, G, S, T):
                      k_tail=kt, v_tail=vt, tail_len=T, tail_cap=T, group=group, k_bits=bits)
     torch.cuda.synchronize()
     cache = _oracle(k_pre, v, svd, consts, h, d, rank, group, bits, 0, S)
-    ref = A.k2b_naive_attention(q[0].cpu().reshape(h * G, 1, d), cache, torch.tensor(consts.inv_freq),
-                                kt[0].float().cpu() if T else torch.zeros(h, 0, d),
-                                vt[0].float().cpu() if T else torch.zeros(h, 0, d), G, d ** -0.5)
+    ref = _attention_ref(q[0].cpu().reshape(h * G, 1, d), cache, consts, kt[0].cpu() if T else None,
+                         vt[0].cpu() if T else None, G, d)
     err = (out[0].cpu().reshape(h * G, 1, d) - ref).abs().max().item()
     rel = ((out[0].cpu().reshape(h * G, 1, d) - ref).norm() / ref.norm()).item()
     print(f"h {h} d {d} R {rank} group {group} bits {bits} G {G} S {S} T {T}: max_abs {err:.3e} rel {rel:.3e}",
@@ -202,9 +214,8 @@ def test_decode_ragged_batch_fold_and_bf16_window():
         for b, S in enumerate(lens):
             k_pre, v, svd = data[b]
             cache = _oracle(k_pre, v, svd, consts, h, d, rank, group, bits, 0, S)
-            ref = A.k2b_naive_attention(q[b].float().cpu().reshape(h * G, 1, d), cache,
-                                        torch.tensor(consts.inv_freq), kt[b].to(wdt).float().cpu(),
-                                        vt[b].to(wdt).float().cpu(), G, d ** -0.5)
+            ref = _attention_ref(q[b].float().cpu().reshape(h * G, 1, d), cache, consts, kt[b].to(wdt).cpu(),
+                                 vt[b].to(wdt).cpu(), G, d)
             err = (out[b].float().cpu().reshape(h * G, 1, d) - ref).abs().max().item()
             print(f"ragged b {b} S {S} window {wdt}: max_abs {err:.3e}", flush=True)
             assert err <= 2e-3 + ref.abs().max().item() * 2 ** -8
