@@ -41,37 +41,39 @@ def k2b_decode(q: torch.Tensor, pages: torch.Tensor, page_table: Optional[torch.
                inv_freq: list[float], rope_scaling: float, codebook: list[float], sign_bits: list[int],
                sm_scale: float, rank: int, k_tail: Optional[torch.Tensor] = None,
                v_tail: Optional[torch.Tensor] = None, tail_len: Optional[torch.Tensor] = None,
-               tail_len_value: int = 0, tail_cap: int = 0, split_tokens: int = 0) -> torch.Tensor:
-    """One fused decode step over packed k2b pages plus the fp16 window; the
+               tail_len_value: int = 0, tail_cap: int = 0, split_tokens: int = 0, group: int = 64,
+               k_bits: int = 3) -> torch.Tensor:
+    """One fused decode step over packed k2b pages plus the recent window; the
     arguments are those of ``bmx_amd.k2b.decode`` (tail_len a device int32 (B,)
-    tensor, or None and the host count tail_len_value)."""
+    tensor, or None and the host count tail_len_value; head_dim from q)."""
     return k2b.decode(q, pages, page_table, packed_len, max_packed_len, basis16,
                       _consts(inv_freq, rope_scaling, codebook, sign_bits), sm_scale, rank=rank,
                       k_tail=k_tail, v_tail=v_tail, tail_len=_tail_len(tail_len, tail_len_value),
-                      tail_cap=tail_cap, split_tokens=split_tokens)
+                      tail_cap=tail_cap, split_tokens=split_tokens, group=group, k_bits=k_bits)
 
 
 @k2b_decode.register_fake
 def _(q, pages, page_table, packed_len, max_packed_len, basis16, inv_freq, rope_scaling, codebook,
       sign_bits, sm_scale, rank, k_tail=None, v_tail=None, tail_len=None, tail_len_value=0, tail_cap=0,
-      split_tokens=0):
-    torch._check(q.dim() == 4 and q.shape[-1] == k2b.HEAD_DIM)
+      split_tokens=0, group=64, k_bits=3):
+    torch._check(q.dim() == 4 and q.shape[-1] in k2b.HEAD_DIMS)
     return torch.empty_like(q)
 
 
 @torch.library.custom_op(f"{_LIB}::k2b_append", mutates_args=("pages",), device_types="cuda")
 def k2b_append(k_pre: torch.Tensor, v: torch.Tensor, basis32: torch.Tensor, basis16: torch.Tensor,
                pages: torch.Tensor, page_ids: torch.Tensor, codebook: list[float], sign_bits: list[int],
-               rank: int, us_first: Optional[torch.Tensor] = None) -> None:
+               rank: int, us_first: Optional[torch.Tensor] = None, group: int = 64, k_bits: int = 3) -> None:
     """Encode 128-token codec pages into the pool (``bmx_amd.k2b.append``);
     writes ``pages`` in place."""
     consts = k2b.CodecConsts(tuple(float(x) for x in codebook), tuple(int(x) for x in sign_bits),
-                             (0.0,) * (k2b.HEAD_DIM // 2))
-    k2b.append(k_pre, v, basis32, basis16, pages, page_ids, consts, rank=rank, us_first=us_first)
+                             (0.0,) * (k_pre.shape[-1] // 2))
+    k2b.append(k_pre, v, basis32, basis16, pages, page_ids, consts, rank=rank, us_first=us_first, group=group,
+               k_bits=k_bits)
 
 
 @k2b_append.register_fake
-def _(k_pre, v, basis32, basis16, pages, page_ids, codebook, sign_bits, rank, us_first=None):
+def _(k_pre, v, basis32, basis16, pages, page_ids, codebook, sign_bits, rank, us_first=None, group=64, k_bits=3):
     return None
 
 
