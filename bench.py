@@ -77,7 +77,8 @@ def parse():
     ap.add_argument("--spectral-values", choices=["perhead", "full"], default="perhead",
                     help="spectral workload: the value codec (full: the reference's k4_b recipe, "
                          "full-C turboquant_mse; perhead: k4ph_b, turboquant_mse_perhead)")
-    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch", "spectral", "e2e"],
+    ap.add_argument("--workload", choices=["decode", "stream", "rtn", "prefill", "batch", "spectral", "e2e",
+                                           "general"],
                     default="decode",
                     help="decode: the headline 64k decode-attention step (default); stream: "
                          "BASELINE config 5, Qwen3-8B geometry, rank 16, an 8192-token prefill "
@@ -89,7 +90,14 @@ def parse():
                          "k4 recipe's decode step (spectral keys at --spectral-budget, one layer "
                          "of Llama-3.1-8B geometry, --ctx tokens); e2e: ms per decode token under "
                          "HF generate() on a random-init Llama-3.1-8B-geometry fp16 model, dense "
-                         "DynamicCache vs the streaming twin vs the packed cache (k2b_ph rank 16)")
+                         "DynamicCache vs the streaming twin vs the packed cache (k2b_ph rank 16); "
+                         "general: the decode step on the general page (--gen-head-dim, --rank, "
+                         "--gen-group, --gen-bits, --gen-kv-heads, --gen-q-groups), --ctx tokens, --layers")
+    ap.add_argument("--gen-head-dim", type=int, default=64)
+    ap.add_argument("--gen-group", type=int, default=32)
+    ap.add_argument("--gen-bits", type=int, default=3)
+    ap.add_argument("--gen-kv-heads", type=int, default=8)
+    ap.add_argument("--gen-q-groups", type=int, default=4)
     ap.add_argument("--e2e-ctx", default="4096,16384,65536")
     ap.add_argument("--e2e-decode", type=int, default=64, help="decode tokens per timed generate")
     ap.add_argument("--e2e-kinds", default="dense,streaming,packed")
@@ -844,6 +852,68 @@ E2E_METRIC = ("ms per decode token under HF generate(), Llama-3.1-8B geometry (r
               "k2b_ph rank 16, 1 MI355X")
 
 
+def run_general(args, torch, dev) -> dict:
+    """The decode step on the general page (any geometry off the recipe's:
+    head_dim 32/64, rank 64/128, residual groups 16/32/128, 2- or 4-bit keys),
+    batch 1, --ctx tokens = packed + --window fp16 window rows, --layers
+    distinct layer caches in one pool, contiguous pages.  A call is
+    gen_split_kernel + gen_merge_kernel; the roofline counts the pages, the
+    basis, the window and q/out."""
+    from bmx_amd import k2b, synth
+
+    d, R, grp, bits = args.gen_head_dim, args.rank, args.gen_group, args.gen_bits
+    H, G, L, W = args.gen_kv_heads, args.gen_q_groups, args.layers, args.window
+    packed = ((args.ctx - W) // 128) * 128
+    tail = args.ctx - packed
+    consts = k2b.CodecConsts.make(head_dim=d)
+    n_pages = packed // 16
+    pool = synth.PagePool(n_pages * L, H, R, dev, head_dim=d, group=grp, k_bits=bits)
+    gen = torch.Generator(device=dev).manual_seed(2025)
+    ws = k2b.DecodeWorkspace()
+    plans = []
+    for li in range(L):
+        k_pre = synth.k2b_keys(H, args.ctx, R, gen, head_dim=d)
+        v = synth.values(H, args.ctx, gen, head_dim=d)
+        seq = synth.encode_sequence(pool, k_pre[:, :packed], v[:, :packed], R, consts)
+        base = seq.page_ids[0]
+        q = torch.randn(1, H, G, d, generator=gen, device=dev)
+        kt = synth.rope_keys(k_pre[:, packed:], packed, consts).unsqueeze(0).contiguous()
+        vt = v[:, packed:].unsqueeze(0).contiguous()
+        plans.append(k2b.DecodePlan(q, pool.pages[base: base + n_pages], None,
+                                    torch.tensor([packed], dtype=torch.int32, device=dev), packed, seq.basis16,
+                                    consts, d ** -0.5, rank=R, k_tail=kt, v_tail=vt, tail_len=tail, tail_cap=tail,
+                                    workspace=ws, group=grp, k_bits=bits))
+        del k_pre, v
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        for pl in plans:
+            pl.run()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        for pl in plans:
+            pl.run()
+    end.record()
+    torch.cuda.synchronize()
+    call_us = start.elapsed_time(end) * 1e3 / (args.steps * L)
+    C = H * d
+    bytes_call = n_pages * pool.page_bytes + C * R * 2 + tail * C * 2 * 2 + 2 * H * G * d * 4
+    return {
+        "metric": f"general-page k2b decode-attn us/call, head_dim {d} rank {R} group {grp} {bits}-bit keys",
+        "value": round(call_us, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": False, "dtype": "fp32 q/out, fp16 MFMA (high + low parts)", "data": "synthetic",
+        "config": {"workload": f"k2b general page, h_kv {H}, G {G}, head_dim {d}, rank {R}, group {grp}, "
+                               f"{bits}-bit keys, batch 1, ctx {args.ctx} = {packed} packed + {tail} window, "
+                               f"{L} layers, contiguous pages",
+                   "page_bytes": pool.page_bytes},
+        "roofline": {"bound": "hbm", "kernel": "gen_split_kernel + gen_merge_kernel", "achieved":
+                     round(bytes_call / (call_us * 1e-6) / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(bytes_call / (call_us * 1e-6) / 8e12, 4), "traffic": None,
+                     "bytes_per_launch": bytes_call},
+    }
+
+
 def run_e2e(args, torch, dev) -> dict:
     """End-to-end decode latency, the reference's Mode A
     (scripts/profile_decode_ab.py:113-141, 248-279): per context and cache kind,
@@ -993,6 +1063,9 @@ def main():
         return
     if args.workload == "e2e":
         print(json.dumps(run_e2e(args, torch, dev)), flush=True)
+        return
+    if args.workload == "general":
+        print(json.dumps(run_general(args, torch, dev)), flush=True)
         return
     W = args.window
     packed = ((args.ctx - W) // 128) * 128

@@ -351,7 +351,13 @@ __device__ __forceinline__ void gen_keys(const GenReadArgs& a, const uint8_t* pg
 
 // RoPE of the lane's keys at position pos: mode 1 exact fp32 cos/sin, mode 2
 // the fp16-rounded tables (cos and sin times rope_scaling, then fp16).
-template <int D>
+// kFast: cos/sin of HF's fp32 angle fl(pos * inv_freq) from its fraction of a
+// revolution (the product scaled by 1/2pi in double, its fraction rounded to
+// fp32) and the hardware sin/cos of revolutions, ~1e-6 absolute: the decode's
+// tables are rounded to fp16 after it (the library's sincosf takes the long
+// argument reduction for the angles of long contexts and was the decode's
+// bound).  Without kFast, sincosf of the fp32 angle.
+template <int D, bool kFast>
 __device__ __forceinline__ void gen_rope(const GenReadArgs& a, float4_t kt[D / 16], int pos, int qd, int mode) {
   constexpr int NP = D / 32;
 #pragma unroll
@@ -360,7 +366,14 @@ __device__ __forceinline__ void gen_rope(const GenReadArgs& a, float4_t kt[D / 1
     for (int e = 0; e < 4; ++e) {
       const float ang = (float)pos * a.inv_freq[16 * rt + 4 * qd + e];
       float sn, cs;
-      sincosf(ang, &sn, &cs);
+      if constexpr (kFast) {
+        const double rev = (double)ang * 0.15915494309189535;
+        const float fr = (float)(rev - floor(rev));
+        cs = __builtin_amdgcn_cosf(fr);
+        sn = __builtin_amdgcn_sinf(fr);
+      } else {
+        sincosf(ang, &sn, &cs);
+      }
       cs = cs * a.rope_scaling;
       sn = sn * a.rope_scaling;
       if (mode == 2) {
@@ -416,7 +429,7 @@ __global__ __launch_bounds__(256) void gen_split_kernel(const GenDecodeArgs a) {
     for (int ct = 0; ct < NT; ++ct) vc[ct] = pg[L.vcode + (h * 4 + qd) * D + n + 16 * ct];
     float4_t kt[NT];
     gen_keys<D, R>(a.r, pg, s_B, b, p, h, n, qd, kt);
-    gen_rope<D>(a.r, kt, p * kPT + n, qd, 2);   // the reference's shared fp16 tables
+    gen_rope<D, true>(a.r, kt, p * kPT + n, qd, 2);   // the reference's shared fp16 tables
     // keys and queries as fp16 high + low parts: the three products that
     // matter carry both to about 2^-22
     float4_t st = {0.f, 0.f, 0.f, 0.f};
@@ -504,41 +517,73 @@ __device__ __forceinline__ void gen_store_io(void* base, int64_t idx, float v, i
   }
 }
 
-__device__ __forceinline__ float gen_win_elem(const uint16_t* p, bool bf16) {
-  return bf16 ? __uint_as_float((uint32_t)*p << 16) : half_bits_to_float(*p);
+// Sum over the 128 threads of v (every thread gets the result); s_red holds 2.
+__device__ __forceinline__ float gen_block_sum(float v, float* s_red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return s_red[0] + s_red[1];
 }
 
-// grid (G, h_kv, B), block 128: output row (b, h, g).  Thread c < d owns
-// channel c.  The splits' partials merge by the split softmax's weights, the
-// inverse value rotation (H_d, the codec's signs, 1/d) turns the sum into
-// values, and the recent window (scored here, rows given apart read from
-// there and copied into the window buffer by query 0's workgroup) joins with
-// its own weight.
+__device__ __forceinline__ float gen_block_max(float v, float* s_red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(s_red[0], s_red[1]);
+}
+
+// grid (G, h_kv, B), block 128: output row (b, h, g).  The splits' partials
+// merge by the split softmax's weights, the inverse value rotation (H_d, the
+// codec's signs, 1/d) turns the sum into values, and the recent window
+// (scored here; rows given apart read from there and copied into the window
+// buffer by query 0's workgroup) joins with its own weight.  Every loop hands
+// each thread independent rows so that their loads are in flight together:
+// thread (part, c4) takes 4 channels of splits / window rows part, part + P, ...
 template <int D>
 __global__ __launch_bounds__(128) void gen_merge_kernel(const GenDecodeArgs a) {
+  constexpr int NC4 = D / 4, P = 128 / NC4;   // channel quads, row parts
   const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int H = a.r.L.h, G = a.G, S = a.n_split;
+  const int c4 = tid % NC4, part = tid / NC4;
   __shared__ float s_x[D], s_q[D], s_red[2];
+  __shared__ float4_t s_part[P][NC4];
   __shared__ float s_s[4096];
   const int64_t row = ((int64_t)b * H + h) * G + g;
   if (tid < D) {
     const float4_t x = load_q4(a.q, row * D + (tid & ~3), a.io_dtype);
     s_q[tid] = x[tid & 3] * a.qscale;
   }
-  // packed partials
-  float Mp = -INFINITY;
-  for (int s = 0; s < S; ++s) Mp = fmaxf(Mp, a.ws_ml[2 * (row * S + s)]);
-  float acc = 0.f, Lp = 0.f;
+  // ---- packed partials: the max, then weighted sums
+  const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + row * S;
+  float mx = -INFINITY;
+  for (int s = tid; s < S; s += 128) mx = fmaxf(mx, ml[s].x);
+  const float Mp = gen_block_max(mx, s_red);
+  float lp = 0.f;
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
   if (Mp != -INFINITY) {
-    for (int s = 0; s < S; ++s) {
-      const float m = a.ws_ml[2 * (row * S + s)];
-      if (m == -INFINITY) continue;
-      const float w = __builtin_amdgcn_exp2f(m - Mp);
-      Lp += w * a.ws_ml[2 * (row * S + s) + 1];
-      if (tid < D) acc += w * a.ws_acc[(row * S + s) * D + tid];
+    for (int s = tid; s < S; s += 128) {
+      const float2 v = ml[s];
+      lp += v.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(v.x - Mp) * v.y;
+    }
+#pragma unroll 4
+    for (int s = part; s < S; s += P) {
+      const float m = ml[s].x;
+      const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - Mp);
+      acc += w * *reinterpret_cast<const float4_t*>(a.ws_acc + (row * S + s) * D + 4 * c4);
     }
   }
-  if (tid < D) s_x[tid] = acc;
+  const float Lp = gen_block_sum(lp, s_red);
+  s_part[part][c4] = acc;
+  __syncthreads();
+  if (tid < NC4) {
+    float4_t t = s_part[0][tid];
+    for (int q = 1; q < P; ++q) t += s_part[q][tid];
+    *reinterpret_cast<float4_t*>(&s_x[4 * tid]) = t;
+  }
   __syncthreads();
   for (int hb = 1; hb < D; hb <<= 1) {   // unnormalised H_d, Sylvester order
     float u = 0.f, v = 0.f;
@@ -560,39 +605,46 @@ __global__ __launch_bounds__(128) void gen_merge_kernel(const GenDecodeArgs a) {
     op = s_x[tid] / (float)D;
     if (sign_neg(a.r.v_sign_bits, tid)) op = -op;
   }
-  // the recent window
+  // ---- the recent window
   const int T = a.tail_len ? min(max(a.tail_len[b], 0), a.tail_cap) : a.nw.T;
   const bool wbf = __builtin_amdgcn_readfirstlane(a.tail_bf16) != 0;
   const int64_t tb = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
   const int64_t nb = (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh;
-  auto krow = [&](int t) {
+  auto wrow = [&](const uint16_t* fresh, const uint16_t* buf, int t) {
     const int i = fresh_row(a.nw, t);
-    return i >= 0 ? a.nw.k + nb + (int64_t)i * a.nw.st : a.k_tail + tb + (int64_t)t * a.ts_t;
+    return i >= 0 ? fresh + nb + (int64_t)i * a.nw.st : buf + tb + (int64_t)t * a.ts_t;
   };
-  auto vrow = [&](int t) {
-    const int i = fresh_row(a.nw, t);
-    return i >= 0 ? a.nw.v + nb + (int64_t)i * a.nw.st : a.v_tail + tb + (int64_t)t * a.ts_t;
+  auto cvt4 = [&](uint2 r) {   // 4 window elements as fp32
+    return wbf ? float4_t{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                          __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u)}
+               : float4_t{half_bits_to_float(r.x & 0xffff), half_bits_to_float(r.x >> 16),
+                          half_bits_to_float(r.y & 0xffff), half_bits_to_float(r.y >> 16)};
   };
   float mw = -INFINITY;
-  for (int t = tid; t < T; t += 128) {
-    const uint16_t* kr = krow(t);
+  for (int t = tid; t < T; t += 128) {   // scores: one row per thread, all its loads at once
+    const uint16_t* kr = wrow(a.nw.k, a.k_tail, t);
+    uint2 kv[NC4];
+#pragma unroll
+    for (int c = 0; c < NC4; ++c) kv[c] = *reinterpret_cast<const uint2*>(kr + 4 * c);
     float sc = 0.f;
-    for (int c = 0; c < D; ++c) sc = __builtin_fmaf(s_q[c], gen_win_elem(kr + c, wbf), sc);
+#pragma unroll
+    for (int c = 0; c < NC4; ++c) {
+      const float4_t x = cvt4(kv[c]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc = __builtin_fmaf(s_q[4 * c + e], x[e], sc);
+    }
     s_s[t] = sc;
     mw = fmaxf(mw, sc);
   }
-  for (int o = 32; o >= 1; o >>= 1) mw = fmaxf(mw, __shfl_xor(mw, o));
-  if ((tid & 63) == 0) s_red[tid >> 6] = mw;
-  __syncthreads();
-  mw = fmaxf(s_red[0], s_red[1]);
-  float ow = 0.f, Lw = 0.f;
-  if (tid < D) {
-    for (int t = 0; t < T; ++t) {
-      const float w = __builtin_amdgcn_exp2f(s_s[t] - mw);
-      Lw += w;
-      ow = __builtin_fmaf(w, gen_win_elem(vrow(t) + tid, wbf), ow);
-    }
-  }
+  mw = gen_block_max(mw, s_red);   // its barriers also publish s_s
+  float lw = 0.f;
+  for (int t = tid; t < T; t += 128) lw += __builtin_amdgcn_exp2f(s_s[t] - mw);
+  float4_t ow = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int t = part; t < T; t += P)
+    ow += __builtin_amdgcn_exp2f(s_s[t] - mw) * cvt4(*reinterpret_cast<const uint2*>(wrow(a.nw.v, a.v_tail, t) + 4 * c4));
+  const float Lw = gen_block_sum(lw, s_red);
+  s_part[part][c4] = ow;
   if (g == 0 && a.nw.n > 0) {   // rows given apart into the window buffer
     for (int e = tid; e < a.nw.n * D; e += 128) {
       const int t = a.nw.T - a.nw.n + e / D, c = e % D;
@@ -601,12 +653,15 @@ __global__ __launch_bounds__(128) void gen_merge_kernel(const GenDecodeArgs a) {
       a.nw.v_dst[dst] = a.nw.v[src];
     }
   }
+  __syncthreads();
   if (tid < D) {
+    float owc = 0.f;
+    for (int q = 0; q < P; ++q) owc += s_part[q][tid / 4][tid % 4];
     const float M = fmaxf(Mp, mw);
     const float wp = Mp == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(Mp - M);
     const float ww = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
     const float den = wp * Lp + ww * Lw;
-    gen_store_io(a.out, row * D + tid, den > 0.f ? (wp * op + ww * ow) / den : 0.f, a.io_dtype);
+    gen_store_io(a.out, row * D + tid, den > 0.f ? (wp * op + ww * owc) / den : 0.f, a.io_dtype);
   }
 }
 
@@ -632,7 +687,7 @@ __global__ __launch_bounds__(64) void gen_dequant_kernel(const GenDequantArgs a)
   const uint8_t* pg = gen_read_page(a.r, 0, p);
   float4_t kt[NT];
   gen_keys<D, R>(a.r, pg, s_B, 0, p, h, n, qd, kt);
-  if (a.apply_rope) gen_rope<D>(a.r, kt, a.pos0 + p * kPT + n, qd, a.apply_rope);
+  if (a.apply_rope) gen_rope<D, false>(a.r, kt, a.pos0 + p * kPT + n, qd, a.apply_rope);
   const int64_t krow = ((int64_t)h * a.out_rows + p * kPT + n) * D;
 #pragma unroll
   for (int rt = 0; rt < NT; ++rt)
