@@ -492,11 +492,13 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
       pidv = load_ids(pid_base, n_pages);
     }
     // every load of group gn is issued here, a whole group before its first
-    // use, and the prefix of group gn + 1 with them
-    const uint4 pre_n = load_prefix(gp);
+    // use, and the prefix of group gn + 1 with them (the last groups fetch
+    // nothing they would not use)
+    uint4 pre_n = make_uint4(0u, 0u, 0u, 0u);
+    if (gi + 2 < n_groups) pre_n = load_prefix(gp);
     uint3 kres_n[kGroupPages];
     uint2 vcd_n[kGroupPages];
-    if (active) {
+    if (active && gi + 1 < n_groups) {   // the last group fetches nothing more
 #pragma unroll
       for (int pp = 0; pp < kGroupPages; ++pp) {
         kres_n[pp] = load_kres(gn, pp);
