@@ -179,42 +179,28 @@ __device__ __forceinline__ void store_partial(const DecodeKArgs& a, int b, int s
                          m_run, l_run);
 }
 
-// Window tiles of split `split` of S: tiles split, split + S, ... (a tile's
-// rows are one memory round trip; dealing several to the splits that own
-// one group less made those splits the last to finish).  Returns the first
-// tile and the stride between the split's tiles.
-__device__ __forceinline__ int first_win_tile(int split, int S, int& stride) {
-  stride = S;
-  return split;
-}
-
-// A workgroup with no packed tokens: its window tiles, then an empty partial
-// (max -inf) that the merge ignores.  Out of line, with the kernel argument
-// block passed by its kernarg-segment address: a second inlined copy of the
-// window code would disturb the group loop's register allocation.
-__device__ __noinline__ void empty_range_partial(const DecodeKArgs& a, int b, int split, int S, int h, int n,
-                                                 int q) {
-  const int n_tiles = (a.tail_cap + 15) >> 4;
-  int stride;
-  const int j0 = first_win_tile(split, S, stride);
-  if (j0 < n_tiles) {
-    const int64_t qrow = (((int64_t)b * a.h_kv + h) * a.G + (n < a.G ? n : 0)) * kD;
+// The recent window is scored in (16-token tile, head) pairs: pair
+// p = tile * h_kv + head goes to split p mod S, and a split's k-th pair to
+// its wave k mod nw (after the group loop: waves 0-3, which end their groups
+// first; in a split with no packed tokens: any wave).  Each pair is one
+// memory round trip (the head's query rows and the tile's rows together), so
+// a wave that owns one pair ends one round trip after its groups.
+__device__ __forceinline__ void score_win_pairs(const DecodeKArgs& a, int b, int split, int S, int wave, int nw,
+                                                int n, int q) {
+  const int n_pairs = ((a.tail_cap + 15) >> 4) * a.h_kv;
+  for (int p = split + wave * S; p < n_pairs; p += nw * S) {
+    const int j = p / a.h_kv, hh = p - j * a.h_kv;
+    const int64_t qrow = (((int64_t)b * a.h_kv + hh) * a.G + (n < a.G ? n : 0)) * kD;
+    const int64_t tb = (int64_t)b * a.ts_b + (int64_t)hh * a.ts_h;
     float4_t qraw[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) qraw[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
+    uint2 kw[8];
+    load_win_tile(a, tb, j, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)hh * a.nw.sh);
     half8_t qh[4], ql[4];
     window_fragments(qraw, n < a.G ? a.qscale_rope : 0.0f, a.tail_bf16, qh, ql);
-    const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
-    for (int j = j0; j < n_tiles; j += stride) {
-      uint2 kw[8];
-      load_win_tile(a, tail_base, j, n, q, kw, (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh);
-      score_win_tile(a, b, h, j, n, q, kw, qh, ql, tail_base);
-    }
+    score_win_tile(a, b, hh, j, n, q, kw, qh, ql, tb);
   }
-  float4_t zero[8];
-#pragma unroll
-  for (int bt = 0; bt < 8; ++bt) zero[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  store_partial(a, b, split, h, n, q, zero, -INFINITY, 0.f, 0.f);
 }
 
 // R: key rank (16 or 32).  SW: query slot width (G rounded up to 4, 8 or 16);
@@ -321,8 +307,6 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
 #pragma unroll
     for (int u = 0; u < 8; ++u) qraw[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
   }
-  const int n_win_tiles = (a.tail_cap + 15) >> 4;   // recent-window score tiles
-  const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
   // dynamic LDS: the cos/sin tables, then the prefix ring
   const int cs_bufs = a.cs_bufs;
   uint32_t* cst = reinterpret_cast<uint32_t*>(smem);                            // [cs_bufs][64][kCsRow]
@@ -437,18 +421,11 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     produce_groups(0, min(g1 - g0, cs_bufs), 0);
     if (contig && g1 > g0) issue_first(g1 - g0);
   }
+  // a workgroup with no packed tokens runs no group: its window pairs, then an
+  // empty partial (max -inf, zeros) that the merge ignores
   const int n_groups = g1 - g0;
-  if (n_groups == 0) {  // nothing packed here: the window tiles and an empty partial
-    if (active)
-      empty_range_partial(*(const DecodeKArgs*)__builtin_amdgcn_kernarg_segment_ptr(), b, split, S, h, n, q);
-    return;
-  }
-  if (!contig) issue_first(n_groups);
+  if (!contig && n_groups > 0) issue_first(n_groups);
   const int n_pages = n_groups * kGroupPages;
-
-  // the recent-window tiles this workgroup owns (scored after the group loop)
-  int win_stride;
-  const int win_j0 = first_win_tile(split, S, win_stride);
 
   if (tid < 256) {
     const uint32_t l0 = a.level_hi[0], l1 = a.level_hi[1], l2 = a.level_hi[2], l3 = a.level_hi[3];
@@ -670,28 +647,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
     // with tables to refill in the loop, all waves move group by group
     if (lockstep) __syncthreads();   // table of group gi+1 visible; group gi's slots free
   }
-  if (wave < 4 && win_j0 < n_win_tiles) {
-    // the window tiles, scored after the group loop by waves 0-3: of the two
-    // waves of a SIMD these finish their groups first, so the tiles take no
-    // time on the workgroup's critical path; wave w takes heads w and w + 4
-    for (int hh = wave; hh < a.h_kv; hh += 4) {
-      const int64_t qrow = (((int64_t)b * a.h_kv + hh) * a.G + (n < a.G ? n : 0)) * kD;
-      const int64_t tb = (int64_t)b * a.ts_b + (int64_t)hh * a.ts_h;
-      const int64_t nb = (int64_t)b * a.nw.sb + (int64_t)hh * a.nw.sh;
-      float4_t qraw2[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) qraw2[u] = load_q4(a.q, qrow + 16 * (u & 3) + 4 * q + 64 * (u >> 2), a.io_dtype);
-      uint2 kw[8];
-      load_win_tile(a, tb, win_j0, n, q, kw, nb);
-      half8_t qh2[4], ql2[4];
-      window_fragments(qraw2, (n < a.G) ? a.qscale_rope : 0.0f, a.tail_bf16, qh2, ql2);
-      score_win_tile(a, b, hh, win_j0, n, q, kw, qh2, ql2, tb);
-      for (int j = win_j0 + win_stride; j < n_win_tiles; j += win_stride) {
-        load_win_tile(a, tb, j, n, q, kw, nb);
-        score_win_tile(a, b, hh, j, n, q, kw, qh2, ql2, tb);
-      }
-    }
-  }
+  // the window pairs this workgroup owns, on waves 0-3: of the two waves of a
+  // SIMD (w, w + 4) these finish their groups first
+  if (wave < 4) score_win_pairs(a, b, split, S, wave, 4, n, q);
   if (active) {
     // fold the page slots: column s*SW + g -> g
     if constexpr (NSLOT == 4) {
