@@ -489,9 +489,11 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
       pid_base = gn * kRGroupPages;
       pidv = load_ids(pid_base, n_pages);
     }
-    const Pre pre_n = load_prefix(gp);
+    // the last groups fetch nothing they would not use
+    Pre pre_n{};
+    if (gi + 2 < n_groups) pre_n = load_prefix(gp);
     uint4 kc_n[kRGroupPages], vc_n[kRGroupPages];
-    if (active) {
+    if (active && gi + 1 < n_groups) {
 #pragma unroll
       for (int pp = 0; pp < kRGroupPages; ++pp) {
         kc_n[pp] = load_kc(gn, pp);
