@@ -413,7 +413,9 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   produce_groups(0, min(g1 - g0, cs_bufs), 0);
 
   if (!contig) pidv = (int)clamp_page(pid_raw, a.n_pool);
-  const int len = min(len_raw, a.max_packed_len) & ~(kGroup - 1);
+  // the length and the range are wave-uniform: held in scalar registers, the
+  // loop's bookkeeping on them is scalar work
+  const int len = __builtin_amdgcn_readfirstlane(min(len_raw, a.max_packed_len) & ~(kGroup - 1));
   if (len != len_spec) {
     range(len, g0, g1);
     pidv = load_ids(0, (g1 - g0) * kGroupPages);
@@ -423,6 +425,8 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   }
   // a workgroup with no packed tokens runs no group: its window pairs, then an
   // empty partial (max -inf, zeros) that the merge ignores
+  g0 = __builtin_amdgcn_readfirstlane(g0);
+  g1 = __builtin_amdgcn_readfirstlane(g1);
   const int n_groups = g1 - g0;
   if (!contig && n_groups > 0) issue_first(n_groups);
   const int n_pages = n_groups * kGroupPages;
