@@ -75,6 +75,7 @@ constexpr int kCsBuf = kGroup * kCsRow;     // dwords per group table
 constexpr int kPidWindow = 64;              // page ids held per lane-vector
 constexpr int kCsMaxBufs = 8;               // RoPE table buffers at most (17 KB each)
 constexpr int kRingSlots = 3;               // prefix ring: group g in slot g % 3
+constexpr int kBufWord3 = 0x00020000;       // buffer descriptor word 3: raw 32-bit data
 
 
 struct DecodeKArgs {
@@ -382,12 +383,18 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   const uint32_t kres_off = (uint32_t)(a.L.kres + h * 768 + lane * 12);
   const uint32_t vcode_off = (uint32_t)(a.L.vcode + h * 512 + lane * 8);
   typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+  // a page's sections through a buffer descriptor on its (uniform) base: the
+  // address is scalar work, the lane offset a constant register, and the load
+  // is non-temporal (aux 2)
+  auto page_rsrc = [&](int gi, int pp) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page_ptr(gi, pp)), (short)0, pb, kBufWord3);
+  };
   auto load_kres = [&](int gi, int pp) -> uint3 {
-    const u32x3_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x3_t*>(page_ptr(gi, pp) + kres_off));
+    const u32x3_t v = __builtin_amdgcn_raw_buffer_load_b96(page_rsrc(gi, pp), (int)kres_off, 0, 2);
     return make_uint3(v[0], v[1], v[2]);
   };
   auto load_vcode = [&](int gi, int pp) -> uint2 {
-    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(page_ptr(gi, pp) + vcode_off));
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(page_rsrc(gi, pp), (int)vcode_off, 0, 2);
     return make_uint2(v[0], v[1]);
   };
 
