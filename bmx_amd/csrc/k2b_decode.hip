@@ -78,12 +78,25 @@ constexpr int kRingSlots = 3;               // prefix ring: group g in slot g % 
 constexpr int kBufWord3 = 0x00020000;       // buffer descriptor word 3: raw 32-bit data
 
 
+// The scalar arguments the prologue reads come first, contiguous, so that one
+// round trip of wide scalar loads fetches them all (the big tables follow).
 struct DecodeKArgs {
   int h_kv, G, max_splits, max_pages, max_packed_len, n_pool;
   int shared_bytes;    // page prefix read by every head: US, VNORM, KSCALE (multiple of 16)
   int cs_bufs;         // RoPE table buffers in LDS (groups produced in the prologue)
-  const void* q;       // [B][h_kv][G][128] in io_dtype
+  int balanced;        // a ragged batch: workgroup w of the flat grid serves the
+                       // sequence batch_shares() gives it (max_splits = the slots per row)
+  int n_seq;
+  // floor(n / max_splits) for n < 2^32 as (t + ((n - t) >> div_sh1)) >> div_sh2,
+  // t = mulhi(n, div_magic) (Granlund-Montgomery); div_ok: split * groups < 2^32
+  uint32_t div_magic;
+  int div_sh1, div_sh2, div_ok;
   int io_dtype;
+  float qscale_rope;   // sm_scale * log2(e) * rope_scaling (the cos/sin table is unscaled)
+  uint32_t level_hi[4];   // fp16 bits of the value levels as used by the MFMA:
+                          // hi_c = kappa * codebook_c + mu (+ < 1e-6 relative)
+  float level_mu;         // mu (the merge divides by kappa)
+  const void* q;       // [B][h_kv][G][128] in io_dtype
   uint16_t* ws_acc;    // [B][h_kv][G][8][max_splits][16] partial records (H8 applied; decode_shared.h)
   float* ws_ml;        // [B][h_kv][G][max_splits][2]     (running max, sum), base 2
   const uint8_t* pages;
@@ -92,15 +105,11 @@ struct DecodeKArgs {
   const uint16_t* basis;
   int64_t basis_stride;
   PageLayout L;
-  float qscale_rope;   // sm_scale * log2(e) * rope_scaling (the cos/sin table is unscaled)
   float inv_freq[64];
   float step_c[64];    // cos / sin of 64 * inv_freq_j (exact angle), the per-group step
   float step_s[64];
   float step8_c[64];   // cos / sin of 8 * inv_freq_j, between a thread's positions
   float step8_s[64];
-  uint32_t level_hi[4];   // fp16 bits of the value levels as used by the MFMA:
-                          // hi_c = kappa * codebook_c + mu (+ < 1e-6 relative)
-  float level_mu;         // mu (the merge divides by kappa)
   // recent window: fp16 (or bf16: tail_bf16) post-RoPE keys [b * ts_b + h * ts_h + t * ts_t][128]
   const uint16_t* k_tail;
   int64_t ts_b, ts_h, ts_t;
@@ -109,13 +118,6 @@ struct DecodeKArgs {
   int tail_cap;
   float win_rescale;      // 1 / rope_scaling: window keys carry the RoPE scaling
   float* ws_win;          // [B][h_kv][G][tail_cap] window scores, base 2
-  int balanced;           // a ragged batch: workgroup w of the flat grid serves the
-                          // sequence batch_shares() gives it (max_splits = the slots per row)
-  int n_seq;
-  // floor(n / max_splits) for n < 2^32 as (t + ((n - t) >> div_sh1)) >> div_sh2,
-  // t = mulhi(n, div_magic) (Granlund-Montgomery); div_ok: split * groups < 2^32
-  uint32_t div_magic;
-  int div_sh1, div_sh2, div_ok;
 };
 
 // v_mov_b32_dpp: lanes enabled by BANK (4-lane banks of each 16-lane row) take
@@ -222,6 +224,14 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   // s, s_sync[3 + s] the waves done reading a group from slot s (monotonic:
   // slot s serves groups s, s + 3, ...)
   __shared__ uint32_t s_sync[2 * kRingSlots];
+  // every scalar argument of the prologue requested at once, at the top: one
+  // round trip of wide scalar loads instead of a chain of them behind the
+  // prologue's branches
+  asm volatile("" ::"s"(a.h_kv), "s"(a.G), "s"(a.max_splits), "s"(a.max_pages), "s"(a.max_packed_len),
+               "s"(a.n_pool), "s"(a.shared_bytes), "s"(a.cs_bufs), "s"(a.balanced), "s"(a.n_seq),
+               "s"(a.div_magic), "s"(a.div_sh1), "s"(a.div_sh2), "s"(a.div_ok), "s"(a.io_dtype));
+  asm volatile("" ::"s"(a.q), "s"(a.pages), "s"(a.page_table), "s"(a.packed_len), "s"(a.basis),
+               "s"(a.basis_stride), "s"(a.L.bytes), "s"(a.L.kres), "s"(a.L.vcode));
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int n = lane & 15;   // token within page (K side) / score column (softmax side)
