@@ -222,8 +222,11 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   // hand-off of the prefix ring between waves, no workgroup barrier per group:
   // s_sync[s] counts the waves that have stored a group's prefix into ring slot
   // s, s_sync[3 + s] the waves done reading a group from slot s (monotonic:
-  // slot s serves groups s, s + 3, ...)
+  // slot s serves groups s, s + 3, ...); s_tab[t] counts the waves that have
+  // made their rows of a RoPE table in buffer t after the prologue (buffer t
+  // serves groups t, t + cs_bufs, ...)
   __shared__ uint32_t s_sync[2 * kRingSlots];
+  __shared__ uint32_t s_tab[kCsMaxBufs];
   // every scalar argument of the prologue requested at once, at the top: one
   // round trip of wide scalar loads instead of a chain of them behind the
   // prologue's branches
@@ -463,6 +466,7 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   store_prefix(pre1, 1);
   // slots 0 and 1 hold groups 0 and 1 (visible at the barrier)
   if (tid < 2 * kRingSlots) s_sync[tid] = tid < 2 ? kWaves : 0;
+  if (tid < kCsMaxBufs) s_tab[tid] = 0;
 
   // ---- per-wave state ----
   float4_t acc[8];
@@ -479,9 +483,10 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
   // on the next group's loads (issued at the top of the same group).
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
 
-  // every RoPE table was made in the prologue: waves hand the prefix ring on
-  // through s_sync and may drift apart by up to a group
-  const bool lockstep = n_groups > cs_bufs;
+  // waves hand the prefix ring and the RoPE table buffers on through LDS
+  // counters and may drift apart by up to a group: a range longer than the
+  // prologue's tables (cs_bufs groups) remakes each buffer once every wave is
+  // done with its group, each wave its own rows, at the end of the next group
   for (int gi = 0; gi < n_groups; ++gi) {
     const int gn = min(gi + 1, n_groups - 1);   // group whose codes are fetched during this one
     const int gp = min(gi + 2, n_groups - 1);   // group whose prefix is fetched during this one
@@ -503,11 +508,11 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
         vcd_n[pp] = load_vcode(gn, pp);
       }
     }
-    // groups past the prologue's tables: refill the buffer group gi-1 left
-    if (gi > 0 && gi - 1 + cs_bufs < n_groups) produce_groups(gi - 1 + cs_bufs, 1, gi - 1);
-    // every wave has stored this group's prefix (use gi / 3 of slot gi % 3)
+    // every wave has stored this group's prefix (use gi / 3 of slot gi % 3),
+    // and past the prologue's tables made its rows of this group's table
     const int slot = gi % kRingSlots;
-    if (!lockstep) wait_count(&s_sync[slot], kWaves * (gi / kRingSlots + 1));
+    wait_count(&s_sync[slot], kWaves * (gi / kRingSlots + 1));
+    if (gi >= cs_bufs) wait_count(&s_tab[gi % cs_bufs], kWaves * (gi / cs_bufs));
 
     if (active) {
       const uint8_t* grp = ring + slot * kGroupPages * SHB;
@@ -646,17 +651,21 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // the prefix of group gi + 2 goes to slot (gi + 2) % 3, last read by group gi - 1
+    // the prefix of group gi + 2 goes to slot (gi + 2) % 3 and the table of
+    // group gi - 1 + cs_bufs to buffer (gi - 1) % cs_bufs: both last read by
+    // group gi - 1, once every wave is done with it
     const int slot2 = (gi + 2) % kRingSlots;
-    if (lockstep) {
-      if (gi + 2 < n_groups) store_prefix(pre_n, slot2);
-    } else {
-      count_wave(&s_sync[kRingSlots + slot]);   // done reading group gi
-      if (gi + 2 < n_groups) {
-        if (gi >= 1) wait_count(&s_sync[kRingSlots + slot2], kWaves * ((gi - 1) / kRingSlots + 1));
-        store_prefix(pre_n, slot2);
-        count_wave(&s_sync[slot2]);
-      }
+    count_wave(&s_sync[kRingSlots + slot]);   // done reading group gi (prefix and table)
+    const bool refill = gi >= 1 && gi - 1 + cs_bufs < n_groups;
+    if (gi >= 1 && (gi + 2 < n_groups || refill))
+      wait_count(&s_sync[kRingSlots + slot2], kWaves * ((gi - 1) / kRingSlots + 1));
+    if (gi + 2 < n_groups) {
+      store_prefix(pre_n, slot2);
+      count_wave(&s_sync[slot2]);
+    }
+    if (refill) {
+      produce_groups(gi - 1 + cs_bufs, 1, gi - 1);
+      count_wave(&s_tab[(gi - 1) % cs_bufs]);
     }
     if (active) {
 #pragma unroll
@@ -665,8 +674,6 @@ __global__ __launch_bounds__(kThreads) void k2b_decode_split_kernel(const Decode
         vcd[pp] = vcd_n[pp];
       }
     }
-    // with tables to refill in the loop, all waves move group by group
-    if (lockstep) __syncthreads();   // table of group gi+1 visible; group gi's slots free
   }
   // the window pairs this workgroup owns, on waves 0-3: of the two waves of a
   // SIMD (w, w + 4) these finish their groups first
