@@ -174,10 +174,11 @@ def fp16_comparator(args, torch, dev, ctx: int, our_us: float) -> dict:
     """The measured fp16 decode at the same context, the bar the packed path
     must beat: dense fp16 K/V of all ctx tokens per layer (8 KV heads, d 128),
     one query step of 32 heads, over args.layers distinct layers (8.6 GB at
-    64k and 32 layers, past the MALL).  Two forms, the faster reported: torch
-    SDPA with grouped heads (ROCm's own attention), and grouped bmm ->
+    64k and 32 layers, past the MALL).  Three forms, the fastest reported:
+    torch SDPA with grouped heads (ROCm's own attention), grouped bmm ->
     softmax -> bmm with the keys stored transposed (two skinny GEMMs that read
-    K and V once each)."""
+    K and V once each), and the library's dense fp16 split-KV decode kernel
+    (bmx_fp16_decode: a bandwidth kernel, every K and V byte read once)."""
     import torch.nn.functional as F
 
     gen = torch.Generator(device=dev).manual_seed(99)
@@ -195,6 +196,33 @@ def fp16_comparator(args, torch, dev, ctx: int, our_us: float) -> dict:
     def bmm(i):
         p = torch.softmax(torch.bmm(qg, KTs[i]).float() * scale, dim=-1).half()
         return torch.bmm(p, Vs[i][0])
+
+    # the library's dense fp16 decode kernel (include/bmx_bench.h): split-KV
+    # over the CUs, every K and V byte read once with wide coalesced loads
+    import ctypes as ct
+
+    from bmx_amd import _lib
+
+    n_split = 64
+    fd_out = torch.empty(H_KV, G, D, dtype=torch.float16, device=dev)
+    fd_ws = torch.empty(int(_lib.lib().bmx_fp16_decode_workspace_bytes(H_KV, G, n_split)), dtype=torch.uint8,
+                        device=dev)
+    fd_args = []
+    for i in range(n_l):
+        fa = _lib.Fp16DecodeArgs()
+        fa.q, fa.k, fa.v = qg.data_ptr(), Ks[i].data_ptr(), Vs[i].data_ptr()
+        fa.stride_h, fa.stride_t = ctx * D, D
+        fa.h_kv, fa.n_q_groups, fa.T, fa.n_split = H_KV, G, ctx, n_split
+        fa.sm_scale = scale
+        fa.out, fa.workspace, fa.workspace_bytes = fd_out.data_ptr(), fd_ws.data_ptr(), fd_ws.numel()
+        fd_args.append(fa)
+    fd_stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def hip_kernel(i):
+        rc = _lib.lib().bmx_fp16_decode(ct.byref(fd_args[i]), fd_stream)
+        if rc != 0:
+            raise RuntimeError(f"bmx_fp16_decode failed ({rc})")
+        return fd_out
 
     def timed(fn, reps=10):
         for _ in range(3):
@@ -219,14 +247,16 @@ def fp16_comparator(args, torch, dev, ctx: int, our_us: float) -> dict:
     except RuntimeError as e:   # a backend without grouped heads: the bmm form stands
         res["sdpa_error"] = str(e)[:200]
     res["bmm_us_per_call"] = round(timed(bmm), 3)
+    res["hip_kernel_vs_bmm_max_abs"] = (hip_kernel(0).float().view(-1) - ref).abs().max().item()
+    res["hip_kernel_us_per_call"] = round(timed(hip_kernel), 3)
     best = min(v for k, v in res.items() if k.endswith("_us_per_call"))
     nbytes = ctx * H_KV * D * 2 * 2
-    res.update({"kind": "dense fp16 K/V decode on the same GPU (faster of the two forms)",
+    res.update({"kind": "dense fp16 K/V decode on the same GPU (fastest of the three forms)",
                 "us_per_call": best, "bytes_per_call": nbytes,
                 "achieved_GBs": round(nbytes / (best * 1e-6) / 1e9, 1),
                 "packed_speedup": round(best / our_us, 3),
                 "fp16_roofline_us": round(nbytes / HBM_PEAK_GBS / 1e3, 3)})
-    del Ks, Vs, KTs
+    del Ks, Vs, KTs, fd_ws, fd_out
     torch.cuda.empty_cache()
     return res
 

@@ -253,6 +253,17 @@ class SpectralMergeArgs(ct.Structure):
                 ("v_codec", ct.c_int32), ("v_sign_bits_c", ct.c_uint32 * 32), ("win_dtype", ct.c_int32)]
 
 
+class Fp16DecodeArgs(ct.Structure):
+    """bmx_fp16_decode_args (include/bmx_bench.h): the dense fp16 comparator."""
+    _fields_ = [
+        ("q", ct.c_void_p), ("k", ct.c_void_p), ("v", ct.c_void_p),
+        ("stride_h", ct.c_int64), ("stride_t", ct.c_int64),
+        ("h_kv", ct.c_int), ("n_q_groups", ct.c_int), ("T", ct.c_int), ("n_split", ct.c_int),
+        ("sm_scale", ct.c_float),
+        ("out", ct.c_void_p), ("workspace", ct.c_void_p), ("workspace_bytes", ct.c_size_t),
+    ]
+
+
 EXPORTS = {
     "bmx_last_error": (ct.c_char_p, []),
     "bmx_k2b_page_bytes": (ct.c_size_t, [ct.POINTER(Geom)]),
@@ -274,6 +285,8 @@ EXPORTS = {
     "bmx_spectral_dequant": (ct.c_int32, [ct.POINTER(SpectralDequantArgs), ct.c_void_p]),
     "bmx_spectral_merge": (ct.c_int32, [ct.POINTER(SpectralMergeArgs), ct.c_void_p]),
     "bmx_spectral_partial_count": (ct.c_int32, [ct.POINTER(SpectralDequantArgs)]),
+    "bmx_fp16_decode_workspace_bytes": (ct.c_size_t, [ct.c_int, ct.c_int, ct.c_int]),
+    "bmx_fp16_decode": (ct.c_int, [ct.POINTER(Fp16DecodeArgs), ct.c_void_p]),
 }
 
 _LIB = None

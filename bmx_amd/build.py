@@ -37,6 +37,7 @@ SOURCES = {
     "rtn.hip": ["-ffp-contract=off"],
     "spectral.hip": ["-ffp-contract=off"],
     "k2b_general.hip": ["-ffp-contract=off"],
+    "fp16_decode.hip": ["-ffp-contract=fast"],
 }
 
 
