@@ -3,21 +3,24 @@
 // bytes an fp16 KV cache reads).  Not a path of the packed cache.
 //
 // fp16_decode_split_kernel: grid (splits, h_kv), block 256 (4 waves).  The
-// workgroup streams its head's token range in 64-token chunks, the next
-// chunk's K and V rows loaded into registers while the current one is used:
-//   * scores: thread (token i / 4, quarter i % 4) takes 32 channels of one
-//     key row (64 contiguous bytes), dots them with the G queries (packed
-//     fp16 dot products, fp32 sums) and the quarters meet by quad DPP;
-//   * softmax: wave g takes query g's 64 scores (one per lane), online over
-//     the chunks (running max and sum, base 2);
-//   * P.V: thread (token lane i / 32, channel quad i % 32) takes tokens
-//     lane + 8k of the chunk, 4 channels each (8 contiguous bytes), and sums
-//     p * v in fp32; the 8 token lanes meet in LDS at the end.
+// workgroup's token range is cut into 32-token chunks and wave w takes
+// tokens 8 w .. 8 w + 7 of each chunk (one "step").  Inside a wave, lane
+// (row r = lane / 16, channel octet c = lane % 16) holds channels 8 c .. +7
+// of tokens r and r + 4 of the step, for K and for V (16-byte loads; a
+// 16-lane row reads 256 contiguous bytes).  The 4 rows are 4 independent
+// online-softmax streams (token residue mod 4), so the loop has no exchange
+// between rows or waves:
+//   * scores: packed fp16 dot products over the lane's 8 channels, summed
+//     over the row's 16 lanes by DPP (every lane of the row gets the sum);
+//   * softmax: running max and sum per (row, query), base 2;
+//   * P.V: the lane's own 8 channels of its tokens, fp32.
+// Loads run NB - 1 steps ahead in a register ring of NB steps, so 12-20 KB
+// per wave is in flight without any LDS.  The 16 streams of the workgroup
+// meet in LDS at the end and leave one partial per (query, split).
 // fp16_decode_merge_kernel: one workgroup per (head, query): the splits'
 // partials by their softmax weights, 8 split lanes in parallel.
 //
-// Both are plain bandwidth kernels: every K and V byte is read once, with
-// 16-byte (keys) and 8-byte (values) coalesced loads.
+// Both are plain bandwidth kernels: every K and V byte is read once.
 
 #include "bmx_bench.h"
 
@@ -31,13 +34,13 @@ namespace bmx {
 namespace {
 
 constexpr int kFdD = 128;          // head dim
-constexpr int kFdChunk = 64;       // tokens per chunk
+constexpr int kFdChunk = 64;       // bound on the tokens of a workgroup step (offset checks)
 constexpr int kFdThreads = 256;
 constexpr int kFdMaxG = 8;
+constexpr int kFdBufWord3 = 0x00020000;   // raw buffer descriptor, word 3
 
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t fd_u4 __attribute__((ext_vector_type(4)));
-typedef uint32_t fd_u2 __attribute__((ext_vector_type(2)));
 
 struct FdArgs {
   const uint16_t* q;      // [h_kv][G][128] fp16
@@ -51,156 +54,173 @@ struct FdArgs {
 
 __device__ __forceinline__ f16x2_t h2(uint32_t u) { return __builtin_bit_cast(f16x2_t, u); }
 
+template <int Ctrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), Ctrl, 0xF, 0xF, true));
+}
+
+// sum over the 16 lanes of a DPP row; every lane of the row gets it
+__device__ __forceinline__ float row16_sum(float s) {
+  s += dpp_mov<0xB1>(s);    // quad_perm [1,0,3,2]
+  s += dpp_mov<0x4E>(s);    // quad_perm [2,3,0,1]
+  s += dpp_mov<0x124>(s);   // row_ror 4
+  s += dpp_mov<0x128>(s);   // row_ror 8
+  return s;
+}
+
+// ring shape per query count: TPR tokens per row per step, NB steps in the
+// ring (NB - 1 in flight), W waves per SIMD asked of the register allocator
+// (measured at 64k tokens, 8 heads, 4 queries: 51.3 us per call at NB 4 with
+// 3 waves, 52.3 at NB 5 with 2, 51.0-53.5 from NB 6 to 8)
 template <int G>
-__global__ __launch_bounds__(kFdThreads) void fp16_decode_split_kernel(const FdArgs a) {
+struct FdRing {
+  static constexpr int TPR = 2;
+  static constexpr int NB = G >= 8 ? 4 : (G >= 4 ? 4 : 6);
+  static constexpr int W = G >= 8 ? 2 : 3;
+};
+
+template <int G>
+__global__ __launch_bounds__(kFdThreads) __attribute__((amdgpu_waves_per_eu(FdRing<G>::W)))
+void fp16_decode_split_kernel(const FdArgs a) {
+  constexpr int NB = FdRing<G>::NB, TPR = FdRing<G>::TPR;
+  constexpr int kStepTok = 4 * TPR, kChunk = 4 * kStepTok;   // tokens per wave step, per workgroup step
   const int split = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int n_chunks = (a.T + kFdChunk - 1) / kFdChunk;
+  const int wave = tid >> 6, lane = tid & 63, r = lane >> 4, c8 = lane & 15;
+  const int n_chunks = (a.T + kChunk - 1) / kChunk;
   const int c0 = (int)((int64_t)split * n_chunks / a.n_split), c1 = (int)((int64_t)(split + 1) * n_chunks / a.n_split);
-  __shared__ float s_sc[kFdMaxG][kFdChunk];
-  __shared__ float s_p[kFdMaxG][kFdChunk];
-  __shared__ float s_alpha[kFdMaxG];
-  __shared__ float s_red[8][kFdMaxG][kFdD];   // the token lanes' channel sums at the end
-  // scores: token tt, quarter qq (channels 32 qq .. + 31)
-  const int tt = tid >> 2, qq = tid & 3;
-  uint32_t qv[G][16];   // the queries' 32 channels of this quarter, fp16 pairs
+  const int n_steps = c1 - c0;
+  // K and V of the head through buffer descriptors: rows past T read zeros
+  // (and are masked), offsets are 32-bit
+  const uint32_t nrec = (uint32_t)((int64_t)a.T * a.st * 2);
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.k + (int64_t)h * a.sh), (short)0, nrec, kFdBufWord3);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.v + (int64_t)h * a.sh), (short)0, nrec, kFdBufWord3);
+  // byte offset of token (step s, j): chunk base + kStepTok wave + r + 4 j
+  const uint32_t lane_off = (uint32_t)(((int64_t)(kStepTok * wave + r) * a.st + 8 * c8) * 2);
+  const uint32_t tok4_off = (uint32_t)(4 * a.st * 2);
+  const uint32_t chunk_off = (uint32_t)((int64_t)kChunk * a.st * 2);
+
+  uint32_t qv[G][4];   // the queries' channels 8 c8 .. +7, fp16 pairs
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const uint4* src = reinterpret_cast<const uint4*>(a.q + ((int64_t)h * a.G + g) * kFdD + 32 * qq);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 w = src[i];
-      qv[g][4 * i] = w.x; qv[g][4 * i + 1] = w.y; qv[g][4 * i + 2] = w.z; qv[g][4 * i + 3] = w.w;
-    }
+    const uint4 w = *reinterpret_cast<const uint4*>(a.q + ((int64_t)h * a.G + g) * kFdD + 8 * c8);
+    qv[g][0] = w.x; qv[g][1] = w.y; qv[g][2] = w.z; qv[g][3] = w.w;
   }
-  // P.V: token lane tl (tokens tl + 8 k), channel quad cq (channels 4 cq .. + 3)
-  const int tl = tid >> 5, cq = tid & 31;
-  const uint16_t* kh = a.k + (int64_t)h * a.sh;
-  const uint16_t* vh = a.v + (int64_t)h * a.sh;
-  auto load_k = [&](int c, uint4 kw[4]) {
-    const int t = min(c * kFdChunk + tt, a.T - 1);
-    const fd_u4* src = reinterpret_cast<const fd_u4*>(kh + (int64_t)t * a.st + 32 * qq);
+  float m[G], l[G], acc[G][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const fd_u4 w = __builtin_nontemporal_load(src + i);
-      kw[i] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+  }
+  fd_u4 kb[NB][TPR], vb[NB][TPR];
+  auto issue = [&](int s, fd_u4 kd[TPR], fd_u4 vd[TPR]) {
+    const uint32_t base = (uint32_t)(c0 + s) * chunk_off + lane_off;
+#pragma unroll
+    for (int j = 0; j < TPR; ++j) kd[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, base + j * tok4_off, 0, 2);
+#pragma unroll
+    for (int j = 0; j < TPR; ++j) vd[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, base + j * tok4_off, 0, 2);
   };
-  auto load_v = [&](int c, uint2 vw[8]) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int t = min(c * kFdChunk + tl + 8 * k, a.T - 1);
-      const fd_u2 w = __builtin_nontemporal_load(reinterpret_cast<const fd_u2*>(vh + (int64_t)t * a.st + 4 * cq));
-      vw[k] = make_uint2(w[0], w[1]);
-    }
-  };
-  __shared__ float s_m[kFdMaxG], s_l[kFdMaxG];   // query g's running max and sum (base 2)
-  if (tid < kFdMaxG) {
-    s_m[tid] = -INFINITY;
-    s_l[tid] = 0.f;
-  }
-  float acc[G][4];
+  for (int b = 0; b < NB - 1; ++b)
+    if (b < n_steps) issue(b, kb[b], vb[b]);
+
+  for (int s0 = 0; s0 < n_steps; s0 += NB) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int b = 0; b < NB; ++b) {
+      const int s = s0 + b;
+      if (s >= n_steps) break;
+      if (s + NB - 1 < n_steps) issue(s + NB - 1, kb[(b + NB - 1) % NB], vb[(b + NB - 1) % NB]);
+      const int t_first = (c0 + s) * kChunk + kStepTok * wave + r;   // token of j = 0; j adds 4 j
+      // ---- scores of the lane's tokens for every query
+      float p[G][TPR];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[g][i] = 0.f;
-  uint4 kw[4], kn[4];
-  uint2 vw[8], vn[8];
-  if (c0 < c1) {
-    load_k(c0, kw);
-    load_v(c0, vw);
-  }
-  for (int c = c0; c < c1; ++c) {
-    if (c + 1 < c1) {   // the next chunk in flight while this one is used
-      load_k(c + 1, kn);
-      load_v(c + 1, vn);
-    }
-    const int t_tok = c * kFdChunk + tt;
-    // ---- scores of this thread's token for every query
-    float sc[G];
+      for (int j = 0; j < TPR; ++j) {
+        const fd_u4 kw = kb[b][j];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float s = 0.f;
+        for (int g = 0; g < G; ++g) {
+          float x = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t w4[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_fdot2(h2(w4[e]), h2(qv[g][4 * i + e]), s, false);
+          for (int e = 0; e < 4; ++e) x = __builtin_amdgcn_fdot2(h2(kw[e]), h2(qv[g][e]), x, false);
+          x = row16_sum(x);
+          p[g][j] = t_first + 4 * j < a.T ? x * a.qscale : -INFINITY;
+        }
       }
-      // the four quarters of the token (lanes 4tt .. 4tt + 3 of a row of 16)
-      s += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, s), 0xB1, 0xF, 0xF, true));
-      s += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, s), 0x4E, 0xF, 0xF, true));
-      sc[g] = t_tok < a.T ? s * a.qscale : -INFINITY;
-    }
-    if (qq == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) s_sc[g][tt] = sc[g];
-    }
-    __syncthreads();
-    // ---- online softmax: wave g % 4 takes query g, lane = token
-    for (int g = wave; g < G; g += 4) {
-      const float x = s_sc[g][lane];
-      float mx = x;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-      const float m_old = s_m[g];
-      const float m_new = fmaxf(m_old, mx);
-      const float alpha = m_old == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_old - m_new);
-      const float p = x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x - m_new);
-      float ps = p;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o);
-      s_p[g][lane] = p;
-      if (lane == 0) {
-        s_alpha[g] = alpha;
-        s_m[g] = m_new;
-        s_l[g] = __builtin_fmaf(s_l[g], alpha, ps);
-      }
-    }
-    __syncthreads();
-    // ---- P.V over the chunk
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float al = s_alpha[g];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[g][i] *= al;
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const f16x2_t v01 = h2(vw[k].x), v23 = h2(vw[k].y);
-      const float v4[4] = {(float)v01[0], (float)v01[1], (float)v23[0], (float)v23[1]};
+      // ---- online softmax per query: p becomes the weights, acc is rescaled
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float p = s_p[g][tl + 8 * k];
+        float mx = p[g][0];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[g][i] = __builtin_fmaf(p, v4[i], acc[g][i]);
+        for (int j = 1; j < TPR; ++j) mx = fmaxf(mx, p[g][j]);
+        const float mn = fmaxf(m[g], mx);
+        // a stream with no token yet (its tokens all past T) keeps m = -inf
+        const float ms = mn == -INFINITY ? 0.f : mn;
+        const float al = __builtin_amdgcn_exp2f(m[g] - ms);   // 0 when m was -inf
+        float ps = 0.f;
+#pragma unroll
+        for (int j = 0; j < TPR; ++j) {
+          p[g][j] = __builtin_amdgcn_exp2f(p[g][j] - ms);
+          ps += p[g][j];
+        }
+        l[g] = __builtin_fmaf(l[g], al, ps);
+        m[g] = mn;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] *= al;
+      }
+      // ---- P.V: token by token, its 8 channels in fp32
+#pragma unroll
+      for (int j = 0; j < TPR; ++j) {
+        const fd_u4 vw = vb[b][j];
+        float vf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2_t p2 = h2(vw[e]);
+          vf[2 * e] = (float)p2[0];
+          vf[2 * e + 1] = (float)p2[1];
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[g][i] = __builtin_fmaf(p[g][j], vf[i], acc[g][i]);
       }
     }
-    if (c + 1 < c1) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) kw[i] = kn[i];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) vw[k] = vn[k];
-    }
-    __syncthreads();   // s_sc / s_p / s_alpha reused by the next chunk
   }
-  // ---- the token lanes meet; (m, l) from their waves
+  // ---- the 16 streams (4 waves x 4 rows) meet: stream st = 4 wave + r
+  __shared__ float s_ml[16][G][2];
+  __shared__ float s_x[16][G][kFdD];
+  const int stream = 4 * wave + r;
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int g = 0; g < G; ++g) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s_red[tl][g][4 * cq + i] = acc[g][i];
+    for (int i = 0; i < 8; ++i) s_x[stream][g][8 * c8 + i] = acc[g][i];
+    if (c8 == 0) {
+      s_ml[stream][g][0] = m[g];
+      s_ml[stream][g][1] = l[g];
+    }
+  }
   __syncthreads();
   for (int e = tid; e < G * kFdD; e += kFdThreads) {
     const int g = e / kFdD, ch = e % kFdD;
-    float s = 0.f;
+    float M = -INFINITY;   // streams that saw no token keep -inf and weigh 0
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += s_red[j][g][ch];
-    a.part[(((int64_t)h * a.G + g) * a.n_split + split) * (2 + kFdD) + 2 + ch] = s;
-  }
-  if (tid < G) {
-    float* dst = a.part + (((int64_t)h * a.G + tid) * a.n_split + split) * (2 + kFdD);
-    dst[0] = s_m[tid];
-    dst[1] = s_l[tid];
+    for (int j = 0; j < 16; ++j) M = fmaxf(M, s_ml[j][g][0]);
+    float L = 0.f, X = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float w = __builtin_amdgcn_exp2f(s_ml[j][g][0] - M);   // 0 for an empty stream
+        L = __builtin_fmaf(w, s_ml[j][g][1], L);
+        X = __builtin_fmaf(w, s_x[j][g][ch], X);
+      }
+    }
+    float* dst = a.part + (((int64_t)h * a.G + g) * a.n_split + split) * (2 + kFdD);
+    dst[2 + ch] = X;
+    if (ch == 0) {
+      dst[0] = M;
+      dst[1] = L;
+    }
   }
 }
 
@@ -211,8 +231,8 @@ struct FdMergeArgs {
 };
 
 // block 256: thread (split lane sl = tid / 32, channel quad cq = tid % 32)
-// takes splits sl, sl + 8, ... for channels 4 cq .. + 3, online; the 8 split
-// lanes meet in LDS.
+// takes splits sl, sl + 8, ... for channels 4 cq .. + 3, 8 splits' loads at a
+// time; the 8 split lanes meet in LDS.
 __global__ __launch_bounds__(256) void fp16_decode_merge_kernel(const FdMergeArgs a) {
   const int row = blockIdx.x, tid = threadIdx.x, sl = tid >> 5, cq = tid & 31;
   const float* base = a.part + (int64_t)row * a.n_split * (2 + kFdD);
@@ -220,16 +240,27 @@ __global__ __launch_bounds__(256) void fp16_decode_merge_kernel(const FdMergeArg
   __shared__ float4 s_x[8][32];
   float m = -INFINITY, l = 0.f;
   float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int sp = sl; sp < a.n_split; sp += 8) {
-    const float* p = base + (int64_t)sp * (2 + kFdD);
-    const float ms = p[0];
-    if (ms == -INFINITY) continue;
-    const float4 v = *reinterpret_cast<const float4*>(p + 2 + 4 * cq);
-    const float mn = fmaxf(m, ms);
-    const float al = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn), w = __builtin_amdgcn_exp2f(ms - mn);
-    l = l * al + w * p[1];
-    x = make_float4(x.x * al + w * v.x, x.y * al + w * v.y, x.z * al + w * v.z, x.w * al + w * v.w);
-    m = mn;
+  for (int sp0 = sl; sp0 < a.n_split; sp0 += 64) {
+    float ms[8], ls[8];
+    float4 vs[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int sp = sp0 + 8 * u;
+      const float* p = base + (int64_t)min(sp, a.n_split - 1) * (2 + kFdD);
+      ms[u] = sp < a.n_split ? p[0] : -INFINITY;
+      ls[u] = p[1];
+      vs[u] = *reinterpret_cast<const float4*>(p + 2 + 4 * cq);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (ms[u] == -INFINITY) continue;
+      const float mn = fmaxf(m, ms[u]);
+      const float al = __builtin_amdgcn_exp2f(m - mn), w = __builtin_amdgcn_exp2f(ms[u] - mn);
+      l = l * al + w * ls[u];
+      x = make_float4(x.x * al + w * vs[u].x, x.y * al + w * vs[u].y, x.z * al + w * vs[u].z,
+                      x.w * al + w * vs[u].w);
+      m = mn;
+    }
   }
   if (cq == 0) {
     s_m[sl] = m;
@@ -276,6 +307,8 @@ extern "C" int bmx_fp16_decode(const bmx_fp16_decode_args* a, void* stream) {
     return BMX_BENCH_E_INVALID;
   if (a->workspace_bytes < bmx_fp16_decode_workspace_bytes(a->h_kv, a->n_q_groups, a->n_split))
     return BMX_BENCH_E_INVALID;
+  // one head's rows are addressed with 32-bit byte offsets (buffer loads)
+  if ((int64_t)(a->T + kFdChunk) * a->stride_t * 2 > INT32_MAX) return BMX_BENCH_E_INVALID;
   FdArgs k{};
   k.q = static_cast<const uint16_t*>(a->q);
   k.k = static_cast<const uint16_t*>(a->k);

@@ -1,7 +1,8 @@
 """The dense fp16 decode kernel bench.py's comparator runs (bmx_fp16_decode,
 include/bmx_bench.h) against a plain fp32 PyTorch attention of the same
 step: every query group size it takes, token counts that leave a partial
-last chunk and more splits than chunks, strided head layouts."""
+last chunk, more splits than chunks and token streams with no token at all
+(5 tokens), strided head layouts."""
 import ctypes as ct
 
 import pytest
@@ -36,7 +37,7 @@ def _ref(q, K, V, sm_scale):
 
 
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
-@pytest.mark.parametrize("T,n_split", [(1000, 7), (4096, 16), (333, 12)])
+@pytest.mark.parametrize("T,n_split", [(1000, 7), (4096, 16), (333, 12), (5, 1), (37, 3)])
 def test_fp16_decode_matches_fp32_attention(G, T, n_split):
     gen = torch.Generator(device=DEV).manual_seed(T + G)
     h, D = 8, 128
