@@ -73,6 +73,14 @@ __device__ __forceinline__ void store_elem(void* base, int64_t idx, float v, int
   }
 }
 
+// v as computed in fp32, opaque to the compiler: a product that made v is not
+// fused with a later conversion to 16 bits (v_fma_mix*, one rounding), so the
+// conversion rounds the fp32 value, as a stored fp32 tensor converted later.
+__device__ __forceinline__ float fp32_rounded(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
@@ -171,11 +179,57 @@ __device__ __forceinline__ int kres_pair_code(uint32_t w0, uint32_t w1, uint32_t
 }
 
 constexpr int kDqPad = kD + 4;   // staging row stride (floats)
+constexpr int kDqPad16 = kD + 8; // staging row stride (16-bit elements): 272-byte rows, 16-byte aligned
 constexpr int kCsPad = 68;       // cos/sin table row stride (floats): 16-byte reads of 16 rows hit distinct banks
 
+// A wave's 16-token staging tile: fp32 (fp32 output) or the output's 16-bit
+// bits (DT = BMX_K2B_F16 or BMX_K2B_BF16 output: each value rounded once,
+// when it is put).
 struct DqTile {
   float v[kPT][kDqPad];
 };
+template <int DT>
+struct DqTile16 {
+  uint16_t v[kPT][kDqPad16];
+};
+
+// Order a wave's LDS writes before its later LDS reads (of other lanes'
+// data): no compiler motion across it, every LDS operation of the wave done.
+__device__ __forceinline__ void wave_lds_order() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ uint16_t to_bits16(float v, int dtype) {
+  if (dtype == 2) {   // BMX_K2B_BF16
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = (u & 0x7fffffffu) > 0x7f800000u ? (u | 0x00400000u) : u + 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+  }
+  return float_to_half_bits(v);
+}
+
+__device__ __forceinline__ void tile_put(DqTile& tl, int t, int c, float v, int) { tl.v[t][c] = v; }
+// the value rounded to fp32, then to 16 bits (as an fp32 tile stored and
+// converted later)
+template <int DT>
+__device__ __forceinline__ void tile_put(DqTile16<DT>& tl, int t, int c, float v, int) {
+  tl.v[t][c] = to_bits16(fp32_rounded(v), DT);
+}
+
+// channels c .. c + 3 (c a multiple of 4) of row t
+__device__ __forceinline__ void tile_put4(DqTile& tl, int t, int c, const float (&v)[4], int) {
+  *reinterpret_cast<float4_t*>(&tl.v[t][c]) = float4_t{v[0], v[1], v[2], v[3]};
+}
+template <int DT>
+__device__ __forceinline__ void tile_put4(DqTile16<DT>& tl, int t, int c, const float (&v)[4], int) {
+  uint16_t b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = to_bits16(fp32_rounded(v[i]), DT);
+  *reinterpret_cast<uint2*>(&tl.v[t][c]) = make_uint2(b[0] | (uint32_t)b[1] << 16, b[2] | (uint32_t)b[3] << 16);
+}
 
 // row t = lane / 4, columns 32 (lane % 4) .. + 31 of the wave's staging tile
 // to out rows base + t (elements of dtype)
@@ -193,15 +247,19 @@ __device__ __forceinline__ void dq_store_tile(const DqTile& tl, void* out, int64
     for (int u = 0; u < 4; ++u) {
       uint16_t hbits[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        uint16_t tmp[1];
-        store_elem(tmp, 0, src[8 * u + e], dtype);
-        hbits[e] = tmp[0];
-      }
+      for (int e = 0; e < 8; ++e) hbits[e] = to_bits16(src[8 * u + e], dtype);
       dst[u] = make_uint4(hbits[0] | (uint32_t)hbits[1] << 16, hbits[2] | (uint32_t)hbits[3] << 16,
                           hbits[4] | (uint32_t)hbits[5] << 16, hbits[6] | (uint32_t)hbits[7] << 16);
     }
   }
+}
+template <int DT>
+__device__ __forceinline__ void dq_store_tile(const DqTile16<DT>& tl, void* out, int64_t row0, int) {
+  const int lane = threadIdx.x & 63, t = lane >> 2, c0 = 32 * (lane & 3);
+  const uint4* src = reinterpret_cast<const uint4*>(&tl.v[t][c0]);
+  uint4* dst = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + (row0 + t) * kD + c0);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) dst[u] = src[u];
 }
 
 // Arguments of the k2b write kernels (k2b_append.hip).
@@ -237,16 +295,45 @@ __device__ __forceinline__ float level4(uint32_t c, float l0, float l1, float l2
   return (c & 2u) ? hi : lo;
 }
 
+// x of lane n ^ HB of the lane's 16-lane row (HB 1, 2, 4 or 8), by DPP:
+// quad_perm [1,0,3,2] and [2,3,0,1] for bits 0 and 1; bit 2 as the half-row
+// mirror (n ^ 7) followed by quad_perm [3,2,1,0] (^ 3); bit 3 as a row
+// rotation by 8.
+template <int HB>
+__device__ __forceinline__ float xor_row16(float x) {
+  const int v = __builtin_bit_cast(int, x);
+  if constexpr (HB == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true));
+  if constexpr (HB == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true));
+  if constexpr (HB == 4)
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF, true));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, true));
+}
+
+// one stage of H16 over n across the row: (y, partner o) -> y + o on the
+// lanes with bit HB of n clear, o - y on the others, as o + s y with s = +-1
+// (s y exact: the same one rounding as either sum)
+template <int HB>
+__device__ __forceinline__ void h16_stage(float (&y)[4][8], int n) {
+  const float s = (n & HB) ? -1.f : 1.f;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int b = 0; b < 8; ++b) y[tt][b] = xor_row16<HB>(y[tt][b]) + s * y[tt][b];
+}
+
 // The rotated-domain values y of one 16-token value tile back to channels:
 // lane 16q + n holds y[tt][b] of token 4q + tt, rotated channel 16b + n; H128
 // (H8 over b, H16 over n across the row), times inv_d and the signs, times
-// the token norms, into tl.v[token][channel].
+// the token norms, into the staging tile at [token][channel].
+// (kFirstHb 2: the H8 stage over bit 0 of b is already applied)
+template <class Tile, int kFirstHb = 1>
 __device__ __forceinline__ void dq_value_tile_rot(float (&y)[4][8], uint2 nrm, const uint32_t sign_bits[4],
-                                                  float inv_d, int n, int q, DqTile& tl) {
+                                                  float inv_d, int n, int q, Tile& tl, int dtype) {
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
-    for (int hb = 1; hb < 8; hb <<= 1)   // H8 over b
+    for (int hb = kFirstHb; hb < 8; hb <<= 1)   // H8 over b
 #pragma unroll
       for (int b = 0; b < 8; ++b)
         if (!(b & hb)) {
@@ -254,14 +341,11 @@ __device__ __forceinline__ void dq_value_tile_rot(float (&y)[4][8], uint2 nrm, c
           y[tt][b] = u + w;
           y[tt][b | hb] = u - w;
         }
-#pragma unroll
-    for (int hb = 1; hb < 16; hb <<= 1)   // H16 over n, across the row
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const float o = __shfl_xor(y[tt][b], hb);
-        y[tt][b] = (n & hb) ? o - y[tt][b] : y[tt][b] + o;
-      }
   }
+  h16_stage<1>(y, n);   // H16 over n, across the row
+  h16_stage<2>(y, n);
+  h16_stage<4>(y, n);
+  h16_stage<8>(y, n);
   const float nv[4] = {half_bits_to_float(nrm.x & 0xffff), half_bits_to_float(nrm.x >> 16),
                        half_bits_to_float(nrm.y & 0xffff), half_bits_to_float(nrm.y >> 16)};
 #pragma unroll
@@ -271,13 +355,14 @@ __device__ __forceinline__ void dq_value_tile_rot(float (&y)[4][8], uint2 nrm, c
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const float v = y[tt][b] * inv_d;   // inv_d a power of two: exact
-      tl.v[4 * q + tt][c] = (neg ? -v : v) * nv[tt];
+      tile_put(tl, 4 * q + tt, c, (neg ? -v : v) * nv[tt], dtype);
     }
   }
 }
 
+template <class Tile>
 __device__ __forceinline__ void dq_value_tile(uint2 vcd, uint2 nrm, const float codebook[4],
-                                              const uint32_t sign_bits[4], int n, int q, DqTile& tl) {
+                                              const uint32_t sign_bits[4], int n, int q, Tile& tl, int dtype) {
   const float l0 = codebook[0], l1 = codebook[1], l2 = codebook[2], l3 = codebook[3];
   float y[4][8];
 #pragma unroll
@@ -286,7 +371,43 @@ __device__ __forceinline__ void dq_value_tile(uint2 vcd, uint2 nrm, const float 
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) y[tt][b] = level4((D >> (8 * (b & 3) + 2 * tt)) & 3u, l0, l1, l2, l3);
   }
-  dq_value_tile_rot(y, nrm, sign_bits, 1.0f / (float)kD, n, q, tl);
+  dq_value_tile_rot(y, nrm, sign_bits, 1.0f / (float)kD, n, q, tl, dtype);
+}
+
+// Level pair table of a 2-bit codebook: entry a + 4 b (codes a, b) holds
+// (l[a] + l[b], l[a] - l[b]), the first H8 stage of channel blocks 2k, 2k + 1
+// (codes a, b of one token).  Built by the first 16 threads.
+struct DqPairLut {
+  float2 e[16];
+};
+__device__ __forceinline__ void dq_pair_lut_build(DqPairLut& t, const float codebook[4]) {
+  const int i = threadIdx.x;
+  if (i < 16) {
+    const float la = codebook[i & 3], lb = codebook[i >> 2];
+    t.e[i] = make_float2(la + lb, la - lb);
+  }
+}
+
+// dq_value_tile with the codebook levels and the first H8 stage from the
+// pair table (same values, same operations as the select chain and the
+// in-register stage)
+template <class Tile>
+__device__ __forceinline__ void dq_value_tile_lut(uint2 vcd, uint2 nrm, const DqPairLut& lut,
+                                                  const uint32_t sign_bits[4], int n, int q, Tile& tl, int dtype) {
+  float y[4][8];
+#pragma unroll
+  for (int bp = 0; bp < 4; ++bp) {   // blocks 2 bp, 2 bp + 1: bytes (2 bp) & 3 and (2 bp + 1) & 3 of a word
+    const uint32_t D = bp < 2 ? vcd.x : vcd.y;
+    const uint32_t x = D >> (16 * (bp & 1));
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const uint32_t idx = ((x >> (2 * tt)) & 3u) | (((x >> (8 + 2 * tt)) & 3u) << 2);
+      const float2 e = lut.e[idx];
+      y[tt][2 * bp] = e.x;
+      y[tt][2 * bp + 1] = e.y;
+    }
+  }
+  dq_value_tile_rot<Tile, 2>(y, nrm, sign_bits, 1.0f / (float)kD, n, q, tl, dtype);
 }
 
 }  // namespace bmx

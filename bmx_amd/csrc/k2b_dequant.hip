@@ -33,12 +33,20 @@ struct DequantKArgs {
 //   values: the lane's code bytes (channel 16b + n, tokens 4q .. 4q + 3) give
 //   codebook levels, H8 over b in registers and H16 over n across the row's
 //   lanes make the 128-point Hadamard, then 1/128, signs and the norm;
-// each tile goes through a per-wave LDS staging tile so that the dense rows
-// are written with 16-byte coalesced stores, rounded once to the output type.
+// each tile goes through a per-wave LDS staging tile (the output's 16-bit
+// bits for fp16 / bf16, else fp32: 26 or 43 KB a workgroup with the table)
+// so that the dense rows are written with 16-byte coalesced stores, rounded
+// once to the output type.  At 16-bit tiles and 5 waves per SIMD (at most
+// 102 VGPRs) an 8k-token prefill's 1,072 workgroups are all resident at once.
+// The codebook levels and the first H8 stage come from a 16-entry pair table
+// (dq_value_tile_lut), the key's code * scale + low-rank part is one fma.
+// Only the cos/sin table is shared between waves; a wave's own tile is
+// ordered by its own LDS waits.
 constexpr int kDqWaves = 4;
 
-template <int R>
-__global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const DequantKArgs a) {
+template <int R, class Tile>
+__global__ __launch_bounds__(64 * kDqWaves) __attribute__((amdgpu_waves_per_eu(5)))
+void k2b_dequant_kernel(const DequantKArgs a) {
   constexpr int KQ = R / 4;
   typedef _Float16 hvec_t __attribute__((ext_vector_type(KQ)));
   const int lp = blockIdx.x;
@@ -48,7 +56,8 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
   const int h = active ? h_raw : 0;
   const int C = kD * a.h_kv, quarter = C / 4;
   __shared__ __align__(16) float s_cs[2][kPT][kCsPad];   // rows padded: conflict-free 16-byte reads
-  __shared__ DqTile s_tile[kDqWaves];
+  __shared__ Tile s_tile[kDqWaves];
+  __shared__ DqPairLut s_lut;
 
   // ---- every load first ----
   const uint8_t* page = a.pages + clamp_page(a.page_table[lp], a.n_pool) * a.L.bytes;
@@ -79,8 +88,8 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
       cn *= a.rope_scaling;
       sn *= a.rope_scaling;
       if (a.apply_rope == 2) {   // the reference's fp16 tables
-        cn = half_bits_to_float(float_to_half_bits(cn));
-        sn = half_bits_to_float(float_to_half_bits(sn));
+        cn = half_bits_to_float(float_to_half_bits(fp32_rounded(cn)));
+        sn = half_bits_to_float(float_to_half_bits(fp32_rounded(sn)));
       }
       s_cs[0][t][j] = cn;
       s_cs[1][t][j] = sn;
@@ -97,24 +106,25 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
     else
       kt[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh[bt], us, z, 0, 0, 0);
   }
+  dq_pair_lut_build(s_lut, a.codebook);
   KresMasks km;
   km.init();
   half2_t cp[16];
   kres_pairs(km, kres.x, kres.y, kres.z, cp);
   __syncthreads();   // s_cs
-  DqTile& tl = s_tile[wave];
+  Tile& tl = s_tile[wave];
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
     const uint32_t sv[4] = {scl[bb].x, scl[bb].y, scl[bb].z, scl[bb].w};
     const float4_t c4 = *reinterpret_cast<const float4_t*>(&s_cs[0][n][16 * bb + 4 * q]);
     const float4_t s4 = *reinterpret_cast<const float4_t*>(&s_cs[1][n][16 * bb + 4 * q]);
+    float o0[4], o1[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int j = 16 * bb + 4 * q + i;
       const half2_t s2 = as_h2(sv[i]);
-      // L + code * scale in fp32 (the product is exact)
-      float k0 = kt[bb][i] + (float)cp[4 * bb + i][0] * (float)s2[0];
-      float k1 = kt[bb + 4][i] + (float)cp[4 * bb + i][1] * (float)s2[1];
+      // L + code * scale in fp32: the product is exact, so the fma rounds as the sum does
+      float k0 = __builtin_fmaf((float)cp[4 * bb + i][0], (float)s2[0], kt[bb][i]);
+      float k1 = __builtin_fmaf((float)cp[4 * bb + i][1], (float)s2[1], kt[bb + 4][i]);
       if (a.apply_rope) {
         const float c = c4[i], sn = s4[i];
         // x*cos + rotate_half(x)*sin, rounded per operation as torch does
@@ -122,17 +132,19 @@ __global__ __launch_bounds__(64 * kDqWaves) void k2b_dequant_kernel(const Dequan
         k1 = __fmul_rn(k1, c) + __fmul_rn(k0, sn);
         k0 = r0;
       }
-      tl.v[n][j] = k0;
-      tl.v[n][j + 64] = k1;
+      o0[i] = k0;
+      o1[i] = k1;
     }
+    tile_put4(tl, n, 16 * bb + 4 * q, o0, a.out_dtype);
+    tile_put4(tl, n, 16 * bb + 4 * q + 64, o1, a.out_dtype);
   }
-  __syncthreads();
+  wave_lds_order();
   const int64_t row0 = (int64_t)h * a.out_rows + (int64_t)lp * kPT;
   if (active) dq_store_tile(tl, a.k_out, row0, a.out_dtype);
-  __syncthreads();   // the staging tile is reused for the values
+  wave_lds_order();   // the staging tile is reused for the values
 
-  dq_value_tile(vcd, nrm, a.codebook, a.v_sign_bits, n, q, tl);
-  __syncthreads();
+  dq_value_tile_lut(vcd, nrm, s_lut, a.v_sign_bits, n, q, tl, a.out_dtype);
+  wave_lds_order();
   if (active) dq_store_tile(tl, a.v_out, row0, a.out_dtype);
 }
 
@@ -186,10 +198,16 @@ extern "C" int bmx_k2b_dequant(const bmx_k2b_dequant_args* a, void* stream) {
   k.pos0 = a->pos0;
   k.out_rows = a->out_rows ? a->out_rows : a->n_tokens;
   const dim3 grid(a->n_tokens / kPT, (g.h_kv + kDqWaves - 1) / kDqWaves);
-  if (g.rank == 32)
-    hipLaunchKernelGGL(k2b_dequant_kernel<32>, grid, dim3(64 * kDqWaves), 0, (hipStream_t)stream, k);
-  else
-    hipLaunchKernelGGL(k2b_dequant_kernel<16>, grid, dim3(64 * kDqWaves), 0, (hipStream_t)stream, k);
+  const hipStream_t st = (hipStream_t)stream;
+  const dim3 block(64 * kDqWaves);
+  switch (a->out_dtype * 2 + (g.rank == 32)) {
+    case BMX_K2B_F16 * 2 + 1: hipLaunchKernelGGL((k2b_dequant_kernel<32, DqTile16<BMX_K2B_F16>>), grid, block, 0, st, k); break;
+    case BMX_K2B_F16 * 2: hipLaunchKernelGGL((k2b_dequant_kernel<16, DqTile16<BMX_K2B_F16>>), grid, block, 0, st, k); break;
+    case BMX_K2B_BF16 * 2 + 1: hipLaunchKernelGGL((k2b_dequant_kernel<32, DqTile16<BMX_K2B_BF16>>), grid, block, 0, st, k); break;
+    case BMX_K2B_BF16 * 2: hipLaunchKernelGGL((k2b_dequant_kernel<16, DqTile16<BMX_K2B_BF16>>), grid, block, 0, st, k); break;
+    case BMX_K2B_F32 * 2 + 1: hipLaunchKernelGGL((k2b_dequant_kernel<32, DqTile>), grid, block, 0, st, k); break;
+    default: hipLaunchKernelGGL((k2b_dequant_kernel<16, DqTile>), grid, block, 0, st, k); break;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     bmx_set_error(std::string("bmx_k2b_dequant: launch: ") + hipGetErrorString(e));

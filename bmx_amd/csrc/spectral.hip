@@ -404,13 +404,6 @@ constexpr size_t sp_dyn_bytes(int k_page_bytes) {
 // Workgroup barrier over LDS only: this wave's LDS accesses complete, then
 // s_barrier.  Global loads in flight stay in flight (__syncthreads would wait
 // for them too, and with them for the next step's prefetched dec rows).
-__device__ __forceinline__ void wave_lds_order() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
-  asm volatile("" ::: "memory");
-}
-
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
@@ -622,8 +615,8 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
       cn *= a.rope_scaling;
       sn *= a.rope_scaling;
       if (a.apply_rope == 2) {
-        cn = half_bits_to_float(float_to_half_bits(cn));
-        sn = half_bits_to_float(float_to_half_bits(sn));
+        cn = half_bits_to_float(float_to_half_bits(fp32_rounded(cn)));
+        sn = half_bits_to_float(float_to_half_bits(fp32_rounded(sn)));
       }
       s_cs[0][t][fj] = cn;
       s_cs[1][t][fj] = sn;
@@ -1011,10 +1004,10 @@ __global__ __launch_bounds__(512) void spectral_dequant_kernel(const SpDequantKA
         float y[4][8];
         vfull_y(vp, a.VL.vcode, a.h_kv, h, lane, a.codebook, y);
         dq_value_tile_rot(y, make_uint2(nrm[pg].x, nrm[pg].y), a.v_sign_c + 4 * h, 1.0f / (float)(kD * a.h_kv), n,
-                          q, tl);
+                          q, tl, a.out_dtype);
       } else {
         dq_value_tile(make_uint2(vcd[pg].x, vcd[pg].y), make_uint2(nrm[pg].x, nrm[pg].y), a.codebook,
-                      a.v_sign_bits, n, q, tl);
+                      a.v_sign_bits, n, q, tl, a.out_dtype);
       }
       wave_lds_order();
       dq_store_tile(tl, a.v_out, row_h + 16 * pg, a.out_dtype);
@@ -1139,7 +1132,7 @@ __global__ __launch_bounds__(512) void spectral_partial128_kernel(const SpDequan
       const float e = __builtin_fmaf(fq, tf, -ang);
       float cn, sn;
       rotate_back(cc, ss, e, &cn, &sn);
-      const half2_t cs = {(_Float16)(cn * a.rope_scaling), (_Float16)(sn * a.rope_scaling)};
+      const half2_t cs = {(_Float16)fp32_rounded(cn * a.rope_scaling), (_Float16)fp32_rounded(sn * a.rope_scaling)};
       s_cs[t][fj] = as_u32(cs);
       const float cnx = cc * c8 - ss * s8;
       ss = ss * c8 + cc * s8;
