@@ -346,11 +346,12 @@ def _dense_out(out, h_kv: int, n_rows: int, dtype, dev, d: int = HEAD_DIM):
     return k, v, k.stride(0) // d
 
 
-def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis16: torch.Tensor,
-            consts: CodecConsts, *, h_kv: int, rank: int, apply_rope: int = ROPE_NONE,
-            dtype: torch.dtype = torch.float32, pos0: int = 0, out: tuple | None = None,
-            group: int = GROUP, k_bits: int = 3):
-    """Committed pages of one sequence -> dense (K (h_kv, n, d), V (h_kv, n, d))
+def dequant_args(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis16: torch.Tensor,
+                 consts: CodecConsts, *, h_kv: int, rank: int, apply_rope: int = ROPE_NONE,
+                 dtype: torch.dtype = torch.float32, pos0: int = 0, out: tuple | None = None,
+                 group: int = GROUP, k_bits: int = 3):
+    """Arguments of one bmx_k2b_dequant call and its outputs: committed pages
+    of one sequence -> dense (K (h_kv, n, d), V (h_kv, n, d))
     in dtype (d = consts.head_dim; group / k_bits as in append).  apply_rope: ROPE_NONE (pre-RoPE keys), ROPE_EXACT (fp32 cos/sin)
     or ROPE_FP16_TABLES (the reference's prefill: fp16-rounded cos/sin); pos0:
     the position of the first listed token; out: (K, V) views to write into (see
@@ -376,5 +377,21 @@ def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis1
     a.k_out, a.v_out = _ptr(k), _ptr(v)
     a.out_dtype = _V_DTYPES[dtype]
     a.pos0, a.out_rows = int(pos0), rows
+    return a, k, v
+
+
+def dequant_launch(a: "_lib.DequantArgs", dev: torch.device) -> None:
+    """One bmx_k2b_dequant call on built arguments (dequant_args) on dev's current stream."""
     _lib.check(_lib.lib().bmx_k2b_dequant(ct.byref(a), _stream(dev)), "bmx_k2b_dequant")
+
+
+def dequant(pages: torch.Tensor, page_table: torch.Tensor, n_tokens: int, basis16: torch.Tensor,
+            consts: CodecConsts, *, h_kv: int, rank: int, apply_rope: int = ROPE_NONE,
+            dtype: torch.dtype = torch.float32, pos0: int = 0, out: tuple | None = None,
+            group: int = GROUP, k_bits: int = 3):
+    """Committed pages of one sequence -> dense (K (h_kv, n, d), V (h_kv, n, d))
+    in dtype: dequant_args, then one dequant_launch."""
+    a, k, v = dequant_args(pages, page_table, n_tokens, basis16, consts, h_kv=h_kv, rank=rank,
+                           apply_rope=apply_rope, dtype=dtype, pos0=pos0, out=out, group=group, k_bits=k_bits)
+    dequant_launch(a, pages.device)
     return k, v
