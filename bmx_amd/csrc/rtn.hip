@@ -282,14 +282,29 @@ __device__ __forceinline__ float dpp_all_r(float x) {
 constexpr int kRRowShr = 0x110;
 constexpr int kRRowRor = 0x120;
 
-// 8 nibbles (offset binary) -> fp16 pairs (n_p, n_{p+4}) - 8, exact
-__device__ __forceinline__ void nibble_pairs(uint32_t x, uint32_t out[4]) {
-  const half2_t bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const uint32_t m = ((x >> (4 * p)) & 0x000F000Fu) | 0x64006400u;   // 1024 + nibble
-    out[p] = as_u32r(as_h2r(m) + bias);
+// 8 nibbles (offset binary) -> fp16 pairs (n_p, n_{p+4}) - 8, exact.  A
+// nibble at mantissa bits [0, 4) under exponent field 25 reads as 1024 + n,
+// at bits [4, 8) under exponent field 21 as 64 + n: nibbles 0, 1 (and 4, 5)
+// in place, 2, 3 (6, 7) after one shift by 8, each pair one AND-OR (masks in
+// registers: a VOP3 takes no two literals) and one packed add.
+struct NibMasks {
+  uint32_t m0, m1;   // nibble bits of slots 0 and 1 (both halves)
+  uint32_t e0, e1;   // exponent fields 25 and 21 (both halves)
+  __device__ __forceinline__ void init() {
+    m0 = 0x000F000Fu; m1 = 0x00F000F0u;
+    e0 = 0x64006400u; e1 = 0x54005400u;
+    asm volatile("" : "+v"(m0), "+v"(m1));
+    asm volatile("" : "+s"(e0), "+s"(e1));
   }
+};
+__device__ __forceinline__ void nibble_pairs(const NibMasks& nm, uint32_t x, uint32_t out[4]) {
+  const half2_t b0 = {(_Float16)-1032.0f, (_Float16)-1032.0f};   // 1024 + 8
+  const half2_t b1 = {(_Float16)-72.0f, (_Float16)-72.0f};       // 64 + 8
+  const uint32_t y = x >> 8;
+  out[0] = as_u32r(as_h2r((x & nm.m0) | nm.e0) + b0);
+  out[1] = as_u32r(as_h2r((x & nm.m1) | nm.e1) + b1);
+  out[2] = as_u32r(as_h2r((y & nm.m0) | nm.e0) + b0);
+  out[3] = as_u32r(as_h2r((y & nm.m1) | nm.e1) + b1);
 }
 
 // The partial of one (sequence, head, split): plain channel sums.
@@ -479,6 +494,8 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
   for (int bt = 0; bt < 8; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
   const int my_slot = NSLOT > 1 ? n / SW : 0;
+  NibMasks nm;
+  nm.init();
   __syncthreads();
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): group 0 has landed
 
@@ -525,7 +542,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
             const uint32_t s4[4] = {sp.x, sp.y, sp.z, sp.w};
             const uint32_t l4[4] = {sl.x, sl.y, sl.z, sl.w};
             uint32_t cp[4];
-            nibble_pairs(kw4[bb], cp);
+            nibble_pairs(nm, kw4[bb], cp);
             union { uint32_t u[4]; half8_t v; } khi, klo;
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
@@ -566,7 +583,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
 #pragma unroll
         for (int bb = 0; bb < 4; ++bb) {
           union { uint32_t u[4]; half8_t v; } ka;
-          nibble_pairs(kw4[bb], ka.u);
+          nibble_pairs(nm, kw4[bb], ka.u);
           const float4_t z = {0.f, 0.f, 0.f, 0.f};
           float4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, qh[bb], z, 0, 0, 0);
           d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka.v, ql[bb], d, 0, 0, 0);
@@ -661,7 +678,7 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
           const uint32_t x = __builtin_amdgcn_perm(vb4[bt >> 1], va4[bt >> 1],
                                                    (bt & 1) ? 0x07060302u : 0x05040100u);
           union { uint32_t u[4]; half8_t v; } av;
-          nibble_pairs(x, av.u);
+          nibble_pairs(nm, x, av.u);
           acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av.v, bp.v, acc[bt], 0, 0, 0);
         }
       }
