@@ -282,6 +282,8 @@ __device__ __forceinline__ float dpp_all_r(float x) {
 constexpr int kRRowShr = 0x110;
 constexpr int kRRowRor = 0x120;
 
+constexpr int kRBufWord3 = 0x00020000;   // buffer descriptor word 3: raw 32-bit data
+
 // 8 nibbles (offset binary) -> fp16 pairs (n_p, n_{p+4}) - 8, exact.  A
 // nibble at mantissa bits [0, 4) under exponent field 25 reads as 1024 + n,
 // at bits [4, 8) under exponent field 21 as 64 + n: nibbles 0, 1 (and 4, 5)
@@ -349,7 +351,8 @@ __device__ __noinline__ void rtn_empty_range(const RtnDecodeKArgs& a, int b, int
 // SW: query slot width (G rounded up to 4, 8 or 16); the 16 score columns of a
 // page hold 16 / SW pages after compaction.  NGK: key scale groups per token
 // (128 / k_group) of token-arm keys, 0 for channel-arm keys.
-template <int SW, int NGK>
+// kNT: page loads non-temporal (calls whose pages stream from HBM)
+template <int SW, int NGK, bool kNT>
 __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDecodeKArgs a) {
   constexpr int NSLOT = 16 / SW;
   constexpr int NCR = kRGroupPages / NSLOT;
@@ -392,11 +395,14 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
   const int64_t tail_base = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
 
   int pidv = (int)clamp_page(pid_raw, a.n_pool);
-  const int len = min(len_raw, a.max_packed_len) & ~(kRGroup - 1);
+  // uniform values in scalar registers: the group loop's bookkeeping is scalar work
+  const int len = __builtin_amdgcn_readfirstlane(min(len_raw, a.max_packed_len) & ~(kRGroup - 1));
   if (len != len_spec) {
     range(len, g0, g1);
     pidv = (int)clamp_page(load_ids_raw(0, (g1 - g0) * kRGroupPages), a.n_pool);
   }
+  g0 = __builtin_amdgcn_readfirstlane(g0);
+  g1 = __builtin_amdgcn_readfirstlane(g1);
   const int n_groups = g1 - g0;
   if (n_groups == 0) {
     if (active)
@@ -421,7 +427,14 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
     c = min(c, pre_chunks - 1);
     const int pp = c / chunks_pp;
     const int id = __shfl(pidv, gi * kRGroupPages + pp - pid_base);
-    return *reinterpret_cast<const uint4*>(a.pages + (int64_t)id * pb + (c - pp * chunks_pp) * 16);
+    const uint8_t* src = a.pages + (int64_t)id * pb + (c - pp * chunks_pp) * 16;
+    if constexpr (kNT) {
+      typedef uint32_t p_u32x4_t __attribute__((ext_vector_type(4)));
+      const p_u32x4_t w = __builtin_nontemporal_load(reinterpret_cast<const p_u32x4_t*>(src));
+      return make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      return *reinterpret_cast<const uint4*>(src);
+    }
   };
   auto load_prefix = [&](int gi) -> Pre {
     Pre r;
@@ -448,8 +461,18 @@ __global__ __launch_bounds__(kRThreads) void rtn_decode_split_kernel(const RtnDe
   };
   const uint32_t kc_off = (uint32_t)(a.L.kcode + h * 1024 + lane * 16);
   const uint32_t vc_off = (uint32_t)(a.L.vcode + h * 1024 + lane * 16);
-  auto load_kc = [&](int gi, int pp) { return *reinterpret_cast<const uint4*>(page_ptr(gi, pp) + kc_off); };
-  auto load_vc = [&](int gi, int pp) { return *reinterpret_cast<const uint4*>(page_ptr(gi, pp) + vc_off); };
+  // a page's code sections through a buffer descriptor on its (uniform) base:
+  // the address is scalar work, the lane offset a constant register, and the
+  // load is non-temporal (aux 2: the codes are read once)
+  typedef uint32_t r_u32x4_t __attribute__((ext_vector_type(4)));
+  auto load_code = [&](int gi, int pp, uint32_t off) -> uint4 {
+    const r_u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(page_ptr(gi, pp)), (short)0, pb, kRBufWord3), (int)off,
+        0, kNT ? 2 : 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+  };
+  auto load_kc = [&](int gi, int pp) { return load_code(gi, pp, kc_off); };
+  auto load_vc = [&](int gi, int pp) { return load_code(gi, pp, vc_off); };
 
   Pre pre = load_prefix(0);
   const Pre pre1 = load_prefix(min(1, n_groups - 1));
@@ -828,16 +851,31 @@ extern "C" size_t bmx_rtn_decode_workspace_bytes(const bmx_rtn_decode_args* a) {
   return rtn_ws_bytes(a, rtn_choose_splits(a));
 }
 
-template <int SW>
-static void launch_rtn_split(int ngk, dim3 grid, const RtnDecodeKArgs& k, hipStream_t st) {
+template <int SW, bool kNT>
+static void launch_rtn_split_nt(int ngk, dim3 grid, const RtnDecodeKArgs& k, hipStream_t st) {
   if (ngk == 0)
-    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 0>), grid, dim3(kRThreads), 0, st, k);
+    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 0, kNT>), grid, dim3(kRThreads), 0, st, k);
   else if (ngk == 4)
-    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 4>), grid, dim3(kRThreads), 0, st, k);
+    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 4, kNT>), grid, dim3(kRThreads), 0, st, k);
   else if (ngk == 2)
-    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 2>), grid, dim3(kRThreads), 0, st, k);
+    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 2, kNT>), grid, dim3(kRThreads), 0, st, k);
   else
-    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 1>), grid, dim3(kRThreads), 0, st, k);
+    hipLaunchKernelGGL((rtn_decode_split_kernel<SW, 1, kNT>), grid, dim3(kRThreads), 0, st, k);
+}
+
+// Page loads are non-temporal when a call reads at least kRNtBytes of pages:
+// from there a 32-layer step's calls exceed the 256 MB MALL and stream from
+// HBM (non-temporal measured faster from 8k tokens at h_kv 8); below it a
+// step's pages stay in the MALL, which non-temporal reads would bypass
+// (measured slower at 4k).
+constexpr int64_t kRNtBytes = 8ll << 20;
+
+template <int SW>
+static void launch_rtn_split(int ngk, bool nt, dim3 grid, const RtnDecodeKArgs& k, hipStream_t st) {
+  if (nt)
+    launch_rtn_split_nt<SW, true>(ngk, grid, k, st);
+  else
+    launch_rtn_split_nt<SW, false>(ngk, grid, k, st);
 }
 
 extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
@@ -908,12 +946,13 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   k.nw.v_dst = const_cast<uint16_t*>(a->v_tail);
   dim3 grid(S, a->batch);
   const int ngk = g.k_arm == BMX_RTN_CHANNEL ? 0 : kD / g.k_group;
+  const bool nt = (int64_t)a->batch * (a->max_packed_len / kPT) * k.L.bytes >= kRNtBytes;
   if (g.n_q_groups <= 4)
-    launch_rtn_split<4>(ngk, grid, k, st);
+    launch_rtn_split<4>(ngk, nt, grid, k, st);
   else if (g.n_q_groups <= 8)
-    launch_rtn_split<8>(ngk, grid, k, st);
+    launch_rtn_split<8>(ngk, nt, grid, k, st);
   else
-    launch_rtn_split<16>(ngk, grid, k, st);
+    launch_rtn_split<16>(ngk, nt, grid, k, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return rfail(BMX_E_HIP, std::string("bmx_rtn_decode: split kernel launch: ") + hipGetErrorString(e));
