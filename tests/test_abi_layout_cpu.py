@@ -1,8 +1,8 @@
 """The ctypes argument structs (bmx_amd/_lib.py) against the C headers they
 mirror (include/*.h): every struct's size and every field's offset, read from
 a small C program that gcc builds against the headers, so that a field added
-on one side only cannot pass silently.  And the ctypes stub shown to a
-maintainer in INTEGRATION.md: its field lists are the shipped ones."""
+on one side only cannot pass silently.  And the ctypes stubs shown to a
+maintainer in INTEGRATION.md: run as written, they have the shipped layouts."""
 import ctypes as ct
 import re
 import shutil
@@ -66,10 +66,21 @@ def test_ctypes_structs_match_the_headers(tmp_path):
             assert got[(py, f[0])] == off, f"{py}.{f[0]}: offset C {got[(py, f[0])]} != ctypes {off}"
 
 
-def test_integration_stub_matches_the_shipped_binding():
+def test_integration_stubs_match_the_shipped_binding():
+    """Every ctypes class INTEGRATION.md shows, run as written (in the order
+    shown: later classes use earlier ones), has the shipped class's field
+    names, size and offsets."""
     text = (ROOT / "INTEGRATION.md").read_text()
-    for py in ("Geom", "DecodeArgs"):
-        start = text.index(f"class {py}(ct.Structure):")
-        block = text[start:text.index("\n\n", start)]
-        names = re.findall(r'\("(\w+)",', block)
-        assert names == [f[0] for f in getattr(_lib, py)._fields_], py
+    ns = {"ct": ct}
+    shown = []
+    for m in re.finditer(r"^class (\w+)\(ct\.Structure\):", text, re.M):
+        block = text[m.start():text.index("\n\n", m.start())]
+        exec(block, ns)   # the document's own stub code
+        shown.append(m.group(1))
+    assert {"Geom", "DecodeArgs", "RtnGeom", "RtnDecodeArgs"} <= set(shown)
+    for py in shown:
+        doc, lib = ns[py], getattr(_lib, py)
+        assert [f[0] for f in doc._fields_] == [f[0] for f in lib._fields_], py
+        assert ct.sizeof(doc) == ct.sizeof(lib), py
+        for f in lib._fields_:
+            assert getattr(doc, f[0]).offset == getattr(lib, f[0]).offset, f"{py}.{f[0]}"
