@@ -133,8 +133,8 @@ int bmx_k2b_page_section(const bmx_k2b_geom* geom, int section, size_t* offset,
 typedef struct {
   bmx_k2b_geom geom;
   int32_t batch;
-  const void* q;              /* device [batch][h_kv][G][128] post-RoPE, in io_dtype */
-  void* out;                  /* device [batch][h_kv][G][128] in io_dtype */
+  const void* q;              /* device [batch][h_kv][G][head_dim] post-RoPE, in io_dtype */
+  void* out;                  /* device [batch][h_kv][G][head_dim] in io_dtype */
   const uint8_t* pages;       /* device page pool; page i at pages + i*page_bytes */
   int32_t n_pool_pages;       /* pages in the pool; table entries are clamped into
                                  [0, n_pool_pages) so a bad entry cannot fault */
@@ -149,14 +149,15 @@ typedef struct {
   int32_t max_packed_len;     /* host upper bound of packed_len (sizes the grid) */
   const uint16_t* basis;      /* device fp16 [C][R] frozen key basis of sequence 0 */
   int64_t basis_stride;       /* elements between sequences' bases (0 = shared) */
-  float inv_freq[64];         /* RoPE inverse frequencies (HF inv_freq, fp32) */
+  float inv_freq[64];         /* RoPE inverse frequencies (HF inv_freq, fp32; the first
+                                 head_dim/2 are read) */
   float rope_scaling;         /* cos/sin multiplier (HF attention_scaling, 1.0) */
   float sm_scale;             /* softmax scale (HF module.scaling) */
   float codebook[4];          /* 2-bit Lloyd levels, ascending */
   uint32_t v_sign_bits[4];    /* bit c set <=> V Hadamard sign of channel c is -1 */
   const uint16_t* k_tail;     /* device fp16 (tail_dtype) post-RoPE recent-window keys */
   const uint16_t* v_tail;     /* device fp16 (tail_dtype) recent-window values */
-  int64_t tail_stride_b;      /* element strides of k_tail/v_tail (dim 128 contiguous) */
+  int64_t tail_stride_b;      /* element strides of k_tail/v_tail (head_dim contiguous) */
   int64_t tail_stride_h;
   int64_t tail_stride_t;
   const int32_t* tail_len;    /* device [batch] recent-window length (clamped to tail_cap), or
@@ -271,14 +272,14 @@ typedef struct {
   const uint8_t* pages;
   int32_t n_pool_pages;       /* pages in the pool (ids are clamped into range) */
   const int32_t* page_table;  /* device [n_tokens/16] logical -> physical page */
-  int32_t n_tokens;           /* multiple of 64 */
+  int32_t n_tokens;           /* multiple of the residual group (64 on the recipe's page) */
   const uint16_t* basis;      /* device fp16 [C][R] */
   float inv_freq[64];
   float rope_scaling;
   int32_t apply_rope;
   float codebook[4];
   uint32_t v_sign_bits[4];
-  void* k_out;                /* device [h_kv][out_rows][128] of out_dtype: rows 0 .. n_tokens - 1 */
+  void* k_out;                /* device [h_kv][out_rows][head_dim] of out_dtype: rows 0 .. n_tokens - 1 */
   void* v_out;                /* of each head written */
   int32_t out_dtype;          /* BMX_K2B_F16 (0), BMX_K2B_F32 or BMX_K2B_BF16 */
   int32_t pos0;               /* RoPE position of the first listed token (0: the sequence's start) */
