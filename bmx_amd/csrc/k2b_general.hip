@@ -540,12 +540,18 @@ __device__ __forceinline__ float gen_block_max(float v, float* s_red) {
 // merge by the split softmax's weights, the inverse value rotation (H_d, the
 // codec's signs, 1/d) turns the sum into values, and the recent window
 // (scored here; rows given apart read from there and copied into the window
-// buffer by query 0's workgroup) joins with its own weight.  Every loop hands
-// each thread independent rows so that their loads are in flight together:
-// thread (part, c4) takes 4 channels of splits / window rows part, part + P, ...
+// buffer by query 0's workgroup) joins with its own weight.  Thread (part,
+// c4) takes 4 channels of splits / window rows part, part + P, ...  Every
+// first-pass load of the four phases (the split maxima and sums, the
+// thread's splits' partial sums, its window row's key, its window value rows)
+// is issued before any of them is used, so the phases share one memory round
+// trip; splits and window rows beyond the first pass are loaded in later
+// passes.
 template <int D>
 __global__ __launch_bounds__(128) void gen_merge_kernel(const GenDecodeArgs a) {
   constexpr int NC4 = D / 4, P = 128 / NC4;   // channel quads, row parts
+  constexpr int kMS = 64 / P;                 // first-pass splits per thread: 64 splits
+  constexpr int kMV = (D == 128 ? 64 : 128) / P;   // first-pass window value rows per thread
   const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   const int H = a.r.L.h, G = a.G, S = a.n_split;
   const int c4 = tid % NC4, part = tid / NC4;
@@ -553,27 +559,69 @@ __global__ __launch_bounds__(128) void gen_merge_kernel(const GenDecodeArgs a) {
   __shared__ float4_t s_part[P][NC4];
   __shared__ float s_s[4096];
   const int64_t row = ((int64_t)b * H + h) * G + g;
-  if (tid < D) {
-    const float4_t x = load_q4(a.q, row * D + (tid & ~3), a.io_dtype);
-    s_q[tid] = x[tid & 3] * a.qscale;
-  }
-  // ---- packed partials: the max, then weighted sums
   const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + row * S;
-  float mx = -INFINITY;
-  for (int s = tid; s < S; s += 128) mx = fmaxf(mx, ml[s].x);
+  const float* accr = a.ws_acc + row * S * D + 4 * c4;
+  const bool wbf = __builtin_amdgcn_readfirstlane(a.tail_bf16) != 0;
+  const int64_t tb = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
+  const int64_t nb = (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh;
+  auto wrow = [&](const uint16_t* fresh, const uint16_t* buf, int t) {
+    const int i = fresh_row(a.nw, t);
+    return i >= 0 ? fresh + nb + (int64_t)i * a.nw.st : buf + tb + (int64_t)t * a.ts_t;
+  };
+  auto cvt4 = [&](uint2 r) {   // 4 window elements as fp32
+    return wbf ? float4_t{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                          __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u)}
+               : float4_t{half_bits_to_float(r.x & 0xffff), half_bits_to_float(r.x >> 16),
+                          half_bits_to_float(r.y & 0xffff), half_bits_to_float(r.y >> 16)};
+  };
+  const int Tc = a.tail_cap;   // the host's bound of the window
+  // ---- every first-pass load at once
+  float4_t qx = {0.f, 0.f, 0.f, 0.f};
+  if (tid < D) qx = load_q4(a.q, row * D + (tid & ~3), a.io_dtype);
+  const float2 mlv = ml[min(tid, S - 1)];
+  float msp[kMS];
+  float4_t accv[kMS];
+#pragma unroll
+  for (int k = 0; k < kMS; ++k) {
+    const int sc = min(part + P * k, S - 1);
+    msp[k] = ml[sc].x;
+    accv[k] = *reinterpret_cast<const float4_t*>(accr + (int64_t)sc * D);
+  }
+  uint2 kv[NC4], vv[kMV];
+  if (Tc > 0) {
+    const uint16_t* kr = wrow(a.nw.k, a.k_tail, min(tid, Tc - 1));
+#pragma unroll
+    for (int c = 0; c < NC4; ++c) kv[c] = *reinterpret_cast<const uint2*>(kr + 4 * c);
+#pragma unroll
+    for (int k = 0; k < kMV; ++k)
+      vv[k] = *reinterpret_cast<const uint2*>(wrow(a.nw.v, a.v_tail, min(part + P * k, Tc - 1)) + 4 * c4);
+  }
+  const int T = a.tail_len ? min(max(a.tail_len[b], 0), Tc) : a.nw.T;
+  if (tid < D) s_q[tid] = qx[tid & 3] * a.qscale;   // published by the block max's barriers
+
+  // ---- packed partials: the max, then weighted sums
+  float mx = tid < S ? mlv.x : -INFINITY;
+  for (int s2 = tid + 128; s2 < S; s2 += 128) mx = fmaxf(mx, ml[s2].x);
   const float Mp = gen_block_max(mx, s_red);
   float lp = 0.f;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
   if (Mp != -INFINITY) {
-    for (int s = tid; s < S; s += 128) {
-      const float2 v = ml[s];
+    if (tid < S && mlv.x != -INFINITY) lp = __builtin_amdgcn_exp2f(mlv.x - Mp) * mlv.y;
+    for (int s2 = tid + 128; s2 < S; s2 += 128) {
+      const float2 v = ml[s2];
       lp += v.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(v.x - Mp) * v.y;
     }
+#pragma unroll
+    for (int k = 0; k < kMS; ++k) {
+      const bool ok = part + P * k < S && msp[k] != -INFINITY;
+      const float w = ok ? __builtin_amdgcn_exp2f(msp[k] - Mp) : 0.f;
+      acc += ok ? w * accv[k] : float4_t{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll 4
-    for (int s = part; s < S; s += P) {
-      const float m = ml[s].x;
+    for (int s2 = part + P * kMS; s2 < S; s2 += P) {
+      const float m = ml[s2].x;
       const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - Mp);
-      acc += w * *reinterpret_cast<const float4_t*>(a.ws_acc + (row * S + s) * D + 4 * c4);
+      acc += w * *reinterpret_cast<const float4_t*>(accr + (int64_t)s2 * D);
     }
   }
   const float Lp = gen_block_sum(lp, s_red);
@@ -605,34 +653,29 @@ __global__ __launch_bounds__(128) void gen_merge_kernel(const GenDecodeArgs a) {
     op = s_x[tid] / (float)D;
     if (sign_neg(a.r.v_sign_bits, tid)) op = -op;
   }
-  // ---- the recent window
-  const int T = a.tail_len ? min(max(a.tail_len[b], 0), a.tail_cap) : a.nw.T;
-  const bool wbf = __builtin_amdgcn_readfirstlane(a.tail_bf16) != 0;
-  const int64_t tb = (int64_t)b * a.ts_b + (int64_t)h * a.ts_h;
-  const int64_t nb = (int64_t)b * a.nw.sb + (int64_t)h * a.nw.sh;
-  auto wrow = [&](const uint16_t* fresh, const uint16_t* buf, int t) {
-    const int i = fresh_row(a.nw, t);
-    return i >= 0 ? fresh + nb + (int64_t)i * a.nw.st : buf + tb + (int64_t)t * a.ts_t;
-  };
-  auto cvt4 = [&](uint2 r) {   // 4 window elements as fp32
-    return wbf ? float4_t{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
-                          __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u)}
-               : float4_t{half_bits_to_float(r.x & 0xffff), half_bits_to_float(r.x >> 16),
-                          half_bits_to_float(r.y & 0xffff), half_bits_to_float(r.y >> 16)};
-  };
-  float mw = -INFINITY;
-  for (int t = tid; t < T; t += 128) {   // scores: one row per thread, all its loads at once
-    const uint16_t* kr = wrow(a.nw.k, a.k_tail, t);
-    uint2 kv[NC4];
-#pragma unroll
-    for (int c = 0; c < NC4; ++c) kv[c] = *reinterpret_cast<const uint2*>(kr + 4 * c);
+  // ---- the recent window: scores, one row per thread (its first from kv)
+  auto score = [&](const uint2 (&k4)[NC4]) {
     float sc = 0.f;
 #pragma unroll
     for (int c = 0; c < NC4; ++c) {
-      const float4_t x = cvt4(kv[c]);
+      const float4_t x = cvt4(k4[c]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) sc = __builtin_fmaf(s_q[4 * c + e], x[e], sc);
     }
+    return sc;
+  };
+  float mw = -INFINITY;
+  if (tid < T) {
+    const float sc = score(kv);
+    s_s[tid] = sc;
+    mw = sc;
+  }
+  for (int t = tid + 128; t < T; t += 128) {
+    const uint16_t* kr = wrow(a.nw.k, a.k_tail, t);
+    uint2 k4[NC4];
+#pragma unroll
+    for (int c = 0; c < NC4; ++c) k4[c] = *reinterpret_cast<const uint2*>(kr + 4 * c);
+    const float sc = score(k4);
     s_s[t] = sc;
     mw = fmaxf(mw, sc);
   }
@@ -640,8 +683,13 @@ __global__ __launch_bounds__(128) void gen_merge_kernel(const GenDecodeArgs a) {
   float lw = 0.f;
   for (int t = tid; t < T; t += 128) lw += __builtin_amdgcn_exp2f(s_s[t] - mw);
   float4_t ow = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < kMV; ++k) {
+    const int t = part + P * k;
+    if (t < T) ow += __builtin_amdgcn_exp2f(s_s[t] - mw) * cvt4(vv[k]);
+  }
 #pragma unroll 4
-  for (int t = part; t < T; t += P)
+  for (int t = part + P * kMV; t < T; t += P)
     ow += __builtin_amdgcn_exp2f(s_s[t] - mw) * cvt4(*reinterpret_cast<const uint2*>(wrow(a.nw.v, a.v_tail, t) + 4 * c4));
   const float Lw = gen_block_sum(lw, s_red);
   s_part[part][c4] = ow;
