@@ -327,7 +327,10 @@ __device__ __forceinline__ float part_weight(float mi, float M) {
 // kRotated: the packed partials are sums of k2b's rotated value levels with
 // the H8 half of the inverse Hadamard applied (the merge applies H16, the
 // signs and packed_scale); otherwise they are plain channel sums.
-template <bool kRotated>
+// kTok: window-token blocks per wave per pass: kCmbTokens (128 tokens per
+// pass), or 4 for windows of more than 128 rows (up to 255 between commits),
+// so that the window is one pass, one memory round trip.
+template <bool kRotated, int kTok>
 __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs a) {
   const int ch = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
   const int h = r / a.G;
@@ -343,12 +346,12 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   // element e of this lane in pass j0: p + 16 (wave + kCmbWaves u) + j0
   auto elem = [&](int j0, int u) { return j0 + p + 16 * (wave + kCmbWaves * u); };
   constexpr int kSplitPass = 16 * kCmbWaves * kCmbSplits;   // splits per pass of the workgroup
-  constexpr int kTokenPass = 16 * kCmbWaves * kCmbTokens;   // window tokens per pass
+  constexpr int kTokenPass = 16 * kCmbWaves * kTok;   // window tokens per pass
 
   f2_t ml[kCmbSplits];
   float4_t pv[kCmbSplits];
-  float ws[kCmbTokens];
-  uint2 wv[kCmbTokens];
+  float ws[kTok];
+  uint2 wv[kTok];
   int S = S_slots;   // the sequence's splits
   auto load_splits = [&](int j0) {
 #pragma unroll
@@ -362,7 +365,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
   };
   auto load_tokens = [&](int t0, int t_end) {   // t_end >= 1
 #pragma unroll
-    for (int u = 0; u < kCmbTokens; ++u) {
+    for (int u = 0; u < kTok; ++u) {
       const int t = min(elem(t0, u), t_end - 1);
       ws[u] = swb[t];
       const int i_new = fresh_row(a.nw, t);
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
     if (t0 != 0) load_tokens(t0, T);
     float mloc = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < kCmbTokens; ++u)
+    for (int u = 0; u < kTok; ++u)
       if (elem(t0, u) < T) mloc = fmaxf(mloc, ws[u]);
     const float mnew = fmaxf(mt, row_reduce16<true>(mloc));
     if (mnew != -INFINITY) {
@@ -423,7 +426,7 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
       xt *= sc;
       lt *= sc;
 #pragma unroll
-      for (int u = 0; u < kCmbTokens; ++u) {
+      for (int u = 0; u < kTok; ++u) {
         // a row given apart goes into the window buffer (once: by query 0's merge)
         if (r % a.G == 0 && elem(t0, u) < T && fresh_row(a.nw, elem(t0, u)) >= 0)
           *reinterpret_cast<uint2*>(a.nw.v_dst + (vb - a.v_tail) + (int64_t)elem(t0, u) * a.ts_t) = wv[u];
@@ -514,6 +517,16 @@ __global__ __launch_bounds__(kCmbThreads) void combine_kernel(const CombineKArgs
     for (int i = 0; i < 4; ++i) o[i] = (y[i] * wp + z[i] * wt) * inv;
     store_o4(a.out, row * kD + kChunk * ch + 4 * c4, o, a.io_dtype);
   }
+}
+
+// The merge launch: the window in one pass when it holds more than 128 rows.
+template <bool kRotated>
+inline void launch_combine(const CombineKArgs& c, int rows, int batch, hipStream_t st) {
+  const dim3 grid(kChunks, rows, batch);
+  if (c.tail_cap > 16 * kCmbWaves * kCmbTokens)
+    hipLaunchKernelGGL((combine_kernel<kRotated, 4>), grid, dim3(kCmbThreads), 0, st, c);
+  else
+    hipLaunchKernelGGL((combine_kernel<kRotated, kCmbTokens>), grid, dim3(kCmbThreads), 0, st, c);
 }
 
 }  // namespace bmx

@@ -1105,8 +1105,7 @@ static int decode_launch(const bmx_k2b_decode_args* a, void* stream, void* ws, s
   c.packed_scale = (float)(1.0 / (kD * (double)lm.kappa));
   c.balanced = k.balanced; c.n_wg = n_wg;
   c.packed_len = a->packed_len; c.max_packed_len = a->max_packed_len;
-  hipLaunchKernelGGL(combine_kernel<true>, dim3(kChunks, g.h_kv * g.n_q_groups, a->batch), dim3(kCmbThreads),
-                     0, st, c);
+  launch_combine<true>(c, g.h_kv * g.n_q_groups, a->batch, st);
   e = hipGetLastError();
   if (e != hipSuccess)
     return fail(BMX_E_HIP, name + std::string(": combine kernel launch: ") + hipGetErrorString(e));

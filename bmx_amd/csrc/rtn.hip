@@ -965,8 +965,7 @@ extern "C" int bmx_rtn_decode(const bmx_rtn_decode_args* a, void* stream) {
   c.tail_len = a->tail_len;
   c.nw = k.nw;
   c.packed_scale = 1.0f;
-  hipLaunchKernelGGL(combine_kernel<false>, dim3(kChunks, g.h_kv * g.n_q_groups, a->batch), dim3(kCmbThreads),
-                     0, st, c);
+  launch_combine<false>(c, g.h_kv * g.n_q_groups, a->batch, st);
   e = hipGetLastError();
   if (e != hipSuccess)
     return rfail(BMX_E_HIP, std::string("bmx_rtn_decode: combine kernel launch: ") + hipGetErrorString(e));
