@@ -1,5 +1,6 @@
 """ctypes binding of libbmx_k2b.so (the C-ABI declared in include/bmx_k2b.h,
-include/bmx_rtn.h and include/bmx_spectral.h).
+include/bmx_rtn.h, include/bmx_spectral.h, include/bmx_prefill.h and
+include/bmx_bench.h).
 
 The library is the product path: there is no fallback.  ``lib()`` raises if the
 shared object was not built (python -m bmx_amd.build) and every wrapper raises
@@ -264,6 +265,18 @@ class Fp16DecodeArgs(ct.Structure):
     ]
 
 
+class PrefillArgs(ct.Structure):
+    """bmx_prefill_args (include/bmx_prefill.h): prefill attention over dense rows."""
+    _fields_ = [
+        ("q", ct.c_void_p), ("q_stride_h", ct.c_int64), ("q_stride_t", ct.c_int64),
+        ("k", ct.c_void_p), ("v", ct.c_void_p), ("kv_stride_h", ct.c_int64), ("kv_stride_t", ct.c_int64),
+        ("out", ct.c_void_p),
+        ("h_kv", ct.c_int), ("n_q_groups", ct.c_int), ("n_q", ct.c_int), ("n_kv", ct.c_int),
+        ("head_dim", ct.c_int), ("dtype", ct.c_int), ("causal", ct.c_int), ("sm_scale", ct.c_float),
+        ("n_split", ct.c_int), ("workspace", ct.c_void_p), ("workspace_bytes", ct.c_size_t),
+    ]
+
+
 EXPORTS = {
     "bmx_last_error": (ct.c_char_p, []),
     "bmx_k2b_page_bytes": (ct.c_size_t, [ct.POINTER(Geom)]),
@@ -287,6 +300,8 @@ EXPORTS = {
     "bmx_spectral_partial_count": (ct.c_int32, [ct.POINTER(SpectralDequantArgs)]),
     "bmx_fp16_decode_workspace_bytes": (ct.c_size_t, [ct.c_int, ct.c_int, ct.c_int]),
     "bmx_fp16_decode": (ct.c_int, [ct.POINTER(Fp16DecodeArgs), ct.c_void_p]),
+    "bmx_prefill_workspace_bytes": (ct.c_size_t, [ct.POINTER(PrefillArgs)]),
+    "bmx_prefill": (ct.c_int, [ct.POINTER(PrefillArgs), ct.c_void_p]),
 }
 
 _LIB = None

@@ -1,4 +1,4 @@
-"""Build libbmx_k2b.so (gfx950: the k2b, RTN and spectral paths) in-tree with hipcc.
+"""Build libbmx_k2b.so (gfx950: the k2b, RTN and spectral paths, prefill attention) in-tree with hipcc.
 
     python -m bmx_amd.build
 
@@ -38,6 +38,7 @@ SOURCES = {
     "spectral.hip": ["-ffp-contract=off"],
     "k2b_general.hip": ["-ffp-contract=off"],
     "fp16_decode.hip": ["-ffp-contract=fast"],
+    "flash_prefill.hip": ["-ffp-contract=fast"],
 }
 
 

@@ -30,12 +30,13 @@ STRUCTS = {
     "SpectralDequantArgs": "bmx_spectral_dequant_args",
     "SpectralMergeArgs": "bmx_spectral_merge_args",
     "Fp16DecodeArgs": "bmx_fp16_decode_args",
+    "PrefillArgs": "bmx_prefill_args",
 }
 
 
 def _c_layouts(tmp_path):
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "bmx_k2b.h"', '#include "bmx_rtn.h"',
-             '#include "bmx_spectral.h"', '#include "bmx_bench.h"', "int main(void) {"]
+             '#include "bmx_spectral.h"', '#include "bmx_bench.h"', '#include "bmx_prefill.h"', "int main(void) {"]
     for py, c in STRUCTS.items():
         cls = getattr(_lib, py)
         lines.append(f'  printf("{py} sizeof %zu\\n", sizeof({c}));')
