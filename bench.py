@@ -620,13 +620,15 @@ def run_prefill(args, torch, dev) -> dict:
     keys, the model's boolean mask, one layer of Llama-3.1-8B geometry (32
     query / 8 KV heads, d 128), k2b rank 32, recent window 128, fp16.  A call
     is PackedStreamingLayer.attend: the page dequant kernel (keys rotated in
-    the pass, fp16 out), the window appended, one SDPA.  Beside it: the dequant
-    kernel alone (HBM-bound: pages in, dense fp16 K and V out) and the same
-    SDPA over the same dense fp16 K/V alone (what a dense fp16 cache pays)."""
+    the pass, fp16 out), the window appended, bmx_prefill (MFMA flash
+    attention, the roofline's kernel).  Beside it: the dequant kernel alone
+    (HBM-bound: pages in, dense fp16 K and V out), bmx_prefill alone over the
+    dense rows, and SDPA over the same dense fp16 K/V (what a dense fp16 cache
+    pays with torch's kernels: the model's mask, and the bottom-right bias)."""
     import torch.nn.functional as F
     from transformers import LlamaConfig
 
-    from bmx_amd import k2b, synth
+    from bmx_amd import k2b, prefill, synth
     from bmx_amd.cache import PackedStreamingLayer
     from bmx_amd.specs import spec_pair
     from oracle import attention as A
@@ -679,12 +681,16 @@ def run_prefill(args, torch, dev) -> dict:
                                             dtype=torch.float16), reps)
     sdpa_us = timed(lambda: F.scaled_dot_product_attention(q.unsqueeze(0), Kf, Vf, attn_mask=mask, scale=scale),
                     reps)
+    # the attention kernel alone (bmx_prefill + its split combine) over the
+    # same dense fp16 K/V, grouped heads: the packed call's attention, and
+    # what a dense fp16 cache would pay with the same kernel
+    Kg, Vg = Kf[:, ::G].contiguous().squeeze(0), Vf[:, ::G].contiguous().squeeze(0)
+    attn_us = timed(lambda: prefill.attention(q, Kg, Vg, scale, causal=True), reps)
     # the same dense fp16 K/V through the bottom-right causal bias the packed
     # layer uses for this mask (grouped heads)
     from torch.nn.attention.bias import causal_lower_right
 
-    Kg, Vg = Kf[:, ::G].contiguous(), Vf[:, ::G].contiguous()
-    sdpa_lr_us = timed(lambda: F.scaled_dot_product_attention(q.unsqueeze(0), Kg, Vg,
+    sdpa_lr_us = timed(lambda: F.scaled_dot_product_attention(q.unsqueeze(0), Kg.unsqueeze(0), Vg.unsqueeze(0),
                                                               attn_mask=causal_lower_right(nq, N), scale=scale,
                                                               enable_gqa=True), reps)
     out = lay.attend(q, scale, is_causal=True, attention_mask=mask).float()
@@ -701,11 +707,15 @@ def run_prefill(args, torch, dev) -> dict:
                                 f"{ctx}..{N - 1} over {N} keys ({P} packed + {N - P} fp16 window), "
                                 f"k2b rank {args.rank}, 32q/8kv heads, d 128, model mask"),
                    "ctx": ctx, "chunk": nq, "packed_tokens": P, "rank": args.rank},
-        "roofline": {"bound": "hbm", "kernel": "k2b_dequant_kernel (pages -> dense fp16 K, V)",
-                     "achieved": round(deq_bytes / (deq_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(deq_bytes / (deq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": deq_bytes, "avg_launch_us": round(deq_us, 3)},
-        "prefill_call": {"dequant_us": round(deq_us, 2), "dequant_wrapper_us": round(deq_wrap_us, 2),
+        "roofline": {"bound": "mfma", "kernel": "prefill_kernel + prefill_combine_kernel (bmx_prefill)",
+                     "achieved": round(flops / (attn_us * 1e-6) / 1e12, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flops / (attn_us * 1e-6) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+                     "traffic": None, "flops_per_launch": flops, "avg_launch_us": round(attn_us, 3)},
+        "prefill_call": {"attention_us": round(attn_us, 2),
+                         "dequant_us": round(deq_us, 2), "dequant_wrapper_us": round(deq_wrap_us, 2),
+                         "dequant_gbs": round(deq_bytes / (deq_us * 1e-6) / 1e9, 1),
+                         "dequant_frac_of_hbm": round(deq_bytes / (deq_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "dequant_bytes": deq_bytes,
                          "sdpa_dense_fp16_us": round(sdpa_us, 2),
                          "sdpa_tflops": round(flops / (sdpa_us * 1e-6) / 1e12, 1),
                          "sdpa_frac_of_fp16_mfma_peak": round(flops / (sdpa_us * 1e-6) / 1e12
@@ -713,6 +723,7 @@ def run_prefill(args, torch, dev) -> dict:
                          "packed_over_dense_fp16": round(call_us / sdpa_us, 3),
                          "sdpa_dense_fp16_lower_right_us": round(sdpa_lr_us, 2),
                          "packed_over_dense_fp16_lower_right": round(call_us / sdpa_lr_us, 3),
+                         "dense_fp16_bmx_prefill_us": round(attn_us, 2),
                          "max_abs_vs_fp32_sdpa": (out - ref).abs().max().item()},
     }
 

@@ -64,7 +64,7 @@ from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
 from . import codecs as K
-from . import k2b, rtn, spectral
+from . import k2b, prefill, rtn, spectral
 from .specs import CacheCodecSpec, packed_path
 
 ATTN_NAME = "chunked_dequant"   # the reference's name (packed_streaming.py:54), set on attach
@@ -628,12 +628,13 @@ class PackedStreamingLayer(DynamicLayer):
         """Prefill (n_q > 1): _prefill_dense_attention (chunked_attention.py:
         320-395).  The page kernel dequantizes the committed pages straight to
         the model dtype (k2b keys rotated in the same pass with the fp16 RoPE
-        tables, as _dense_kv does), the fp16 window follows, and one SDPA
-        attends: flash attention over the grouped heads (no G-fold copy of K
-        and V) when no mask is needed; with fewer queries than keys and no
-        mask, or the model's mask equal to it, the queries are the last n_q
-        positions and the bottom-right causal bias serves the grouped heads;
-        any other mask takes the memory-efficient kernel over expanded heads."""
+        tables, as _dense_kv does), the fp16 window follows, and one attention
+        call reads the grouped heads in place (no G-fold copy of K and V).
+        With no mask, or fewer queries than keys and the model's mask equal to
+        the causal mask of the last n_q positions (bottom right), that is
+        bmx_prefill (fp16 / bf16, head dim 128); other head dims take SDPA's
+        flash kernel or its bottom-right causal bias for the same masks; any
+        other mask takes SDPA's memory-efficient kernel over expanded heads."""
         dev, dt = q.device, q.dtype
         P = self._committed_S_q
         wk, wv = self.window()
@@ -660,8 +661,13 @@ class PackedStreamingLayer(DynamicLayer):
         else:
             Kd, Vd = wk.squeeze(0).to(dt), wv.squeeze(0).to(dt)
         n_q, n_kv = q.shape[1], Kd.shape[1]
-        if n_q != n_kv and ((causal and attention_mask is None)
-                            or _is_lower_right_causal(attention_mask, n_q, n_kv)):
+        lower_right = n_q != n_kv and ((causal and attention_mask is None)
+                                       or _is_lower_right_causal(attention_mask, n_q, n_kv))
+        if (lower_right or attention_mask is None) and prefill.supported(q, Kd, Vd):
+            # bmx_prefill: grouped heads read their K/V head in place; causal
+            # is the bottom-right mask (n_q == n_kv: the ordinary one)
+            return prefill.attention(q, Kd, Vd, scaling, causal=causal or lower_right)
+        if lower_right:
             # the queries are the last n_q positions: causal from the bottom
             # right, which ROCm's kernels take as a bias of their own (grouped
             # heads, no mask tensor: ~1.5x the memory-efficient kernel's speed

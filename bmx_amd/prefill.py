@@ -26,9 +26,16 @@ DTYPES = {torch.float16: 0, torch.bfloat16: 1}   # BMX_PREFILL_F16 / BF16
 _WS: dict = {}
 
 
-def supported(q: torch.Tensor, k: torch.Tensor) -> bool:
-    """Whether bmx_prefill takes these operands (head dim 128, fp16/bf16)."""
-    return q.shape[-1] == HEAD_DIM and q.dtype in DTYPES and k.dtype == q.dtype and q.is_cuda
+def supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether bmx_prefill takes these operands: head dim 128, fp16 / bf16,
+    16-byte aligned rows, K and V with the same strides, grouped heads."""
+    def rows_ok(t):
+        return (t.dim() == 3 and t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0
+                and t.data_ptr() % 16 == 0)
+    return (q.is_cuda and q.shape[-1] == HEAD_DIM and k.shape[-1] == HEAD_DIM and q.dtype in DTYPES
+            and k.dtype == q.dtype and v.dtype == q.dtype and v.shape == k.shape and v.stride() == k.stride()
+            and rows_ok(q) and rows_ok(k) and rows_ok(v) and k.stride(1) >= HEAD_DIM
+            and q.shape[0] % k.shape[0] == 0)
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, *, causal: bool,
