@@ -35,6 +35,7 @@
 
 #include <cmath>
 #include <string>
+#include <type_traits>
 
 namespace bmx {
 namespace {
@@ -87,6 +88,20 @@ __device__ __forceinline__ uint32_t pf_pack(float x, float y) {
   }
 }
 
+// max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one row of the
+// scores' MFMA layout).  (gfx950's v_permlane16/32_swap give the same
+// exchange without LDS, but as this compiler schedules them inside the loop
+// the results were wrong on the GPU while a lone probe of them was right.)
+__device__ __forceinline__ float row4_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+
+__device__ __forceinline__ float row4_sum(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
 // byte offset of 16-byte column c of key row `key` in the K tile: the 16
 // keys one MFMA operand reads (key bits 0-1 and 3-4 vary) land on 16
 // different columns of the 256-byte bank window
@@ -122,11 +137,15 @@ void prefill_kernel(const PfArgs a) {
   for (int rb = 0; rb < 2; ++rb) {
     const int r = min(R0 + 32 * wave + 16 * rb + col, a.R - 1);
     const int i = r / a.G, g = r - i * a.G;
-    last_key[rb] = a.causal ? i + a.off : a.n_kv - 1;
+    last_key[rb] = a.causal ? i + a.off : a.n_kv - 1;   // < n_kv either way
     const uint16_t* qp = a.q + (int64_t)(h * a.G + g) * a.qsh + (int64_t)i * a.qst + 8 * grp;
 #pragma unroll
     for (int dc = 0; dc < 4; ++dc) qb[rb][dc] = *reinterpret_cast<const u32x4_t*>(qp + 32 * dc);
   }
+  // Q is in registers before the loop starts (vmcnt(0)): a wait inside the
+  // loop, where the next tile's loads are in flight, is never needed for it
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_sched_barrier(0);
 
   // K and V of the head through buffer descriptors: rows past n_kv read zeros
   const uint32_t nrec = (uint32_t)((int64_t)a.n_kv * a.st * 2);
@@ -134,10 +153,14 @@ void prefill_kernel(const PfArgs a) {
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.k + (int64_t)h * a.sh), (short)0, nrec, kPfBufWord3);
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.v + (int64_t)h * a.sh), (short)0, nrec, kPfBufWord3);
-  // tile loads: thread (row part tid / 16, column tid % 16).  K: keys tid/16 +
-  // 16 j; V: keys 4 (tid/16) + j, so that the thread holds a 4-key x
-  // 8-channel block to transpose
+  // tile loads.  K: thread (lr, lc) = (tid / 16, tid % 16) loads 16 bytes of
+  // key lr + 16 j at column lc (a 16-lane row reads a whole key row).  V:
+  // thread (vr4, vc) = (tid % 16, tid / 16) loads keys 4 vr4 + j at channels
+  // 8 vc .. +7, a 4-key x 8-channel block it writes transposed; the 16 lanes
+  // of an LDS write phase then hold 16 different key groups of one channel
+  // row: 128 contiguous bytes, every bank once
   const int lr = tid >> 4, lc = tid & 15;
+  const int vr4 = tid & 15, vc = tid >> 4;
   u32x4_t kr[4], vr[4];
   auto issue = [&](int t) {
     const int k0 = t * kPfKeys;
@@ -148,7 +171,7 @@ void prefill_kernel(const PfArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       vr[j] = __builtin_amdgcn_raw_buffer_load_b128(
-          vrs, (uint32_t)(((int64_t)(k0 + 4 * lr + j) * a.st + 8 * lc) * 2), 0, 0);
+          vrs, (uint32_t)(((int64_t)(k0 + 4 * vr4 + j) * a.st + 8 * vc) * 2), 0, 0);
   };
   auto stash = [&](int stage) {
     uint8_t* ks = smem + stage * kPfStage;
@@ -156,13 +179,13 @@ void prefill_kernel(const PfArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(ks + ks_off(lr + 16 * j, lc)) = kr[j];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {   // dword p of a key row: channels 8 lc + 2 p, + 1
+    for (int p = 0; p < 4; ++p) {   // dword p of a key row: channels 8 vc + 2 p, + 1
       const u32x2_t lo = {__builtin_amdgcn_perm(vr[1][p], vr[0][p], 0x05040100u),
                           __builtin_amdgcn_perm(vr[3][p], vr[2][p], 0x05040100u)};
       const u32x2_t hi = {__builtin_amdgcn_perm(vr[1][p], vr[0][p], 0x07060302u),
                           __builtin_amdgcn_perm(vr[3][p], vr[2][p], 0x07060302u)};
-      *reinterpret_cast<u32x2_t*>(vt + (8 * lc + 2 * p) * kPfVtPitch + 8 * lr) = lo;
-      *reinterpret_cast<u32x2_t*>(vt + (8 * lc + 2 * p + 1) * kPfVtPitch + 8 * lr) = hi;
+      *reinterpret_cast<u32x2_t*>(vt + (8 * vc + 2 * p) * kPfVtPitch + 8 * vr4) = lo;
+      *reinterpret_cast<u32x2_t*>(vt + (8 * vc + 2 * p + 1) * kPfVtPitch + 8 * vr4) = hi;
     }
   };
 
@@ -173,12 +196,10 @@ void prefill_kernel(const PfArgs a) {
     for (int rb = 0; rb < 2; ++rb) o[db][rb] = {0.f, 0.f, 0.f, 0.f};
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
 
-  if (t0 < t1) {
-    issue(t0);
-    stash(0);
-    __syncthreads();
-  }
-  for (int t = t0; t < t1; ++t) {
+  // one 64-key tile; kMasked: the tile crosses the causal edge of some row
+  // or the end of the keys
+  auto tile = [&](int t, auto masked_c) {
+    constexpr bool kMasked = decltype(masked_c)::value;
     const int stage = (t - t0) & 1;
     if (t + 1 < t1) issue(t + 1);
     const uint8_t* ks = smem + stage * kPfStage;
@@ -199,18 +220,17 @@ void prefill_kernel(const PfArgs a) {
         s[kb][rb] = acc;
       }
     }
-    // ---- online softmax; P^T as the values' B operand
-    u32x4_t pb[2][2];
-    const bool masked = t >= t_mask;
+    // ---- online softmax (base 2); P^T as the values' B operand
+    float m_use[2], alpha[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      if (masked) {
+      if constexpr (kMasked) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int key = t * kPfKeys + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + e;
-            if (key > last_key[rb] || key >= a.n_kv) s[kb][rb][e] = -INFINITY;
+            if (key > last_key[rb]) s[kb][rb][e] = -INFINITY;
           }
       }
       float mx = s[0][rb][0];
@@ -218,23 +238,34 @@ void prefill_kernel(const PfArgs a) {
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[kb][rb][e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = row4_max(mx);
       const float m_new = fmaxf(m[rb], mx * a.qscale);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;   // no visible key yet
-      const float alpha = __builtin_amdgcn_exp2f(m[rb] - m_use);
+      m_use[rb] = m_new == -INFINITY ? 0.f : m_new;   // no visible key yet
+      alpha[rb] = __builtin_amdgcn_exp2f(m[rb] - m_use[rb]);
       m[rb] = m_new;
+    }
+    // the running sums and outputs move only when some row's maximum moved
+    // (scaling by 1 is exact, so skipping it changes nothing)
+    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        l[rb] *= alpha[rb];
+#pragma unroll
+        for (int db = 0; db < 8; ++db) o[db][rb] *= alpha[rb];
+      }
+    }
+    u32x4_t pb[2][2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
       float p[4][4], ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          p[kb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][rb][e], a.qscale, -m_use));
+          p[kb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][rb][e], a.qscale, -m_use[rb]));
           ps += p[kb][e];
         }
-      l[rb] = __builtin_fmaf(l[rb], alpha, ps);
-#pragma unroll
-      for (int db = 0; db < 8; ++db) o[db][rb] *= alpha;
+      l[rb] += ps;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const u32x4_t w = {pf_pack<DT>(p[2 * hh][0], p[2 * hh][1]), pf_pack<DT>(p[2 * hh][2], p[2 * hh][3]),
@@ -245,24 +276,33 @@ void prefill_kernel(const PfArgs a) {
     }
     // ---- values
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
+    for (int hh = 0; hh < 2; ++hh) {
+      u32x4_t va[8];
 #pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        const u32x4_t va =
-            *reinterpret_cast<const u32x4_t*>(vt + (16 * db + col) * kPfVtPitch + 64 * hh + 16 * grp);
+      for (int db = 0; db < 8; ++db)
+        va[db] = *reinterpret_cast<const u32x4_t*>(vt + (16 * db + col) * kPfVtPitch + 64 * hh + 16 * grp);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) o[db][rb] = pf_mma<DT>(va, pb[hh][rb], o[db][rb]);
-      }
+      for (int db = 0; db < 8; ++db)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) o[db][rb] = pf_mma<DT>(va[db], pb[hh][rb], o[db][rb]);
+    }
     if (t + 1 < t1) stash(stage ^ 1);
     __syncthreads();
+  };
+
+  if (t0 < t1) {
+    issue(t0);
+    stash(0);
+    __syncthreads();
   }
+  const int t_split = max(t0, min(t1, t_mask));
+  for (int t = t0; t < t_split; ++t) tile(t, std::false_type{});
+  for (int t = t_split; t < t1; ++t) tile(t, std::true_type{});
 
   // ---- rows out: lane (col, grp) holds row col of each block, channels 16 db + 4 grp .. +3
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    float lt = l[rb];
-    lt += __shfl_xor(lt, 16);
-    lt += __shfl_xor(lt, 32);
+    const float lt = row4_sum(l[rb]);
     const int r = R0 + 32 * wave + 16 * rb + col;
     if (r >= a.R) continue;
     if (a.n_split == 1) {
