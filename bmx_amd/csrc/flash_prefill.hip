@@ -204,7 +204,10 @@ void prefill_kernel(const PfArgs a) {
     if (t + 1 < t1) issue(t + 1);
     const uint8_t* ks = smem + stage * kPfStage;
     const uint8_t* vt = ks + kPfKsBytes;
-    // ---- scores
+    // ---- scores.  The MFMA blocks run at raised wave priority: of the two
+    // waves on a SIMD, the one entering its MFMA block takes the issue slots
+    // while the other does its softmax or stash (-4 % per call at 64k keys)
+    __builtin_amdgcn_s_setprio(1);
     float4_t s[4][2];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -220,6 +223,7 @@ void prefill_kernel(const PfArgs a) {
         s[kb][rb] = acc;
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     // ---- online softmax (base 2); P^T as the values' B operand
     float m_use[2], alpha[2];
 #pragma unroll
@@ -274,7 +278,11 @@ void prefill_kernel(const PfArgs a) {
         pb[hh][rb] = w;
       }
     }
+    // the next tile goes to the other stage ahead of the values' MFMAs, so
+    // that its writes overlap them
+    if (t + 1 < t1) stash(stage ^ 1);
     // ---- values
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       u32x4_t va[8];
@@ -286,7 +294,7 @@ void prefill_kernel(const PfArgs a) {
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) o[db][rb] = pf_mma<DT>(va[db], pb[hh][rb], o[db][rb]);
     }
-    if (t + 1 < t1) stash(stage ^ 1);
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
   };
 
