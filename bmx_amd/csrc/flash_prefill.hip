@@ -15,14 +15,14 @@
 //     columns XOR-swizzled by key, V transposed (one 144-byte row of 64 keys
 //     per channel), so that every MFMA operand is one conflict-free 16-byte
 //     LDS read;
-//   * scores S^T = K . Q^T on v_mfma_f32_16x16x32 (Q in registers).  The
-//     A-operand row n of key block kb is key 32 (kb/2) + 8 (n/4) + n%4 +
-//     4 (kb%2), so across the block pair (2 hh, 2 hh + 1) lane group j of the
-//     result holds keys 32 hh + 8 j .. +7 of its row: the B operand of P^T
-//     for the values' MFMA, converted in place;
-//   * online softmax in base 2 per row: a lane holds 16 scores of one row,
-//     the row's 4 lanes exchange the maximum; only tiles that cross the
-//     causal edge or the end of the keys are masked;
+//   * scores S^T = K . Q^T on v_mfma_f32_32x32x16 (Q in registers), one
+//     32x32 block per 32 keys.  The A-operand rows are a permutation of the
+//     block's keys chosen so that result elements 8 u .. 8 u + 7 of lane half
+//     hf are keys 16 u + 8 hf .. +7: the B operand of P^T for the values'
+//     MFMA over key sub-block u, converted in place;
+//   * online softmax in base 2: a lane holds 32 scores of one row, the row's
+//     2 lanes exchange the maximum; only tiles that cross the causal edge or
+//     the end of the keys are masked;
 //   * O^T += V^T . P^T (V^T read from the transposed tile).
 // With one key split per row tile the workgroup writes the normalized rows;
 // with several it writes (O, m, l) partials that prefill_combine_kernel
@@ -67,16 +67,6 @@ struct PfArgs {
 };
 
 template <int DT>
-__device__ __forceinline__ float4_t pf_mma(u32x4_t a, u32x4_t b, float4_t c) {
-  if constexpr (DT == BMX_PREFILL_F16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b),
-                                                  c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-
-template <int DT>
 __device__ __forceinline__ uint32_t pf_pack(float x, float y) {
   if constexpr (DT == BMX_PREFILL_F16) {
     const half2_t h = {(_Float16)x, (_Float16)y};
@@ -88,26 +78,23 @@ __device__ __forceinline__ uint32_t pf_pack(float x, float y) {
   }
 }
 
-// max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one row of the
-// scores' MFMA layout).  (gfx950's v_permlane16/32_swap give the same
-// exchange without LDS, but as this compiler schedules them inside the loop
-// the results were wrong on the GPU while a lone probe of them was right.)
-__device__ __forceinline__ float row4_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
-}
+typedef float float16_t __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ float row4_sum(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
+template <int DT>
+__device__ __forceinline__ float16_t pf_mma32(u32x4_t a, u32x4_t b, float16_t c) {
+  if constexpr (DT == BMX_PREFILL_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b),
+                                                  c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
 // byte offset of 16-byte column c of key row `key` in the K tile: the 16
-// keys one MFMA operand reads (key bits 0-1 and 3-4 vary) land on 16
+// keys one MFMA operand phase reads (16 consecutive keys) land on 16
 // different columns of the 256-byte bank window
 __device__ __forceinline__ int ks_off(int key, int c) {
-  const int swz = (key & 3) | (((key >> 3) & 3) << 2);
-  return key * (2 * kPfD) + ((c ^ swz) << 4);
+  return key * (2 * kPfD) + ((c ^ (key & 15)) << 4);
 }
 
 template <int DT>
@@ -129,18 +116,19 @@ void prefill_kernel(const PfArgs a) {
   const int t0 = (int)((int64_t)split * nt / a.n_split), t1 = (int)((int64_t)(split + 1) * nt / a.n_split);
   const int t_mask = edge / kPfKeys;   // tiles from here on cross the edge or the end of the keys
 
-  // the wave's two 16-row blocks: Q as the B operand (row = lane % 16,
-  // channels 32 dc + 8 grp .. +7), and the last key each row sees
-  u32x4_t qb[2][4];
-  int last_key[2];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int r = min(R0 + 32 * wave + 16 * rb + col, a.R - 1);
+  // the wave's 32 rows: Q as the B operand of the 32x32x16 MFMA (row =
+  // lane % 32, channels 16 dc + 8 hf .. +7, hf = lane / 32), and the last key
+  // the lane's row sees
+  const int r32 = lane & 31, hf = lane >> 5;
+  u32x4_t qb[8];
+  int last_key;
+  {
+    const int r = min(R0 + 32 * wave + r32, a.R - 1);
     const int i = r / a.G, g = r - i * a.G;
-    last_key[rb] = a.causal ? i + a.off : a.n_kv - 1;   // < n_kv either way
-    const uint16_t* qp = a.q + (int64_t)(h * a.G + g) * a.qsh + (int64_t)i * a.qst + 8 * grp;
+    last_key = a.causal ? i + a.off : a.n_kv - 1;   // < n_kv either way
+    const uint16_t* qp = a.q + (int64_t)(h * a.G + g) * a.qsh + (int64_t)i * a.qst + 8 * hf;
 #pragma unroll
-    for (int dc = 0; dc < 4; ++dc) qb[rb][dc] = *reinterpret_cast<const u32x4_t*>(qp + 32 * dc);
+    for (int dc = 0; dc < 8; ++dc) qb[dc] = *reinterpret_cast<const u32x4_t*>(qp + 16 * dc);
   }
   // Q is in registers before the loop starts (vmcnt(0)): a wait inside the
   // loop, where the next tile's loads are in flight, is never needed for it
@@ -189,12 +177,16 @@ void prefill_kernel(const PfArgs a) {
     }
   };
 
-  float4_t o[8][2];
+  float16_t o[4];   // O^T by 32-channel block: element e = channel 32 cb + 8 (e / 4) + 4 hf + e % 4
 #pragma unroll
-  for (int db = 0; db < 8; ++db)
+  for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) o[db][rb] = {0.f, 0.f, 0.f, 0.f};
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    for (int e = 0; e < 16; ++e) o[cb][e] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  // A-operand row n (= 8 j + 4 x + e) of a 32-key block reads key 16 (j / 2)
+  // + 8 x + 4 (j % 2) + e: result element 8 u + w of lane half hf is then key
+  // 16 u + 8 hf + w of the block, the B operand of P^T for key sub-block u
+  const int kperm = 16 * (r32 >> 4) + 8 * ((r32 >> 2) & 1) + 4 * ((r32 >> 3) & 1) + (r32 & 3);
 
   // one 64-key tile; kMasked: the tile crosses the causal edge of some row
   // or the end of the keys
@@ -206,93 +198,81 @@ void prefill_kernel(const PfArgs a) {
     const uint8_t* vt = ks + kPfKsBytes;
     // ---- scores.  The MFMA blocks run at raised wave priority: of the two
     // waves on a SIMD, the one entering its MFMA block takes the issue slots
-    // while the other does its softmax or stash (-4 % per call at 64k keys)
+    // while the other does its softmax or stash
     __builtin_amdgcn_s_setprio(1);
-    float4_t s[4][2];
+    float16_t s[2];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int key = 32 * (kb >> 1) + 8 * (col >> 2) + (col & 3) + 4 * (kb & 1);
-      u32x4_t ka[4];
+    for (int kb = 0; kb < 2; ++kb) {
+      const int key = 32 * kb + kperm;
+      float16_t acc;
 #pragma unroll
-      for (int dc = 0; dc < 4; ++dc) ka[dc] = *reinterpret_cast<const u32x4_t*>(ks + ks_off(key, 4 * dc + grp));
+      for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int dc = 0; dc < 4; ++dc) acc = pf_mma<DT>(ka[dc], qb[rb][dc], acc);
-        s[kb][rb] = acc;
+      for (int dc = 0; dc < 8; ++dc) {
+        const u32x4_t ka = *reinterpret_cast<const u32x4_t*>(ks + ks_off(key, 2 * dc + hf));
+        acc = pf_mma32<DT>(ka, qb[dc], acc);
       }
+      s[kb] = acc;
     }
     __builtin_amdgcn_s_setprio(0);
-    // ---- online softmax (base 2); P^T as the values' B operand
-    float m_use[2], alpha[2];
+    // ---- online softmax (base 2) of the lane's row; P^T as the values' B operand
+    if constexpr (kMasked) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      if constexpr (kMasked) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int key = t * kPfKeys + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + e;
-            if (key > last_key[rb]) s[kb][rb][e] = -INFINITY;
-          }
-      }
-      float mx = s[0][rb][0];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[kb][rb][e]);
-      mx = row4_max(mx);
-      const float m_new = fmaxf(m[rb], mx * a.qscale);
-      m_use[rb] = m_new == -INFINITY ? 0.f : m_new;   // no visible key yet
-      alpha[rb] = __builtin_amdgcn_exp2f(m[rb] - m_use[rb]);
-      m[rb] = m_new;
-    }
-    // the running sums and outputs move only when some row's maximum moved
-    // (scaling by 1 is exact, so skipping it changes nothing)
-    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        l[rb] *= alpha[rb];
-#pragma unroll
-        for (int db = 0; db < 8; ++db) o[db][rb] *= alpha[rb];
-      }
-    }
-    u32x4_t pb[2][2];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      float p[4][4], ps = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          p[kb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][rb][e], a.qscale, -m_use[rb]));
-          ps += p[kb][e];
+        for (int e = 0; e < 16; ++e) {
+          const int key = t * kPfKeys + 32 * kb + 16 * (e >> 3) + 8 * hf + (e & 7);
+          if (key > last_key) s[kb][e] = -INFINITY;
         }
-      l[rb] += ps;
+    }
+    float mx = s[0][0];
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const u32x4_t w = {pf_pack<DT>(p[2 * hh][0], p[2 * hh][1]), pf_pack<DT>(p[2 * hh][2], p[2 * hh][3]),
-                           pf_pack<DT>(p[2 * hh + 1][0], p[2 * hh + 1][1]),
-                           pf_pack<DT>(p[2 * hh + 1][2], p[2 * hh + 1][3])};
-        pb[hh][rb] = w;
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx * a.qscale);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;   // no visible key yet
+    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+    m = m_new;
+    // the running sum and outputs move only when some row's maximum moved
+    // (scaling by 1 is exact, so skipping it changes nothing)
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+      l *= alpha;
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) o[cb] *= alpha;
+    }
+    u32x4_t pb[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float p[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][e], a.qscale, -m_use));
+        ps += p[e];
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x4_t w = {pf_pack<DT>(p[8 * u], p[8 * u + 1]), pf_pack<DT>(p[8 * u + 2], p[8 * u + 3]),
+                           pf_pack<DT>(p[8 * u + 4], p[8 * u + 5]), pf_pack<DT>(p[8 * u + 6], p[8 * u + 7])};
+        pb[2 * kb + u] = w;
       }
     }
+    l += ps;
     // the next tile goes to the other stage ahead of the values' MFMAs, so
     // that its writes overlap them
     if (t + 1 < t1) stash(stage ^ 1);
-    // ---- values
+    // ---- values: O^T += V^T . P^T over the tile's four 16-key sub-blocks
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      u32x4_t va[8];
+    for (int sb = 0; sb < 4; ++sb) {
+      u32x4_t va[4];
 #pragma unroll
-      for (int db = 0; db < 8; ++db)
-        va[db] = *reinterpret_cast<const u32x4_t*>(vt + (16 * db + col) * kPfVtPitch + 64 * hh + 16 * grp);
+      for (int cb = 0; cb < 4; ++cb)
+        va[cb] = *reinterpret_cast<const u32x4_t*>(vt + (32 * cb + r32) * kPfVtPitch + 32 * sb + 16 * hf);
 #pragma unroll
-      for (int db = 0; db < 8; ++db)
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) o[db][rb] = pf_mma<DT>(va[db], pb[hh][rb], o[db][rb]);
+      for (int cb = 0; cb < 4; ++cb) o[cb] = pf_mma32<DT>(va[cb], pb[sb], o[cb]);
     }
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();
@@ -307,30 +287,37 @@ void prefill_kernel(const PfArgs a) {
   for (int t = t0; t < t_split; ++t) tile(t, std::false_type{});
   for (int t = t_split; t < t1; ++t) tile(t, std::true_type{});
 
-  // ---- rows out: lane (col, grp) holds row col of each block, channels 16 db + 4 grp .. +3
+  // ---- rows out: lane (r32, hf) holds row r32, channels 32 cb + 8 j + 4 hf .. +3
+  {
+    const float lt = l + __shfl_xor(l, 32);
+    const int r = R0 + 32 * wave + r32;
+    if (r < a.R) {
+      if (a.n_split == 1) {
+        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+        const int i = r / a.G, g = r - i * a.G;
+        uint16_t* op = a.out + ((int64_t)(h * a.G + g) * a.n_q + i) * kPfD + 4 * hf;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const float lt = row4_sum(l[rb]);
-    const int r = R0 + 32 * wave + 16 * rb + col;
-    if (r >= a.R) continue;
-    if (a.n_split == 1) {
-      const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-      const int i = r / a.G, g = r - i * a.G;
-      uint16_t* op = a.out + ((int64_t)(h * a.G + g) * a.n_q + i) * kPfD + 4 * grp;
+        for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        const u32x2_t w = {pf_pack<DT>(o[db][rb][0] * inv, o[db][rb][1] * inv),
-                           pf_pack<DT>(o[db][rb][2] * inv, o[db][rb][3] * inv)};
-        *reinterpret_cast<u32x2_t*>(op + 16 * db) = w;
-      }
-    } else {
-      const int64_t prow = ((int64_t)h * a.n_split + split) * a.R + r;
-      float* po = a.part_o + prow * kPfD + 4 * grp;
+          for (int j = 0; j < 4; ++j) {
+            const u32x2_t w = {pf_pack<DT>(o[cb][4 * j] * inv, o[cb][4 * j + 1] * inv),
+                               pf_pack<DT>(o[cb][4 * j + 2] * inv, o[cb][4 * j + 3] * inv)};
+            *reinterpret_cast<u32x2_t*>(op + 32 * cb + 8 * j) = w;
+          }
+      } else {
+        const int64_t prow = ((int64_t)h * a.n_split + split) * a.R + r;
+        float* po = a.part_o + prow * kPfD + 4 * hf;
 #pragma unroll
-      for (int db = 0; db < 8; ++db) *reinterpret_cast<float4_t*>(po + 16 * db) = o[db][rb];
-      if (grp == 0) {
-        const float2 ml = make_float2(m[rb], lt);
-        *reinterpret_cast<float2*>(a.part_ml + 2 * prow) = ml;
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float4_t w = {o[cb][4 * j], o[cb][4 * j + 1], o[cb][4 * j + 2], o[cb][4 * j + 3]};
+            *reinterpret_cast<float4_t*>(po + 32 * cb + 8 * j) = w;
+          }
+        if (hf == 0) {
+          const float2 ml = make_float2(m, lt);
+          *reinterpret_cast<float2*>(a.part_ml + 2 * prow) = ml;
+        }
       }
     }
   }
