@@ -2,7 +2,9 @@
 
 ``torch.ops.bmx.k2b_decode`` / ``k2b_append`` / ``rtn_decode`` / ``rtn_append``
 are the same C-ABI calls as ``bmx_amd.k2b`` / ``bmx_amd.rtn`` (one ctypes call
-each on the current stream), registered so that the dispatcher, FakeTensor
+each on the current stream), and ``torch.ops.bmx.prefill_attention`` the
+prefill attention of ``bmx_amd.prefill`` (chunked_attention.py:320-395 calls
+SDPA there), registered so that the dispatcher, FakeTensor
 tracing, ``torch.compile`` (no graph break) and CUDA-graph capture see them as
 single operators.  The reference exposes these steps as Python functions that
 launch Triton kernels (cache/triton_dequant_attention.py:1232-1246 for the
@@ -21,7 +23,7 @@ from typing import Optional
 
 import torch
 
-from . import k2b, rtn
+from . import k2b, prefill, rtn
 
 _LIB = "bmx"
 
@@ -108,6 +110,21 @@ def rtn_append(k: torch.Tensor, v: torch.Tensor, pages: torch.Tensor, page_ids: 
 @rtn_append.register_fake
 def _(k, v, pages, page_ids, k_bits, v_bits, k_group, v_group, k_arm=rtn.TOKEN):
     return None
+
+
+@torch.library.custom_op(f"{_LIB}::prefill_attention", mutates_args=(), device_types="cuda")
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sm_scale: float, causal: bool,
+                      n_split: int = 0) -> torch.Tensor:
+    """Attention of (h_kv * G, n_q, 128) queries over (h_kv, n_kv, 128) K/V
+    rows, grouped heads, bottom-right causal or no mask
+    (``bmx_amd.prefill.attention``)."""
+    return prefill.attention(q, k, v, sm_scale, causal=causal, n_split=n_split)
+
+
+@prefill_attention.register_fake
+def _(q, k, v, sm_scale, causal, n_split=0):
+    torch._check(q.dim() == 3 and q.shape[-1] == prefill.HEAD_DIM and k.dim() == 3)
+    return torch.empty(q.shape, dtype=q.dtype, device=q.device)
 
 
 def consts_args(consts: k2b.CodecConsts) -> dict:

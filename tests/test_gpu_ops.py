@@ -115,3 +115,26 @@ def test_rtn_operators_equal_direct_calls():
     ref = rtn.decode(q, p1, table, ln, S, 128 ** -0.5, k_tail=kt, v_tail=vt, tail_len=T, tail_cap=T, **codec)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def test_prefill_operator_equals_direct_call_and_compiles():
+    from bmx_amd import prefill
+
+    g = torch.Generator(device=DEV).manual_seed(33)
+    q = torch.randn(16, 200, 128, device=DEV, generator=g).half()
+    k = torch.randn(4, 1000, 128, device=DEV, generator=g).half()
+    v = torch.randn(4, 1000, 128, device=DEV, generator=g).half()
+    out = torch.ops.bmx.prefill_attention(q, k, v, 128 ** -0.5, True)
+    ref = prefill.attention(q, k, v, 128 ** -0.5, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+    def layer(q):   # the attention with work either side
+        return torch.ops.bmx.prefill_attention(q * 1.0, k, v, 128 ** -0.5, True).float().sum(dim=0)
+
+    compiled = torch.compile(layer, fullgraph=True, backend="aot_eager")
+    got = compiled(q)
+    torch.cuda.synchronize()
+    assert torch.equal(got, layer(q))
+    torch.library.opcheck(torch.ops.bmx.prefill_attention.default, (q, k, v, 128 ** -0.5, True), {},
+                          test_utils=("test_schema", "test_faketensor"))

@@ -10,13 +10,13 @@ from bmx_amd import k2b, ops, rtn
 
 
 def test_operators_registered_with_their_schemas():
-    for name in ("k2b_decode", "k2b_append", "rtn_decode", "rtn_append"):
+    for name in ("k2b_decode", "k2b_append", "rtn_decode", "rtn_append", "prefill_attention"):
         op = getattr(torch.ops.bmx, name).default
         assert op._schema.name == f"bmx::{name}"
     for name in ("k2b_append", "rtn_append"):   # the page pool is the one argument written
         sch = getattr(torch.ops.bmx, name).default._schema
         assert [a.name for a in sch.arguments if a.alias_info is not None and a.alias_info.is_write] == ["pages"]
-    for name in ("k2b_decode", "rtn_decode"):    # decode writes only its fresh output
+    for name in ("k2b_decode", "rtn_decode", "prefill_attention"):   # fresh outputs only
         sch = getattr(torch.ops.bmx, name).default._schema
         assert all(a.alias_info is None for a in sch.arguments)
 
@@ -37,6 +37,15 @@ def test_fake_decode_gives_the_query_shape_and_dtype(dt):
                          dtype=torch.uint8, device="cuda")
         o = torch.ops.bmx.rtn_decode(q, rp, table, ln, 1024, 128 ** -0.5, 4, 4, 32, 32)
         assert o.shape == q.shape and o.dtype == dt
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_fake_prefill_gives_the_query_shape_and_dtype(dt):
+    with FakeTensorMode():
+        q = torch.empty(16, 100, 128, dtype=dt, device="cuda").transpose(0, 1).transpose(0, 1)
+        k = torch.empty(4, 900, 128, dtype=dt, device="cuda")
+        o = torch.ops.bmx.prefill_attention(q, k, k, 128 ** -0.5, True)
+        assert o.shape == (16, 100, 128) and o.dtype == dt and o.is_contiguous()
 
 
 def test_cpu_tensors_are_refused_by_the_dispatcher():
