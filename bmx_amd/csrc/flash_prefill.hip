@@ -231,7 +231,11 @@ void prefill_kernel(const PfArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kb][e]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx * a.qscale);
+    // the row keeps its offset until a score passes it by more than 8 (base
+    // 2): P stays <= 256, exact in the 16-bit types' range, and the wave
+    // rescales only when some row's offset moved
+    const float m_cand = fmaxf(m, mx * a.qscale);
+    const float m_new = m_cand > m + 8.f ? m_cand : m;
     const float m_use = m_new == -INFINITY ? 0.f : m_new;   // no visible key yet
     const float alpha = __builtin_amdgcn_exp2f(m - m_use);
     m = m_new;
